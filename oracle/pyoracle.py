@@ -1,0 +1,263 @@
+"""ctypes binding of the oracle (liboracle.so) and of oracle/_ref/libref.so.
+
+TEST INFRASTRUCTURE ONLY: imported by the test suite, the smoke check and the
+CPU-baseline leg of bench.py.  It is the checker, never the thing measured.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+_REF = None
+
+F32P = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+F64P = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+
+
+class FbankCfg(C.Structure):
+    _fields_ = [("sample_rate", C.c_int), ("n_mels", C.c_int), ("n_fft", C.c_int),
+                ("win_length", C.c_int), ("hop_length", C.c_int), ("preemph", C.c_float),
+                ("low_freq", C.c_float), ("high_freq", C.c_float), ("cmn", C.c_int)]
+
+
+MAXB = 32
+_fp = C.POINTER(C.c_float)
+
+
+class ResNet(C.Structure):
+    _fields_ = [("n_mels", C.c_int), ("stem_oc", C.c_int), ("stem_w", _fp), ("stem_b", _fp),
+                ("n_blocks", C.c_int),
+                ("in_c", C.c_int * MAXB), ("out_c", C.c_int * MAXB), ("stride", C.c_int * MAXB),
+                ("conv1_w", _fp * MAXB), ("conv1_b", _fp * MAXB),
+                ("conv2_w", _fp * MAXB), ("conv2_b", _fp * MAXB),
+                ("down_w", _fp * MAXB), ("down_b", _fp * MAXB),
+                ("seg_w", _fp), ("seg_b", _fp), ("mean_vec", _fp),
+                ("emb_dim", C.c_int), ("var_eps", C.c_float), ("l2_normalize", C.c_int)]
+
+
+class ResNetCaps(C.Structure):
+    _fields_ = [("stem", _fp), ("block", _fp * MAXB), ("pooled", _fp), ("pre_norm", _fp)]
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"oracle not built: {path} (run make -C oracle)")
+        L = C.CDLL(path)
+        L.orc_fbank_frames.argtypes = [C.c_int, C.POINTER(FbankCfg)]
+        L.orc_fbank.argtypes = [F32P, C.c_int, C.POINTER(FbankCfg), F32P]
+        L.orc_powspec.argtypes = [F32P, C.c_int, C.c_int, C.c_int, F64P]
+        L.orc_mel_filters.argtypes = [C.POINTER(FbankCfg), F64P]
+        L.orc_povey_window.argtypes = [C.c_int, F64P]
+        conv = [F32P, C.c_int, C.c_int, C.c_int, F32P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                C.c_void_p, C.c_void_p, C.c_int]
+        L.orc_conv2d_f32.argtypes = conv + [F32P]
+        L.orc_conv2d_f64.argtypes = conv + [F64P]
+        L.orc_tstp.argtypes = [F32P, C.c_int, C.c_int, C.c_int, C.c_float, F32P]
+        L.orc_linear.argtypes = [F32P, C.c_int, F32P, C.c_void_p, C.c_void_p, C.c_int, F32P]
+        L.orc_l2norm.argtypes = [F32P, C.c_int]
+        L.orc_resnet34_forward.argtypes = [C.POINTER(ResNet), F32P, C.c_int, F32P, C.POINTER(ResNetCaps)]
+        L.orc_embed_batch.argtypes = [C.POINTER(ResNet), C.POINTER(FbankCfg), F32P, C.c_int, C.c_int,
+                                      C.c_int, F32P]
+        _LIB = L
+    return _LIB
+
+
+def ref_lib():
+    """oracle/_ref/libref.so (the reference's own FBank/WAV code) or None if not built."""
+    global _REF
+    if _REF is None:
+        path = os.path.join(HERE, "_ref", "libref.so")
+        if not os.path.exists(path):
+            return None
+        L = C.CDLL(path)
+        L.ref_fbank.argtypes = [F32P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                C.c_float, C.c_float, C.c_int, F32P, C.c_long]
+        L.ref_fbank.restype = C.c_int
+        L.ref_load_wav.argtypes = [C.c_char_p, F32P, C.c_long]
+        L.ref_load_wav.restype = C.c_long
+        L.ref_resample.argtypes = [F32P, C.c_long, C.c_int, C.c_int, F32P, C.c_long]
+        L.ref_resample.restype = C.c_long
+        _REF = L
+    return _REF
+
+
+def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
+              sample_rate=16000):
+    return FbankCfg(sample_rate, n_mels, n_fft, win, hop, preemph, low, high, int(cmn))
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def fbank(pcm, cfg=None):
+    cfg = cfg or fbank_cfg()
+    pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+    T = lib().orc_fbank_frames(len(pcm), C.byref(cfg))
+    out = np.zeros((cfg.n_mels, max(T, 1)), dtype=np.float32)
+    T2 = lib().orc_fbank(pcm, len(pcm), C.byref(cfg), out)
+    assert T2 == T
+    return out[:, :T]
+
+
+def ref_fbank(pcm, cfg=None):
+    cfg = cfg or fbank_cfg()
+    L = ref_lib()
+    pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+    cap = cfg.n_mels * (len(pcm) // max(cfg.hop_length, 1) + 2)
+    out = np.zeros(cap, dtype=np.float32)
+    T = L.ref_fbank(pcm, len(pcm), cfg.n_mels, cfg.n_fft, cfg.win_length, cfg.hop_length,
+                    cfg.preemph, cfg.low_freq, cfg.high_freq, cfg.cmn, out, cap)
+    assert T >= 0
+    return out[: cfg.n_mels * T].reshape(cfg.n_mels, T)
+
+
+def powspec(frame, n_fft, use_dft=False):
+    frame = np.ascontiguousarray(frame, dtype=np.float32)
+    out = np.zeros(n_fft // 2 + 1)
+    lib().orc_powspec(frame, len(frame), n_fft, int(use_dft), out)
+    return out
+
+
+def mel_filters(cfg=None):
+    cfg = cfg or fbank_cfg()
+    fb = np.zeros((cfg.n_mels, cfg.n_fft // 2 + 1))
+    lib().orc_mel_filters(C.byref(cfg), fb)
+    return fb
+
+
+def povey(win):
+    w = np.zeros(win)
+    lib().orc_povey_window(win, w)
+    return w
+
+
+def conv2d(x, w, stride=1, pad=1, bias=None, residual=None, relu=False, f64=False):
+    """x [IC,H,W] f32, w [OC,IC,KH,KW] -> [OC,Ho,Wo] (f32 or f64)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    IC, H, W = x.shape
+    OC, IC2, KH, KW = w.shape
+    assert IC == IC2
+    Ho, Wo = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    r = None if residual is None else np.ascontiguousarray(residual, dtype=np.float32)
+    if r is not None:
+        assert r.shape == (OC, Ho, Wo)
+    y = np.zeros((OC, Ho, Wo), dtype=np.float64 if f64 else np.float32)
+    fn = lib().orc_conv2d_f64 if f64 else lib().orc_conv2d_f32
+    fn(x, IC, H, W, w, OC, KH, KW, stride, pad, _p(b), _p(r), int(relu), y)
+    return y
+
+
+def tstp(x, eps=1e-8):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    Cc, H, W = x.shape
+    out = np.zeros(2 * Cc * H, dtype=np.float32)
+    lib().orc_tstp(x, Cc, H, W, eps, out)
+    return out
+
+
+def linear(x, w, b=None, mean_vec=None):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out_dim, in_dim = w.shape
+    y = np.zeros(out_dim, dtype=np.float32)
+    bb = None if b is None else np.ascontiguousarray(b, dtype=np.float32)
+    mv = None if mean_vec is None else np.ascontiguousarray(mean_vec, dtype=np.float32)
+    lib().orc_linear(x, in_dim, w, _p(bb), _p(mv), out_dim, y)
+    return y
+
+
+def l2norm(v):
+    v = np.array(v, dtype=np.float32, copy=True)
+    lib().orc_l2norm(v, len(v))
+    return v
+
+
+class OracleResNet:
+    """orc_resnet built from a parsed GGUF (vdamd.gguf.GGUFFile), weights dequantised to f32."""
+
+    def __init__(self, g):
+        kv = g.kv
+        self.keep = []
+        n = ResNet()
+
+        def ptr(name):
+            a = np.ascontiguousarray(g.array(name), dtype=np.float32)
+            self.keep.append(a)
+            return a.ctypes.data_as(_fp)
+
+        pre = "voicedetect.resnet."
+        n.n_mels = int(kv.get("voicedetect.fbank.n_mels", 80))
+        stem = g.array(kv[pre + "stem_weight"])
+        n.stem_oc = stem.shape[0]
+        n.stem_w = ptr(kv[pre + "stem_weight"])
+        n.stem_b = ptr(kv[pre + "stem_bias"])
+        nb = len(kv[pre + "conv1_weight"])
+        assert nb <= MAXB
+        n.n_blocks = nb
+        for i in range(nb):
+            w1 = g.array(kv[pre + "conv1_weight"][i])
+            n.out_c[i], n.in_c[i] = w1.shape[0], w1.shape[1]
+            n.stride[i] = kv[pre + "stride"][i]
+            n.conv1_w[i] = ptr(kv[pre + "conv1_weight"][i])
+            n.conv1_b[i] = ptr(kv[pre + "conv1_bias"][i])
+            n.conv2_w[i] = ptr(kv[pre + "conv2_weight"][i])
+            n.conv2_b[i] = ptr(kv[pre + "conv2_bias"][i])
+            dw = kv[pre + "down_weight"][i]
+            n.down_w[i] = ptr(dw) if dw else None
+            n.down_b[i] = ptr(kv[pre + "down_bias"][i]) if dw else None
+        seg = g.array(kv[pre + "seg_weight"])
+        n.emb_dim = seg.shape[0]
+        n.seg_w = ptr(kv[pre + "seg_weight"])
+        n.seg_b = ptr(kv[pre + "seg_bias"]) if kv.get(pre + "seg_bias") else None
+        mv = kv.get(pre + "mean_vec", "")
+        n.mean_vec = ptr(mv) if mv else None
+        n.var_eps = float(kv.get(pre + "var_eps", 1e-8))
+        n.l2_normalize = int(bool(kv.get("voicedetect.l2_normalize", True)))
+        self.net = n
+        self.blocks = [(n.in_c[i], n.out_c[i], n.stride[i]) for i in range(nb)]
+
+    def block_shapes(self, T):
+        H, W = self.net.n_mels, T
+        out = []
+        for (_, oc, s) in self.blocks:
+            H, W = (H - 1) // s + 1, (W - 1) // s + 1
+            out.append((oc, H, W))
+        return out
+
+    def forward(self, feats, capture=False):
+        feats = np.ascontiguousarray(feats, dtype=np.float32)
+        T = feats.shape[1]
+        emb = np.zeros(self.net.emb_dim, dtype=np.float32)
+        caps = ResNetCaps()
+        bufs = {}
+        if capture:
+            bufs["stem"] = np.zeros((self.net.stem_oc, self.net.n_mels, T), dtype=np.float32)
+            caps.stem = bufs["stem"].ctypes.data_as(_fp)
+            for i, shp in enumerate(self.block_shapes(T)):
+                bufs[f"block{i}"] = np.zeros(shp, dtype=np.float32)
+                caps.block[i] = bufs[f"block{i}"].ctypes.data_as(_fp)
+            oc, H, W = self.block_shapes(T)[-1]
+            bufs["pooled"] = np.zeros(2 * oc * H, dtype=np.float32)
+            caps.pooled = bufs["pooled"].ctypes.data_as(_fp)
+            bufs["pre_norm"] = np.zeros(self.net.emb_dim, dtype=np.float32)
+            caps.pre_norm = bufs["pre_norm"].ctypes.data_as(_fp)
+        rc = lib().orc_resnet34_forward(C.byref(self.net), feats, T, emb, C.byref(caps))
+        assert rc == 0
+        return (emb, bufs) if capture else emb
+
+    def embed_batch(self, pcm, n_threads=1, cfg=None):
+        cfg = cfg or fbank_cfg(n_mels=self.net.n_mels)
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        B, n = pcm.shape
+        out = np.zeros((B, self.net.emb_dim), dtype=np.float32)
+        rc = lib().orc_embed_batch(C.byref(self.net), C.byref(cfg), pcm, B, n, n_threads, out)
+        assert rc == 0
+        return out

@@ -1,0 +1,185 @@
+"""Seeded synthetic clips and random-init speaker-encoder models.
+
+Clip (16 kHz mono f32): x[n] = sum_{h=1..5} 0.1 sin(2 pi h f0 n / 16000) + N(0, 0.01)
+with f0 ~ U(100, 250) Hz; phase 0, noise standard deviation 0.01.  The stream
+seeds are derived from (seed, clip index) with `rng.derive_seed`.
+
+Models follow the shapes of the published encoders with random weights:
+conv weights N(0, sqrt(2 / fan_in)) with fan_in = IC*KH*KW; a BatchNorm after
+every conv with mean N(0, 0.1), var U(0.5, 1.5), gamma 1, beta 0, eps 1e-5,
+folded into the conv (w' = w * g/sqrt(var+eps), b' = beta - mean*g/sqrt(var+eps))
+in f32 before the weight is stored as f16 (or Q8_0).  Biases stay f32.
+
+The GGUF layout mirrors the reference converter's WeSpeaker ResNet34 schema
+(docs/conversion.md "WeSpeaker ResNet34 block manifest"): conv weights with
+ggml ne = [KW, KH, IC, OC], a per-block manifest in `voicedetect.resnet.*`.
+"""
+import numpy as np
+
+from . import gguf as G
+from .rng import derive_seed, normal, uniform
+
+SR = 16000
+BN_EPS = 1e-5
+
+
+def clip(seed, n_samples, index=0):
+    """One synthetic clip as float32[n_samples]."""
+    s = derive_seed(seed, 0xC11B, index)
+    f0 = 100.0 + 150.0 * uniform(derive_seed(s, 1), 1)[0]
+    n = np.arange(n_samples, dtype=np.float64)
+    x = np.zeros(n_samples, dtype=np.float64)
+    for h in range(1, 6):
+        x += 0.1 * np.sin(2.0 * np.pi * h * f0 * n / SR)
+    x += 0.01 * normal(derive_seed(s, 2), n_samples)
+    return x.astype(np.float32)
+
+
+def clips(seed, batch, n_samples):
+    """float32[batch, n_samples]; clip b uses stream (seed, b)."""
+    return np.stack([clip(seed, n_samples, b) for b in range(batch)])
+
+
+def seconds_to_samples(sec):
+    return int(round(sec * SR))
+
+
+def frames_for(n_samples, win=400, hop=160):
+    """Kaldi snip_edges frame count (src/fbank.cpp:130)."""
+    return 0 if n_samples < win else 1 + (n_samples - win) // hop
+
+
+class _WeightStream:
+    """Hands out per-tensor seeds in creation order so a model is a pure function of its seed."""
+
+    def __init__(self, seed):
+        self.seed = seed
+        self.k = 0
+
+    def next(self):
+        self.k += 1
+        return derive_seed(self.seed, 0x5EED, self.k)
+
+
+def conv_bn_folded(ws, oc, ic, kh, kw, bn=True):
+    """Random conv (+ folded BN) -> (w f32 [OC,IC,KH,KW], b f32 [OC])."""
+    fan_in = ic * kh * kw
+    w = normal(ws.next(), oc * ic * kh * kw).reshape(oc, ic, kh, kw) * np.sqrt(2.0 / fan_in)
+    w = w.astype(np.float32)
+    if not bn:
+        return w, np.zeros(oc, dtype=np.float32)
+    mean = (0.1 * normal(ws.next(), oc)).astype(np.float32)
+    var = (0.5 + uniform(ws.next(), oc)).astype(np.float32)
+    scale = (np.float32(1.0) / np.sqrt(var + np.float32(BN_EPS))).astype(np.float32)
+    return (w * scale[:, None, None, None]).astype(np.float32), (-mean * scale).astype(np.float32)
+
+
+def _fbank_kv(n_mels=80):
+    return {
+        "voicedetect.fbank.sample_rate": 16000,
+        "voicedetect.fbank.n_mels": n_mels,
+        "voicedetect.fbank.n_fft": 512,
+        "voicedetect.fbank.win_length": 400,
+        "voicedetect.fbank.hop_length": 160,
+        "voicedetect.fbank.preemph": G.F32(0.97),
+        "voicedetect.fbank.low_freq": G.F32(20.0),
+        "voicedetect.fbank.high_freq": G.F32(0.0),
+        "voicedetect.fbank.use_energy": False,
+        "voicedetect.fbank.cmn": True,
+        "voicedetect.fbank.window": "povey",
+    }
+
+
+def resnet34_spec(channels=(32, 64, 128, 256), blocks=(3, 4, 6, 3), emb_dim=256, n_mels=80):
+    """Block list of WeSpeaker ResNet34: (in_c, out_c, stride, has_down)."""
+    out = []
+    in_c = channels[0]
+    for si, (c, nb) in enumerate(zip(channels, blocks)):
+        for bi in range(nb):
+            stride = 2 if (si > 0 and bi == 0) else 1
+            down = stride != 1 or in_c != c
+            out.append((in_c, c, stride, down))
+            in_c = c
+    return out
+
+
+def make_resnet34(seed, wtype=G.GGML_F16, channels=(32, 64, 128, 256), blocks=(3, 4, 6, 3),
+                  emb_dim=256, n_mels=80, mean_vec=False):
+    """Random-init WeSpeaker ResNet34 -> (kv dict, tensor list) ready for gguf.write_gguf."""
+    ws = _WeightStream(seed)
+    tensors = []
+
+    def add(name, w, b):
+        tensors.append((name + ".weight", wtype, list(w.shape), w))
+        tensors.append((name + ".bias", G.GGML_F32, [w.shape[0]], b))
+
+    c0 = channels[0]
+    w, b = conv_bn_folded(ws, c0, 1, 3, 3)
+    add("front.conv1", w, b)
+    m = {k: [] for k in ("conv1_weight", "conv1_bias", "conv2_weight", "conv2_bias",
+                         "down_weight", "down_bias", "stride")}
+    spec = resnet34_spec(channels, blocks, emb_dim, n_mels)
+    li, bi = 1, 0
+    counts = list(blocks)
+    for (ic, oc, stride, down) in spec:
+        pre = f"front.layer{li}.{bi}"
+        w, b = conv_bn_folded(ws, oc, ic, 3, 3)
+        add(pre + ".conv1", w, b)
+        w, b = conv_bn_folded(ws, oc, oc, 3, 3)
+        add(pre + ".conv2", w, b)
+        m["conv1_weight"].append(pre + ".conv1.weight")
+        m["conv1_bias"].append(pre + ".conv1.bias")
+        m["conv2_weight"].append(pre + ".conv2.weight")
+        m["conv2_bias"].append(pre + ".conv2.bias")
+        if down:
+            w, b = conv_bn_folded(ws, oc, ic, 1, 1)
+            add(pre + ".shortcut.0", w, b)
+            m["down_weight"].append(pre + ".shortcut.0.weight")
+            m["down_bias"].append(pre + ".shortcut.0.bias")
+        else:
+            m["down_weight"].append("")
+            m["down_bias"].append("")
+        m["stride"].append(G.I32(stride))
+        bi += 1
+        if bi == counts[li - 1]:
+            li, bi = li + 1, 0
+    h_out = n_mels
+    for s in range(len(channels) - 1):
+        h_out = (h_out - 1) // 2 + 1
+    pooled = 2 * channels[-1] * h_out
+    seg_w = (normal(ws.next(), emb_dim * pooled).reshape(emb_dim, pooled) * np.sqrt(2.0 / pooled)).astype(np.float32)
+    seg_b = (0.01 * normal(ws.next(), emb_dim)).astype(np.float32)
+    tensors.append(("seg_1.weight", wtype, [emb_dim, pooled], seg_w))
+    tensors.append(("seg_1.bias", G.GGML_F32, [emb_dim], seg_b))
+    kv = {
+        "general.architecture": "voicedetect",
+        "general.name": f"synthetic-wespeaker-resnet34-seed{seed}",
+        "voicedetect.arch": "wespeaker_resnet34",
+        "voicedetect.embedding_dim": emb_dim,
+        "voicedetect.l2_normalize": True,
+    }
+    kv.update(_fbank_kv(n_mels))
+    kv.update({
+        "voicedetect.resnet.stem_weight": "front.conv1.weight",
+        "voicedetect.resnet.stem_bias": "front.conv1.bias",
+        "voicedetect.resnet.conv1_weight": m["conv1_weight"],
+        "voicedetect.resnet.conv1_bias": m["conv1_bias"],
+        "voicedetect.resnet.conv2_weight": m["conv2_weight"],
+        "voicedetect.resnet.conv2_bias": m["conv2_bias"],
+        "voicedetect.resnet.down_weight": m["down_weight"],
+        "voicedetect.resnet.down_bias": m["down_bias"],
+        "voicedetect.resnet.stride": m["stride"],
+        "voicedetect.resnet.seg_weight": "seg_1.weight",
+        "voicedetect.resnet.seg_bias": "seg_1.bias",
+        "voicedetect.resnet.mean_vec": "mean_vec" if mean_vec else "",
+        "voicedetect.resnet.var_eps": G.F32(1e-8),
+    })
+    if mean_vec:
+        tensors.append(("mean_vec", G.GGML_F32, [emb_dim], (0.05 * normal(ws.next(), emb_dim)).astype(np.float32)))
+    return kv, tensors
+
+
+def write_resnet34(path, seed, **kw):
+    kv, tensors = make_resnet34(seed, **kw)
+    G.write_gguf(path, kv, tensors)
+    return path
