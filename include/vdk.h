@@ -1,0 +1,113 @@
+/*
+ * vdk.h - low-level C ABI of the MI355X (gfx950) speaker-encoder kernels.
+ *
+ * Every entry point takes device pointers, plain sizes and a HIP stream
+ * (`void* stream`, NULL = the default stream), enqueues its kernels and
+ * returns 0, or a nonzero code with a message from vdk_last_error().  Nothing
+ * here allocates device memory except vdk_malloc.  Shapes are checked on the
+ * host before any launch.
+ *
+ * Layouts: PCM [B][n] f32; FBank features feat-major [B][n_mels][T] f32 (the
+ * reference's [n_mels, T] per clip); activations NHWC f16 [B][H=freq][W=time][C];
+ * conv weights [OC][KH][KW][IC] f16 (the reference's [OC][IC][KH][KW] with the
+ * channel axis moved innermost); biases f32.
+ *
+ * These replace the reference's operator seam: the conv2d_auto router and the
+ * ggml custom ops it dispatches to (src/backend.cpp:665-793), the host FBank
+ * (src/fbank.cpp:121-205) and the ggml pooling / FC / host L2 tail of
+ * src/encoder_resnet.cpp:140-183.
+ */
+#ifndef VDK_H
+#define VDK_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- device memory helpers (for callers without another HIP runtime) ---- */
+int         vdk_device_count(void);
+int         vdk_set_device(int device);
+void*       vdk_malloc(size_t bytes);          /* NULL on failure */
+int         vdk_free(void* p);
+int         vdk_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int         vdk_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int         vdk_memset(void* dst, int value, size_t bytes);
+int         vdk_synchronize(void);
+const char* vdk_last_error(void);             /* thread-local; "" if none */
+
+/* ---- host utilities (no GPU needed) ---- */
+/* Decode a WAV, average channels, resample linearly to 16 kHz
+ * (src/audio_io.cpp:25-38).  Returns the sample count (copies at most cap
+ * samples into out; out may be NULL to query), or -1 on failure. */
+long vdk_load_wav_16k(const char* path, float* out, long cap);
+/* Linear resampler of src/audio_io.cpp:9-23; returns the output length
+ * (copies at most cap samples). */
+long vdk_resample_linear(const float* in, long n, int in_sr, int out_sr, float* out, long cap);
+/* IEEE f32 -> f16 bit patterns, round to nearest even (weight packing). */
+void vdk_f32_to_f16(const float* in, unsigned short* out, size_t n);
+
+/* ---- FBank front end ----
+ * Replaces vd::FBank::compute (src/fbank.cpp:121-205), batched: B clips of
+ * n_samples each.  `tables` is a device block built by vdk_fbank_tables_size /
+ * vdk_fbank_tables_fill (window, FFT twiddles, packed mel filters).  Output
+ * feat-major [B][n_mels][T], T = 1 + (n_samples - win) / hop. */
+typedef struct {
+    int sample_rate, n_mels, n_fft, win_length, hop_length;
+    float preemph, low_freq, high_freq; /* high_freq <= 0 means Nyquist */
+    int cmn;
+} vdk_fbank_cfg;
+
+size_t vdk_fbank_tables_size(const vdk_fbank_cfg* cfg);
+/* Computes the tables on the host and copies them to d_tables (synchronous). */
+int    vdk_fbank_tables_fill(const vdk_fbank_cfg* cfg, void* d_tables);
+int    vdk_fbank(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pcm,
+                 int batch, int n_samples, float* d_feats, void* stream);
+
+/* ---- 2D convolution, implicit GEMM on f16 MFMA with f32 accumulation ----
+ * Replaces the blocked-island ops blocked_conv3x3 / blocked_conv1x1 with their
+ * fused bias(+ReLU) epilogue and blocked_add_relu (src/directconv.cpp:1496-1546,
+ * src/directconv.hpp:22-51), and the per-conv directconv_conv3x3 / winograd
+ * custom ops (src/directconv.cpp:1449-1458, src/winograd.cpp:638-648):
+ *   y = act(conv(x, w) + bias [+ residual])
+ * x [B][H][W][IC], w [OC][KH][KW][IC], bias [OC] (may be NULL),
+ * residual [B][Ho][Wo][OC] (may be NULL), y [B][Ho][Wo][OC], all f16 except bias.
+ * Ho = (H + 2*pad - KH)/stride + 1 (same for W).  Requires IC % 16 == 0 and
+ * OC % 32 == 0.  relu: 0 = none, 1 = max(v, 0). */
+int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC,
+                    const void* d_w, int OC, int KH, int KW, int stride, int pad,
+                    const float* d_bias, const void* d_residual, int relu,
+                    void* d_y, void* stream);
+
+/* ---- stem: single-input-channel 3x3 conv from f32 features ----
+ * Replaces the ResNet stem conv2d_auto -> directconv_conv3x3 + bias + ReLU
+ * (src/encoder_resnet.cpp:115-117).  feats [B][H][W] f32, w [OC][3][3] f32,
+ * bias [OC] f32, y [B][H][W][OC] f16 (stride 1, pad 1), OC in {16, 32, 64}. */
+int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,
+                     const float* d_w, const float* d_bias, int OC, int relu,
+                     void* d_y, void* stream);
+
+/* ---- temporal statistics pooling ----
+ * Replaces the TSTP graph of src/encoder_resnet.cpp:140-157: per (c, h) mean
+ * over time and sqrt(unbiased var + eps), flattened C-outer/H-inner:
+ * pooled[b] = [mean(c,h) ; std(c,h)], length 2*C*H.  x [B][H][W][C] f16. */
+int vdk_tstp(const void* d_x, int batch, int H, int W, int C, float eps,
+             float* d_pooled, void* stream);
+
+/* ---- embedding FC ----
+ * Replaces the seg_1 mul_mat + bias - mean_vec of src/encoder_resnet.cpp:159-169:
+ * y[b] = w x[b] + bias - mean_vec; w [out][in] f32; bias/mean_vec may be NULL. */
+int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w,
+               const float* d_bias, const float* d_mean_vec, int out_dim,
+               float* d_y, void* stream);
+
+/* ---- L2 normalisation ----
+ * Replaces the host L2 of src/encoder_resnet.cpp:177-183 (double accumulation,
+ * skipped when the norm is 0).  In place on x [B][dim]. */
+int vdk_l2norm(float* d_x, int batch, int dim, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

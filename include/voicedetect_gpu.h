@@ -1,0 +1,50 @@
+/*
+ * voicedetect_gpu.h - device-resident entry points of the MI355X library.
+ *
+ * For callers that keep PCM and embeddings in HBM (serving loops, batch
+ * pipelines).  No counterpart in the reference, whose ABI is host-only and one
+ * clip per call (reference include/voicedetect_capi.h:59-67); these add the
+ * batched device path over the same context.  Same status convention as the
+ * C ABI: 0 = success, nonzero = error with voicedetect_capi_last_error(ctx).
+ */
+#ifndef VOICEDETECT_GPU_H
+#define VOICEDETECT_GPU_H
+
+#include "voicedetect_capi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Enqueue the whole path for `batch` clips of n_samples 16 kHz f32 PCM at
+ * d_pcm (device, clip-major) writing batch x dim f32 embeddings to d_out
+ * (device) on the context's stream.  Returns once enqueued. */
+int voicedetect_gpu_embed_batch_async(voicedetect_ctx* ctx, const float* d_pcm,
+                                      int batch, int n_samples, float* d_out);
+
+/* Wait for the context's stream. */
+int voicedetect_gpu_synchronize(voicedetect_ctx* ctx);
+
+/* The context's hipStream_t (initialises the device on first use); NULL on error. */
+void* voicedetect_gpu_stream(voicedetect_ctx* ctx);
+
+/* Host-buffer embed that also returns intermediates (any output may be NULL):
+ * feats [batch][n_mels][T], pooled [batch][pooled_dim], pre_norm / out [batch][dim].
+ * *pooled_dim receives the pooled width when not NULL. */
+int voicedetect_gpu_embed_capture(voicedetect_ctx* ctx, const float* pcm, int batch,
+                                  int n_samples, float* feats, float* pooled,
+                                  int* pooled_dim, float* pre_norm, float* out);
+
+/* Per-launch timing with HIP events recorded on the context's stream. */
+int voicedetect_gpu_set_profiling(voicedetect_ctx* ctx, int on);
+/* Waits, then returns the number of launch records collected since the last
+ * read (or -1 on error); records are read with voicedetect_gpu_profile_get. */
+int voicedetect_gpu_profile_collect(voicedetect_ctx* ctx);
+int voicedetect_gpu_profile_get(voicedetect_ctx* ctx, int i, char* name, int name_cap,
+                                double* ms, double* flops, double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

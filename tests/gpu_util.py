@@ -1,0 +1,63 @@
+"""Helpers shared by the GPU parity tests: run single vdk kernels through the
+C ABI on host arrays, and the parity metrics (the reference's atol + rtol*|ref|
+form of tests/parity.hpp:44-70, cosine)."""
+import ctypes as C
+
+import numpy as np
+
+from vdamd import lib
+
+
+def device_ok():
+    try:
+        return lib.lib().vdk_device_count() > 0
+    except Exception:
+        return False
+
+
+def announce(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def conv_gpu(x_nhwc, w_oihw, bias=None, residual=None, stride=1, pad=1, relu=False):
+    """x [B,H,W,IC] f16, w [OC,IC,KH,KW] (f16 values) -> y [B,Ho,Wo,OC] f16 via vdk_conv2d_nhwc."""
+    L = lib.lib()
+    x = np.ascontiguousarray(x_nhwc, dtype=np.float16)
+    B, H, W, IC = x.shape
+    OC, IC2, KH, KW = w_oihw.shape
+    assert IC == IC2
+    Ho, Wo = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    wp = np.ascontiguousarray(np.asarray(w_oihw, dtype=np.float16).transpose(0, 2, 3, 1))
+    dx = lib.DeviceBuffer.from_array(x)
+    dw = lib.DeviceBuffer.from_array(wp)
+    db = lib.DeviceBuffer.from_array(np.asarray(bias, dtype=np.float32)) if bias is not None else None
+    dr = None
+    if residual is not None:
+        r = np.ascontiguousarray(residual, dtype=np.float16)
+        assert r.shape == (B, Ho, Wo, OC)
+        dr = lib.DeviceBuffer.from_array(r)
+    dy = lib.DeviceBuffer(B * Ho * Wo * OC * 2)
+    rc = L.vdk_conv2d_nhwc(dx.ptr, B, H, W, IC, dw.ptr, OC, KH, KW, stride, pad,
+                           db.ptr if db else None, dr.ptr if dr else None, int(relu), dy.ptr, None)
+    lib.check(rc)
+    lib.check(L.vdk_synchronize())
+    return dy.to_array(np.float16, (B, Ho, Wo, OC))
+
+
+def close_report(got, ref, rtol, atol_rel_rms):
+    """Elementwise |got-ref| <= atol + rtol*|ref| with atol = atol_rel_rms * rms(ref).
+    Returns (ok, max_excess_ratio, rel_l2)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    rms = np.sqrt(np.mean(ref ** 2)) if ref.size else 0.0
+    tol = atol_rel_rms * rms + rtol * np.abs(ref)
+    d = np.abs(got - ref)
+    ratio = float(np.max(d / np.maximum(tol, 1e-30))) if ref.size else 0.0
+    rel_l2 = float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+    return ratio <= 1.0, ratio, rel_l2
+
+
+def cosine(a, b):
+    a = np.asarray(a, dtype=np.float64).reshape(-1)
+    b = np.asarray(b, dtype=np.float64).reshape(-1)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))

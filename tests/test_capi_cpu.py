@@ -1,0 +1,171 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+headers declare, and follows the reference's error/ownership contract
+(src/voicedetect_capi.cpp:61-178) on the paths that fail before any device work.
+Also pins the host utilities: WAV decode against the reference's dr_wav-based
+loader output (golden PCM), the resampler and f16 packing against closed forms.
+"""
+import ctypes as C
+import os
+import re
+import tempfile
+
+import numpy as np
+import pytest
+
+from vdamd import gguf, lib, synth
+
+
+def _declared(header):
+    src = open(os.path.join(lib.INCLUDE_DIR, header)).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return set(re.findall(r"\b((?:voicedetect_capi|voicedetect_gpu|vdk)_\w+)\s*\(", src))
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib.lib()
+    declared = set()
+    for h in ("voicedetect_capi.h", "voicedetect_gpu.h", "vdk.h"):
+        declared |= _declared(h)
+    assert len(declared) >= 35
+    for name in sorted(declared):
+        assert hasattr(L, name), name
+    # the binding covers exactly the declared surface
+    assert declared == set(lib.exported_symbols())
+    frozen = {"voicedetect_capi_abi_version", "voicedetect_capi_load", "voicedetect_capi_free",
+              "voicedetect_capi_last_error", "voicedetect_capi_free_string", "voicedetect_capi_free_vec",
+              "voicedetect_capi_embed_path", "voicedetect_capi_embed_pcm", "voicedetect_capi_verify_paths",
+              "voicedetect_capi_analyze_path_json"}
+    assert frozen <= declared
+
+
+def test_abi_version_and_null_safety():
+    L = lib.lib()
+    assert L.voicedetect_capi_abi_version() == 1
+    assert L.voicedetect_capi_load(None) is None
+    assert L.voicedetect_capi_load(b"/nonexistent/model.gguf") is None
+    assert L.voicedetect_capi_last_error(None) == b""
+    L.voicedetect_capi_free(None)
+    L.voicedetect_capi_free_vec(None)
+    L.voicedetect_capi_free_string(None)
+    vec = C.POINTER(C.c_float)()
+    dim = C.c_int(7)
+    assert L.voicedetect_capi_embed_pcm(None, None, 0, 16000, C.byref(vec), C.byref(dim)) == 1
+    assert not vec and dim.value == 0
+    assert L.voicedetect_capi_verify_paths(None, b"a", b"b", 0.25, None, None) == 1
+    assert L.voicedetect_capi_analyze_path_json(None, b"a") is None
+
+
+def test_load_rejects_bad_files():
+    L = lib.lib()
+    with tempfile.TemporaryDirectory() as tmp:
+        p = os.path.join(tmp, "junk.gguf")
+        open(p, "wb").write(b"not a gguf at all")
+        assert L.voicedetect_capi_load(p.encode()) is None
+        # valid container without voicedetect.embedding_dim (src/model_loader.cpp:212-214)
+        q = os.path.join(tmp, "nodim.gguf")
+        gguf.write_gguf(q, {"voicedetect.arch": "wespeaker_resnet34"}, [])
+        assert L.voicedetect_capi_load(q.encode()) is None
+
+
+@pytest.fixture(scope="module")
+def tiny_model():
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "tiny.gguf")
+    synth.write_resnet34(path, seed=5, channels=(32, 32, 64, 64), blocks=(1, 1, 1, 1), emb_dim=64)
+    return path
+
+
+def test_error_contract_without_device_work(tiny_model):
+    ctx = lib.Context(tiny_model)
+    L = ctx.L
+    assert ctx.dim == 64
+    assert ctx.last_error() == ""
+    vec = C.POINTER(C.c_float)()
+    dim = C.c_int(5)
+    # NULL pcm / negative length: "invalid pcm buffer", outputs reset
+    assert L.voicedetect_capi_embed_pcm(ctx.ctx, None, 10, 16000, C.byref(vec), C.byref(dim)) == 1
+    assert ctx.last_error() == "invalid pcm buffer" and not vec and dim.value == 0
+    x = np.zeros(100, dtype=np.float32)
+    assert L.voicedetect_capi_embed_pcm(ctx.ctx, x.ctypes.data, -1, 16000, C.byref(vec), C.byref(dim)) == 1
+    # fewer samples than one window (src/fbank.cpp:126-127, src/model.cpp:27-28)
+    assert L.voicedetect_capi_embed_pcm(ctx.ctx, x.ctypes.data, 100, 16000, C.byref(vec), C.byref(dim)) == 1
+    assert "FBank produced no frames" in ctx.last_error()
+    # verify with NULL path / unreadable file
+    d, v = C.c_float(-7.0), C.c_int(-7)
+    assert L.voicedetect_capi_verify_paths(ctx.ctx, None, b"x", 0.25, C.byref(d), C.byref(v)) == 1
+    assert ctx.last_error() == "clip path is NULL" and d.value == -7.0 and v.value == -7
+    assert L.voicedetect_capi_verify_paths(ctx.ctx, b"/nonexistent.wav", b"/n2.wav", 0.25, C.byref(d),
+                                           C.byref(v)) == 1
+    assert "failed to load audio" in ctx.last_error() and d.value == -7.0
+    assert L.voicedetect_capi_embed_path(ctx.ctx, None, C.byref(vec), C.byref(dim)) == 1
+    assert ctx.last_error() == "wav_path is NULL"
+    # analyze heads are outside this library: NULL + the reference's message
+    assert L.voicedetect_capi_analyze_path_json(ctx.ctx, b"x.wav") is None
+    assert ctx.last_error() == "voicedetect: this model has no age/gender/emotion analyze heads"
+    if L.vdk_device_count() == 0:
+        y = np.zeros(16000, dtype=np.float32)
+        assert L.voicedetect_capi_embed_pcm(ctx.ctx, y.ctypes.data, 16000, 16000, C.byref(vec), C.byref(dim)) == 1
+        assert "no HIP device" in ctx.last_error()
+    ctx.close()
+
+
+def test_wav_reader_matches_reference_decoder(golden_dir):
+    z = np.load(os.path.join(golden_dir, "fbank_golden.npz"))
+    L = lib.lib()
+    for name in ("clip_a", "clip_b_same", "clip_c_diff"):
+        path = os.path.join(golden_dir, name + ".wav").encode()
+        n = L.vdk_load_wav_16k(path, None, 0)
+        assert n == 48000
+        out = np.zeros(n, dtype=np.float32)
+        assert L.vdk_load_wav_16k(path, out.ctypes.data, n) == n
+        assert np.array_equal(out, z[f"wav_{name}/pcm"])   # bit-exact vs dr_wav
+    assert L.vdk_load_wav_16k(b"/nonexistent.wav", None, 0) == -1
+
+
+def test_wav_formats_and_downmix():
+    L = lib.lib()
+    with tempfile.TemporaryDirectory() as tmp:
+        import wave
+        p = os.path.join(tmp, "st.wav")
+        left = (np.arange(320) * 50 - 8000).astype(np.int16)
+        right = (-left).astype(np.int16)
+        inter = np.stack([left, right], axis=1).reshape(-1)
+        with wave.open(p, "wb") as w:
+            w.setnchannels(2)
+            w.setsampwidth(2)
+            w.setframerate(16000)
+            w.writeframes(inter.tobytes())
+        out = np.zeros(320, dtype=np.float32)
+        assert L.vdk_load_wav_16k(p.encode(), out.ctypes.data, 320) == 320
+        assert np.all(out == 0.0)                 # L + R cancel exactly
+        p8 = os.path.join(tmp, "k.wav")
+        with wave.open(p8, "wb") as w:
+            w.setnchannels(1)
+            w.setsampwidth(2)
+            w.setframerate(8000)
+            w.writeframes(left.tobytes())
+        n = L.vdk_load_wav_16k(p8.encode(), None, 0)
+        assert n == 640                           # 8 kHz -> 16 kHz doubles the length
+
+
+def test_resampler_closed_form():
+    L = lib.lib()
+    x = np.arange(10, dtype=np.float32)
+    out = np.zeros(20, dtype=np.float32)
+    assert L.vdk_resample_linear(x.ctypes.data, 10, 8000, 16000, out.ctypes.data, 20) == 20
+    # linear interpolation of a ramp, last point holds the final sample
+    assert np.allclose(out[:19], np.arange(19) / 2.0) and out[19] == 9.0
+    same = np.zeros(10, dtype=np.float32)
+    assert L.vdk_resample_linear(x.ctypes.data, 10, 16000, 16000, same.ctypes.data, 10) == 10
+    assert np.array_equal(same, x)
+
+
+def test_f16_packing_matches_ieee_round_to_nearest_even():
+    L = lib.lib()
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * s for s in (1e-6, 1e-3, 1.0, 1e3, 3e4)])
+    x = np.concatenate([x, np.array([0.0, -0.0, 65504.0, 65520.0, 1e6, -1e6, 5.96e-8, 2.98e-8, 6.1e-5,
+                                     np.inf, -np.inf], dtype=np.float32)])
+    out = np.zeros(len(x), dtype=np.uint16)
+    L.vdk_f32_to_f16(x.ctypes.data, out.ctypes.data, len(x))
+    assert np.array_equal(out, x.astype(np.float16).view(np.uint16))

@@ -1,0 +1,222 @@
+"""Per-kernel parity of the HIP path against the oracle, through the vdk C ABI.
+
+Gates: FBank within 1e-4 absolute of the oracle (and of the reference's golden
+vectors); every conv layer shape of ResNet34 at batch 64 (the real launch
+shape) within |d| <= 2e-3*|ref| + 2e-3*rms(ref) of the oracle's f32 conv fed
+the same f16 input and weights, checked on the first, a middle and the last
+clip of the batch; stats pooling, FC and L2 against the oracle at 1e-5..1e-4.
+"""
+import os
+import zlib
+
+import numpy as np
+import pytest
+
+import pyoracle as O
+from gpu_util import announce, close_report, conv_gpu, device_ok
+from test_oracle_fbank import _cases, _cfg, golden_pcm
+from vdamd import lib, synth
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
+
+CONV_RTOL = 2e-3
+CONV_ATOL_RMS = 2e-3
+
+
+def fbank_gpu(pcm_batch, cfg):
+    L = lib.lib()
+    pcm = np.ascontiguousarray(pcm_batch, dtype=np.float32)
+    B, n = pcm.shape
+    T = 1 + (n - cfg.win_length) // cfg.hop_length
+    size = L.vdk_fbank_tables_size(cfg)
+    assert size > 0
+    tab = lib.DeviceBuffer(size)
+    lib.check(L.vdk_fbank_tables_fill(cfg, tab.ptr))
+    dp = lib.DeviceBuffer.from_array(pcm)
+    df = lib.DeviceBuffer(B * cfg.n_mels * T * 4)
+    lib.check(L.vdk_fbank(cfg, tab.ptr, dp.ptr, B, n, df.ptr, None))
+    lib.check(L.vdk_synchronize())
+    return df.to_array(np.float32, (B, cfg.n_mels, T))
+
+
+def test_fbank_matches_goldens_and_oracle(golden_dir):
+    z = np.load(os.path.join(golden_dir, "fbank_golden.npz"))
+    for name in _cases(z):
+        announce(f"fbank golden {name}")
+        ocfg = _cfg(z, name)
+        cfg = lib.fbank_cfg(n_mels=ocfg.n_mels, n_fft=ocfg.n_fft, win=ocfg.win_length, hop=ocfg.hop_length,
+                            preemph=ocfg.preemph, low=ocfg.low_freq, high=ocfg.high_freq, cmn=bool(ocfg.cmn))
+        pcm = golden_pcm(z, name)
+        got = fbank_gpu(pcm[None], cfg)[0]
+        ref = z[name + "/fbank"]
+        assert got.shape == ref.shape, name
+        assert np.abs(got - ref).max() <= 1e-4, (name, np.abs(got - ref).max())
+        assert np.abs(got - O.fbank(pcm, ocfg)).max() <= 1e-4
+
+
+@pytest.mark.parametrize("seconds,batch", [(3.0, 64), (4.0, 8), (10.0, 4), (20.0, 2)])
+def test_fbank_batched_config_lengths(seconds, batch):
+    n = synth.seconds_to_samples(seconds)
+    announce(f"fbank batch={batch} n={n}")
+    pcm = synth.clips(100 + int(seconds), batch, n)
+    got = fbank_gpu(pcm, lib.fbank_cfg())
+    for b in sorted({0, batch // 2, batch - 1}):
+        ref = O.fbank(pcm[b])
+        assert np.abs(got[b] - ref).max() <= 1e-4
+    # CMN: every mel bin has zero mean over time
+    assert np.abs(got.mean(axis=2)).max() < 1e-5
+
+
+def test_fbank_rejects_short_input():
+    L = lib.lib()
+    cfg = lib.fbank_cfg()
+    tab = lib.DeviceBuffer(L.vdk_fbank_tables_size(cfg))
+    d = lib.DeviceBuffer(1024)
+    assert L.vdk_fbank(cfg, tab.ptr, d.ptr, 1, 399, d.ptr, None) != 0
+    assert "no frames" in L.vdk_last_error().decode()
+
+
+def _rand_act(rng, shape, scale=1.0):
+    return np.maximum(rng.standard_normal(shape, dtype=np.float32) * scale, 0).astype(np.float16)
+
+
+def _check_conv(x, w, b, res, stride, pad, relu, clips, tag):
+    announce(f"conv {tag} x={x.shape} w={w.shape} s={stride} p={pad} res={res is not None}")
+    got = conv_gpu(x, w, b, res, stride, pad, relu)
+    wf = w.astype(np.float32)
+    for c in clips:
+        r = None if res is None else res[c].astype(np.float32).transpose(2, 0, 1)
+        ref = O.conv2d(x[c].astype(np.float32).transpose(2, 0, 1), wf, stride, pad, bias=b, residual=r, relu=relu)
+        ok, ratio, rel = close_report(got[c].astype(np.float32).transpose(2, 0, 1), ref, CONV_RTOL, CONV_ATOL_RMS)
+        assert ok, f"{tag} clip {c}: max tol ratio {ratio:.3f}, rel-L2 {rel:.2e}"
+        assert rel <= 2e-3, f"{tag} clip {c}: rel-L2 {rel:.2e}"
+    return got
+
+
+# every distinct conv of WeSpeaker ResNet34 at B=64, 3 s clips (H=80 mel, W=298 frames)
+RESNET34_LAYERS = [
+    # (tag, IC, OC, H, W, K, stride, pad, residual)
+    ("s1_conv", 32, 32, 80, 298, 3, 1, 1, True),
+    ("s2_conv1", 32, 64, 80, 298, 3, 2, 1, False),
+    ("s2_down", 32, 64, 80, 298, 1, 2, 0, False),
+    ("s2_conv", 64, 64, 40, 149, 3, 1, 1, True),
+    ("s3_conv1", 64, 128, 40, 149, 3, 2, 1, False),
+    ("s3_down", 64, 128, 40, 149, 1, 2, 0, False),
+    ("s3_conv", 128, 128, 20, 75, 3, 1, 1, True),
+    ("s4_conv1", 128, 256, 20, 75, 3, 2, 1, False),
+    ("s4_down", 128, 256, 20, 75, 1, 2, 0, False),
+    ("s4_conv", 256, 256, 10, 38, 3, 1, 1, True),
+]
+
+
+@pytest.mark.parametrize("layer", RESNET34_LAYERS, ids=[l[0] for l in RESNET34_LAYERS])
+def test_conv_resnet34_layer_shapes_batch64(layer):
+    tag, IC, OC, H, W, K, s, p, with_res = layer
+    rng = np.random.default_rng(zlib.crc32(tag.encode()))
+    B = 64
+    x = _rand_act(rng, (B, H, W, IC))
+    w = (rng.standard_normal((OC, IC, K, K), dtype=np.float32) * np.sqrt(2.0 / (IC * K * K))).astype(np.float16)
+    b = (rng.standard_normal(OC, dtype=np.float32) * 0.1).astype(np.float32)
+    Ho, Wo = (H + 2 * p - K) // s + 1, (W + 2 * p - K) // s + 1
+    res = _rand_act(rng, (B, Ho, Wo, OC)) if with_res else None
+    _check_conv(x, w, b, res, s, p, relu=True, clips=(0, 37, 63), tag=tag)
+
+
+@pytest.mark.parametrize("case", [
+    # (B, H, W, IC, OC, K, stride, pad, relu, bias, res)
+    (1, 5, 7, 16, 16 * 2, 3, 1, 1, False, False, False),   # IC=16 chunking, tiny map
+    (3, 11, 20, 32, 64, 3, 1, 1, True, True, False),       # test_blocked.cpp shapes
+    (2, 11, 20, 64, 128, 3, 2, 1, True, True, False),
+    (2, 9, 15, 32, 64, 1, 2, 0, False, False, False),
+    (2, 9, 13, 48, 96, 3, 1, 0, False, True, True),        # valid conv, OC=96, IC=48
+    (1, 1, 1, 32, 32, 3, 1, 1, True, True, True),          # single pixel
+    (5, 3, 300, 64, 64, 3, 1, 1, True, True, True),        # long time axis
+])
+def test_conv_edge_shapes(case):
+    B, H, W, IC, OC, K, s, p, relu, with_b, with_res = case
+    rng = np.random.default_rng(B * 1000 + H * 10 + W)
+    x = (rng.standard_normal((B, H, W, IC), dtype=np.float32)).astype(np.float16)
+    w = rng.uniform(-1, 1, (OC, IC, K, K)).astype(np.float16)
+    b = rng.uniform(-1, 1, OC).astype(np.float32) if with_b else None
+    Ho, Wo = (H + 2 * p - K) // s + 1, (W + 2 * p - K) // s + 1
+    res = rng.standard_normal((B, Ho, Wo, OC)).astype(np.float16) if with_res else None
+    _check_conv(x, w, b, res, s, p, relu, clips=range(B), tag=f"edge{case}")
+
+
+def test_conv_invariants_delta_and_zero():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((2, 6, 70, 32)).astype(np.float16)
+    w = np.zeros((32, 32, 3, 3), dtype=np.float16)
+    for c in range(32):
+        w[c, c, 1, 1] = 1.0                        # identity kernel
+    y = conv_gpu(x, w, None, None, 1, 1, False)
+    assert np.array_equal(y, x)                    # exact: one product per output
+    b = rng.uniform(-1, 1, 32).astype(np.float32)
+    y0 = conv_gpu(x, np.zeros_like(w), b, None, 1, 1, False)
+    assert np.array_equal(y0, np.broadcast_to(b.astype(np.float16), y0.shape))
+
+
+def test_conv_rejects_bad_shapes():
+    L = lib.lib()
+    d = lib.DeviceBuffer(1 << 16)
+    assert L.vdk_conv2d_nhwc(d.ptr, 1, 4, 4, 24, d.ptr, 32, 3, 3, 1, 1, None, None, 0, d.ptr, None) != 0
+    assert "IC" in L.vdk_last_error().decode()
+    assert L.vdk_conv2d_nhwc(d.ptr, 1, 4, 4, 32, d.ptr, 48, 3, 3, 1, 1, None, None, 0, d.ptr, None) != 0
+    assert L.vdk_conv2d_nhwc(None, 1, 4, 4, 32, d.ptr, 32, 3, 3, 1, 1, None, None, 0, d.ptr, None) != 0
+    assert L.vdk_conv2d_nhwc(d.ptr, 1, 1, 1, 32, d.ptr, 32, 3, 3, 1, 0, None, None, 0, d.ptr, None) != 0
+
+
+def test_stem_conv_matches_oracle():
+    L = lib.lib()
+    rng = np.random.default_rng(3)
+    B, H, W, OC = 64, 80, 298, 32
+    announce(f"stem B={B} H={H} W={W}")
+    feats = rng.standard_normal((B, H, W)).astype(np.float32) * 3
+    w = rng.standard_normal((OC, 1, 3, 3)).astype(np.float16).astype(np.float32)
+    b = rng.standard_normal(OC).astype(np.float32) * 0.1
+    df = lib.DeviceBuffer.from_array(feats)
+    dw = lib.DeviceBuffer.from_array(w.reshape(OC, 9))
+    db = lib.DeviceBuffer.from_array(b)
+    dy = lib.DeviceBuffer(B * H * W * OC * 2)
+    lib.check(L.vdk_stem_conv3x3(df.ptr, B, H, W, dw.ptr, db.ptr, OC, 1, dy.ptr, None))
+    lib.check(L.vdk_synchronize())
+    y = dy.to_array(np.float16, (B, H, W, OC))
+    for c in (0, 31, 63):
+        ref = O.conv2d(feats[c][None], w, 1, 1, bias=b, relu=True)
+        ok, ratio, rel = close_report(y[c].astype(np.float32).transpose(2, 0, 1), ref, CONV_RTOL, CONV_ATOL_RMS)
+        assert ok, (ratio, rel)
+
+
+def test_tstp_linear_l2_match_oracle():
+    L = lib.lib()
+    rng = np.random.default_rng(4)
+    B, H, W, C, E = 64, 10, 38, 256, 256
+    announce("tstp/linear/l2")
+    x = (rng.standard_normal((B, H, W, C)) * 30).astype(np.float16)
+    dx = lib.DeviceBuffer.from_array(x)
+    P = 2 * C * H
+    dp = lib.DeviceBuffer(B * P * 4)
+    lib.check(L.vdk_tstp(dx.ptr, B, H, W, C, 1e-8, dp.ptr, None))
+    wfc = rng.standard_normal((E, P)).astype(np.float32) * np.sqrt(2.0 / P)
+    bfc = rng.standard_normal(E).astype(np.float32) * 0.01
+    mv = rng.standard_normal(E).astype(np.float32) * 0.05
+    dw, db, dm = (lib.DeviceBuffer.from_array(a) for a in (wfc, bfc, mv))
+    dy = lib.DeviceBuffer(B * E * 4)
+    lib.check(L.vdk_linear(dp.ptr, B, P, dw.ptr, db.ptr, dm.ptr, E, dy.ptr, None))
+    lib.check(L.vdk_synchronize())
+    pooled = dp.to_array(np.float32, (B, P))
+    pre = dy.to_array(np.float32, (B, E))
+    lib.check(L.vdk_l2norm(dy.ptr, B, E, None))
+    lib.check(L.vdk_synchronize())
+    emb = dy.to_array(np.float32, (B, E))
+    for c in (0, 17, 63):
+        rp = O.tstp(x[c].astype(np.float32).transpose(2, 0, 1), 1e-8)
+        assert np.allclose(pooled[c], rp, rtol=1e-5, atol=1e-5)
+        rl = O.linear(pooled[c], wfc, bfc, mv)
+        assert np.allclose(pre[c], rl, rtol=1e-4, atol=1e-4)
+        assert np.allclose(emb[c], O.l2norm(pre[c]), rtol=1e-6, atol=1e-6)
+    # zero vectors stay zero (norm 0 is skipped)
+    z = lib.DeviceBuffer.from_array(np.zeros((2, 8), np.float32))
+    lib.check(L.vdk_l2norm(z.ptr, 2, 8, None))
+    lib.check(L.vdk_synchronize())
+    assert np.array_equal(z.to_array(np.float32, (2, 8)), np.zeros((2, 8), np.float32))

@@ -1,0 +1,292 @@
+// capi.cpp - the flat C ABI (include/voicedetect_capi.h, include/voicedetect_gpu.h).
+//
+// Same contract as the reference's src/voicedetect_capi.cpp:61-178: an owning
+// opaque context holding the model and the last error; exception-free
+// boundary; malloc'd outputs; outputs reset/untouched exactly as there.
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "audio.hpp"
+#include "common.hpp"
+#include "model.hpp"
+#include "voicedetect_capi.h"
+#include "voicedetect_gpu.h"
+
+#define VOICEDETECT_CAPI_ABI_VERSION 1
+
+struct voicedetect_ctx {
+    std::unique_ptr<vdk::Model> model;
+    std::string last_error;
+    std::vector<vdk::ProfileRecord> profile;
+};
+
+namespace {
+
+float* dup_vec(const std::vector<float>& v) {
+    if (v.empty()) return nullptr;
+    float* buf = static_cast<float*>(std::malloc(v.size() * sizeof(float)));
+    if (buf) std::memcpy(buf, v.data(), v.size() * sizeof(float));
+    return buf;
+}
+
+int emit(voicedetect_ctx* ctx, const std::vector<float>& v, int dim, float** out_vec, int* out_dim) {
+    float* buf = dup_vec(v);
+    if (!buf) {
+        ctx->last_error = "out of memory";
+        return 1;
+    }
+    if (out_vec) *out_vec = buf;
+    else std::free(buf);
+    if (out_dim) *out_dim = dim;
+    ctx->last_error.clear();
+    return 0;
+}
+
+template <class F>
+int run(voicedetect_ctx* ctx, F&& body) {
+    try {
+        return body();
+    } catch (const std::exception& e) {
+        ctx->last_error = e.what();
+        return 1;
+    } catch (...) {
+        ctx->last_error = "unknown error";
+        return 1;
+    }
+}
+
+std::vector<float> embed_path(vdk::Model& m, const char* path) {
+    std::vector<float> pcm;
+    if (!vdk::load_audio_16k_mono(path, pcm))
+        throw vdk::Error(std::string("voicedetect: failed to load audio: ") + path);
+    return m.embed_pcm(pcm, 16000);
+}
+
+// src/model.cpp:65-78: dot in double, distance = 1 - (float)dot, verified = distance <= threshold.
+void verdict(const std::vector<float>& ea, const std::vector<float>& eb, float threshold, float& distance,
+             bool& verified) {
+    if (ea.size() != eb.size() || ea.empty())
+        throw vdk::Error("voicedetect: embedding dimension mismatch in verify");
+    double dot = 0.0;
+    for (size_t i = 0; i < ea.size(); ++i) dot += (double)ea[i] * (double)eb[i];
+    distance = 1.0f - (float)dot;
+    verified = distance <= threshold;
+}
+
+}  // namespace
+
+extern "C" int voicedetect_capi_abi_version(void) { return VOICEDETECT_CAPI_ABI_VERSION; }
+
+extern "C" voicedetect_ctx* voicedetect_capi_load(const char* gguf_path) {
+    if (!gguf_path) return nullptr;
+    try {
+        std::unique_ptr<vdk::Model> m = vdk::Model::load(gguf_path);
+        if (!m) return nullptr;
+        auto* ctx = new (std::nothrow) voicedetect_ctx();
+        if (!ctx) return nullptr;
+        ctx->model = std::move(m);
+        return ctx;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "[voicedetect] load failed: %s\n", e.what());
+        return nullptr;
+    } catch (...) {
+        return nullptr;
+    }
+}
+
+extern "C" void voicedetect_capi_free(voicedetect_ctx* ctx) { delete ctx; }
+
+extern "C" const char* voicedetect_capi_last_error(voicedetect_ctx* ctx) {
+    return ctx ? ctx->last_error.c_str() : "";
+}
+
+extern "C" void voicedetect_capi_free_string(char* s) { std::free(s); }
+
+extern "C" void voicedetect_capi_free_vec(float* v) { std::free(v); }
+
+extern "C" int voicedetect_capi_embed_path(voicedetect_ctx* ctx, const char* wav_path, float** out_vec,
+                                           int* out_dim) {
+    if (out_vec) *out_vec = nullptr;
+    if (out_dim) *out_dim = 0;
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!wav_path) { ctx->last_error = "wav_path is NULL"; return 1; }
+    return run(ctx, [&] {
+        std::vector<float> e = embed_path(*ctx->model, wav_path);
+        return emit(ctx, e, (int)e.size(), out_vec, out_dim);
+    });
+}
+
+extern "C" int voicedetect_capi_embed_pcm(voicedetect_ctx* ctx, const float* pcm, int n_samples, int sample_rate,
+                                          float** out_vec, int* out_dim) {
+    if (out_vec) *out_vec = nullptr;
+    if (out_dim) *out_dim = 0;
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!pcm || n_samples < 0) { ctx->last_error = "invalid pcm buffer"; return 1; }
+    return run(ctx, [&] {
+        std::vector<float> x(pcm, pcm + n_samples);
+        std::vector<float> e = ctx->model->embed_pcm(x, sample_rate);
+        return emit(ctx, e, (int)e.size(), out_vec, out_dim);
+    });
+}
+
+extern "C" int voicedetect_capi_verify_paths(voicedetect_ctx* ctx, const char* a, const char* b, float threshold,
+                                             float* out_distance, int* out_verified) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!a || !b) { ctx->last_error = "clip path is NULL"; return 1; }
+    return run(ctx, [&] {
+        const std::vector<float> ea = embed_path(*ctx->model, a);
+        const std::vector<float> eb = embed_path(*ctx->model, b);
+        float d = 0.0f;
+        bool ok = false;
+        verdict(ea, eb, threshold, d, ok);
+        if (out_distance) *out_distance = d;
+        if (out_verified) *out_verified = ok ? 1 : 0;
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" char* voicedetect_capi_analyze_path_json(voicedetect_ctx* ctx, const char* wav_path) {
+    if (!ctx) return nullptr;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return nullptr; }
+    if (!wav_path) { ctx->last_error = "wav_path is NULL"; return nullptr; }
+    if (!ctx->model->config().analyze_present)
+        ctx->last_error = "voicedetect: this model has no age/gender/emotion analyze heads";
+    else
+        ctx->last_error = "voicedetect: analyze heads are not supported by this build";
+    return nullptr;
+}
+
+extern "C" int voicedetect_capi_embedding_dim(voicedetect_ctx* ctx) {
+    return (ctx && ctx->model) ? ctx->model->embedding_dim() : 0;
+}
+
+extern "C" int voicedetect_capi_embed_pcm_batch(voicedetect_ctx* ctx, const float* pcm, int batch, int n_samples,
+                                                int sample_rate, float** out_vec, int* out_dim) {
+    if (out_vec) *out_vec = nullptr;
+    if (out_dim) *out_dim = 0;
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!pcm || n_samples < 0 || batch <= 0) { ctx->last_error = "invalid pcm buffer"; return 1; }
+    return run(ctx, [&] {
+        vdk::Model& m = *ctx->model;
+        const int dim = m.embedding_dim();
+        std::vector<float> out((size_t)batch * dim);
+        if (sample_rate == 16000) {
+            m.embed_batch_host(pcm, batch, n_samples, out.data());
+        } else {
+            std::vector<float> all;
+            int n16 = -1;
+            for (int b = 0; b < batch; ++b) {
+                std::vector<float> x(pcm + (size_t)b * n_samples, pcm + (size_t)(b + 1) * n_samples);
+                std::vector<float> y = vdk::resample_linear(x, sample_rate, 16000);
+                n16 = (int)y.size();
+                all.insert(all.end(), y.begin(), y.end());
+            }
+            m.embed_batch_host(all.data(), batch, n16, out.data());
+        }
+        return emit(ctx, out, dim, out_vec, out_dim);
+    });
+}
+
+extern "C" int voicedetect_capi_verify_pcm(voicedetect_ctx* ctx, const float* a, int n_a, const float* b, int n_b,
+                                           int sample_rate, float threshold, float* out_distance,
+                                           int* out_verified) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!a || !b || n_a < 0 || n_b < 0) { ctx->last_error = "invalid pcm buffer"; return 1; }
+    return run(ctx, [&] {
+        const std::vector<float> ea = ctx->model->embed_pcm(std::vector<float>(a, a + n_a), sample_rate);
+        const std::vector<float> eb = ctx->model->embed_pcm(std::vector<float>(b, b + n_b), sample_rate);
+        float d = 0.0f;
+        bool ok = false;
+        verdict(ea, eb, threshold, d, ok);
+        if (out_distance) *out_distance = d;
+        if (out_verified) *out_verified = ok ? 1 : 0;
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" int voicedetect_gpu_embed_batch_async(voicedetect_ctx* ctx, const float* d_pcm, int batch,
+                                                 int n_samples, float* d_out) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    return run(ctx, [&] {
+        ctx->model->embed_batch_device(d_pcm, batch, n_samples, d_out);
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" int voicedetect_gpu_synchronize(voicedetect_ctx* ctx) {
+    if (!ctx || !ctx->model) return 1;
+    return run(ctx, [&] {
+        ctx->model->synchronize();
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" void* voicedetect_gpu_stream(voicedetect_ctx* ctx) {
+    if (!ctx || !ctx->model) return nullptr;
+    void* s = nullptr;
+    run(ctx, [&] {
+        s = ctx->model->stream();
+        return 0;
+    });
+    return s;
+}
+
+extern "C" int voicedetect_gpu_embed_capture(voicedetect_ctx* ctx, const float* pcm, int batch, int n_samples,
+                                             float* feats, float* pooled, int* pooled_dim, float* pre_norm,
+                                             float* out) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!pcm || batch <= 0 || n_samples < 0) { ctx->last_error = "invalid pcm buffer"; return 1; }
+    return run(ctx, [&] {
+        ctx->model->embed_capture(pcm, batch, n_samples, feats, pooled, pre_norm, out);
+        if (pooled_dim) *pooled_dim = ctx->model->pooled_dim();
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" int voicedetect_gpu_set_profiling(voicedetect_ctx* ctx, int on) {
+    if (!ctx || !ctx->model) return 1;
+    ctx->model->set_profiling(on != 0);
+    return 0;
+}
+
+extern "C" int voicedetect_gpu_profile_collect(voicedetect_ctx* ctx) {
+    if (!ctx || !ctx->model) return -1;
+    int n = -1;
+    const int rc = run(ctx, [&] {
+        ctx->profile = ctx->model->take_profile();
+        n = (int)ctx->profile.size();
+        return 0;
+    });
+    return rc == 0 ? n : -1;
+}
+
+extern "C" int voicedetect_gpu_profile_get(voicedetect_ctx* ctx, int i, char* name, int name_cap, double* ms,
+                                           double* flops, double* bytes) {
+    if (!ctx || i < 0 || i >= (int)ctx->profile.size()) return 1;
+    const vdk::ProfileRecord& r = ctx->profile[(size_t)i];
+    if (name && name_cap > 0) {
+        std::strncpy(name, r.name.c_str(), (size_t)name_cap - 1);
+        name[name_cap - 1] = '\0';
+    }
+    if (ms) *ms = r.ms;
+    if (flops) *flops = r.flops;
+    if (bytes) *bytes = r.bytes;
+    return 0;
+}

@@ -1,0 +1,385 @@
+// model.cpp - see model.hpp.
+#include "model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "audio.hpp"
+#include "common.hpp"
+
+namespace vdk {
+
+namespace {
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+void check(int rc) {
+    if (rc != 0) throw Error(vdk_last_error());
+}
+
+}  // namespace
+
+std::unique_ptr<Model> Model::load(const std::string& path) {
+    std::unique_ptr<Model> m(new Model());
+    m->gguf_.reset(new GgufFile(path));
+    const GgufFile& g = *m->gguf_;
+    ModelConfig& c = m->cfg_;
+    // src/model_loader.cpp:114-133
+    c.arch = g.str("voicedetect.arch");
+    c.embedding_dim = (int)g.u32("voicedetect.embedding_dim", 0);
+    c.l2_normalize = g.boolean("voicedetect.l2_normalize", true);
+    c.fbank.sample_rate = (int)g.u32("voicedetect.fbank.sample_rate", 16000);
+    c.fbank.n_mels = (int)g.u32("voicedetect.fbank.n_mels", 80);
+    c.fbank.n_fft = (int)g.u32("voicedetect.fbank.n_fft", 512);
+    c.fbank.win_length = (int)g.u32("voicedetect.fbank.win_length", 400);
+    c.fbank.hop_length = (int)g.u32("voicedetect.fbank.hop_length", 160);
+    c.fbank.preemph = g.f32("voicedetect.fbank.preemph", 0.97f);
+    c.fbank.low_freq = g.f32("voicedetect.fbank.low_freq", 20.0f);
+    c.fbank.high_freq = g.f32("voicedetect.fbank.high_freq", 0.0f);
+    c.fbank.cmn = g.boolean("voicedetect.fbank.cmn", true) ? 1 : 0;
+    c.analyze_present = g.boolean("voicedetect.analyze.present", false);
+    if (c.arch == "wespeaker_resnet34") {
+        ResNetCfg& r = c.resnet;   // src/model_loader.cpp:135-150
+        const std::string p = "voicedetect.resnet.";
+        r.stem_weight = g.str(p + "stem_weight");
+        r.stem_bias = g.str(p + "stem_bias");
+        r.conv1_weight = g.str_arr(p + "conv1_weight");
+        r.conv1_bias = g.str_arr(p + "conv1_bias");
+        r.conv2_weight = g.str_arr(p + "conv2_weight");
+        r.conv2_bias = g.str_arr(p + "conv2_bias");
+        r.down_weight = g.str_arr(p + "down_weight");
+        r.down_bias = g.str_arr(p + "down_bias");
+        r.stride = g.i32_arr(p + "stride");
+        r.seg_weight = g.str(p + "seg_weight");
+        r.seg_bias = g.str(p + "seg_bias");
+        r.mean_vec = g.str(p + "mean_vec");
+        r.var_eps = g.f32(p + "var_eps", 1e-8f);
+    }
+    // src/model_loader.cpp:212-214: a speaker model needs an embedding dim.
+    if (c.embedding_dim <= 0 && !c.analyze_present) throw Error("gguf: voicedetect.embedding_dim missing");
+    return m;
+}
+
+Model::~Model() {
+    free_workspace();
+    for (hipEvent_t e : event_pool_) (void)hipEventDestroy(e);
+    for (auto& p : pending_) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
+    if (arena_) (void)hipFree(arena_);
+    if (fb_tables_) (void)hipFree(fb_tables_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+int Model::frames(int n_samples) const {
+    const vdk_fbank_cfg& f = cfg_.fbank;
+    if (n_samples < f.win_length || f.hop_length <= 0) return 0;
+    return 1 + (n_samples - f.win_length) / f.hop_length;
+}
+
+void Model::ensure_device() {
+    if (ready_) return;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) throw Error("voicedetect: no HIP device available");
+    VDK_HIP(hipGetDevice(&device_));
+    if (cfg_.arch != "wespeaker_resnet34") {
+        if (cfg_.arch == "ecapa_tdnn" || cfg_.arch == "eres2net" || cfg_.arch == "campplus")
+            throw Error("voicedetect: arch '" + cfg_.arch + "' is not implemented by this build yet");
+        throw Error("voicedetect: unsupported arch '" + cfg_.arch + "'");
+    }
+    VDK_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    const size_t tb = vdk_fbank_tables_size(&cfg_.fbank);
+    if (tb == 0) throw Error(vdk_last_error());
+    VDK_HIP(hipMalloc(&fb_tables_, tb));
+    check(vdk_fbank_tables_fill(&cfg_.fbank, fb_tables_));
+    upload_resnet();
+    ready_ = true;
+}
+
+void Model::upload_resnet() {
+    const GgufFile& g = *gguf_;
+    const ResNetCfg& r = cfg_.resnet;
+    const size_t nb = r.conv1_weight.size();
+    require(nb > 0 && r.conv1_bias.size() == nb && r.conv2_weight.size() == nb && r.conv2_bias.size() == nb &&
+                r.down_weight.size() == nb && r.down_bias.size() == nb && r.stride.size() == nb,
+            "voicedetect: inconsistent resnet block manifest");
+    std::vector<uint8_t> host;
+    struct Fix { size_t off; void** dst_void; float** dst_float; };
+    std::vector<Fix> fixes;
+    auto put = [&](const void* src, size_t bytes) {
+        const size_t off = align256(host.size());
+        host.resize(off + bytes);
+        std::memcpy(host.data() + off, src, bytes);
+        return off;
+    };
+    auto put_f32 = [&](const std::string& name, size_t expect, float** dst) {
+        std::vector<float> v = g.to_f32(name);
+        require(expect == 0 || v.size() == expect, "voicedetect: tensor '" + name + "' has the wrong size");
+        fixes.push_back({put(v.data(), v.size() * 4), nullptr, dst});
+        return v.size();
+    };
+    // conv weight ne = [KW, KH, IC, OC] -> f16 [OC][KH][KW][IC]
+    auto put_conv = [&](const std::string& wn, const std::string& bn, int ic, int k, int stride, int pad,
+                        Conv& c) {
+        const GgufTensor* t = g.tensor(wn);
+        require(t != nullptr, "voicedetect: missing tensor '" + wn + "'");
+        require(t->ne.size() == 4 && t->ne[0] == k && t->ne[1] == k && t->ne[2] == ic,
+                "voicedetect: conv weight '" + wn + "' has an unexpected shape");
+        const int oc = (int)t->ne[3];
+        require(oc % 32 == 0 && ic % 16 == 0,
+                "voicedetect: conv '" + wn + "' needs IC % 16 == 0 and OC % 32 == 0");
+        std::vector<uint16_t> packed((size_t)oc * k * k * ic);
+        const uint16_t* h16 = t->type == GGML_F16 ? reinterpret_cast<const uint16_t*>(t->data) : nullptr;
+        std::vector<float> f32;
+        if (!h16) f32 = g.to_f32(wn);
+        for (int o = 0; o < oc; ++o)
+            for (int i = 0; i < ic; ++i)
+                for (int kh = 0; kh < k; ++kh)
+                    for (int kw = 0; kw < k; ++kw) {
+                        const size_t src = (((size_t)o * ic + i) * k + kh) * k + kw;
+                        const size_t dst = (((size_t)o * k + kh) * k + kw) * ic + i;
+                        packed[dst] = h16 ? h16[src] : float_to_half_bits(f32[src]);
+                    }
+        c.ic = ic; c.oc = oc; c.k = k; c.stride = stride; c.pad = pad;
+        fixes.push_back({put(packed.data(), packed.size() * 2), &c.w, nullptr});
+        put_f32(bn, (size_t)oc, &c.b);
+        return oc;
+    };
+
+    // stem: ne [3, 3, 1, OC], f32 on the device (the stem runs in f32)
+    const GgufTensor* st = g.tensor(r.stem_weight);
+    require(st && st->ne.size() == 4 && st->ne[0] == 3 && st->ne[1] == 3 && st->ne[2] == 1,
+            "voicedetect: stem weight must be [3,3,1,OC]");
+    stem_oc_ = (int)st->ne[3];
+    require(stem_oc_ == 16 || stem_oc_ == 32 || stem_oc_ == 64, "voicedetect: stem OC must be 16, 32 or 64");
+    put_f32(r.stem_weight, (size_t)stem_oc_ * 9, &stem_w_);
+    put_f32(r.stem_bias, (size_t)stem_oc_, &stem_b_);
+    blocks_.assign(nb, Block());
+    int C = stem_oc_, H = cfg_.fbank.n_mels;
+    for (size_t i = 0; i < nb; ++i) {
+        Block& b = blocks_[i];
+        const int s = r.stride[i];
+        require(s == 1 || s == 2, "voicedetect: block stride must be 1 or 2");
+        const int oc = put_conv(r.conv1_weight[i], r.conv1_bias[i], C, 3, s, 1, b.c1);
+        put_conv(r.conv2_weight[i], r.conv2_bias[i], oc, 3, 1, 1, b.c2);
+        require(b.c2.oc == oc, "voicedetect: conv2 width differs from conv1");
+        b.has_down = !r.down_weight[i].empty();
+        if (b.has_down) {
+            put_conv(r.down_weight[i], r.down_bias[i], C, 1, s, 0, b.down);
+            require(b.down.oc == oc, "voicedetect: downsample width differs from conv1");
+        } else {
+            require(s == 1 && C == oc, "voicedetect: identity shortcut needs stride 1 and equal widths");
+        }
+        C = oc;
+        H = (H - 1) / s + 1;
+    }
+    pooled_dim_ = 2 * C * H;
+    const size_t nseg = put_f32(r.seg_weight, 0, &seg_w_);
+    require(nseg == (size_t)pooled_dim_ * cfg_.embedding_dim,
+            "voicedetect: seg weight must be [embedding_dim, 2*C*H']");
+    if (!r.seg_bias.empty()) put_f32(r.seg_bias, (size_t)cfg_.embedding_dim, &seg_b_);
+    if (!r.mean_vec.empty()) put_f32(r.mean_vec, (size_t)cfg_.embedding_dim, &mean_vec_);
+
+    VDK_HIP(hipMalloc(&arena_, host.size()));
+    VDK_HIP(hipMemcpy(arena_, host.data(), host.size(), hipMemcpyHostToDevice));
+    uint8_t* base = static_cast<uint8_t*>(arena_);
+    for (const Fix& f : fixes) {
+        if (f.dst_void) *f.dst_void = base + f.off;
+        if (f.dst_float) *f.dst_float = reinterpret_cast<float*>(base + f.off);
+    }
+}
+
+void Model::free_workspace() {
+    Workspace& w = ws_;
+    for (void* p : {(void*)w.pcm, (void*)w.feats, w.act[0], w.act[1], w.act[2], w.act[3], (void*)w.pooled,
+                    (void*)w.pre, (void*)w.emb})
+        if (p) (void)hipFree(p);
+    ws_ = Workspace();
+}
+
+void Model::ensure_workspace(int batch, int n_samples) {
+    if (ws_.act[0] && batch <= ws_.batch && n_samples == ws_.n_samples) return;
+    VDK_HIP(hipStreamSynchronize(stream_));
+    free_workspace();
+    const int T = frames(n_samples);
+    const int nmel = cfg_.fbank.n_mels;
+    size_t act = (size_t)nmel * T * stem_oc_;
+    int H = nmel, W = T;
+    for (const Block& b : blocks_) {
+        H = (H - 1) / b.c1.stride + 1;
+        W = (W - 1) / b.c1.stride + 1;
+        act = std::max(act, (size_t)H * W * b.c1.oc);
+    }
+    Workspace& w = ws_;
+    w.batch = batch;
+    w.n_samples = n_samples;
+    w.act_bytes = act * 2 * batch;
+    VDK_HIP(hipMalloc((void**)&w.pcm, sizeof(float) * (size_t)batch * n_samples));
+    VDK_HIP(hipMalloc((void**)&w.feats, sizeof(float) * (size_t)batch * nmel * T));
+    for (int i = 0; i < 4; ++i) VDK_HIP(hipMalloc(&w.act[i], w.act_bytes));
+    VDK_HIP(hipMalloc((void**)&w.pooled, sizeof(float) * (size_t)batch * pooled_dim_));
+    VDK_HIP(hipMalloc((void**)&w.pre, sizeof(float) * (size_t)batch * cfg_.embedding_dim));
+    VDK_HIP(hipMalloc((void**)&w.emb, sizeof(float) * (size_t)batch * cfg_.embedding_dim));
+}
+
+void Model::prof_begin(const char* name, double flops, double bytes) {
+    if (!profiling_) return;
+    auto ev = [&] {
+        hipEvent_t e;
+        if (!event_pool_.empty()) { e = event_pool_.back(); event_pool_.pop_back(); }
+        else VDK_HIP(hipEventCreate(&e));
+        return e;
+    };
+    Pending p{name, flops, bytes, ev(), ev()};
+    VDK_HIP(hipEventRecord(p.a, stream_));
+    pending_.push_back(p);
+}
+
+void Model::prof_end() {
+    if (!profiling_) return;
+    VDK_HIP(hipEventRecord(pending_.back().b, stream_));
+}
+
+void Model::conv(const Conv& c, const void* x, int batch, int H, int W, const void* res, int relu, void* y) {
+    const int Ho = (H + 2 * c.pad - c.k) / c.stride + 1, Wo = (W + 2 * c.pad - c.k) / c.stride + 1;
+    if (profiling_) {
+        const double npix = (double)batch * Ho * Wo;
+        const double flops = 2.0 * c.k * c.k * c.ic * c.oc * npix;
+        const double bytes = 2.0 * ((double)batch * H * W * c.ic + (double)c.oc * c.k * c.k * c.ic +
+                                    npix * c.oc * (res ? 2.0 : 1.0)) + 4.0 * c.oc;
+        std::string name = "conv" + std::to_string(c.k) + "x" + std::to_string(c.k) + "_s" +
+                           std::to_string(c.stride) + "_" + std::to_string(c.ic) + "to" + std::to_string(c.oc);
+        prof_begin(name.c_str(), flops, bytes);
+    }
+    check(vdk_conv2d_nhwc(x, batch, H, W, c.ic, c.w, c.oc, c.k, c.k, c.stride, c.pad, c.b, res, relu, y, stream_));
+    prof_end();
+}
+
+void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) {
+    const int T = frames(n_samples);
+    if (T <= 0) throw Error("voicedetect: FBank produced no frames");
+    const int nmel = cfg_.fbank.n_mels;
+    // FBank front end
+    prof_begin("fbank", 0.0, 4.0 * batch * ((double)n_samples + (double)nmel * T));
+    check(vdk_fbank(&cfg_.fbank, fb_tables_, d_pcm, batch, n_samples, ws_.feats, stream_));
+    prof_end();
+    // stem conv + ReLU
+    prof_begin("stem3x3", 2.0 * 9 * stem_oc_ * (double)batch * nmel * T,
+               4.0 * batch * nmel * T + 2.0 * batch * nmel * T * stem_oc_);
+    check(vdk_stem_conv3x3(ws_.feats, batch, nmel, T, stem_w_, stem_b_, stem_oc_, 1, ws_.act[0], stream_));
+    prof_end();
+    int xi = 0, C = stem_oc_, H = nmel, W = T;
+    for (const Block& b : blocks_) {
+        int others[3], k = 0;
+        for (int i = 0; i < 4; ++i)
+            if (i != xi) others[k++] = i;
+        void* x = ws_.act[xi];
+        void* h = ws_.act[others[0]];
+        void* d = ws_.act[others[1]];
+        void* y = ws_.act[others[2]];
+        const int s = b.c1.stride;
+        const int Ho = (H - 1) / s + 1, Wo = (W - 1) / s + 1;
+        conv(b.c1, x, batch, H, W, nullptr, 1, h);
+        const void* sc = x;
+        if (b.has_down) {
+            conv(b.down, x, batch, H, W, nullptr, 0, d);
+            sc = d;
+        }
+        conv(b.c2, h, batch, Ho, Wo, sc, 1, y);
+        xi = others[2];
+        C = b.c1.oc;
+        H = Ho;
+        W = Wo;
+    }
+    prof_begin("tstp", 0.0, 2.0 * batch * (double)H * W * C + 4.0 * batch * pooled_dim_);
+    check(vdk_tstp(ws_.act[xi], batch, H, W, C, cfg_.resnet.var_eps, ws_.pooled, stream_));
+    prof_end();
+    const int E = cfg_.embedding_dim;
+    prof_begin("linear", 2.0 * batch * (double)pooled_dim_ * E,
+               4.0 * ((double)batch * pooled_dim_ + (double)pooled_dim_ * E + (double)batch * E));
+    check(vdk_linear(ws_.pooled, batch, pooled_dim_, seg_w_, seg_b_, mean_vec_, E, ws_.pre, stream_));
+    prof_end();
+    VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));
+    if (cfg_.l2_normalize) {
+        prof_begin("l2norm", 0.0, 8.0 * batch * E);
+        check(vdk_l2norm(d_out, batch, E, stream_));
+        prof_end();
+    }
+}
+
+void Model::embed_batch_device(const float* d_pcm, int batch, int n_samples, float* d_out) {
+    std::lock_guard<std::mutex> lock(mu_);
+    require(batch > 0, "voicedetect: batch must be positive");
+    require(d_pcm && d_out, "voicedetect: NULL device pointer");
+    if (frames(n_samples) <= 0) throw Error("voicedetect: FBank produced no frames");
+    ensure_device();
+    ensure_workspace(batch, n_samples);
+    forward(d_pcm, batch, n_samples, d_out);
+}
+
+void Model::embed_capture(const float* pcm, int batch, int n_samples, float* feats, float* pooled,
+                          float* pre_norm, float* out) {
+    std::lock_guard<std::mutex> lock(mu_);
+    require(batch > 0 && pcm, "voicedetect: invalid pcm batch");
+    if (frames(n_samples) <= 0) throw Error("voicedetect: FBank produced no frames");
+    ensure_device();
+    ensure_workspace(batch, n_samples);
+    const size_t E = (size_t)cfg_.embedding_dim;
+    VDK_HIP(hipMemcpyAsync(ws_.pcm, pcm, sizeof(float) * (size_t)batch * n_samples, hipMemcpyHostToDevice, stream_));
+    forward(ws_.pcm, batch, n_samples, ws_.emb);
+    const size_t T = (size_t)frames(n_samples);
+    if (feats)
+        VDK_HIP(hipMemcpyAsync(feats, ws_.feats, sizeof(float) * batch * cfg_.fbank.n_mels * T,
+                               hipMemcpyDeviceToHost, stream_));
+    if (pooled)
+        VDK_HIP(hipMemcpyAsync(pooled, ws_.pooled, sizeof(float) * batch * pooled_dim_, hipMemcpyDeviceToHost,
+                               stream_));
+    if (pre_norm)
+        VDK_HIP(hipMemcpyAsync(pre_norm, ws_.pre, sizeof(float) * batch * E, hipMemcpyDeviceToHost, stream_));
+    if (out) VDK_HIP(hipMemcpyAsync(out, ws_.emb, sizeof(float) * batch * E, hipMemcpyDeviceToHost, stream_));
+    VDK_HIP(hipStreamSynchronize(stream_));
+}
+
+void Model::embed_batch_host(const float* pcm, int batch, int n_samples, float* out) {
+    embed_capture(pcm, batch, n_samples, nullptr, nullptr, nullptr, out);
+}
+
+std::vector<float> Model::embed_pcm(const std::vector<float>& pcm, int sample_rate) {
+    const std::vector<float> x = sample_rate == 16000 ? pcm : resample_linear(pcm, sample_rate, 16000);
+    if (frames((int)x.size()) <= 0) throw Error("voicedetect: FBank produced no frames");
+    std::vector<float> out((size_t)cfg_.embedding_dim);
+    embed_batch_host(x.data(), 1, (int)x.size(), out.data());
+    return out;
+}
+
+void Model::synchronize() {
+    std::lock_guard<std::mutex> lock(mu_);
+    if (stream_) VDK_HIP(hipStreamSynchronize(stream_));
+}
+
+hipStream_t Model::stream() {
+    std::lock_guard<std::mutex> lock(mu_);
+    ensure_device();
+    return stream_;
+}
+
+void Model::set_profiling(bool on) {
+    std::lock_guard<std::mutex> lock(mu_);
+    profiling_ = on;
+}
+
+std::vector<ProfileRecord> Model::take_profile() {
+    std::lock_guard<std::mutex> lock(mu_);
+    std::vector<ProfileRecord> out;
+    if (stream_) VDK_HIP(hipStreamSynchronize(stream_));
+    for (auto& p : pending_) {
+        float ms = 0.0f;
+        VDK_HIP(hipEventElapsedTime(&ms, p.a, p.b));
+        out.push_back({p.name, p.flops, p.bytes, (double)ms});
+        event_pool_.push_back(p.a);
+        event_pool_.push_back(p.b);
+    }
+    pending_.clear();
+    return out;
+}
+
+}  // namespace vdk

@@ -1,0 +1,134 @@
+// model.hpp - load-once speaker-embedding context on one MI355X.
+//
+// Counterpart of vd::Model (src/model.hpp:18-57): parses the GGUF once on the
+// host (no GPU needed), and on the first embed uploads the weights into one
+// device arena in kernel-ready layouts and creates the context's HIP stream.
+// Every embed runs the whole path on the GPU (FBank -> encoder -> pooling ->
+// FC -> L2) for a batch of equal-length clips.  A context is driven by one
+// caller at a time; an internal mutex serialises concurrent calls.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "gguf.hpp"
+#include "vdk.h"
+
+namespace vdk {
+
+struct ResNetCfg {
+    std::string stem_weight, stem_bias;
+    std::vector<std::string> conv1_weight, conv1_bias, conv2_weight, conv2_bias, down_weight, down_bias;
+    std::vector<int32_t> stride;
+    std::string seg_weight, seg_bias, mean_vec;
+    float var_eps = 1e-8f;
+};
+
+struct ModelConfig {
+    std::string arch;
+    int embedding_dim = 0;
+    bool l2_normalize = true;
+    bool analyze_present = false;
+    vdk_fbank_cfg fbank{};
+    ResNetCfg resnet;
+};
+
+struct ProfileRecord {
+    std::string name;
+    double flops = 0.0, bytes = 0.0, ms = 0.0;
+};
+
+class Model {
+public:
+    // Throws vdk::Error on a missing/malformed GGUF or a missing required key.
+    static std::unique_ptr<Model> load(const std::string& path);
+    ~Model();
+
+    const ModelConfig& config() const { return cfg_; }
+    int embedding_dim() const { return cfg_.embedding_dim; }
+    // 2 * C * H' of the pooled statistics (known once the weights are on the device).
+    int pooled_dim() const { return pooled_dim_; }
+
+    // 16 kHz (resampled if needed) mono PCM -> L2-normalised embedding.
+    std::vector<float> embed_pcm(const std::vector<float>& pcm, int sample_rate);
+    // batch x n_samples host PCM (16 kHz) -> batch x dim host embeddings.
+    void embed_batch_host(const float* pcm, int batch, int n_samples, float* out);
+    // Device-resident batch on this context's stream; returns without waiting.
+    void embed_batch_device(const float* d_pcm, int batch, int n_samples, float* d_out);
+    // Same as embed_batch_host, also copying intermediate results (NULL = skip):
+    // feats [B][n_mels][T], pooled [B][P], pre_norm [B][dim].
+    void embed_capture(const float* pcm, int batch, int n_samples, float* feats, float* pooled,
+                       float* pre_norm, float* out);
+    void synchronize();
+    hipStream_t stream();
+
+    void set_profiling(bool on);
+    // Waits for the stream and returns the per-launch records since the last call.
+    std::vector<ProfileRecord> take_profile();
+
+    Model(const Model&) = delete;
+    Model& operator=(const Model&) = delete;
+
+private:
+    Model() = default;
+    struct Conv {
+        int ic = 0, oc = 0, k = 0, stride = 1, pad = 0;
+        void* w = nullptr;     // f16 [OC][K][K][IC]
+        float* b = nullptr;    // f32 [OC]
+    };
+    struct Block {
+        Conv c1, c2, down;
+        bool has_down = false;
+    };
+    struct Workspace {
+        int batch = 0, n_samples = 0;
+        size_t act_bytes = 0;
+        float* pcm = nullptr;
+        float* feats = nullptr;
+        void* act[4] = {nullptr, nullptr, nullptr, nullptr};
+        float* pooled = nullptr;
+        float* pre = nullptr;
+        float* emb = nullptr;
+    };
+
+    void ensure_device();
+    void upload_resnet();
+    void ensure_workspace(int batch, int n_samples);
+    void free_workspace();
+    // The whole forward for device PCM into device embeddings (pre-norm copy in ws_.pre).
+    void forward(const float* d_pcm, int batch, int n_samples, float* d_out);
+    void conv(const Conv& c, const void* x, int batch, int H, int W, const void* res, int relu, void* y);
+    void prof_begin(const char* name, double flops, double bytes);
+    void prof_end();
+    int frames(int n_samples) const;
+
+    std::unique_ptr<GgufFile> gguf_;
+    ModelConfig cfg_;
+    std::mutex mu_;
+
+    bool ready_ = false;
+    int device_ = 0;
+    hipStream_t stream_ = nullptr;
+    void* arena_ = nullptr;
+    void* fb_tables_ = nullptr;
+    float* stem_w_ = nullptr;
+    float* stem_b_ = nullptr;
+    int stem_oc_ = 0;
+    std::vector<Block> blocks_;
+    float* seg_w_ = nullptr;
+    float* seg_b_ = nullptr;
+    float* mean_vec_ = nullptr;
+    int pooled_dim_ = 0;
+    Workspace ws_;
+
+    bool profiling_ = false;
+    struct Pending { std::string name; double flops, bytes; hipEvent_t a, b; };
+    std::vector<Pending> pending_;
+    std::vector<hipEvent_t> event_pool_;
+};
+
+}  // namespace vdk

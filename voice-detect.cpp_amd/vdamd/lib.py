@@ -1,0 +1,263 @@
+"""ctypes binding of lib/libvoicedetect.so (include/voicedetect_capi.h,
+include/voicedetect_gpu.h, include/vdk.h).
+
+Loading fails loudly when the library has not been built: there is no
+fallback path.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG, "lib", "libvoicedetect.so")
+INCLUDE_DIR = os.path.join(os.path.dirname(PKG), "include")
+
+_LIB = None
+
+F32P = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_vp = C.c_void_p
+
+
+class FbankCfg(C.Structure):
+    _fields_ = [("sample_rate", C.c_int), ("n_mels", C.c_int), ("n_fft", C.c_int),
+                ("win_length", C.c_int), ("hop_length", C.c_int), ("preemph", C.c_float),
+                ("low_freq", C.c_float), ("high_freq", C.c_float), ("cmn", C.c_int)]
+
+
+def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
+              sample_rate=16000):
+    return FbankCfg(sample_rate, n_mels, n_fft, win, hop, preemph, low, high, int(cmn))
+
+
+_SIGS = {
+    # frozen C ABI
+    "voicedetect_capi_abi_version": (C.c_int, []),
+    "voicedetect_capi_load": (_vp, [C.c_char_p]),
+    "voicedetect_capi_free": (None, [_vp]),
+    "voicedetect_capi_last_error": (C.c_char_p, [_vp]),
+    "voicedetect_capi_free_string": (None, [_vp]),
+    "voicedetect_capi_free_vec": (None, [_vp]),
+    "voicedetect_capi_embed_path": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.c_int)]),
+    "voicedetect_capi_embed_pcm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.POINTER(C.POINTER(C.c_float)),
+                                              C.POINTER(C.c_int)]),
+    "voicedetect_capi_verify_paths": (C.c_int, [_vp, C.c_char_p, C.c_char_p, C.c_float, C.POINTER(C.c_float),
+                                                 C.POINTER(C.c_int)]),
+    "voicedetect_capi_analyze_path_json": (_vp, [_vp, C.c_char_p]),
+    # additive
+    "voicedetect_capi_embedding_dim": (C.c_int, [_vp]),
+    "voicedetect_capi_embed_pcm_batch": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int,
+                                                    C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.c_int)]),
+    "voicedetect_capi_verify_pcm": (C.c_int, [_vp, _vp, C.c_int, _vp, C.c_int, C.c_int, C.c_float,
+                                               C.POINTER(C.c_float), C.POINTER(C.c_int)]),
+    "voicedetect_gpu_embed_batch_async": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp]),
+    "voicedetect_gpu_synchronize": (C.c_int, [_vp]),
+    "voicedetect_gpu_stream": (_vp, [_vp]),
+    "voicedetect_gpu_embed_capture": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp, C.POINTER(C.c_int), _vp, _vp]),
+    "voicedetect_gpu_set_profiling": (C.c_int, [_vp, C.c_int]),
+    "voicedetect_gpu_profile_collect": (C.c_int, [_vp]),
+    "voicedetect_gpu_profile_get": (C.c_int, [_vp, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_double),
+                                              C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    # vdk
+    "vdk_device_count": (C.c_int, []),
+    "vdk_set_device": (C.c_int, [C.c_int]),
+    "vdk_malloc": (_vp, [C.c_size_t]),
+    "vdk_free": (C.c_int, [_vp]),
+    "vdk_memcpy_h2d": (C.c_int, [_vp, _vp, C.c_size_t]),
+    "vdk_memcpy_d2h": (C.c_int, [_vp, _vp, C.c_size_t]),
+    "vdk_memset": (C.c_int, [_vp, C.c_int, C.c_size_t]),
+    "vdk_synchronize": (C.c_int, []),
+    "vdk_last_error": (C.c_char_p, []),
+    "vdk_load_wav_16k": (C.c_long, [C.c_char_p, _vp, C.c_long]),
+    "vdk_resample_linear": (C.c_long, [_vp, C.c_long, C.c_int, C.c_int, _vp, C.c_long]),
+    "vdk_f32_to_f16": (None, [_vp, _vp, C.c_size_t]),
+    "vdk_fbank_tables_size": (C.c_size_t, [C.POINTER(FbankCfg)]),
+    "vdk_fbank_tables_fill": (C.c_int, [C.POINTER(FbankCfg), _vp]),
+    "vdk_fbank": (C.c_int, [C.POINTER(FbankCfg), _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_conv2d_nhwc": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
+                                  C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp]),
+    "vdk_stem_conv3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_tstp": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "vdk_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp]),
+    "vdk_l2norm": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
+}
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built (run __graft_entry__.build() or make -C voice-detect.cpp_amd)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+class VdkError(RuntimeError):
+    pass
+
+
+def _ok(rc):
+    if rc != 0:
+        raise VdkError(lib().vdk_last_error().decode())
+
+
+class DeviceBuffer:
+    """A device allocation made through vdk_malloc (freed on close/GC)."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = lib().vdk_malloc(max(self.nbytes, 1))
+        if not self.ptr:
+            raise VdkError(lib().vdk_last_error().decode())
+
+    @classmethod
+    def from_array(cls, a):
+        a = np.ascontiguousarray(a)
+        d = cls(a.nbytes)
+        _ok(lib().vdk_memcpy_h2d(d.ptr, a.ctypes.data, a.nbytes))
+        return d
+
+    def to_array(self, dtype, shape):
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        _ok(lib().vdk_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def close(self):
+        if self.ptr:
+            lib().vdk_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def check(rc):
+    _ok(rc)
+
+
+class Context:
+    """Owning wrapper over a voicedetect_ctx."""
+
+    def __init__(self, gguf_path):
+        self.L = lib()
+        self.ctx = self.L.voicedetect_capi_load(gguf_path.encode())
+        if not self.ctx:
+            raise VdkError(f"voicedetect_capi_load failed for {gguf_path}")
+
+    def close(self):
+        if self.ctx:
+            self.L.voicedetect_capi_free(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def last_error(self):
+        return self.L.voicedetect_capi_last_error(self.ctx).decode()
+
+    @property
+    def dim(self):
+        return self.L.voicedetect_capi_embedding_dim(self.ctx)
+
+    def _take(self, vec, n):
+        a = np.ctypeslib.as_array(vec, shape=(n,)).copy()
+        self.L.voicedetect_capi_free_vec(vec)
+        return a
+
+    def embed_pcm(self, pcm, sample_rate=16000):
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        vec = C.POINTER(C.c_float)()
+        dim = C.c_int()
+        rc = self.L.voicedetect_capi_embed_pcm(self.ctx, pcm.ctypes.data, len(pcm), sample_rate, C.byref(vec),
+                                               C.byref(dim))
+        if rc != 0:
+            raise VdkError(self.last_error())
+        return self._take(vec, dim.value)
+
+    def embed_path(self, path):
+        vec = C.POINTER(C.c_float)()
+        dim = C.c_int()
+        rc = self.L.voicedetect_capi_embed_path(self.ctx, path.encode(), C.byref(vec), C.byref(dim))
+        if rc != 0:
+            raise VdkError(self.last_error())
+        return self._take(vec, dim.value)
+
+    def embed_batch(self, pcm, sample_rate=16000):
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        B, n = pcm.shape
+        vec = C.POINTER(C.c_float)()
+        dim = C.c_int()
+        rc = self.L.voicedetect_capi_embed_pcm_batch(self.ctx, pcm.ctypes.data, B, n, sample_rate, C.byref(vec),
+                                                     C.byref(dim))
+        if rc != 0:
+            raise VdkError(self.last_error())
+        return self._take(vec, B * dim.value).reshape(B, dim.value)
+
+    def verify_paths(self, a, b, threshold):
+        d = C.c_float(-1.0)
+        v = C.c_int(-1)
+        rc = self.L.voicedetect_capi_verify_paths(self.ctx, a.encode(), b.encode(), threshold, C.byref(d), C.byref(v))
+        if rc != 0:
+            raise VdkError(self.last_error())
+        return d.value, bool(v.value)
+
+    def capture(self, pcm, n_mels=80):
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        B, n = pcm.shape
+        T = 1 + (n - 400) // 160
+        feats = np.zeros((B, n_mels, T), dtype=np.float32)
+        pdim = C.c_int(0)
+        pooled = np.zeros((B, 1 << 16), dtype=np.float32)
+        pre = np.zeros((B, self.dim), dtype=np.float32)
+        out = np.zeros((B, self.dim), dtype=np.float32)
+        rc = self.L.voicedetect_gpu_embed_capture(self.ctx, pcm.ctypes.data, B, n, feats.ctypes.data,
+                                                  None, C.byref(pdim), pre.ctypes.data, out.ctypes.data)
+        if rc != 0:
+            raise VdkError(self.last_error())
+        pooled = np.zeros((B, pdim.value), dtype=np.float32)
+        rc = self.L.voicedetect_gpu_embed_capture(self.ctx, pcm.ctypes.data, B, n, None, pooled.ctypes.data,
+                                                  None, None, None)
+        if rc != 0:
+            raise VdkError(self.last_error())
+        return {"feats": feats, "pooled": pooled, "pre_norm": pre, "emb": out}
+
+    # device-resident path
+    def embed_device_async(self, d_pcm, batch, n_samples, d_out):
+        rc = self.L.voicedetect_gpu_embed_batch_async(self.ctx, d_pcm, batch, n_samples, d_out)
+        if rc != 0:
+            raise VdkError(self.last_error())
+
+    def synchronize(self):
+        if self.L.voicedetect_gpu_synchronize(self.ctx) != 0:
+            raise VdkError(self.last_error())
+
+    def set_profiling(self, on):
+        self.L.voicedetect_gpu_set_profiling(self.ctx, int(on))
+
+    def profile(self):
+        n = self.L.voicedetect_gpu_profile_collect(self.ctx)
+        if n < 0:
+            raise VdkError(self.last_error())
+        out = []
+        name = C.create_string_buffer(128)
+        ms, fl, by = C.c_double(), C.c_double(), C.c_double()
+        for i in range(n):
+            self.L.voicedetect_gpu_profile_get(self.ctx, i, name, 128, C.byref(ms), C.byref(fl), C.byref(by))
+            out.append((name.value.decode(), ms.value, fl.value, by.value))
+        return out
