@@ -1,0 +1,180 @@
+"""Throughput benchmark: WeSpeaker ResNet34 speaker embeddings on one MI355X.
+
+Workload: batch 64 x 3 s 16 kHz synthetic clips (FBank 64x80x298), random-init
+f16 weights with folded BN, the full path PCM -> FBank -> ResNet34 -> TSTP ->
+FC -> L2 on the GPU.  A step is one batch; inputs are resident in HBM before
+the timed region.  Prints one JSON line (rank 0, N=1).
+
+The conv roofline comes from HIP events recorded around every launch on the
+library's stream, in a profiled pass of the same number of steps right after
+the timed pass: achieved = direct-conv algorithmic FLOPs / event time.  The CPU
+baseline times the oracle (this repository's C restatement of the reference
+CPU path) on a bounded sample of the same clips.
+"""
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "voice-detect.cpp_amd"))
+
+from vdamd import lib, synth  # noqa: E402
+
+METRIC = "embeddings/s, ResNet34 B=64 3 s clips; conv MFMA util vs f16 peak"
+PEAK_F16_TFLOPS = 2500.0     # MI355X dense f16 MFMA
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+BATCH = 64
+N_SAMPLES = 48000            # 3 s at 16 kHz -> 298 frames
+MODEL_SEED = 2024
+CLIP_SEED = 1234
+
+
+def classify(name):
+    if name.startswith("conv"):
+        return "conv"
+    return name
+
+
+def profile_pass(ctx, d_pcm, d_out, steps):
+    ctx.set_profiling(True)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.embed_device_async(d_pcm.ptr, BATCH, N_SAMPLES, d_out.ptr)
+    ctx.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    recs = ctx.profile()
+    ctx.set_profiling(False)
+    per = {}
+    for name, ms, fl, by in recs:
+        p = per.setdefault(name, {"launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+        p["launches"] += 1
+        p["ms"] += ms
+        p["flops"] += fl
+        p["bytes"] += by
+    return per, wall * 1e3
+
+
+def cpu_baseline(gguf_path, pcm):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    from vdamd import gguf
+
+    net = pyoracle.OracleResNet(gguf.GGUFFile(gguf_path))
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    threads = max(1, min(8, avail))            # the reference's default min(hw, 8) threads
+    sample = pcm[: 2 * threads]
+    t0 = time.perf_counter()
+    net.embed_batch(sample, n_threads=threads)
+    dt = time.perf_counter() - t0
+    cpu_name = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(len(sample) / dt, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
+            "sample": f"{len(sample)} of the same 3 s clips through oracle FBank+ResNet34 (f32), "
+                      f"clip-parallel on {threads} threads, {dt:.1f} s wall; host {cpu_name}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "clips are independent, so N GPUs would each run this same per-GPU batch.", file=sys.stderr)
+        sys.exit(2)
+    L = lib.lib()
+    if L.vdk_device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "resnet34_f16.gguf")
+    synth.write_resnet34(path, seed=MODEL_SEED)
+    ctx = lib.Context(path)
+    pcm = synth.clips(CLIP_SEED, BATCH, N_SAMPLES)
+    d_pcm = lib.DeviceBuffer.from_array(pcm)
+    d_out = lib.DeviceBuffer(BATCH * ctx.dim * 4)
+
+    for _ in range(args.warmup):
+        ctx.embed_device_async(d_pcm.ptr, BATCH, N_SAMPLES, d_out.ptr)
+    ctx.synchronize()
+    lib.check(L.vdk_synchronize())
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.embed_device_async(d_pcm.ptr, BATCH, N_SAMPLES, d_out.ptr)
+    ctx.synchronize()
+    lib.check(L.vdk_synchronize())
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = BATCH * args.steps / elapsed
+    emb = d_out.to_array(np.float32, (BATCH, ctx.dim))
+    assert np.all(np.isfinite(emb)) and np.allclose(np.linalg.norm(emb, axis=1), 1.0, atol=1e-4)
+
+    per, prof_ms = profile_pass(ctx, d_pcm, d_out, args.steps)
+    conv = {"ms": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0}
+    for name, p in per.items():
+        if classify(name) == "conv":
+            for k in conv:
+                conv[k] += p[k]
+    steps = args.steps
+    conv_ms_step = conv["ms"] / steps
+    achieved = conv["flops"] / (conv["ms"] * 1e-3) / 1e12 if conv["ms"] > 0 else 0.0
+    kernels = []
+    for name, p in sorted(per.items(), key=lambda kv: -kv[1]["ms"]):
+        t = p["ms"] * 1e-3
+        kernels.append({
+            "name": name, "launches_per_step": p["launches"] // steps,
+            "ms_per_step": round(p["ms"] / steps, 5),
+            "tflops": round(p["flops"] / t / 1e12, 2) if p["flops"] and t > 0 else None,
+            "gbs": round(p["bytes"] / t / 1e9, 1) if t > 0 else None,
+        })
+    roofline = {
+        "kernel": "all conv launches (implicit-GEMM MFMA conv, 35 per step)",
+        "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
+        "frac": round(achieved / PEAK_F16_TFLOPS, 4),
+        "traffic": None,
+        "flops_per_step": conv["flops"] / steps,
+        "conv_ms_per_step": round(conv_ms_step, 4),
+        "profiled_ms_per_step": round(prof_ms, 4),
+        "kernels": kernels,
+    }
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "embeddings/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "WeSpeaker ResNet34 embed, batch 64 x 3 s 16 kHz clips (FBank 64x80x298), "
+                               "random-init f16 weights with folded BN, PCM->FBank->ResNet34->TSTP->FC->L2 on GPU",
+                   "batch": BATCH, "clip_seconds": 3.0, "frames": 298, "channels": [32, 64, 128, 256],
+                   "blocks": [3, 4, 6, 3]},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(path, pcm)
+    ctx.close()
+    for k in kernels:
+        print(f"  {k['name']:28s} x{k['launches_per_step']:2d} {k['ms_per_step']*1e3:9.1f} us/step "
+              f"{k['tflops'] or 0:8.1f} TFLOP/s {k['gbs'] or 0:8.1f} GB/s", file=sys.stderr)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -95,11 +95,10 @@ def test_verify_fixture_wavs_same_verdict_as_oracle(resnet, golden_dir):
         d, ok = ctx.verify_paths(os.path.join(golden_dir, a + ".wav"), os.path.join(golden_dir, b + ".wav"), thr)
         assert abs(d - d_ref) <= 2e-3
         assert ok == (d_ref <= thr)
-        # and at a threshold between the two distances the verdict flips identically
-        mid = (d + d_ref) / 2
-        if abs(d - d_ref) < 1e-6:
-            assert ctx.verify_paths(os.path.join(golden_dir, a + ".wav"), os.path.join(golden_dir, b + ".wav"),
-                                    mid)[1] == (d_ref <= mid)
+        # identical verdicts at thresholds just outside the 2e-3 distance tolerance band
+        for t in (d_ref - 5e-3, d_ref + 5e-3):
+            path_a, path_b = os.path.join(golden_dir, a + ".wav"), os.path.join(golden_dir, b + ".wav")
+            assert ctx.verify_paths(path_a, path_b, t)[1] == (d_ref <= t)
 
 
 def test_other_lengths_and_mean_vec():

@@ -197,7 +197,7 @@ def test_tstp_linear_l2_match_oracle():
     P = 2 * C * H
     dp = lib.DeviceBuffer(B * P * 4)
     lib.check(L.vdk_tstp(dx.ptr, B, H, W, C, 1e-8, dp.ptr, None))
-    wfc = rng.standard_normal((E, P)).astype(np.float32) * np.sqrt(2.0 / P)
+    wfc = (rng.standard_normal((E, P)) * np.sqrt(2.0 / P)).astype(np.float32)
     bfc = rng.standard_normal(E).astype(np.float32) * 0.01
     mv = rng.standard_normal(E).astype(np.float32) * 0.05
     dw, db, dm = (lib.DeviceBuffer.from_array(a) for a in (wfc, bfc, mv))

@@ -122,6 +122,8 @@ class DeviceBuffer:
     @classmethod
     def from_array(cls, a):
         a = np.ascontiguousarray(a)
+        if a.dtype not in (np.float32, np.float16, np.int32, np.uint16, np.int8, np.uint8):
+            raise TypeError(f"DeviceBuffer.from_array: unexpected dtype {a.dtype} (kernels take f32/f16/int)")
         d = cls(a.nbytes)
         _ok(lib().vdk_memcpy_h2d(d.ptr, a.ctypes.data, a.nbytes))
         return d
