@@ -80,6 +80,16 @@ int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC,
                     const float* d_bias, const void* d_residual, int relu,
                     void* d_y, void* stream);
 
+/* Same contract with an explicit kernel/tile choice (index into the library's
+ * tile table; vdk_conv2d_tile_fits tells which apply to a shape).  For
+ * validation and tuning; vdk_conv2d_nhwc picks the tile itself. */
+int vdk_conv2d_nhwc_tile(const void* d_x, int batch, int H, int W, int IC,
+                         const void* d_w, int OC, int KH, int KW, int stride, int pad,
+                         const float* d_bias, const void* d_residual, int relu,
+                         void* d_y, void* stream, int tile);
+int vdk_conv2d_tile_count(void);
+int vdk_conv2d_tile_fits(int tile, int IC, int OC, int KH, int KW, int stride, int pad);
+
 /* ---- stem: single-input-channel 3x3 conv from f32 features ----
  * Replaces the ResNet stem conv2d_auto -> directconv_conv3x3 + bias + ReLU
  * (src/encoder_resnet.cpp:115-117).  feats [B][H][W] f32, w [OC][3][3] f32,

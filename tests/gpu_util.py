@@ -19,7 +19,7 @@ def announce(msg):
     print(f"[gpu-case] {msg}", flush=True)
 
 
-def conv_gpu(x_nhwc, w_oihw, bias=None, residual=None, stride=1, pad=1, relu=False):
+def conv_gpu(x_nhwc, w_oihw, bias=None, residual=None, stride=1, pad=1, relu=False, tile=-1):
     """x [B,H,W,IC] f16, w [OC,IC,KH,KW] (f16 values) -> y [B,Ho,Wo,OC] f16 via vdk_conv2d_nhwc."""
     L = lib.lib()
     x = np.ascontiguousarray(x_nhwc, dtype=np.float16)
@@ -37,8 +37,8 @@ def conv_gpu(x_nhwc, w_oihw, bias=None, residual=None, stride=1, pad=1, relu=Fal
         assert r.shape == (B, Ho, Wo, OC)
         dr = lib.DeviceBuffer.from_array(r)
     dy = lib.DeviceBuffer(B * Ho * Wo * OC * 2)
-    rc = L.vdk_conv2d_nhwc(dx.ptr, B, H, W, IC, dw.ptr, OC, KH, KW, stride, pad,
-                           db.ptr if db else None, dr.ptr if dr else None, int(relu), dy.ptr, None)
+    rc = L.vdk_conv2d_nhwc_tile(dx.ptr, B, H, W, IC, dw.ptr, OC, KH, KW, stride, pad,
+                                db.ptr if db else None, dr.ptr if dr else None, int(relu), dy.ptr, None, tile)
     lib.check(rc)
     lib.check(L.vdk_synchronize())
     return dy.to_array(np.float16, (B, Ho, Wo, OC))

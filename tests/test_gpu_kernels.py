@@ -143,6 +143,42 @@ def test_conv_edge_shapes(case):
     _check_conv(x, w, b, res, s, p, relu, clips=range(B), tag=f"edge{case}")
 
 
+TILE_SHAPES = [
+    # (B, H, W, IC, OC, K, stride, pad): small maps with ragged tile edges per kernel family
+    (2, 13, 75, 32, 32, 3, 1, 1), (2, 9, 70, 64, 64, 3, 1, 1), (2, 7, 38, 128, 128, 3, 1, 1),
+    (2, 6, 19, 256, 256, 3, 1, 1), (2, 11, 37, 32, 64, 3, 2, 1), (2, 11, 37, 64, 128, 1, 2, 0),
+]
+
+
+@pytest.mark.parametrize("shape", TILE_SHAPES, ids=[f"{s[3]}to{s[4]}k{s[5]}s{s[6]}" for s in TILE_SHAPES])
+def test_conv_every_tile_config(shape):
+    """Every kernel/tile variant the dispatcher can pick, on shapes with partial tiles."""
+    L = lib.lib()
+    B, H, W, IC, OC, K, s, p = shape
+    rng = np.random.default_rng(IC * 7 + OC + K)
+    x = rng.standard_normal((B, H, W, IC)).astype(np.float16)
+    w = (rng.standard_normal((OC, IC, K, K)) * np.sqrt(1.0 / (IC * K * K))).astype(np.float16)
+    b = rng.uniform(-1, 1, OC).astype(np.float32)
+    Ho, Wo = (H + 2 * p - K) // s + 1, (W + 2 * p - K) // s + 1
+    res = rng.standard_normal((B, Ho, Wo, OC)).astype(np.float16)
+    refs = []
+    for c in range(B):
+        refs.append(O.conv2d(x[c].astype(np.float32).transpose(2, 0, 1), w.astype(np.float32), s, p, bias=b,
+                             residual=res[c].astype(np.float32).transpose(2, 0, 1), relu=True))
+    n = 0
+    for t in range(L.vdk_conv2d_tile_count()):
+        if not L.vdk_conv2d_tile_fits(t, IC, OC, K, K, s, p):
+            continue
+        announce(f"tile {t} shape {shape}")
+        got = conv_gpu(x, w, b, res, s, p, True, tile=t)
+        for c in range(B):
+            ok, ratio, rel = close_report(got[c].astype(np.float32).transpose(2, 0, 1), refs[c], CONV_RTOL,
+                                          CONV_ATOL_RMS)
+            assert ok and rel <= 2e-3, f"tile {t} clip {c}: ratio {ratio:.3f} rel {rel:.2e}"
+        n += 1
+    assert n >= 2
+
+
 def test_conv_invariants_delta_and_zero():
     rng = np.random.default_rng(9)
     x = rng.standard_normal((2, 6, 70, 32)).astype(np.float16)

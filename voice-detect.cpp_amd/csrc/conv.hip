@@ -16,6 +16,8 @@
 //
 // stem_conv3x3_kernel: the IC=1 stem (K = 9 is too short for MFMA); one
 // thread per output pixel computes all OC channels in f32 from f32 features.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "vdk.h"
 
@@ -29,7 +31,8 @@ struct ConvArgs {
     const half_t* res;
     half_t* y;
     int H, W, IC, Ho, Wo, OC, KH, KW, stride, pad, relu;
-    int npix;  // B * Ho * Wo
+    int npix;     // B * Ho * Wo
+    int npix_in;  // B * H * W
 };
 
 // Spread consecutive workgroup ids over the 8 XCDs in contiguous ranges so that
@@ -44,12 +47,14 @@ template <int BM, int BN, int WM, int WN, int KC>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(ConvArgs a) {
     constexpr int NWM = BM / WM, NWN = BN / WN, NT = NWM * NWN * 64;
     constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int LDK = KC + 8;           // +16 bytes per LDS row
+    constexpr int LDK = KC + 8;           // +16 bytes per LDS row: conflict-free operand reads
     constexpr int CPR = KC / 8;           // 16-byte chunks per row
     constexpr int XCH = (BN * CPR + NT - 1) / NT;
+    constexpr int WCH = (BM * CPR + NT - 1) / NT;
     static_assert(WM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0, "tile shape");
-    __shared__ __attribute__((aligned(16))) half_t sW[BM * LDK];
-    __shared__ __attribute__((aligned(16))) half_t sX[BN * LDK];
+    // two LDS stages: chunk k is read from stage k&1 while chunk k+1 is written to the other
+    __shared__ __attribute__((aligned(16))) half_t sW[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) half_t sX[2][BN * LDK];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % NWM, wn = wave / NWM;
@@ -57,16 +62,19 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
     const int oc0 = blockIdx.y * BM;
     const int HoWo = a.Ho * a.Wo;
     const int KHW = a.KH * a.KW;
+    const int nc = a.IC / KC;
+    const int nk = KHW * nc;
 
-    // Each thread loads the same pixel rows for every K chunk: decode them once.
+    // Each thread loads the same pixel rows / weight rows for every K chunk: decode once.
     int x_img[XCH], x_ih[XCH], x_iw[XCH], x_lds[XCH], x_c[XCH];
-    bool x_on[XCH];
+    bool x_on[XCH], x_row[XCH];
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
         const int q = tid + i * NT;
         const int r = q / CPR, c8 = q - r * CPR;
         const int P = p0 + r;
-        x_on[i] = q < BN * CPR && P < a.npix;
+        x_row[i] = q < BN * CPR;
+        x_on[i] = x_row[i] && P < a.npix;
         const int Pc = x_on[i] ? P : 0;
         const int b = Pc / HoWo, rem = Pc - b * HoWo;
         const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
@@ -76,6 +84,43 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         x_lds[i] = r * LDK + c8 * 8;
         x_c[i] = c8 * 8;
     }
+    const half_t* w_src[WCH];
+    int w_lds[WCH];
+    bool w_on[WCH];
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) {
+        const int q = tid + i * NT;
+        const int r = q / CPR, c8 = q - r * CPR;
+        w_on[i] = q < BM * CPR;
+        w_src[i] = a.w + (size_t)(oc0 + (w_on[i] ? r : 0)) * KHW * a.IC + c8 * 8;
+        w_lds[i] = r * LDK + c8 * 8;
+    }
+
+    const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+    half8 xr[XCH], wr[WCH];
+    auto fetch = [&](int k) {
+        const int tap = k / nc, c0 = (k - tap * nc) * KC;
+        const int kh = tap / a.KW, kw = tap - kh * a.KW;
+#pragma unroll
+        for (int i = 0; i < WCH; ++i)
+            if (w_on[i]) wr[i] = *reinterpret_cast<const half8*>(w_src[i] + (size_t)tap * a.IC + c0);
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+            const int ih = x_ih[i] + kh, iw = x_iw[i] + kw;
+            xr[i] = zero8;
+            if (x_on[i] && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
+                xr[i] = *reinterpret_cast<const half8*>(a.x + ((size_t)(x_img[i] + ih) * a.W + iw) * a.IC + c0 +
+                                                        x_c[i]);
+        }
+    };
+    auto stash = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < WCH; ++i)
+            if (w_on[i]) *reinterpret_cast<half8*>(&sW[st][w_lds[i]]) = wr[i];
+#pragma unroll
+        for (int i = 0; i < XCH; ++i)
+            if (x_row[i]) *reinterpret_cast<half8*>(&sX[st][x_lds[i]]) = xr[i];
+    };
 
     float16v acc[TM][TN];
 #pragma unroll
@@ -85,46 +130,30 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int tap = 0; tap < KHW; ++tap) {
-        const int kh = tap / a.KW, kw = tap - kh * a.KW;
-        for (int c0 = 0; c0 < a.IC; c0 += KC) {
-            for (int q = tid; q < BM * CPR; q += NT) {
-                const int r = q / CPR, c8 = q - r * CPR;
-                const half8 v = *reinterpret_cast<const half8*>(
-                    a.w + ((size_t)(oc0 + r) * KHW + tap) * a.IC + c0 + c8 * 8);
-                *reinterpret_cast<half8*>(sW + r * LDK + c8 * 8) = v;
-            }
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int k = 0; k < nk; ++k) {
+        const int st = k & 1;
+        if (k + 1 < nk) fetch(k + 1);     // global loads in flight during this chunk's MFMAs
 #pragma unroll
-            for (int i = 0; i < XCH; ++i) {
-                if (tid + i * NT < BN * CPR) {
-                    const int ih = x_ih[i] + kh, iw = x_iw[i] + kw;
-                    half8 v = zero8;
-                    if (x_on[i] && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
-                        v = *reinterpret_cast<const half8*>(
-                            a.x + ((size_t)(x_img[i] + ih) * a.W + iw) * a.IC + c0 + x_c[i]);
-                    *reinterpret_cast<half8*>(sX + x_lds[i]) = v;
-                }
-            }
-            __syncthreads();
+        for (int kk = 0; kk < KC / 16; ++kk) {
+            half8 af[TM], bf[TN];
+            const int koff = kk * 16 + (lane >> 5) * 8;
 #pragma unroll
-            for (int kk = 0; kk < KC / 16; ++kk) {
-                half8 af[TM], bf[TN];
-                const int koff = kk * 16 + (lane >> 5) * 8;
+            for (int i = 0; i < TM; ++i)
+                af[i] = *reinterpret_cast<const half8*>(&sW[st][(wm * WM + i * 32 + (lane & 31)) * LDK + koff]);
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
-                    af[i] = *reinterpret_cast<const half8*>(sW + (wm * WM + i * 32 + (lane & 31)) * LDK + koff);
+            for (int j = 0; j < TN; ++j)
+                bf[j] = *reinterpret_cast<const half8*>(&sX[st][(wn * WN + j * 32 + (lane & 31)) * LDK + koff]);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    bf[j] = *reinterpret_cast<const half8*>(sX + (wn * WN + j * 32 + (lane & 31)) * LDK + koff);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
-            __syncthreads();
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
+        if (k + 1 < nk) stash(st ^ 1);
+        __syncthreads();
     }
 
     // Epilogue.  32x32 accumulator layout: register r of lane l holds
@@ -160,6 +189,367 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// conv_dma_kernel: the same implicit GEMM with the operand tiles moved
+// HBM/L2 -> LDS by buffer_load_dwordx4 ... lds (no VGPR staging, no ds_write).
+//  * Buffer loads return zero past the end of the buffer, so padding taps are
+//    fetched from an out-of-range offset instead of being branched around.
+//  * Tap and channel-chunk offsets are wave-uniform (SGPR soffset); each lane
+//    keeps one precomputed voffset per slot it fills.
+//  * LDS rows are unpadded (KC*2 bytes); the 16-byte chunk c of row r lives at
+//    slot c ^ key(r), so the MFMA operand reads (32 rows, one chunk column)
+//    touch distinct banks.  A DMA instruction fills 64 consecutive slots, so a
+//    lane picks the global chunk that belongs in its slot.
+//  * Two LDS stages; chunk k+1 is in flight while chunk k feeds the MFMAs; one
+//    barrier per chunk.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr uint32_t kOOB = 0x80000000u;   // any offset >= num_records reads as zero
+
+template <int KC>
+__device__ __forceinline__ int swz(int r, int c) {
+    // gfx950 LDS serves a ds_read_b128 16 lanes (256 bytes, 64 banks) per
+    // cycle; an MFMA operand read has 16 lanes on 16 consecutive rows and one
+    // chunk column, so the key makes those 16 (row, chunk) pairs hit distinct
+    // 16-byte bank groups.  KC=64: 128-byte rows, key = (r/2) % 8.
+    // KC=32: 64-byte rows, key = (r/4) % 4.
+    if constexpr (KC == 64) return c ^ ((r >> 1) & 7);
+    else return c ^ ((r >> 2) & 3);
+}
+
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+    // s_waitcnt with vmcnt = n (6-bit field split [3:0] / [15:14]), expcnt and
+    // lgkmcnt left at their "no wait" maxima.
+    switch (n) {
+#define VDK_VM(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
+        VDK_VM(0) VDK_VM(1) VDK_VM(2) VDK_VM(3) VDK_VM(4) VDK_VM(5) VDK_VM(6) VDK_VM(7) VDK_VM(8)
+        VDK_VM(9) VDK_VM(10) VDK_VM(11) VDK_VM(12) VDK_VM(13) VDK_VM(14) VDK_VM(15) VDK_VM(16)
+        VDK_VM(18) VDK_VM(20) VDK_VM(24) VDK_VM(27) VDK_VM(28) VDK_VM(30) VDK_VM(32) VDK_VM(36) VDK_VM(40)
+        VDK_VM(42) VDK_VM(45) VDK_VM(48) VDK_VM(54) VDK_VM(56) VDK_VM(60)
+#undef VDK_VM
+        default: __builtin_amdgcn_s_waitcnt(0); break;
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int KC, int NST>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(ConvArgs a) {
+    constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int CPR = KC / 8;                    // 16-byte chunks per row
+    constexpr int RB = KC * 2;                     // bytes per LDS row
+    constexpr int ROWS = BM + BN;
+    constexpr int NINS = ROWS * CPR / 64;          // DMA instructions per stage
+    constexpr int IPW = (NINS + NW - 1) / NW;      // per wave; every wave issues exactly IPW
+    constexpr int STAGE = IPW * NW * 1024;         // padding instructions land past the tiles
+    static_assert(KC == 32 || KC == 64, "KC");
+    static_assert((ROWS * CPR) % 64 == 0, "whole DMA instructions per stage");
+    static_assert(BM % (64 / CPR) == 0, "weight rows fill whole DMA instructions");
+    static_assert(NST >= 2 && IPW * (NST - 2) <= 60, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % NWM, wn = wave / NWM;
+    const int p0 = xcd_swizzle(blockIdx.x, gridDim.x) * BN;
+    const int oc0 = blockIdx.y * BM;
+    const int HoWo = a.Ho * a.Wo;
+    const int KHW = a.KH * a.KW;
+    const int nc = a.IC / KC;
+    const int nk = KHW * nc;
+
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.x, 0, (int)((size_t)(a.npix_in) * a.IC * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.w, 0, (int)((size_t)a.OC * KHW * a.IC * 2), 0x00020000);
+
+    // Per DMA slot of this lane: weight rows keep a fixed voffset (the tap /
+    // chunk part is uniform); pixel rows keep the tap-0 offset and a mask of
+    // the taps that fall inside the image.
+    int s_off[IPW];
+    uint32_t s_mask[IPW];
+    bool s_is_w[IPW];
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+        const int ins = wave + j * NW;
+        const int p = ins * 64 + lane;
+        const int r = p / CPR, slot = p - r * CPR;
+        const int c = swz<KC>(r, slot);
+        // one instruction covers 64/CPR whole rows and BM is a multiple of
+        // that, so the weight/pixel split is per instruction (wave-uniform)
+        s_is_w[j] = ins * (64 / CPR) < BM;
+        s_mask[j] = 0;
+        if (ins >= NINS) {
+            s_off[j] = 0;   // padding instruction: zeros into the spare slots
+        } else if (s_is_w[j]) {
+            s_off[j] = ((oc0 + r) * KHW * a.IC + c * 8) * 2;
+        } else {
+            const int P = p0 + (r - BM);
+            s_off[j] = 0;   // rows past the end: mask 0, every tap reads zeros
+            if (P < a.npix) {
+                const int b = P / HoWo, rem = P - b * HoWo;
+                const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
+                const int ih0 = oh * a.stride - a.pad, iw0 = ow * a.stride - a.pad;
+                s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.IC + c * 8) * 2;
+                for (int kh = 0; kh < a.KH; ++kh)
+                    for (int kw = 0; kw < a.KW; ++kw) {
+                        const int ih = ih0 + kh, iw = iw0 + kw;
+                        if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W) s_mask[j] |= 1u << (kh * a.KW + kw);
+                    }
+            }
+        }
+    }
+
+    // Chunk cursor for the DMA side: tap (kh, kw) and channel offset c0,
+    // advanced incrementally (no divisions in the loop).
+    int f_tap = 0, f_kw = 0, f_c0 = 0, f_x = 0;   // f_x = byte offset of (kh, kw, c0) in the input
+    const int row_bytes = a.W * a.IC * 2;
+    auto issue = [&](int st) {
+        const int w_soff = (f_tap * a.IC + f_c0) * 2;
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) {
+            lds_void* dst = (lds_void*)(smem + st * STAGE + (wave + j * NW) * 1024);
+            if (s_is_w[j]) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, dst, 16, (uint32_t)s_off[j], w_soff, 0, 0);
+            } else {
+                const uint32_t off = ((s_mask[j] >> f_tap) & 1u) ? (uint32_t)(s_off[j] + f_x) : kOOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, off, 0, 0, 0);
+            }
+        }
+        f_c0 += KC;
+        f_x += KC * 2;
+        if (f_c0 == a.IC) {
+            f_c0 = 0;
+            ++f_tap;
+            if (++f_kw == a.KW) {
+                f_kw = 0;
+                f_x += row_bytes - a.KW * a.IC * 2;   // next kernel row
+            }
+        }
+    };
+
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    // prologue: NST-1 chunks in flight
+#pragma unroll
+    for (int k = 0; k < NST - 1; ++k)
+        if (k < nk) issue(k);
+    int st = 0;
+    for (int k = 0; k < nk; ++k) {
+        // chunk k has landed once at most (NST-2) younger chunks are outstanding
+        const int younger = nk - 1 - k < NST - 2 ? nk - 1 - k : NST - 2;
+        wait_vmcnt_le(younger * IPW);
+        // Plain barrier + LDS acquire fence.  __syncthreads() would add a
+        // release fence, which must drain every in-flight DMA stage
+        // (vmcnt(0)) and collapse the ring; this wave's own chunk-k DMA is
+        // already complete by the vmcnt wait above, and no ds_write precedes.
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        if (k + NST - 1 < nk) issue(st == 0 ? NST - 1 : st - 1);
+        const uint8_t* sa = smem + st * STAGE;
+        const uint8_t* sb = sa + BM * RB;
+#pragma unroll
+        for (int kk = 0; kk < KC / 16; ++kk) {
+            const int c = kk * 2 + lhalf;
+            half8 af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int r = wm * WM + i * 32 + lrow;
+                af[i] = *reinterpret_cast<const half8*>(sa + r * RB + swz<KC>(r, c) * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int r = wn * WN + j * 32 + lrow;
+                bf[j] = *reinterpret_cast<const half8*>(sb + r * RB + swz<KC>(r + BM, c) * 16);
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        st = st + 1 == NST ? 0 : st + 1;
+    }
+
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int P = p0 + wn * WN + j * 32 + lrow;
+        if (P >= a.npix) continue;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int oc = oc0 + wm * WM + i * 32 + g * 8 + lhalf * 4;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e] + (a.bias ? a.bias[oc + e] : 0.0f);
+                const size_t o = (size_t)P * a.OC + oc;
+                if (a.res) {
+                    const half4 r = *reinterpret_cast<const half4*>(a.res + o);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
+                }
+                if (a.relu) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
+                }
+                half4 h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) h[e] = (half_t)v[e];
+                *reinterpret_cast<half4*>(a.y + o) = h;
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int KC, int NST>
+void launch_dma(const ConvArgs& a, hipStream_t s) {
+    constexpr int NT = (BM / WM) * (BN / WN) * 64;
+    dim3 grid(cdiv(a.npix, BN), a.OC / BM);
+    hipLaunchKernelGGL((conv_dma_kernel<BM, BN, WM, WN, KC, NST>), grid, dim3(NT), 0, s, a);
+}
+
+// ---------------------------------------------------------------------------
+// conv3x3_halo_kernel: stride-1 3x3 conv for narrow layers (IC, OC <= 64).
+// A workgroup owns a TH x TW output tile of one image and OCB output
+// channels.  Per IC chunk it DMAs the (TH+2) x (TW+2) input halo and the
+// weights of all 9 taps into LDS once, then runs 9 * KC/16 MFMA k-steps per
+// barrier; each input pixel is fetched once per tile instead of once per tap.
+// An MFMA column block is 32 consecutive output columns of one tile row, so
+// its B operand for tap (kh, kw) is 32 consecutive halo pixels.
+// ---------------------------------------------------------------------------
+template <int OCB, int KC, int TH, int TW>
+__global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
+    constexpr int NW = 4;
+    constexpr int CPR = KC / 8, RB = KC * 2;
+    constexpr int HW = TW + 2, HH = TH + 2, HPIX = HH * HW;
+    constexpr int WROWS = 9 * OCB;                       // weight rows: (tap, oc)
+    constexpr int NBLK_N = TH * TW / 32, NBLK_M = OCB / 32;
+    constexpr int NBLK = NBLK_N * NBLK_M;                // 32x32 output blocks
+    static_assert(NBLK % NW == 0, "blocks split evenly over 4 waves");
+    constexpr int BPW = NBLK / NW;
+    constexpr int W_INS = WROWS * CPR / 64;              // DMA instructions for weights
+    constexpr int X_SLOTS = HPIX * CPR;
+    constexpr int X_INS = (X_SLOTS + 63) / 64;
+    static_assert((WROWS * CPR) % 64 == 0, "weight rows fill whole DMA instructions");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[(W_INS + X_INS) * 1024];
+    uint8_t* sw = smem;
+    uint8_t* sx = smem + W_INS * 1024;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tiles_w = (a.Wo + TW - 1) / TW, tiles_h = (a.Ho + TH - 1) / TH;
+    const int t = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int b = t / (tiles_h * tiles_w);
+    const int trem = t - b * tiles_h * tiles_w;
+    const int oh0 = (trem / tiles_w) * TH, ow0 = (trem % tiles_w) * TW;
+    const int oc0 = blockIdx.y * OCB;
+    const int nc = a.IC / KC;
+
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.x, 0, (int)((size_t)(a.npix_in) * a.IC * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.w, 0, (int)((size_t)a.OC * 9 * a.IC * 2), 0x00020000);
+
+    float16v acc[BPW];
+#pragma unroll
+    for (int q = 0; q < BPW; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[q][r] = 0.0f;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+
+    for (int ci = 0; ci < nc; ++ci) {
+        const int c0 = ci * KC;
+        // weights: LDS row (tap*OCB + oc) holds w[oc0+oc][tap][c0 .. c0+KC)
+        for (int ins = wave; ins < W_INS; ins += NW) {
+            const int p = ins * 64 + lane;
+            const int r = p / CPR, slot = p - r * CPR;
+            const int tap = r / OCB, oc = r - tap * OCB;
+            const uint32_t off = (uint32_t)((((oc0 + oc) * 9 + tap) * a.IC + c0 + swz<KC>(r, slot) * 8) * 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(sw + ins * 1024), 16, off, 0, 0, 0);
+        }
+        // input halo: LDS row (hr*HW + hc) holds x[b][oh0-1+hr][ow0-1+hc][c0 .. c0+KC)
+        for (int ins = wave; ins < X_INS; ins += NW) {
+            const int p = ins * 64 + lane;
+            const int r = p / CPR, slot = p - r * CPR;
+            uint32_t off = kOOB;
+            if (r < HPIX) {
+                const int hr = r / HW, hc = r - hr * HW;
+                const int ih = oh0 - 1 + hr, iw = ow0 - 1 + hc;
+                if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
+                    off = (uint32_t)((((b * a.H + ih) * a.W + iw) * a.IC + c0 + swz<KC>(r, slot) * 8) * 2);
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx + ins * 1024), 16, off, 0, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const int kh = tap / 3, kw = tap - kh * 3;
+#pragma unroll
+            for (int kk = 0; kk < KC / 16; ++kk) {
+                const int c = kk * 2 + lhalf;
+#pragma unroll
+                for (int q = 0; q < BPW; ++q) {
+                    const int blk = wave * BPW + q;
+                    const int mb = blk % NBLK_M, nb = blk / NBLK_M;
+                    const int orow = nb / (TW / 32), ocol = (nb % (TW / 32)) * 32 + lrow;
+                    const int wr = tap * OCB + mb * 32 + lrow;
+                    const int xrow = (orow + kh) * HW + ocol + kw;
+                    const half8 af = *reinterpret_cast<const half8*>(sw + wr * RB + swz<KC>(wr, c) * 16);
+                    const half8 bf = *reinterpret_cast<const half8*>(sx + xrow * RB + swz<KC>(xrow, c) * 16);
+                    acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[q], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int q = 0; q < BPW; ++q) {
+        const int blk = wave * BPW + q;
+        const int mb = blk % NBLK_M, nb = blk / NBLK_M;
+        const int oh = oh0 + nb / (TW / 32), ow = ow0 + (nb % (TW / 32)) * 32 + lrow;
+        if (oh >= a.Ho || ow >= a.Wo) continue;
+        const size_t P = ((size_t)b * a.Ho + oh) * a.Wo + ow;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int oc = oc0 + mb * 32 + g * 8 + lhalf * 4;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[q][g * 4 + e] + (a.bias ? a.bias[oc + e] : 0.0f);
+            const size_t o = P * a.OC + oc;
+            if (a.res) {
+                const half4 r = *reinterpret_cast<const half4*>(a.res + o);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
+            }
+            if (a.relu) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
+            }
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)v[e];
+            *reinterpret_cast<half4*>(a.y + o) = h;
+        }
+    }
+}
+
+template <int OCB, int KC, int TH, int TW>
+void launch_halo(const ConvArgs& a, hipStream_t s) {
+    const int B = a.npix / (a.Ho * a.Wo);
+    const int tiles = B * ((a.Ho + TH - 1) / TH) * ((a.Wo + TW - 1) / TW);
+    hipLaunchKernelGGL((conv3x3_halo_kernel<OCB, KC, TH, TW>), dim3(tiles, a.OC / OCB), dim3(256), 0, s, a);
+}
+
 template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
@@ -167,11 +557,85 @@ void launch_igemm(const ConvArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC>), grid, dim3(NT), 0, s, a);
 }
 
-template <int BM, int BN, int WM, int WN>
-void launch_kc(const ConvArgs& a, hipStream_t s) {
-    if (a.IC % 64 == 0) launch_igemm<BM, BN, WM, WN, 64>(a, s);
-    else if (a.IC % 32 == 0) launch_igemm<BM, BN, WM, WN, 32>(a, s);
-    else launch_igemm<BM, BN, WM, WN, 16>(a, s);
+struct TileCfg {
+    int bm, bn, kc;
+    void (*launch)(const ConvArgs&, hipStream_t);
+    bool halo;   // 3x3 stride-1 pad-1 only
+};
+
+// Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
+// 4 waves per workgroup; entries are selected per layer by pick_tile().
+const TileCfg kTiles[] = {
+    {32, 256, 32, launch_igemm<32, 256, 32, 64, 32>},     // 0: OC=32 layers
+    {64, 256, 32, launch_igemm<64, 256, 64, 64, 32>},     // 1
+    {64, 128, 32, launch_igemm<64, 128, 32, 64, 32>},     // 2
+    {128, 128, 32, launch_igemm<128, 128, 64, 64, 32>},   // 3
+    {128, 128, 64, launch_igemm<128, 128, 64, 64, 64>},   // 4
+    {128, 64, 32, launch_igemm<128, 64, 64, 32, 32>},     // 5
+    {128, 64, 64, launch_igemm<128, 64, 64, 32, 64>},     // 6
+    {128, 256, 32, launch_igemm<128, 256, 64, 128, 32>},  // 7
+    {256, 128, 32, launch_igemm<256, 128, 128, 64, 32>},  // 8
+    {64, 256, 32, launch_igemm<64, 256, 32, 128, 32>},    // 9
+    {32, 128, 32, launch_igemm<32, 128, 32, 32, 32>},     // 10
+    {32, 256, 16, launch_igemm<32, 256, 32, 64, 16>},     // 11: IC % 32 != 0
+    {64, 128, 16, launch_igemm<64, 128, 32, 64, 16>},     // 12
+    {128, 64, 16, launch_igemm<128, 64, 64, 32, 16>},     // 13
+    {32, 256, 32, launch_dma<32, 256, 32, 64, 32, 2>},    // 14: DMA ring variants
+    {64, 128, 64, launch_dma<64, 128, 32, 64, 64, 2>},    // 15
+    {64, 256, 32, launch_dma<64, 256, 64, 64, 32, 2>},    // 16
+    {128, 128, 64, launch_dma<128, 128, 64, 64, 64, 2>},  // 17
+    {128, 64, 64, launch_dma<128, 64, 64, 32, 64, 2>},    // 18
+    {128, 64, 64, launch_dma<128, 64, 64, 32, 64, 3>},    // 19
+    {256, 128, 64, launch_dma<256, 128, 128, 64, 64, 2>}, // 20
+    {64, 256, 64, launch_dma<64, 256, 64, 64, 64, 2>},    // 21
+    {32, 256, 32, launch_dma<32, 256, 32, 64, 32, 3>},    // 22
+    {64, 128, 64, launch_dma<64, 128, 32, 64, 64, 3>},    // 23
+    {64, 256, 32, launch_dma<64, 256, 64, 64, 32, 3>},    // 24
+    {128, 256, 64, launch_dma<128, 256, 64, 128, 64, 2>}, // 25
+    {32, 256, 32, launch_halo<32, 32, 4, 64>, true},      // 26: halo tiles
+    {32, 256, 32, launch_halo<32, 32, 8, 32>, true},      // 27
+    {32, 128, 32, launch_halo<32, 32, 4, 32>, true},      // 28
+    {32, 128, 64, launch_halo<32, 64, 4, 32>, true},      // 29
+    {64, 128, 32, launch_halo<64, 32, 4, 32>, true},      // 30
+    {64, 128, 64, launch_halo<64, 64, 2, 64>, true},      // 31
+    {32, 256, 64, launch_halo<32, 64, 4, 64>, true},      // 32
+};
+constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
+
+bool tile_fits(const TileCfg& t, const ConvArgs& a) {
+    if (t.halo && !(a.KH == 3 && a.KW == 3 && a.stride == 1 && a.pad == 1)) return false;
+    return a.OC % t.bm == 0 && a.IC % t.kc == 0;
+}
+
+// Optional override for tuning sweeps: VDK_CONV_TILE=<index into kTiles>.
+int tile_override() {
+    static const int v = [] {
+        const char* e = std::getenv("VDK_CONV_TILE");
+        return (e && *e) ? std::atoi(e) : -1;
+    }();
+    return v;
+}
+
+// Per-layer-class defaults, from a sweep of every ResNet34 conv shape at
+// batch 64 on MI355X (narrow 3x3 stride-1 layers: halo tiles; the rest:
+// DMA implicit GEMM with a 128-wide OC tile where the layer allows it).
+int pick_tile(const ConvArgs& a) {
+    const int o = tile_override();
+    if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
+    const bool s1_3x3 = a.KH == 3 && a.KW == 3 && a.stride == 1 && a.pad == 1;
+    if (s1_3x3 && a.OC == 32 && a.IC % 32 == 0 && a.IC <= 64) return 28;
+    if (s1_3x3 && a.OC == 64 && a.IC % 32 == 0 && a.IC <= 64) return 30;
+    if (a.IC % 64 == 0) {
+        if (a.OC % 128 == 0) return 18;
+        if (a.OC % 64 == 0) return 15;
+    } else if (a.IC % 32 == 0) {
+        if (a.OC % 64 == 0) return 16;
+        if (a.OC % 32 == 0) return 14;
+    }
+    if (a.IC % 32 != 0) return a.OC % 128 == 0 ? 13 : (a.OC % 64 == 0 ? 12 : 11);
+    if (a.OC % 128 == 0) return 5;
+    if (a.OC % 64 == 0) return 2;
+    return 10;
 }
 
 template <int OC>
@@ -218,10 +682,10 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 using namespace vdk;
 
-extern "C" int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC,
-                               const void* d_w, int OC, int KH, int KW, int stride, int pad,
-                               const float* d_bias, const void* d_residual, int relu,
-                               void* d_y, void* stream) {
+namespace {
+int conv_impl(const void* d_x, int batch, int H, int W, int IC, const void* d_w, int OC, int KH, int KW,
+              int stride, int pad, const float* d_bias, const void* d_residual, int relu, void* d_y, void* stream,
+              int tile) {
     return guarded([&] {
         require(d_x && d_w && d_y, "conv2d: NULL device pointer");
         require(batch > 0 && H > 0 && W > 0, "conv2d: empty input");
@@ -244,17 +708,41 @@ extern "C" int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC,
         a.H = H; a.W = W; a.IC = IC; a.Ho = Ho; a.Wo = Wo; a.OC = OC;
         a.KH = KH; a.KW = KW; a.stride = stride; a.pad = pad; a.relu = relu ? 1 : 0;
         a.npix = batch * Ho * Wo;
+        a.npix_in = batch * H * W;
         hipStream_t s = static_cast<hipStream_t>(stream);
-        if (OC % 128 == 0) {
-            if (a.npix >= 64 * 1024) launch_kc<128, 128, 64, 64>(a, s);
-            else launch_kc<128, 64, 64, 32>(a, s);
-        } else if (OC % 64 == 0) {
-            launch_kc<64, 128, 32, 64>(a, s);
+        int t = tile;
+        if (t < 0) {
+            t = pick_tile(a);
         } else {
-            launch_kc<32, 256, 32, 64>(a, s);
+            require(t < kNumTiles, "conv2d: tile index out of range");
+            require(tile_fits(kTiles[t], a), "conv2d: tile " + std::to_string(t) + " does not fit this shape");
         }
+        kTiles[t].launch(a, s);
         VDK_HIP(hipGetLastError());
     });
+}
+
+}  // namespace
+
+extern "C" int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC, const void* d_w, int OC, int KH,
+                               int KW, int stride, int pad, const float* d_bias, const void* d_residual, int relu,
+                               void* d_y, void* stream) {
+    return conv_impl(d_x, batch, H, W, IC, d_w, OC, KH, KW, stride, pad, d_bias, d_residual, relu, d_y, stream, -1);
+}
+
+extern "C" int vdk_conv2d_nhwc_tile(const void* d_x, int batch, int H, int W, int IC, const void* d_w, int OC,
+                                    int KH, int KW, int stride, int pad, const float* d_bias, const void* d_residual,
+                                    int relu, void* d_y, void* stream, int tile) {
+    return conv_impl(d_x, batch, H, W, IC, d_w, OC, KH, KW, stride, pad, d_bias, d_residual, relu, d_y, stream, tile);
+}
+
+extern "C" int vdk_conv2d_tile_count(void) { return kNumTiles; }
+
+extern "C" int vdk_conv2d_tile_fits(int tile, int IC, int OC, int KH, int KW, int stride, int pad) {
+    if (tile < 0 || tile >= kNumTiles) return 0;
+    ConvArgs a{};
+    a.IC = IC; a.OC = OC; a.KH = KH; a.KW = KW; a.stride = stride; a.pad = pad;
+    return tile_fits(kTiles[tile], a) ? 1 : 0;
 }
 
 extern "C" int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,

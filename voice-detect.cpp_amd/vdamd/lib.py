@@ -76,6 +76,10 @@ _SIGS = {
     "vdk_fbank": (C.c_int, [C.POINTER(FbankCfg), _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_conv2d_nhwc": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
                                   C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp]),
+    "vdk_conv2d_nhwc_tile": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int]),
+    "vdk_conv2d_tile_count": (C.c_int, []),
+    "vdk_conv2d_tile_fits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "vdk_stem_conv3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_tstp": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "vdk_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp]),
