@@ -107,10 +107,14 @@ int vdk_tstp(const void* d_x, int batch, int H, int W, int C, float eps,
 
 /* ---- embedding FC ----
  * Replaces the seg_1 mul_mat + bias - mean_vec of src/encoder_resnet.cpp:159-169:
- * y[b] = w x[b] + bias - mean_vec; w [out][in] f32; bias/mean_vec may be NULL. */
+ * y[b] = w x[b] + bias - mean_vec; w [out][in] f32; bias/mean_vec may be NULL.
+ * d_work: caller-provided device workspace of at least
+ * vdk_linear_workspace_size(batch, in_dim, out_dim) bytes (split-K partials;
+ * the result is bitwise reproducible). */
+size_t vdk_linear_workspace_size(int batch, int in_dim, int out_dim);
 int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w,
                const float* d_bias, const float* d_mean_vec, int out_dim,
-               float* d_y, void* stream);
+               float* d_y, void* d_work, size_t work_bytes, void* stream);
 
 /* ---- L2 normalisation ----
  * Replaces the host L2 of src/encoder_resnet.cpp:177-183 (double accumulation,

@@ -238,7 +238,10 @@ def test_tstp_linear_l2_match_oracle():
     mv = rng.standard_normal(E).astype(np.float32) * 0.05
     dw, db, dm = (lib.DeviceBuffer.from_array(a) for a in (wfc, bfc, mv))
     dy = lib.DeviceBuffer(B * E * 4)
-    lib.check(L.vdk_linear(dp.ptr, B, P, dw.ptr, db.ptr, dm.ptr, E, dy.ptr, None))
+    wsz = L.vdk_linear_workspace_size(B, P, E)
+    dwk = lib.DeviceBuffer(wsz)
+    assert L.vdk_linear(dp.ptr, B, P, dw.ptr, db.ptr, dm.ptr, E, dy.ptr, dwk.ptr, wsz - 4, None) != 0
+    lib.check(L.vdk_linear(dp.ptr, B, P, dw.ptr, db.ptr, dm.ptr, E, dy.ptr, dwk.ptr, wsz, None))
     lib.check(L.vdk_synchronize())
     pooled = dp.to_array(np.float32, (B, P))
     pre = dy.to_array(np.float32, (B, E))

@@ -643,8 +643,17 @@ __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restri
                                                            const float* __restrict__ w,
                                                            const float* __restrict__ bias, int relu,
                                                            half_t* __restrict__ y) {
-    const long P = (long)blockIdx.x * 256 + threadIdx.x;
+    // OC/8 threads per output pixel, 8 channels each: the OC/8 lanes of a pixel
+    // write its OC*2 bytes as consecutive 16-byte chunks.
+    constexpr int G = OC / 8;
+    __shared__ float sw[OC * 9], sb[OC];
+    for (int i = threadIdx.x; i < OC * 9; i += 256) sw[i] = w[i];
+    for (int i = threadIdx.x; i < OC; i += 256) sb[i] = bias[i];
+    __syncthreads();
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
     const long HW = (long)H * W;
+    const long P = idx / G;
+    const int g = (int)(idx - P * G);
     if (P >= (long)B * HW) return;
     const int b = (int)(P / HW);
     const int rem = (int)(P - (long)b * HW);
@@ -657,22 +666,18 @@ __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restri
             const int ih = h - 1 + kh, iw = t - 1 + kw;
             xv[kh * 3 + kw] = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? feats[((long)b * H + ih) * W + iw] : 0.0f;
         }
-    half_t* out = y + P * OC;
+    half8 hv;
 #pragma unroll
-    for (int o8 = 0; o8 < OC / 8; ++o8) {
-        half8 hv;
+    for (int e = 0; e < 8; ++e) {
+        const int oc = g * 8 + e;
+        float acc = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int oc = o8 * 8 + e;
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 9; ++k) acc += w[oc * 9 + k] * xv[k];
-            float v = acc + bias[oc];
-            if (relu) v = v > 0.0f ? v : 0.0f;
-            hv[e] = (half_t)v;
-        }
-        *reinterpret_cast<half8*>(out + o8 * 8) = hv;
+        for (int k = 0; k < 9; ++k) acc += sw[oc * 9 + k] * xv[k];
+        float v = acc + sb[oc];
+        if (relu) v = v > 0.0f ? v : 0.0f;
+        hv[e] = (half_t)v;
     }
+    *reinterpret_cast<half8*>(y + P * OC + g * 8) = hv;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -754,7 +759,8 @@ extern "C" int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,
         require((long)batch * H * W < (1L << 31), "stem: too many pixels for one launch");
         require(aligned16(d_y), "stem: output must be 16-byte aligned");
         hipStream_t s = static_cast<hipStream_t>(stream);
-        const long n = (long)batch * H * W;
+        const long n = (long)batch * H * W * (OC / 8);
+        require(n < (1L << 31), "stem: too many pixels for one launch");
         dim3 grid(cdiv(n, 256));
         half_t* y = static_cast<half_t*>(d_y);
         switch (OC) {

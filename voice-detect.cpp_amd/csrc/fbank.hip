@@ -27,15 +27,10 @@ constexpr int kFbMaxWaves = 4;   // frames (wavefronts) per workgroup at n_fft <
 constexpr double kPi = 3.14159265358979323846;
 
 struct FbankDev {
-    const double* window;   // [win]
-    const double* tw_re;    // [n_fft/2]  cos(-2 pi j / n_fft)
-    const double* tw_im;    // [n_fft/2]  sin(-2 pi j / n_fft)
-    const int* mel_start;   // [n_mels] first non-zero bin
-    const int* mel_len;     // [n_mels] number of non-zero bins
-    const int* mel_off;     // [n_mels] offset into mel_w
-    const double* mel_w;    // packed non-zero filter weights
+    // byte offsets of the tables inside the table block (copied to LDS)
+    int off_window, off_tw_re, off_tw_im, off_mel_start, off_mel_len, off_mel_off, off_mel_w;
     int n_mels, n_fft, log2n, pow2, win, hop, T, n_samples;
-    int waves;              // frames per workgroup (LDS stays <= 40 KB)
+    int waves;              // frames processed concurrently per workgroup (one per wavefront)
     float preemph;
 };
 
@@ -111,87 +106,266 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-__global__ __launch_bounds__(kFbMaxWaves * 64) void fbank_frames_kernel(FbankDev p, const float* __restrict__ pcm,
+// Wavefront-scope LDS ordering: one wave owns one frame, so the FFT stages
+// need no workgroup barrier, only program order on the LDS accesses.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One workgroup copies the constant tables (window, twiddles, packed mel
+// filters; `tab_bytes` from the host layout) into LDS once, then each of its
+// wavefronts processes `fpw` consecutive frames.
+__global__ __launch_bounds__(kFbMaxWaves * 64) void fbank_frames_kernel(FbankDev p, const uint8_t* __restrict__ tables,
+                                                                     int tab_bytes, int fpw,
+                                                                     const float* __restrict__ pcm,
                                                                      float* __restrict__ feats) {
 #pragma clang fp contract(off)
     extern __shared__ double smem[];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int t = blockIdx.x * p.waves + wave;
-    const int b = blockIdx.y;
-    const bool valid = t < p.T;
-    const int nfft = p.n_fft;
-    double* re = smem + (size_t)wave * 2 * nfft;
-    double* im = re + nfft;
-    float* raw = reinterpret_cast<float*>(smem + (size_t)p.waves * 2 * nfft) + (size_t)wave * nfft;
+    uint8_t* tab = reinterpret_cast<uint8_t*>(smem);
+    for (int i = threadIdx.x * 16; i < tab_bytes; i += blockDim.x * 16)
+        *reinterpret_cast<uint4*>(tab + i) = *reinterpret_cast<const uint4*>(tables + i);
+    __syncthreads();
+    const double* window = reinterpret_cast<const double*>(tab + p.off_window);
+    const double* tw_re = reinterpret_cast<const double*>(tab + p.off_tw_re);
+    const double* tw_im = reinterpret_cast<const double*>(tab + p.off_tw_im);
+    const int* mel_start = reinterpret_cast<const int*>(tab + p.off_mel_start);
+    const int* mel_len = reinterpret_cast<const int*>(tab + p.off_mel_len);
+    const int* mel_off = reinterpret_cast<const int*>(tab + p.off_mel_off);
+    const double* mel_w = reinterpret_cast<const double*>(tab + p.off_mel_w);
 
-    const float* src = pcm + (size_t)b * p.n_samples + (size_t)(valid ? t : 0) * p.hop;
-    // remove_dc_offset: double sum of the frame (src/fbank.cpp:170-174)
-    double s = 0.0;
-    if (valid)
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = blockIdx.y;
+    const int nfft = p.n_fft, half = nfft >> 1;
+    double* re = smem + tab_bytes / 8 + (size_t)wave * (2 * nfft + nfft / 2);
+    double* im = re + nfft;
+    float* raw = reinterpret_cast<float*>(im + nfft);
+
+    for (int f = 0; f < fpw; ++f) {
+        const int t = (blockIdx.x * p.waves + wave) * fpw + f;
+        if (t >= p.T) break;                       // uniform per wavefront
+        const float* src = pcm + (size_t)b * p.n_samples + (size_t)t * p.hop;
+        // remove_dc_offset: double sum of the frame (src/fbank.cpp:170-174)
+        double s = 0.0;
         for (int i = lane; i < p.win; i += 64) s += (double)src[i];
-    s = wave_sum(s);
-    const float mean = (float)(s / p.win);
-    for (int i = lane; i < p.win; i += 64) raw[i] = valid ? src[i] - mean : 0.0f;
-    __syncthreads();
-    // pre-emphasis with replicate padding, window in double, zero pad, and the
-    // bit-reversed placement of the FFT input (src/fbank.cpp:176-183)
-    for (int i = lane; i < nfft; i += 64) {
-        float v = 0.0f;
-        if (i < p.win) {
-            const float cur = raw[i];
-            const float prev = raw[i > 0 ? i - 1 : 0];
-            const float y = cur - p.preemph * prev;
-            v = (float)((double)y * p.window[i]);
-        }
-        const int j = p.pow2 ? (int)(__builtin_bitreverse32((unsigned)i) >> (32 - p.log2n)) : i;
-        re[j] = (double)v;
-        im[j] = 0.0;
-    }
-    __syncthreads();
-    const int half = nfft >> 1;
-    if (p.pow2) {
-        // iterative radix-2 decimation in time; every butterfly of a stage is independent
-        for (int lg = 1; lg <= p.log2n; ++lg) {
-            const int h = 1 << (lg - 1);
-            const int tws = nfft >> lg;            // twiddle stride n_fft / len
-            for (int q = lane; q < half; q += 64) {
-                const int pos = q & (h - 1);
-                const int a = ((q >> (lg - 1)) << lg) + pos, c = a + h;
-                const double wr = p.tw_re[pos * tws], wi = p.tw_im[pos * tws];
-                const double xr = wr * re[c] - wi * im[c];
-                const double xi = wr * im[c] + wi * re[c];
-                re[c] = re[a] - xr;
-                im[c] = im[a] - xi;
-                re[a] = re[a] + xr;
-                im[a] = im[a] + xi;
+        s = wave_sum(s);
+        const float mean = (float)(s / p.win);
+        for (int i = lane; i < p.win; i += 64) raw[i] = src[i] - mean;
+        wave_sync();
+        // pre-emphasis with replicate padding, window in double, zero pad, and
+        // the bit-reversed placement of the FFT input (src/fbank.cpp:176-183)
+        for (int i = lane; i < nfft; i += 64) {
+            float v = 0.0f;
+            if (i < p.win) {
+                const float cur = raw[i];
+                const float prev = raw[i > 0 ? i - 1 : 0];
+                const float y = cur - p.preemph * prev;
+                v = (float)((double)y * window[i]);
             }
-            __syncthreads();
+            const int j = p.pow2 ? (int)(__builtin_bitreverse32((unsigned)i) >> (32 - p.log2n)) : i;
+            re[j] = (double)v;
+            im[j] = 0.0;
         }
-        for (int k = lane; k <= half; k += 64) {
-            const double r = re[k], i2 = im[k];
-            im[k] = r * r + i2 * i2;                 // power spectrum into im[]
-        }
-    } else {
-        // naive DFT for non power-of-two sizes (src/fbank.cpp:97-107)
-        for (int k = lane; k <= half; k += 64) {
-            double r = 0.0, i2 = 0.0;
-            for (int n = 0; n < nfft; ++n) {
-                const double a = -2.0 * kPi * k * n / nfft;
-                r += re[n] * cos(a);
-                i2 += re[n] * sin(a);
+        wave_sync();
+        if (p.pow2) {
+            // iterative radix-2 decimation in time; a stage's butterflies are independent
+            for (int lg = 1; lg <= p.log2n; ++lg) {
+                const int h = 1 << (lg - 1);
+                const int tws = nfft >> lg;            // twiddle stride n_fft / len
+                for (int q = lane; q < half; q += 64) {
+                    const int pos = q & (h - 1);
+                    const int a = ((q >> (lg - 1)) << lg) + pos, c = a + h;
+                    const double wr = tw_re[pos * tws], wi = tw_im[pos * tws];
+                    const double xr = wr * re[c] - wi * im[c];
+                    const double xi = wr * im[c] + wi * re[c];
+                    const double ar = re[a], ai = im[a];
+                    re[c] = ar - xr;
+                    im[c] = ai - xi;
+                    re[a] = ar + xr;
+                    im[a] = ai + xi;
+                }
+                wave_sync();
             }
-            im[k] = r * r + i2 * i2;
+            for (int k = lane; k <= half; k += 64) {
+                const double r = re[k], i2 = im[k];
+                im[k] = r * r + i2 * i2;                 // power spectrum into im[]
+            }
+        } else {
+            // naive DFT for non power-of-two sizes (src/fbank.cpp:97-107)
+            for (int k = lane; k <= half; k += 64) {
+                double r = 0.0, i2 = 0.0;
+                for (int n = 0; n < nfft; ++n) {
+                    const double a = -2.0 * kPi * k * n / nfft;
+                    r += re[n] * cos(a);
+                    i2 += re[n] * sin(a);
+                }
+                im[k] = r * r + i2 * i2;
+            }
         }
+        wave_sync();
+        const double* ps = im;
+        for (int m = lane; m < p.n_mels; m += 64) {
+            double e = 0.0;
+            const int st = mel_start[m], n = mel_len[m];
+            const double* w = mel_w + mel_off[m];
+            for (int k = 0; k < n; ++k) e += w[k] * ps[st + k];
+            const double fl = (double)FLT_EPSILON;
+            feats[((size_t)b * p.n_mels + m) * p.T + t] = (float)log(e > fl ? e : fl);
+        }
+        wave_sync();
     }
+}
+
+// ---------------------------------------------------------------------------
+// 512-point path (the size every speaker encoder uses): a register-resident
+// radix-8 FFT.  With n = a + 64 b and k = c + 8 d (a in [0,64), b, c in [0,8)):
+//   X[c + 8 d] = sum_a W64^(a d) * W512^(a c) * sum_b x[a + 64 b] W8^(b c)
+// and the 64-point DFT over a = a0 + 8 a1, d = d0 + 8 d1 splits the same way.
+// Lane a does the first 8-point DFT on its 8 samples; two LDS exchanges
+// (rows padded so each 16-lane group of a ds_*_b128 hits distinct banks) hand
+// the next 8-point DFTs to lane (c, a0) and then lane (c, d0), which ends up
+// holding X[c + 8 d0 + 64 d1] for d1 = 0..7.
+// ---------------------------------------------------------------------------
+struct cplx {
+    double r, i;
+};
+
+__device__ __forceinline__ cplx cmul(cplx a, cplx b) { return {a.r * b.r - a.i * b.i, a.r * b.i + a.i * b.r}; }
+
+// In-place 8-point DFT, natural order in and out: X[k] = sum_n x[n] W8^(n k).
+__device__ __forceinline__ void dft8(cplx* x) {
+    const double h = 0.70710678118654752440;   // sqrt(2)/2
+    // radix-2 DIT on bit-reversed input order
+    cplx v[8] = {x[0], x[4], x[2], x[6], x[1], x[5], x[3], x[7]};
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        const cplx a = v[j], b = v[j + 1];
+        v[j] = {a.r + b.r, a.i + b.i};
+        v[j + 1] = {a.r - b.r, a.i - b.i};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j += 4) {
+        const cplx a0 = v[j], b0 = v[j + 2];
+        v[j] = {a0.r + b0.r, a0.i + b0.i};
+        v[j + 2] = {a0.r - b0.r, a0.i - b0.i};
+        const cplx a1 = v[j + 1], b1 = {v[j + 3].i, -v[j + 3].r};   // * W4^1 = -i
+        v[j + 1] = {a1.r + b1.r, a1.i + b1.i};
+        v[j + 3] = {a1.r - b1.r, a1.i - b1.i};
+    }
+    const cplx w1 = {h, -h}, w3 = {-h, -h};
+    const cplx t0 = v[4], t1 = cmul(v[5], w1), t2 = {v[6].i, -v[6].r}, t3 = cmul(v[7], w3);
+    x[0] = {v[0].r + t0.r, v[0].i + t0.i};
+    x[4] = {v[0].r - t0.r, v[0].i - t0.i};
+    x[1] = {v[1].r + t1.r, v[1].i + t1.i};
+    x[5] = {v[1].r - t1.r, v[1].i - t1.i};
+    x[2] = {v[2].r + t2.r, v[2].i + t2.i};
+    x[6] = {v[2].r - t2.r, v[2].i - t2.i};
+    x[3] = {v[3].r + t3.r, v[3].i + t3.i};
+    x[7] = {v[3].r - t3.r, v[3].i - t3.i};
+}
+
+constexpr int kX1 = 72;   // exchange-1 row stride (complex): row c, column a
+constexpr int kX2 = 9;    // exchange-2: index c * 72 + d0 * 9 + a0
+
+__global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, const uint8_t* __restrict__ tables,
+                                                                   int tab_bytes, int fpw,
+                                                                   const float* __restrict__ pcm,
+                                                                   float* __restrict__ feats) {
+#pragma clang fp contract(off)
+    extern __shared__ double smem[];
+    uint8_t* tab = reinterpret_cast<uint8_t*>(smem);
+    for (int i = threadIdx.x * 16; i < tab_bytes; i += blockDim.x * 16)
+        *reinterpret_cast<uint4*>(tab + i) = *reinterpret_cast<const uint4*>(tables + i);
     __syncthreads();
-    const double* ps = im;
-    for (int m = lane; m < p.n_mels; m += 64) {
-        double e = 0.0;
-        const int st = p.mel_start[m], n = p.mel_len[m];
-        const double* w = p.mel_w + p.mel_off[m];
-        for (int k = 0; k < n; ++k) e += w[k] * ps[st + k];
-        const double fl = (double)FLT_EPSILON;
-        if (valid) feats[((size_t)b * p.n_mels + m) * p.T + t] = (float)log(e > fl ? e : fl);
+    const double* window = reinterpret_cast<const double*>(tab + p.off_window);
+    const double* tw_re = reinterpret_cast<const double*>(tab + p.off_tw_re);   // cos(-2 pi j / 512)
+    const double* tw_im = reinterpret_cast<const double*>(tab + p.off_tw_im);
+    const int* mel_start = reinterpret_cast<const int*>(tab + p.off_mel_start);
+    const int* mel_len = reinterpret_cast<const int*>(tab + p.off_mel_len);
+    const int* mel_off = reinterpret_cast<const int*>(tab + p.off_mel_off);
+    const double* mel_w = reinterpret_cast<const double*>(tab + p.off_mel_w);
+
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = blockIdx.y;
+    cplx* xch = reinterpret_cast<cplx*>(smem + tab_bytes / 8) + (size_t)wave * (8 * kX1);
+    double* ps = reinterpret_cast<double*>(xch);   // reused after the last exchange (257 bins)
+
+    // per-lane twiddles, constant over frames: W512^(a c) for lane a and
+    // W64^(a0 d0) = W512^(8 a0 d0) for lane (c, a0) = (lane / 8, lane % 8)
+    cplx tw1[8], tw2[8];
+    const int a0 = lane & 7, cl = lane >> 3;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int j1 = (lane * c) & 511, j2 = (8 * a0 * c) & 511;
+        tw1[c] = {j1 < 256 ? tw_re[j1] : -tw_re[j1 - 256], j1 < 256 ? tw_im[j1] : -tw_im[j1 - 256]};
+        tw2[c] = {j2 < 256 ? tw_re[j2] : -tw_re[j2 - 256], j2 < 256 ? tw_im[j2] : -tw_im[j2 - 256]};
+    }
+
+    for (int f = 0; f < fpw; ++f) {
+        const int t = (blockIdx.x * p.waves + wave) * fpw + f;
+        if (t >= p.T) break;                       // uniform per wavefront
+        const float* src = pcm + (size_t)b * p.n_samples + (size_t)t * p.hop;
+        // samples n = lane + 64 j; DC removal with a double sum (src/fbank.cpp:170-174)
+        float xs[8];
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int n = lane + 64 * j;
+            xs[j] = n < p.win ? src[n] : 0.0f;
+            s += (double)xs[j];
+        }
+        s = wave_sum(s);
+        const float mean = (float)(s / p.win);
+        // pre-emphasis (replicate at n = 0) and povey window (src/fbank.cpp:176-183)
+        cplx v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int n = lane + 64 * j;
+            double y = 0.0;
+            if (n < p.win) {
+                const float cur = xs[j] - mean;
+                const float prev = (n > 0 ? src[n - 1] : src[0]) - mean;
+                const float e = cur - p.preemph * prev;
+                y = (double)(float)((double)e * window[n]);
+            }
+            v[j] = {y, 0.0};
+        }
+        // pass 1: 8-point DFT over b, twiddle W512^(a c); store row c, column a
+        dft8(v);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) xch[c * kX1 + lane] = cmul(v[c], tw1[c]);
+        wave_sync();
+        // pass 2: lane (c, a0) gathers a = a0 + 8 a1, DFT over a1 -> d0, twiddle W64^(a0 d0)
+#pragma unroll
+        for (int a1 = 0; a1 < 8; ++a1) v[a1] = xch[cl * kX1 + a0 + 8 * a1];
+        dft8(v);
+        wave_sync();
+#pragma unroll
+        for (int d0 = 0; d0 < 8; ++d0) xch[cl * kX1 + d0 * kX2 + a0] = cmul(v[d0], tw2[d0]);
+        wave_sync();
+        // pass 3: lane (c, d0) gathers a0, DFT over a0 -> d1: X[c + 8 d0 + 64 d1]
+        const int d0 = a0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = xch[cl * kX1 + d0 * kX2 + q];
+        dft8(v);
+        wave_sync();
+        // power spectrum |X_k|^2 for k <= 256
+#pragma unroll
+        for (int d1 = 0; d1 < 8; ++d1) {
+            const int k = cl + 8 * d0 + 64 * d1;
+            if (k <= 256) ps[k] = v[d1].r * v[d1].r + v[d1].i * v[d1].i;
+        }
+        wave_sync();
+        for (int m = lane; m < p.n_mels; m += 64) {
+            double e = 0.0;
+            const int st = mel_start[m], n = mel_len[m];
+            const double* w = mel_w + mel_off[m];
+            for (int k = 0; k < n; ++k) e += w[k] * ps[st + k];
+            const double fl = (double)FLT_EPSILON;
+            feats[((size_t)b * p.n_mels + m) * p.T + t] = (float)log(e > fl ? e : fl);
+        }
+        wave_sync();
     }
 }
 
@@ -267,15 +441,14 @@ extern "C" int vdk_fbank(const vdk_fbank_cfg* cfg, const void* d_tables, const f
         std::vector<double> w;
         mel_sparse(c, st, ln, of, w);
         const TableLayout L = layout(c, (int)w.size());
-        const uint8_t* base = static_cast<const uint8_t*>(d_tables);
         FbankDev p;
-        p.window = reinterpret_cast<const double*>(base + L.window);
-        p.tw_re = reinterpret_cast<const double*>(base + L.tw_re);
-        p.tw_im = reinterpret_cast<const double*>(base + L.tw_im);
-        p.mel_start = reinterpret_cast<const int*>(base + L.mel_start);
-        p.mel_len = reinterpret_cast<const int*>(base + L.mel_len);
-        p.mel_off = reinterpret_cast<const int*>(base + L.mel_off);
-        p.mel_w = reinterpret_cast<const double*>(base + L.mel_w);
+        p.off_window = (int)L.window;
+        p.off_tw_re = (int)L.tw_re;
+        p.off_tw_im = (int)L.tw_im;
+        p.off_mel_start = (int)L.mel_start;
+        p.off_mel_len = (int)L.mel_len;
+        p.off_mel_off = (int)L.mel_off;
+        p.off_mel_w = (int)L.mel_w;
         p.n_mels = c.n_mels;
         p.n_fft = c.n_fft;
         p.pow2 = (c.n_fft & (c.n_fft - 1)) == 0;
@@ -287,10 +460,25 @@ extern "C" int vdk_fbank(const vdk_fbank_cfg* cfg, const void* d_tables, const f
         p.n_samples = n_samples;
         p.preemph = c.preemph;
         p.waves = c.n_fft <= 512 ? kFbMaxWaves : 2;
-        const size_t shmem = (size_t)p.waves * (2 * c.n_fft * sizeof(double) + c.n_fft * sizeof(float));
+        // frames per wavefront: enough to amortise the table copy, while
+        // keeping >= ~4 workgroups per CU at batch 64
+        const int fpw = p.T >= 256 ? 4 : (p.T >= 64 ? 2 : 1);
         hipStream_t s = static_cast<hipStream_t>(stream);
-        dim3 grid(cdiv(p.T, p.waves), batch);
-        hipLaunchKernelGGL(fbank_frames_kernel, grid, dim3(p.waves * 64), shmem, s, p, d_pcm, d_feats);
+        dim3 grid(cdiv(p.T, p.waves * fpw), batch);
+        const bool radix8 = c.n_fft == 512 && c.win_length <= 512;
+        const size_t per_wave = radix8 ? (size_t)8 * kX1 * sizeof(cplx)
+                                       : (size_t)(2 * c.n_fft + c.n_fft / 2) * sizeof(double);
+        const size_t shmem = L.total + (size_t)p.waves * per_wave;
+        require(shmem <= 160 * 1024, "fbank: configuration needs more LDS than a workgroup has");
+        const void* fn = radix8 ? (const void*)fbank512_kernel : (const void*)fbank_frames_kernel;
+        if (shmem > 64 * 1024)
+            VDK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
+        if (radix8)
+            hipLaunchKernelGGL(fbank512_kernel, grid, dim3(p.waves * 64), shmem, s, p,
+                               static_cast<const uint8_t*>(d_tables), (int)L.total, fpw, d_pcm, d_feats);
+        else
+            hipLaunchKernelGGL(fbank_frames_kernel, grid, dim3(p.waves * 64), shmem, s, p,
+                               static_cast<const uint8_t*>(d_tables), (int)L.total, fpw, d_pcm, d_feats);
         VDK_HIP(hipGetLastError());
         if (c.cmn) {
             hipLaunchKernelGGL(fbank_cmn_kernel, dim3(c.n_mels, batch), dim3(256), 0, s, d_feats, c.n_mels, p.T);

@@ -2,7 +2,7 @@
 //
 // These are bandwidth-bound reductions: TSTP reads the last feature map once
 // (coalesced over channels, one thread per (clip, freq row, channel)); the FC is
-// one wavefront per output element with a shuffle reduction; L2 is one
+// a split-K tiled dot product with a fixed-order reduction; L2 is one
 // wavefront per clip.  Sums are accumulated in f64 like the reference's ggml
 // reductions and host L2 (src/encoder_resnet.cpp:140-183).
 #include <cmath>
@@ -28,9 +28,11 @@ __global__ __launch_bounds__(256) void tstp_kernel(const half_t* __restrict__ x,
     const half_t* row = x + ((size_t)b * H + h) * W * C;
     for (int c = threadIdx.x; c < C; c += blockDim.x) {
         double s = 0.0;
+#pragma unroll 8
         for (int t = 0; t < W; ++t) s += (double)(float)row[(size_t)t * C + c];
         const float mean = (float)(s / W);
         double s2 = 0.0;
+#pragma unroll 8
         for (int t = 0; t < W; ++t) {
             const float d = (float)row[(size_t)t * C + c] - mean;
             s2 += (double)(d * d);
@@ -42,26 +44,64 @@ __global__ __launch_bounds__(256) void tstp_kernel(const half_t* __restrict__ x,
     }
 }
 
-// y[b][o] = sum_i w[o][i] x[b][i] + bias[o] - mean_vec[o]; one wavefront per (b, o).
-__global__ __launch_bounds__(256) void linear_kernel(const float* __restrict__ x, int B, int in_dim,
-                                                     const float* __restrict__ w, const float* __restrict__ bias,
-                                                     const float* __restrict__ mv, int out_dim,
-                                                     float* __restrict__ y) {
-    const long gw = ((long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int lane = threadIdx.x & 63;
-    if (gw >= (long)B * out_dim) return;   // uniform per wavefront
-    const int b = (int)(gw / out_dim), o = (int)(gw - (long)b * out_dim);
-    const float* wr = w + (size_t)o * in_dim;
-    const float* xr = x + (size_t)b * in_dim;
-    double s = 0.0;
-    for (int i = lane; i < in_dim; i += 64) s += (double)wr[i] * (double)xr[i];
-    s = wave_sum_d(s);
-    if (lane == 0) {
-        float v = (float)s;
-        if (bias) v += bias[o];
-        if (mv) v -= mv[o];
-        y[(size_t)b * out_dim + o] = v;
+// FC, split over the input dimension: workgroup (o-tile, b-tile, split s)
+// computes a 32x32 block of partial dot products over its slice of the input
+// from LDS-staged tiles; linear_reduce_kernel adds the slices in a fixed order
+// (bitwise reproducible) with bias and mean_vec.
+constexpr int kLinTile = 16, kLinK = 64;
+
+__global__ __launch_bounds__(256) void linear_partial_kernel(const float* __restrict__ x, int B, int in_dim,
+                                                             const float* __restrict__ w, int out_dim, int slice,
+                                                             float* __restrict__ part) {
+    __shared__ float sx[kLinTile][kLinK + 1];
+    __shared__ float sw[kLinTile][kLinK + 1];
+    const int o0 = blockIdx.x * kLinTile, b0 = blockIdx.y * kLinTile, s = blockIdx.z;
+    const int k_begin = s * slice, k_end = min(in_dim, k_begin + slice);
+    const int tid = threadIdx.x;
+    const int tb = tid / kLinTile, to = tid % kLinTile;   // one output (b0+tb, o0+to) per thread
+    float acc = 0.0f;
+    for (int k0 = k_begin; k0 < k_end; k0 += kLinK) {
+        for (int e = tid; e < kLinTile * kLinK; e += 256) {
+            const int r = e / kLinK, c = e % kLinK, k = k0 + c;
+            sx[r][c] = (b0 + r < B && k < k_end) ? x[(size_t)(b0 + r) * in_dim + k] : 0.0f;
+            sw[r][c] = (o0 + r < out_dim && k < k_end) ? w[(size_t)(o0 + r) * in_dim + k] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 16
+        for (int c = 0; c < kLinK; ++c) acc += sx[tb][c] * sw[to][c];
+        __syncthreads();
     }
+    const int b = b0 + tb, o = o0 + to;
+    if (b < B && o < out_dim) part[((size_t)s * B + b) * out_dim + o] = acc;
+}
+
+__global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restrict__ part, int nsplit, int B,
+                                                            int out_dim, const float* __restrict__ bias,
+                                                            const float* __restrict__ mv, float* __restrict__ y) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)B * out_dim) return;
+    const int o = (int)(i % out_dim);
+    const size_t stride = (size_t)B * out_dim;
+    // fixed summation order, 8 loads in flight per step
+    double s = 0.0;
+    int k = 0;
+    for (; k + 8 <= nsplit; k += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = part[(size_t)(k + j) * stride + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += (double)v[j];
+    }
+    for (; k < nsplit; ++k) s += (double)part[(size_t)k * stride + i];
+    float r = (float)s;
+    if (bias) r += bias[o];
+    if (mv) r -= mv[o];
+    y[i] = r;
+}
+
+int linear_splits(int in_dim) {
+    const int want = (in_dim + 255) / 256;              // ~256 inputs per slice
+    return want < 1 ? 1 : (want > 64 ? 64 : want);
 }
 
 // In-place L2 normalisation, one wavefront per clip (src/encoder_resnet.cpp:177-183).
@@ -91,14 +131,29 @@ extern "C" int vdk_tstp(const void* d_x, int batch, int H, int W, int C, float e
     });
 }
 
+extern "C" size_t vdk_linear_workspace_size(int batch, int in_dim, int out_dim) {
+    if (batch <= 0 || in_dim <= 0 || out_dim <= 0) return 0;
+    return sizeof(float) * (size_t)linear_splits(in_dim) * batch * out_dim;
+}
+
 extern "C" int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
-                          const float* d_mean_vec, int out_dim, float* d_y, void* stream) {
+                          const float* d_mean_vec, int out_dim, float* d_y, void* d_work, size_t work_bytes,
+                          void* stream) {
     return guarded([&] {
-        require(d_x && d_w && d_y, "linear: NULL device pointer");
+        require(d_x && d_w && d_y && d_work, "linear: NULL device pointer");
         require(batch > 0 && in_dim > 0 && out_dim > 0, "linear: empty shape");
-        const long waves = (long)batch * out_dim;
-        hipLaunchKernelGGL(linear_kernel, dim3(cdiv(waves, 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                           d_x, batch, in_dim, d_w, d_bias, d_mean_vec, out_dim, d_y);
+        require(work_bytes >= vdk_linear_workspace_size(batch, in_dim, out_dim),
+                "linear: workspace smaller than vdk_linear_workspace_size()");
+        const int ns = linear_splits(in_dim);
+        const int slice = ((in_dim + ns - 1) / ns + kLinK - 1) / kLinK * kLinK;
+        const int nsplit = (in_dim + slice - 1) / slice;
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        float* part = static_cast<float*>(d_work);
+        hipLaunchKernelGGL(linear_partial_kernel, dim3(cdiv(out_dim, kLinTile), cdiv(batch, kLinTile), nsplit),
+                           dim3(256), 0, s, d_x, batch, in_dim, d_w, out_dim, slice, part);
+        VDK_HIP(hipGetLastError());
+        hipLaunchKernelGGL(linear_reduce_kernel, dim3(cdiv((long)batch * out_dim, 256)), dim3(256), 0, s, part,
+                           nsplit, batch, out_dim, d_bias, d_mean_vec, d_y);
         VDK_HIP(hipGetLastError());
     });
 }

@@ -191,7 +191,7 @@ void Model::upload_resnet() {
 void Model::free_workspace() {
     Workspace& w = ws_;
     for (void* p : {(void*)w.pcm, (void*)w.feats, w.act[0], w.act[1], w.act[2], w.act[3], (void*)w.pooled,
-                    (void*)w.pre, (void*)w.emb})
+                    (void*)w.pre, (void*)w.emb, w.fc_work})
         if (p) (void)hipFree(p);
     ws_ = Workspace();
 }
@@ -219,6 +219,8 @@ void Model::ensure_workspace(int batch, int n_samples) {
     VDK_HIP(hipMalloc((void**)&w.pooled, sizeof(float) * (size_t)batch * pooled_dim_));
     VDK_HIP(hipMalloc((void**)&w.pre, sizeof(float) * (size_t)batch * cfg_.embedding_dim));
     VDK_HIP(hipMalloc((void**)&w.emb, sizeof(float) * (size_t)batch * cfg_.embedding_dim));
+    w.fc_work_bytes = vdk_linear_workspace_size(batch, pooled_dim_, cfg_.embedding_dim);
+    VDK_HIP(hipMalloc(&w.fc_work, w.fc_work_bytes));
 }
 
 void Model::prof_begin(const char* name, double flops, double bytes) {
@@ -296,7 +298,8 @@ void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) 
     const int E = cfg_.embedding_dim;
     prof_begin("linear", 2.0 * batch * (double)pooled_dim_ * E,
                4.0 * ((double)batch * pooled_dim_ + (double)pooled_dim_ * E + (double)batch * E));
-    check(vdk_linear(ws_.pooled, batch, pooled_dim_, seg_w_, seg_b_, mean_vec_, E, ws_.pre, stream_));
+    check(vdk_linear(ws_.pooled, batch, pooled_dim_, seg_w_, seg_b_, mean_vec_, E, ws_.pre, ws_.fc_work,
+                     ws_.fc_work_bytes, stream_));
     prof_end();
     VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));
     if (cfg_.l2_normalize) {

@@ -93,6 +93,8 @@ private:
         float* pooled = nullptr;
         float* pre = nullptr;
         float* emb = nullptr;
+        void* fc_work = nullptr;
+        size_t fc_work_bytes = 0;
     };
 
     void ensure_device();

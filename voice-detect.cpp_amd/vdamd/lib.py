@@ -82,7 +82,8 @@ _SIGS = {
     "vdk_conv2d_tile_fits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "vdk_stem_conv3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_tstp": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
-    "vdk_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp]),
+    "vdk_linear_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
+    "vdk_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp, C.c_size_t, _vp]),
     "vdk_l2norm": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
 }
 
