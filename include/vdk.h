@@ -80,6 +80,26 @@ int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC,
                     const float* d_bias, const void* d_residual, int relu,
                     void* d_y, void* stream);
 
+/* General form.  Pixel strides let a layer read or write a channel slice of a
+ * wider NHWC tensor in place (pass the slice's base pointer; stride 0 means
+ * dense).  Epilogue, in order: v = acc + bias [+ residual]; relu; v*post_scale
+ * + post_shift (a BatchNorm that follows the activation); tanh; store f16 or
+ * f32.  bias_batch_stride > 0 selects a per-clip bias vector (clip b reads
+ * bias + b*bias_batch_stride).  Padding is zero padding; reflect padding is
+ * materialised by the caller.  tile = -1 picks the kernel automatically. */
+typedef struct {
+    const void* x; int batch, H, W, IC, x_stride;
+    const void* w; int OC, KH, KW, stride, pad, dilation;
+    const float* bias; int bias_batch_stride;
+    const void* residual; int res_stride;
+    const float* post_scale; const float* post_shift;
+    int relu, tanh_after;
+    void* y; int y_stride, y_f32;
+    int tile;
+} vdk_conv_desc;
+int vdk_conv2d_ex(const vdk_conv_desc* desc, void* stream);
+int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* desc);
+
 /* Same contract with an explicit kernel/tile choice (index into the library's
  * tile table; vdk_conv2d_tile_fits tells which apply to a shape).  For
  * validation and tuning; vdk_conv2d_nhwc picks the tile itself. */
@@ -115,6 +135,39 @@ size_t vdk_linear_workspace_size(int batch, int in_dim, int out_dim);
 int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w,
                const float* d_bias, const float* d_mean_vec, int out_dim,
                float* d_y, void* d_work, size_t work_bytes, void* stream);
+/* Same, with an optional ReLU on the result (relu != 0): the SE bottleneck
+ * conv1 + ReLU of src/encoder.cpp:207-219 and the ASP global-context term. */
+int vdk_linear_ex(const float* d_x, int batch, int in_dim, const float* d_w,
+                  const float* d_bias, const float* d_mean_vec, int out_dim, int relu,
+                  float* d_y, void* d_work, size_t work_bytes, void* stream);
+
+/* ---- ECAPA-TDNN helpers (src/encoder.cpp) ----
+ * Activations are time-major f16 [B][T][stride] (channel slices by pointer
+ * offset + stride; strides and channel counts of the half8 kernels are
+ * multiples of 8 and pointers 16-byte aligned). */
+/* FBank [B][n_mels][T] f32 -> [B][T+2*pad][c_pad] f16, reflect padded in time
+ * without edge repeat (src/encoder.cpp:32-52) and zero channels n_mels..c_pad. */
+int vdk_feats_tmajor(const float* d_feats, int batch, int n_mels, int T, int pad, int c_pad,
+                     void* d_out, void* stream);
+/* out [B][T+2*pad][G] = reflect_pad(a (+ b)) over time: the Res2Net group
+ * input x_i + y_{i-1} of src/encoder.cpp:174-200 padded for its dilated conv.
+ * d_b may be NULL. */
+int vdk_reflect_pad_add(const void* d_a, int a_stride, const void* d_b, int b_stride, int batch, int T,
+                        int G, int pad, void* d_out, void* stream);
+/* out [B][C] f32 = mean over time (SE squeeze, src/encoder.cpp:207-209). */
+int vdk_channel_mean(const void* d_x, int x_stride, int batch, int T, int C, float* d_out, void* stream);
+/* y = x * sigmoid(gate[b][c]) + res (SE excitation and the block residual,
+ * src/encoder.cpp:218-244). */
+int vdk_se_gate_residual(const void* d_x, int x_stride, const float* d_gate, const void* d_res,
+                         int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream);
+/* out [B][2C] = [mean_t x ; sqrt(max(var_t x, eps))] (ASP global context,
+ * src/encoder.cpp:269-271). */
+int vdk_asp_stats(const void* d_x, int x_stride, int batch, int T, int C, float eps, float* d_out,
+                  void* stream);
+/* softmax over time of logits [B][T][l_stride] f32 per channel, then
+ * out [B][2C] = [sum a x ; sqrt(max(sum a (x-mu)^2, eps))] (src/encoder.cpp:282-294). */
+int vdk_asp_pool(const float* d_logits, int l_stride, const void* d_x, int x_stride, int batch, int T,
+                 int C, float eps, float* d_out, void* stream);
 
 /* ---- L2 normalisation ----
  * Replaces the host L2 of src/encoder_resnet.cpp:177-183 (double accumulation,

@@ -114,6 +114,46 @@ int orc_resnet34_forward(const orc_resnet* net, const float* feats, int T,
 int orc_embed_batch(const orc_resnet* net, const orc_fbank_cfg* fcfg,
                     const float* pcm, int batch, int n_samples, int n_threads, float* emb);
 
+/* ------------------------------------------------------------ ECAPA-TDNN */
+
+/* Conv1d weight [oc][ic][k] and bias [oc] (src/encoder.cpp:62-109). */
+typedef struct { const float* w; const float* b; int oc, ic, k; } orc_conv1d;
+/* Eval BatchNorm1d parameters (src/encoder.cpp:125-151, eps 1e-5). */
+typedef struct { const float* gamma; const float* beta; const float* mean; const float* var; int c; } orc_bn;
+
+#define ORC_MAX_RES 8
+#define ORC_MAX_SCALE 16
+
+typedef struct {
+    int n_mels, channels, scale, n_res, mfa_ch, emb_dim, l2_normalize;
+    orc_conv1d block0; orc_bn bn0;
+    orc_conv1d tdnn1[ORC_MAX_RES], tdnn2[ORC_MAX_RES], se1[ORC_MAX_RES], se2[ORC_MAX_RES];
+    orc_bn bn_t1[ORC_MAX_RES], bn_t2[ORC_MAX_RES];
+    orc_conv1d res[ORC_MAX_RES][ORC_MAX_SCALE]; orc_bn bn_res[ORC_MAX_RES][ORC_MAX_SCALE];
+    orc_conv1d mfa; orc_bn bn_mfa;
+    orc_conv1d asp_tdnn; orc_bn bn_asp; orc_conv1d asp_conv; orc_bn asp_bn;
+    orc_conv1d fc;
+} orc_ecapa;
+
+typedef struct {
+    float* block[ORC_MAX_RES + 1];   /* block0 .. block n_res outputs, [C][T] */
+    float* mfa;                      /* [mfa_ch][T] */
+    float* pooled;                   /* [2*mfa_ch] raw ASP output (before asp_bn) */
+    float* pre_norm;                 /* [emb_dim] */
+} orc_ecapa_caps;
+
+/* Reflect-padded ("same") dilated conv1d, stride 1: x [ic][T] -> y [oc][T]
+ * (src/encoder.cpp:32-109: pad (k-1)/2*dil, reflect without edge repeat). */
+void orc_conv1d_same(const float* x, int T, const orc_conv1d* c, int dilation, float* y);
+/* y = x * g/sqrt(var+eps) + (beta - mean*g/sqrt(var+eps)), x [C][T] in place. */
+void orc_bn_apply(float* x, int T, const orc_bn* bn);
+/* Attentive statistics pooling with global context (src/encoder.cpp:262-295):
+ * x [C][T] -> pooled [2C] = [mu ; sd]. */
+void orc_ecapa_asp(const orc_ecapa* net, const float* x, int T, float* pooled);
+/* Full ECAPA forward of one clip from FBank features [n_mels][T]
+ * (src/encoder.cpp:299-400). Returns 0. */
+int orc_ecapa_forward(const orc_ecapa* net, const float* feats, int T, float* emb, orc_ecapa_caps* caps);
+
 #ifdef __cplusplus
 }
 #endif

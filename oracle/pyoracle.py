@@ -261,3 +261,143 @@ class OracleResNet:
         rc = lib().orc_embed_batch(C.byref(self.net), C.byref(cfg), pcm, B, n, n_threads, out)
         assert rc == 0
         return out
+
+
+# ---------------------------------------------------------------- ECAPA-TDNN
+
+class Conv1d(C.Structure):
+    _fields_ = [("w", _fp), ("b", _fp), ("oc", C.c_int), ("ic", C.c_int), ("k", C.c_int)]
+
+
+class BN(C.Structure):
+    _fields_ = [("gamma", _fp), ("beta", _fp), ("mean", _fp), ("var", _fp), ("c", C.c_int)]
+
+
+MAXR, MAXS = 8, 16
+
+
+class Ecapa(C.Structure):
+    _fields_ = [("n_mels", C.c_int), ("channels", C.c_int), ("scale", C.c_int), ("n_res", C.c_int),
+                ("mfa_ch", C.c_int), ("emb_dim", C.c_int), ("l2_normalize", C.c_int),
+                ("block0", Conv1d), ("bn0", BN),
+                ("tdnn1", Conv1d * MAXR), ("tdnn2", Conv1d * MAXR), ("se1", Conv1d * MAXR), ("se2", Conv1d * MAXR),
+                ("bn_t1", BN * MAXR), ("bn_t2", BN * MAXR),
+                ("res", (Conv1d * MAXS) * MAXR), ("bn_res", (BN * MAXS) * MAXR),
+                ("mfa", Conv1d), ("bn_mfa", BN),
+                ("asp_tdnn", Conv1d), ("bn_asp", BN), ("asp_conv", Conv1d), ("asp_bn", BN),
+                ("fc", Conv1d)]
+
+
+class EcapaCaps(C.Structure):
+    _fields_ = [("block", _fp * (MAXR + 1)), ("mfa", _fp), ("pooled", _fp), ("pre_norm", _fp)]
+
+
+def _ecapa_sigs():
+    L = lib()
+    if not hasattr(L, "_ecapa_ready"):
+        L.orc_conv1d_same.argtypes = [F32P, C.c_int, C.POINTER(Conv1d), C.c_int, F32P]
+        L.orc_bn_apply.argtypes = [F32P, C.c_int, C.POINTER(BN)]
+        L.orc_ecapa_asp.argtypes = [C.POINTER(Ecapa), F32P, C.c_int, F32P]
+        L.orc_ecapa_forward.argtypes = [C.POINTER(Ecapa), F32P, C.c_int, F32P, C.POINTER(EcapaCaps)]
+        L._ecapa_ready = True
+    return L
+
+
+class OracleEcapa:
+    """orc_ecapa built from a parsed ECAPA GGUF (weights as stored, dequantised to f32)."""
+
+    def __init__(self, g):
+        self.keep = []
+        self.g = g
+        kv = g.kv
+        n = Ecapa()
+
+        def arr(name):
+            a = np.ascontiguousarray(g.array(name), dtype=np.float32)
+            self.keep.append(a)
+            return a
+
+        def conv(dst, prefix):
+            w = arr(prefix + ".weight")
+            if w.ndim == 2:
+                w = w.reshape(w.shape[0], w.shape[1], 1)
+                self.keep.append(w)
+            dst.w = w.ctypes.data_as(_fp)
+            dst.b = arr(prefix + ".bias").ctypes.data_as(_fp)
+            dst.oc, dst.ic, dst.k = w.shape
+
+        def bn(dst, prefix):
+            dst.gamma = arr(prefix + ".weight").ctypes.data_as(_fp)
+            dst.beta = arr(prefix + ".bias").ctypes.data_as(_fp)
+            dst.mean = arr(prefix + ".running_mean").ctypes.data_as(_fp)
+            v = arr(prefix + ".running_var")
+            dst.var = v.ctypes.data_as(_fp)
+            dst.c = v.shape[0]
+
+        n.n_mels = int(kv.get("voicedetect.fbank.n_mels", 80))
+        conv(n.block0, "blocks.0.conv.conv")
+        bn(n.bn0, "blocks.0.norm.norm")
+        n.channels = n.block0.oc
+        R = 0
+        while f"blocks.{R + 1}.tdnn1.conv.conv.weight" in g.tensors:
+            R += 1
+        n.n_res = R
+        scale = 1
+        while f"blocks.1.res2net_block.blocks.{scale - 1}.conv.conv.weight" in g.tensors:
+            scale += 1
+        n.scale = scale
+        for i in range(R):
+            p = f"blocks.{i + 1}"
+            conv(n.tdnn1[i], p + ".tdnn1.conv.conv")
+            bn(n.bn_t1[i], p + ".tdnn1.norm.norm")
+            conv(n.tdnn2[i], p + ".tdnn2.conv.conv")
+            bn(n.bn_t2[i], p + ".tdnn2.norm.norm")
+            conv(n.se1[i], p + ".se_block.conv1.conv")
+            conv(n.se2[i], p + ".se_block.conv2.conv")
+            for j in range(scale - 1):
+                conv(n.res[i][j], f"{p}.res2net_block.blocks.{j}.conv.conv")
+                bn(n.bn_res[i][j], f"{p}.res2net_block.blocks.{j}.norm.norm")
+        conv(n.mfa, "mfa.conv.conv")
+        bn(n.bn_mfa, "mfa.norm.norm")
+        n.mfa_ch = n.mfa.oc
+        conv(n.asp_tdnn, "asp.tdnn.conv.conv")
+        bn(n.bn_asp, "asp.tdnn.norm.norm")
+        conv(n.asp_conv, "asp.conv.conv")
+        bn(n.asp_bn, "asp_bn.norm")
+        conv(n.fc, "fc.conv")
+        n.emb_dim = n.fc.oc
+        n.l2_normalize = int(bool(kv.get("voicedetect.l2_normalize", True)))
+        self.net = n
+
+    def forward(self, feats, capture=False):
+        L = _ecapa_sigs()
+        feats = np.ascontiguousarray(feats, dtype=np.float32)
+        T = feats.shape[1]
+        n = self.net
+        emb = np.zeros(n.emb_dim, dtype=np.float32)
+        caps = EcapaCaps()
+        bufs = {}
+        if capture:
+            for i in range(n.n_res + 1):
+                bufs[f"block{i}"] = np.zeros((n.channels, T), dtype=np.float32)
+                caps.block[i] = bufs[f"block{i}"].ctypes.data_as(_fp)
+            bufs["mfa"] = np.zeros((n.mfa_ch, T), dtype=np.float32)
+            caps.mfa = bufs["mfa"].ctypes.data_as(_fp)
+            bufs["pooled"] = np.zeros(2 * n.mfa_ch, dtype=np.float32)
+            caps.pooled = bufs["pooled"].ctypes.data_as(_fp)
+            bufs["pre_norm"] = np.zeros(n.emb_dim, dtype=np.float32)
+            caps.pre_norm = bufs["pre_norm"].ctypes.data_as(_fp)
+        assert L.orc_ecapa_forward(C.byref(n), feats, T, emb, C.byref(caps)) == 0
+        return (emb, bufs) if capture else emb
+
+
+def conv1d_same(x, w, b, dilation=1):
+    """Oracle reflect-padded conv1d: x [ic, T], w [oc, ic, k] -> [oc, T]."""
+    L = _ecapa_sigs()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    c = Conv1d(w.ctypes.data_as(_fp), b.ctypes.data_as(_fp), w.shape[0], w.shape[1], w.shape[2])
+    y = np.zeros((w.shape[0], x.shape[1]), dtype=np.float32)
+    L.orc_conv1d_same(x, x.shape[1], C.byref(c), dilation, y)
+    return y

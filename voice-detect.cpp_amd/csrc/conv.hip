@@ -29,11 +29,53 @@ struct ConvArgs {
     const half_t* w;
     const float* bias;
     const half_t* res;
-    half_t* y;
-    int H, W, IC, Ho, Wo, OC, KH, KW, stride, pad, relu;
-    int npix;     // B * Ho * Wo
-    int npix_in;  // B * H * W
+    void* y;
+    const float* post_scale;   // per-OC affine applied after the activation (may be NULL)
+    const float* post_shift;
+    int H, W, IC, Ho, Wo, OC, KH, KW, stride, pad, dil, relu, tanh_after, y_f32;
+    int xs, ys, rs;            // elements between consecutive pixels of x / y / residual
+    int bias_bs;               // elements between clips' bias vectors (0: one shared vector)
+    int npix;                  // B * Ho * Wo
+    int npix_in;               // B * H * W
+    int plain;                 // xs == IC, dil == 1: layouts every kernel family accepts
 };
+
+// Shared epilogue for 4 consecutive output channels of pixel P:
+// v = acc + bias [+ residual]; [relu]; [* post_scale + post_shift]; [tanh].
+__device__ __forceinline__ void epilogue4(const ConvArgs& a, int P, int oc, const float* acc) {
+    float v[4];
+    const float* bias = a.bias;
+    if (bias && a.bias_bs) bias += (size_t)(P / (a.Ho * a.Wo)) * a.bias_bs;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = acc[e] + (bias ? bias[oc + e] : 0.0f);
+    if (a.res) {
+        const half4 r = *reinterpret_cast<const half4*>(a.res + (size_t)P * a.rs + oc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
+    }
+    if (a.relu) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
+    }
+    if (a.post_scale) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] * a.post_scale[oc + e] + a.post_shift[oc + e];
+    }
+    if (a.tanh_after) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = tanhf(v[e]);
+    }
+    const size_t o = (size_t)P * a.ys + oc;
+    if (a.y_f32) {
+        float4v f = {v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<float4v*>(static_cast<float*>(a.y) + o) = f;
+    } else {
+        half4 h;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = (half_t)v[e];
+        *reinterpret_cast<half4*>(static_cast<half_t*>(a.y) + o) = h;
+    }
+}
 
 // Spread consecutive workgroup ids over the 8 XCDs in contiguous ranges so that
 // neighbouring pixel tiles (which share input rows) run under the same L2.
@@ -169,21 +211,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
                 const int oc = oc0 + wm * WM + i * 32 + g * 8 + (lane >> 5) * 4;
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e] + (a.bias ? a.bias[oc + e] : 0.0f);
-                const size_t o = (size_t)P * a.OC + oc;
-                if (a.res) {
-                    const half4 r = *reinterpret_cast<const half4*>(a.res + o);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
-                }
-                if (a.relu) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
-                }
-                half4 h;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) h[e] = (half_t)v[e];
-                *reinterpret_cast<half4*>(a.y + o) = h;
+                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e];
+                epilogue4(a, P, oc, v);
             }
         }
     }
@@ -259,7 +288,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     const int nk = KHW * nc;
 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)a.x, 0, (int)((size_t)(a.npix_in) * a.IC * 2), 0x00020000);
+        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.w, 0, (int)((size_t)a.OC * KHW * a.IC * 2), 0x00020000);
 
@@ -290,10 +319,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
                 const int b = P / HoWo, rem = P - b * HoWo;
                 const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
                 const int ih0 = oh * a.stride - a.pad, iw0 = ow * a.stride - a.pad;
-                s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.IC + c * 8) * 2;
+                s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.xs + c * 8) * 2;
                 for (int kh = 0; kh < a.KH; ++kh)
                     for (int kw = 0; kw < a.KW; ++kw) {
-                        const int ih = ih0 + kh, iw = iw0 + kw;
+                        const int ih = ih0 + kh * a.dil, iw = iw0 + kw * a.dil;
                         if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W) s_mask[j] |= 1u << (kh * a.KW + kw);
                     }
             }
@@ -303,7 +332,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     // Chunk cursor for the DMA side: tap (kh, kw) and channel offset c0,
     // advanced incrementally (no divisions in the loop).
     int f_tap = 0, f_kw = 0, f_c0 = 0, f_x = 0;   // f_x = byte offset of (kh, kw, c0) in the input
-    const int row_bytes = a.W * a.IC * 2;
+    const int tap_bytes = a.dil * a.xs * 2;                       // next kw
+    const int row_bytes = a.dil * a.W * a.xs * 2 - a.KW * tap_bytes;   // next kh, back to kw = 0
     auto issue = [&](int st) {
         const int w_soff = (f_tap * a.IC + f_c0) * 2;
 #pragma unroll
@@ -320,10 +350,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
         f_x += KC * 2;
         if (f_c0 == a.IC) {
             f_c0 = 0;
+            f_x += tap_bytes - a.IC * 2;
             ++f_tap;
             if (++f_kw == a.KW) {
                 f_kw = 0;
-                f_x += row_bytes - a.KW * a.IC * 2;   // next kernel row
+                f_x += row_bytes;              // next kernel row
             }
         }
     };
@@ -389,21 +420,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
                 const int oc = oc0 + wm * WM + i * 32 + g * 8 + lhalf * 4;
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e] + (a.bias ? a.bias[oc + e] : 0.0f);
-                const size_t o = (size_t)P * a.OC + oc;
-                if (a.res) {
-                    const half4 r = *reinterpret_cast<const half4*>(a.res + o);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
-                }
-                if (a.relu) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
-                }
-                half4 h;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) h[e] = (half_t)v[e];
-                *reinterpret_cast<half4*>(a.y + o) = h;
+                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e];
+                epilogue4(a, P, oc, v);
             }
         }
     }
@@ -454,7 +472,7 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
     const int nc = a.IC / KC;
 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)a.x, 0, (int)((size_t)(a.npix_in) * a.IC * 2), 0x00020000);
+        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.w, 0, (int)((size_t)a.OC * 9 * a.IC * 2), 0x00020000);
 
@@ -484,7 +502,7 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
                 const int hr = r / HW, hc = r - hr * HW;
                 const int ih = oh0 - 1 + hr, iw = ow0 - 1 + hc;
                 if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
-                    off = (uint32_t)((((b * a.H + ih) * a.W + iw) * a.IC + c0 + swz<KC>(r, slot) * 8) * 2);
+                    off = (uint32_t)((((b * a.H + ih) * a.W + iw) * a.xs + c0 + swz<KC>(r, slot) * 8) * 2);
             }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx + ins * 1024), 16, off, 0, 0, 0);
         }
@@ -524,21 +542,8 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
             const int oc = oc0 + mb * 32 + g * 8 + lhalf * 4;
             float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[q][g * 4 + e] + (a.bias ? a.bias[oc + e] : 0.0f);
-            const size_t o = P * a.OC + oc;
-            if (a.res) {
-                const half4 r = *reinterpret_cast<const half4*>(a.res + o);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
-            }
-            if (a.relu) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
-            }
-            half4 h;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = (half_t)v[e];
-            *reinterpret_cast<half4*>(a.y + o) = h;
+            for (int e = 0; e < 4; ++e) v[e] = acc[q][g * 4 + e];
+            epilogue4(a, (int)P, oc, v);
         }
     }
 }
@@ -560,8 +565,12 @@ void launch_igemm(const ConvArgs& a, hipStream_t s) {
 struct TileCfg {
     int bm, bn, kc;
     void (*launch)(const ConvArgs&, hipStream_t);
-    bool halo;   // 3x3 stride-1 pad-1 only
+    bool halo;   // 3x3 stride-1 pad-1 dilation-1 only
 };
+
+// Entries 0-13 are the register-staged kernel (plain layouts only), 14-25 the
+// LDS-DMA kernel (any strides / dilation), 26+ the halo kernel.
+constexpr int kFirstDma = 14;
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -603,7 +612,9 @@ const TileCfg kTiles[] = {
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
-    if (t.halo && !(a.KH == 3 && a.KW == 3 && a.stride == 1 && a.pad == 1)) return false;
+    if (t.halo && !(a.KH == 3 && a.KW == 3 && a.stride == 1 && a.pad == 1 && a.dil == 1)) return false;
+    const bool dma = !t.halo && (&t - kTiles) >= kFirstDma;
+    if (!dma && !t.halo && !a.plain) return false;
     return a.OC % t.bm == 0 && a.IC % t.kc == 0;
 }
 
@@ -622,7 +633,7 @@ int tile_override() {
 int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
-    const bool s1_3x3 = a.KH == 3 && a.KW == 3 && a.stride == 1 && a.pad == 1;
+    const bool s1_3x3 = a.KH == 3 && a.KW == 3 && a.stride == 1 && a.pad == 1 && a.dil == 1;
     if (s1_3x3 && a.OC == 32 && a.IC % 32 == 0 && a.IC <= 64) return 28;
     if (s1_3x3 && a.OC == 64 && a.IC % 32 == 0 && a.IC <= 64) return 30;
     if (a.IC % 64 == 0) {
@@ -632,6 +643,7 @@ int pick_tile(const ConvArgs& a) {
         if (a.OC % 64 == 0) return 16;
         if (a.OC % 32 == 0) return 14;
     }
+    if (a.IC % 32 != 0 && !a.plain) return -1;   // needs KC=16, which only the plain-layout kernel has
     if (a.IC % 32 != 0) return a.OC % 128 == 0 ? 13 : (a.OC % 64 == 0 ? 12 : 11);
     if (a.OC % 128 == 0) return 5;
     if (a.OC % 64 == 0) return 2;
@@ -688,57 +700,90 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 using namespace vdk;
 
 namespace {
-int conv_impl(const void* d_x, int batch, int H, int W, int IC, const void* d_w, int OC, int KH, int KW,
-              int stride, int pad, const float* d_bias, const void* d_residual, int relu, void* d_y, void* stream,
-              int tile) {
+int conv_impl(const vdk_conv_desc& d, void* stream) {
     return guarded([&] {
-        require(d_x && d_w && d_y, "conv2d: NULL device pointer");
-        require(batch > 0 && H > 0 && W > 0, "conv2d: empty input");
-        require(IC > 0 && IC % 16 == 0, "conv2d: IC must be a positive multiple of 16");
-        require(OC > 0 && OC % 32 == 0, "conv2d: OC must be a positive multiple of 32");
-        require(KH >= 1 && KW >= 1 && KH <= 7 && KW <= 7, "conv2d: kernel size out of range");
-        require(stride >= 1 && pad >= 0, "conv2d: invalid stride/pad");
-        const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
-        require(H + 2 * pad >= KH && W + 2 * pad >= KW && Ho > 0 && Wo > 0, "conv2d: output would be empty");
-        require((long)batch * Ho * Wo < (1L << 31) && (long)batch * H * W < (1L << 31),
+        require(d.x && d.w && d.y, "conv2d: NULL device pointer");
+        require(d.batch > 0 && d.H > 0 && d.W > 0, "conv2d: empty input");
+        require(d.IC > 0 && d.IC % 16 == 0, "conv2d: IC must be a positive multiple of 16");
+        require(d.OC > 0 && d.OC % 32 == 0, "conv2d: OC must be a positive multiple of 32");
+        require(d.KH >= 1 && d.KW >= 1 && d.KH <= 7 && d.KW <= 7, "conv2d: kernel size out of range");
+        require(d.stride >= 1 && d.pad >= 0 && d.dilation >= 1, "conv2d: invalid stride/pad/dilation");
+        const int ekh = (d.KH - 1) * d.dilation + 1, ekw = (d.KW - 1) * d.dilation + 1;
+        require(d.H + 2 * d.pad >= ekh && d.W + 2 * d.pad >= ekw, "conv2d: output would be empty");
+        const int Ho = (d.H + 2 * d.pad - ekh) / d.stride + 1, Wo = (d.W + 2 * d.pad - ekw) / d.stride + 1;
+        const int xs = d.x_stride ? d.x_stride : d.IC, ys = d.y_stride ? d.y_stride : d.OC;
+        const int rs = d.res_stride ? d.res_stride : d.OC;
+        require(xs >= d.IC && ys >= d.OC && rs >= d.OC, "conv2d: pixel stride smaller than the channel count");
+        require(xs % 8 == 0 && ys % 8 == 0 && rs % 8 == 0, "conv2d: pixel strides must be multiples of 8");
+        require((long)d.batch * Ho * Wo < (1L << 31) && (long)d.batch * d.H * d.W * xs < (1L << 30),
                 "conv2d: too many pixels for one launch");
-        require(aligned16(d_x) && aligned16(d_w) && aligned16(d_y) && (!d_residual || aligned16(d_residual)),
+        require(aligned16(d.x) && aligned16(d.w) && aligned16(d.y) && (!d.residual || aligned16(d.residual)),
                 "conv2d: device pointers must be 16-byte aligned");
+        require(!d.post_scale == !d.post_shift, "conv2d: post_scale and post_shift go together");
         ConvArgs a;
-        a.x = static_cast<const half_t*>(d_x);
-        a.w = static_cast<const half_t*>(d_w);
-        a.bias = d_bias;
-        a.res = static_cast<const half_t*>(d_residual);
-        a.y = static_cast<half_t*>(d_y);
-        a.H = H; a.W = W; a.IC = IC; a.Ho = Ho; a.Wo = Wo; a.OC = OC;
-        a.KH = KH; a.KW = KW; a.stride = stride; a.pad = pad; a.relu = relu ? 1 : 0;
-        a.npix = batch * Ho * Wo;
-        a.npix_in = batch * H * W;
+        a.x = static_cast<const half_t*>(d.x);
+        a.w = static_cast<const half_t*>(d.w);
+        a.bias = d.bias;
+        a.res = static_cast<const half_t*>(d.residual);
+        a.y = d.y;
+        a.post_scale = d.post_scale;
+        a.post_shift = d.post_shift;
+        a.H = d.H; a.W = d.W; a.IC = d.IC; a.Ho = Ho; a.Wo = Wo; a.OC = d.OC;
+        a.KH = d.KH; a.KW = d.KW; a.stride = d.stride; a.pad = d.pad; a.dil = d.dilation;
+        a.relu = d.relu ? 1 : 0;
+        a.tanh_after = d.tanh_after ? 1 : 0;
+        a.y_f32 = d.y_f32 ? 1 : 0;
+        a.xs = xs; a.ys = ys; a.rs = rs;
+        a.bias_bs = d.bias_batch_stride;
+        a.npix = d.batch * Ho * Wo;
+        a.npix_in = d.batch * d.H * d.W;
+        a.plain = (xs == d.IC && d.dilation == 1) ? 1 : 0;
         hipStream_t s = static_cast<hipStream_t>(stream);
-        int t = tile;
+        int t = d.tile;
         if (t < 0) {
             t = pick_tile(a);
+            require(t >= 0, "conv2d: no kernel for IC % 32 != 0 with strided input or dilation");
         } else {
             require(t < kNumTiles, "conv2d: tile index out of range");
-            require(tile_fits(kTiles[t], a), "conv2d: tile " + std::to_string(t) + " does not fit this shape");
         }
+        require(tile_fits(kTiles[t], a), "conv2d: tile " + std::to_string(t) + " does not fit this shape");
         kTiles[t].launch(a, s);
         VDK_HIP(hipGetLastError());
     });
 }
 
+vdk_conv_desc plain_desc(const void* d_x, int batch, int H, int W, int IC, const void* d_w, int OC, int KH, int KW,
+                         int stride, int pad, const float* d_bias, const void* d_residual, int relu, void* d_y,
+                         int tile) {
+    vdk_conv_desc d{};
+    d.x = d_x; d.batch = batch; d.H = H; d.W = W; d.IC = IC;
+    d.w = d_w; d.OC = OC; d.KH = KH; d.KW = KW; d.stride = stride; d.pad = pad; d.dilation = 1;
+    d.bias = d_bias; d.residual = d_residual; d.relu = relu; d.y = d_y; d.tile = tile;
+    return d;
+}
+
 }  // namespace
+
+extern "C" int vdk_conv2d_ex(const vdk_conv_desc* d, void* stream) {
+    if (!d) {
+        set_error("conv2d: descriptor is NULL");
+        return 1;
+    }
+    return conv_impl(*d, stream);
+}
 
 extern "C" int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC, const void* d_w, int OC, int KH,
                                int KW, int stride, int pad, const float* d_bias, const void* d_residual, int relu,
                                void* d_y, void* stream) {
-    return conv_impl(d_x, batch, H, W, IC, d_w, OC, KH, KW, stride, pad, d_bias, d_residual, relu, d_y, stream, -1);
+    return conv_impl(plain_desc(d_x, batch, H, W, IC, d_w, OC, KH, KW, stride, pad, d_bias, d_residual, relu, d_y, -1),
+                     stream);
 }
 
 extern "C" int vdk_conv2d_nhwc_tile(const void* d_x, int batch, int H, int W, int IC, const void* d_w, int OC,
                                     int KH, int KW, int stride, int pad, const float* d_bias, const void* d_residual,
                                     int relu, void* d_y, void* stream, int tile) {
-    return conv_impl(d_x, batch, H, W, IC, d_w, OC, KH, KW, stride, pad, d_bias, d_residual, relu, d_y, stream, tile);
+    return conv_impl(plain_desc(d_x, batch, H, W, IC, d_w, OC, KH, KW, stride, pad, d_bias, d_residual, relu, d_y,
+                                tile), stream);
 }
 
 extern "C" int vdk_conv2d_tile_count(void) { return kNumTiles; }
@@ -746,7 +791,17 @@ extern "C" int vdk_conv2d_tile_count(void) { return kNumTiles; }
 extern "C" int vdk_conv2d_tile_fits(int tile, int IC, int OC, int KH, int KW, int stride, int pad) {
     if (tile < 0 || tile >= kNumTiles) return 0;
     ConvArgs a{};
-    a.IC = IC; a.OC = OC; a.KH = KH; a.KW = KW; a.stride = stride; a.pad = pad;
+    a.IC = IC; a.OC = OC; a.KH = KH; a.KW = KW; a.stride = stride; a.pad = pad; a.dil = 1; a.plain = 1;
+    return tile_fits(kTiles[tile], a) ? 1 : 0;
+}
+
+extern "C" int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* d) {
+    if (tile < 0 || tile >= kNumTiles || !d) return 0;
+    ConvArgs a{};
+    a.IC = d->IC; a.OC = d->OC; a.KH = d->KH; a.KW = d->KW; a.stride = d->stride; a.pad = d->pad;
+    a.dil = d->dilation > 0 ? d->dilation : 1;
+    const int xs = d->x_stride ? d->x_stride : d->IC;
+    a.plain = (xs == d->IC && a.dil == 1) ? 1 : 0;
     return tile_fits(kTiles[tile], a) ? 1 : 0;
 }
 

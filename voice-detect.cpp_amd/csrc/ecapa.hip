@@ -1,0 +1,237 @@
+// ecapa.hip - the non-GEMM pieces of the ECAPA-TDNN encoder on gfx950.
+//
+// The convolutions of src/encoder.cpp run on the implicit-GEMM kernels
+// (vdk_conv2d_ex, time as the W axis, H = 1).  What remains is bandwidth-bound
+// and lives here:
+//  * feats_tmajor: FBank [B][n_mels][T] f32 -> time-major f16 [B][T+2p][Cpad]
+//    with SpeechBrain's reflect padding (src/encoder.cpp:32-52) and zero
+//    channels up to Cpad;
+//  * reflect_pad_add: the Res2Net group input x_j (+ y_{j-1}), reflect padded
+//    for the dilated k=3 conv (src/encoder.cpp:174-200);
+//  * channel_mean / se_gate_residual: SE squeeze and x * sigmoid(s) + residual
+//    (src/encoder.cpp:207-244);
+//  * asp_stats / asp_pool: attentive statistics pooling with global context
+//    (src/encoder.cpp:262-295): global mean/std (clamp 1e-12), softmax over
+//    time per channel, weighted mean/std.
+// Sums are accumulated in f64.
+#include <cmath>
+
+#include "common.hpp"
+#include "vdk.h"
+
+namespace vdk {
+namespace {
+
+// Reflect without repeating the edge sample; indices past a 1-sample clip clamp.
+__device__ __forceinline__ int reflect_idx(int j, int pad, int T) {
+    int t;
+    if (j < pad) t = pad - j;
+    else if (j < pad + T) t = j - pad;
+    else t = (T - 2) - (j - pad - T);
+    return t < 0 ? 0 : (t > T - 1 ? T - 1 : t);
+}
+
+__device__ __forceinline__ double wsum(double v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void feats_tmajor_kernel(const float* __restrict__ f, int B, int C, int T,
+                                                           int pad, int Cpad, half_t* __restrict__ out) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    const int Tp = T + 2 * pad;
+    if (i >= (long)B * Tp * Cpad) return;
+    const int c = (int)(i % Cpad);
+    const long r = i / Cpad;
+    const int j = (int)(r % Tp), b = (int)(r / Tp);
+    const float v = c < C ? f[((size_t)b * C + c) * T + reflect_idx(j, pad, T)] : 0.0f;
+    out[i] = (half_t)v;
+}
+
+__global__ __launch_bounds__(256) void reflect_pad_add_kernel(const half_t* __restrict__ a, int as,
+                                                              const half_t* __restrict__ bsrc, int bs, int B,
+                                                              int T, int G, int pad, half_t* __restrict__ out) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;   // one 8-channel chunk
+    const int G8 = G / 8, Tp = T + 2 * pad;
+    if (i >= (long)B * Tp * G8) return;
+    const int c = (int)(i % G8) * 8;
+    const long r = i / G8;
+    const int j = (int)(r % Tp), b = (int)(r / Tp);
+    const size_t src = (size_t)b * T + reflect_idx(j, pad, T);
+    half8 v = *reinterpret_cast<const half8*>(a + src * as + c);
+    if (bsrc) {
+        const half8 w = *reinterpret_cast<const half8*>(bsrc + src * bs + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (half_t)((float)v[e] + (float)w[e]);
+    }
+    *reinterpret_cast<half8*>(out + ((size_t)b * Tp + j) * G + c) = v;
+}
+
+__global__ __launch_bounds__(256) void channel_mean_kernel(const half_t* __restrict__ x, int xs, int T, int C,
+                                                           float* __restrict__ out) {
+    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (c >= C) return;
+    const half_t* p = x + (size_t)b * T * xs + c;
+    double s = 0.0;
+#pragma unroll 8
+    for (int t = 0; t < T; ++t) s += (double)(float)p[(size_t)t * xs];
+    out[(size_t)b * C + c] = (float)(s / T);
+}
+
+__global__ __launch_bounds__(256) void se_gate_residual_kernel(const half_t* __restrict__ x, int xs,
+                                                               const float* __restrict__ gate,
+                                                               const half_t* __restrict__ res, int rs, int B, int T,
+                                                               int C, half_t* __restrict__ y, int ys) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;   // one 8-channel chunk
+    const int C8 = C / 8;
+    if (i >= (long)B * T * C8) return;
+    const int c = (int)(i % C8) * 8;
+    const long r = i / C8;                                  // b * T + t
+    const int b = (int)(r / T);
+    const half8 xv = *reinterpret_cast<const half8*>(x + r * xs + c);
+    const half8 rv = *reinterpret_cast<const half8*>(res + r * rs + c);
+    half8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float g = 1.0f / (1.0f + expf(-gate[(size_t)b * C + c + e]));
+        o[e] = (half_t)((float)xv[e] * g + (float)rv[e]);
+    }
+    *reinterpret_cast<half8*>(y + r * ys + c) = o;
+}
+
+// Global statistics over time per (clip, channel): out[b] = [mean ; sqrt(clamp(var, eps))].
+__global__ __launch_bounds__(256) void asp_stats_kernel(const half_t* __restrict__ x, int xs, int T, int C,
+                                                        float eps, float* __restrict__ out) {
+    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (c >= C) return;
+    const half_t* p = x + (size_t)b * T * xs + c;
+    double s = 0.0;
+#pragma unroll 8
+    for (int t = 0; t < T; ++t) s += (double)(float)p[(size_t)t * xs];
+    const float m = (float)(s / T);
+    double s2 = 0.0;
+#pragma unroll 8
+    for (int t = 0; t < T; ++t) {
+        const float d = (float)p[(size_t)t * xs] - m;
+        s2 += (double)(d * d);
+    }
+    float v = (float)(s2 / T);
+    if (v < eps) v = eps;
+    out[(size_t)b * 2 * C + c] = m;
+    out[(size_t)b * 2 * C + C + c] = sqrtf(v);
+}
+
+// Softmax over time of the attention logits, then attention-weighted mean / std.
+__global__ __launch_bounds__(256) void asp_pool_kernel(const float* __restrict__ logits, int ls,
+                                                       const half_t* __restrict__ x, int xs, int T, int C, float eps,
+                                                       float* __restrict__ out) {
+    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (c >= C) return;
+    const float* l = logits + (size_t)b * T * ls + c;
+    const half_t* p = x + (size_t)b * T * xs + c;
+    float mx = -INFINITY;
+    for (int t = 0; t < T; ++t) mx = fmaxf(mx, l[(size_t)t * ls]);
+    double z = 0.0, mu = 0.0;
+#pragma unroll 4
+    for (int t = 0; t < T; ++t) {
+        const double e = (double)expf(l[(size_t)t * ls] - mx);
+        z += e;
+        mu += e * (double)(float)p[(size_t)t * xs];
+    }
+    const float muf = (float)(mu / z);
+    double var = 0.0;
+#pragma unroll 4
+    for (int t = 0; t < T; ++t) {
+        const double e = (double)expf(l[(size_t)t * ls] - mx);
+        const float d = (float)p[(size_t)t * xs] - muf;
+        var += e * (double)(d * d);
+    }
+    float v = (float)(var / z);
+    if (v < eps) v = eps;
+    out[(size_t)b * 2 * C + c] = muf;
+    out[(size_t)b * 2 * C + C + c] = sqrtf(v);
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace vdk
+
+using namespace vdk;
+
+extern "C" int vdk_feats_tmajor(const float* d_feats, int batch, int n_mels, int T, int pad, int c_pad, void* d_out,
+                                void* stream) {
+    return guarded([&] {
+        require(d_feats && d_out, "feats_tmajor: NULL device pointer");
+        require(batch > 0 && n_mels > 0 && T > 0 && pad >= 0 && c_pad >= n_mels, "feats_tmajor: bad shape");
+        const long n = (long)batch * (T + 2 * pad) * c_pad;
+        hipLaunchKernelGGL(feats_tmajor_kernel, dim3(cdiv(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           d_feats, batch, n_mels, T, pad, c_pad, static_cast<half_t*>(d_out));
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_reflect_pad_add(const void* d_a, int a_stride, const void* d_b, int b_stride, int batch, int T,
+                                   int G, int pad, void* d_out, void* stream) {
+    return guarded([&] {
+        require(d_a && d_out, "reflect_pad_add: NULL device pointer");
+        require(batch > 0 && T > 0 && G > 0 && G % 8 == 0 && pad >= 0, "reflect_pad_add: bad shape");
+        require(a_stride % 8 == 0 && (!d_b || b_stride % 8 == 0) && al16(d_a) && (!d_b || al16(d_b)) && al16(d_out),
+                "reflect_pad_add: strides/pointers must be 8-channel aligned");
+        const long n = (long)batch * (T + 2 * pad) * (G / 8);
+        hipLaunchKernelGGL(reflect_pad_add_kernel, dim3(cdiv(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<const half_t*>(d_a), a_stride, static_cast<const half_t*>(d_b), b_stride, batch,
+                           T, G, pad, static_cast<half_t*>(d_out));
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_channel_mean(const void* d_x, int x_stride, int batch, int T, int C, float* d_out, void* stream) {
+    return guarded([&] {
+        require(d_x && d_out, "channel_mean: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0 && x_stride >= C, "channel_mean: bad shape");
+        hipLaunchKernelGGL(channel_mean_kernel, dim3(cdiv(C, 256), batch), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, d_out);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_se_gate_residual(const void* d_x, int x_stride, const float* d_gate, const void* d_res,
+                                    int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream) {
+    return guarded([&] {
+        require(d_x && d_gate && d_res && d_y, "se_gate_residual: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0 && C % 8 == 0, "se_gate_residual: bad shape");
+        require(x_stride % 8 == 0 && res_stride % 8 == 0 && y_stride % 8 == 0 && al16(d_x) && al16(d_res) &&
+                    al16(d_y), "se_gate_residual: strides/pointers must be 8-channel aligned");
+        const long n = (long)batch * T * (C / 8);
+        hipLaunchKernelGGL(se_gate_residual_kernel, dim3(cdiv(n, 256)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, d_gate,
+                           static_cast<const half_t*>(d_res), res_stride, batch, T, C, static_cast<half_t*>(d_y),
+                           y_stride);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_asp_stats(const void* d_x, int x_stride, int batch, int T, int C, float eps, float* d_out,
+                             void* stream) {
+    return guarded([&] {
+        require(d_x && d_out, "asp_stats: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0 && x_stride >= C, "asp_stats: bad shape");
+        hipLaunchKernelGGL(asp_stats_kernel, dim3(cdiv(C, 256), batch), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, eps,
+                           d_out);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_asp_pool(const float* d_logits, int l_stride, const void* d_x, int x_stride, int batch, int T,
+                            int C, float eps, float* d_out, void* stream) {
+    return guarded([&] {
+        require(d_logits && d_x && d_out, "asp_pool: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0 && x_stride >= C && l_stride >= C, "asp_pool: bad shape");
+        hipLaunchKernelGGL(asp_pool_kernel, dim3(cdiv(C, 256), batch), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), d_logits, l_stride, static_cast<const half_t*>(d_x),
+                           x_stride, T, C, eps, d_out);
+        VDK_HIP(hipGetLastError());
+    });
+}

@@ -77,7 +77,8 @@ __global__ __launch_bounds__(256) void linear_partial_kernel(const float* __rest
 
 __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restrict__ part, int nsplit, int B,
                                                             int out_dim, const float* __restrict__ bias,
-                                                            const float* __restrict__ mv, float* __restrict__ y) {
+                                                            const float* __restrict__ mv, int relu,
+                                                            float* __restrict__ y) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     if (i >= (long)B * out_dim) return;
     const int o = (int)(i % out_dim);
@@ -96,6 +97,7 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restr
     float r = (float)s;
     if (bias) r += bias[o];
     if (mv) r -= mv[o];
+    if (relu) r = fmaxf(r, 0.0f);
     y[i] = r;
 }
 
@@ -136,9 +138,9 @@ extern "C" size_t vdk_linear_workspace_size(int batch, int in_dim, int out_dim) 
     return sizeof(float) * (size_t)linear_splits(in_dim) * batch * out_dim;
 }
 
-extern "C" int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
-                          const float* d_mean_vec, int out_dim, float* d_y, void* d_work, size_t work_bytes,
-                          void* stream) {
+extern "C" int vdk_linear_ex(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
+                             const float* d_mean_vec, int out_dim, int relu, float* d_y, void* d_work,
+                             size_t work_bytes, void* stream) {
     return guarded([&] {
         require(d_x && d_w && d_y && d_work, "linear: NULL device pointer");
         require(batch > 0 && in_dim > 0 && out_dim > 0, "linear: empty shape");
@@ -153,9 +155,15 @@ extern "C" int vdk_linear(const float* d_x, int batch, int in_dim, const float* 
                            dim3(256), 0, s, d_x, batch, in_dim, d_w, out_dim, slice, part);
         VDK_HIP(hipGetLastError());
         hipLaunchKernelGGL(linear_reduce_kernel, dim3(cdiv((long)batch * out_dim, 256)), dim3(256), 0, s, part,
-                           nsplit, batch, out_dim, d_bias, d_mean_vec, d_y);
+                           nsplit, batch, out_dim, d_bias, d_mean_vec, relu ? 1 : 0, d_y);
         VDK_HIP(hipGetLastError());
     });
+}
+
+extern "C" int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
+                          const float* d_mean_vec, int out_dim, float* d_y, void* d_work, size_t work_bytes,
+                          void* stream) {
+    return vdk_linear_ex(d_x, batch, in_dim, d_w, d_bias, d_mean_vec, out_dim, 0, d_y, d_work, work_bytes, stream);
 }
 
 extern "C" int vdk_l2norm(float* d_x, int batch, int dim, void* stream) {

@@ -25,6 +25,20 @@ class FbankCfg(C.Structure):
                 ("low_freq", C.c_float), ("high_freq", C.c_float), ("cmn", C.c_int)]
 
 
+class ConvDesc(C.Structure):
+    """vdk_conv_desc (include/vdk.h)."""
+    _fields_ = [("x", _vp), ("batch", C.c_int), ("H", C.c_int), ("W", C.c_int), ("IC", C.c_int),
+                ("x_stride", C.c_int),
+                ("w", _vp), ("OC", C.c_int), ("KH", C.c_int), ("KW", C.c_int), ("stride", C.c_int),
+                ("pad", C.c_int), ("dilation", C.c_int),
+                ("bias", _vp), ("bias_batch_stride", C.c_int),
+                ("residual", _vp), ("res_stride", C.c_int),
+                ("post_scale", _vp), ("post_shift", _vp),
+                ("relu", C.c_int), ("tanh_after", C.c_int),
+                ("y", _vp), ("y_stride", C.c_int), ("y_f32", C.c_int),
+                ("tile", C.c_int)]
+
+
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
               sample_rate=16000):
     return FbankCfg(sample_rate, n_mels, n_fft, win, hop, preemph, low, high, int(cmn))
@@ -78,13 +92,24 @@ _SIGS = {
                                   C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp]),
     "vdk_conv2d_nhwc_tile": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int]),
+    "vdk_conv2d_ex": (C.c_int, [C.POINTER(ConvDesc), _vp]),
+    "vdk_conv2d_tile_fits_ex": (C.c_int, [C.c_int, C.POINTER(ConvDesc)]),
     "vdk_conv2d_tile_count": (C.c_int, []),
     "vdk_conv2d_tile_fits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "vdk_stem_conv3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_tstp": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "vdk_linear_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "vdk_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp, C.c_size_t, _vp]),
+    "vdk_linear_ex": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _vp, C.c_size_t,
+                                _vp]),
     "vdk_l2norm": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
+    "vdk_feats_tmajor": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_reflect_pad_add": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_channel_mean": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_se_gate_residual": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int,
+                                       _vp]),
+    "vdk_asp_stats": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "vdk_asp_pool": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
 }
 
 

@@ -183,3 +183,85 @@ def write_resnet34(path, seed, **kw):
     kv, tensors = make_resnet34(seed, **kw)
     G.write_gguf(path, kv, tensors)
     return path
+
+
+# ---------------------------------------------------------------- ECAPA-TDNN
+
+def _bn(ws, prefix, c, tensors):
+    """Eval-mode BatchNorm1d parameters (gamma 1, beta 0, mean N(0,0.1), var U(0.5,1.5))."""
+    tensors.append((prefix + ".weight", G.GGML_F32, [c], np.ones(c, dtype=np.float32)))
+    tensors.append((prefix + ".bias", G.GGML_F32, [c], np.zeros(c, dtype=np.float32)))
+    tensors.append((prefix + ".running_mean", G.GGML_F32, [c], (0.1 * normal(ws.next(), c)).astype(np.float32)))
+    tensors.append((prefix + ".running_var", G.GGML_F32, [c], (0.5 + uniform(ws.next(), c)).astype(np.float32)))
+
+
+def _f16_exact(a):
+    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def make_ecapa(seed, channels=1024, mfa=1536, n_mels=80, scale=8, se_ch=128, att_ch=128, emb_dim=192,
+               n_res_blocks=3, k0=5, wtype=G.GGML_F16):
+    """Random-init SpeechBrain ECAPA-TDNN in the reference GGUF schema.
+
+    Tensor names and torch shapes follow models/ecapa_tdnn_manifest.txt of the
+    reference.  Weight values are f16-representable; storage follows the
+    reference converter's f16 plan (scripts/convert_voicedetect_to_gguf.py
+    quant_plan): 1x1 weights outside fc/asp/se/tdnn1/tdnn2 (i.e. mfa) are stored
+    F16 as a 2-D [OC, IC] matrix, everything else F32 (so k>1 convs keep the
+    [OC, IC, K] F32 layout the reference's im2col path needs).  BatchNorm
+    follows the ReLU (Conv -> ReLU -> BN), so it is kept as explicit eval-mode
+    parameters, not folded.
+    """
+    ws = _WeightStream(seed)
+    T = []
+
+    def conv(name, oc, ic, k, quantizable=False):
+        w = _f16_exact(normal(ws.next(), oc * ic * k).reshape(oc, ic, k) * np.sqrt(2.0 / (ic * k)))
+        b = (0.01 * normal(ws.next(), oc)).astype(np.float32)
+        if quantizable and k == 1 and wtype != G.GGML_F32:
+            T.append((name + ".weight", wtype, [oc, ic], w.reshape(oc, ic)))
+        else:
+            T.append((name + ".weight", G.GGML_F32, [oc, ic, k], w))
+        T.append((name + ".bias", G.GGML_F32, [oc], b))
+
+    conv("blocks.0.conv.conv", channels, n_mels, k0)
+    _bn(ws, "blocks.0.norm.norm", channels, T)
+    g = channels // scale
+    for i in range(1, n_res_blocks + 1):
+        p = f"blocks.{i}"
+        conv(p + ".tdnn1.conv.conv", channels, channels, 1)
+        _bn(ws, p + ".tdnn1.norm.norm", channels, T)
+        for j in range(scale - 1):
+            conv(f"{p}.res2net_block.blocks.{j}.conv.conv", g, g, 3)
+            _bn(ws, f"{p}.res2net_block.blocks.{j}.norm.norm", g, T)
+        conv(p + ".tdnn2.conv.conv", channels, channels, 1)
+        _bn(ws, p + ".tdnn2.norm.norm", channels, T)
+        conv(p + ".se_block.conv1.conv", se_ch, channels, 1)
+        conv(p + ".se_block.conv2.conv", channels, se_ch, 1)
+    conv("mfa.conv.conv", mfa, channels * n_res_blocks, 1, quantizable=True)
+    _bn(ws, "mfa.norm.norm", mfa, T)
+    conv("asp.tdnn.conv.conv", att_ch, 3 * mfa, 1)
+    _bn(ws, "asp.tdnn.norm.norm", att_ch, T)
+    conv("asp.conv.conv", mfa, att_ch, 1)
+    _bn(ws, "asp_bn.norm", 2 * mfa, T)
+    conv("fc.conv", emb_dim, 2 * mfa, 1)
+    kv = {
+        "general.architecture": "voicedetect",
+        "general.name": f"synthetic-ecapa-tdnn-seed{seed}",
+        "voicedetect.arch": "ecapa_tdnn",
+        "voicedetect.embedding_dim": emb_dim,
+        "voicedetect.l2_normalize": True,
+        "voicedetect.ecapa.channels": channels,
+        "voicedetect.ecapa.n_blocks": n_res_blocks + 1,
+        "voicedetect.ecapa.se_channels": se_ch,
+        "voicedetect.ecapa.res2net_scale": scale,
+        "voicedetect.ecapa.attention_channels": att_ch,
+    }
+    kv.update(_fbank_kv(n_mels))
+    return kv, T
+
+
+def write_ecapa(path, seed, **kw):
+    kv, tensors = make_ecapa(seed, **kw)
+    G.write_gguf(path, kv, tensors)
+    return path
