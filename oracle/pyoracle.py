@@ -401,3 +401,22 @@ def conv1d_same(x, w, b, dilation=1):
     y = np.zeros((w.shape[0], x.shape[1]), dtype=np.float32)
     L.orc_conv1d_same(x, x.shape[1], C.byref(c), dilation, y)
     return y
+
+
+def bn_apply(x, gamma, beta, mean, var):
+    """Oracle eval BatchNorm1d on x [C, T] (returns a new array)."""
+    L = _ecapa_sigs()
+    y = np.array(x, dtype=np.float32, order="C", copy=True)
+    keep = [np.ascontiguousarray(a, dtype=np.float32) for a in (gamma, beta, mean, var)]
+    bn = BN(*(a.ctypes.data_as(_fp) for a in keep), y.shape[0])
+    L.orc_bn_apply(y, y.shape[1], C.byref(bn))
+    return y
+
+
+def ecapa_asp(net, x):
+    """Oracle attentive statistics pooling of an OracleEcapa on x [mfa, T] -> [2*mfa]."""
+    L = _ecapa_sigs()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(2 * x.shape[0], dtype=np.float32)
+    L.orc_ecapa_asp(C.byref(net.net), x, x.shape[1], out)
+    return out

@@ -1,0 +1,339 @@
+"""Parity of the ECAPA-TDNN GPU path (src/encoder.cpp) against the oracle.
+
+Per layer, at the 4 s / batch-64 shape (T = 398 frames): every TDNN conv
+form the encoder uses (block0 k=5 over reflect-padded FBank, the dilated k=3
+Res2Net group convs written into their channel slice, 1x1 layers over channel
+slices, the ASP attention convs with per-clip bias / tanh / f32 logits) within
+2e-3 relative of the oracle's f32 conv1d + ReLU + BatchNorm; the data-movement
+kernels bit-exact against numpy; the reductions (SE mean, gate, ASP stats and
+pooling, FC+ReLU) against f64 closed forms.  End to end: a random-init
+ECAPA-TDNN (C=1024, scale 8, MFA 1536, 192-d) behind the C ABI, pooled
+statistics within 2e-3 relative L2 and embeddings at cosine >= 0.9999.
+"""
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import pyoracle as O
+from gpu_util import announce, close_report, cosine, device_ok
+from vdamd import gguf, lib, synth
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
+
+RTOL = 2e-3
+ATOL_RMS = 2e-3
+B = 64
+N4S = 64000
+T4S = 398
+CLIPS = (0, 31, 63)
+
+
+def _sync():
+    lib.check(lib.lib().vdk_synchronize())
+
+
+def _f16w(rng, oc, ic, k):
+    return (rng.standard_normal((oc, ic, k), dtype=np.float32) * np.sqrt(2.0 / (ic * k))).astype(np.float16)
+
+
+def _bn_params(rng, c):
+    return (1.0 + 0.1 * rng.standard_normal(c, dtype=np.float32), 0.1 * rng.standard_normal(c, dtype=np.float32),
+            0.1 * rng.standard_normal(c, dtype=np.float32), 0.5 + rng.random(c, dtype=np.float32))
+
+
+def _scale_shift(bn):
+    g, b, m, v = bn
+    s = (g / np.sqrt(v + np.float32(1e-5))).astype(np.float32)
+    return s, (b - s * m).astype(np.float32)
+
+
+def tdnn_gpu(x_ptr, batch, W, IC, xs, w, dil, bias_dev, y_ptr, ys, bias_bs=0, bn=None, relu=True, tanh=False,
+             y_f32=False, ic_pad=None):
+    """One vdk_conv2d_ex launch of a time-major TDNN layer (H = 1, pad 0)."""
+    OC, ic_w, K = w.shape
+    icp = ic_pad or IC
+    wp = np.zeros((OC, K, icp), dtype=np.float16)
+    wp[:, :, :ic_w] = w.transpose(0, 2, 1)
+    dw = lib.DeviceBuffer.from_array(wp)
+    keep = [dw]
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = x_ptr, batch, 1, W, icp, xs
+    d.w, d.OC, d.KH, d.KW, d.stride, d.pad, d.dilation = dw.ptr, OC, 1, K, 1, 0, dil
+    d.bias, d.bias_batch_stride = bias_dev.ptr, bias_bs
+    if bn is not None:
+        s, t = _scale_shift(bn)
+        ds, dt = lib.DeviceBuffer.from_array(s), lib.DeviceBuffer.from_array(t)
+        keep += [ds, dt]
+        d.post_scale, d.post_shift = ds.ptr, dt.ptr
+    d.relu, d.tanh_after = int(relu), int(tanh)
+    d.y, d.y_stride, d.y_f32 = y_ptr, ys, int(y_f32)
+    d.tile = -1
+    lib.check(lib.lib().vdk_conv2d_ex(d, None))
+    _sync()
+
+
+def _oracle_tdnn(x_ct, w, b, dil, bn=None, relu=True):
+    y = O.conv1d_same(x_ct, w.astype(np.float32), b, dilation=dil)
+    if relu:
+        y = np.maximum(y, 0)
+    if bn is not None:
+        y = O.bn_apply(y, *bn)
+    return y
+
+
+def _assert_close(got, ref, tag):
+    ok, ratio, rel = close_report(got, ref, RTOL, ATOL_RMS)
+    assert ok and rel <= 2e-3, f"{tag}: max tol ratio {ratio:.3f}, rel-L2 {rel:.2e}"
+    return rel
+
+
+def test_block0_reflect_pad_and_k5_conv():
+    rng = np.random.default_rng(11)
+    T, nm, C = T4S, 80, 1024
+    feats = (3.0 * rng.standard_normal((B, nm, T), dtype=np.float32))
+    announce(f"ecapa block0 B={B} T={T} 80->1024 k5")
+    L = lib.lib()
+    df = lib.DeviceBuffer.from_array(feats)
+    x0p = lib.DeviceBuffer(B * (T + 4) * 96 * 2)
+    lib.check(L.vdk_feats_tmajor(df.ptr, B, nm, T, 2, 96, x0p.ptr, None))
+    _sync()
+    got_x = x0p.to_array(np.float16, (B, T + 4, 96))
+    want = np.zeros((B, T + 4, 96), dtype=np.float16)
+    want[:, :, :nm] = np.pad(feats, ((0, 0), (0, 0), (2, 2)), mode="reflect").transpose(0, 2, 1).astype(np.float16)
+    assert np.array_equal(got_x.view(np.uint16), want.view(np.uint16))
+    w = _f16w(rng, C, nm, 5)
+    b = (0.01 * rng.standard_normal(C)).astype(np.float32)
+    bn = _bn_params(rng, C)
+    db = lib.DeviceBuffer.from_array(b)
+    y = lib.DeviceBuffer(B * T * C * 2)
+    tdnn_gpu(x0p.ptr, B, T + 4, 96, 96, w, 1, db, y.ptr, C, bn=bn, ic_pad=96)
+    got = y.to_array(np.float16, (B, T, C)).astype(np.float32)
+    for c in CLIPS:
+        rel = _assert_close(got[c].T, _oracle_tdnn(feats[c], w, b, 1, bn), f"block0 clip {c}")
+        announce(f"block0 clip {c} rel-L2 {rel:.2e}")
+
+
+@pytest.mark.parametrize("dil", [2, 3, 4])
+def test_res2net_group_conv_in_place(dil):
+    rng = np.random.default_rng(20 + dil)
+    T, C, G, j = T4S, 1024, 128, 3
+    announce(f"ecapa res2 group conv B={B} T={T} dil={dil}")
+    t1 = rng.standard_normal((B, T, C), dtype=np.float32).astype(np.float16)
+    L = lib.lib()
+    dt1 = lib.DeviceBuffer.from_array(t1)
+    padb = lib.DeviceBuffer(B * (T + 2 * dil) * G * 2)
+    lib.check(L.vdk_reflect_pad_add(dt1.ptr + j * G * 2, C, dt1.ptr + (j - 1) * G * 2, C, B, T, G, dil, padb.ptr,
+                                    None))
+    _sync()
+    s = t1[:, :, j * G:(j + 1) * G].astype(np.float32) + t1[:, :, (j - 1) * G:j * G].astype(np.float32)
+    want = np.pad(s, ((0, 0), (dil, dil), (0, 0)), mode="reflect").astype(np.float16)
+    got_pad = padb.to_array(np.float16, (B, T + 2 * dil, G))
+    assert np.array_equal(got_pad.view(np.uint16), want.view(np.uint16))
+    w = _f16w(rng, G, G, 3)
+    b = (0.01 * rng.standard_normal(G)).astype(np.float32)
+    bn = _bn_params(rng, G)
+    db = lib.DeviceBuffer.from_array(b)
+    tdnn_gpu(padb.ptr, B, T + 2 * dil, G, G, w, dil, db, dt1.ptr + j * G * 2, C, bn=bn)
+    out = dt1.to_array(np.float16, (B, T, C))
+    keep = np.ones(C, dtype=bool)
+    keep[j * G:(j + 1) * G] = False
+    assert np.array_equal(out[:, :, keep].view(np.uint16), t1[:, :, keep].view(np.uint16))
+    got = out[:, :, j * G:(j + 1) * G].astype(np.float32)
+    for c in CLIPS:
+        ref = _oracle_tdnn(s[c].T, w, b, dil, bn)
+        rel = _assert_close(got[c].T, ref, f"res2 dil {dil} clip {c}")
+        announce(f"res2 dil {dil} clip {c} rel-L2 {rel:.2e}")
+
+
+def test_1x1_layers_over_channel_slices():
+    rng = np.random.default_rng(31)
+    T, C, M = T4S, 1024, 1536
+    announce(f"ecapa 1x1 slices B={B} T={T}")
+    cat = rng.standard_normal((B, T, 3 * C), dtype=np.float32).astype(np.float16)
+    dcat = lib.DeviceBuffer.from_array(cat)
+    # tdnn1 of block 3 reads slice 1 of the MFA input (stride 3C)
+    w = _f16w(rng, C, C, 1)
+    b = (0.01 * rng.standard_normal(C)).astype(np.float32)
+    bn = _bn_params(rng, C)
+    db = lib.DeviceBuffer.from_array(b)
+    y = lib.DeviceBuffer(B * T * C * 2)
+    tdnn_gpu(dcat.ptr + C * 2, B, T, C, 3 * C, w, 1, db, y.ptr, C, bn=bn)
+    got = y.to_array(np.float16, (B, T, C)).astype(np.float32)
+    for c in CLIPS:
+        _assert_close(got[c].T, _oracle_tdnn(cat[c, :, C:2 * C].astype(np.float32).T, w, b, 1, bn),
+                      f"tdnn1 slice clip {c}")
+    # MFA over the whole concatenation
+    wm = _f16w(rng, M, 3 * C, 1)
+    bm = (0.01 * rng.standard_normal(M)).astype(np.float32)
+    bnm = _bn_params(rng, M)
+    dbm = lib.DeviceBuffer.from_array(bm)
+    ym = lib.DeviceBuffer(B * T * M * 2)
+    tdnn_gpu(dcat.ptr, B, T, 3 * C, 3 * C, wm, 1, dbm, ym.ptr, M, bn=bnm)
+    gotm = ym.to_array(np.float16, (B, T, M)).astype(np.float32)
+    for c in CLIPS:
+        rel = _assert_close(gotm[c].T, _oracle_tdnn(cat[c].astype(np.float32).T, wm, bm, 1, bnm), f"mfa clip {c}")
+        announce(f"mfa clip {c} rel-L2 {rel:.2e}")
+
+
+def test_asp_attention_convs():
+    rng = np.random.default_rng(41)
+    T, M, A = T4S, 1536, 128
+    announce(f"ecapa asp convs B={B} T={T}")
+    x = np.abs(rng.standard_normal((B, T, M), dtype=np.float32) * 4).astype(np.float16)
+    dx = lib.DeviceBuffer.from_array(x)
+    w = _f16w(rng, A, M, 1)
+    pb = rng.standard_normal((B, A), dtype=np.float32)
+    bn = _bn_params(rng, A)
+    dpb = lib.DeviceBuffer.from_array(pb)
+    a1 = lib.DeviceBuffer(B * T * A * 2)
+    tdnn_gpu(dx.ptr, B, T, M, M, w, 1, dpb, a1.ptr, A, bias_bs=A, bn=bn, tanh=True)
+    ga1 = a1.to_array(np.float16, (B, T, A))
+    for c in CLIPS:
+        ref = np.tanh(_oracle_tdnn(x[c].astype(np.float32).T, w, pb[c], 1, bn))
+        _assert_close(ga1[c].astype(np.float32).T, ref, f"asp.tdnn clip {c}")
+    wc = _f16w(rng, M, A, 1)
+    bc = (0.01 * rng.standard_normal(M)).astype(np.float32)
+    dbc = lib.DeviceBuffer.from_array(bc)
+    lg = lib.DeviceBuffer(B * T * M * 4)
+    tdnn_gpu(a1.ptr, B, T, A, A, wc, 1, dbc, lg.ptr, M, relu=False, y_f32=True)
+    glg = lg.to_array(np.float32, (B, T, M))
+    for c in CLIPS:
+        ref = _oracle_tdnn(ga1[c].astype(np.float32).T, wc, bc, 1, None, relu=False)
+        rel = _assert_close(glg[c].T, ref, f"asp.conv clip {c}")
+        announce(f"asp.conv clip {c} rel-L2 {rel:.2e}")
+
+
+def test_se_and_asp_reductions():
+    rng = np.random.default_rng(51)
+    T, C, M = T4S, 1024, 1536
+    L = lib.lib()
+    announce(f"ecapa reductions B={B} T={T}")
+    # SE squeeze over a channel slice of a wider tensor
+    t2 = rng.standard_normal((B, T, 2 * C), dtype=np.float32).astype(np.float16)
+    dt2 = lib.DeviceBuffer.from_array(t2)
+    dm = lib.DeviceBuffer(B * C * 4)
+    lib.check(L.vdk_channel_mean(dt2.ptr + C * 2, 2 * C, B, T, C, dm.ptr, None))
+    _sync()
+    want = t2[:, :, C:].astype(np.float64).mean(axis=1)
+    assert np.abs(dm.to_array(np.float32, (B, C)) - want).max() <= 1e-6 * max(1.0, np.abs(want).max())
+    # gate + residual into a slice of the MFA input
+    gate = rng.standard_normal((B, C), dtype=np.float32) * 3
+    res = rng.standard_normal((B, T, C), dtype=np.float32).astype(np.float16)
+    dg, dr = lib.DeviceBuffer.from_array(gate), lib.DeviceBuffer.from_array(res)
+    cat = np.zeros((B, T, 3 * C), dtype=np.float16)
+    dcat = lib.DeviceBuffer.from_array(cat)
+    lib.check(L.vdk_se_gate_residual(dt2.ptr, 2 * C, dg.ptr, dr.ptr, C, B, T, C, dcat.ptr + 2 * C * 2, 3 * C, None))
+    _sync()
+    gcat = dcat.to_array(np.float16, (B, T, 3 * C))
+    sig = 1.0 / (1.0 + np.exp(-gate.astype(np.float64)))
+    want = t2[:, :, :C].astype(np.float64) * sig[:, None, :] + res.astype(np.float64)
+    got = gcat[:, :, 2 * C:].astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2.0 ** -10 * np.abs(want) + 1e-6)
+    assert not gcat[:, :, :2 * C].any()
+    # ASP global statistics and attentive pooling
+    x = (rng.standard_normal((B, T, M), dtype=np.float32) * 2 + 1).astype(np.float16)
+    x[1, :, 5] = 0.5           # a constant channel: variance clamps to eps
+    dx = lib.DeviceBuffer.from_array(x)
+    ds = lib.DeviceBuffer(B * 2 * M * 4)
+    lib.check(L.vdk_asp_stats(dx.ptr, M, B, T, M, 1e-12, ds.ptr, None))
+    _sync()
+    xs = x.astype(np.float64)
+    mu = xs.mean(axis=1)
+    sd = np.sqrt(np.maximum(((xs - mu[:, None, :]) ** 2).mean(axis=1), 1e-12))
+    gs = ds.to_array(np.float32, (B, 2 * M))
+    assert np.allclose(gs[:, :M], mu, rtol=1e-5, atol=1e-6)
+    assert np.allclose(gs[:, M:], sd, rtol=1e-5, atol=1e-6)
+    assert gs[1, M + 5] == np.float32(1e-6)
+    logits = rng.standard_normal((B, T, M), dtype=np.float32) * 4
+    dl = lib.DeviceBuffer.from_array(logits)
+    dp = lib.DeviceBuffer(B * 2 * M * 4)
+    lib.check(L.vdk_asp_pool(dl.ptr, M, dx.ptr, M, B, T, M, 1e-12, dp.ptr, None))
+    _sync()
+    lg = logits.astype(np.float64)
+    a = np.exp(lg - lg.max(axis=1, keepdims=True))
+    a /= a.sum(axis=1, keepdims=True)
+    mu = (a * xs).sum(axis=1)
+    sd = np.sqrt(np.maximum((a * (xs - mu[:, None, :]) ** 2).sum(axis=1), 1e-12))
+    gp = dp.to_array(np.float32, (B, 2 * M))
+    assert np.allclose(gp[:, :M], mu, rtol=1e-5, atol=1e-5)
+    assert np.allclose(gp[:, M:], sd, rtol=1e-5, atol=1e-5)
+
+
+def test_linear_relu():
+    rng = np.random.default_rng(61)
+    L = lib.lib()
+    Bn, I, Oo = 64, 1024, 128
+    x = rng.standard_normal((Bn, I), dtype=np.float32)
+    w = (rng.standard_normal((Oo, I), dtype=np.float32) / 32).astype(np.float32)
+    b = rng.standard_normal(Oo, dtype=np.float32)
+    dx, dw, db = (lib.DeviceBuffer.from_array(a) for a in (x, w, b))
+    dy = lib.DeviceBuffer(Bn * Oo * 4)
+    nw = L.vdk_linear_workspace_size(Bn, I, Oo)
+    work = lib.DeviceBuffer(nw)
+    lib.check(L.vdk_linear_ex(dx.ptr, Bn, I, dw.ptr, db.ptr, None, Oo, 1, dy.ptr, work.ptr, nw, None))
+    _sync()
+    want = np.maximum(x.astype(np.float64) @ w.astype(np.float64).T + b, 0)
+    got = dy.to_array(np.float32, (Bn, Oo))
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5)
+    assert (got == 0).sum() == (want == 0).sum()
+
+
+# ------------------------------------------------------------------ end to end
+
+@pytest.fixture(scope="module")
+def ecapa():
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "ecapa_f16.gguf")
+    synth.write_ecapa(path, seed=7)
+    ctx = lib.Context(path)
+    net = O.OracleEcapa(gguf.GGUFFile(path))
+    yield path, ctx, net
+    ctx.close()
+
+
+def test_ecapa_batch64_matches_oracle(ecapa):
+    path, ctx, net = ecapa
+    pcm = synth.clips(4711, B, N4S)
+    announce("e2e ecapa B=64 4s capture")
+    cap = ctx.capture(pcm)
+    assert cap["pooled"].shape[1] == 2 * 1536
+    for c in CLIPS:
+        feats = O.fbank(pcm[c])
+        assert np.abs(cap["feats"][c] - feats).max() <= 1e-4
+        emb, caps = net.forward(feats, capture=True)
+        rel = np.linalg.norm(cap["pooled"][c] - caps["pooled"]) / np.linalg.norm(caps["pooled"])
+        assert rel <= 2e-3, f"pooled rel-L2 {rel:.2e} clip {c}"
+        assert cosine(cap["pre_norm"][c], caps["pre_norm"]) >= 0.9999
+        cs = cosine(cap["emb"][c], emb)
+        announce(f"ecapa clip {c}: cosine {cs:.7f} pooled rel {rel:.2e}")
+        assert cs >= 0.9999
+        assert abs(np.linalg.norm(cap["emb"][c]) - 1.0) < 1e-5
+    # batch invariance: the same clip alone gives the same bits
+    one = ctx.embed_batch(pcm[31:32])
+    assert np.array_equal(one[0], cap["emb"][31])
+
+
+@pytest.mark.parametrize("n", [400, 4000, 40000])
+def test_ecapa_embed_pcm_lengths(ecapa, n):
+    path, ctx, net = ecapa
+    announce(f"e2e ecapa B=1 n={n}")
+    pcm = synth.clip(900 + n, n)
+    got = ctx.embed_pcm(pcm)
+    ref = net.forward(O.fbank(pcm))
+    assert got.shape == (192,)
+    assert cosine(got, ref) >= 0.9999
+
+
+def test_ecapa_verify_matches_oracle(ecapa, golden_dir):
+    path, ctx, net = ecapa
+    announce("e2e ecapa verify")
+    a = synth.clip(1, 48000)
+    b = synth.clip(2, 56000)
+    d_gpu, _ = ctx.verify_pcm(a, b, 0.5)
+    ea, eb = net.forward(O.fbank(a)), net.forward(O.fbank(b))
+    d_ref = 1.0 - float(np.dot(ea.astype(np.float64), eb.astype(np.float64)))
+    assert abs(d_gpu - d_ref) <= 2e-3
+    for thr in (d_ref - 5e-3, d_ref + 5e-3):
+        assert ctx.verify_pcm(a, b, thr)[1] == (d_ref <= thr)

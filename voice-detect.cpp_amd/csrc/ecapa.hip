@@ -31,11 +31,6 @@ __device__ __forceinline__ int reflect_idx(int j, int pad, int T) {
     return t < 0 ? 0 : (t > T - 1 ? T - 1 : t);
 }
 
-__device__ __forceinline__ double wsum(double v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
 __global__ __launch_bounds__(256) void feats_tmajor_kernel(const float* __restrict__ f, int B, int C, int T,
                                                            int pad, int Cpad, half_t* __restrict__ out) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
@@ -175,7 +170,8 @@ extern "C" int vdk_reflect_pad_add(const void* d_a, int a_stride, const void* d_
                                    int G, int pad, void* d_out, void* stream) {
     return guarded([&] {
         require(d_a && d_out, "reflect_pad_add: NULL device pointer");
-        require(batch > 0 && T > 0 && G > 0 && G % 8 == 0 && pad >= 0, "reflect_pad_add: bad shape");
+        require(batch > 0 && T > 0 && G > 0 && G % 8 == 0 && pad >= 0 && a_stride >= G && (!d_b || b_stride >= G),
+                "reflect_pad_add: bad shape");
         require(a_stride % 8 == 0 && (!d_b || b_stride % 8 == 0) && al16(d_a) && (!d_b || al16(d_b)) && al16(d_out),
                 "reflect_pad_add: strides/pointers must be 8-channel aligned");
         const long n = (long)batch * (T + 2 * pad) * (G / 8);
@@ -200,7 +196,8 @@ extern "C" int vdk_se_gate_residual(const void* d_x, int x_stride, const float* 
                                     int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream) {
     return guarded([&] {
         require(d_x && d_gate && d_res && d_y, "se_gate_residual: NULL device pointer");
-        require(batch > 0 && T > 0 && C > 0 && C % 8 == 0, "se_gate_residual: bad shape");
+        require(batch > 0 && T > 0 && C > 0 && C % 8 == 0 && x_stride >= C && res_stride >= C && y_stride >= C,
+                "se_gate_residual: bad shape");
         require(x_stride % 8 == 0 && res_stride % 8 == 0 && y_stride % 8 == 0 && al16(d_x) && al16(d_res) &&
                     al16(d_y), "se_gate_residual: strides/pointers must be 8-channel aligned");
         const long n = (long)batch * T * (C / 8);

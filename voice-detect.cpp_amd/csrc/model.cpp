@@ -5,19 +5,18 @@
 #include <cmath>
 #include <cstring>
 
+#include "arena.hpp"
 #include "audio.hpp"
 #include "common.hpp"
 
 namespace vdk {
 
-namespace {
-
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-void check(int rc) {
+void check_rc(int rc) {
     if (rc != 0) throw Error(vdk_last_error());
 }
 
+namespace {
+void check(int rc) { check_rc(rc); }
 }  // namespace
 
 std::unique_ptr<Model> Model::load(const std::string& path) {
@@ -81,17 +80,19 @@ void Model::ensure_device() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) throw Error("voicedetect: no HIP device available");
     VDK_HIP(hipGetDevice(&device_));
-    if (cfg_.arch != "wespeaker_resnet34") {
-        if (cfg_.arch == "ecapa_tdnn" || cfg_.arch == "eres2net" || cfg_.arch == "campplus")
+    const bool resnet = cfg_.arch == "wespeaker_resnet34", ecapa = cfg_.arch == "ecapa_tdnn";
+    if (!resnet && !ecapa) {
+        if (cfg_.arch == "eres2net" || cfg_.arch == "campplus")
             throw Error("voicedetect: arch '" + cfg_.arch + "' is not implemented by this build yet");
         throw Error("voicedetect: unsupported arch '" + cfg_.arch + "'");
     }
-    VDK_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    if (!stream_) VDK_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     const size_t tb = vdk_fbank_tables_size(&cfg_.fbank);
     if (tb == 0) throw Error(vdk_last_error());
-    VDK_HIP(hipMalloc(&fb_tables_, tb));
+    if (!fb_tables_) VDK_HIP(hipMalloc(&fb_tables_, tb));
     check(vdk_fbank_tables_fill(&cfg_.fbank, fb_tables_));
-    upload_resnet();
+    if (resnet) upload_resnet();
+    else upload_ecapa();
     ready_ = true;
 }
 
@@ -102,19 +103,11 @@ void Model::upload_resnet() {
     require(nb > 0 && r.conv1_bias.size() == nb && r.conv2_weight.size() == nb && r.conv2_bias.size() == nb &&
                 r.down_weight.size() == nb && r.down_bias.size() == nb && r.stride.size() == nb,
             "voicedetect: inconsistent resnet block manifest");
-    std::vector<uint8_t> host;
-    struct Fix { size_t off; void** dst_void; float** dst_float; };
-    std::vector<Fix> fixes;
-    auto put = [&](const void* src, size_t bytes) {
-        const size_t off = align256(host.size());
-        host.resize(off + bytes);
-        std::memcpy(host.data() + off, src, bytes);
-        return off;
-    };
+    ArenaBuilder arena;
     auto put_f32 = [&](const std::string& name, size_t expect, float** dst) {
         std::vector<float> v = g.to_f32(name);
         require(expect == 0 || v.size() == expect, "voicedetect: tensor '" + name + "' has the wrong size");
-        fixes.push_back({put(v.data(), v.size() * 4), nullptr, dst});
+        arena.put(v, dst);
         return v.size();
     };
     // conv weight ne = [KW, KH, IC, OC] -> f16 [OC][KH][KW][IC]
@@ -140,7 +133,7 @@ void Model::upload_resnet() {
                         packed[dst] = h16 ? h16[src] : float_to_half_bits(f32[src]);
                     }
         c.ic = ic; c.oc = oc; c.k = k; c.stride = stride; c.pad = pad;
-        fixes.push_back({put(packed.data(), packed.size() * 2), &c.w, nullptr});
+        arena.put(packed, &c.w);
         put_f32(bn, (size_t)oc, &c.b);
         return oc;
     };
@@ -179,28 +172,40 @@ void Model::upload_resnet() {
     if (!r.seg_bias.empty()) put_f32(r.seg_bias, (size_t)cfg_.embedding_dim, &seg_b_);
     if (!r.mean_vec.empty()) put_f32(r.mean_vec, (size_t)cfg_.embedding_dim, &mean_vec_);
 
-    VDK_HIP(hipMalloc(&arena_, host.size()));
-    VDK_HIP(hipMemcpy(arena_, host.data(), host.size(), hipMemcpyHostToDevice));
-    uint8_t* base = static_cast<uint8_t*>(arena_);
-    for (const Fix& f : fixes) {
-        if (f.dst_void) *f.dst_void = base + f.off;
-        if (f.dst_float) *f.dst_float = reinterpret_cast<float*>(base + f.off);
-    }
+    arena_ = arena.upload();
+}
+
+void* Model::ws_alloc(size_t bytes) {
+    void* p = nullptr;
+    VDK_HIP(hipMalloc(&p, bytes < 256 ? 256 : bytes));
+    ws_.allocs.push_back(p);
+    return p;
 }
 
 void Model::free_workspace() {
-    Workspace& w = ws_;
-    for (void* p : {(void*)w.pcm, (void*)w.feats, w.act[0], w.act[1], w.act[2], w.act[3], (void*)w.pooled,
-                    (void*)w.pre, (void*)w.emb, w.fc_work})
-        if (p) (void)hipFree(p);
+    for (void* p : ws_.allocs) (void)hipFree(p);
     ws_ = Workspace();
 }
 
 void Model::ensure_workspace(int batch, int n_samples) {
-    if (ws_.act[0] && batch <= ws_.batch && n_samples == ws_.n_samples) return;
+    if (!ws_.allocs.empty() && batch <= ws_.batch && n_samples == ws_.n_samples) return;
     VDK_HIP(hipStreamSynchronize(stream_));
     free_workspace();
     const int T = frames(n_samples);
+    const int nmel = cfg_.fbank.n_mels;
+    Workspace& w = ws_;
+    w.batch = batch;
+    w.n_samples = n_samples;
+    w.pcm = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * n_samples));
+    w.feats = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * nmel * T));
+    w.pooled = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * pooled_dim_));
+    w.pre = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * cfg_.embedding_dim));
+    w.emb = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * cfg_.embedding_dim));
+    if (cfg_.arch == "ecapa_tdnn") alloc_ecapa_workspace(batch, T);
+    else alloc_resnet_workspace(batch, T);
+}
+
+void Model::alloc_resnet_workspace(int batch, int T) {
     const int nmel = cfg_.fbank.n_mels;
     size_t act = (size_t)nmel * T * stem_oc_;
     int H = nmel, W = T;
@@ -210,17 +215,10 @@ void Model::ensure_workspace(int batch, int n_samples) {
         act = std::max(act, (size_t)H * W * b.c1.oc);
     }
     Workspace& w = ws_;
-    w.batch = batch;
-    w.n_samples = n_samples;
     w.act_bytes = act * 2 * batch;
-    VDK_HIP(hipMalloc((void**)&w.pcm, sizeof(float) * (size_t)batch * n_samples));
-    VDK_HIP(hipMalloc((void**)&w.feats, sizeof(float) * (size_t)batch * nmel * T));
-    for (int i = 0; i < 4; ++i) VDK_HIP(hipMalloc(&w.act[i], w.act_bytes));
-    VDK_HIP(hipMalloc((void**)&w.pooled, sizeof(float) * (size_t)batch * pooled_dim_));
-    VDK_HIP(hipMalloc((void**)&w.pre, sizeof(float) * (size_t)batch * cfg_.embedding_dim));
-    VDK_HIP(hipMalloc((void**)&w.emb, sizeof(float) * (size_t)batch * cfg_.embedding_dim));
+    for (int i = 0; i < 4; ++i) w.act[i] = ws_alloc(w.act_bytes);
     w.fc_work_bytes = vdk_linear_workspace_size(batch, pooled_dim_, cfg_.embedding_dim);
-    VDK_HIP(hipMalloc(&w.fc_work, w.fc_work_bytes));
+    w.fc_work = ws_alloc(w.fc_work_bytes);
 }
 
 void Model::prof_begin(const char* name, double flops, double bytes) {
@@ -264,6 +262,19 @@ void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) 
     prof_begin("fbank", 0.0, 4.0 * batch * ((double)n_samples + (double)nmel * T));
     check(vdk_fbank(&cfg_.fbank, fb_tables_, d_pcm, batch, n_samples, ws_.feats, stream_));
     prof_end();
+    if (cfg_.arch == "ecapa_tdnn") encode_ecapa(batch, T);
+    else encode_resnet(batch, T);
+    const int E = cfg_.embedding_dim;
+    VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));
+    if (cfg_.l2_normalize) {
+        prof_begin("l2norm", 0.0, 8.0 * batch * E);
+        check(vdk_l2norm(d_out, batch, E, stream_));
+        prof_end();
+    }
+}
+
+void Model::encode_resnet(int batch, int T) {
+    const int nmel = cfg_.fbank.n_mels;
     // stem conv + ReLU
     prof_begin("stem3x3", 2.0 * 9 * stem_oc_ * (double)batch * nmel * T,
                4.0 * batch * nmel * T + 2.0 * batch * nmel * T * stem_oc_);
@@ -301,12 +312,6 @@ void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) 
     check(vdk_linear(ws_.pooled, batch, pooled_dim_, seg_w_, seg_b_, mean_vec_, E, ws_.pre, ws_.fc_work,
                      ws_.fc_work_bytes, stream_));
     prof_end();
-    VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));
-    if (cfg_.l2_normalize) {
-        prof_begin("l2norm", 0.0, 8.0 * batch * E);
-        check(vdk_l2norm(d_out, batch, E, stream_));
-        prof_end();
-    }
 }
 
 void Model::embed_batch_device(const float* d_pcm, int batch, int n_samples, float* d_out) {

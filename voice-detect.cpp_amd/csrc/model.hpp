@@ -37,6 +37,9 @@ struct ModelConfig {
     ResNetCfg resnet;
 };
 
+// Throws vdk::Error with vdk_last_error() when a vdk_* call returned nonzero.
+void check_rc(int rc);
+
 struct ProfileRecord {
     std::string name;
     double flops = 0.0, bytes = 0.0, ms = 0.0;
@@ -84,8 +87,37 @@ private:
         Conv c1, c2, down;
         bool has_down = false;
     };
+    // A conv1d / 1x1 layer of the TDNN encoders on the implicit-GEMM kernels
+    // (time is the W axis, H = 1): y = bn(relu(conv(x) + b)) with the eval
+    // BatchNorm as a per-channel affine after the activation.
+    struct Layer {
+        int ic = 0, oc = 0, k = 1;
+        void* w = nullptr;          // f16 [OC][K][IC]
+        float* b = nullptr;         // f32 [OC]
+        float* scale = nullptr;     // BatchNorm after ReLU (nullptr = none)
+        float* shift = nullptr;
+    };
+    struct EcapaBlock {
+        Layer tdnn1, tdnn2;
+        std::vector<Layer> res;     // scale - 1 dilated k=3 group convs
+        float* se1_w = nullptr;     // f32 [se][C]
+        float* se1_b = nullptr;
+        float* se2_w = nullptr;     // f32 [C][se]
+        float* se2_b = nullptr;
+        int se_ch = 0, dil = 1;
+    };
+    struct Ecapa {
+        int n_mels = 0, c_pad0 = 0, C = 0, scale = 0, group = 0, mfa = 0, att = 0;
+        Layer block0, mfa_l, asp_x, asp_conv;
+        std::vector<EcapaBlock> blocks;
+        float* asp_stats_w = nullptr;   // f32 [att][2*mfa]: the global-context columns of asp.tdnn
+        float* asp_b = nullptr;
+        float* fc_w = nullptr;          // fc with asp_bn folded in, f32 [E][2*mfa]
+        float* fc_b = nullptr;
+    };
     struct Workspace {
         int batch = 0, n_samples = 0;
+        std::vector<void*> allocs;      // every allocation below, freed together
         size_t act_bytes = 0;
         float* pcm = nullptr;
         float* feats = nullptr;
@@ -95,15 +127,33 @@ private:
         float* emb = nullptr;
         void* fc_work = nullptr;
         size_t fc_work_bytes = 0;
+        // ECAPA: time-major f16 activations and f32 per-clip vectors
+        void *x0p = nullptr, *h0 = nullptr, *t1 = nullptr, *t2 = nullptr, *padb = nullptr, *cat = nullptr,
+             *mfa = nullptr, *a1 = nullptr;
+        float *logits = nullptr, *se_m = nullptr, *se_h = nullptr, *se_g = nullptr, *stats = nullptr,
+              *pb = nullptr;
     };
 
     void ensure_device();
     void upload_resnet();
+    void upload_ecapa();
     void ensure_workspace(int batch, int n_samples);
+    void alloc_resnet_workspace(int batch, int T);
+    void alloc_ecapa_workspace(int batch, int T);
+    void* ws_alloc(size_t bytes);
     void free_workspace();
     // The whole forward for device PCM into device embeddings (pre-norm copy in ws_.pre).
     void forward(const float* d_pcm, int batch, int n_samples, float* d_out);
+    // Encoder from ws_.feats to ws_.pooled (raw pooling statistics) and ws_.pre.
+    void encode_resnet(int batch, int T);
+    void encode_ecapa(int batch, int T);
     void conv(const Conv& c, const void* x, int batch, int H, int W, const void* res, int relu, void* y);
+    // Time-major TDNN layer: x [B][W][x_stride] (W = T + 2*pad of a pre-padded
+    // input) -> y [B][W - (k-1)*dil][y_stride].
+    void tdnn(const char* name, const Layer& l, const void* x, int x_stride, int batch, int W, int dil,
+              const float* bias, int bias_bs, int relu, int tanh_after, void* y, int y_stride, int y_f32);
+    void linear(const char* name, const float* x, int batch, int in_dim, const float* w, const float* b,
+                const float* mv, int out_dim, int relu, float* y);
     void prof_begin(const char* name, double flops, double bytes);
     void prof_end();
     int frames(int n_samples) const;
@@ -121,6 +171,7 @@ private:
     float* stem_b_ = nullptr;
     int stem_oc_ = 0;
     std::vector<Block> blocks_;
+    Ecapa ecapa_;
     float* seg_w_ = nullptr;
     float* seg_b_ = nullptr;
     float* mean_vec_ = nullptr;

@@ -249,6 +249,17 @@ class Context:
             raise VdkError(self.last_error())
         return d.value, bool(v.value)
 
+    def verify_pcm(self, a, b, threshold, sample_rate=16000):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        d = C.c_float(-1.0)
+        v = C.c_int(-1)
+        rc = self.L.voicedetect_capi_verify_pcm(self.ctx, a.ctypes.data, a.size, b.ctypes.data, b.size, sample_rate,
+                                                threshold, C.byref(d), C.byref(v))
+        if rc != 0:
+            raise VdkError(self.last_error())
+        return d.value, bool(v.value)
+
     def capture(self, pcm, n_mels=80):
         pcm = np.ascontiguousarray(pcm, dtype=np.float32)
         B, n = pcm.shape
