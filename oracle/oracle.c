@@ -13,36 +13,36 @@
 
 /* ------------------------------------------------------------ convolution */
 
-static void out_range(int W, int Wo, int stride, int pad, int kw, int* lo, int* hi) {
-    /* ow such that 0 <= ow*stride - pad + kw <= W-1 */
-    const int a = pad - kw;
+static void out_range(int W, int Wo, int stride, int pad, int off, int* lo, int* hi) {
+    /* ow such that 0 <= ow*stride - pad + off <= W-1 (off = kw*dilation) */
+    const int a = pad - off;
     *lo = a <= 0 ? 0 : (a + stride - 1) / stride;
-    const int b = W - 1 + pad - kw;
+    const int b = W - 1 + pad - off;
     *hi = b < 0 ? -1 : b / stride;
     if (*hi > Wo - 1) *hi = Wo - 1;
 }
 
-void orc_conv2d_f32(const float* x, int IC, int H, int W,
-                    const float* w, int OC, int KH, int KW, int stride, int pad,
-                    const float* bias, const float* residual, int relu, float* y) {
-    const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
+void orc_conv2d_f32_g(const float* x, int IC, int H, int W, const float* w, int OC, int KH, int KW,
+                      int sh, int sw, int ph, int pw, int dh, int dw,
+                      const float* bias, const float* residual, int relu, float* y) {
+    const int Ho = (H + 2 * ph - (KH - 1) * dh - 1) / sh + 1, Wo = (W + 2 * pw - (KW - 1) * dw - 1) / sw + 1;
     float* acc = malloc(sizeof(float) * (Wo > 0 ? Wo : 1));
     for (int oc = 0; oc < OC; ++oc) {
         for (int oh = 0; oh < Ho; ++oh) {
             memset(acc, 0, sizeof(float) * Wo);
             for (int kh = 0; kh < KH; ++kh) {
-                const int ih = oh * stride - pad + kh;
+                const int ih = oh * sh - ph + kh * dh;
                 if (ih < 0 || ih >= H) continue;
                 for (int kw = 0; kw < KW; ++kw) {
                     int lo, hi;
-                    out_range(W, Wo, stride, pad, kw, &lo, &hi);
+                    out_range(W, Wo, sw, pw, kw * dw, &lo, &hi);
                     for (int ic = 0; ic < IC; ++ic) {
                         const float wv = w[(((size_t)oc * IC + ic) * KH + kh) * KW + kw];
-                        const float* xr = x + ((size_t)ic * H + ih) * W - pad + kw;
-                        if (stride == 1) {
+                        const float* xr = x + ((size_t)ic * H + ih) * W - pw + kw * dw;
+                        if (sw == 1) {
                             for (int ow = lo; ow <= hi; ++ow) acc[ow] += wv * xr[ow];
                         } else {
-                            for (int ow = lo; ow <= hi; ++ow) acc[ow] += wv * xr[ow * stride];
+                            for (int ow = lo; ow <= hi; ++ow) acc[ow] += wv * xr[(size_t)ow * sw];
                         }
                     }
                 }
@@ -61,10 +61,16 @@ void orc_conv2d_f32(const float* x, int IC, int H, int W,
     free(acc);
 }
 
-void orc_conv2d_f64(const float* x, int IC, int H, int W,
+void orc_conv2d_f32(const float* x, int IC, int H, int W,
                     const float* w, int OC, int KH, int KW, int stride, int pad,
-                    const float* bias, const float* residual, int relu, double* y) {
-    const int Ho = (H + 2 * pad - KH) / stride + 1, Wo = (W + 2 * pad - KW) / stride + 1;
+                    const float* bias, const float* residual, int relu, float* y) {
+    orc_conv2d_f32_g(x, IC, H, W, w, OC, KH, KW, stride, stride, pad, pad, 1, 1, bias, residual, relu, y);
+}
+
+void orc_conv2d_f64_g(const float* x, int IC, int H, int W, const float* w, int OC, int KH, int KW,
+                      int sh, int sw, int ph, int pw, int dh, int dw,
+                      const float* bias, const float* residual, int relu, double* y) {
+    const int Ho = (H + 2 * ph - (KH - 1) * dh - 1) / sh + 1, Wo = (W + 2 * pw - (KW - 1) * dw - 1) / sw + 1;
     for (int oc = 0; oc < OC; ++oc)
         for (int oh = 0; oh < Ho; ++oh)
             for (int ow = 0; ow < Wo; ++ow) {
@@ -72,7 +78,7 @@ void orc_conv2d_f64(const float* x, int IC, int H, int W,
                 for (int ic = 0; ic < IC; ++ic)
                     for (int kh = 0; kh < KH; ++kh)
                         for (int kw = 0; kw < KW; ++kw) {
-                            const int ih = oh * stride - pad + kh, iw = ow * stride - pad + kw;
+                            const int ih = oh * sh - ph + kh * dh, iw = ow * sw - pw + kw * dw;
                             if (ih < 0 || ih >= H || iw < 0 || iw >= W) continue;
                             s += (double)x[((size_t)ic * H + ih) * W + iw] *
                                  (double)w[(((size_t)oc * IC + ic) * KH + kh) * KW + kw];
@@ -85,7 +91,13 @@ void orc_conv2d_f64(const float* x, int IC, int H, int W,
             }
 }
 
-/* ---------------------------------------------------------- pooling / head */
+void orc_conv2d_f64(const float* x, int IC, int H, int W,
+                    const float* w, int OC, int KH, int KW, int stride, int pad,
+                    const float* bias, const float* residual, int relu, double* y) {
+    orc_conv2d_f64_g(x, IC, H, W, w, OC, KH, KW, stride, stride, pad, pad, 1, 1, bias, residual, relu, y);
+}
+
+/* --------------------------------------------------------- pooling and FC */
 
 void orc_tstp(const float* x, int C, int H, int W, float eps, float* pooled) {
     /* src/encoder_resnet.cpp:140-157: mean over time, unbiased var, sqrt(var+eps) */

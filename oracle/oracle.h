@@ -60,6 +60,16 @@ void orc_conv2d_f32(const float* x, int IC, int H, int W,
                     const float* w, int OC, int KH, int KW, int stride, int pad,
                     const float* bias, const float* residual, int relu, float* y);
 
+/* General form: separate strides / zero pads / dilations per axis
+ * (Ho = (H + 2*ph - (KH-1)*dh - 1)/sh + 1).  The CAM++ FCM strides only the
+ * frequency axis (src/encoder_campplus.cpp:67-76); its 1-D convs are H = 1. */
+void orc_conv2d_f32_g(const float* x, int IC, int H, int W, const float* w, int OC, int KH, int KW,
+                      int sh, int sw, int ph, int pw, int dh, int dw,
+                      const float* bias, const float* residual, int relu, float* y);
+void orc_conv2d_f64_g(const float* x, int IC, int H, int W, const float* w, int OC, int KH, int KW,
+                      int sh, int sw, int ph, int pw, int dh, int dw,
+                      const float* bias, const float* residual, int relu, double* y);
+
 /* Same contract, every product and sum in double (the brute-force pin). */
 void orc_conv2d_f64(const float* x, int IC, int H, int W,
                     const float* w, int OC, int KH, int KW, int stride, int pad,
@@ -153,6 +163,40 @@ void orc_ecapa_asp(const orc_ecapa* net, const float* x, int T, float* pooled);
 /* Full ECAPA forward of one clip from FBank features [n_mels][T]
  * (src/encoder.cpp:299-400). Returns 0. */
 int orc_ecapa_forward(const orc_ecapa* net, const float* feats, int T, float* emb, orc_ecapa_caps* caps);
+
+/* ---------------------------------------------------------------- CAM++ */
+
+/* One conv in manifest order: weight [oc][ic][kh][kw] (1-D convs kh = 1,
+ * 1x1 kh = kw = 1), bias may be NULL. */
+typedef struct { const float* w; const float* b; int oc, ic, kh, kw; } orc_conv;
+
+#define ORC_CAMPP_MAX_CONV 256
+#define ORC_CAMPP_MAX_BN 64
+
+/* 3D-Speaker CAM++ from its flat execution-order manifests
+ * (model_loader.hpp:82-99): conv[] in forward order, bn[] the affine BNs in
+ * forward order, emb_mean/emb_var the final affine-free BN. */
+typedef struct {
+    int n_mels, n_conv, n_bn, l2_normalize;
+    float bn_eps;
+    orc_conv conv[ORC_CAMPP_MAX_CONV];
+    orc_bn bn[ORC_CAMPP_MAX_BN];
+    const float* emb_mean; const float* emb_var;
+} orc_campplus;
+
+typedef struct {
+    float* fcm;        /* [C*H'][T] FCM output, channel c*H' + h */
+    float* tdnn;       /* [128][T'] */
+    float* block[3];   /* transit outputs [C_b][T'] */
+    float* pooled;     /* [2C] mean ; unbiased std */
+    float* pre_norm;   /* [emb] */
+} orc_campplus_caps;
+
+/* Full CAM++ forward of one clip from FBank features [n_mels][T]
+ * (src/encoder_campplus.cpp:148-320).  Returns 0, or 1 when the manifest does
+ * not match the fixed topology. */
+int orc_campplus_forward(const orc_campplus* net, const float* feats, int T, float* emb,
+                         orc_campplus_caps* caps);
 
 #ifdef __cplusplus
 }

@@ -420,3 +420,139 @@ def ecapa_asp(net, x):
     out = np.zeros(2 * x.shape[0], dtype=np.float32)
     L.orc_ecapa_asp(C.byref(net.net), x, x.shape[1], out)
     return out
+
+
+# ---------------------------------------------------------------- CAM++
+
+class Conv(C.Structure):
+    _fields_ = [("w", _fp), ("b", _fp), ("oc", C.c_int), ("ic", C.c_int), ("kh", C.c_int), ("kw", C.c_int)]
+
+
+class Campplus(C.Structure):
+    _fields_ = [("n_mels", C.c_int), ("n_conv", C.c_int), ("n_bn", C.c_int), ("l2_normalize", C.c_int),
+                ("bn_eps", C.c_float), ("conv", Conv * 256), ("bn", BN * 64),
+                ("emb_mean", _fp), ("emb_var", _fp)]
+
+
+class CampplusCaps(C.Structure):
+    _fields_ = [("fcm", _fp), ("tdnn", _fp), ("block", _fp * 3), ("pooled", _fp), ("pre_norm", _fp)]
+
+
+def _campplus_sigs():
+    L = lib()
+    if not hasattr(L, "_campplus_ready"):
+        L.orc_campplus_forward.argtypes = [C.POINTER(Campplus), F32P, C.c_int, F32P, C.POINTER(CampplusCaps)]
+        L.orc_campplus_forward.restype = C.c_int
+        L.orc_conv2d_f32_g.argtypes = [F32P, C.c_int, C.c_int, C.c_int, F32P, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                       _fp, _fp, C.c_int, F32P]
+        L.orc_conv2d_f64_g.argtypes = [F32P, C.c_int, C.c_int, C.c_int, F32P, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                       _fp, _fp, C.c_int, np.ctypeslib.ndpointer(dtype=np.float64,
+                                                                               flags="C_CONTIGUOUS")]
+        L._campplus_ready = True
+    return L
+
+
+def conv2d_g(x, w, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1, bias=None, residual=None, relu=False, f64=False):
+    """Oracle conv with per-axis stride / zero pad / dilation: x [IC,H,W], w [OC,IC,KH,KW]."""
+    L = _campplus_sigs()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    IC, H, W = x.shape
+    OC, _, KH, KW = w.shape
+    Ho = (H + 2 * ph - (KH - 1) * dh - 1) // sh + 1
+    Wo = (W + 2 * pw - (KW - 1) * dw - 1) // sw + 1
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    r = None if residual is None else np.ascontiguousarray(residual, dtype=np.float32)
+    y = np.zeros((OC, Ho, Wo), dtype=np.float64 if f64 else np.float32)
+    fn = L.orc_conv2d_f64_g if f64 else L.orc_conv2d_f32_g
+    fn(x, IC, H, W, w, OC, KH, KW, sh, sw, ph, pw, dh, dw,
+       None if b is None else b.ctypes.data_as(_fp), None if r is None else r.ctypes.data_as(_fp), int(relu), y)
+    return y
+
+
+def _weight4(g, name):
+    """A manifest conv weight as [OC, IC, KH, KW] f32 (1-D convs KH = 1, 2-D matrices 1x1)."""
+    w = np.asarray(g.array(name), dtype=np.float32)
+    if w.ndim == 2:
+        return w.reshape(w.shape[0], w.shape[1], 1, 1)
+    if w.ndim == 3:
+        return w.reshape(w.shape[0], w.shape[1], 1, w.shape[2])
+    return w
+
+
+class OracleCampplus:
+    """orc_campplus built from a parsed CAM++ GGUF (weights dequantised to f32)."""
+
+    def __init__(self, g):
+        self.keep = []
+        kv = g.kv
+        n = Campplus()
+        names_w = kv["voicedetect.campplus.conv_weight"]
+        names_b = kv["voicedetect.campplus.conv_bias"]
+        bns = kv["voicedetect.campplus.bn_prefix"]
+        n.n_mels = int(kv.get("voicedetect.fbank.n_mels", 80))
+        n.n_conv = len(names_w)
+        n.n_bn = len(bns)
+        n.bn_eps = float(kv.get("voicedetect.campplus.bn_eps", 1e-5))
+        n.l2_normalize = int(bool(kv.get("voicedetect.l2_normalize", True)))
+
+        def arr(a):
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            self.keep.append(a)
+            return a.ctypes.data_as(_fp)
+
+        self.weights = []
+        for i, (wn, bn) in enumerate(zip(names_w, names_b)):
+            w = _weight4(g, wn)
+            self.weights.append(w)
+            c = n.conv[i]
+            c.w = arr(w)
+            c.b = arr(g.array(bn)) if bn else None
+            c.oc, c.ic, c.kh, c.kw = w.shape
+        for i, p in enumerate(bns):
+            b = n.bn[i]
+            b.gamma = arr(g.array(p + ".weight"))
+            b.beta = arr(g.array(p + ".bias"))
+            b.mean = arr(g.array(p + ".running_mean"))
+            v = np.asarray(g.array(p + ".running_var"), dtype=np.float32)
+            b.var = arr(v)
+            b.c = v.shape[0]
+        n.emb_mean = arr(g.array(kv["voicedetect.campplus.emb_bn_mean"]))
+        n.emb_var = arr(g.array(kv["voicedetect.campplus.emb_bn_var"]))
+        self.net = n
+        self.emb_dim = n.conv[n.n_conv - 1].oc
+
+    def forward(self, feats, capture=False):
+        L = _campplus_sigs()
+        feats = np.ascontiguousarray(feats, dtype=np.float32)
+        T = feats.shape[1]
+        Tp = (T - 1) // 2 + 1
+        n = self.net
+        emb = np.zeros(self.emb_dim, dtype=np.float32)
+        caps = CampplusCaps()
+        bufs = {}
+        if capture:
+            H = n.n_mels
+            for _ in range(3):
+                H = (H - 1) // 2 + 1
+            bufs["fcm"] = np.zeros((n.conv[11].oc * H, T), dtype=np.float32)
+            caps.fcm = bufs["fcm"].ctypes.data_as(_fp)
+            bufs["tdnn"] = np.zeros((n.conv[12].oc, Tp), dtype=np.float32)
+            caps.tdnn = bufs["tdnn"].ctypes.data_as(_fp)
+            # transit convs: the last conv of each block (index walk over the fixed topology)
+            ci = 13
+            for b, nl in enumerate((12, 24, 16)):
+                ci += 4 * nl
+                bufs[f"block{b}"] = np.zeros((n.conv[ci].oc, Tp), dtype=np.float32)
+                caps.block[b] = bufs[f"block{b}"].ctypes.data_as(_fp)
+                ci += 1
+            c_out = n.conv[ci - 1].oc
+            bufs["pooled"] = np.zeros(2 * c_out, dtype=np.float32)
+            caps.pooled = bufs["pooled"].ctypes.data_as(_fp)
+            bufs["pre_norm"] = np.zeros(self.emb_dim, dtype=np.float32)
+            caps.pre_norm = bufs["pre_norm"].ctypes.data_as(_fp)
+        rc = L.orc_campplus_forward(C.byref(n), feats, T, emb, C.byref(caps))
+        assert rc == 0, "CAM++ manifest does not match the fixed topology"
+        return (emb, bufs) if capture else emb

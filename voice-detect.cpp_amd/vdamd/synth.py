@@ -265,3 +265,124 @@ def write_ecapa(path, seed, **kw):
     kv, tensors = make_ecapa(seed, **kw)
     G.write_gguf(path, kv, tensors)
     return path
+
+
+# ---------------------------------------------------------------- CAM++
+
+def _q8_eligible(kh, kw, ic, oc):
+    """The converter's quantisation rule (scripts/convert_voicedetect_to_gguf.py
+    quant_plan): only 1x1 Conv1d / linear weights, blocked by 32 along IC."""
+    return kh == 1 and kw == 1 and ic % 32 == 0 and ic >= 32 and oc >= 32
+
+
+def _put_conv(T, wname, bname, w, b, wtype, conv1d):
+    """Store a conv weight: q8_0/f16-eligible 1x1 Conv1d weights squeezed to a 2-D
+    [OC, IC] matrix of `wtype`, everything else F32 ([OC,IC,K] for Conv1d,
+    [OC,IC,KH,KW] for Conv2d) with f16-representable values."""
+    oc, ic, kh, kw = w.shape
+    if conv1d and wtype != G.GGML_F32 and _q8_eligible(kh, kw, ic, oc):
+        T.append((wname, wtype, [oc, ic], w.reshape(oc, ic)))
+    elif conv1d:
+        T.append((wname, G.GGML_F32, [oc, ic, kw], _f16_exact(w.reshape(oc, ic, kw))))
+    else:
+        T.append((wname, G.GGML_F32, [oc, ic, kh, kw], _f16_exact(w)))
+    if bname:
+        T.append((bname, G.GGML_F32, [oc], b.astype(np.float32)))
+
+
+def make_campplus(seed, n_mels=80, m_ch=32, init_ch=128, growth=32, bn_ch=128, emb_dim=192,
+                  layers=(12, 24, 16), wtype=G.GGML_Q8_0):
+    """Random-init 3D-Speaker CAM++ in the reference GGUF schema
+    (src/model_loader.hpp:82-99, scripts/convert_voicedetect_to_gguf.py
+    parse_campplus_onnx): flat execution-order conv / BN manifests.
+
+    Convs whose BatchNorm the ONNX export folds (FCM, TDNN, each dense layer's
+    linear1, the last transit) carry opaque `onnx::Conv_*` names and a bias;
+    the others keep semantic names (linear_local without bias, the CAM linear1 /
+    linear2 with bias, transit 1-2 and the dense head without).  Standalone
+    affine BNs: each layer's nonlinear1 and each transit's nonlinear; the head
+    BN is affine-free.  Weight storage follows the converter's kernel==1 rule.
+    """
+    ws = _WeightStream(seed)
+    T = []
+    conv_w, conv_b, bn_prefix = [], [], []
+    nid = [0]
+
+    def onnx_name():
+        nid[0] += 1
+        return f"onnx::Conv_{1000 + 2 * nid[0]}", f"onnx::Conv_{1001 + 2 * nid[0]}"
+
+    def folded(oc, ic, kh, kw, conv1d):
+        wn, bn = onnx_name()
+        w, b = conv_bn_folded(ws, oc, ic, kh, kw)
+        _put_conv(T, wn, bn, w, b, wtype, conv1d)
+        conv_w.append(wn)
+        conv_b.append(bn)
+
+    def plain(name, oc, ic, k, bias):
+        w = (normal(ws.next(), oc * ic * k).reshape(oc, ic, 1, k) * np.sqrt(2.0 / (ic * k))).astype(np.float32)
+        b = (0.01 * normal(ws.next(), oc)).astype(np.float32) if bias else None
+        _put_conv(T, name + ".weight", name + ".bias" if bias else "", w, b, wtype, True)
+        conv_w.append(name + ".weight")
+        conv_b.append(name + ".bias" if bias else "")
+
+    def affine_bn(prefix, c):
+        _bn(ws, prefix, c, T)
+        bn_prefix.append(prefix)
+
+    # FCM: stem, 2 x (stride-2 block with shortcut, stride-1 block), final conv
+    folded(m_ch, 1, 3, 3, False)
+    for stride in (2, 1, 2, 1):
+        folded(m_ch, m_ch, 3, 3, False)
+        folded(m_ch, m_ch, 3, 3, False)
+        if stride != 1:
+            folded(m_ch, m_ch, 1, 1, False)
+    folded(m_ch, m_ch, 3, 3, False)
+    H = n_mels
+    for _ in range(3):
+        H = (H - 1) // 2 + 1
+    fcm_out = m_ch * H
+    # TDNN 320 -> init_ch, k=5 s2 (BN folded)
+    folded(init_ch, fcm_out, 1, 5, True)
+    C = init_ch
+    for b, nl in enumerate(layers, start=1):
+        for l in range(1, nl + 1):
+            p = f"xvector.block{b}.tdnnd{l}"
+            affine_bn(p + ".nonlinear1.batchnorm", C)
+            folded(bn_ch, C, 1, 1, True)                                   # linear1 (+ nonlinear2 BN)
+            plain(p + ".cam_layer.linear_local", growth, bn_ch, 3, False)
+            plain(p + ".cam_layer.linear1", bn_ch // 2, bn_ch, 1, True)
+            plain(p + ".cam_layer.linear2", growth, bn_ch // 2, 1, True)
+            C += growth
+        affine_bn(f"xvector.transit{b}.nonlinear.batchnorm", C)
+        if b < len(layers):
+            plain(f"xvector.transit{b}.linear", C // 2, C, 1, False)
+        else:
+            folded(C // 2, C, 1, 1, True)                                  # transit3 (+ out BN)
+        C //= 2
+    plain("xvector.dense.linear", emb_dim, 2 * C, 1, False)
+    mean = (0.1 * normal(ws.next(), emb_dim)).astype(np.float32)
+    var = (0.5 + uniform(ws.next(), emb_dim)).astype(np.float32)
+    T.append(("xvector.dense.nonlinear.batchnorm.running_mean", G.GGML_F32, [emb_dim], mean))
+    T.append(("xvector.dense.nonlinear.batchnorm.running_var", G.GGML_F32, [emb_dim], var))
+    kv = {
+        "general.architecture": "voicedetect",
+        "general.name": f"synthetic-campplus-seed{seed}",
+        "voicedetect.arch": "campplus",
+        "voicedetect.embedding_dim": emb_dim,
+        "voicedetect.l2_normalize": True,
+        "voicedetect.campplus.conv_weight": conv_w,
+        "voicedetect.campplus.conv_bias": conv_b,
+        "voicedetect.campplus.bn_prefix": bn_prefix,
+        "voicedetect.campplus.emb_bn_mean": "xvector.dense.nonlinear.batchnorm.running_mean",
+        "voicedetect.campplus.emb_bn_var": "xvector.dense.nonlinear.batchnorm.running_var",
+        "voicedetect.campplus.bn_eps": 1e-5,
+    }
+    kv.update(_fbank_kv(n_mels))
+    return kv, T
+
+
+def write_campplus(path, seed, **kw):
+    kv, tensors = make_campplus(seed, **kw)
+    G.write_gguf(path, kv, tensors)
+    return path
