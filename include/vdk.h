@@ -74,27 +74,42 @@ int    vdk_fbank(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_
  * x [B][H][W][IC], w [OC][KH][KW][IC], bias [OC] (may be NULL),
  * residual [B][Ho][Wo][OC] (may be NULL), y [B][Ho][Wo][OC], all f16 except bias.
  * Ho = (H + 2*pad - KH)/stride + 1 (same for W).  Requires IC % 16 == 0 and
- * OC % 32 == 0.  relu: 0 = none, 1 = max(v, 0). */
+ * OC % 8 == 0.  relu: 0 = none, 1 = max(v, 0). */
 int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC,
                     const void* d_w, int OC, int KH, int KW, int stride, int pad,
                     const float* d_bias, const void* d_residual, int relu,
                     void* d_y, void* stream);
 
+/* Activations of the fused epilogues (conv and FC). */
+enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3 };
+
 /* General form.  Pixel strides let a layer read or write a channel slice of a
- * wider NHWC tensor in place (pass the slice's base pointer; stride 0 means
- * dense).  Epilogue, in order: v = acc + bias [+ residual]; relu; v*post_scale
- * + post_shift (a BatchNorm that follows the activation); tanh; store f16 or
- * f32.  bias_batch_stride > 0 selects a per-clip bias vector (clip b reads
- * bias + b*bias_batch_stride).  Padding is zero padding; reflect padding is
- * materialised by the caller.  tile = -1 picks the kernel automatically. */
+ * wider NHWC tensor in place (pass the slice's base pointer; 0 means dense).
+ * Stride, zero pad and dilation are per axis (0 stride / dilation means 1):
+ * Ho = (H + 2*pad_h - (KH-1)*dil_h - 1)/stride_h + 1, likewise Wo.  A 1-D
+ * time conv over a time-major [B][T][C] map is H = 1, W = T, KH = 1.
+ * Epilogue, in order:
+ *   v = acc + bias                 (bias_batch_stride > 0: clip b reads bias + b*stride)
+ *   v *= gate[b][ow / gate_seg][oc]  (gate [B][gate_nseg][OC] f32, may be NULL)
+ *   v += residual
+ *   v = act(v)                     (RELU then min(v, clamp_hi) if clamp_hi > 0; SIGMOID; SILU)
+ *   v = v*post_scale + post_shift  (a BatchNorm after the activation; may be NULL)
+ *   v = tanh(v)                    (tanh_after)
+ * stored f16 (or f32 if y_f32) at pixel (b, oh, ow), or at (b, ow, oh) when
+ * y_time_major (an NHWC [B][H][W][C] map written as [B][W][H*C], no residual).
+ * OC needs only be a multiple of 8: surplus rows of a tile are masked.
+ * tile = -1 picks the kernel automatically. */
 typedef struct {
     const void* x; int batch, H, W, IC, x_stride;
-    const void* w; int OC, KH, KW, stride, pad, dilation;
+    const void* w; int OC, KH, KW;
+    int stride_h, stride_w, pad_h, pad_w, dil_h, dil_w;
     const float* bias; int bias_batch_stride;
+    const float* gate; int gate_seg, gate_nseg;
     const void* residual; int res_stride;
+    int act; float clamp_hi;
     const float* post_scale; const float* post_shift;
-    int relu, tanh_after;
-    void* y; int y_stride, y_f32;
+    int tanh_after;
+    void* y; int y_stride, y_f32, y_time_major;
     int tile;
 } vdk_conv_desc;
 int vdk_conv2d_ex(const vdk_conv_desc* desc, void* stream);
@@ -135,10 +150,11 @@ size_t vdk_linear_workspace_size(int batch, int in_dim, int out_dim);
 int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w,
                const float* d_bias, const float* d_mean_vec, int out_dim,
                float* d_y, void* d_work, size_t work_bytes, void* stream);
-/* Same, with an optional ReLU on the result (relu != 0): the SE bottleneck
- * conv1 + ReLU of src/encoder.cpp:207-219 and the ASP global-context term. */
+/* Same, with an activation on the result (act: VDK_ACT_NONE / RELU /
+ * SIGMOID): the SE bottleneck of src/encoder.cpp:207-219, the ASP
+ * global-context term, the CAM++ context MLP (src/encoder_campplus.cpp:266-267). */
 int vdk_linear_ex(const float* d_x, int batch, int in_dim, const float* d_w,
-                  const float* d_bias, const float* d_mean_vec, int out_dim, int relu,
+                  const float* d_bias, const float* d_mean_vec, int out_dim, int act,
                   float* d_y, void* d_work, size_t work_bytes, void* stream);
 
 /* ---- ECAPA-TDNN helpers (src/encoder.cpp) ----
@@ -173,6 +189,22 @@ int vdk_asp_pool(const float* d_logits, int l_stride, const void* d_x, int x_str
  * Replaces the host L2 of src/encoder_resnet.cpp:177-183 (double accumulation,
  * skipped when the norm is 0).  In place on x [B][dim]. */
 int vdk_l2norm(float* d_x, int batch, int dim, void* stream);
+
+/* ---- CAM++ helpers (src/encoder_campplus.cpp) ---- */
+/* y = act(x * scale[c] + shift[c]) over rows x C channels (the standalone
+ * BatchNorm -> ReLU of each dense layer / transit, src/encoder_campplus.cpp:110-134). */
+int vdk_bn_act(const void* d_x, int x_stride, long rows, int C, const float* d_scale,
+               const float* d_shift, int act, void* d_y, int y_stride, void* stream);
+/* out [B][nseg][C] f32: sums of x [B][T][x_stride] over each seg-frame segment
+ * (nseg = ceil(T / seg)). */
+int vdk_segment_sums(const void* d_x, int x_stride, int batch, int T, int C, int seg, float* d_out,
+                     void* stream);
+/* CAM context mask per (clip, segment) (src/encoder_campplus.cpp:159-182, 260-268):
+ * ctx = sum_all / T + sum_seg / seg; gate = sigmoid(w2 relu(w1 ctx + b1) + b2),
+ * w1 [H1][C], w2 [G][H1] f32; gate [B][nseg][G]. */
+int vdk_cam_context(const float* d_sums, int batch, int T, int C, int seg, const float* d_w1,
+                    const float* d_b1, int H1, const float* d_w2, const float* d_b2, int G,
+                    float* d_gate, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,249 @@
+"""Parity of the CAM++ GPU path (src/encoder_campplus.cpp) against the oracle.
+
+Per layer at the 10 s / batch-32 shape (T = 998 frames, T' = 499): the FCM
+convs with a frequency-only stride, the final FCM conv's time-major store
+feeding the k=5 stride-2 TDNN (input channels permuted from the reference's
+c*H + h), the dilated linear_local with the per-segment context gate stored
+into its slice of the dense state; the BN+ReLU, segment-sum and context-MLP
+kernels against closed forms.  End to end: a random-init CAM++ with q8_0 1x1
+weights behind the C ABI, pooled statistics within 2e-3 relative L2 and
+embeddings at cosine >= 0.9999 vs the oracle on the same dequantised weights.
+"""
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import pyoracle as O
+from gpu_util import announce, close_report, cosine, device_ok
+from vdamd import gguf, lib, synth
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
+
+RTOL = 2e-3
+ATOL_RMS = 2e-3
+B = 32
+N10S = 160000
+T10S = 998
+TP = 499
+CLIPS = (0, 15, 31)
+
+
+def _sync():
+    lib.check(lib.lib().vdk_synchronize())
+
+
+def _assert_close(got, ref, tag):
+    ok, ratio, rel = close_report(got, ref, RTOL, ATOL_RMS)
+    assert ok and rel <= 2e-3, f"{tag}: max tol ratio {ratio:.3f}, rel-L2 {rel:.2e}"
+    return rel
+
+
+def _w(rng, oc, ic, kh, kw):
+    return (rng.standard_normal((oc, ic, kh, kw), dtype=np.float32) * np.sqrt(2.0 / (ic * kh * kw))).astype(
+        np.float16)
+
+
+def conv_ex(x_ptr, batch, H, W, IC, xs, w_khkwic, OC, KH, KW, y_ptr, ys=0, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1,
+            bias=None, residual=None, act=lib.ACT_NONE, gate=None, gate_seg=0, gate_nseg=0, y_time_major=0):
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(w_khkwic, dtype=np.float16))]
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = x_ptr, batch, H, W, IC, xs
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, OC, KH, KW
+    d.stride_h, d.stride_w, d.pad_h, d.pad_w, d.dil_h, d.dil_w = sh, sw, ph, pw, dh, dw
+    if bias is not None:
+        keep.append(lib.DeviceBuffer.from_array(bias.astype(np.float32)))
+        d.bias = keep[-1].ptr
+    if residual is not None:
+        d.residual = residual
+    if gate is not None:
+        keep.append(lib.DeviceBuffer.from_array(gate.astype(np.float32)))
+        d.gate, d.gate_seg, d.gate_nseg = keep[-1].ptr, gate_seg, gate_nseg
+    d.act = act
+    d.y, d.y_stride, d.y_time_major = y_ptr, ys, y_time_major
+    d.tile = -1
+    lib.check(lib.lib().vdk_conv2d_ex(d, None))
+    _sync()
+
+
+def test_fcm_freq_stride_convs():
+    """3x3 stride (2, 1) pad 1 and the 1x1 stride (2, 1) shortcut on [B][80][T][32]."""
+    rng = np.random.default_rng(71)
+    H, T, C = 80, T10S, 32
+    announce(f"campp fcm convs B={B} H={H} T={T}")
+    x = np.maximum(rng.standard_normal((B, H, T, C), dtype=np.float32), 0).astype(np.float16)
+    dx = lib.DeviceBuffer.from_array(x)
+    Ho = 40
+    for K, pad, tag in ((3, 1, "conv1"), (1, 0, "shortcut")):
+        w = _w(rng, C, C, K, K)
+        b = rng.uniform(-0.5, 0.5, C).astype(np.float32)
+        y = lib.DeviceBuffer(B * Ho * T * C * 2)
+        conv_ex(dx.ptr, B, H, T, C, 0, w.transpose(0, 2, 3, 1), C, K, K, y.ptr, sh=2, sw=1, ph=pad, pw=pad,
+                bias=b, act=lib.ACT_RELU if K == 3 else lib.ACT_NONE)
+        got = y.to_array(np.float16, (B, Ho, T, C)).astype(np.float32)
+        for c in CLIPS[:2]:
+            ref = O.conv2d_g(x[c].astype(np.float32).transpose(2, 0, 1), w.astype(np.float32), sh=2, sw=1, ph=pad,
+                             pw=pad, bias=b, relu=K == 3)
+            rel = _assert_close(got[c].transpose(2, 0, 1), ref, f"fcm {tag} clip {c}")
+            announce(f"fcm {tag} clip {c} rel-L2 {rel:.2e}")
+
+
+def test_fcm_out_time_major_and_tdnn():
+    """Final FCM conv stored time-major, then the k=5 stride-2 TDNN whose 320
+    input channels are the reference's c*10 + h, read here at h*32 + c."""
+    rng = np.random.default_rng(72)
+    H, T, C, OCT = 20, T10S, 32, 128
+    announce(f"campp fcm_out + tdnn B={B} T={T}")
+    x = np.maximum(rng.standard_normal((B, H, T, C), dtype=np.float32), 0).astype(np.float16)
+    dx = lib.DeviceBuffer.from_array(x)
+    w = _w(rng, C, C, 3, 3)
+    b = rng.uniform(-0.5, 0.5, C).astype(np.float32)
+    yt = lib.DeviceBuffer(B * T * 10 * C * 2)
+    conv_ex(dx.ptr, B, H, T, C, 0, w.transpose(0, 2, 3, 1), C, 3, 3, yt.ptr, sh=2, ph=1, pw=1, bias=b,
+            act=lib.ACT_RELU, y_time_major=1)
+    got = yt.to_array(np.float16, (B, T, 10, C))
+    fcm = []
+    for c in CLIPS:
+        ref = O.conv2d_g(x[c].astype(np.float32).transpose(2, 0, 1), w.astype(np.float32), sh=2, ph=1, pw=1,
+                         bias=b, relu=True)                                     # [32][10][T]
+        _assert_close(got[c].astype(np.float32).transpose(2, 1, 0), ref, f"fcm_out clip {c}")
+        fcm.append(got[c].astype(np.float32).transpose(2, 1, 0).reshape(C * 10, T))   # channel c*10 + h
+    wt = _w(rng, OCT, C * 10, 1, 5)[:, :, 0, :]                                # reference [OC][c*10+h][k]
+    bt = rng.uniform(-0.5, 0.5, OCT).astype(np.float32)
+    wp = wt.reshape(OCT, C, 10, 5).transpose(0, 3, 2, 1).reshape(OCT, 1, 5, 10 * C)   # [OC][1][k][h*32+c]
+    dense = lib.DeviceBuffer(B * TP * 512 * 2)
+    conv_ex(yt.ptr, B, 1, T, 10 * C, 0, wp, OCT, 1, 5, dense.ptr, ys=512, sw=2, pw=2, bias=bt, act=lib.ACT_RELU)
+    gd = dense.to_array(np.float16, (B, TP, 512))
+    for i, c in enumerate(CLIPS):
+        ref = O.conv2d_g(fcm[i][:, None, :], wt[:, :, None, :].astype(np.float32), sw=2, pw=2, bias=bt,
+                         relu=True)[:, 0, :]
+        rel = _assert_close(gd[c, :, :OCT].astype(np.float32).T, ref, f"tdnn clip {c}")
+        announce(f"tdnn clip {c} rel-L2 {rel:.2e}")
+
+
+@pytest.mark.parametrize("dil", [1, 2])
+def test_linear_local_gated_into_dense_slice(dil):
+    rng = np.random.default_rng(80 + dil)
+    T, BC, G, CMAX, C0, SEG = TP, 128, 32, 512, 160, 100
+    nseg = (T + SEG - 1) // SEG
+    announce(f"campp linear_local dil={dil} B={B} T'={T}")
+    cc = np.maximum(rng.standard_normal((B, T, BC), dtype=np.float32), 0).astype(np.float16)
+    gate = rng.uniform(0, 1, (B, nseg, G)).astype(np.float32)
+    dense = rng.standard_normal((B, T, CMAX), dtype=np.float32).astype(np.float16)
+    dcc, dd = lib.DeviceBuffer.from_array(cc), lib.DeviceBuffer.from_array(dense)
+    w = _w(rng, G, BC, 1, 3)
+    conv_ex(dcc.ptr, B, 1, T, BC, 0, w.transpose(0, 2, 3, 1), G, 1, 3, dd.ptr + C0 * 2, ys=CMAX, pw=dil, dw=dil,
+            gate=gate, gate_seg=SEG, gate_nseg=nseg)
+    out = dd.to_array(np.float16, (B, T, CMAX))
+    keep = np.ones(CMAX, dtype=bool)
+    keep[C0:C0 + G] = False
+    assert np.array_equal(out[:, :, keep].view(np.uint16), dense[:, :, keep].view(np.uint16))
+    seg_of_t = np.arange(T) // SEG
+    for c in CLIPS:
+        y = O.conv2d_g(cc[c].astype(np.float32).T[:, None, :], w.astype(np.float32), pw=dil, dw=dil)[:, 0, :]
+        ref = y * gate[c][seg_of_t].T
+        rel = _assert_close(out[c, :, C0:C0 + G].astype(np.float32).T, ref, f"linear_local dil {dil} clip {c}")
+        announce(f"linear_local dil {dil} clip {c} rel-L2 {rel:.2e}")
+
+
+def test_bn_act_segment_sums_and_context():
+    rng = np.random.default_rng(90)
+    L = lib.lib()
+    T, C, XS, SEG, H1, G = TP, 384, 512, 100, 64, 32
+    announce(f"campp helpers B={B} T'={T}")
+    x = rng.standard_normal((B, T, XS), dtype=np.float32).astype(np.float16)
+    s = rng.uniform(0.5, 1.5, C).astype(np.float32)
+    t = rng.uniform(-0.5, 0.5, C).astype(np.float32)
+    dx, ds, dt = (lib.DeviceBuffer.from_array(a) for a in (x, s, t))
+    dy = lib.DeviceBuffer(B * T * C * 2)
+    lib.check(L.vdk_bn_act(dx.ptr, XS, B * T, C, ds.ptr, dt.ptr, lib.ACT_RELU, dy.ptr, C, None))
+    _sync()
+    got = dy.to_array(np.float16, (B, T, C)).astype(np.float64)
+    want = np.maximum(x[:, :, :C].astype(np.float64) * s + t, 0)
+    assert np.all(np.abs(got - want) <= 2.0 ** -10 * np.abs(want) + 1e-6)
+    # segment sums over a 128-channel map with a partial last segment
+    BC = 128
+    cc = np.maximum(rng.standard_normal((B, T, BC), dtype=np.float32), 0).astype(np.float16)
+    dcc = lib.DeviceBuffer.from_array(cc)
+    nseg = (T + SEG - 1) // SEG
+    dsum = lib.DeviceBuffer(B * nseg * BC * 4)
+    lib.check(L.vdk_segment_sums(dcc.ptr, BC, B, T, BC, SEG, dsum.ptr, None))
+    _sync()
+    sums = dsum.to_array(np.float32, (B, nseg, BC))
+    ref = np.stack([cc[:, i * SEG:(i + 1) * SEG].astype(np.float64).sum(axis=1) for i in range(nseg)], axis=1)
+    assert np.allclose(sums, ref, rtol=1e-6, atol=1e-5)
+    # context MLP: Q-matrix form of the context (mean over T' + segment average / 100)
+    w1 = rng.standard_normal((H1, BC), dtype=np.float32) / 8
+    b1 = rng.standard_normal(H1, dtype=np.float32) / 4
+    w2 = rng.standard_normal((G, H1), dtype=np.float32) / 8
+    b2 = rng.standard_normal(G, dtype=np.float32) / 4
+    dw1, db1, dw2, db2 = (lib.DeviceBuffer.from_array(a) for a in (w1, b1, w2, b2))
+    dg = lib.DeviceBuffer(B * nseg * G * 4)
+    lib.check(L.vdk_cam_context(dsum.ptr, B, T, BC, SEG, dw1.ptr, db1.ptr, H1, dw2.ptr, db2.ptr, G, dg.ptr, None))
+    _sync()
+    gate = dg.to_array(np.float32, (B, nseg, G))
+    xc = cc.astype(np.float64)
+    ctx = xc.mean(axis=1)[:, None, :] + ref / SEG                              # [B][nseg][BC]
+    h = np.maximum(ctx @ w1.T.astype(np.float64) + b1, 0)
+    want = 1.0 / (1.0 + np.exp(-(h @ w2.T.astype(np.float64) + b2)))
+    assert np.allclose(gate, want, rtol=1e-5, atol=1e-6)
+
+
+# ------------------------------------------------------------------ end to end
+
+@pytest.fixture(scope="module")
+def campp():
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "campplus_q8_0.gguf")
+    synth.write_campplus(path, seed=5)
+    g = gguf.GGUFFile(path)
+    assert sum(1 for v in g.tensors.values() if v[0] == gguf.GGML_Q8_0) > 50
+    ctx = lib.Context(path)
+    net = O.OracleCampplus(g)
+    yield path, ctx, net
+    ctx.close()
+
+
+def test_campplus_batch32_matches_oracle(campp):
+    path, ctx, net = campp
+    pcm = synth.clips(5150, B, N10S)
+    announce("e2e campplus B=32 10s capture")
+    cap = ctx.capture(pcm)
+    assert cap["pooled"].shape[1] == 1024
+    for c in CLIPS:
+        feats = O.fbank(pcm[c])
+        assert np.abs(cap["feats"][c] - feats).max() <= 1e-4
+        emb, caps = net.forward(feats, capture=True)
+        rel = np.linalg.norm(cap["pooled"][c] - caps["pooled"]) / np.linalg.norm(caps["pooled"])
+        assert rel <= 2e-3, f"pooled rel-L2 {rel:.2e} clip {c}"
+        assert cosine(cap["pre_norm"][c], caps["pre_norm"]) >= 0.9999
+        cs = cosine(cap["emb"][c], emb)
+        announce(f"campplus clip {c}: cosine {cs:.7f} pooled rel {rel:.2e}")
+        assert cs >= 0.9999
+    one = ctx.embed_batch(pcm[15:16])
+    assert np.array_equal(one[0], cap["emb"][15])
+
+
+@pytest.mark.parametrize("n", [400, 4000, 40000])
+def test_campplus_embed_pcm_lengths(campp, n):
+    path, ctx, net = campp
+    announce(f"e2e campplus B=1 n={n}")
+    pcm = synth.clip(700 + n, n)
+    got = ctx.embed_pcm(pcm)
+    ref = net.forward(O.fbank(pcm))
+    assert got.shape == (192,)
+    assert cosine(got, ref) >= 0.9999
+
+
+def test_campplus_verify_matches_oracle(campp):
+    path, ctx, net = campp
+    announce("e2e campplus verify")
+    a = synth.clip(11, 48000)
+    b = synth.clip(12, 56000)
+    d_gpu, _ = ctx.verify_pcm(a, b, 0.5)
+    ea, eb = net.forward(O.fbank(a)), net.forward(O.fbank(b))
+    d_ref = 1.0 - float(np.dot(ea.astype(np.float64), eb.astype(np.float64)))
+    assert abs(d_gpu - d_ref) <= 2e-3
+    for thr in (d_ref - 5e-3, d_ref + 5e-3):
+        assert ctx.verify_pcm(a, b, thr)[1] == (d_ref <= thr)

@@ -60,14 +60,15 @@ def tdnn_gpu(x_ptr, batch, W, IC, xs, w, dil, bias_dev, y_ptr, ys, bias_bs=0, bn
     keep = [dw]
     d = lib.ConvDesc()
     d.x, d.batch, d.H, d.W, d.IC, d.x_stride = x_ptr, batch, 1, W, icp, xs
-    d.w, d.OC, d.KH, d.KW, d.stride, d.pad, d.dilation = dw.ptr, OC, 1, K, 1, 0, dil
+    d.w, d.OC, d.KH, d.KW = dw.ptr, OC, 1, K
+    d.stride_h, d.stride_w, d.pad_h, d.pad_w, d.dil_h, d.dil_w = 1, 1, 0, 0, 1, dil
     d.bias, d.bias_batch_stride = bias_dev.ptr, bias_bs
     if bn is not None:
         s, t = _scale_shift(bn)
         ds, dt = lib.DeviceBuffer.from_array(s), lib.DeviceBuffer.from_array(t)
         keep += [ds, dt]
         d.post_scale, d.post_shift = ds.ptr, dt.ptr
-    d.relu, d.tanh_after = int(relu), int(tanh)
+    d.act, d.tanh_after = (lib.ACT_RELU if relu else lib.ACT_NONE), int(tanh)
     d.y, d.y_stride, d.y_f32 = y_ptr, ys, int(y_f32)
     d.tile = -1
     lib.check(lib.lib().vdk_conv2d_ex(d, None))

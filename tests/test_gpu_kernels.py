@@ -197,7 +197,8 @@ def test_conv_rejects_bad_shapes():
     d = lib.DeviceBuffer(1 << 16)
     assert L.vdk_conv2d_nhwc(d.ptr, 1, 4, 4, 24, d.ptr, 32, 3, 3, 1, 1, None, None, 0, d.ptr, None) != 0
     assert "IC" in L.vdk_last_error().decode()
-    assert L.vdk_conv2d_nhwc(d.ptr, 1, 4, 4, 32, d.ptr, 48, 3, 3, 1, 1, None, None, 0, d.ptr, None) != 0
+    assert L.vdk_conv2d_nhwc(d.ptr, 1, 4, 4, 32, d.ptr, 20, 3, 3, 1, 1, None, None, 0, d.ptr, None) != 0
+    assert "OC" in L.vdk_last_error().decode()
     assert L.vdk_conv2d_nhwc(None, 1, 4, 4, 32, d.ptr, 32, 3, 3, 1, 1, None, None, 0, d.ptr, None) != 0
     assert L.vdk_conv2d_nhwc(d.ptr, 1, 1, 1, 32, d.ptr, 32, 3, 3, 1, 0, None, None, 0, d.ptr, None) != 0
 

@@ -1,0 +1,150 @@
+// campplus.hip - the non-GEMM pieces of the CAM++ D-TDNN backbone on gfx950.
+//
+// The convolutions of src/encoder_campplus.cpp (FCM 2D convs, the strided
+// TDNN, every dense layer's 1x1 / dilated linear_local, the transits) run on
+// the implicit-GEMM kernels over time-major [B][T'][C] maps.  What remains:
+//  * bn_act: the standalone BatchNorm -> ReLU in front of each dense layer's
+//    linear1 and each transit (src/encoder_campplus.cpp:110-134, 254-255, 286);
+//  * segment_sums + cam_context: the context-aware mask.  The context
+//    c.mean(T') + seg100(c) is constant over a 100-frame segment, so the mask
+//    m = sigmoid(W2 relu(W1 ctx + b1) + b2) is computed once per (clip,
+//    segment) (src/encoder_campplus.cpp:159-182, 260-268) and applied in the
+//    linear_local conv epilogue as a per-segment gate.
+// Sums are accumulated in f64.
+#include <cmath>
+
+#include "common.hpp"
+#include "vdk.h"
+
+namespace vdk {
+namespace {
+
+__global__ __launch_bounds__(256) void bn_act_kernel(const half_t* __restrict__ x, int xs, long rows, int C,
+                                                     const float* __restrict__ scale,
+                                                     const float* __restrict__ shift, int act,
+                                                     half_t* __restrict__ y, int ys) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;   // one 8-channel chunk
+    const int C8 = C / 8;
+    if (i >= rows * C8) return;
+    const int c = (int)(i % C8) * 8;
+    const long r = i / C8;
+    const half8 v = *reinterpret_cast<const half8*>(x + r * xs + c);
+    half8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        float f = (float)v[e] * scale[c + e] + shift[c + e];
+        if (act == VDK_ACT_RELU) f = f > 0.0f ? f : 0.0f;
+        o[e] = (half_t)f;
+    }
+    *reinterpret_cast<half8*>(y + r * ys + c) = o;
+}
+
+// Workgroup (b, s, 64-channel group): 4 lanes of 64 channels split the frames
+// of segment s; the 4 partial sums are added in a fixed order.
+__global__ __launch_bounds__(256) void segment_sums_kernel(const half_t* __restrict__ x, int xs, int T, int C,
+                                                           int seg, float* __restrict__ out) {
+    __shared__ double part[4][64];
+    const int b = blockIdx.x, s = blockIdx.y, c0 = blockIdx.z * 64;
+    const int nseg = gridDim.y;
+    const int lane_c = threadIdx.x & 63, lane_t = threadIdx.x >> 6;
+    const int c = c0 + lane_c;
+    const int t0 = s * seg, t1 = min(T, t0 + seg);
+    double acc = 0.0;
+    if (c < C) {
+        const half_t* p = x + (size_t)b * T * xs + c;
+        for (int t = t0 + lane_t; t < t1; t += 4) acc += (double)(float)p[(size_t)t * xs];
+    }
+    part[lane_t][lane_c] = acc;
+    __syncthreads();
+    if (lane_t == 0 && c < C) {
+        const double v = ((part[0][lane_c] + part[1][lane_c]) + part[2][lane_c]) + part[3][lane_c];
+        out[((size_t)b * nseg + s) * C + c] = (float)v;
+    }
+}
+
+// One workgroup per (clip, segment): ctx = mean_T' + sum_seg / seg_len, then
+// h = relu(W1 ctx + b1), gate = sigmoid(W2 h + b2).
+__global__ __launch_bounds__(256) void cam_context_kernel(const float* __restrict__ sums, int nseg, int T, int C,
+                                                          int seg, const float* __restrict__ w1,
+                                                          const float* __restrict__ b1, int H1,
+                                                          const float* __restrict__ w2,
+                                                          const float* __restrict__ b2, int G,
+                                                          float* __restrict__ gate) {
+    extern __shared__ float sm[];
+    float* ctx = sm;          // [C]
+    float* hid = sm + C;      // [H1]
+    const int b = blockIdx.x, s = blockIdx.y;
+    const float* sb = sums + (size_t)b * nseg * C;
+    for (int c = threadIdx.x; c < C; c += blockDim.x) {
+        double tot = 0.0;
+        for (int q = 0; q < nseg; ++q) tot += (double)sb[(size_t)q * C + c];
+        ctx[c] = (float)(tot / T) + (float)((double)sb[(size_t)s * C + c] / seg);
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < H1; o += blockDim.x) {
+        const float* wr = w1 + (size_t)o * C;
+        double a = 0.0;
+        for (int c = 0; c < C; ++c) a += (double)wr[c] * (double)ctx[c];
+        float v = (float)a + (b1 ? b1[o] : 0.0f);
+        hid[o] = v > 0.0f ? v : 0.0f;
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < G; o += blockDim.x) {
+        const float* wr = w2 + (size_t)o * H1;
+        double a = 0.0;
+        for (int c = 0; c < H1; ++c) a += (double)wr[c] * (double)hid[c];
+        const float v = (float)a + (b2 ? b2[o] : 0.0f);
+        gate[((size_t)b * nseg + s) * G + o] = 1.0f / (1.0f + expf(-v));
+    }
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace vdk
+
+using namespace vdk;
+
+extern "C" int vdk_bn_act(const void* d_x, int x_stride, long rows, int C, const float* d_scale,
+                          const float* d_shift, int act, void* d_y, int y_stride, void* stream) {
+    return guarded([&] {
+        require(d_x && d_scale && d_shift && d_y, "bn_act: NULL device pointer");
+        require(rows > 0 && C > 0 && C % 8 == 0 && x_stride >= C && y_stride >= C && x_stride % 8 == 0 &&
+                    y_stride % 8 == 0, "bn_act: bad shape");
+        require(act == VDK_ACT_NONE || act == VDK_ACT_RELU, "bn_act: unknown activation");
+        require(al16(d_x) && al16(d_y), "bn_act: pointers must be 16-byte aligned");
+        const long n = rows * (C / 8);
+        hipLaunchKernelGGL(bn_act_kernel, dim3(cdiv(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<const half_t*>(d_x), x_stride, rows, C, d_scale, d_shift, act,
+                           static_cast<half_t*>(d_y), y_stride);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_segment_sums(const void* d_x, int x_stride, int batch, int T, int C, int seg, float* d_out,
+                                void* stream) {
+    return guarded([&] {
+        require(d_x && d_out, "segment_sums: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0 && seg > 0 && x_stride >= C, "segment_sums: bad shape");
+        const int nseg = (T + seg - 1) / seg;
+        hipLaunchKernelGGL(segment_sums_kernel, dim3(batch, nseg, cdiv(C, 64)), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, seg,
+                           d_out);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_cam_context(const float* d_sums, int batch, int T, int C, int seg, const float* d_w1,
+                               const float* d_b1, int H1, const float* d_w2, const float* d_b2, int G,
+                               float* d_gate, void* stream) {
+    return guarded([&] {
+        require(d_sums && d_w1 && d_w2 && d_gate, "cam_context: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0 && seg > 0 && H1 > 0 && G > 0 && C + H1 <= 16384,
+                "cam_context: bad shape");
+        const int nseg = (T + seg - 1) / seg;
+        hipLaunchKernelGGL(cam_context_kernel, dim3(batch, nseg), dim3(256), sizeof(float) * (C + H1),
+                           static_cast<hipStream_t>(stream), d_sums, nseg, T, C, seg, d_w1, d_b1, H1, d_w2, d_b2,
+                           G, d_gate);
+        VDK_HIP(hipGetLastError());
+    });
+}

@@ -32,30 +32,54 @@ struct ConvArgs {
     void* y;
     const float* post_scale;   // per-OC affine applied after the activation (may be NULL)
     const float* post_shift;
-    int H, W, IC, Ho, Wo, OC, KH, KW, stride, pad, dil, relu, tanh_after, y_f32;
+    const float* gate;         // per-(clip, time segment, OC) multiplier (may be NULL)
+    int H, W, IC, Ho, Wo, OC, KH, KW;
+    int sh, sw, ph, pw, dh, dw;  // stride / zero pad / dilation per axis
+    int act, tanh_after, y_f32, y_tr;   // act: VDK_ACT_NONE / RELU / SIGMOID / SILU
+    float clamp_hi;            // > 0: min(v, clamp_hi) after the ReLU
+    int gate_seg, gate_nseg;   // output columns per gate segment, segments per clip
     int xs, ys, rs;            // elements between consecutive pixels of x / y / residual
     int bias_bs;               // elements between clips' bias vectors (0: one shared vector)
     int npix;                  // B * Ho * Wo
     int npix_in;               // B * H * W
-    int plain;                 // xs == IC, dil == 1: layouts every kernel family accepts
 };
 
-// Shared epilogue for 4 consecutive output channels of pixel P:
-// v = acc + bias [+ residual]; [relu]; [* post_scale + post_shift]; [tanh].
+// Shared epilogue for 4 consecutive output channels of pixel P (P enumerates
+// (clip, oh, ow) row-major): v = acc + bias; [* gate]; [+ residual];
+// [relu [min(v, clamp_hi)] | sigmoid | silu]; [* post_scale + post_shift];
+// [tanh]; store f16 / f32 at
+// pixel P, or at (clip, ow, oh) when y_tr (time-major output of an NHWC map).
 __device__ __forceinline__ void epilogue4(const ConvArgs& a, int P, int oc, const float* acc) {
     float v[4];
     const float* bias = a.bias;
-    if (bias && a.bias_bs) bias += (size_t)(P / (a.Ho * a.Wo)) * a.bias_bs;
+    const int HoWo = a.Ho * a.Wo;
+    if (bias && a.bias_bs) bias += (size_t)(P / HoWo) * a.bias_bs;
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = acc[e] + (bias ? bias[oc + e] : 0.0f);
+    if (a.gate) {
+        const int b = P / HoWo, ow = (P - b * HoWo) % a.Wo;
+        const float* g = a.gate + ((size_t)b * a.gate_nseg + ow / a.gate_seg) * a.OC + oc;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] *= g[e];
+    }
     if (a.res) {
         const half4 r = *reinterpret_cast<const half4*>(a.res + (size_t)P * a.rs + oc);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
     }
-    if (a.relu) {
+    if (a.act == VDK_ACT_RELU) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
+        if (a.clamp_hi > 0.0f) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = v[e] < a.clamp_hi ? v[e] : a.clamp_hi;
+        }
+    } else if (a.act == VDK_ACT_SIGMOID) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = 1.0f / (1.0f + expf(-v[e]));
+    } else if (a.act == VDK_ACT_SILU) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] / (1.0f + expf(-v[e]));
     }
     if (a.post_scale) {
 #pragma unroll
@@ -65,7 +89,12 @@ __device__ __forceinline__ void epilogue4(const ConvArgs& a, int P, int oc, cons
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = tanhf(v[e]);
     }
-    const size_t o = (size_t)P * a.ys + oc;
+    size_t Po = (size_t)P;
+    if (a.y_tr) {
+        const int b = P / HoWo, rem = P - b * HoWo, oh = rem / a.Wo, ow = rem - oh * a.Wo;
+        Po = ((size_t)b * a.Wo + ow) * a.Ho + oh;
+    }
+    const size_t o = Po * a.ys + oc;
     if (a.y_f32) {
         float4v f = {v[0], v[1], v[2], v[3]};
         *reinterpret_cast<float4v*>(static_cast<float*>(a.y) + o) = f;
@@ -121,20 +150,21 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         const int b = Pc / HoWo, rem = Pc - b * HoWo;
         const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
         x_img[i] = b * a.H;
-        x_ih[i] = oh * a.stride - a.pad;
-        x_iw[i] = ow * a.stride - a.pad;
+        x_ih[i] = oh * a.sh - a.ph;
+        x_iw[i] = ow * a.sw - a.pw;
         x_lds[i] = r * LDK + c8 * 8;
         x_c[i] = c8 * 8;
     }
     const half_t* w_src[WCH];
     int w_lds[WCH];
-    bool w_on[WCH];
+    bool w_on[WCH], w_ok[WCH];   // slot is part of the tile / its weight row exists (oc < OC)
 #pragma unroll
     for (int i = 0; i < WCH; ++i) {
         const int q = tid + i * NT;
         const int r = q / CPR, c8 = q - r * CPR;
         w_on[i] = q < BM * CPR;
-        w_src[i] = a.w + (size_t)(oc0 + (w_on[i] ? r : 0)) * KHW * a.IC + c8 * 8;
+        w_ok[i] = w_on[i] && oc0 + r < a.OC;
+        w_src[i] = a.w + (size_t)(oc0 + (w_ok[i] ? r : 0)) * KHW * a.IC + c8 * 8;
         w_lds[i] = r * LDK + c8 * 8;
     }
 
@@ -145,13 +175,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         const int kh = tap / a.KW, kw = tap - kh * a.KW;
 #pragma unroll
         for (int i = 0; i < WCH; ++i)
-            if (w_on[i]) wr[i] = *reinterpret_cast<const half8*>(w_src[i] + (size_t)tap * a.IC + c0);
+            wr[i] = w_ok[i] ? *reinterpret_cast<const half8*>(w_src[i] + (size_t)tap * a.IC + c0) : zero8;
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
-            const int ih = x_ih[i] + kh, iw = x_iw[i] + kw;
+            const int ih = x_ih[i] + kh * a.dh, iw = x_iw[i] + kw * a.dw;
             xr[i] = zero8;
             if (x_on[i] && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
-                xr[i] = *reinterpret_cast<const half8*>(a.x + ((size_t)(x_img[i] + ih) * a.W + iw) * a.IC + c0 +
+                xr[i] = *reinterpret_cast<const half8*>(a.x + ((size_t)(x_img[i] + ih) * a.W + iw) * a.xs + c0 +
                                                         x_c[i]);
         }
     };
@@ -209,6 +239,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int oc = oc0 + wm * WM + i * 32 + g * 8 + (lane >> 5) * 4;
+                if (oc >= a.OC) continue;
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e];
@@ -318,11 +349,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
             if (P < a.npix) {
                 const int b = P / HoWo, rem = P - b * HoWo;
                 const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
-                const int ih0 = oh * a.stride - a.pad, iw0 = ow * a.stride - a.pad;
+                const int ih0 = oh * a.sh - a.ph, iw0 = ow * a.sw - a.pw;
                 s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.xs + c * 8) * 2;
                 for (int kh = 0; kh < a.KH; ++kh)
                     for (int kw = 0; kw < a.KW; ++kw) {
-                        const int ih = ih0 + kh * a.dil, iw = iw0 + kw * a.dil;
+                        const int ih = ih0 + kh * a.dh, iw = iw0 + kw * a.dw;
                         if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W) s_mask[j] |= 1u << (kh * a.KW + kw);
                     }
             }
@@ -332,8 +363,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     // Chunk cursor for the DMA side: tap (kh, kw) and channel offset c0,
     // advanced incrementally (no divisions in the loop).
     int f_tap = 0, f_kw = 0, f_c0 = 0, f_x = 0;   // f_x = byte offset of (kh, kw, c0) in the input
-    const int tap_bytes = a.dil * a.xs * 2;                       // next kw
-    const int row_bytes = a.dil * a.W * a.xs * 2 - a.KW * tap_bytes;   // next kh, back to kw = 0
+    const int tap_bytes = a.dw * a.xs * 2;                       // next kw
+    const int row_bytes = a.dh * a.W * a.xs * 2 - a.KW * tap_bytes;   // next kh, back to kw = 0
     auto issue = [&](int st) {
         const int w_soff = (f_tap * a.IC + f_c0) * 2;
 #pragma unroll
@@ -418,6 +449,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int oc = oc0 + wm * WM + i * 32 + g * 8 + lhalf * 4;
+                if (oc >= a.OC) continue;
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e];
@@ -430,7 +462,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
 template <int BM, int BN, int WM, int WN, int KC, int NST>
 void launch_dma(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
-    dim3 grid(cdiv(a.npix, BN), a.OC / BM);
+    dim3 grid(cdiv(a.npix, BN), cdiv(a.OC, BM));
     hipLaunchKernelGGL((conv_dma_kernel<BM, BN, WM, WN, KC, NST>), grid, dim3(NT), 0, s, a);
 }
 
@@ -540,6 +572,7 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int oc = oc0 + mb * 32 + g * 8 + lhalf * 4;
+            if (oc >= a.OC) continue;
             float v[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = acc[q][g * 4 + e];
@@ -552,13 +585,13 @@ template <int OCB, int KC, int TH, int TW>
 void launch_halo(const ConvArgs& a, hipStream_t s) {
     const int B = a.npix / (a.Ho * a.Wo);
     const int tiles = B * ((a.Ho + TH - 1) / TH) * ((a.Wo + TW - 1) / TW);
-    hipLaunchKernelGGL((conv3x3_halo_kernel<OCB, KC, TH, TW>), dim3(tiles, a.OC / OCB), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((conv3x3_halo_kernel<OCB, KC, TH, TW>), dim3(tiles, cdiv(a.OC, OCB)), dim3(256), 0, s, a);
 }
 
 template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
-    dim3 grid(cdiv(a.npix, BN), a.OC / BM);
+    dim3 grid(cdiv(a.npix, BN), cdiv(a.OC, BM));
     hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC>), grid, dim3(NT), 0, s, a);
 }
 
@@ -568,9 +601,8 @@ struct TileCfg {
     bool halo;   // 3x3 stride-1 pad-1 dilation-1 only
 };
 
-// Entries 0-13 are the register-staged kernel (plain layouts only), 14-25 the
-// LDS-DMA kernel (any strides / dilation), 26+ the halo kernel.
-constexpr int kFirstDma = 14;
+// Entries 0-13 are the register-staged kernel (any layout; the only one with
+// KC=16 for IC % 32 != 0), 14-25 the LDS-DMA kernel, 26+ the halo kernel.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -611,11 +643,13 @@ const TileCfg kTiles[] = {
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
+bool is_s1_3x3(const ConvArgs& a) {
+    return a.KH == 3 && a.KW == 3 && a.sh == 1 && a.sw == 1 && a.ph == 1 && a.pw == 1 && a.dh == 1 && a.dw == 1;
+}
+
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
-    if (t.halo && !(a.KH == 3 && a.KW == 3 && a.stride == 1 && a.pad == 1 && a.dil == 1)) return false;
-    const bool dma = !t.halo && (&t - kTiles) >= kFirstDma;
-    if (!dma && !t.halo && !a.plain) return false;
-    return a.OC % t.bm == 0 && a.IC % t.kc == 0;
+    if (t.halo && !is_s1_3x3(a)) return false;
+    return a.IC % t.kc == 0;
 }
 
 // Optional override for tuning sweeps: VDK_CONV_TILE=<index into kTiles>.
@@ -629,25 +663,18 @@ int tile_override() {
 
 // Per-layer-class defaults, from a sweep of every ResNet34 conv shape at
 // batch 64 on MI355X (narrow 3x3 stride-1 layers: halo tiles; the rest:
-// DMA implicit GEMM with a 128-wide OC tile where the layer allows it).
+// DMA implicit GEMM with the widest OC tile that divides OC; IC % 32 != 0:
+// the register-staged kernel with KC = 16).  OC that no tile divides runs on
+// 32-wide tiles with the surplus rows masked.
 int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
-    const bool s1_3x3 = a.KH == 3 && a.KW == 3 && a.stride == 1 && a.pad == 1 && a.dil == 1;
-    if (s1_3x3 && a.OC == 32 && a.IC % 32 == 0 && a.IC <= 64) return 28;
-    if (s1_3x3 && a.OC == 64 && a.IC % 32 == 0 && a.IC <= 64) return 30;
-    if (a.IC % 64 == 0) {
-        if (a.OC % 128 == 0) return 18;
-        if (a.OC % 64 == 0) return 15;
-    } else if (a.IC % 32 == 0) {
-        if (a.OC % 64 == 0) return 16;
-        if (a.OC % 32 == 0) return 14;
-    }
-    if (a.IC % 32 != 0 && !a.plain) return -1;   // needs KC=16, which only the plain-layout kernel has
-    if (a.IC % 32 != 0) return a.OC % 128 == 0 ? 13 : (a.OC % 64 == 0 ? 12 : 11);
-    if (a.OC % 128 == 0) return 5;
-    if (a.OC % 64 == 0) return 2;
-    return 10;
+    const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
+    if (is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return a.OC <= 32 ? 28 : 30;
+    if (a.IC % 64 == 0) return bm == 128 ? 18 : (bm == 64 ? 15 : 14);
+    if (a.IC % 32 == 0) return bm >= 64 ? 16 : 14;
+    if (a.IC % 16 == 0) return bm == 128 ? 13 : (bm == 64 ? 12 : 11);
+    return -1;
 }
 
 template <int OC>
@@ -705,22 +732,29 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(d.x && d.w && d.y, "conv2d: NULL device pointer");
         require(d.batch > 0 && d.H > 0 && d.W > 0, "conv2d: empty input");
         require(d.IC > 0 && d.IC % 16 == 0, "conv2d: IC must be a positive multiple of 16");
-        require(d.OC > 0 && d.OC % 32 == 0, "conv2d: OC must be a positive multiple of 32");
+        require(d.OC > 0 && d.OC % 8 == 0, "conv2d: OC must be a positive multiple of 8");
         require(d.KH >= 1 && d.KW >= 1 && d.KH <= 7 && d.KW <= 7, "conv2d: kernel size out of range");
-        require(d.stride >= 1 && d.pad >= 0 && d.dilation >= 1, "conv2d: invalid stride/pad/dilation");
-        const int ekh = (d.KH - 1) * d.dilation + 1, ekw = (d.KW - 1) * d.dilation + 1;
-        require(d.H + 2 * d.pad >= ekh && d.W + 2 * d.pad >= ekw, "conv2d: output would be empty");
-        const int Ho = (d.H + 2 * d.pad - ekh) / d.stride + 1, Wo = (d.W + 2 * d.pad - ekw) / d.stride + 1;
+        const int sh = d.stride_h ? d.stride_h : 1, sw = d.stride_w ? d.stride_w : 1;
+        const int dh = d.dil_h ? d.dil_h : 1, dw = d.dil_w ? d.dil_w : 1;
+        require(sh >= 1 && sw >= 1 && dh >= 1 && dw >= 1 && d.pad_h >= 0 && d.pad_w >= 0,
+                "conv2d: invalid stride/pad/dilation");
+        const int ekh = (d.KH - 1) * dh + 1, ekw = (d.KW - 1) * dw + 1;
+        require(d.H + 2 * d.pad_h >= ekh && d.W + 2 * d.pad_w >= ekw, "conv2d: output would be empty");
+        const int Ho = (d.H + 2 * d.pad_h - ekh) / sh + 1, Wo = (d.W + 2 * d.pad_w - ekw) / sw + 1;
         const int xs = d.x_stride ? d.x_stride : d.IC, ys = d.y_stride ? d.y_stride : d.OC;
         const int rs = d.res_stride ? d.res_stride : d.OC;
         require(xs >= d.IC && ys >= d.OC && rs >= d.OC, "conv2d: pixel stride smaller than the channel count");
         require(xs % 8 == 0 && ys % 8 == 0 && rs % 8 == 0, "conv2d: pixel strides must be multiples of 8");
-        require((long)d.batch * Ho * Wo < (1L << 31) && (long)d.batch * d.H * d.W * xs < (1L << 30),
+        require((long)d.batch * Ho * Wo < (1L << 31) && (long)d.batch * d.H * d.W * xs < (1L << 30) &&
+                    (long)d.batch * Ho * Wo * ys < (1L << 31),
                 "conv2d: too many pixels for one launch");
         require(aligned16(d.x) && aligned16(d.w) && aligned16(d.y) && (!d.residual || aligned16(d.residual)),
                 "conv2d: device pointers must be 16-byte aligned");
         require(!d.post_scale == !d.post_shift, "conv2d: post_scale and post_shift go together");
-        ConvArgs a;
+        require(!d.gate || (d.gate_seg > 0 && d.gate_nseg > 0 && (Wo + d.gate_seg - 1) / d.gate_seg <= d.gate_nseg),
+                "conv2d: gate needs gate_seg > 0 and enough segments for the output width");
+        require(!d.y_time_major || !d.residual, "conv2d: a time-major store takes no residual");
+        ConvArgs a{};
         a.x = static_cast<const half_t*>(d.x);
         a.w = static_cast<const half_t*>(d.w);
         a.bias = d.bias;
@@ -728,21 +762,27 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         a.y = d.y;
         a.post_scale = d.post_scale;
         a.post_shift = d.post_shift;
+        a.gate = d.gate;
+        a.gate_seg = d.gate ? d.gate_seg : 1;
+        a.gate_nseg = d.gate ? d.gate_nseg : 1;
         a.H = d.H; a.W = d.W; a.IC = d.IC; a.Ho = Ho; a.Wo = Wo; a.OC = d.OC;
-        a.KH = d.KH; a.KW = d.KW; a.stride = d.stride; a.pad = d.pad; a.dil = d.dilation;
-        a.relu = d.relu ? 1 : 0;
+        a.KH = d.KH; a.KW = d.KW;
+        a.sh = sh; a.sw = sw; a.ph = d.pad_h; a.pw = d.pad_w; a.dh = dh; a.dw = dw;
+        require(d.act >= VDK_ACT_NONE && d.act <= VDK_ACT_SILU, "conv2d: unknown activation");
+        a.act = d.act;
+        a.clamp_hi = d.act == VDK_ACT_RELU ? d.clamp_hi : 0.0f;
         a.tanh_after = d.tanh_after ? 1 : 0;
         a.y_f32 = d.y_f32 ? 1 : 0;
+        a.y_tr = d.y_time_major ? 1 : 0;
         a.xs = xs; a.ys = ys; a.rs = rs;
         a.bias_bs = d.bias_batch_stride;
         a.npix = d.batch * Ho * Wo;
         a.npix_in = d.batch * d.H * d.W;
-        a.plain = (xs == d.IC && d.dilation == 1) ? 1 : 0;
         hipStream_t s = static_cast<hipStream_t>(stream);
         int t = d.tile;
         if (t < 0) {
             t = pick_tile(a);
-            require(t >= 0, "conv2d: no kernel for IC % 32 != 0 with strided input or dilation");
+            require(t >= 0, "conv2d: no kernel for this channel count");
         } else {
             require(t < kNumTiles, "conv2d: tile index out of range");
         }
@@ -757,9 +797,21 @@ vdk_conv_desc plain_desc(const void* d_x, int batch, int H, int W, int IC, const
                          int tile) {
     vdk_conv_desc d{};
     d.x = d_x; d.batch = batch; d.H = H; d.W = W; d.IC = IC;
-    d.w = d_w; d.OC = OC; d.KH = KH; d.KW = KW; d.stride = stride; d.pad = pad; d.dilation = 1;
-    d.bias = d_bias; d.residual = d_residual; d.relu = relu; d.y = d_y; d.tile = tile;
+    d.w = d_w; d.OC = OC; d.KH = KH; d.KW = KW;
+    d.stride_h = d.stride_w = stride;
+    d.pad_h = d.pad_w = pad;
+    d.dil_h = d.dil_w = 1;
+    d.bias = d_bias; d.residual = d_residual; d.act = relu ? VDK_ACT_RELU : VDK_ACT_NONE; d.y = d_y; d.tile = tile;
     return d;
+}
+
+ConvArgs shape_args(const vdk_conv_desc& d) {
+    ConvArgs a{};
+    a.IC = d.IC; a.OC = d.OC; a.KH = d.KH; a.KW = d.KW;
+    a.sh = d.stride_h ? d.stride_h : 1; a.sw = d.stride_w ? d.stride_w : 1;
+    a.ph = d.pad_h; a.pw = d.pad_w;
+    a.dh = d.dil_h ? d.dil_h : 1; a.dw = d.dil_w ? d.dil_w : 1;
+    return a;
 }
 
 }  // namespace
@@ -790,19 +842,14 @@ extern "C" int vdk_conv2d_tile_count(void) { return kNumTiles; }
 
 extern "C" int vdk_conv2d_tile_fits(int tile, int IC, int OC, int KH, int KW, int stride, int pad) {
     if (tile < 0 || tile >= kNumTiles) return 0;
-    ConvArgs a{};
-    a.IC = IC; a.OC = OC; a.KH = KH; a.KW = KW; a.stride = stride; a.pad = pad; a.dil = 1; a.plain = 1;
-    return tile_fits(kTiles[tile], a) ? 1 : 0;
+    const vdk_conv_desc d = plain_desc(nullptr, 1, 1, 1, IC, nullptr, OC, KH, KW, stride, pad, nullptr, nullptr, 0,
+                                       nullptr, tile);
+    return tile_fits(kTiles[tile], shape_args(d)) ? 1 : 0;
 }
 
 extern "C" int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* d) {
     if (tile < 0 || tile >= kNumTiles || !d) return 0;
-    ConvArgs a{};
-    a.IC = d->IC; a.OC = d->OC; a.KH = d->KH; a.KW = d->KW; a.stride = d->stride; a.pad = d->pad;
-    a.dil = d->dilation > 0 ? d->dilation : 1;
-    const int xs = d->x_stride ? d->x_stride : d->IC;
-    a.plain = (xs == d->IC && a.dil == 1) ? 1 : 0;
-    return tile_fits(kTiles[tile], a) ? 1 : 0;
+    return tile_fits(kTiles[tile], shape_args(*d)) ? 1 : 0;
 }
 
 extern "C" int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,

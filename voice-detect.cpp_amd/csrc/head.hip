@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void linear_partial_kernel(const float* __rest
 
 __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restrict__ part, int nsplit, int B,
                                                             int out_dim, const float* __restrict__ bias,
-                                                            const float* __restrict__ mv, int relu,
+                                                            const float* __restrict__ mv, int act,
                                                             float* __restrict__ y) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     if (i >= (long)B * out_dim) return;
@@ -97,7 +97,8 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restr
     float r = (float)s;
     if (bias) r += bias[o];
     if (mv) r -= mv[o];
-    if (relu) r = fmaxf(r, 0.0f);
+    if (act == VDK_ACT_RELU) r = fmaxf(r, 0.0f);
+    else if (act == VDK_ACT_SIGMOID) r = 1.0f / (1.0f + expf(-r));
     y[i] = r;
 }
 
@@ -139,11 +140,12 @@ extern "C" size_t vdk_linear_workspace_size(int batch, int in_dim, int out_dim) 
 }
 
 extern "C" int vdk_linear_ex(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
-                             const float* d_mean_vec, int out_dim, int relu, float* d_y, void* d_work,
+                             const float* d_mean_vec, int out_dim, int act, float* d_y, void* d_work,
                              size_t work_bytes, void* stream) {
     return guarded([&] {
         require(d_x && d_w && d_y && d_work, "linear: NULL device pointer");
         require(batch > 0 && in_dim > 0 && out_dim > 0, "linear: empty shape");
+        require(act == VDK_ACT_NONE || act == VDK_ACT_RELU || act == VDK_ACT_SIGMOID, "linear: unknown activation");
         require(work_bytes >= vdk_linear_workspace_size(batch, in_dim, out_dim),
                 "linear: workspace smaller than vdk_linear_workspace_size()");
         const int ns = linear_splits(in_dim);
@@ -155,7 +157,7 @@ extern "C" int vdk_linear_ex(const float* d_x, int batch, int in_dim, const floa
                            dim3(256), 0, s, d_x, batch, in_dim, d_w, out_dim, slice, part);
         VDK_HIP(hipGetLastError());
         hipLaunchKernelGGL(linear_reduce_kernel, dim3(cdiv((long)batch * out_dim, 256)), dim3(256), 0, s, part,
-                           nsplit, batch, out_dim, d_bias, d_mean_vec, relu ? 1 : 0, d_y);
+                           nsplit, batch, out_dim, d_bias, d_mean_vec, act, d_y);
         VDK_HIP(hipGetLastError());
     });
 }

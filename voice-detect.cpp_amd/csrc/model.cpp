@@ -55,6 +55,16 @@ std::unique_ptr<Model> Model::load(const std::string& path) {
         r.mean_vec = g.str(p + "mean_vec");
         r.var_eps = g.f32(p + "var_eps", 1e-8f);
     }
+    if (c.arch == "campplus") {
+        CamPPlusCfg& cp = c.campplus;   // src/model_loader.cpp:165-173
+        const std::string p = "voicedetect.campplus.";
+        cp.conv_weight = g.str_arr(p + "conv_weight");
+        cp.conv_bias = g.str_arr(p + "conv_bias");
+        cp.bn_prefix = g.str_arr(p + "bn_prefix");
+        cp.emb_bn_mean = g.str(p + "emb_bn_mean");
+        cp.emb_bn_var = g.str(p + "emb_bn_var");
+        cp.bn_eps = g.f32(p + "bn_eps", 1e-5f);
+    }
     // src/model_loader.cpp:212-214: a speaker model needs an embedding dim.
     if (c.embedding_dim <= 0 && !c.analyze_present) throw Error("gguf: voicedetect.embedding_dim missing");
     return m;
@@ -81,8 +91,9 @@ void Model::ensure_device() {
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) throw Error("voicedetect: no HIP device available");
     VDK_HIP(hipGetDevice(&device_));
     const bool resnet = cfg_.arch == "wespeaker_resnet34", ecapa = cfg_.arch == "ecapa_tdnn";
-    if (!resnet && !ecapa) {
-        if (cfg_.arch == "eres2net" || cfg_.arch == "campplus")
+    const bool campp = cfg_.arch == "campplus";
+    if (!resnet && !ecapa && !campp) {
+        if (cfg_.arch == "eres2net")
             throw Error("voicedetect: arch '" + cfg_.arch + "' is not implemented by this build yet");
         throw Error("voicedetect: unsupported arch '" + cfg_.arch + "'");
     }
@@ -92,7 +103,8 @@ void Model::ensure_device() {
     if (!fb_tables_) VDK_HIP(hipMalloc(&fb_tables_, tb));
     check(vdk_fbank_tables_fill(&cfg_.fbank, fb_tables_));
     if (resnet) upload_resnet();
-    else upload_ecapa();
+    else if (ecapa) upload_ecapa();
+    else upload_campplus();
     ready_ = true;
 }
 
@@ -202,6 +214,7 @@ void Model::ensure_workspace(int batch, int n_samples) {
     w.pre = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * cfg_.embedding_dim));
     w.emb = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * cfg_.embedding_dim));
     if (cfg_.arch == "ecapa_tdnn") alloc_ecapa_workspace(batch, T);
+    else if (cfg_.arch == "campplus") alloc_campplus_workspace(batch, T);
     else alloc_resnet_workspace(batch, T);
 }
 
@@ -263,6 +276,7 @@ void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) 
     check(vdk_fbank(&cfg_.fbank, fb_tables_, d_pcm, batch, n_samples, ws_.feats, stream_));
     prof_end();
     if (cfg_.arch == "ecapa_tdnn") encode_ecapa(batch, T);
+    else if (cfg_.arch == "campplus") encode_campplus(batch, T);
     else encode_resnet(batch, T);
     const int E = cfg_.embedding_dim;
     VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));

@@ -28,6 +28,13 @@ struct ResNetCfg {
     float var_eps = 1e-8f;
 };
 
+// src/model_loader.hpp:82-99
+struct CamPPlusCfg {
+    std::vector<std::string> conv_weight, conv_bias, bn_prefix;
+    std::string emb_bn_mean, emb_bn_var;
+    float bn_eps = 1e-5f;
+};
+
 struct ModelConfig {
     std::string arch;
     int embedding_dim = 0;
@@ -35,6 +42,7 @@ struct ModelConfig {
     bool analyze_present = false;
     vdk_fbank_cfg fbank{};
     ResNetCfg resnet;
+    CamPPlusCfg campplus;
 };
 
 // Throws vdk::Error with vdk_last_error() when a vdk_* call returned nonzero.
@@ -91,8 +99,8 @@ private:
     // (time is the W axis, H = 1): y = bn(relu(conv(x) + b)) with the eval
     // BatchNorm as a per-channel affine after the activation.
     struct Layer {
-        int ic = 0, oc = 0, k = 1;
-        void* w = nullptr;          // f16 [OC][K][IC]
+        int ic = 0, oc = 0, k = 1, kh = 1;
+        void* w = nullptr;          // f16 [OC][KH][K][IC]
         float* b = nullptr;         // f32 [OC]
         float* scale = nullptr;     // BatchNorm after ReLU (nullptr = none)
         float* shift = nullptr;
@@ -115,6 +123,36 @@ private:
         float* fc_w = nullptr;          // fc with asp_bn folded in, f32 [E][2*mfa]
         float* fc_b = nullptr;
     };
+    // CAM++ (src/encoder_campplus.cpp): FCM convs, strided TDNN, three dense
+    // blocks of context-masked layers with halving transits, stats, dense head.
+    struct CamDense {
+        float* bn_s = nullptr;      // nonlinear1 BN as scale / shift over c_in
+        float* bn_t = nullptr;
+        Layer l1, local;            // 1x1 c_in -> bn_ch (+ReLU); k=3 bn_ch -> growth (gated)
+        float* c1_w = nullptr;      // CAM context MLP, f32 [h1][bn_ch], [growth][h1]
+        float* c1_b = nullptr;
+        float* c2_w = nullptr;
+        float* c2_b = nullptr;
+        int c_in = 0, h1 = 0;
+    };
+    struct CamBlock {
+        std::vector<CamDense> layers;
+        float* bn_s = nullptr;      // transit nonlinear BN
+        float* bn_t = nullptr;
+        Layer transit;
+        int dil = 1, cmax = 0;
+    };
+    struct Campplus {
+        int n_mels = 0, m_ch = 0, hf = 0, bn_ch = 0, growth = 0, c_out = 0;
+        float* stem_w = nullptr;    // f32 [m_ch][9]
+        float* stem_b = nullptr;
+        std::vector<Layer> fcm;     // FCM convs after the stem, manifest order
+        Layer fcm_out;              // final 3x3 freq-stride-2 conv
+        Layer tdnn;                 // k=5 s2 over [B][T][hf*m_ch] (channels in (h, c) order)
+        CamBlock blocks[3];
+        float* dense_w = nullptr;   // head with the affine-free BN folded, f32 [E][2*c_out]
+        float* dense_b = nullptr;
+    };
     struct Workspace {
         int batch = 0, n_samples = 0;
         std::vector<void*> allocs;      // every allocation below, freed together
@@ -132,14 +170,22 @@ private:
              *mfa = nullptr, *a1 = nullptr;
         float *logits = nullptr, *se_m = nullptr, *se_h = nullptr, *se_g = nullptr, *stats = nullptr,
               *pb = nullptr;
+        // CAM++
+        void* fcm[3] = {nullptr, nullptr, nullptr};
+        void* fcm_t = nullptr;
+        void* dense[3] = {nullptr, nullptr, nullptr};
+        void *abuf = nullptr, *cc = nullptr, *fin = nullptr;
+        float *sums = nullptr, *gate = nullptr;
     };
 
     void ensure_device();
     void upload_resnet();
     void upload_ecapa();
+    void upload_campplus();
     void ensure_workspace(int batch, int n_samples);
     void alloc_resnet_workspace(int batch, int T);
     void alloc_ecapa_workspace(int batch, int T);
+    void alloc_campplus_workspace(int batch, int T);
     void* ws_alloc(size_t bytes);
     void free_workspace();
     // The whole forward for device PCM into device embeddings (pre-norm copy in ws_.pre).
@@ -147,6 +193,9 @@ private:
     // Encoder from ws_.feats to ws_.pooled (raw pooling statistics) and ws_.pre.
     void encode_resnet(int batch, int T);
     void encode_ecapa(int batch, int T);
+    void encode_campplus(int batch, int T);
+    // One vdk_conv2d_ex launch with profiling (flops from the descriptor's shape).
+    void conv_ex(const char* name, const vdk_conv_desc& d);
     void conv(const Conv& c, const void* x, int batch, int H, int W, const void* res, int relu, void* y);
     // Time-major TDNN layer: x [B][W][x_stride] (W = T + 2*pad of a pre-padded
     // input) -> y [B][W - (k-1)*dil][y_stride].
@@ -172,6 +221,7 @@ private:
     int stem_oc_ = 0;
     std::vector<Block> blocks_;
     Ecapa ecapa_;
+    Campplus campp_;
     float* seg_w_ = nullptr;
     float* seg_b_ = nullptr;
     float* mean_vec_ = nullptr;

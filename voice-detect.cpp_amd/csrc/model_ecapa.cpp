@@ -239,10 +239,11 @@ void Model::tdnn(const char* name, const Layer& l, const void* x, int x_stride, 
     }
     vdk_conv_desc d{};
     d.x = x; d.batch = batch; d.H = 1; d.W = W; d.IC = l.ic; d.x_stride = x_stride;
-    d.w = l.w; d.OC = l.oc; d.KH = 1; d.KW = l.k; d.stride = 1; d.pad = 0; d.dilation = dil;
+    d.w = l.w; d.OC = l.oc; d.KH = 1; d.KW = l.k;
+    d.stride_h = d.stride_w = 1; d.dil_h = 1; d.dil_w = dil;
     d.bias = bias; d.bias_batch_stride = bias_bs;
     d.post_scale = l.scale; d.post_shift = l.shift;
-    d.relu = relu; d.tanh_after = tanh_after;
+    d.act = relu ? VDK_ACT_RELU : VDK_ACT_NONE; d.tanh_after = tanh_after;
     d.y = y; d.y_stride = y_stride; d.y_f32 = y_f32;
     d.tile = -1;
     check_rc(vdk_conv2d_ex(&d, stream_));

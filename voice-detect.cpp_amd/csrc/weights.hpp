@@ -1,0 +1,59 @@
+// weights.hpp - reading GGUF conv / linear weights into kernel layouts.
+//
+// A manifest conv weight arrives in one of the reference converter's forms
+// (scripts/convert_voicedetect_to_gguf.py quant_plan): F32/F16 with ggml
+// ne = [KW, KH, IC, OC] (Conv2d) or [K, IC, OC] (Conv1d), or a 1x1 weight
+// squeezed to a 2-D [IC, OC] matrix (F16 / Q8_0 blocks along IC).  read_conv
+// dequantises any of them to f32 [OC][IC][KH][KW]; pack_conv_f16 reorders to
+// the conv kernels' f16 [OC][KH][KW][ICp] with an optional input-channel
+// permutation and zero channels up to ICp.
+#pragma once
+
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "gguf.hpp"
+
+namespace vdk {
+
+struct HostConv {
+    int oc = 0, ic = 0, kh = 1, kw = 1;
+    std::vector<float> w;   // [OC][IC][KH][KW]
+};
+
+inline HostConv read_conv(const GgufFile& g, const std::string& name) {
+    const GgufTensor* t = g.tensor(name);
+    require(t != nullptr, "voicedetect: missing tensor '" + name + "'");
+    HostConv c;
+    if (t->ne.size() == 2) {
+        c.ic = (int)t->ne[0]; c.oc = (int)t->ne[1];
+    } else if (t->ne.size() == 3) {
+        c.kw = (int)t->ne[0]; c.ic = (int)t->ne[1]; c.oc = (int)t->ne[2];
+    } else if (t->ne.size() == 4) {
+        c.kw = (int)t->ne[0]; c.kh = (int)t->ne[1]; c.ic = (int)t->ne[2]; c.oc = (int)t->ne[3];
+    } else {
+        throw Error("voicedetect: conv weight '" + name + "' must be 2-D, 3-D or 4-D");
+    }
+    c.w = g.to_f32(name);
+    require(c.w.size() == (size_t)c.oc * c.ic * c.kh * c.kw, "voicedetect: tensor '" + name + "' has the wrong size");
+    return c;
+}
+
+// f16 [OC][KH][KW][icp]; source channel i lands at ic_map(i) (identity if empty).
+inline std::vector<uint16_t> pack_conv_f16(const HostConv& c, int icp,
+                                           const std::function<int(int)>& ic_map = nullptr) {
+    std::vector<uint16_t> p((size_t)c.oc * c.kh * c.kw * icp, 0);
+    for (int o = 0; o < c.oc; ++o)
+        for (int i = 0; i < c.ic; ++i) {
+            const int d = ic_map ? ic_map(i) : i;
+            for (int kh = 0; kh < c.kh; ++kh)
+                for (int kw = 0; kw < c.kw; ++kw)
+                    p[(((size_t)o * c.kh + kh) * c.kw + kw) * icp + d] =
+                        float_to_half_bits(c.w[(((size_t)o * c.ic + i) * c.kh + kh) * c.kw + kw]);
+        }
+    return p;
+}
+
+}  // namespace vdk

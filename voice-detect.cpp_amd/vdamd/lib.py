@@ -25,17 +25,23 @@ class FbankCfg(C.Structure):
                 ("low_freq", C.c_float), ("high_freq", C.c_float), ("cmn", C.c_int)]
 
 
+ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_SILU = 0, 1, 2, 3
+
+
 class ConvDesc(C.Structure):
     """vdk_conv_desc (include/vdk.h)."""
     _fields_ = [("x", _vp), ("batch", C.c_int), ("H", C.c_int), ("W", C.c_int), ("IC", C.c_int),
                 ("x_stride", C.c_int),
-                ("w", _vp), ("OC", C.c_int), ("KH", C.c_int), ("KW", C.c_int), ("stride", C.c_int),
-                ("pad", C.c_int), ("dilation", C.c_int),
+                ("w", _vp), ("OC", C.c_int), ("KH", C.c_int), ("KW", C.c_int),
+                ("stride_h", C.c_int), ("stride_w", C.c_int), ("pad_h", C.c_int), ("pad_w", C.c_int),
+                ("dil_h", C.c_int), ("dil_w", C.c_int),
                 ("bias", _vp), ("bias_batch_stride", C.c_int),
+                ("gate", _vp), ("gate_seg", C.c_int), ("gate_nseg", C.c_int),
                 ("residual", _vp), ("res_stride", C.c_int),
+                ("act", C.c_int), ("clamp_hi", C.c_float),
                 ("post_scale", _vp), ("post_shift", _vp),
-                ("relu", C.c_int), ("tanh_after", C.c_int),
-                ("y", _vp), ("y_stride", C.c_int), ("y_f32", C.c_int),
+                ("tanh_after", C.c_int),
+                ("y", _vp), ("y_stride", C.c_int), ("y_f32", C.c_int), ("y_time_major", C.c_int),
                 ("tile", C.c_int)]
 
 
@@ -110,6 +116,10 @@ _SIGS = {
                                        _vp]),
     "vdk_asp_stats": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "vdk_asp_pool": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "vdk_bn_act": (C.c_int, [_vp, C.c_int, C.c_long, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, _vp]),
+    "vdk_segment_sums": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_cam_context": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int,
+                                  _vp, _vp]),
 }
 
 
