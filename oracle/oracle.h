@@ -198,6 +198,35 @@ typedef struct {
 int orc_campplus_forward(const orc_campplus* net, const float* feats, int T, float* emb,
                          orc_campplus_caps* caps);
 
+/* ------------------------------------------------------------- ERes2Net */
+
+#define ORC_ERES_MAX_CONV 128
+
+/* 3D-Speaker ERes2Net from its flat execution-order manifest
+ * (model_loader.hpp:68-79): conv[] with per-conv stride[], blocks per layer,
+ * m_channels, the Res2Net scale, the seg_1 embedding FC. */
+typedef struct {
+    int n_mels, n_conv, m_channels, scale, emb_dim, l2_normalize;
+    int num_blocks[4];
+    float relu_clamp, var_eps;
+    orc_conv conv[ORC_ERES_MAX_CONV];
+    int stride[ORC_ERES_MAX_CONV];
+    const float* seg_w; const float* seg_b;
+} orc_eres2net;
+
+typedef struct {
+    float* stem;       /* [M][n_mels][T] after ReLU */
+    float* fused;      /* [16M][H'][W'] the last AFF output */
+    float* pooled;     /* [2 * 16M * H'] */
+    float* pre_norm;   /* [emb] */
+} orc_eres2net_caps;
+
+/* Full ERes2Net forward of one clip from FBank features [n_mels][T]
+ * (src/encoder_eres2net.cpp:139-265).  Returns 0, or 1 when the manifest
+ * does not match the topology. */
+int orc_eres2net_forward(const orc_eres2net* net, const float* feats, int T, float* emb,
+                         orc_eres2net_caps* caps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -556,3 +556,82 @@ class OracleCampplus:
         rc = L.orc_campplus_forward(C.byref(n), feats, T, emb, C.byref(caps))
         assert rc == 0, "CAM++ manifest does not match the fixed topology"
         return (emb, bufs) if capture else emb
+
+
+# ---------------------------------------------------------------- ERes2Net
+
+class Eres2net(C.Structure):
+    _fields_ = [("n_mels", C.c_int), ("n_conv", C.c_int), ("m_channels", C.c_int), ("scale", C.c_int),
+                ("emb_dim", C.c_int), ("l2_normalize", C.c_int), ("num_blocks", C.c_int * 4),
+                ("relu_clamp", C.c_float), ("var_eps", C.c_float), ("conv", Conv * 128), ("stride", C.c_int * 128),
+                ("seg_w", _fp), ("seg_b", _fp)]
+
+
+class Eres2netCaps(C.Structure):
+    _fields_ = [("stem", _fp), ("fused", _fp), ("pooled", _fp), ("pre_norm", _fp)]
+
+
+class OracleEres2net:
+    """orc_eres2net built from a parsed ERes2Net GGUF (weights dequantised to f32)."""
+
+    def __init__(self, g):
+        self.keep = []
+        kv = g.kv
+        n = Eres2net()
+        names_w = kv["voicedetect.eres2net.conv_weight"]
+        names_b = kv["voicedetect.eres2net.conv_bias"]
+        strides = kv["voicedetect.eres2net.conv_stride"]
+        n.n_mels = int(kv.get("voicedetect.fbank.n_mels", 80))
+        n.n_conv = len(names_w)
+        n.m_channels = int(kv["voicedetect.eres2net.m_channels"])
+        n.scale = int(kv.get("voicedetect.eres2net.scale", 2))
+        for i, v in enumerate(kv["voicedetect.eres2net.num_blocks"]):
+            n.num_blocks[i] = int(v)
+        n.relu_clamp = float(kv.get("voicedetect.eres2net.relu_clamp", 20.0))
+        n.var_eps = float(kv.get("voicedetect.eres2net.var_eps", 1e-8))
+        n.l2_normalize = int(bool(kv.get("voicedetect.l2_normalize", True)))
+
+        def arr(a):
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            self.keep.append(a)
+            return a.ctypes.data_as(_fp)
+
+        for i, (wn, bn) in enumerate(zip(names_w, names_b)):
+            w = _weight4(g, wn)
+            c = n.conv[i]
+            c.w = arr(w)
+            c.b = arr(g.array(bn)) if bn else None
+            c.oc, c.ic, c.kh, c.kw = w.shape
+            n.stride[i] = int(strides[i])
+        sw = np.asarray(g.array(kv["voicedetect.eres2net.seg_weight"]), dtype=np.float32)
+        n.seg_w = arr(sw)
+        n.seg_b = arr(g.array(kv["voicedetect.eres2net.seg_bias"]))
+        n.emb_dim = sw.shape[0]
+        self.net = n
+
+    def forward(self, feats, capture=False):
+        L = lib()
+        if not hasattr(L, "_eres_ready"):
+            L.orc_eres2net_forward.argtypes = [C.POINTER(Eres2net), F32P, C.c_int, F32P, C.POINTER(Eres2netCaps)]
+            L.orc_eres2net_forward.restype = C.c_int
+            L._eres_ready = True
+        feats = np.ascontiguousarray(feats, dtype=np.float32)
+        T = feats.shape[1]
+        n = self.net
+        emb = np.zeros(n.emb_dim, dtype=np.float32)
+        caps = Eres2netCaps()
+        bufs = {}
+        if capture:
+            M = n.m_channels
+            H, W = n.n_mels, T
+            bufs["stem"] = np.zeros((M, H, W), dtype=np.float32)
+            for _ in range(3):
+                H, W = (H - 1) // 2 + 1, (W - 1) // 2 + 1
+            bufs["fused"] = np.zeros((16 * M, H, W), dtype=np.float32)
+            bufs["pooled"] = np.zeros(2 * 16 * M * H, dtype=np.float32)
+            bufs["pre_norm"] = np.zeros(n.emb_dim, dtype=np.float32)
+            for k in ("stem", "fused", "pooled", "pre_norm"):
+                setattr(caps, k, bufs[k].ctypes.data_as(_fp))
+        rc = L.orc_eres2net_forward(C.byref(n), feats, T, emb, C.byref(caps))
+        assert rc == 0, "ERes2Net manifest does not match the topology"
+        return (emb, bufs) if capture else emb

@@ -386,3 +386,94 @@ def write_campplus(path, seed, **kw):
     kv, tensors = make_campplus(seed, **kw)
     G.write_gguf(path, kv, tensors)
     return path
+
+
+# ---------------------------------------------------------------- ERes2Net
+
+def make_eres2net(seed, n_mels=80, m_ch=32, num_blocks=(3, 4, 6, 3), base_width=32, scale=2, emb_dim=512,
+                  wtype=G.GGML_Q8_0):
+    """Random-init 3D-Speaker ERes2Net in the reference GGUF schema
+    (src/model_loader.hpp:68-79, scripts/convert_voicedetect_to_gguf.py
+    parse_eres2net_onnx): every conv BN-folded with an opaque `onnx::Conv_*`
+    name and a bias, except the three bias-free cross-stage downsample convs;
+    the flat manifest lists the convs in forward order with their strides.
+    Storage follows the converter's kernel==1 rule (1x1 convs and seg_1 as
+    2-D matrices of `wtype`, 3x3 convs F32 with f16-representable values)."""
+    ws = _WeightStream(seed)
+    T = []
+    conv_w, conv_b, conv_s = [], [], []
+    nid = [0]
+
+    def conv(oc, ic, k, stride, bias=True):
+        nid[0] += 1
+        wn, bn = f"onnx::Conv_{3000 + 2 * nid[0]}", f"onnx::Conv_{3001 + 2 * nid[0]}"
+        w, b = conv_bn_folded(ws, oc, ic, k, k, bn=bias)
+        if k == 1 and wtype != G.GGML_F32 and _q8_eligible(1, 1, ic, oc):
+            T.append((wn, wtype, [oc, ic], w.reshape(oc, ic)))
+        else:
+            T.append((wn, G.GGML_F32, [oc, ic, k, k], _f16_exact(w)))
+        if bias:
+            T.append((bn, G.GGML_F32, [oc], b))
+        conv_w.append(wn)
+        conv_b.append(bn if bias else "")
+        conv_s.append(stride)
+
+    def aff(channels):
+        inter = channels // 4
+        conv(inter, 2 * channels, 1, 1)
+        conv(channels, inter, 1, 1)
+
+    conv(m_ch, 1, 3, 1)                                     # stem
+    in_planes = m_ch
+    for li, (nb, stride) in enumerate(zip(num_blocks, (1, 2, 2, 2))):
+        planes = m_ch * (2 ** li)
+        width = planes * base_width // 64
+        for bi in range(nb):
+            s = stride if bi == 0 else 1
+            conv(width * scale, in_planes, 1, s)            # conv1
+            for i in range(scale):
+                if i > 0 and li >= 2:
+                    aff(width)                              # diff_AFF scale fusion
+                conv(width, width, 3, 1)                    # convs[i]
+            conv(2 * planes, width * scale, 1, 1)           # conv3
+            if s != 1 or in_planes != 2 * planes:
+                conv(2 * planes, in_planes, 1, s)           # shortcut
+            in_planes = 2 * planes
+        if li >= 1:
+            # after layer li+1: downsample of the previous fused feature, then AFF
+            conv(2 * planes, planes, 3, 2, bias=False)
+            aff(2 * planes)
+    H = n_mels // 8
+    stats = 2 * in_planes * H
+    w = (normal(ws.next(), emb_dim * stats).reshape(emb_dim, stats) * np.sqrt(1.0 / stats)).astype(np.float32)
+    b = (0.01 * normal(ws.next(), emb_dim)).astype(np.float32)
+    if wtype != G.GGML_F32 and stats % 32 == 0:
+        T.append(("seg_1.weight", wtype, [emb_dim, stats], w))
+    else:
+        T.append(("seg_1.weight", G.GGML_F32, [emb_dim, stats], _f16_exact(w)))
+    T.append(("seg_1.bias", G.GGML_F32, [emb_dim], b))
+    kv = {
+        "general.architecture": "voicedetect",
+        "general.name": f"synthetic-eres2net-seed{seed}",
+        "voicedetect.arch": "eres2net",
+        "voicedetect.embedding_dim": emb_dim,
+        "voicedetect.l2_normalize": True,
+        "voicedetect.eres2net.conv_weight": conv_w,
+        "voicedetect.eres2net.conv_bias": conv_b,
+        "voicedetect.eres2net.conv_stride": [G.I32(s) for s in conv_s],
+        "voicedetect.eres2net.num_blocks": [G.I32(n) for n in num_blocks],
+        "voicedetect.eres2net.m_channels": m_ch,
+        "voicedetect.eres2net.scale": scale,
+        "voicedetect.eres2net.seg_weight": "seg_1.weight",
+        "voicedetect.eres2net.seg_bias": "seg_1.bias",
+        "voicedetect.eres2net.relu_clamp": 20.0,
+        "voicedetect.eres2net.var_eps": 1e-8,
+    }
+    kv.update(_fbank_kv(n_mels))
+    return kv, T
+
+
+def write_eres2net(path, seed, **kw):
+    kv, tensors = make_eres2net(seed, **kw)
+    G.write_gguf(path, kv, tensors)
+    return path
