@@ -98,6 +98,11 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * stored f16 (or f32 if y_f32) at pixel (b, oh, ow), or at (b, ow, oh) when
  * y_time_major (an NHWC [B][H][W][C] map written as [B][W][H*C], no residual).
  * OC needs only be a multiple of 8: surplus rows of a tile are masked.
+ * split != 0 selects split-f16 arithmetic (~2^-21 relative instead of f16's
+ * 2^-11, for ill-conditioned networks): x, residual and y hold value = hi + lo
+ * with the lo halves x_lo / res_lo / y_lo elements after the hi halves (same
+ * pixel strides), w is [OC][KH][KW][3*IC] = [hi | hi | lo] per tap, and the
+ * GEMM runs x_hi.w_hi + x_lo.w_hi + x_hi.w_lo on f16 MFMA (3x the work).
  * tile = -1 picks the kernel automatically. */
 typedef struct {
     const void* x; int batch, H, W, IC, x_stride;
@@ -110,6 +115,7 @@ typedef struct {
     const float* post_scale; const float* post_shift;
     int tanh_after;
     void* y; int y_stride, y_f32, y_time_major;
+    int split; int x_lo, res_lo, y_lo;
     int tile;
 } vdk_conv_desc;
 int vdk_conv2d_ex(const vdk_conv_desc* desc, void* stream);
@@ -132,6 +138,10 @@ int vdk_conv2d_tile_fits(int tile, int IC, int OC, int KH, int KW, int stride, i
 int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,
                      const float* d_w, const float* d_bias, int OC, int relu,
                      void* d_y, void* stream);
+/* Same; split != 0 stores split-f16 [hi(OC) | lo(OC)] per pixel (see vdk_conv_desc). */
+int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W,
+                        const float* d_w, const float* d_bias, int OC, int relu, int split,
+                        void* d_y, void* stream);
 
 /* ---- temporal statistics pooling ----
  * Replaces the TSTP graph of src/encoder_resnet.cpp:140-157: per (c, h) mean
@@ -139,6 +149,10 @@ int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,
  * pooled[b] = [mean(c,h) ; std(c,h)], length 2*C*H.  x [B][H][W][C] f16. */
 int vdk_tstp(const void* d_x, int batch, int H, int W, int C, float eps,
              float* d_pooled, void* stream);
+/* Same over x with pixel stride x_stride (0 = C); x_lo > 0: split-f16 input,
+ * value = x + x[.. + x_lo]. */
+int vdk_tstp_ex(const void* d_x, int x_stride, int x_lo, int batch, int H, int W, int C, float eps,
+                float* d_pooled, void* stream);
 
 /* ---- embedding FC ----
  * Replaces the seg_1 mul_mat + bias - mean_vec of src/encoder_resnet.cpp:159-169:
@@ -205,6 +219,15 @@ int vdk_segment_sums(const void* d_x, int x_stride, int batch, int T, int C, int
 int vdk_cam_context(const float* d_sums, int batch, int T, int C, int seg, const float* d_w1,
                     const float* d_b1, int H1, const float* d_w2, const float* d_b2, int G,
                     float* d_gate, void* stream);
+
+/* ---- ERes2Net helper (src/encoder_eres2net.cpp:91-101) ----
+ * AFF output y = (x + ds) + t * (x - ds) with t = tanh(local_att(cat(x, ds)))
+ * already computed; all f16 rows of C channels with their own strides.  With
+ * split != 0 every tensor is split-f16 (value = hi + lo, lo *_lo elements
+ * after hi), as in vdk_conv_desc. */
+int vdk_aff_combine(const void* d_t, int t_stride, int t_lo, const void* d_x, int x_stride, int x_lo,
+                    const void* d_ds, int ds_stride, int ds_lo, long rows, int C, int split, void* d_y,
+                    int y_stride, int y_lo, void* stream);
 
 #ifdef __cplusplus
 }

@@ -61,3 +61,27 @@ def cosine(a, b):
     a = np.asarray(a, dtype=np.float64).reshape(-1)
     b = np.asarray(b, dtype=np.float64).reshape(-1)
     return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def conv_ex(x_ptr, batch, H, W, IC, xs, w_khkwic, OC, KH, KW, y_ptr, ys=0, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1,
+            bias=None, residual=None, act=lib.ACT_NONE, gate=None, gate_seg=0, gate_nseg=0, y_time_major=0,
+            clamp_hi=0.0, tanh_after=0):
+    """One vdk_conv2d_ex launch; w_khkwic is the packed f16 [OC][KH][KW][IC] weight."""
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(w_khkwic, dtype=np.float16))]
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = x_ptr, batch, H, W, IC, xs
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, OC, KH, KW
+    d.stride_h, d.stride_w, d.pad_h, d.pad_w, d.dil_h, d.dil_w = sh, sw, ph, pw, dh, dw
+    if bias is not None:
+        keep.append(lib.DeviceBuffer.from_array(bias.astype(np.float32)))
+        d.bias = keep[-1].ptr
+    if residual is not None:
+        d.residual = residual
+    if gate is not None:
+        keep.append(lib.DeviceBuffer.from_array(gate.astype(np.float32)))
+        d.gate, d.gate_seg, d.gate_nseg = keep[-1].ptr, gate_seg, gate_nseg
+    d.act, d.clamp_hi, d.tanh_after = act, clamp_hi, tanh_after
+    d.y, d.y_stride, d.y_time_major = y_ptr, ys, y_time_major
+    d.tile = -1
+    lib.check(lib.lib().vdk_conv2d_ex(d, None))
+    lib.check(lib.lib().vdk_synchronize())

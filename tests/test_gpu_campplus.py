@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import pyoracle as O
-from gpu_util import announce, close_report, cosine, device_ok
+from gpu_util import announce, close_report, conv_ex, cosine, device_ok
 from vdamd import gguf, lib, synth
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
@@ -43,28 +43,6 @@ def _assert_close(got, ref, tag):
 def _w(rng, oc, ic, kh, kw):
     return (rng.standard_normal((oc, ic, kh, kw), dtype=np.float32) * np.sqrt(2.0 / (ic * kh * kw))).astype(
         np.float16)
-
-
-def conv_ex(x_ptr, batch, H, W, IC, xs, w_khkwic, OC, KH, KW, y_ptr, ys=0, sh=1, sw=1, ph=0, pw=0, dh=1, dw=1,
-            bias=None, residual=None, act=lib.ACT_NONE, gate=None, gate_seg=0, gate_nseg=0, y_time_major=0):
-    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(w_khkwic, dtype=np.float16))]
-    d = lib.ConvDesc()
-    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = x_ptr, batch, H, W, IC, xs
-    d.w, d.OC, d.KH, d.KW = keep[0].ptr, OC, KH, KW
-    d.stride_h, d.stride_w, d.pad_h, d.pad_w, d.dil_h, d.dil_w = sh, sw, ph, pw, dh, dw
-    if bias is not None:
-        keep.append(lib.DeviceBuffer.from_array(bias.astype(np.float32)))
-        d.bias = keep[-1].ptr
-    if residual is not None:
-        d.residual = residual
-    if gate is not None:
-        keep.append(lib.DeviceBuffer.from_array(gate.astype(np.float32)))
-        d.gate, d.gate_seg, d.gate_nseg = keep[-1].ptr, gate_seg, gate_nseg
-    d.act = act
-    d.y, d.y_stride, d.y_time_major = y_ptr, ys, y_time_major
-    d.tile = -1
-    lib.check(lib.lib().vdk_conv2d_ex(d, None))
-    _sync()
 
 
 def test_fcm_freq_stride_convs():

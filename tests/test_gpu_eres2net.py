@@ -1,0 +1,283 @@
+"""Parity of the ERes2Net GPU path (src/encoder_eres2net.cpp) against the oracle.
+
+Per layer at the 20 s / batch-16 shape (T = 1998 frames): the Res2Net 3x3
+convs over channel slices with the Hardtanh(0, 20) clamp (including the
+16-channel chunks of layer 1, masked output rows), the strided 1x1 conv1 /
+shortcut with residual + clamp, the cross-stage 3x3 stride-2 downsample
+stored into its half of the concatenation buffer, the AFF local_att convs
+(SiLU, tanh epilogues) and the AFF combine.  End to end: a random-init
+ERes2Net base (m_channels 32, q8_0 1x1 weights, 512-d) behind the C ABI,
+pooled statistics within 2e-3 relative L2 and embeddings at cosine >= 0.9999.
+"""
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import pyoracle as O
+from gpu_util import announce, close_report, conv_ex, cosine, device_ok
+from vdamd import gguf, lib, synth
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
+
+RTOL = 2e-3
+ATOL_RMS = 2e-3
+B = 16
+N20S = 320000
+T20S = 1998
+
+
+def _assert_close(got, ref, tag):
+    ok, ratio, rel = close_report(got, ref, RTOL, ATOL_RMS)
+    assert ok and rel <= 2e-3, f"{tag}: max tol ratio {ratio:.3f}, rel-L2 {rel:.2e}"
+    return rel
+
+
+def _w(rng, oc, ic, k):
+    return (rng.standard_normal((oc, ic, k, k), dtype=np.float32) * np.sqrt(2.0 / (ic * k * k))).astype(np.float16)
+
+
+def _clamp(v):
+    return np.clip(v, 0.0, 20.0)
+
+
+def test_chunk_convs_over_slices_with_clamp():
+    """Layer-1 shapes: [chunk0 | chunk1 | sp0 | sp1] with w = 16 at 80 x 1998."""
+    rng = np.random.default_rng(101)
+    H, T, w = 80, T20S, 16
+    S = 4 * w
+    announce(f"eres chunk convs B={B} H={H} T={T} w={w}")
+    s4 = (np.abs(rng.standard_normal((B, H, T, S), dtype=np.float32)) * 3).astype(np.float16)
+    d4 = lib.DeviceBuffer.from_array(s4)
+    wa = _w(rng, w, w, 3)
+    ba = rng.uniform(-0.5, 0.5, w).astype(np.float32)
+    # chunk 0 read as [chunk0 | chunk1] with zero weights on chunk1 -> sp0
+    wpad = np.zeros((w, 2 * w, 3, 3), dtype=np.float16)
+    wpad[:, :w] = wa
+    conv_ex(d4.ptr, B, H, T, 2 * w, S, wpad.transpose(0, 2, 3, 1), w, 3, 3, d4.ptr + 2 * w * 2, ys=S, ph=1, pw=1,
+            bias=ba, act=lib.ACT_RELU)
+    out = d4.to_array(np.float16, (B, H, T, S))
+    for c in (0, B - 1):
+        ref = O.conv2d_g(s4[c, :, :, :w].astype(np.float32).transpose(2, 0, 1), wa.astype(np.float32), ph=1, pw=1,
+                         bias=ba, relu=True)
+        rel = _assert_close(out[c, :, :, 2 * w:3 * w].astype(np.float32).transpose(2, 0, 1), ref, f"chunk0 clip {c}")
+        announce(f"chunk0 clip {c} rel-L2 {rel:.2e}")
+    assert np.array_equal(out[..., :2 * w].view(np.uint16), s4[..., :2 * w].view(np.uint16))
+    wb = _w(rng, w, w, 3)
+    bb = rng.uniform(-0.5, 0.5, w).astype(np.float32)
+    wdup = np.concatenate([wb, wb], axis=1)
+    d = lib.ConvDesc()
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(wdup.transpose(0, 2, 3, 1))),
+            lib.DeviceBuffer.from_array(bb)]
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = d4.ptr + w * 2, B, H, T, 2 * w, S
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, w, 3, 3
+    d.stride_h = d.stride_w = 1
+    d.pad_h = d.pad_w = 1
+    d.dil_h = d.dil_w = 1
+    d.bias = keep[1].ptr
+    d.act, d.clamp_hi = lib.ACT_RELU, 20.0
+    d.y, d.y_stride, d.tile = d4.ptr + 3 * w * 2, S, -1
+    lib.check(lib.lib().vdk_conv2d_ex(d, None))
+    lib.check(lib.lib().vdk_synchronize())
+    out2 = d4.to_array(np.float16, (B, H, T, S))
+    for c in (0, B - 1):
+        xin = out[c, :, :, w:2 * w].astype(np.float32) + out[c, :, :, 2 * w:3 * w].astype(np.float32)
+        ref = _clamp(O.conv2d_g(xin.transpose(2, 0, 1), wb.astype(np.float32), ph=1, pw=1, bias=bb))
+        rel = _assert_close(out2[c, :, :, 3 * w:].astype(np.float32).transpose(2, 0, 1), ref, f"chunk1 clip {c}")
+        announce(f"chunk1 (sum folded) clip {c} rel-L2 {rel:.2e}")
+
+
+def test_strided_1x1_with_residual_clamp_and_downsample_into_cat():
+    rng = np.random.default_rng(102)
+    H, T, C = 40, 999, 128
+    announce(f"eres strided convs B={B} H={H} T={T}")
+    x = (np.abs(rng.standard_normal((B, H, T, C), dtype=np.float32)) * 4).astype(np.float16)
+    dx = lib.DeviceBuffer.from_array(x)
+    Ho, Wo = 20, 500
+    w1 = _w(rng, 2 * C, C, 1)
+    b1 = rng.uniform(-0.5, 0.5, 2 * C).astype(np.float32)
+    res = (np.abs(rng.standard_normal((B, Ho, Wo, 2 * C), dtype=np.float32)) * 8).astype(np.float16)
+    dres = lib.DeviceBuffer.from_array(res)
+    y = lib.DeviceBuffer(B * Ho * Wo * 2 * C * 2)
+    d = lib.ConvDesc()
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(w1.transpose(0, 2, 3, 1))),
+            lib.DeviceBuffer.from_array(b1)]
+    d.x, d.batch, d.H, d.W, d.IC = dx.ptr, B, H, T, C
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, 2 * C, 1, 1
+    d.stride_h = d.stride_w = 2
+    d.dil_h = d.dil_w = 1
+    d.bias, d.residual = keep[1].ptr, dres.ptr
+    d.act, d.clamp_hi = lib.ACT_RELU, 20.0
+    d.y, d.tile = y.ptr, -1
+    lib.check(lib.lib().vdk_conv2d_ex(d, None))
+    lib.check(lib.lib().vdk_synchronize())
+    got = y.to_array(np.float16, (B, Ho, Wo, 2 * C))
+    for c in (0, B - 1):
+        ref = _clamp(O.conv2d_g(x[c].astype(np.float32).transpose(2, 0, 1), w1.astype(np.float32), sh=2, sw=2,
+                                bias=b1, residual=res[c].astype(np.float32).transpose(2, 0, 1)))
+        rel = _assert_close(got[c].astype(np.float32).transpose(2, 0, 1), ref, f"1x1 s2 clip {c}")
+        announce(f"1x1 s2 + residual + clamp clip {c} rel-L2 {rel:.2e} (clamped {np.mean(ref == 20.0):.3f})")
+    # 3x3 stride-2 downsample (no bias) into the second half of a [.. 4C] buffer
+    wd = _w(rng, 2 * C, C, 3)
+    cat = lib.DeviceBuffer(B * Ho * Wo * 4 * C * 2)
+    conv_ex(dx.ptr, B, H, T, C, 0, wd.transpose(0, 2, 3, 1), 2 * C, 3, 3, cat.ptr + 2 * C * 2, ys=4 * C, sh=2, sw=2,
+            ph=1, pw=1)
+    gc = cat.to_array(np.float16, (B, Ho, Wo, 4 * C))
+    for c in (0, B - 1):
+        ref = O.conv2d_g(x[c].astype(np.float32).transpose(2, 0, 1), wd.astype(np.float32), sh=2, sw=2, ph=1, pw=1)
+        _assert_close(gc[c, :, :, 2 * C:].astype(np.float32).transpose(2, 0, 1), ref, f"downsample clip {c}")
+
+
+def test_aff_local_att_and_combine():
+    rng = np.random.default_rng(103)
+    L = lib.lib()
+    H, T, C = 20, 500, 64
+    announce(f"eres aff B={B} H={H} T={T} C={C}")
+    cat = rng.standard_normal((B, H, T, 2 * C), dtype=np.float32).astype(np.float16)   # [ds | x]
+    dcat = lib.DeviceBuffer.from_array(cat)
+    w1 = _w(rng, C // 4, 2 * C, 1)
+    b1 = rng.uniform(-0.5, 0.5, C // 4).astype(np.float32)
+    z = lib.DeviceBuffer(B * H * T * (C // 4) * 2)
+    conv_ex(dcat.ptr, B, H, T, 2 * C, 0, w1.transpose(0, 2, 3, 1), C // 4, 1, 1, z.ptr, bias=b1, act=lib.ACT_SILU)
+    gz = z.to_array(np.float16, (B, H, T, C // 4))
+    w2 = _w(rng, C, C // 4, 1)
+    b2 = rng.uniform(-0.5, 0.5, C).astype(np.float32)
+    z2 = lib.DeviceBuffer(B * H * T * C * 2)
+    d = lib.ConvDesc()
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(w2.transpose(0, 2, 3, 1))),
+            lib.DeviceBuffer.from_array(b2)]
+    d.x, d.batch, d.H, d.W, d.IC = z.ptr, B, H, T, C // 4
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, C, 1, 1
+    d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+    d.bias, d.act, d.tanh_after = keep[1].ptr, lib.ACT_NONE, 1
+    d.y, d.tile = z2.ptr, -1
+    lib.check(L.vdk_conv2d_ex(d, None))
+    lib.check(L.vdk_synchronize())
+    gt = z2.to_array(np.float16, (B, H, T, C))
+    for c in (0, B - 1):
+        pre = O.conv2d_g(cat[c].astype(np.float32).transpose(2, 0, 1), w1.astype(np.float32), bias=b1)
+        ref = pre / (1.0 + np.exp(-pre))
+        _assert_close(gz[c].astype(np.float32).transpose(2, 0, 1), ref, f"aff silu clip {c}")
+        ref2 = np.tanh(O.conv2d_g(gz[c].astype(np.float32).transpose(2, 0, 1), w2.astype(np.float32), bias=b2))
+        _assert_close(gt[c].astype(np.float32).transpose(2, 0, 1), ref2, f"aff tanh clip {c}")
+    y = lib.DeviceBuffer(B * H * T * C * 2)
+    lib.check(L.vdk_aff_combine(z2.ptr, C, 0, dcat.ptr + C * 2, 2 * C, 0, dcat.ptr, 2 * C, 0, B * H * T, C, 0, y.ptr,
+                                C, 0, None))
+    lib.check(L.vdk_synchronize())
+    gy = y.to_array(np.float16, (B, H, T, C)).astype(np.float64)
+    xv, dv, tv = cat[..., C:].astype(np.float64), cat[..., :C].astype(np.float64), gt.astype(np.float64)
+    want = xv * (1 + tv) + dv * (1 - tv)            # the module's form x*x_att + ds*(2 - x_att)
+    assert np.all(np.abs(gy - want) <= 2.0 ** -10 * np.abs(want) + 2e-3)
+
+
+def _split(a):
+    """f32 -> (hi, lo) f16 with hi + lo ~ a to ~2^-22."""
+    hi = a.astype(np.float16)
+    lo = (a - hi.astype(np.float32)).astype(np.float16)
+    return hi, lo
+
+
+def test_split_f16_conv_is_f32_accurate():
+    """Split-f16 convs (3x3 s1 with clamp, 1x1 s2 with split residual) match the
+    f64 brute force to ~1e-6 relative, where plain f16 is ~1e-3."""
+    rng = np.random.default_rng(104)
+    H, T, IC, OC = 20, 250, 64, 64
+    announce(f"eres split-f16 convs B={B} H={H} T={T}")
+    x = rng.standard_normal((B, H, T, IC)).astype(np.float32) * 3
+    xh, xl = _split(x)
+    xs = np.concatenate([xh, xl], axis=3)                       # [hi(IC) | lo(IC)] per pixel
+    dx = lib.DeviceBuffer.from_array(xs)
+    for K, stride in ((3, 1), (1, 2)):
+        w = (rng.standard_normal((OC, IC, K, K)) * np.sqrt(2.0 / (IC * K * K))).astype(np.float32)
+        b = rng.uniform(-0.5, 0.5, OC).astype(np.float32)
+        wh, wl = _split(w.transpose(0, 2, 3, 1))
+        wpack = np.concatenate([wh, wh, wl], axis=3)            # [OC][K][K][3*IC]
+        Ho, Wo = (H - 1) // stride + 1, (T - 1) // stride + 1
+        res = rng.standard_normal((B, Ho, Wo, OC)).astype(np.float32) * 4 if stride == 2 else None
+        dres = lib.DeviceBuffer.from_array(np.concatenate(_split(res), axis=3)) if res is not None else None
+        y = lib.DeviceBuffer(B * Ho * Wo * 2 * OC * 2)
+        d = lib.ConvDesc()
+        keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(wpack)), lib.DeviceBuffer.from_array(b)]
+        d.x, d.batch, d.H, d.W, d.IC, d.x_stride = dx.ptr, B, H, T, IC, 2 * IC
+        d.w, d.OC, d.KH, d.KW = keep[0].ptr, OC, K, K
+        d.stride_h = d.stride_w = stride
+        d.pad_h = d.pad_w = (K - 1) // 2
+        d.dil_h = d.dil_w = 1
+        d.bias = keep[1].ptr
+        if dres is not None:
+            d.residual, d.res_stride, d.res_lo = dres.ptr, 2 * OC, OC
+        d.act, d.clamp_hi = lib.ACT_RELU, 20.0
+        d.y, d.y_stride = y.ptr, 2 * OC
+        d.split, d.x_lo, d.y_lo = 1, IC, OC
+        d.tile = -1
+        lib.check(lib.lib().vdk_conv2d_ex(d, None))
+        lib.check(lib.lib().vdk_synchronize())
+        got = y.to_array(np.float16, (B, Ho, Wo, 2 * OC)).astype(np.float64)
+        got = got[..., :OC] + got[..., OC:]
+        for c in (0, B - 1):
+            ref = O.conv2d_g(x[c].transpose(2, 0, 1), w, sh=stride, sw=stride, ph=(K - 1) // 2, pw=(K - 1) // 2,
+                             bias=b, residual=None if res is None else res[c].transpose(2, 0, 1), f64=True)
+            ref = np.clip(ref, 0.0, 20.0)
+            err = np.abs(got[c].transpose(2, 0, 1) - ref).max() / np.abs(ref).max()
+            announce(f"split-f16 K={K} s={stride} clip {c}: max err / max {err:.2e}")
+            assert err <= 2e-6
+
+
+# ------------------------------------------------------------------ end to end
+
+@pytest.fixture(scope="module")
+def eres():
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "eres2net_q8_0.gguf")
+    synth.write_eres2net(path, seed=9)
+    g = gguf.GGUFFile(path)
+    assert sum(1 for v in g.tensors.values() if v[0] == gguf.GGML_Q8_0) > 40
+    ctx = lib.Context(path)
+    net = O.OracleEres2net(g)
+    yield path, ctx, net
+    ctx.close()
+
+
+def test_eres2net_batch16_matches_oracle(eres):
+    path, ctx, net = eres
+    pcm = synth.clips(9090, B, N20S)
+    announce("e2e eres2net B=16 20s capture")
+    cap = ctx.capture(pcm)
+    assert cap["pooled"].shape[1] == 2 * 512 * 10
+    for c in (0, B - 1):
+        feats = O.fbank(pcm[c])
+        assert np.abs(cap["feats"][c] - feats).max() <= 1e-4
+        emb, caps = net.forward(feats, capture=True)
+        rel = np.linalg.norm(cap["pooled"][c] - caps["pooled"]) / np.linalg.norm(caps["pooled"])
+        assert rel <= 2e-3, f"pooled rel-L2 {rel:.2e} clip {c}"
+        assert cosine(cap["pre_norm"][c], caps["pre_norm"]) >= 0.9999
+        cs = cosine(cap["emb"][c], emb)
+        announce(f"eres2net clip {c}: cosine {cs:.7f} pooled rel {rel:.2e}")
+        assert cs >= 0.9999
+    one = ctx.embed_batch(pcm[B - 1:B])
+    assert np.array_equal(one[0], cap["emb"][B - 1])
+
+
+@pytest.mark.parametrize("n", [400, 4000, 48000])
+def test_eres2net_embed_pcm_lengths(eres, n):
+    path, ctx, net = eres
+    announce(f"e2e eres2net B=1 n={n}")
+    pcm = synth.clip(300 + n, n)
+    got = ctx.embed_pcm(pcm)
+    ref = net.forward(O.fbank(pcm))
+    assert got.shape == (512,)
+    assert cosine(got, ref) >= 0.9999
+
+
+def test_eres2net_verify_matches_oracle(eres):
+    path, ctx, net = eres
+    announce("e2e eres2net verify")
+    a = synth.clip(21, 48000)
+    b = synth.clip(22, 40000)
+    d_gpu, _ = ctx.verify_pcm(a, b, 0.5)
+    ea, eb = net.forward(O.fbank(a)), net.forward(O.fbank(b))
+    d_ref = 1.0 - float(np.dot(ea.astype(np.float64), eb.astype(np.float64)))
+    assert abs(d_gpu - d_ref) <= 2e-3
+    for thr in (d_ref - 5e-3, d_ref + 5e-3):
+        assert ctx.verify_pcm(a, b, thr)[1] == (d_ref <= thr)

@@ -40,6 +40,8 @@ struct ConvArgs {
     int gate_seg, gate_nseg;   // output columns per gate segment, segments per clip
     int xs, ys, rs;            // elements between consecutive pixels of x / y / residual
     int bias_bs;               // elements between clips' bias vectors (0: one shared vector)
+    int split;                 // split-f16 tensors: value = hi + lo, lo at +x_lo / +r_lo / +y_lo elements;
+    int x_lo, r_lo, y_lo;      //   weights [OC][KH][KW][3*IC] = [hi | hi | lo] per tap
     int npix;                  // B * Ho * Wo
     int npix_in;               // B * H * W
 };
@@ -66,6 +68,11 @@ __device__ __forceinline__ void epilogue4(const ConvArgs& a, int P, int oc, cons
         const half4 r = *reinterpret_cast<const half4*>(a.res + (size_t)P * a.rs + oc);
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
+        if (a.split) {
+            const half4 rl = *reinterpret_cast<const half4*>(a.res + (size_t)P * a.rs + a.r_lo + oc);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] += (float)rl[e];
+        }
     }
     if (a.act == VDK_ACT_RELU) {
 #pragma unroll
@@ -103,6 +110,12 @@ __device__ __forceinline__ void epilogue4(const ConvArgs& a, int P, int oc, cons
 #pragma unroll
         for (int e = 0; e < 4; ++e) h[e] = (half_t)v[e];
         *reinterpret_cast<half4*>(static_cast<half_t*>(a.y) + o) = h;
+        if (a.split) {
+            half4 l;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) l[e] = (half_t)(v[e] - (float)h[e]);
+            *reinterpret_cast<half4*>(static_cast<half_t*>(a.y) + o + a.y_lo) = l;
+        }
     }
 }
 
@@ -315,13 +328,15 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     const int oc0 = blockIdx.y * BM;
     const int HoWo = a.Ho * a.Wo;
     const int KHW = a.KH * a.KW;
-    const int nc = a.IC / KC;
+    // Split-f16: per tap the K range runs over [x_hi . w_hi | x_lo . w_hi | x_hi . w_lo].
+    const int ICW = a.split ? 3 * a.IC : a.IC;
+    const int nc = ICW / KC;
     const int nk = KHW * nc;
 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
+        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC + (a.split ? a.x_lo : 0)) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)a.w, 0, (int)((size_t)a.OC * KHW * a.IC * 2), 0x00020000);
+        (void*)a.w, 0, (int)((size_t)a.OC * KHW * ICW * 2), 0x00020000);
 
     // Per DMA slot of this lane: weight rows keep a fixed voffset (the tap /
     // chunk part is uniform); pixel rows keep the tap-0 offset and a mask of
@@ -342,7 +357,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
         if (ins >= NINS) {
             s_off[j] = 0;   // padding instruction: zeros into the spare slots
         } else if (s_is_w[j]) {
-            s_off[j] = ((oc0 + r) * KHW * a.IC + c * 8) * 2;
+            s_off[j] = ((oc0 + r) * KHW * ICW + c * 8) * 2;
         } else {
             const int P = p0 + (r - BM);
             s_off[j] = 0;   // rows past the end: mask 0, every tap reads zeros
@@ -360,33 +375,39 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
         }
     }
 
-    // Chunk cursor for the DMA side: tap (kh, kw) and channel offset c0,
-    // advanced incrementally (no divisions in the loop).
-    int f_tap = 0, f_kw = 0, f_c0 = 0, f_x = 0;   // f_x = byte offset of (kh, kw, c0) in the input
+    // Chunk cursor for the DMA side: tap (kh, kw) and logical channel offset
+    // c0 in [0, ICW), advanced incrementally (no divisions in the loop).
+    // f_x = byte offset of tap (kh, kw) in the input, f_xc = of the channel chunk.
+    int f_tap = 0, f_kw = 0, f_c0 = 0, f_x = 0, f_xc = 0;
     const int tap_bytes = a.dw * a.xs * 2;                       // next kw
     const int row_bytes = a.dh * a.W * a.xs * 2 - a.KW * tap_bytes;   // next kh, back to kw = 0
     auto issue = [&](int st) {
-        const int w_soff = (f_tap * a.IC + f_c0) * 2;
+        const int w_soff = (f_tap * ICW + f_c0) * 2;
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
             lds_void* dst = (lds_void*)(smem + st * STAGE + (wave + j * NW) * 1024);
             if (s_is_w[j]) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, dst, 16, (uint32_t)s_off[j], w_soff, 0, 0);
             } else {
-                const uint32_t off = ((s_mask[j] >> f_tap) & 1u) ? (uint32_t)(s_off[j] + f_x) : kOOB;
+                const uint32_t off = ((s_mask[j] >> f_tap) & 1u) ? (uint32_t)(s_off[j] + f_x + f_xc) : kOOB;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, off, 0, 0, 0);
             }
         }
         f_c0 += KC;
-        f_x += KC * 2;
-        if (f_c0 == a.IC) {
+        f_xc += KC * 2;
+        if (f_c0 == ICW) {
             f_c0 = 0;
-            f_x += tap_bytes - a.IC * 2;
+            f_xc = 0;
+            f_x += tap_bytes;
             ++f_tap;
             if (++f_kw == a.KW) {
                 f_kw = 0;
                 f_x += row_bytes;              // next kernel row
             }
+        } else if (a.split && f_c0 == a.IC) {
+            f_xc = a.x_lo * 2;                 // lo plane (with the hi weights)
+        } else if (a.split && f_c0 == 2 * a.IC) {
+            f_xc = 0;                          // hi plane again (with the lo weights)
         }
     };
 
@@ -647,8 +668,12 @@ bool is_s1_3x3(const ConvArgs& a) {
     return a.KH == 3 && a.KW == 3 && a.sh == 1 && a.sw == 1 && a.ph == 1 && a.pw == 1 && a.dh == 1 && a.dw == 1;
 }
 
+constexpr int kFirstDma = 14, kFirstHalo = 26;
+
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
+    const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
+    if (a.split && (idx < kFirstDma || idx >= kFirstHalo)) return false;   // split-f16: DMA kernel only
     return a.IC % t.kc == 0;
 }
 
@@ -670,9 +695,10 @@ int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
-    if (is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return a.OC <= 32 ? 28 : 30;
+    if (!a.split && is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return a.OC <= 32 ? 28 : 30;
     if (a.IC % 64 == 0) return bm == 128 ? 18 : (bm == 64 ? 15 : 14);
     if (a.IC % 32 == 0) return bm >= 64 ? 16 : 14;
+    if (a.split) return -1;
     if (a.IC % 16 == 0) return bm == 128 ? 13 : (bm == 64 ? 12 : 11);
     return -1;
 }
@@ -680,7 +706,7 @@ int pick_tile(const ConvArgs& a) {
 template <int OC>
 __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restrict__ feats, int B, int H, int W,
                                                            const float* __restrict__ w,
-                                                           const float* __restrict__ bias, int relu,
+                                                           const float* __restrict__ bias, int relu, int split,
                                                            half_t* __restrict__ y) {
     // OC/8 threads per output pixel, 8 channels each: the OC/8 lanes of a pixel
     // write its OC*2 bytes as consecutive 16-byte chunks.
@@ -705,7 +731,7 @@ __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restri
             const int ih = h - 1 + kh, iw = t - 1 + kw;
             xv[kh * 3 + kw] = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? feats[((long)b * H + ih) * W + iw] : 0.0f;
         }
-    half8 hv;
+    half8 hv, lv;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int oc = g * 8 + e;
@@ -715,8 +741,14 @@ __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restri
         float v = acc + sb[oc];
         if (relu) v = v > 0.0f ? v : 0.0f;
         hv[e] = (half_t)v;
+        lv[e] = (half_t)(v - (float)hv[e]);
     }
-    *reinterpret_cast<half8*>(y + P * OC + g * 8) = hv;
+    if (split) {   // [hi(OC) | lo(OC)] per pixel
+        *reinterpret_cast<half8*>(y + P * 2 * OC + g * 8) = hv;
+        *reinterpret_cast<half8*>(y + P * 2 * OC + OC + g * 8) = lv;
+    } else {
+        *reinterpret_cast<half8*>(y + P * OC + g * 8) = hv;
+    }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -746,7 +778,8 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(xs >= d.IC && ys >= d.OC && rs >= d.OC, "conv2d: pixel stride smaller than the channel count");
         require(xs % 8 == 0 && ys % 8 == 0 && rs % 8 == 0, "conv2d: pixel strides must be multiples of 8");
         require((long)d.batch * Ho * Wo < (1L << 31) && (long)d.batch * d.H * d.W * xs < (1L << 30) &&
-                    (long)d.batch * Ho * Wo * ys < (1L << 31),
+                    (long)d.batch * Ho * Wo * ys < (1L << 31) &&
+                    (long)d.OC * d.KH * d.KW * d.IC * (d.split ? 3 : 1) < (1L << 30),
                 "conv2d: too many pixels for one launch");
         require(aligned16(d.x) && aligned16(d.w) && aligned16(d.y) && (!d.residual || aligned16(d.residual)),
                 "conv2d: device pointers must be 16-byte aligned");
@@ -754,6 +787,10 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(!d.gate || (d.gate_seg > 0 && d.gate_nseg > 0 && (Wo + d.gate_seg - 1) / d.gate_seg <= d.gate_nseg),
                 "conv2d: gate needs gate_seg > 0 and enough segments for the output width");
         require(!d.y_time_major || !d.residual, "conv2d: a time-major store takes no residual");
+        require(!d.split || (!d.y_f32 && !d.y_time_major && d.x_lo >= d.IC && d.y_lo >= d.OC &&
+                             (!d.residual || d.res_lo >= d.OC) && d.x_lo % 8 == 0 && d.y_lo % 8 == 0 &&
+                             d.res_lo % 8 == 0 && d.IC % 32 == 0),
+                "conv2d: split-f16 needs IC % 32 == 0, f16 output and lo offsets past the channels");
         ConvArgs a{};
         a.x = static_cast<const half_t*>(d.x);
         a.w = static_cast<const half_t*>(d.w);
@@ -776,6 +813,8 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         a.y_tr = d.y_time_major ? 1 : 0;
         a.xs = xs; a.ys = ys; a.rs = rs;
         a.bias_bs = d.bias_batch_stride;
+        a.split = d.split ? 1 : 0;
+        a.x_lo = d.x_lo; a.r_lo = d.res_lo; a.y_lo = d.y_lo;
         a.npix = d.batch * Ho * Wo;
         a.npix_in = d.batch * d.H * d.W;
         hipStream_t s = static_cast<hipStream_t>(stream);
@@ -807,6 +846,7 @@ vdk_conv_desc plain_desc(const void* d_x, int batch, int H, int W, int IC, const
 
 ConvArgs shape_args(const vdk_conv_desc& d) {
     ConvArgs a{};
+    a.split = d.split ? 1 : 0;
     a.IC = d.IC; a.OC = d.OC; a.KH = d.KH; a.KW = d.KW;
     a.sh = d.stride_h ? d.stride_h : 1; a.sw = d.stride_w ? d.stride_w : 1;
     a.ph = d.pad_h; a.pw = d.pad_w;
@@ -852,9 +892,8 @@ extern "C" int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* d) {
     return tile_fits(kTiles[tile], shape_args(*d)) ? 1 : 0;
 }
 
-extern "C" int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,
-                                const float* d_w, const float* d_bias, int OC, int relu,
-                                void* d_y, void* stream) {
+extern "C" int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W, const float* d_w,
+                                   const float* d_bias, int OC, int relu, int split, void* d_y, void* stream) {
     return guarded([&] {
         require(d_feats && d_w && d_bias && d_y, "stem: NULL device pointer");
         require(batch > 0 && H > 0 && W > 0, "stem: empty input");
@@ -865,12 +904,18 @@ extern "C" int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,
         require(n < (1L << 31), "stem: too many pixels for one launch");
         dim3 grid(cdiv(n, 256));
         half_t* y = static_cast<half_t*>(d_y);
+        const int sp = split ? 1 : 0;
         switch (OC) {
-            case 16: hipLaunchKernelGGL(stem_conv3x3_kernel<16>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y); break;
-            case 32: hipLaunchKernelGGL(stem_conv3x3_kernel<32>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y); break;
-            case 64: hipLaunchKernelGGL(stem_conv3x3_kernel<64>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y); break;
+            case 16: hipLaunchKernelGGL(stem_conv3x3_kernel<16>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
+            case 32: hipLaunchKernelGGL(stem_conv3x3_kernel<32>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
+            case 64: hipLaunchKernelGGL(stem_conv3x3_kernel<64>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
             default: throw Error("stem: OC must be 16, 32 or 64");
         }
         VDK_HIP(hipGetLastError());
     });
+}
+
+extern "C" int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W, const float* d_w, const float* d_bias,
+                                int OC, int relu, void* d_y, void* stream) {
+    return vdk_stem_conv3x3_ex(d_feats, batch, H, W, d_w, d_bias, OC, relu, 0, d_y, stream);
 }

@@ -19,22 +19,27 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 }
 
 // TSTP (src/encoder_resnet.cpp:140-157): mean over time, var * N/(N-1), sqrt(var + eps).
-__global__ __launch_bounds__(256) void tstp_kernel(const half_t* __restrict__ x, int H, int W, int C, float eps,
-                                                   float* __restrict__ pooled) {
+// x [B][H][W][xs] f16; split (x_lo > 0): value = x + x[.. + x_lo].
+__device__ __forceinline__ float tstp_val(const half_t* p, int x_lo) {
+    return x_lo ? (float)p[0] + (float)p[x_lo] : (float)p[0];
+}
+
+__global__ __launch_bounds__(256) void tstp_kernel(const half_t* __restrict__ x, int xs, int x_lo, int H, int W,
+                                                   int C, float eps, float* __restrict__ pooled) {
 #pragma clang fp contract(off)
     const int h = blockIdx.x, b = blockIdx.y;
     const size_t CH = (size_t)C * H;
     float* out = pooled + (size_t)b * 2 * CH;
-    const half_t* row = x + ((size_t)b * H + h) * W * C;
+    const half_t* row = x + ((size_t)b * H + h) * W * xs;
     for (int c = threadIdx.x; c < C; c += blockDim.x) {
         double s = 0.0;
 #pragma unroll 8
-        for (int t = 0; t < W; ++t) s += (double)(float)row[(size_t)t * C + c];
+        for (int t = 0; t < W; ++t) s += (double)tstp_val(row + (size_t)t * xs + c, x_lo);
         const float mean = (float)(s / W);
         double s2 = 0.0;
 #pragma unroll 8
         for (int t = 0; t < W; ++t) {
-            const float d = (float)row[(size_t)t * C + c] - mean;
+            const float d = tstp_val(row + (size_t)t * xs + c, x_lo) - mean;
             s2 += (double)(d * d);
         }
         float var = (float)(s2 / W);
@@ -123,15 +128,22 @@ __global__ __launch_bounds__(64) void l2norm_kernel(float* __restrict__ x, int d
 
 using namespace vdk;
 
-extern "C" int vdk_tstp(const void* d_x, int batch, int H, int W, int C, float eps, float* d_pooled,
-                        void* stream) {
+extern "C" int vdk_tstp_ex(const void* d_x, int x_stride, int x_lo, int batch, int H, int W, int C, float eps,
+                           float* d_pooled, void* stream) {
     return guarded([&] {
         require(d_x && d_pooled, "tstp: NULL device pointer");
         require(batch > 0 && H > 0 && W > 0 && C > 0, "tstp: empty input");
+        const int xs = x_stride ? x_stride : C;
+        require(xs >= C && (x_lo == 0 || (x_lo >= C && x_lo + C <= xs)), "tstp: bad pixel stride / lo offset");
         hipLaunchKernelGGL(tstp_kernel, dim3(H, batch), dim3(256), 0, static_cast<hipStream_t>(stream),
-                           static_cast<const half_t*>(d_x), H, W, C, eps, d_pooled);
+                           static_cast<const half_t*>(d_x), xs, x_lo, H, W, C, eps, d_pooled);
         VDK_HIP(hipGetLastError());
     });
+}
+
+extern "C" int vdk_tstp(const void* d_x, int batch, int H, int W, int C, float eps, float* d_pooled,
+                        void* stream) {
+    return vdk_tstp_ex(d_x, 0, 0, batch, H, W, C, eps, d_pooled, stream);
 }
 
 extern "C" size_t vdk_linear_workspace_size(int batch, int in_dim, int out_dim) {

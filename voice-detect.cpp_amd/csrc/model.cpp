@@ -55,6 +55,20 @@ std::unique_ptr<Model> Model::load(const std::string& path) {
         r.mean_vec = g.str(p + "mean_vec");
         r.var_eps = g.f32(p + "var_eps", 1e-8f);
     }
+    if (c.arch == "eres2net") {
+        ERes2NetCfg& e = c.eres2net;   // src/model_loader.cpp:151-163
+        const std::string p = "voicedetect.eres2net.";
+        e.conv_weight = g.str_arr(p + "conv_weight");
+        e.conv_bias = g.str_arr(p + "conv_bias");
+        e.conv_stride = g.i32_arr(p + "conv_stride");
+        e.num_blocks = g.i32_arr(p + "num_blocks");
+        e.m_channels = (int)g.u32(p + "m_channels", 0);
+        e.scale = (int)g.u32(p + "scale", 2);
+        e.seg_weight = g.str(p + "seg_weight");
+        e.seg_bias = g.str(p + "seg_bias");
+        e.relu_clamp = g.f32(p + "relu_clamp", 20.0f);
+        e.var_eps = g.f32(p + "var_eps", 1e-8f);
+    }
     if (c.arch == "campplus") {
         CamPPlusCfg& cp = c.campplus;   // src/model_loader.cpp:165-173
         const std::string p = "voicedetect.campplus.";
@@ -91,12 +105,8 @@ void Model::ensure_device() {
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) throw Error("voicedetect: no HIP device available");
     VDK_HIP(hipGetDevice(&device_));
     const bool resnet = cfg_.arch == "wespeaker_resnet34", ecapa = cfg_.arch == "ecapa_tdnn";
-    const bool campp = cfg_.arch == "campplus";
-    if (!resnet && !ecapa && !campp) {
-        if (cfg_.arch == "eres2net")
-            throw Error("voicedetect: arch '" + cfg_.arch + "' is not implemented by this build yet");
-        throw Error("voicedetect: unsupported arch '" + cfg_.arch + "'");
-    }
+    const bool campp = cfg_.arch == "campplus", eres = cfg_.arch == "eres2net";
+    if (!resnet && !ecapa && !campp && !eres) throw Error("voicedetect: unsupported arch '" + cfg_.arch + "'");
     if (!stream_) VDK_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     const size_t tb = vdk_fbank_tables_size(&cfg_.fbank);
     if (tb == 0) throw Error(vdk_last_error());
@@ -104,7 +114,8 @@ void Model::ensure_device() {
     check(vdk_fbank_tables_fill(&cfg_.fbank, fb_tables_));
     if (resnet) upload_resnet();
     else if (ecapa) upload_ecapa();
-    else upload_campplus();
+    else if (campp) upload_campplus();
+    else upload_eres2net();
     ready_ = true;
 }
 
@@ -215,6 +226,7 @@ void Model::ensure_workspace(int batch, int n_samples) {
     w.emb = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * cfg_.embedding_dim));
     if (cfg_.arch == "ecapa_tdnn") alloc_ecapa_workspace(batch, T);
     else if (cfg_.arch == "campplus") alloc_campplus_workspace(batch, T);
+    else if (cfg_.arch == "eres2net") alloc_eres2net_workspace(batch, T);
     else alloc_resnet_workspace(batch, T);
 }
 
@@ -277,6 +289,7 @@ void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) 
     prof_end();
     if (cfg_.arch == "ecapa_tdnn") encode_ecapa(batch, T);
     else if (cfg_.arch == "campplus") encode_campplus(batch, T);
+    else if (cfg_.arch == "eres2net") encode_eres2net(batch, T);
     else encode_resnet(batch, T);
     const int E = cfg_.embedding_dim;
     VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));

@@ -35,6 +35,15 @@ struct CamPPlusCfg {
     float bn_eps = 1e-5f;
 };
 
+// src/model_loader.hpp:68-79
+struct ERes2NetCfg {
+    std::vector<std::string> conv_weight, conv_bias;
+    std::vector<int32_t> conv_stride, num_blocks;
+    int m_channels = 0, scale = 2;
+    std::string seg_weight, seg_bias;
+    float relu_clamp = 20.0f, var_eps = 1e-8f;
+};
+
 struct ModelConfig {
     std::string arch;
     int embedding_dim = 0;
@@ -43,6 +52,7 @@ struct ModelConfig {
     vdk_fbank_cfg fbank{};
     ResNetCfg resnet;
     CamPPlusCfg campplus;
+    ERes2NetCfg eres2net;
 };
 
 // Throws vdk::Error with vdk_last_error() when a vdk_* call returned nonzero.
@@ -153,6 +163,33 @@ private:
         float* dense_w = nullptr;   // head with the affine-free BN folded, f32 [E][2*c_out]
         float* dense_b = nullptr;
     };
+    // ERes2Net (src/encoder_eres2net.cpp).  A block's conv1 output and its two
+    // chunk outputs share one [.. 4w] buffer laid out [chunk0 | chunk1 | sp0 | sp1]
+    // so that every concatenation the block needs is a contiguous channel slice.
+    struct EresAff { Layer c1, c2; };   // local_att: 1x1 -> SiLU -> 1x1 -> tanh
+    struct EresBlock {
+        Layer conv1;      // 1x1, block stride, -> 2w, clamp
+        Layer conv_a;     // chunk 0: 3x3 over [chunk0 (| chunk1 with zero weights when w % 32 != 0)]
+        Layer conv_b;     // chunk 1: 3x3 over [chunk1 | sp0] with weights [W | W] (sum folded into the GEMM),
+                          // or over the AFF output (diff_AFF blocks)
+        bool aff = false;
+        EresAff fuse;     // AFF(sp0, chunk1); conv1 input order [chunk1 | sp0]
+        Layer conv3;      // 1x1 over [sp0 | sp1] -> 2*planes (+ residual, clamp)
+        bool has_sc = false;
+        Layer sc;         // 1x1 shortcut, block stride
+        int stride = 1, width = 0, planes = 0, in_c = 0;
+    };
+    struct Eres2net {
+        int m = 0, n_mels = 0, c_out = 0, h_out = 0;
+        float clamp = 20.0f, eps = 1e-8f;
+        float* stem_w = nullptr;   // f32 [m][9]
+        float* stem_b = nullptr;
+        std::vector<EresBlock> layers[4];
+        Layer down[3];             // cross-stage 3x3 stride-2 downsamples (no bias)
+        EresAff cross[3];          // cross-stage AFF(layer output, downsample)
+        float* seg_w = nullptr;    // f32 [E][2*c_out*h_out]
+        float* seg_b = nullptr;
+    };
     struct Workspace {
         int batch = 0, n_samples = 0;
         std::vector<void*> allocs;      // every allocation below, freed together
@@ -176,16 +213,22 @@ private:
         void* dense[3] = {nullptr, nullptr, nullptr};
         void *abuf = nullptr, *cc = nullptr, *fin = nullptr;
         float *sums = nullptr, *gate = nullptr;
+        // ERes2Net
+        void *ex[2] = {nullptr, nullptr}, *es4 = nullptr, *esc = nullptr, *ez = nullptr, *ez2 = nullptr,
+             *ef = nullptr;
+        void *ecat[3] = {nullptr, nullptr, nullptr}, *efuse[3] = {nullptr, nullptr, nullptr};
     };
 
     void ensure_device();
     void upload_resnet();
     void upload_ecapa();
     void upload_campplus();
+    void upload_eres2net();
     void ensure_workspace(int batch, int n_samples);
     void alloc_resnet_workspace(int batch, int T);
     void alloc_ecapa_workspace(int batch, int T);
     void alloc_campplus_workspace(int batch, int T);
+    void alloc_eres2net_workspace(int batch, int T);
     void* ws_alloc(size_t bytes);
     void free_workspace();
     // The whole forward for device PCM into device embeddings (pre-norm copy in ws_.pre).
@@ -194,6 +237,7 @@ private:
     void encode_resnet(int batch, int T);
     void encode_ecapa(int batch, int T);
     void encode_campplus(int batch, int T);
+    void encode_eres2net(int batch, int T);
     // One vdk_conv2d_ex launch with profiling (flops from the descriptor's shape).
     void conv_ex(const char* name, const vdk_conv_desc& d);
     void conv(const Conv& c, const void* x, int batch, int H, int W, const void* res, int relu, void* y);
@@ -222,6 +266,7 @@ private:
     std::vector<Block> blocks_;
     Ecapa ecapa_;
     Campplus campp_;
+    Eres2net eres_;
     float* seg_w_ = nullptr;
     float* seg_b_ = nullptr;
     float* mean_vec_ = nullptr;

@@ -1,0 +1,312 @@
+// model_eres2net.cpp - the ERes2Net encoder of vdk::Model (src/encoder_eres2net.cpp:139-265).
+//
+// Precision: with random-init weights this network amplifies f16 rounding of
+// activations or weights about a hundredfold (pooled statistics move by ~4%
+// under either alone), so it runs in split-f16: every activation is stored as
+// hi + lo f16 halves, weights as [hi | hi | lo], and each conv computes
+// x_hi.w_hi + x_lo.w_hi + x_hi.w_lo on f16 MFMA with f32 accumulation
+// (~2^-21 relative per value; 3x the MFMA work and 2x the activation bytes).
+//
+// Device layout: NHWC, every tensor [B][freq][T][hi(C) | lo(C)]; a channel
+// slice of a tensor is (base + c, pixel stride 2C, lo offset C).  Every conv
+// is one implicit-GEMM launch with bias, residual and the Hardtanh(0, 20)
+// clamp in its epilogue.  Per Res2Net block (width w, scale 2) one tensor holds
+//   [chunk0 | chunk1 | sp0 | sp1]      (4w channels)
+// so that: conv1 writes [chunk0 | chunk1]; the chunk-0 3x3 conv reads chunk0
+// (or [chunk0 | chunk1] with zero weights on chunk1 when w is not a multiple
+// of 32) and writes sp0; the chunk-1 input sp0 + chunk1 is folded into the
+// GEMM by reading [chunk1 | sp0] with the weights duplicated; in the diff_AFF
+// blocks AFF(sp0, chunk1) reads [chunk1 | sp0] with its first conv's input
+// channels swapped; conv3 reads [sp0 | sp1].  A layer's last block writes the
+// first half of a 2C-channel tensor whose second half receives the
+// cross-stage downsample, so the cross-stage AFF reads its concatenation in
+// place.  Weights: split f16 [OC][KH][KW][3*IC] (Q8_0 / F32 dequantised at
+// load); seg_1 f32.
+#include <algorithm>
+#include <cmath>
+#include <string>
+
+#include "arena.hpp"
+#include "common.hpp"
+#include "model.hpp"
+#include "weights.hpp"
+
+namespace vdk {
+
+namespace {
+
+// A channel slice of a split-f16 tensor.
+struct View {
+    void* p;
+    int stride, lo;   // elements between pixels / from hi to lo
+    View at(int ch) const { return {static_cast<uint8_t*>(p) + 2 * (size_t)ch, stride, lo}; }
+};
+
+View split_tensor(void* p, int channels) { return {p, 2 * channels, channels}; }
+
+}  // namespace
+
+void Model::upload_eres2net() {
+    const GgufFile& g = *gguf_;
+    const ERes2NetCfg& ec = cfg_.eres2net;
+    Eres2net& m = eres_;
+    ArenaBuilder arena;
+    const size_t nconv = ec.conv_weight.size();
+    require(nconv > 0 && ec.conv_bias.size() == nconv && ec.conv_stride.size() == nconv,
+            "voicedetect: eres2net conv manifests differ in length");
+    require(ec.num_blocks.size() == 4, "voicedetect: eres2net needs 4 layers");
+    require(ec.scale == 2, "voicedetect: eres2net Res2Net scale must be 2");
+    m.m = ec.m_channels;
+    m.n_mels = cfg_.fbank.n_mels;
+    m.clamp = ec.relu_clamp;
+    m.eps = ec.var_eps;
+    size_t ci = 0;
+    auto next = [&](int ic_expect, int k_expect, int stride_expect) {
+        require(ci < nconv, "voicedetect: eres2net manifest has too few convs");
+        const size_t idx = ci++;
+        HostConv c = read_conv(g, ec.conv_weight[idx]);
+        require(c.ic == ic_expect && c.kh == k_expect && c.kw == k_expect,
+                "voicedetect: '" + ec.conv_weight[idx] + "' has an unexpected shape");
+        require(ec.conv_stride[idx] == stride_expect,
+                "voicedetect: '" + ec.conv_weight[idx] + "' has an unexpected stride");
+        return std::make_pair(c, idx);
+    };
+    // split weights; oc_pad > oc adds zero output rows (and zero bias)
+    auto put = [&](const HostConv& c, size_t idx, int icp, Layer& l, const std::function<int(int)>& map = nullptr,
+                   int oc_pad = 0) {
+        require(c.oc % 8 == 0, "voicedetect: eres2net conv widths must be multiples of 8");
+        const int ocp = std::max(c.oc, oc_pad);
+        l.ic = icp; l.oc = ocp; l.kh = c.kh; l.k = c.kw;
+        arena.put(pack_conv_f16_split(c, icp, ocp, map), &l.w);
+        if (!ec.conv_bias[idx].empty()) {
+            std::vector<float> b = g.to_f32(ec.conv_bias[idx]);
+            require(b.size() == (size_t)c.oc, "voicedetect: '" + ec.conv_bias[idx] + "' has the wrong size");
+            b.resize(ocp, 0.0f);
+            arena.put(b, &l.b);
+        } else {
+            l.b = nullptr;
+        }
+    };
+    // AFF local_att over cat(x, ds); swap = the tensor holds [ds | x].  The
+    // bottleneck is padded to a multiple of 32 channels (zero rows / columns)
+    // so that both convs run on the split-f16 DMA kernel.
+    auto aff = [&](int C, bool swap, EresAff& a) {
+        auto p1 = next(2 * C, 1, 1);
+        const int zc = (p1.first.oc + 31) / 32 * 32;
+        put(p1.first, p1.second, 2 * C, a.c1,
+            swap ? std::function<int(int)>([C](int i) { return i < C ? i + C : i - C; }) : nullptr, zc);
+        auto p2 = next(p1.first.oc, 1, 1);
+        require(p2.first.oc == C, "voicedetect: eres2net AFF must return its channel count");
+        put(p2.first, p2.second, zc, a.c2);
+    };
+
+    {   // stem: 1 -> m, 3x3, f32 for the single-channel kernel
+        auto st = next(1, 3, 1);
+        require(st.first.oc == m.m, "voicedetect: eres2net stem width differs from m_channels");
+        require(m.m == 16 || m.m == 32 || m.m == 64, "voicedetect: eres2net m_channels must be 16, 32 or 64");
+        require(!ec.conv_bias[st.second].empty(), "voicedetect: eres2net stem needs its folded bias");
+        arena.put(st.first.w, &m.stem_w);
+        arena.put(g.to_f32(ec.conv_bias[st.second]), &m.stem_b);
+    }
+    int in_planes = m.m, H = m.n_mels;
+    for (int li = 0; li < 4; ++li) {
+        const int planes = m.m << li;
+        const int stride = li == 0 ? 1 : 2;
+        m.layers[li].assign(ec.num_blocks[li], EresBlock());
+        for (int bi = 0; bi < ec.num_blocks[li]; ++bi) {
+            EresBlock& b = m.layers[li][bi];
+            b.stride = bi == 0 ? stride : 1;
+            b.planes = planes;
+            b.in_c = in_planes;
+            b.aff = li >= 2;
+            auto c1 = next(in_planes, 1, b.stride);
+            put(c1.first, c1.second, in_planes, b.conv1);
+            const int w = c1.first.oc / 2;
+            b.width = w;
+            require(w % 8 == 0, "voicedetect: eres2net chunk width must be a multiple of 8");
+            // chunk 0: [chunk0 (| chunk1 zero-weighted)]
+            auto ca = next(w, 3, 1);
+            put(ca.first, ca.second, w % 32 == 0 ? w : 2 * w, b.conv_a);
+            if (b.aff) {
+                aff(w, true, b.fuse);
+                auto cb = next(w, 3, 1);
+                put(cb.first, cb.second, w, b.conv_b);
+            } else {
+                // [chunk1 | sp0] with the weights on both halves: conv(sp0 + chunk1)
+                auto cb = next(w, 3, 1);
+                HostConv dup = cb.first;
+                dup.ic = 2 * w;
+                dup.w.assign((size_t)dup.oc * 2 * w * 9, 0.0f);
+                for (int o = 0; o < dup.oc; ++o)
+                    for (int half = 0; half < 2; ++half)
+                        std::copy(cb.first.w.begin() + (size_t)o * w * 9, cb.first.w.begin() + (size_t)(o + 1) * w * 9,
+                                  dup.w.begin() + ((size_t)o * 2 * w + (size_t)half * w) * 9);
+                put(dup, cb.second, 2 * w, b.conv_b);
+            }
+            auto c3 = next(2 * w, 1, 1);
+            require(c3.first.oc == 2 * planes, "voicedetect: eres2net conv3 must produce 2*planes channels");
+            put(c3.first, c3.second, 2 * w, b.conv3);
+            b.has_sc = b.stride != 1 || in_planes != 2 * planes;
+            if (b.has_sc) {
+                auto sc = next(in_planes, 1, b.stride);
+                require(sc.first.oc == 2 * planes, "voicedetect: eres2net shortcut width differs");
+                put(sc.first, sc.second, in_planes, b.sc);
+            }
+            in_planes = 2 * planes;
+        }
+        if (li > 0) H = (H - 1) / 2 + 1;
+        if (li >= 1) {
+            // cross-stage: downsample of the previous fused feature (3x3 s2, no bias), then AFF
+            auto dn = next(planes, 3, 2);
+            require(dn.first.oc == 2 * planes && ec.conv_bias[dn.second].empty(),
+                    "voicedetect: eres2net cross-stage downsample must be a bias-free 3x3 to 2*planes");
+            put(dn.first, dn.second, planes, m.down[li - 1]);
+            aff(2 * planes, false, m.cross[li - 1]);
+        }
+    }
+    require(ci == nconv, "voicedetect: eres2net manifest has unused convs");
+    m.c_out = in_planes;
+    m.h_out = H;
+    pooled_dim_ = 2 * m.c_out * m.h_out;
+    {
+        std::vector<float> sw = g.to_f32(ec.seg_weight);
+        require(sw.size() == (size_t)cfg_.embedding_dim * pooled_dim_,
+                "voicedetect: eres2net seg_1 must be [embedding_dim, 2*C*H']");
+        arena.put(sw, &m.seg_w);
+        std::vector<float> sb = g.to_f32(ec.seg_bias);
+        require(sb.size() == (size_t)cfg_.embedding_dim, "voicedetect: eres2net seg_1 bias has the wrong size");
+        arena.put(sb, &m.seg_b);
+    }
+    arena_ = arena.upload();
+}
+
+void Model::alloc_eres2net_workspace(int batch, int T) {
+    const Eres2net& m = eres_;
+    Workspace& w = ws_;
+    size_t x_max = 0, s4_max = 0, z_max = 0, f_max = 0;   // channels x pixels (one half)
+    int H = m.n_mels, W = T;
+    for (int li = 0; li < 4; ++li) {
+        if (li > 0) { H = (H - 1) / 2 + 1; W = (W - 1) / 2 + 1; }
+        const size_t pix = (size_t)batch * H * W;
+        x_max = std::max(x_max, pix * m.m);   // stem output
+        for (const EresBlock& b : m.layers[li]) {
+            x_max = std::max(x_max, pix * 2 * b.planes);
+            s4_max = std::max(s4_max, pix * 4 * b.width);
+            if (b.aff) {
+                z_max = std::max(z_max, pix * std::max(b.fuse.c1.oc, b.fuse.c2.oc));
+                f_max = std::max(f_max, pix * b.width);
+            }
+        }
+        if (li >= 1) {
+            const int C = 2 * (m.m << li);
+            w.ecat[li - 1] = ws_alloc(2 * 2 * pix * 2 * C);
+            w.efuse[li - 1] = ws_alloc(2 * 2 * pix * C);
+            z_max = std::max(z_max, pix * std::max(m.cross[li - 1].c1.oc, m.cross[li - 1].c2.oc));
+        }
+    }
+    // split-f16: two f16 halves per value
+    w.ex[0] = ws_alloc(4 * x_max);
+    w.ex[1] = ws_alloc(4 * x_max);
+    w.esc = ws_alloc(4 * x_max);
+    w.es4 = ws_alloc(4 * s4_max);
+    w.ez = ws_alloc(4 * std::max<size_t>(z_max, 8));
+    w.ez2 = ws_alloc(4 * std::max<size_t>(z_max, 8));
+    w.ef = ws_alloc(4 * std::max<size_t>(f_max, 8));
+    w.fc_work_bytes = vdk_linear_workspace_size(batch, pooled_dim_, cfg_.embedding_dim);
+    w.fc_work = ws_alloc(w.fc_work_bytes);
+}
+
+void Model::encode_eres2net(int batch, int T) {
+    const Eres2net& m = eres_;
+    Workspace& w = ws_;
+    auto conv = [&](const char* name, const Layer& l, View x, int H, int W, int stride, const View* res, int act,
+                    float clamp, int tanh_after, View y) {
+        vdk_conv_desc d{};
+        d.x = x.p; d.batch = batch; d.H = H; d.W = W; d.IC = l.ic; d.x_stride = x.stride;
+        d.w = l.w; d.OC = l.oc; d.KH = l.kh; d.KW = l.k;
+        d.stride_h = d.stride_w = stride;
+        d.pad_h = (l.kh - 1) / 2; d.pad_w = (l.k - 1) / 2;
+        d.bias = l.b;
+        if (res) { d.residual = res->p; d.res_stride = res->stride; d.res_lo = res->lo; }
+        d.act = act; d.clamp_hi = clamp; d.tanh_after = tanh_after;
+        d.y = y.p; d.y_stride = y.stride;
+        d.split = 1; d.x_lo = x.lo; d.y_lo = y.lo;
+        d.tile = -1;
+        conv_ex(name, d);
+    };
+    // AFF(x, ds): local_att over the [.. 2C] input `cat`, then the combine into y
+    auto aff = [&](const char* name, const EresAff& a, View cat, View x, View ds, int C, int H, int W, View y) {
+        const View z = split_tensor(w.ez, a.c1.oc), z2 = split_tensor(w.ez2, C);
+        conv(name, a.c1, cat, H, W, 1, nullptr, VDK_ACT_SILU, 0.0f, 0, z);
+        conv(name, a.c2, z, H, W, 1, nullptr, VDK_ACT_NONE, 0.0f, 1, z2);
+        prof_begin("eres_aff_combine", 0.0, 16.0 * batch * (double)H * W * C);
+        check_rc(vdk_aff_combine(z2.p, z2.stride, z2.lo, x.p, x.stride, x.lo, ds.p, ds.stride, ds.lo,
+                                 (long)batch * H * W, C, 1, y.p, y.stride, y.lo, stream_));
+        prof_end();
+    };
+
+    int H = m.n_mels, W = T;
+    prof_begin("eres_stem3x3", 2.0 * 9 * m.m * (double)batch * H * W, 4.0 * batch * H * W + 4.0 * batch * H * W * m.m);
+    check_rc(vdk_stem_conv3x3_ex(w.feats, batch, H, W, m.stem_w, m.stem_b, m.m, 1, 1, w.ex[0], stream_));
+    prof_end();
+    View x = split_tensor(w.ex[0], m.m);
+    int xi = 0;
+    const float hi = m.clamp;
+    // The cross-stage convs run as soon as their input exists (the manifest
+    // order is only the load order): down[li] right after the map it reads.
+    for (int li = 0; li < 4; ++li) {
+        const int nb = (int)m.layers[li].size();
+        for (int bi = 0; bi < nb; ++bi) {
+            const EresBlock& b = m.layers[li][bi];
+            const int Ho = (H - 1) / b.stride + 1, Wo = (W - 1) / b.stride + 1;
+            const int wd = b.width;
+            const View s4 = split_tensor(w.es4, 4 * wd);
+            // conv1 -> [chunk0 | chunk1]
+            conv("eres_conv1", b.conv1, x, H, W, b.stride, nullptr, VDK_ACT_RELU, hi, 0, s4);
+            // chunk 0 -> sp0
+            conv("eres_conv3x3", b.conv_a, s4, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(2 * wd));
+            // chunk 1 -> sp1
+            if (b.aff) {
+                const View f = split_tensor(w.ef, wd);
+                aff("eres_aff_block", b.fuse, s4.at(wd), s4.at(2 * wd), s4.at(wd), wd, Ho, Wo, f);
+                conv("eres_conv3x3", b.conv_b, f, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(3 * wd));
+            } else {
+                conv("eres_conv3x3", b.conv_b, s4.at(wd), Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(3 * wd));
+            }
+            // shortcut, then conv3 + residual -> clamp
+            View res = x;
+            if (b.has_sc) {
+                res = split_tensor(w.esc, 2 * b.planes);
+                conv("eres_shortcut", b.sc, x, H, W, b.stride, nullptr, VDK_ACT_NONE, 0.0f, 0, res);
+            }
+            const bool last = bi == nb - 1 && li >= 1;
+            const View y = last ? split_tensor(w.ecat[li - 1], 4 * b.planes) : split_tensor(w.ex[xi ^ 1], 2 * b.planes);
+            conv("eres_conv3", b.conv3, s4.at(2 * wd), Ho, Wo, 1, &res, VDK_ACT_RELU, hi, 0, y);
+            if (!last) xi ^= 1;
+            x = y;
+            H = Ho;
+            W = Wo;
+        }
+        const int C = 2 * (m.m << li);   // this layer's output channels
+        if (li >= 1) {
+            // AFF(layer output, downsample) from the [out | down] tensor (src/encoder_eres2net.cpp:203-223)
+            const View cat = split_tensor(w.ecat[li - 1], 2 * C);
+            aff("eres_aff_cross", m.cross[li - 1], cat, cat, cat.at(C), C, H, W, split_tensor(w.efuse[li - 1], C));
+        }
+        if (li < 3) {
+            // downsample of this stage's feature (layer 1 output, else the fused map) into the
+            // second half of the next layer's [out | down] tensor
+            const View src = li == 0 ? x : split_tensor(w.efuse[li - 1], C);
+            conv("eres_downsample", m.down[li], src, H, W, 2, nullptr, VDK_ACT_NONE, 0.0f, 0,
+                 split_tensor(w.ecat[li], 4 * C).at(2 * C));
+        }
+    }
+    // TSTP over the last fused map, then seg_1 (src/encoder_eres2net.cpp:228-250)
+    const View fin = split_tensor(w.efuse[2], m.c_out);
+    prof_begin("eres_tstp", 0.0, 4.0 * batch * (double)H * W * m.c_out + 4.0 * batch * pooled_dim_);
+    check_rc(vdk_tstp_ex(fin.p, fin.stride, fin.lo, batch, H, W, m.c_out, m.eps, w.pooled, stream_));
+    prof_end();
+    linear("eres_seg1", w.pooled, batch, pooled_dim_, m.seg_w, m.seg_b, nullptr, cfg_.embedding_dim, 0, w.pre);
+}
+
+}  // namespace vdk

@@ -56,4 +56,28 @@ inline std::vector<uint16_t> pack_conv_f16(const HostConv& c, int icp,
     return p;
 }
 
+// Split-f16 weights: f16 [OC][KH][KW][3*icp] holding [hi | hi | lo] per tap
+// (hi = f16(w), lo = f16(w - hi)); rows oc_pad > oc are zero.
+inline std::vector<uint16_t> pack_conv_f16_split(const HostConv& c, int icp, int oc_pad = 0,
+                                                 const std::function<int(int)>& ic_map = nullptr) {
+    const int ocp = oc_pad > c.oc ? oc_pad : c.oc;
+    const size_t row = (size_t)3 * icp;
+    std::vector<uint16_t> p((size_t)ocp * c.kh * c.kw * row, 0);
+    for (int o = 0; o < c.oc; ++o)
+        for (int i = 0; i < c.ic; ++i) {
+            const int d = ic_map ? ic_map(i) : i;
+            for (int kh = 0; kh < c.kh; ++kh)
+                for (int kw = 0; kw < c.kw; ++kw) {
+                    const float v = c.w[(((size_t)o * c.ic + i) * c.kh + kh) * c.kw + kw];
+                    const uint16_t hi = float_to_half_bits(v);
+                    const uint16_t lo = float_to_half_bits(v - half_bits_to_float(hi));
+                    uint16_t* q = &p[(((size_t)o * c.kh + kh) * c.kw + kw) * row];
+                    q[d] = hi;
+                    q[icp + d] = hi;
+                    q[2 * icp + d] = lo;
+                }
+        }
+    return p;
+}
+
 }  // namespace vdk
