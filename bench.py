@@ -1,15 +1,20 @@
-"""Throughput benchmark: WeSpeaker ResNet34 speaker embeddings on one MI355X.
+"""Throughput benchmark: speaker embeddings on one MI355X.
 
-Workload: batch 64 x 3 s 16 kHz synthetic clips (FBank 64x80x298), random-init
-f16 weights with folded BN, the full path PCM -> FBank -> ResNet34 -> TSTP ->
-FC -> L2 on the GPU.  A step is one batch; inputs are resident in HBM before
-the timed region.  Prints one JSON line (rank 0, N=1).
+Default workload (the headline line): WeSpeaker ResNet34, batch 64 x 3 s 16 kHz
+synthetic clips (FBank 64x80x298), random-init f16 weights with folded BN, the
+full path PCM -> FBank -> ResNet34 -> TSTP -> FC -> L2 on the GPU.  `--model`
+selects one of the other encoder workloads (ECAPA-TDNN B=64 x 4 s, CAM++
+B=32 x 10 s q8_0, ERes2Net B=16 x 20 s q8_0) for the same measurement.
+
+A step is one batch; inputs are resident in HBM before the timed region.
+Prints one JSON line (rank 0, N=1).
 
 The conv roofline comes from HIP events recorded around every launch on the
 library's stream, in a profiled pass of the same number of steps right after
 the timed pass: achieved = direct-conv algorithmic FLOPs / event time.  The CPU
 baseline times the oracle (this repository's C restatement of the reference
-CPU path) on a bounded sample of the same clips.
+CPU path) on a bounded sample of the same clips, clip-parallel on
+min(cores, 8) threads like the reference's default.
 """
 import argparse
 import json
@@ -17,6 +22,7 @@ import os
 import sys
 import tempfile
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -25,27 +31,52 @@ sys.path.insert(0, os.path.join(ROOT, "voice-detect.cpp_amd"))
 
 from vdamd import lib, synth  # noqa: E402
 
-METRIC = "embeddings/s, ResNet34 B=64 3 s clips; conv MFMA util vs f16 peak"
 PEAK_F16_TFLOPS = 2500.0     # MI355X dense f16 MFMA
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
-BATCH = 64
-N_SAMPLES = 48000            # 3 s at 16 kHz -> 298 frames
-MODEL_SEED = 2024
 CLIP_SEED = 1234
 
+MODELS = {
+    "resnet34": {
+        "metric": "embeddings/s, ResNet34 B=64 3 s clips; conv MFMA util vs f16 peak",
+        "write": synth.write_resnet34, "seed": 2024, "batch": 64, "n": 48000, "oracle": "OracleResNet",
+        "dtype": "f16",
+        "config": {"workload": "WeSpeaker ResNet34 embed, batch 64 x 3 s 16 kHz clips (FBank 64x80x298), "
+                               "random-init f16 weights with folded BN, PCM->FBank->ResNet34->TSTP->FC->L2 on GPU",
+                   "batch": 64, "clip_seconds": 3.0, "frames": 298, "channels": [32, 64, 128, 256],
+                   "blocks": [3, 4, 6, 3]},
+    },
+    "ecapa": {
+        "metric": "embeddings/s, ECAPA-TDNN B=64 4 s clips; conv MFMA util vs f16 peak",
+        "write": synth.write_ecapa, "seed": 7, "batch": 64, "n": 64000, "oracle": "OracleEcapa", "dtype": "f16",
+        "config": {"workload": "ECAPA-TDNN embed, batch 64 x 4 s clips (398 frames), C=1024 k=5, 3 SE-Res2 "
+                               "blocks (dil 2/3/4, scale 8, SE 128), MFA 1536, ASP, 192-d, random-init f16 weights",
+                   "batch": 64, "clip_seconds": 4.0, "frames": 398},
+    },
+    "campplus": {
+        "metric": "embeddings/s, CAM++ B=32 10 s clips q8_0; conv MFMA util vs f16 peak",
+        "write": synth.write_campplus, "seed": 5, "batch": 32, "n": 160000, "oracle": "OracleCampplus",
+        "dtype": "f16",
+        "config": {"workload": "CAM++ embed, batch 32 x 10 s clips (998 frames), FCM 32ch, D-TDNN 12/24/16 "
+                               "growth 32 bottleneck 128 with context masks, stats, 192-d, q8_0 1x1 weights",
+                   "batch": 32, "clip_seconds": 10.0, "frames": 998},
+    },
+    "eres2net": {
+        "metric": "embeddings/s, ERes2Net B=16 20 s clips q8_0; conv MFMA util vs f16 peak",
+        "write": synth.write_eres2net, "seed": 9, "batch": 16, "n": 320000, "oracle": "OracleEres2net",
+        "dtype": "split-f16",
+        "config": {"workload": "ERes2Net base embed, batch 16 x 20 s clips (1998 frames), m_channels 32, "
+                               "blocks 3/4/6/3, Res2 scale 2, AFF, TSTP, 512-d, q8_0 1x1 weights, split-f16 convs",
+                   "batch": 16, "clip_seconds": 20.0, "frames": 1998},
+    },
+}
 
-def classify(name):
-    if name.startswith("conv"):
-        return "conv"
-    return name
 
-
-def profile_pass(ctx, d_pcm, d_out, steps):
+def profile_pass(ctx, d_pcm, d_out, batch, n, steps):
     ctx.set_profiling(True)
     ctx.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        ctx.embed_device_async(d_pcm.ptr, BATCH, N_SAMPLES, d_out.ptr)
+        ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
     ctx.synchronize()
     wall = (time.perf_counter() - t0) / steps
     recs = ctx.profile()
@@ -60,20 +91,26 @@ def profile_pass(ctx, d_pcm, d_out, steps):
     return per, wall * 1e3
 
 
-def cpu_baseline(gguf_path, pcm):
+def cpu_baseline(model, gguf_path, pcm, n_seconds):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
     from vdamd import gguf
 
-    net = pyoracle.OracleResNet(gguf.GGUFFile(gguf_path))
+    net = getattr(pyoracle, model["oracle"])(gguf.GGUFFile(gguf_path))
     try:
         avail = len(os.sched_getaffinity(0))
     except AttributeError:
         avail = os.cpu_count() or 1
     threads = max(1, min(8, avail))            # the reference's default min(hw, 8) threads
-    sample = pcm[: 2 * threads]
+    per_thread = 2 if model["n"] <= 64000 else 1
+    sample = pcm[: per_thread * threads]
     t0 = time.perf_counter()
-    net.embed_batch(sample, n_threads=threads)
+    if model["oracle"] == "OracleResNet":
+        net.embed_batch(sample, n_threads=threads)
+    else:
+        # the oracle releases the GIL inside its C calls: one clip per thread
+        with ThreadPoolExecutor(threads) as ex:
+            list(ex.map(lambda x: net.forward(pyoracle.fbank(x)), sample))
     dt = time.perf_counter() - t0
     cpu_name = ""
     try:
@@ -84,7 +121,7 @@ def cpu_baseline(gguf_path, pcm):
     except OSError:
         pass
     return {"value": round(len(sample) / dt, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
-            "sample": f"{len(sample)} of the same 3 s clips through oracle FBank+ResNet34 (f32), "
+            "sample": f"{len(sample)} of the same {n_seconds:g} s clips through the oracle's FBank + encoder (f32), "
                       f"clip-parallel on {threads} threads, {dt:.1f} s wall; host {cpu_name}"}
 
 
@@ -93,6 +130,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--model", choices=sorted(MODELS), default="resnet34")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -104,38 +142,39 @@ def main():
     if L.vdk_device_count() < 1:
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
+    model = MODELS[args.model]
+    batch, n = model["batch"], model["n"]
 
     tmp = tempfile.mkdtemp()
-    path = os.path.join(tmp, "resnet34_f16.gguf")
-    synth.write_resnet34(path, seed=MODEL_SEED)
+    path = os.path.join(tmp, f"{args.model}.gguf")
+    model["write"](path, seed=model["seed"])
     ctx = lib.Context(path)
-    pcm = synth.clips(CLIP_SEED, BATCH, N_SAMPLES)
+    pcm = synth.clips(CLIP_SEED, batch, n)
     d_pcm = lib.DeviceBuffer.from_array(pcm)
-    d_out = lib.DeviceBuffer(BATCH * ctx.dim * 4)
+    d_out = lib.DeviceBuffer(batch * ctx.dim * 4)
 
     for _ in range(args.warmup):
-        ctx.embed_device_async(d_pcm.ptr, BATCH, N_SAMPLES, d_out.ptr)
+        ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
     ctx.synchronize()
     lib.check(L.vdk_synchronize())
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        ctx.embed_device_async(d_pcm.ptr, BATCH, N_SAMPLES, d_out.ptr)
+        ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
     ctx.synchronize()
     lib.check(L.vdk_synchronize())
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
-    value = BATCH * args.steps / elapsed
-    emb = d_out.to_array(np.float32, (BATCH, ctx.dim))
+    value = batch * args.steps / elapsed
+    emb = d_out.to_array(np.float32, (batch, ctx.dim))
     assert np.all(np.isfinite(emb)) and np.allclose(np.linalg.norm(emb, axis=1), 1.0, atol=1e-4)
 
-    per, prof_ms = profile_pass(ctx, d_pcm, d_out, args.steps)
+    per, prof_ms = profile_pass(ctx, d_pcm, d_out, batch, n, args.steps)
     conv = {"ms": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0}
     for name, p in per.items():
-        if classify(name) == "conv":
+        if name.startswith("conv"):
             for k in conv:
                 conv[k] += p[k]
     steps = args.steps
-    conv_ms_step = conv["ms"] / steps
     achieved = conv["flops"] / (conv["ms"] * 1e-3) / 1e12 if conv["ms"] > 0 else 0.0
     kernels = []
     for name, p in sorted(per.items(), key=lambda kv: -kv[1]["ms"]):
@@ -147,31 +186,26 @@ def main():
             "gbs": round(p["bytes"] / t / 1e9, 1) if t > 0 else None,
         })
     roofline = {
-        "kernel": "all conv launches (implicit-GEMM MFMA conv, 35 per step)",
+        "kernel": f"all conv launches (implicit-GEMM MFMA conv, {conv['launches'] // steps} per step)",
         "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_F16_TFLOPS, "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_F16_TFLOPS, 4),
         "traffic": None,
         "flops_per_step": conv["flops"] / steps,
-        "conv_ms_per_step": round(conv_ms_step, 4),
+        "conv_ms_per_step": round(conv["ms"] / steps, 4),
         "profiled_ms_per_step": round(prof_ms, 4),
         "kernels": kernels,
     }
     out = {
-        "metric": METRIC, "value": round(value, 2), "unit": "embeddings/s", "n_gpus": 1,
+        "metric": model["metric"], "value": round(value, 2), "unit": "embeddings/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
-        "data": "synthetic",
-        "config": {"workload": "WeSpeaker ResNet34 embed, batch 64 x 3 s 16 kHz clips (FBank 64x80x298), "
-                               "random-init f16 weights with folded BN, PCM->FBank->ResNet34->TSTP->FC->L2 on GPU",
-                   "batch": BATCH, "clip_seconds": 3.0, "frames": 298, "channels": [32, 64, 128, 256],
-                   "blocks": [3, 4, 6, 3]},
-        "roofline": roofline,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": model["dtype"],
+        "data": "synthetic", "config": model["config"], "roofline": roofline,
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(path, pcm)
+        out["cpu_baseline"] = cpu_baseline(model, path, pcm, n / 16000.0)
     ctx.close()
     for k in kernels:
-        print(f"  {k['name']:28s} x{k['launches_per_step']:2d} {k['ms_per_step']*1e3:9.1f} us/step "
+        print(f"  {k['name']:28s} x{k['launches_per_step']:3d} {k['ms_per_step']*1e3:9.1f} us/step "
               f"{k['tflops'] or 0:8.1f} TFLOP/s {k['gbs'] or 0:8.1f} GB/s", file=sys.stderr)
     print(json.dumps(out), flush=True)
 

@@ -202,9 +202,10 @@ void Model::conv_ex(const char* name, const vdk_conv_desc& d) {
         const int Wo = (d.W + 2 * d.pad_w - (d.KW - 1) * dw - 1) / sw + 1;
         const double npix = (double)d.batch * Ho * Wo;
         const double flops = 2.0 * d.KH * d.KW * d.IC * (double)d.OC * npix;
-        const double bytes = 2.0 * ((double)d.batch * d.H * d.W * d.IC + (double)d.OC * d.KH * d.KW * d.IC +
-                                    npix * d.OC * (d.residual ? 2.0 : 1.0));
-        prof_begin(name, flops, bytes);
+        const double halves = d.split ? 2.0 : 1.0;   // split-f16 moves hi and lo
+        const double bytes = 2.0 * halves * ((double)d.batch * d.H * d.W * d.IC + npix * d.OC * (d.residual ? 2.0 : 1.0)) +
+                             2.0 * (d.split ? 3.0 : 1.0) * (double)d.OC * d.KH * d.KW * d.IC;
+        prof_begin((std::string("conv.") + name).c_str(), flops, bytes);
     }
     check_rc(vdk_conv2d_ex(&d, stream_));
     prof_end();

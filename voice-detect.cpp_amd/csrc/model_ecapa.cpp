@@ -235,7 +235,7 @@ void Model::tdnn(const char* name, const Layer& l, const void* x, int x_stride, 
         const double flops = 2.0 * l.k * l.ic * l.oc * npix;
         const double bytes = 2.0 * ((double)batch * W * l.ic + (double)l.oc * l.k * l.ic) +
                              npix * l.oc * (y_f32 ? 4.0 : 2.0);
-        prof_begin(name, flops, bytes);
+        prof_begin((std::string("conv.") + name).c_str(), flops, bytes);
     }
     vdk_conv_desc d{};
     d.x = x; d.batch = batch; d.H = 1; d.W = W; d.IC = l.ic; d.x_stride = x_stride;
