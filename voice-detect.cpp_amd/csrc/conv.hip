@@ -46,55 +46,61 @@ struct ConvArgs {
     int npix_in;               // B * H * W
 };
 
-// Shared epilogue for 4 consecutive output channels of pixel P (P enumerates
-// (clip, oh, ow) row-major): v = acc + bias; [* gate]; [+ residual];
-// [relu [min(v, clamp_hi)] | sigmoid | silu]; [* post_scale + post_shift];
-// [tanh]; store f16 / f32 at
-// pixel P, or at (clip, ow, oh) when y_tr (time-major output of an NHWC map).
-__device__ __forceinline__ void epilogue4(const ConvArgs& a, int P, int oc, const float* acc) {
-    float v[4];
-    const float* bias = a.bias;
-    const int HoWo = a.Ho * a.Wo;
-    if (bias && a.bias_bs) bias += (size_t)(P / HoWo) * a.bias_bs;
+// Epilogue for 8 consecutive output channels oc..oc+7 of pixel P (P
+// enumerates (clip, oh, ow) row-major), with every operand moved as 16-byte
+// vectors: v = acc + bias; [* gate]; [+ residual]; [relu [min(v, clamp_hi)] |
+// sigmoid | silu]; [* post_scale + post_shift]; [tanh]; store f16 / f32 /
+// split-f16 at pixel P, or at (clip, ow, oh) when y_tr (time-major output of
+// an NHWC map).  Bias, gate and post-affine pointers are 16-byte aligned.
+__device__ __forceinline__ void add8(float* v, const float* p, bool mul = false) {
+    const float4v a = *reinterpret_cast<const float4v*>(p), b = *reinterpret_cast<const float4v*>(p + 4);
+    if (mul) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = acc[e] + (bias ? bias[oc + e] : 0.0f);
+        for (int e = 0; e < 4; ++e) { v[e] *= a[e]; v[e + 4] *= b[e]; }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { v[e] += a[e]; v[e + 4] += b[e]; }
+    }
+}
+
+__device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float* v) {
+    const int HoWo = a.Ho * a.Wo;
+    if (a.bias) add8(v, a.bias + oc + (a.bias_bs ? (size_t)(P / HoWo) * a.bias_bs : 0));
     if (a.gate) {
         const int b = P / HoWo, ow = (P - b * HoWo) % a.Wo;
-        const float* g = a.gate + ((size_t)b * a.gate_nseg + ow / a.gate_seg) * a.OC + oc;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] *= g[e];
+        add8(v, a.gate + ((size_t)b * a.gate_nseg + ow / a.gate_seg) * a.OC + oc, true);
     }
     if (a.res) {
-        const half4 r = *reinterpret_cast<const half4*>(a.res + (size_t)P * a.rs + oc);
+        const half8 r = *reinterpret_cast<const half8*>(a.res + (size_t)P * a.rs + oc);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
+        for (int e = 0; e < 8; ++e) v[e] += (float)r[e];
         if (a.split) {
-            const half4 rl = *reinterpret_cast<const half4*>(a.res + (size_t)P * a.rs + a.r_lo + oc);
+            const half8 rl = *reinterpret_cast<const half8*>(a.res + (size_t)P * a.rs + a.r_lo + oc);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] += (float)rl[e];
+            for (int e = 0; e < 8; ++e) v[e] += (float)rl[e];
         }
     }
     if (a.act == VDK_ACT_RELU) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
+        for (int e = 0; e < 8; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
         if (a.clamp_hi > 0.0f) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = v[e] < a.clamp_hi ? v[e] : a.clamp_hi;
+            for (int e = 0; e < 8; ++e) v[e] = v[e] < a.clamp_hi ? v[e] : a.clamp_hi;
         }
     } else if (a.act == VDK_ACT_SIGMOID) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = 1.0f / (1.0f + expf(-v[e]));
+        for (int e = 0; e < 8; ++e) v[e] = 1.0f / (1.0f + expf(-v[e]));
     } else if (a.act == VDK_ACT_SILU) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = v[e] / (1.0f + expf(-v[e]));
+        for (int e = 0; e < 8; ++e) v[e] = v[e] / (1.0f + expf(-v[e]));
     }
     if (a.post_scale) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = v[e] * a.post_scale[oc + e] + a.post_shift[oc + e];
+        add8(v, a.post_scale + oc, true);
+        add8(v, a.post_shift + oc);
     }
     if (a.tanh_after) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = tanhf(v[e]);
+        for (int e = 0; e < 8; ++e) v[e] = tanhf(v[e]);
     }
     size_t Po = (size_t)P;
     if (a.y_tr) {
@@ -103,19 +109,53 @@ __device__ __forceinline__ void epilogue4(const ConvArgs& a, int P, int oc, cons
     }
     const size_t o = Po * a.ys + oc;
     if (a.y_f32) {
-        float4v f = {v[0], v[1], v[2], v[3]};
-        *reinterpret_cast<float4v*>(static_cast<float*>(a.y) + o) = f;
+        float* y = static_cast<float*>(a.y) + o;
+        *reinterpret_cast<float4v*>(y) = float4v{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<float4v*>(y + 4) = float4v{v[4], v[5], v[6], v[7]};
     } else {
-        half4 h;
+        half8 h;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = (half_t)v[e];
-        *reinterpret_cast<half4*>(static_cast<half_t*>(a.y) + o) = h;
+        for (int e = 0; e < 8; ++e) h[e] = (half_t)v[e];
+        *reinterpret_cast<half8*>(static_cast<half_t*>(a.y) + o) = h;
         if (a.split) {
-            half4 l;
+            half8 l;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) l[e] = (half_t)(v[e] - (float)h[e]);
-            *reinterpret_cast<half4*>(static_cast<half_t*>(a.y) + o + a.y_lo) = l;
+            for (int e = 0; e < 8; ++e) l[e] = (half_t)(v[e] - (float)h[e]);
+            *reinterpret_cast<half8*>(static_cast<half_t*>(a.y) + o + a.y_lo) = l;
         }
+    }
+}
+
+// The finished 32x32 MFMA blocks are staged through LDS as f32 [pixel][oc]
+// (row stride TS = M + 4 floats, so consecutive pixels start 16 bytes apart
+// across the 64 banks) and then every thread finishes 8 consecutive channels
+// of one pixel: bias, gate, residual and the output move as coalesced
+// 16-byte rows instead of the MFMA layout's 8-byte pieces 32 pixels apart.
+// Accumulator layout: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4
+// and column l%32 of its 32x32 block.
+__device__ __forceinline__ void stage_block(float* sT, int TS, int pix0, int row0, const float16v& acc, int lane) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int r = row0 + g * 8 + (lane >> 5) * 4;
+        *reinterpret_cast<float4v*>(sT + (pix0 + (lane & 31)) * TS + r) =
+            float4v{acc[g * 4], acc[g * 4 + 1], acc[g * 4 + 2], acc[g * 4 + 3]};
+    }
+}
+
+// Finish NPIX staged pixels x M channels; pix(pl) maps a staged pixel to P
+// (or -1 when outside the output).
+template <int M, class PixFn>
+__device__ __forceinline__ void finish_staged(const ConvArgs& a, const float* sT, int npix_tile, int oc0, int tid,
+                                              int nthreads, PixFn pix) {
+    constexpr int TS = M + 4, C8 = M / 8;
+    for (int q = tid; q < npix_tile * C8; q += nthreads) {
+        const int pl = q / C8, c8 = q - pl * C8;
+        const int P = pix(pl), oc = oc0 + c8 * 8;
+        if (P < 0 || oc >= a.OC) continue;
+        const float4v u0 = *reinterpret_cast<const float4v*>(sT + pl * TS + c8 * 8);
+        const float4v u1 = *reinterpret_cast<const float4v*>(sT + pl * TS + c8 * 8 + 4);
+        float v[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
+        finish8(a, P, oc, v);
     }
 }
 
@@ -125,6 +165,34 @@ __device__ __forceinline__ int xcd_swizzle(int bid, int nb) {
     const int per = nb >> 3;
     if (bid >= (per << 3)) return bid;
     return (bid & 7) * per + (bid >> 3);
+}
+
+// Staged epilogue of an implicit-GEMM tile (BM channels x BN consecutive
+// pixels): waves write their blocks in passes of PB pixel columns that fit the
+// kernel's LDS buffer, then all threads finish 8-channel rows.
+template <int BM, int BN, int WN, int SMEM, int NT, int TM, int TN>
+__device__ __forceinline__ void stage_epilogue_impl(const ConvArgs& a, uint8_t* smem, const float16v (*acc)[TN],
+                                                    int m_off, int n_off, int p0, int oc0, int tid, int lane) {
+    constexpr int TS = BM + 4;
+    constexpr int FIT = SMEM / (TS * 4);
+    constexpr int PB = FIT >= BN ? BN : (FIT / WN) * WN;
+    static_assert(PB >= WN, "epilogue staging holds at least one wave's pixel columns");
+    float* sT = reinterpret_cast<float*>(smem);
+    for (int pb = 0; pb < BN; pb += PB) {
+        __syncthreads();   // every wave is done with the previous contents of smem
+        if (n_off >= pb && n_off < pb + PB) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int i = 0; i < TM; ++i) stage_block(sT, TS, n_off - pb + j * 32, m_off + i * 32, acc[i][j], lane);
+        }
+        __syncthreads();
+        const int np = BN - pb < PB ? BN - pb : PB;
+        finish_staged<BM>(a, sT, np, oc0, tid, NT, [&](int pl) {
+            const int P = p0 + pb + pl;
+            return P < a.npix ? P : -1;
+        });
+    }
 }
 
 template <int BM, int BN, int WM, int WN, int KC>
@@ -137,8 +205,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
     constexpr int WCH = (BM * CPR + NT - 1) / NT;
     static_assert(WM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0, "tile shape");
     // two LDS stages: chunk k is read from stage k&1 while chunk k+1 is written to the other
-    __shared__ __attribute__((aligned(16))) half_t sW[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) half_t sX[2][BN * LDK];
+    constexpr int SMEM_K = 2 * (BM + BN) * LDK * 2, SMEM_E = WN * (BM + 4) * 4;   // K stages / epilogue pass
+    constexpr int SMEM = SMEM_K > SMEM_E ? SMEM_K : SMEM_E;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
+    half_t (*sW)[BM * LDK] = reinterpret_cast<half_t (*)[BM * LDK]>(smem);
+    half_t (*sX)[BN * LDK] = reinterpret_cast<half_t (*)[BN * LDK]>(smem + 2 * BM * LDK * 2);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave % NWM, wn = wave / NWM;
@@ -241,25 +312,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         __syncthreads();
     }
 
-    // Epilogue.  32x32 accumulator layout: register r of lane l holds
-    // row (OC) 8*(r/4) + 4*(l/32) + r%4 and column (pixel) l%32.
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int P = p0 + wn * WN + j * 32 + (lane & 31);
-        if (P >= a.npix) continue;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int oc = oc0 + wm * WM + i * 32 + g * 8 + (lane >> 5) * 4;
-                if (oc >= a.OC) continue;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e];
-                epilogue4(a, P, oc, v);
-            }
-        }
-    }
+    stage_epilogue_impl<BM, BN, WN, SMEM, NT, TM, TN>(a, smem, acc, wm * WM, wn * WN, p0, oc0, tid, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -319,7 +372,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     static_assert((ROWS * CPR) % 64 == 0, "whole DMA instructions per stage");
     static_assert(BM % (64 / CPR) == 0, "weight rows fill whole DMA instructions");
     static_assert(NST >= 2 && IPW * (NST - 2) <= 60, "vmcnt range");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NST * STAGE];
+    constexpr int SMEM_E = WN * (BM + 4) * 4;   // one epilogue pass of a wave's pixel columns
+    constexpr int SMEM = NST * STAGE > SMEM_E ? NST * STAGE : SMEM_E;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -461,23 +516,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
         st = st + 1 == NST ? 0 : st + 1;
     }
 
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int P = p0 + wn * WN + j * 32 + lrow;
-        if (P >= a.npix) continue;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int oc = oc0 + wm * WM + i * 32 + g * 8 + lhalf * 4;
-                if (oc >= a.OC) continue;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = acc[i][j][g * 4 + e];
-                epilogue4(a, P, oc, v);
-            }
-        }
-    }
+    stage_epilogue_impl<BM, BN, WN, SMEM, NW * 64, TM, TN>(a, smem, acc, wm * WM, wn * WN, p0, oc0, tid, lane);
 }
 
 template <int BM, int BN, int WM, int WN, int KC, int NST>
@@ -583,23 +622,22 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
         __syncthreads();
     }
 
+    // staged epilogue: the TH x TW x OCB tile as [pixel][oc] f32 in LDS
+    constexpr int TS = OCB + 4;
+    static_assert(TH * TW * TS * 4 <= (W_INS + X_INS) * 1024, "halo epilogue staging fits the LDS buffer");
+    float* sT = reinterpret_cast<float*>(smem);
+    // (the loop above ends with a barrier: every wave is done reading smem)
 #pragma unroll
     for (int q = 0; q < BPW; ++q) {
         const int blk = wave * BPW + q;
         const int mb = blk % NBLK_M, nb = blk / NBLK_M;
-        const int oh = oh0 + nb / (TW / 32), ow = ow0 + (nb % (TW / 32)) * 32 + lrow;
-        if (oh >= a.Ho || ow >= a.Wo) continue;
-        const size_t P = ((size_t)b * a.Ho + oh) * a.Wo + ow;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int oc = oc0 + mb * 32 + g * 8 + lhalf * 4;
-            if (oc >= a.OC) continue;
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[q][g * 4 + e];
-            epilogue4(a, (int)P, oc, v);
-        }
+        stage_block(sT, TS, nb * 32, mb * 32, acc[q], lane);
     }
+    __syncthreads();
+    finish_staged<OCB>(a, sT, TH * TW, oc0, tid, 256, [&](int pl) {
+        const int oh = oh0 + pl / TW, ow = ow0 + pl % TW;
+        return (oh < a.Ho && ow < a.Wo) ? (b * a.Ho + oh) * a.Wo + ow : -1;
+    });
 }
 
 template <int OCB, int KC, int TH, int TW>
@@ -623,7 +661,8 @@ struct TileCfg {
 };
 
 // Entries 0-13 are the register-staged kernel (any layout; the only one with
-// KC=16 for IC % 32 != 0), 14-25 the LDS-DMA kernel, 26+ the halo kernel.
+// KC=16 for IC % 32 != 0), 14-25 the LDS-DMA kernel, 26-32 the halo kernel,
+// 33+ LDS-DMA tiles with 8 waves per workgroup.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -661,6 +700,26 @@ const TileCfg kTiles[] = {
     {64, 128, 32, launch_halo<64, 32, 4, 32>, true},      // 30
     {64, 128, 64, launch_halo<64, 64, 2, 64>, true},      // 31
     {32, 256, 64, launch_halo<32, 64, 4, 64>, true},      // 32
+    {128, 256, 64, launch_dma<128, 256, 64, 64, 64, 2>},  // 33: 8-wave DMA tiles
+    {256, 128, 64, launch_dma<256, 128, 64, 64, 64, 2>},  // 34
+    {128, 128, 64, launch_dma<128, 128, 64, 64, 64, 3>},  // 35
+    {128, 256, 32, launch_dma<128, 256, 64, 64, 32, 2>},  // 36
+    {128, 256, 64, launch_dma<128, 256, 64, 64, 64, 3>},  // 37
+    {256, 256, 64, launch_dma<256, 256, 128, 64, 64, 2>}, // 38
+    {128, 128, 32, launch_dma<128, 128, 64, 64, 32, 2>},  // 39
+    {128, 128, 64, launch_dma<128, 128, 64, 32, 64, 2>},  // 40: 8 waves, 64x32 wave tiles
+    {128, 256, 32, launch_dma<128, 256, 64, 64, 32, 4>},  // 41: deeper rings
+    {128, 256, 32, launch_dma<128, 256, 64, 64, 32, 6>},  // 42
+    {256, 128, 32, launch_dma<256, 128, 64, 64, 32, 4>},  // 43
+    {256, 128, 32, launch_dma<256, 128, 64, 64, 32, 6>},  // 44
+    {128, 128, 32, launch_dma<128, 128, 64, 32, 32, 4>},  // 45
+    {128, 128, 32, launch_dma<128, 128, 64, 32, 32, 6>},  // 46
+    {128, 64, 32, launch_dma<128, 64, 64, 32, 32, 2>},    // 47: small-footprint tiles
+    {128, 64, 32, launch_dma<128, 64, 64, 32, 32, 3>},    // 48
+    {128, 64, 32, launch_dma<128, 64, 64, 32, 32, 4>},    // 49
+    {256, 64, 32, launch_dma<256, 64, 64, 64, 32, 2>},    // 50
+    {256, 64, 64, launch_dma<256, 64, 64, 64, 64, 2>},    // 51
+    {128, 32, 64, launch_dma<128, 32, 32, 32, 64, 2>},    // 52
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -668,12 +727,12 @@ bool is_s1_3x3(const ConvArgs& a) {
     return a.KH == 3 && a.KW == 3 && a.sh == 1 && a.sw == 1 && a.ph == 1 && a.pw == 1 && a.dh == 1 && a.dw == 1;
 }
 
-constexpr int kFirstDma = 14, kFirstHalo = 26;
+constexpr int kFirstDma = 14, kFirstHalo = 26, kFirstDma8 = 33;
 
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
-    if (a.split && (idx < kFirstDma || idx >= kFirstHalo)) return false;   // split-f16: DMA kernel only
+    if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8))) return false;   // split: DMA only
     return a.IC % t.kc == 0;
 }
 
@@ -687,15 +746,17 @@ int tile_override() {
 }
 
 // Per-layer-class defaults, from a sweep of every ResNet34 conv shape at
-// batch 64 on MI355X (narrow 3x3 stride-1 layers: halo tiles; the rest:
-// DMA implicit GEMM with the widest OC tile that divides OC; IC % 32 != 0:
-// the register-staged kernel with KC = 16).  OC that no tile divides runs on
+// batch 64 on MI355X (narrow 3x3 stride-1 layers: the 32-channel halo tile;
+// 128 output channels: the 128x128 DMA tile with KC = 32; the rest: DMA
+// implicit GEMM with the widest OC tile that divides OC; IC % 32 != 0: the
+// register-staged kernel with KC = 16).  OC that no tile divides runs on
 // 32-wide tiles with the surplus rows masked.
 int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
-    if (!a.split && is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return a.OC <= 32 ? 28 : 30;
+    if (!a.split && is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return 28;
+    if (a.IC % 32 == 0 && a.OC == 128) return 39;   // 128x128 tile, KC = 32
     if (a.IC % 64 == 0) return bm == 128 ? 18 : (bm == 64 ? 15 : 14);
     if (a.IC % 32 == 0) return bm >= 64 ? 16 : 14;
     if (a.split) return -1;
@@ -784,6 +845,9 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(aligned16(d.x) && aligned16(d.w) && aligned16(d.y) && (!d.residual || aligned16(d.residual)),
                 "conv2d: device pointers must be 16-byte aligned");
         require(!d.post_scale == !d.post_shift, "conv2d: post_scale and post_shift go together");
+        require(aligned16(d.bias) && aligned16(d.gate) && aligned16(d.post_scale) && aligned16(d.post_shift) &&
+                    d.bias_batch_stride % 4 == 0,
+                "conv2d: bias / gate / post-affine vectors must be 16-byte aligned");
         require(!d.gate || (d.gate_seg > 0 && d.gate_nseg > 0 && (Wo + d.gate_seg - 1) / d.gate_seg <= d.gate_nseg),
                 "conv2d: gate needs gate_seg > 0 and enough segments for the output width");
         require(!d.y_time_major || !d.residual, "conv2d: a time-major store takes no residual");
