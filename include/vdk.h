@@ -131,6 +131,24 @@ int vdk_conv2d_nhwc_tile(const void* d_x, int batch, int H, int W, int IC,
 int vdk_conv2d_tile_count(void);
 int vdk_conv2d_tile_fits(int tile, int IC, int OC, int KH, int KW, int stride, int pad);
 
+/* ---- fused stride-1 identity BasicBlock ----
+ * Replaces one ResNet BasicBlock without downsample (src/encoder_resnet.cpp:33-48
+ * basic_block / 50-73 basic_block_blocked: conv1 3x3 + bias -> ReLU -> conv2
+ * 3x3 + bias -> + x -> ReLU, src/directconv.cpp:1364 blocked_add_relu) in one
+ * launch whose intermediate map never leaves LDS:
+ *   y = relu(conv2(relu(conv1(x) + b1)) + b2 + x)
+ * x, y [B][H][W][C] f16 (must not overlap), w1, w2 [C][3][3][C] f16,
+ * b1, b2 [C] f32; the intermediate is rounded to f16 as vdk_conv2d_nhwc stores
+ * it.  C must be 32. */
+int vdk_resblock3x3(const void* d_x, int batch, int H, int W, int C,
+                    const void* d_w1, const float* d_b1, const void* d_w2, const float* d_b2,
+                    void* d_y, void* stream);
+/* Same with an explicit tile height (variant 0: 6 rows, 1: 4, 2: 8; -1 picks);
+ * for validation and tuning. */
+int vdk_resblock3x3_variant(const void* d_x, int batch, int H, int W, int C,
+                            const void* d_w1, const float* d_b1, const void* d_w2, const float* d_b2,
+                            void* d_y, int variant, void* stream);
+
 /* ---- stem: single-input-channel 3x3 conv from f32 features ----
  * Replaces the ResNet stem conv2d_auto -> directconv_conv3x3 + bias + ReLU
  * (src/encoder_resnet.cpp:115-117).  feats [B][H][W] f32, w [OC][3][3] f32,

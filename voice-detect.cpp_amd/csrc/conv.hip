@@ -647,6 +647,335 @@ void launch_halo(const ConvArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((conv3x3_halo_kernel<OCB, KC, TH, TW>), dim3(tiles, cdiv(a.OC, OCB)), dim3(256), 0, s, a);
 }
 
+// ---------------------------------------------------------------------------
+// resblock3x3_kernel: one whole stride-1 identity BasicBlock of the ResNet
+// trunk (src/encoder_resnet.cpp:33-48: conv1 -> ReLU -> conv2 -> + x -> ReLU,
+// with BN folded into both convs), for C = 32 channels:
+//   t = f16(relu(conv1(x) + b1)),   y = f16(relu(conv2(t) + b2 + x)).
+// Tiles are TH output rows x 30 output columns of one image, ordered rows
+// fastest, and each persistent workgroup walks a contiguous range of them, so
+// consecutive tiles share halo rows in L2.  Every wave holds both weight
+// tensors' MFMA A fragments in VGPRs for the whole launch (18 + 18 fragments
+// for C = 32), so LDS carries only pixels:
+//   * the (TH+4) x 34 input halo, double-buffered: tile k+1's DMA is issued
+//     before tile k's convs start;
+//   * the (TH+2) x 32 intermediate tile, written by conv1 straight from its
+//     accumulators (zero outside the image: conv2's zero padding);
+//   * a 2 KB staging block per wave that turns conv2's MFMA layout into
+//     16-byte channel rows for coalesced stores.
+// conv2 runs over TH rows x 32 columns (the last two of each row are
+// discarded); the residual comes from the halo already in LDS.  HBM sees x
+// read about once and y written once; the block as two convolutions also
+// writes t, reads it back and reads x a second time.  The arithmetic (f16
+// products, f32 sums in tap-major, channel-minor order, f16 rounding of t,
+// then + b2, + x, ReLU) is the halo conv kernel's, so y equals the two-launch
+// block bit for bit.  Barriers wait for LDS traffic only; global stores drain
+// in the background.
+// ---------------------------------------------------------------------------
+// Workgroup barrier over LDS traffic only: this wave's LDS reads and writes
+// complete (lgkmcnt(0)) before s_barrier, while its global stores and LDS DMA
+// stay in flight.  (A workgroup-scope release fence would also drain vmcnt,
+// because LDS DMA counts as a pending LDS write.)
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7, lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// LDS pixel rows of the fused block are C*2 bytes of channels plus 16 bytes of
+// padding (80 bytes for C = 32): 16 consecutive rows then start in 16
+// distinct 16-byte bank groups (5r mod 16 is a permutation), so every MFMA
+// operand read (32 consecutive rows, one 16-byte chunk) is conflict-free for
+// any base row, and its address is a per-lane base plus a compile-time
+// immediate per (tap, k-step).
+template <int C>
+struct PadRow {
+    static constexpr int RB = C * 2 + 16;   // bytes per LDS row
+    static constexpr int SPR = C / 8 + 1;   // 16-byte slots per row (the last is padding)
+};
+
+// NR rows (row0, row0 + step, ...) of a stride-1 3x3 conv whose 32-column
+// MFMA block for tap (kh, kw) is 32 consecutive pixels of LDS source row
+// row + kh (SW pixels per row) from column kw; wf holds the A fragments of
+// the 9 * C/16 (tap, k-step) steps in order.  The B reads run PD steps ahead
+// of the MFMAs (a register ring), so with two waves per SIMD the MFMAs issue
+// back to back instead of each waiting out one LDS round trip.
+template <int C, int NR, int SW, int PD = 4>
+__device__ __forceinline__ void conv_rows(const half8* wf, const uint8_t* src, int row0, int step, int lrow,
+                                          int lhalf, float16v* acc) {
+    constexpr int RB = PadRow<C>::RB, KS = C / 16, NS = 9 * KS, NQ = NR > 0 ? NR : 1;
+    static_assert(PD >= 1 && PD < NS, "prefetch distance within the step count");
+    if constexpr (NR == 0) return;
+    const uint8_t* base = src + lrow * RB + lhalf * 16;
+    auto load = [&](int s, half8* dst) {
+        const int tap = s / KS, kk = s - tap * KS;
+        const int kh = tap / 3, kw = tap - kh * 3;
+#pragma unroll
+        for (int q = 0; q < NR; ++q)
+            dst[q] = *reinterpret_cast<const half8*>(base + ((row0 + q * step + kh) * SW + kw) * RB + kk * 32);
+    };
+    half8 ring[PD][NQ];
+#pragma unroll
+    for (int s = 0; s < PD; ++s) load(s, ring[s]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        half8 cur[NQ];
+#pragma unroll
+        for (int q = 0; q < NR; ++q) cur[q] = ring[s % PD][q];
+        if (s + PD < NS) load(s + PD, ring[s % PD]);
+        // keep the scheduler from sinking the reads back next to their MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < NR; ++q) acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[s], cur[q], acc[q], 0, 0, 0);
+    }
+}
+
+// Geometry of the fused block's tiles.
+template <int C, int TH, int NW>
+struct ResTile {
+    static constexpr int RB = PadRow<C>::RB, SPR = PadRow<C>::SPR, NF = 9 * C / 16;   // NF: A fragments per conv
+    static constexpr int XW = 34, XH = TH + 4, XPIX = XH * XW;       // input halo
+    static constexpr int TW = 32, TH1 = TH + 2;                      // intermediate tile
+    static constexpr int TPIX = TH1 * TW + 2;                        // + 2 pixels read only for discarded columns
+    static constexpr int OW = TW - 2;                                // stored output columns per row
+    static constexpr int X_INS = (XPIX * SPR + 63) / 64;             // DMA instructions per halo
+    static constexpr int X_IPW = (X_INS + NW - 1) / NW;              // ... per wave
+    static constexpr int X_BYTES = X_INS * 1024, T_BYTES = (TPIX * RB + 1023) / 1024 * 1024, S_BYTES = 32 * RB;
+};
+
+// One tile of the fused block.  The LDS regions arrive as distinct
+// __restrict__ pointers: the inlined accesses then carry alias scopes, which
+// lets the compiler see that conv1 / conv2 / the epilogue never touch the
+// buffer the next halo is DMA'd into, so it does not make them wait for it.
+// hofs / hpos: this lane's slot of each of its halo DMA instructions as a
+// byte offset from the halo's origin pixel and as (row << 8 | column), with
+// row 255 for padding slots.
+template <int C, int TH, int NW>
+__device__ __forceinline__ void resblock_tile(const uint8_t* __restrict__ sx, uint8_t* __restrict__ sxn,
+                                              uint8_t* __restrict__ st, uint8_t* __restrict__ sstage,
+                                              const float* __restrict__ sbias, const half8* wf1, const half8* wf2,
+                                              const int* hofs, const int* hpos, __amdgpu_buffer_rsrc_t xr,
+                                              bool prefetch, int nb, int noh0, int now0, int b, int oh0, int ow0,
+                                              int H, int W, half_t* __restrict__ y, int wave, int lane) {
+    using G = ResTile<C, TH, NW>;
+    constexpr int RB = G::RB, XW = G::XW, TW = G::TW, TH1 = G::TH1, OW = G::OW, CPR = C / 8;
+    constexpr int F1 = TH1 / NW, R1 = TH1 % NW, NB1 = F1 + (R1 ? 1 : 0);   // conv1 rows per wave
+    constexpr int F2 = TH / NW, R2 = TH % NW, NB2 = F2 + (R2 ? 1 : 0);     // conv2 rows per wave
+    const int lrow = lane & 31, lhalf = lane >> 5;
+
+    // next tile's halo: LDS row hr * 34 + hc holds x[nb][noh0 - 2 + hr][now0 - 2 + hc][0 .. C)
+    if (prefetch) {
+        const int origin = ((nb * H + noh0 - 2) * W + now0 - 2) * C * 2;
+#pragma unroll
+        for (int i = 0; i < G::X_IPW; ++i) {
+            const int ins = wave + i * NW;
+            if (ins >= G::X_INS) break;
+            const int ih = noh0 - 2 + (hpos[i] >> 8), iw = now0 - 2 + (hpos[i] & 255);
+            const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) ? (uint32_t)(origin + hofs[i])
+                                                                                            : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sxn + ins * 1024), 16, off, 0, 0, 0);
+        }
+    }
+
+    // conv1: intermediate row j (image row oh0 - 1 + j, columns ow0 - 1 ..
+    // ow0 + 30) is one MFMA column block; its B operand for tap (kh, kw) is
+    // 32 consecutive halo pixels of halo row j + kh from column kw.  Wave w
+    // owns rows w, w + NW, ...; a remainder row (waves < R1) runs as its own
+    // branch-free chain.
+    float16v acc1[NB1];
+#pragma unroll
+    for (int q = 0; q < NB1; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc1[q][r] = 0.0f;
+    conv_rows<C, F1, XW>(wf1, sx, wave, NW, lrow, lhalf, acc1);
+    if (R1 && wave < R1) conv_rows<C, 1, XW>(wf1, sx, wave + F1 * NW, NW, lrow, lhalf, acc1 + F1);
+    // t = f16(relu(acc + b1)), zero outside the image.  Register g*4+e of a
+    // lane holds channel 8g + 4*lhalf + e of intermediate column lrow.
+#pragma unroll
+    for (int q = 0; q < NB1; ++q) {
+        const int j = wave + q * NW;
+        if (j >= TH1) continue;
+        const int ih = oh0 - 1 + j, iw = ow0 - 1 + lrow;
+        const bool inside = ih >= 0 && ih < H && iw >= 0 && iw < W;
+        uint8_t* const trow = st + (j * TW + lrow) * RB + lhalf * 8;
+#pragma unroll
+        for (int g = 0; g < C / 8; ++g) {
+            const float4v bb = *reinterpret_cast<const float4v*>(sbias + g * 8 + lhalf * 4);
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v = acc1[q][g * 4 + e] + bb[e];
+                v = v > 0.0f ? v : 0.0f;
+                h[e] = inside ? (half_t)v : (half_t)0.0f;
+            }
+            *reinterpret_cast<half4*>(trow + g * 16) = h;
+        }
+    }
+    lds_barrier();
+
+    // conv2: output row i (columns ow0 .. ow0 + 31) reads intermediate rows
+    // i .. i + 2, 32 consecutive pixels from column kw.
+    float16v acc2[NB2];
+#pragma unroll
+    for (int q = 0; q < NB2; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc2[q][r] = 0.0f;
+    conv_rows<C, F2, TW>(wf2, st, wave, NW, lrow, lhalf, acc2);
+    if (R2 && wave < R2) conv_rows<C, 1, TW>(wf2, st, wave + F2 * NW, NW, lrow, lhalf, acc2 + F2);
+    // this wave's share of the next halo must land before the next barrier;
+    // waiting here, ahead of the epilogue, keeps this tile's stores out of it
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // y = f16(relu(acc + b2 + x)) in the MFMA layout (residual from the
+    // halo), through this wave's staging block to 16-byte channel rows
+#pragma unroll
+    for (int q = 0; q < NB2; ++q) {
+        const int i = wave + q * NW;
+        if (i >= TH) continue;
+        const uint8_t* const xrow = sx + ((i + 2) * XW + lrow + 2) * RB + lhalf * 8;
+        uint8_t* const srow = sstage + lrow * RB + lhalf * 8;
+#pragma unroll
+        for (int g = 0; g < C / 8; ++g) {
+            const float4v bb = *reinterpret_cast<const float4v*>(sbias + C + g * 8 + lhalf * 4);
+            const half4 r = *reinterpret_cast<const half4*>(xrow + g * 16);
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v = acc2[q][g * 4 + e] + bb[e];
+                const float o = v + (float)r[e];
+                h[e] = (half_t)(o > 0.0f ? o : 0.0f);
+            }
+            *reinterpret_cast<half4*>(srow + g * 16) = h;
+        }
+        const int oh = oh0 + i;
+#pragma unroll
+        for (int hp = 0; hp < 32 * CPR / 64; ++hp) {
+            const int pix = hp * (64 / CPR) + lane / CPR, ch = lane % CPR;
+            const half8 v = *reinterpret_cast<const half8*>(sstage + pix * RB + ch * 16);
+            const int ow = ow0 + pix;
+            if (pix < OW && oh < H && ow < W)
+                *reinterpret_cast<half8*>(y + ((size_t)(b * H + oh) * W + ow) * C + ch * 8) = v;
+        }
+    }
+}
+
+template <int C, int TH, int NW>
+__global__ __launch_bounds__(NW * 64) void resblock3x3_kernel(const half_t* __restrict__ x,
+                                                              const half_t* __restrict__ w1,
+                                                              const float* __restrict__ b1,
+                                                              const half_t* __restrict__ w2,
+                                                              const float* __restrict__ b2, half_t* __restrict__ y,
+                                                              int H, int W, int npix_in, int ntiles, int per_wg) {
+    static_assert(C == 32, "both weight tensors live in VGPRs only for 32 channels");
+    using G = ResTile<C, TH, NW>;
+    __shared__ __attribute__((aligned(1024))) uint8_t sx0[G::X_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sx1[G::X_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t st[G::T_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t sstage[NW * G::S_BYTES];
+    __shared__ float sbias[2 * C];   // b1, b2: read from LDS so no global load waits behind the halo DMA
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int tiles_w = (W + G::OW - 1) / G::OW, tiles_h = (H + TH - 1) / TH;
+    const int t_begin = blockIdx.x * per_wg;
+    const int t_end = t_begin + per_wg < ntiles ? t_begin + per_wg : ntiles;
+    if (t_begin >= t_end) return;   // the whole workgroup: no barrier is pending
+
+    // A fragments: lane l holds w[oc = l % 32][tap][8 (kk*2 + l/32) .. + 8)
+    half8 wf1[G::NF], wf2[G::NF];
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+        for (int kk = 0; kk < C / 16; ++kk) {
+            const size_t off = (size_t)(lrow * 9 + tap) * C + (kk * 2 + lhalf) * 8;
+            wf1[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(w1 + off);
+            wf2[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(w2 + off);
+        }
+    if (tid < 2 * C) sbias[tid] = tid < C ? b1[tid] : b2[tid - C];
+    // this lane's halo DMA slots (the same for every tile)
+    int hofs[G::X_IPW], hpos[G::X_IPW];
+#pragma unroll
+    for (int i = 0; i < G::X_IPW; ++i) {
+        const int p = (wave + i * NW) * 64 + lane;
+        const int r = p / G::SPR, cc = p - r * G::SPR;
+        const int hr = r / G::XW, hc = r - hr * G::XW;
+        const bool data = r < G::XPIX && cc < C / 8;
+        hofs[i] = (hr * W + hc) * C * 2 + cc * 16;
+        hpos[i] = data ? (hr << 8 | hc) : (255 << 8);
+    }
+
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)x, 0, npix_in * C * 2, 0x00020000);
+    // tile t: rows fastest, then columns, then images
+    auto coords = [&](int t, int& b, int& oh0, int& ow0) {
+        const int th = t % tiles_h, r = t / tiles_h;
+        const int tw = r % tiles_w;
+        b = r / tiles_w;
+        oh0 = th * TH;
+        ow0 = tw * G::OW;
+    };
+
+    int b, oh0, ow0;
+    coords(t_begin, b, oh0, ow0);
+    {
+        const int origin = ((b * H + oh0 - 2) * W + ow0 - 2) * C * 2;
+#pragma unroll
+        for (int i = 0; i < G::X_IPW; ++i) {
+            const int ins = wave + i * NW;
+            if (ins >= G::X_INS) break;
+            const int ih = oh0 - 2 + (hpos[i] >> 8), iw = ow0 - 2 + (hpos[i] & 255);
+            const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) ? (uint32_t)(origin + hofs[i])
+                                                                                            : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx0 + ins * 1024), 16, off, 0, 0, 0);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // weights in VGPRs and this wave's share of the first halo
+#pragma unroll 1
+    for (int t = t_begin; t < t_end; t += 2) {
+        // Two tiles per trip so each buffer has a fixed role: tile t reads
+        // sx0 while tile t+1's halo lands in sx1, and the other way round.
+        // Before each tile: every wave's halo has landed (each waited for its
+        // own DMA before the barrier) and the previous tile is done with the
+        // intermediate buffer, its staging blocks and the halo buffer about
+        // to be refilled.
+        int nb, noh0, now0;
+        lds_barrier();
+        coords(t + 1 < t_end ? t + 1 : t, nb, noh0, now0);
+        resblock_tile<C, TH, NW>(sx0, sx1, st, sstage + wave * G::S_BYTES, sbias, wf1, wf2, hofs, hpos, xr,
+                                 t + 1 < t_end, nb, noh0, now0, b, oh0, ow0, H, W, y, wave, lane);
+        if (t + 1 >= t_end) break;
+        b = nb; oh0 = noh0; ow0 = now0;
+        lds_barrier();
+        coords(t + 2 < t_end ? t + 2 : t + 1, nb, noh0, now0);
+        resblock_tile<C, TH, NW>(sx1, sx0, st, sstage + wave * G::S_BYTES, sbias, wf1, wf2, hofs, hpos, xr,
+                                 t + 2 < t_end, nb, noh0, now0, b, oh0, ow0, H, W, y, wave, lane);
+        b = nb; oh0 = noh0; ow0 = now0;
+    }
+}
+
+int device_cu_count() {
+    static const int n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        return cus;
+    }();
+    return n;
+}
+
+template <int TH, int NW, int WG_PER_CU>
+void launch_resblock(const half_t* x, const half_t* w1, const float* b1, const half_t* w2, const float* b2, half_t* y,
+                     int batch, int H, int W, hipStream_t s) {
+    const int ntiles = batch * cdiv(H, TH) * cdiv(W, 30);
+    const int slots = device_cu_count() * WG_PER_CU;
+    const int per = cdiv(ntiles, slots);
+    hipLaunchKernelGGL((resblock3x3_kernel<32, TH, NW>), dim3(cdiv(ntiles, per)), dim3(NW * 64), 0, s, x, w1, b1, w2,
+                       b2, y, H, W, batch * H * W, ntiles, per);
+}
+
 template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
@@ -982,4 +1311,37 @@ extern "C" int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W
 extern "C" int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W, const float* d_w, const float* d_bias,
                                 int OC, int relu, void* d_y, void* stream) {
     return vdk_stem_conv3x3_ex(d_feats, batch, H, W, d_w, d_bias, OC, relu, 0, d_y, stream);
+}
+
+extern "C" int vdk_resblock3x3_variant(const void* d_x, int batch, int H, int W, int C, const void* d_w1,
+                                       const float* d_b1, const void* d_w2, const float* d_b2, void* d_y,
+                                       int variant, void* stream) {
+    return guarded([&] {
+        require(d_x && d_w1 && d_b1 && d_w2 && d_b2 && d_y, "resblock3x3: NULL device pointer");
+        require(batch > 0 && H > 0 && W > 0, "resblock3x3: empty input");
+        require(C == 32, "resblock3x3: only C = 32 has a fused kernel");
+        const size_t bytes = (size_t)batch * H * W * C * 2;
+        require(bytes < (1ull << 31), "resblock3x3: too many pixels for one launch");
+        const uintptr_t xa = reinterpret_cast<uintptr_t>(d_x), ya = reinterpret_cast<uintptr_t>(d_y);
+        require(xa + bytes <= ya || ya + bytes <= xa, "resblock3x3: y must not overlap x");
+        require(aligned16(d_x) && aligned16(d_w1) && aligned16(d_w2) && aligned16(d_y) && aligned16(d_b1) &&
+                    aligned16(d_b2), "resblock3x3: device pointers must be 16-byte aligned");
+        require(variant >= -1 && variant <= 2, "resblock3x3: variant out of range");
+        const auto* x = static_cast<const half_t*>(d_x);
+        const auto* w1 = static_cast<const half_t*>(d_w1);
+        const auto* w2 = static_cast<const half_t*>(d_w2);
+        auto* y = static_cast<half_t*>(d_y);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        switch (variant) {
+            case 1: launch_resblock<6, 8, 1>(x, w1, d_b1, w2, d_b2, y, batch, H, W, s); break;
+            case 2: launch_resblock<14, 8, 1>(x, w1, d_b1, w2, d_b2, y, batch, H, W, s); break;
+            default: launch_resblock<10, 8, 1>(x, w1, d_b1, w2, d_b2, y, batch, H, W, s); break;
+        }
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_resblock3x3(const void* d_x, int batch, int H, int W, int C, const void* d_w1, const float* d_b1,
+                               const void* d_w2, const float* d_b2, void* d_y, void* stream) {
+    return vdk_resblock3x3_variant(d_x, batch, H, W, C, d_w1, d_b1, d_w2, d_b2, d_y, -1, stream);
 }

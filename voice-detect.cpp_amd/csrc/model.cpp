@@ -318,6 +318,18 @@ void Model::encode_resnet(int batch, int T) {
         void* y = ws_.act[others[2]];
         const int s = b.c1.stride;
         const int Ho = (H - 1) / s + 1, Wo = (W - 1) / s + 1;
+        if (s == 1 && !b.has_down && C == 32 && b.c1.oc == 32) {
+            // the whole block in one launch; its intermediate stays in LDS
+            if (profiling_) {
+                const double npix = (double)batch * H * W;
+                prof_begin("conv_block3x3_32", 2.0 * 2.0 * 9 * C * C * npix,
+                           2.0 * (2.0 * npix * C + 2.0 * 9 * C * C) + 8.0 * C);
+            }
+            check(vdk_resblock3x3(x, batch, H, W, C, b.c1.w, b.c1.b, b.c2.w, b.c2.b, y, stream_));
+            prof_end();
+            xi = others[2];
+            continue;
+        }
         conv(b.c1, x, batch, H, W, nullptr, 1, h);
         const void* sc = x;
         if (b.has_down) {

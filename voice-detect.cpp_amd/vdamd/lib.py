@@ -103,6 +103,9 @@ _SIGS = {
     "vdk_conv2d_tile_fits_ex": (C.c_int, [C.c_int, C.POINTER(ConvDesc)]),
     "vdk_conv2d_tile_count": (C.c_int, []),
     "vdk_conv2d_tile_fits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "vdk_resblock3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "vdk_resblock3x3_variant": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
+                                          C.c_int, _vp]),
     "vdk_stem_conv3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_tstp": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "vdk_tstp_ex": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
