@@ -37,6 +37,9 @@ int voicedetect_gpu_embed_capture(voicedetect_ctx* ctx, const float* pcm, int ba
 
 /* Per-launch timing with HIP events recorded on the context's stream. */
 int voicedetect_gpu_set_profiling(voicedetect_ctx* ctx, int on);
+/* Same, recording only launches whose name starts with name_prefix (NULL or
+ * "": all), so one kernel can be timed with few events in the stream. */
+int voicedetect_gpu_set_profiling_filter(voicedetect_ctx* ctx, int on, const char* name_prefix);
 /* Waits, then returns the number of launch records collected since the last
  * read (or -1 on error); records are read with voicedetect_gpu_profile_get. */
 int voicedetect_gpu_profile_collect(voicedetect_ctx* ctx);

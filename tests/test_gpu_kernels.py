@@ -179,6 +179,39 @@ def test_conv_every_tile_config(shape):
     assert n >= 2
 
 
+@pytest.mark.parametrize("case", [
+    # (B, H, W, C, bias, residual, relu): the register-weight 3x3 kernels'
+    # other epilogues (every tile above runs bias + residual + ReLU)
+    (2, 9, 70, 64, False, False, False),
+    (1, 5, 33, 64, True, False, True),
+    (3, 4, 31, 32, True, True, False),
+    (1, 1, 1, 64, True, True, True),
+])
+def test_conv_register_weight_tiles_plain_epilogues(case):
+    L = lib.lib()
+    B, H, W, C, with_bias, with_res, relu = case
+    rng = np.random.default_rng(B * 1000 + H * 10 + W + C)
+    x = rng.standard_normal((B, H, W, C)).astype(np.float16)
+    w = (rng.standard_normal((C, C, 3, 3)) * np.sqrt(1.0 / (9 * C))).astype(np.float16)
+    b = rng.uniform(-1, 1, C).astype(np.float32) if with_bias else None
+    res = rng.standard_normal((B, H, W, C)).astype(np.float16) if with_res else None
+    n = 0
+    for t in range(L.vdk_conv2d_tile_count()):
+        if not L.vdk_conv2d_tile_fits(t, C, C, 3, 3, 1, 1) or t < 53:
+            continue
+        announce(f"rw tile {t} case {case}")
+        got = conv_gpu(x, w, b, res, 1, 1, relu, tile=t)
+        for c in range(B):
+            r = None if res is None else res[c].astype(np.float32).transpose(2, 0, 1)
+            ref = O.conv2d(x[c].astype(np.float32).transpose(2, 0, 1), w.astype(np.float32), 1, 1, bias=b,
+                           residual=r, relu=relu)
+            ok, ratio, rel = close_report(got[c].astype(np.float32).transpose(2, 0, 1), ref, CONV_RTOL,
+                                          CONV_ATOL_RMS)
+            assert ok and rel <= 2e-3, f"tile {t} clip {c}: ratio {ratio:.3f} rel {rel:.2e}"
+        n += 1
+    assert n >= 1
+
+
 def test_conv_invariants_delta_and_zero():
     rng = np.random.default_rng(9)
     x = rng.standard_normal((2, 6, 70, 32)).astype(np.float16)

@@ -266,6 +266,12 @@ extern "C" int voicedetect_gpu_set_profiling(voicedetect_ctx* ctx, int on) {
     return 0;
 }
 
+extern "C" int voicedetect_gpu_set_profiling_filter(voicedetect_ctx* ctx, int on, const char* name_prefix) {
+    if (!ctx || !ctx->model) return 1;
+    ctx->model->set_profiling(on != 0, name_prefix ? std::string(name_prefix) : std::string());
+    return 0;
+}
+
 extern "C" int voicedetect_gpu_profile_collect(voicedetect_ctx* ctx) {
     if (!ctx || !ctx->model) return -1;
     int n = -1;

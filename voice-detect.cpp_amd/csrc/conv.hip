@@ -976,6 +976,241 @@ void launch_resblock(const half_t* x, const half_t* w1, const float* b1, const h
                        b2, y, H, W, batch * H * W, ntiles, per);
 }
 
+// ---------------------------------------------------------------------------
+// conv3x3_rw_kernel: persistent stride-1 3x3 conv (pad 1) for the narrow
+// ResNet stages, IC and OC in {32, 64}, with the plain epilogue
+// y = act(conv(x) + bias [+ residual]) (act: none or ReLU), dense f16 NHWC.
+// The machinery of the fused block: the OC/32 MFMA row blocks are split over
+// wave groups and every wave keeps the A fragments of its 32 output channels
+// (9 * IC/16 fragments, 144 VGPRs at IC = 64) in registers for the whole
+// launch; each workgroup walks a contiguous range of TH x 32 output tiles
+// (rows fastest), DMAing the next tile's (TH+2) x 34 input halo and its
+// residual tile into LDS (80/144-byte padded rows) while the current tile
+// computes; the B reads run a few MFMAs ahead; the epilogue stages each
+// 32 x 32 block per wave for 16-byte stores.  Products and sums are the
+// other conv kernels' (f16 x f16, f32 accumulation in tap-major,
+// channel-minor order, then + bias, + residual, act).
+// ---------------------------------------------------------------------------
+template <int IC, int OC, int TH, int NW>
+struct RwTile {
+    static constexpr int RBX = PadRow<IC>::RB, SPRX = PadRow<IC>::SPR;   // halo rows
+    static constexpr int RBR = PadRow<OC>::RB, SPRR = PadRow<OC>::SPR;   // residual rows
+    static constexpr int XW = 34, XPIX = (TH + 2) * XW, RPIX = TH * 32;
+    static constexpr int X_INS = (XPIX * SPRX + 63) / 64, R_INS = (RPIX * SPRR + 63) / 64;
+    static constexpr int X_IPW = (X_INS + NW - 1) / NW, R_IPW = (R_INS + NW - 1) / NW;
+    static constexpr int NWM = OC / 32, WPM = NW / NWM;                 // wave groups, waves per group
+    static constexpr int F = TH / WPM, R = TH % WPM, NB = F + (R ? 1 : 0);
+    static constexpr int NF = 9 * IC / 16;
+    static constexpr int S_BYTES = 32 * 64;                             // staging block per wave (swizzled)
+};
+
+template <int IC, int OC, int TH, int NW>
+__device__ __forceinline__ void rw_tile(const uint8_t* __restrict__ sx, uint8_t* __restrict__ sxn,
+                                        const uint8_t* __restrict__ sr, uint8_t* __restrict__ srn,
+                                        uint8_t* __restrict__ sstage, const float* __restrict__ sbias,
+                                        const half8* wf, const int* hofs, const int* hpos, const int* rofs,
+                                        const int* rpos, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t rr,
+                                        bool prefetch, bool has_res, int nb, int noh0, int now0, int b, int oh0,
+                                        int ow0, const ConvArgs& a, int wave, int lane) {
+    using G = RwTile<IC, OC, TH, NW>;
+    const int H = a.H, W = a.W;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int mg = wave / G::WPM, wr = wave - mg * G::WPM;   // wave group (32 output channels), row slot
+    if (prefetch) {
+        const int xo = ((nb * H + noh0 - 1) * W + now0 - 1) * IC * 2;
+#pragma unroll
+        for (int i = 0; i < G::X_IPW; ++i) {
+            const int ins = wave + i * NW;
+            if (ins >= G::X_INS) break;
+            const int ih = noh0 - 1 + (hpos[i] >> 8), iw = now0 - 1 + (hpos[i] & 255);
+            const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) ? (uint32_t)(xo + hofs[i])
+                                                                                            : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sxn + ins * 1024), 16, off, 0, 0, 0);
+        }
+        if (has_res) {
+            const int ro = ((nb * H + noh0) * W + now0) * OC * 2;
+#pragma unroll
+            for (int i = 0; i < G::R_IPW; ++i) {
+                const int ins = wave + i * NW;
+                if (ins >= G::R_INS) break;
+                const int ih = noh0 + (rpos[i] >> 8), iw = now0 + (rpos[i] & 255);
+                const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
+                                         ? (uint32_t)(ro + rofs[i]) : kOOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void*)(srn + ins * 1024), 16, off, 0, 0, 0);
+            }
+        }
+    }
+
+    // output row i (columns ow0 .. ow0 + 31) is one MFMA column block; its B
+    // operand for tap (kh, kw) is 32 consecutive halo pixels of halo row
+    // i + kh from column kw
+    float16v acc[G::NB];
+#pragma unroll
+    for (int q = 0; q < G::NB; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[q][r] = 0.0f;
+    conv_rows<IC, G::F, G::XW>(wf, sx, wr, G::WPM, lrow, lhalf, acc);
+    if (G::R && wr < G::R) conv_rows<IC, 1, G::XW>(wf, sx, wr + G::F * G::WPM, G::WPM, lrow, lhalf, acc + G::F);
+    // this wave's share of the next halo / residual must land before the
+    // next barrier; waiting here keeps this tile's stores out of the wait
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // act(acc + bias [+ residual]) in the MFMA layout: register g*4+e of a
+    // lane is channel 8g + 4*lhalf + e of its block, pixel column lrow
+    const int oc0 = mg * 32;
+#pragma unroll
+    for (int q = 0; q < G::NB; ++q) {
+        const int i = wr + q * G::WPM;
+        if (i >= TH) continue;
+        const uint8_t* const rrow = sr + (i * 32 + lrow) * G::RBR + oc0 * 2 + lhalf * 8;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4v bb = *reinterpret_cast<const float4v*>(sbias + oc0 + g * 8 + lhalf * 4);
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[q][g * 4 + e] + bb[e];
+            if (has_res) {
+                const half4 r = *reinterpret_cast<const half4*>(rrow + g * 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
+            }
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)(a.act == VDK_ACT_RELU ? (v[e] > 0.0f ? v[e] : 0.0f) : v[e]);
+            *reinterpret_cast<half4*>(sstage + lrow * 64 + swz<32>(lrow, g) * 16 + lhalf * 8) = h;
+        }
+        const int oh = oh0 + i;
+#pragma unroll
+        for (int hp = 0; hp < 2; ++hp) {
+            const int pix = hp * 16 + (lane >> 2), ch = lane & 3;
+            const half8 v = *reinterpret_cast<const half8*>(sstage + pix * 64 + swz<32>(pix, ch) * 16);
+            const int ow = ow0 + pix;
+            if (oh < H && ow < W)
+                *reinterpret_cast<half8*>(static_cast<half_t*>(a.y) + ((size_t)(b * H + oh) * W + ow) * OC + oc0 +
+                                          ch * 8) = v;
+        }
+    }
+}
+
+template <int IC, int OC, int TH, int NW>
+__global__ __launch_bounds__(NW * 64) void conv3x3_rw_kernel(ConvArgs a, int ntiles, int per_wg) {
+    using G = RwTile<IC, OC, TH, NW>;
+    static_assert(G::NWM * G::WPM == NW && G::WPM >= 1, "wave groups split the workgroup evenly");
+    __shared__ __attribute__((aligned(1024))) uint8_t sx0[G::X_INS * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t sx1[G::X_INS * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t sr0[G::R_INS * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t sr1[G::R_INS * 1024];
+    __shared__ __attribute__((aligned(16))) uint8_t sstage[NW * G::S_BYTES];
+    __shared__ float sbias[OC];
+
+    const int H = a.H, W = a.W;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int tiles_w = (W + 31) / 32, tiles_h = (H + TH - 1) / TH;
+    const int t_begin = blockIdx.x * per_wg;
+    const int t_end = t_begin + per_wg < ntiles ? t_begin + per_wg : ntiles;
+    if (t_begin >= t_end) return;   // the whole workgroup: no barrier is pending
+    const bool has_res = a.res != nullptr;
+
+    // A fragments of this wave's 32 output channels
+    const int oc = (wave / G::WPM) * 32 + lrow;
+    half8 wf[G::NF];
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+        for (int kk = 0; kk < IC / 16; ++kk)
+            wf[tap * (IC / 16) + kk] =
+                *reinterpret_cast<const half8*>(a.w + (size_t)(oc * 9 + tap) * IC + (kk * 2 + lhalf) * 8);
+    if (tid < OC) sbias[tid] = a.bias ? a.bias[tid] : 0.0f;
+    // this lane's DMA slots (the same for every tile): byte offset from the
+    // tile origin and (row << 8 | column), row 255 for padding slots
+    int hofs[G::X_IPW], hpos[G::X_IPW], rofs[G::R_IPW], rpos[G::R_IPW];
+#pragma unroll
+    for (int i = 0; i < G::X_IPW; ++i) {
+        const int p = (wave + i * NW) * 64 + lane;
+        const int r = p / G::SPRX, cc = p - r * G::SPRX;
+        const int hr = r / G::XW, hc = r - hr * G::XW;
+        hofs[i] = (hr * W + hc) * IC * 2 + cc * 16;
+        hpos[i] = (r < G::XPIX && cc < IC / 8) ? (hr << 8 | hc) : (255 << 8);
+    }
+#pragma unroll
+    for (int i = 0; i < G::R_IPW; ++i) {
+        const int p = (wave + i * NW) * 64 + lane;
+        const int r = p / G::SPRR, cc = p - r * G::SPRR;
+        const int pr = r / 32, pc = r - pr * 32;
+        rofs[i] = (pr * W + pc) * OC * 2 + cc * 16;
+        rpos[i] = (r < G::RPIX && cc < OC / 8) ? (pr << 8 | pc) : (255 << 8);
+    }
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, a.npix_in * IC * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(has_res ? a.res : a.x), 0, has_res ? a.npix * OC * 2 : 0,
+                                          0x00020000);
+    auto coords = [&](int t, int& b, int& oh0, int& ow0) {
+        const int th = t % tiles_h, r = t / tiles_h;
+        const int tw = r % tiles_w;
+        b = r / tiles_w;
+        oh0 = th * TH;
+        ow0 = tw * 32;
+    };
+
+    int b, oh0, ow0;
+    coords(t_begin, b, oh0, ow0);
+    // the first tile's halo and residual: a tile body with nothing to compute
+    // is not worth a second code path, so issue them here directly
+    {
+        const int xo = ((b * H + oh0 - 1) * W + ow0 - 1) * IC * 2;
+#pragma unroll
+        for (int i = 0; i < G::X_IPW; ++i) {
+            const int ins = wave + i * NW;
+            if (ins >= G::X_INS) break;
+            const int ih = oh0 - 1 + (hpos[i] >> 8), iw = ow0 - 1 + (hpos[i] & 255);
+            const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) ? (uint32_t)(xo + hofs[i])
+                                                                                            : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx0 + ins * 1024), 16, off, 0, 0, 0);
+        }
+        if (has_res) {
+            const int ro = ((b * H + oh0) * W + ow0) * OC * 2;
+#pragma unroll
+            for (int i = 0; i < G::R_IPW; ++i) {
+                const int ins = wave + i * NW;
+                if (ins >= G::R_INS) break;
+                const int ih = oh0 + (rpos[i] >> 8), iw = ow0 + (rpos[i] & 255);
+                const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
+                                         ? (uint32_t)(ro + rofs[i]) : kOOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void*)(sr0 + ins * 1024), 16, off, 0, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // weights in VGPRs and this wave's share of the first tile
+#pragma unroll 1
+    for (int t = t_begin; t < t_end; t += 2) {
+        // two tiles per trip so each buffer pair has a fixed role
+        int nb, noh0, now0;
+        lds_barrier();
+        coords(t + 1 < t_end ? t + 1 : t, nb, noh0, now0);
+        rw_tile<IC, OC, TH, NW>(sx0, sx1, sr0, sr1, sstage + wave * G::S_BYTES, sbias, wf, hofs, hpos, rofs, rpos,
+                                xr, rr, t + 1 < t_end, has_res, nb, noh0, now0, b, oh0, ow0, a, wave, lane);
+        if (t + 1 >= t_end) break;
+        b = nb; oh0 = noh0; ow0 = now0;
+        lds_barrier();
+        coords(t + 2 < t_end ? t + 2 : t + 1, nb, noh0, now0);
+        rw_tile<IC, OC, TH, NW>(sx1, sx0, sr1, sr0, sstage + wave * G::S_BYTES, sbias, wf, hofs, hpos, rofs, rpos,
+                                xr, rr, t + 2 < t_end, has_res, nb, noh0, now0, b, oh0, ow0, a, wave, lane);
+        b = nb; oh0 = noh0; ow0 = now0;
+    }
+}
+
+template <int IC, int OC, int TH, int NW>
+void launch_rw(const ConvArgs& a, hipStream_t s) {
+    const int B = a.npix / (a.Ho * a.Wo);
+    const int ntiles = B * cdiv(a.Ho, TH) * cdiv(a.Wo, 32);
+    const int per = cdiv(ntiles, device_cu_count());
+    hipLaunchKernelGGL((conv3x3_rw_kernel<IC, OC, TH, NW>), dim3(cdiv(ntiles, per)), dim3(NW * 64), 0, s, a, ntiles,
+                       per);
+}
+
 template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
@@ -986,12 +1221,14 @@ void launch_igemm(const ConvArgs& a, hipStream_t s) {
 struct TileCfg {
     int bm, bn, kc;
     void (*launch)(const ConvArgs&, hipStream_t);
-    bool halo;   // 3x3 stride-1 pad-1 dilation-1 only
+    bool halo;       // 3x3 stride-1 pad-1 dilation-1 only
+    int rw_ic = 0;   // register-weight kernels: exactly IC = rw_ic and OC = bm, plain epilogue
 };
 
 // Entries 0-13 are the register-staged kernel (any layout; the only one with
 // KC=16 for IC % 32 != 0), 14-25 the LDS-DMA kernel, 26-32 the halo kernel,
-// 33+ LDS-DMA tiles with 8 waves per workgroup.
+// 33-52 LDS-DMA tiles with 8 waves per workgroup, 53+ the register-weight
+// persistent 3x3 kernel.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -1049,6 +1286,10 @@ const TileCfg kTiles[] = {
     {256, 64, 32, launch_dma<256, 64, 64, 64, 32, 2>},    // 50
     {256, 64, 64, launch_dma<256, 64, 64, 64, 64, 2>},    // 51
     {128, 32, 64, launch_dma<128, 32, 32, 32, 64, 2>},    // 52
+    {64, 128, 64, launch_rw<64, 64, 4, 8>, true, 64},     // 53: register-weight persistent 3x3
+    {64, 192, 64, launch_rw<64, 64, 6, 8>, true, 64},     // 54
+    {64, 64, 64, launch_rw<64, 64, 2, 8>, true, 64},      // 55
+    {32, 128, 32, launch_rw<32, 32, 4, 8>, true, 32},     // 56
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -1058,9 +1299,18 @@ bool is_s1_3x3(const ConvArgs& a) {
 
 constexpr int kFirstDma = 14, kFirstHalo = 26, kFirstDma8 = 33;
 
+// The register-weight kernels take the plain epilogue only: bias, residual,
+// ReLU or none, dense f16 NHWC in and out.
+bool plain_epilogue(const ConvArgs& a) {
+    return !a.gate && !a.post_scale && !a.tanh_after && !a.y_f32 && !a.y_tr && !a.bias_bs && !a.split &&
+           (a.act == VDK_ACT_NONE || (a.act == VDK_ACT_RELU && a.clamp_hi <= 0.0f)) && a.xs == a.IC &&
+           a.ys == a.OC && (!a.res || a.rs == a.OC);
+}
+
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
+    if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
     if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8))) return false;   // split: DMA only
     return a.IC % t.kc == 0;
 }
@@ -1075,7 +1325,9 @@ int tile_override() {
 }
 
 // Per-layer-class defaults, from a sweep of every ResNet34 conv shape at
-// batch 64 on MI355X (narrow 3x3 stride-1 layers: the 32-channel halo tile;
+// batch 64 on MI355X (64-channel 3x3 stride-1 layers with the plain
+// epilogue: the register-weight kernel; other narrow 3x3 stride-1 layers: the
+// 32-channel halo tile;
 // 128 output channels: the 128x128 DMA tile with KC = 32; the rest: DMA
 // implicit GEMM with the widest OC tile that divides OC; IC % 32 != 0: the
 // register-staged kernel with KC = 16).  OC that no tile divides runs on
@@ -1084,6 +1336,7 @@ int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
+    if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (!a.split && is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return 28;
     if (a.IC % 32 == 0 && a.OC == 128) return 39;   // 128x128 tile, KC = 32
     if (a.IC % 64 == 0) return bm == 128 ? 18 : (bm == 64 ? 15 : 14);
@@ -1237,6 +1490,8 @@ vdk_conv_desc plain_desc(const void* d_x, int batch, int H, int W, int IC, const
     return d;
 }
 
+// The fields of a descriptor that decide which tiles apply (shape, layout,
+// which epilogue stages are present); pointers only by presence.
 ConvArgs shape_args(const vdk_conv_desc& d) {
     ConvArgs a{};
     a.split = d.split ? 1 : 0;
@@ -1244,6 +1499,18 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.sh = d.stride_h ? d.stride_h : 1; a.sw = d.stride_w ? d.stride_w : 1;
     a.ph = d.pad_h; a.pw = d.pad_w;
     a.dh = d.dil_h ? d.dil_h : 1; a.dw = d.dil_w ? d.dil_w : 1;
+    a.xs = d.x_stride ? d.x_stride : d.IC;
+    a.ys = d.y_stride ? d.y_stride : d.OC;
+    a.rs = d.res_stride ? d.res_stride : d.OC;
+    a.res = static_cast<const half_t*>(d.residual);
+    a.gate = d.gate;
+    a.post_scale = d.post_scale;
+    a.act = d.act;
+    a.clamp_hi = d.act == VDK_ACT_RELU ? d.clamp_hi : 0.0f;
+    a.tanh_after = d.tanh_after ? 1 : 0;
+    a.y_f32 = d.y_f32 ? 1 : 0;
+    a.y_tr = d.y_time_major ? 1 : 0;
+    a.bias_bs = d.bias_batch_stride;
     return a;
 }
 

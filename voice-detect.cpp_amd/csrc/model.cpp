@@ -247,7 +247,9 @@ void Model::alloc_resnet_workspace(int batch, int T) {
 }
 
 void Model::prof_begin(const char* name, double flops, double bytes) {
+    prof_open_ = false;
     if (!profiling_) return;
+    if (!prof_filter_.empty() && std::strncmp(name, prof_filter_.c_str(), prof_filter_.size()) != 0) return;
     auto ev = [&] {
         hipEvent_t e;
         if (!event_pool_.empty()) { e = event_pool_.back(); event_pool_.pop_back(); }
@@ -257,11 +259,13 @@ void Model::prof_begin(const char* name, double flops, double bytes) {
     Pending p{name, flops, bytes, ev(), ev()};
     VDK_HIP(hipEventRecord(p.a, stream_));
     pending_.push_back(p);
+    prof_open_ = true;
 }
 
 void Model::prof_end() {
-    if (!profiling_) return;
+    if (!prof_open_) return;
     VDK_HIP(hipEventRecord(pending_.back().b, stream_));
+    prof_open_ = false;
 }
 
 void Model::conv(const Conv& c, const void* x, int batch, int H, int W, const void* res, int relu, void* y) {
@@ -409,9 +413,10 @@ hipStream_t Model::stream() {
     return stream_;
 }
 
-void Model::set_profiling(bool on) {
+void Model::set_profiling(bool on, const std::string& name_prefix) {
     std::lock_guard<std::mutex> lock(mu_);
     profiling_ = on;
+    prof_filter_ = name_prefix;
 }
 
 std::vector<ProfileRecord> Model::take_profile() {

@@ -87,7 +87,7 @@ public:
     void synchronize();
     hipStream_t stream();
 
-    void set_profiling(bool on);
+    void set_profiling(bool on, const std::string& name_prefix = std::string());
     // Waits for the stream and returns the per-launch records since the last call.
     std::vector<ProfileRecord> take_profile();
 
@@ -274,6 +274,8 @@ private:
     Workspace ws_;
 
     bool profiling_ = false;
+    std::string prof_filter_;   // record only launches whose name starts with this (empty: all)
+    bool prof_open_ = false;    // the last prof_begin recorded a start event
     struct Pending { std::string name; double flops, bytes; hipEvent_t a, b; };
     std::vector<Pending> pending_;
     std::vector<hipEvent_t> event_pool_;

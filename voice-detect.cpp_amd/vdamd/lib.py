@@ -76,6 +76,7 @@ _SIGS = {
     "voicedetect_gpu_stream": (_vp, [_vp]),
     "voicedetect_gpu_embed_capture": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp, C.POINTER(C.c_int), _vp, _vp]),
     "voicedetect_gpu_set_profiling": (C.c_int, [_vp, C.c_int]),
+    "voicedetect_gpu_set_profiling_filter": (C.c_int, [_vp, C.c_int, C.c_char_p]),
     "voicedetect_gpu_profile_collect": (C.c_int, [_vp]),
     "voicedetect_gpu_profile_get": (C.c_int, [_vp, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_double),
                                               C.POINTER(C.c_double), C.POINTER(C.c_double)]),
@@ -309,8 +310,11 @@ class Context:
         if self.L.voicedetect_gpu_synchronize(self.ctx) != 0:
             raise VdkError(self.last_error())
 
-    def set_profiling(self, on):
-        self.L.voicedetect_gpu_set_profiling(self.ctx, int(on))
+    def set_profiling(self, on, name_prefix=None):
+        if name_prefix:
+            self.L.voicedetect_gpu_set_profiling_filter(self.ctx, int(on), name_prefix.encode())
+        else:
+            self.L.voicedetect_gpu_set_profiling(self.ctx, int(on))
 
     def profile(self):
         n = self.L.voicedetect_gpu_profile_collect(self.ctx)
