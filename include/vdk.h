@@ -33,6 +33,7 @@ void*       vdk_malloc(size_t bytes);          /* NULL on failure */
 int         vdk_free(void* p);
 int         vdk_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int         vdk_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int         vdk_memcpy_d2d(void* dst, const void* src, size_t bytes);
 int         vdk_memset(void* dst, int value, size_t bytes);
 int         vdk_synchronize(void);
 const char* vdk_last_error(void);             /* thread-local; "" if none */

@@ -253,7 +253,10 @@ void Model::prof_begin(const char* name, double flops, double bytes) {
     auto ev = [&] {
         hipEvent_t e;
         if (!event_pool_.empty()) { e = event_pool_.back(); event_pool_.pop_back(); }
-        else VDK_HIP(hipEventCreate(&e));
+        // timing-only events: no system-scope fence, so recording one does
+        // not write back and invalidate the caches around the kernel it brackets
+        // (take_profile synchronizes the stream before reading them)
+        else VDK_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
         return e;
     };
     Pending p{name, flops, bytes, ev(), ev()};

@@ -94,6 +94,10 @@ extern "C" int vdk_memcpy_d2h(void* dst, const void* src, size_t bytes) {
     return guarded([&] { VDK_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost)); });
 }
 
+extern "C" int vdk_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+    return guarded([&] { VDK_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice)); });
+}
+
 extern "C" int vdk_memset(void* dst, int value, size_t bytes) {
     return guarded([&] { VDK_HIP(hipMemset(dst, value, bytes)); });
 }

@@ -87,6 +87,7 @@ _SIGS = {
     "vdk_free": (C.c_int, [_vp]),
     "vdk_memcpy_h2d": (C.c_int, [_vp, _vp, C.c_size_t]),
     "vdk_memcpy_d2h": (C.c_int, [_vp, _vp, C.c_size_t]),
+    "vdk_memcpy_d2d": (C.c_int, [_vp, _vp, C.c_size_t]),
     "vdk_memset": (C.c_int, [_vp, C.c_int, C.c_size_t]),
     "vdk_synchronize": (C.c_int, []),
     "vdk_last_error": (C.c_char_p, []),
