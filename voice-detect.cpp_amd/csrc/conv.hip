@@ -1211,6 +1211,261 @@ void launch_rw(const ConvArgs& a, hipStream_t s) {
                        per);
 }
 
+// ---------------------------------------------------------------------------
+// conv3x3_band_kernel: stride-1 3x3 conv (pad 1) for the wide layers
+// (IC % 16 == 0, OC % 128 == 0).  A workgroup of 8 waves owns a band of TH
+// full image rows of one clip and 128 output channels; the band's pixels,
+// flattened row-major, form NB = 2*NBW MFMA column blocks of 32 (so a
+// 75- or 38-wide map wastes at most a couple of percent of the lanes, where
+// 32-wide row tiles would waste 22-40 %).  Per 16-channel chunk of the input
+// the workgroup DMAs into LDS
+//   * the weights of all 9 taps for its 128 output channels (rows (tap, oc)
+//     of 32 bytes, the two 16-byte halves swapped on every other group of 8
+//     rows so an operand read of 16 consecutive rows hits 16 distinct bank
+//     groups), and
+//   * the band's (TH+2) x (W+2) input halo (48-byte rows: 32 bytes of
+//     channels + 16 of padding, so 16 consecutive rows start in 16 distinct
+//     bank groups and a tap is a constant offset from a lane's base row),
+// double-buffered: chunk k+1 is in flight while chunk k runs 9 taps x NBW
+// MFMAs per wave (wave w: output channels 32*(w%4).., column blocks
+// NBW*(w/4)..).  Every B fragment is read once per tap from the halo instead
+// of being re-fetched per tap as an im2col row.  The epilogue stages each
+// 32x32 block per wave through LDS and runs the shared finish8 epilogue on
+// 16-byte channel rows.  Products and sums are the other conv kernels'
+// (f16 x f16 -> f32, tap-major / channel-minor within a chunk).
+// ---------------------------------------------------------------------------
+template <int TH, int NBW>
+struct BandTile {
+    static constexpr int NW = 8, OCB = 128;
+    static constexpr int A_BYTES = 9 * OCB * 32, A_INS = A_BYTES / 1024;   // weights of one chunk
+    static constexpr int NB = 2 * NBW;                                    // column blocks per band
+    static constexpr int MAXW = NB * 32 / TH;                             // widest map a band holds
+    static constexpr int XPIX = (TH + 2) * (MAXW + 2);                    // halo pixels, upper bound
+    static constexpr int RB = 48;                                         // halo row bytes
+    static constexpr int X_INS = (XPIX * 3 + 63) / 64;
+    static constexpr int A_IPW = (A_INS + NW - 1) / NW, X_IPW = (X_INS + NW - 1) / NW;
+    static constexpr int STAGE = A_BYTES + X_INS * 1024;                  // one pipeline buffer pair
+    // epilogue: the band's residual rows (128 channels + 16 bytes of padding)
+    // and a 2 KB f16 staging block per wave, in the freed pipeline buffers
+    static constexpr int RRB = 272, RES_BYTES = NB * 32 * RRB, SBLK = 32 * 64;
+    static_assert(RES_BYTES + NW * SBLK <= 2 * STAGE, "the epilogue fits the pipeline buffers");
+};
+
+// Weight slot p of a chunk: row p/2 = (tap, oc), 16-byte half (p & 1) xor
+// ((row >> 3) & 1) of the row's 16 channels; recomputed per chunk from the
+// lane (a few integer ops) rather than held in registers across the loop.
+template <int TH, int NBW>
+__device__ __forceinline__ void band_issue(uint8_t* __restrict__ sa, uint8_t* __restrict__ sx, int c0, int oc0,
+                                           int IC, const int* xoff, __amdgpu_buffer_rsrc_t wr,
+                                           __amdgpu_buffer_rsrc_t xr, int wave, int lane) {
+    using G = BandTile<TH, NBW>;
+    asm volatile("" : "+v"(lane));
+#pragma unroll
+    for (int i = 0; i < G::A_IPW; ++i) {
+        const int ins = wave + i * G::NW;
+        if (ins >= G::A_INS) break;
+        const int p = ins * 64 + lane;
+        const int row = p >> 1, tap = row >> 7, oc = row & 127;
+        const int half = (p & 1) ^ ((row >> 3) & 1);
+        const uint32_t off = (uint32_t)((((oc0 + oc) * 9 + tap) * IC + c0) * 2 + half * 16);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(sa + ins * 1024), 16, off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < G::X_IPW; ++i) {
+        const int ins = wave + i * G::NW;
+        if (ins >= G::X_INS) break;
+        const uint32_t off = xoff[i] < 0 ? kOOB : (uint32_t)(xoff[i] + c0 * 2);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx + ins * 1024), 16, off, 0, 0, 0);
+    }
+}
+
+// One chunk: the next chunk's DMA (into the other buffer pair, passed as
+// distinct __restrict__ pointers so the reads below are not made to wait for
+// it), then 9 taps x NBW MFMAs with the fragment reads one tap ahead.
+template <int TH, int NBW>
+__device__ __forceinline__ void band_chunk(const uint8_t* __restrict__ sa, const uint8_t* __restrict__ sx,
+                                           uint8_t* __restrict__ sa_n, uint8_t* __restrict__ sx_n, bool prefetch,
+                                           int c0n, int oc0, int IC, const int* xoff, __amdgpu_buffer_rsrc_t wr,
+                                           __amdgpu_buffer_rsrc_t xr, int abase, int* bb, int hw,
+                                           float16v* acc, int wave, int lane) {
+    using G = BandTile<TH, NBW>;
+    if (prefetch) band_issue<TH, NBW>(sa_n, sx_n, c0n, oc0, IC, xoff, wr, xr, wave, lane);
+    // the B bases go behind an empty asm per chunk: otherwise the 9 x NBW
+    // (base + tap offset) sums are hoisted out of the chunk loop and spill
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) asm volatile("" : "+v"(bb[j]));
+    // the 9 x NBW MFMAs as one sequence of steps (tap-major); B fragments are
+    // read D steps ahead through a D-slot ring, the next tap's A fragment at
+    // the first step of the current tap
+    constexpr int S = 9 * NBW, D = NBW > 4 ? 2 : 3;
+    half8 aq[2], bq[D];
+    auto load_a = [&](int tap, int slot) {
+        aq[slot] = *reinterpret_cast<const half8*>(sa + abase + tap * G::OCB * 32);
+    };
+    auto load_b = [&](int st, int slot) {
+        const int tap = st / NBW, j = st - tap * NBW;
+        const int kh = tap / 3, kw = tap - kh * 3;
+        bq[slot] = *reinterpret_cast<const half8*>(sx + bb[j] + (kh * hw + kw) * G::RB);
+    };
+    load_a(0, 0);
+#pragma unroll
+    for (int st = 0; st < D; ++st) load_b(st, st);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+        const int tap = st / NBW, j = st - tap * NBW;
+        const half8 cur = bq[st % D];
+        if (st + D < S) load_b(st + D, st % D);
+        if (j == 0 && tap + 1 < 9) load_a(tap + 1, (tap + 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq[tap & 1], cur, acc[j], 0, 0, 0);
+    }
+}
+
+template <int TH, int NBW>
+__global__ __launch_bounds__(512) void conv3x3_band_kernel(ConvArgs a) {
+    using G = BandTile<TH, NBW>;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
+    uint8_t* const sa0 = smem;
+    uint8_t* const sx0 = smem + G::A_BYTES;
+    uint8_t* const sa1 = smem + G::STAGE;
+    uint8_t* const sx1 = sa1 + G::A_BYTES;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int H = a.H, W = a.W, IC = a.IC, HW = W + 2;
+    const int bands = (H + TH - 1) / TH;
+    const int b = blockIdx.x / bands, r0 = (blockIdx.x - b * bands) * TH;
+    const int oc0 = blockIdx.y * G::OCB;
+    const int mb = wave & 3, ng = wave >> 2;
+    const int npx = TH * W;   // band pixels (rows past H are computed and dropped)
+
+    // this lane's halo DMA slots, as byte offsets at channel 0 (add 2*c0 per chunk)
+    int xoff[G::X_IPW];
+#pragma unroll
+    for (int i = 0; i < G::X_IPW; ++i) {
+        const int p = (wave + i * G::NW) * 64 + lane;
+        const int hrow = p / 3, s = p - hrow * 3;
+        const int hr = hrow / HW, hc = hrow - hr * HW;
+        const int ih = r0 - 1 + hr, iw = hc - 1;
+        const bool ok = s < 2 && hr < TH + 2 && ih >= 0 && ih < H && iw >= 0 && iw < W;
+        xoff[i] = ok ? (int)(((size_t)(b * H + ih) * W + iw) * a.xs * 2) + s * 16 : -1;
+    }
+    // operand read bases: A row (tap, mb*32 + lrow) with its halves swapped
+    // on odd groups of 8 rows; B halo row of pixel p = block*32 + lrow
+    const int abase = (mb * 32 + lrow) * 32 + ((lhalf ^ ((lrow >> 3) & 1)) * 16);
+    int bbase[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        int p = (ng * NBW + j) * 32 + lrow;
+        if (p >= npx) p = 0;   // masked lane: any valid row, result dropped
+        const int r = p / W, c = p - r * W;
+        bbase[j] = (r * HW + c) * G::RB + lhalf * 16;
+    }
+    const __amdgpu_buffer_rsrc_t wr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)((size_t)a.OC * 9 * IC * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + IC) * 2), 0x00020000);
+
+    float16v acc[NBW];
+#pragma unroll
+    for (int j = 0; j < NBW; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+
+    const int nk = IC / 16;
+    band_issue<TH, NBW>(sa0, sx0, 0, oc0, IC, xoff, wr, xr, wave, lane);
+#pragma unroll 1
+    for (int k = 0; k < nk; k += 2) {
+        // chunk k: this wave's DMA has landed (nothing else is outstanding),
+        // then every wave's has, and chunk k-1's reads of the other pair are done
+        __builtin_amdgcn_s_waitcnt(0);
+        lds_barrier();
+        band_chunk<TH, NBW>(sa0, sx0, sa1, sx1, k + 1 < nk, (k + 1) * 16, oc0, IC, xoff, wr, xr, abase, bbase, HW,
+                            acc, wave, lane);
+        if (k + 1 >= nk) break;
+        __builtin_amdgcn_s_waitcnt(0);
+        lds_barrier();
+        band_chunk<TH, NBW>(sa1, sx1, sa0, sx0, k + 2 < nk, (k + 2) * 16, oc0, IC, xoff, wr, xr, abase, bbase, HW,
+                            acc, wave, lane);
+    }
+    lds_barrier();   // every wave is done reading the buffers the epilogue reuses
+
+    // Epilogue y = act(acc + bias [+ residual]) in the MFMA layout (register
+    // g*4+e of a lane: channel 8g + 4*lhalf + e of its 32-channel block,
+    // pixel lrow of the column block).  The band's residual rows arrive in one
+    // DMA burst into the freed pipeline buffers and the bias sits in
+    // registers, so no global load waits behind a store; each finished 32x32
+    // block goes through the wave's f16 staging block to 16-byte channel-row
+    // stores.
+    const bool has_res = a.res != nullptr;
+    uint8_t* const sres = smem;
+    uint8_t* const sstg = smem + G::RES_BYTES + wave * G::SBLK;
+    const int ocw = oc0 + mb * 32;                   // this wave's first output channel
+    float bias[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bias[g * 4 + e] = a.bias ? a.bias[ocw + g * 8 + lhalf * 4 + e] : 0.0f;
+    if (has_res) {
+        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)a.res, 0, (int)(((size_t)(a.npix - 1) * a.rs + a.OC) * 2), 0x00020000);
+        constexpr int SPR = G::RRB / 16;             // 17 slots per row, the last is padding
+        const int nins = (npx * SPR + 63) / 64;
+        for (int ins = wave; ins < nins; ins += G::NW) {
+            const int p = ins * 64 + lane;
+            const int px = p / SPR, ch = p - px * SPR;
+            const int r = px / W, c = px - r * W;
+            const bool ok = ch < 16 && px < npx && r0 + r < H;
+            const uint32_t off =
+                ok ? (uint32_t)((((size_t)(b * H + r0 + r) * W + c) * a.rs + oc0) * 2 + ch * 16) : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void*)(sres + ins * 1024), 16, off, 0, 0, 0);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    lds_barrier();
+    half_t* const y = static_cast<half_t*>(a.y);
+    const bool relu = a.act == VDK_ACT_RELU;
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const int p0 = (ng * NBW + j) * 32;
+        int pr = p0 + lrow;
+        pr = pr < npx ? pr : npx - 1;
+        const uint8_t* const rrow = sres + pr * G::RRB + (mb * 32 + lhalf * 4) * 2;
+        uint8_t* const srow = sstg + lrow * 64 + lhalf * 8;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[j][g * 4 + e] + bias[g * 4 + e];
+            if (has_res) {
+                const half4 r4 = *reinterpret_cast<const half4*>(rrow + g * 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] += (float)r4[e];
+            }
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)(relu ? (v[e] > 0.0f ? v[e] : 0.0f) : v[e]);
+            *reinterpret_cast<half4*>(srow + (swz<32>(lrow, g) * 16)) = h;
+        }
+#pragma unroll
+        for (int hp = 0; hp < 2; ++hp) {
+            const int pix = hp * 16 + (lane >> 2), ch = lane & 3;
+            const half8 v8 = *reinterpret_cast<const half8*>(sstg + pix * 64 + swz<32>(pix, ch) * 16);
+            const int p = p0 + pix, r = p / W, c = p - r * W;
+            if (p < npx && r0 + r < H)
+                *reinterpret_cast<half8*>(y + ((size_t)(b * H + r0 + r) * W + c) * a.ys + ocw + ch * 8) = v8;
+        }
+    }
+}
+
+template <int TH, int NBW>
+void launch_band(const ConvArgs& a, hipStream_t s) {
+    const int B = a.npix / (a.Ho * a.Wo);
+    hipLaunchKernelGGL((conv3x3_band_kernel<TH, NBW>), dim3(B * cdiv(a.H, TH), a.OC / 128), dim3(512), 0, s, a);
+}
+
 template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
@@ -1223,12 +1478,13 @@ struct TileCfg {
     void (*launch)(const ConvArgs&, hipStream_t);
     bool halo;       // 3x3 stride-1 pad-1 dilation-1 only
     int rw_ic = 0;   // register-weight kernels: exactly IC = rw_ic and OC = bm, plain epilogue
+    int band_w = 0;  // band kernels: W <= band_w, OC % 128 == 0, IC % 16 == 0
 };
 
 // Entries 0-13 are the register-staged kernel (any layout; the only one with
 // KC=16 for IC % 32 != 0), 14-25 the LDS-DMA kernel, 26-32 the halo kernel,
-// 33-52 LDS-DMA tiles with 8 waves per workgroup, 53+ the register-weight
-// persistent 3x3 kernel.
+// 33-52 LDS-DMA tiles with 8 waves per workgroup, 53-56 the register-weight
+// persistent 3x3 kernel, 57+ the band kernel for wide 3x3 layers.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -1290,6 +1546,9 @@ const TileCfg kTiles[] = {
     {64, 192, 64, launch_rw<64, 64, 6, 8>, true, 64},     // 54
     {64, 64, 64, launch_rw<64, 64, 2, 8>, true, 64},      // 55
     {32, 128, 32, launch_rw<32, 32, 4, 8>, true, 32},     // 56
+    {128, 384, 16, launch_band<5, 6>, true, 0, BandTile<5, 6>::MAXW},   // 57: band kernels
+    {128, 192, 16, launch_band<5, 3>, true, 0, BandTile<5, 3>::MAXW},   // 58
+    {128, 320, 16, launch_band<4, 5>, true, 0, BandTile<4, 5>::MAXW},   // 59
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -1311,6 +1570,7 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
+    if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % 128 == 0 && a.IC % 16 == 0;
     if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8))) return false;   // split: DMA only
     return a.IC % t.kc == 0;
 }
@@ -1326,8 +1586,9 @@ int tile_override() {
 
 // Per-layer-class defaults, from a sweep of every ResNet34 conv shape at
 // batch 64 on MI355X (64-channel 3x3 stride-1 layers with the plain
-// epilogue: the register-weight kernel; other narrow 3x3 stride-1 layers: the
-// 32-channel halo tile;
+// epilogue: the register-weight kernel; 128-channel ones whose map is 39-76
+// wide: the band kernel; other narrow 3x3 stride-1 layers: the 32-channel
+// halo tile;
 // 128 output channels: the 128x128 DMA tile with KC = 32; the rest: DMA
 // implicit GEMM with the widest OC tile that divides OC; IC % 32 != 0: the
 // register-staged kernel with KC = 16).  OC that no tile divides runs on
@@ -1337,6 +1598,7 @@ int pick_tile(const ConvArgs& a) {
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
+    if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
     if (!a.split && is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return 28;
     if (a.IC % 32 == 0 && a.OC == 128) return 39;   // 128x128 tile, KC = 32
     if (a.IC % 64 == 0) return bm == 128 ? 18 : (bm == 64 ? 15 : 14);
@@ -1499,6 +1761,7 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.sh = d.stride_h ? d.stride_h : 1; a.sw = d.stride_w ? d.stride_w : 1;
     a.ph = d.pad_h; a.pw = d.pad_w;
     a.dh = d.dil_h ? d.dil_h : 1; a.dw = d.dil_w ? d.dil_w : 1;
+    a.H = d.H; a.W = d.W;
     a.xs = d.x_stride ? d.x_stride : d.IC;
     a.ys = d.y_stride ? d.y_stride : d.OC;
     a.rs = d.res_stride ? d.res_stride : d.OC;
