@@ -123,6 +123,31 @@ def dominant_pass(ctx, d_pcm, d_out, batch, n, steps, name):
     return recs, wall * 1e3
 
 
+def registry_bench(L, d_emb, batch, dim, rows, k, steps):
+    """Identify: the batch's embeddings against `rows` random unit rows, top k
+    (vdk_registry_topk; f64 sums of exact f32 products)."""
+    rng = np.random.default_rng(99)
+    reg = rng.standard_normal((rows, dim)).astype(np.float32)
+    reg /= np.linalg.norm(reg, axis=1, keepdims=True)
+    d_reg = lib.DeviceBuffer.from_array(reg)
+    ws = L.vdk_registry_topk_workspace_size(batch, rows, k)
+    d_ws, d_idx, d_sc = lib.DeviceBuffer(ws), lib.DeviceBuffer(batch * k * 4), lib.DeviceBuffer(batch * k * 4)
+    call = lambda: lib.check(L.vdk_registry_topk(d_emb.ptr, batch, d_reg.ptr, rows, dim, k, d_ws.ptr, ws,
+                                                 d_idx.ptr, d_sc.ptr, None))
+    for _ in range(3):
+        call()
+    lib.check(L.vdk_synchronize())
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call()
+    lib.check(L.vdk_synchronize())
+    dt = (time.perf_counter() - t0) / steps
+    flops = 2.0 * batch * rows * dim
+    return {"queries": batch, "rows": rows, "dim": dim, "k": k, "ms_per_call": round(dt * 1e3, 4),
+            "queries_per_s": round(batch / dt, 1), "f64_tflops": round(flops / dt / 1e12, 3),
+            "f64_peak_tflops": 78.6, "registry_gbs": round(rows * dim * 4 / dt / 1e9, 1)}
+
+
 def cpu_baseline(model, gguf_path, pcm, n_seconds, min_seconds=10.0):
     """The oracle on the host: rounds of `threads` clips (cycling through the
     batch's clips) until at least min_seconds of wall time have passed."""
@@ -171,6 +196,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--model", choices=sorted(MODELS), default="resnet34")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--registry", type=int, default=0,
+                    help="also time identify: the batch's embeddings scored against this many enrolled rows, top 10")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the bench, run 3 device-to-device copies of this many MiB (PMC traffic calibration)")
     args = ap.parse_args()
@@ -258,6 +285,8 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": model["dtype"],
         "data": "synthetic", "config": model["config"], "roofline": roofline,
     }
+    if args.registry > 0:
+        out["registry"] = registry_bench(L, d_out, batch, ctx.dim, args.registry, 10, args.steps)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(model, path, pcm, n / 16000.0)
     ctx.close()

@@ -223,6 +223,19 @@ int vdk_asp_pool(const float* d_logits, int l_stride, const void* d_x, int x_str
  * skipped when the norm is 0).  In place on x [B][dim]. */
 int vdk_l2norm(float* d_x, int batch, int dim, void* stream);
 
+/* ---- registry scoring: identify queries against enrolled embeddings ----
+ * No counterpart in the reference's code: README.md:15 promises `identify`,
+ * which no function or ABI symbol provides; the scoring follows its verify
+ * (src/model.cpp:65-78, distance = 1 - sum(ea*eb) in double).
+ * scores S[b][n] = sum_d q[b][d] * reg[n][d], each f32 x f32 product exact in
+ * f64 and summed in f64; writes the k best rows per query (1 <= k <= 64,
+ * k <= N) as idx[b][j] / score[b][j] (f32), highest first, equal scores by the
+ * lower row index.  q [B][D], reg [N][D] f32 device (D % 4 == 0, 16-byte
+ * aligned); d_work of at least vdk_registry_topk_workspace_size(B, N, k) bytes. */
+size_t vdk_registry_topk_workspace_size(int B, int N, int k);
+int vdk_registry_topk(const float* d_queries, int B, const float* d_registry, int N, int D, int k,
+                      void* d_work, size_t work_bytes, int* d_idx, float* d_score, void* stream);
+
 /* ---- CAM++ helpers (src/encoder_campplus.cpp) ---- */
 /* y = act(x * scale[c] + shift[c]) over rows x C channels (the standalone
  * BatchNorm -> ReLU of each dense layer / transit, src/encoder_campplus.cpp:110-134). */

@@ -46,6 +46,28 @@ int voicedetect_gpu_profile_collect(voicedetect_ctx* ctx);
 int voicedetect_gpu_profile_get(voicedetect_ctx* ctx, int i, char* name, int name_cap,
                                 double* ms, double* flops, double* bytes);
 
+/* ---- identify: score clips against an enrolled registry ----
+ * No counterpart in the reference's code (README.md:15 promises identify; no
+ * function or ABI symbol provides it); scores follow its verify
+ * (src/model.cpp:65-78): score = sum(e_query * e_enrolled) with exact f32
+ * products summed in f64, i.e. 1 - verify's distance; top k rows per clip,
+ * highest score first, equal scores by the lower row. */
+
+/* Copy n enrolled embeddings (host f32 [n][dim], dim = the model's embedding
+ * dim) into HBM, replacing the previous registry; n = 0 clears it. */
+int voicedetect_gpu_registry_set(voicedetect_ctx* ctx, const float* emb, int n, int dim);
+
+/* Embed `batch` clips of host PCM on the GPU and return each clip's k best
+ * registry rows (1 <= k <= min(64, n)): out_idx / out_score [batch][k] (host). */
+int voicedetect_gpu_identify_pcm(voicedetect_ctx* ctx, const float* pcm, int batch, int n_samples,
+                                 int sample_rate, int k, int* out_idx, float* out_score);
+
+/* Same for device-resident embeddings d_emb [batch][dim]; writes d_idx /
+ * d_score [batch][k] (device) on the context's stream and returns once
+ * enqueued (the scratch it needs is allocated on first use). */
+int voicedetect_gpu_identify_device_async(voicedetect_ctx* ctx, const float* d_emb, int batch, int k,
+                                          int* d_idx, float* d_score);
+
 #ifdef __cplusplus
 }
 #endif

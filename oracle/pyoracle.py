@@ -180,6 +180,23 @@ def l2norm(v):
     return v
 
 
+def verify_distance(ea, eb):
+    """The reference's verify distance, 1 - sum(ea * eb) accumulated in double
+    (src/model.cpp:65-78)."""
+    return 1.0 - float(np.dot(np.asarray(ea, dtype=np.float64), np.asarray(eb, dtype=np.float64)))
+
+
+def registry_topk(q, reg, k):
+    """Identify against an enrolled registry (no reference function: README.md:15
+    promises identify; the score follows verify, src/model.cpp:65-78): scores
+    q @ reg.T in f64 over f32 values (each product exact), the k best rows per
+    query, highest score first, equal scores by the lower row index.
+    Returns (idx [B][k] int32, score [B][k] f64)."""
+    s = np.asarray(q, dtype=np.float32).astype(np.float64) @ np.asarray(reg, dtype=np.float32).astype(np.float64).T
+    idx = np.argsort(-s, axis=1, kind="stable")[:, :k]   # stable: equal scores keep the lower row first
+    return idx.astype(np.int32), np.take_along_axis(s, idx, axis=1)
+
+
 class OracleResNet:
     """orc_resnet built from a parsed GGUF (vdamd.gguf.GGUFFile), weights dequantised to f32."""
 

@@ -23,6 +23,17 @@ struct voicedetect_ctx {
     std::unique_ptr<vdk::Model> model;
     std::string last_error;
     std::vector<vdk::ProfileRecord> profile;
+    // enrolled embeddings for identify (device, [reg_n][reg_dim]) and a
+    // grow-only device scratch for the identify calls
+    float* reg = nullptr;
+    int reg_n = 0, reg_dim = 0;
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    ~voicedetect_ctx() {
+        if (model) model->synchronize();
+        if (reg) (void)hipFree(reg);
+        if (scratch) (void)hipFree(scratch);
+    }
 };
 
 namespace {
@@ -295,4 +306,114 @@ extern "C" int voicedetect_gpu_profile_get(voicedetect_ctx* ctx, int i, char* na
     if (flops) *flops = r.flops;
     if (bytes) *bytes = r.bytes;
     return 0;
+}
+
+namespace {
+
+// Grows ctx->scratch to at least `bytes` (waiting for the stream before
+// releasing the old block, which queued work may still use).
+void* ctx_scratch(voicedetect_ctx* ctx, size_t bytes) {
+    if (bytes > ctx->scratch_bytes) {
+        ctx->model->synchronize();
+        if (ctx->scratch) VDK_HIP(hipFree(ctx->scratch));
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+        VDK_HIP(hipMalloc(&ctx->scratch, bytes));
+        ctx->scratch_bytes = bytes;
+    }
+    return ctx->scratch;
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+}  // namespace
+
+extern "C" int voicedetect_gpu_registry_set(voicedetect_ctx* ctx, const float* emb, int n, int dim) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (n < 0 || (n > 0 && !emb)) { ctx->last_error = "invalid registry buffer"; return 1; }
+    return run(ctx, [&] {
+        vdk::require(n == 0 || dim == ctx->model->embedding_dim(),
+                     "registry dim " + std::to_string(dim) + " differs from the model's embedding dim " +
+                         std::to_string(ctx->model->embedding_dim()));
+        ctx->model->synchronize();
+        if (ctx->reg) VDK_HIP(hipFree(ctx->reg));
+        ctx->reg = nullptr;
+        ctx->reg_n = ctx->reg_dim = 0;
+        if (n > 0) {
+            VDK_HIP(hipMalloc(&ctx->reg, sizeof(float) * (size_t)n * dim));
+            VDK_HIP(hipMemcpy(ctx->reg, emb, sizeof(float) * (size_t)n * dim, hipMemcpyHostToDevice));
+            ctx->reg_n = n;
+            ctx->reg_dim = dim;
+        }
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" int voicedetect_gpu_identify_device_async(voicedetect_ctx* ctx, const float* d_emb, int batch, int k,
+                                                     int* d_idx, float* d_score) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    return run(ctx, [&] {
+        vdk::require(ctx->reg_n > 0, "identify: no registry (voicedetect_gpu_registry_set)");
+        vdk::require(batch > 0 && d_emb && d_idx && d_score, "identify: invalid buffers");
+        vdk::require(k >= 1 && k <= 64 && k <= ctx->reg_n, "identify: k must be in 1..min(64, registry size)");
+        const size_t ws = vdk_registry_topk_workspace_size(batch, ctx->reg_n, k);
+        void* work = ctx_scratch(ctx, ws);
+        if (vdk_registry_topk(d_emb, batch, ctx->reg, ctx->reg_n, ctx->reg_dim, k, work, ws, d_idx, d_score,
+                              ctx->model->stream()) != 0)
+            throw vdk::Error(vdk_last_error());
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" int voicedetect_gpu_identify_pcm(voicedetect_ctx* ctx, const float* pcm, int batch, int n_samples,
+                                            int sample_rate, int k, int* out_idx, float* out_score) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!pcm || n_samples < 0 || batch <= 0 || !out_idx || !out_score) {
+        ctx->last_error = "invalid buffers";
+        return 1;
+    }
+    return run(ctx, [&] {
+        vdk::Model& m = *ctx->model;
+        vdk::require(ctx->reg_n > 0, "identify: no registry (voicedetect_gpu_registry_set)");
+        vdk::require(k >= 1 && k <= 64 && k <= ctx->reg_n, "identify: k must be in 1..min(64, registry size)");
+        std::vector<float> resampled;
+        const float* x = pcm;
+        int n16 = n_samples;
+        if (sample_rate != 16000) {
+            for (int b = 0; b < batch; ++b) {
+                const std::vector<float> y = vdk::resample_linear(
+                    std::vector<float>(pcm + (size_t)b * n_samples, pcm + (size_t)(b + 1) * n_samples), sample_rate,
+                    16000);
+                n16 = (int)y.size();
+                resampled.insert(resampled.end(), y.begin(), y.end());
+            }
+            x = resampled.data();
+        }
+        const int dim = m.embedding_dim();
+        const size_t pcm_b = align256(sizeof(float) * (size_t)batch * n16);
+        const size_t emb_b = align256(sizeof(float) * (size_t)batch * dim);
+        const size_t out_b = align256(sizeof(int) * (size_t)batch * k);
+        const size_t ws = vdk_registry_topk_workspace_size(batch, ctx->reg_n, k);
+        uint8_t* base = static_cast<uint8_t*>(ctx_scratch(ctx, pcm_b + emb_b + 2 * out_b + ws));
+        float* d_pcm = reinterpret_cast<float*>(base);
+        float* d_emb = reinterpret_cast<float*>(base + pcm_b);
+        int* d_idx = reinterpret_cast<int*>(base + pcm_b + emb_b);
+        float* d_score = reinterpret_cast<float*>(base + pcm_b + emb_b + out_b);
+        void* work = base + pcm_b + emb_b + 2 * out_b;
+        hipStream_t s = m.stream();
+        VDK_HIP(hipMemcpyAsync(d_pcm, x, sizeof(float) * (size_t)batch * n16, hipMemcpyHostToDevice, s));
+        m.embed_batch_device(d_pcm, batch, n16, d_emb);
+        if (vdk_registry_topk(d_emb, batch, ctx->reg, ctx->reg_n, ctx->reg_dim, k, work, ws, d_idx, d_score, s) != 0)
+            throw vdk::Error(vdk_last_error());
+        VDK_HIP(hipMemcpyAsync(out_idx, d_idx, sizeof(int) * (size_t)batch * k, hipMemcpyDeviceToHost, s));
+        VDK_HIP(hipMemcpyAsync(out_score, d_score, sizeof(float) * (size_t)batch * k, hipMemcpyDeviceToHost, s));
+        VDK_HIP(hipStreamSynchronize(s));
+        ctx->last_error.clear();
+        return 0;
+    });
 }

@@ -73,6 +73,9 @@ _SIGS = {
                                                C.POINTER(C.c_float), C.POINTER(C.c_int)]),
     "voicedetect_gpu_embed_batch_async": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp]),
     "voicedetect_gpu_synchronize": (C.c_int, [_vp]),
+    "voicedetect_gpu_registry_set": (C.c_int, [_vp, _vp, C.c_int, C.c_int]),
+    "voicedetect_gpu_identify_pcm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "voicedetect_gpu_identify_device_async": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "voicedetect_gpu_stream": (_vp, [_vp]),
     "voicedetect_gpu_embed_capture": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp, C.POINTER(C.c_int), _vp, _vp]),
     "voicedetect_gpu_set_profiling": (C.c_int, [_vp, C.c_int]),
@@ -105,6 +108,8 @@ _SIGS = {
     "vdk_conv2d_tile_fits_ex": (C.c_int, [C.c_int, C.POINTER(ConvDesc)]),
     "vdk_conv2d_tile_count": (C.c_int, []),
     "vdk_conv2d_tile_fits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "vdk_registry_topk_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
+    "vdk_registry_topk": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp, _vp, _vp]),
     "vdk_resblock3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdk_resblock3x3_variant": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                           C.c_int, _vp]),
@@ -280,6 +285,28 @@ class Context:
         if rc != 0:
             raise VdkError(self.last_error())
         return d.value, bool(v.value)
+
+    def registry_set(self, emb):
+        """Enrol emb [n][dim] (host f32) as the identify registry; n = 0 clears it."""
+        emb = np.ascontiguousarray(emb, dtype=np.float32).reshape(-1, self.dim)
+        rc = self.L.voicedetect_gpu_registry_set(self.ctx, emb.ctypes.data if emb.size else None, emb.shape[0],
+                                                 self.dim)
+        if rc != 0:
+            raise VdkError(self.last_error())
+
+    def identify_pcm(self, pcm, k, sample_rate=16000):
+        """Each clip's k best registry rows: (idx [B][k] int32, score [B][k] f32)."""
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        if pcm.ndim == 1:
+            pcm = pcm[None, :]
+        B, n = pcm.shape
+        idx = np.zeros((B, k), dtype=np.int32)
+        score = np.zeros((B, k), dtype=np.float32)
+        rc = self.L.voicedetect_gpu_identify_pcm(self.ctx, pcm.ctypes.data, B, n, sample_rate, k, idx.ctypes.data,
+                                                 score.ctypes.data)
+        if rc != 0:
+            raise VdkError(self.last_error())
+        return idx, score
 
     def capture(self, pcm, n_mels=80):
         pcm = np.ascontiguousarray(pcm, dtype=np.float32)
