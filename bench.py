@@ -285,6 +285,17 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": model["dtype"],
         "data": "synthetic", "config": model["config"], "roofline": roofline,
     }
+    # the drop-in boundary hands over host PCM: the same batch through the
+    # host-buffer entry point (H2D copy of the PCM and D2H of the embeddings
+    # included), reported beside `value`, never as it
+    ctx.embed_batch(pcm)
+    hs = min(args.steps, 10)
+    t0 = time.perf_counter()
+    for _ in range(hs):
+        ctx.embed_batch(pcm)
+    dt = (time.perf_counter() - t0) / hs
+    out["host_buffers"] = {"value": round(batch / dt, 2), "unit": "embeddings/s", "ms_per_step": round(dt * 1e3, 4),
+                           "note": "voicedetect_capi_embed_pcm_batch: host PCM in, host embeddings out (PCIe included)"}
     if args.registry > 0:
         out["registry"] = registry_bench(L, d_out, batch, ctx.dim, args.registry, 10, args.steps)
     if not args.no_cpu_baseline:
