@@ -44,6 +44,18 @@ def conv_gpu(x_nhwc, w_oihw, bias=None, residual=None, stride=1, pad=1, relu=Fal
     return dy.to_array(np.float16, (B, Ho, Wo, OC))
 
 
+def tile_fits(tile, B, H, W, IC, OC, K, stride, pad, residual=True, relu=True):
+    """Whether conv tile `tile` takes this exact shape (map width included,
+    which the width-limited band kernels need), via vdk_conv2d_tile_fits_ex."""
+    d = lib.ConvDesc()
+    d.batch, d.H, d.W, d.IC, d.OC, d.KH, d.KW = B, H, W, IC, OC, K, K
+    d.stride_h = d.stride_w = stride
+    d.pad_h = d.pad_w = pad
+    d.residual = 16 if residual else None   # only its presence matters
+    d.act = lib.ACT_RELU if relu else lib.ACT_NONE
+    return bool(lib.lib().vdk_conv2d_tile_fits_ex(tile, d))
+
+
 def close_report(got, ref, rtol, atol_rel_rms):
     """Elementwise |got-ref| <= atol + rtol*|ref| with atol = atol_rel_rms * rms(ref).
     Returns (ok, max_excess_ratio, rel_l2)."""

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import pyoracle as O
-from gpu_util import announce, close_report, conv_gpu, device_ok
+from gpu_util import announce, close_report, conv_gpu, device_ok, tile_fits
 from test_oracle_fbank import _cases, _cfg, golden_pcm
 from vdamd import lib, synth
 
@@ -167,7 +167,7 @@ def test_conv_every_tile_config(shape):
                              residual=res[c].astype(np.float32).transpose(2, 0, 1), relu=True))
     n = 0
     for t in range(L.vdk_conv2d_tile_count()):
-        if not L.vdk_conv2d_tile_fits(t, IC, OC, K, K, s, p):
+        if not tile_fits(t, B, H, W, IC, OC, K, s, p):
             continue
         announce(f"tile {t} shape {shape}")
         got = conv_gpu(x, w, b, res, s, p, True, tile=t)
@@ -180,8 +180,9 @@ def test_conv_every_tile_config(shape):
 
 
 @pytest.mark.parametrize("case", [
-    # (B, H, W, C, bias, residual, relu): the register-weight 3x3 kernels'
-    # other epilogues (every tile above runs bias + residual + ReLU)
+    # (B, H, W, C, bias, residual, relu): the other epilogues of the
+    # persistent register-weight and band 3x3 kernels (tiles 53+; every tile
+    # above runs bias + residual + ReLU)
     (2, 9, 70, 64, False, False, False),
     (1, 5, 33, 64, True, False, True),
     (3, 4, 31, 32, True, True, False),
@@ -197,7 +198,7 @@ def test_conv_register_weight_tiles_plain_epilogues(case):
     res = rng.standard_normal((B, H, W, C)).astype(np.float16) if with_res else None
     n = 0
     for t in range(L.vdk_conv2d_tile_count()):
-        if not L.vdk_conv2d_tile_fits(t, C, C, 3, 3, 1, 1) or t < 53:
+        if not tile_fits(t, B, H, W, C, C, 3, 1, 1, residual=with_res, relu=relu) or t < 53:
             continue
         announce(f"rw tile {t} case {case}")
         got = conv_gpu(x, w, b, res, 1, 1, relu, tile=t)

@@ -1570,7 +1570,7 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
-    if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % 128 == 0 && a.IC % 16 == 0;
+    if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % t.bm == 0 && a.IC % 16 == 0;
     if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8))) return false;   // split: DMA only
     return a.IC % t.kc == 0;
 }
