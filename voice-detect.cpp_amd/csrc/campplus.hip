@@ -29,10 +29,14 @@ __global__ __launch_bounds__(256) void bn_act_kernel(const half_t* __restrict__ 
     const int c = (int)(i % C8) * 8;
     const long r = i / C8;
     const half8 v = *reinterpret_cast<const half8*>(x + r * xs + c);
+    const float4v s0 = *reinterpret_cast<const float4v*>(scale + c), s1 = *reinterpret_cast<const float4v*>(scale + c + 4);
+    const float4v h0 = *reinterpret_cast<const float4v*>(shift + c), h1 = *reinterpret_cast<const float4v*>(shift + c + 4);
+    const float sc[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+    const float sh[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
     half8 o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        float f = (float)v[e] * scale[c + e] + shift[c + e];
+        float f = (float)v[e] * sc[e] + sh[e];
         if (act == VDK_ACT_RELU) f = f > 0.0f ? f : 0.0f;
         o[e] = (half_t)f;
     }
@@ -52,6 +56,7 @@ __global__ __launch_bounds__(256) void segment_sums_kernel(const half_t* __restr
     double acc = 0.0;
     if (c < C) {
         const half_t* p = x + (size_t)b * T * xs + c;
+#pragma unroll 8
         for (int t = t0 + lane_t; t < t1; t += 4) acc += (double)(float)p[(size_t)t * xs];
     }
     part[lane_t][lane_c] = acc;
@@ -81,20 +86,31 @@ __global__ __launch_bounds__(256) void cam_context_kernel(const float* __restric
         ctx[c] = (float)(tot / T) + (float)((double)sb[(size_t)s * C + c] / seg);
     }
     __syncthreads();
-    for (int o = threadIdx.x; o < H1; o += blockDim.x) {
+    // each output's dot product split over 4 lanes (k = q, q+4, ...), the
+    // 4 partial sums added in a fixed order by lane q = 0
+    const int q = threadIdx.x & 3;
+    for (int o = threadIdx.x >> 2; o < H1; o += blockDim.x >> 2) {
         const float* wr = w1 + (size_t)o * C;
         double a = 0.0;
-        for (int c = 0; c < C; ++c) a += (double)wr[c] * (double)ctx[c];
-        float v = (float)a + (b1 ? b1[o] : 0.0f);
-        hid[o] = v > 0.0f ? v : 0.0f;
+#pragma unroll 4
+        for (int c = q; c < C; c += 4) a += (double)wr[c] * (double)ctx[c];
+        const double a1 = __shfl_down(a, 1, 4), a2 = __shfl_down(a, 2, 4), a3 = __shfl_down(a, 3, 4);
+        if (q == 0) {
+            const float v = (float)((a + a1) + (a2 + a3)) + (b1 ? b1[o] : 0.0f);
+            hid[o] = v > 0.0f ? v : 0.0f;
+        }
     }
     __syncthreads();
-    for (int o = threadIdx.x; o < G; o += blockDim.x) {
+    for (int o = threadIdx.x >> 2; o < G; o += blockDim.x >> 2) {
         const float* wr = w2 + (size_t)o * H1;
         double a = 0.0;
-        for (int c = 0; c < H1; ++c) a += (double)wr[c] * (double)hid[c];
-        const float v = (float)a + (b2 ? b2[o] : 0.0f);
-        gate[((size_t)b * nseg + s) * G + o] = 1.0f / (1.0f + expf(-v));
+#pragma unroll 4
+        for (int c = q; c < H1; c += 4) a += (double)wr[c] * (double)hid[c];
+        const double a1 = __shfl_down(a, 1, 4), a2 = __shfl_down(a, 2, 4), a3 = __shfl_down(a, 3, 4);
+        if (q == 0) {
+            const float v = (float)((a + a1) + (a2 + a3)) + (b2 ? b2[o] : 0.0f);
+            gate[((size_t)b * nseg + s) * G + o] = 1.0f / (1.0f + expf(-v));
+        }
     }
 }
 
@@ -112,7 +128,7 @@ extern "C" int vdk_bn_act(const void* d_x, int x_stride, long rows, int C, const
         require(rows > 0 && C > 0 && C % 8 == 0 && x_stride >= C && y_stride >= C && x_stride % 8 == 0 &&
                     y_stride % 8 == 0, "bn_act: bad shape");
         require(act == VDK_ACT_NONE || act == VDK_ACT_RELU, "bn_act: unknown activation");
-        require(al16(d_x) && al16(d_y), "bn_act: pointers must be 16-byte aligned");
+        require(al16(d_x) && al16(d_y) && al16(d_scale) && al16(d_shift), "bn_act: pointers must be 16-byte aligned");
         const long n = rows * (C / 8);
         hipLaunchKernelGGL(bn_act_kernel, dim3(cdiv(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
                            static_cast<const half_t*>(d_x), x_stride, rows, C, d_scale, d_shift, act,

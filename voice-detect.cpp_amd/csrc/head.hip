@@ -1,7 +1,7 @@
 // head.hip - statistics pooling, embedding FC and L2 normalisation on gfx950.
 //
-// These are bandwidth-bound reductions: TSTP reads the last feature map once
-// (coalesced over channels, one thread per (clip, freq row, channel)); the FC is
+// These are bandwidth-bound reductions: TSTP reads the last feature map twice
+// (coalesced over channels; 64 channels x 4 time partitions per workgroup); the FC is
 // a split-K tiled dot product with a fixed-order reduction; L2 is one
 // wavefront per clip.  Sums are accumulated in f64 like the reference's ggml
 // reductions and host L2 (src/encoder_resnet.cpp:140-183).
@@ -24,26 +24,43 @@ __device__ __forceinline__ float tstp_val(const half_t* p, int x_lo) {
     return x_lo ? (float)p[0] + (float)p[x_lo] : (float)p[0];
 }
 
+// A workgroup covers 64 channels of one (clip, freq row): thread (p, c)
+// = (tid / 64, tid % 64) sums time steps p, p + 4, ... of channel c in f64,
+// and the four partial sums are added in a fixed order (so the result does
+// not depend on scheduling); the same for the squared deviations from the
+// f32 mean.
 __global__ __launch_bounds__(256) void tstp_kernel(const half_t* __restrict__ x, int xs, int x_lo, int H, int W,
                                                    int C, float eps, float* __restrict__ pooled) {
 #pragma clang fp contract(off)
-    const int h = blockIdx.x, b = blockIdx.y;
+    __shared__ double part[4][64];
+    const int tx = threadIdx.x & 63, tp = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + tx, h = blockIdx.y, b = blockIdx.z;
+    const bool ok = c < C;
     const size_t CH = (size_t)C * H;
-    float* out = pooled + (size_t)b * 2 * CH;
-    const half_t* row = x + ((size_t)b * H + h) * W * xs;
-    for (int c = threadIdx.x; c < C; c += blockDim.x) {
-        double s = 0.0;
-#pragma unroll 8
-        for (int t = 0; t < W; ++t) s += (double)tstp_val(row + (size_t)t * xs + c, x_lo);
-        const float mean = (float)(s / W);
-        double s2 = 0.0;
-#pragma unroll 8
-        for (int t = 0; t < W; ++t) {
-            const float d = tstp_val(row + (size_t)t * xs + c, x_lo) - mean;
+    const half_t* row = x + ((size_t)b * H + h) * W * xs + (ok ? c : 0);
+    double s = 0.0;
+    if (ok) {
+#pragma unroll 4
+        for (int t = tp; t < W; t += 4) s += (double)tstp_val(row + (size_t)t * xs, x_lo);
+    }
+    part[tp][tx] = s;
+    __syncthreads();
+    const float mean = (float)(((part[0][tx] + part[1][tx]) + (part[2][tx] + part[3][tx])) / W);
+    __syncthreads();
+    double s2 = 0.0;
+    if (ok) {
+#pragma unroll 4
+        for (int t = tp; t < W; t += 4) {
+            const float d = tstp_val(row + (size_t)t * xs, x_lo) - mean;
             s2 += (double)(d * d);
         }
-        float var = (float)(s2 / W);
+    }
+    part[tp][tx] = s2;
+    __syncthreads();
+    if (tp == 0 && ok) {
+        float var = (float)(((part[0][tx] + part[1][tx]) + (part[2][tx] + part[3][tx])) / W);
         if (W > 1) var = var * ((float)W / (float)(W - 1));
+        float* out = pooled + (size_t)b * 2 * CH;
         out[(size_t)c * H + h] = mean;
         out[CH + (size_t)c * H + h] = sqrtf(var + eps);
     }
@@ -135,7 +152,7 @@ extern "C" int vdk_tstp_ex(const void* d_x, int x_stride, int x_lo, int batch, i
         require(batch > 0 && H > 0 && W > 0 && C > 0, "tstp: empty input");
         const int xs = x_stride ? x_stride : C;
         require(xs >= C && (x_lo == 0 || (x_lo >= C && x_lo + C <= xs)), "tstp: bad pixel stride / lo offset");
-        hipLaunchKernelGGL(tstp_kernel, dim3(H, batch), dim3(256), 0, static_cast<hipStream_t>(stream),
+        hipLaunchKernelGGL(tstp_kernel, dim3(cdiv(C, 64), H, batch), dim3(256), 0, static_cast<hipStream_t>(stream),
                            static_cast<const half_t*>(d_x), xs, x_lo, H, W, C, eps, d_pooled);
         VDK_HIP(hipGetLastError());
     });
