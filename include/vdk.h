@@ -81,8 +81,10 @@ int vdk_conv2d_nhwc(const void* d_x, int batch, int H, int W, int IC,
                     const float* d_bias, const void* d_residual, int relu,
                     void* d_y, void* stream);
 
-/* Activations of the fused epilogues (conv and FC). */
-enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3 };
+/* Activations of the fused epilogues (conv and FC).  GELU is the exact erf
+ * form x * Phi(x) (the wav2vec2 activation, src/analyze_w2v2.cpp:126-128). */
+enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3, VDK_ACT_GELU = 4,
+       VDK_ACT_TANH = 5 };
 
 /* General form.  Pixel strides let a layer read or write a channel slice of a
  * wider NHWC tensor in place (pass the slice's base pointer; 0 means dense).
@@ -92,12 +94,17 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * Epilogue, in order:
  *   v = acc + bias                 (bias_batch_stride > 0: clip b reads bias + b*stride)
  *   v *= gate[b][ow / gate_seg][oc]  (gate [B][gate_nseg][OC] f32, may be NULL)
- *   v += residual
- *   v = act(v)                     (RELU then min(v, clamp_hi) if clamp_hi > 0; SIGMOID; SILU)
+ *   v += residual                  (f16, or f32 when res_f32)
+ *   v = act(v)                     (RELU then min(v, clamp_hi) if clamp_hi > 0; SIGMOID; SILU; GELU)
+ *   v += residual                  (instead of the add above when res_after_act)
  *   v = v*post_scale + post_shift  (a BatchNorm after the activation; may be NULL)
  *   v = tanh(v)                    (tanh_after)
  * stored f16 (or f32 if y_f32) at pixel (b, oh, ow), or at (b, ow, oh) when
  * y_time_major (an NHWC [B][H][W][C] map written as [B][W][H*C], no residual).
+ * out_w > 0 keeps only the first out_w output columns of each row (a conv
+ * whose right pad is one shorter than its left, e.g. wav2vec2's positional
+ * conv with its last step dropped).  y and an f32 residual may be the same
+ * buffer (each element is read before it is written, by the same thread).
  * OC needs only be a multiple of 8: surplus rows of a tile are masked.
  * split != 0 selects split-f16 arithmetic (~2^-21 relative instead of f16's
  * 2^-11, for ill-conditioned networks): x, residual and y hold value = hi + lo
@@ -118,6 +125,7 @@ typedef struct {
     void* y; int y_stride, y_f32, y_time_major;
     int split; int x_lo, res_lo, y_lo;
     int tile;
+    int res_f32, res_after_act, out_w;
 } vdk_conv_desc;
 int vdk_conv2d_ex(const vdk_conv_desc* desc, void* stream);
 int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* desc);
@@ -184,8 +192,9 @@ int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w,
                const float* d_bias, const float* d_mean_vec, int out_dim,
                float* d_y, void* d_work, size_t work_bytes, void* stream);
 /* Same, with an activation on the result (act: VDK_ACT_NONE / RELU /
- * SIGMOID): the SE bottleneck of src/encoder.cpp:207-219, the ASP
- * global-context term, the CAM++ context MLP (src/encoder_campplus.cpp:266-267). */
+ * SIGMOID / TANH): the SE bottleneck of src/encoder.cpp:207-219, the ASP
+ * global-context term, the CAM++ context MLP (src/encoder_campplus.cpp:266-267),
+ * the age/gender ModelHead dense + tanh (src/analyze_w2v2.cpp:614-623). */
 int vdk_linear_ex(const float* d_x, int batch, int in_dim, const float* d_w,
                   const float* d_bias, const float* d_mean_vec, int out_dim, int act,
                   float* d_y, void* d_work, size_t work_bytes, void* stream);
@@ -260,6 +269,48 @@ int vdk_cam_context(const float* d_sums, int batch, int T, int C, int seg, const
 int vdk_aff_combine(const void* d_t, int t_stride, int t_lo, const void* d_x, int x_stride, int x_lo,
                     const void* d_ds, int ds_stride, int ds_lo, long rows, int C, int split, void* d_y,
                     int y_stride, int y_lo, void* stream);
+
+/* ---- wav2vec2 analyze (src/analyze_w2v2.cpp) ----
+ * Activations are time-major [B][T][C]; the GEMM-shaped layers run on
+ * vdk_conv2d_ex (H = 1, W = T).  These cover the rest of the graph. */
+
+/* do_normalize statistics of the raw waveform (src/analyze_w2v2.cpp:63-70):
+ * stats[b] = {mean, 1/sqrt(biased var + eps)} of clip b, f64 two-pass. */
+int vdk_wave_stats(const float* d_x, int batch, int n, float eps, float* d_stats, void* stream);
+
+/* Conv layer 0 of the feature encoder (src/analyze_w2v2.cpp:34-45, 52-131):
+ * one input channel, y[b][t][c] = gelu(norm(bias[c] + sum_k w[c][k] xn[b][t*S+k]))
+ * with xn = (x - mean) * rstd when d_stats (vdk_wave_stats) is given, else x.
+ * norm 0: none; 1: GroupNorm with one group per channel (mean / biased var of
+ * each channel over the clip's T0 frames, f64 two-pass); 2: LayerNorm over the
+ * C channels of each frame; affine gamma / beta, eps.  x [B][n] f32,
+ * w [C][K] f32, y [B][T0][C] f16, T0 = (n - K)/S + 1, C in {256, 512, 1024},
+ * K <= 16, S <= 8.  norm 1 needs vdk_w2v2_conv0_workspace_size() bytes of d_work. */
+size_t vdk_w2v2_conv0_workspace_size(int batch, int n, int C, int K, int S);
+int vdk_w2v2_conv0(const float* d_x, int batch, int n, const float* d_stats, const float* d_w,
+                   const float* d_bias, int C, int K, int S, int norm, const float* d_gamma,
+                   const float* d_beta, float eps, void* d_work, size_t work_bytes, void* d_y,
+                   void* stream);
+
+/* LayerNorm over rows of C values, biased variance (src/analyze_w2v2.cpp:187-193):
+ * o = (x - mean) / sqrt(var + eps) * gamma + beta [then GELU]; y f16 or f32 (may
+ * be NULL); when d_acc != NULL also acc = [acc +] acc_w * (o, or x with
+ * VDK_LN_ACC_INPUT) in f32 - the emotion head's weighted layer sum
+ * (src/analyze_w2v2.cpp:528-538).  C % 64 == 0, C <= 4096. */
+enum { VDK_LN_X_F32 = 1, VDK_LN_Y_F32 = 2, VDK_LN_GELU = 4, VDK_LN_ACC_INPUT = 8, VDK_LN_ACC_INIT = 16 };
+int vdk_layer_norm(const void* d_x, int rows, int C, const float* d_gamma, const float* d_beta, float eps,
+                   int flags, void* d_y, float* d_acc, float acc_w, void* stream);
+
+/* Multi-head self-attention core (src/analyze_w2v2.cpp:222-270): per clip and
+ * head, out = softmax(q k^T * scale) v over all T tokens (no mask).
+ * qkv [B][T][3H] f16 = [q | k | v] with head h at columns h*head_dim of each,
+ * out [B][T][H] f16, H = n_heads * head_dim; head_dim must be 64. */
+int vdk_attention(const void* d_qkv, int batch, int T, int n_heads, int head_dim, float scale,
+                  void* d_out, void* stream);
+
+/* out[b][c] = mean over t of x[b][t][c] (f16 or f32 input, f64 sums): the
+ * time mean-pool of the analyze heads (src/analyze_w2v2.cpp:546-550, 607-610). */
+int vdk_time_mean(const void* d_x, int x_f32, int batch, int T, int C, float* d_out, void* stream);
 
 #ifdef __cplusplus
 }

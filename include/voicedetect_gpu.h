@@ -68,6 +68,35 @@ int voicedetect_gpu_identify_pcm(voicedetect_ctx* ctx, const float* pcm, int bat
 int voicedetect_gpu_identify_device_async(voicedetect_ctx* ctx, const float* d_emb, int batch, int k,
                                           int* d_idx, float* d_score);
 
+/* ---- analyze: the wav2vec2 emotion / age-gender heads ----
+ * Batched counterparts of voicedetect_capi_analyze_path_json for a context
+ * loaded from an analyze GGUF (arch wav2vec2_emotion / wav2vec2_age_gender;
+ * reference src/analyze_w2v2.cpp:503-558 emotion_logits, :596-630
+ * age_gender_raw).  Raw outputs per clip: the emotion logits, or
+ * [age_raw, gender logits...] (age in years = 100 * age_raw; probabilities are
+ * the softmax of the logits). */
+
+/* Raw outputs per clip (0 for a speaker-embedding model). */
+int voicedetect_gpu_analyze_outputs(voicedetect_ctx* ctx);
+/* Frames T' after the conv feature encoder for n_samples (0 if too short). */
+int voicedetect_gpu_analyze_frames(voicedetect_ctx* ctx, int n_samples);
+
+/* `batch` clips of host PCM -> out_raw [batch][outputs] (host). */
+int voicedetect_gpu_analyze_pcm(voicedetect_ctx* ctx, const float* pcm, int batch, int n_samples,
+                                int sample_rate, float* out_raw);
+
+/* Device-resident batch of 16 kHz PCM d_pcm [batch][n_samples] -> d_raw
+ * [batch][outputs] on the context's stream; returns once enqueued. */
+int voicedetect_gpu_analyze_batch_async(voicedetect_ctx* ctx, const float* d_pcm, int batch,
+                                        int n_samples, float* d_raw);
+
+/* Host-buffer analyze that also returns intermediates (any may be NULL):
+ * feat [batch][T'][conv_dim] (the conv feature encoder output, time-major),
+ * hidden [batch][T'][hidden] (the last hidden state of the transformer stack),
+ * out_raw [batch][outputs]. */
+int voicedetect_gpu_analyze_capture(voicedetect_ctx* ctx, const float* pcm, int batch, int n_samples,
+                                    float* feat, float* hidden, float* out_raw);
+
 #ifdef __cplusplus
 }
 #endif

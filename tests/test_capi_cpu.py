@@ -99,7 +99,7 @@ def test_error_contract_without_device_work(tiny_model):
     assert "failed to load audio" in ctx.last_error() and d.value == -7.0
     assert L.voicedetect_capi_embed_path(ctx.ctx, None, C.byref(vec), C.byref(dim)) == 1
     assert ctx.last_error() == "wav_path is NULL"
-    # analyze heads are outside this library: NULL + the reference's message
+    # a speaker model has no analyze heads: NULL + the reference's message
     assert L.voicedetect_capi_analyze_path_json(ctx.ctx, b"x.wav") is None
     assert ctx.last_error() == "voicedetect: this model has no age/gender/emotion analyze heads"
     if L.vdk_device_count() == 0:
@@ -169,3 +169,25 @@ def test_f16_packing_matches_ieee_round_to_nearest_even():
     out = np.zeros(len(x), dtype=np.uint16)
     L.vdk_f32_to_f16(x.ctypes.data, out.ctypes.data, len(x))
     assert np.array_equal(out, x.astype(np.float16).view(np.uint16))
+
+
+def test_analyze_model_host_side(tmp_path):
+    """An analyze GGUF (wav2vec2 emotion / age-gender) loads through the C ABI;
+    its shape queries and error paths need no GPU (src/model.cpp:80-101)."""
+    from vdamd import synth
+    L = lib.lib()
+    small = dict(hidden=128, n_layers=1, n_heads=2, ff=256, conv_dims=(256,) * 7, pos_k=8, pos_groups=2, proj=32)
+    for kind, n_out in (("emotion", 4), ("age_gender", 4)):
+        path = str(tmp_path / f"{kind}.gguf")
+        synth.write_w2v2(path, 3, kind, **small)
+        ctx = lib.Context(path)
+        assert ctx.analyze_outputs() == n_out
+        # T' = 49 for 1 s at 16 kHz (kernels 10,3,3,3,3,2,2, strides 5,2,...)
+        assert ctx.analyze_frames(16000) == 49 and ctx.analyze_frames(399) == 0 and ctx.analyze_frames(400) == 1
+        vec, dim = C.POINTER(C.c_float)(), C.c_int(-1)
+        x = np.zeros(16000, dtype=np.float32)
+        assert L.voicedetect_capi_embed_pcm(ctx.ctx, x.ctypes.data, 16000, 16000, C.byref(vec), C.byref(dim)) == 1
+        assert "no speaker embedding head" in ctx.last_error() and not vec and dim.value == 0
+        assert L.voicedetect_capi_analyze_path_json(ctx.ctx, b"/nonexistent.wav") is None
+        assert "failed to load audio" in ctx.last_error()
+        ctx.close()

@@ -169,11 +169,29 @@ extern "C" char* voicedetect_capi_analyze_path_json(voicedetect_ctx* ctx, const 
     if (!ctx) return nullptr;
     if (!ctx->model) { ctx->last_error = "context has no loaded model"; return nullptr; }
     if (!wav_path) { ctx->last_error = "wav_path is NULL"; return nullptr; }
-    if (!ctx->model->config().analyze_present)
+    // src/model.cpp:80-101: analyze needs the heads and a wav2vec2 arch
+    const vdk::ModelConfig& cfg = ctx->model->config();
+    if (!cfg.analyze_present) {
         ctx->last_error = "voicedetect: this model has no age/gender/emotion analyze heads";
-    else
-        ctx->last_error = "voicedetect: analyze heads are not supported by this build";
-    return nullptr;
+        return nullptr;
+    }
+    if (!ctx->model->is_analyzer()) {
+        ctx->last_error = "voicedetect: analyze head unsupported for arch '" + cfg.arch + "'";
+        return nullptr;
+    }
+    char* out = nullptr;
+    run(ctx, [&] {
+        std::vector<float> pcm;
+        if (!vdk::load_audio_16k_mono(wav_path, pcm))
+            throw vdk::Error(std::string("voicedetect: failed to load audio: ") + wav_path);
+        const std::string js = ctx->model->analyze_json(pcm, 16000);
+        out = static_cast<char*>(std::malloc(js.size() + 1));
+        if (!out) throw vdk::Error("out of memory");
+        std::memcpy(out, js.c_str(), js.size() + 1);
+        ctx->last_error.clear();
+        return 0;
+    });
+    return out;
 }
 
 extern "C" int voicedetect_capi_embedding_dim(voicedetect_ctx* ctx) {
@@ -413,6 +431,62 @@ extern "C" int voicedetect_gpu_identify_pcm(voicedetect_ctx* ctx, const float* p
         VDK_HIP(hipMemcpyAsync(out_idx, d_idx, sizeof(int) * (size_t)batch * k, hipMemcpyDeviceToHost, s));
         VDK_HIP(hipMemcpyAsync(out_score, d_score, sizeof(float) * (size_t)batch * k, hipMemcpyDeviceToHost, s));
         VDK_HIP(hipStreamSynchronize(s));
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" int voicedetect_gpu_analyze_outputs(voicedetect_ctx* ctx) {
+    return (ctx && ctx->model) ? ctx->model->analyze_outputs() : 0;
+}
+
+extern "C" int voicedetect_gpu_analyze_frames(voicedetect_ctx* ctx, int n_samples) {
+    return (ctx && ctx->model && ctx->model->is_analyzer()) ? ctx->model->analyze_frames(n_samples) : 0;
+}
+
+extern "C" int voicedetect_gpu_analyze_pcm(voicedetect_ctx* ctx, const float* pcm, int batch, int n_samples,
+                                           int sample_rate, float* out_raw) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!pcm || !out_raw || batch <= 0 || n_samples <= 0) { ctx->last_error = "invalid pcm buffer"; return 1; }
+    return run(ctx, [&] {
+        vdk::Model& m = *ctx->model;
+        if (sample_rate == 16000) {
+            m.analyze_batch_host(pcm, batch, n_samples, out_raw);
+        } else {
+            std::vector<float> all;
+            int n16 = -1;
+            for (int b = 0; b < batch; ++b) {
+                std::vector<float> x(pcm + (size_t)b * n_samples, pcm + (size_t)(b + 1) * n_samples);
+                std::vector<float> y = vdk::resample_linear(x, sample_rate, 16000);
+                n16 = (int)y.size();
+                all.insert(all.end(), y.begin(), y.end());
+            }
+            m.analyze_batch_host(all.data(), batch, n16, out_raw);
+        }
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" int voicedetect_gpu_analyze_batch_async(voicedetect_ctx* ctx, const float* d_pcm, int batch,
+                                                   int n_samples, float* d_raw) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    return run(ctx, [&] {
+        ctx->model->analyze_batch_device(d_pcm, batch, n_samples, d_raw);
+        ctx->last_error.clear();
+        return 0;
+    });
+}
+
+extern "C" int voicedetect_gpu_analyze_capture(voicedetect_ctx* ctx, const float* pcm, int batch, int n_samples,
+                                               float* feat, float* hidden, float* out_raw) {
+    if (!ctx) return 1;
+    if (!ctx->model) { ctx->last_error = "context has no loaded model"; return 1; }
+    if (!pcm || batch <= 0 || n_samples <= 0) { ctx->last_error = "invalid pcm buffer"; return 1; }
+    return run(ctx, [&] {
+        ctx->model->analyze_capture(pcm, batch, n_samples, feat, hidden, out_raw);
         ctx->last_error.clear();
         return 0;
     });

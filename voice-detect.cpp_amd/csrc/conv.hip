@@ -19,6 +19,7 @@
 #include <cstdlib>
 
 #include "common.hpp"
+#include "devmath.hpp"
 #include "vdk.h"
 
 namespace vdk {
@@ -42,6 +43,7 @@ struct ConvArgs {
     int bias_bs;               // elements between clips' bias vectors (0: one shared vector)
     int split;                 // split-f16 tensors: value = hi + lo, lo at +x_lo / +r_lo / +y_lo elements;
     int x_lo, r_lo, y_lo;      //   weights [OC][KH][KW][3*IC] = [hi | hi | lo] per tap
+    int res_f32, res_after;    // f32 residual; residual added after the activation
     int npix;                  // B * Ho * Wo
     int npix_in;               // B * H * W
 };
@@ -63,6 +65,21 @@ __device__ __forceinline__ void add8(float* v, const float* p, bool mul = false)
     }
 }
 
+__device__ __forceinline__ void add_residual(const ConvArgs& a, int P, int oc, float* v) {
+    if (a.res_f32) {
+        add8(v, reinterpret_cast<const float*>(a.res) + (size_t)P * a.rs + oc);
+        return;
+    }
+    const half8 r = *reinterpret_cast<const half8*>(a.res + (size_t)P * a.rs + oc);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += (float)r[e];
+    if (a.split) {
+        const half8 rl = *reinterpret_cast<const half8*>(a.res + (size_t)P * a.rs + a.r_lo + oc);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += (float)rl[e];
+    }
+}
+
 __device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float* v) {
     const int HoWo = a.Ho * a.Wo;
     if (a.bias) add8(v, a.bias + oc + (a.bias_bs ? (size_t)(P / HoWo) * a.bias_bs : 0));
@@ -70,16 +87,7 @@ __device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float*
         const int b = P / HoWo, ow = (P - b * HoWo) % a.Wo;
         add8(v, a.gate + ((size_t)b * a.gate_nseg + ow / a.gate_seg) * a.OC + oc, true);
     }
-    if (a.res) {
-        const half8 r = *reinterpret_cast<const half8*>(a.res + (size_t)P * a.rs + oc);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] += (float)r[e];
-        if (a.split) {
-            const half8 rl = *reinterpret_cast<const half8*>(a.res + (size_t)P * a.rs + a.r_lo + oc);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] += (float)rl[e];
-        }
-    }
+    if (a.res && !a.res_after) add_residual(a, P, oc, v);
     if (a.act == VDK_ACT_RELU) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
@@ -93,7 +101,11 @@ __device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float*
     } else if (a.act == VDK_ACT_SILU) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = v[e] / (1.0f + expf(-v[e]));
+    } else if (a.act == VDK_ACT_GELU) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = gelu_erf(v[e]);
     }
+    if (a.res && a.res_after) add_residual(a, P, oc, v);
     if (a.post_scale) {
         add8(v, a.post_scale + oc, true);
         add8(v, a.post_shift + oc);
@@ -1563,12 +1575,16 @@ constexpr int kFirstDma = 14, kFirstHalo = 26, kFirstDma8 = 33;
 bool plain_epilogue(const ConvArgs& a) {
     return !a.gate && !a.post_scale && !a.tanh_after && !a.y_f32 && !a.y_tr && !a.bias_bs && !a.split &&
            (a.act == VDK_ACT_NONE || (a.act == VDK_ACT_RELU && a.clamp_hi <= 0.0f)) && a.xs == a.IC &&
-           a.ys == a.OC && (!a.res || a.rs == a.OC);
+           a.ys == a.OC && (!a.res || a.rs == a.OC) && !a.res_f32 && !a.res_after;
 }
 
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
+    // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask;
+    // longer kernels (wav2vec2's 128-tap positional conv) take the
+    // register-staged kernel
+    if (a.KH * a.KW > 32 && idx >= kFirstDma) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
     if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % t.bm == 0 && a.IC % 16 == 0;
     if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8))) return false;   // split: DMA only
@@ -1597,6 +1613,10 @@ int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
+    if (a.KH * a.KW > 32) {   // register-staged kernel only
+        if (a.IC % 32 == 0) return bm == 128 ? 5 : (bm == 64 ? 2 : 10);
+        return a.IC % 16 == 0 ? (bm == 128 ? 13 : (bm == 64 ? 12 : 11)) : -1;
+    }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
     if (!a.split && is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return 28;
@@ -1670,14 +1690,16 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(d.batch > 0 && d.H > 0 && d.W > 0, "conv2d: empty input");
         require(d.IC > 0 && d.IC % 16 == 0, "conv2d: IC must be a positive multiple of 16");
         require(d.OC > 0 && d.OC % 8 == 0, "conv2d: OC must be a positive multiple of 8");
-        require(d.KH >= 1 && d.KW >= 1 && d.KH <= 7 && d.KW <= 7, "conv2d: kernel size out of range");
+        require(d.KH >= 1 && d.KW >= 1 && d.KH * d.KW <= 256, "conv2d: kernel size out of range (KH*KW <= 256)");
         const int sh = d.stride_h ? d.stride_h : 1, sw = d.stride_w ? d.stride_w : 1;
         const int dh = d.dil_h ? d.dil_h : 1, dw = d.dil_w ? d.dil_w : 1;
         require(sh >= 1 && sw >= 1 && dh >= 1 && dw >= 1 && d.pad_h >= 0 && d.pad_w >= 0,
                 "conv2d: invalid stride/pad/dilation");
         const int ekh = (d.KH - 1) * dh + 1, ekw = (d.KW - 1) * dw + 1;
         require(d.H + 2 * d.pad_h >= ekh && d.W + 2 * d.pad_w >= ekw, "conv2d: output would be empty");
-        const int Ho = (d.H + 2 * d.pad_h - ekh) / sh + 1, Wo = (d.W + 2 * d.pad_w - ekw) / sw + 1;
+        const int Ho = (d.H + 2 * d.pad_h - ekh) / sh + 1, Wo_full = (d.W + 2 * d.pad_w - ekw) / sw + 1;
+        require(d.out_w >= 0 && d.out_w <= Wo_full, "conv2d: out_w exceeds the output width");
+        const int Wo = d.out_w > 0 ? d.out_w : Wo_full;
         const int xs = d.x_stride ? d.x_stride : d.IC, ys = d.y_stride ? d.y_stride : d.OC;
         const int rs = d.res_stride ? d.res_stride : d.OC;
         require(xs >= d.IC && ys >= d.OC && rs >= d.OC, "conv2d: pixel stride smaller than the channel count");
@@ -1695,6 +1717,7 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(!d.gate || (d.gate_seg > 0 && d.gate_nseg > 0 && (Wo + d.gate_seg - 1) / d.gate_seg <= d.gate_nseg),
                 "conv2d: gate needs gate_seg > 0 and enough segments for the output width");
         require(!d.y_time_major || !d.residual, "conv2d: a time-major store takes no residual");
+        require(!d.res_f32 || (d.residual && !d.split), "conv2d: an f32 residual needs a residual and no split-f16");
         require(!d.split || (!d.y_f32 && !d.y_time_major && d.x_lo >= d.IC && d.y_lo >= d.OC &&
                              (!d.residual || d.res_lo >= d.OC) && d.x_lo % 8 == 0 && d.y_lo % 8 == 0 &&
                              d.res_lo % 8 == 0 && d.IC % 32 == 0),
@@ -1713,7 +1736,7 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         a.H = d.H; a.W = d.W; a.IC = d.IC; a.Ho = Ho; a.Wo = Wo; a.OC = d.OC;
         a.KH = d.KH; a.KW = d.KW;
         a.sh = sh; a.sw = sw; a.ph = d.pad_h; a.pw = d.pad_w; a.dh = dh; a.dw = dw;
-        require(d.act >= VDK_ACT_NONE && d.act <= VDK_ACT_SILU, "conv2d: unknown activation");
+        require(d.act >= VDK_ACT_NONE && d.act <= VDK_ACT_GELU, "conv2d: unknown activation");
         a.act = d.act;
         a.clamp_hi = d.act == VDK_ACT_RELU ? d.clamp_hi : 0.0f;
         a.tanh_after = d.tanh_after ? 1 : 0;
@@ -1723,6 +1746,8 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         a.bias_bs = d.bias_batch_stride;
         a.split = d.split ? 1 : 0;
         a.x_lo = d.x_lo; a.r_lo = d.res_lo; a.y_lo = d.y_lo;
+        a.res_f32 = d.res_f32 ? 1 : 0;
+        a.res_after = d.res_after_act ? 1 : 0;
         a.npix = d.batch * Ho * Wo;
         a.npix_in = d.batch * d.H * d.W;
         hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1766,6 +1791,8 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.ys = d.y_stride ? d.y_stride : d.OC;
     a.rs = d.res_stride ? d.res_stride : d.OC;
     a.res = static_cast<const half_t*>(d.residual);
+    a.res_f32 = d.res_f32 ? 1 : 0;
+    a.res_after = d.res_after_act ? 1 : 0;
     a.gate = d.gate;
     a.post_scale = d.post_scale;
     a.act = d.act;

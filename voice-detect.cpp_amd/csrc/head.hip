@@ -121,6 +121,7 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restr
     if (mv) r -= mv[o];
     if (act == VDK_ACT_RELU) r = fmaxf(r, 0.0f);
     else if (act == VDK_ACT_SIGMOID) r = 1.0f / (1.0f + expf(-r));
+    else if (act == VDK_ACT_TANH) r = tanhf(r);
     y[i] = r;
 }
 
@@ -174,7 +175,8 @@ extern "C" int vdk_linear_ex(const float* d_x, int batch, int in_dim, const floa
     return guarded([&] {
         require(d_x && d_w && d_y && d_work, "linear: NULL device pointer");
         require(batch > 0 && in_dim > 0 && out_dim > 0, "linear: empty shape");
-        require(act == VDK_ACT_NONE || act == VDK_ACT_RELU || act == VDK_ACT_SIGMOID, "linear: unknown activation");
+        require(act == VDK_ACT_NONE || act == VDK_ACT_RELU || act == VDK_ACT_SIGMOID || act == VDK_ACT_TANH,
+                "linear: unknown activation");
         require(work_bytes >= vdk_linear_workspace_size(batch, in_dim, out_dim),
                 "linear: workspace smaller than vdk_linear_workspace_size()");
         const int ns = linear_splits(in_dim);

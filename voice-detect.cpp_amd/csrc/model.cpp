@@ -79,6 +79,33 @@ std::unique_ptr<Model> Model::load(const std::string& path) {
         cp.emb_bn_var = g.str(p + "emb_bn_var");
         cp.bn_eps = g.f32(p + "bn_eps", 1e-5f);
     }
+    if (c.analyze_present) {   // src/model_loader.cpp:175-180
+        c.emotion_labels = g.str_arr("voicedetect.analyze.emotion_labels");
+        c.gender_labels = g.str_arr("voicedetect.analyze.gender_labels");
+    }
+    if (c.arch == "wav2vec2_emotion" || c.arch == "wav2vec2_age_gender") {
+        W2v2Cfg& w = c.w2v2;   // src/model_loader.cpp:181-207
+        const std::string p = "voicedetect.w2v2.";
+        w.hidden = (int)g.u32(p + "hidden_size", 0);
+        w.n_layers = (int)g.u32(p + "n_layers", 0);
+        w.n_heads = (int)g.u32(p + "n_heads", 0);
+        w.ff = (int)g.u32(p + "ff_dim", 0);
+        w.conv_dims = g.i32_arr(p + "conv_dims");
+        w.conv_kernels = g.i32_arr(p + "conv_kernels");
+        w.conv_strides = g.i32_arr(p + "conv_strides");
+        w.feat_extract_norm = g.str(p + "feat_extract_norm");
+        w.conv_bias = g.boolean(p + "conv_bias", false);
+        w.do_normalize = g.boolean(p + "do_normalize", false);
+        w.feat_extract_activation = g.str(p + "feat_extract_activation");
+        w.hidden_act = g.str(p + "hidden_act");
+        w.stable_layer_norm = g.boolean(p + "do_stable_layer_norm", false);
+        w.eps = g.f32(p + "layer_norm_eps", 1e-5f);
+        w.pos_k = (int)g.u32(p + "num_conv_pos_embeddings", 0);
+        w.pos_groups = (int)g.u32(p + "num_conv_pos_embedding_groups", 0);
+        w.pos_norm_dim = (int)g.u32(p + "pos_conv_weight_norm_dim", 2);
+        w.weighted_layer_sum = g.boolean(p + "use_weighted_layer_sum", false);
+        w.proj = (int)g.u32(p + "classifier_proj_size", 0);
+    }
     // src/model_loader.cpp:212-214: a speaker model needs an embedding dim.
     if (c.embedding_dim <= 0 && !c.analyze_present) throw Error("gguf: voicedetect.embedding_dim missing");
     return m;
@@ -106,8 +133,14 @@ void Model::ensure_device() {
     VDK_HIP(hipGetDevice(&device_));
     const bool resnet = cfg_.arch == "wespeaker_resnet34", ecapa = cfg_.arch == "ecapa_tdnn";
     const bool campp = cfg_.arch == "campplus", eres = cfg_.arch == "eres2net";
-    if (!resnet && !ecapa && !campp && !eres) throw Error("voicedetect: unsupported arch '" + cfg_.arch + "'");
+    if (!resnet && !ecapa && !campp && !eres && !is_analyzer())
+        throw Error("voicedetect: unsupported arch '" + cfg_.arch + "'");
     if (!stream_) VDK_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    if (is_analyzer()) {   // raw-waveform model: no FBank front end
+        upload_w2v2();
+        ready_ = true;
+        return;
+    }
     const size_t tb = vdk_fbank_tables_size(&cfg_.fbank);
     if (tb == 0) throw Error(vdk_last_error());
     if (!fb_tables_) VDK_HIP(hipMalloc(&fb_tables_, tb));
@@ -220,6 +253,10 @@ void Model::ensure_workspace(int batch, int n_samples) {
     w.batch = batch;
     w.n_samples = n_samples;
     w.pcm = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * n_samples));
+    if (is_analyzer()) {
+        alloc_w2v2_workspace(batch, n_samples);
+        return;
+    }
     w.feats = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * nmel * T));
     w.pooled = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * pooled_dim_));
     w.pre = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * cfg_.embedding_dim));
@@ -364,6 +401,7 @@ void Model::embed_batch_device(const float* d_pcm, int batch, int n_samples, flo
     std::lock_guard<std::mutex> lock(mu_);
     require(batch > 0, "voicedetect: batch must be positive");
     require(d_pcm && d_out, "voicedetect: NULL device pointer");
+    require(!is_analyzer(), "voicedetect: this model has no speaker embedding head (an analyze model)");
     if (frames(n_samples) <= 0) throw Error("voicedetect: FBank produced no frames");
     ensure_device();
     ensure_workspace(batch, n_samples);
@@ -374,6 +412,7 @@ void Model::embed_capture(const float* pcm, int batch, int n_samples, float* fea
                           float* pre_norm, float* out) {
     std::lock_guard<std::mutex> lock(mu_);
     require(batch > 0 && pcm, "voicedetect: invalid pcm batch");
+    require(!is_analyzer(), "voicedetect: this model has no speaker embedding head (an analyze model)");
     if (frames(n_samples) <= 0) throw Error("voicedetect: FBank produced no frames");
     ensure_device();
     ensure_workspace(batch, n_samples);
@@ -398,6 +437,7 @@ void Model::embed_batch_host(const float* pcm, int batch, int n_samples, float* 
 }
 
 std::vector<float> Model::embed_pcm(const std::vector<float>& pcm, int sample_rate) {
+    require(!is_analyzer(), "voicedetect: this model has no speaker embedding head (an analyze model)");
     const std::vector<float> x = sample_rate == 16000 ? pcm : resample_linear(pcm, sample_rate, 16000);
     if (frames((int)x.size()) <= 0) throw Error("voicedetect: FBank produced no frames");
     std::vector<float> out((size_t)cfg_.embedding_dim);

@@ -44,6 +44,16 @@ struct ERes2NetCfg {
     float relu_clamp = 20.0f, var_eps = 1e-8f;
 };
 
+// wav2vec2 analyze models, `voicedetect.w2v2.*` (src/model_loader.hpp:112-135).
+struct W2v2Cfg {
+    int hidden = 0, n_layers = 0, n_heads = 0, ff = 0;
+    std::vector<int32_t> conv_dims, conv_kernels, conv_strides;
+    std::string feat_extract_norm, feat_extract_activation, hidden_act;
+    bool conv_bias = false, do_normalize = false, stable_layer_norm = false, weighted_layer_sum = false;
+    float eps = 1e-5f;
+    int pos_k = 0, pos_groups = 0, pos_norm_dim = 2, proj = 0;
+};
+
 struct ModelConfig {
     std::string arch;
     int embedding_dim = 0;
@@ -53,6 +63,8 @@ struct ModelConfig {
     ResNetCfg resnet;
     CamPPlusCfg campplus;
     ERes2NetCfg eres2net;
+    W2v2Cfg w2v2;
+    std::vector<std::string> emotion_labels, gender_labels;   // src/model_loader.hpp:140-142
 };
 
 // Throws vdk::Error with vdk_last_error() when a vdk_* call returned nonzero.
@@ -86,6 +98,24 @@ public:
                        float* pre_norm, float* out);
     void synchronize();
     hipStream_t stream();
+
+    // ---- wav2vec2 analyze models (arch wav2vec2_emotion / wav2vec2_age_gender) ----
+    bool is_analyzer() const;
+    // Raw head outputs per clip: emotion logits, or [age_raw, gender logits...].
+    int analyze_outputs() const;
+    // Frames T' after the conv feature encoder for n samples (0 if too short).
+    int analyze_frames(int n_samples) const;
+    int analyze_hidden() const { return cfg_.w2v2.hidden; }
+    int analyze_feat_dim() const { return cfg_.w2v2.conv_dims.empty() ? 0 : cfg_.w2v2.conv_dims.back(); }
+    // batch x n_samples host PCM (16 kHz) -> batch x analyze_outputs() host raw outputs.
+    void analyze_batch_host(const float* pcm, int batch, int n_samples, float* raw);
+    // Device-resident batch on this context's stream; returns without waiting.
+    void analyze_batch_device(const float* d_pcm, int batch, int n_samples, float* d_raw);
+    // Same as analyze_batch_host, also copying (NULL = skip) the conv features
+    // [B][T'][feat_dim] and the last hidden state [B][T'][hidden].
+    void analyze_capture(const float* pcm, int batch, int n_samples, float* feat, float* hidden, float* raw);
+    // The reference's analyze JSON for one clip (src/analyze_w2v2.cpp:561-594, 632-668).
+    std::string analyze_json(const std::vector<float>& pcm, int sample_rate);
 
     void set_profiling(bool on, const std::string& name_prefix = std::string());
     // Waits for the stream and returns the per-launch records since the last call.
@@ -190,6 +220,30 @@ private:
         float* seg_w = nullptr;    // f32 [E][2*c_out*h_out]
         float* seg_b = nullptr;
     };
+    // wav2vec2: every f16 matrix in the implicit-GEMM layout [OC][K][IC].
+    struct W2Norm { float* g = nullptr; float* b = nullptr; };
+    struct W2Layer {
+        Layer qkv, out, ff1, ff2;   // qkv: q, k, v weights stacked [3H][H]
+        W2Norm ln1, ln2;            // layer_norm, final_layer_norm
+    };
+    struct W2v2 {
+        float* conv0_w = nullptr;   // f32 [C0][K0]
+        float* conv0_b = nullptr;
+        W2Norm conv0_n;
+        std::vector<Layer> convs;   // conv layers 1.. (k = kernel, stride in strides)
+        std::vector<W2Norm> conv_n; // their LayerNorms ("layer" feature norm)
+        W2Norm fp_n;                // feature_projection.layer_norm
+        Layer proj;
+        std::vector<void*> pos_w;   // per group f16 [icg][K][icg] (weight norm applied)
+        float* pos_b = nullptr;
+        W2Norm enc_n;
+        std::vector<W2Layer> layers;
+        std::vector<float> state_w; // softmax(layer_weights) per hidden state (host)
+        float *head_w1 = nullptr, *head_b1 = nullptr, *head_w2 = nullptr, *head_b2 = nullptr;   // projector / classifier
+        float *age_w1 = nullptr, *age_b1 = nullptr, *age_w2 = nullptr, *age_b2 = nullptr;
+        float *gen_w1 = nullptr, *gen_b1 = nullptr, *gen_w2 = nullptr, *gen_b2 = nullptr;
+        int n_out = 0;
+    };
     struct Workspace {
         int batch = 0, n_samples = 0;
         std::vector<void*> allocs;      // every allocation below, freed together
@@ -217,6 +271,13 @@ private:
         void *ex[2] = {nullptr, nullptr}, *es4 = nullptr, *esc = nullptr, *ez = nullptr, *ez2 = nullptr,
              *ef = nullptr;
         void *ecat[3] = {nullptr, nullptr, nullptr}, *efuse[3] = {nullptr, nullptr, nullptr};
+        // wav2vec2
+        float *wstats = nullptr, *fe32 = nullptr, *z = nullptr, *acc = nullptr, *wpool = nullptr, *wt1 = nullptr,
+              *wt2 = nullptr, *raw = nullptr;
+        void *fe[2] = {nullptr, nullptr}, *u = nullptr, *wproj = nullptr, *wh = nullptr, *wh1 = nullptr,
+             *qkv = nullptr, *att = nullptr, *ffb = nullptr, *c0_work = nullptr;
+        size_t c0_work_bytes = 0;
+        int feat_buf = 0;           // which fe[] holds the conv features after a forward
     };
 
     void ensure_device();
@@ -224,7 +285,10 @@ private:
     void upload_ecapa();
     void upload_campplus();
     void upload_eres2net();
+    void upload_w2v2();
     void ensure_workspace(int batch, int n_samples);
+    void alloc_w2v2_workspace(int batch, int n_samples);
+    void analyze_forward(const float* d_pcm, int batch, int n_samples, float* d_raw);
     void alloc_resnet_workspace(int batch, int T);
     void alloc_ecapa_workspace(int batch, int T);
     void alloc_campplus_workspace(int batch, int T);
@@ -267,6 +331,7 @@ private:
     Ecapa ecapa_;
     Campplus campp_;
     Eres2net eres_;
+    W2v2 w2_;
     float* seg_w_ = nullptr;
     float* seg_b_ = nullptr;
     float* mean_vec_ = nullptr;

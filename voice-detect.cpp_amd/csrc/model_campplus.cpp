@@ -199,7 +199,7 @@ void Model::conv_ex(const char* name, const vdk_conv_desc& d) {
         const int sh = d.stride_h ? d.stride_h : 1, sw = d.stride_w ? d.stride_w : 1;
         const int dh = d.dil_h ? d.dil_h : 1, dw = d.dil_w ? d.dil_w : 1;
         const int Ho = (d.H + 2 * d.pad_h - (d.KH - 1) * dh - 1) / sh + 1;
-        const int Wo = (d.W + 2 * d.pad_w - (d.KW - 1) * dw - 1) / sw + 1;
+        const int Wo = d.out_w > 0 ? d.out_w : (d.W + 2 * d.pad_w - (d.KW - 1) * dw - 1) / sw + 1;
         const double npix = (double)d.batch * Ho * Wo;
         const double flops = 2.0 * d.KH * d.KW * d.IC * (double)d.OC * npix;
         const double halves = d.split ? 2.0 : 1.0;   // split-f16 moves hi and lo

@@ -1,0 +1,523 @@
+// w2v2.hip - wav2vec2 analyze kernels on gfx950 (reference src/analyze_w2v2.cpp).
+//
+// The GEMM-shaped work of the analyze path (feature-encoder convs 1..n,
+// feature projection, q/k/v/out projections, feed-forward, positional conv)
+// runs on the implicit-GEMM conv kernels (conv.hip) over time-major f16
+// [B][T][C] maps.  This file holds the rest:
+//   wave_stats_kernel      do_normalize statistics of the raw waveform
+//   conv0_*_kernel         conv layer 0 (one input channel, so no GEMM) with its
+//                          GroupNorm (per channel over time) or LayerNorm (per
+//                          frame over channels) and the exact GELU
+//   layer_norm_kernel      LayerNorm over rows, optional GELU and a weighted
+//                          accumulation (the emotion head's layer sum)
+//   attention_kernel       softmax(q k^T * scale) v per (clip, head) on f16
+//                          MFMA, streaming 64-key blocks with an online softmax
+//   time_mean_kernel       per-clip mean over time
+// Reductions run in a fixed order (f64 where they feed a normalisation), so
+// results do not depend on scheduling.
+#include <cfloat>
+#include <cmath>
+
+#include "common.hpp"
+#include "devmath.hpp"
+#include "vdk.h"
+
+namespace vdk {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum over a workgroup of NT threads, fixed order; every thread gets the total.
+template <int NT>
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+    v = wave_sum_d(v);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) s += red[i];
+    return s;
+}
+
+// ---- do_normalize statistics: mean and 1/sqrt(biased var + eps) per clip,
+// two passes in f64 (src/analyze_w2v2.cpp:63-70).
+__global__ __launch_bounds__(1024) void wave_stats_kernel(const float* __restrict__ x, int n, float eps,
+                                                          float* __restrict__ stats) {
+    __shared__ double red[16];
+    const float* xc = x + (size_t)blockIdx.x * n;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += 1024) s += (double)xc[i];
+    const double mean = block_sum_d<1024>(s, red) / n;
+    double v = 0.0;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const double d = (double)xc[i] - mean;
+        v += d * d;
+    }
+    v = block_sum_d<1024>(v, red) / n;
+    if (threadIdx.x == 0) {
+        stats[2 * blockIdx.x] = (float)mean;
+        stats[2 * blockIdx.x + 1] = (float)(1.0 / sqrt(v + (double)eps));
+    }
+}
+
+// ---- conv layer 0: y[b][t][c] = bias[c] + sum_k w[c][k] xn[b][t*S + k] ----
+// xn = (x - mean) * rstd when do_normalize statistics are given.  A
+// workgroup covers kFrames frames of one clip; the waveform window it needs
+// is staged in LDS once.
+constexpr int kFrames = 64, kMaxK = 16, kMaxS = 8;
+constexpr int kWin = (kFrames - 1) * kMaxS + kMaxK;
+
+__device__ __forceinline__ void load_window(const float* x, int n, const float* wstats, int b, int start, int len,
+                                            float* sx) {
+    const float* xc = x + (size_t)b * n;
+    const float mean = wstats ? wstats[2 * b] : 0.0f, rstd = wstats ? wstats[2 * b + 1] : 1.0f;
+    for (int i = threadIdx.x; i < len; i += blockDim.x) {
+        const float v = xc[start + i];
+        sx[i] = wstats ? (v - mean) * rstd : v;
+    }
+}
+
+// GroupNorm statistics (num_groups == channels): per (clip, chunk, channel)
+// sum of y (mean == NULL) or of (y - mean)^2, in f64.
+__global__ __launch_bounds__(256) void conv0_stats_kernel(const float* __restrict__ x, int n,
+                                                          const float* __restrict__ wstats,
+                                                          const float* __restrict__ w, const float* __restrict__ bias,
+                                                          int C, int K, int S, int T0,
+                                                          const double* __restrict__ mean,
+                                                          double* __restrict__ part) {
+    __shared__ float sx[kWin];
+    const int b = blockIdx.y, chunk = blockIdx.x, t0 = chunk * kFrames;
+    const int nt = T0 - t0 < kFrames ? T0 - t0 : kFrames;
+    load_window(x, n, wstats, b, t0 * S, (nt - 1) * S + K, sx);
+    __syncthreads();
+    for (int c = threadIdx.x; c < C; c += 256) {
+        float wk[kMaxK];
+#pragma unroll
+        for (int k = 0; k < kMaxK; ++k) wk[k] = k < K ? w[c * K + k] : 0.0f;
+        const float bc = bias ? bias[c] : 0.0f;
+        const double mc = mean ? mean[(size_t)b * C + c] : 0.0;
+        double acc = 0.0;
+        for (int t = 0; t < nt; ++t) {
+            float y = bc;
+#pragma unroll
+            for (int k = 0; k < kMaxK; ++k)
+                if (k < K) y += wk[k] * sx[t * S + k];
+            const double d = (double)y - mc;
+            acc += mean ? d * d : (double)y;
+        }
+        part[((size_t)b * gridDim.x + chunk) * C + c] = acc;
+    }
+}
+
+// Chunk partials -> mean (pass 0) or the GroupNorm affine (pass 1):
+// scale = gamma / sqrt(var + eps), shift = beta - mean * scale.
+__global__ __launch_bounds__(256) void conv0_finalize_kernel(const double* __restrict__ part, int nchunk, int C,
+                                                             int T0, int pass, double* __restrict__ mean,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, float eps,
+                                                             float* __restrict__ scale, float* __restrict__ shift) {
+    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (c >= C) return;
+    double s = 0.0;
+    for (int j = 0; j < nchunk; ++j) s += part[((size_t)b * nchunk + j) * C + c];
+    const size_t o = (size_t)b * C + c;
+    if (pass == 0) {
+        mean[o] = s / T0;
+        return;
+    }
+    const double var = s / T0;
+    const double sc = (double)gamma[c] / sqrt(var + (double)eps);
+    scale[o] = (float)sc;
+    shift[o] = (float)((double)beta[c] - mean[o] * sc);
+}
+
+// One wave per frame; lane l owns channels l*CPL .. l*CPL + CPL - 1.
+// norm 0: none; 1: GroupNorm affine from scale/shift [B][C]; 2: LayerNorm over
+// the frame's C channels (gamma, beta, eps).  Then GELU, stored f16.
+template <int CPL>
+__global__ __launch_bounds__(256) void conv0_apply_kernel(const float* __restrict__ x, int n,
+                                                          const float* __restrict__ wstats,
+                                                          const float* __restrict__ w, const float* __restrict__ bias,
+                                                          int K, int S, int T0, int norm,
+                                                          const float* __restrict__ scale,
+                                                          const float* __restrict__ shift,
+                                                          const float* __restrict__ gamma,
+                                                          const float* __restrict__ beta, float eps,
+                                                          half_t* __restrict__ y) {
+    constexpr int C = CPL * 64;
+    __shared__ float sx[kWin];
+    const int b = blockIdx.y, t0 = blockIdx.x * kFrames;
+    const int nt = T0 - t0 < kFrames ? T0 - t0 : kFrames;
+    load_window(x, n, wstats, b, t0 * S, (nt - 1) * S + K, sx);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c0 = lane * CPL;
+    float wr[CPL][kMaxK], bc[CPL], sa[CPL], sb[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int k = 0; k < kMaxK; ++k) wr[j][k] = k < K ? w[(c0 + j) * K + k] : 0.0f;
+        bc[j] = bias ? bias[c0 + j] : 0.0f;
+        sa[j] = norm == 1 ? scale[(size_t)b * C + c0 + j] : (norm == 2 ? gamma[c0 + j] : 1.0f);
+        sb[j] = norm == 1 ? shift[(size_t)b * C + c0 + j] : (norm == 2 ? beta[c0 + j] : 0.0f);
+    }
+    __syncthreads();
+    for (int t = wave; t < nt; t += 4) {
+        float v[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            float a = bc[j];
+#pragma unroll
+            for (int k = 0; k < kMaxK; ++k)
+                if (k < K) a += wr[j][k] * sx[t * S + k];
+            v[j] = a;
+        }
+        if (norm == 2) {
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) s += v[j];
+            const float mu = wave_sum(s) / C;
+            float q = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) q += (v[j] - mu) * (v[j] - mu);
+            const float rstd = 1.0f / sqrtf(wave_sum(q) / C + eps);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) v[j] = (v[j] - mu) * rstd;
+        }
+        half_t* yo = y + ((size_t)b * T0 + t0 + t) * C + c0;
+#pragma unroll
+        for (int j0 = 0; j0 < CPL; j0 += 4) {
+            half4 h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)gelu_erf(v[j0 + e] * sa[j0 + e] + sb[j0 + e]);
+            *reinterpret_cast<half4*>(yo + j0) = h;
+        }
+    }
+}
+
+// ---- LayerNorm over rows of C (one wave per row, lane l owns elements
+// l + 64 j) with optional GELU and acc = [acc +] acc_w * (input | output).
+template <int EMAX>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const void* __restrict__ x, int rows, int C,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ beta, float eps, int flags,
+                                                         void* __restrict__ y, float* __restrict__ acc, float acc_w) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int E = C >> 6;
+    const bool xf = flags & VDK_LN_X_F32;
+    const size_t base = (size_t)row * C;
+    float v[EMAX];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j) {
+        v[j] = 0.0f;
+        if (j < E) {
+            const size_t i = base + lane + 64 * j;
+            v[j] = xf ? static_cast<const float*>(x)[i] : (float)static_cast<const half_t*>(x)[i];
+            s += v[j];
+        }
+    }
+    const float mu = wave_sum(s) / C;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j)
+        if (j < E) q += (v[j] - mu) * (v[j] - mu);
+    const float rstd = 1.0f / sqrtf(wave_sum(q) / C + eps);
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j) {
+        if (j >= E) continue;
+        const int e = lane + 64 * j;
+        const size_t i = base + e;
+        float o = (v[j] - mu) * rstd * gamma[e] + beta[e];
+        if (flags & VDK_LN_GELU) o = gelu_erf(o);
+        if (acc) {
+            const float src = (flags & VDK_LN_ACC_INPUT) ? v[j] : o;
+            acc[i] = (flags & VDK_LN_ACC_INIT) ? acc_w * src : acc[i] + acc_w * src;
+        }
+        if (y) {
+            if (flags & VDK_LN_Y_F32) static_cast<float*>(y)[i] = o;
+            else static_cast<half_t*>(y)[i] = (half_t)o;
+        }
+    }
+}
+
+// ---- self-attention per (clip, head), head_dim 64 ----
+// qkv [B][T][3H] f16 (q | k | v, head h at columns h*64 of each), out [B][T][H].
+// A workgroup (4 waves) owns 128 queries of one (clip, head); wave w owns 32.
+// Scores are computed transposed, S^T = K Q^T (32 keys x 32 queries per MFMA
+// block), so each lane holds one query's column: the row max / sum need one
+// exchange with lane ^ 32, and P^T is already the B operand of
+// O^T += V^T P^T.  MFMA k-slot j of lane half h stands for key
+// 16c + 4h + j (j < 4) or 16c + 8 + 4h + (j - 4): the keys the S^T
+// accumulator gives that lane, so P^T needs no shuffle; V is staged in LDS
+// transposed ([dim][key]) so the matching A operand is two 8-byte reads.
+constexpr int kHD = 64, kKB = 64, kKR = kHD + 8, kVR = kKB + 8;
+
+__global__ __launch_bounds__(256) void attention_kernel(const half_t* __restrict__ qkv, int T, int H, float scale_log2,
+                                                        half_t* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) half_t sK[kKB * kKR];   // [key][dim]
+    __shared__ __attribute__((aligned(16))) half_t sV[kHD * kVR];   // [dim][key]
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, lr = lane & 31;
+    const size_t rs = 3 * (size_t)H;
+    const half_t* base = qkv + (size_t)b * T * rs;
+    const int q0 = blockIdx.x * 128 + wave * 32;
+    const int qr = q0 + lr < T ? q0 + lr : T - 1;
+    half8 qf[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+        qf[kk] = *reinterpret_cast<const half8*>(base + qr * rs + h * kHD + 16 * kk + 8 * hl);
+    float16v o0, o1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { o0[r] = 0.0f; o1[r] = 0.0f; }
+    float m = -INFINITY, l = 0.0f;
+    const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int kb = 0; kb < T; kb += kKB) {
+        __syncthreads();   // the previous block's operands are no longer read
+#pragma unroll
+        for (int i = tid; i < kKB * kHD / 8; i += 256) {
+            const int key = i >> 3, d0 = (i & 7) * 8, kg = kb + key;
+            const half_t* src = base + (size_t)kg * rs + h * kHD + d0;
+            const half8 kv = kg < T ? *reinterpret_cast<const half8*>(src + H) : zero8;
+            const half8 vv = kg < T ? *reinterpret_cast<const half8*>(src + 2 * H) : zero8;
+            *reinterpret_cast<half8*>(&sK[key * kKR + d0]) = kv;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sV[(d0 + e) * kVR + key] = vv[e];
+        }
+        __syncthreads();
+        float16v s[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const half8 a = *reinterpret_cast<const half8*>(&sK[(kt * 32 + lr) * kKR + 16 * kk + 8 * hl]);
+                s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], s[kt], 0, 0, 0);
+            }
+        }
+        // s[kt][r]: key kb + 32 kt + 8 (r / 4) + 4 hl + r % 4 of query q0 + lr
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kb + kt * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+                const float v = key < T ? s[kt][r] * scale_log2 : -INFINITY;
+                s[kt][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m, mx);   // finite: every block holds a key < T
+        const float alpha = exp2f(m - m_new);
+        float ls = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = exp2f(s[kt][r] - m_new);
+                s[kt][r] = p;
+                ls += p;
+            }
+        ls += __shfl_xor(ls, 32, 64);
+        l = l * alpha + ls;
+        m = m_new;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) { o0[r] *= alpha; o1[r] *= alpha; }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            half8 pb;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pb[j] = (half_t)s[c >> 1][8 * (c & 1) + j];
+            const int kc = 16 * c + 4 * hl;
+            const half4 a0l = *reinterpret_cast<const half4*>(&sV[lr * kVR + kc]);
+            const half4 a0h = *reinterpret_cast<const half4*>(&sV[lr * kVR + kc + 8]);
+            const half4 a1l = *reinterpret_cast<const half4*>(&sV[(lr + 32) * kVR + kc]);
+            const half4 a1h = *reinterpret_cast<const half4*>(&sV[(lr + 32) * kVR + kc + 8]);
+            const half8 a0 = {a0l[0], a0l[1], a0l[2], a0l[3], a0h[0], a0h[1], a0h[2], a0h[3]};
+            const half8 a1 = {a1l[0], a1l[1], a1l[2], a1l[3], a1h[0], a1h[1], a1h[2], a1h[3]};
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pb, o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pb, o1, 0, 0, 0);
+        }
+    }
+    if (q0 + lr >= T) return;
+    const float inv = 1.0f / l;
+    half_t* dst = out + ((size_t)b * T + q0 + lr) * H + h * kHD;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int d = 8 * g + 4 * hl;
+        half4 v0, v1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v0[e] = (half_t)(o0[4 * g + e] * inv);
+            v1[e] = (half_t)(o1[4 * g + e] * inv);
+        }
+        *reinterpret_cast<half4*>(dst + d) = v0;
+        *reinterpret_cast<half4*>(dst + 32 + d) = v1;
+    }
+}
+
+// ---- per-clip mean over time: out[b][c] = mean_t x[b][t][c] (f64, 4 time
+// partitions combined in a fixed order).
+__global__ __launch_bounds__(256) void time_mean_kernel(const void* __restrict__ x, int x_f32, int T, int C,
+                                                        float* __restrict__ out) {
+    __shared__ double part[4][64];
+    const int tx = threadIdx.x & 63, tp = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + tx, b = blockIdx.y;
+    double s = 0.0;
+    if (c < C) {
+        for (int t = tp; t < T; t += 4) {
+            const size_t i = ((size_t)b * T + t) * C + c;
+            s += x_f32 ? (double)static_cast<const float*>(x)[i] : (double)(float)static_cast<const half_t*>(x)[i];
+        }
+    }
+    part[tp][tx] = s;
+    __syncthreads();
+    if (tp == 0 && c < C) out[(size_t)b * C + c] = (float)(((part[0][tx] + part[1][tx]) + (part[2][tx] + part[3][tx])) / T);
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int conv0_frames(int n, int K, int S) { return n < K ? 0 : (n - K) / S + 1; }
+
+size_t conv0_work(int batch, int n, int C, int K, int S) {
+    const int T0 = conv0_frames(n, K, S);
+    const size_t nchunk = (size_t)(T0 + kFrames - 1) / kFrames;
+    // partials [B][nchunk][C] f64, mean [B][C] f64, scale / shift [B][C] f32
+    return (size_t)batch * C * (8 * nchunk + 8 + 4 + 4) + 256;
+}
+
+}  // namespace
+}  // namespace vdk
+
+using namespace vdk;
+
+extern "C" int vdk_wave_stats(const float* d_x, int batch, int n, float eps, float* d_stats, void* stream) {
+    return guarded([&] {
+        require(d_x && d_stats, "wave_stats: NULL device pointer");
+        require(batch > 0 && n > 0, "wave_stats: empty input");
+        hipLaunchKernelGGL(wave_stats_kernel, dim3(batch), dim3(1024), 0, static_cast<hipStream_t>(stream), d_x, n,
+                           eps, d_stats);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" size_t vdk_w2v2_conv0_workspace_size(int batch, int n, int C, int K, int S) {
+    if (batch <= 0 || C <= 0 || K <= 0 || S <= 0 || conv0_frames(n, K, S) <= 0) return 0;
+    return conv0_work(batch, n, C, K, S);
+}
+
+extern "C" int vdk_w2v2_conv0(const float* d_x, int batch, int n, const float* d_stats, const float* d_w,
+                              const float* d_bias, int C, int K, int S, int norm, const float* d_gamma,
+                              const float* d_beta, float eps, void* d_work, size_t work_bytes, void* d_y,
+                              void* stream) {
+    return guarded([&] {
+        require(d_x && d_w && d_y, "w2v2_conv0: NULL device pointer");
+        require(batch > 0 && K >= 1 && K <= kMaxK && S >= 1 && S <= kMaxS, "w2v2_conv0: kernel 1..16, stride 1..8");
+        require(C == 256 || C == 512 || C == 1024, "w2v2_conv0: channels must be 256, 512 or 1024");
+        require(norm >= 0 && norm <= 2, "w2v2_conv0: norm must be 0 (none), 1 (group) or 2 (layer)");
+        require(norm == 0 || (d_gamma && d_beta), "w2v2_conv0: a norm needs gamma and beta");
+        const int T0 = conv0_frames(n, K, S);
+        require(T0 > 0, "w2v2_conv0: clip shorter than the kernel");
+        require((size_t)batch * n < (1ull << 31) && (size_t)batch * T0 * C < (1ull << 31),
+                "w2v2_conv0: input too large for one launch");
+        require(al16(d_y), "w2v2_conv0: output must be 16-byte aligned");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const int nchunk = (T0 + kFrames - 1) / kFrames;
+        const float* scale = nullptr;
+        const float* shift = nullptr;
+        if (norm == 1) {
+            require(d_work && work_bytes >= conv0_work(batch, n, C, K, S), "w2v2_conv0: workspace too small");
+            double* part = static_cast<double*>(d_work);
+            double* mean = part + (size_t)batch * nchunk * C;
+            float* sc = reinterpret_cast<float*>(mean + (size_t)batch * C);
+            float* sh = sc + (size_t)batch * C;
+            const dim3 g(nchunk, batch), gf(cdiv(C, 256), batch);
+            for (int pass = 0; pass < 2; ++pass) {
+                hipLaunchKernelGGL(conv0_stats_kernel, g, dim3(256), 0, s, d_x, n, d_stats, d_w, d_bias, C, K, S, T0,
+                                   pass ? mean : nullptr, part);
+                VDK_HIP(hipGetLastError());
+                hipLaunchKernelGGL(conv0_finalize_kernel, gf, dim3(256), 0, s, part, nchunk, C, T0, pass, mean,
+                                   d_gamma, d_beta, eps, sc, sh);
+                VDK_HIP(hipGetLastError());
+            }
+            scale = sc;
+            shift = sh;
+        }
+        half_t* y = static_cast<half_t*>(d_y);
+        const dim3 g(nchunk, batch);
+        switch (C) {
+            case 256:
+                hipLaunchKernelGGL(conv0_apply_kernel<4>, g, dim3(256), 0, s, d_x, n, d_stats, d_w, d_bias, K, S, T0,
+                                   norm, scale, shift, d_gamma, d_beta, eps, y);
+                break;
+            case 512:
+                hipLaunchKernelGGL(conv0_apply_kernel<8>, g, dim3(256), 0, s, d_x, n, d_stats, d_w, d_bias, K, S, T0,
+                                   norm, scale, shift, d_gamma, d_beta, eps, y);
+                break;
+            default:
+                hipLaunchKernelGGL(conv0_apply_kernel<16>, g, dim3(256), 0, s, d_x, n, d_stats, d_w, d_bias, K, S,
+                                   T0, norm, scale, shift, d_gamma, d_beta, eps, y);
+                break;
+        }
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_layer_norm(const void* d_x, int rows, int C, const float* d_gamma, const float* d_beta, float eps,
+                              int flags, void* d_y, float* d_acc, float acc_w, void* stream) {
+    return guarded([&] {
+        require(d_x && d_gamma && d_beta && (d_y || d_acc), "layer_norm: NULL device pointer");
+        require(rows > 0 && C > 0 && C % 64 == 0 && C <= 4096, "layer_norm: C must be a multiple of 64 up to 4096");
+        require((flags & ~(VDK_LN_X_F32 | VDK_LN_Y_F32 | VDK_LN_GELU | VDK_LN_ACC_INPUT | VDK_LN_ACC_INIT)) == 0,
+                "layer_norm: unknown flag");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const dim3 g(cdiv(rows, 4));
+        if (C <= 1024)
+            hipLaunchKernelGGL(layer_norm_kernel<16>, g, dim3(256), 0, s, d_x, rows, C, d_gamma, d_beta, eps, flags,
+                               d_y, d_acc, acc_w);
+        else
+            hipLaunchKernelGGL(layer_norm_kernel<64>, g, dim3(256), 0, s, d_x, rows, C, d_gamma, d_beta, eps, flags,
+                               d_y, d_acc, acc_w);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_attention(const void* d_qkv, int batch, int T, int n_heads, int head_dim, float scale,
+                             void* d_out, void* stream) {
+    return guarded([&] {
+        require(d_qkv && d_out, "attention: NULL device pointer");
+        require(batch > 0 && T > 0 && n_heads > 0, "attention: empty shape");
+        require(head_dim == kHD, "attention: head_dim must be 64");
+        require(al16(d_qkv) && al16(d_out), "attention: buffers must be 16-byte aligned");
+        const size_t H = (size_t)n_heads * head_dim;
+        require((size_t)batch * T * 3 * H < (1ull << 31), "attention: too many tokens for one launch");
+        require(T <= 65535 * 128 && n_heads <= 65535 && batch <= 65535, "attention: grid too large");
+        hipLaunchKernelGGL(attention_kernel, dim3(cdiv(T, 128), n_heads, batch), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_qkv), T, (int)H,
+                           scale * 1.4426950408889634f, static_cast<half_t*>(d_out));
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_time_mean(const void* d_x, int x_f32, int batch, int T, int C, float* d_out, void* stream) {
+    return guarded([&] {
+        require(d_x && d_out, "time_mean: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0, "time_mean: empty shape");
+        hipLaunchKernelGGL(time_mean_kernel, dim3(cdiv(C, 64), batch), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           d_x, x_f32 ? 1 : 0, T, C, d_out);
+        VDK_HIP(hipGetLastError());
+    });
+}

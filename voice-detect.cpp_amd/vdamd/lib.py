@@ -25,7 +25,7 @@ class FbankCfg(C.Structure):
                 ("low_freq", C.c_float), ("high_freq", C.c_float), ("cmn", C.c_int)]
 
 
-ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_SILU = 0, 1, 2, 3
+ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_SILU, ACT_GELU, ACT_TANH = 0, 1, 2, 3, 4, 5
 
 
 class ConvDesc(C.Structure):
@@ -43,7 +43,7 @@ class ConvDesc(C.Structure):
                 ("tanh_after", C.c_int),
                 ("y", _vp), ("y_stride", C.c_int), ("y_f32", C.c_int), ("y_time_major", C.c_int),
                 ("split", C.c_int), ("x_lo", C.c_int), ("res_lo", C.c_int), ("y_lo", C.c_int),
-                ("tile", C.c_int)]
+                ("tile", C.c_int), ("res_f32", C.c_int), ("res_after_act", C.c_int), ("out_w", C.c_int)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
@@ -76,6 +76,11 @@ _SIGS = {
     "voicedetect_gpu_registry_set": (C.c_int, [_vp, _vp, C.c_int, C.c_int]),
     "voicedetect_gpu_identify_pcm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "voicedetect_gpu_identify_device_async": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "voicedetect_gpu_analyze_outputs": (C.c_int, [_vp]),
+    "voicedetect_gpu_analyze_frames": (C.c_int, [_vp, C.c_int]),
+    "voicedetect_gpu_analyze_pcm": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
+    "voicedetect_gpu_analyze_batch_async": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp]),
+    "voicedetect_gpu_analyze_capture": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp, _vp]),
     "voicedetect_gpu_stream": (_vp, [_vp]),
     "voicedetect_gpu_embed_capture": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp, C.POINTER(C.c_int), _vp, _vp]),
     "voicedetect_gpu_set_profiling": (C.c_int, [_vp, C.c_int]),
@@ -110,6 +115,13 @@ _SIGS = {
     "vdk_conv2d_tile_fits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "vdk_registry_topk_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "vdk_registry_topk": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_size_t, _vp, _vp, _vp]),
+    "vdk_wave_stats": (C.c_int, [_vp, C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "vdk_w2v2_conv0_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "vdk_w2v2_conv0": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp,
+                                 C.c_float, _vp, C.c_size_t, _vp, _vp]),
+    "vdk_layer_norm": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, C.c_float, C.c_int, _vp, _vp, C.c_float, _vp]),
+    "vdk_attention": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "vdk_time_mean": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_resblock3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdk_resblock3x3_variant": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                           C.c_int, _vp]),
@@ -307,6 +319,48 @@ class Context:
         if rc != 0:
             raise VdkError(self.last_error())
         return idx, score
+
+    # ---- analyze (wav2vec2 emotion / age-gender models) ----
+    def analyze_outputs(self):
+        return self.L.voicedetect_gpu_analyze_outputs(self.ctx)
+
+    def analyze_frames(self, n):
+        return self.L.voicedetect_gpu_analyze_frames(self.ctx, n)
+
+    def analyze_pcm(self, pcm, sample_rate=16000):
+        """Raw head outputs [B][outputs] for a batch of equal-length clips."""
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        if pcm.ndim == 1:
+            pcm = pcm[None, :]
+        B, n = pcm.shape
+        out = np.zeros((B, max(self.analyze_outputs(), 1)), dtype=np.float32)
+        if self.L.voicedetect_gpu_analyze_pcm(self.ctx, pcm.ctypes.data, B, n, sample_rate, out.ctypes.data) != 0:
+            raise VdkError(self.last_error())
+        return out
+
+    def analyze_capture(self, pcm, feat_dim, hidden):
+        """(feat [B][T'][feat_dim], last hidden state [B][T'][hidden], raw [B][outputs])."""
+        pcm = np.ascontiguousarray(pcm, dtype=np.float32)
+        B, n = pcm.shape
+        T = self.analyze_frames(n)
+        feat = np.zeros((B, T, feat_dim), dtype=np.float32)
+        hid = np.zeros((B, T, hidden), dtype=np.float32)
+        raw = np.zeros((B, max(self.analyze_outputs(), 1)), dtype=np.float32)
+        rc = self.L.voicedetect_gpu_analyze_capture(self.ctx, pcm.ctypes.data, B, n, feat.ctypes.data,
+                                                    hid.ctypes.data, raw.ctypes.data)
+        if rc != 0:
+            raise VdkError(self.last_error())
+        return feat, hid, raw
+
+    def analyze_path_json(self, path):
+        """voicedetect_capi_analyze_path_json: the JSON text, or raises VdkError."""
+        p = self.L.voicedetect_capi_analyze_path_json(self.ctx, path.encode())
+        if not p:
+            raise VdkError(self.last_error())
+        try:
+            return C.string_at(p).decode()
+        finally:
+            self.L.voicedetect_capi_free_string(p)
 
     def capture(self, pcm, n_mels=80):
         pcm = np.ascontiguousarray(pcm, dtype=np.float32)

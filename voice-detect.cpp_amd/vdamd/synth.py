@@ -477,3 +477,150 @@ def write_eres2net(path, seed, **kw):
     kv, tensors = make_eres2net(seed, **kw)
     G.write_gguf(path, kv, tensors)
     return path
+
+
+# ---------------------------------------------------------------- wav2vec2 analyze
+
+EMOTION_LABELS = ["neu", "hap", "ang", "sad"]
+GENDER_LABELS = ["female", "male", "child"]
+
+
+def w2v2_store_name(name):
+    """The reference converter's name transform for the analyze archs
+    (scripts/convert_voicedetect_to_gguf.py:127-140): module prefix wav2vec2. ->
+    w2v2., weight-norm parametrization original0/original1 -> weight_g/weight_v."""
+    if name.startswith("wav2vec2."):
+        name = "w2v2." + name[len("wav2vec2."):]
+    name = name.replace(".parametrizations.weight.original0", ".weight_g")
+    return name.replace(".parametrizations.weight.original1", ".weight_v")
+
+
+def w2v2_kv(kind, hidden, n_layers, n_heads, ff, conv_dims, conv_kernels, conv_strides, pos_k, pos_groups,
+            proj, labels, eps=1e-5):
+    """KV of an analyze GGUF (scripts/convert_voicedetect_to_gguf.py:725-763;
+    docs/conversion.md "wav2vec2 emotion / age-gender analyze head")."""
+    large = kind == "age_gender"
+    kv = {
+        "general.architecture": "voicedetect",
+        "voicedetect.arch": "wav2vec2_age_gender" if large else "wav2vec2_emotion",
+        "voicedetect.analyze.present": True,
+        "voicedetect.analyze.kind": kind,
+        "voicedetect.analyze.pooling": "mean",
+        "voicedetect.w2v2.conv_bias": large,
+        "voicedetect.w2v2.do_normalize": large,
+        "voicedetect.w2v2.hidden_size": hidden,
+        "voicedetect.w2v2.n_layers": n_layers,
+        "voicedetect.w2v2.n_heads": n_heads,
+        "voicedetect.w2v2.ff_dim": ff,
+        "voicedetect.w2v2.num_conv_layers": len(conv_dims),
+        "voicedetect.w2v2.conv_dims": [G.I32(v) for v in conv_dims],
+        "voicedetect.w2v2.conv_kernels": [G.I32(v) for v in conv_kernels],
+        "voicedetect.w2v2.conv_strides": [G.I32(v) for v in conv_strides],
+        "voicedetect.w2v2.feat_extract_norm": "layer" if large else "group",
+        "voicedetect.w2v2.feat_extract_activation": "gelu",
+        "voicedetect.w2v2.hidden_act": "gelu",
+        "voicedetect.w2v2.do_stable_layer_norm": large,
+        "voicedetect.w2v2.layer_norm_eps": float(eps),
+        "voicedetect.w2v2.num_conv_pos_embeddings": pos_k,
+        "voicedetect.w2v2.num_conv_pos_embedding_groups": pos_groups,
+        "voicedetect.w2v2.pos_conv_weight_norm_dim": 2,
+        "voicedetect.w2v2.use_weighted_layer_sum": not large,
+        "voicedetect.w2v2.classifier_proj_size": proj,
+    }
+    if large:
+        kv["voicedetect.analyze.gender_labels"] = list(labels)
+        kv["voicedetect.analyze.num_genders"] = len(labels)
+    else:
+        kv["voicedetect.analyze.emotion_labels"] = list(labels)
+        kv["voicedetect.analyze.num_emotions"] = len(labels)
+    return kv
+
+
+W2V2_BASE = dict(hidden=768, n_layers=12, n_heads=12, ff=3072, conv_dims=(512,) * 7,
+                 conv_kernels=(10, 3, 3, 3, 3, 2, 2), conv_strides=(5, 2, 2, 2, 2, 2, 2), pos_k=128,
+                 pos_groups=16, proj=256)
+W2V2_LARGE = dict(W2V2_BASE, hidden=1024, n_layers=24, n_heads=16, ff=4096)
+
+
+def make_w2v2(seed, kind="emotion", labels=None, **dims):
+    """Random-init wav2vec2 analyze model (emotion: wav2vec2-base with the
+    weighted-layer-sum classifier; age_gender: wav2vec2-large-robust with the
+    audeering age/gender heads) in the reference GGUF schema, all tensors F32
+    as the reference converter stores them.  Matrix values are f16-exact.
+
+    Init: conv N(0, sqrt(2/fan_in)); linear N(0, sqrt(1/fan_in)), bias N(0, 0.02);
+    LayerNorm / GroupNorm gamma 1 + N(0, 0.1), beta N(0, 0.1); positional conv
+    weight_v N(0, 1), weight_g U(1, 3); layer_weights N(0, 1).
+    """
+    d = dict(W2V2_LARGE if kind == "age_gender" else W2V2_BASE)
+    d.update(dims)
+    large = kind == "age_gender"
+    if labels is None:
+        labels = GENDER_LABELS if large else EMOTION_LABELS
+    H, L, FF = d["hidden"], d["n_layers"], d["ff"]
+    ws = _WeightStream(seed)
+    T = []
+
+    def put(name, arr):
+        arr = np.asarray(arr, dtype=np.float32)
+        T.append((w2v2_store_name(name), G.GGML_F32, list(arr.shape), arr))
+
+    def mat(shape, std):
+        n = int(np.prod(shape))
+        return _f16_exact(normal(ws.next(), n).reshape(shape) * std)
+
+    def vec(n, std, mean=0.0):
+        return (mean + std * normal(ws.next(), n)).astype(np.float32)
+
+    def norm(name, c):
+        put(name + ".weight", vec(c, 0.1, 1.0))
+        put(name + ".bias", vec(c, 0.1))
+
+    def linear(name, o, i):
+        put(name + ".weight", mat((o, i), np.sqrt(1.0 / i)))
+        put(name + ".bias", vec(o, 0.02))
+
+    ic = 1
+    for i, (oc, k) in enumerate(zip(d["conv_dims"], d["conv_kernels"])):
+        p = f"wav2vec2.feature_extractor.conv_layers.{i}"
+        put(p + ".conv.weight", mat((oc, ic, k), np.sqrt(2.0 / (ic * k))))
+        if large:
+            put(p + ".conv.bias", vec(oc, 0.02))
+            norm(p + ".layer_norm", oc)
+        elif i == 0:
+            norm(p + ".layer_norm", oc)
+        ic = oc
+    norm("wav2vec2.feature_projection.layer_norm", ic)
+    linear("wav2vec2.feature_projection.projection", H, ic)
+    K, groups = d["pos_k"], d["pos_groups"]
+    pc = "wav2vec2.encoder.pos_conv_embed.conv"
+    put(pc + ".parametrizations.weight.original0", (1.0 + 2.0 * uniform(ws.next(), K)).reshape(1, 1, K))
+    put(pc + ".parametrizations.weight.original1", mat((H, H // groups, K), 1.0))
+    put(pc + ".bias", vec(H, 0.02))
+    norm("wav2vec2.encoder.layer_norm", H)
+    for i in range(L):
+        p = f"wav2vec2.encoder.layers.{i}"
+        for n in ("q_proj", "k_proj", "v_proj", "out_proj"):
+            linear(f"{p}.attention.{n}", H, H)
+        norm(p + ".layer_norm", H)
+        linear(p + ".feed_forward.intermediate_dense", FF, H)
+        linear(p + ".feed_forward.output_dense", H, FF)
+        norm(p + ".final_layer_norm", H)
+    if large:
+        for head, n_out in (("age", 1), ("gender", len(labels))):
+            linear(head + ".dense", H, H)
+            linear(head + ".out_proj", n_out, H)
+    else:
+        put("layer_weights", vec(L + 1, 1.0))
+        linear("projector", d["proj"], H)
+        linear("classifier", len(labels), d["proj"])
+    kv = w2v2_kv(kind, H, L, d["n_heads"], FF, d["conv_dims"], d["conv_kernels"], d["conv_strides"], K, groups,
+                 d["proj"], labels)
+    kv["general.name"] = f"synthetic-wav2vec2-{kind}-seed{seed}"
+    return kv, T
+
+
+def write_w2v2(path, seed, kind="emotion", **kw):
+    kv, tensors = make_w2v2(seed, kind, **kw)
+    G.write_gguf(path, kv, tensors)
+    return path
