@@ -4,7 +4,10 @@ Default workload (the headline line): WeSpeaker ResNet34, batch 64 x 3 s 16 kHz
 synthetic clips (FBank 64x80x298), random-init f16 weights with folded BN, the
 full path PCM -> FBank -> ResNet34 -> TSTP -> FC -> L2 on the GPU.  `--model`
 selects one of the other encoder workloads (ECAPA-TDNN B=64 x 4 s, CAM++
-B=32 x 10 s q8_0, ERes2Net B=16 x 20 s q8_0) for the same measurement.
+B=32 x 10 s q8_0, ERes2Net B=16 x 20 s q8_0) for the same measurement, or
+one of the wav2vec2 analyze workloads (emotion: wav2vec2-base + weighted-sum
+classifier; age/gender: wav2vec2-large-robust + two heads; B=64 x 3 s raw
+waveform, clips/s).
 
 A step is one batch; inputs are resident in HBM before the timed region.
 Prints one JSON line (rank 0, N=1).
@@ -78,6 +81,24 @@ MODELS = {
                                "growth 32 bottleneck 128 with context masks, stats, 192-d, q8_0 1x1 weights",
                    "batch": 32, "clip_seconds": 10.0, "frames": 998},
     },
+    "w2v2_emotion": {
+        "metric": "analyzed clips/s, wav2vec2-base emotion B=64 3 s clips; GEMM MFMA util vs f16 peak",
+        "write": lambda path, seed: synth.write_w2v2(path, seed, "emotion"), "seed": 7, "batch": 64, "n": 48000,
+        "oracle": "w2v2", "dtype": "f16", "kind": "analyze",
+        "config": {"workload": "wav2vec2-base emotion analyze, batch 64 x 3 s 16 kHz clips (149 frames): 7 conv "
+                               "feature layers (512), 12 post-norm layers 768/12 heads/3072, pos conv 128x16 groups, "
+                               "weighted layer sum, projector 256, 4 labels; random-init f16 weights",
+                   "batch": 64, "clip_seconds": 3.0, "frames": 149},
+    },
+    "w2v2_age_gender": {
+        "metric": "analyzed clips/s, wav2vec2-large-robust age/gender B=64 3 s clips; GEMM MFMA util vs f16 peak",
+        "write": lambda path, seed: synth.write_w2v2(path, seed, "age_gender"), "seed": 7, "batch": 64, "n": 48000,
+        "oracle": "w2v2", "dtype": "f16", "kind": "analyze",
+        "config": {"workload": "wav2vec2-large-robust age/gender analyze, batch 64 x 3 s 16 kHz clips (149 frames): "
+                               "waveform normalisation, 7 LayerNorm conv layers (512, bias), 24 pre-norm layers "
+                               "1024/16 heads/4096, age + gender tanh heads; random-init f16 weights",
+                   "batch": 64, "clip_seconds": 3.0, "frames": 149},
+    },
     "eres2net": {
         "metric": "embeddings/s, ERes2Net B=16 20 s clips q8_0; conv MFMA util vs f16 peak",
         "write": synth.write_eres2net, "seed": 9, "batch": 16, "n": 320000, "oracle": "OracleEres2net",
@@ -89,12 +110,12 @@ MODELS = {
 }
 
 
-def profile_pass(ctx, d_pcm, d_out, batch, n, steps):
+def profile_pass(ctx, run, steps):
     ctx.set_profiling(True)
     ctx.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
+        run()
     ctx.synchronize()
     wall = (time.perf_counter() - t0) / steps
     recs = ctx.profile()
@@ -109,13 +130,13 @@ def profile_pass(ctx, d_pcm, d_out, batch, n, steps):
     return per, wall * 1e3
 
 
-def dominant_pass(ctx, d_pcm, d_out, batch, n, steps, name):
+def dominant_pass(ctx, run, steps, name):
     """Timed steps with events around the launches named `name` only."""
     ctx.set_profiling(True, name)
     ctx.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
+        run()
     ctx.synchronize()
     wall = (time.perf_counter() - t0) / steps
     recs = [r for r in ctx.profile() if r[0] == name]
@@ -155,12 +176,14 @@ def cpu_baseline(model, gguf_path, pcm, n_seconds, min_seconds=10.0):
     import pyoracle
     from vdamd import gguf
 
-    net = getattr(pyoracle, model["oracle"])(gguf.GGUFFile(gguf_path))
     try:
         avail = len(os.sched_getaffinity(0))
     except AttributeError:
         avail = os.cpu_count() or 1
     threads = max(1, min(8, avail))            # the reference's default min(hw, 8) threads
+    if model["oracle"] == "w2v2":
+        return cpu_baseline_w2v2(gguf_path, pcm, n_seconds, threads, avail, min_seconds)
+    net = getattr(pyoracle, model["oracle"])(gguf.GGUFFile(gguf_path))
     done = 0
     t0 = time.perf_counter()
     with ThreadPoolExecutor(threads) as ex:
@@ -175,18 +198,43 @@ def cpu_baseline(model, gguf_path, pcm, n_seconds, min_seconds=10.0):
             if time.perf_counter() - t0 >= min_seconds:
                 break
     dt = time.perf_counter() - t0
-    cpu_name = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_name = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    cpu_name = _cpu_name()
     return {"value": round(done / dt, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
             "sample": f"{done} clips (the batch's {len(pcm)} synthetic {n_seconds:g} s clips, cycled) through the "
                       f"oracle's FBank + encoder (f32), clip-parallel on {threads} threads, {dt:.1f} s wall; "
                       f"host {cpu_name}, {avail} cores available"}
+
+
+def _cpu_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_baseline_w2v2(gguf_path, pcm, n_seconds, threads, avail, min_seconds):
+    """The wav2vec2 oracle (numpy f64, its GEMMs on `threads` BLAS threads),
+    one clip after another until min_seconds have passed."""
+    import oracle_w2v2
+    from threadpoolctl import threadpool_limits
+
+    net = oracle_w2v2.OracleW2V2(gguf_path)
+    done = 0
+    with threadpool_limits(limits=threads):
+        t0 = time.perf_counter()
+        while True:
+            net.raw_outputs(pcm[done % len(pcm)])
+            done += 1
+            if time.perf_counter() - t0 >= min_seconds:
+                break
+        dt = time.perf_counter() - t0
+    return {"value": round(done / dt, 3), "unit": "clips/s", "cores": threads, "kind": "port",
+            "sample": f"{done} clips (the batch's synthetic {n_seconds:g} s clips, cycled) through the oracle's "
+                      f"wav2vec2 forward (numpy f64, BLAS on {threads} threads), {dt:.1f} s wall; "
+                      f"host {_cpu_name()}, {avail} cores available"}
 
 
 def main():
@@ -219,24 +267,33 @@ def main():
     ctx = lib.Context(path)
     pcm = synth.clips(CLIP_SEED, batch, n)
     d_pcm = lib.DeviceBuffer.from_array(pcm)
-    d_out = lib.DeviceBuffer(batch * ctx.dim * 4)
+    analyze = model.get("kind") == "analyze"
+    width = ctx.analyze_outputs() if analyze else ctx.dim
+    unit = "clips/s" if analyze else "embeddings/s"
+    d_out = lib.DeviceBuffer(batch * width * 4)
+    if analyze:
+        run = lambda: ctx.analyze_device_async(d_pcm.ptr, batch, n, d_out.ptr)
+    else:
+        run = lambda: ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
 
     for _ in range(args.warmup):
-        ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
+        run()
     ctx.synchronize()
     lib.check(L.vdk_synchronize())
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
+        run()
     ctx.synchronize()
     lib.check(L.vdk_synchronize())
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
     value = batch * args.steps / elapsed
-    emb = d_out.to_array(np.float32, (batch, ctx.dim))
-    assert np.all(np.isfinite(emb)) and np.allclose(np.linalg.norm(emb, axis=1), 1.0, atol=1e-4)
+    res = d_out.to_array(np.float32, (batch, width))
+    assert np.all(np.isfinite(res))
+    if not analyze:
+        assert np.allclose(np.linalg.norm(res, axis=1), 1.0, atol=1e-4)
 
-    per, prof_ms = profile_pass(ctx, d_pcm, d_out, batch, n, args.steps)
+    per, prof_ms = profile_pass(ctx, run, args.steps)
     steps = args.steps
     conv = {"ms": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0}
     for name, p in per.items():
@@ -256,18 +313,18 @@ def main():
 
     # the dominant kernel, timed again with events around its launches only
     dom = max((k for k in per if k.startswith("conv")), key=lambda k: per[k]["ms"])
-    recs, dom_wall_ms = dominant_pass(ctx, d_pcm, d_out, batch, n, steps, dom)
+    recs, dom_wall_ms = dominant_pass(ctx, run, steps, dom)
     nl = len(recs)
     avg_s = sum(r[1] for r in recs) / nl * 1e-3
     fl = sum(r[2] for r in recs) / nl
     by = sum(r[3] for r in recs) / nl
     if fl / by >= RIDGE_FLOP_PER_BYTE:
-        bound, achieved, peak, unit = "mfma", fl / avg_s / 1e12, PEAK_F16_TFLOPS, "TFLOP/s"
+        bound, achieved, peak, r_unit = "mfma", fl / avg_s / 1e12, PEAK_F16_TFLOPS, "TFLOP/s"
     else:
-        bound, achieved, peak, unit = "hbm", by / avg_s / 1e9, PEAK_HBM_GBS, "GB/s"
+        bound, achieved, peak, r_unit = "hbm", by / avg_s / 1e9, PEAK_HBM_GBS, "GB/s"
     traffic = TRAFFIC_BYTES_PER_LAUNCH.get((args.model, dom))
     roofline = {
-        "kernel": dom, "bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+        "kernel": dom, "bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": r_unit,
         "frac": round(achieved / peak, 4), "traffic": traffic,
         "launches_per_step": nl // steps, "avg_launch_us": round(avg_s * 1e6, 2),
         "flops_per_launch": fl, "algorithmic_bytes_per_launch": by,
@@ -280,7 +337,7 @@ def main():
         "kernels": kernels,
     }
     out = {
-        "metric": model["metric"], "value": round(value, 2), "unit": "embeddings/s", "n_gpus": 1,
+        "metric": model["metric"], "value": round(value, 2), "unit": unit, "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": model["dtype"],
         "data": "synthetic", "config": model["config"], "roofline": roofline,
@@ -288,15 +345,17 @@ def main():
     # the drop-in boundary hands over host PCM: the same batch through the
     # host-buffer entry point (H2D copy of the PCM and D2H of the embeddings
     # included), reported beside `value`, never as it
-    ctx.embed_batch(pcm)
+    host = (lambda: ctx.analyze_pcm(pcm)) if analyze else (lambda: ctx.embed_batch(pcm))
+    host()
     hs = min(args.steps, 10)
     t0 = time.perf_counter()
     for _ in range(hs):
-        ctx.embed_batch(pcm)
+        host()
     dt = (time.perf_counter() - t0) / hs
-    out["host_buffers"] = {"value": round(batch / dt, 2), "unit": "embeddings/s", "ms_per_step": round(dt * 1e3, 4),
-                           "note": "voicedetect_capi_embed_pcm_batch: host PCM in, host embeddings out (PCIe included)"}
-    if args.registry > 0:
+    out["host_buffers"] = {"value": round(batch / dt, 2), "unit": unit, "ms_per_step": round(dt * 1e3, 4),
+                           "note": ("voicedetect_gpu_analyze_pcm" if analyze else "voicedetect_capi_embed_pcm_batch") +
+                                   ": host PCM in, host results out (PCIe included)"}
+    if args.registry > 0 and not analyze:
         out["registry"] = registry_bench(L, d_out, batch, ctx.dim, args.registry, 10, args.steps)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(model, path, pcm, n / 16000.0)

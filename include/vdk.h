@@ -282,7 +282,7 @@ int vdk_wave_stats(const float* d_x, int batch, int n, float eps, float* d_stats
  * one input channel, y[b][t][c] = gelu(norm(bias[c] + sum_k w[c][k] xn[b][t*S+k]))
  * with xn = (x - mean) * rstd when d_stats (vdk_wave_stats) is given, else x.
  * norm 0: none; 1: GroupNorm with one group per channel (mean / biased var of
- * each channel over the clip's T0 frames, f64 two-pass); 2: LayerNorm over the
+ * each channel over the clip's T0 frames); 2: LayerNorm over the
  * C channels of each frame; affine gamma / beta, eps.  x [B][n] f32,
  * w [C][K] f32, y [B][T0][C] f16, T0 = (n - K)/S + 1, C in {256, 512, 1024},
  * K <= 16, S <= 8.  norm 1 needs vdk_w2v2_conv0_workspace_size() bytes of d_work. */
@@ -307,6 +307,16 @@ int vdk_layer_norm(const void* d_x, int rows, int C, const float* d_gamma, const
  * out [B][T][H] f16, H = n_heads * head_dim; head_dim must be 64. */
 int vdk_attention(const void* d_qkv, int batch, int T, int n_heads, int head_dim, float scale,
                   void* d_out, void* stream);
+
+/* Positional conv embedding of wav2vec2 (src/analyze_w2v2.cpp:280-326): a
+ * grouped 1-D conv with kernel K and zero pad `pad` (frame t reads input frames
+ * t - pad .. t - pad + K - 1; only the first T outputs are kept, as
+ * Wav2Vec2SamePadLayer does for even K), its bias, GELU and the residual:
+ *   y[b][t][gC+o] = x[b][t][gC+o] + gelu(bias[gC+o] + sum_k,i w[g][o][k][i] x[b][t+k-pad][gC+i])
+ * x [B][T][H] f16, w [groups][64][K][C] f16 (C = H / groups in {48, 64}, output
+ * rows C..63 zero), bias [H] f32, y [B][T][H] f32; K <= 128. */
+int vdk_pos_conv(const void* d_x, int batch, int T, int H, int groups, const void* d_w, const float* d_bias,
+                 int K, int pad, float* d_y, void* stream);
 
 /* out[b][c] = mean over t of x[b][t][c] (f16 or f32 input, f64 sums): the
  * time mean-pool of the analyze heads (src/analyze_w2v2.cpp:546-550, 607-610). */

@@ -255,6 +255,39 @@ def test_conv_epilogue_gelu_residual_crop():
     assert ok, f"f32 residual: ratio {ratio:.2f} rel-L2 {rel:.2e}"
 
 
+@pytest.mark.parametrize("case", [
+    # (B, T, H, groups, K): base (48 per group) and large-robust (64) shapes,
+    # clips shorter than the kernel, longer than one 192-frame workgroup
+    (2, 149, 768, 16, 128),
+    (1, 400, 1024, 16, 128),
+    (3, 7, 192, 4, 16),
+    (1, 1, 128, 2, 128),
+    (2, 193, 96, 2, 33),
+])
+def test_pos_conv(case):
+    B, T, H, G, K = case
+    announce(f"pos_conv {case}")
+    rng = _rng(("pos", case))
+    icg = H // G
+    x = rng.standard_normal((B, T, H)).astype(np.float16)
+    w = (rng.standard_normal((G, icg, icg, K)) * np.sqrt(1.0 / (icg * K))).astype(np.float16)   # [g][o][i][k]
+    bias = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    wp = np.zeros((G, 64, K, icg), np.float16)
+    wp[:, :icg] = w.transpose(0, 1, 3, 2)
+    dx, dw, db = lib.DeviceBuffer.from_array(x), lib.DeviceBuffer.from_array(wp), lib.DeviceBuffer.from_array(bias)
+    dy = lib.DeviceBuffer(B * T * H * 4)
+    lib.check(lib.lib().vdk_pos_conv(dx.ptr, B, T, H, G, dw.ptr, db.ptr, K, K // 2, dy.ptr, None))
+    _sync()
+    y = dy.to_array(np.float32, (B, T, H))
+    for i in range(B):
+        xs = x[i].astype(np.float64)
+        conv = np.concatenate([W.conv1d_strided(xs[:, g * icg:(g + 1) * icg], w[g].astype(np.float64), 1, K // 2)[:T]
+                               for g in range(G)], axis=1)
+        ref = xs + W.gelu(conv + bias)
+        ok, ratio, rel = close_report(y[i], ref, 2e-3, 2e-3)
+        assert ok, f"clip {i}: ratio {ratio:.2f} rel-L2 {rel:.2e}"
+
+
 def C_ref(d):
     import ctypes
     return ctypes.byref(d)
@@ -283,16 +316,18 @@ def _gates(kind, got_hidden, ref_hidden, got_raw, ref_raw, tag):
     assert np.abs(W.probs_f32(logits) - W.probs_f32(rlog)).max() <= 1e-3
 
 
-@pytest.mark.parametrize("kind", ["emotion", "age_gender"])
-def test_analyze_small_matches_oracle(kind):
-    path = _model(kind, 5, SMALL)
+@pytest.mark.parametrize("kind,dims", [("emotion", SMALL), ("age_gender", SMALL),
+                                       ("emotion", dict(SMALL, pos_groups=8))],   # 32 channels per pos-conv group
+                         ids=["emotion", "age_gender", "emotion-pos32"])
+def test_analyze_small_matches_oracle(kind, dims):
+    path = _model(kind, 5, dims)
     orc = W.OracleW2V2(path)
     ctx = lib.Context(path)
     try:
         n = 8000
         pcm = synth.clips(31, 3, n)
         announce(f"analyze {kind} small B=3 n={n}")
-        feat, hid, raw = ctx.analyze_capture(pcm, 512, SMALL["hidden"])
+        feat, hid, raw = ctx.analyze_capture(pcm, 512, dims["hidden"])
         assert raw.shape == (3, ctx.analyze_outputs())
         for i in range(3):
             rfeat = orc.conv_encoder(pcm[i])

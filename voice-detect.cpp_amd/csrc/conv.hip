@@ -407,7 +407,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
 
     // Per DMA slot of this lane: weight rows keep a fixed voffset (the tap /
     // chunk part is uniform); pixel rows keep the tap-0 offset and a mask of
-    // the taps that fall inside the image.
+    // the taps that fall inside the image - one bit per tap, or for a single
+    // row of more than 32 taps the in-image range [lo, hi) as lo | hi << 16.
+    const bool tap_range = a.KH == 1 && a.KW > 32;
     int s_off[IPW];
     uint32_t s_mask[IPW];
     bool s_is_w[IPW];
@@ -433,11 +435,19 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
                 const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
                 const int ih0 = oh * a.sh - a.ph, iw0 = ow * a.sw - a.pw;
                 s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.xs + c * 8) * 2;
-                for (int kh = 0; kh < a.KH; ++kh)
-                    for (int kw = 0; kw < a.KW; ++kw) {
-                        const int ih = ih0 + kh * a.dh, iw = iw0 + kw * a.dw;
-                        if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W) s_mask[j] |= 1u << (kh * a.KW + kw);
-                    }
+                if (tap_range) {
+                    // one row of taps: the in-image ones are kw in [lo, hi)
+                    const int lo = iw0 >= 0 ? 0 : (-iw0 + a.dw - 1) / a.dw;
+                    int hi = a.W - 1 - iw0 >= 0 ? (a.W - 1 - iw0) / a.dw + 1 : 0;
+                    hi = hi < a.KW ? hi : a.KW;
+                    s_mask[j] = lo < hi ? (uint32_t)lo | ((uint32_t)hi << 16) : 0u;
+                } else {
+                    for (int kh = 0; kh < a.KH; ++kh)
+                        for (int kw = 0; kw < a.KW; ++kw) {
+                            const int ih = ih0 + kh * a.dh, iw = iw0 + kw * a.dw;
+                            if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W) s_mask[j] |= 1u << (kh * a.KW + kw);
+                        }
+                }
             }
         }
     }
@@ -456,7 +466,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
             if (s_is_w[j]) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, dst, 16, (uint32_t)s_off[j], w_soff, 0, 0);
             } else {
-                const uint32_t off = ((s_mask[j] >> f_tap) & 1u) ? (uint32_t)(s_off[j] + f_x + f_xc) : kOOB;
+                const bool in = tap_range ? (uint32_t)(f_tap - (int)(s_mask[j] & 0xFFFFu)) <
+                                                (uint32_t)((int)(s_mask[j] >> 16) - (int)(s_mask[j] & 0xFFFFu))
+                                          : ((s_mask[j] >> f_tap) & 1u) != 0;
+                const uint32_t off = in ? (uint32_t)(s_off[j] + f_x + f_xc) : kOOB;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, off, 0, 0, 0);
             }
         }
@@ -1581,10 +1594,10 @@ bool plain_epilogue(const ConvArgs& a) {
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
-    // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask;
-    // longer kernels (wav2vec2's 128-tap positional conv) take the
-    // register-staged kernel
-    if (a.KH * a.KW > 32 && idx >= kFirstDma) return false;
+    // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
+    // the in-image tap range for a single row of taps; longer 2-D kernels
+    // take the register-staged kernel
+    if (a.KH * a.KW > 32 && a.KH != 1 && idx >= kFirstDma) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
     if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % t.bm == 0 && a.IC % 16 == 0;
     if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8))) return false;   // split: DMA only
@@ -1613,9 +1626,19 @@ int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
-    if (a.KH * a.KW > 32) {   // register-staged kernel only
+    if (a.KH * a.KW > 32 && a.KH != 1) {   // register-staged kernel only
         if (a.IC % 32 == 0) return bm == 128 ? 5 : (bm == 64 ? 2 : 10);
         return a.IC % 16 == 0 ? (bm == 128 ? 13 : (bm == 64 ? 12 : 11)) : -1;
+    }
+    if (a.KH == 1 && !a.split) {
+        // 1-D convs over time-major maps (wav2vec2, ECAPA), from a sweep of
+        // the wav2vec2 / ECAPA layer shapes at batch 64 on MI355X: long
+        // kernels (the 128-tap positional conv) on the 128x32 tile, wide
+        // 1x1 GEMMs on the 128x256 8-wave tile, the big strided feature
+        // convs on the 256x256 tile
+        if (a.KW > 32 && a.IC % 64 == 0) return 52;
+        if (a.KW == 1 && a.IC >= 512 && a.OC >= 512 && a.OC % 128 == 0 && a.IC % 32 == 0) return 36;
+        if (a.KW <= 4 && a.OC % 256 == 0 && a.IC % 64 == 0 && a.npix >= 131072) return 38;
     }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;

@@ -234,7 +234,11 @@ private:
         std::vector<W2Norm> conv_n; // their LayerNorms ("layer" feature norm)
         W2Norm fp_n;                // feature_projection.layer_norm
         Layer proj;
-        std::vector<void*> pos_w;   // per group f16 [icg][K][icg] (weight norm applied)
+        // weight norm applied; vdk_pos_conv: one f16 [G][64][K][icg] array;
+        // otherwise per group f16 [icg][K][icp] (input channels zero padded)
+        std::vector<void*> pos_w;
+        int pos_icp = 0;
+        bool pos_fused = false;
         float* pos_b = nullptr;
         W2Norm enc_n;
         std::vector<W2Layer> layers;

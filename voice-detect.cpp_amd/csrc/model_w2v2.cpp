@@ -144,16 +144,35 @@ void Model::upload_w2v2() {
             const double nrm = std::sqrt(sumsq[k]);
             sc[k] = nrm > 0.0 ? (double)gv[k] / nrm : 0.0;
         }
-        m.pos_w.assign(c.pos_groups, nullptr);
-        for (int gi = 0; gi < c.pos_groups; ++gi) {
-            std::vector<uint16_t> packed((size_t)icg * K * icg);
-            for (int o = 0; o < icg; ++o)
-                for (int i = 0; i < icg; ++i)
-                    for (int k = 0; k < K; ++k) {
-                        const size_t src = ((size_t)(gi * icg + o) * icg + i) * K + k;
-                        packed[((size_t)o * K + k) * icg + i] = float_to_half_bits((float)((double)v[src] * sc[k]));
-                    }
-            arena.put(packed, &m.pos_w[gi]);
+        auto wn = [&](int gi, int o, int i, int k) {
+            const size_t src = ((size_t)(gi * icg + o) * icg + i) * K + k;
+            return float_to_half_bits((float)((double)v[src] * sc[k]));
+        };
+        m.pos_fused = (icg == 48 || icg == 64) && K <= 128;
+        if (m.pos_fused) {
+            // vdk_pos_conv layout [G][64][K][icg], outputs padded to 64 with zeros
+            std::vector<uint16_t> packed((size_t)c.pos_groups * 64 * K * icg, 0);
+            for (int gi = 0; gi < c.pos_groups; ++gi)
+                for (int o = 0; o < icg; ++o)
+                    for (int k = 0; k < K; ++k)
+                        for (int i = 0; i < icg; ++i)
+                            packed[(((size_t)gi * 64 + o) * K + k) * icg + i] = wn(gi, o, i, k);
+            m.pos_w.assign(1, nullptr);
+            arena.put(packed, &m.pos_w[0]);
+        } else {
+            // one implicit-GEMM launch per group: input channels padded to a
+            // multiple of 32 with zero weights (the GEMM's channel chunk), so
+            // group g reads channels g*icg .. g*icg + icp of the projection
+            const int icp = (icg + 31) / 32 * 32;
+            m.pos_icp = icp;
+            m.pos_w.assign(c.pos_groups, nullptr);
+            for (int gi = 0; gi < c.pos_groups; ++gi) {
+                std::vector<uint16_t> packed((size_t)icg * K * icp, 0);
+                for (int o = 0; o < icg; ++o)
+                    for (int i = 0; i < icg; ++i)
+                        for (int k = 0; k < K; ++k) packed[((size_t)o * K + k) * icp + i] = wn(gi, o, i, k);
+                arena.put(packed, &m.pos_w[gi]);
+            }
         }
         arena.put(f32("w2v2.encoder.pos_conv_embed.conv.bias", H), &m.pos_b);
     }
@@ -251,7 +270,10 @@ void Model::alloc_w2v2_workspace(int batch, int n) {
     w.fe[1] = ws_alloc(2 * fe_max);
     if (fe32_max) w.fe32 = static_cast<float*>(ws_alloc(4 * fe32_max));
     w.u = ws_alloc(2 * BT * c.conv_dims.back());
-    w.wproj = ws_alloc(2 * BT * H);
+    // + a zeroed tail: the last positional-conv group reads up to icp - icg
+    // channels past the end of the last row (with zero weights)
+    w.wproj = ws_alloc(2 * (BT * H + 64));
+    VDK_HIP(hipMemsetAsync(w.wproj, 0, 2 * (BT * H + 64), stream_));
     w.z = static_cast<float*>(ws_alloc(4 * BT * H));
     w.acc = static_cast<float*>(ws_alloc(4 * BT * H));
     w.wh = ws_alloc(2 * BT * H);
@@ -341,10 +363,16 @@ void Model::analyze_forward(const float* d_pcm, int batch, int n, float* d_raw) 
     // -- feature projection + positional conv ----------------------------------
     ln("w2v2_fp_ln", w.fe[cur], BT, Cf, m.fp_n, 0, w.u, nullptr, 0.0f);
     gemm("w2v2_proj", m.proj, w.u, Cf, T, 1, 0, 0, m.proj.b, VDK_ACT_NONE, nullptr, 0, 0, 0, w.wproj, H, 0);
-    {
+    if (m.pos_fused) {
+        prof_begin("w2v2_pos_conv", 2.0 * BT * (double)H * (H / c.pos_groups) * c.pos_k,
+                   2.0 * BT * H * 2.0 + 4.0 * BT * H);
+        check_rc(vdk_pos_conv(w.wproj, batch, T, H, c.pos_groups, m.pos_w[0], m.pos_b, c.pos_k, c.pos_k / 2, w.z,
+                              stream_));
+        prof_end();
+    } else {
         const int icg = H / c.pos_groups;
         Layer pl;
-        pl.ic = icg; pl.oc = icg; pl.k = c.pos_k;
+        pl.ic = m.pos_icp; pl.oc = icg; pl.k = c.pos_k;
         for (int gi = 0; gi < c.pos_groups; ++gi) {
             pl.w = m.pos_w[gi];
             const half_t* xg = static_cast<const half_t*>(w.wproj) + (size_t)gi * icg;

@@ -89,64 +89,90 @@ __device__ __forceinline__ void load_window(const float* x, int n, const float* 
     }
 }
 
-// GroupNorm statistics (num_groups == channels): per (clip, chunk, channel)
-// sum of y (mean == NULL) or of (y - mean)^2, in f64.
-__global__ __launch_bounds__(256) void conv0_stats_kernel(const float* __restrict__ x, int n,
-                                                          const float* __restrict__ wstats,
-                                                          const float* __restrict__ w, const float* __restrict__ bias,
-                                                          int C, int K, int S, int T0,
-                                                          const double* __restrict__ mean,
-                                                          double* __restrict__ part) {
+// GroupNorm statistics (num_groups == channels) without a pass over the
+// conv output: y_c(t) = bias_c + w_c . u(t) with u(t) = xn[t*S .. t*S+K-1], so
+//   mean_c = bias_c + w_c . m,   var_c = w_c^T (G - m m^T) w_c
+// with m = mean_t u(t) and G = mean_t u(t) u(t)^T (biased, as GroupNorm).
+// conv0_moments_kernel sums u_k and u_k u_k' (k <= k') over the clip's frames
+// in f64, one sum per thread; conv0_finalize_kernel forms the per-channel
+// affine scale = gamma / sqrt(var + eps), shift = beta - mean * scale.
+__global__ __launch_bounds__(256) void conv0_moments_kernel(const float* __restrict__ x, int n,
+                                                            const float* __restrict__ wstats, int K, int S, int T0,
+                                                            double* __restrict__ part) {
     __shared__ float sx[kWin];
-    const int b = blockIdx.y, chunk = blockIdx.x, t0 = chunk * kFrames;
+    const int b = blockIdx.y, chunk = blockIdx.x, p = threadIdx.x, t0 = chunk * kFrames;
+    const int NP = K + K * (K + 1) / 2;
     const int nt = T0 - t0 < kFrames ? T0 - t0 : kFrames;
     load_window(x, n, wstats, b, t0 * S, (nt - 1) * S + K, sx);
     __syncthreads();
-    for (int c = threadIdx.x; c < C; c += 256) {
-        float wk[kMaxK];
-#pragma unroll
-        for (int k = 0; k < kMaxK; ++k) wk[k] = k < K ? w[c * K + k] : 0.0f;
-        const float bc = bias ? bias[c] : 0.0f;
-        const double mc = mean ? mean[(size_t)b * C + c] : 0.0;
-        double acc = 0.0;
-        for (int t = 0; t < nt; ++t) {
-            float y = bc;
-#pragma unroll
-            for (int k = 0; k < kMaxK; ++k)
-                if (k < K) y += wk[k] * sx[t * S + k];
-            const double d = (double)y - mc;
-            acc += mean ? d * d : (double)y;
-        }
-        part[((size_t)b * gridDim.x + chunk) * C + c] = acc;
+    if (p >= NP) return;
+    int k1 = p, k2 = -1;   // p < K: the sum of u_p; then the pairs k1 <= k2 in row order
+    if (p >= K) {
+        int q = p - K;
+        k1 = 0;
+        while (q >= K - k1) { q -= K - k1; ++k1; }
+        k2 = k1 + q;
     }
+    double acc = 0.0;
+    for (int t = 0; t < nt; ++t) {
+        const float u = sx[t * S + k1];
+        acc += k2 < 0 ? (double)u : (double)u * (double)sx[t * S + k2];
+    }
+    part[((size_t)b * gridDim.x + chunk) * NP + p] = acc;
 }
 
-// Chunk partials -> mean (pass 0) or the GroupNorm affine (pass 1):
-// scale = gamma / sqrt(var + eps), shift = beta - mean * scale.
-__global__ __launch_bounds__(256) void conv0_finalize_kernel(const double* __restrict__ part, int nchunk, int C,
-                                                             int T0, int pass, double* __restrict__ mean,
+// Chunk partials -> per-clip moment sums, in chunk order.
+__global__ __launch_bounds__(256) void conv0_moments_reduce_kernel(const double* __restrict__ part, int nchunk,
+                                                                   int NP, double* __restrict__ mom) {
+    const int b = blockIdx.x, p = threadIdx.x;
+    if (p >= NP) return;
+    double s = 0.0;
+    for (int j = 0; j < nchunk; ++j) s += part[((size_t)b * nchunk + j) * NP + p];
+    mom[(size_t)b * NP + p] = s;
+}
+
+__global__ __launch_bounds__(256) void conv0_finalize_kernel(const double* __restrict__ mom,
+                                                             const float* __restrict__ w,
+                                                             const float* __restrict__ bias, int C, int K, int T0,
                                                              const float* __restrict__ gamma,
                                                              const float* __restrict__ beta, float eps,
                                                              float* __restrict__ scale, float* __restrict__ shift) {
     const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
     if (c >= C) return;
-    double s = 0.0;
-    for (int j = 0; j < nchunk; ++j) s += part[((size_t)b * nchunk + j) * C + c];
-    const size_t o = (size_t)b * C + c;
-    if (pass == 0) {
-        mean[o] = s / T0;
-        return;
+    const int NP = K + K * (K + 1) / 2;
+    const double* mb = mom + (size_t)b * NP;
+    double wc[kMaxK], m[kMaxK];
+    double mean = bias ? (double)bias[c] : 0.0;
+    for (int k = 0; k < K; ++k) {
+        wc[k] = (double)w[c * K + k];
+        m[k] = mb[k] / T0;
+        mean += wc[k] * m[k];
     }
-    const double var = s / T0;
+    double var = 0.0;
+    int q = K;
+    for (int k1 = 0; k1 < K; ++k1)
+        for (int k2 = k1; k2 < K; ++k2, ++q) {
+            const double cov = mb[q] / T0 - m[k1] * m[k2];
+            var += (k1 == k2 ? 1.0 : 2.0) * wc[k1] * wc[k2] * cov;
+        }
+    var = var > 0.0 ? var : 0.0;
     const double sc = (double)gamma[c] / sqrt(var + (double)eps);
+    const size_t o = (size_t)b * C + c;
     scale[o] = (float)sc;
-    shift[o] = (float)((double)beta[c] - mean[o] * sc);
+    shift[o] = (float)((double)beta[c] - mean * sc);
 }
 
-// One wave per frame; lane l owns channels l*CPL .. l*CPL + CPL - 1.
-// norm 0: none; 1: GroupNorm affine from scale/shift [B][C]; 2: LayerNorm over
-// the frame's C channels (gamma, beta, eps).  Then GELU, stored f16.
-template <int CPL>
+// One wave per frame; lane l owns channels l*CPL .. l*CPL + CPL - 1 and
+// holds their KT taps (zero past K) in registers.  A workgroup covers
+// kApplyFrames frames of one clip: the waveform window and the weights
+// (staged through LDS as [K][C] so every global read is coalesced) are loaded
+// once per workgroup.  norm 0: none; 1: GroupNorm affine from scale/shift
+// [B][C]; 2: LayerNorm over the frame's C channels (gamma, beta, eps).  Then
+// GELU, stored f16.
+constexpr int kApplyFrames = 256;
+constexpr int kApplyWin = (kApplyFrames - 1) * kMaxS + kMaxK;
+
+template <int CPL, int KT>
 __global__ __launch_bounds__(256) void conv0_apply_kernel(const float* __restrict__ x, int n,
                                                           const float* __restrict__ wstats,
                                                           const float* __restrict__ w, const float* __restrict__ bias,
@@ -157,30 +183,53 @@ __global__ __launch_bounds__(256) void conv0_apply_kernel(const float* __restric
                                                           const float* __restrict__ beta, float eps,
                                                           half_t* __restrict__ y) {
     constexpr int C = CPL * 64;
-    __shared__ float sx[kWin];
-    const int b = blockIdx.y, t0 = blockIdx.x * kFrames;
-    const int nt = T0 - t0 < kFrames ? T0 - t0 : kFrames;
-    load_window(x, n, wstats, b, t0 * S, (nt - 1) * S + K, sx);
+    __shared__ float sx[kApplyWin];
+    __shared__ __attribute__((aligned(16))) float sw[KT * C];   // [tap][channel]
+    const int b = blockIdx.y, t0 = blockIdx.x * kApplyFrames;
+    const int nt = T0 - t0 < kApplyFrames ? T0 - t0 : kApplyFrames;
+    const int len = (nt - 1) * S + K;
+    load_window(x, n, wstats, b, t0 * S, len, sx);
+    for (int i = len + threadIdx.x; i < (nt - 1) * S + KT; i += 256) sx[i] = 0.0f;   // taps K..KT-1
+    for (int i = threadIdx.x; i < KT * C; i += 256) {
+        const int c = i / KT, k = i - c * KT;   // coalesced read of w [C][K]
+        sw[k * C + c] = k < K ? w[c * K + k] : 0.0f;
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c0 = lane * CPL;
-    float wr[CPL][kMaxK], bc[CPL], sa[CPL], sb[CPL];
+    float bc[CPL], sa[CPL], sb[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-#pragma unroll
-        for (int k = 0; k < kMaxK; ++k) wr[j][k] = k < K ? w[(c0 + j) * K + k] : 0.0f;
         bc[j] = bias ? bias[c0 + j] : 0.0f;
-        sa[j] = norm == 1 ? scale[(size_t)b * C + c0 + j] : (norm == 2 ? gamma[c0 + j] : 1.0f);
-        sb[j] = norm == 1 ? shift[(size_t)b * C + c0 + j] : (norm == 2 ? beta[c0 + j] : 0.0f);
+        sa[j] = 1.0f;
+        sb[j] = 0.0f;
+        if (norm == 1) {
+            sa[j] = scale[(size_t)b * C + c0 + j];
+            sb[j] = shift[(size_t)b * C + c0 + j];
+        } else if (norm == 2) {
+            sa[j] = gamma[c0 + j];
+            sb[j] = beta[c0 + j];
+        }
     }
     __syncthreads();
+    float wr[CPL][KT];
+#pragma unroll
+    for (int k = 0; k < KT; ++k)
+#pragma unroll
+        for (int j = 0; j < CPL; j += 4) {
+            const float4v v = *reinterpret_cast<const float4v*>(&sw[k * C + c0 + j]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) wr[j + e][k] = v[e];
+        }
     for (int t = wave; t < nt; t += 4) {
+        float u[KT];
+#pragma unroll
+        for (int k = 0; k < KT; ++k) u[k] = sx[t * S + k];
         float v[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             float a = bc[j];
 #pragma unroll
-            for (int k = 0; k < kMaxK; ++k)
-                if (k < K) a += wr[j][k] * sx[t * S + k];
+            for (int k = 0; k < KT; ++k) a += wr[j][k] * u[k];
             v[j] = a;
         }
         if (norm == 2) {
@@ -204,6 +253,18 @@ __global__ __launch_bounds__(256) void conv0_apply_kernel(const float* __restric
             *reinterpret_cast<half4*>(yo + j0) = h;
         }
     }
+}
+
+template <int CPL>
+void launch_conv0_apply(dim3 g, hipStream_t s, const float* x, int n, const float* wstats, const float* w,
+                        const float* bias, int K, int S, int T0, int norm, const float* scale, const float* shift,
+                        const float* gamma, const float* beta, float eps, half_t* y) {
+    if (K == 10)
+        hipLaunchKernelGGL((conv0_apply_kernel<CPL, 10>), g, dim3(256), 0, s, x, n, wstats, w, bias, K, S, T0, norm,
+                           scale, shift, gamma, beta, eps, y);
+    else
+        hipLaunchKernelGGL((conv0_apply_kernel<CPL, kMaxK>), g, dim3(256), 0, s, x, n, wstats, w, bias, K, S, T0,
+                           norm, scale, shift, gamma, beta, eps, y);
 }
 
 // ---- LayerNorm over rows of C (one wave per row, lane l owns elements
@@ -369,6 +430,113 @@ __global__ __launch_bounds__(256) void attention_kernel(const half_t* __restrict
     }
 }
 
+// ---- positional conv embedding (src/analyze_w2v2.cpp:280-326) ----
+// Grouped 1-D conv with a long kernel, its bias, GELU and the residual:
+//   y[b][t][gC + o] = x[b][t][gC + o]
+//                     + gelu(bias[gC + o] + sum_k sum_i W[g][o][k][i] x[b][t + k - pad][gC + i])
+// for C = ICG channels per group.  An implicit GEMM per (clip, group) whose
+// im2col rows are the same input frames shifted by one per tap, so a
+// workgroup stages its frames' input halo (kPosTT + K - 1 rows of the group's
+// ICG channels, zero outside the clip) in LDS once and runs every tap from it;
+// the weights of tap k ([64 padded outputs][ICG]) are double-buffered through
+// LDS.  MFMA 32x32x16: M = 32 frames, N = 32 outputs, K = 16 channels; each
+// of the 3 waves owns 64 frames x 64 outputs (2 x 2 blocks).
+constexpr int kPosTT = 192, kPosMaxK = 128;
+
+template <int ICG>
+__global__ __launch_bounds__(192) void pos_conv_kernel(const half_t* __restrict__ x, const half_t* __restrict__ w,
+                                                       const float* __restrict__ bias, float* __restrict__ y, int T,
+                                                       int H, int K, int pad) {
+    constexpr int RS = ICG + 8;              // halo / weight row stride in halfs (16 B of padding)
+    constexpr int CH = ICG / 8;              // 16-byte chunks per row
+    constexpr int NWCH = 64 * CH;            // chunks per tap of weights
+    constexpr int WPT = (NWCH + 191) / 192;  // weight chunks per thread
+    __shared__ __attribute__((aligned(16))) half_t sx[(kPosTT + kPosMaxK - 1) * RS];
+    __shared__ __attribute__((aligned(16))) half_t sw[2][64 * RS];
+    const int b = blockIdx.z, g = blockIdx.y, t0 = blockIdx.x * kPosTT;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, hl = lane >> 5;
+    const size_t cb = (size_t)g * ICG;
+    const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+    // input halo: row r is frame t0 - pad + r
+    const int rows = kPosTT + K - 1;
+    for (int i = tid; i < rows * CH; i += 192) {
+        const int r = i / CH, c = i - r * CH, f = t0 - pad + r;
+        const half8 v = (f >= 0 && f < T) ? *reinterpret_cast<const half8*>(x + ((size_t)b * T + f) * H + cb + c * 8)
+                                          : zero8;
+        *reinterpret_cast<half8*>(&sx[r * RS + c * 8]) = v;
+    }
+    const half_t* wg = w + (size_t)g * 64 * K * ICG;
+    half8 wr[WPT];
+    auto fetch_w = [&](int k) {
+#pragma unroll
+        for (int j = 0; j < WPT; ++j) {
+            const int i = tid + j * 192;
+            wr[j] = zero8;
+            if (i < NWCH) {
+                const int o = i / CH, c = i - o * CH;
+                wr[j] = *reinterpret_cast<const half8*>(wg + ((size_t)o * K + k) * ICG + c * 8);
+            }
+        }
+    };
+    auto stash_w = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < WPT; ++j) {
+            const int i = tid + j * 192;
+            if (i < NWCH) {
+                const int o = i / CH, c = i - o * CH;
+                *reinterpret_cast<half8*>(&sw[buf][o * RS + c * 8]) = wr[j];
+            }
+        }
+    };
+    float16v acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    fetch_w(0);
+    stash_w(0);
+    __syncthreads();
+    const int f0 = wave * 64 + lr;   // this lane's A row (frame) in M block 0
+    for (int k = 0; k < K; ++k) {
+        const int buf = k & 1;
+        if (k + 1 < K) fetch_w(k + 1);
+#pragma unroll
+        for (int kk = 0; kk < ICG / 16; ++kk) {
+            const int c = 16 * kk + 8 * hl;
+            half8 a[2], bw[2];
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi) a[mi] = *reinterpret_cast<const half8*>(&sx[(f0 + 32 * mi + k) * RS + c]);
+#pragma unroll
+            for (int ni = 0; ni < 2; ++ni) bw[ni] = *reinterpret_cast<const half8*>(&sw[buf][(32 * ni + lr) * RS + c]);
+#pragma unroll
+            for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 2; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mi], bw[ni], acc[mi][ni], 0, 0, 0);
+        }
+        if (k + 1 < K) stash_w(buf ^ 1);
+        __syncthreads();
+    }
+    // lane holds output o = 32 ni + lr, frames 8 (r / 4) + 4 hl + r % 4 of each 32-frame block
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+        const int o = 32 * ni + lr;
+        if (o >= ICG) continue;
+        const float bo = bias[cb + o];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int t = t0 + wave * 64 + 32 * mi + 8 * (r >> 2) + 4 * hl + (r & 3);
+                if (t >= T) continue;
+                const size_t i = ((size_t)b * T + t) * H + cb + o;
+                y[i] = (float)x[i] + gelu_erf(acc[mi][ni][r] + bo);
+            }
+    }
+}
+
 // ---- per-clip mean over time: out[b][c] = mean_t x[b][t][c] (f64, 4 time
 // partitions combined in a fixed order).
 __global__ __launch_bounds__(256) void time_mean_kernel(const void* __restrict__ x, int x_f32, int T, int C,
@@ -393,10 +561,11 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 int conv0_frames(int n, int K, int S) { return n < K ? 0 : (n - K) / S + 1; }
 
 size_t conv0_work(int batch, int n, int C, int K, int S) {
-    const int T0 = conv0_frames(n, K, S);
-    const size_t nchunk = (size_t)(T0 + kFrames - 1) / kFrames;
-    // partials [B][nchunk][C] f64, mean [B][C] f64, scale / shift [B][C] f32
-    return (size_t)batch * C * (8 * nchunk + 8 + 4 + 4) + 256;
+    // per-chunk moment partials [B][nchunk][NP] and sums [B][NP] f64
+    // (NP = K + K(K+1)/2), then scale / shift [B][C] f32
+    const size_t np = (size_t)K + (size_t)K * (K + 1) / 2;
+    const size_t nchunk = (size_t)(conv0_frames(n, K, S) + kFrames - 1) / kFrames;
+    return (size_t)batch * (np * 8 * (nchunk + 1) + (size_t)C * 8) + 256;
 }
 
 }  // namespace
@@ -435,41 +604,41 @@ extern "C" int vdk_w2v2_conv0(const float* d_x, int batch, int n, const float* d
                 "w2v2_conv0: input too large for one launch");
         require(al16(d_y), "w2v2_conv0: output must be 16-byte aligned");
         hipStream_t s = static_cast<hipStream_t>(stream);
-        const int nchunk = (T0 + kFrames - 1) / kFrames;
         const float* scale = nullptr;
         const float* shift = nullptr;
         if (norm == 1) {
             require(d_work && work_bytes >= conv0_work(batch, n, C, K, S), "w2v2_conv0: workspace too small");
+            const int NP = K + K * (K + 1) / 2;
+            const int nchunk = (T0 + kFrames - 1) / kFrames;
             double* part = static_cast<double*>(d_work);
-            double* mean = part + (size_t)batch * nchunk * C;
-            float* sc = reinterpret_cast<float*>(mean + (size_t)batch * C);
+            double* mom = part + (size_t)batch * nchunk * NP;
+            float* sc = reinterpret_cast<float*>(mom + (size_t)batch * NP);
             float* sh = sc + (size_t)batch * C;
-            const dim3 g(nchunk, batch), gf(cdiv(C, 256), batch);
-            for (int pass = 0; pass < 2; ++pass) {
-                hipLaunchKernelGGL(conv0_stats_kernel, g, dim3(256), 0, s, d_x, n, d_stats, d_w, d_bias, C, K, S, T0,
-                                   pass ? mean : nullptr, part);
-                VDK_HIP(hipGetLastError());
-                hipLaunchKernelGGL(conv0_finalize_kernel, gf, dim3(256), 0, s, part, nchunk, C, T0, pass, mean,
-                                   d_gamma, d_beta, eps, sc, sh);
-                VDK_HIP(hipGetLastError());
-            }
+            hipLaunchKernelGGL(conv0_moments_kernel, dim3(nchunk, batch), dim3(256), 0, s, d_x, n, d_stats, K, S, T0,
+                               part);
+            VDK_HIP(hipGetLastError());
+            hipLaunchKernelGGL(conv0_moments_reduce_kernel, dim3(batch), dim3(256), 0, s, part, nchunk, NP, mom);
+            VDK_HIP(hipGetLastError());
+            hipLaunchKernelGGL(conv0_finalize_kernel, dim3(cdiv(C, 256), batch), dim3(256), 0, s, mom, d_w, d_bias,
+                               C, K, T0, d_gamma, d_beta, eps, sc, sh);
+            VDK_HIP(hipGetLastError());
             scale = sc;
             shift = sh;
         }
         half_t* y = static_cast<half_t*>(d_y);
-        const dim3 g(nchunk, batch);
+        const dim3 g(cdiv(T0, kApplyFrames), batch);
         switch (C) {
             case 256:
-                hipLaunchKernelGGL(conv0_apply_kernel<4>, g, dim3(256), 0, s, d_x, n, d_stats, d_w, d_bias, K, S, T0,
-                                   norm, scale, shift, d_gamma, d_beta, eps, y);
+                launch_conv0_apply<4>(g, s, d_x, n, d_stats, d_w, d_bias, K, S, T0, norm, scale, shift, d_gamma,
+                                      d_beta, eps, y);
                 break;
             case 512:
-                hipLaunchKernelGGL(conv0_apply_kernel<8>, g, dim3(256), 0, s, d_x, n, d_stats, d_w, d_bias, K, S, T0,
-                                   norm, scale, shift, d_gamma, d_beta, eps, y);
+                launch_conv0_apply<8>(g, s, d_x, n, d_stats, d_w, d_bias, K, S, T0, norm, scale, shift, d_gamma,
+                                      d_beta, eps, y);
                 break;
             default:
-                hipLaunchKernelGGL(conv0_apply_kernel<16>, g, dim3(256), 0, s, d_x, n, d_stats, d_w, d_bias, K, S,
-                                   T0, norm, scale, shift, d_gamma, d_beta, eps, y);
+                launch_conv0_apply<16>(g, s, d_x, n, d_stats, d_w, d_bias, K, S, T0, norm, scale, shift, d_gamma,
+                                       d_beta, eps, y);
                 break;
         }
         VDK_HIP(hipGetLastError());
@@ -518,6 +687,29 @@ extern "C" int vdk_time_mean(const void* d_x, int x_f32, int batch, int T, int C
         require(batch > 0 && T > 0 && C > 0, "time_mean: empty shape");
         hipLaunchKernelGGL(time_mean_kernel, dim3(cdiv(C, 64), batch), dim3(256), 0, static_cast<hipStream_t>(stream),
                            d_x, x_f32 ? 1 : 0, T, C, d_out);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_pos_conv(const void* d_x, int batch, int T, int H, int groups, const void* d_w, const float* d_bias,
+                            int K, int pad, float* d_y, void* stream) {
+    return guarded([&] {
+        require(d_x && d_w && d_bias && d_y, "pos_conv: NULL device pointer");
+        require(batch > 0 && T > 0 && groups > 0 && H % groups == 0, "pos_conv: groups must divide H");
+        const int icg = H / groups;
+        require(icg == 48 || icg == 64, "pos_conv: channels per group must be 48 or 64");
+        require(K >= 1 && K <= kPosMaxK && pad >= 0 && pad < K, "pos_conv: kernel 1..128, pad < kernel");
+        require(al16(d_x) && al16(d_w), "pos_conv: buffers must be 16-byte aligned");
+        require((size_t)batch * T * H < (1ull << 31), "pos_conv: too many frames for one launch");
+        require(batch <= 65535 && groups <= 65535, "pos_conv: grid too large");
+        const dim3 grid(cdiv(T, kPosTT), groups, batch);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const half_t* x = static_cast<const half_t*>(d_x);
+        const half_t* w = static_cast<const half_t*>(d_w);
+        if (icg == 48)
+            hipLaunchKernelGGL(pos_conv_kernel<48>, grid, dim3(192), 0, s, x, w, d_bias, d_y, T, H, K, pad);
+        else
+            hipLaunchKernelGGL(pos_conv_kernel<64>, grid, dim3(192), 0, s, x, w, d_bias, d_y, T, H, K, pad);
         VDK_HIP(hipGetLastError());
     });
 }

@@ -122,6 +122,7 @@ _SIGS = {
     "vdk_layer_norm": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, C.c_float, C.c_int, _vp, _vp, C.c_float, _vp]),
     "vdk_attention": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "vdk_time_mean": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_pos_conv": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_resblock3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdk_resblock3x3_variant": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp,
                                           C.c_int, _vp]),
@@ -385,6 +386,11 @@ class Context:
     # device-resident path
     def embed_device_async(self, d_pcm, batch, n_samples, d_out):
         rc = self.L.voicedetect_gpu_embed_batch_async(self.ctx, d_pcm, batch, n_samples, d_out)
+        if rc != 0:
+            raise VdkError(self.last_error())
+
+    def analyze_device_async(self, d_pcm, batch, n_samples, d_raw):
+        rc = self.L.voicedetect_gpu_analyze_batch_async(self.ctx, d_pcm, batch, n_samples, d_raw)
         if rc != 0:
             raise VdkError(self.last_error())
 
