@@ -321,6 +321,10 @@ int vdk_pos_conv(const void* d_x, int batch, int T, int H, int groups, const voi
 /* out[b][c] = mean over t of x[b][t][c] (f16 or f32 input, f64 sums): the
  * time mean-pool of the analyze heads (src/analyze_w2v2.cpp:546-550, 607-610). */
 int vdk_time_mean(const void* d_x, int x_f32, int batch, int T, int C, float* d_out, void* stream);
+/* out[b][c] = [out[b][c] +] w * mean over t of x[b][t][c] (accumulate != 0 adds):
+ * the emotion head's weighted layer sum, one hidden state at a time. */
+int vdk_time_mean_acc(const void* d_x, int x_f32, int batch, int T, int C, float w, int accumulate,
+                      float* d_out, void* stream);
 
 #ifdef __cplusplus
 }

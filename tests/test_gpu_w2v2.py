@@ -201,8 +201,13 @@ def test_wave_stats_and_time_mean():
         dh, do = lib.DeviceBuffer.from_array(arr), lib.DeviceBuffer(2 * 200 * 4)
         lib.check(L.vdk_time_mean(dh.ptr, f32, 2, 149, 200, do.ptr, None))
         _sync()
-        np.testing.assert_allclose(do.to_array(np.float32, (2, 200)), arr.astype(np.float64).mean(axis=1),
-                                   rtol=1e-6, atol=1e-6)
+        m = arr.astype(np.float64).mean(axis=1)
+        np.testing.assert_allclose(do.to_array(np.float32, (2, 200)), m, rtol=1e-6, atol=1e-6)
+        # weighted accumulation: out = 0.25 m, then out += -0.5 m
+        lib.check(L.vdk_time_mean_acc(dh.ptr, f32, 2, 149, 200, 0.25, 0, do.ptr, None))
+        lib.check(L.vdk_time_mean_acc(dh.ptr, f32, 2, 149, 200, -0.5, 1, do.ptr, None))
+        _sync()
+        np.testing.assert_allclose(do.to_array(np.float32, (2, 200)), -0.25 * m, rtol=1e-5, atol=1e-6)
 
 
 # ---------------------------------------------------------------- conv epilogue forms

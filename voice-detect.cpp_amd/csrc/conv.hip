@@ -1633,10 +1633,11 @@ int pick_tile(const ConvArgs& a) {
     if (a.KH == 1 && !a.split) {
         // 1-D convs over time-major maps (wav2vec2, ECAPA), from a sweep of
         // the wav2vec2 / ECAPA layer shapes at batch 64 on MI355X: long
-        // kernels (the 128-tap positional conv) on the 128x32 tile, wide
-        // 1x1 GEMMs on the 128x256 8-wave tile, the big strided feature
-        // convs on the 256x256 tile
+        // kernels (a 128-tap positional conv) on the 128x32 tile, wide 1x1
+        // GEMMs on the 128x256 8-wave tile (768 outputs: the 256x128 one),
+        // the big strided feature convs on the 256x256 tile
         if (a.KW > 32 && a.IC % 64 == 0) return 52;
+        if (a.KW == 1 && a.IC >= 512 && a.OC == 768 && a.IC % 64 == 0) return 34;
         if (a.KW == 1 && a.IC >= 512 && a.OC >= 512 && a.OC % 128 == 0 && a.IC % 32 == 0) return 36;
         if (a.KW <= 4 && a.OC % 256 == 0 && a.IC % 64 == 0 && a.npix >= 131072) return 38;
     }

@@ -15,12 +15,14 @@
 //   layers     post-norm (base): h = LN(h + out(attn(qkv(h)))), h = LN(h + ff(h));
 //              pre-norm (large-robust): r += out(attn(qkv(LN(r)))), r += ff(LN(r)),
 //              final LN.  q/k/v is one GEMM over stacked weights.
-//   heads      emotion: weighted layer sum (accumulated by the LayerNorm
-//              kernels) -> time mean -> projector -> classifier; age/gender:
-//              time mean of the last state -> two dense+tanh -> out_proj heads.
-// The emotion head applies the projector after the time mean: both are
-// linear, so mean_t(W x_t + b) = W mean_t(x_t) + b (the reference projects
-// every frame first, src/analyze_w2v2.cpp:541-550).
+//   heads      emotion: weighted layer sum -> time mean -> projector ->
+//              classifier; age/gender: time mean of the last state -> two
+//              dense+tanh -> out_proj heads.
+// The emotion head takes the time mean of each hidden state and sums those
+// with the layer weights, then applies the projector: the reference sums the
+// states frame by frame, projects every frame and then takes the time mean
+// (src/analyze_w2v2.cpp:528-550), and mean_t(W sum_i w_i x_it + b) =
+// W sum_i w_i mean_t(x_it) + b since every step is linear.
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -396,43 +398,48 @@ void Model::analyze_forward(const float* d_pcm, int batch, int n, float* d_raw) 
         gemm("w2v2_ff1", L.ff1, hin, H, T, 1, 0, 0, L.ff1.b, VDK_ACT_GELU, nullptr, 0, 0, 0, w.ffb, c.ff, 0);
         gemm("w2v2_ff2", L.ff2, w.ffb, c.ff, T, 1, 0, 0, L.ff2.b, VDK_ACT_NONE, res, H, res_f32, 0, y, H, y_f32);
     };
-    const float* last = nullptr;   // f32 [B][T][H] the heads pool (age/gender)
+    // The heads pool sum_i w_i mean_t(hidden_states[i]) (w: softmax(layer_weights)
+    // for the emotion head's weighted layer sum, else one-hot on the last state)
+    // into wpool, one state at a time.
+    bool pooled = false;
+    auto pool_state = [&](const void* xs, int x_f32, int i) {
+        if (sw[i] == 0.0f) return;
+        prof_begin("w2v2_time_mean", 0.0, (x_f32 ? 4.0 : 2.0) * BT * H);
+        check_rc(vdk_time_mean_acc(xs, x_f32, batch, T, H, sw[i], pooled ? 1 : 0, w.wpool, stream_));
+        prof_end();
+        pooled = true;
+    };
     if (c.stable_layer_norm) {
         // pre-norm (src/analyze_w2v2.cpp:398-427): w.z is the residual stream r;
         // hidden_states[i] is the input of layer i, the last one the final LN
         for (int li = 0; li < c.n_layers; ++li) {
             const W2Layer& L = m.layers[li];
-            const bool acc = emotion;
-            ln("w2v2_ln", w.z, BT, H, L.ln1, VDK_LN_X_F32 | (acc ? VDK_LN_ACC_INPUT : 0) | (li == 0 ? VDK_LN_ACC_INIT : 0),
-               w.wh, acc ? w.acc : nullptr, sw[li]);
+            pool_state(w.z, 1, li);
+            ln("w2v2_ln", w.z, BT, H, L.ln1, VDK_LN_X_F32, w.wh, nullptr, 0.0f);
             attention(L, w.wh, 1, w.z, w.z, 1);
             ln("w2v2_ln", w.z, BT, H, L.ln2, VDK_LN_X_F32, w.wh1, nullptr, 0.0f);
             feed_forward(L, w.wh1, 1, w.z, w.z, 1);
         }
-        if (emotion) {
-            ln("w2v2_ln", w.z, BT, H, m.enc_n, VDK_LN_X_F32, w.wh, w.acc, sw[c.n_layers]);
-        } else {
-            ln("w2v2_ln", w.z, BT, H, m.enc_n, VDK_LN_X_F32 | VDK_LN_Y_F32, w.acc, nullptr, 0.0f);
-            last = w.acc;
-        }
+        // the final LN in f32 (the last hidden state; read back by analyze_capture)
+        ln("w2v2_ln", w.z, BT, H, m.enc_n, VDK_LN_X_F32 | VDK_LN_Y_F32, w.acc, nullptr, 0.0f);
+        pool_state(w.acc, 1, c.n_layers);
     } else {
         // post-norm (src/analyze_w2v2.cpp:429-468): hidden_states[0] is the
         // encoder LN of (projection + pos conv), then every layer's output
-        ln("w2v2_ln", w.z, BT, H, m.enc_n, VDK_LN_X_F32 | VDK_LN_ACC_INIT, w.wh, w.acc, sw[0]);
+        ln("w2v2_ln", w.z, BT, H, m.enc_n, VDK_LN_X_F32, w.wh, nullptr, 0.0f);
+        pool_state(w.wh, 0, 0);
         for (int li = 0; li < c.n_layers; ++li) {
             const W2Layer& L = m.layers[li];
             attention(L, w.wh, 0, w.wh, w.z, 1);
             ln("w2v2_ln", w.z, BT, H, L.ln1, VDK_LN_X_F32, w.wh1, nullptr, 0.0f);
             feed_forward(L, w.wh1, 0, w.wh1, w.z, 1);
-            ln("w2v2_ln", w.z, BT, H, L.ln2, VDK_LN_X_F32, w.wh, w.acc, sw[li + 1]);
+            ln("w2v2_ln", w.z, BT, H, L.ln2, VDK_LN_X_F32, w.wh, nullptr, 0.0f);
+            pool_state(w.wh, 0, li + 1);
         }
-        last = w.acc;   // emotion: the weighted sum; age/gender reads it with weights [0..0, 1]
     }
+    require(pooled, "voicedetect: the analyze head pools no hidden state");
 
     // -- heads ------------------------------------------------------------------
-    prof_begin("w2v2_time_mean", 0.0, 4.0 * BT * H);
-    check_rc(vdk_time_mean(emotion ? w.acc : last, 1, batch, T, H, w.wpool, stream_));
-    prof_end();
     if (emotion) {
         const int P = c.proj, ne = m.n_out;
         linear("w2v2_projector", w.wpool, batch, H, m.head_w1, m.head_b1, nullptr, P, 0, w.wt1);
@@ -489,7 +496,7 @@ void Model::analyze_capture(const float* pcm, int batch, int n, float* feat, flo
     if (hidden) {
         // the last hidden state: the final LN output (f32) for the pre-norm
         // stack, the last layer's f16 LN output for the post-norm one
-        if (c.stable_layer_norm && cfg_.arch == "wav2vec2_age_gender")
+        if (c.stable_layer_norm)
             VDK_HIP(hipMemcpyAsync(hidden, ws_.acc, 4 * BT * c.hidden, hipMemcpyDeviceToHost, stream_));
         else
             widen(ws_.wh, BT * c.hidden, hidden);

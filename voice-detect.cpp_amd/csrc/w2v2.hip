@@ -314,6 +314,75 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const void* __restrict_
     }
 }
 
+// Same for C = 256 * NV: lane l owns the 4-element groups l + 64 j (j < NV),
+// moved as 16-byte (f32) / 8-byte (f16) vectors.
+template <int NV>
+__global__ __launch_bounds__(256) void layer_norm_vec_kernel(const void* __restrict__ x, int rows,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, float eps, int flags,
+                                                             void* __restrict__ y, float* __restrict__ acc,
+                                                             float acc_w) {
+    constexpr int C = 256 * NV;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const bool xf = flags & VDK_LN_X_F32;
+    const size_t base = (size_t)row * C;
+    float v[NV][4];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const size_t i = base + 4 * (lane + 64 * j);
+        if (xf) {
+            const float4v u = *reinterpret_cast<const float4v*>(static_cast<const float*>(x) + i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[j][e] = u[e];
+        } else {
+            const half4 u = *reinterpret_cast<const half4*>(static_cast<const half_t*>(x) + i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[j][e] = (float)u[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s += v[j][e];
+    }
+    const float mu = wave_sum(s) / C;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q += (v[j][e] - mu) * (v[j][e] - mu);
+    const float rstd = 1.0f / sqrtf(wave_sum(q) / C + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e0 = 4 * (lane + 64 * j);
+        const size_t i = base + e0;
+        const float4v gm = *reinterpret_cast<const float4v*>(gamma + e0);
+        const float4v bt = *reinterpret_cast<const float4v*>(beta + e0);
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            o[e] = (v[j][e] - mu) * rstd * gm[e] + bt[e];
+            if (flags & VDK_LN_GELU) o[e] = gelu_erf(o[e]);
+        }
+        if (acc) {
+            float4v a = (flags & VDK_LN_ACC_INIT) ? float4v{0.0f, 0.0f, 0.0f, 0.0f}
+                                                  : *reinterpret_cast<const float4v*>(acc + i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[e] += acc_w * ((flags & VDK_LN_ACC_INPUT) ? v[j][e] : o[e]);
+            *reinterpret_cast<float4v*>(acc + i) = a;
+        }
+        if (y) {
+            if (flags & VDK_LN_Y_F32) {
+                *reinterpret_cast<float4v*>(static_cast<float*>(y) + i) = float4v{o[0], o[1], o[2], o[3]};
+            } else {
+                half4 h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) h[e] = (half_t)o[e];
+                *reinterpret_cast<half4*>(static_cast<half_t*>(y) + i) = h;
+            }
+        }
+    }
+}
+
 // ---- self-attention per (clip, head), head_dim 64 ----
 // qkv [B][T][3H] f16 (q | k | v, head h at columns h*64 of each), out [B][T][H].
 // A workgroup (4 waves) owns 128 queries of one (clip, head); wave w owns 32.
@@ -326,15 +395,20 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const void* __restrict_
 // transposed ([dim][key]) so the matching A operand is two 8-byte reads.
 constexpr int kHD = 64, kKB = 64, kKR = kHD + 8, kVR = kKB + 8;
 
-__global__ __launch_bounds__(256) void attention_kernel(const half_t* __restrict__ qkv, int T, int H, float scale_log2,
-                                                        half_t* __restrict__ out) {
+// NWQ waves per workgroup (32 queries each); the next key block's K and V rows
+// are loaded into registers while the current block is computed.
+template <int NWQ>
+__global__ __launch_bounds__(64 * NWQ) void attention_kernel(const half_t* __restrict__ qkv, int T, int H,
+                                                             float scale_log2, half_t* __restrict__ out) {
+    constexpr int NT = 64 * NWQ;
+    constexpr int NLD = kKB * kHD / 8 / NT;   // 16-byte K (and V) chunks per thread per block
     __shared__ __attribute__((aligned(16))) half_t sK[kKB * kKR];   // [key][dim]
     __shared__ __attribute__((aligned(16))) half_t sV[kHD * kVR];   // [dim][key]
     const int b = blockIdx.z, h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, lr = lane & 31;
     const size_t rs = 3 * (size_t)H;
     const half_t* base = qkv + (size_t)b * T * rs;
-    const int q0 = blockIdx.x * 128 + wave * 32;
+    const int q0 = blockIdx.x * 32 * NWQ + wave * 32;
     const int qr = q0 + lr < T ? q0 + lr : T - 1;
     half8 qf[4];
 #pragma unroll
@@ -345,19 +419,28 @@ __global__ __launch_bounds__(256) void attention_kernel(const half_t* __restrict
     for (int r = 0; r < 16; ++r) { o0[r] = 0.0f; o1[r] = 0.0f; }
     float m = -INFINITY, l = 0.0f;
     const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+    half8 kn[NLD], vn[NLD];
+    auto fetch = [&](int kb) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int i = tid + j * NT, key = i >> 3, d0 = (i & 7) * 8, kg = kb + key;
+            const half_t* src = base + (size_t)kg * rs + h * kHD + d0;
+            kn[j] = kg < T ? *reinterpret_cast<const half8*>(src + H) : zero8;
+            vn[j] = kg < T ? *reinterpret_cast<const half8*>(src + 2 * H) : zero8;
+        }
+    };
+    fetch(0);
     for (int kb = 0; kb < T; kb += kKB) {
         __syncthreads();   // the previous block's operands are no longer read
 #pragma unroll
-        for (int i = tid; i < kKB * kHD / 8; i += 256) {
-            const int key = i >> 3, d0 = (i & 7) * 8, kg = kb + key;
-            const half_t* src = base + (size_t)kg * rs + h * kHD + d0;
-            const half8 kv = kg < T ? *reinterpret_cast<const half8*>(src + H) : zero8;
-            const half8 vv = kg < T ? *reinterpret_cast<const half8*>(src + 2 * H) : zero8;
-            *reinterpret_cast<half8*>(&sK[key * kKR + d0]) = kv;
+        for (int j = 0; j < NLD; ++j) {
+            const int i = tid + j * NT, key = i >> 3, d0 = (i & 7) * 8;
+            *reinterpret_cast<half8*>(&sK[key * kKR + d0]) = kn[j];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) sV[(d0 + e) * kVR + key] = vv[e];
+            for (int e = 0; e < 8; ++e) sV[(d0 + e) * kVR + key] = vn[j][e];
         }
         __syncthreads();
+        if (kb + kKB < T) fetch(kb + kKB);
         float16v s[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
@@ -537,23 +620,44 @@ __global__ __launch_bounds__(192) void pos_conv_kernel(const half_t* __restrict_
     }
 }
 
-// ---- per-clip mean over time: out[b][c] = mean_t x[b][t][c] (f64, 4 time
-// partitions combined in a fixed order).
-__global__ __launch_bounds__(256) void time_mean_kernel(const void* __restrict__ x, int x_f32, int T, int C,
-                                                        float* __restrict__ out) {
-    __shared__ double part[4][64];
-    const int tx = threadIdx.x & 63, tp = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + tx, b = blockIdx.y;
-    double s = 0.0;
+// ---- per-clip mean over time: out[b][c] = [out +] w * mean_t x[b][t][c] ----
+// A workgroup covers 256 channels of one clip: 64 lanes x 4 channels (one
+// 8- or 16-byte load per row) x 16 time partitions, f64 sums combined in a
+// fixed order.  C % 4 == 0.
+__global__ __launch_bounds__(1024) void time_mean_kernel(const void* __restrict__ x, int x_f32, int T, int C, float w,
+                                                         int accumulate, float* __restrict__ out) {
+    __shared__ double part[16][256];
+    const int cg = threadIdx.x & 63, tp = threadIdx.x >> 6;
+    const int c = blockIdx.x * 256 + cg * 4, b = blockIdx.y;
+    double s[4] = {0.0, 0.0, 0.0, 0.0};
     if (c < C) {
-        for (int t = tp; t < T; t += 4) {
+        for (int t = tp; t < T; t += 16) {
             const size_t i = ((size_t)b * T + t) * C + c;
-            s += x_f32 ? (double)static_cast<const float*>(x)[i] : (double)(float)static_cast<const half_t*>(x)[i];
+            if (x_f32) {
+                const float4v v = *reinterpret_cast<const float4v*>(static_cast<const float*>(x) + i);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s[e] += (double)v[e];
+            } else {
+                const half4 v = *reinterpret_cast<const half4*>(static_cast<const half_t*>(x) + i);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s[e] += (double)(float)v[e];
+            }
         }
     }
-    part[tp][tx] = s;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[tp][cg * 4 + e] = s[e];
     __syncthreads();
-    if (tp == 0 && c < C) out[(size_t)b * C + c] = (float)(((part[0][tx] + part[1][tx]) + (part[2][tx] + part[3][tx])) / T);
+    if (threadIdx.x < 256) {
+        const int cc = blockIdx.x * 256 + threadIdx.x;
+        if (cc < C) {
+            double a = 0.0;
+#pragma unroll
+            for (int p = 0; p < 16; ++p) a += part[p][threadIdx.x];
+            const float m = (float)(a / T);
+            const size_t o = (size_t)b * C + cc;
+            out[o] = accumulate ? out[o] + w * m : w * m;
+        }
+    }
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -654,6 +758,23 @@ extern "C" int vdk_layer_norm(const void* d_x, int rows, int C, const float* d_g
                 "layer_norm: unknown flag");
         hipStream_t s = static_cast<hipStream_t>(stream);
         const dim3 g(cdiv(rows, 4));
+        const bool vec = C % 256 == 0 && al16(d_x) && al16(d_gamma) && al16(d_beta) && al16(d_y) && al16(d_acc);
+#define VDK_LN_VEC(NV)                                                                                              \
+    case NV:                                                                                                        \
+        hipLaunchKernelGGL(layer_norm_vec_kernel<NV>, g, dim3(256), 0, s, d_x, rows, d_gamma, d_beta, eps, flags, \
+                           d_y, d_acc, acc_w);                                                                     \
+        break;
+        if (vec) {
+            switch (C / 256) {
+                VDK_LN_VEC(1) VDK_LN_VEC(2) VDK_LN_VEC(3) VDK_LN_VEC(4) VDK_LN_VEC(6) VDK_LN_VEC(8)
+                VDK_LN_VEC(12) VDK_LN_VEC(16)
+                default: goto scalar;
+            }
+            VDK_HIP(hipGetLastError());
+            return;
+        }
+#undef VDK_LN_VEC
+    scalar:
         if (C <= 1024)
             hipLaunchKernelGGL(layer_norm_kernel<16>, g, dim3(256), 0, s, d_x, rows, C, d_gamma, d_beta, eps, flags,
                                d_y, d_acc, acc_w);
@@ -673,10 +794,31 @@ extern "C" int vdk_attention(const void* d_qkv, int batch, int T, int n_heads, i
         require(al16(d_qkv) && al16(d_out), "attention: buffers must be 16-byte aligned");
         const size_t H = (size_t)n_heads * head_dim;
         require((size_t)batch * T * 3 * H < (1ull << 31), "attention: too many tokens for one launch");
-        require(T <= 65535 * 128 && n_heads <= 65535 && batch <= 65535, "attention: grid too large");
-        hipLaunchKernelGGL(attention_kernel, dim3(cdiv(T, 128), n_heads, batch), dim3(256), 0,
-                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_qkv), T, (int)H,
-                           scale * 1.4426950408889634f, static_cast<half_t*>(d_out));
+        require(T <= 65535 * 64 && n_heads <= 65535 && batch <= 65535, "attention: grid too large");
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const half_t* q = static_cast<const half_t*>(d_qkv);
+        half_t* o = static_cast<half_t*>(d_out);
+        const float sl2 = scale * 1.4426950408889634f;
+        // short clips: 64 queries per workgroup (less padding past T); long
+        // ones: 128, so each staged key block serves more queries
+        if (T <= 512)
+            hipLaunchKernelGGL(attention_kernel<2>, dim3(cdiv(T, 64), n_heads, batch), dim3(128), 0, s, q, T, (int)H,
+                               sl2, o);
+        else
+            hipLaunchKernelGGL(attention_kernel<4>, dim3(cdiv(T, 128), n_heads, batch), dim3(256), 0, s, q, T, (int)H,
+                               sl2, o);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_time_mean_acc(const void* d_x, int x_f32, int batch, int T, int C, float w, int accumulate,
+                                 float* d_out, void* stream) {
+    return guarded([&] {
+        require(d_x && d_out, "time_mean: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0 && C % 4 == 0, "time_mean: C must be a positive multiple of 4");
+        require(al16(d_x), "time_mean: input must be 16-byte aligned");
+        hipLaunchKernelGGL(time_mean_kernel, dim3(cdiv(C, 256), batch), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                           d_x, x_f32 ? 1 : 0, T, C, w, accumulate ? 1 : 0, d_out);
         VDK_HIP(hipGetLastError());
     });
 }
@@ -684,9 +826,10 @@ extern "C" int vdk_attention(const void* d_qkv, int batch, int T, int n_heads, i
 extern "C" int vdk_time_mean(const void* d_x, int x_f32, int batch, int T, int C, float* d_out, void* stream) {
     return guarded([&] {
         require(d_x && d_out, "time_mean: NULL device pointer");
-        require(batch > 0 && T > 0 && C > 0, "time_mean: empty shape");
-        hipLaunchKernelGGL(time_mean_kernel, dim3(cdiv(C, 64), batch), dim3(256), 0, static_cast<hipStream_t>(stream),
-                           d_x, x_f32 ? 1 : 0, T, C, d_out);
+        require(batch > 0 && T > 0 && C > 0 && C % 4 == 0, "time_mean: C must be a positive multiple of 4");
+        require(al16(d_x), "time_mean: input must be 16-byte aligned");
+        hipLaunchKernelGGL(time_mean_kernel, dim3(cdiv(C, 256), batch), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                           d_x, x_f32 ? 1 : 0, T, C, 1.0f, 0, d_out);
         VDK_HIP(hipGetLastError());
     });
 }
