@@ -1616,8 +1616,9 @@ int tile_override() {
 // Per-layer-class defaults, from a sweep of every ResNet34 conv shape at
 // batch 64 on MI355X (64-channel 3x3 stride-1 layers with the plain
 // epilogue: the register-weight kernel; 128-channel ones whose map is 39-76
-// wide: the band kernel; other narrow 3x3 stride-1 layers: the 32-channel
-// halo tile;
+// wide: the band kernel, 256+-channel ones on maps up to 38 wide: the
+// 3-block band; the strided / 1x1 32 -> 64 convs: the register-staged 64x128
+// tile; other narrow 3x3 stride-1 layers: the 32-channel halo tile;
 // 128 output channels: the 128x128 DMA tile with KC = 32; the rest: DMA
 // implicit GEMM with the widest OC tile that divides OC; IC % 32 != 0: the
 // register-staged kernel with KC = 16).  OC that no tile divides runs on
@@ -1643,6 +1644,8 @@ int pick_tile(const ConvArgs& a) {
     }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
+    if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[58], a)) return 58;
+    if (!a.split && !is_s1_3x3(a) && a.IC == 32 && a.OC == 64) return 2;
     if (!a.split && is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return 28;
     if (a.IC % 32 == 0 && a.OC == 128) return 39;   // 128x128 tile, KC = 32
     if (a.IC % 64 == 0) return bm == 128 ? 18 : (bm == 64 ? 15 : 14);
