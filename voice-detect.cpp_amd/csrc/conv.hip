@@ -1641,6 +1641,7 @@ int pick_tile(const ConvArgs& a) {
         if (a.KW == 1 && a.IC >= 512 && a.OC == 768 && a.IC % 64 == 0) return 34;
         if (a.KW == 1 && a.IC >= 512 && a.OC >= 512 && a.OC % 128 == 0 && a.IC % 32 == 0) return 36;
         if (a.KW <= 4 && a.OC % 256 == 0 && a.IC % 64 == 0 && a.npix >= 131072) return 38;
+        if (a.KW == 3 && a.IC == 128 && a.OC == 128) return 40;   // ECAPA's Res2Net group convs
     }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;

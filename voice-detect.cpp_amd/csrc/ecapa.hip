@@ -62,15 +62,26 @@ __global__ __launch_bounds__(256) void reflect_pad_add_kernel(const half_t* __re
     *reinterpret_cast<half8*>(out + ((size_t)b * Tp + j) * G + c) = v;
 }
 
-__global__ __launch_bounds__(256) void channel_mean_kernel(const half_t* __restrict__ x, int xs, int T, int C,
-                                                           float* __restrict__ out) {
-    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-    if (c >= C) return;
-    const half_t* p = x + (size_t)b * T * xs + c;
+// Per-channel mean over time: 64 channels x 16 time partitions per
+// workgroup, f64 partition sums combined in a fixed order.
+__global__ __launch_bounds__(1024) void channel_mean_kernel(const half_t* __restrict__ x, int xs, int T, int C,
+                                                            float* __restrict__ out) {
+    __shared__ double sp[16][64];
+    const int tx = threadIdx.x & 63, tp = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + tx, b = blockIdx.y;
     double s = 0.0;
-#pragma unroll 8
-    for (int t = 0; t < T; ++t) s += (double)(float)p[(size_t)t * xs];
-    out[(size_t)b * C + c] = (float)(s / T);
+    if (c < C) {
+        const half_t* p = x + (size_t)b * T * xs + c;
+        for (int t = tp; t < T; t += 16) s += (double)(float)p[(size_t)t * xs];
+    }
+    sp[tp][tx] = s;
+    __syncthreads();
+    if (tp == 0 && c < C) {
+        double S = 0.0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S += sp[i][tx];
+        out[(size_t)b * C + c] = (float)(S / T);
+    }
 }
 
 __global__ __launch_bounds__(256) void se_gate_residual_kernel(const half_t* __restrict__ x, int xs,
@@ -95,56 +106,103 @@ __global__ __launch_bounds__(256) void se_gate_residual_kernel(const half_t* __r
 }
 
 // Global statistics over time per (clip, channel): out[b] = [mean ; sqrt(clamp(var, eps))].
-__global__ __launch_bounds__(256) void asp_stats_kernel(const half_t* __restrict__ x, int xs, int T, int C,
-                                                        float eps, float* __restrict__ out) {
-    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-    if (c >= C) return;
-    const half_t* p = x + (size_t)b * T * xs + c;
+// Per-channel mean and std over time (biased, clamped at eps): 64 channels x
+// 16 time partitions per workgroup, two passes of f64 partition sums
+// combined in a fixed order.
+__global__ __launch_bounds__(1024) void asp_stats_kernel(const half_t* __restrict__ x, int xs, int T, int C,
+                                                         float eps, float* __restrict__ out) {
+    __shared__ double sp[16][64];
+    const int tx = threadIdx.x & 63, tp = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + tx, b = blockIdx.y;
+    const bool on = c < C;
+    const half_t* p = x + (size_t)b * T * xs + (on ? c : 0);
     double s = 0.0;
-#pragma unroll 8
-    for (int t = 0; t < T; ++t) s += (double)(float)p[(size_t)t * xs];
-    const float m = (float)(s / T);
+    if (on)
+        for (int t = tp; t < T; t += 16) s += (double)(float)p[(size_t)t * xs];
+    sp[tp][tx] = s;
+    __syncthreads();
+    double S = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S += sp[i][tx];
+    const float m = (float)(S / T);
     double s2 = 0.0;
-#pragma unroll 8
-    for (int t = 0; t < T; ++t) {
-        const float d = (float)p[(size_t)t * xs] - m;
-        s2 += (double)(d * d);
+    if (on)
+        for (int t = tp; t < T; t += 16) {
+            const float d = (float)p[(size_t)t * xs] - m;
+            s2 += (double)(d * d);
+        }
+    __syncthreads();   // every thread has read sp
+    sp[tp][tx] = s2;
+    __syncthreads();
+    if (tp == 0 && on) {
+        double S2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S2 += sp[i][tx];
+        float v = (float)(S2 / T);
+        if (v < eps) v = eps;
+        out[(size_t)b * 2 * C + c] = m;
+        out[(size_t)b * 2 * C + C + c] = sqrtf(v);
     }
-    float v = (float)(s2 / T);
-    if (v < eps) v = eps;
-    out[(size_t)b * 2 * C + c] = m;
-    out[(size_t)b * 2 * C + C + c] = sqrtf(v);
 }
 
 // Softmax over time of the attention logits, then attention-weighted mean / std.
-__global__ __launch_bounds__(256) void asp_pool_kernel(const float* __restrict__ logits, int ls,
-                                                       const half_t* __restrict__ x, int xs, int T, int C, float eps,
-                                                       float* __restrict__ out) {
-    const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-    if (c >= C) return;
-    const float* l = logits + (size_t)b * T * ls + c;
-    const half_t* p = x + (size_t)b * T * xs + c;
-    float mx = -INFINITY;
-    for (int t = 0; t < T; ++t) mx = fmaxf(mx, l[(size_t)t * ls]);
+// A workgroup covers 64 channels of one clip with 16 time partitions per
+// channel: max, then the f64 sums of e = exp(l - max) and e*x, then of
+// e*(x - mu)^2, each partitioned over time and combined in a fixed order.
+__global__ __launch_bounds__(1024) void asp_pool_kernel(const float* __restrict__ logits, int ls,
+                                                        const half_t* __restrict__ x, int xs, int T, int C, float eps,
+                                                        float* __restrict__ out) {
+    __shared__ float smax[16][64];
+    __shared__ double sz[16][64], smu[16][64];
+    const int tx = threadIdx.x & 63, tp = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + tx, b = blockIdx.y;
+    const bool on = c < C;
+    const float* l = logits + (size_t)b * T * ls + (on ? c : 0);
+    const half_t* p = x + (size_t)b * T * xs + (on ? c : 0);
+    float m = -INFINITY;
+    if (on)
+        for (int t = tp; t < T; t += 16) m = fmaxf(m, l[(size_t)t * ls]);
+    smax[tp][tx] = m;
+    __syncthreads();
+    float mx = smax[0][tx];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, smax[i][tx]);
     double z = 0.0, mu = 0.0;
-#pragma unroll 4
-    for (int t = 0; t < T; ++t) {
-        const double e = (double)expf(l[(size_t)t * ls] - mx);
-        z += e;
-        mu += e * (double)(float)p[(size_t)t * xs];
+    if (on)
+        for (int t = tp; t < T; t += 16) {
+            const double e = (double)expf(l[(size_t)t * ls] - mx);
+            z += e;
+            mu += e * (double)(float)p[(size_t)t * xs];
+        }
+    sz[tp][tx] = z;
+    smu[tp][tx] = mu;
+    __syncthreads();
+    double Z = 0.0, MU = 0.0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        Z += sz[i][tx];
+        MU += smu[i][tx];
     }
-    const float muf = (float)(mu / z);
+    const float muf = (float)(MU / Z);
     double var = 0.0;
-#pragma unroll 4
-    for (int t = 0; t < T; ++t) {
-        const double e = (double)expf(l[(size_t)t * ls] - mx);
-        const float d = (float)p[(size_t)t * xs] - muf;
-        var += e * (double)(d * d);
+    if (on)
+        for (int t = tp; t < T; t += 16) {
+            const double e = (double)expf(l[(size_t)t * ls] - mx);
+            const float d = (float)p[(size_t)t * xs] - muf;
+            var += e * (double)(d * d);
+        }
+    __syncthreads();   // every thread has read sz / smu
+    sz[tp][tx] = var;
+    __syncthreads();
+    if (tp == 0 && on) {
+        double V = 0.0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) V += sz[i][tx];
+        float v = (float)(V / Z);
+        if (v < eps) v = eps;
+        out[(size_t)b * 2 * C + c] = muf;
+        out[(size_t)b * 2 * C + C + c] = sqrtf(v);
     }
-    float v = (float)(var / z);
-    if (v < eps) v = eps;
-    out[(size_t)b * 2 * C + c] = muf;
-    out[(size_t)b * 2 * C + C + c] = sqrtf(v);
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -186,7 +244,7 @@ extern "C" int vdk_channel_mean(const void* d_x, int x_stride, int batch, int T,
     return guarded([&] {
         require(d_x && d_out, "channel_mean: NULL device pointer");
         require(batch > 0 && T > 0 && C > 0 && x_stride >= C, "channel_mean: bad shape");
-        hipLaunchKernelGGL(channel_mean_kernel, dim3(cdiv(C, 256), batch), dim3(256), 0,
+        hipLaunchKernelGGL(channel_mean_kernel, dim3(cdiv(C, 64), batch), dim3(1024), 0,
                            static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, d_out);
         VDK_HIP(hipGetLastError());
     });
@@ -214,7 +272,7 @@ extern "C" int vdk_asp_stats(const void* d_x, int x_stride, int batch, int T, in
     return guarded([&] {
         require(d_x && d_out, "asp_stats: NULL device pointer");
         require(batch > 0 && T > 0 && C > 0 && x_stride >= C, "asp_stats: bad shape");
-        hipLaunchKernelGGL(asp_stats_kernel, dim3(cdiv(C, 256), batch), dim3(256), 0,
+        hipLaunchKernelGGL(asp_stats_kernel, dim3(cdiv(C, 64), batch), dim3(1024), 0,
                            static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, eps,
                            d_out);
         VDK_HIP(hipGetLastError());
@@ -226,7 +284,7 @@ extern "C" int vdk_asp_pool(const float* d_logits, int l_stride, const void* d_x
     return guarded([&] {
         require(d_logits && d_x && d_out, "asp_pool: NULL device pointer");
         require(batch > 0 && T > 0 && C > 0 && x_stride >= C && l_stride >= C, "asp_pool: bad shape");
-        hipLaunchKernelGGL(asp_pool_kernel, dim3(cdiv(C, 256), batch), dim3(256), 0,
+        hipLaunchKernelGGL(asp_pool_kernel, dim3(cdiv(C, 64), batch), dim3(1024), 0,
                            static_cast<hipStream_t>(stream), d_logits, l_stride, static_cast<const half_t*>(d_x),
                            x_stride, T, C, eps, d_out);
         VDK_HIP(hipGetLastError());
