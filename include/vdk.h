@@ -101,6 +101,9 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  *   v = tanh(v)                    (tanh_after)
  * stored f16 (or f32 if y_f32) at pixel (b, oh, ow), or at (b, ow, oh) when
  * y_time_major (an NHWC [B][H][W][C] map written as [B][W][H*C], no residual).
+ * in_scale / in_shift (1x1 convs without padding): the input channels pass
+ * through relu(x * in_scale[c] + in_shift[c]), rounded to f16, on their way to
+ * the MFMA (a standalone BatchNorm + ReLU before the conv, fused).
  * out_w > 0 keeps only the first out_w output columns of each row (a conv
  * whose right pad is one shorter than its left, e.g. wav2vec2's positional
  * conv with its last step dropped).  y and an f32 residual may be the same
@@ -126,6 +129,7 @@ typedef struct {
     int split; int x_lo, res_lo, y_lo;
     int tile;
     int res_f32, res_after_act, out_w;
+    const float* in_scale; const float* in_shift;
 } vdk_conv_desc;
 int vdk_conv2d_ex(const vdk_conv_desc* desc, void* stream);
 int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* desc);

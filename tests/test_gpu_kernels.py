@@ -294,3 +294,51 @@ def test_tstp_linear_l2_match_oracle():
     lib.check(L.vdk_l2norm(z.ptr, 2, 8, None))
     lib.check(L.vdk_synchronize())
     assert np.array_equal(z.to_array(np.float32, (2, 8)), np.zeros((2, 8), np.float32))
+
+
+@pytest.mark.parametrize("case", [
+    # (B, T, IC, x_stride, OC): CAM++ dense-layer linear1 shapes (the BatchNorm +
+    # ReLU of the concatenated features folded into the GEMM's operand loads)
+    (2, 499, 128, 512, 128),
+    (1, 97, 480, 896, 128),
+    (3, 33, 96, 96, 64),
+    (1, 5, 64, 64, 32),
+])
+def test_conv_input_prologue(case):
+    """y = relu(W relu(x*s + t) + b) for every tile that takes the input prologue,
+    against numpy with the prologue rounded to f16 (as the GPU feeds it to the MFMA)."""
+    L = lib.lib()
+    B, T, IC, xs, OC = case
+    rng = np.random.default_rng(IC + OC + T)
+    x = rng.standard_normal((B, T, xs)).astype(np.float16)
+    s = (0.5 + rng.random(IC)).astype(np.float32)
+    t = (0.3 * rng.standard_normal(IC)).astype(np.float32)
+    w = (rng.standard_normal((OC, IC)) * np.sqrt(1.0 / IC)).astype(np.float16)
+    b = (0.1 * rng.standard_normal(OC)).astype(np.float32)
+    u = np.maximum(x[..., :IC].astype(np.float32) * s + t, 0).astype(np.float16).astype(np.float64)
+    ref = np.maximum(u @ w.astype(np.float64).T + b, 0)
+    dx, dw, db, ds, dt = (lib.DeviceBuffer.from_array(a) for a in (x, w, b, s, t))
+    dy = lib.DeviceBuffer(B * T * OC * 2)
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = dx.ptr, B, 1, T, IC, xs
+    d.w, d.OC, d.KH, d.KW = dw.ptr, OC, 1, 1
+    d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+    d.bias, d.act, d.y = db.ptr, lib.ACT_RELU, dy.ptr
+    d.in_scale, d.in_shift = ds.ptr, dt.ptr
+    n = 0
+    for tile in [-1] + list(range(L.vdk_conv2d_tile_count())):
+        if tile >= 0 and not L.vdk_conv2d_tile_fits_ex(tile, d):
+            continue
+        d.tile = tile
+        announce(f"input prologue tile {tile} {case}")
+        lib.check(L.vdk_conv2d_ex(d, None))
+        lib.check(L.vdk_synchronize())
+        got = dy.to_array(np.float16, (B, T, OC)).astype(np.float64)
+        ok, ratio, rel = close_report(got, ref, CONV_RTOL, CONV_ATOL_RMS)
+        assert ok, f"tile {tile}: ratio {ratio:.3f} rel {rel:.2e}"
+        n += 1
+    assert n >= 3
+    # the prologue needs a 1x1 conv without padding
+    d.KW, d.pad_w, d.tile = 3, 1, -1
+    assert L.vdk_conv2d_ex(d, None) != 0
+    assert "input prologue" in L.vdk_last_error().decode()

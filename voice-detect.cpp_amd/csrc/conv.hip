@@ -44,6 +44,8 @@ struct ConvArgs {
     int split;                 // split-f16 tensors: value = hi + lo, lo at +x_lo / +r_lo / +y_lo elements;
     int x_lo, r_lo, y_lo;      //   weights [OC][KH][KW][3*IC] = [hi | hi | lo] per tap
     int res_f32, res_after;    // f32 residual; residual added after the activation
+    const float* in_scale;     // input prologue x' = relu(x * in_scale[c] + in_shift[c]) (may be NULL)
+    const float* in_shift;
     int npix;                  // B * Ho * Wo
     int npix_in;               // B * H * W
 };
@@ -277,8 +279,22 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
             const int ih = x_ih[i] + kh * a.dh, iw = x_iw[i] + kw * a.dw;
             xr[i] = zero8;
             if (x_on[i] && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
+            {
                 xr[i] = *reinterpret_cast<const half8*>(a.x + ((size_t)(x_img[i] + ih) * a.W + iw) * a.xs + c0 +
                                                         x_c[i]);
+                if (a.in_scale) {   // BatchNorm + ReLU of the input channels, as the f16 operand
+                    const int cc = c0 + x_c[i];
+                    const float4v s0 = *reinterpret_cast<const float4v*>(a.in_scale + cc);
+                    const float4v s1 = *reinterpret_cast<const float4v*>(a.in_scale + cc + 4);
+                    const float4v t0 = *reinterpret_cast<const float4v*>(a.in_shift + cc);
+                    const float4v t1 = *reinterpret_cast<const float4v*>(a.in_shift + cc + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        xr[i][e] = (half_t)fmaxf((float)xr[i][e] * s0[e] + t0[e], 0.0f);
+                        xr[i][e + 4] = (half_t)fmaxf((float)xr[i][e + 4] * s1[e] + t1[e], 0.0f);
+                    }
+                }
+            }
         }
     };
     auto stash = [&](int st) {
@@ -1509,7 +1525,8 @@ struct TileCfg {
 // Entries 0-13 are the register-staged kernel (any layout; the only one with
 // KC=16 for IC % 32 != 0), 14-25 the LDS-DMA kernel, 26-32 the halo kernel,
 // 33-52 LDS-DMA tiles with 8 waves per workgroup, 53-56 the register-weight
-// persistent 3x3 kernel, 57+ the band kernel for wide 3x3 layers.
+// persistent 3x3 kernel, 57-59 the band kernel for wide 3x3 layers, 60-61
+// narrow LDS-DMA tiles, 62-63 narrow register-staged tiles.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -1574,6 +1591,10 @@ const TileCfg kTiles[] = {
     {128, 384, 16, launch_band<5, 6>, true, 0, BandTile<5, 6>::MAXW},   // 57: band kernels
     {128, 192, 16, launch_band<5, 3>, true, 0, BandTile<5, 3>::MAXW},   // 58
     {128, 320, 16, launch_band<4, 5>, true, 0, BandTile<4, 5>::MAXW},   // 59
+    {32, 64, 32, launch_dma<32, 64, 32, 32, 32, 2>},      // 60: narrow DMA tiles (OC = 32, few pixels)
+    {32, 128, 32, launch_dma<32, 128, 32, 32, 32, 2>},    // 61
+    {128, 32, 32, launch_igemm<128, 32, 64, 32, 32>},     // 62: register-staged, more workgroups
+    {64, 64, 32, launch_igemm<64, 64, 32, 32, 32>},       // 63
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -1594,13 +1615,16 @@ bool plain_epilogue(const ConvArgs& a) {
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
+    // the input prologue lives in the register-staged kernel's operand loads
+    if (a.in_scale && !(idx < kFirstDma || idx >= 62)) return false;
     // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
     // the in-image tap range for a single row of taps; longer 2-D kernels
     // take the register-staged kernel
     if (a.KH * a.KW > 32 && a.KH != 1 && idx >= kFirstDma) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
     if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % t.bm == 0 && a.IC % 16 == 0;
-    if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8))) return false;   // split: DMA only
+    if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8) || idx >= 62))
+        return false;   // split: DMA only
     return a.IC % t.kc == 0;
 }
 
@@ -1627,6 +1651,10 @@ int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
+    if (a.in_scale) {   // register-staged kernel only; 64x64 tiles for a few ten thousand pixels
+        if (a.IC % 32 == 0) return bm >= 64 ? (a.npix < 32768 ? 63 : (bm == 128 ? 5 : 2)) : 10;
+        return bm == 128 ? 13 : (bm == 64 ? 12 : 11);
+    }
     if (a.KH * a.KW > 32 && a.KH != 1) {   // register-staged kernel only
         if (a.IC % 32 == 0) return bm == 128 ? 5 : (bm == 64 ? 2 : 10);
         return a.IC % 16 == 0 ? (bm == 128 ? 13 : (bm == 64 ? 12 : 11)) : -1;
@@ -1642,6 +1670,7 @@ int pick_tile(const ConvArgs& a) {
         if (a.KW == 1 && a.IC >= 512 && a.OC >= 512 && a.OC % 128 == 0 && a.IC % 32 == 0) return 36;
         if (a.KW <= 4 && a.OC % 256 == 0 && a.IC % 64 == 0 && a.npix >= 131072) return 38;
         if (a.KW == 3 && a.IC == 128 && a.OC == 128) return 40;   // ECAPA's Res2Net group convs
+        if (a.KW == 3 && a.OC == 32 && a.IC % 32 == 0) return 60;     // CAM++'s gated linear_local
     }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
@@ -1746,6 +1775,10 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
                 "conv2d: gate needs gate_seg > 0 and enough segments for the output width");
         require(!d.y_time_major || !d.residual, "conv2d: a time-major store takes no residual");
         require(!d.res_f32 || (d.residual && !d.split), "conv2d: an f32 residual needs a residual and no split-f16");
+        require(!d.in_scale == !d.in_shift, "conv2d: in_scale and in_shift go together");
+        require(!d.in_scale || (d.KH == 1 && d.KW == 1 && d.pad_h == 0 && d.pad_w == 0 && !d.split &&
+                                aligned16(d.in_scale) && aligned16(d.in_shift)),
+                "conv2d: the input prologue needs a 1x1 conv without padding and 16-byte aligned vectors");
         require(!d.split || (!d.y_f32 && !d.y_time_major && d.x_lo >= d.IC && d.y_lo >= d.OC &&
                              (!d.residual || d.res_lo >= d.OC) && d.x_lo % 8 == 0 && d.y_lo % 8 == 0 &&
                              d.res_lo % 8 == 0 && d.IC % 32 == 0),
@@ -1776,6 +1809,8 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         a.x_lo = d.x_lo; a.r_lo = d.res_lo; a.y_lo = d.y_lo;
         a.res_f32 = d.res_f32 ? 1 : 0;
         a.res_after = d.res_after_act ? 1 : 0;
+        a.in_scale = d.in_scale;
+        a.in_shift = d.in_shift;
         a.npix = d.batch * Ho * Wo;
         a.npix_in = d.batch * d.H * d.W;
         hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1821,6 +1856,8 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.res = static_cast<const half_t*>(d.residual);
     a.res_f32 = d.res_f32 ? 1 : 0;
     a.res_after = d.res_after_act ? 1 : 0;
+    a.in_scale = d.in_scale;
+    a.in_shift = d.in_shift;
     a.gate = d.gate;
     a.post_scale = d.post_scale;
     a.act = d.act;

@@ -269,7 +269,7 @@ private:
         void* fcm[3] = {nullptr, nullptr, nullptr};
         void* fcm_t = nullptr;
         void* dense[3] = {nullptr, nullptr, nullptr};
-        void *abuf = nullptr, *cc = nullptr, *fin = nullptr;
+        void *cc = nullptr, *fin = nullptr;
         float *sums = nullptr, *gate = nullptr;
         // ERes2Net
         void *ex[2] = {nullptr, nullptr}, *es4 = nullptr, *esc = nullptr, *ez = nullptr, *ez2 = nullptr,

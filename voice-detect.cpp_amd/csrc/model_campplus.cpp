@@ -185,7 +185,6 @@ void Model::alloc_campplus_workspace(int batch, int T) {
         w.dense[b] = ws_alloc(2 * BTp * m.blocks[b].cmax);
         cmax = std::max(cmax, m.blocks[b].cmax);
     }
-    w.abuf = ws_alloc(2 * BTp * cmax);
     w.cc = ws_alloc(2 * BTp * m.bn_ch);
     w.fin = ws_alloc(2 * BTp * m.c_out);
     w.sums = static_cast<float*>(ws_alloc(4 * (size_t)batch * nseg * m.bn_ch));
@@ -263,8 +262,10 @@ void Model::encode_campplus(int batch, int T) {
 
     // TDNN k=5 s2 p2 -> ReLU into the first dense buffer (src/encoder_campplus.cpp:236-239)
     auto tconv = [&](const char* name, const Layer& l, const void* x, int xs, int W, int sw, int pad, int dil,
-                     const float* gate, int act, void* y, int ys) {
+                     const float* gate, int act, void* y, int ys, const float* in_scale = nullptr,
+                     const float* in_shift = nullptr) {
         vdk_conv_desc d{};
+        d.in_scale = in_scale; d.in_shift = in_shift;
         d.x = x; d.batch = batch; d.H = 1; d.W = W; d.IC = l.ic; d.x_stride = xs;
         d.w = l.w; d.OC = l.oc; d.KH = 1; d.KW = l.k;
         d.stride_h = 1; d.stride_w = sw; d.pad_w = pad; d.dil_w = dil;
@@ -280,10 +281,10 @@ void Model::encode_campplus(int batch, int T) {
         const CamBlock& blk = m.blocks[b];
         uint8_t* D = static_cast<uint8_t*>(w.dense[b]);
         for (const CamDense& d : blk.layers) {
-            prof_begin("campp_bn_relu", 0.0, 4.0 * rows * d.c_in);
-            check_rc(vdk_bn_act(D, blk.cmax, rows, d.c_in, d.bn_s, d.bn_t, VDK_ACT_RELU, w.abuf, d.c_in, stream_));
-            prof_end();
-            tconv("campp_linear1", d.l1, w.abuf, d.c_in, Tp, 1, 0, 1, nullptr, VDK_ACT_RELU, w.cc, m.bn_ch);
+            // nonlinear1 BN + ReLU (src/encoder_campplus.cpp:110-134) folded into
+            // linear1's operand loads
+            tconv("campp_linear1", d.l1, D, blk.cmax, Tp, 1, 0, 1, nullptr, VDK_ACT_RELU, w.cc, m.bn_ch, d.bn_s,
+                  d.bn_t);
             prof_begin("campp_seg_sums", 0.0, 2.0 * rows * m.bn_ch);
             check_rc(vdk_segment_sums(w.cc, m.bn_ch, batch, Tp, m.bn_ch, kCamSeg, w.sums, stream_));
             prof_end();
@@ -295,14 +296,9 @@ void Model::encode_campplus(int batch, int T) {
             tconv("campp_linear_local", d.local, w.cc, m.bn_ch, Tp, 1, blk.dil, blk.dil, w.gate, VDK_ACT_NONE,
                   D + 2 * (size_t)d.c_in, blk.cmax);
         }
-        prof_begin("campp_bn_relu", 0.0, 4.0 * rows * blk.cmax);
-        check_rc(vdk_bn_act(D, blk.cmax, rows, blk.cmax, blk.bn_s, blk.bn_t, VDK_ACT_RELU, w.abuf, blk.cmax,
-                            stream_));
-        prof_end();
         const bool last = b == 2;
-        tconv("campp_transit", blk.transit, w.abuf, blk.cmax, Tp, 1, 0, 1, nullptr,
-              last ? VDK_ACT_RELU : VDK_ACT_NONE, last ? w.fin : w.dense[b + 1],
-              last ? m.c_out : m.blocks[b + 1].cmax);
+        tconv("campp_transit", blk.transit, D, blk.cmax, Tp, 1, 0, 1, nullptr, last ? VDK_ACT_RELU : VDK_ACT_NONE,
+              last ? w.fin : w.dense[b + 1], last ? m.c_out : m.blocks[b + 1].cmax, blk.bn_s, blk.bn_t);
     }
 
     // stats pooling: mean + unbiased std, no eps (src/encoder_campplus.cpp:284-296)

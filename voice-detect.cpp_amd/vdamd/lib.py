@@ -43,7 +43,8 @@ class ConvDesc(C.Structure):
                 ("tanh_after", C.c_int),
                 ("y", _vp), ("y_stride", C.c_int), ("y_f32", C.c_int), ("y_time_major", C.c_int),
                 ("split", C.c_int), ("x_lo", C.c_int), ("res_lo", C.c_int), ("y_lo", C.c_int),
-                ("tile", C.c_int), ("res_f32", C.c_int), ("res_after_act", C.c_int), ("out_w", C.c_int)]
+                ("tile", C.c_int), ("res_f32", C.c_int), ("res_after_act", C.c_int), ("out_w", C.c_int),
+                ("in_scale", _vp), ("in_shift", _vp)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
