@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void bn_act_kernel(const half_t* __restrict__ 
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         float f = (float)v[e] * sc[e] + sh[e];
-        if (act == VDK_ACT_RELU) f = f > 0.0f ? f : 0.0f;
+        if (act == VDK_ACT_RELU) f = fmaxf(f, 0.0f);
         o[e] = (half_t)f;
     }
     *reinterpret_cast<half8*>(y + r * ys + c) = o;
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void cam_context_kernel(const float* __restric
         const double a1 = __shfl_down(a, 1, 4), a2 = __shfl_down(a, 2, 4), a3 = __shfl_down(a, 3, 4);
         if (q == 0) {
             const float v = (float)((a + a1) + (a2 + a3)) + (b1 ? b1[o] : 0.0f);
-            hid[o] = v > 0.0f ? v : 0.0f;
+            hid[o] = fmaxf(v, 0.0f);
         }
     }
     __syncthreads();

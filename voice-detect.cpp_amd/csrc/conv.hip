@@ -92,10 +92,10 @@ __device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float*
     if (a.res && !a.res_after) add_residual(a, P, oc, v);
     if (a.act == VDK_ACT_RELU) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = v[e] > 0.0f ? v[e] : 0.0f;
+        for (int e = 0; e < 8; ++e) v[e] = fmaxf(v[e], 0.0f);
         if (a.clamp_hi > 0.0f) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = v[e] < a.clamp_hi ? v[e] : a.clamp_hi;
+            for (int e = 0; e < 8; ++e) v[e] = fminf(v[e], a.clamp_hi);
         }
     } else if (a.act == VDK_ACT_SIGMOID) {
 #pragma unroll
@@ -847,8 +847,7 @@ __device__ __forceinline__ void resblock_tile(const uint8_t* __restrict__ sx, ui
             half4 h;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                float v = acc1[q][g * 4 + e] + bb[e];
-                v = v > 0.0f ? v : 0.0f;
+                const float v = fmaxf(acc1[q][g * 4 + e] + bb[e], 0.0f);
                 h[e] = inside ? (half_t)v : (half_t)0.0f;
             }
             *reinterpret_cast<half4*>(trow + g * 16) = h;
@@ -886,7 +885,7 @@ __device__ __forceinline__ void resblock_tile(const uint8_t* __restrict__ sx, ui
             for (int e = 0; e < 4; ++e) {
                 const float v = acc2[q][g * 4 + e] + bb[e];
                 const float o = v + (float)r[e];
-                h[e] = (half_t)(o > 0.0f ? o : 0.0f);
+                h[e] = (half_t)fmaxf(o, 0.0f);
             }
             *reinterpret_cast<half4*>(srow + g * 16) = h;
         }
@@ -1117,7 +1116,7 @@ __device__ __forceinline__ void rw_tile(const uint8_t* __restrict__ sx, uint8_t*
             }
             half4 h;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = (half_t)(a.act == VDK_ACT_RELU ? (v[e] > 0.0f ? v[e] : 0.0f) : v[e]);
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)(a.act == VDK_ACT_RELU ? fmaxf(v[e], 0.0f) : v[e]);
             *reinterpret_cast<half4*>(sstage + lrow * 64 + swz<32>(lrow, g) * 16 + lhalf * 8) = h;
         }
         const int oh = oh0 + i;
@@ -1475,19 +1474,20 @@ __global__ __launch_bounds__(512) void conv3x3_band_kernel(ConvArgs a) {
         pr = pr < npx ? pr : npx - 1;
         const uint8_t* const rrow = sres + pr * G::RRB + (mb * 32 + lhalf * 4) * 2;
         uint8_t* const srow = sstg + lrow * 64 + lhalf * 8;
+        // the block's 4 residual reads go out together (zero without a residual)
+        half4 r4[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            float v[4];
+            r4[g] = has_res ? *reinterpret_cast<const half4*>(rrow + g * 16) : half4{};
+        }
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[j][g * 4 + e] + bias[g * 4 + e];
-            if (has_res) {
-                const half4 r4 = *reinterpret_cast<const half4*>(rrow + g * 16);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] += (float)r4[e];
-            }
+        for (int g = 0; g < 4; ++g) {
             half4 h;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = (half_t)(relu ? (v[e] > 0.0f ? v[e] : 0.0f) : v[e]);
+            for (int e = 0; e < 4; ++e) {
+                const float v = acc[j][g * 4 + e] + bias[g * 4 + e] + (float)r4[g][e];
+                h[e] = (half_t)(relu ? fmaxf(v, 0.0f) : v);
+            }
             *reinterpret_cast<half4*>(srow + (swz<32>(lrow, g) * 16)) = h;
         }
 #pragma unroll
@@ -1721,7 +1721,7 @@ __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restri
 #pragma unroll
         for (int k = 0; k < 9; ++k) acc += sw[oc * 9 + k] * xv[k];
         float v = acc + sb[oc];
-        if (relu) v = v > 0.0f ? v : 0.0f;
+        if (relu) v = fmaxf(v, 0.0f);
         hv[e] = (half_t)v;
         lv[e] = (half_t)(v - (float)hv[e]);
     }
