@@ -9,10 +9,12 @@
 //            channels are permuted from the reference's c*H + h at load).
 //   backbone time-major f16 [B][T'][C]; each dense block keeps one buffer wide
 //            enough for its final width, every layer appending its growth
-//            channels in place (the reference's concat).  Per layer: BN+ReLU
-//            (bn_act) -> linear1 1x1 (+ReLU) -> segment sums -> context MLP
-//            (one gate per clip and 100-frame segment) -> linear_local k=3
-//            dilated conv with the gate applied in its epilogue.
+//            channels in place (the reference's concat).  Per layer: linear1
+//            1x1 (+ReLU) with the layer's BN+ReLU applied to its operand as it
+//            is fetched (the normalised map is never stored) -> segment sums
+//            -> context MLP (one gate per clip and 100-frame segment) ->
+//            linear_local k=3 dilated conv with the gate applied in its
+//            epilogue.  The transit convs fold their BN+ReLU the same way.
 //   head     stats pooling (mean, unbiased std, no eps) -> dense 1x1 with the
 //            affine-free BatchNorm folded in -> L2.
 // Weights: conv weights f16 [OC][KH][KW][IC] (Q8_0 / F16 / F32 dequantised at
