@@ -17,6 +17,7 @@
 // stem_conv3x3_kernel: the IC=1 stem (K = 9 is too short for MFMA); one
 // thread per output pixel computes all OC channels in f32 from f32 features.
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 #include "devmath.hpp"
@@ -209,7 +210,11 @@ __device__ __forceinline__ void stage_epilogue_impl(const ConvArgs& a, uint8_t* 
     }
 }
 
-template <int BM, int BN, int WM, int WN, int KC>
+constexpr uint32_t kOOB = 0x80000000u;   // any offset >= num_records reads as zero
+
+// PRO: the input prologue relu(x * in_scale + in_shift) (its scale / shift
+// registers exist only in these instantiations).
+template <int BM, int BN, int WM, int WN, int KC, bool PRO>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(ConvArgs a) {
     constexpr int NWM = BM / WM, NWN = BN / WN, NT = NWM * NWN * 64;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -253,57 +258,76 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         x_lds[i] = r * LDK + c8 * 8;
         x_c[i] = c8 * 8;
     }
-    const half_t* w_src[WCH];
+    uint32_t w_off[WCH];   // byte offset of the slot's weight row at chunk 0 (kOOB: no such row)
     int w_lds[WCH];
-    bool w_on[WCH], w_ok[WCH];   // slot is part of the tile / its weight row exists (oc < OC)
+    bool w_on[WCH];        // slot is part of the tile
 #pragma unroll
     for (int i = 0; i < WCH; ++i) {
         const int q = tid + i * NT;
         const int r = q / CPR, c8 = q - r * CPR;
         w_on[i] = q < BM * CPR;
-        w_ok[i] = w_on[i] && oc0 + r < a.OC;
-        w_src[i] = a.w + (size_t)(oc0 + (w_ok[i] ? r : 0)) * KHW * a.IC + c8 * 8;
+        w_off[i] = w_on[i] && oc0 + r < a.OC ? (uint32_t)(((size_t)(oc0 + r) * KHW * a.IC + c8 * 8) * 2) : kOOB;
         w_lds[i] = r * LDK + c8 * 8;
     }
+    // buffer loads: a masked lane reads an out-of-range offset (zero), so every
+    // fetch issues the same number of loads and the waits below count exactly
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)((size_t)a.OC * KHW * a.IC * 2), 0x00020000);
 
-    const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-    half8 xr[XCH], wr[WCH];
-    auto fetch = [&](int k) {
+    // With the prologue (long-K 1x1 GEMMs) two register slots: chunk k+2 is
+    // loaded while chunk k feeds the MFMAs and chunk k+1 waits in the other
+    // slot for its turn in LDS, so two chunks of loads are in flight across
+    // every barrier; the loop is unrolled by two so each slot is a fixed set
+    // of registers.  Otherwise one slot (chunk k+1 in flight), which keeps
+    // the register count, and so the residency, of the short-K convs.
+    half8 xr[2][XCH], wr[2][WCH];
+    constexpr int XP = PRO ? XCH : 1;
+    float4v isc[2][XP][2], ish[2][XP][2];   // input prologue scale / shift of the slot's channels
+    auto fetch = [&](int k, auto slot) {
+        constexpr int s = decltype(slot)::value;
         const int tap = k / nc, c0 = (k - tap * nc) * KC;
         const int kh = tap / a.KW, kw = tap - kh * a.KW;
+        const uint32_t wd = (uint32_t)((tap * a.IC + c0) * 2);
 #pragma unroll
-        for (int i = 0; i < WCH; ++i)
-            wr[i] = w_ok[i] ? *reinterpret_cast<const half8*>(w_src[i] + (size_t)tap * a.IC + c0) : zero8;
+        for (int i = 0; i < WCH; ++i) {
+            const uint32_t off = w_off[i] == kOOB ? kOOB : w_off[i] + wd;
+            wr[s][i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+        }
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
             const int ih = x_ih[i] + kh * a.dh, iw = x_iw[i] + kw * a.dw;
-            xr[i] = zero8;
-            if (x_on[i] && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
-            {
-                xr[i] = *reinterpret_cast<const half8*>(a.x + ((size_t)(x_img[i] + ih) * a.W + iw) * a.xs + c0 +
-                                                        x_c[i]);
-                if (a.in_scale) {   // BatchNorm + ReLU of the input channels, as the f16 operand
-                    const int cc = c0 + x_c[i];
-                    const float4v s0 = *reinterpret_cast<const float4v*>(a.in_scale + cc);
-                    const float4v s1 = *reinterpret_cast<const float4v*>(a.in_scale + cc + 4);
-                    const float4v t0 = *reinterpret_cast<const float4v*>(a.in_shift + cc);
-                    const float4v t1 = *reinterpret_cast<const float4v*>(a.in_shift + cc + 4);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        xr[i][e] = (half_t)fmaxf((float)xr[i][e] * s0[e] + t0[e], 0.0f);
-                        xr[i][e + 4] = (half_t)fmaxf((float)xr[i][e + 4] * s1[e] + t1[e], 0.0f);
-                    }
-                }
+            const bool in = x_on[i] && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+            const uint32_t off =
+                in ? (uint32_t)((((size_t)(x_img[i] + ih) * a.W + iw) * a.xs + c0 + x_c[i]) * 2) : kOOB;
+            xr[s][i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+            if constexpr (PRO) {   // 1x1 unpadded only (conv_impl): every fetched value is a real input
+                const int cc = c0 + x_c[i];
+                isc[s][i][0] = *reinterpret_cast<const float4v*>(a.in_scale + cc);
+                isc[s][i][1] = *reinterpret_cast<const float4v*>(a.in_scale + cc + 4);
+                ish[s][i][0] = *reinterpret_cast<const float4v*>(a.in_shift + cc);
+                ish[s][i][1] = *reinterpret_cast<const float4v*>(a.in_shift + cc + 4);
             }
         }
     };
-    auto stash = [&](int st) {
+    auto stash = [&](int st, auto slot) {
+        constexpr int s = decltype(slot)::value;
 #pragma unroll
         for (int i = 0; i < WCH; ++i)
-            if (w_on[i]) *reinterpret_cast<half8*>(&sW[st][w_lds[i]]) = wr[i];
+            if (w_on[i]) *reinterpret_cast<half8*>(&sW[st][w_lds[i]]) = wr[s][i];
 #pragma unroll
-        for (int i = 0; i < XCH; ++i)
-            if (x_row[i]) *reinterpret_cast<half8*>(&sX[st][x_lds[i]]) = xr[i];
+        for (int i = 0; i < XCH; ++i) {
+            half8 v = xr[s][i];
+            if constexpr (PRO) {   // BatchNorm + ReLU of the input channels, as the f16 operand
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = (half_t)fmaxf((float)v[e] * isc[s][i][0][e] + ish[s][i][0][e], 0.0f);
+                    v[e + 4] = (half_t)fmaxf((float)v[e + 4] * isc[s][i][1][e] + ish[s][i][1][e], 0.0f);
+                }
+            }
+            if (x_row[i]) *reinterpret_cast<half8*>(&sX[st][x_lds[i]]) = v;
+        }
     };
 
     float16v acc[TM][TN];
@@ -314,12 +338,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    for (int k = 0; k < nk; ++k) {
-        const int st = k & 1;
-        if (k + 1 < nk) fetch(k + 1);     // global loads in flight during this chunk's MFMAs
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    auto mfma_chunk = [&](int st) {
 #pragma unroll
         for (int kk = 0; kk < KC / 16; ++kk) {
             half8 af[TM], bf[TN];
@@ -336,8 +357,38 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        if (k + 1 < nk) stash(st ^ 1);
+    };
+    if constexpr (PRO) {
+        // chunk k sits in LDS stage k&1 (and arrived through register slot k&1)
+        auto step = [&](int k, auto slot) {
+            constexpr int s = decltype(slot)::value;
+            // slot s was stashed for chunk k one step ago; past the end the last
+            // chunk is fetched again (unused) to keep the load count fixed
+            fetch(k + 2 < nk ? k + 2 : nk - 1, slot);
+            mfma_chunk(s);
+            if (k + 1 < nk) stash(s ^ 1, std::integral_constant<int, s ^ 1>());
+            __syncthreads();
+        };
+        fetch(0, S0());
+        fetch(nk > 1 ? 1 : 0, S1());
+        stash(0, S0());
         __syncthreads();
+        for (int k = 0; k < nk; k += 2) {
+            step(k, S0());
+            if (k + 1 >= nk) break;
+            step(k + 1, S1());
+        }
+    } else {
+        fetch(0, S0());
+        stash(0, S0());
+        __syncthreads();
+        for (int k = 0; k < nk; ++k) {
+            const int st = k & 1;
+            if (k + 1 < nk) fetch(k + 1, S0());   // global loads in flight during this chunk's MFMAs
+            mfma_chunk(st);
+            if (k + 1 < nk) stash(st ^ 1, S0());
+            __syncthreads();
+        }
     }
 
     stage_epilogue_impl<BM, BN, WN, SMEM, NT, TM, TN>(a, smem, acc, wm * WM, wn * WN, p0, oc0, tid, lane);
@@ -359,7 +410,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr uint32_t kOOB = 0x80000000u;   // any offset >= num_records reads as zero
 
 template <int KC>
 __device__ __forceinline__ int swz(int r, int c) {
@@ -1511,7 +1561,10 @@ template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
     dim3 grid(cdiv(a.npix, BN), cdiv(a.OC, BM));
-    hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC>), grid, dim3(NT), 0, s, a);
+    if (a.in_scale)
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, true>), grid, dim3(NT), 0, s, a);
+    else
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, false>), grid, dim3(NT), 0, s, a);
 }
 
 struct TileCfg {
