@@ -43,11 +43,13 @@ __global__ __launch_bounds__(256) void bn_act_kernel(const half_t* __restrict__ 
     *reinterpret_cast<half8*>(y + r * ys + c) = o;
 }
 
-// Workgroup (b, s, 64-channel group): 4 lanes of 64 channels split the frames
-// of segment s; the 4 partial sums are added in a fixed order.
-__global__ __launch_bounds__(256) void segment_sums_kernel(const half_t* __restrict__ x, int xs, int T, int C,
-                                                           int seg, float* __restrict__ out) {
-    __shared__ double part[4][64];
+// Workgroup (b, s, 64-channel group): 16 waves split the frames of segment s
+// (frame t to wave t mod 16, a handful of loads each, all in flight at once);
+// the 16 partial sums are added in a fixed order.
+constexpr int kSegParts = 16;
+__global__ __launch_bounds__(64 * kSegParts) void segment_sums_kernel(const half_t* __restrict__ x, int xs, int T,
+                                                                      int C, int seg, float* __restrict__ out) {
+    __shared__ double part[kSegParts][64];
     const int b = blockIdx.x, s = blockIdx.y, c0 = blockIdx.z * 64;
     const int nseg = gridDim.y;
     const int lane_c = threadIdx.x & 63, lane_t = threadIdx.x >> 6;
@@ -57,14 +59,40 @@ __global__ __launch_bounds__(256) void segment_sums_kernel(const half_t* __restr
     if (c < C) {
         const half_t* p = x + (size_t)b * T * xs + c;
 #pragma unroll 8
-        for (int t = t0 + lane_t; t < t1; t += 4) acc += (double)(float)p[(size_t)t * xs];
+        for (int t = t0 + lane_t; t < t1; t += kSegParts) acc += (double)(float)p[(size_t)t * xs];
     }
     part[lane_t][lane_c] = acc;
     __syncthreads();
     if (lane_t == 0 && c < C) {
-        const double v = ((part[0][lane_c] + part[1][lane_c]) + part[2][lane_c]) + part[3][lane_c];
+        double v = 0.0;
+#pragma unroll
+        for (int q = 0; q < kSegParts; ++q) v += part[q][lane_c];
         out[((size_t)b * nseg + s) * C + c] = (float)v;
     }
+}
+
+// Dot product of a weight row with an LDS vector, split over 4 lanes: lane q
+// takes the q-th contiguous quarter (16-byte loads, all issued together when
+// n % 16 == 0), else every 4th element; lane 0 adds the 4 partial sums in a
+// fixed order.
+__device__ __forceinline__ double dot4(const float* __restrict__ wr, const float* v, int n, int q) {
+    double a = 0.0;
+    if ((n & 15) == 0) {
+        const int len = n >> 2;
+        const float4v* w4 = reinterpret_cast<const float4v*>(wr + q * len);
+        const float4v* v4 = reinterpret_cast<const float4v*>(v + q * len);
+#pragma unroll 8
+        for (int i = 0; i < (len >> 2); ++i) {
+            const float4v wv = w4[i], xv = v4[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a += (double)wv[e] * (double)xv[e];
+        }
+    } else {
+#pragma unroll 4
+        for (int c = q; c < n; c += 4) a += (double)wr[c] * (double)v[c];
+    }
+    const double a1 = __shfl_down(a, 1, 4), a2 = __shfl_down(a, 2, 4), a3 = __shfl_down(a, 3, 4);
+    return (a + a1) + (a2 + a3);
 }
 
 // One workgroup per (clip, segment): ctx = mean_T' + sum_seg / seg_len, then
@@ -77,7 +105,7 @@ __global__ __launch_bounds__(256) void cam_context_kernel(const float* __restric
                                                           float* __restrict__ gate) {
     extern __shared__ float sm[];
     float* ctx = sm;          // [C]
-    float* hid = sm + C;      // [H1]
+    float* hid = sm + ((C + 3) & ~3);   // [H1], 16-byte aligned
     const int b = blockIdx.x, s = blockIdx.y;
     const float* sb = sums + (size_t)b * nseg * C;
     for (int c = threadIdx.x; c < C; c += blockDim.x) {
@@ -86,31 +114,16 @@ __global__ __launch_bounds__(256) void cam_context_kernel(const float* __restric
         ctx[c] = (float)(tot / T) + (float)((double)sb[(size_t)s * C + c] / seg);
     }
     __syncthreads();
-    // each output's dot product split over 4 lanes (k = q, q+4, ...), the
-    // 4 partial sums added in a fixed order by lane q = 0
+    // each output's dot product split over 4 lanes (dot4)
     const int q = threadIdx.x & 3;
     for (int o = threadIdx.x >> 2; o < H1; o += blockDim.x >> 2) {
-        const float* wr = w1 + (size_t)o * C;
-        double a = 0.0;
-#pragma unroll 4
-        for (int c = q; c < C; c += 4) a += (double)wr[c] * (double)ctx[c];
-        const double a1 = __shfl_down(a, 1, 4), a2 = __shfl_down(a, 2, 4), a3 = __shfl_down(a, 3, 4);
-        if (q == 0) {
-            const float v = (float)((a + a1) + (a2 + a3)) + (b1 ? b1[o] : 0.0f);
-            hid[o] = fmaxf(v, 0.0f);
-        }
+        const double a = dot4(w1 + (size_t)o * C, ctx, C, q);
+        if (q == 0) hid[o] = fmaxf((float)a + (b1 ? b1[o] : 0.0f), 0.0f);
     }
     __syncthreads();
     for (int o = threadIdx.x >> 2; o < G; o += blockDim.x >> 2) {
-        const float* wr = w2 + (size_t)o * H1;
-        double a = 0.0;
-#pragma unroll 4
-        for (int c = q; c < H1; c += 4) a += (double)wr[c] * (double)hid[c];
-        const double a1 = __shfl_down(a, 1, 4), a2 = __shfl_down(a, 2, 4), a3 = __shfl_down(a, 3, 4);
-        if (q == 0) {
-            const float v = (float)((a + a1) + (a2 + a3)) + (b2 ? b2[o] : 0.0f);
-            gate[((size_t)b * nseg + s) * G + o] = 1.0f / (1.0f + expf(-v));
-        }
+        const double a = dot4(w2 + (size_t)o * H1, hid, H1, q);
+        if (q == 0) gate[((size_t)b * nseg + s) * G + o] = 1.0f / (1.0f + expf(-((float)a + (b2 ? b2[o] : 0.0f))));
     }
 }
 
@@ -143,7 +156,7 @@ extern "C" int vdk_segment_sums(const void* d_x, int x_stride, int batch, int T,
         require(d_x && d_out, "segment_sums: NULL device pointer");
         require(batch > 0 && T > 0 && C > 0 && seg > 0 && x_stride >= C, "segment_sums: bad shape");
         const int nseg = (T + seg - 1) / seg;
-        hipLaunchKernelGGL(segment_sums_kernel, dim3(batch, nseg, cdiv(C, 64)), dim3(256), 0,
+        hipLaunchKernelGGL(segment_sums_kernel, dim3(batch, nseg, cdiv(C, 64)), dim3(64 * kSegParts), 0,
                            static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, seg,
                            d_out);
         VDK_HIP(hipGetLastError());
@@ -157,8 +170,9 @@ extern "C" int vdk_cam_context(const float* d_sums, int batch, int T, int C, int
         require(d_sums && d_w1 && d_w2 && d_gate, "cam_context: NULL device pointer");
         require(batch > 0 && T > 0 && C > 0 && seg > 0 && H1 > 0 && G > 0 && C + H1 <= 16384,
                 "cam_context: bad shape");
+        require(al16(d_w1) && al16(d_w2), "cam_context: weights must be 16-byte aligned");
         const int nseg = (T + seg - 1) / seg;
-        hipLaunchKernelGGL(cam_context_kernel, dim3(batch, nseg), dim3(256), sizeof(float) * (C + H1),
+        hipLaunchKernelGGL(cam_context_kernel, dim3(batch, nseg), dim3(256), sizeof(float) * (((C + 3) & ~3) + H1),
                            static_cast<hipStream_t>(stream), d_sums, nseg, T, C, seg, d_w1, d_b1, H1, d_w2, d_b2,
                            G, d_gate);
         VDK_HIP(hipGetLastError());
