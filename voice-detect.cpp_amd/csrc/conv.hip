@@ -1728,7 +1728,9 @@ int pick_tile(const ConvArgs& a) {
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
     if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[58], a)) return 58;
-    if (!a.split && !is_s1_3x3(a) && a.IC == 32 && a.OC == 64) return 2;
+    // ResNet's stride-2 32->64 pair (random-data sweep): the 1x1 on the 64x64
+    // register-staged tile, the 3x3 on the 64x128 one
+    if (!a.split && !is_s1_3x3(a) && a.IC == 32 && a.OC == 64) return a.KH * a.KW == 1 ? 63 : 2;
     if (!a.split && is_s1_3x3(a) && a.IC % 32 == 0 && a.IC <= 64 && a.OC <= 64) return 28;
     if (a.IC % 32 == 0 && a.OC == 128) return 39;   // 128x128 tile, KC = 32
     if (a.IC % 64 == 0) return bm == 128 ? 18 : (bm == 64 ? 15 : 14);
