@@ -67,34 +67,82 @@ __global__ __launch_bounds__(256) void tstp_kernel(const half_t* __restrict__ x,
 }
 
 // FC, split over the input dimension: workgroup (o-tile, b-tile, split s)
-// computes a 32x32 block of partial dot products over its slice of the input
-// from LDS-staged tiles; linear_reduce_kernel adds the slices in a fixed order
-// (bitwise reproducible) with bias and mean_vec.
-constexpr int kLinTile = 16, kLinK = 64;
+// computes a (16 RB) x (16 RB) block of partial dot products over its slice
+// of the input, RB x RB per thread from k-major LDS tiles (RB = 4: one
+// 16-byte read of 4 batch rows and one of 4 outputs per 16 FMAs; RB = 1 for
+// small products, where 64-wide tiles would leave too few workgroups); every
+// output accumulates its slice in k order, so the result does not depend on
+// the tiling.  linear_reduce_kernel adds the slices in a fixed order (bitwise
+// reproducible) with bias and mean_vec.
+constexpr int kLinK = 64, kLinSlice = 128;
 
+template <int RB>
 __global__ __launch_bounds__(256) void linear_partial_kernel(const float* __restrict__ x, int B, int in_dim,
                                                              const float* __restrict__ w, int out_dim, int slice,
-                                                             float* __restrict__ part) {
-    __shared__ float sx[kLinTile][kLinK + 1];
-    __shared__ float sw[kLinTile][kLinK + 1];
-    const int o0 = blockIdx.x * kLinTile, b0 = blockIdx.y * kLinTile, s = blockIdx.z;
+                                                             int vec4, float* __restrict__ part) {
+    constexpr int TILE = 16 * RB, NQ = TILE * (kLinK / 4) / 256;   // 4-k groups per thread per operand
+    __shared__ __attribute__((aligned(16))) float sx[kLinK][TILE + 4];   // [k][batch row]
+    __shared__ __attribute__((aligned(16))) float sw[kLinK][TILE + 4];   // [k][output]
+    const int o0 = blockIdx.x * TILE, b0 = blockIdx.y * TILE, s = blockIdx.z;
     const int k_begin = s * slice, k_end = min(in_dim, k_begin + slice);
     const int tid = threadIdx.x;
-    const int tb = tid / kLinTile, to = tid % kLinTile;   // one output (b0+tb, o0+to) per thread
-    float acc = 0.0f;
+    const int tb = tid >> 4, to = tid & 15;   // batch rows b0 + RB tb .., outputs o0 + RB to ..
+    float acc[RB][RB];
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int j = 0; j < RB; ++j) acc[i][j] = 0.0f;
     for (int k0 = k_begin; k0 < k_end; k0 += kLinK) {
-        for (int e = tid; e < kLinTile * kLinK; e += 256) {
-            const int r = e / kLinK, c = e % kLinK, k = k0 + c;
-            sx[r][c] = (b0 + r < B && k < k_end) ? x[(size_t)(b0 + r) * in_dim + k] : 0.0f;
-            sw[r][c] = (o0 + r < out_dim && k < k_end) ? w[(size_t)(o0 + r) * in_dim + k] : 0.0f;
+        // TILE rows x 64 k of each operand in groups of 4 consecutive k
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int e = tid + q * 256, r = e >> 4, c = (e & 15) * 4, k = k0 + c;
+            float xv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, wv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            const float* xp = x + (size_t)(b0 + r) * in_dim + k;
+            const float* wp = w + (size_t)(o0 + r) * in_dim + k;
+            const bool xr = b0 + r < B, wr = o0 + r < out_dim;
+            if (vec4 && k + 3 < k_end) {
+                if (xr) { const float4v v = *reinterpret_cast<const float4v*>(xp); xv[0] = v[0]; xv[1] = v[1]; xv[2] = v[2]; xv[3] = v[3]; }
+                if (wr) { const float4v v = *reinterpret_cast<const float4v*>(wp); wv[0] = v[0]; wv[1] = v[1]; wv[2] = v[2]; wv[3] = v[3]; }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (xr && k + i < k_end) xv[i] = xp[i];
+                    if (wr && k + i < k_end) wv[i] = wp[i];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sx[c + i][r] = xv[i];
+                sw[c + i][r] = wv[i];
+            }
         }
         __syncthreads();
-#pragma unroll 16
-        for (int c = 0; c < kLinK; ++c) acc += sx[tb][c] * sw[to][c];
+#pragma unroll 8
+        for (int kk = 0; kk < kLinK; ++kk) {
+            if constexpr (RB == 4) {
+                const float4v xb = *reinterpret_cast<const float4v*>(&sx[kk][tb * 4]);
+                const float4v wo = *reinterpret_cast<const float4v*>(&sw[kk][to * 4]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] += xb[i] * wo[j];
+            } else {
+                acc[0][0] += sx[kk][tb] * sw[kk][to];
+            }
+        }
         __syncthreads();
     }
-    const int b = b0 + tb, o = o0 + to;
-    if (b < B && o < out_dim) part[((size_t)s * B + b) * out_dim + o] = acc;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+        const int b = b0 + tb * RB + i;
+        if (b >= B) continue;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int o = o0 + to * RB + j;
+            if (o < out_dim) part[((size_t)s * B + b) * out_dim + o] = acc[i][j];
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restrict__ part, int nsplit, int B,
@@ -126,7 +174,7 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restr
 }
 
 int linear_splits(int in_dim) {
-    const int want = (in_dim + 255) / 256;              // ~256 inputs per slice
+    const int want = (in_dim + kLinSlice - 1) / kLinSlice;   // ~128 inputs per slice
     return want < 1 ? 1 : (want > 64 ? 64 : want);
 }
 
@@ -184,8 +232,14 @@ extern "C" int vdk_linear_ex(const float* d_x, int batch, int in_dim, const floa
         const int nsplit = (in_dim + slice - 1) / slice;
         hipStream_t s = static_cast<hipStream_t>(stream);
         float* part = static_cast<float*>(d_work);
-        hipLaunchKernelGGL(linear_partial_kernel, dim3(cdiv(out_dim, kLinTile), cdiv(batch, kLinTile), nsplit),
-                           dim3(256), 0, s, d_x, batch, in_dim, d_w, out_dim, slice, part);
+        const int vec4 = in_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(d_w) & 15) == 0;
+        if ((long)cdiv(out_dim, 64) * cdiv(batch, 64) * nsplit >= 64)
+            hipLaunchKernelGGL(linear_partial_kernel<4>, dim3(cdiv(out_dim, 64), cdiv(batch, 64), nsplit), dim3(256),
+                               0, s, d_x, batch, in_dim, d_w, out_dim, slice, vec4, part);
+        else
+            hipLaunchKernelGGL(linear_partial_kernel<1>, dim3(cdiv(out_dim, 16), cdiv(batch, 16), nsplit), dim3(256),
+                               0, s, d_x, batch, in_dim, d_w, out_dim, slice, vec4, part);
         VDK_HIP(hipGetLastError());
         hipLaunchKernelGGL(linear_reduce_kernel, dim3(cdiv((long)batch * out_dim, 256)), dim3(256), 0, s, part,
                            nsplit, batch, out_dim, d_bias, d_mean_vec, act, d_y);
