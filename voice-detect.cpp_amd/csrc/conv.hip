@@ -1718,10 +1718,16 @@ int pick_tile(const ConvArgs& a) {
         // kernels (a 128-tap positional conv) on the 128x32 tile, wide 1x1
         // GEMMs on the 128x256 8-wave tile (768 outputs: the 256x128 one),
         // the big strided feature convs on the 256x256 tile
+        // (re-checked with random data: zeros draw less MFMA power and run
+        // at higher clocks, which had favoured some tiles)
         if (a.KW > 32 && a.IC % 64 == 0) return 52;
+        if (a.KW == 1 && a.IC == 768 && a.OC == 768 && tile_fits(kTiles[40], a)) return 40;
         if (a.KW == 1 && a.IC >= 512 && a.OC == 768 && a.IC % 64 == 0) return 34;
+        if (a.KW == 1 && a.IC >= 2048 && a.OC >= 1536 && a.OC % 256 == 0 && a.IC % 64 == 0) return 38;
         if (a.KW == 1 && a.IC >= 512 && a.OC >= 512 && a.OC % 128 == 0 && a.IC % 32 == 0) return 36;
         if (a.KW <= 4 && a.OC % 256 == 0 && a.IC % 64 == 0 && a.npix >= 131072) return 38;
+        if (a.KW <= 4 && a.OC % 256 == 0 && a.IC % 64 == 0 && a.npix >= 32768 && tile_fits(kTiles[40], a))
+            return 40;
         if (a.KW == 3 && a.IC == 128 && a.OC == 128) return 40;   // ECAPA's Res2Net group convs
         if (a.KW == 3 && a.OC == 32 && a.IC % 32 == 0) return 60;     // CAM++'s gated linear_local
     }
