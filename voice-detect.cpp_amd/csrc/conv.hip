@@ -1665,18 +1665,21 @@ bool plain_epilogue(const ConvArgs& a) {
            a.ys == a.OC && (!a.res || a.rs == a.OC) && !a.res_f32 && !a.res_after;
 }
 
+// The register-staged (igemm) entries: 0-13 and 62-63.
+bool igemm_tile(int idx) { return idx < kFirstDma || idx == 62 || idx == 63; }
+
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
     // the input prologue lives in the register-staged kernel's operand loads
-    if (a.in_scale && !(idx < kFirstDma || idx >= 62)) return false;
+    if (a.in_scale && !igemm_tile(idx)) return false;
     // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
     // the in-image tap range for a single row of taps; longer 2-D kernels
     // take the register-staged kernel
     if (a.KH * a.KW > 32 && a.KH != 1 && idx >= kFirstDma) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
     if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % t.bm == 0 && a.IC % 16 == 0;
-    if (a.split && (idx < kFirstDma || (idx >= kFirstHalo && idx < kFirstDma8) || idx >= 62))
+    if (a.split && (igemm_tile(idx) || (idx >= kFirstHalo && idx < kFirstDma8) || idx >= 62))
         return false;   // split: DMA only
     return a.IC % t.kc == 0;
 }
