@@ -296,6 +296,40 @@ def test_tstp_linear_l2_match_oracle():
     assert np.array_equal(z.to_array(np.float32, (2, 8)), np.zeros((2, 8), np.float32))
 
 
+@pytest.mark.parametrize("case", [(1, 3, 5, 0), (70, 130, 33, 1), (130, 5120, 200, 2), (64, 1024, 1024, 5),
+                                  (64, 128, 1024, 2), (3, 769, 64, 0)])
+def test_linear_shapes_and_batch_invariance(case):
+    """y = act(W x + b - mv) against numpy f64 over ragged shapes: K not a
+    multiple of 4 (scalar loads), several batch tiles, output counts off the
+    tile grid, both per-thread blockings; each clip's row is bitwise the
+    same computed alone (every output sums its slice in k order)."""
+    L = lib.lib()
+    B, I, E, act = case
+    rng = np.random.default_rng(B * 1000 + I + E)
+    x = rng.standard_normal((B, I)).astype(np.float32)
+    w = (rng.standard_normal((E, I)) / np.sqrt(I)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(E)).astype(np.float32)
+    mv = (0.05 * rng.standard_normal(E)).astype(np.float32)
+    dx, dw, db, dm = (lib.DeviceBuffer.from_array(a) for a in (x, w, b, mv))
+    dy = lib.DeviceBuffer(B * E * 4)
+    wsz = L.vdk_linear_workspace_size(B, I, E)
+    dwk = lib.DeviceBuffer(wsz)
+    announce(f"linear {case}")
+    lib.check(L.vdk_linear_ex(dx.ptr, B, I, dw.ptr, db.ptr, dm.ptr, E, act, dy.ptr, dwk.ptr, wsz, None))
+    lib.check(L.vdk_synchronize())
+    got = dy.to_array(np.float32, (B, E))
+    ref = x.astype(np.float64) @ w.astype(np.float64).T + b - mv
+    ref = {0: ref, 1: np.maximum(ref, 0), 2: 1 / (1 + np.exp(-ref)), 5: np.tanh(ref)}[act]   # VDK_ACT_* codes
+    np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-5)
+    for c in sorted({0, B // 2, B - 1}):
+        d1 = lib.DeviceBuffer.from_array(x[c:c + 1])
+        w1 = L.vdk_linear_workspace_size(1, I, E)
+        k1 = lib.DeviceBuffer(w1)
+        lib.check(L.vdk_linear_ex(d1.ptr, 1, I, dw.ptr, db.ptr, dm.ptr, E, act, dy.ptr, k1.ptr, w1, None))
+        lib.check(L.vdk_synchronize())
+        assert np.array_equal(dy.to_array(np.float32, (1, E))[0], got[c]), c
+
+
 @pytest.mark.parametrize("case", [
     # (B, T, IC, x_stride, OC): CAM++ dense-layer linear1 shapes (the BatchNorm +
     # ReLU of the concatenated features folded into the GEMM's operand loads)
