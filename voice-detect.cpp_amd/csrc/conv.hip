@@ -1467,18 +1467,18 @@ __global__ __launch_bounds__(512) void conv3x3_band_kernel(ConvArgs a) {
     const int nk = IC / 16;
     band_issue<TH, NBW>(sa0, sx0, 0, oc0, IC, xoff, wr, xr, wave, lane);
 #pragma unroll 1
-    for (int k = 0; k < nk; k += 2) {
+    for (int k = 0; k < nk; ++k) {
         // chunk k: this wave's DMA has landed (nothing else is outstanding),
-        // then every wave's has, and chunk k-1's reads of the other pair are done
+        // then every wave's has, and chunk k-1's reads of the other pair are
+        // done.  One chunk per trip with the buffer pair picked per chunk (the
+        // inlined chunk keeps its distinct __restrict__ views, so its reads
+        // still do not wait for the other pair's DMA), which keeps the
+        // accumulators in one set of registers.
         __builtin_amdgcn_s_waitcnt(0);
         lds_barrier();
-        band_chunk<TH, NBW>(sa0, sx0, sa1, sx1, k + 1 < nk, (k + 1) * 16, oc0, IC, xoff, wr, xr, abase, bbase, HW,
-                            acc, wave, lane);
-        if (k + 1 >= nk) break;
-        __builtin_amdgcn_s_waitcnt(0);
-        lds_barrier();
-        band_chunk<TH, NBW>(sa1, sx1, sa0, sx0, k + 2 < nk, (k + 2) * 16, oc0, IC, xoff, wr, xr, abase, bbase, HW,
-                            acc, wave, lane);
+        const bool odd = k & 1;
+        band_chunk<TH, NBW>(odd ? sa1 : sa0, odd ? sx1 : sx0, odd ? sa0 : sa1, odd ? sx0 : sx1, k + 1 < nk,
+                            (k + 1) * 16, oc0, IC, xoff, wr, xr, abase, bbase, HW, acc, wave, lane);
     }
     lds_barrier();   // every wave is done reading the buffers the epilogue reuses
 
