@@ -337,6 +337,8 @@ def test_linear_shapes_and_batch_invariance(case):
     (1, 97, 480, 896, 128),
     (3, 33, 96, 96, 64),
     (1, 5, 64, 64, 32),
+    (2, 40, 32, 32, 64),   # one K chunk on the 32-wide tiles (the two-slot loop's shortest trip)
+    (1, 9, 16, 16, 32),    # one K chunk on the 16-wide tiles
 ])
 def test_conv_input_prologue(case):
     """y = relu(W relu(x*s + t) + b) for every tile that takes the input prologue,
