@@ -401,7 +401,8 @@ template <int NWQ>
 __global__ __launch_bounds__(64 * NWQ) void attention_kernel(const half_t* __restrict__ qkv, int T, int H,
                                                              float scale_log2, half_t* __restrict__ out) {
     constexpr int NT = 64 * NWQ;
-    constexpr int NLD = kKB * kHD / 8 / NT;   // 16-byte K (and V) chunks per thread per block
+    constexpr int NCH = kKB * kHD / 8;          // 16-byte K (and V) chunks per block
+    constexpr int NLD = (NCH + NT - 1) / NT;     // per thread (the last slot partial when NT does not divide NCH)
     __shared__ __attribute__((aligned(16))) half_t sK[kKB * kKR];   // [key][dim]
     __shared__ __attribute__((aligned(16))) half_t sV[kHD * kVR];   // [dim][key]
     const int b = blockIdx.z, h = blockIdx.y;
@@ -425,8 +426,9 @@ __global__ __launch_bounds__(64 * NWQ) void attention_kernel(const half_t* __res
         for (int j = 0; j < NLD; ++j) {
             const int i = tid + j * NT, key = i >> 3, d0 = (i & 7) * 8, kg = kb + key;
             const half_t* src = base + (size_t)kg * rs + h * kHD + d0;
-            kn[j] = kg < T ? *reinterpret_cast<const half8*>(src + H) : zero8;
-            vn[j] = kg < T ? *reinterpret_cast<const half8*>(src + 2 * H) : zero8;
+            const bool ok = (NCH % NT == 0 || i < NCH) && kg < T;
+            kn[j] = ok ? *reinterpret_cast<const half8*>(src + H) : zero8;
+            vn[j] = ok ? *reinterpret_cast<const half8*>(src + 2 * H) : zero8;
         }
     };
     fetch(0);
@@ -435,6 +437,7 @@ __global__ __launch_bounds__(64 * NWQ) void attention_kernel(const half_t* __res
 #pragma unroll
         for (int j = 0; j < NLD; ++j) {
             const int i = tid + j * NT, key = i >> 3, d0 = (i & 7) * 8;
+            if (NCH % NT != 0 && i >= NCH) continue;
             *reinterpret_cast<half8*>(&sK[key * kKR + d0]) = kn[j];
 #pragma unroll
             for (int e = 0; e < 8; ++e) sV[(d0 + e) * kVR + key] = vn[j][e];
@@ -799,9 +802,13 @@ extern "C" int vdk_attention(const void* d_qkv, int batch, int T, int n_heads, i
         const half_t* q = static_cast<const half_t*>(d_qkv);
         half_t* o = static_cast<half_t*>(d_out);
         const float sl2 = scale * 1.4426950408889634f;
+        // up to 160 frames (clips up to ~3.2 s): the whole clip's queries in one
+        // 5-wave workgroup per (clip, head), so K and V are staged once;
         // short clips: 64 queries per workgroup (less padding past T); long
         // ones: 128, so each staged key block serves more queries
-        if (T <= 512)
+        if (T <= 160)
+            hipLaunchKernelGGL(attention_kernel<5>, dim3(1, n_heads, batch), dim3(320), 0, s, q, T, (int)H, sl2, o);
+        else if (T <= 512)
             hipLaunchKernelGGL(attention_kernel<2>, dim3(cdiv(T, 64), n_heads, batch), dim3(128), 0, s, q, T, (int)H,
                                sl2, o);
         else
