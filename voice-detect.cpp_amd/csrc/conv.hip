@@ -1734,6 +1734,10 @@ int pick_tile(const ConvArgs& a) {
         if (a.KW == 3 && a.IC == 128 && a.OC == 128) return 40;   // ECAPA's Res2Net group convs
         if (a.KW == 3 && a.OC == 32 && a.IC % 32 == 0) return 60;     // CAM++'s gated linear_local
     }
+    if (a.split && is_s1_3x3(a)) {   // ERes2Net's split-f16 group convs (random-data sweep)
+        if (a.IC == 32 && a.OC == 32) return 61;
+        if (a.IC == 128 && a.OC == 128 && tile_fits(kTiles[40], a)) return 40;
+    }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
     if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[58], a)) return 58;
