@@ -1738,6 +1738,13 @@ int pick_tile(const ConvArgs& a) {
         if (a.IC == 32 && a.OC == 32) return 61;
         if (a.IC == 128 && a.OC == 128 && tile_fits(kTiles[40], a)) return 40;
     }
+    if (a.split && a.KH * a.KW == 1 && a.sh == 1 && a.sw == 1) {   // ERes2Net's split-f16 1x1s (same sweep)
+        if (a.IC == 64 && a.OC == 32) return 61;
+        if (a.IC == 128 && a.OC == 64) return 23;
+        if (a.IC == 256 && a.OC == 128) return 45;
+        if (a.IC == 128 && a.OC == 256) return 39;
+        if (a.IC == 256 && a.OC == 512) return 51;
+    }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
     if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[58], a)) return 58;
