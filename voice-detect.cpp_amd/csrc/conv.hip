@@ -1734,6 +1734,14 @@ int pick_tile(const ConvArgs& a) {
         if (a.KW == 3 && a.IC == 128 && a.OC == 128) return 40;   // ECAPA's Res2Net group convs
         if (a.KW == 3 && a.OC == 32 && a.IC % 32 == 0) return 60;     // CAM++'s gated linear_local
     }
+    // CAM++'s FCM: 32 -> 32 convs with a frequency stride (measured in the
+    // model): the 1x1 shortcuts on the 128x32 register-staged tile, the final
+    // 20 -> 10 conv on the narrow 32x64 DMA tile (the wider maps' strided 3x3s
+    // stay on the default)
+    if (!a.split && a.IC == 32 && a.OC == 32 && (a.sh != 1 || a.sw != 1)) {
+        if (a.KH * a.KW == 1) return 10;
+        if (a.H <= 20) return 60;
+    }
     if (a.split && is_s1_3x3(a)) {   // ERes2Net's split-f16 group convs (random-data sweep)
         if (a.IC == 32 && a.OC == 32) return 61;
         if (a.IC == 128 && a.OC == 128 && tile_fits(kTiles[40], a)) return 40;
