@@ -202,6 +202,19 @@ int vdk_linear(const float* d_x, int batch, int in_dim, const float* d_w,
 int vdk_linear_ex(const float* d_x, int batch, int in_dim, const float* d_w,
                   const float* d_bias, const float* d_mean_vec, int out_dim, int act,
                   float* d_y, void* d_work, size_t work_bytes, void* stream);
+/* No counterpart in the reference.  vdk_linear_ex for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the split-K partials live in a fixed
+ * per-GPU array of VDK_LINEAR_SCRATCH_BYTES, held until the process ends, so
+ * the call allocates nothing.  Fails (nothing launched) when
+ * vdk_linear_workspace_size(batch, in_dim, out_dim) exceeds that size.  Every
+ * call on one GPU shares its array: calls that overlap in time on one GPU
+ * (e.g. on two streams) race; calls in one stream order do not.  Same result,
+ * bit for bit, as vdk_linear_ex. */
+#define VDK_LINEAR_SCRATCH_BYTES (4u << 20)
+int vdk_linear_ex_noalloc(const float* d_x, int batch, int in_dim, const float* d_w,
+                          const float* d_bias, const float* d_mean_vec, int out_dim, int act,
+                          float* d_y, void* stream);
 
 /* ---- ECAPA-TDNN helpers (src/encoder.cpp) ----
  * Activations are time-major f16 [B][T][stride] (channel slices by pointer

@@ -6,6 +6,8 @@
 // wavefront per clip.  Sums are accumulated in f64 like the reference's ggml
 // reductions and host L2 (src/encoder_resnet.cpp:140-183).
 #include <cmath>
+#include <mutex>
+#include <string>
 
 #include "common.hpp"
 #include "vdk.h"
@@ -217,33 +219,93 @@ extern "C" size_t vdk_linear_workspace_size(int batch, int in_dim, int out_dim) 
     return sizeof(float) * (size_t)linear_splits(in_dim) * batch * out_dim;
 }
 
+namespace vdk {
+namespace {
+
+void linear_check(const float* d_x, int batch, int in_dim, const float* d_w, int out_dim, int act, float* d_y) {
+    require(d_x && d_w && d_y, "linear: NULL device pointer");
+    require(batch > 0 && in_dim > 0 && out_dim > 0, "linear: empty shape");
+    require(act == VDK_ACT_NONE || act == VDK_ACT_RELU || act == VDK_ACT_SIGMOID || act == VDK_ACT_TANH,
+            "linear: unknown activation");
+}
+
+// The two launches of the split-K FC; `part` holds nsplit x batch x out_dim
+// floats, every one of which the partial kernel writes before the reduce
+// reads it (nothing needs clearing between calls).
+void linear_launch(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
+                   const float* d_mean_vec, int out_dim, int act, float* d_y, float* part, hipStream_t s) {
+    const int ns = linear_splits(in_dim);
+    const int slice = ((in_dim + ns - 1) / ns + kLinK - 1) / kLinK * kLinK;
+    const int nsplit = (in_dim + slice - 1) / slice;
+    const int vec4 = in_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(d_w) & 15) == 0;
+    if ((long)cdiv(out_dim, 64) * cdiv(batch, 64) * nsplit >= 64)
+        hipLaunchKernelGGL(linear_partial_kernel<4>, dim3(cdiv(out_dim, 64), cdiv(batch, 64), nsplit), dim3(256),
+                           0, s, d_x, batch, in_dim, d_w, out_dim, slice, vec4, part);
+    else
+        hipLaunchKernelGGL(linear_partial_kernel<1>, dim3(cdiv(out_dim, 16), cdiv(batch, 16), nsplit), dim3(256),
+                           0, s, d_x, batch, in_dim, d_w, out_dim, slice, vec4, part);
+    VDK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(linear_reduce_kernel, dim3(cdiv((long)batch * out_dim, 256)), dim3(256), 0, s, part,
+                       nsplit, batch, out_dim, d_bias, d_mean_vec, act, d_y);
+    VDK_HIP(hipGetLastError());
+}
+
+}  // namespace
+}  // namespace vdk
+
 extern "C" int vdk_linear_ex(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
                              const float* d_mean_vec, int out_dim, int act, float* d_y, void* d_work,
                              size_t work_bytes, void* stream) {
     return guarded([&] {
-        require(d_x && d_w && d_y && d_work, "linear: NULL device pointer");
-        require(batch > 0 && in_dim > 0 && out_dim > 0, "linear: empty shape");
-        require(act == VDK_ACT_NONE || act == VDK_ACT_RELU || act == VDK_ACT_SIGMOID || act == VDK_ACT_TANH,
-                "linear: unknown activation");
+        linear_check(d_x, batch, in_dim, d_w, out_dim, act, d_y);
+        require(d_work != nullptr, "linear: NULL device pointer");
         require(work_bytes >= vdk_linear_workspace_size(batch, in_dim, out_dim),
                 "linear: workspace smaller than vdk_linear_workspace_size()");
-        const int ns = linear_splits(in_dim);
-        const int slice = ((in_dim + ns - 1) / ns + kLinK - 1) / kLinK * kLinK;
-        const int nsplit = (in_dim + slice - 1) / slice;
-        hipStream_t s = static_cast<hipStream_t>(stream);
-        float* part = static_cast<float*>(d_work);
-        const int vec4 = in_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0 &&
-                         (reinterpret_cast<uintptr_t>(d_w) & 15) == 0;
-        if ((long)cdiv(out_dim, 64) * cdiv(batch, 64) * nsplit >= 64)
-            hipLaunchKernelGGL(linear_partial_kernel<4>, dim3(cdiv(out_dim, 64), cdiv(batch, 64), nsplit), dim3(256),
-                               0, s, d_x, batch, in_dim, d_w, out_dim, slice, vec4, part);
-        else
-            hipLaunchKernelGGL(linear_partial_kernel<1>, dim3(cdiv(out_dim, 16), cdiv(batch, 16), nsplit), dim3(256),
-                               0, s, d_x, batch, in_dim, d_w, out_dim, slice, vec4, part);
-        VDK_HIP(hipGetLastError());
-        hipLaunchKernelGGL(linear_reduce_kernel, dim3(cdiv((long)batch * out_dim, 256)), dim3(256), 0, s, part,
-                           nsplit, batch, out_dim, d_bias, d_mean_vec, act, d_y);
-        VDK_HIP(hipGetLastError());
+        linear_launch(d_x, batch, in_dim, d_w, d_bias, d_mean_vec, out_dim, act, d_y, static_cast<float*>(d_work),
+                      static_cast<hipStream_t>(stream));
+    });
+}
+
+// Split-K partials of vdk_linear_ex_noalloc: a fixed device array, one copy
+// per GPU, held until the process ends.  Host code never passes `scratch`
+// itself to a kernel (on the host it names a stand-in, not device memory):
+// its device address is looked up once per device with that device current
+// and kept in g_scratch_dev.
+static __device__ __align__(256) float scratch[VDK_LINEAR_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kMaxDevices] = {};
+
+float* scratch_on_current_device() {
+    int dev = -1;
+    VDK_HIP(hipGetDevice(&dev));
+    require(dev >= 0 && dev < kMaxDevices, "linear_noalloc: device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        VDK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        require(p != nullptr, "linear_noalloc: no device address for the scratch array");
+        g_scratch_dev[dev] = static_cast<float*>(p);
+    }
+    return g_scratch_dev[dev];
+}
+}  // namespace
+
+extern "C" int vdk_linear_ex_noalloc(const float* d_x, int batch, int in_dim, const float* d_w,
+                                     const float* d_bias, const float* d_mean_vec, int out_dim, int act,
+                                     float* d_y, void* stream) {
+    return guarded([&] {
+        linear_check(d_x, batch, in_dim, d_w, out_dim, act, d_y);
+        const size_t need = vdk_linear_workspace_size(batch, in_dim, out_dim);
+        require(need <= VDK_LINEAR_SCRATCH_BYTES,
+                "linear_noalloc: batch * out_dim * splits needs " + std::to_string(need) +
+                    " bytes of scratch, above the fixed " + std::to_string((size_t)VDK_LINEAR_SCRATCH_BYTES) +
+                    " (use vdk_linear_ex with a workspace)");
+        linear_launch(d_x, batch, in_dim, d_w, d_bias, d_mean_vec, out_dim, act, d_y, scratch_on_current_device(),
+                      static_cast<hipStream_t>(stream));
     });
 }
 
