@@ -3,6 +3,7 @@
 TEST INFRASTRUCTURE ONLY: imported by the test suite, the smoke check and the
 CPU-baseline leg of bench.py.  It is the checker, never the thing measured.
 """
+import contextlib
 import ctypes as C
 import os
 
@@ -47,24 +48,41 @@ def lib():
         path = os.path.join(HERE, "liboracle.so")
         if not os.path.exists(path):
             raise RuntimeError(f"oracle not built: {path} (run make -C oracle)")
-        L = C.CDLL(path)
-        L.orc_fbank_frames.argtypes = [C.c_int, C.POINTER(FbankCfg)]
-        L.orc_fbank.argtypes = [F32P, C.c_int, C.POINTER(FbankCfg), F32P]
-        L.orc_powspec.argtypes = [F32P, C.c_int, C.c_int, C.c_int, F64P]
-        L.orc_mel_filters.argtypes = [C.POINTER(FbankCfg), F64P]
-        L.orc_povey_window.argtypes = [C.c_int, F64P]
-        conv = [F32P, C.c_int, C.c_int, C.c_int, F32P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
-                C.c_void_p, C.c_void_p, C.c_int]
-        L.orc_conv2d_f32.argtypes = conv + [F32P]
-        L.orc_conv2d_f64.argtypes = conv + [F64P]
-        L.orc_tstp.argtypes = [F32P, C.c_int, C.c_int, C.c_int, C.c_float, F32P]
-        L.orc_linear.argtypes = [F32P, C.c_int, F32P, C.c_void_p, C.c_void_p, C.c_int, F32P]
-        L.orc_l2norm.argtypes = [F32P, C.c_int]
-        L.orc_resnet34_forward.argtypes = [C.POINTER(ResNet), F32P, C.c_int, F32P, C.POINTER(ResNetCaps)]
-        L.orc_embed_batch.argtypes = [C.POINTER(ResNet), C.POINTER(FbankCfg), F32P, C.c_int, C.c_int,
-                                      C.c_int, F32P]
-        _LIB = L
+        _LIB = _load(path)
     return _LIB
+
+
+@contextlib.contextmanager
+def using_library(path):
+    """Run the oracle wrappers against another build of the oracle sources
+    (the mutation tests' deliberately broken copies), then restore."""
+    global _LIB
+    saved = _LIB
+    _LIB = _load(path)
+    try:
+        yield _LIB
+    finally:
+        _LIB = saved
+
+
+def _load(path):
+    L = C.CDLL(path)
+    L.orc_fbank_frames.argtypes = [C.c_int, C.POINTER(FbankCfg)]
+    L.orc_fbank.argtypes = [F32P, C.c_int, C.POINTER(FbankCfg), F32P]
+    L.orc_powspec.argtypes = [F32P, C.c_int, C.c_int, C.c_int, F64P]
+    L.orc_mel_filters.argtypes = [C.POINTER(FbankCfg), F64P]
+    L.orc_povey_window.argtypes = [C.c_int, F64P]
+    conv = [F32P, C.c_int, C.c_int, C.c_int, F32P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+            C.c_void_p, C.c_void_p, C.c_int]
+    L.orc_conv2d_f32.argtypes = conv + [F32P]
+    L.orc_conv2d_f64.argtypes = conv + [F64P]
+    L.orc_tstp.argtypes = [F32P, C.c_int, C.c_int, C.c_int, C.c_float, F32P]
+    L.orc_linear.argtypes = [F32P, C.c_int, F32P, C.c_void_p, C.c_void_p, C.c_int, F32P]
+    L.orc_l2norm.argtypes = [F32P, C.c_int]
+    L.orc_resnet34_forward.argtypes = [C.POINTER(ResNet), F32P, C.c_int, F32P, C.POINTER(ResNetCaps)]
+    L.orc_embed_batch.argtypes = [C.POINTER(ResNet), C.POINTER(FbankCfg), F32P, C.c_int, C.c_int,
+                                  C.c_int, F32P]
+    return L
 
 
 def ref_lib():

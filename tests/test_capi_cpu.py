@@ -12,6 +12,7 @@ import tempfile
 import numpy as np
 import pytest
 
+import pyoracle as O
 from vdamd import gguf, lib, synth
 
 
@@ -65,6 +66,76 @@ def test_load_rejects_bad_files():
         q = os.path.join(tmp, "nodim.gguf")
         gguf.write_gguf(q, {"voicedetect.arch": "wespeaker_resnet34"}, [])
         assert L.voicedetect_capi_load(q.encode()) is None
+
+
+def _with_extra_tensor(src, dst, ne_words, gtype=0, offset=0, truncate_to=None):
+    """Copy GGUF `src` to `dst` with one more tensor info (raw u64 dim words,
+    type, offset) after the existing ones; the data section is moved to the
+    new aligned base so every existing offset stays valid."""
+    import struct
+    g = gguf.GGUFFile(src)
+    end = g.pos                                   # end of the tensor infos
+    buf = g.buf
+    old_base = (end + 31) // 32 * 32
+    (nt,) = struct.unpack_from("<Q", buf, 8)
+    info = struct.pack("<Q", 5) + b"bogus" + struct.pack("<I", len(ne_words))
+    info += b"".join(struct.pack("<Q", w & (2 ** 64 - 1)) for w in ne_words) + struct.pack("<IQ", gtype, offset)
+    head = bytearray(buf[:end]) + info
+    head[8:16] = struct.pack("<Q", nt + 1)
+    head += b"\0" * ((-len(head)) % 32)
+    out = bytes(head) + buf[old_base:]
+    if truncate_to is not None:
+        out = out[:truncate_to]
+    open(dst, "wb").write(out)
+
+
+def test_load_rejects_corrupt_tensor_headers():
+    """Tensor infos a corrupt or crafted file can hold: negative dims, dims whose
+    product overflows int64, offsets that wrap the bounds check, unaligned
+    offsets, data cut short.  Each makes load return NULL; the same file with a
+    well-formed extra tensor loads (the construction itself is sound)."""
+    L = lib.lib()
+    with tempfile.TemporaryDirectory() as tmp:
+        base = os.path.join(tmp, "base.gguf")
+        synth.write_resnet34(base, seed=5, channels=(32, 32, 64, 64), blocks=(1, 1, 1, 1), emb_dim=64)
+        ok = os.path.join(tmp, "ok.gguf")
+        _with_extra_tensor(base, ok, [8])
+        ctx = L.voicedetect_capi_load(ok.encode())
+        assert ctx is not None
+        L.voicedetect_capi_free(ctx)
+        cases = {
+            "negative_dim": dict(ne_words=[-8, 4]),
+            "dim_past_int32": dict(ne_words=[2 ** 31, 1]),
+            "product_overflow": dict(ne_words=[2 ** 31 - 1, 2 ** 31 - 1, 2 ** 31 - 1, 4]),
+            "offset_wraps": dict(ne_words=[8], offset=2 ** 64 - 64),
+            "offset_past_end": dict(ne_words=[8], offset=1 << 40),
+            "offset_unaligned": dict(ne_words=[8], offset=4),
+            "larger_than_file": dict(ne_words=[1 << 30, 4]),
+        }
+        for name, kw in cases.items():
+            bad = os.path.join(tmp, name + ".gguf")
+            _with_extra_tensor(base, bad, **kw)
+            assert L.voicedetect_capi_load(bad.encode()) is None, name
+        cut = os.path.join(tmp, "truncated.gguf")
+        _with_extra_tensor(base, cut, [8], truncate_to=os.path.getsize(ok) - 100)
+        assert L.voicedetect_capi_load(cut.encode()) is None
+
+
+def test_ecapa_refuses_clips_shorter_than_its_reflect_pad():
+    """ECAPA's reflect padding needs pad < T (src/encoder.cpp:32-52; the widest
+    pad is the last SE-Res2Net block's dilation, 4): 1039 samples give 4 FBank
+    frames and are refused before any device work, with a clear message."""
+    L = lib.lib()
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "ecapa.gguf")
+        synth.write_ecapa(path, 3, channels=64, mfa=96, n_mels=80, scale=2, se_ch=16, att_ch=32, emb_dim=16)
+        ctx = lib.Context(path)
+        vec, dim = C.POINTER(C.c_float)(), C.c_int(5)
+        x = np.zeros(1039, dtype=np.float32)
+        assert L.voicedetect_capi_embed_pcm(ctx.ctx, x.ctypes.data, 1039, 16000, C.byref(vec), C.byref(dim)) == 1
+        assert "clip too short for reflect padding (4 frames, the model needs 5)" in ctx.last_error()
+        assert not vec and dim.value == 0
+        ctx.close()
 
 
 @pytest.fixture(scope="module")
@@ -158,6 +229,33 @@ def test_resampler_closed_form():
     same = np.zeros(10, dtype=np.float32)
     assert L.vdk_resample_linear(x.ctypes.data, 10, 16000, 16000, same.ctypes.data, 10) == 10
     assert np.array_equal(same, x)
+    # 48 kHz -> 16 kHz: every output sits on an input sample (src = 3i exactly)
+    y = np.random.default_rng(4).standard_normal(3001).astype(np.float32)
+    dec = np.zeros(1000, dtype=np.float32)
+    assert L.vdk_resample_linear(y.ctypes.data, 3001, 48000, 16000, dec.ctypes.data, 1000) == 1000
+    assert np.array_equal(dec, y[0:3000:3])
+
+
+@pytest.mark.parametrize("in_sr,out_sr", [(44100, 16000), (22050, 16000), (48000, 16000), (8000, 16000),
+                                          (11025, 16000), (32000, 16000), (16000, 8000), (16000, 44100)])
+def test_resampler_bit_exact_with_reference(in_sr, out_sr):
+    """vdk_resample_linear against the reference's own resample_linear
+    (src/audio_io.cpp:9-23, compiled from the reference sources into
+    oracle/_ref/libref.so): identical output length and bits at non-integer
+    ratios, on a noisy clip and on a ramp."""
+    R = O.ref_lib()
+    if R is None:
+        pytest.skip("oracle/_ref/libref.so not built (the reference checkout is absent)")
+    L = lib.lib()
+    rng = np.random.default_rng(in_sr + out_sr)
+    for x in (rng.standard_normal(in_sr * 37 // 100).astype(np.float32),
+              np.linspace(-1.0, 1.0, 4801, dtype=np.float32)):
+        cap = int(len(x) * out_sr / in_sr) + 4
+        got, want = np.zeros(cap, np.float32), np.zeros(cap, np.float32)
+        n = L.vdk_resample_linear(x.ctypes.data, len(x), in_sr, out_sr, got.ctypes.data, cap)
+        m = R.ref_resample(x, len(x), in_sr, out_sr, want, cap)
+        assert n == m and n > 0
+        assert np.array_equal(got[:n].view(np.uint32), want[:m].view(np.uint32))
 
 
 def test_f16_packing_matches_ieee_round_to_nearest_even():
