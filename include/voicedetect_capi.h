@@ -62,8 +62,12 @@ int voicedetect_capi_verify_paths(voicedetect_ctx* ctx, const char* a,
                                   const char* b, float threshold,
                                   float* out_distance, int* out_verified);
 
-/* The age/gender/emotion heads are not part of this library: returns NULL and
- * sets the reference's error text (reference :160-178, src/model.cpp:80-84). */
+/* Age/gender/emotion analysis of a WAV file as a malloc'd JSON string (free
+ * with voicedetect_capi_free_string), for a context loaded from a wav2vec2
+ * analyze GGUF (arch wav2vec2_emotion / wav2vec2_age_gender), run on the GPU
+ * (reference :160-178, src/model.cpp:80-101, src/analyze_w2v2.cpp).  On a
+ * speaker-embedding model: NULL with the reference's error text
+ * "voicedetect: this model has no age/gender/emotion analyze heads". */
 char* voicedetect_capi_analyze_path_json(voicedetect_ctx* ctx,
                                          const char* wav_path);
 

@@ -26,7 +26,8 @@ void orc_conv1d_same(const float* x, int T, const orc_conv1d* c, int dilation, f
             if (j < pad) t = pad - j;                    /* left reflect, no edge repeat */
             else if (j < pad + T) t = j - pad;
             else t = (T - 2) - (j - pad - T);            /* right reflect */
-            if (t < 0) t = 0;                            /* only reachable when T < pad + 1 */
+            if (t < 0) t = 0;                            /* only reachable when T < pad + 1, */
+                                                         /* a length the library refuses */
             if (t > T - 1) t = T - 1;
             pr[j] = xr[t];
         }

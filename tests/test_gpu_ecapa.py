@@ -316,7 +316,7 @@ def test_ecapa_batch64_matches_oracle(ecapa):
     assert np.array_equal(one[0], cap["emb"][31])
 
 
-@pytest.mark.parametrize("n", [400, 4000, 40000])
+@pytest.mark.parametrize("n", [1040, 4000, 40000])   # 1040 samples = 5 frames, the fewest ECAPA takes
 def test_ecapa_embed_pcm_lengths(ecapa, n):
     path, ctx, net = ecapa
     announce(f"e2e ecapa B=1 n={n}")

@@ -2,14 +2,16 @@
 
 The reference's analyze goldens are HF transformers outputs
 (scripts/gen_baseline.py --analyze; tests/test_analyze.cpp,
-tests/test_age_gender.cpp).  Here HF's own Wav2Vec2 modules are built offline
-from a small config with random weights, run in f64, exported through the
-reference converter's naming (w2v2_store_name) into a GGUF, and the oracle run
-on that GGUF must reproduce every hidden state and the head outputs to ~1e-10.
-The checks cover both reference variants: wav2vec2-base emotion (group-norm conv0,
-post-norm layers, weighted layer sum, projector + classifier) and
-wav2vec2-large-robust age/gender (layer-norm convs with bias, do_normalize,
-pre-norm layers, two tanh heads).  Closed forms pin the pieces on their own.
+tests/test_age_gender.cpp).  tests/golden/make_w2v2_golden.py builds HF's own
+Wav2Vec2 modules offline from a small config with seeded random weights, runs
+them in f64 and stores their weights (under the reference converter's names,
+w2v2_store_name) and outputs in tests/golden/w2v2_golden.npz; here the weights
+go into a GGUF and the oracle run on it must reproduce every hidden state and
+the head outputs to ~1e-10.  The checks cover both reference variants:
+wav2vec2-base emotion (group-norm conv0, post-norm layers, weighted layer sum,
+projector + classifier) and wav2vec2-large-robust age/gender (layer-norm convs
+with bias, do_normalize, pre-norm layers, two tanh heads).  Closed forms pin the
+pieces on their own.  No torch or transformers import happens here.
 """
 import json
 import os
@@ -22,46 +24,23 @@ import oracle_w2v2 as W
 from vdamd import gguf as G
 from vdamd import synth
 
-torch = pytest.importorskip("torch")
-transformers = pytest.importorskip("transformers")
-os.environ.setdefault("HF_HUB_OFFLINE", "1")
-os.environ.setdefault("TRANSFORMERS_OFFLINE", "1")
-
-CONV = dict(conv_dim=(32, 32, 32, 32, 32, 32, 32), conv_kernel=(10, 3, 3, 3, 3, 2, 2),
-            conv_stride=(5, 2, 2, 2, 2, 2, 2))
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "w2v2_golden.npz")
 
 
-def _hf_config(large):
-    from transformers import Wav2Vec2Config
-    return Wav2Vec2Config(
-        hidden_size=64, num_hidden_layers=3, num_attention_heads=4, intermediate_size=96, **CONV,
-        feat_extract_norm="layer" if large else "group", conv_bias=large, do_stable_layer_norm=large,
-        num_conv_pos_embeddings=16, num_conv_pos_embedding_groups=4, use_weighted_layer_sum=not large,
-        classifier_proj_size=24, num_labels=4, layer_norm_eps=1e-5, hidden_dropout=0.0, attention_dropout=0.0,
-        activation_dropout=0.0, feat_proj_dropout=0.0, final_dropout=0.0, layerdrop=0.0, mask_time_prob=0.0)
+def _golden():
+    return np.load(GOLDEN, allow_pickle=False)
 
 
-def _export(state, kind, cfg, labels, path):
-    tensors = []
-    for name, t in state.items():
-        if name.startswith("wav2vec2.masked_spec_embed"):
-            continue
-        a = t.detach().cpu().numpy().astype(np.float32)
-        tensors.append((synth.w2v2_store_name(name), G.GGML_F32, list(a.shape), a))
-    kv = synth.w2v2_kv(kind, cfg.hidden_size, cfg.num_hidden_layers, cfg.num_attention_heads,
-                       cfg.intermediate_size, cfg.conv_dim, cfg.conv_kernel, cfg.conv_stride,
-                       cfg.num_conv_pos_embeddings, cfg.num_conv_pos_embedding_groups,
-                       cfg.classifier_proj_size, labels, cfg.layer_norm_eps)
+def _oracle(z, kind, labels):
+    prefix = f"{kind}/w/"
+    tensors = [(k[len(prefix):], G.GGML_F32, list(z[k].shape), z[k]) for k in z.files if k.startswith(prefix)]
+    c = json.loads(str(z[f"{kind}/config"]))
+    kv = synth.w2v2_kv(kind, c["hidden"], c["n_layers"], c["n_heads"], c["ff"], tuple(c["conv_dims"]),
+                       tuple(c["conv_kernels"]), tuple(c["conv_strides"]), c["pos_k"], c["pos_groups"], c["proj"],
+                       labels, c["eps"])
+    path = os.path.join(tempfile.mkdtemp(), kind + ".gguf")
     G.write_gguf(path, kv, tensors)
-    return path
-
-
-def _f32_weights(model):
-    # the GGUF stores f32: round the f64 model's weights to f32 so both sides
-    # see the same values
-    with torch.no_grad():
-        for p in model.parameters():
-            p.copy_(p.float().double())
+    return W.OracleW2V2(path)
 
 
 def _pcm(n, seed):
@@ -70,46 +49,14 @@ def _pcm(n, seed):
 
 @pytest.fixture(scope="module")
 def emotion_pair():
-    from transformers import Wav2Vec2ForSequenceClassification
-    torch.manual_seed(7)
-    cfg = _hf_config(False)
-    m = Wav2Vec2ForSequenceClassification(cfg).double().eval()
-    with torch.no_grad():
-        m.layer_weights.copy_(torch.randn(cfg.num_hidden_layers + 1, dtype=torch.float64))
-    _f32_weights(m)
-    path = _export(m.state_dict(), "emotion", cfg, synth.EMOTION_LABELS,
-                   os.path.join(tempfile.mkdtemp(), "emo.gguf"))
-    return m, W.OracleW2V2(path)
-
-
-class _AgeGender(torch.nn.Module):
-    """audeering AgeGenderModel: Wav2Vec2Model + two ModelHeads
-    out_proj(tanh(dense(mean_t(last_hidden_state))))."""
-
-    def __init__(self, cfg):
-        super().__init__()
-        from transformers import Wav2Vec2Model
-        self.wav2vec2 = Wav2Vec2Model(cfg)
-        H = cfg.hidden_size
-        self.age = torch.nn.ModuleDict(dict(dense=torch.nn.Linear(H, H), out_proj=torch.nn.Linear(H, 1)))
-        self.gender = torch.nn.ModuleDict(dict(dense=torch.nn.Linear(H, H), out_proj=torch.nn.Linear(H, 3)))
-
-    def forward(self, x):
-        out = self.wav2vec2(x, output_hidden_states=True)
-        pooled = out.last_hidden_state.mean(dim=1)
-        heads = [h["out_proj"](torch.tanh(h["dense"](pooled))) for h in (self.age, self.gender)]
-        return out, torch.cat(heads, dim=1)
+    z = _golden()
+    return z, _oracle(z, "emotion", synth.EMOTION_LABELS)
 
 
 @pytest.fixture(scope="module")
 def age_gender_pair():
-    torch.manual_seed(11)
-    cfg = _hf_config(True)
-    m = _AgeGender(cfg).double().eval()
-    _f32_weights(m)
-    path = _export(m.state_dict(), "age_gender", cfg, synth.GENDER_LABELS,
-                   os.path.join(tempfile.mkdtemp(), "ag.gguf"))
-    return m, W.OracleW2V2(path)
+    z = _golden()
+    return z, _oracle(z, "age_gender", synth.GENDER_LABELS)
 
 
 def _close(a, b, tol=1e-9):
@@ -121,39 +68,36 @@ def _close(a, b, tol=1e-9):
 
 @pytest.mark.parametrize("n", [4000, 8000, 12345])
 def test_emotion_matches_hf(emotion_pair, n):
-    m, orc = emotion_pair
+    z, orc = emotion_pair
     pcm = _pcm(n, 100 + n)
-    with torch.no_grad():
-        out = m(torch.from_numpy(pcm)[None], output_hidden_states=True)
-        feat = m.wav2vec2.feature_extractor(torch.from_numpy(pcm)[None]).transpose(1, 2)[0].numpy()
-    _close(orc.conv_encoder(pcm), feat)
+    g = f"emotion/n{n}/"
+    _close(orc.conv_encoder(pcm), z[g + "feat"])
     states = orc.hidden_states(pcm)
-    assert len(states) == len(out.hidden_states) == orc.n_layers + 1
+    hidden = z[g + "hidden"]
+    assert len(states) == len(hidden) == orc.n_layers + 1
     assert states[0].shape[0] == orc.frames(n)
-    for s, h in zip(states, out.hidden_states):
-        _close(s, h[0].numpy())
-    _close(orc.raw_outputs(pcm), out.logits[0].numpy())
+    for s, h in zip(states, hidden):
+        _close(s, h)
+    _close(orc.raw_outputs(pcm), z[g + "raw"])
 
 
 @pytest.mark.parametrize("n", [4000, 9001])
 def test_age_gender_matches_hf(age_gender_pair, n):
-    from transformers import Wav2Vec2FeatureExtractor
-    m, orc = age_gender_pair
+    z, orc = age_gender_pair
     pcm = _pcm(n, 200 + n)
-    # do_normalize is the feature extractor's zero-mean / unit-variance step
-    fe = Wav2Vec2FeatureExtractor(do_normalize=True, feature_size=1, sampling_rate=16000, padding_value=0.0)
-    x = np.asarray(fe(pcm, sampling_rate=16000).input_values[0], dtype=np.float64)
-    with torch.no_grad():
-        out, raw = m(torch.from_numpy(x)[None])
-        feat = m.wav2vec2.feature_extractor(torch.from_numpy(x)[None]).transpose(1, 2)[0].numpy()
-    # the feature extractor normalises in f32; compare the conv stack on its input
+    g = f"age_gender/n{n}/"
+    # do_normalize is the feature extractor's zero-mean / unit-variance step;
+    # it normalises in f32, so the conv stack is compared on its output
+    x = z[g + "normalized"]
     orc.do_normalize = False
     try:
-        _close(orc.conv_encoder(x), feat)
+        _close(orc.conv_encoder(x), z[g + "feat"])
         states = orc.hidden_states(x)
-        for s, h in zip(states, out.hidden_states):
-            _close(s, h[0].numpy())
-        _close(orc.raw_outputs(x), raw[0].numpy())
+        hidden = z[g + "hidden"]
+        assert len(states) == len(hidden)
+        for s, h in zip(states, hidden):
+            _close(s, h)
+        _close(orc.raw_outputs(x), z[g + "raw"])
     finally:
         orc.do_normalize = True
     # and the oracle's own normalisation agrees with the extractor's to f32 rounding

@@ -1,6 +1,7 @@
 // gguf.cpp - GGUF reader (see gguf.hpp).
 #include "gguf.hpp"
 
+#include <climits>
 #include <cstring>
 #include <fstream>
 
@@ -111,7 +112,7 @@ size_t tensor_bytes(uint32_t type, int64_t n) {
 
 int64_t GgufTensor::nelements() const {
     int64_t n = 1;
-    for (int64_t d : ne) n *= d;
+    for (int64_t d : ne) n *= d;   // dims and their product are range-checked at load
     return n;
 }
 
@@ -134,7 +135,7 @@ GgufFile::GgufFile(const std::string& path) {
     }
     uint64_t align = 32;
     if (kv_.count("general.alignment")) align = (uint64_t)kv_["general.alignment"].i;
-    if (align == 0 || (align & (align - 1))) throw Error("gguf: bad alignment");
+    if (align == 0 || (align & (align - 1)) || align > (1u << 24)) throw Error("gguf: bad alignment");
     struct Info { std::string name; std::vector<int64_t> ne; uint32_t type; uint64_t off; };
     std::vector<Info> infos;
     for (uint64_t k = 0; k < nt; ++k) {
@@ -142,20 +143,35 @@ GgufFile::GgufFile(const std::string& path) {
         in.name = r.str();
         const uint32_t nd = r.get<uint32_t>();
         if (nd > 4) throw Error("gguf: tensor rank above 4");
-        for (uint32_t d = 0; d < nd; ++d) in.ne.push_back((int64_t)r.get<uint64_t>());
+        for (uint32_t d = 0; d < nd; ++d) {
+            // ggml dims are int64; anything negative or past INT32_MAX is a
+            // corrupt header (the encoders index tensors with int)
+            const uint64_t v = r.get<uint64_t>();
+            if (v > (uint64_t)INT32_MAX) throw Error("gguf: tensor dimension out of range: " + in.name);
+            in.ne.push_back((int64_t)v);
+        }
         in.type = r.get<uint32_t>();
         in.off = r.get<uint64_t>();
         infos.push_back(in);
     }
     const size_t hdr = (size_t)(r.p - buf_.data());
     const size_t base = (hdr + align - 1) / align * align;
+    const size_t size = buf_.size();
     for (const Info& in : infos) {
         GgufTensor t;
         t.name = in.name;
         t.type = in.type;
         t.ne = in.ne;
-        t.nbytes = tensor_bytes(in.type, t.nelements());
-        if (base + in.off + t.nbytes > buf_.size()) throw Error("gguf: tensor data out of range: " + in.name);
+        // element count without overflow; every element takes at least one
+        // byte of the file (F32 4, F16 2, Q8_0 34/32), which bounds nbytes too
+        int64_t n = 1;
+        for (int64_t d : in.ne)
+            if (__builtin_mul_overflow(n, d, &n)) throw Error("gguf: tensor size overflows: " + in.name);
+        if ((uint64_t)n > (uint64_t)size) throw Error("gguf: tensor larger than the file: " + in.name);
+        t.nbytes = tensor_bytes(in.type, n);
+        if (in.off % align) throw Error("gguf: tensor offset not aligned: " + in.name);
+        if (base > size || in.off > size - base || t.nbytes > size - base - in.off)
+            throw Error("gguf: tensor data out of range: " + in.name);
         t.data = buf_.data() + base + in.off;
         tensors_[in.name] = t;
     }

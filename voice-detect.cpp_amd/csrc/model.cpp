@@ -126,6 +126,30 @@ int Model::frames(int n_samples) const {
     return 1 + (n_samples - f.win_length) / f.hop_length;
 }
 
+// ECAPA pads every conv by reflection without repeating the edge frame
+// (src/encoder.cpp:32-52), which needs pad < T; the reference builds
+// out-of-range row indices below that and SpeechBrain's reflect pad raises.
+// The widest pad is max((k0 - 1) / 2, the last SE-Res2Net block's dilation).
+int Model::min_frames() const {
+    if (cfg_.arch != "ecapa_tdnn") return 1;
+    int pad = 0;
+    if (const GgufTensor* t = gguf_->tensor("blocks.0.conv.conv.weight"))
+        if (t->ne.size() == 3) pad = (int)(t->ne[0] - 1) / 2;
+    int n_res = 0;
+    while (gguf_->tensor("blocks." + std::to_string(n_res + 1) + ".tdnn1.conv.conv.weight")) ++n_res;
+    if (n_res > 0) pad = std::max(pad, n_res + 1);
+    return pad + 1;
+}
+
+void Model::check_frames(int n_samples) const {
+    const int T = frames(n_samples);
+    if (T <= 0) throw Error("voicedetect: FBank produced no frames");
+    const int need = min_frames();
+    if (T < need)
+        throw Error("voicedetect: clip too short for reflect padding (" + std::to_string(T) + " frames, the model needs " +
+                    std::to_string(need) + ")");
+}
+
 void Model::ensure_device() {
     if (ready_) return;
     int n = 0;
@@ -402,7 +426,7 @@ void Model::embed_batch_device(const float* d_pcm, int batch, int n_samples, flo
     require(batch > 0, "voicedetect: batch must be positive");
     require(d_pcm && d_out, "voicedetect: NULL device pointer");
     require(!is_analyzer(), "voicedetect: this model has no speaker embedding head (an analyze model)");
-    if (frames(n_samples) <= 0) throw Error("voicedetect: FBank produced no frames");
+    check_frames(n_samples);
     ensure_device();
     ensure_workspace(batch, n_samples);
     forward(d_pcm, batch, n_samples, d_out);
@@ -413,7 +437,7 @@ void Model::embed_capture(const float* pcm, int batch, int n_samples, float* fea
     std::lock_guard<std::mutex> lock(mu_);
     require(batch > 0 && pcm, "voicedetect: invalid pcm batch");
     require(!is_analyzer(), "voicedetect: this model has no speaker embedding head (an analyze model)");
-    if (frames(n_samples) <= 0) throw Error("voicedetect: FBank produced no frames");
+    check_frames(n_samples);
     ensure_device();
     ensure_workspace(batch, n_samples);
     const size_t E = (size_t)cfg_.embedding_dim;
@@ -439,7 +463,7 @@ void Model::embed_batch_host(const float* pcm, int batch, int n_samples, float* 
 std::vector<float> Model::embed_pcm(const std::vector<float>& pcm, int sample_rate) {
     require(!is_analyzer(), "voicedetect: this model has no speaker embedding head (an analyze model)");
     const std::vector<float> x = sample_rate == 16000 ? pcm : resample_linear(pcm, sample_rate, 16000);
-    if (frames((int)x.size()) <= 0) throw Error("voicedetect: FBank produced no frames");
+    check_frames((int)x.size());
     std::vector<float> out((size_t)cfg_.embedding_dim);
     embed_batch_host(x.data(), 1, (int)x.size(), out.data());
     return out;

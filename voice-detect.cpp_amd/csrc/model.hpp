@@ -318,6 +318,8 @@ private:
     void prof_begin(const char* name, double flops, double bytes);
     void prof_end();
     int frames(int n_samples) const;
+    int min_frames() const;                 // fewest FBank frames the encoder accepts
+    void check_frames(int n_samples) const; // throws for clips the encoder cannot take
 
     std::unique_ptr<GgufFile> gguf_;
     ModelConfig cfg_;
