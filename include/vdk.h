@@ -109,6 +109,9 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * conv with its last step dropped).  y and an f32 residual may be the same
  * buffer (each element is read before it is written, by the same thread).
  * OC needs only be a multiple of 8: surplus rows of a tile are masked.
+ * w_chunked (may be NULL): the same weights re-ordered chunk-major,
+ * [IC/16][KH*KW][OC][16] (vdk_conv_pack_chunked); kernels that stream 16-channel
+ * weight chunks read it as whole cache lines.  Results do not depend on it.
  * split != 0 selects split-f16 arithmetic (~2^-21 relative instead of f16's
  * 2^-11, for ill-conditioned networks): x, residual and y hold value = hi + lo
  * with the lo halves x_lo / res_lo / y_lo elements after the hi halves (same
@@ -130,7 +133,11 @@ typedef struct {
     int tile;
     int res_f32, res_after_act, out_w;
     const float* in_scale; const float* in_shift;
+    const void* w_chunked;
 } vdk_conv_desc;
+/* Host: re-order f16 conv weights [OC][KH][KW][IC] (IC % 16 == 0) into the
+ * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */
+void vdk_conv_pack_chunked(const unsigned short* w, int OC, int KH, int KW, int IC, unsigned short* out);
 int vdk_conv2d_ex(const vdk_conv_desc* desc, void* stream);
 int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* desc);
 

@@ -187,6 +187,9 @@ def test_conv_every_tile_config(shape):
     (1, 5, 33, 64, True, False, True),
     (3, 4, 31, 32, True, True, False),
     (1, 1, 1, 64, True, True, True),
+    (2, 9, 75, 128, True, False, True),      # band kernels: the widest map, no residual
+    (1, 5, 38, 128, False, True, False),
+    (3, 4, 31, 128, True, True, True),
 ])
 def test_conv_register_weight_tiles_plain_epilogues(case):
     L = lib.lib()

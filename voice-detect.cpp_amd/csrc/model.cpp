@@ -214,6 +214,11 @@ void Model::upload_resnet() {
                     }
         c.ic = ic; c.oc = oc; c.k = k; c.stride = stride; c.pad = pad;
         arena.put(packed, &c.w);
+        if (k == 3 && stride == 1 && oc % 128 == 0) {   // the band kernels stream whole-line weight chunks
+            std::vector<uint16_t> chunked(packed.size());
+            vdk_conv_pack_chunked(packed.data(), oc, k, k, ic, chunked.data());
+            arena.put(chunked, &c.wc);
+        }
         put_f32(bn, (size_t)oc, &c.b);
         return oc;
     };
@@ -343,7 +348,13 @@ void Model::conv(const Conv& c, const void* x, int batch, int H, int W, const vo
                            std::to_string(c.stride) + "_" + std::to_string(c.ic) + "to" + std::to_string(c.oc);
         prof_begin(name.c_str(), flops, bytes);
     }
-    check(vdk_conv2d_nhwc(x, batch, H, W, c.ic, c.w, c.oc, c.k, c.k, c.stride, c.pad, c.b, res, relu, y, stream_));
+    vdk_conv_desc d{};
+    d.x = x; d.batch = batch; d.H = H; d.W = W; d.IC = c.ic;
+    d.w = c.w; d.w_chunked = c.wc; d.OC = c.oc; d.KH = d.KW = c.k;
+    d.stride_h = d.stride_w = c.stride;
+    d.pad_h = d.pad_w = c.pad;
+    d.bias = c.b; d.residual = res; d.act = relu ? VDK_ACT_RELU : VDK_ACT_NONE; d.y = y; d.tile = -1;
+    check(vdk_conv2d_ex(&d, stream_));
     prof_end();
 }
 

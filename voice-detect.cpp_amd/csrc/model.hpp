@@ -129,6 +129,7 @@ private:
     struct Conv {
         int ic = 0, oc = 0, k = 0, stride = 1, pad = 0;
         void* w = nullptr;     // f16 [OC][K][K][IC]
+        void* wc = nullptr;    // chunk-major copy [IC/16][K*K][OC][16] (stride-1 3x3, OC % 128 == 0)
         float* b = nullptr;    // f32 [OC]
     };
     struct Block {

@@ -44,7 +44,7 @@ class ConvDesc(C.Structure):
                 ("y", _vp), ("y_stride", C.c_int), ("y_f32", C.c_int), ("y_time_major", C.c_int),
                 ("split", C.c_int), ("x_lo", C.c_int), ("res_lo", C.c_int), ("y_lo", C.c_int),
                 ("tile", C.c_int), ("res_f32", C.c_int), ("res_after_act", C.c_int), ("out_w", C.c_int),
-                ("in_scale", _vp), ("in_shift", _vp)]
+                ("in_scale", _vp), ("in_shift", _vp), ("w_chunked", _vp)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
@@ -111,6 +111,7 @@ _SIGS = {
     "vdk_conv2d_nhwc_tile": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int]),
     "vdk_conv2d_ex": (C.c_int, [C.POINTER(ConvDesc), _vp]),
+    "vdk_conv_pack_chunked": (None, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp]),
     "vdk_conv2d_tile_fits_ex": (C.c_int, [C.c_int, C.POINTER(ConvDesc)]),
     "vdk_conv2d_tile_count": (C.c_int, []),
     "vdk_conv2d_tile_fits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
