@@ -10,7 +10,13 @@ classifier; age/gender: wav2vec2-large-robust + two heads; B=64 x 3 s raw
 waveform, clips/s).
 
 A step is one batch; inputs are resident in HBM before the timed region.
-Prints one JSON line (rank 0, N=1).
+Prints one JSON line (rank 0, N=1).  Without --model the line's `value`,
+`roofline` and `cpu_baseline` are the headline workload's and `configs` carries
+every workload of the benchmark's config list, measured the same way in the
+same process: the batch-1 ResNet34 latency (median ms per clip, device-resident
+and host-buffer paths, beside the reference's published per-clip figures) and
+the ECAPA-TDNN, CAM++ and ERes2Net batches (throughput, dominant kernel's
+roofline fraction, a bounded CPU-baseline sample).
 
 `roofline` covers the dominant kernel: the conv class with the most time in a
 pass with HIP events around every launch (on the library's stream).  A second
@@ -55,6 +61,28 @@ TRAFFIC_BYTES_PER_LAUNCH = {
     # FETCH 23413 KiB x 2.00, WRITE 24000 KiB x 1.00
     ("resnet34", "conv3x3_s1_128to128"): 72.52e6,
 }
+
+# The reference's own published figures for these workloads (per clip, batch 1;
+# it publishes nothing batched): reported beside ours, not divided into them.
+REFERENCE_PUBLISHED = {
+    "resnet34_cpu_encoder_8t_emb_s": {
+        "value": 115.0, "unit": "embeddings/s",
+        "note": "WeSpeaker ResNet34 encoder only (FBank excluded), 3 s clip, ~8.7 ms at 8 threads on a Ryzen 9 "
+                "9950X3D, f32 blocked direct conv (docs/cpu-optimization.md:142-146)"},
+    "resnet34_b1_ms": [
+        {"value": 8.46, "unit": "ms per clip", "note": "ggml GPU backend (cuDNN conv), NVIDIA GB10, batch 1 "
+                                                       "(benchmarks/RESULTS.md:183-190)"},
+        {"value": 15.01, "unit": "ms per clip", "note": "wav -> embedding end to end, 8 threads, Ryzen 9 9950X3D "
+                                                        "(benchmarks/demo/spec.json:2-3)"}],
+    "per_clip_8t_ms": {"ecapa": 54.1, "resnet34": 56.1, "eres2net": 82.9, "campplus": 30.5,
+                       "note": "per-clip end to end at 8 threads, older build, Ryzen 9 9950X3D "
+                               "(benchmarks/RESULTS.md:163-170)"},
+    "gb10_b1_ms": {"ecapa": 8.92, "resnet34": 8.46, "eres2net": 10.06, "campplus": 15.74,
+                   "note": "ggml GPU backend, NVIDIA GB10, batch 1 (benchmarks/RESULTS.md:183-190)"},
+}
+
+# The workloads of the benchmark's config list beside the headline (ResNet34 B=64).
+CONFIG_SET = ("ecapa", "campplus", "eres2net")
 
 MODELS = {
     "resnet34": {
@@ -202,7 +230,10 @@ def cpu_baseline(model, gguf_path, pcm, n_seconds, min_seconds=10.0):
     return {"value": round(done / dt, 3), "unit": "embeddings/s", "cores": threads, "kind": "port",
             "sample": f"{done} clips (the batch's {len(pcm)} synthetic {n_seconds:g} s clips, cycled) through the "
                       f"oracle's FBank + encoder (f32), clip-parallel on {threads} threads, {dt:.1f} s wall; "
-                      f"host {cpu_name}, {avail} cores available"}
+                      f"host {cpu_name}, {avail} cores available",
+            "note": "the port is this repository's plain scalar C restatement of the reference's CPU path (the "
+                    "parity oracle), not the reference's AVX-512 blocked build, which the reference publishes at "
+                    "about 7x this rate for ResNet34 (see reference_published)"}
 
 
 def _cpu_name():
@@ -237,32 +268,14 @@ def cpu_baseline_w2v2(gguf_path, pcm, n_seconds, threads, avail, min_seconds):
                       f"host {_cpu_name()}, {avail} cores available"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--model", choices=sorted(MODELS), default="resnet34")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--registry", type=int, default=0,
-                    help="also time identify: the batch's embeddings scored against this many enrolled rows, top 10")
-    ap.add_argument("--copy-calibration-mib", type=int, default=0,
-                    help="after the bench, run 3 device-to-device copies of this many MiB (PMC traffic calibration)")
-    args = ap.parse_args()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
-              "clips are independent, so N GPUs would each run this same per-GPU batch.", file=sys.stderr)
-        sys.exit(2)
-    L = lib.lib()
-    if L.vdk_device_count() < 1:
-        print("bench.py: no HIP device visible", file=sys.stderr)
-        sys.exit(1)
-    model = MODELS[args.model]
+def measure(L, key, steps, warmup, cpu_seconds, registry=0, copy_mib=0, b1_reps=0):
+    """One workload: throughput over `steps` batches, a per-kernel events pass,
+    the dominant kernel's roofline from an events pass over its launches only,
+    the host-buffer rate, optionally the batch-1 latency and the CPU baseline."""
+    model = MODELS[key]
     batch, n = model["batch"], model["n"]
-
     tmp = tempfile.mkdtemp()
-    path = os.path.join(tmp, f"{args.model}.gguf")
+    path = os.path.join(tmp, f"{key}.gguf")
     model["write"](path, seed=model["seed"])
     ctx = lib.Context(path)
     pcm = synth.clips(CLIP_SEED, batch, n)
@@ -276,25 +289,24 @@ def main():
     else:
         run = lambda: ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         run()
     ctx.synchronize()
     lib.check(L.vdk_synchronize())
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         run()
     ctx.synchronize()
     lib.check(L.vdk_synchronize())
     elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
-    value = batch * args.steps / elapsed
+    ms_per_step = elapsed * 1e3 / steps
+    value = batch * steps / elapsed
     res = d_out.to_array(np.float32, (batch, width))
     assert np.all(np.isfinite(res))
     if not analyze:
         assert np.allclose(np.linalg.norm(res, axis=1), 1.0, atol=1e-4)
 
-    per, prof_ms = profile_pass(ctx, run, args.steps)
-    steps = args.steps
+    per, prof_ms = profile_pass(ctx, run, steps)
     conv = {"ms": 0.0, "flops": 0.0, "bytes": 0.0, "launches": 0}
     for name, p in per.items():
         if name.startswith("conv"):
@@ -318,11 +330,11 @@ def main():
     avg_s = sum(r[1] for r in recs) / nl * 1e-3
     fl = sum(r[2] for r in recs) / nl
     by = sum(r[3] for r in recs) / nl
-    if fl / by >= RIDGE_FLOP_PER_BYTE:
+    if by > 0 and fl / by >= RIDGE_FLOP_PER_BYTE:
         bound, achieved, peak, r_unit = "mfma", fl / avg_s / 1e12, PEAK_F16_TFLOPS, "TFLOP/s"
     else:
         bound, achieved, peak, r_unit = "hbm", by / avg_s / 1e9, PEAK_HBM_GBS, "GB/s"
-    traffic = TRAFFIC_BYTES_PER_LAUNCH.get((args.model, dom))
+    traffic = TRAFFIC_BYTES_PER_LAUNCH.get((key, dom))
     roofline = {
         "kernel": dom, "bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": r_unit,
         "frac": round(achieved / peak, 4), "traffic": traffic,
@@ -336,18 +348,13 @@ def main():
         "all_events_pass_ms_per_step": round(prof_ms, 4),
         "kernels": kernels,
     }
-    out = {
-        "metric": model["metric"], "value": round(value, 2), "unit": unit, "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": model["dtype"],
-        "data": "synthetic", "config": model["config"], "roofline": roofline,
-    }
+    out = {"value": round(value, 2), "unit": unit, "ms_per_step": round(ms_per_step, 4), "roofline": roofline}
     # the drop-in boundary hands over host PCM: the same batch through the
     # host-buffer entry point (H2D copy of the PCM and D2H of the embeddings
     # included), reported beside `value`, never as it
     host = (lambda: ctx.analyze_pcm(pcm)) if analyze else (lambda: ctx.embed_batch(pcm))
     host()
-    hs = min(args.steps, 10)
+    hs = min(steps, 10)
     t0 = time.perf_counter()
     for _ in range(hs):
         host()
@@ -355,13 +362,15 @@ def main():
     out["host_buffers"] = {"value": round(batch / dt, 2), "unit": unit, "ms_per_step": round(dt * 1e3, 4),
                            "note": ("voicedetect_gpu_analyze_pcm" if analyze else "voicedetect_capi_embed_pcm_batch") +
                                    ": host PCM in, host results out (PCIe included)"}
-    if args.registry > 0 and not analyze:
-        out["registry"] = registry_bench(L, d_out, batch, ctx.dim, args.registry, 10, args.steps)
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(model, path, pcm, n / 16000.0)
+    if b1_reps > 0 and not analyze:
+        out["batch1"] = batch1_latency(ctx, pcm[0], n, b1_reps)
+    if registry > 0 and not analyze:
+        out["registry"] = registry_bench(L, d_out, batch, ctx.dim, registry, 10, steps)
+    if cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_baseline(model, path, pcm, n / 16000.0, min_seconds=cpu_seconds)
     ctx.close()
-    if args.copy_calibration_mib > 0:
-        nb = args.copy_calibration_mib << 20
+    if copy_mib > 0:
+        nb = copy_mib << 20
         src, dst = lib.DeviceBuffer(nb), lib.DeviceBuffer(nb)
         lib.check(L.vdk_memset(src.ptr, 1, nb))
         for _ in range(3):
@@ -369,8 +378,99 @@ def main():
         lib.check(L.vdk_synchronize())
         print(f"copy calibration: 3 device copies of {nb} bytes", file=sys.stderr)
     for k in kernels:
-        print(f"  {k['name']:28s} x{k['launches_per_step']:3d} {k['ms_per_step']*1e3:9.1f} us/step "
-              f"{k['tflops'] or 0:8.1f} TFLOP/s {k['gbs'] or 0:8.1f} GB/s", file=sys.stderr)
+        print(f"  [{key}] {k['name']:28s} x{k['launches_per_step']:3d} {k['ms_per_step']*1e3:9.1f} us/step "
+              f"{k['tflops'] or 0:8.1f} TFLOP/s {k['gbs'] or 0:8.1f} GB/s", file=sys.stderr, flush=True)
+    return out
+
+
+def batch1_latency(ctx, clip, n, reps):
+    """One clip per call: the device-resident path (PCM already in HBM, the
+    embedding left there; the call returns once the stream has finished) and
+    the host-buffer path voicedetect_capi_embed_pcm (PCM in and embedding out
+    through host memory); median and 90th percentile over `reps` calls."""
+    d_pcm = lib.DeviceBuffer.from_array(clip[None])
+    d_out = lib.DeviceBuffer(ctx.dim * 4)
+    dev, hst = [], []
+    for i in range(reps + 5):
+        t0 = time.perf_counter()
+        ctx.embed_device_async(d_pcm.ptr, 1, n, d_out.ptr)
+        ctx.synchronize()
+        t1 = time.perf_counter()
+        ctx.embed_pcm(clip)
+        t2 = time.perf_counter()
+        if i >= 5:
+            dev.append((t1 - t0) * 1e3)
+            hst.append((t2 - t1) * 1e3)
+    med = float(np.median(dev))
+    return {"device_ms_median": round(med, 4), "device_ms_p90": round(float(np.percentile(dev, 90)), 4),
+            "host_ms_median": round(float(np.median(hst)), 4), "host_ms_p90": round(float(np.percentile(hst, 90)), 4),
+            "clips_per_s": round(1e3 / med, 1), "calls": reps,
+            "reference_published": REFERENCE_PUBLISHED["resnet34_b1_ms"]}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--model", choices=sorted(MODELS), default=None,
+                    help="one workload only (default: the ResNet34 B=64 headline plus the config set)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="wall time of the headline's CPU-baseline sample (the config set's get half)")
+    ap.add_argument("--registry", type=int, default=0,
+                    help="also time identify: the batch's embeddings scored against this many enrolled rows, top 10")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after the bench, run 3 device-to-device copies of this many MiB (PMC traffic calibration)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "clips are independent, so N GPUs would each run this same per-GPU batch.", file=sys.stderr)
+        sys.exit(2)
+    L = lib.lib()
+    if L.vdk_device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    key = args.model or "resnet34"
+    cpu_s = 0.0 if args.no_cpu_baseline else args.cpu_seconds
+    head = measure(L, key, args.steps, args.warmup, cpu_s, registry=args.registry,
+                   copy_mib=args.copy_calibration_mib, b1_reps=50 if key == "resnet34" else 0)
+    model = MODELS[key]
+    out = {
+        "metric": model["metric"], "value": head["value"], "unit": head["unit"], "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": model["dtype"],
+        "data": "synthetic", "config": model["config"], "roofline": head["roofline"],
+        "host_buffers": head["host_buffers"],
+    }
+    for k in ("registry", "cpu_baseline"):
+        if k in head:
+            out[k] = head[k]
+    if "cpu_baseline" in out and key == "resnet34":
+        out["cpu_baseline"]["reference_published"] = REFERENCE_PUBLISHED["resnet34_cpu_encoder_8t_emb_s"]
+    if args.model is None:
+        # every workload of the config list, measured the same way
+        cfgs = [{"config": "ResNet34 batch 1 x 3 s (latency)", "model": "resnet34", "batch": 1, **head["batch1"]},
+                {"config": "ResNet34 batch 64 x 3 s (the headline above)", "model": "resnet34", "batch": 64,
+                 "value": head["value"], "unit": head["unit"], "ms_per_step": head["ms_per_step"],
+                 "dominant_kernel": head["roofline"]["kernel"], "roofline_frac": head["roofline"]["frac"]}]
+        for ck in CONFIG_SET:
+            r = measure(L, ck, max(10, args.steps // 2), args.warmup, cpu_s / 2)
+            m = MODELS[ck]
+            e = {"config": m["config"]["workload"], "model": ck, "batch": m["batch"], "dtype": m["dtype"],
+                 "value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
+                 "dominant_kernel": r["roofline"]["kernel"], "roofline": {
+                     k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "avg_launch_us")},
+                 "all_conv_frac": r["roofline"]["all_conv"]["frac"], "host_buffers": r["host_buffers"]["value"],
+                 "reference_published_ms_per_clip": {"cpu_8t": REFERENCE_PUBLISHED["per_clip_8t_ms"][ck],
+                                                     "gb10_b1": REFERENCE_PUBLISHED["gb10_b1_ms"][ck]}}
+            if "cpu_baseline" in r:
+                e["cpu_baseline"] = r["cpu_baseline"]
+            cfgs.append(e)
+        out["configs"] = cfgs
+        out["reference_published_sources"] = {k: v for k, v in REFERENCE_PUBLISHED.items()
+                                              if k in ("per_clip_8t_ms", "gb10_b1_ms")}
     print(json.dumps(out), flush=True)
 
 

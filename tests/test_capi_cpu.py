@@ -289,3 +289,17 @@ def test_analyze_model_host_side(tmp_path):
         assert L.voicedetect_capi_analyze_path_json(ctx.ctx, b"/nonexistent.wav") is None
         assert "failed to load audio" in ctx.last_error()
         ctx.close()
+
+
+def test_conv_pack_chunked_layout():
+    """vdk_conv_pack_chunked: [OC][KH][KW][IC] -> [IC/16][KH*KW][OC][16], element
+    (oc, tap, ic) at ((ic // 16) * taps + tap) * OC * 16 + oc * 16 + ic % 16."""
+    L = lib.lib()
+    OC, KH, KW, IC = 96, 3, 3, 48
+    w = np.random.default_rng(5).integers(0, 65536, (OC, KH, KW, IC), dtype=np.uint16)
+    out = np.zeros(w.size, dtype=np.uint16)
+    L.vdk_conv_pack_chunked(w.ctypes.data, OC, KH, KW, IC, out.ctypes.data)
+    want = w.reshape(OC, KH * KW, IC // 16, 16).transpose(2, 1, 0, 3).reshape(-1)
+    assert np.array_equal(out, want)
+    oc, tap, ic = 37, 5, 33
+    assert out[((ic // 16) * 9 + tap) * OC * 16 + oc * 16 + ic % 16] == w[oc, tap // 3, tap % 3, ic]

@@ -216,6 +216,47 @@ def test_conv_register_weight_tiles_plain_epilogues(case):
     assert n >= 1
 
 
+@pytest.mark.parametrize("shape", [(2, 7, 75, 128, True), (3, 20, 75, 128, False), (1, 6, 40, 256, True)])
+def test_conv_chunked_weights_bitwise(shape):
+    """A conv given the chunk-major weight copy (vdk_conv_pack_chunked) as
+    w_chunked returns the same bits as without it, on every tile that fits
+    (the band kernels stream it; the others ignore it)."""
+    L = lib.lib()
+    B, H, W, C, with_res = shape
+    rng = np.random.default_rng(B * 100 + H + W + C)
+    x = np.maximum(rng.standard_normal((B, H, W, C)), 0).astype(np.float16)
+    w = (rng.standard_normal((C, 3, 3, C)) * np.sqrt(2.0 / (9 * C))).astype(np.float16)
+    b = rng.uniform(-0.1, 0.1, C).astype(np.float32)
+    res = rng.standard_normal((B, H, W, C)).astype(np.float16) if with_res else None
+    wc = np.zeros(w.size, dtype=np.uint16)
+    L.vdk_conv_pack_chunked(w.view(np.uint16).ctypes.data, C, 3, 3, C, wc.ctypes.data)
+    dx, dw, dwc, db = (lib.DeviceBuffer.from_array(a) for a in (x, w, wc, b))
+    dr = lib.DeviceBuffer.from_array(res) if with_res else None
+    n = 0
+    for t in range(L.vdk_conv2d_tile_count()):
+        if not tile_fits(t, B, H, W, C, C, 3, 1, 1, residual=with_res):
+            continue
+        outs = []
+        for chunked in (False, True):
+            d = lib.ConvDesc()
+            d.x, d.batch, d.H, d.W, d.IC = dx.ptr, B, H, W, C
+            d.w, d.OC, d.KH, d.KW = dw.ptr, C, 3, 3
+            d.stride_h = d.stride_w = 1
+            d.pad_h = d.pad_w = 1
+            d.bias, d.act, d.tile = db.ptr, lib.ACT_RELU, t
+            d.residual = dr.ptr if dr else None
+            d.w_chunked = dwc.ptr if chunked else None
+            dy = lib.DeviceBuffer(B * H * W * C * 2)
+            d.y = dy.ptr
+            announce(f"chunked weights tile {t} shape {shape} chunked={chunked}")
+            lib.check(L.vdk_conv2d_ex(d, None))
+            lib.check(L.vdk_synchronize())
+            outs.append(dy.to_array(np.uint16, (B, H, W, C)))
+        assert np.array_equal(outs[0], outs[1]), f"tile {t}"
+        n += 1
+    assert n >= 2
+
+
 def test_conv_invariants_delta_and_zero():
     rng = np.random.default_rng(9)
     x = rng.standard_normal((2, 6, 70, 32)).astype(np.float16)
