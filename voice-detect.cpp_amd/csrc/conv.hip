@@ -1559,49 +1559,59 @@ void launch_band(const ConvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// conv3x3_band3_kernel: the band scheme (a workgroup per band of TH full rows
-// x 128 output channels, flattened 32-pixel MFMA blocks, halo + weights DMA'd
-// per 16-channel chunk) with
-//  * 8 waves = 2 channel groups x 4 pixel groups, each wave holding a 64 x
-//    (32 NJ) tile: per tap 2 A and NJ B fragment reads feed 2 NJ MFMAs
-//    (5 reads per 6 MFMAs at NJ = 3, against 7 per 6 with 32-channel waves);
-//  * a 3-stage ring: chunk k+2 is DMA'd while chunk k computes, and each wave
-//    waits only for its own chunk-k loads (a counted vmcnt) before the one
-//    barrier per chunk;
-//  * halo rows of 32 bytes (16 channels) with the two 16-byte halves swapped
-//    on every other group of 8 rows, so the 16 lanes of a B read (16
-//    consecutive halo rows) cover all 64 banks; three stages then fit in LDS;
-//  * the residual tile DMA'd into the two stages the last chunk leaves free,
-//    while the last chunk computes, so the epilogue reads it from LDS; the
-//    finished f16 values are written back over it and leave as 16-byte
-//    channel rows.
-// Products and sums are the other conv kernels' (f16 x f16 -> f32 in tap-major,
-// channel-minor order, then + bias, + residual, act).
+// conv3x3_bandws_kernel: stride-1 3x3 conv (pad 1) for maps up to MAXW wide
+// and OC % 128 == 0, one workgroup per band of TH full rows x 128 output
+// channels (flattened 32-pixel MFMA blocks), with the waves split by role:
+//  * NCW compute waves in a WMG x WNG grid, each holding 4/WMG 32-channel A
+//    blocks x NJ 32-pixel B blocks of accumulators; they only read LDS and
+//    run MFMAs, never a global load, so no MFMA stream stalls behind the
+//    memory queue;
+//  * NP producer waves that move all data: per 16-channel chunk the 9 taps'
+//    weights of the 128 channels and the band's input halo, DMA'd
+//    (buffer_load ... lds) two chunks ahead into a 3-stage ring, and the
+//    residual tile, in two halves, into the two stages the last chunks free;
+//  * one barrier per chunk, reached by producers once their own chunk-k loads
+//    have landed and by compute waves once they have finished chunk k-1;
+//  * halo rows of 32 bytes (16 channels) whose 16-byte halves swap on every
+//    other group of 8 rows, so the 16 lanes of a B read cover all 64 banks;
+//  * weights read from the chunk-major copy ([IC/16][9][OC][16],
+//    vdk_conv_desc.w_chunked) when there is one, so a DMA instruction's 64
+//    slots are one contiguous kilobyte instead of pieces of 32 cache lines;
+//  * accumulators that start at the bias; the residual added by two MFMAs per
+//    32x32 block with identity A operands (products r x 1, one rounding of
+//    acc + r), then [ReLU], f16, written over the residual rows, and stored
+//    as 16-byte channel chunks.
+// Products are f16 x f16 with f32 accumulation in tap-major, channel-minor
+// order, like the other conv kernels, with the bias entering first.
 // ---------------------------------------------------------------------------
-template <int TH, int NJ, int MAXW>
-struct Band3Tile {
-    static constexpr int NW = 8, OCB = 128, WNG = 4;                  // waves, channels, pixel groups
+template <int TH, int MAXW, int WMG, int WNG, int NJ, int NP>
+struct BandWsTile {
+    static constexpr int OCB = 128, NCW = WMG * WNG, MI = 4 / WMG, NW = NCW + NP;
     static constexpr int NB = WNG * NJ;                               // 32-pixel blocks per band
     static constexpr int A_BYTES = 9 * OCB * 32, A_INS = A_BYTES / 1024;
     static constexpr int HWM = MAXW + 2, XPIX = (TH + 2) * HWM;      // halo pixels (widest map)
     static constexpr int X_INS = (XPIX * 2 + 63) / 64;                // 32-byte rows = two 16-byte slots
-    static constexpr int INS = A_INS + X_INS, IPW = (INS + NW - 1) / NW;
     static constexpr int STAGE = A_BYTES + X_INS * 1024;
     static constexpr int RRB = 272, SPR = RRB / 16;                   // residual rows: 128 channels + 16 B
     static constexpr int HALF_ROWS = NB * 16;                         // residual rows per free stage
     static constexpr int R_INS = (HALF_ROWS * SPR + 63) / 64;         // DMA instructions per half
-    static constexpr int LDS = 3 * STAGE + OCB * 4;                   // + the bias
-    static_assert(LDS <= 163840, "three stages and the bias fit the 160 KB of LDS");
+    static constexpr int XPP = (X_INS + NP - 1) / NP, RPP = (R_INS + NP - 1) / NP;
+    static constexpr int CPR = MI * 4;                                // 16-byte output chunks per row and wave
+    static_assert(WMG * MI == 4, "the channel groups cover the 128 channels");
+    static_assert(3 * STAGE <= 163840, "three stages fit the 160 KB of LDS");
     static_assert(R_INS * 1024 <= STAGE, "half the residual tile fits one stage");
     static_assert(NB * 32 >= TH * MAXW, "the band's pixel blocks cover TH rows");
+    static_assert(A_INS % NP == 0, "the weight instructions split evenly over the producers");
 };
 
-// Row address of band pixel row pr in the residual / staging tile, whose two
-// halves sit in the two free stages.
-template <int TH, int NJ, int MAXW>
-__device__ __forceinline__ uint8_t* band3_rrow(uint8_t* r0, uint8_t* r1, int pr) {
-    using G = Band3Tile<TH, NJ, MAXW>;
-    return pr < G::HALF_ROWS ? r0 + pr * G::RRB : r1 + (pr - G::HALF_ROWS) * G::RRB;
+// Global byte offset of weight slot p (row p/2 = (tap, oc), 16-byte half
+// p & 1, swapped on odd groups of 8 rows) of 16-channel chunk c0, from the
+// chunk-major copy or the plain [OC][3][3][IC] layout.
+__device__ __forceinline__ uint32_t band_woff(int p, int c0, int oc0, int IC, int OC, bool chunked) {
+    const int row = p >> 1, tap = row >> 7, oc = row & 127;
+    const int half = (p & 1) ^ ((row >> 3) & 1);
+    return chunked ? (uint32_t)((((c0 >> 4) * 9 + tap) * OC + oc0 + oc) * 32 + half * 16)
+                   : (uint32_t)((((oc0 + oc) * 9 + tap) * IC + c0) * 2 + half * 16);
 }
 
 // n / d for 0 <= n < 2^20 and d >= 1, given inv_d = 1 / d: (n + 1/2) / d lies
@@ -1610,288 +1620,11 @@ __device__ __forceinline__ int div_small(int n, float inv_d) {
     return (int)(((float)n + 0.5f) * inv_d);
 }
 
-// Global byte offset of weight slot p (row p/2 = (tap, oc), 16-byte half
-// p & 1, swapped on odd groups of 8 rows) of 16-channel chunk c0.  Chunked
-// weights ([IC/16][9][OC][16], w_chunked) make a DMA instruction's 64 slots
-// one contiguous kilobyte; the plain [OC][3][3][IC] layout spreads them over
-// 32 cache lines.
-__device__ __forceinline__ uint32_t band3_woff(int p, int c0, int oc0, int IC, int OC, bool chunked) {
-    const int row = p >> 1, tap = row >> 7, oc = row & 127;
-    const int half = (p & 1) ^ ((row >> 3) & 1);
-    return chunked ? (uint32_t)((((c0 >> 4) * 9 + tap) * OC + oc0 + oc) * 32 + half * 16)
-                   : (uint32_t)((((oc0 + oc) * 9 + tap) * IC + c0) * 2 + half * 16);
-}
-
-// DMA instruction i of this wave for a 16-channel chunk into stage nx:
-// instructions wave, wave + 8, ... < A_INS are weight slots, the rest halo.
-template <int TH, int NJ, int MAXW>
-__device__ __forceinline__ void band3_issue_one(int i, uint8_t* __restrict__ nx, int c0n, int oc0, const ConvArgs& a,
-                                                bool chunked, const int* xoff, __amdgpu_buffer_rsrc_t wr,
-                                                __amdgpu_buffer_rsrc_t xr, int wave, int lane) {
-    using G = Band3Tile<TH, NJ, MAXW>;
-    const int ins = wave + i * G::NW;
-    if (ins >= G::INS) return;
-    if (ins < G::A_INS) {
-        const uint32_t off = band3_woff(ins * 64 + lane, c0n, oc0, a.IC, a.OC, chunked);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(nx + ins * 1024), 16, off, 0, 0, 0);
-    } else {
-        const uint32_t off = xoff[i] < 0 ? kOOB : (uint32_t)(xoff[i] + c0n * 2);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(nx + ins * 1024), 16, off, 0, 0, 0);
-    }
-}
-
-// Residual DMA instruction i of this wave (rows of 128 channels + 16 bytes,
-// the first half of the band's rows into nx, the second into nx2); the slot's
-// source offset is worked out here, in the one chunk that issues these.
-template <int TH, int NJ, int MAXW>
-__device__ __forceinline__ void band3_issue_res(int i, uint8_t* __restrict__ nx, uint8_t* __restrict__ nx2,
-                                                const ConvArgs& a, int b, int r0, int oc0, float inv_w,
-                                                __amdgpu_buffer_rsrc_t rr, int wave, int lane) {
-    using G = Band3Tile<TH, NJ, MAXW>;
-    const int ins = wave + i * G::NW;
-    if (ins >= 2 * G::R_INS) return;
-    const bool second = ins >= G::R_INS;
-    const int sl = (second ? ins - G::R_INS : ins) * 64 + lane;
-    const int pr = (second ? G::HALF_ROWS : 0) + sl / G::SPR, ch = sl % G::SPR;
-    const int r = div_small(pr, inv_w), c = pr - r * a.W;
-    const bool ok = ch < 16 && pr < TH * a.W && r0 + r < a.H;
-    const uint32_t off = ok ? (uint32_t)(((((size_t)(b * a.H + r0 + r) * a.W + c) * a.rs + oc0) * 2) + ch * 16) : kOOB;
-    uint8_t* dst = second ? nx2 + (ins - G::R_INS) * 1024 : nx + ins * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void*)dst, 16, off, 0, 0, 0);
-}
-
-// One chunk: 9 taps x 2 NJ MFMAs; the next tap's 2 + NJ fragment reads are
-// interleaved between this tap's MFMAs (double-buffered registers), and the
-// DMA this chunk starts (mode 1: the chunk two ahead into nx; mode 2: the
-// residual tile into nx / nx2) goes out one or two instructions per tap, so
-// no wave stalls its MFMA stream behind a full memory queue.  B fragment
-// addresses are formed per read from the lane's halo row qb[j] at tap (0, 0)
-// and the tap's row offset.  The DMA targets are distinct __restrict__ views,
-// so the reads of `cur` are not made to wait for them.
-template <int TH, int NJ, int MAXW>
-__device__ __forceinline__ void band3_chunk(const uint8_t* __restrict__ cur, uint8_t* __restrict__ nx,
-                                            uint8_t* __restrict__ nx2, int mode, int c0n, int oc0, const ConvArgs& a,
-                                            bool chunked, const int* xoff, int b, int r0, float inv_w,
-                                            __amdgpu_buffer_rsrc_t wr, __amdgpu_buffer_rsrc_t xr,
-                                            __amdgpu_buffer_rsrc_t rr, int abase, const int* qb, int lhalf,
-                                            float16v (*acc)[NJ], int wave, int lane) {
-    using G = Band3Tile<TH, NJ, MAXW>;
-    constexpr int RI = (2 * G::R_INS + G::NW - 1) / G::NW;
-    static_assert(G::IPW <= 9 && RI <= 18, "the chunk's DMA fits one or two instructions per tap");
-    const uint8_t* const xs = cur + G::A_BYTES;
-    const int HW = a.W + 2;
-    int qv[NJ];   // the halo bases behind an empty asm per chunk, so the addresses are not hoisted and spilled
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        qv[j] = qb[j];
-        asm volatile("" : "+v"(qv[j]));
-    }
-    half8 af[2][2], bf[2][NJ];
-    auto load = [&](int tap, int buf) {
-        const int toff = (tap / 3) * HW + tap % 3;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            af[buf][i] = *reinterpret_cast<const half8*>(cur + abase + tap * (G::OCB * 32) + i * 1024);
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int q = qv[j] + toff;
-            bf[buf][j] = *reinterpret_cast<const half8*>(xs + q * 32 + ((((q >> 3) ^ lhalf) & 1) << 4));
-        }
-    };
-    load(0, 0);
-#pragma unroll
-    for (int tap = 0; tap < 9; ++tap) {
-        const int c = tap & 1;
-        if (tap + 1 < 9) load(tap + 1, c ^ 1);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
-        // one MFMA, then one fragment read (with its address VALU), in turn
-        if (tap + 1 < 9) {
-#pragma unroll
-            for (int k = 0; k < 2 + NJ; ++k) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU (address)
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 2 * NJ - (2 + NJ), 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (mode == 1) {
-            if (tap < G::IPW) band3_issue_one<TH, NJ, MAXW>(tap, nx, c0n, oc0, a, chunked, xoff, wr, xr, wave, lane);
-        } else if (mode == 2) {
-            if (2 * tap < RI) band3_issue_res<TH, NJ, MAXW>(2 * tap, nx, nx2, a, b, r0, oc0, inv_w, rr, wave, lane);
-            if (2 * tap + 1 < RI)
-                band3_issue_res<TH, NJ, MAXW>(2 * tap + 1, nx, nx2, a, b, r0, oc0, inv_w, rr, wave, lane);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-template <int TH, int NJ, int MAXW>
-__global__ __launch_bounds__(512) void conv3x3_band3_kernel(ConvArgs a) {
-    using G = Band3Tile<TH, NJ, MAXW>;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[G::LDS];
-    float* const sbias = reinterpret_cast<float*>(smem + 3 * G::STAGE);
-    uint8_t* const st0 = smem;
-    uint8_t* const st1 = smem + G::STAGE;
-    uint8_t* const st2 = smem + 2 * G::STAGE;
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lrow = lane & 31, lhalf = lane >> 5;
-    const int H = a.H, W = a.W, IC = a.IC, HW = W + 2;
-    const int bands = (H + TH - 1) / TH;
-    const int b = blockIdx.x / bands, r0 = (blockIdx.x - b * bands) * TH;
-    const int oc0 = blockIdx.y * G::OCB;
-    const int og = wave & 1, pg = wave >> 1;          // 64-channel group, pixel group
-    const int npx = TH * W;                           // band pixels (rows past H are computed and dropped)
-    const bool has_res = a.res != nullptr;
-    const bool chunked = a.wc != nullptr;
-    const float inv_w = 1.0f / (float)W, inv_hw = 1.0f / (float)HW;
-
-    // the first two chunks go out before the rest of the set-up
-    int xoff[G::IPW];   // this lane's halo slots as byte offsets at channel 0
-#pragma unroll
-    for (int i = 0; i < G::IPW; ++i) {
-        const int ins = wave + i * G::NW;
-        xoff[i] = -1;
-        if (ins >= G::A_INS && ins < G::INS) {
-            const int s = (ins - G::A_INS) * 64 + lane;
-            const int q = s >> 1, hr = div_small(q, inv_hw), hc = q - hr * HW;
-            const int ghalf = (s & 1) ^ ((q >> 3) & 1);
-            const int ih = r0 - 1 + hr, iw = hc - 1;
-            if (hr < TH + 2 && ih >= 0 && ih < H && iw >= 0 && iw < W)
-                xoff[i] = (int)(((size_t)(b * H + ih) * W + iw) * a.xs * 2) + ghalf * 16;
-        }
-    }
-    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(chunked ? a.wc : a.w), 0, (int)((size_t)a.OC * 9 * IC * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t xr =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + IC) * 2), 0x00020000);
-    const int nk = IC / 16;
-#pragma unroll
-    for (int i = 0; i < G::IPW; ++i) band3_issue_one<TH, NJ, MAXW>(i, st0, 0, oc0, a, chunked, xoff, wr, xr, wave, lane);
-    if (nk > 1) {
-#pragma unroll
-        for (int i = 0; i < G::IPW; ++i)
-            band3_issue_one<TH, NJ, MAXW>(i, st1, 16, oc0, a, chunked, xoff, wr, xr, wave, lane);
-    }
-
-    if (tid < G::OCB) sbias[tid] = a.bias ? a.bias[oc0 + tid] : 0.0f;
-    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(has_res ? a.res : a.x), 0, has_res ? (int)(((size_t)(a.npix - 1) * a.rs + a.OC) * 2) : 0, 0x00020000);
-    // operand reads: A row (tap, og*64 + i*32 + lrow), halves swapped on odd
-    // groups of 8 rows; B halo row q = qb[j] + (kh * HW + kw) of pixel
-    // p = block*32 + lrow, halves swapped on odd groups of 8 halo rows
-    const int abase = (og * 64 + lrow) * 32 + ((lhalf ^ ((lrow >> 3) & 1)) * 16);
-    int qb[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        int p = (pg * NJ + j) * 32 + lrow;
-        if (p >= npx) p = 0;   // masked lane: any valid row, result dropped
-        const int r = div_small(p, inv_w), c = p - r * W;
-        qb[j] = r * HW + c;
-    }
-
-    float16v acc[2][NJ];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    // this wave's DMA instructions per chunk (for the counted wait)
-    const int nins = (G::INS - wave + G::NW - 1) / G::NW;
-    auto stage = [&](int k) { const int m = k % 3; return m == 0 ? st0 : (m == 1 ? st1 : st2); };
-#pragma unroll 1
-    for (int k = 0; k < nk; ++k) {
-        // chunk k has landed for this wave (chunk k+1's loads may still be in
-        // flight), then for every wave, and chunk k-1's reads are done, which
-        // frees its stage for chunk k+2
-        wait_vmcnt_le(k + 1 < nk ? nins : 0);
-        lds_barrier();
-        const int mode = k + 2 < nk ? 1 : (k + 1 == nk && has_res ? 2 : 0);
-        band3_chunk<TH, NJ, MAXW>(stage(k), stage(k + 2), stage(k + 1), mode, (k + 2) * 16, oc0, a, chunked, xoff, b,
-                                  r0, inv_w, wr, xr, rr, abase, qb, lhalf, acc, wave, lane);
-    }
-
-    // Epilogue.  The residual rows (or nothing) sit in the two stages after
-    // the last chunk's; each wave finishes its 2 x NJ blocks in the MFMA
-    // layout (register g*4+e of a lane: channel 8g + 4*lhalf + e of its 32-row
-    // block, pixel lrow of the column block), writes the f16 results over the
-    // residual values it read, and then stores its 64-channel halves of the
-    // pixel rows as 16-byte chunks (8 lanes per pixel).
-    uint8_t* const rs0 = stage(nk + 1);   // the stages of chunks nk-2 and nk-3, free since the last barrier
-    uint8_t* const rs1 = stage(nk);
-    if (has_res) {
-        __builtin_amdgcn_s_waitcnt(0);
-        lds_barrier();
-    }
-    const bool relu = a.act == VDK_ACT_RELU;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int cw = og * 64 + i * 32;               // block's first channel within the 128
-        float bias[16];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const float4v bv = *reinterpret_cast<const float4v*>(sbias + cw + g * 8 + lhalf * 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) bias[g * 4 + e] = bv[e];
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int pr = (pg * NJ + j) * 32 + lrow;
-            uint8_t* const row = band3_rrow<TH, NJ, MAXW>(rs0, rs1, pr) + (cw + lhalf * 4) * 2;
-            half4 r4[4];
-#pragma unroll
-            for (int g = 0; g < 4; ++g) r4[g] = has_res ? *reinterpret_cast<const half4*>(row + g * 16) : half4{};
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                half4 h;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float v = acc[i][j][g * 4 + e] + bias[g * 4 + e] + (float)r4[g][e];
-                    h[e] = (half_t)(relu ? fmaxf(v, 0.0f) : v);
-                }
-                *reinterpret_cast<half4*>(row + g * 16) = h;
-            }
-        }
-    }
-    half_t* const y = static_cast<half_t*>(a.y) + oc0 + og * 64;
-    constexpr int NST = NJ * 32 * 8 / 64;             // 16-byte stores per wave
-    const int ch = lane & 7;
-#pragma unroll
-    for (int it = 0; it < NST; ++it) {
-        const int pr = pg * NJ * 32 + it * 8 + (lane >> 3);
-        const half8 v8 = *reinterpret_cast<const half8*>(band3_rrow<TH, NJ, MAXW>(rs0, rs1, pr) + og * 128 + ch * 16);
-        const int r = div_small(pr, inv_w), c = pr - r * W;
-        if (pr < npx && r0 + r < H)
-            *reinterpret_cast<half8*>(y + ((size_t)(b * H + r0 + r) * W + c) * a.ys + ch * 8) = v8;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// conv3x3_bandws_kernel: the band3 geometry, ring and epilogue with the
-// waves split by role.  Waves 0-7 (two per SIMD) only compute: band3's
-// 64-channel x NJ-block wave tiles, fed from LDS, never issuing a global
-// load, so no MFMA stream stalls behind the memory queue.  Waves 8-11 (one
-// per SIMD) only move data: the ring's chunk DMA two chunks ahead and the
-// residual tile, in two halves, into the stages the last two chunks free.
-// Both roles meet at the same one barrier per chunk (producers after their
-// own chunk-k loads have landed, compute waves after finishing chunk k-1).
-// ---------------------------------------------------------------------------
-template <int TH, int NJ, int MAXW>
-__global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
-    using G = Band3Tile<TH, NJ, MAXW>;
-    constexpr int NP = 4;                             // producer waves
-    constexpr int XPP = (G::X_INS + NP - 1) / NP;     // halo instructions per producer and chunk
-    constexpr int RPP = (G::R_INS + NP - 1) / NP;     // residual instructions per producer and half
-    static_assert(G::A_INS % NP == 0, "the weight instructions split evenly over the producers");
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[G::LDS];
+template <int TH, int MAXW, int WMG, int WNG, int NJ, int NP>
+__global__ __launch_bounds__((WMG * WNG + NP) * 64) void conv3x3_bandws_kernel(ConvArgs a) {
+    using G = BandWsTile<TH, MAXW, WMG, WNG, NJ, NP>;
+    constexpr int MI = G::MI;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * G::STAGE];
     uint8_t* const st0 = smem;
     uint8_t* const st1 = smem + G::STAGE;
     uint8_t* const st2 = smem + 2 * G::STAGE;
@@ -1909,15 +1642,16 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
     const int nk = IC / 16;
     uint8_t* const rs0 = stage(nk);                   // residual rows [0, HALF_ROWS): free from chunk nk-2 on
     uint8_t* const rs1 = stage(nk + 1);               // the other half: free from chunk nk-1 on
+    auto rrow = [&](int pr) { return pr < G::HALF_ROWS ? rs0 + pr * G::RRB : rs1 + (pr - G::HALF_ROWS) * G::RRB; };
 
-    if (wave >= G::NW) {
+    if (wave >= G::NCW) {
         // ---------------- producers ----------------
-        const int p = wave - G::NW;
+        const int p = wave - G::NCW;
         const bool chunked = a.wc != nullptr;
         const float inv_hw = 1.0f / (float)HW;
-        int xoff[XPP];
+        int xoff[G::XPP];   // this lane's halo slots as byte offsets at channel 0
 #pragma unroll
-        for (int i = 0; i < XPP; ++i) {
+        for (int i = 0; i < G::XPP; ++i) {
             const int xi = p + NP * i;
             xoff[i] = -1;
             if (xi < G::X_INS) {
@@ -1938,10 +1672,10 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
             for (int i = 0; i < G::A_INS / NP; ++i) {
                 const int ins = p + NP * i;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    wr, (lds_void*)(nx + ins * 1024), 16, band3_woff(ins * 64 + lane, c0, oc0, IC, a.OC, chunked), 0, 0, 0);
+                    wr, (lds_void*)(nx + ins * 1024), 16, band_woff(ins * 64 + lane, c0, oc0, IC, a.OC, chunked), 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < XPP; ++i) {
+            for (int i = 0; i < G::XPP; ++i) {
                 const int xi = p + NP * i;
                 if (xi < G::X_INS) {
                     const uint32_t off = xoff[i] < 0 ? kOOB : (uint32_t)(xoff[i] + c0 * 2);
@@ -1954,7 +1688,7 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
             const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
                 (void*)a.res, 0, (int)(((size_t)(a.npix - 1) * a.rs + a.OC) * 2), 0x00020000);
 #pragma unroll
-            for (int i = 0; i < RPP; ++i) {
+            for (int i = 0; i < G::RPP; ++i) {
                 const int ri = p + NP * i;
                 if (ri < G::R_INS) {
                     const int sl = ri * 64 + lane;
@@ -1967,7 +1701,7 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
                 }
             }
         };
-        const int nper = G::A_INS / NP + (p + NP * (XPP - 1) < G::X_INS ? XPP : XPP - 1);   // loads per chunk
+        const int nper = G::A_INS / NP + (p + NP * (G::XPP - 1) < G::X_INS ? G::XPP : G::XPP - 1);   // per chunk
         // chunk 0 alone goes out first, so the compute waves start as soon as
         // it has landed; chunks 1 and 2 follow together after the first
         // barrier, then the ring keeps two chunks ahead
@@ -1990,8 +1724,11 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
 
     // ---------------- compute waves ----------------
     const int lrow = lane & 31, lhalf = lane >> 5;
-    const int og = wave & 1, pg = wave >> 1;          // 64-channel group, pixel group
-    const int abase = (og * 64 + lrow) * 32 + ((lhalf ^ ((lrow >> 3) & 1)) * 16);
+    const int og = wave % WMG, pg = wave / WMG;       // channel group, pixel group
+    const int cg0 = og * MI * 32;                     // the group's first channel within the 128
+    // A row (tap, cg0 + i*32 + lrow) with its halves swapped on odd groups of 8
+    // rows; B halo row q = qb[j] + (kh * HW + kw) of pixel p = block*32 + lrow
+    const int abase = (cg0 + lrow) * 32 + ((lhalf ^ ((lrow >> 3) & 1)) * 16);
     int qb[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -2002,14 +1739,13 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
     }
     // the accumulators start at the bias (register g*4+e of a lane: channel
     // 8g + 4*lhalf + e of its 32-row block)
-    float16v acc[2][NJ];
+    float16v acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < MI; ++i) {
         float16v bv;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const float4v v = a.bias ? *reinterpret_cast<const float4v*>(a.bias + oc0 + og * 64 + i * 32 + g * 8 +
-                                                                          lhalf * 4)
+            const float4v v = a.bias ? *reinterpret_cast<const float4v*>(a.bias + oc0 + cg0 + i * 32 + g * 8 + lhalf * 4)
                                      : float4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int e = 0; e < 4; ++e) bv[g * 4 + e] = v[e];
@@ -2027,11 +1763,11 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
         // (base + tap offset) addresses are hoisted out of the loop and spill
 #pragma unroll
         for (int j = 0; j < NJ; ++j) asm volatile("" : "+v"(qb[j]));
-        half8 af[2][2], bf[2][NJ];
+        half8 af[2][MI], bf[2][NJ];
         auto load = [&](int tap, int buf) {
             const int toff = (tap / 3) * HW + tap % 3;
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < MI; ++i)
                 af[buf][i] = *reinterpret_cast<const half8*>(cur + abase + tap * (G::OCB * 32) + i * 1024);
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
@@ -2045,30 +1781,28 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
             const int c = tap & 1;
             if (tap + 1 < 9) load(tap + 1, c ^ 1);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int j = 0; j < NJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
             if (tap + 1 < 9) {
+                // one MFMA, then one fragment read with its address VALU, in turn
 #pragma unroll
-                for (int q = 0; q < 2 + NJ; ++q) {
+                for (int q = 0; q < MI + NJ; ++q) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU (address)
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, 2 * NJ - (2 + NJ), 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, MI * NJ - (MI + NJ), 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
     if (has_res) lds_barrier();                       // the producers' residual tile has landed
 
-    // Epilogue.  The residual is added by two MFMAs per 32x32 block with
-    // identity A operands ([I16; 0] and [0; I16], K = 16 channels of the
-    // residual rows in LDS as the B operand): each product is r x 1 and the sum
-    // acc + r is rounded once, as an f32 add would be.  Then [ReLU], f16, and
-    // the values are written over the residual rows they came from; the wave's
-    // 64-channel halves of its pixel rows then leave as 16-byte chunks.
+    // Epilogue: the residual through identity-operand MFMAs, [ReLU], f16 over
+    // the residual rows, then the wave's channel range of its pixel rows out
+    // as 16-byte chunks.
     const bool relu = a.act == VDK_ACT_RELU;
     half8 eye[2];
 #pragma unroll
@@ -2076,12 +1810,11 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) eye[h][e] = (half_t)((lrow == h * 16 + lhalf * 8 + e) ? 1.0f : 0.0f);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int cw = og * 64 + i * 32;
+    for (int i = 0; i < MI; ++i) {
+        const int cw = cg0 + i * 32;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            const int pr = (pg * NJ + j) * 32 + lrow;
-            uint8_t* const prow = band3_rrow<TH, NJ, MAXW>(rs0, rs1, pr);
+            uint8_t* const prow = rrow((pg * NJ + j) * 32 + lrow);
             if (has_res) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
@@ -2102,30 +1835,26 @@ __global__ __launch_bounds__(768) void conv3x3_bandws_kernel(ConvArgs a) {
             }
         }
     }
-    half_t* const y = static_cast<half_t*>(a.y) + oc0 + og * 64;
-    constexpr int NST = NJ * 32 * 8 / 64;             // 16-byte stores per wave
-    const int ch = lane & 7;
+    half_t* const y = static_cast<half_t*>(a.y) + oc0 + cg0;
+    constexpr int NST = NJ * 32 * G::CPR / 64;        // 16-byte stores per wave
+    const int ch = lane % G::CPR;
 #pragma unroll
     for (int it = 0; it < NST; ++it) {
-        const int pr = pg * NJ * 32 + it * 8 + (lane >> 3);
-        const half8 v8 = *reinterpret_cast<const half8*>(band3_rrow<TH, NJ, MAXW>(rs0, rs1, pr) + og * 128 + ch * 16);
+        const int pr = pg * NJ * 32 + (it * 64 + lane) / G::CPR;
+        const half8 v8 = *reinterpret_cast<const half8*>(rrow(pr) + cg0 * 2 + ch * 16);
         const int r = div_small(pr, inv_w), c = pr - r * W;
         if (pr < npx && r0 + r < H)
             *reinterpret_cast<half8*>(y + ((size_t)(b * H + r0 + r) * W + c) * a.ys + ch * 8) = v8;
     }
 }
 
-template <int TH, int NJ, int MAXW>
+template <int TH, int MAXW, int WMG, int WNG, int NJ, int NP>
 void launch_bandws(const ConvArgs& a, hipStream_t s) {
     const int B = a.npix / (a.Ho * a.Wo);
-    hipLaunchKernelGGL((conv3x3_bandws_kernel<TH, NJ, MAXW>), dim3(B * cdiv(a.H, TH), a.OC / 128), dim3(768), 0, s, a);
+    hipLaunchKernelGGL((conv3x3_bandws_kernel<TH, MAXW, WMG, WNG, NJ, NP>), dim3(B * cdiv(a.H, TH), a.OC / 128),
+                       dim3((WMG * WNG + NP) * 64), 0, s, a);
 }
 
-template <int TH, int NJ, int MAXW>
-void launch_band3(const ConvArgs& a, hipStream_t s) {
-    const int B = a.npix / (a.Ho * a.Wo);
-    hipLaunchKernelGGL((conv3x3_band3_kernel<TH, NJ, MAXW>), dim3(B * cdiv(a.H, TH), a.OC / 128), dim3(512), 0, s, a);
-}
 
 template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
@@ -2149,7 +1878,9 @@ struct TileCfg {
 // KC=16 for IC % 32 != 0), 14-25 the LDS-DMA kernel, 26-32 the halo kernel,
 // 33-52 LDS-DMA tiles with 8 waves per workgroup, 53-56 the register-weight
 // persistent 3x3 kernel, 57-59 the band kernel for wide 3x3 layers, 60-61
-// narrow LDS-DMA tiles, 62-63 narrow register-staged tiles.
+// narrow LDS-DMA tiles, 62-63 narrow register-staged tiles, 64-65 the band
+// kernel with producer / compute waves (128-channel groups, maps up to 75 /
+// 38 wide).
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -2218,8 +1949,8 @@ const TileCfg kTiles[] = {
     {32, 128, 32, launch_dma<32, 128, 32, 32, 32, 2>},    // 61
     {128, 32, 32, launch_igemm<128, 32, 64, 32, 32>},     // 62: register-staged, more workgroups
     {64, 64, 32, launch_igemm<64, 64, 32, 32, 32>},       // 63
-    {128, 384, 16, launch_band3<5, 3, 75>, true, 0, 75},  // 64: 3-stage band kernel, 64-channel waves
-    {128, 384, 16, launch_bandws<5, 3, 75>, true, 0, 75}, // 65: the same, producer / compute waves
+    {128, 384, 16, launch_bandws<5, 75, 2, 4, 3, 4>, true, 0, 75},   // 64: producer / compute band kernels
+    {128, 192, 16, launch_bandws<5, 38, 2, 2, 3, 4>, true, 0, 38},   // 65
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -2326,8 +2057,9 @@ int pick_tile(const ConvArgs& a) {
         if (a.IC == 256 && a.OC == 512) return 51;
     }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
-    if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[65], a)) return 65;
+    if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[64], a)) return 64;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
+    if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[65], a)) return 65;
     if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[58], a)) return 58;
     // ResNet's stride-2 32->64 pair (random-data sweep): the 1x1 on the 64x64
     // register-staged tile, the 3x3 on the 64x128 one
