@@ -14,8 +14,8 @@
 // 3x3 or 1x1, stride 1 or 2, bias(+ReLU) fused, residual add+ReLU fused); the
 // reference's f32 direct accumulation is replaced by f16 products with f32 sums.
 //
-// stem_conv3x3_kernel: the IC=1 stem (K = 9 is too short for MFMA); one
-// thread per output pixel computes all OC channels in f32 from f32 features.
+// stem_mfma_kernel: the IC=1 stem in f32 on v_mfma_f32_32x32x2_f32 (K = the 9
+// taps padded to 10); stem_conv3x3_kernel, the f32 FMA loop, serves OC = 16.
 #include <cstdlib>
 #include <type_traits>
 
@@ -2121,6 +2121,110 @@ __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restri
     }
 }
 
+// The stem as f32 MFMA (v_mfma_f32_32x32x2_f32: f32 products and sums, the
+// precision of the f32 FMA loop above).  A wavefront walks up to kStemRuns
+// runs of 32 consecutive output pixels of one row; per run the GEMM rows are
+// the output channels (OC/32 blocks), the columns its 32 pixels and K the 9
+// taps padded to 10: five K=2 MFMAs per block whose B operand lane l reads
+// tap 2q + l/32 of pixel l%32 straight from the features (the three input
+// rows stay in the L1), loaded one run ahead.  The accumulators (+bias,
+// [ReLU]) are rounded to f16 (and the split-f16 remainder) into a per-wave LDS
+// tile that leaves as 16-byte channel chunks, so each store instruction
+// writes 16 whole pixels.
+constexpr int kStemRuns = 10;
+
+template <int OC, bool SPLIT>
+__global__ __launch_bounds__(256) void stem_mfma_kernel(const float* __restrict__ feats, int B, int H, int W,
+                                                        const float* __restrict__ w, const float* __restrict__ bias,
+                                                        int relu, half_t* __restrict__ y) {
+    constexpr int NOB = OC / 32, PITCH = OC * 2 + 16;   // LDS row: OC f16 channels + 16 bytes
+    static_assert(OC % 32 == 0, "whole 32-channel MFMA blocks");
+    __shared__ __attribute__((aligned(16))) uint8_t stile[4][SPLIT ? 2 : 1][32 * PITCH];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 31, kk = lane >> 5;
+    const int ntb = (W + 31) >> 5, nch = (ntb + kStemRuns - 1) / kStemRuns;
+    const int item = blockIdx.x * 4 + wave;
+    if (item >= B * H * nch) return;   // no barrier below: a wave may leave alone
+    const int row = item / nch, r0 = (item - row * nch) * kStemRuns;
+    const int r1 = r0 + kStemRuns < ntb ? r0 + kStemRuns : ntb;
+    const int b = row / H, h = row - b * H;
+    float wa[NOB][5];
+    float16v bv[NOB];   // the accumulators start at the bias (register g*4+e: channel 8g + 4*kk + e)
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob) {
+#pragma unroll
+        for (int q = 0; q < 5; ++q) {
+            const int tap = 2 * q + kk;
+            wa[ob][q] = tap < 9 ? w[(ob * 32 + j) * 9 + tap] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bv[ob][r] = bias[ob * 32 + (r >> 2) * 8 + kk * 4 + (r & 3)];
+    }
+    auto load = [&](int r, float* xb) {
+        const int t0 = r * 32;
+#pragma unroll
+        for (int q = 0; q < 5; ++q) {
+            const int tap = 2 * q + kk, kh = tap / 3, kw = tap - kh * 3;
+            const int ih = h - 1 + kh, iw = t0 + j - 1 + kw;
+            xb[q] = (tap < 9 && ih >= 0 && ih < H && iw >= 0 && iw < W) ? feats[((size_t)b * H + ih) * W + iw]
+                                                                           : 0.0f;
+        }
+    };
+    uint8_t* const hi = stile[wave][0];
+    uint8_t* const lo = stile[wave][SPLIT ? 1 : 0];
+    constexpr int CPP = OC / 8;                  // 16-byte chunks per pixel
+    constexpr int PPI = 64 / CPP;                // pixels per store instruction
+    constexpr int ostride = SPLIT ? 2 * OC : OC;
+    float xn[5];
+    load(r0, xn);
+    for (int r = r0; r < r1; ++r) {
+        float xb[5];
+#pragma unroll
+        for (int q = 0; q < 5; ++q) xb[q] = xn[q];
+        if (r + 1 < r1) load(r + 1, xn);
+#pragma unroll
+        for (int ob = 0; ob < NOB; ++ob) {
+            float16v acc = bv[ob];
+#pragma unroll
+            for (int q = 0; q < 5; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[ob][q], xb[q], acc, 0, 0, 0);
+            // register g*4+e: channel ob*32 + 8g + 4*kk + e of pixel j
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int c = ob * 32 + g * 8 + kk * 4;
+                half4 hv, lv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v = acc[g * 4 + e];
+                    if (relu) v = fmaxf(v, 0.0f);
+                    hv[e] = (half_t)v;
+                    if constexpr (SPLIT) lv[e] = (half_t)(v - (float)hv[e]);
+                }
+                *reinterpret_cast<half4*>(hi + j * PITCH + c * 2) = hv;
+                if constexpr (SPLIT) *reinterpret_cast<half4*>(lo + j * PITCH + c * 2) = lv;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int t0 = r * 32;
+        const size_t pix0 = (size_t)row * W + t0;
+#pragma unroll
+        for (int it = 0; it < 32 / PPI; ++it) {
+            const int p = it * PPI + lane / CPP, ch = lane % CPP;
+            if (t0 + p < W) {
+                half_t* const dst = y + (pix0 + p) * ostride + ch * 8;
+                *reinterpret_cast<half8*>(dst) = *reinterpret_cast<const half8*>(hi + p * PITCH + ch * 16);
+                if constexpr (SPLIT)
+                    *reinterpret_cast<half8*>(dst + OC) = *reinterpret_cast<const half8*>(lo + p * PITCH + ch * 16);
+            }
+        }
+        // this run's tile reads are issued before the next run's writes (in-order LDS per wavefront)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -2314,13 +2418,20 @@ extern "C" int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W
         hipStream_t s = static_cast<hipStream_t>(stream);
         const long n = (long)batch * H * W * (OC / 8);
         require(n < (1L << 31), "stem: too many pixels for one launch");
-        dim3 grid(cdiv(n, 256));
         half_t* y = static_cast<half_t*>(d_y);
         const int sp = split ? 1 : 0;
+        // 32 / 64 channels: f32 MFMA, one wavefront per kStemRuns 32-pixel runs of a row
+        const long runs = (long)batch * H * cdiv(cdiv(W, 32), kStemRuns);
         switch (OC) {
-            case 16: hipLaunchKernelGGL(stem_conv3x3_kernel<16>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
-            case 32: hipLaunchKernelGGL(stem_conv3x3_kernel<32>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
-            case 64: hipLaunchKernelGGL(stem_conv3x3_kernel<64>, grid, dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
+            case 16: hipLaunchKernelGGL(stem_conv3x3_kernel<16>, dim3(cdiv(n, 256)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
+            case 32:
+                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<32, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y);
+                else hipLaunchKernelGGL((stem_mfma_kernel<32, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y);
+                break;
+            case 64:
+                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<64, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y);
+                else hipLaunchKernelGGL((stem_mfma_kernel<64, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y);
+                break;
             default: throw Error("stem: OC must be 16, 32 or 64");
         }
         VDK_HIP(hipGetLastError());
