@@ -115,8 +115,10 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * split != 0 selects split-f16 arithmetic (~2^-21 relative instead of f16's
  * 2^-11, for ill-conditioned networks): x, residual and y hold value = hi + lo
  * with the lo halves x_lo / res_lo / y_lo elements after the hi halves (same
- * pixel strides), w is [OC][KH][KW][3*IC] = [hi | hi | lo] per tap, and the
- * GEMM runs x_hi.w_hi + x_lo.w_hi + x_hi.w_lo on f16 MFMA (3x the work).
+ * pixel strides).  split = 1: w is [OC][KH][KW][3*IC] = [hi | hi | lo] per tap
+ * and the GEMM runs x_hi.w_hi + x_lo.w_hi + x_hi.w_lo on f16 MFMA (3x the
+ * work); split = 2, for weights that f16 holds exactly (lo = 0): w is
+ * [OC][KH][KW][2*IC] = [hi | hi] and the GEMM runs x_hi.w + x_lo.w (2x).
  * tile = -1 picks the kernel automatically. */
 typedef struct {
     const void* x; int batch, H, W, IC, x_stride;

@@ -178,21 +178,28 @@ def _split(a):
     return hi, lo
 
 
-def test_split_f16_conv_is_f32_accurate():
+@pytest.mark.parametrize("terms,IC,OC,tile", [(3, 64, 64, -1), (2, 64, 64, -1), (2, 32, 16, 27), (3, 32, 32, 28),
+                                          (2, 64, 32, 28), (3, 128, 64, 30), (2, 64, 64, 17)])
+def test_split_f16_conv_is_f32_accurate(terms, IC, OC, tile):
     """Split-f16 convs (3x3 s1 with clamp, 1x1 s2 with split residual) match the
-    f64 brute force to ~1e-6 relative, where plain f16 is ~1e-3."""
-    rng = np.random.default_rng(104)
-    H, T, IC, OC = 20, 250, 64, 64
-    announce(f"eres split-f16 convs B={B} H={H} T={T}")
+    f64 brute force to ~1e-6 relative, where plain f16 is ~1e-3.  terms = 2:
+    weights that f16 holds exactly, packed [hi | hi] (split = 2), which must
+    equal the three-term form with its all-zero lo plane."""
+    rng = np.random.default_rng(104 + IC + OC + terms)
+    H, T = 20, 250
+    announce(f"eres split-f16 convs B={B} H={H} T={T} IC={IC} OC={OC} terms={terms} tile={tile}")
     x = rng.standard_normal((B, H, T, IC)).astype(np.float32) * 3
     xh, xl = _split(x)
     xs = np.concatenate([xh, xl], axis=3)                       # [hi(IC) | lo(IC)] per pixel
     dx = lib.DeviceBuffer.from_array(xs)
     for K, stride in ((3, 1), (1, 2)):
         w = (rng.standard_normal((OC, IC, K, K)) * np.sqrt(2.0 / (IC * K * K))).astype(np.float32)
+        if terms == 2:
+            w = w.astype(np.float16).astype(np.float32)          # exact in f16: lo = 0
         b = rng.uniform(-0.5, 0.5, OC).astype(np.float32)
         wh, wl = _split(w.transpose(0, 2, 3, 1))
-        wpack = np.concatenate([wh, wh, wl], axis=3)            # [OC][K][K][3*IC]
+        # [OC][K][K][3*IC], or [OC][K][K][2*IC] for two terms
+        wpack = np.concatenate([wh, wh, wl] if terms == 3 else [wh, wh], axis=3)
         Ho, Wo = (H - 1) // stride + 1, (T - 1) // stride + 1
         res = rng.standard_normal((B, Ho, Wo, OC)).astype(np.float32) * 4 if stride == 2 else None
         dres = lib.DeviceBuffer.from_array(np.concatenate(_split(res), axis=3)) if res is not None else None
@@ -209,11 +216,21 @@ def test_split_f16_conv_is_f32_accurate():
             d.residual, d.res_stride, d.res_lo = dres.ptr, 2 * OC, OC
         d.act, d.clamp_hi = lib.ACT_RELU, 20.0
         d.y, d.y_stride = y.ptr, 2 * OC
-        d.split, d.x_lo, d.y_lo = 1, IC, OC
-        d.tile = -1
+        d.split, d.x_lo, d.y_lo = (1 if terms == 3 else 2), IC, OC
+        d.tile = tile if K == 3 else -1
         lib.check(lib.lib().vdk_conv2d_ex(d, None))
         lib.check(lib.lib().vdk_synchronize())
         got = y.to_array(np.float16, (B, Ho, Wo, 2 * OC)).astype(np.float64)
+        if terms == 2:
+            assert not np.any(wl)
+            keep.append(lib.DeviceBuffer.from_array(np.ascontiguousarray(np.concatenate([wh, wh, wl], axis=3))))
+            d.w, d.split = keep[-1].ptr, 1
+            y3 = lib.DeviceBuffer(B * Ho * Wo * 2 * OC * 2)
+            d.y = y3.ptr
+            lib.check(lib.lib().vdk_conv2d_ex(d, None))
+            lib.check(lib.lib().vdk_synchronize())
+            # the same sums (the skipped products are all zero), up to the sign of zero
+            assert np.array_equal(y3.to_array(np.float16, (B, Ho, Wo, 2 * OC)).astype(np.float64), got)
         got = got[..., :OC] + got[..., OC:]
         for c in (0, B - 1):
             ref = O.conv2d_g(x[c].transpose(2, 0, 1), w, sh=stride, sw=stride, ph=(K - 1) // 2, pw=(K - 1) // 2,

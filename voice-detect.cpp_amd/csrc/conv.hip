@@ -44,7 +44,7 @@ struct ConvArgs {
     int xs, ys, rs;            // elements between consecutive pixels of x / y / residual
     int bias_bs;               // elements between clips' bias vectors (0: one shared vector)
     int split;                 // split-f16 tensors: value = hi + lo, lo at +x_lo / +r_lo / +y_lo elements;
-    int x_lo, r_lo, y_lo;      //   weights [OC][KH][KW][3*IC] = [hi | hi | lo] per tap
+    int x_lo, r_lo, y_lo;      //   weights per tap [hi | hi | lo] (split 1) or [hi | hi] (split 2: lo = 0)
     int res_f32, res_after;    // f32 residual; residual added after the activation
     const float* in_scale;     // input prologue x' = relu(x * in_scale[c] + in_shift[c]) (may be NULL)
     const float* in_shift;
@@ -462,8 +462,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     const int oc0 = blockIdx.y * BM;
     const int HoWo = a.Ho * a.Wo;
     const int KHW = a.KH * a.KW;
-    // Split-f16: per tap the K range runs over [x_hi . w_hi | x_lo . w_hi | x_hi . w_lo].
-    const int ICW = a.split ? 3 * a.IC : a.IC;
+    // Split-f16: per tap the K range runs over [x_hi . w_hi | x_lo . w_hi | x_hi . w_lo]
+    // (split 2, weights exact in f16: the first two terms only).
+    const int ICW = a.split ? (a.split == 2 ? 2 : 3) * a.IC : a.IC;
     const int nc = ICW / KC;
     const int nk = KHW * nc;
 
@@ -653,12 +654,15 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
     const int trem = t - b * tiles_h * tiles_w;
     const int oh0 = (trem / tiles_w) * TH, ow0 = (trem % tiles_w) * TW;
     const int oc0 = blockIdx.y * OCB;
-    const int nc = a.IC / KC;
+    // split-f16: the chunks run over ICW = terms * IC weight columns, [hi | lo
+    // (| hi)] planes of the input (each chunk inside one plane: IC % KC == 0)
+    const int ICW = a.split ? (a.split == 2 ? 2 : 3) * a.IC : a.IC;
+    const int nc = ICW / KC;
 
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
+        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC + (a.split ? a.x_lo : 0)) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)a.w, 0, (int)((size_t)a.OC * 9 * a.IC * 2), 0x00020000);
+        (void*)a.w, 0, (int)((size_t)a.OC * 9 * ICW * 2), 0x00020000);
 
     float16v acc[BPW];
 #pragma unroll
@@ -669,12 +673,14 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
 
     for (int ci = 0; ci < nc; ++ci) {
         const int c0 = ci * KC;
+        const int plane = c0 / a.IC;                    // 0: hi, 1: lo, 2: hi again
+        const int xc0 = c0 - plane * a.IC + (plane == 1 ? a.x_lo : 0);
         // weights: LDS row (tap*OCB + oc) holds w[oc0+oc][tap][c0 .. c0+KC)
         for (int ins = wave; ins < W_INS; ins += NW) {
             const int p = ins * 64 + lane;
             const int r = p / CPR, slot = p - r * CPR;
             const int tap = r / OCB, oc = r - tap * OCB;
-            const uint32_t off = (uint32_t)((((oc0 + oc) * 9 + tap) * a.IC + c0 + swz<KC>(r, slot) * 8) * 2);
+            const uint32_t off = (uint32_t)((((oc0 + oc) * 9 + tap) * ICW + c0 + swz<KC>(r, slot) * 8) * 2);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(sw + ins * 1024), 16, off, 0, 0, 0);
         }
         // input halo: LDS row (hr*HW + hc) holds x[b][oh0-1+hr][ow0-1+hc][c0 .. c0+KC)
@@ -686,7 +692,7 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
                 const int hr = r / HW, hc = r - hr * HW;
                 const int ih = oh0 - 1 + hr, iw = ow0 - 1 + hc;
                 if (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
-                    off = (uint32_t)((((b * a.H + ih) * a.W + iw) * a.xs + c0 + swz<KC>(r, slot) * 8) * 2);
+                    off = (uint32_t)((((b * a.H + ih) * a.W + iw) * a.xs + xc0 + swz<KC>(r, slot) * 8) * 2);
             }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx + ins * 1024), 16, off, 0, 0, 0);
         }
@@ -1982,8 +1988,8 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     if (a.KH * a.KW > 32 && a.KH != 1 && idx >= kFirstDma) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
     if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % t.bm == 0 && a.IC % 16 == 0;
-    if (a.split && (igemm_tile(idx) || (idx >= kFirstHalo && idx < kFirstDma8) || idx >= 62))
-        return false;   // split: DMA only
+    // split: the DMA and halo kernels only (IC % kc == 0 below keeps a chunk inside one plane)
+    if (a.split && (igemm_tile(idx) || idx >= 62)) return false;
     return a.IC % t.kc == 0;
 }
 
@@ -2045,8 +2051,12 @@ int pick_tile(const ConvArgs& a) {
         if (a.KH * a.KW == 1) return 10;
         if (a.H <= 20) return 60;
     }
-    if (a.split && is_s1_3x3(a)) {   // ERes2Net's split-f16 group convs (random-data sweep)
-        if (a.IC == 32 && a.OC == 32) return 61;
+    if (a.split && is_s1_3x3(a)) {   // ERes2Net's split-f16 group convs (random-data sweeps)
+        // up to 64 output channels: the halo kernel (each input pixel fetched
+        // once per chunk for all 9 taps; 2.5-2.8x faster than the DMA tiles
+        // on the 16-64-channel layers), 8-row tiles on the 1998-frame maps
+        if (a.OC <= 32 && a.IC % 32 == 0) return a.W >= 1000 ? 27 : 28;
+        if (a.OC == 64 && a.IC % 32 == 0) return 30;
         if (a.IC == 128 && a.OC == 128 && tile_fits(kTiles[40], a)) return 40;
     }
     if (a.split && a.KH * a.KW == 1 && a.sh == 1 && a.sw == 1) {   // ERes2Net's split-f16 1x1s (same sweep)
@@ -2255,7 +2265,7 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(xs % 8 == 0 && ys % 8 == 0 && rs % 8 == 0, "conv2d: pixel strides must be multiples of 8");
         require((long)d.batch * Ho * Wo < (1L << 31) && (long)d.batch * d.H * d.W * xs < (1L << 30) &&
                     (long)d.batch * Ho * Wo * ys < (1L << 31) &&
-                    (long)d.OC * d.KH * d.KW * d.IC * (d.split ? 3 : 1) < (1L << 30),
+                    (long)d.OC * d.KH * d.KW * d.IC * (d.split == 2 ? 2 : (d.split ? 3 : 1)) < (1L << 30),
                 "conv2d: too many pixels for one launch");
         require(aligned16(d.x) && aligned16(d.w) && aligned16(d.y) && (!d.residual || aligned16(d.residual)),
                 "conv2d: device pointers must be 16-byte aligned");
@@ -2271,6 +2281,7 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(!d.in_scale || (d.KH == 1 && d.KW == 1 && d.pad_h == 0 && d.pad_w == 0 && !d.split &&
                                 aligned16(d.in_scale) && aligned16(d.in_shift)),
                 "conv2d: the input prologue needs a 1x1 conv without padding and 16-byte aligned vectors");
+        require(d.split >= 0 && d.split <= 2, "conv2d: split must be 0, 1 or 2");
         require(!d.split || (!d.y_f32 && !d.y_time_major && d.x_lo >= d.IC && d.y_lo >= d.OC &&
                              (!d.residual || d.res_lo >= d.OC) && d.x_lo % 8 == 0 && d.y_lo % 8 == 0 &&
                              d.res_lo % 8 == 0 && d.IC % 32 == 0),
@@ -2298,7 +2309,7 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         a.y_tr = d.y_time_major ? 1 : 0;
         a.xs = xs; a.ys = ys; a.rs = rs;
         a.bias_bs = d.bias_batch_stride;
-        a.split = d.split ? 1 : 0;
+        a.split = d.split;
         a.x_lo = d.x_lo; a.r_lo = d.res_lo; a.y_lo = d.y_lo;
         a.res_f32 = d.res_f32 ? 1 : 0;
         a.res_after = d.res_after_act ? 1 : 0;
@@ -2337,7 +2348,7 @@ vdk_conv_desc plain_desc(const void* d_x, int batch, int H, int W, int IC, const
 // which epilogue stages are present); pointers only by presence.
 ConvArgs shape_args(const vdk_conv_desc& d) {
     ConvArgs a{};
-    a.split = d.split ? 1 : 0;
+    a.split = d.split;
     a.IC = d.IC; a.OC = d.OC; a.KH = d.KH; a.KW = d.KW;
     a.sh = d.stride_h ? d.stride_h : 1; a.sw = d.stride_w ? d.stride_w : 1;
     a.ph = d.pad_h; a.pw = d.pad_w;

@@ -21,7 +21,8 @@
 // first half of a 2C-channel tensor whose second half receives the
 // cross-stage downsample, so the cross-stage AFF reads its concatenation in
 // place.  Weights: split f16 [OC][KH][KW][3*IC] (Q8_0 / F32 dequantised at
-// load); seg_1 f32.
+// load), or [OC][KH][KW][2*IC] for a layer whose weights f16 holds exactly
+// (the x_hi . w_lo term is zero and is skipped); seg_1 f32.
 #include <algorithm>
 #include <cmath>
 #include <string>
@@ -77,7 +78,10 @@ void Model::upload_eres2net() {
         require(c.oc % 8 == 0, "voicedetect: eres2net conv widths must be multiples of 8");
         const int ocp = std::max(c.oc, oc_pad);
         l.ic = icp; l.oc = ocp; l.kh = c.kh; l.k = c.kw;
-        arena.put(pack_conv_f16_split(c, icp, ocp, map), &l.w);
+        // weights that f16 holds exactly need no x_hi . w_lo term
+        const bool exact = conv_f16_exact(c);
+        l.split = exact ? 2 : 1;
+        arena.put(pack_conv_f16_split(c, icp, ocp, map, exact ? 2 : 3), &l.w);
         if (!ec.conv_bias[idx].empty()) {
             std::vector<float> b = g.to_f32(ec.conv_bias[idx]);
             require(b.size() == (size_t)c.oc, "voicedetect: '" + ec.conv_bias[idx] + "' has the wrong size");
@@ -230,7 +234,7 @@ void Model::encode_eres2net(int batch, int T) {
         if (res) { d.residual = res->p; d.res_stride = res->stride; d.res_lo = res->lo; }
         d.act = act; d.clamp_hi = clamp; d.tanh_after = tanh_after;
         d.y = y.p; d.y_stride = y.stride;
-        d.split = 1; d.x_lo = x.lo; d.y_lo = y.lo;
+        d.split = l.split; d.x_lo = x.lo; d.y_lo = y.lo;
         d.tile = -1;
         conv_ex(name, d);
     };

@@ -56,12 +56,21 @@ inline std::vector<uint16_t> pack_conv_f16(const HostConv& c, int icp,
     return p;
 }
 
-// Split-f16 weights: f16 [OC][KH][KW][3*icp] holding [hi | hi | lo] per tap
-// (hi = f16(w), lo = f16(w - hi)); rows oc_pad > oc are zero.
+// Whether f16 holds every weight exactly (the split-f16 lo halves are all 0).
+inline bool conv_f16_exact(const HostConv& c) {
+    for (float v : c.w)
+        if (half_bits_to_float(float_to_half_bits(v)) != v) return false;
+    return true;
+}
+
+// Split-f16 weights: f16 [OC][KH][KW][terms*icp] holding [hi | hi | lo] per tap
+// (hi = f16(w), lo = f16(w - hi)), or [hi | hi] when terms = 2 (weights that
+// conv_f16_exact accepts, whose lo halves are 0); rows oc_pad > oc are zero.
 inline std::vector<uint16_t> pack_conv_f16_split(const HostConv& c, int icp, int oc_pad = 0,
-                                                 const std::function<int(int)>& ic_map = nullptr) {
+                                                 const std::function<int(int)>& ic_map = nullptr, int terms = 3) {
+    require(terms == 2 || terms == 3, "voicedetect: split-f16 weights have 2 or 3 terms");
     const int ocp = oc_pad > c.oc ? oc_pad : c.oc;
-    const size_t row = (size_t)3 * icp;
+    const size_t row = (size_t)terms * icp;
     std::vector<uint16_t> p((size_t)ocp * c.kh * c.kw * row, 0);
     for (int o = 0; o < c.oc; ++o)
         for (int i = 0; i < c.ic; ++i) {
@@ -74,7 +83,7 @@ inline std::vector<uint16_t> pack_conv_f16_split(const HostConv& c, int icp, int
                     uint16_t* q = &p[(((size_t)o * c.kh + kh) * c.kw + kw) * row];
                     q[d] = hi;
                     q[icp + d] = hi;
-                    q[2 * icp + d] = lo;
+                    if (terms == 3) q[2 * icp + d] = lo;
                 }
         }
     return p;
