@@ -119,6 +119,12 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * and the GEMM runs x_hi.w_hi + x_lo.w_hi + x_hi.w_lo on f16 MFMA (3x the
  * work); split = 2, for weights that f16 holds exactly (lo = 0): w is
  * [OC][KH][KW][2*IC] = [hi | hi] and the GEMM runs x_hi.w + x_lo.w (2x).
+ * reflect_pad != 0 (1-D convs, KH = 1): the time axis is padded by reflection
+ * without repeating the edge sample (x[-i] = x[i], x[W-1+i] = x[W-1-i],
+ * SpeechBrain's padding, src/encoder.cpp:32-52) instead of with zeros; pad_w
+ * must be below W.  y2 (may be NULL): a second f16 output y2 = v + res2 (v the
+ * finished value above, res2 f16 at the same pixel, both with their own pixel
+ * strides), e.g. the next Res2Net group's input y_j + x_{j+1}.
  * tile = -1 picks the kernel automatically. */
 typedef struct {
     const void* x; int batch, H, W, IC, x_stride;
@@ -136,6 +142,9 @@ typedef struct {
     int res_f32, res_after_act, out_w;
     const float* in_scale; const float* in_shift;
     const void* w_chunked;
+    int reflect_pad;
+    void* y2; int y2_stride;
+    const void* res2; int res2_stride;
 } vdk_conv_desc;
 /* Host: re-order f16 conv weights [OC][KH][KW][IC] (IC % 16 == 0) into the
  * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */
@@ -286,6 +295,16 @@ int vdk_segment_sums(const void* d_x, int x_stride, int batch, int T, int C, int
 int vdk_cam_context(const float* d_sums, int batch, int T, int C, int seg, const float* d_w1,
                     const float* d_b1, int H1, const float* d_w2, const float* d_b2, int G,
                     float* d_gate, void* stream);
+/* One dense layer's CAM layer in one launch (src/encoder_campplus.cpp:159-182,
+ * 260-268): the context mask of vdk_cam_context computed per (clip, segment)
+ * from x itself (its segment sums in f64), then
+ * y = (linear_local(x) + bl) * gate, linear_local the k = 3 conv with
+ * dilation dil and zero padding, C -> 32 channels, wl f16 [32][3][C]
+ * (tap-major), bl [32] f32 (may be NULL); x [B][T][x_stride] f16 (C a
+ * multiple of 16, 16..256), y [B][T][y_stride] f16 (the 32 outputs). */
+int vdk_cam_local(const void* d_x, int x_stride, int batch, int T, int C, int seg, int dil,
+                  const float* d_w1, const float* d_b1, int H1, const float* d_w2, const float* d_b2,
+                  const void* d_wl, const float* d_bl, void* d_y, int y_stride, void* stream);
 
 /* ---- ERes2Net helper (src/encoder_eres2net.cpp:91-101) ----
  * AFF output y = (x + ds) + t * (x - ds) with t = tanh(local_att(cat(x, ds)))

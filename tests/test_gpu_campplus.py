@@ -168,6 +168,65 @@ def test_bn_act_segment_sums_and_context():
     assert np.allclose(gate, want, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("batch,T,dil,bias", [(B, TP, 1, False), (B, TP, 2, True), (3, 257, 2, True), (2, 40, 1, True)])
+def test_cam_local_fused_layer(batch, T, dil, bias):
+    """vdk_cam_local (context sums, mask MLP and the gated k=3 linear_local in
+    one launch) against the f64 context of the dense Q-matrix form and the
+    oracle's conv, and against the three-launch path (segment sums, context,
+    gated conv); the other channels of the dense buffer stay untouched."""
+    rng = np.random.default_rng(100 + T + dil)
+    L = lib.lib()
+    BC, G, H1, SEG, CMAX, C0 = 128, 32, 64, 100, 384, 224
+    nseg = (T + SEG - 1) // SEG
+    announce(f"campp cam_local B={batch} T'={T} dil={dil} bias={bias}")
+    cc = np.maximum(rng.standard_normal((batch, T, BC), dtype=np.float32), 0).astype(np.float16)
+    dense = rng.standard_normal((batch, T, CMAX), dtype=np.float32).astype(np.float16)
+    w1 = rng.standard_normal((H1, BC), dtype=np.float32) / 8
+    b1 = rng.standard_normal(H1, dtype=np.float32) / 4
+    w2 = rng.standard_normal((G, H1), dtype=np.float32) / 8
+    b2 = rng.standard_normal(G, dtype=np.float32) / 4
+    w = _w(rng, G, BC, 1, 3)                                             # [G][BC][1][3] f16
+    bl = (rng.standard_normal(G, dtype=np.float32) * 0.1) if bias else None
+    dcc, dd = lib.DeviceBuffer.from_array(cc), lib.DeviceBuffer.from_array(dense)
+    dw1, db1, dw2, db2 = (lib.DeviceBuffer.from_array(a) for a in (w1, b1, w2, b2))
+    dwl = lib.DeviceBuffer.from_array(np.ascontiguousarray(w[:, :, 0, :].transpose(0, 2, 1)))   # [G][3][BC]
+    dbl = lib.DeviceBuffer.from_array(bl) if bias else None
+    lib.check(L.vdk_cam_local(dcc.ptr, BC, batch, T, BC, SEG, dil, dw1.ptr, db1.ptr, H1, dw2.ptr, db2.ptr, dwl.ptr,
+                              dbl.ptr if dbl else None, dd.ptr + C0 * 2, CMAX, None))
+    _sync()
+    out = dd.to_array(np.float16, (batch, T, CMAX))
+    keep = np.ones(CMAX, dtype=bool)
+    keep[C0:C0 + G] = False
+    assert np.array_equal(out[:, :, keep].view(np.uint16), dense[:, :, keep].view(np.uint16))
+    xc = cc.astype(np.float64)
+    segs = np.stack([xc[:, i * SEG:(i + 1) * SEG].sum(axis=1) for i in range(nseg)], axis=1)
+    ctx = xc.mean(axis=1)[:, None, :] + segs / SEG
+    h = np.maximum(ctx @ w1.T.astype(np.float64) + b1, 0)
+    gate = 1.0 / (1.0 + np.exp(-(h @ w2.T.astype(np.float64) + b2)))         # [batch][nseg][G]
+    seg_of_t = np.arange(T) // SEG
+    for c in sorted({0, batch // 2, batch - 1}):
+        y = O.conv2d_g(cc[c].astype(np.float32).T[:, None, :], w.astype(np.float32), pw=dil, dw=dil,
+                       bias=bl)[:, 0, :]
+        ref = y * gate[c][seg_of_t].T
+        rel = _assert_close(out[c, :, C0:C0 + G].astype(np.float32).T, ref, f"cam_local clip {c}")
+        announce(f"cam_local clip {c} rel-L2 {rel:.2e}")
+    # the three-launch path on the same inputs
+    dsum = lib.DeviceBuffer(batch * nseg * BC * 4)
+    dg = lib.DeviceBuffer(batch * nseg * G * 4)
+    lib.check(L.vdk_segment_sums(dcc.ptr, BC, batch, T, BC, SEG, dsum.ptr, None))
+    lib.check(L.vdk_cam_context(dsum.ptr, batch, T, BC, SEG, dw1.ptr, db1.ptr, H1, dw2.ptr, db2.ptr, G, dg.ptr, None))
+    _sync()
+    g3 = dg.to_array(np.float32, (batch, nseg, G))
+    assert np.allclose(g3, gate, rtol=1e-5, atol=1e-6)
+    d3 = lib.DeviceBuffer(batch * T * G * 2)
+    conv_ex(dcc.ptr, batch, 1, T, BC, 0, w.transpose(0, 2, 3, 1), G, 1, 3, d3.ptr, ys=G, pw=dil, dw=dil, bias=bl,
+            gate=g3, gate_seg=SEG, gate_nseg=nseg)
+    y3 = d3.to_array(np.float16, (batch, T, G)).astype(np.float32)
+    got = out[:, :, C0:C0 + G].astype(np.float32)
+    # same products and sums; the gates agree to f32 rounding
+    assert np.all(np.abs(got - y3) <= 2.0 ** -9 * np.abs(y3) + 1e-6)
+
+
 # ------------------------------------------------------------------ end to end
 
 @pytest.fixture(scope="module")

@@ -117,10 +117,11 @@ def test_block0_reflect_pad_and_k5_conv():
 
 
 @pytest.mark.parametrize("dil", [2, 3, 4])
-def test_res2net_group_conv_in_place(dil):
+def test_reflect_pad_add_kernel(dil):
+    """vdk_reflect_pad_add: the Res2Net group input x_j + y_{j-1}, reflect padded, bit-exact."""
     rng = np.random.default_rng(20 + dil)
     T, C, G, j = T4S, 1024, 128, 3
-    announce(f"ecapa res2 group conv B={B} T={T} dil={dil}")
+    announce(f"ecapa reflect_pad_add B={B} T={T} dil={dil}")
     t1 = rng.standard_normal((B, T, C), dtype=np.float32).astype(np.float16)
     L = lib.lib()
     dt1 = lib.DeviceBuffer.from_array(t1)
@@ -132,20 +133,66 @@ def test_res2net_group_conv_in_place(dil):
     want = np.pad(s, ((0, 0), (dil, dil), (0, 0)), mode="reflect").astype(np.float16)
     got_pad = padb.to_array(np.float16, (B, T + 2 * dil, G))
     assert np.array_equal(got_pad.view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("batch,T,dil", [(B, T4S, 2), (B, T4S, 3), (B, T4S, 4), (3, 9, 4), (2, 5, 2)])
+def test_res2net_group_conv_reflect_and_next_input(batch, T, dil):
+    """The encoder's Res2Net group conv: k=3 dilated over a channel slot of a
+    wide time-major tensor with SpeechBrain's reflect padding done by the conv
+    (no padded copy), + bias -> ReLU -> BN written into another slot, and the
+    second output y + r2 (the next group's input y_j + x_{j+1}); the other
+    slots stay untouched."""
+    rng = np.random.default_rng(30 + dil + T)
+    G = 128
+    S = 9 * G
+    announce(f"ecapa res2 group conv (reflect fold) B={batch} T={T} dil={dil}")
+    t1 = rng.standard_normal((batch, T, S), dtype=np.float32).astype(np.float16)
+    L = lib.lib()
+    dt1 = lib.DeviceBuffer.from_array(t1)
+    dy2 = lib.DeviceBuffer(batch * T * G * 2)
     w = _f16w(rng, G, G, 3)
     b = (0.01 * rng.standard_normal(G)).astype(np.float32)
     bn = _bn_params(rng, G)
-    db = lib.DeviceBuffer.from_array(b)
-    tdnn_gpu(padb.ptr, B, T + 2 * dil, G, G, w, dil, db, dt1.ptr + j * G * 2, C, bn=bn)
-    out = dt1.to_array(np.float16, (B, T, C))
-    keep = np.ones(C, dtype=bool)
-    keep[j * G:(j + 1) * G] = False
-    assert np.array_equal(out[:, :, keep].view(np.uint16), t1[:, :, keep].view(np.uint16))
-    got = out[:, :, j * G:(j + 1) * G].astype(np.float32)
-    for c in CLIPS:
-        ref = _oracle_tdnn(s[c].T, w, b, dil, bn)
+    sc, sh = _scale_shift(bn)
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(w.transpose(0, 2, 1))), lib.DeviceBuffer.from_array(b),
+            lib.DeviceBuffer.from_array(sc), lib.DeviceBuffer.from_array(sh)]
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = dt1.ptr + 2 * G * 2, batch, 1, T, G, S
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, G, 1, 3
+    d.stride_h, d.stride_w, d.pad_h, d.pad_w, d.dil_h, d.dil_w = 1, 1, 0, dil, 1, dil
+    d.reflect_pad = 1
+    d.bias, d.post_scale, d.post_shift = keep[1].ptr, keep[2].ptr, keep[3].ptr
+    d.act = lib.ACT_RELU
+    d.y, d.y_stride = dt1.ptr, S
+    d.y2, d.y2_stride, d.res2, d.res2_stride = dy2.ptr, G, dt1.ptr + 3 * G * 2, S
+    d.tile = -1
+    lib.check(L.vdk_conv2d_ex(d, None))
+    _sync()
+    out = dt1.to_array(np.float16, (batch, T, S))
+    assert np.array_equal(out[:, :, G:].view(np.uint16), t1[:, :, G:].view(np.uint16))
+    got = out[:, :, :G].astype(np.float32)
+    got2 = dy2.to_array(np.float16, (batch, T, G)).astype(np.float32)
+    r2 = t1[:, :, 3 * G:4 * G].astype(np.float32)
+    for c in sorted({0, batch // 2, batch - 1}):
+        x = t1[c, :, 2 * G:3 * G].astype(np.float32).T
+        ref = _oracle_tdnn(x, w, b, dil, bn)
         rel = _assert_close(got[c].T, ref, f"res2 dil {dil} clip {c}")
+        _assert_close(got2[c].T, ref + r2[c].T, f"res2 next input dil {dil} clip {c}")
+        # y2 = f16(v + r2) and y = f16(v) of the same v: within one f16 rounding of each other
+        lim = 2.0 ** -10 * (np.abs(got2[c]) + np.abs(got[c]) + np.abs(r2[c])) + 1e-6
+        assert np.all(np.abs(got2[c] - (got[c] + r2[c])) <= lim)
         announce(f"res2 dil {dil} clip {c} rel-L2 {rel:.2e}")
+    # the same conv without reflect padding reads zeros past the edges: the
+    # first / last dil frames must differ from the reflected result
+    d.reflect_pad = 0
+    dz = lib.DeviceBuffer(batch * T * S * 2)
+    d.y, d.y2 = dz.ptr, None
+    d.res2 = None
+    lib.check(L.vdk_conv2d_ex(d, None))
+    _sync()
+    z = dz.to_array(np.float16, (batch, T, S))[:, :, :G].astype(np.float32)
+    assert np.array_equal(z[:, dil:T - dil], got[:, dil:T - dil])
+    assert not np.array_equal(z[:, :dil], got[:, :dil])
 
 
 def test_1x1_layers_over_channel_slices():

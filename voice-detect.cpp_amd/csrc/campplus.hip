@@ -127,6 +127,174 @@ __global__ __launch_bounds__(256) void cam_context_kernel(const float* __restric
     }
 }
 
+// One dense layer's CAM layer in one launch (src/encoder_campplus.cpp:159-182,
+// 260-268): workgroup (clip b, segment s) of 256 threads
+//  0. DMAs the segment's input frames (with dil frames of halo each side,
+//     zeros outside the clip) and the linear_local weights into LDS (rows
+//     padded by 16 bytes), in flight during steps 1-2;
+//  1. sums x [b][.][C] over all T frames and over segment s (f64; thread
+//     (frame lane, 8-channel chunk), the frame lanes combined in a fixed order),
+//     ctx = sum_all / T + sum_seg / seg;
+//  2. gate = sigmoid(w2 relu(w1 ctx + b1) + b2) (f64 dot products, dot4);
+//  3. y = (linear_local(x) + bias) * gate for the segment's frames: the k = 3
+//     conv with dilation dil and zero padding as one 32 x 32 MFMA block per
+//     wave and 32 frames (K = 3 * C in tap-major, channel-minor order, the
+//     implicit-GEMM kernels' order), operands from LDS.
+// The segment's G = 32 outputs go to y [b][t][y_stride] f16.
+constexpr int kLocalOC = 32;
+constexpr uint32_t kOOB = 0x80000000u;   // any offset >= num_records reads as zero
+typedef __attribute__((address_space(3))) void lds_void;
+
+struct CamLocalLds {
+    int xrow, wrow, nrow, xins, wins, part_bytes, x_off, w_off, ctx_off, total;
+};
+__host__ __device__ inline CamLocalLds cam_local_lds(int C, int seg, int dil, int H1) {
+    CamLocalLds L;
+    L.xrow = C * 2 + 16;                         // frame row: C f16 + 16 bytes
+    L.wrow = 3 * C * 2 + 16;                     // weight row (output channel): 3*C f16 + 16 bytes
+    L.nrow = seg + 2 * dil;
+    L.xins = (L.nrow * (L.xrow / 16) + 63) / 64;   // DMA instructions (64 slots of 16 bytes each)
+    L.wins = (kLocalOC * (L.wrow / 16) + 63) / 64;
+    L.part_bytes = 8 * 2 * (256 / (C / 8)) * C;
+    L.x_off = 0;
+    L.w_off = L.xins * 1024;                       // the f64 partial sums follow the weights
+    L.ctx_off = L.w_off + L.wins * 1024 + L.part_bytes;
+    L.total = L.ctx_off + 4 * (((C + 3) & ~3) + ((H1 + 3) & ~3) + 32);
+    return L;
+}
+
+__global__ __launch_bounds__(256) void cam_local_kernel(const half_t* __restrict__ x, int xs, int T, int C, int seg,
+                                                        int dil, const float* __restrict__ w1,
+                                                        const float* __restrict__ b1, int H1,
+                                                        const float* __restrict__ w2, const float* __restrict__ b2,
+                                                        const half_t* __restrict__ wl, const float* __restrict__ bl,
+                                                        half_t* __restrict__ y, int ys) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const CamLocalLds Lo = cam_local_lds(C, seg, dil, H1);
+    uint8_t* const sx = smem + Lo.x_off;
+    uint8_t* const sw = smem + Lo.w_off;
+    double* part = reinterpret_cast<double*>(smem + Lo.w_off + Lo.wins * 1024);   // [2][256 / C8][C]
+    const int C8 = C >> 3, NFL = 256 / C8;
+    float* ctx = reinterpret_cast<float*>(smem + Lo.ctx_off);   // [C]
+    float* hid = ctx + ((C + 3) & ~3);                          // [H1]
+    float* gate = hid + ((H1 + 3) & ~3);                        // [32]
+    const int b = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int t0 = s * seg, t1 = min(T, t0 + seg);
+    const half_t* xb = x + (size_t)b * T * xs;
+    {   // 0. the segment's frames t0 - dil .. t1 + dil and the weights into LDS
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)xb, 0, (int)(((size_t)(T - 1) * xs + C) * 2), 0x00020000);
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)wl, 0, (int)((size_t)kLocalOC * 3 * C * 2), 0x00020000);
+        const int xspr = Lo.xrow / 16, wspr = Lo.wrow / 16;
+        for (int ins = wave; ins < Lo.xins; ins += 4) {
+            const int sl = ins * 64 + lane, r = sl / xspr, ch = sl - r * xspr;
+            const int tf = t0 - dil + r;
+            const uint32_t off = (r < Lo.nrow && ch < C / 8 && tf >= 0 && tf < T)
+                                     ? (uint32_t)(((size_t)tf * xs + ch * 8) * 2) : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx + ins * 1024), 16, off, 0, 0, 0);
+        }
+        for (int ins = wave; ins < Lo.wins; ins += 4) {
+            const int sl = ins * 64 + lane, r = sl / wspr, ch = sl - r * wspr;
+            const uint32_t off = (r < kLocalOC && ch < 3 * C / 8) ? (uint32_t)((r * 3 * C + ch * 8) * 2) : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(sw + ins * 1024), 16, off, 0, 0, 0);
+        }
+    }
+    {   // 1. sums
+        const int cc = tid % C8, fl = tid / C8;
+        double tot[8], sg[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tot[e] = sg[e] = 0.0;
+        if (fl < NFL) {
+            // kSumU frames per trip, their loads issued together
+            constexpr int kSumU = 16;
+            for (int t = fl; t < T; t += NFL * kSumU) {
+                half8 v[kSumU];
+#pragma unroll
+                for (int u = 0; u < kSumU; ++u) {
+                    const int tu = t + u * NFL;
+                    if (tu < T) {
+                        v[u] = *reinterpret_cast<const half8*>(xb + (size_t)tu * xs + cc * 8);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[u][e] = (half_t)0.0f;
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kSumU; ++u) {
+                    const int tu = t + u * NFL;
+                    const bool in = tu >= t0 && tu < t1;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const double f = (double)(float)v[u][e];
+                        tot[e] += f;
+                        if (in) sg[e] += f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                part[(size_t)fl * C + cc * 8 + e] = tot[e];
+                part[(size_t)(NFL + fl) * C + cc * 8 + e] = sg[e];
+            }
+        }
+    }
+    __syncthreads();
+    for (int c = tid; c < C; c += 256) {
+        double a = 0.0, g = 0.0;
+        for (int q = 0; q < NFL; ++q) {
+            a += part[(size_t)q * C + c];
+            g += part[(size_t)(NFL + q) * C + c];
+        }
+        ctx[c] = (float)(a / T) + (float)(g / seg);
+    }
+    __syncthreads();
+    {   // 2. the mask MLP
+        const int q = tid & 3;
+        for (int o = tid >> 2; o < H1; o += 64) {
+            const double a = dot4(w1 + (size_t)o * C, ctx, C, q);
+            if (q == 0) hid[o] = fmaxf((float)a + (b1 ? b1[o] : 0.0f), 0.0f);
+        }
+        __syncthreads();
+        for (int o = tid >> 2; o < kLocalOC; o += 64) {
+            const double a = dot4(w2 + (size_t)o * H1, hid, H1, q);
+            if (q == 0) gate[o] = 1.0f / (1.0f + expf(-((float)a + (b2 ? b2[o] : 0.0f))));
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's share of step 0 has landed
+    __syncthreads();
+
+    // 3. the gated conv: wave w covers frames t0 + 32 w .. + 31 of the segment;
+    // LDS row of frame t, tap k: (t - t0) + k * dil
+    const int j = lane & 31, kg = lane >> 5;
+    const int nks = 3 * C / 16;
+    for (int tb = t0 + wave * 32; tb < t1; tb += 4 * 32) {
+        const int t = tb + j;
+        const int rb = t - t0 < seg ? t - t0 : 0;   // lanes past the segment: any row, result dropped
+        float16v acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        for (int ks = 0; ks < nks; ++ks) {
+            const int k = ks * 16 + kg * 8, tap = k / C, ic = k - tap * C;
+            const half8 af = *reinterpret_cast<const half8*>(sw + j * Lo.wrow + k * 2);
+            const half8 bf = *reinterpret_cast<const half8*>(sx + (rb + tap * dil) * Lo.xrow + ic * 2);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc, 0, 0, 0);
+        }
+        if (t < t1) {
+            half_t* yr = y + ((size_t)b * T + t) * ys;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int oc = g * 8 + kg * 4;
+                half4 h;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) h[e] = (half_t)((acc[g * 4 + e] + (bl ? bl[oc + e] : 0.0f)) * gate[oc + e]);
+                *reinterpret_cast<half4*>(yr + oc) = h;
+            }
+        }
+    }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -175,6 +343,32 @@ extern "C" int vdk_cam_context(const float* d_sums, int batch, int T, int C, int
         hipLaunchKernelGGL(cam_context_kernel, dim3(batch, nseg), dim3(256), sizeof(float) * (((C + 3) & ~3) + H1),
                            static_cast<hipStream_t>(stream), d_sums, nseg, T, C, seg, d_w1, d_b1, H1, d_w2, d_b2,
                            G, d_gate);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_cam_local(const void* d_x, int x_stride, int batch, int T, int C, int seg, int dil,
+                             const float* d_w1, const float* d_b1, int H1, const float* d_w2, const float* d_b2,
+                             const void* d_wl, const float* d_bl, void* d_y, int y_stride, void* stream) {
+    return guarded([&] {
+        require(d_x && d_w1 && d_w2 && d_wl && d_y, "cam_local: NULL device pointer");
+        require(batch > 0 && T > 0 && seg > 0 && dil > 0 && H1 > 0, "cam_local: bad shape");
+        require(C % 16 == 0 && C >= 16 && C <= 256 && 256 % (C / 8) == 0,
+                "cam_local: C must be a multiple of 16 that divides into 256 / 8-channel lanes (16..256)");
+        require(x_stride >= C && x_stride % 8 == 0 && y_stride >= kLocalOC && y_stride % 4 == 0,
+                "cam_local: bad strides");
+        require(al16(d_x) && al16(d_wl) && al16(d_w1) && al16(d_w2) &&
+                    (reinterpret_cast<uintptr_t>(d_y) & 7) == 0,
+                "cam_local: x / weights must be 16-byte and y 8-byte aligned");
+        const int nseg = (T + seg - 1) / seg;
+        const size_t smem = (size_t)cam_local_lds(C, seg, dil, H1).total;
+        require(smem <= 160 * 1024, "cam_local: the segment tile and context buffers exceed the workgroup's LDS");
+        if (smem > 64 * 1024)
+            VDK_HIP(hipFuncSetAttribute((const void*)cam_local_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)smem));
+        hipLaunchKernelGGL(cam_local_kernel, dim3(batch, nseg), dim3(256), smem, static_cast<hipStream_t>(stream),
+                           static_cast<const half_t*>(d_x), x_stride, T, C, seg, dil, d_w1, d_b1, H1, d_w2, d_b2,
+                           static_cast<const half_t*>(d_wl), d_bl, static_cast<half_t*>(d_y), y_stride);
         VDK_HIP(hipGetLastError());
     });
 }

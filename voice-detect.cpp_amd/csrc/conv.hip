@@ -16,6 +16,7 @@
 //
 // stem_mfma_kernel: the IC=1 stem in f32 on v_mfma_f32_32x32x2_f32 (K = the 9
 // taps padded to 10); stem_conv3x3_kernel, the f32 FMA loop, serves OC = 16.
+#include <climits>
 #include <cstdlib>
 #include <type_traits>
 
@@ -50,6 +51,10 @@ struct ConvArgs {
     const float* in_shift;
     int npix;                  // B * Ho * Wo
     int npix_in;               // B * H * W
+    int reflect;               // 1-D time axis padded by reflection (DMA kernel only)
+    half_t* y2;                // second output y2 = v + r2 (may be NULL)
+    const half_t* r2;
+    int y2s, r2s;
 };
 
 // Epilogue for 8 consecutive output channels oc..oc+7 of pixel P (P
@@ -124,6 +129,13 @@ __device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float*
         Po = ((size_t)b * a.Wo + ow) * a.Ho + oh;
     }
     const size_t o = Po * a.ys + oc;
+    if (a.y2) {   // f16 only, no split, no time-major store (conv_impl)
+        const half8 r = *reinterpret_cast<const half8*>(a.r2 + (size_t)P * a.r2s + oc);
+        half8 h2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h2[e] = (half_t)(v[e] + (float)r[e]);
+        *reinterpret_cast<half8*>(a.y2 + (size_t)P * a.y2s + oc) = h2;
+    }
     if (a.y_f32) {
         float* y = static_cast<float*>(a.y) + o;
         *reinterpret_cast<float4v*>(y) = float4v{v[0], v[1], v[2], v[3]};
@@ -481,6 +493,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     int s_off[IPW];
     uint32_t s_mask[IPW];
     bool s_is_w[IPW];
+    int s_iw[IPW];   // reflect padding: the slot's tap-0 column (INT_MIN: no pixel)
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
         const int ins = wave + j * NW;
@@ -491,6 +504,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
         // that, so the weight/pixel split is per instruction (wave-uniform)
         s_is_w[j] = ins * (64 / CPR) < BM;
         s_mask[j] = 0;
+        s_iw[j] = INT_MIN;
         if (ins >= NINS) {
             s_off[j] = 0;   // padding instruction: zeros into the spare slots
         } else if (s_is_w[j]) {
@@ -503,6 +517,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
                 const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
                 const int ih0 = oh * a.sh - a.ph, iw0 = ow * a.sw - a.pw;
                 s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.xs + c * 8) * 2;
+                s_iw[j] = iw0;
                 if (tap_range) {
                     // one row of taps: the in-image ones are kw in [lo, hi)
                     const int lo = iw0 >= 0 ? 0 : (-iw0 + a.dw - 1) / a.dw;
@@ -537,7 +552,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
                 const bool in = tap_range ? (uint32_t)(f_tap - (int)(s_mask[j] & 0xFFFFu)) <
                                                 (uint32_t)((int)(s_mask[j] >> 16) - (int)(s_mask[j] & 0xFFFFu))
                                           : ((s_mask[j] >> f_tap) & 1u) != 0;
-                const uint32_t off = in ? (uint32_t)(s_off[j] + f_x + f_xc) : kOOB;
+                uint32_t off = in ? (uint32_t)(s_off[j] + f_x + f_xc) : kOOB;
+                if (a.reflect && !in && s_iw[j] != INT_MIN) {
+                    // the tap's column reflected back into [0, W) (KH = 1: f_tap is the column tap)
+                    int iw = s_iw[j] + f_tap * a.dw;
+                    iw = iw < 0 ? -iw : (iw >= a.W ? 2 * (a.W - 1) - iw : iw);
+                    iw = iw < 0 ? 0 : (iw >= a.W ? a.W - 1 : iw);
+                    off = (uint32_t)(s_off[j] + (iw - s_iw[j]) * a.xs * 2 + f_xc);
+                }
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, off, 0, 0, 0);
             }
         }
@@ -1964,14 +1986,14 @@ bool is_s1_3x3(const ConvArgs& a) {
     return a.KH == 3 && a.KW == 3 && a.sh == 1 && a.sw == 1 && a.ph == 1 && a.pw == 1 && a.dh == 1 && a.dw == 1;
 }
 
-constexpr int kFirstDma = 14, kFirstHalo = 26, kFirstDma8 = 33;
+constexpr int kFirstDma = 14;   // then the halo tiles from 26, 8-wave DMA tiles from 33
 
 // The register-weight kernels take the plain epilogue only: bias, residual,
 // ReLU or none, dense f16 NHWC in and out.
 bool plain_epilogue(const ConvArgs& a) {
     return !a.gate && !a.post_scale && !a.tanh_after && !a.y_f32 && !a.y_tr && !a.bias_bs && !a.split &&
            (a.act == VDK_ACT_NONE || (a.act == VDK_ACT_RELU && a.clamp_hi <= 0.0f)) && a.xs == a.IC &&
-           a.ys == a.OC && (!a.res || a.rs == a.OC) && !a.res_f32 && !a.res_after;
+           a.ys == a.OC && (!a.res || a.rs == a.OC) && !a.res_f32 && !a.res_after && !a.y2 && !a.reflect;
 }
 
 // The register-staged (igemm) entries: 0-13 and 62-63.
@@ -1982,6 +2004,8 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     if (t.halo && !is_s1_3x3(a)) return false;
     // the input prologue lives in the register-staged kernel's operand loads
     if (a.in_scale && !igemm_tile(idx)) return false;
+    // reflect padding lives in the LDS-DMA kernel's pixel offsets
+    if (a.reflect && (igemm_tile(idx) || t.halo)) return false;
     // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
     // the in-image tap range for a single row of taps; longer 2-D kernels
     // take the register-staged kernel
@@ -2286,7 +2310,17 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
                              (!d.residual || d.res_lo >= d.OC) && d.x_lo % 8 == 0 && d.y_lo % 8 == 0 &&
                              d.res_lo % 8 == 0 && d.IC % 32 == 0),
                 "conv2d: split-f16 needs IC % 32 == 0, f16 output and lo offsets past the channels");
+        require(!d.reflect_pad || (d.KH == 1 && d.pad_h == 0 && d.pad_w < d.W),
+                "conv2d: reflect padding is for 1-D convs (KH = 1) with pad_w < W");
+        const int y2s = d.y2_stride ? d.y2_stride : d.OC, r2s = d.res2_stride ? d.res2_stride : d.OC;
+        require(!d.y2 || (d.res2 && !d.split && !d.y_f32 && !d.y_time_major && aligned16(d.y2) &&
+                          aligned16(d.res2) && y2s >= d.OC && r2s >= d.OC && y2s % 8 == 0 && r2s % 8 == 0),
+                "conv2d: the second output needs res2, f16 NHWC output, 16-byte alignment and strides >= OC");
         ConvArgs a{};
+        a.reflect = d.reflect_pad ? 1 : 0;
+        a.y2 = static_cast<half_t*>(d.y2);
+        a.r2 = static_cast<const half_t*>(d.res2);
+        a.y2s = y2s; a.r2s = r2s;
         a.x = static_cast<const half_t*>(d.x);
         a.w = static_cast<const half_t*>(d.w);
         a.wc = static_cast<const half_t*>(d.w_chunked);
@@ -2370,6 +2404,8 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.y_f32 = d.y_f32 ? 1 : 0;
     a.y_tr = d.y_time_major ? 1 : 0;
     a.bias_bs = d.bias_batch_stride;
+    a.reflect = d.reflect_pad ? 1 : 0;
+    a.y2 = static_cast<half_t*>(d.y2);
     return a;
 }
 

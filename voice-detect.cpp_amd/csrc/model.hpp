@@ -263,7 +263,7 @@ private:
         void* fc_work = nullptr;
         size_t fc_work_bytes = 0;
         // ECAPA: time-major f16 activations and f32 per-clip vectors
-        void *x0p = nullptr, *h0 = nullptr, *t1 = nullptr, *t2 = nullptr, *padb = nullptr, *cat = nullptr,
+        void *x0p = nullptr, *h0 = nullptr, *t1 = nullptr, *t2 = nullptr, *s2b[2] = {nullptr, nullptr}, *cat = nullptr,
              *mfa = nullptr, *a1 = nullptr;
         float *logits = nullptr, *se_m = nullptr, *se_h = nullptr, *se_g = nullptr, *stats = nullptr,
               *pb = nullptr;
@@ -272,7 +272,6 @@ private:
         void* fcm_t = nullptr;
         void* dense[3] = {nullptr, nullptr, nullptr};
         void *cc = nullptr, *fin = nullptr;
-        float *sums = nullptr, *gate = nullptr;
         // ERes2Net
         void *ex[2] = {nullptr, nullptr}, *es4 = nullptr, *esc = nullptr, *ez = nullptr, *ez2 = nullptr,
              *ef = nullptr;
@@ -315,6 +314,8 @@ private:
     // input) -> y [B][W - (k-1)*dil][y_stride].
     void tdnn(const char* name, const Layer& l, const void* x, int x_stride, int batch, int W, int dil,
               const float* bias, int bias_bs, int relu, int tanh_after, void* y, int y_stride, int y_f32);
+    void res2_conv(const Layer& l, const void* x, int x_stride, int batch, int T, int dil, void* y, int y_stride,
+                   const void* r2, int r2_stride, void* y2);
     void linear(const char* name, const float* x, int batch, int in_dim, const float* w, const float* b,
                 const float* mv, int out_dim, int relu, float* y);
     void prof_begin(const char* name, double flops, double bytes);

@@ -11,10 +11,11 @@
 //            enough for its final width, every layer appending its growth
 //            channels in place (the reference's concat).  Per layer: linear1
 //            1x1 (+ReLU) with the layer's BN+ReLU applied to its operand as it
-//            is fetched (the normalised map is never stored) -> segment sums
-//            -> context MLP (one gate per clip and 100-frame segment) ->
-//            linear_local k=3 dilated conv with the gate applied in its
-//            epilogue.  The transit convs fold their BN+ReLU the same way.
+//            is fetched (the normalised map is never stored) -> one launch per
+//            (clip, 100-frame segment) for the CAM layer: segment sums,
+//            context MLP (one gate per clip and segment) and the k=3 dilated
+//            linear_local with the gate applied to its outputs.  The transit
+//            convs fold their BN+ReLU the same way.
 //   head     stats pooling (mean, unbiased std, no eps) -> dense 1x1 with the
 //            affine-free BatchNorm folded in -> L2.
 // Weights: conv weights f16 [OC][KH][KW][IC] (Q8_0 / F16 / F32 dequantised at
@@ -130,6 +131,8 @@ void Model::upload_campplus() {
             const HostConv& lc = conv(m.bn_ch, m.bn_ch, d.local);
             require(lc.kw == 3 && lc.kh == 1, "voicedetect: campplus linear_local must be a k=3 conv1d");
             m.growth = lc.oc;
+            require(m.growth == 32 && m.bn_ch % 16 == 0 && m.bn_ch <= 256,
+                    "voicedetect: campplus needs growth 32 and a bottleneck of 16..256 channels (multiple of 16)");
             // context MLP in f32 (dequantised)
             const int i1 = ci++, i2 = ci++;
             const HostConv c1 = read_conv(g, cp.conv_weight[i1]);
@@ -178,7 +181,6 @@ void Model::alloc_campplus_workspace(int batch, int T) {
     const Campplus& m = campp_;
     Workspace& w = ws_;
     const int Tp = (T - 1) / 2 + 1;
-    const int nseg = (Tp + kCamSeg - 1) / kCamSeg;
     const size_t BTp = (size_t)batch * Tp;
     for (int i = 0; i < 3; ++i) w.fcm[i] = ws_alloc(2 * (size_t)batch * m.n_mels * T * m.m_ch);
     w.fcm_t = ws_alloc(2 * (size_t)batch * T * m.hf * m.m_ch);
@@ -189,8 +191,6 @@ void Model::alloc_campplus_workspace(int batch, int T) {
     }
     w.cc = ws_alloc(2 * BTp * m.bn_ch);
     w.fin = ws_alloc(2 * BTp * m.c_out);
-    w.sums = static_cast<float*>(ws_alloc(4 * (size_t)batch * nseg * m.bn_ch));
-    w.gate = static_cast<float*>(ws_alloc(4 * (size_t)batch * nseg * m.growth));
     w.fc_work_bytes = vdk_linear_workspace_size(batch, pooled_dim_, cfg_.embedding_dim);
     w.fc_work = ws_alloc(w.fc_work_bytes);
 }
@@ -287,16 +287,14 @@ void Model::encode_campplus(int batch, int T) {
             // linear1's operand loads
             tconv("campp_linear1", d.l1, D, blk.cmax, Tp, 1, 0, 1, nullptr, VDK_ACT_RELU, w.cc, m.bn_ch, d.bn_s,
                   d.bn_t);
-            prof_begin("campp_seg_sums", 0.0, 2.0 * rows * m.bn_ch);
-            check_rc(vdk_segment_sums(w.cc, m.bn_ch, batch, Tp, m.bn_ch, kCamSeg, w.sums, stream_));
+            // the CAM layer: context sums, mask MLP and the gated linear_local in one launch
+            prof_begin("campp_cam_local",
+                       2.0 * rows * 3 * m.bn_ch * m.growth +
+                           2.0 * batch * nseg * ((double)d.h1 * m.bn_ch + (double)m.growth * d.h1),
+                       2.0 * rows * m.bn_ch * (1.0 + nseg) + 2.0 * rows * m.growth);
+            check_rc(vdk_cam_local(w.cc, m.bn_ch, batch, Tp, m.bn_ch, kCamSeg, blk.dil, d.c1_w, d.c1_b, d.h1, d.c2_w,
+                                   d.c2_b, d.local.w, d.local.b, D + 2 * (size_t)d.c_in, blk.cmax, stream_));
             prof_end();
-            prof_begin("campp_cam_context", 2.0 * batch * nseg * ((double)d.h1 * m.bn_ch + (double)m.growth * d.h1),
-                       4.0 * ((double)d.h1 * m.bn_ch + (double)m.growth * d.h1));
-            check_rc(vdk_cam_context(w.sums, batch, Tp, m.bn_ch, kCamSeg, d.c1_w, d.c1_b, d.h1, d.c2_w, d.c2_b,
-                                     m.growth, w.gate, stream_));
-            prof_end();
-            tconv("campp_linear_local", d.local, w.cc, m.bn_ch, Tp, 1, blk.dil, blk.dil, w.gate, VDK_ACT_NONE,
-                  D + 2 * (size_t)d.c_in, blk.cmax);
         }
         const bool last = b == 2;
         tconv("campp_transit", blk.transit, D, blk.cmax, Tp, 1, 0, 1, nullptr, last ? VDK_ACT_RELU : VDK_ACT_NONE,

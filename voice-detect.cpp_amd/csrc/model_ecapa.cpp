@@ -4,8 +4,10 @@
 // NHWC layout of the conv kernels with H = 1, W = T), so a TDNN layer is one
 // implicit-GEMM launch with its ReLU and eval BatchNorm in the epilogue:
 //   block0     feats -> reflect-padded [B][T+4][96] -> conv k=5 1024
-//   block i    tdnn1 (1x1) -> Res2Net groups (reflect-pad(+add) -> k=3 dil i+1,
-//              written back into the group's channel slice) -> tdnn2 (1x1)
+//   block i    tdnn1 (1x1) -> Res2Net groups (k=3 dil i+1 convs with the
+//              reflect padding in the conv's input offsets; each group's
+//              epilogue also writes the next group's input y_j + x_{j+1})
+//              -> tdnn2 (1x1)
 //              -> SE (mean -> FC+ReLU -> FC -> sigmoid gate + residual), stored
 //              straight into channel slice i-1 of the MFA input `cat`
 //   mfa        1x1 over cat
@@ -17,6 +19,7 @@
 // 80 -> 96), f32 for the SE / ASP-context / fc matrices.
 #include <algorithm>
 #include <cmath>
+#include <functional>
 #include <string>
 
 #include "arena.hpp"
@@ -55,8 +58,10 @@ void Model::upload_ecapa() {
         require(v.size() == expect, "voicedetect: tensor '" + name + "' has the wrong size");
         return v;
     };
-    // Conv weight [OC][IC][K] -> f16 [OC][K][icp], channels ic..icp zero.
-    auto layer = [&](const std::string& prefix, int ic_expect, int icp, Layer& l) {
+    // Conv weight [OC][IC][K] -> f16 [OC][K][icp], channels ic..icp zero;
+    // input channel i lands at ic_map(i) when given.
+    auto layer = [&](const std::string& prefix, int ic_expect, int icp, Layer& l,
+                     const std::function<int(int)>& ic_map = nullptr) {
         const std::string wn = prefix + ".weight";
         const ConvShape s = conv_shape(g, wn);
         require(s.ic == ic_expect, "voicedetect: '" + wn + "' has " + std::to_string(s.ic) +
@@ -67,7 +72,8 @@ void Model::upload_ecapa() {
         for (int o = 0; o < s.oc; ++o)
             for (int i = 0; i < s.ic; ++i)
                 for (int k = 0; k < s.k; ++k)
-                    packed[((size_t)o * s.k + k) * icp + i] = float_to_half_bits(w[((size_t)o * s.ic + i) * s.k + k]);
+                    packed[((size_t)o * s.k + k) * icp + (ic_map ? ic_map(i) : i)] =
+                        float_to_half_bits(w[((size_t)o * s.ic + i) * s.k + k]);
         l.ic = icp; l.oc = s.oc; l.k = s.k;
         arena.put(packed, &l.w);
         arena.put(f32(prefix + ".bias", (size_t)s.oc), &l.b);
@@ -123,7 +129,11 @@ void Model::upload_ecapa() {
             require(sj.oc == grp && sj.k == 3, "voicedetect: " + q + " must be a k=3 conv of the group width");
             bn(q + ".norm.norm", grp, b.res[j]);
         }
-        layer(p + ".tdnn2.conv.conv", C, C, b.tdnn2);
+        // tdnn2 reads the Res2Net output slots in the order [y_1 | x_0 | y_2 .. y_{scale-1}]
+        // (encode_ecapa): input channel groups 0 and 1 swap
+        layer(p + ".tdnn2.conv.conv", C, C, b.tdnn2, [grp](int c) {
+            return c < grp ? c + grp : (c < 2 * grp ? c - grp : c);
+        });
         require(b.tdnn2.oc == C, "voicedetect: " + p + ".tdnn2 must keep the channel count");
         bn(p + ".tdnn2.norm.norm", C, b.tdnn2);
         const ConvShape se1 = conv_shape(g, p + ".se_block.conv1.conv.weight");
@@ -198,11 +208,9 @@ void Model::alloc_ecapa_workspace(int batch, int T) {
     Workspace& w = ws_;
     const size_t BT = (size_t)batch * T;
     const int pad0 = (e.block0.k - 1) / 2;
-    int dmax = 1;
     size_t fc_work = vdk_linear_workspace_size(batch, 2 * e.mfa, cfg_.embedding_dim);
     fc_work = std::max(fc_work, vdk_linear_workspace_size(batch, 2 * e.mfa, e.att));
     for (const EcapaBlock& b : e.blocks) {
-        dmax = std::max(dmax, b.dil);
         fc_work = std::max(fc_work, vdk_linear_workspace_size(batch, e.C, b.se_ch));
         fc_work = std::max(fc_work, vdk_linear_workspace_size(batch, b.se_ch, e.C));
     }
@@ -211,9 +219,10 @@ void Model::alloc_ecapa_workspace(int batch, int T) {
     for (const EcapaBlock& b : e.blocks) se_max = std::max(se_max, b.se_ch);
     w.x0p = ws_alloc(2 * (size_t)batch * (T + 2 * pad0) * e.c_pad0);
     w.h0 = ws_alloc(2 * BT * e.C);
-    w.t1 = ws_alloc(2 * BT * e.C);
+    w.t1 = ws_alloc(2 * BT * (e.C + e.group));   // scale + 1 group slots per frame
+    w.s2b[0] = ws_alloc(2 * BT * e.group);
+    w.s2b[1] = ws_alloc(2 * BT * e.group);
     w.t2 = ws_alloc(2 * BT * e.C);
-    w.padb = ws_alloc(2 * (size_t)batch * (T + 2 * dmax) * e.group);
     w.cat = ws_alloc(2 * BT * nb * e.C);
     w.mfa = ws_alloc(2 * BT * e.mfa);
     w.a1 = ws_alloc(2 * BT * e.att);
@@ -250,6 +259,32 @@ void Model::tdnn(const char* name, const Layer& l, const void* x, int x_stride, 
     prof_end();
 }
 
+// One Res2Net group conv: k=3 dilated over T frames with SpeechBrain's
+// reflect padding (src/encoder.cpp:32-52) folded into the conv's input
+// offsets, + bias -> ReLU -> BN; y2 (optional) = that output + r2 (the next
+// group's input).
+void Model::res2_conv(const Layer& l, const void* x, int x_stride, int batch, int T, int dil, void* y, int y_stride,
+                      const void* r2, int r2_stride, void* y2) {
+    if (profiling_) {
+        const double npix = (double)batch * T;
+        const double bytes = 2.0 * (npix * l.ic + (double)l.oc * l.k * l.ic) + npix * l.oc * (y2 ? 6.0 : 2.0);
+        prof_begin("conv.ecapa_res2_conv", 2.0 * l.k * l.ic * l.oc * npix, bytes);
+    }
+    vdk_conv_desc d{};
+    d.x = x; d.batch = batch; d.H = 1; d.W = T; d.IC = l.ic; d.x_stride = x_stride;
+    d.w = l.w; d.OC = l.oc; d.KH = 1; d.KW = l.k;
+    d.stride_h = d.stride_w = 1; d.dil_h = 1; d.dil_w = dil;
+    d.pad_w = (l.k - 1) / 2 * dil; d.reflect_pad = 1;
+    d.bias = l.b;
+    d.post_scale = l.scale; d.post_shift = l.shift;
+    d.act = VDK_ACT_RELU;
+    d.y = y; d.y_stride = y_stride;
+    d.y2 = y2; d.y2_stride = l.oc; d.res2 = r2; d.res2_stride = r2_stride;
+    d.tile = -1;
+    check_rc(vdk_conv2d_ex(&d, stream_));
+    prof_end();
+}
+
 void Model::linear(const char* name, const float* x, int batch, int in_dim, const float* w, const float* b,
                    const float* mv, int out_dim, int relu, float* y) {
     prof_begin(name, 2.0 * batch * (double)in_dim * out_dim,
@@ -276,20 +311,24 @@ void Model::encode_ecapa(int batch, int T) {
         const EcapaBlock& b = e.blocks[i];
         const void* xin = i == 0 ? w.h0 : static_cast<const uint8_t*>(w.cat) + 2 * (size_t)(i - 1) * C;
         const int xs = i == 0 ? C : catS;
-        tdnn("ecapa_tdnn1", b.tdnn1, xin, xs, batch, T, 1, b.tdnn1.b, 0, 1, 0, w.t1, C, 0);
-        // Res2Net: group 0 passes through; group j reads x_j (+ y_{j-1}) and
-        // overwrites its own slice of t1 with y_j (src/encoder.cpp:174-200).
+        // t1 holds scale + 1 group slots per frame (stride S = C + G): tdnn1
+        // writes x_0 .. x_{scale-1} to slots 1 .. scale; group j reads its
+        // input (x_1 from slot 2, then y_{j-1} + x_j from s2b[j & 1]) with the
+        // reflect padding done by the conv, writes y_j to slot j (group 1:
+        // slot 0), whose x_{j-1} every earlier launch has consumed, and, for
+        // j < scale - 1, y_j + x_{j+1} to s2b[(j + 1) & 1]; tdnn2 then reads
+        // slots 0 .. scale-1 = [y_1 | x_0 | y_2 .. y_{scale-1}] (its weight
+        // columns permuted to match) (src/encoder.cpp:174-200).
+        const int S = C + G;
         uint8_t* t1 = static_cast<uint8_t*>(w.t1);
+        tdnn("ecapa_tdnn1", b.tdnn1, xin, xs, batch, T, 1, b.tdnn1.b, 0, 1, 0, t1 + gB, S, 0);
         for (int j = 1; j < e.scale; ++j) {
-            prof_begin("ecapa_res2_pad", 0.0, 2.0 * batch * (double)T * G * (j >= 2 ? 2 : 1) +
-                                                  2.0 * batch * (T + 2.0 * b.dil) * G);
-            check_rc(vdk_reflect_pad_add(t1 + j * gB, C, j >= 2 ? t1 + (j - 1) * gB : nullptr, C, batch, T, G,
-                                         b.dil, w.padb, stream_));
-            prof_end();
-            tdnn("ecapa_res2_conv", b.res[j - 1], w.padb, G, batch, T + 2 * b.dil, b.dil, b.res[j - 1].b, 0, 1, 0,
-                 t1 + j * gB, C, 0);
+            const bool last = j + 1 == e.scale;
+            const void* in = j == 1 ? static_cast<const void*>(t1 + 2 * gB) : w.s2b[j & 1];
+            res2_conv(b.res[j - 1], in, j == 1 ? S : G, batch, T, b.dil, t1 + (j == 1 ? 0 : j) * gB, S,
+                      last ? nullptr : t1 + (j + 2) * gB, S, last ? nullptr : w.s2b[(j + 1) & 1]);
         }
-        tdnn("ecapa_tdnn2", b.tdnn2, w.t1, C, batch, T, 1, b.tdnn2.b, 0, 1, 0, w.t2, C, 0);
+        tdnn("ecapa_tdnn2", b.tdnn2, w.t1, S, batch, T, 1, b.tdnn2.b, 0, 1, 0, w.t2, C, 0);
         // SE (src/encoder.cpp:207-219) and the residual (src/encoder.cpp:243)
         prof_begin("ecapa_se_mean", 0.0, 2.0 * batch * (double)T * C);
         check_rc(vdk_channel_mean(w.t2, C, batch, T, C, w.se_m, stream_));

@@ -44,7 +44,9 @@ class ConvDesc(C.Structure):
                 ("y", _vp), ("y_stride", C.c_int), ("y_f32", C.c_int), ("y_time_major", C.c_int),
                 ("split", C.c_int), ("x_lo", C.c_int), ("res_lo", C.c_int), ("y_lo", C.c_int),
                 ("tile", C.c_int), ("res_f32", C.c_int), ("res_after_act", C.c_int), ("out_w", C.c_int),
-                ("in_scale", _vp), ("in_shift", _vp), ("w_chunked", _vp)]
+                ("in_scale", _vp), ("in_shift", _vp), ("w_chunked", _vp),
+                ("reflect_pad", C.c_int), ("y2", _vp), ("y2_stride", C.c_int), ("res2", _vp),
+                ("res2_stride", C.c_int)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
@@ -151,6 +153,8 @@ _SIGS = {
                                   C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp]),
     "vdk_bn_act": (C.c_int, [_vp, C.c_int, C.c_long, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, _vp]),
     "vdk_segment_sums": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_cam_local": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int,
+                                _vp, _vp, _vp, _vp, _vp, C.c_int, _vp]),
     "vdk_cam_context": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int,
                                   _vp, _vp]),
 }
