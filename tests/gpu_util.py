@@ -9,10 +9,9 @@ from vdamd import lib
 
 
 def device_ok():
-    try:
-        return lib.lib().vdk_device_count() > 0
-    except Exception:
-        return False
+    """Whether a HIP device is visible.  A library that fails to load raises
+    here (every GPU test then errors) instead of reading as "no device"."""
+    return lib.lib().vdk_device_count() > 0
 
 
 def announce(msg):
