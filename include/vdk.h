@@ -125,6 +125,12 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * must be below W.  y2 (may be NULL): a second f16 output y2 = v + res2 (v the
  * finished value above, res2 f16 at the same pixel, both with their own pixel
  * strides), e.g. the next Res2Net group's input y_j + x_{j+1}.
+ * w_q8_0 (may be NULL; 1x1 convs with IC % 32 == 0, no split): the weights as
+ * ggml q8_0 blocks straight from the model file, [OC][IC/32] blocks of 34
+ * bytes (an f16 scale d, then 32 int8 quants q along IC), dequantised in the
+ * kernel's registers to f16(q * d) (the product in f32: the f16 weights a
+ * host dequantisation would store, so results equal those from w); w is then
+ * not read.
  * tile = -1 picks the kernel automatically. */
 typedef struct {
     const void* x; int batch, H, W, IC, x_stride;
@@ -145,6 +151,7 @@ typedef struct {
     int reflect_pad;
     void* y2; int y2_stride;
     const void* res2; int res2_stride;
+    const void* w_q8_0;
 } vdk_conv_desc;
 /* Host: re-order f16 conv weights [OC][KH][KW][IC] (IC % 16 == 0) into the
  * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */

@@ -15,7 +15,7 @@ import pytest
 import pyoracle as O
 from gpu_util import announce, close_report, conv_gpu, device_ok, tile_fits
 from test_oracle_fbank import _cases, _cfg, golden_pcm
-from vdamd import lib, synth
+from vdamd import gguf, lib, synth
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
 
@@ -279,6 +279,58 @@ def test_conv_rejects_bad_shapes():
     assert "OC" in L.vdk_last_error().decode()
     assert L.vdk_conv2d_nhwc(None, 1, 4, 4, 32, d.ptr, 32, 3, 3, 1, 1, None, None, 0, d.ptr, None) != 0
     assert L.vdk_conv2d_nhwc(d.ptr, 1, 1, 1, 32, d.ptr, 32, 3, 3, 1, 0, None, None, 0, d.ptr, None) != 0
+
+
+@pytest.mark.parametrize("IC,OC,npix,prologue", [(128, 128, 15968, True), (352, 128, 15968, True),
+                                               (1024, 512, 4096, True), (96, 40, 777, False), (32, 64, 300, True)])
+def test_conv_q8_0_weights_dequantised_in_registers(IC, OC, npix, prologue):
+    """1x1 convs reading q8_0 blocks straight from the model-file layout
+    (vdk_conv_desc.w_q8_0) equal, bit for bit, the same convs on the
+    host-dequantised f16 weights f16(q * d), on every register-staged tile
+    that takes the shape, with and without the BN+ReLU input prologue."""
+    L = lib.lib()
+    rng = np.random.default_rng(IC + OC + npix)
+    announce(f"q8_0 1x1 IC={IC} OC={OC} npix={npix} prologue={prologue}")
+    w = (rng.standard_normal((OC, IC)) * np.sqrt(2.0 / IC)).astype(np.float32)
+    w[3 % OC, :32] = 0.0                                   # an all-zero block (d = 0)
+    raw = gguf.quantize_q8_0(w)                            # [OC][IC/32] blocks of 34 bytes
+    wdeq = gguf.dequantize_q8_0(raw.tobytes(), OC * IC).reshape(OC, IC)
+    wf16 = wdeq.astype(np.float16)                         # what the host upload stores
+    x = rng.standard_normal((1, 1, npix, IC)).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, OC).astype(np.float32)
+    sc = rng.uniform(0.5, 1.5, IC).astype(np.float32)
+    sh = rng.uniform(-0.5, 0.5, IC).astype(np.float32)
+    keep = [lib.DeviceBuffer.from_array(a) for a in (x, wf16, raw, b, sc, sh)]
+    dx, dwf, dwq, db, dsc, dsh = keep
+    outs = {}
+    for q8 in (False, True):
+        for t in range(L.vdk_conv2d_tile_count()):
+            d = lib.ConvDesc()
+            d.x, d.batch, d.H, d.W, d.IC = dx.ptr, 1, 1, npix, IC
+            d.w, d.OC, d.KH, d.KW = (None if q8 else dwf.ptr), OC, 1, 1
+            d.w_q8_0 = dwq.ptr if q8 else None
+            d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+            d.bias, d.act = db.ptr, lib.ACT_RELU
+            if prologue:
+                d.in_scale, d.in_shift = dsc.ptr, dsh.ptr
+            if not L.vdk_conv2d_tile_fits_ex(t, d) or (t >= 14 and t < 62):
+                continue
+            dy = lib.DeviceBuffer(npix * OC * 2)
+            d.y, d.tile = dy.ptr, t
+            lib.check(L.vdk_conv2d_ex(d, None))
+            lib.check(L.vdk_synchronize())
+            outs[(q8, t)] = dy.to_array(np.float16, (npix, OC))
+    tiles = sorted(t for (q, t) in outs if q)
+    assert tiles and tiles == sorted(t for (q, t) in outs if not q)
+    for t in tiles:
+        assert np.array_equal(outs[(True, t)].view(np.uint16), outs[(False, t)].view(np.uint16)), f"tile {t}"
+    # and the f16 path against the oracle's conv on the dequantised weights
+    xin = x[0, 0].astype(np.float32)
+    if prologue:
+        xin = np.maximum(xin * sc + sh, 0).astype(np.float16).astype(np.float32)
+    ref = np.maximum(xin @ wf16.astype(np.float32).T + b, 0)
+    ok, ratio, rel = close_report(outs[(True, tiles[0])].astype(np.float32), ref, CONV_RTOL, CONV_ATOL_RMS)
+    assert ok, (ratio, rel)
 
 
 @pytest.mark.parametrize("B,H,W,OC,split", [(64, 80, 298, 32, 0), (3, 7, 37, 64, 0), (2, 9, 33, 32, 1),

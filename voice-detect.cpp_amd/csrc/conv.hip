@@ -55,6 +55,7 @@ struct ConvArgs {
     half_t* y2;                // second output y2 = v + r2 (may be NULL)
     const half_t* r2;
     int y2s, r2s;
+    const uint8_t* wq;         // 1x1 weights as q8_0 blocks [OC][IC/32] x {f16 d, 32 x int8} (register-staged kernel)
 };
 
 // Epilogue for 8 consecutive output channels oc..oc+7 of pixel P (P
@@ -226,8 +227,11 @@ __device__ __forceinline__ void stage_epilogue_impl(const ConvArgs& a, uint8_t* 
 constexpr uint32_t kOOB = 0x80000000u;   // any offset >= num_records reads as zero
 
 // PRO: the input prologue relu(x * in_scale + in_shift) (its scale / shift
-// registers exist only in these instantiations).
-template <int BM, int BN, int WM, int WN, int KC, bool PRO>
+// registers exist only in these instantiations).  Q8: 1x1 weights read as
+// q8_0 blocks (34 bytes: an f16 scale d and 32 int8 quants q along IC) and
+// dequantised in registers, w = f16(q * d) with the product in f32, the value
+// a host-side dequantisation to f16 stores.
+template <int BM, int BN, int WM, int WN, int KC, bool PRO, bool Q8 = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(ConvArgs a) {
     constexpr int NWM = BM / WM, NWN = BN / WN, NT = NWM * NWN * 64;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -274,12 +278,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
     uint32_t w_off[WCH];   // byte offset of the slot's weight row at chunk 0 (kOOB: no such row)
     int w_lds[WCH];
     bool w_on[WCH];        // slot is part of the tile
+    const int nqb = a.IC >> 5;   // Q8: blocks per weight row
 #pragma unroll
     for (int i = 0; i < WCH; ++i) {
         const int q = tid + i * NT;
         const int r = q / CPR, c8 = q - r * CPR;
         w_on[i] = q < BM * CPR;
-        w_off[i] = w_on[i] && oc0 + r < a.OC ? (uint32_t)(((size_t)(oc0 + r) * KHW * a.IC + c8 * 8) * 2) : kOOB;
+        if constexpr (Q8)   // the row's first block; the slot's channels c8*8.. are added per chunk
+            w_off[i] = w_on[i] && oc0 + r < a.OC ? (uint32_t)((oc0 + r) * nqb * 34) : kOOB;
+        else
+            w_off[i] = w_on[i] && oc0 + r < a.OC ? (uint32_t)(((size_t)(oc0 + r) * KHW * a.IC + c8 * 8) * 2) : kOOB;
         w_lds[i] = r * LDK + c8 * 8;
     }
     // buffer loads: a masked lane reads an out-of-range offset (zero), so every
@@ -287,7 +295,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)((size_t)a.OC * KHW * a.IC * 2), 0x00020000);
+        Q8 ? __builtin_amdgcn_make_buffer_rsrc((void*)a.wq, 0, a.OC * nqb * 34, 0x00020000)
+           : __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)((size_t)a.OC * KHW * a.IC * 2), 0x00020000);
 
     // With the prologue (long-K 1x1 GEMMs) two register slots: chunk k+2 is
     // loaded while chunk k feeds the MFMAs and chunk k+1 waits in the other
@@ -305,8 +314,28 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         const uint32_t wd = (uint32_t)((tap * a.IC + c0) * 2);
 #pragma unroll
         for (int i = 0; i < WCH; ++i) {
-            const uint32_t off = w_off[i] == kOOB ? kOOB : w_off[i] + wd;
-            wr[s][i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+            if constexpr (Q8) {
+                // channels k .. k+7 of the row (1x1: k = c0 + c8*8) sit at byte
+                // 2 + k%32 of block k/32: a 2-byte aligned run, read as three
+                // aligned dwords and shifted into place
+                const int kq = c0 + ((tid + i * NT) % CPR) * 8;
+                const uint32_t blk = w_off[i] == kOOB ? kOOB : w_off[i] + (uint32_t)((kq >> 5) * 34);
+                const uint32_t qo = blk == kOOB ? kOOB : blk + 2 + (uint32_t)(kq & 31);
+                const uint32_t sh = (qo & 3) * 8;
+                const auto d3 = __builtin_amdgcn_raw_buffer_load_b96(wrs, qo & ~3u, 0, 0);
+                const uint32_t lo = sh ? (d3[0] >> sh) | (d3[1] << (32 - sh)) : d3[0];
+                const uint32_t hi = sh ? (d3[1] >> sh) | (d3[2] << (32 - sh)) : d3[1];
+                const float d = (float)__builtin_bit_cast(half_t, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(
+                                                                      wrs, blk, 0, 0));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    wr[s][i][e] = (half_t)((float)(int8_t)(lo >> (8 * e)) * d);
+                    wr[s][i][e + 4] = (half_t)((float)(int8_t)(hi >> (8 * e)) * d);
+                }
+            } else {
+                const uint32_t off = w_off[i] == kOOB ? kOOB : w_off[i] + wd;
+                wr[s][i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+            }
         }
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
@@ -1888,8 +1917,12 @@ template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
     dim3 grid(cdiv(a.npix, BN), cdiv(a.OC, BM));
-    if (a.in_scale)
+    if (a.in_scale && a.wq)
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, true, true>), grid, dim3(NT), 0, s, a);
+    else if (a.in_scale)
         hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, true>), grid, dim3(NT), 0, s, a);
+    else if (a.wq)
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, false, true>), grid, dim3(NT), 0, s, a);
     else
         hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, false>), grid, dim3(NT), 0, s, a);
 }
@@ -2006,6 +2039,8 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     if (a.in_scale && !igemm_tile(idx)) return false;
     // reflect padding lives in the LDS-DMA kernel's pixel offsets
     if (a.reflect && (igemm_tile(idx) || t.halo)) return false;
+    // q8_0 weights are dequantised in the register-staged kernel's weight loads
+    if (a.wq && !igemm_tile(idx)) return false;
     // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
     // the in-image tap range for a single row of taps; longer 2-D kernels
     // take the register-staged kernel
@@ -2269,7 +2304,7 @@ using namespace vdk;
 namespace {
 int conv_impl(const vdk_conv_desc& d, void* stream) {
     return guarded([&] {
-        require(d.x && d.w && d.y, "conv2d: NULL device pointer");
+        require(d.x && (d.w || d.w_q8_0) && d.y, "conv2d: NULL device pointer");
         require(d.batch > 0 && d.H > 0 && d.W > 0, "conv2d: empty input");
         require(d.IC > 0 && d.IC % 16 == 0, "conv2d: IC must be a positive multiple of 16");
         require(d.OC > 0 && d.OC % 8 == 0, "conv2d: OC must be a positive multiple of 8");
@@ -2316,7 +2351,12 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         require(!d.y2 || (d.res2 && !d.split && !d.y_f32 && !d.y_time_major && aligned16(d.y2) &&
                           aligned16(d.res2) && y2s >= d.OC && r2s >= d.OC && y2s % 8 == 0 && r2s % 8 == 0),
                 "conv2d: the second output needs res2, f16 NHWC output, 16-byte alignment and strides >= OC");
+        require(!d.w_q8_0 || (d.KH == 1 && d.KW == 1 && d.IC % 32 == 0 && !d.split &&
+                               (reinterpret_cast<uintptr_t>(d.w_q8_0) & 3) == 0 &&
+                               (long)d.OC * (d.IC / 32) * 34 < (1L << 31)),
+                "conv2d: q8_0 weights are for 1x1 convs with IC % 32 == 0 and no split-f16");
         ConvArgs a{};
+        a.wq = static_cast<const uint8_t*>(d.w_q8_0);
         a.reflect = d.reflect_pad ? 1 : 0;
         a.y2 = static_cast<half_t*>(d.y2);
         a.r2 = static_cast<const half_t*>(d.res2);
@@ -2406,6 +2446,7 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.bias_bs = d.bias_batch_stride;
     a.reflect = d.reflect_pad ? 1 : 0;
     a.y2 = static_cast<half_t*>(d.y2);
+    a.wq = static_cast<const uint8_t*>(d.w_q8_0);
     return a;
 }
 

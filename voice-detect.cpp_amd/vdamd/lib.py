@@ -46,7 +46,7 @@ class ConvDesc(C.Structure):
                 ("tile", C.c_int), ("res_f32", C.c_int), ("res_after_act", C.c_int), ("out_w", C.c_int),
                 ("in_scale", _vp), ("in_shift", _vp), ("w_chunked", _vp),
                 ("reflect_pad", C.c_int), ("y2", _vp), ("y2_stride", C.c_int), ("res2", _vp),
-                ("res2_stride", C.c_int)]
+                ("res2_stride", C.c_int), ("w_q8_0", _vp)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
