@@ -57,9 +57,10 @@ CLIP_SEED = 1234
 # launches), each scaled by copy bytes / the counter's reading for a 256 MiB
 # device copy in the same run.
 TRAFFIC_BYTES_PER_LAUNCH = {
-    # conv3x3_band_kernel<5,6> (the 11 stride-1 128->128 convs per step):
-    # FETCH 23413 KiB x 2.00, WRITE 24000 KiB x 1.00
-    ("resnet34", "conv3x3_s1_128to128"): 72.52e6,
+    # conv3x3_bandws_kernel<5, 75, 2, 4, 3, 4> (the 11 stride-1 128->128 convs
+    # per step): FETCH 48.03 MB, WRITE 24.58 MB per launch after the copy
+    # calibration, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this bench
+    ("resnet34", "conv3x3_s1_128to128"): 72.61e6,
 }
 
 # The reference's own published figures for these workloads (per clip, batch 1;

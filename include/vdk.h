@@ -273,6 +273,8 @@ int vdk_asp_pool(const float* d_logits, int l_stride, const void* d_x, int x_str
  * Replaces the host L2 of src/encoder_resnet.cpp:177-183 (double accumulation,
  * skipped when the norm is 0).  In place on x [B][dim]. */
 int vdk_l2norm(float* d_x, int batch, int dim, void* stream);
+/* Same, out of place: y [B][dim] = x / ||x|| (y may equal x; a zero row is copied). */
+int vdk_l2norm_to(const float* d_x, int batch, int dim, float* d_y, void* stream);
 
 /* ---- registry scoring: identify queries against enrolled embeddings ----
  * No counterpart in the reference's code: README.md:15 promises `identify`,

@@ -388,9 +388,12 @@ def test_tstp_linear_l2_match_oracle():
     lib.check(L.vdk_synchronize())
     pooled = dp.to_array(np.float32, (B, P))
     pre = dy.to_array(np.float32, (B, E))
+    dn = lib.DeviceBuffer(B * E * 4)
+    lib.check(L.vdk_l2norm_to(dy.ptr, B, E, dn.ptr, None))     # out of place: y keeps the pre-norm rows
     lib.check(L.vdk_l2norm(dy.ptr, B, E, None))
     lib.check(L.vdk_synchronize())
     emb = dy.to_array(np.float32, (B, E))
+    assert np.array_equal(dn.to_array(np.float32, (B, E)), emb)
     for c in (0, 17, 63):
         rp = O.tstp(x[c].astype(np.float32).transpose(2, 0, 1), 1e-8)
         assert np.allclose(pooled[c], rp, rtol=1e-5, atol=1e-5)

@@ -181,14 +181,15 @@ int linear_splits(int in_dim) {
 }
 
 // In-place L2 normalisation, one wavefront per clip (src/encoder_resnet.cpp:177-183).
-__global__ __launch_bounds__(64) void l2norm_kernel(float* __restrict__ x, int dim) {
-    float* v = x + (size_t)blockIdx.x * dim;
+// y = x / ||x|| per row (y may be x); a zero row is copied unchanged.
+__global__ __launch_bounds__(64) void l2norm_kernel(const float* x, int dim, float* y) {
+    const float* v = x + (size_t)blockIdx.x * dim;
+    float* o = y + (size_t)blockIdx.x * dim;
     double s = 0.0;
     for (int i = threadIdx.x; i < dim; i += 64) s += (double)v[i] * (double)v[i];
     s = wave_sum_d(s);
     const double norm = sqrt(s);
-    if (norm > 0.0)
-        for (int i = threadIdx.x; i < dim; i += 64) v[i] = (float)((double)v[i] / norm);
+    for (int i = threadIdx.x; i < dim; i += 64) o[i] = norm > 0.0 ? (float)((double)v[i] / norm) : v[i];
 }
 
 }  // namespace
@@ -316,10 +317,17 @@ extern "C" int vdk_linear(const float* d_x, int batch, int in_dim, const float* 
 }
 
 extern "C" int vdk_l2norm(float* d_x, int batch, int dim, void* stream) {
+    return vdk_l2norm_to(d_x, batch, dim, d_x, stream);
+}
+
+extern "C" int vdk_l2norm_to(const float* d_x, int batch, int dim, float* d_y, void* stream) {
     return guarded([&] {
-        require(d_x, "l2norm: NULL device pointer");
+        require(d_x && d_y, "l2norm: NULL device pointer");
         require(batch > 0 && dim > 0, "l2norm: empty shape");
-        hipLaunchKernelGGL(l2norm_kernel, dim3(batch), dim3(64), 0, static_cast<hipStream_t>(stream), d_x, dim);
+        const uintptr_t xa = reinterpret_cast<uintptr_t>(d_x), ya = reinterpret_cast<uintptr_t>(d_y);
+        const size_t bytes = sizeof(float) * (size_t)batch * dim;
+        require(xa == ya || xa + bytes <= ya || ya + bytes <= xa, "l2norm: x and y overlap without being equal");
+        hipLaunchKernelGGL(l2norm_kernel, dim3(batch), dim3(64), 0, static_cast<hipStream_t>(stream), d_x, dim, d_y);
         VDK_HIP(hipGetLastError());
     });
 }

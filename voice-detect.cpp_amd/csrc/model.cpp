@@ -371,11 +371,12 @@ void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) 
     else if (cfg_.arch == "eres2net") encode_eres2net(batch, T);
     else encode_resnet(batch, T);
     const int E = cfg_.embedding_dim;
-    VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));
-    if (cfg_.l2_normalize) {
+    if (cfg_.l2_normalize) {   // normalised straight into the output (the pre-norm rows stay in ws_.pre)
         prof_begin("l2norm", 0.0, 8.0 * batch * E);
-        check(vdk_l2norm(d_out, batch, E, stream_));
+        check(vdk_l2norm_to(ws_.pre, batch, E, d_out, stream_));
         prof_end();
+    } else {
+        VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));
     }
 }
 

@@ -142,6 +142,7 @@ _SIGS = {
                                 _vp]),
     "vdk_linear_ex_noalloc": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_l2norm": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
+    "vdk_l2norm_to": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_feats_tmajor": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_reflect_pad_add": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_channel_mean": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
