@@ -195,12 +195,14 @@ def _bn(ws, prefix, c, tensors):
     tensors.append((prefix + ".running_var", G.GGML_F32, [c], (0.5 + uniform(ws.next(), c)).astype(np.float32)))
 
 
-def _f16_exact(a):
-    return np.asarray(a, dtype=np.float32).astype(np.float16).astype(np.float32)
+def _f16_exact(a, on=True):
+    """a rounded to f16-representable f32 values (on=False: a unchanged, f32)."""
+    a = np.asarray(a, dtype=np.float32)
+    return a.astype(np.float16).astype(np.float32) if on else a
 
 
 def make_ecapa(seed, channels=1024, mfa=1536, n_mels=80, scale=8, se_ch=128, att_ch=128, emb_dim=192,
-               n_res_blocks=3, k0=5, wtype=G.GGML_F16):
+               n_res_blocks=3, k0=5, wtype=G.GGML_F16, f16_exact=True):
     """Random-init SpeechBrain ECAPA-TDNN in the reference GGUF schema.
 
     Tensor names and torch shapes follow models/ecapa_tdnn_manifest.txt of the
@@ -216,7 +218,7 @@ def make_ecapa(seed, channels=1024, mfa=1536, n_mels=80, scale=8, se_ch=128, att
     T = []
 
     def conv(name, oc, ic, k, quantizable=False):
-        w = _f16_exact(normal(ws.next(), oc * ic * k).reshape(oc, ic, k) * np.sqrt(2.0 / (ic * k)))
+        w = _f16_exact(normal(ws.next(), oc * ic * k).reshape(oc, ic, k) * np.sqrt(2.0 / (ic * k)), f16_exact)
         b = (0.01 * normal(ws.next(), oc)).astype(np.float32)
         if quantizable and k == 1 and wtype != G.GGML_F32:
             T.append((name + ".weight", wtype, [oc, ic], w.reshape(oc, ic)))
@@ -275,7 +277,7 @@ def _q8_eligible(kh, kw, ic, oc):
     return kh == 1 and kw == 1 and ic % 32 == 0 and ic >= 32 and oc >= 32
 
 
-def _put_conv(T, wname, bname, w, b, wtype, conv1d):
+def _put_conv(T, wname, bname, w, b, wtype, conv1d, f16_exact=True):
     """Store a conv weight: q8_0/f16-eligible 1x1 Conv1d weights squeezed to a 2-D
     [OC, IC] matrix of `wtype`, everything else F32 ([OC,IC,K] for Conv1d,
     [OC,IC,KH,KW] for Conv2d) with f16-representable values."""
@@ -283,15 +285,15 @@ def _put_conv(T, wname, bname, w, b, wtype, conv1d):
     if conv1d and wtype != G.GGML_F32 and _q8_eligible(kh, kw, ic, oc):
         T.append((wname, wtype, [oc, ic], w.reshape(oc, ic)))
     elif conv1d:
-        T.append((wname, G.GGML_F32, [oc, ic, kw], _f16_exact(w.reshape(oc, ic, kw))))
+        T.append((wname, G.GGML_F32, [oc, ic, kw], _f16_exact(w.reshape(oc, ic, kw), f16_exact)))
     else:
-        T.append((wname, G.GGML_F32, [oc, ic, kh, kw], _f16_exact(w)))
+        T.append((wname, G.GGML_F32, [oc, ic, kh, kw], _f16_exact(w, f16_exact)))
     if bname:
         T.append((bname, G.GGML_F32, [oc], b.astype(np.float32)))
 
 
 def make_campplus(seed, n_mels=80, m_ch=32, init_ch=128, growth=32, bn_ch=128, emb_dim=192,
-                  layers=(12, 24, 16), wtype=G.GGML_Q8_0):
+                  layers=(12, 24, 16), wtype=G.GGML_Q8_0, f16_exact=True):
     """Random-init 3D-Speaker CAM++ in the reference GGUF schema
     (src/model_loader.hpp:82-99, scripts/convert_voicedetect_to_gguf.py
     parse_campplus_onnx): flat execution-order conv / BN manifests.
@@ -315,14 +317,14 @@ def make_campplus(seed, n_mels=80, m_ch=32, init_ch=128, growth=32, bn_ch=128, e
     def folded(oc, ic, kh, kw, conv1d):
         wn, bn = onnx_name()
         w, b = conv_bn_folded(ws, oc, ic, kh, kw)
-        _put_conv(T, wn, bn, w, b, wtype, conv1d)
+        _put_conv(T, wn, bn, w, b, wtype, conv1d, f16_exact)
         conv_w.append(wn)
         conv_b.append(bn)
 
     def plain(name, oc, ic, k, bias):
         w = (normal(ws.next(), oc * ic * k).reshape(oc, ic, 1, k) * np.sqrt(2.0 / (ic * k))).astype(np.float32)
         b = (0.01 * normal(ws.next(), oc)).astype(np.float32) if bias else None
-        _put_conv(T, name + ".weight", name + ".bias" if bias else "", w, b, wtype, True)
+        _put_conv(T, name + ".weight", name + ".bias" if bias else "", w, b, wtype, True, f16_exact)
         conv_w.append(name + ".weight")
         conv_b.append(name + ".bias" if bias else "")
 
@@ -391,7 +393,7 @@ def write_campplus(path, seed, **kw):
 # ---------------------------------------------------------------- ERes2Net
 
 def make_eres2net(seed, n_mels=80, m_ch=32, num_blocks=(3, 4, 6, 3), base_width=32, scale=2, emb_dim=512,
-                  wtype=G.GGML_Q8_0):
+                  wtype=G.GGML_Q8_0, f16_exact=True):
     """Random-init 3D-Speaker ERes2Net in the reference GGUF schema
     (src/model_loader.hpp:68-79, scripts/convert_voicedetect_to_gguf.py
     parse_eres2net_onnx): every conv BN-folded with an opaque `onnx::Conv_*`
@@ -411,7 +413,7 @@ def make_eres2net(seed, n_mels=80, m_ch=32, num_blocks=(3, 4, 6, 3), base_width=
         if k == 1 and wtype != G.GGML_F32 and _q8_eligible(1, 1, ic, oc):
             T.append((wn, wtype, [oc, ic], w.reshape(oc, ic)))
         else:
-            T.append((wn, G.GGML_F32, [oc, ic, k, k], _f16_exact(w)))
+            T.append((wn, G.GGML_F32, [oc, ic, k, k], _f16_exact(w, f16_exact)))
         if bias:
             T.append((bn, G.GGML_F32, [oc], b))
         conv_w.append(wn)
