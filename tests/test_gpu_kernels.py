@@ -216,11 +216,53 @@ def test_conv_register_weight_tiles_plain_epilogues(case):
     assert n >= 1
 
 
-@pytest.mark.parametrize("shape", [(2, 7, 75, 128, True), (3, 20, 75, 128, False), (1, 6, 40, 256, True)])
+@pytest.mark.parametrize("case", [
+    # (B, H, W, C, residual): enough tiles that each persistent workgroup
+    # walks several, with walk lengths of every remainder modulo the ring
+    # depths across the cases (13, 4, 5, 8 and 2 tiles per workgroup for the
+    # 4-row tiles on 256 CUs)
+    (64, 40, 149, 64, True), (16, 40, 149, 64, False), (24, 40, 149, 64, True), (36, 40, 149, 64, False),
+    (7, 40, 149, 64, True), (64, 80, 298, 32, True), (9, 80, 298, 32, False),
+])
+def test_conv_register_weight_rings_bitwise(case):
+    """The register-weight kernels (tiles 53-56: 2-stage ring with 2-, 4- and
+    6-row tiles; 66-69: 3- and 4-stage rings) return the same bits for every
+    tile height and ring depth, on maps where each workgroup walks several
+    tiles; the 4-row 2-stage kernel's last clip is checked against the
+    oracle."""
+    B, H, W, C, with_res = case
+    rng = np.random.default_rng(B * 7 + H + C)
+    x = np.maximum(rng.standard_normal((B, H, W, C)), 0).astype(np.float16)
+    w = (rng.standard_normal((C, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float16)
+    b = rng.uniform(-0.1, 0.1, C).astype(np.float32)
+    res = rng.standard_normal((B, H, W, C)).astype(np.float16) if with_res else None
+    ref_tile = 53 if C == 64 else 56
+    assert tile_fits(ref_tile, B, H, W, C, C, 3, 1, 1, residual=with_res)
+    want = conv_gpu(x, w, b, res, 1, 1, True, tile=ref_tile)
+    r0 = None if res is None else res[B - 1].astype(np.float32).transpose(2, 0, 1)
+    ref = O.conv2d(x[B - 1].astype(np.float32).transpose(2, 0, 1), w.astype(np.float32), 1, 1, bias=b,
+                   residual=r0, relu=True)
+    ok, ratio, rel = close_report(want[B - 1].astype(np.float32).transpose(2, 0, 1), ref, CONV_RTOL, CONV_ATOL_RMS)
+    assert ok and rel <= 2e-3, f"tile {ref_tile}: ratio {ratio:.3f} rel {rel:.2e}"
+    n = 0
+    for t in (53, 54, 55, 56, 66, 67, 68, 69):
+        if t == ref_tile or not tile_fits(t, B, H, W, C, C, 3, 1, 1, residual=with_res):
+            continue
+        announce(f"rw tile {t} case {case}")
+        got = conv_gpu(x, w, b, res, 1, 1, True, tile=t)
+        bad = np.flatnonzero(got.view(np.uint16) != want.view(np.uint16))
+        assert bad.size == 0, f"tile {t}: {bad.size} values differ from tile {ref_tile}, first at {bad[0]}"
+        n += 1
+    assert n >= 1
+
+
+@pytest.mark.parametrize("shape", [(2, 7, 75, 128, True), (3, 20, 75, 128, False), (1, 6, 40, 256, True),
+                                   (5, 40, 149, 64, True), (3, 21, 149, 64, False), (4, 80, 298, 32, True)])
 def test_conv_chunked_weights_bitwise(shape):
     """A conv given the chunk-major weight copy (vdk_conv_pack_chunked) as
     w_chunked returns the same bits as without it, on every tile that fits
-    (the band kernels stream it; the others ignore it)."""
+    (the band kernels stream it, the register-weight kernels load their
+    weight fragments from it; the others ignore it)."""
     L = lib.lib()
     B, H, W, C, with_res = shape
     rng = np.random.default_rng(B * 100 + H + W + C)

@@ -451,6 +451,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
 //    barrier per chunk.
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void;
+typedef int int4v __attribute__((ext_vector_type(4)));
 
 
 template <int KC>
@@ -850,9 +851,15 @@ struct PadRow {
 // the 9 * C/16 (tap, k-step) steps in order.  The B reads run PD steps ahead
 // of the MFMAs (a register ring), so with two waves per SIMD the MFMAs issue
 // back to back instead of each waiting out one LDS round trip.
-template <int C, int NR, int SW, int PD = 4>
+struct NoSide {
+    __device__ __forceinline__ void operator()(int) const {}
+};
+
+// side(s) runs after step s's MFMAs are issued: work spread over the steps
+// (e.g. DMA instructions) so it never stalls all waves at once.
+template <int C, int NR, int SW, int PD = 4, class Side = NoSide>
 __device__ __forceinline__ void conv_rows(const half8* wf, const uint8_t* src, int row0, int step, int lrow,
-                                          int lhalf, float16v* acc) {
+                                          int lhalf, float16v* acc, const Side& side = Side()) {
     constexpr int RB = PadRow<C>::RB, KS = C / 16, NS = 9 * KS, NQ = NR > 0 ? NR : 1;
     static_assert(PD >= 1 && PD < NS, "prefetch distance within the step count");
     if constexpr (NR == 0) return;
@@ -878,6 +885,7 @@ __device__ __forceinline__ void conv_rows(const half8* wf, const uint8_t* src, i
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int q = 0; q < NR; ++q) acc[q] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[s], cur[q], acc[q], 0, 0, 0);
+        side(s);
     }
 }
 
@@ -1032,16 +1040,24 @@ __global__ __launch_bounds__(NW * 64) void resblock3x3_kernel(const half_t* __re
     const int t_end = t_begin + per_wg < ntiles ? t_begin + per_wg : ntiles;
     if (t_begin >= t_end) return;   // the whole workgroup: no barrier is pending
 
-    // A fragments: lane l holds w[oc = l % 32][tap][8 (kk*2 + l/32) .. + 8)
-    half8 wf1[G::NF], wf2[G::NF];
+    // Both weight tensors go to LDS as whole kilobytes first (w1 to sx1, w2
+    // to st: free until the first tile prefetches into sx1 and writes its
+    // intermediate rows); read from global memory directly, each A fragment
+    // would be 32 pieces 9*C*2 bytes apart.
+    constexpr int WB = C * 9 * C * 2, W_INS = WB / 1024;
+    static_assert(WB % 1024 == 0 && WB <= G::X_BYTES && WB <= G::T_BYTES, "the weights fit sx1 and st");
+    {
+        const __amdgpu_buffer_rsrc_t wr1 = __builtin_amdgcn_make_buffer_rsrc((void*)w1, 0, WB, 0x00020000);
+        const __amdgpu_buffer_rsrc_t wr2 = __builtin_amdgcn_make_buffer_rsrc((void*)w2, 0, WB, 0x00020000);
 #pragma unroll
-    for (int tap = 0; tap < 9; ++tap)
-#pragma unroll
-        for (int kk = 0; kk < C / 16; ++kk) {
-            const size_t off = (size_t)(lrow * 9 + tap) * C + (kk * 2 + lhalf) * 8;
-            wf1[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(w1 + off);
-            wf2[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(w2 + off);
+        for (int i = 0; i < (2 * W_INS + NW - 1) / NW; ++i) {
+            const int ins = wave + i * NW;
+            if (ins >= 2 * W_INS) break;
+            const int which = ins >= W_INS, wi = ins - which * W_INS;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(which ? wr2 : wr1, (lds_void*)((which ? st : sx1) + wi * 1024),
+                                                     16, wi * 1024 + lane * 16, 0, 0, 0);
         }
+    }
     if (tid < 2 * C) sbias[tid] = tid < C ? b1[tid] : b2[tid - C];
     // this lane's halo DMA slots (the same for every tile)
     int hofs[G::X_IPW], hpos[G::X_IPW];
@@ -1079,7 +1095,18 @@ __global__ __launch_bounds__(NW * 64) void resblock3x3_kernel(const half_t* __re
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx0 + ins * 1024), 16, off, 0, 0, 0);
         }
     }
-    __builtin_amdgcn_s_waitcnt(0);   // weights in VGPRs and this wave's share of the first halo
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's share of the weights and of the first halo
+    lds_barrier();                   // ... and every other wave's
+    // A fragments: lane l holds w[oc = l % 32][tap][8 (kk*2 + l/32) .. + 8)
+    half8 wf1[G::NF], wf2[G::NF];
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+        for (int kk = 0; kk < C / 16; ++kk) {
+            const int off = ((lrow * 9 + tap) * C + (kk * 2 + lhalf) * 8) * 2;
+            wf1[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(sx1 + off);
+            wf2[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(st + off);
+        }
 #pragma unroll 1
     for (int t = t_begin; t < t_end; t += 2) {
         // Two tiles per trip so each buffer has a fixed role: tile t reads
@@ -1130,16 +1157,24 @@ void launch_resblock(const half_t* x, const half_t* w1, const float* b1, const h
 // y = act(conv(x) + bias [+ residual]) (act: none or ReLU), dense f16 NHWC.
 // The machinery of the fused block: the OC/32 MFMA row blocks are split over
 // wave groups and every wave keeps the A fragments of its 32 output channels
-// (9 * IC/16 fragments, 144 VGPRs at IC = 64) in registers for the whole
-// launch; each workgroup walks a contiguous range of TH x 32 output tiles
-// (rows fastest), DMAing the next tile's (TH+2) x 34 input halo and its
-// residual tile into LDS (80/144-byte padded rows) while the current tile
-// computes; the B reads run a few MFMAs ahead; the epilogue stages each
-// 32 x 32 block per wave for 16-byte stores.  Products and sums are the
-// other conv kernels' (f16 x f16, f32 accumulation in tap-major,
-// channel-minor order, then + bias, + residual, act).
+// (9 * IC/16 fragments, 144 VGPRs at IC = 64) and their biases in registers
+// for the whole launch; each workgroup walks a contiguous range of TH x 32
+// output tiles (rows fastest) through an NS-stage LDS ring: a stage holds
+// one tile's (TH+2) x 34 input halo and its residual tile (80/144-byte
+// padded rows), and tile t+NS-1 is DMA'd while tile t computes, so NS-1
+// tiles' loads are in flight per workgroup (one tile's load takes longer
+// than its convolution).  The B reads run a few MFMAs ahead; results leave
+// straight from the accumulators as 8-byte stores (4 channels of one pixel
+// per lane, the two lane halves filling 16 contiguous bytes).  Products and
+// sums are the other conv kernels' (f16 x f16, f32 accumulation in
+// tap-major, channel-minor order, then + bias, + residual, act).
+//
+// The ring's DMA goes through rw_dma (inline assembly): the compiler does not
+// see it as a write to LDS, so it never makes the convolution's LDS reads
+// wait for the loads in flight into the other stages; the kernel orders them
+// itself with explicit vmcnt waits and the per-tile barrier.
 // ---------------------------------------------------------------------------
-template <int IC, int OC, int TH, int NW>
+template <int IC, int OC, int TH, int NW, int NS>
 struct RwTile {
     static constexpr int RBX = PadRow<IC>::RB, SPRX = PadRow<IC>::SPR;   // halo rows
     static constexpr int RBR = PadRow<OC>::RB, SPRR = PadRow<OC>::SPR;   // residual rows
@@ -1149,45 +1184,103 @@ struct RwTile {
     static constexpr int NWM = OC / 32, WPM = NW / NWM;                 // wave groups, waves per group
     static constexpr int F = TH / WPM, R = TH % WPM, NB = F + (R ? 1 : 0);
     static constexpr int NF = 9 * IC / 16;
-    static constexpr int S_BYTES = 32 * 64;                             // staging block per wave (swizzled)
+    static constexpr int X_BYTES = X_INS * 1024, STAGE = X_BYTES + R_INS * 1024;
+    static_assert(NS >= 2, "the tile being computed and at least the next one");
+    static_assert(NS * STAGE <= 163840, "the ring fits the 160 KB of LDS");
 };
 
-template <int IC, int OC, int TH, int NW>
-__device__ __forceinline__ void rw_tile(const uint8_t* __restrict__ sx, uint8_t* __restrict__ sxn,
-                                        const uint8_t* __restrict__ sr, uint8_t* __restrict__ srn,
-                                        uint8_t* __restrict__ sstage, const float* __restrict__ sbias,
-                                        const half8* wf, const int* hofs, const int* hpos, const int* rofs,
-                                        const int* rpos, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t rr,
-                                        bool prefetch, bool has_res, int nb, int noh0, int now0, int b, int oh0,
-                                        int ow0, const ConvArgs& a, int wave, int lane) {
-    using G = RwTile<IC, OC, TH, NW>;
-    const int H = a.H, W = a.W;
-    const int lrow = lane & 31, lhalf = lane >> 5;
-    const int mg = wave / G::WPM, wr = wave - mg * G::WPM;   // wave group (32 output channels), row slot
-    if (prefetch) {
-        const int xo = ((nb * H + noh0 - 1) * W + now0 - 1) * IC * 2;
-#pragma unroll
-        for (int i = 0; i < G::X_IPW; ++i) {
+// Buffer resource words of [base, base + bytes) for rw_dma (raw buffer,
+// offsets at or past `bytes` read as zero).
+__device__ __forceinline__ int4v rw_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    return int4v{(int)(uint32_t)p, (int)(uint32_t)(p >> 32), (int)bytes, 0x00020000};
+}
+
+// One 16-byte-per-lane DMA from the buffer at byte offset voff to LDS
+// lds_dst + 16 * lane (lds_dst is wave-uniform).
+__device__ __forceinline__ void rw_dma(uint8_t* lds_dst, int4v rsrc, uint32_t voff) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_dst);
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(m0v) : "memory");
+}
+
+// Per-workgroup constants of the register-weight kernel's tile walk.
+struct RwWalk {
+    const int* hofs; const int* hpos; const int* rofs; const int* rpos;
+    int4v xr, rr;
+    int tiles_w, tiles_h, t_end, per_tile, H, W;
+};
+
+// This wave's DMA instructions for tile t's input halo and (RES) residual
+// into stage st, issued one at a time from the convolution of the tile
+// before it: instruction j after step j * SP, so the issue stalls of the
+// memory pipeline (every wave has a tile's worth to issue) fall between
+// MFMAs instead of holding all waves at the top of the tile.
+template <int IC, int OC, int TH, int NW, int NS, bool RES>
+struct RwSide {
+    using G = RwTile<IC, OC, TH, NW, NS>;
+    static constexpr int NI = G::X_IPW + (RES ? G::R_IPW : 0), STEPS = 9 * IC / 16;
+    static constexpr int SP = STEPS / NI > 0 ? STEPS / NI : 1;
+    static_assert(NI * SP <= STEPS, "every instruction has a step");
+    uint8_t* st;
+    const RwWalk* k;
+    int oh0, ow0, xo, ro, wave;
+    bool on;
+    __device__ __forceinline__ RwSide(uint8_t* st_, const RwWalk& k_, int t, int wave_, bool on_)
+        : st(st_), k(&k_), wave(wave_), on(on_) {
+        const int th = t % k_.tiles_h, r = t / k_.tiles_h, tw = r % k_.tiles_w;
+        const int b = r / k_.tiles_w;
+        oh0 = th * TH;
+        ow0 = tw * 32;
+        xo = ((b * k_.H + oh0 - 1) * k_.W + ow0 - 1) * IC * 2;
+        ro = ((b * k_.H + oh0) * k_.W + ow0) * OC * 2;
+    }
+    __device__ __forceinline__ void operator()(int s) const {
+        if (s % SP != 0 || !on) return;
+        const int j = s / SP;
+        if (j < G::X_IPW) {
+            const int ins = wave + j * NW;
+            if (ins >= G::X_INS) return;
+            const int ih = oh0 - 1 + (k->hpos[j] >> 8), iw = ow0 - 1 + (k->hpos[j] & 255);
+            const uint32_t off = ((unsigned)ih < (unsigned)k->H && (unsigned)iw < (unsigned)k->W)
+                                     ? (uint32_t)(xo + k->hofs[j]) : kOOB;
+            rw_dma(st + ins * 1024, k->xr, off);
+        } else if constexpr (RES) {
+            const int i = j - G::X_IPW;
+            if (i >= G::R_IPW) return;
             const int ins = wave + i * NW;
-            if (ins >= G::X_INS) break;
-            const int ih = noh0 - 1 + (hpos[i] >> 8), iw = now0 - 1 + (hpos[i] & 255);
-            const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) ? (uint32_t)(xo + hofs[i])
-                                                                                            : kOOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sxn + ins * 1024), 16, off, 0, 0, 0);
-        }
-        if (has_res) {
-            const int ro = ((nb * H + noh0) * W + now0) * OC * 2;
-#pragma unroll
-            for (int i = 0; i < G::R_IPW; ++i) {
-                const int ins = wave + i * NW;
-                if (ins >= G::R_INS) break;
-                const int ih = noh0 + (rpos[i] >> 8), iw = now0 + (rpos[i] & 255);
-                const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
-                                         ? (uint32_t)(ro + rofs[i]) : kOOB;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void*)(srn + ins * 1024), 16, off, 0, 0, 0);
-            }
+            if (ins >= G::R_INS) return;
+            const int ih = oh0 + (k->rpos[i] >> 8), iw = ow0 + (k->rpos[i] & 255);
+            const uint32_t off = ((unsigned)ih < (unsigned)k->H && (unsigned)iw < (unsigned)k->W)
+                                     ? (uint32_t)(ro + k->rofs[i]) : kOOB;
+            rw_dma(st + G::X_BYTES + ins * 1024, k->rr, off);
         }
     }
+};
+
+// All of this wave's DMA instructions for tile t into stage st at once.
+template <int IC, int OC, int TH, int NW, int NS, bool RES>
+__device__ __forceinline__ void rw_issue(uint8_t* st, const RwWalk& k, int t, int wave) {
+    const RwSide<IC, OC, TH, NW, NS, RES> side(st, k, t, wave, true);
+#pragma unroll
+    for (int j = 0; j < RwSide<IC, OC, TH, NW, NS, RES>::NI; ++j) side(j * RwSide<IC, OC, TH, NW, NS, RES>::SP);
+}
+
+// Tile t from stage st while tile t+NS-1's DMA goes out into stage nst
+// (prefetch: it is in the walk): conv, then wait until at most `younger` of
+// this wave's DMA instructions are in flight (those of the tiles after t+1:
+// loads complete in issue order, so tile t+1's have landed; this tile's
+// stores stay out of the wait), then the epilogue.
+template <int IC, int OC, int TH, int NW, int NS, bool RES>
+__device__ __forceinline__ void rw_tile(const uint8_t* st, uint8_t* nst, bool prefetch, const half8* wf,
+                                        const float* bv, const RwWalk& k, int t, int younger, const ConvArgs& a,
+                                        int wave, int lane) {
+    using G = RwTile<IC, OC, TH, NW, NS>;
+    const int H = k.H, W = k.W;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int mg = wave / G::WPM, wr = wave - mg * G::WPM;   // wave group (32 output channels), row slot
+    const int th = t % k.tiles_h, r = t / k.tiles_h, tw = r % k.tiles_w;
+    const int b = r / k.tiles_w, oh0 = th * TH, ow0 = tw * 32;
+    const RwSide<IC, OC, TH, NW, NS, RES> side(nst, k, t + NS - 1, wave, prefetch);
 
     // output row i (columns ow0 .. ow0 + 31) is one MFMA column block; its B
     // operand for tap (kh, kw) is 32 consecutive halo pixels of halo row
@@ -1196,81 +1289,61 @@ __device__ __forceinline__ void rw_tile(const uint8_t* __restrict__ sx, uint8_t*
 #pragma unroll
     for (int q = 0; q < G::NB; ++q)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[q][r] = 0.0f;
-    conv_rows<IC, G::F, G::XW>(wf, sx, wr, G::WPM, lrow, lhalf, acc);
-    if (G::R && wr < G::R) conv_rows<IC, 1, G::XW>(wf, sx, wr + G::F * G::WPM, G::WPM, lrow, lhalf, acc + G::F);
-    // this wave's share of the next halo / residual must land before the
-    // next barrier; waiting here keeps this tile's stores out of the wait
-    __builtin_amdgcn_s_waitcnt(0);
+        for (int e = 0; e < 16; ++e) acc[q][e] = 0.0f;
+    if constexpr (G::F > 0) {
+        conv_rows<IC, G::F, G::XW>(wf, st, wr, G::WPM, lrow, lhalf, acc, side);
+    } else {
+        // fewer rows than waves per group: not every wave runs a conv, so
+        // the DMA goes out up front
+#pragma unroll
+        for (int j = 0; j < side.NI; ++j) side(j * side.SP);
+    }
+    if (G::R && wr < G::R) conv_rows<IC, 1, G::XW>(wf, st, wr + G::F * G::WPM, G::WPM, lrow, lhalf, acc + G::F);
+    wait_vmcnt_le(younger);
 
-    // act(acc + bias [+ residual]) in the MFMA layout: register g*4+e of a
-    // lane is channel 8g + 4*lhalf + e of its block, pixel column lrow
-    const int oc0 = mg * 32;
+    // act(acc + bias [+ residual]) straight from the accumulators: register
+    // g*4+e of a lane is channel oc0 + 8g + 4*lhalf + e of pixel column lrow
+    const int oc0 = mg * 32, ow = ow0 + lrow;
+    half_t* const y = static_cast<half_t*>(a.y);
+    const bool relu = a.act == VDK_ACT_RELU;
 #pragma unroll
     for (int q = 0; q < G::NB; ++q) {
-        const int i = wr + q * G::WPM;
-        if (i >= TH) continue;
-        const uint8_t* const rrow = sr + (i * 32 + lrow) * G::RBR + oc0 * 2 + lhalf * 8;
+        const int i = wr + q * G::WPM, oh = oh0 + i;
+        if (i >= TH || oh >= H || ow >= W) continue;
+        const uint8_t* const rrow = st + G::X_BYTES + (i * 32 + lrow) * G::RBR + oc0 * 2 + lhalf * 8;
+        half_t* const yp = y + ((size_t)(b * H + oh) * W + ow) * OC + oc0 + lhalf * 4;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const float4v bb = *reinterpret_cast<const float4v*>(sbias + oc0 + g * 8 + lhalf * 4);
             float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = acc[q][g * 4 + e] + bb[e];
-            if (has_res) {
-                const half4 r = *reinterpret_cast<const half4*>(rrow + g * 16);
+            for (int e = 0; e < 4; ++e) v[e] = acc[q][g * 4 + e] + bv[g * 4 + e];
+            if constexpr (RES) {
+                const half4 rv = *reinterpret_cast<const half4*>(rrow + g * 16);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] += (float)r[e];
+                for (int e = 0; e < 4; ++e) v[e] += (float)rv[e];
             }
             half4 h;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) h[e] = (half_t)(a.act == VDK_ACT_RELU ? fmaxf(v[e], 0.0f) : v[e]);
-            *reinterpret_cast<half4*>(sstage + lrow * 64 + swz<32>(lrow, g) * 16 + lhalf * 8) = h;
-        }
-        const int oh = oh0 + i;
-#pragma unroll
-        for (int hp = 0; hp < 2; ++hp) {
-            const int pix = hp * 16 + (lane >> 2), ch = lane & 3;
-            const half8 v = *reinterpret_cast<const half8*>(sstage + pix * 64 + swz<32>(pix, ch) * 16);
-            const int ow = ow0 + pix;
-            if (oh < H && ow < W)
-                *reinterpret_cast<half8*>(static_cast<half_t*>(a.y) + ((size_t)(b * H + oh) * W + ow) * OC + oc0 +
-                                          ch * 8) = v;
+            for (int e = 0; e < 4; ++e) h[e] = (half_t)(relu ? fmaxf(v[e], 0.0f) : v[e]);
+            *reinterpret_cast<half4*>(yp + g * 8) = h;
         }
     }
 }
 
-template <int IC, int OC, int TH, int NW>
+template <int IC, int OC, int TH, int NW, int NS, bool RES>
 __global__ __launch_bounds__(NW * 64) void conv3x3_rw_kernel(ConvArgs a, int ntiles, int per_wg) {
-    using G = RwTile<IC, OC, TH, NW>;
+    using G = RwTile<IC, OC, TH, NW, NS>;
     static_assert(G::NWM * G::WPM == NW && G::WPM >= 1, "wave groups split the workgroup evenly");
-    __shared__ __attribute__((aligned(1024))) uint8_t sx0[G::X_INS * 1024];
-    __shared__ __attribute__((aligned(1024))) uint8_t sx1[G::X_INS * 1024];
-    __shared__ __attribute__((aligned(1024))) uint8_t sr0[G::R_INS * 1024];
-    __shared__ __attribute__((aligned(1024))) uint8_t sr1[G::R_INS * 1024];
-    __shared__ __attribute__((aligned(16))) uint8_t sstage[NW * G::S_BYTES];
-    __shared__ float sbias[OC];
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * G::STAGE];
 
-    const int H = a.H, W = a.W;
+    const int W = a.W;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lrow = lane & 31, lhalf = lane >> 5;
-    const int tiles_w = (W + 31) / 32, tiles_h = (H + TH - 1) / TH;
     const int t_begin = blockIdx.x * per_wg;
     const int t_end = t_begin + per_wg < ntiles ? t_begin + per_wg : ntiles;
     if (t_begin >= t_end) return;   // the whole workgroup: no barrier is pending
-    const bool has_res = a.res != nullptr;
 
-    // A fragments of this wave's 32 output channels
-    const int oc = (wave / G::WPM) * 32 + lrow;
-    half8 wf[G::NF];
-#pragma unroll
-    for (int tap = 0; tap < 9; ++tap)
-#pragma unroll
-        for (int kk = 0; kk < IC / 16; ++kk)
-            wf[tap * (IC / 16) + kk] =
-                *reinterpret_cast<const half8*>(a.w + (size_t)(oc * 9 + tap) * IC + (kk * 2 + lhalf) * 8);
-    if (tid < OC) sbias[tid] = a.bias ? a.bias[tid] : 0.0f;
     // this lane's DMA slots (the same for every tile): byte offset from the
     // tile origin and (row << 8 | column), row 255 for padding slots
     int hofs[G::X_IPW], hpos[G::X_IPW], rofs[G::R_IPW], rpos[G::R_IPW];
@@ -1290,73 +1363,83 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_rw_kernel(ConvArgs a, int nti
         rofs[i] = (pr * W + pc) * OC * 2 + cc * 16;
         rpos[i] = (r < G::RPIX && cc < OC / 8) ? (pr << 8 | pc) : (255 << 8);
     }
-    const __amdgpu_buffer_rsrc_t xr =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, a.npix_in * IC * 2, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rr =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(has_res ? a.res : a.x), 0, has_res ? a.npix * OC * 2 : 0,
-                                          0x00020000);
-    auto coords = [&](int t, int& b, int& oh0, int& ow0) {
-        const int th = t % tiles_h, r = t / tiles_h;
-        const int tw = r % tiles_w;
-        b = r / tiles_w;
-        oh0 = th * TH;
-        ow0 = tw * 32;
-    };
+    RwWalk k;
+    k.hofs = hofs; k.hpos = hpos; k.rofs = rofs; k.rpos = rpos;
+    k.xr = rw_rsrc(a.x, (uint32_t)a.npix_in * IC * 2);
+    k.rr = rw_rsrc(RES ? (const void*)a.res : (const void*)a.x, RES ? (uint32_t)a.npix * OC * 2 : 0u);
+    k.H = a.H;
+    k.W = W;
+    k.tiles_w = (W + 31) / 32;
+    k.tiles_h = (a.H + TH - 1) / TH;
+    k.t_end = t_end;
+    // this wave's DMA instructions per tile
+    k.per_tile = (G::X_INS - wave + NW - 1) / NW + (RES ? (G::R_INS - wave + NW - 1) / NW : 0);
 
-    int b, oh0, ow0;
-    coords(t_begin, b, oh0, ow0);
-    // the first tile's halo and residual: a tile body with nothing to compute
-    // is not worth a second code path, so issue them here directly
-    {
-        const int xo = ((b * H + oh0 - 1) * W + ow0 - 1) * IC * 2;
+    // the first tile's DMA goes out ahead of the weight loads, which it
+    // overlaps
+    rw_issue<IC, OC, TH, NW, NS, RES>(ring, k, t_begin, wave);
+    // A fragments and biases of this wave's 32 output channels; from the
+    // chunk-major weight copy ([IC/16][9][OC][16]) a fragment is one
+    // contiguous kilobyte, from the plain layout 32 pieces 9*IC*2 bytes apart
+    const int oc0 = (wave / G::WPM) * 32;
+    half8 wf[G::NF];
+    if (a.wc) {
 #pragma unroll
-        for (int i = 0; i < G::X_IPW; ++i) {
-            const int ins = wave + i * NW;
-            if (ins >= G::X_INS) break;
-            const int ih = oh0 - 1 + (hpos[i] >> 8), iw = ow0 - 1 + (hpos[i] & 255);
-            const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W) ? (uint32_t)(xo + hofs[i])
-                                                                                            : kOOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx0 + ins * 1024), 16, off, 0, 0, 0);
-        }
-        if (has_res) {
-            const int ro = ((b * H + oh0) * W + ow0) * OC * 2;
+        for (int tap = 0; tap < 9; ++tap)
 #pragma unroll
-            for (int i = 0; i < G::R_IPW; ++i) {
-                const int ins = wave + i * NW;
-                if (ins >= G::R_INS) break;
-                const int ih = oh0 + (rpos[i] >> 8), iw = ow0 + (rpos[i] & 255);
-                const uint32_t off = ((unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W)
-                                         ? (uint32_t)(ro + rofs[i]) : kOOB;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rr, (lds_void*)(sr0 + ins * 1024), 16, off, 0, 0, 0);
-            }
-        }
+            for (int kk = 0; kk < IC / 16; ++kk)
+                wf[tap * (IC / 16) + kk] = *reinterpret_cast<const half8*>(
+                    a.wc + ((size_t)(kk * 9 + tap) * OC + oc0 + lrow) * 16 + lhalf * 8);
+    } else {
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+            for (int kk = 0; kk < IC / 16; ++kk)
+                wf[tap * (IC / 16) + kk] = *reinterpret_cast<const half8*>(
+                    a.w + (size_t)((oc0 + lrow) * 9 + tap) * IC + (kk * 2 + lhalf) * 8);
     }
-    __builtin_amdgcn_s_waitcnt(0);   // weights in VGPRs and this wave's share of the first tile
+    float bv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4v v = a.bias ? *reinterpret_cast<const float4v*>(a.bias + oc0 + g * 8 + lhalf * 4)
+                                 : float4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[g * 4 + e] = v[e];
+    }
+    // a full wait the compiler sees, so the weights count as loaded inside
+    // the loop; the tiles after the first go out behind it
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int s = 1; s + 1 < NS; ++s)
+        if (t_begin + s < t_end) rw_issue<IC, OC, TH, NW, NS, RES>(ring + s * G::STAGE, k, t_begin + s, wave);
+    int slot = 0;
 #pragma unroll 1
-    for (int t = t_begin; t < t_end; t += 2) {
-        // two tiles per trip so each buffer pair has a fixed role
-        int nb, noh0, now0;
+    for (int t = t_begin; t < t_end; ++t) {
+        // every wave's share of tile t has landed (each waited for its own
+        // DMA before the barrier) and tile t-1 is done with its stage, which
+        // tile t+NS-1 takes over (its DMA goes out during tile t's conv)
         lds_barrier();
-        coords(t + 1 < t_end ? t + 1 : t, nb, noh0, now0);
-        rw_tile<IC, OC, TH, NW>(sx0, sx1, sr0, sr1, sstage + wave * G::S_BYTES, sbias, wf, hofs, hpos, rofs, rpos,
-                                xr, rr, t + 1 < t_end, has_res, nb, noh0, now0, b, oh0, ow0, a, wave, lane);
-        if (t + 1 >= t_end) break;
-        b = nb; oh0 = noh0; ow0 = now0;
-        lds_barrier();
-        coords(t + 2 < t_end ? t + 2 : t + 1, nb, noh0, now0);
-        rw_tile<IC, OC, TH, NW>(sx1, sx0, sr1, sr0, sstage + wave * G::S_BYTES, sbias, wf, hofs, hpos, rofs, rpos,
-                                xr, rr, t + 2 < t_end, has_res, nb, noh0, now0, b, oh0, ow0, a, wave, lane);
-        b = nb; oh0 = noh0; ow0 = now0;
+        const int prev = slot == 0 ? NS - 1 : slot - 1;
+        // DMA instructions issued after tile t+1's: those of tiles t+2 .. t+NS-1
+        const int last = t + NS - 1 < t_end - 1 ? t + NS - 1 : t_end - 1;
+        const int younger = last > t + 1 ? (last - t - 1) * k.per_tile : 0;
+        rw_tile<IC, OC, TH, NW, NS, RES>(ring + slot * G::STAGE, ring + prev * G::STAGE, t + NS - 1 < t_end, wf, bv,
+                                         k, t, younger, a, wave, lane);
+        slot = slot + 1 == NS ? 0 : slot + 1;
     }
 }
 
-template <int IC, int OC, int TH, int NW>
+template <int IC, int OC, int TH, int NW, int NS>
 void launch_rw(const ConvArgs& a, hipStream_t s) {
     const int B = a.npix / (a.Ho * a.Wo);
     const int ntiles = B * cdiv(a.Ho, TH) * cdiv(a.Wo, 32);
     const int per = cdiv(ntiles, device_cu_count());
-    hipLaunchKernelGGL((conv3x3_rw_kernel<IC, OC, TH, NW>), dim3(cdiv(ntiles, per)), dim3(NW * 64), 0, s, a, ntiles,
-                       per);
+    if (a.res)
+        hipLaunchKernelGGL((conv3x3_rw_kernel<IC, OC, TH, NW, NS, true>), dim3(cdiv(ntiles, per)), dim3(NW * 64), 0, s,
+                           a, ntiles, per);
+    else
+        hipLaunchKernelGGL((conv3x3_rw_kernel<IC, OC, TH, NW, NS, false>), dim3(cdiv(ntiles, per)), dim3(NW * 64), 0,
+                           s, a, ntiles, per);
 }
 
 // ---------------------------------------------------------------------------
@@ -1941,7 +2024,7 @@ struct TileCfg {
 // persistent 3x3 kernel, 57-59 the band kernel for wide 3x3 layers, 60-61
 // narrow LDS-DMA tiles, 62-63 narrow register-staged tiles, 64-65 the band
 // kernel with producer / compute waves (128-channel groups, maps up to 75 /
-// 38 wide).
+// 38 wide), 66-69 the register-weight kernel with 3- and 4-stage rings.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -1999,10 +2082,10 @@ const TileCfg kTiles[] = {
     {256, 64, 32, launch_dma<256, 64, 64, 64, 32, 2>},    // 50
     {256, 64, 64, launch_dma<256, 64, 64, 64, 64, 2>},    // 51
     {128, 32, 64, launch_dma<128, 32, 32, 32, 64, 2>},    // 52
-    {64, 128, 64, launch_rw<64, 64, 4, 8>, true, 64},     // 53: register-weight persistent 3x3
-    {64, 192, 64, launch_rw<64, 64, 6, 8>, true, 64},     // 54
-    {64, 64, 64, launch_rw<64, 64, 2, 8>, true, 64},      // 55
-    {32, 128, 32, launch_rw<32, 32, 4, 8>, true, 32},     // 56
+    {64, 128, 64, launch_rw<64, 64, 4, 8, 2>, true, 64},  // 53: register-weight persistent 3x3
+    {64, 192, 64, launch_rw<64, 64, 6, 8, 2>, true, 64},  // 54
+    {64, 64, 64, launch_rw<64, 64, 2, 8, 2>, true, 64},   // 55
+    {32, 128, 32, launch_rw<32, 32, 4, 8, 2>, true, 32},  // 56
     {128, 384, 16, launch_band<5, 6>, true, 0, BandTile<5, 6>::MAXW},   // 57: band kernels
     {128, 192, 16, launch_band<5, 3>, true, 0, BandTile<5, 3>::MAXW},   // 58
     {128, 320, 16, launch_band<4, 5>, true, 0, BandTile<4, 5>::MAXW},   // 59
@@ -2012,6 +2095,10 @@ const TileCfg kTiles[] = {
     {64, 64, 32, launch_igemm<64, 64, 32, 32, 32>},       // 63
     {128, 384, 16, launch_bandws<5, 75, 2, 4, 3, 4>, true, 0, 75},   // 64: producer / compute band kernels
     {128, 192, 16, launch_bandws<5, 38, 2, 2, 3, 4>, true, 0, 38},   // 65
+    {64, 128, 64, launch_rw<64, 64, 4, 8, 3>, true, 64},  // 66: register-weight kernel, deeper rings
+    {64, 64, 64, launch_rw<64, 64, 2, 8, 4>, true, 64},   // 67
+    {32, 128, 32, launch_rw<32, 32, 4, 8, 4>, true, 32},  // 68
+    {32, 256, 32, launch_rw<32, 32, 8, 8, 3>, true, 32},  // 69
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -2125,7 +2212,7 @@ int pick_tile(const ConvArgs& a) {
         if (a.IC == 128 && a.OC == 256) return 39;
         if (a.IC == 256 && a.OC == 512) return 51;
     }
-    if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 53;
+    if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 66;   // 3-stage ring
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[64], a)) return 64;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
     if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[65], a)) return 65;

@@ -214,7 +214,9 @@ void Model::upload_resnet() {
                     }
         c.ic = ic; c.oc = oc; c.k = k; c.stride = stride; c.pad = pad;
         arena.put(packed, &c.w);
-        if (k == 3 && stride == 1 && oc % 128 == 0) {   // the band kernels stream whole-line weight chunks
+        // the band kernels stream whole-line weight chunks; the register-weight
+        // kernels load their A fragments from it as whole kilobytes
+        if (k == 3 && stride == 1 && ic % 16 == 0 && (oc % 128 == 0 || oc == 32 || oc == 64)) {
             std::vector<uint16_t> chunked(packed.size());
             vdk_conv_pack_chunked(packed.data(), oc, k, k, ic, chunked.data());
             arena.put(chunked, &c.wc);
