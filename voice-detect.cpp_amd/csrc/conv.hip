@@ -1040,24 +1040,16 @@ __global__ __launch_bounds__(NW * 64) void resblock3x3_kernel(const half_t* __re
     const int t_end = t_begin + per_wg < ntiles ? t_begin + per_wg : ntiles;
     if (t_begin >= t_end) return;   // the whole workgroup: no barrier is pending
 
-    // Both weight tensors go to LDS as whole kilobytes first (w1 to sx1, w2
-    // to st: free until the first tile prefetches into sx1 and writes its
-    // intermediate rows); read from global memory directly, each A fragment
-    // would be 32 pieces 9*C*2 bytes apart.
-    constexpr int WB = C * 9 * C * 2, W_INS = WB / 1024;
-    static_assert(WB % 1024 == 0 && WB <= G::X_BYTES && WB <= G::T_BYTES, "the weights fit sx1 and st");
-    {
-        const __amdgpu_buffer_rsrc_t wr1 = __builtin_amdgcn_make_buffer_rsrc((void*)w1, 0, WB, 0x00020000);
-        const __amdgpu_buffer_rsrc_t wr2 = __builtin_amdgcn_make_buffer_rsrc((void*)w2, 0, WB, 0x00020000);
+    // A fragments: lane l holds w[oc = l % 32][tap][8 (kk*2 + l/32) .. + 8)
+    half8 wf1[G::NF], wf2[G::NF];
 #pragma unroll
-        for (int i = 0; i < (2 * W_INS + NW - 1) / NW; ++i) {
-            const int ins = wave + i * NW;
-            if (ins >= 2 * W_INS) break;
-            const int which = ins >= W_INS, wi = ins - which * W_INS;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(which ? wr2 : wr1, (lds_void*)((which ? st : sx1) + wi * 1024),
-                                                     16, wi * 1024 + lane * 16, 0, 0, 0);
+    for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+        for (int kk = 0; kk < C / 16; ++kk) {
+            const size_t off = (size_t)(lrow * 9 + tap) * C + (kk * 2 + lhalf) * 8;
+            wf1[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(w1 + off);
+            wf2[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(w2 + off);
         }
-    }
     if (tid < 2 * C) sbias[tid] = tid < C ? b1[tid] : b2[tid - C];
     // this lane's halo DMA slots (the same for every tile)
     int hofs[G::X_IPW], hpos[G::X_IPW];
@@ -1095,18 +1087,7 @@ __global__ __launch_bounds__(NW * 64) void resblock3x3_kernel(const half_t* __re
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(sx0 + ins * 1024), 16, off, 0, 0, 0);
         }
     }
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's share of the weights and of the first halo
-    lds_barrier();                   // ... and every other wave's
-    // A fragments: lane l holds w[oc = l % 32][tap][8 (kk*2 + l/32) .. + 8)
-    half8 wf1[G::NF], wf2[G::NF];
-#pragma unroll
-    for (int tap = 0; tap < 9; ++tap)
-#pragma unroll
-        for (int kk = 0; kk < C / 16; ++kk) {
-            const int off = ((lrow * 9 + tap) * C + (kk * 2 + lhalf) * 8) * 2;
-            wf1[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(sx1 + off);
-            wf2[tap * (C / 16) + kk] = *reinterpret_cast<const half8*>(st + off);
-        }
+    __builtin_amdgcn_s_waitcnt(0);   // weights in VGPRs and this wave's share of the first halo
 #pragma unroll 1
     for (int t = t_begin; t < t_end; t += 2) {
         // Two tiles per trip so each buffer has a fixed role: tile t reads
