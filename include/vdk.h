@@ -268,6 +268,17 @@ int vdk_asp_stats(const void* d_x, int x_stride, int batch, int T, int C, float 
  * out [B][2C] = [sum a x ; sqrt(max(sum a (x-mu)^2, eps))] (src/encoder.cpp:282-294). */
 int vdk_asp_pool(const float* d_logits, int l_stride, const void* d_x, int x_stride, int batch, int T,
                  int C, float eps, float* d_out, void* stream);
+/* The asp.conv logits and the pooling of vdk_asp_pool in one launch
+ * (src/encoder.cpp:283-294): l[b][t][c] = b_c[c] + sum_k w[c][k] a1[b][t][k]
+ * (f16 products, f32 sums, the conv kernels' order), softmax over time per
+ * channel, out [B][2C] = [sum a x ; sqrt(max(sum a (x-mu)^2, eps))]; the
+ * logits never reach memory.  a1 [B][T][att] f16 dense (att = 128), w [C][att]
+ * f16, b_c [C] f32, x [B][T][C] f16 dense, C % 64 == 0.  One pass over the
+ * frames: the softmax normaliser and the weighted sums of x and x^2 are f64
+ * with online rescaling of the running max; var = E_a[x^2] - mu^2 in f64. */
+int vdk_asp_attn_pool(const void* d_a1, int a1_stride, const void* d_w, const float* d_b, int att,
+                      const void* d_x, int x_stride, int batch, int T, int C, float eps, float* d_out,
+                      void* stream);
 
 /* ---- L2 normalisation ----
  * Replaces the host L2 of src/encoder_resnet.cpp:177-183 (double accumulation,

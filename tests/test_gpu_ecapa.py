@@ -309,6 +309,46 @@ def test_se_and_asp_reductions():
     assert np.allclose(gp[:, M:], sd, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("batch,T", [(64, 398), (3, 1), (2, 63), (2, 64), (2, 65), (2, 130), (1, 998)])
+def test_asp_attention_pool_fused(batch, T):
+    """vdk_asp_attn_pool (the asp.conv logits and the pooling in one launch)
+    against the f64 softmax pooling of the same f16 operands and against the
+    two-launch path (f32 logits from the conv kernel, then vdk_asp_pool); T
+    covers one frame, the 64-frame chunk edges and a 10 s clip."""
+    L = lib.lib()
+    rng = np.random.default_rng(batch * 1000 + T)
+    M, A = 1536, 128
+    announce(f"asp attn pool B={batch} T={T}")
+    a1 = np.tanh(rng.standard_normal((batch, T, A), dtype=np.float32)).astype(np.float16)
+    w = (rng.standard_normal((M, A), dtype=np.float32) * 0.3).astype(np.float16)
+    bc = (rng.standard_normal(M) * 0.5).astype(np.float32)
+    x = (rng.standard_normal((batch, T, M), dtype=np.float32) * 2 + 1).astype(np.float16)
+    x[:, :, 7] = 0.25                      # constant channel: the variance clamps to eps
+    w[11] *= 16                            # sharp attention on channel 11: the running max moves a lot
+    da1, dw, db, dx = (lib.DeviceBuffer.from_array(v) for v in (a1, w, bc, x))
+    dp = lib.DeviceBuffer(batch * 2 * M * 4)
+    lib.check(L.vdk_asp_attn_pool(da1.ptr, A, dw.ptr, db.ptr, A, dx.ptr, M, batch, T, M, 1e-12, dp.ptr, None))
+    _sync()
+    got = dp.to_array(np.float32, (batch, 2 * M)).astype(np.float64)
+    lg = a1.astype(np.float64) @ w.astype(np.float64).T + bc
+    a = np.exp(lg - lg.max(axis=1, keepdims=True))
+    a /= a.sum(axis=1, keepdims=True)
+    xs = x.astype(np.float64)
+    mu = (a * xs).sum(axis=1)
+    sd = np.sqrt(np.maximum((a * (xs - mu[:, None, :]) ** 2).sum(axis=1), 1e-12))
+    assert np.allclose(got[:, :M], mu, rtol=1e-5, atol=1e-5), np.abs(got[:, :M] - mu).max()
+    assert np.allclose(got[:, M:], sd, rtol=1e-5, atol=1e-5), np.abs(got[:, M:] - sd).max()
+    assert np.all(got[:, M + 7] == np.float32(1e-6))
+    # the two-launch path on the same operands
+    lgd = lib.DeviceBuffer(batch * T * M * 4)
+    tdnn_gpu(da1.ptr, batch, T, A, A, w.reshape(M, A, 1), 1, db, lgd.ptr, M, relu=False, y_f32=True)
+    dq = lib.DeviceBuffer(batch * 2 * M * 4)
+    lib.check(L.vdk_asp_pool(lgd.ptr, M, dx.ptr, M, batch, T, M, 1e-12, dq.ptr, None))
+    _sync()
+    two = dq.to_array(np.float32, (batch, 2 * M)).astype(np.float64)
+    assert np.allclose(got, two, rtol=1e-5, atol=1e-5), np.abs(got - two).max()
+
+
 def test_linear_relu():
     rng = np.random.default_rng(61)
     L = lib.lib()

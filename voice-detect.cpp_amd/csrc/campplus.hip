@@ -142,8 +142,6 @@ __global__ __launch_bounds__(256) void cam_context_kernel(const float* __restric
 //     implicit-GEMM kernels' order), operands from LDS.
 // The segment's G = 32 outputs go to y [b][t][y_stride] f16.
 constexpr int kLocalOC = 32;
-constexpr uint32_t kOOB = 0x80000000u;   // any offset >= num_records reads as zero
-typedef __attribute__((address_space(3))) void lds_void;
 
 struct CamLocalLds {
     int xrow, wrow, nrow, xins, wins, part_bytes, x_off, w_off, ctx_off, total;

@@ -58,4 +58,47 @@ uint16_t float_to_half_bits(float f);
 
 inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
+// ---- device helpers shared by the kernels ----
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kOOB = 0x80000000u;   // any buffer offset >= num_records reads as zero
+
+// Workgroup barrier over LDS traffic only: this wave's LDS reads and writes
+// complete (lgkmcnt(0)) before s_barrier, while its global stores and LDS DMA
+// stay in flight.  (A workgroup-scope release fence would also drain vmcnt,
+// because LDS DMA counts as a pending LDS write.)
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7, lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// s_waitcnt until at most N vector memory operations of this wave are in
+// flight (expcnt and lgkmcnt left at their "no wait" maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Buffer resource words of [base, base + bytes) for dma16 (raw buffer,
+// offsets at or past `bytes` read as zero).
+__device__ __forceinline__ int4v dma_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    return int4v{(int)(uint32_t)p, (int)(uint32_t)(p >> 32), (int)bytes, 0x00020000};
+}
+
+// One 16-byte-per-lane DMA (buffer_load ... lds) from the buffer at byte
+// offset voff to LDS lds_dst + 16 * lane (lds_dst is wave-uniform).  Written
+// as inline assembly, so the compiler does not see it as a write to LDS and
+// never makes LDS reads wait for it: the caller orders it with vmcnt waits
+// and barriers of its own.
+__device__ __forceinline__ void dma16(uint8_t* lds_dst, int4v rsrc, uint32_t voff) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_dst);
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(m0v) : "memory");
+}
+
 }  // namespace vdk

@@ -224,7 +224,6 @@ __device__ __forceinline__ void stage_epilogue_impl(const ConvArgs& a, uint8_t* 
     }
 }
 
-constexpr uint32_t kOOB = 0x80000000u;   // any offset >= num_records reads as zero
 
 // PRO: the input prologue relu(x * in_scale + in_shift) (its scale / shift
 // registers exist only in these instantiations).  Q8: 1x1 weights read as
@@ -450,8 +449,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
 //  * Two LDS stages; chunk k+1 is in flight while chunk k feeds the MFMAs; one
 //    barrier per chunk.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void lds_void;
-typedef int int4v __attribute__((ext_vector_type(4)));
 
 
 template <int KC>
@@ -822,16 +819,6 @@ void launch_halo(const ConvArgs& a, hipStream_t s) {
 // block bit for bit.  Barriers wait for LDS traffic only; global stores drain
 // in the background.
 // ---------------------------------------------------------------------------
-// Workgroup barrier over LDS traffic only: this wave's LDS reads and writes
-// complete (lgkmcnt(0)) before s_barrier, while its global stores and LDS DMA
-// stay in flight.  (A workgroup-scope release fence would also drain vmcnt,
-// because LDS DMA counts as a pending LDS write.)
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7, lgkmcnt 0
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // LDS pixel rows of the fused block are C*2 bytes of channels plus 16 bytes of
 // padding (80 bytes for C = 32): 16 consecutive rows then start in 16
@@ -1150,7 +1137,7 @@ void launch_resblock(const half_t* x, const half_t* w1, const float* b1, const h
 // sums are the other conv kernels' (f16 x f16, f32 accumulation in
 // tap-major, channel-minor order, then + bias, + residual, act).
 //
-// The ring's DMA goes through rw_dma (inline assembly): the compiler does not
+// The ring's DMA goes through dma16 (inline assembly): the compiler does not
 // see it as a write to LDS, so it never makes the convolution's LDS reads
 // wait for the loads in flight into the other stages; the kernel orders them
 // itself with explicit vmcnt waits and the per-tile barrier.
@@ -1170,19 +1157,6 @@ struct RwTile {
     static_assert(NS * STAGE <= 163840, "the ring fits the 160 KB of LDS");
 };
 
-// Buffer resource words of [base, base + bytes) for rw_dma (raw buffer,
-// offsets at or past `bytes` read as zero).
-__device__ __forceinline__ int4v rw_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t p = (uint64_t)(uintptr_t)base;
-    return int4v{(int)(uint32_t)p, (int)(uint32_t)(p >> 32), (int)bytes, 0x00020000};
-}
-
-// One 16-byte-per-lane DMA from the buffer at byte offset voff to LDS
-// lds_dst + 16 * lane (lds_dst is wave-uniform).
-__device__ __forceinline__ void rw_dma(uint8_t* lds_dst, int4v rsrc, uint32_t voff) {
-    const uint32_t m0v = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds_dst);
-    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(m0v) : "memory");
-}
 
 // Per-workgroup constants of the register-weight kernel's tile walk.
 struct RwWalk {
@@ -1224,7 +1198,7 @@ struct RwSide {
             const int ih = oh0 - 1 + (k->hpos[j] >> 8), iw = ow0 - 1 + (k->hpos[j] & 255);
             const uint32_t off = ((unsigned)ih < (unsigned)k->H && (unsigned)iw < (unsigned)k->W)
                                      ? (uint32_t)(xo + k->hofs[j]) : kOOB;
-            rw_dma(st + ins * 1024, k->xr, off);
+            dma16(st + ins * 1024, k->xr, off);
         } else if constexpr (RES) {
             const int i = j - G::X_IPW;
             if (i >= G::R_IPW) return;
@@ -1233,7 +1207,7 @@ struct RwSide {
             const int ih = oh0 + (k->rpos[i] >> 8), iw = ow0 + (k->rpos[i] & 255);
             const uint32_t off = ((unsigned)ih < (unsigned)k->H && (unsigned)iw < (unsigned)k->W)
                                      ? (uint32_t)(ro + k->rofs[i]) : kOOB;
-            rw_dma(st + G::X_BYTES + ins * 1024, k->rr, off);
+            dma16(st + G::X_BYTES + ins * 1024, k->rr, off);
         }
     }
 };
@@ -1346,8 +1320,8 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_rw_kernel(ConvArgs a, int nti
     }
     RwWalk k;
     k.hofs = hofs; k.hpos = hpos; k.rofs = rofs; k.rpos = rpos;
-    k.xr = rw_rsrc(a.x, (uint32_t)a.npix_in * IC * 2);
-    k.rr = rw_rsrc(RES ? (const void*)a.res : (const void*)a.x, RES ? (uint32_t)a.npix * OC * 2 : 0u);
+    k.xr = dma_rsrc(a.x, (uint32_t)a.npix_in * IC * 2);
+    k.rr = dma_rsrc(RES ? (const void*)a.res : (const void*)a.x, RES ? (uint32_t)a.npix * OC * 2 : 0u);
     k.H = a.H;
     k.W = W;
     k.tiles_w = (W + 31) / 32;

@@ -205,6 +205,214 @@ __global__ __launch_bounds__(1024) void asp_pool_kernel(const float* __restrict_
     }
 }
 
+// ---------------------------------------------------------------------------
+// asp_attn_pool_kernel: the attention logits and the pooling in one launch
+// (src/encoder.cpp:283-294): l[t][c] = b[c] + sum_k W[c][k] a1[t][k] (the
+// 1x1 asp.conv), softmax over time per channel, then
+//   mu = sum_t a_t x_t,  sd = sqrt(clamp(sum_t a_t (x_t - mu)^2, eps)).
+// The logits never reach memory: a workgroup owns 64 channels of one clip
+// and streams the clip's frames once, in chunks of 64 (the chunk's a1 rows,
+// all ATT channels, and x rows, its 64 channels, DMA'd two chunks ahead
+// into a three-stage LDS ring), computing each 32-channel x 32-frame logit
+// block with MFMAs (W from registers, a1 from LDS, the bias added after the
+// K sum like the conv kernels).  Each (lane, register) keeps an online
+// softmax state: running max m and the sums z = sum e, s1 = sum e x,
+// s2 = sum e x^2 with e = exp(l - m), in f64, rescaled when m grows; the
+// states of the 32 frame lanes merge by a butterfly and the two frame-block
+// waves in a fixed order.  Then mu = s1 / z and var = s2 / z - mu^2 (f64:
+// the cancellation loses ~1e-16 mu^2, far below the f16 resolution of x).
+// Rows 256 / 128 bytes wide with their 16-byte chunks XOR-swizzled by row,
+// so the MFMA operand reads hit 16 distinct chunks per 16 lanes.
+// ---------------------------------------------------------------------------
+constexpr int kAspChunk = 64;   // frames per LDS chunk
+constexpr int kAspStages = 3;
+
+template <int ATT>
+struct AspLds {
+    static constexpr int A_ROW = ATT * 2, X_ROW = 128;                 // bytes per frame
+    static constexpr int A_BYTES = kAspChunk * A_ROW, X_BYTES = kAspChunk * X_ROW;
+    static constexpr int STAGE = A_BYTES + X_BYTES;
+    static constexpr int A_INS = A_BYTES / 1024, X_INS = X_BYTES / 1024, INS = A_INS + X_INS;
+    static_assert(ATT % 16 == 0 && A_BYTES % 1024 == 0 && INS % 4 == 0, "whole DMA instructions, even per wave");
+};
+
+// DMA of frames [t0, t0 + 64) of clip b: a1 rows (ATT channels) and x rows
+// (the workgroup's 64 channels from c0); frames past T read as zeros.
+template <int ATT>
+__device__ __forceinline__ void asp_issue(uint8_t* st, int4v ar, int4v xr, int as, int xs, int b, int T, int t0, int c0,
+                                          int wave, int lane) {
+    using G = AspLds<ATT>;
+    constexpr int ACH = ATT / 8;   // 16-byte chunks per a1 row
+#pragma unroll
+    for (int i = 0; i < G::INS / 4; ++i) {
+        const int ins = wave + 4 * i;
+        uint32_t off;
+        if (ins < G::A_INS) {
+            const int slot = ins * 64 + lane, row = slot / ACH, pos = slot % ACH;
+            const int g = pos ^ (row & (ACH - 1) & 15);   // global chunk held at this position
+            const int t = t0 + row;
+            off = t < T ? (uint32_t)((((size_t)b * T + t) * as + g * 8) * 2) : kOOB;
+        } else {
+            const int slot = (ins - G::A_INS) * 64 + lane, row = slot / 8, pos = slot % 8;
+            const int g = pos ^ (row & 7);
+            const int t = t0 + row;
+            off = t < T ? (uint32_t)((((size_t)b * T + t) * xs + c0 + g * 8) * 2) : kOOB;
+        }
+        dma16(st + ins * 1024, ins < G::A_INS ? ar : xr, off);
+    }
+}
+
+// One 32-channel x 32-frame block of logits into acc: channels c0 + cb*32 +
+// (8g + 4*lhalf + e) for register g*4+e, frame tb*32 + lrow of the chunk.
+template <int ATT>
+__device__ __forceinline__ void asp_logits(const uint8_t* st, const half8* wf, int tb, int lrow, int lhalf,
+                                           float16v& acc) {
+    constexpr int ACH = ATT / 8;
+    const int row = tb * 32 + lrow;
+    const uint8_t* const ab = st + row * (ATT * 2);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < ATT / 16; ++kk) {
+        const int g = kk * 2 + lhalf;
+        const half8 bf = *reinterpret_cast<const half8*>(ab + ((g ^ (row & (ACH - 1) & 15)) * 16));
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[kk], bf, acc, 0, 0, 0);
+    }
+}
+
+// x (4 channels: register group g of this lane's channel block) of frame
+// row `row` of a stage's swizzled x rows.
+__device__ __forceinline__ half4 asp_x4(const uint8_t* xs_lds, int row, int cb, int g, int lhalf) {
+    return *reinterpret_cast<const half4*>(xs_lds + row * 128 + (((cb * 4 + g) ^ (row & 7)) * 16) + lhalf * 8);
+}
+
+// Online-softmax state: running max and the sums scaled by exp(-m).
+struct AspState {
+    float m;
+    double z, s1, s2;
+};
+
+// Merge of two states; commutative, so both lanes of a butterfly pair get
+// the same bits.
+__device__ __forceinline__ void asp_merge(AspState& a, const AspState& o) {
+    if (o.m == -INFINITY) return;
+    if (a.m == -INFINITY) { a = o; return; }
+    const float M = fmaxf(a.m, o.m);
+    const double f1 = (double)__expf(a.m - M), f2 = (double)__expf(o.m - M);
+    a.z = a.z * f1 + o.z * f2;
+    a.s1 = a.s1 * f1 + o.s1 * f2;
+    a.s2 = a.s2 * f1 + o.s2 * f2;
+    a.m = M;
+}
+
+template <int ATT>
+__global__ __launch_bounds__(256, 2) void asp_attn_pool_kernel(const half_t* __restrict__ a1, int as,
+                                                               const half_t* __restrict__ wc,
+                                                               const float* __restrict__ bc,
+                                                               const half_t* __restrict__ x, int xs, int T, int C,
+                                                               float eps, float* __restrict__ out) {
+    using G = AspLds<ATT>;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[kAspStages * G::STAGE];
+    __shared__ float pm[2][64];            // per frame-block wave: merged state of each channel
+    __shared__ double pz[2][64], ps1[2][64], ps2[2][64];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int cb = wave & 1, tb = wave >> 1;   // 32-channel block, 32-frame block of the chunk
+    const int b = blockIdx.y, c0 = blockIdx.x * 64;
+    const int4v ar = dma_rsrc(a1, (uint32_t)((size_t)gridDim.y * T * as * 2));
+    const int4v xr = dma_rsrc(x, (uint32_t)((size_t)gridDim.y * T * xs * 2));
+    const int nq = (T + kAspChunk - 1) / kAspChunk;
+
+    // A fragments of this wave's 32 channels and their biases (register
+    // g*4+e: channel 8g + 4*lhalf + e of the block)
+    half8 wf[ATT / 16];
+#pragma unroll
+    for (int kk = 0; kk < ATT / 16; ++kk)
+        wf[kk] = *reinterpret_cast<const half8*>(wc + (size_t)(c0 + cb * 32 + lrow) * ATT + kk * 16 + lhalf * 8);
+    float bv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[g * 4 + e] = bc[c0 + cb * 32 + g * 8 + lhalf * 4 + e];
+    __builtin_amdgcn_s_waitcnt(0);
+
+    AspState st_[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st_[r] = AspState{-INFINITY, 0.0, 0.0, 0.0};
+    // chunks 0 and 1 go out together; then the ring stays two chunks ahead
+    asp_issue<ATT>(ring, ar, xr, as, xs, b, T, 0, c0, wave, lane);
+    if (nq > 1) asp_issue<ATT>(ring + G::STAGE, ar, xr, as, xs, b, T, kAspChunk, c0, wave, lane);
+    int slot = 0;
+    for (int q = 0; q < nq; ++q) {
+        // this wave's share of chunk q has landed (at most chunk q+1's
+        // instructions are younger; loads complete in issue order)
+        if (q + 1 < nq) wait_vmcnt<G::INS / 4>();
+        else __builtin_amdgcn_s_waitcnt(0);
+        lds_barrier();   // everyone's; chunk q-1's stage is free for chunk q+2
+        const uint8_t* const st = ring + slot * G::STAGE;
+        if (q + 2 < nq) {
+            const int s2 = slot == 0 ? 2 : slot - 1;
+            asp_issue<ATT>(ring + s2 * G::STAGE, ar, xr, as, xs, b, T, (q + 2) * kAspChunk, c0, wave, lane);
+        }
+        const int row = tb * 32 + lrow, t = q * kAspChunk + row;
+        float16v acc;
+        asp_logits<ATT>(st, wf, tb, lrow, lhalf, acc);
+        if (t < T) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const half4 xv = asp_x4(st + G::A_BYTES, row, cb, g, lhalf);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // branch-free update: rescale by exp(m - m') (1 while the
+                    // max holds, 0 for the first frame)
+                    AspState& S = st_[g * 4 + e];
+                    const float l = acc[g * 4 + e] + bv[g * 4 + e];
+                    const float mn = fmaxf(S.m, l);
+                    const double f = (double)__expf(S.m - mn), ex = (double)__expf(l - mn);
+                    const double xd = (double)(float)xv[e], ex_x = ex * xd;
+                    S.z = S.z * f + ex;
+                    S.s1 = S.s1 * f + ex_x;
+                    S.s2 = S.s2 * f + ex_x * xd;
+                    S.m = mn;
+                }
+            }
+        }
+        slot = slot == 2 ? 0 : slot + 1;
+    }
+    // merge over the 32 frame lanes (butterfly, fixed order), then over the
+    // two frame-block waves
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int msk = 1; msk < 32; msk <<= 1) {
+            const AspState o{__shfl_xor(st_[r].m, msk), __shfl_xor(st_[r].z, msk), __shfl_xor(st_[r].s1, msk),
+                             __shfl_xor(st_[r].s2, msk)};
+            asp_merge(st_[r], o);
+        }
+    if (lrow == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int ch = cb * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
+            pm[tb][ch] = st_[r].m;
+            pz[tb][ch] = st_[r].z;
+            ps1[tb][ch] = st_[r].s1;
+            ps2[tb][ch] = st_[r].s2;
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        AspState S{pm[0][tid], pz[0][tid], ps1[0][tid], ps2[0][tid]};
+        asp_merge(S, AspState{pm[1][tid], pz[1][tid], ps1[1][tid], ps2[1][tid]});
+        const double mu = S.s1 / S.z;
+        float var = (float)(S.s2 / S.z - mu * mu);
+        if (var < eps) var = eps;
+        out[(size_t)b * 2 * C + c0 + tid] = (float)mu;
+        out[(size_t)b * 2 * C + C + c0 + tid] = sqrtf(var);
+    }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -274,6 +482,24 @@ extern "C" int vdk_asp_stats(const void* d_x, int x_stride, int batch, int T, in
         require(batch > 0 && T > 0 && C > 0 && x_stride >= C, "asp_stats: bad shape");
         hipLaunchKernelGGL(asp_stats_kernel, dim3(cdiv(C, 64), batch), dim3(1024), 0,
                            static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, eps,
+                           d_out);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_asp_attn_pool(const void* d_a1, int a1_stride, const void* d_w, const float* d_b, int att,
+                                 const void* d_x, int x_stride, int batch, int T, int C, float eps, float* d_out,
+                                 void* stream) {
+    return guarded([&] {
+        require(d_a1 && d_w && d_b && d_x && d_out, "asp_attn_pool: NULL device pointer");
+        require(batch > 0 && T > 0 && C > 0 && C % 64 == 0, "asp_attn_pool: bad shape (C % 64 == 0)");
+        require(att == 128, "asp_attn_pool: only 128 attention channels have a kernel");
+        require(a1_stride == att && x_stride == C, "asp_attn_pool: a1 / x must be dense");
+        require(al16(d_a1) && al16(d_w) && al16(d_x), "asp_attn_pool: device pointers must be 16-byte aligned");
+        require((size_t)batch * T * C * 2 < (1ull << 31), "asp_attn_pool: too many frames for one launch");
+        hipLaunchKernelGGL(asp_attn_pool_kernel<128>, dim3(C / 64, batch), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_a1), a1_stride,
+                           static_cast<const half_t*>(d_w), d_b, static_cast<const half_t*>(d_x), x_stride, T, C, eps,
                            d_out);
         VDK_HIP(hipGetLastError());
     });

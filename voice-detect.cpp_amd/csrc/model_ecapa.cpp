@@ -226,7 +226,7 @@ void Model::alloc_ecapa_workspace(int batch, int T) {
     w.cat = ws_alloc(2 * BT * nb * e.C);
     w.mfa = ws_alloc(2 * BT * e.mfa);
     w.a1 = ws_alloc(2 * BT * e.att);
-    w.logits = static_cast<float*>(ws_alloc(4 * BT * e.mfa));
+    if (!(e.att == 128 && e.mfa % 64 == 0)) w.logits = static_cast<float*>(ws_alloc(4 * BT * e.mfa));
     w.se_m = static_cast<float*>(ws_alloc(4 * (size_t)batch * e.C));
     w.se_h = static_cast<float*>(ws_alloc(4 * (size_t)batch * se_max));
     w.se_g = static_cast<float*>(ws_alloc(4 * (size_t)batch * e.C));
@@ -349,10 +349,18 @@ void Model::encode_ecapa(int batch, int T) {
     prof_end();
     linear("ecapa_asp_ctx", w.stats, batch, 2 * M, e.asp_stats_w, e.asp_b, nullptr, e.att, 0, w.pb);
     tdnn("ecapa_asp_tdnn", e.asp_x, w.mfa, M, batch, T, 1, w.pb, e.att, 1, 1, w.a1, e.att, 0);
-    tdnn("ecapa_asp_conv", e.asp_conv, w.a1, e.att, batch, T, 1, e.asp_conv.b, 0, 0, 0, w.logits, M, 1);
-    prof_begin("ecapa_asp_pool", 0.0, 4.0 * batch * (double)T * M * 2 + 2.0 * batch * (double)T * M * 2);
-    check_rc(vdk_asp_pool(w.logits, M, w.mfa, M, batch, T, M, kAspEps, w.pooled, stream_));
-    prof_end();
+    if (e.att == 128 && M % 64 == 0) {
+        // the asp.conv logits and the pooling in one launch (logits stay on chip)
+        prof_begin("ecapa_asp_attn_pool", 2.0 * batch * (double)T * M * e.att, 2.0 * batch * (double)T * (M + e.att) * 2);
+        check_rc(vdk_asp_attn_pool(w.a1, e.att, e.asp_conv.w, e.asp_conv.b, e.att, w.mfa, M, batch, T, M, kAspEps,
+                                   w.pooled, stream_));
+        prof_end();
+    } else {
+        tdnn("ecapa_asp_conv", e.asp_conv, w.a1, e.att, batch, T, 1, e.asp_conv.b, 0, 0, 0, w.logits, M, 1);
+        prof_begin("ecapa_asp_pool", 0.0, 4.0 * batch * (double)T * M * 2 + 2.0 * batch * (double)T * M * 2);
+        check_rc(vdk_asp_pool(w.logits, M, w.mfa, M, batch, T, M, kAspEps, w.pooled, stream_));
+        prof_end();
+    }
 
     linear("ecapa_fc", w.pooled, batch, 2 * M, e.fc_w, e.fc_b, nullptr, cfg_.embedding_dim, 0, w.pre);
 }

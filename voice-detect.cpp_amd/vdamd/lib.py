@@ -150,6 +150,8 @@ _SIGS = {
                                        _vp]),
     "vdk_asp_stats": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "vdk_asp_pool": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
+    "vdk_asp_attn_pool": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                    C.c_float, _vp, _vp]),
     "vdk_aff_combine": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_long,
                                   C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp]),
     "vdk_bn_act": (C.c_int, [_vp, C.c_int, C.c_long, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, _vp]),
