@@ -254,14 +254,16 @@ int vdk_feats_tmajor(const float* d_feats, int batch, int n_mels, int T, int pad
  * d_b may be NULL. */
 int vdk_reflect_pad_add(const void* d_a, int a_stride, const void* d_b, int b_stride, int batch, int T,
                         int G, int pad, void* d_out, void* stream);
-/* out [B][C] f32 = mean over time (SE squeeze, src/encoder.cpp:207-209). */
+/* out [B][C] f32 = mean over time (SE squeeze, src/encoder.cpp:207-209), f64
+ * sums; C, x_stride and d_x 8-channel (16-byte) aligned. */
 int vdk_channel_mean(const void* d_x, int x_stride, int batch, int T, int C, float* d_out, void* stream);
 /* y = x * sigmoid(gate[b][c]) + res (SE excitation and the block residual,
  * src/encoder.cpp:218-244). */
 int vdk_se_gate_residual(const void* d_x, int x_stride, const float* d_gate, const void* d_res,
                          int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream);
 /* out [B][2C] = [mean_t x ; sqrt(max(var_t x, eps))] (ASP global context,
- * src/encoder.cpp:269-271). */
+ * src/encoder.cpp:269-271): one pass of f64 sums of x and x^2, var =
+ * E[x^2] - mean^2; C, x_stride and d_x 8-channel (16-byte) aligned. */
 int vdk_asp_stats(const void* d_x, int x_stride, int batch, int T, int C, float eps, float* d_out,
                   void* stream);
 /* softmax over time of logits [B][T][l_stride] f32 per channel, then

@@ -10,7 +10,8 @@
 //    for the dilated k=3 conv (src/encoder.cpp:174-200);
 //  * channel_mean / se_gate_residual: SE squeeze and x * sigmoid(s) + residual
 //    (src/encoder.cpp:207-244);
-//  * asp_stats / asp_pool: attentive statistics pooling with global context
+//  * channel_stats (asp_stats), asp_attn_pool / asp_pool: attentive statistics
+//    pooling with global context
 //    (src/encoder.cpp:262-295): global mean/std (clamp 1e-12), softmax over
 //    time per channel, weighted mean/std.
 // Sums are accumulated in f64.
@@ -62,25 +63,57 @@ __global__ __launch_bounds__(256) void reflect_pad_add_kernel(const half_t* __re
     *reinterpret_cast<half8*>(out + ((size_t)b * Tp + j) * G + c) = v;
 }
 
-// Per-channel mean over time: 64 channels x 16 time partitions per
-// workgroup, f64 partition sums combined in a fixed order.
-__global__ __launch_bounds__(1024) void channel_mean_kernel(const half_t* __restrict__ x, int xs, int T, int C,
-                                                            float* __restrict__ out) {
-    __shared__ double sp[16][64];
-    const int tx = threadIdx.x & 63, tp = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + tx, b = blockIdx.y;
-    double s = 0.0;
-    if (c < C) {
-        const half_t* p = x + (size_t)b * T * xs + c;
-        for (int t = tp; t < T; t += 16) s += (double)(float)p[(size_t)t * xs];
-    }
-    sp[tp][tx] = s;
-    __syncthreads();
-    if (tp == 0 && c < C) {
-        double S = 0.0;
+// Per-channel sums over time of x [B][T][xs] f16 (and, MODE 1, of x^2): a
+// workgroup covers 128 channels (16 lanes x 8 channels, 16-byte loads) of
+// one clip in 16 time partitions; f64 partition sums combined in a fixed
+// order.  MODE 0: out [B][C] = mean; MODE 1: out [B][2C] = [mean ;
+// sqrt(max(var, eps))] with var = E[x^2] - mean^2 in f64 (x is f16, so the
+// cancellation costs ~1e-16 of E[x^2], far below the statistic's rounding).
+template <int MODE>
+__global__ __launch_bounds__(256) void channel_stats_kernel(const half_t* __restrict__ x, int xs, int T, int C,
+                                                            float eps, float* __restrict__ out) {
+    constexpr int NP = 16, CW = 128;
+    __shared__ double sp[NP][CW], sq[MODE == 1 ? NP : 1][CW];
+    const int lx = threadIdx.x & 15, tp = threadIdx.x >> 4;
+    const int c8 = blockIdx.x * CW + lx * 8, b = blockIdx.y;
+    double s[8], q[8];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) S += sp[i][tx];
-        out[(size_t)b * C + c] = (float)(S / T);
+    for (int e = 0; e < 8; ++e) { s[e] = 0.0; q[e] = 0.0; }
+    if (c8 < C) {
+        const half_t* p = x + (size_t)b * T * xs + c8;
+        for (int t = tp; t < T; t += NP) {
+            const half8 v = *reinterpret_cast<const half8*>(p + (size_t)t * xs);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const double d = (double)(float)v[e];
+                s[e] += d;
+                if constexpr (MODE == 1) q[e] += d * d;
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        sp[tp][lx * 8 + e] = s[e];
+        if constexpr (MODE == 1) sq[tp][lx * 8 + e] = q[e];
+    }
+    __syncthreads();
+    const int c = blockIdx.x * CW + threadIdx.x;
+    if (threadIdx.x < CW && c < C) {
+        double S = 0.0, Q = 0.0;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            S += sp[i][threadIdx.x];
+            if constexpr (MODE == 1) Q += sq[i][threadIdx.x];
+        }
+        const double mean = S / T;
+        if constexpr (MODE == 0) {
+            out[(size_t)b * C + c] = (float)mean;
+        } else {
+            float v = (float)(Q / T - mean * mean);
+            if (v < eps) v = eps;
+            out[(size_t)b * 2 * C + c] = (float)mean;
+            out[(size_t)b * 2 * C + C + c] = sqrtf(v);
+        }
     }
 }
 
@@ -103,46 +136,6 @@ __global__ __launch_bounds__(256) void se_gate_residual_kernel(const half_t* __r
         o[e] = (half_t)((float)xv[e] * g + (float)rv[e]);
     }
     *reinterpret_cast<half8*>(y + r * ys + c) = o;
-}
-
-// Global statistics over time per (clip, channel): out[b] = [mean ; sqrt(clamp(var, eps))].
-// Per-channel mean and std over time (biased, clamped at eps): 64 channels x
-// 16 time partitions per workgroup, two passes of f64 partition sums
-// combined in a fixed order.
-__global__ __launch_bounds__(1024) void asp_stats_kernel(const half_t* __restrict__ x, int xs, int T, int C,
-                                                         float eps, float* __restrict__ out) {
-    __shared__ double sp[16][64];
-    const int tx = threadIdx.x & 63, tp = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + tx, b = blockIdx.y;
-    const bool on = c < C;
-    const half_t* p = x + (size_t)b * T * xs + (on ? c : 0);
-    double s = 0.0;
-    if (on)
-        for (int t = tp; t < T; t += 16) s += (double)(float)p[(size_t)t * xs];
-    sp[tp][tx] = s;
-    __syncthreads();
-    double S = 0.0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) S += sp[i][tx];
-    const float m = (float)(S / T);
-    double s2 = 0.0;
-    if (on)
-        for (int t = tp; t < T; t += 16) {
-            const float d = (float)p[(size_t)t * xs] - m;
-            s2 += (double)(d * d);
-        }
-    __syncthreads();   // every thread has read sp
-    sp[tp][tx] = s2;
-    __syncthreads();
-    if (tp == 0 && on) {
-        double S2 = 0.0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) S2 += sp[i][tx];
-        float v = (float)(S2 / T);
-        if (v < eps) v = eps;
-        out[(size_t)b * 2 * C + c] = m;
-        out[(size_t)b * 2 * C + C + c] = sqrtf(v);
-    }
 }
 
 // Softmax over time of the attention logits, then attention-weighted mean / std.
@@ -452,8 +445,10 @@ extern "C" int vdk_channel_mean(const void* d_x, int x_stride, int batch, int T,
     return guarded([&] {
         require(d_x && d_out, "channel_mean: NULL device pointer");
         require(batch > 0 && T > 0 && C > 0 && x_stride >= C, "channel_mean: bad shape");
-        hipLaunchKernelGGL(channel_mean_kernel, dim3(cdiv(C, 64), batch), dim3(1024), 0,
-                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, d_out);
+        require(C % 8 == 0 && x_stride % 8 == 0 && al16(d_x), "channel_mean: channels must be 8-aligned");
+        hipLaunchKernelGGL(channel_stats_kernel<0>, dim3(cdiv(C, 128), batch), dim3(256), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, 0.0f,
+                           d_out);
         VDK_HIP(hipGetLastError());
     });
 }
@@ -480,7 +475,8 @@ extern "C" int vdk_asp_stats(const void* d_x, int x_stride, int batch, int T, in
     return guarded([&] {
         require(d_x && d_out, "asp_stats: NULL device pointer");
         require(batch > 0 && T > 0 && C > 0 && x_stride >= C, "asp_stats: bad shape");
-        hipLaunchKernelGGL(asp_stats_kernel, dim3(cdiv(C, 64), batch), dim3(1024), 0,
+        require(C % 8 == 0 && x_stride % 8 == 0 && al16(d_x), "asp_stats: channels must be 8-aligned");
+        hipLaunchKernelGGL(channel_stats_kernel<1>, dim3(cdiv(C, 128), batch), dim3(256), 0,
                            static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, T, C, eps,
                            d_out);
         VDK_HIP(hipGetLastError());
