@@ -131,6 +131,13 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * kernel's registers to f16(q * d) (the product in f32: the f16 weights a
  * host dequantisation would store, so results equal those from w); w is then
  * not read.
+ * seg_sum (may be NULL; H = 1 maps, f16 output, no split or time-major
+ * store): the stored f16 outputs of each clip's segments of seg_len frames
+ * (the last one may be shorter) are summed per channel and added to seg_sum
+ * [B][ceil(W_out / seg_len)][OC] f64, which the caller zeroes; every term is
+ * an f16, so the f64 sums are exact and independent of the order they are
+ * added in (CAM++'s context pooling, src/encoder_campplus.cpp:159-170).
+ * Register-staged tiles (f16 weights) whose pixel tile is at most seg_len wide.
  * tile = -1 picks the kernel automatically. */
 typedef struct {
     const void* x; int batch, H, W, IC, x_stride;
@@ -152,6 +159,7 @@ typedef struct {
     void* y2; int y2_stride;
     const void* res2; int res2_stride;
     const void* w_q8_0;
+    double* seg_sum; int seg_len;
 } vdk_conv_desc;
 /* Host: re-order f16 conv weights [OC][KH][KW][IC] (IC % 16 == 0) into the
  * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */
@@ -323,10 +331,17 @@ int vdk_cam_context(const float* d_sums, int batch, int T, int C, int seg, const
  * y = (linear_local(x) + bl) * gate, linear_local the k = 3 conv with
  * dilation dil and zero padding, C -> 32 channels, wl f16 [32][3][C]
  * (tap-major), bl [32] f32 (may be NULL); x [B][T][x_stride] f16 (C a
- * multiple of 16, 16..256), y [B][T][y_stride] f16 (the 32 outputs). */
+ * multiple of 16, 16..256), y [B][T][y_stride] f16 (the 32 outputs).
+ * segsum (may be NULL): the f64 per-(clip, segment, channel) sums of x that
+ * the conv producing x accumulated (vdk_conv_desc.seg_sum, seg_len = seg),
+ * [B][ceil(T / seg)][C]; the context then comes from them instead of a pass
+ * over x (same values: both sums are exact).  zero_next (may be NULL, needs
+ * segsum): a buffer of the same shape that each (clip, segment) workgroup
+ * clears, ready for the next layer's seg_sum. */
 int vdk_cam_local(const void* d_x, int x_stride, int batch, int T, int C, int seg, int dil,
                   const float* d_w1, const float* d_b1, int H1, const float* d_w2, const float* d_b2,
-                  const void* d_wl, const float* d_bl, void* d_y, int y_stride, void* stream);
+                  const void* d_wl, const float* d_bl, void* d_y, int y_stride, const double* d_segsum,
+                  double* d_zero_next, void* stream);
 
 /* ---- ERes2Net helper (src/encoder_eres2net.cpp:91-101) ----
  * AFF output y = (x + ds) + t * (x - ds) with t = tanh(local_att(cat(x, ds)))

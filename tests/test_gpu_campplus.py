@@ -192,7 +192,7 @@ def test_cam_local_fused_layer(batch, T, dil, bias):
     dwl = lib.DeviceBuffer.from_array(np.ascontiguousarray(w[:, :, 0, :].transpose(0, 2, 1)))   # [G][3][BC]
     dbl = lib.DeviceBuffer.from_array(bl) if bias else None
     lib.check(L.vdk_cam_local(dcc.ptr, BC, batch, T, BC, SEG, dil, dw1.ptr, db1.ptr, H1, dw2.ptr, db2.ptr, dwl.ptr,
-                              dbl.ptr if dbl else None, dd.ptr + C0 * 2, CMAX, None))
+                              dbl.ptr if dbl else None, dd.ptr + C0 * 2, CMAX, None, None, None))
     _sync()
     out = dd.to_array(np.float16, (batch, T, CMAX))
     keep = np.ones(CMAX, dtype=bool)
@@ -284,3 +284,66 @@ def test_campplus_verify_matches_oracle(campp):
     assert abs(d_gpu - d_ref) <= 2e-3
     for thr in (d_ref - 5e-3, d_ref + 5e-3):
         assert ctx.verify_pcm(a, b, thr)[1] == (d_ref <= thr)
+
+
+@pytest.mark.parametrize("batch,T,c_in", [(B, TP, 320), (3, 257, 160), (2, 40, 128)])
+def test_linear1_segment_sums_feed_cam_local(batch, T, c_in):
+    """linear1 with seg_sum (the per-(clip, segment) f64 sums of its stored
+    f16 outputs, accumulated in the conv's epilogue) equals the exact f64
+    sums of h and leaves h bit-identical; cam_local fed those sums (and
+    clearing the next layer's buffer) writes the same bits as cam_local
+    summing h itself."""
+    rng = np.random.default_rng(7 * T + c_in)
+    L = lib.lib()
+    BC, G, H1, SEG, CMAX = 128, 32, 64, 100, 512
+    nseg = (T + SEG - 1) // SEG
+    announce(f"campp linear1 seg sums B={batch} T'={T} c_in={c_in}")
+    dense = rng.standard_normal((batch, T, CMAX), dtype=np.float32).astype(np.float16)
+    s1 = (rng.random(c_in, dtype=np.float32) + 0.5).astype(np.float32)
+    t1 = (rng.standard_normal(c_in, dtype=np.float32) * 0.2).astype(np.float32)
+    w = (rng.standard_normal((BC, c_in), dtype=np.float32) / np.sqrt(c_in)).astype(np.float16)
+    bias = (rng.standard_normal(BC, dtype=np.float32) * 0.1).astype(np.float32)
+    dd, ds1, dt1, dw, db = (lib.DeviceBuffer.from_array(a) for a in (dense, s1, t1, w, bias))
+
+    def linear1(seg_buf):
+        dh = lib.DeviceBuffer(batch * T * BC * 2)
+        d = lib.ConvDesc()
+        d.x, d.batch, d.H, d.W, d.IC, d.x_stride = dd.ptr, batch, 1, T, c_in, CMAX
+        d.w, d.OC, d.KH, d.KW = dw.ptr, BC, 1, 1
+        d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+        d.bias, d.act = db.ptr, lib.ACT_RELU
+        d.in_scale, d.in_shift = ds1.ptr, dt1.ptr
+        d.y, d.y_stride, d.tile = dh.ptr, BC, -1
+        if seg_buf is not None:
+            d.seg_sum, d.seg_len = seg_buf.ptr, SEG
+        lib.check(L.vdk_conv2d_ex(d, None))
+        _sync()
+        return dh
+
+    seg = lib.DeviceBuffer.from_array(np.zeros((batch, nseg, BC), dtype=np.float64))
+    dh = linear1(seg)
+    h = dh.to_array(np.float16, (batch, T, BC))
+    h0 = linear1(None).to_array(np.float16, (batch, T, BC))
+    assert np.array_equal(h.view(np.uint16), h0.view(np.uint16))
+    got = seg.to_array(np.float64, (batch, nseg, BC))
+    hd = h.astype(np.float64)
+    want = np.stack([hd[:, i * SEG:(i + 1) * SEG].sum(axis=1) for i in range(nseg)], axis=1)
+    assert np.array_equal(got, want), np.abs(got - want).max()
+    # cam_local from the sums against cam_local summing h itself
+    w1 = rng.standard_normal((H1, BC), dtype=np.float32) / 8
+    b1 = rng.standard_normal(H1, dtype=np.float32) / 4
+    w2 = rng.standard_normal((G, H1), dtype=np.float32) / 8
+    b2 = rng.standard_normal(G, dtype=np.float32) / 4
+    wl = (rng.standard_normal((G, 3, BC), dtype=np.float32) / np.sqrt(3 * BC)).astype(np.float16)
+    bl = (rng.standard_normal(G, dtype=np.float32) * 0.1).astype(np.float32)
+    dw1, db1, dw2, db2, dwl, dbl = (lib.DeviceBuffer.from_array(a) for a in (w1, b1, w2, b2, wl, bl))
+    nxt = lib.DeviceBuffer.from_array(rng.standard_normal((batch, nseg, BC)))
+    outs = []
+    for use in (False, True):
+        dy = lib.DeviceBuffer(batch * T * G * 2)
+        lib.check(L.vdk_cam_local(dh.ptr, BC, batch, T, BC, SEG, 2, dw1.ptr, db1.ptr, H1, dw2.ptr, db2.ptr, dwl.ptr,
+                                  dbl.ptr, dy.ptr, G, seg.ptr if use else None, nxt.ptr if use else None, None))
+        _sync()
+        outs.append(dy.to_array(np.float16, (batch, T, G)))
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
+    assert not nxt.to_array(np.float64, (batch, nseg, BC)).any()

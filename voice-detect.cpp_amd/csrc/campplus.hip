@@ -166,7 +166,9 @@ __global__ __launch_bounds__(256) void cam_local_kernel(const half_t* __restrict
                                                         const float* __restrict__ b1, int H1,
                                                         const float* __restrict__ w2, const float* __restrict__ b2,
                                                         const half_t* __restrict__ wl, const float* __restrict__ bl,
-                                                        half_t* __restrict__ y, int ys) {
+                                                        half_t* __restrict__ y, int ys,
+                                                        const double* __restrict__ segsum,
+                                                        double* __restrict__ zero_next) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
     const CamLocalLds Lo = cam_local_lds(C, seg, dil, H1);
     uint8_t* const sx = smem + Lo.x_off;
@@ -199,7 +201,16 @@ __global__ __launch_bounds__(256) void cam_local_kernel(const half_t* __restrict
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(sw + ins * 1024), 16, off, 0, 0, 0);
         }
     }
-    {   // 1. sums
+    if (segsum) {   // 1. the segment sums came with the input: ctx from them
+        const int nseg = (T + seg - 1) / seg;
+        const double* sb = segsum + (size_t)b * nseg * C;
+        for (int c = tid; c < C; c += 256) {
+            double a = 0.0;
+            for (int q = 0; q < nseg; ++q) a += sb[(size_t)q * C + c];
+            ctx[c] = (float)(a / T) + (float)(sb[(size_t)s * C + c] / seg);
+            if (zero_next) zero_next[((size_t)b * nseg + s) * C + c] = 0.0;
+        }
+    } else {   // 1. sums
         const int cc = tid % C8, fl = tid / C8;
         double tot[8], sg[8];
 #pragma unroll
@@ -237,15 +248,15 @@ __global__ __launch_bounds__(256) void cam_local_kernel(const half_t* __restrict
                 part[(size_t)(NFL + fl) * C + cc * 8 + e] = sg[e];
             }
         }
-    }
-    __syncthreads();
-    for (int c = tid; c < C; c += 256) {
-        double a = 0.0, g = 0.0;
-        for (int q = 0; q < NFL; ++q) {
-            a += part[(size_t)q * C + c];
-            g += part[(size_t)(NFL + q) * C + c];
+        __syncthreads();
+        for (int c = tid; c < C; c += 256) {
+            double a = 0.0, g = 0.0;
+            for (int q = 0; q < NFL; ++q) {
+                a += part[(size_t)q * C + c];
+                g += part[(size_t)(NFL + q) * C + c];
+            }
+            ctx[c] = (float)(a / T) + (float)(g / seg);
         }
-        ctx[c] = (float)(a / T) + (float)(g / seg);
     }
     __syncthreads();
     {   // 2. the mask MLP
@@ -347,7 +358,8 @@ extern "C" int vdk_cam_context(const float* d_sums, int batch, int T, int C, int
 
 extern "C" int vdk_cam_local(const void* d_x, int x_stride, int batch, int T, int C, int seg, int dil,
                              const float* d_w1, const float* d_b1, int H1, const float* d_w2, const float* d_b2,
-                             const void* d_wl, const float* d_bl, void* d_y, int y_stride, void* stream) {
+                             const void* d_wl, const float* d_bl, void* d_y, int y_stride, const double* d_segsum,
+                             double* d_zero_next, void* stream) {
     return guarded([&] {
         require(d_x && d_w1 && d_w2 && d_wl && d_y, "cam_local: NULL device pointer");
         require(batch > 0 && T > 0 && seg > 0 && dil > 0 && H1 > 0, "cam_local: bad shape");
@@ -361,12 +373,14 @@ extern "C" int vdk_cam_local(const void* d_x, int x_stride, int batch, int T, in
         const int nseg = (T + seg - 1) / seg;
         const size_t smem = (size_t)cam_local_lds(C, seg, dil, H1).total;
         require(smem <= 160 * 1024, "cam_local: the segment tile and context buffers exceed the workgroup's LDS");
+        require(!d_zero_next || d_segsum, "cam_local: zero_next goes with segsum");
         if (smem > 64 * 1024)
             VDK_HIP(hipFuncSetAttribute((const void*)cam_local_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                         (int)smem));
         hipLaunchKernelGGL(cam_local_kernel, dim3(batch, nseg), dim3(256), smem, static_cast<hipStream_t>(stream),
                            static_cast<const half_t*>(d_x), x_stride, T, C, seg, dil, d_w1, d_b1, H1, d_w2, d_b2,
-                           static_cast<const half_t*>(d_wl), d_bl, static_cast<half_t*>(d_y), y_stride);
+                           static_cast<const half_t*>(d_wl), d_bl, static_cast<half_t*>(d_y), y_stride, d_segsum,
+                           d_zero_next);
         VDK_HIP(hipGetLastError());
     });
 }

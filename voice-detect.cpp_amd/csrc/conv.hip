@@ -56,6 +56,8 @@ struct ConvArgs {
     const half_t* r2;
     int y2s, r2s;
     const uint8_t* wq;         // 1x1 weights as q8_0 blocks [OC][IC/32] x {f16 d, 32 x int8} (register-staged kernel)
+    double* segsum;            // per-(clip, segment, OC) f64 sums of the stored outputs (may be NULL)
+    int seg_len, seg_n;        // output columns per segment, segments per clip
 };
 
 // Epilogue for 8 consecutive output channels oc..oc+7 of pixel P (P
@@ -90,7 +92,7 @@ __device__ __forceinline__ void add_residual(const ConvArgs& a, int P, int oc, f
     }
 }
 
-__device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float* v) {
+__device__ __forceinline__ void epi8(const ConvArgs& a, int P, int oc, float* v) {
     const int HoWo = a.Ho * a.Wo;
     if (a.bias) add8(v, a.bias + oc + (a.bias_bs ? (size_t)(P / HoWo) * a.bias_bs : 0));
     if (a.gate) {
@@ -124,6 +126,10 @@ __device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float*
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = tanhf(v[e]);
     }
+}
+
+__device__ __forceinline__ void store8(const ConvArgs& a, int P, int oc, const float* v) {
+    const int HoWo = a.Ho * a.Wo;
     size_t Po = (size_t)P;
     if (a.y_tr) {
         const int b = P / HoWo, rem = P - b * HoWo, oh = rem / a.Wo, ow = rem - oh * a.Wo;
@@ -155,6 +161,11 @@ __device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float*
     }
 }
 
+__device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float* v) {
+    epi8(a, P, oc, v);
+    store8(a, P, oc, v);
+}
+
 // The finished 32x32 MFMA blocks are staged through LDS as f32 [pixel][oc]
 // (row stride TS = M + 4 floats, so consecutive pixels start 16 bytes apart
 // across the 64 banks) and then every thread finishes 8 consecutive channels
@@ -173,9 +184,16 @@ __device__ __forceinline__ void stage_block(float* sT, int TS, int pix0, int row
 
 // Finish NPIX staged pixels x M channels; pix(pl) maps a staged pixel to P
 // (or -1 when outside the output).
-template <int M, class PixFn>
+__device__ __forceinline__ int seg_id(const ConvArgs& a, int P) {
+    const int HoWo = a.Ho * a.Wo, b = P / HoWo;
+    return b * a.seg_n + (P - b * HoWo) / a.seg_len;
+}
+
+// SEGS: part accumulates f64 sums of the stored f16 values of this thread's
+// 8 channels, per segment relative to sid0 (0 or 1); see stage_epilogue_impl.
+template <int M, bool SEGS = false, class PixFn>
 __device__ __forceinline__ void finish_staged(const ConvArgs& a, const float* sT, int npix_tile, int oc0, int tid,
-                                              int nthreads, PixFn pix) {
+                                              int nthreads, PixFn pix, double (&part)[2][8], int sid0) {
     constexpr int TS = M + 4, C8 = M / 8;
     for (int q = tid; q < npix_tile * C8; q += nthreads) {
         const int pl = q / C8, c8 = q - pl * C8;
@@ -184,7 +202,17 @@ __device__ __forceinline__ void finish_staged(const ConvArgs& a, const float* sT
         const float4v u0 = *reinterpret_cast<const float4v*>(sT + pl * TS + c8 * 8);
         const float4v u1 = *reinterpret_cast<const float4v*>(sT + pl * TS + c8 * 8 + 4);
         float v[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
-        finish8(a, P, oc, v);
+        epi8(a, P, oc, v);
+        if constexpr (SEGS) {
+            const bool first = seg_id(a, P) == sid0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const double h = (double)(float)(half_t)v[e];   // the stored value
+                part[0][e] += first ? h : 0.0;
+                part[1][e] += first ? 0.0 : h;
+            }
+        }
+        store8(a, P, oc, v);
     }
 }
 
@@ -199,14 +227,27 @@ __device__ __forceinline__ int xcd_swizzle(int bid, int nb) {
 // Staged epilogue of an implicit-GEMM tile (BM channels x BN consecutive
 // pixels): waves write their blocks in passes of PB pixel columns that fit the
 // kernel's LDS buffer, then all threads finish 8-channel rows.
-template <int BM, int BN, int WN, int SMEM, int NT, int TM, int TN>
+// Segment sums of the stored f16 outputs (ConvArgs::segsum): the tile's
+// pixels fall in at most two segments (the pixel tile is at most seg_len
+// wide), part 0 the segment of the tile's first pixel.  Each thread keeps
+// its 8 channels' sums per part (a fixed channel chunk: NT is a multiple of
+// BM / 8), the threads of a chunk are summed within the wave and then across
+// the waves, and each (part, channel) goes out as one f64 atomic add; every
+// term is an f16, so all these sums are exact and the result does not depend
+// on the order of the additions.
+template <int BM, int BN, int WN, int SMEM, int NT, int TM, int TN, bool SEGS = false>
 __device__ __forceinline__ void stage_epilogue_impl(const ConvArgs& a, uint8_t* smem, const float16v (*acc)[TN],
                                                     int m_off, int n_off, int p0, int oc0, int tid, int lane) {
     constexpr int TS = BM + 4;
     constexpr int FIT = SMEM / (TS * 4);
     constexpr int PB = FIT >= BN ? BN : (FIT / WN) * WN;
     static_assert(PB >= WN, "epilogue staging holds at least one wave's pixel columns");
+    static_assert(NT % (BM / 8) == 0 && SMEM >= 2 * BM * 8, "segment sums: fixed channel chunk per thread");
     float* sT = reinterpret_cast<float*>(smem);
+    const int sid0 = SEGS ? seg_id(a, p0) : 0;
+    double part[2][8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[0][e] = part[1][e] = 0.0;
     for (int pb = 0; pb < BN; pb += PB) {
         __syncthreads();   // every wave is done with the previous contents of smem
         if (n_off >= pb && n_off < pb + PB) {
@@ -217,10 +258,46 @@ __device__ __forceinline__ void stage_epilogue_impl(const ConvArgs& a, uint8_t* 
         }
         __syncthreads();
         const int np = BN - pb < PB ? BN - pb : PB;
-        finish_staged<BM>(a, sT, np, oc0, tid, NT, [&](int pl) {
-            const int P = p0 + pb + pl;
-            return P < a.npix ? P : -1;
-        });
+        finish_staged<BM, SEGS>(
+            a, sT, np, oc0, tid, NT,
+            [&](int pl) {
+                const int P = p0 + pb + pl;
+                return P < a.npix ? P : -1;
+            },
+            part, sid0);
+    }
+    if constexpr (SEGS) {
+        // lanes of a wave with the same channel chunk (lane % C8) first, by a
+        // butterfly, then the waves through LDS, then one global add per
+        // (part, channel)
+        constexpr int C8 = BM / 8, NWV = NT / 64;
+        static_assert(C8 <= 64 && NWV * 2 * BM * 8 <= SMEM, "per-wave segment sums fit the staging area");
+#pragma unroll
+        for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+#pragma unroll
+                for (int m = C8; m < 64; m <<= 1) part[pt][e] += __shfl_xor(part[pt][e], m);
+        double* wsum = reinterpret_cast<double*>(smem);   // [NWV][2][BM]
+        __syncthreads();   // the staged tile is consumed
+        const int wave = tid >> 6;
+        if (lane < C8) {
+#pragma unroll
+            for (int pt = 0; pt < 2; ++pt)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) wsum[(wave * 2 + pt) * BM + lane * 8 + e] = part[pt][e];
+        }
+        __syncthreads();
+        const int last = (p0 + BN < a.npix ? p0 + BN : a.npix) - 1;
+        const int nparts = seg_id(a, last) - sid0 + 1;
+        for (int i = tid; i < 2 * BM; i += NT) {
+            const int pt = i / BM, c = i - pt * BM;
+            double v = 0.0;
+#pragma unroll
+            for (int w = 0; w < NWV; ++w) v += wsum[(w * 2 + pt) * BM + c];
+            if (pt < nparts && oc0 + c < a.OC && v != 0.0)
+                atomicAdd(a.segsum + (size_t)(sid0 + pt) * a.OC + oc0 + c, v);
+        }
     }
 }
 
@@ -230,7 +307,7 @@ __device__ __forceinline__ void stage_epilogue_impl(const ConvArgs& a, uint8_t* 
 // q8_0 blocks (34 bytes: an f16 scale d and 32 int8 quants q along IC) and
 // dequantised in registers, w = f16(q * d) with the product in f32, the value
 // a host-side dequantisation to f16 stores.
-template <int BM, int BN, int WM, int WN, int KC, bool PRO, bool Q8 = false>
+template <int BM, int BN, int WM, int WN, int KC, bool PRO, bool Q8 = false, bool SEG = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(ConvArgs a) {
     constexpr int NWM = BM / WM, NWN = BN / WN, NT = NWM * NWN * 64;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -432,7 +509,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         }
     }
 
-    stage_epilogue_impl<BM, BN, WN, SMEM, NT, TM, TN>(a, smem, acc, wm * WM, wn * WN, p0, oc0, tid, lane);
+    stage_epilogue_impl<BM, BN, WN, SMEM, NT, TM, TN, SEG>(a, smem, acc, wm * WM, wn * WN, p0, oc0, tid, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -781,10 +858,14 @@ __global__ __launch_bounds__(256) void conv3x3_halo_kernel(ConvArgs a) {
         stage_block(sT, TS, nb * 32, mb * 32, acc[q], lane);
     }
     __syncthreads();
-    finish_staged<OCB>(a, sT, TH * TW, oc0, tid, 256, [&](int pl) {
-        const int oh = oh0 + pl / TW, ow = ow0 + pl % TW;
-        return (oh < a.Ho && ow < a.Wo) ? (b * a.Ho + oh) * a.Wo + ow : -1;
-    });
+    double nopart[2][8];
+    finish_staged<OCB>(
+        a, sT, TH * TW, oc0, tid, 256,
+        [&](int pl) {
+            const int oh = oh0 + pl / TW, ow = ow0 + pl % TW;
+            return (oh < a.Ho && ow < a.Wo) ? (b * a.Ho + oh) * a.Wo + ow : -1;
+        },
+        nopart, 0);
 }
 
 template <int OCB, int KC, int TH, int TW>
@@ -1955,7 +2036,11 @@ template <int BM, int BN, int WM, int WN, int KC>
 void launch_igemm(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
     dim3 grid(cdiv(a.npix, BN), cdiv(a.OC, BM));
-    if (a.in_scale && a.wq)
+    if (a.segsum && a.in_scale)   // segment sums: the f16-weight variants only
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, true, false, true>), grid, dim3(NT), 0, s, a);
+    else if (a.segsum)
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, false, false, true>), grid, dim3(NT), 0, s, a);
+    else if (a.in_scale && a.wq)
         hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, true, true>), grid, dim3(NT), 0, s, a);
     else if (a.in_scale)
         hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, WM, WN, KC, true>), grid, dim3(NT), 0, s, a);
@@ -2083,6 +2168,9 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     if (a.reflect && (igemm_tile(idx) || t.halo)) return false;
     // q8_0 weights are dequantised in the register-staged kernel's weight loads
     if (a.wq && !igemm_tile(idx)) return false;
+    // segment sums live in the staged epilogue of the register-staged
+    // kernel (f16 weights), for pixel tiles that touch at most two segments
+    if (a.segsum && (!igemm_tile(idx) || a.wq || t.bn > a.seg_len)) return false;
     // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
     // the in-image tap range for a single row of taps; longer 2-D kernels
     // take the register-staged kernel
@@ -2405,6 +2493,13 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
                 "conv2d: q8_0 weights are for 1x1 convs with IC % 32 == 0 and no split-f16");
         ConvArgs a{};
         a.wq = static_cast<const uint8_t*>(d.w_q8_0);
+        require(!d.seg_sum || (Ho == 1 && d.seg_len > 0 && !d.split && !d.y_f32 && !d.y_time_major && !d.y2 &&
+                               (reinterpret_cast<uintptr_t>(d.seg_sum) & 7) == 0),
+                "conv2d: seg_sum needs H_out = 1, seg_len > 0, an f16 output (no split, time-major store or y2) and "
+                "8-byte alignment");
+        a.segsum = d.seg_sum;
+        a.seg_len = d.seg_sum ? d.seg_len : 1;
+        a.seg_n = d.seg_sum ? (Wo + d.seg_len - 1) / d.seg_len : 1;
         a.reflect = d.reflect_pad ? 1 : 0;
         a.y2 = static_cast<half_t*>(d.y2);
         a.r2 = static_cast<const half_t*>(d.res2);
@@ -2495,6 +2590,8 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.reflect = d.reflect_pad ? 1 : 0;
     a.y2 = static_cast<half_t*>(d.y2);
     a.wq = static_cast<const uint8_t*>(d.w_q8_0);
+    a.segsum = d.seg_sum;
+    a.seg_len = d.seg_sum && d.seg_len > 0 ? d.seg_len : 1;
     return a;
 }
 

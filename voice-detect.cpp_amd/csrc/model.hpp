@@ -272,6 +272,8 @@ private:
         void* fcm_t = nullptr;
         void* dense[3] = {nullptr, nullptr, nullptr};
         void *cc = nullptr, *fin = nullptr;
+        double* segsum[2] = {nullptr, nullptr};   // per-(clip, segment) sums of linear1's output, two layers' worth
+        size_t segsum_bytes = 0;
         // ERes2Net
         void *ex[2] = {nullptr, nullptr}, *es4 = nullptr, *esc = nullptr, *ez = nullptr, *ez2 = nullptr,
              *ef = nullptr;

@@ -190,6 +190,9 @@ void Model::alloc_campplus_workspace(int batch, int T) {
         cmax = std::max(cmax, m.blocks[b].cmax);
     }
     w.cc = ws_alloc(2 * BTp * m.bn_ch);
+    w.segsum_bytes = 8 * (size_t)batch * ((Tp + kCamSeg - 1) / kCamSeg) * m.bn_ch;
+    w.segsum[0] = static_cast<double*>(ws_alloc(w.segsum_bytes));
+    w.segsum[1] = static_cast<double*>(ws_alloc(w.segsum_bytes));
     w.fin = ws_alloc(2 * BTp * m.c_out);
     w.fc_work_bytes = vdk_linear_workspace_size(batch, pooled_dim_, cfg_.embedding_dim);
     w.fc_work = ws_alloc(w.fc_work_bytes);
@@ -265,9 +268,10 @@ void Model::encode_campplus(int batch, int T) {
     // TDNN k=5 s2 p2 -> ReLU into the first dense buffer (src/encoder_campplus.cpp:236-239)
     auto tconv = [&](const char* name, const Layer& l, const void* x, int xs, int W, int sw, int pad, int dil,
                      const float* gate, int act, void* y, int ys, const float* in_scale = nullptr,
-                     const float* in_shift = nullptr) {
+                     const float* in_shift = nullptr, double* seg_sum = nullptr) {
         vdk_conv_desc d{};
         d.in_scale = in_scale; d.in_shift = in_shift;
+        d.seg_sum = seg_sum; d.seg_len = seg_sum ? kCamSeg : 0;
         d.x = x; d.batch = batch; d.H = 1; d.W = W; d.IC = l.ic; d.x_stride = xs;
         d.w = l.w; d.OC = l.oc; d.KH = 1; d.KW = l.k;
         d.stride_h = 1; d.stride_w = sw; d.pad_w = pad; d.dil_w = dil;
@@ -278,22 +282,33 @@ void Model::encode_campplus(int batch, int T) {
     };
     tconv("campp_tdnn", m.tdnn, w.fcm_t, m.tdnn.ic, T, 2, 2, 1, nullptr, VDK_ACT_RELU, w.dense[0], m.blocks[0].cmax);
 
-    // dense blocks (src/encoder_campplus.cpp:250-281)
+    // dense blocks (src/encoder_campplus.cpp:250-281).  linear1 adds its
+    // output's per-(clip, segment) sums to segsum[layer & 1] (the CAM
+    // context's pooling, exact in f64) and the CAM launch clears the other
+    // buffer for the next layer; both start cleared.
+    VDK_HIP(hipMemsetAsync(w.segsum[0], 0, w.segsum_bytes, stream_));
+    VDK_HIP(hipMemsetAsync(w.segsum[1], 0, w.segsum_bytes, stream_));
+    int layer = 0;
     for (int b = 0; b < 3; ++b) {
         const CamBlock& blk = m.blocks[b];
         uint8_t* D = static_cast<uint8_t*>(w.dense[b]);
         for (const CamDense& d : blk.layers) {
+            double* seg = w.segsum[layer & 1];
+            double* seg_next = w.segsum[(layer + 1) & 1];
+            ++layer;
             // nonlinear1 BN + ReLU (src/encoder_campplus.cpp:110-134) folded into
             // linear1's operand loads
             tconv("campp_linear1", d.l1, D, blk.cmax, Tp, 1, 0, 1, nullptr, VDK_ACT_RELU, w.cc, m.bn_ch, d.bn_s,
-                  d.bn_t);
-            // the CAM layer: context sums, mask MLP and the gated linear_local in one launch
+                  d.bn_t, seg);
+            // the CAM layer: context from the segment sums, mask MLP and the gated
+            // linear_local in one launch
             prof_begin("campp_cam_local",
                        2.0 * rows * 3 * m.bn_ch * m.growth +
                            2.0 * batch * nseg * ((double)d.h1 * m.bn_ch + (double)m.growth * d.h1),
                        2.0 * rows * m.bn_ch * (1.0 + nseg) + 2.0 * rows * m.growth);
             check_rc(vdk_cam_local(w.cc, m.bn_ch, batch, Tp, m.bn_ch, kCamSeg, blk.dil, d.c1_w, d.c1_b, d.h1, d.c2_w,
-                                   d.c2_b, d.local.w, d.local.b, D + 2 * (size_t)d.c_in, blk.cmax, stream_));
+                                   d.c2_b, d.local.w, d.local.b, D + 2 * (size_t)d.c_in, blk.cmax, seg, seg_next,
+                                   stream_));
             prof_end();
         }
         const bool last = b == 2;

@@ -46,7 +46,7 @@ class ConvDesc(C.Structure):
                 ("tile", C.c_int), ("res_f32", C.c_int), ("res_after_act", C.c_int), ("out_w", C.c_int),
                 ("in_scale", _vp), ("in_shift", _vp), ("w_chunked", _vp),
                 ("reflect_pad", C.c_int), ("y2", _vp), ("y2_stride", C.c_int), ("res2", _vp),
-                ("res2_stride", C.c_int), ("w_q8_0", _vp)]
+                ("res2_stride", C.c_int), ("w_q8_0", _vp), ("seg_sum", _vp), ("seg_len", C.c_int)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
@@ -157,7 +157,7 @@ _SIGS = {
     "vdk_bn_act": (C.c_int, [_vp, C.c_int, C.c_long, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, _vp]),
     "vdk_segment_sums": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_cam_local": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int,
-                                _vp, _vp, _vp, _vp, _vp, C.c_int, _vp]),
+                                _vp, _vp, _vp, _vp, _vp, C.c_int, _vp, _vp, _vp]),
     "vdk_cam_context": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int,
                                   _vp, _vp]),
 }
@@ -202,8 +202,8 @@ class DeviceBuffer:
     @classmethod
     def from_array(cls, a):
         a = np.ascontiguousarray(a)
-        if a.dtype not in (np.float32, np.float16, np.int32, np.uint16, np.int8, np.uint8):
-            raise TypeError(f"DeviceBuffer.from_array: unexpected dtype {a.dtype} (kernels take f32/f16/int)")
+        if a.dtype not in (np.float32, np.float16, np.float64, np.int32, np.uint16, np.int8, np.uint8):
+            raise TypeError(f"DeviceBuffer.from_array: unexpected dtype {a.dtype} (kernels take f64/f32/f16/int)")
         d = cls(a.nbytes)
         _ok(lib().vdk_memcpy_h2d(d.ptr, a.ctypes.data, a.nbytes))
         return d
