@@ -375,6 +375,46 @@ def test_conv_q8_0_weights_dequantised_in_registers(IC, OC, npix, prologue):
     assert ok, (ratio, rel)
 
 
+@pytest.mark.parametrize("IC,OC,npix", [(320, 128, 15968), (128, 128, 15968), (512, 128, 1000), (96, 32, 777)])
+def test_conv_input_prologue_every_tile_bitwise(IC, OC, npix):
+    """1x1 convs with the BN+ReLU input prologue relu(x * in_scale +
+    in_shift): every tile that takes the shape (register-staged: applied on
+    the operand loads; LDS-DMA: applied to the B fragments leaving LDS) gives
+    the same bits, and the oracle's conv of the prologued input agrees."""
+    L = lib.lib()
+    rng = np.random.default_rng(3 * IC + OC + npix)
+    announce(f"prologue 1x1 IC={IC} OC={OC} npix={npix}")
+    x = rng.standard_normal((1, 1, npix, IC)).astype(np.float16)
+    w = (rng.standard_normal((OC, IC)) * np.sqrt(2.0 / IC)).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, OC).astype(np.float32)
+    sc = rng.uniform(0.5, 1.5, IC).astype(np.float32)
+    sh = rng.uniform(-0.5, 0.5, IC).astype(np.float32)
+    dx, dw, db, dsc, dsh = (lib.DeviceBuffer.from_array(a) for a in (x, w, b, sc, sh))
+    outs = {}
+    for t in range(L.vdk_conv2d_tile_count()):
+        d = lib.ConvDesc()
+        d.x, d.batch, d.H, d.W, d.IC = dx.ptr, 1, 1, npix, IC
+        d.w, d.OC, d.KH, d.KW = dw.ptr, OC, 1, 1
+        d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+        d.bias, d.act = db.ptr, lib.ACT_RELU
+        d.in_scale, d.in_shift = dsc.ptr, dsh.ptr
+        if not L.vdk_conv2d_tile_fits_ex(t, d):
+            continue
+        dy = lib.DeviceBuffer(npix * OC * 2)
+        d.y, d.tile = dy.ptr, t
+        lib.check(L.vdk_conv2d_ex(d, None))
+        lib.check(L.vdk_synchronize())
+        outs[t] = dy.to_array(np.float16, (npix, OC))
+    assert any(t < 14 for t in outs) and any(14 <= t < 62 for t in outs)
+    ref_t = min(outs)
+    for t, o in outs.items():
+        assert np.array_equal(o.view(np.uint16), outs[ref_t].view(np.uint16)), f"tile {t} vs {ref_t}"
+    xin = np.maximum(x[0, 0].astype(np.float32) * sc + sh, 0).astype(np.float16).astype(np.float32)
+    ref = np.maximum(xin @ w.astype(np.float32).T + b, 0)
+    ok, ratio, rel = close_report(outs[ref_t].astype(np.float32), ref, CONV_RTOL, CONV_ATOL_RMS)
+    assert ok, (ratio, rel)
+
+
 @pytest.mark.parametrize("B,H,W,OC,split", [(64, 80, 298, 32, 0), (3, 7, 37, 64, 0), (2, 9, 33, 32, 1),
                                            (2, 5, 31, 16, 0), (1, 80, 1998, 32, 1)])
 def test_stem_conv_matches_oracle(B, H, W, OC, split):

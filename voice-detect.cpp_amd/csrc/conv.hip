@@ -525,6 +525,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
 //    lane picks the global chunk that belongs in its slot.
 //  * Two LDS stages; chunk k+1 is in flight while chunk k feeds the MFMAs; one
 //    barrier per chunk.
+//  * PRO: the input prologue relu(x * in_scale + in_shift) (1x1 convs without
+//    padding) applied to each B fragment as it leaves LDS, with the scale /
+//    shift vectors staged in LDS once; rounded to f16 like the register-staged
+//    kernel's, so both give the same operands.
 // ---------------------------------------------------------------------------
 
 
@@ -553,7 +557,7 @@ __device__ __forceinline__ void wait_vmcnt_le(int n) {
     }
 }
 
-template <int BM, int BN, int WM, int WN, int KC, int NST>
+template <int BM, int BN, int WM, int WN, int KC, int NST, bool PRO = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(ConvArgs a) {
     constexpr int NWM = BM / WM, NWN = BN / WN, NW = NWM * NWN;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -569,7 +573,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     static_assert(NST >= 2 && IPW * (NST - 2) <= 60, "vmcnt range");
     constexpr int SMEM_E = WN * (BM + 4) * 4;   // one epilogue pass of a wave's pixel columns
     constexpr int SMEM = NST * STAGE > SMEM_E ? NST * STAGE : SMEM_E;
+    constexpr int PRO_MAX = 1024;               // input channels with a staged prologue
     __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+    __shared__ __attribute__((aligned(16))) float s_in[PRO ? 2 * PRO_MAX : 4];   // in_scale | in_shift
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -698,6 +704,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
 #pragma unroll
     for (int k = 0; k < NST - 1; ++k)
         if (k < nk) issue(k);
+    if constexpr (PRO) {   // 1x1: chunk k covers input channels k*KC .. (conv_impl: IC <= PRO_MAX)
+        for (int c = tid; c < a.IC; c += NW * 64) {
+            s_in[c] = a.in_scale[c];
+            s_in[PRO_MAX + c] = a.in_shift[c];
+        }
+        __syncthreads();
+    }
     int st = 0;
     for (int k = 0; k < nk; ++k) {
         // chunk k has landed once at most (NST-2) younger chunks are outstanding
@@ -726,6 +739,20 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
                 const int r = wn * WN + j * 32 + lrow;
                 bf[j] = *reinterpret_cast<const half8*>(sb + r * RB + swz<KC>(r + BM, c) * 16);
             }
+            if constexpr (PRO) {   // BatchNorm + ReLU of the input channels, as the f16 operand
+                const int ch = k * KC + c * 8;
+                const float4v sc0 = *reinterpret_cast<const float4v*>(s_in + ch);
+                const float4v sc1 = *reinterpret_cast<const float4v*>(s_in + ch + 4);
+                const float4v sh0 = *reinterpret_cast<const float4v*>(s_in + PRO_MAX + ch);
+                const float4v sh1 = *reinterpret_cast<const float4v*>(s_in + PRO_MAX + ch + 4);
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        bf[j][e] = (half_t)fmaxf((float)bf[j][e] * sc0[e] + sh0[e], 0.0f);
+                        bf[j][e + 4] = (half_t)fmaxf((float)bf[j][e + 4] * sc1[e] + sh1[e], 0.0f);
+                    }
+            }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -742,7 +769,10 @@ template <int BM, int BN, int WM, int WN, int KC, int NST>
 void launch_dma(const ConvArgs& a, hipStream_t s) {
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
     dim3 grid(cdiv(a.npix, BN), cdiv(a.OC, BM));
-    hipLaunchKernelGGL((conv_dma_kernel<BM, BN, WM, WN, KC, NST>), grid, dim3(NT), 0, s, a);
+    if (a.in_scale)
+        hipLaunchKernelGGL((conv_dma_kernel<BM, BN, WM, WN, KC, NST, true>), grid, dim3(NT), 0, s, a);
+    else
+        hipLaunchKernelGGL((conv_dma_kernel<BM, BN, WM, WN, KC, NST>), grid, dim3(NT), 0, s, a);
 }
 
 // ---------------------------------------------------------------------------
@@ -2163,7 +2193,8 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
     // the input prologue lives in the register-staged kernel's operand loads
-    if (a.in_scale && !igemm_tile(idx)) return false;
+    // and the LDS-DMA kernel's B fragments (up to 1024 input channels)
+    if (a.in_scale && (t.halo || t.rw_ic || t.band_w || (!igemm_tile(idx) && a.IC > 1024))) return false;
     // reflect padding lives in the LDS-DMA kernel's pixel offsets
     if (a.reflect && (igemm_tile(idx) || t.halo)) return false;
     // q8_0 weights are dequantised in the register-staged kernel's weight loads
@@ -2205,7 +2236,8 @@ int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
-    if (a.in_scale) {   // register-staged kernel only; 64x64 tiles for a few ten thousand pixels
+    if (a.in_scale) {   // 64x64 register-staged tiles for a few ten thousand pixels (CAM++'s
+        // linear1: the LDS-DMA tiles, faster in isolation, measured slower in the model)
         if (a.IC % 32 == 0) return bm >= 64 ? (a.npix < 32768 ? 63 : (bm == 128 ? 5 : 2)) : 10;
         return bm == 128 ? 13 : (bm == 64 ? 12 : 11);
     }
