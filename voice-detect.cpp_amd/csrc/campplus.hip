@@ -161,7 +161,10 @@ __host__ __device__ inline CamLocalLds cam_local_lds(int C, int seg, int dil, in
     return L;
 }
 
-__global__ __launch_bounds__(256) void cam_local_kernel(const half_t* __restrict__ x, int xs, int T, int C, int seg,
+// CT > 0: the channel count fixed at compile time (the K loop of step 3
+// unrolls, so its LDS reads run ahead of the MFMAs); 0: C at run time.
+template <int CT>
+__global__ __launch_bounds__(256) void cam_local_kernel(const half_t* __restrict__ x, int xs, int T, int Cr, int seg,
                                                         int dil, const float* __restrict__ w1,
                                                         const float* __restrict__ b1, int H1,
                                                         const float* __restrict__ w2, const float* __restrict__ b2,
@@ -170,6 +173,7 @@ __global__ __launch_bounds__(256) void cam_local_kernel(const half_t* __restrict
                                                         const double* __restrict__ segsum,
                                                         double* __restrict__ zero_next) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+    const int C = CT > 0 ? CT : Cr;
     const CamLocalLds Lo = cam_local_lds(C, seg, dil, H1);
     uint8_t* const sx = smem + Lo.x_off;
     uint8_t* const sw = smem + Lo.w_off;
@@ -284,11 +288,24 @@ __global__ __launch_bounds__(256) void cam_local_kernel(const half_t* __restrict
         float16v acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-        for (int ks = 0; ks < nks; ++ks) {
-            const int k = ks * 16 + kg * 8, tap = k / C, ic = k - tap * C;
-            const half8 af = *reinterpret_cast<const half8*>(sw + j * Lo.wrow + k * 2);
-            const half8 bf = *reinterpret_cast<const half8*>(sx + (rb + tap * dil) * Lo.xrow + ic * 2);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc, 0, 0, 0);
+        if constexpr (CT > 0) {
+            constexpr int NKS = 3 * CT / 16;
+            const uint8_t* const wrow = sw + j * Lo.wrow + kg * 16;
+            const uint8_t* const xrow = sx + rb * Lo.xrow + kg * 16;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const int tap = (ks * 16) / CT, ic = ks * 16 - tap * CT;
+                const half8 af = *reinterpret_cast<const half8*>(wrow + ks * 32);
+                const half8 bf = *reinterpret_cast<const half8*>(xrow + tap * dil * Lo.xrow + ic * 2);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc, 0, 0, 0);
+            }
+        } else {
+            for (int ks = 0; ks < nks; ++ks) {
+                const int k = ks * 16 + kg * 8, tap = k / C, ic = k - tap * C;
+                const half8 af = *reinterpret_cast<const half8*>(sw + j * Lo.wrow + k * 2);
+                const half8 bf = *reinterpret_cast<const half8*>(sx + (rb + tap * dil) * Lo.xrow + ic * 2);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc, 0, 0, 0);
+            }
         }
         if (t < t1) {
             half_t* yr = y + ((size_t)b * T + t) * ys;
@@ -374,10 +391,10 @@ extern "C" int vdk_cam_local(const void* d_x, int x_stride, int batch, int T, in
         const size_t smem = (size_t)cam_local_lds(C, seg, dil, H1).total;
         require(smem <= 160 * 1024, "cam_local: the segment tile and context buffers exceed the workgroup's LDS");
         require(!d_zero_next || d_segsum, "cam_local: zero_next goes with segsum");
+        auto kern = C == 128 ? cam_local_kernel<128> : cam_local_kernel<0>;
         if (smem > 64 * 1024)
-            VDK_HIP(hipFuncSetAttribute((const void*)cam_local_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        (int)smem));
-        hipLaunchKernelGGL(cam_local_kernel, dim3(batch, nseg), dim3(256), smem, static_cast<hipStream_t>(stream),
+            VDK_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        hipLaunchKernelGGL(kern, dim3(batch, nseg), dim3(256), smem, static_cast<hipStream_t>(stream),
                            static_cast<const half_t*>(d_x), x_stride, T, C, seg, dil, d_w1, d_b1, H1, d_w2, d_b2,
                            static_cast<const half_t*>(d_wl), d_bl, static_cast<half_t*>(d_y), y_stride, d_segsum,
                            d_zero_next);
