@@ -244,12 +244,21 @@ void Model::encode_campplus(int batch, int T) {
         const int Ho = (H - 1) / stride + 1;
         const Layer& c1 = m.fcm[li++];
         const Layer& c2 = m.fcm[li++];
-        fconv("campp_fcm_conv1", c1, w.fcm[cur], H, stride, 1, nullptr, 1, w.fcm[o1]);
         if (stride != 1) {
+            fconv("campp_fcm_conv1", c1, w.fcm[cur], H, stride, 1, nullptr, 1, w.fcm[o1]);
             const Layer& sc = m.fcm[li++];
             fconv("campp_fcm_shortcut", sc, w.fcm[cur], H, stride, 0, nullptr, 0, w.fcm[o2]);
             fconv("campp_fcm_conv2", c2, w.fcm[o1], Ho, 1, 1, w.fcm[o2], 1, w.fcm[cur]);
+        } else if (c1.ic == 32 && c1.oc == 32 && c2.oc == 32 && c1.kh == 3 && c1.k == 3 && c2.kh == 3 && c2.k == 3) {
+            // the identity block as one fused launch (conv1 -> ReLU -> conv2 -> + x -> ReLU,
+            // the intermediate kept on chip; the same bits as the two convs)
+            prof_begin("campp_fcm_block", 2.0 * 2 * 9 * 32 * 32 * (double)batch * H * T,
+                       2.0 * 2 * 32 * (double)batch * H * T);
+            check_rc(vdk_resblock3x3(w.fcm[cur], batch, H, T, 32, c1.w, c1.b, c2.w, c2.b, w.fcm[o2], stream_));
+            prof_end();
+            cur = o2;
         } else {
+            fconv("campp_fcm_conv1", c1, w.fcm[cur], H, stride, 1, nullptr, 1, w.fcm[o1]);
             fconv("campp_fcm_conv2", c2, w.fcm[o1], Ho, 1, 1, w.fcm[cur], 1, w.fcm[o2]);
             cur = o2;
         }
