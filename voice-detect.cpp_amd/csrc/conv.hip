@@ -319,7 +319,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
     // two LDS stages: chunk k is read from stage k&1 while chunk k+1 is written to the other
     constexpr int SMEM_K = 2 * (BM + BN) * LDK * 2, SMEM_E = WN * (BM + 4) * 4;   // K stages / epilogue pass
     constexpr int SMEM = SMEM_K > SMEM_E ? SMEM_K : SMEM_E;
+    constexpr int PRO_MAX = 1024;         // input channels whose prologue scale / shift stage in LDS
     __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
+    __shared__ __attribute__((aligned(16))) float s_pro[PRO ? 2 * PRO_MAX : 4];   // in_scale | in_shift
     half_t (*sW)[BM * LDK] = reinterpret_cast<half_t (*)[BM * LDK]>(smem);
     half_t (*sX)[BN * LDK] = reinterpret_cast<half_t (*)[BN * LDK]>(smem + 2 * BM * LDK * 2);
 
@@ -381,8 +383,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
     // of registers.  Otherwise one slot (chunk k+1 in flight), which keeps
     // the register count, and so the residency, of the short-K convs.
     half8 xr[2][XCH], wr[2][WCH];
-    constexpr int XP = PRO ? XCH : 1;
-    float4v isc[2][XP][2], ish[2][XP][2];   // input prologue scale / shift of the slot's channels
     auto fetch = [&](int k, auto slot) {
         constexpr int s = decltype(slot)::value;
         const int tap = k / nc, c0 = (k - tap * nc) * KC;
@@ -420,16 +420,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
             const uint32_t off =
                 in ? (uint32_t)((((size_t)(x_img[i] + ih) * a.W + iw) * a.xs + c0 + x_c[i]) * 2) : kOOB;
             xr[s][i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
-            if constexpr (PRO) {   // 1x1 unpadded only (conv_impl): every fetched value is a real input
-                const int cc = c0 + x_c[i];
-                isc[s][i][0] = *reinterpret_cast<const float4v*>(a.in_scale + cc);
-                isc[s][i][1] = *reinterpret_cast<const float4v*>(a.in_scale + cc + 4);
-                ish[s][i][0] = *reinterpret_cast<const float4v*>(a.in_shift + cc);
-                ish[s][i][1] = *reinterpret_cast<const float4v*>(a.in_shift + cc + 4);
-            }
         }
     };
-    auto stash = [&](int st, auto slot) {
+    // the prologue's scale / shift of chunk k's channels come from LDS (1x1
+    // unpadded only, conv_impl: every fetched value is a real input)
+    auto stash = [&](int st, auto slot, int k) {
         constexpr int s = decltype(slot)::value;
 #pragma unroll
         for (int i = 0; i < WCH; ++i)
@@ -438,10 +433,15 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         for (int i = 0; i < XCH; ++i) {
             half8 v = xr[s][i];
             if constexpr (PRO) {   // BatchNorm + ReLU of the input channels, as the f16 operand
+                const int cc = k * KC + x_c[i];
+                const float4v sc0 = *reinterpret_cast<const float4v*>(s_pro + cc);
+                const float4v sc1 = *reinterpret_cast<const float4v*>(s_pro + cc + 4);
+                const float4v sh0 = *reinterpret_cast<const float4v*>(s_pro + PRO_MAX + cc);
+                const float4v sh1 = *reinterpret_cast<const float4v*>(s_pro + PRO_MAX + cc + 4);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    v[e] = (half_t)fmaxf((float)v[e] * isc[s][i][0][e] + ish[s][i][0][e], 0.0f);
-                    v[e + 4] = (half_t)fmaxf((float)v[e + 4] * isc[s][i][1][e] + ish[s][i][1][e], 0.0f);
+                    v[e] = (half_t)fmaxf((float)v[e] * sc0[e] + sh0[e], 0.0f);
+                    v[e + 4] = (half_t)fmaxf((float)v[e + 4] * sc1[e] + sh1[e], 0.0f);
                 }
             }
             if (x_row[i]) *reinterpret_cast<half8*>(&sX[st][x_lds[i]]) = v;
@@ -484,12 +484,17 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
             // chunk is fetched again (unused) to keep the load count fixed
             fetch(k + 2 < nk ? k + 2 : nk - 1, slot);
             mfma_chunk(s);
-            if (k + 1 < nk) stash(s ^ 1, std::integral_constant<int, s ^ 1>());
+            if (k + 1 < nk) stash(s ^ 1, std::integral_constant<int, s ^ 1>(), k + 1);
             __syncthreads();
         };
         fetch(0, S0());
         fetch(nk > 1 ? 1 : 0, S1());
-        stash(0, S0());
+        for (int c = tid; c < a.IC; c += NT) {
+            s_pro[c] = a.in_scale[c];
+            s_pro[PRO_MAX + c] = a.in_shift[c];
+        }
+        __syncthreads();
+        stash(0, S0(), 0);
         __syncthreads();
         for (int k = 0; k < nk; k += 2) {
             step(k, S0());
@@ -498,13 +503,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_igemm_kernel(
         }
     } else {
         fetch(0, S0());
-        stash(0, S0());
+        stash(0, S0(), 0);
         __syncthreads();
         for (int k = 0; k < nk; ++k) {
             const int st = k & 1;
             if (k + 1 < nk) fetch(k + 1, S0());   // global loads in flight during this chunk's MFMAs
             mfma_chunk(st);
-            if (k + 1 < nk) stash(st ^ 1, S0());
+            if (k + 1 < nk) stash(st ^ 1, S0(), k + 1);
             __syncthreads();
         }
     }
@@ -2193,8 +2198,9 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
     if (t.halo && !is_s1_3x3(a)) return false;
     // the input prologue lives in the register-staged kernel's operand loads
-    // and the LDS-DMA kernel's B fragments (up to 1024 input channels)
-    if (a.in_scale && (t.halo || t.rw_ic || t.band_w || (!igemm_tile(idx) && a.IC > 1024))) return false;
+    // and the LDS-DMA kernel's B fragments (up to 1024 input channels: their
+    // scale / shift stage in LDS)
+    if (a.in_scale && (t.halo || t.rw_ic || t.band_w || a.IC > 1024)) return false;
     // reflect padding lives in the LDS-DMA kernel's pixel offsets
     if (a.reflect && (igemm_tile(idx) || t.halo)) return false;
     // q8_0 weights are dequantised in the register-staged kernel's weight loads
