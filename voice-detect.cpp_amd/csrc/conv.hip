@@ -2242,8 +2242,11 @@ int pick_tile(const ConvArgs& a) {
     const int o = tile_override();
     if (o >= 0 && o < kNumTiles && tile_fits(kTiles[o], a)) return o;
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
-    if (a.in_scale) {   // 64x64 register-staged tiles for a few ten thousand pixels (CAM++'s
-        // linear1: the LDS-DMA tiles, faster in isolation, measured slower in the model)
+    if (a.in_scale) {   // register-staged tiles for a few ten thousand pixels (CAM++'s
+        // linear1: the LDS-DMA tiles, faster in isolation, measured slower in the model):
+        // 64-channel chunks on the 128x64 tile from 256 input channels (half the
+        // chunk steps, each a load round trip), else the 64x64 tile
+        if (a.IC >= 256 && a.IC % 64 == 0 && a.OC == 128 && a.npix < 65536 && tile_fits(kTiles[6], a)) return 6;
         if (a.IC % 32 == 0) return bm >= 64 ? (a.npix < 32768 ? 63 : (bm == 128 ? 5 : 2)) : 10;
         return bm == 128 ? 13 : (bm == 64 ? 12 : 11);
     }
