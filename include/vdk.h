@@ -119,6 +119,9 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * and the GEMM runs x_hi.w_hi + x_lo.w_hi + x_hi.w_lo on f16 MFMA (3x the
  * work); split = 2, for weights that f16 holds exactly (lo = 0): w is
  * [OC][KH][KW][2*IC] = [hi | hi] and the GEMM runs x_hi.w + x_lo.w (2x).
+ * Split needs IC % 32 == 0, or IC = 16 with split = 2 (16 output channels,
+ * 3x3 stride 1: the split-f16 register-weight kernel); a w_chunked copy of
+ * split weights re-orders the [OC][KH][KW][terms*IC] array.
  * reflect_pad != 0 (1-D convs, KH = 1): the time axis is padded by reflection
  * without repeating the edge sample (x[-i] = x[i], x[W-1+i] = x[W-1-i],
  * SpeechBrain's padding, src/encoder.cpp:32-52) instead of with zeros; pad_w
@@ -138,6 +141,14 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * an f16, so the f64 sums are exact and independent of the order they are
  * added in (CAM++'s context pooling, src/encoder_campplus.cpp:159-170).
  * Register-staged tiles (f16 weights) whose pixel tile is at most seg_len wide.
+ * x_group_stride / y_group_stride (0: 16, channels contiguous): split-f16
+ * tensors stored in 16-channel groups, channel c of the hi plane at element
+ * (c / 16) * group_stride + c % 16 of its pixel row (the lo plane x_lo / y_lo
+ * after it), e.g. group_stride = 32 with x_lo = 16 keeps each group's hi and
+ * lo halves as one 64-byte piece ([hi 16 | lo 16]), so 16-channel slices are
+ * read and written as whole 64-byte blocks (narrower writes cost a
+ * read-modify-write in HBM).  IC and OC % 16 == 0; the LDS-DMA and split-f16
+ * register-weight kernels.
  * tile = -1 picks the kernel automatically. */
 typedef struct {
     const void* x; int batch, H, W, IC, x_stride;
@@ -160,6 +171,7 @@ typedef struct {
     const void* res2; int res2_stride;
     const void* w_q8_0;
     double* seg_sum; int seg_len;
+    int x_group_stride, y_group_stride;
 } vdk_conv_desc;
 /* Host: re-order f16 conv weights [OC][KH][KW][IC] (IC % 16 == 0) into the
  * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */

@@ -241,6 +241,165 @@ def test_split_f16_conv_is_f32_accurate(terms, IC, OC, tile):
             assert err <= 2e-6
 
 
+@pytest.mark.parametrize("IC,OC,tile,ref_tile", [(32, 16, 70, 27), (16, 16, 71, None), (32, 32, 72, 27),
+                                                 (64, 32, 73, 28), (64, 32, 74, 28), (64, 64, 75, 30)])
+def test_split_register_weight_3x3(IC, OC, tile, ref_tile):
+    """The split-f16 register-weight 3x3 kernel on channel slices of the Res2Net
+    [chunk0 | chunk1 | sp0 | sp1] layout (pixel rows [hi S | lo S]) on a 42 x 300
+    map (partial last row tile and 32-column tile), bias + ReLU + clamp.  Against the f64 brute force (<= 2e-6 of the max,
+    split-f16's accuracy) and the halo kernel: bit for bit for the 32x32 MFMA
+    tiles (same MFMA order), to f32 rounding for the 16x16x32 ones; channels
+    outside the output slice keep their bytes."""
+    rng = np.random.default_rng(700 + IC + OC + tile)
+    Bt, H, T = 2, 42, 300
+    S = 256                                      # channels per plane of a pixel row
+    cin, cout = 16, 128                          # input / output slice offsets (disjoint slices)
+    announce(f"eres split register-weight 3x3 B={Bt} H={H} T={T} IC={IC} OC={OC} tile={tile} ref={ref_tile}")
+    x = (rng.standard_normal((Bt, H, T, IC)).astype(np.float32) * 3)
+    xh, xl = _split(x)
+    buf = rng.standard_normal((Bt, H, T, 2 * S)).astype(np.float16)
+    buf[..., cin:cin + IC] = xh
+    buf[..., S + cin:S + cin + IC] = xl
+    w = (rng.standard_normal((OC, IC, 3, 3)) * np.sqrt(2.0 / (IC * 9))).astype(np.float16).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, OC).astype(np.float32)
+    wh = w.transpose(0, 2, 3, 1).astype(np.float16)
+    wpack = np.ascontiguousarray(np.concatenate([wh, wh], axis=3))
+    wch = np.zeros_like(wpack)
+    lib.lib().vdk_conv_pack_chunked(wpack.ctypes.data, OC, 3, 3, 2 * IC, wch.ctypes.data)
+    keep = [lib.DeviceBuffer.from_array(wpack), lib.DeviceBuffer.from_array(wch), lib.DeviceBuffer.from_array(b)]
+
+    def run(t, chunked):
+        d4 = lib.DeviceBuffer.from_array(buf)
+        d = lib.ConvDesc()
+        d.x, d.batch, d.H, d.W, d.IC, d.x_stride = d4.ptr + cin * 2, Bt, H, T, IC, 2 * S
+        d.w, d.OC, d.KH, d.KW = keep[0].ptr, OC, 3, 3
+        d.w_chunked = keep[1].ptr if chunked else None
+        d.stride_h = d.stride_w = 1
+        d.pad_h = d.pad_w = 1
+        d.dil_h = d.dil_w = 1
+        d.bias = keep[2].ptr
+        d.act, d.clamp_hi = lib.ACT_RELU, 20.0
+        d.y, d.y_stride = d4.ptr + cout * 2, 2 * S
+        d.split, d.x_lo, d.y_lo = 2, S, S
+        d.tile = t
+        lib.check(lib.lib().vdk_conv2d_ex(d, None))
+        lib.check(lib.lib().vdk_synchronize())
+        return d4.to_array(np.float16, (Bt, H, T, 2 * S))
+
+    out = run(tile, True)
+    assert np.array_equal(run(tile, False), out)             # the weight copy changes nothing
+    keepmask = np.ones(2 * S, bool)
+    keepmask[cout:cout + OC] = keepmask[S + cout:S + cout + OC] = False
+    assert np.array_equal(out[..., keepmask], buf[..., keepmask])
+    got = out[..., cout:cout + OC].astype(np.float64) + out[..., S + cout:S + cout + OC].astype(np.float64)
+    if ref_tile is not None:
+        ref = run(ref_tile, False)
+        rsum = ref[..., cout:cout + OC].astype(np.float64) + ref[..., S + cout:S + cout + OC].astype(np.float64)
+        if tile in (72, 74, 75):
+            assert np.array_equal(out, ref)
+        else:
+            assert np.abs(got - rsum).max() <= 1e-6 * np.abs(rsum).max()
+    for c in (0, Bt - 1):
+        want = O.conv2d_g(x[c].transpose(2, 0, 1), w, sh=1, sw=1, ph=1, pw=1, bias=b, f64=True)
+        want = np.clip(want, 0.0, 20.0)
+        err = np.abs(got[c].transpose(2, 0, 1) - want).max() / np.abs(want).max()
+        announce(f"split register-weight 3x3 clip {c}: max err / max {err:.2e}")
+        assert err <= 2e-6
+
+
+def _grouped(vals, groups):
+    """f32 [.., 16 * n] -> f16 rows of `groups` 16-channel groups [hi 16 | lo 16]."""
+    hi, lo = _split(vals)
+    out = np.zeros(vals.shape[:-1] + (32 * groups,), np.float16)
+    for k in range(vals.shape[-1] // 16):
+        out[..., 32 * k:32 * k + 16] = hi[..., 16 * k:16 * k + 16]
+        out[..., 32 * k + 16:32 * k + 32] = lo[..., 16 * k:16 * k + 16]
+    return out
+
+
+def _ungroup(rows, g0, n):
+    """The split values of groups g0 .. g0+n of grouped rows, as f64."""
+    parts = [rows[..., 32 * k:32 * k + 16].astype(np.float64) + rows[..., 32 * k + 16:32 * k + 32].astype(np.float64)
+             for k in range(g0, g0 + n)]
+    return np.concatenate(parts, axis=-1)
+
+
+@pytest.mark.parametrize("case", ["3x3_32_16", "3x3_16_16", "1x1_32_64_res", "1x1_64_32"])
+def test_split_grouped_layout(case):
+    """Split-f16 tensors stored as 16-channel groups [hi 16 | lo 16] (group stride
+    32, lo offset 16: layer 1's Res2Net chunks as whole 64-byte pieces): the
+    3x3 group convs on the split register-weight kernel and the LDS-DMA kernel,
+    and the 1x1 convs around them (grouped input with a contiguous split
+    residual; contiguous input into grouped output) on the LDS-DMA kernel,
+    against the f64 brute force; bytes outside the output groups keep their
+    values."""
+    rng = np.random.default_rng(880 + len(case))
+    Bt, H, T, G = 2, 42, 300, 4                           # 4 groups = 64 channels per pixel row
+    K, IC, OC = (3, 32, 16) if case == "3x3_32_16" else (3, 16, 16) if case == "3x3_16_16" else \
+        (1, 32, 64) if case == "1x1_32_64_res" else (1, 64, 32)
+    announce(f"eres grouped split layout {case} B={Bt} H={H} T={T}")
+    w = (rng.standard_normal((OC, IC, K, K)) * np.sqrt(2.0 / (IC * K * K))).astype(np.float16).astype(np.float32)
+    bias = rng.uniform(-0.5, 0.5, OC).astype(np.float32)
+    wh = w.transpose(0, 2, 3, 1).astype(np.float16)
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(np.concatenate([wh, wh], axis=3))),
+            lib.DeviceBuffer.from_array(bias)]
+    x = rng.standard_normal((Bt, H, T, IC)).astype(np.float32) * 3
+    res = None
+    d = lib.ConvDesc()
+    d.batch, d.H, d.W, d.IC = Bt, H, T, IC
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, OC, K, K
+    d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+    d.pad_h = d.pad_w = K // 2
+    d.bias, d.act, d.clamp_hi, d.split = keep[1].ptr, lib.ACT_RELU, 20.0, 2
+    if K == 3 or case == "1x1_32_64_res":                 # grouped input from group 1, grouped / contiguous out
+        rows = rng.standard_normal((Bt, H, T, 32 * G)).astype(np.float16)
+        rows[..., 32:32 + 2 * IC] = _grouped(x, IC // 16)
+        din = lib.DeviceBuffer.from_array(rows)
+        d.x, d.x_stride, d.x_lo, d.x_group_stride = din.ptr + 32 * 2, 32 * G, 16, 32
+    else:
+        din = lib.DeviceBuffer.from_array(np.concatenate(_split(x), axis=3))
+        d.x, d.x_stride, d.x_lo = din.ptr, 2 * IC, IC
+    if case == "1x1_32_64_res":                            # contiguous split output and residual
+        res = rng.standard_normal((Bt, H, T, OC)).astype(np.float32) * 2
+        dres = lib.DeviceBuffer.from_array(np.concatenate(_split(res), axis=3))
+        d.residual, d.res_stride, d.res_lo = dres.ptr, 2 * OC, OC
+        yrows = np.zeros((Bt, H, T, 2 * OC), np.float16)
+        dy = lib.DeviceBuffer.from_array(yrows)
+        d.y, d.y_stride, d.y_lo = dy.ptr, 2 * OC, OC
+    else:                                                  # grouped output into group 3 (K = 3) or 1
+        g0 = 3 if K == 3 else 1
+        yrows = rows.copy() if K == 3 else rng.standard_normal((Bt, H, T, 32 * G)).astype(np.float16)
+        dy = din if K == 3 else lib.DeviceBuffer.from_array(yrows)
+        d.y, d.y_stride, d.y_lo, d.y_group_stride = dy.ptr + 32 * g0 * 2, 32 * G, 16, 32
+    tiles = {"3x3_32_16": [70, 14], "3x3_16_16": [71], "1x1_32_64_res": [-1, 16], "1x1_64_32": [-1, 14]}[case]
+    outs = []
+    for t in tiles:
+        if K == 3:
+            dy.copy_from(rows)
+        d.tile = t
+        lib.check(lib.lib().vdk_conv2d_ex(d, None))
+        lib.check(lib.lib().vdk_synchronize())
+        if case == "1x1_32_64_res":
+            o = dy.to_array(np.float16, (Bt, H, T, 2 * OC))
+            got = o[..., :OC].astype(np.float64) + o[..., OC:].astype(np.float64)
+        else:
+            o = dy.to_array(np.float16, (Bt, H, T, 32 * G))
+            got = _ungroup(o, g0, OC // 16)
+            mask = np.ones(32 * G, bool)
+            mask[32 * g0:32 * (g0 + OC // 16)] = False
+            assert np.array_equal(o[..., mask], yrows[..., mask])
+        outs.append(got)
+        for c in (0, Bt - 1):
+            want = O.conv2d_g(x[c].transpose(2, 0, 1), w, ph=K // 2, pw=K // 2, bias=bias,
+                              residual=None if res is None else res[c].transpose(2, 0, 1), f64=True)
+            want = np.clip(want, 0.0, 20.0)
+            err = np.abs(got[c].transpose(2, 0, 1) - want).max() / np.abs(want).max()
+            announce(f"grouped {case} tile {t} clip {c}: max err / max {err:.2e}")
+            assert err <= 2e-6
+    for o in outs[1:]:
+        assert np.abs(o - outs[0]).max() <= 1e-6 * np.abs(outs[0]).max()
+
+
 # ------------------------------------------------------------------ end to end
 
 @pytest.fixture(scope="module")

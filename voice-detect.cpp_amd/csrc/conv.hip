@@ -58,7 +58,11 @@ struct ConvArgs {
     const uint8_t* wq;         // 1x1 weights as q8_0 blocks [OC][IC/32] x {f16 d, 32 x int8} (register-staged kernel)
     double* segsum;            // per-(clip, segment, OC) f64 sums of the stored outputs (may be NULL)
     int seg_len, seg_n;        // output columns per segment, segments per clip
+    int xgs = 16, ygs = 16;    // elements between 16-channel groups of x / y (16: contiguous channels)
 };
+
+// Element offset of channel c (c % 8 == 0 reads / writes 8 channels of one group).
+__device__ __forceinline__ int chan_off(int c, int gs) { return (c >> 4) * gs + (c & 15); }
 
 // Epilogue for 8 consecutive output channels oc..oc+7 of pixel P (P
 // enumerates (clip, oh, ow) row-major), with every operand moved as 16-byte
@@ -135,7 +139,7 @@ __device__ __forceinline__ void store8(const ConvArgs& a, int P, int oc, const f
         const int b = P / HoWo, rem = P - b * HoWo, oh = rem / a.Wo, ow = rem - oh * a.Wo;
         Po = ((size_t)b * a.Wo + ow) * a.Ho + oh;
     }
-    const size_t o = Po * a.ys + oc;
+    const size_t o = Po * a.ys + chan_off(oc, a.ygs);
     if (a.y2) {   // f16 only, no split, no time-major store (conv_impl)
         const half8 r = *reinterpret_cast<const half8*>(a.r2 + (size_t)P * a.r2s + oc);
         half8 h2;
@@ -159,11 +163,6 @@ __device__ __forceinline__ void store8(const ConvArgs& a, int P, int oc, const f
             *reinterpret_cast<half8*>(static_cast<half_t*>(a.y) + o + a.y_lo) = l;
         }
     }
-}
-
-__device__ __forceinline__ void finish8(const ConvArgs& a, int P, int oc, float* v) {
-    epi8(a, P, oc, v);
-    store8(a, P, oc, v);
 }
 
 // The finished 32x32 MFMA blocks are staged through LDS as f32 [pixel][oc]
@@ -595,8 +594,9 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     const int nc = ICW / KC;
     const int nk = KHW * nc;
 
+    const int xext = (a.IC / 16 - 1) * a.xgs + 16;   // elements of a pixel's channels (one plane)
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC + (a.split ? a.x_lo : 0)) * 2), 0x00020000);
+        (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + xext + (a.split ? a.x_lo : 0)) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.w, 0, (int)((size_t)a.OC * KHW * ICW * 2), 0x00020000);
 
@@ -631,7 +631,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
                 const int b = P / HoWo, rem = P - b * HoWo;
                 const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
                 const int ih0 = oh * a.sh - a.ph, iw0 = ow * a.sw - a.pw;
-                s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.xs + c * 8) * 2;
+                s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.xs + chan_off(c * 8, a.xgs)) * 2;
                 s_iw[j] = iw0;
                 if (tap_range) {
                     // one row of taps: the in-image ones are kw in [lo, hi)
@@ -679,7 +679,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
             }
         }
         f_c0 += KC;
-        f_xc += KC * 2;
+        f_xc += KC / 16 * a.xgs * 2;
         if (f_c0 == ICW) {
             f_c0 = 0;
             f_xc = 0;
@@ -1514,6 +1514,320 @@ void launch_rw(const ConvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// conv3x3_split_kernel: persistent stride-1 3x3 conv (pad 1) on split-f16
+// maps (value = hi + lo, the lo plane x_lo / y_lo elements after the hi one,
+// any pixel stride) with f16-exact weights (split 2: w.x_hi + w.x_lo), for
+// ERes2Net's narrow Res2Net group convs (src/encoder_eres2net.cpp:111-137).
+// The register-weight kernel's scheme: every wave keeps the A fragments of its
+// output channels in VGPRs for the whole launch (one set serves both planes),
+// each workgroup walks a contiguous range of TH x 32 output tiles (rows
+// fastest) through an NS-stage LDS ring whose stage holds one tile's
+// (TH+2) x 34 halo as [hi IC | lo IC] pixel rows, and tile t+NS-1's DMA goes
+// out spread over tile t's MFMA steps.  Two MFMA shapes:
+//   * M16: 16x16x32 MFMAs over 16-pixel column blocks, every wave computing
+//     all OC/16 (1 or 2) row blocks of its pixel blocks; K = 32 is one plane's
+//     32-channel chunk, or at IC = 16 both planes of a tap at once;
+//   * M32: the 32x32x16 blocks of the other conv kernels in the halo kernel's
+//     order (plane, 32-channel chunk, tap, 16-channel step), so the results
+//     equal the halo kernel's bit for bit; wave groups of 32 output channels.
+// Epilogue straight from the accumulators: + bias, [ReLU [min(v, clamp_hi)]],
+// hi = f16(v), lo = f16(v - hi), 8-byte stores into both planes.
+// ---------------------------------------------------------------------------
+template <int IC, int OC, int TH, int NW, int NS, bool M16>
+struct SpTile {
+    static constexpr int kIC = IC, kOC = OC, kTH = TH, kNW = NW, kNS = NS;
+    static constexpr bool kM16 = M16;
+    static constexpr int C2 = 2 * IC;                                    // [hi | lo] channels per halo pixel
+    static constexpr int RB = PadRow<C2>::RB, SPR = PadRow<C2>::SPR;
+    static constexpr int XW = 34, XPIX = (TH + 2) * XW;
+    static constexpr int X_INS = (XPIX * SPR + 63) / 64, X_IPW = (X_INS + NW - 1) / NW;
+    static constexpr int STAGE = X_INS * 1024;
+    static constexpr int PN = M16 ? 16 : 32;                             // pixels per MFMA column block
+    static constexpr int MB = M16 ? OC / 16 : 1;                         // row blocks per wave
+    static constexpr int NWM = M16 ? 1 : OC / 32, WPM = NW / NWM;        // wave groups, waves per group
+    static constexpr int NBT = TH * (32 / PN);                           // column blocks per tile
+    static constexpr int BPW = NBT / WPM;                                // ... per wave
+    static constexpr int NFT = M16 ? (IC >= 32 ? IC / 32 : 1) : IC / 16; // A fragments per tap and row block
+    static constexpr int NF = 9 * NFT * MB;
+    static constexpr int NSTEP = M16 ? (IC == 16 ? 9 : 18 * IC / 32) : 36 * IC / 32;
+    static constexpr int NBV = M16 ? 4 * MB : 16;                        // bias registers
+    static_assert(M16 ? ((OC == 16 || OC == 32) && (IC == 16 || IC % 32 == 0)) : (OC % 32 == 0 && IC % 32 == 0),
+                  "supported widths");
+    static_assert(NWM * WPM == NW && NBT % WPM == 0 && BPW >= 1, "column blocks split evenly over the waves");
+    static_assert(NS >= 2 && NS * STAGE <= 163840, "the ring fits the 160 KB of LDS");
+};
+
+// MFMA step s: tap, element offset of its K chunk in the [hi | lo] halo row,
+// A fragment (per row block)
+struct SpStep {
+    int tap, coff, frag;
+};
+template <int IC, bool M16>
+__device__ __forceinline__ constexpr SpStep sp_step(int s) {
+    if constexpr (M16) {
+        if constexpr (IC == 16) return {s, 0, s};
+        const int pc = s / 9, tap = s - pc * 9, p = pc / (IC / 32), c = pc - p * (IC / 32);
+        return {tap, p * IC + c * 32, tap * (IC / 32) + c};
+    } else {
+        constexpr int PER = IC / 32 * 18;
+        const int p = s / PER, r = s - p * PER, c = r / 18, r2 = r - c * 18, tap = r2 / 2, kk = r2 - tap * 2;
+        return {tap, p * IC + c * 32 + kk * 16, tap * (IC / 16) + c * 2 + kk};
+    }
+}
+
+__device__ __forceinline__ float4v sp_mfma(const half8& a, const half8& b, const float4v& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float16v sp_mfma(const half8& a, const half8& b, const float16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Per-workgroup constants of the split kernel's tile walk; hpos < 0 marks a
+// padding slot.
+struct SpWalk {
+    const int* hofs; const int* hpos;
+    int4v xr;
+    int tiles_w, tiles_h, per_tile, H, W, xs2;
+};
+
+// This wave's DMA instructions for tile t's halo into stage st, instruction j
+// issued after MFMA step j * SP of the tile before it.
+template <class G>
+struct SpSide {
+    static constexpr int NI = G::X_IPW, SP = G::NSTEP / NI > 0 ? G::NSTEP / NI : 1;
+    static_assert(NI * SP <= G::NSTEP, "every instruction has a step");
+    uint8_t* st;
+    const SpWalk* k;
+    int oh0, ow0, xo, wave;
+    bool on;
+    __device__ __forceinline__ SpSide(uint8_t* st_, const SpWalk& k_, int t, int wave_, bool on_)
+        : st(st_), k(&k_), wave(wave_), on(on_) {
+        const int th = t % k_.tiles_h, r = t / k_.tiles_h, tw = r % k_.tiles_w;
+        const int b = r / k_.tiles_w;
+        oh0 = th * G::kTH;
+        ow0 = tw * 32;
+        xo = ((b * k_.H + oh0 - 1) * k_.W + ow0 - 1) * k_.xs2;
+    }
+    __device__ __forceinline__ void operator()(int s) const {
+        if (s % SP != 0 || !on) return;
+        const int j = s / SP;
+        if (j >= NI) return;
+        const int ins = wave + j * G::kNW;
+        if (ins >= G::X_INS) return;
+        const int hp = k->hpos[j];
+        const int ih = oh0 - 1 + (hp >> 8), iw = ow0 - 1 + (hp & 255);
+        const uint32_t off = (hp >= 0 && (unsigned)ih < (unsigned)k->H && (unsigned)iw < (unsigned)k->W)
+                                 ? (uint32_t)(xo + k->hofs[j]) : kOOB;
+        dma16(st + ins * 1024, k->xr, off);
+    }
+};
+
+template <class G>
+__device__ __forceinline__ void sp_issue(uint8_t* st, const SpWalk& k, int t, int wave) {
+    const SpSide<G> side(st, k, t, wave, true);
+#pragma unroll
+    for (int j = 0; j < SpSide<G>::NI; ++j) side(j * SpSide<G>::SP);
+}
+
+// The convolution of one tile from stage st: the B reads run PD steps ahead
+// of the MFMAs; side(s) after step s.
+template <class G, class Acc, class Side>
+__device__ __forceinline__ void sp_conv(const half8* wf, const uint8_t* st, int wr, int lane,
+                                        Acc (&acc)[G::BPW][G::MB], const Side& side) {
+    constexpr int PD = 3, BPW = G::BPW, MB = G::MB;
+    static_assert(PD < G::NSTEP, "prefetch distance within the step count");
+    const int lp = lane % G::PN, kg = lane / G::PN;
+    const uint8_t* const base = st + lp * G::RB + kg * 16;
+    int boff[BPW];
+#pragma unroll
+    for (int q = 0; q < BPW; ++q) {
+        const int j = wr + q * G::WPM;
+        const int i = G::PN == 16 ? j >> 1 : j, cb = G::PN == 16 ? (j & 1) : 0;
+        boff[q] = (i * G::XW + cb * G::PN) * G::RB;
+    }
+    auto load = [&](int s, half8* dst) {
+        const SpStep si = sp_step<G::kIC, G::kM16>(s);
+        const int kh = si.tap / 3, kw = si.tap - kh * 3;
+#pragma unroll
+        for (int q = 0; q < BPW; ++q)
+            dst[q] = *reinterpret_cast<const half8*>(base + boff[q] + (kh * G::XW + kw) * G::RB + si.coff * 2);
+    };
+    half8 ring[PD][BPW];
+#pragma unroll
+    for (int s = 0; s < PD; ++s) load(s, ring[s]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < G::NSTEP; ++s) {
+        half8 cur[BPW];
+#pragma unroll
+        for (int q = 0; q < BPW; ++q) cur[q] = ring[s % PD][q];
+        if (s + PD < G::NSTEP) load(s + PD, ring[s % PD]);
+        __builtin_amdgcn_sched_barrier(0);
+        const int f = sp_step<G::kIC, G::kM16>(s).frag;
+#pragma unroll
+        for (int q = 0; q < BPW; ++q)
+#pragma unroll
+            for (int m = 0; m < MB; ++m) acc[q][m] = sp_mfma(wf[f * MB + m], cur[q], acc[q][m]);
+        side(s);
+    }
+}
+
+// Tile t from stage st while tile t+NS-1's DMA goes out into stage nst, then
+// (after tile t+1's loads have landed, see rw_tile) the epilogue.
+template <class G>
+__device__ __forceinline__ void sp_tile(const uint8_t* st, uint8_t* nst, bool prefetch, const half8* wf,
+                                        const float* bv, const SpWalk& k, int t, int younger, const ConvArgs& a,
+                                        int wave, int lane) {
+    using Acc = std::conditional_t<G::kM16, float4v, float16v>;
+    constexpr int NE = G::kM16 ? 4 : 16, NG = NE / 4;
+    const int mg = wave / G::WPM, wr = wave - mg * G::WPM;
+    const int th = t % k.tiles_h, r = t / k.tiles_h, tw = r % k.tiles_w;
+    const int b = r / k.tiles_w, oh0 = th * G::kTH, ow0 = tw * 32;
+    const SpSide<G> side(nst, k, t + G::kNS - 1, wave, prefetch);
+    Acc acc[G::BPW][G::MB];
+#pragma unroll
+    for (int q = 0; q < G::BPW; ++q)
+#pragma unroll
+        for (int m = 0; m < G::MB; ++m)
+#pragma unroll
+            for (int e = 0; e < NE; ++e) acc[q][m][e] = 0.0f;
+    sp_conv<G>(wf, st, wr, lane, acc, side);
+    wait_vmcnt_le(younger);
+
+    half_t* const y = static_cast<half_t*>(a.y);
+    const bool relu = a.act == VDK_ACT_RELU;
+    const float chi = a.clamp_hi;
+#pragma unroll
+    for (int q = 0; q < G::BPW; ++q) {
+        const int j = wr + q * G::WPM;
+        const int oh = oh0 + (G::kM16 ? j >> 1 : j);
+        const int ow = ow0 + (G::kM16 ? (j & 1) * 16 + (lane & 15) : (lane & 31));
+        if (oh >= k.H || ow >= k.W) continue;
+        half_t* const yp = y + ((size_t)(b * k.H + oh) * k.W + ow) * a.ys;
+#pragma unroll
+        for (int m = 0; m < G::MB; ++m)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                // register g*4+e: channel 16m + 4*(lane/16) + e (M16), 32mg + 8g + 4*(lane/32) + e (M32)
+                const int oc = chan_off(G::kM16 ? m * 16 + (lane >> 4) * 4 : mg * 32 + g * 8 + (lane >> 5) * 4, a.ygs);
+                half4 h, l;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v = acc[q][m][g * 4 + e] + bv[(m * NG + g) * 4 + e];
+                    if (relu) {
+                        v = fmaxf(v, 0.0f);
+                        if (chi > 0.0f) v = fminf(v, chi);
+                    }
+                    h[e] = (half_t)v;
+                    l[e] = (half_t)(v - (float)h[e]);
+                }
+                *reinterpret_cast<half4*>(yp + oc) = h;
+                *reinterpret_cast<half4*>(yp + a.y_lo + oc) = l;
+            }
+    }
+}
+
+template <int IC, int OC, int TH, int NW, int NS, bool M16>
+__global__ __launch_bounds__(NW * 64) void conv3x3_split_kernel(ConvArgs a, int ntiles, int per_wg) {
+    using G = SpTile<IC, OC, TH, NW, NS, M16>;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * G::STAGE];
+
+    const int W = a.W;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t_begin = blockIdx.x * per_wg;
+    const int t_end = t_begin + per_wg < ntiles ? t_begin + per_wg : ntiles;
+    if (t_begin >= t_end) return;   // the whole workgroup: no barrier is pending
+
+    // this lane's DMA slots (the same for every tile): byte offset from the
+    // tile origin (hi-plane slots, then lo-plane ones) and (row << 8 | column)
+    const int xs2 = a.xs * 2;
+    int hofs[G::X_IPW], hpos[G::X_IPW];
+#pragma unroll
+    for (int i = 0; i < G::X_IPW; ++i) {
+        const int p = (wave + i * NW) * 64 + lane;
+        const int r = p / G::SPR, cc = p - r * G::SPR;
+        const int hr = r / G::XW, hc = r - hr * G::XW;
+        const bool lo = cc >= IC / 8;
+        hofs[i] = (hr * W + hc) * xs2 + (lo ? a.x_lo : 0) * 2 + chan_off((lo ? cc - IC / 8 : cc) * 8, a.xgs) * 2;
+        hpos[i] = (r < G::XPIX && cc < G::C2 / 8) ? (hr << 8 | hc) : -1;
+    }
+    SpWalk k;
+    k.hofs = hofs; k.hpos = hpos;
+    k.xr = dma_rsrc(a.x, (uint32_t)(((size_t)(a.npix_in - 1) * a.xs + a.x_lo + (IC / 16 - 1) * a.xgs + 16) * 2));
+    k.H = a.H;
+    k.W = W;
+    k.xs2 = xs2;
+    k.tiles_w = (W + 31) / 32;
+    k.tiles_h = (a.H + TH - 1) / TH;
+    k.per_tile = (G::X_INS - wave + NW - 1) / NW;   // this wave's DMA instructions per tile
+
+    sp_issue<G>(ring, k, t_begin, wave);
+    // A fragments (columns of the weights' hi copy, whose second copy the lo
+    // plane uses) and biases of this wave's output channels
+    const int mg = wave / G::WPM;
+    constexpr int ICW = 2 * IC;
+    auto wfrag = [&](int oc, int tap, int col) {
+        return a.wc ? *reinterpret_cast<const half8*>(a.wc + (((size_t)(col >> 4) * 9 + tap) * OC + oc) * 16 + (col & 15))
+                    : *reinterpret_cast<const half8*>(a.w + ((size_t)oc * 9 + tap) * ICW + col);
+    };
+    half8 wf[G::NF];
+    float bv[G::NBV];
+    if constexpr (M16) {
+        const int orow = lane & 15, g = lane >> 4;
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+            for (int c = 0; c < G::NFT; ++c)
+#pragma unroll
+                for (int m = 0; m < G::MB; ++m)
+                    wf[(tap * G::NFT + c) * G::MB + m] = wfrag(m * 16 + orow, tap, c * 32 + g * 8);
+#pragma unroll
+        for (int m = 0; m < G::MB; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[m * 4 + e] = a.bias ? a.bias[m * 16 + g * 4 + e] : 0.0f;
+    } else {
+        const int orow = lane & 31, g = lane >> 5;
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap)
+#pragma unroll
+            for (int f = 0; f < IC / 16; ++f) wf[tap * (IC / 16) + f] = wfrag(mg * 32 + orow, tap, f * 16 + g * 8);
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv[gg * 4 + e] = a.bias ? a.bias[mg * 32 + gg * 8 + g * 4 + e] : 0.0f;
+    }
+    // a full wait the compiler sees, so the weights count as loaded inside
+    // the loop; the tiles after the first go out behind it
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int s = 1; s + 1 < NS; ++s)
+        if (t_begin + s < t_end) sp_issue<G>(ring + s * G::STAGE, k, t_begin + s, wave);
+    int slot = 0;
+#pragma unroll 1
+    for (int t = t_begin; t < t_end; ++t) {
+        // every wave's share of tile t has landed and tile t-1 is done with
+        // its stage, which tile t+NS-1 takes over
+        lds_barrier();
+        const int prev = slot == 0 ? NS - 1 : slot - 1;
+        const int last = t + NS - 1 < t_end - 1 ? t + NS - 1 : t_end - 1;
+        const int younger = last > t + 1 ? (last - t - 1) * k.per_tile : 0;
+        sp_tile<G>(ring + slot * G::STAGE, ring + prev * G::STAGE, t + NS - 1 < t_end, wf, bv, k, t, younger, a, wave,
+                   lane);
+        slot = slot + 1 == NS ? 0 : slot + 1;
+    }
+}
+
+template <int IC, int OC, int TH, int NW, int NS, bool M16>
+void launch_sp(const ConvArgs& a, hipStream_t s) {
+    const int B = a.npix / (a.Ho * a.Wo);
+    const int ntiles = B * cdiv(a.Ho, TH) * cdiv(a.Wo, 32);
+    const int per = cdiv(ntiles, device_cu_count());
+    hipLaunchKernelGGL((conv3x3_split_kernel<IC, OC, TH, NW, NS, M16>), dim3(cdiv(ntiles, per)), dim3(NW * 64), 0, s,
+                       a, ntiles, per);
+}
+
+// ---------------------------------------------------------------------------
 // conv3x3_band_kernel: stride-1 3x3 conv (pad 1) for the wide layers
 // (IC % 16 == 0, OC % 128 == 0).  A workgroup of 8 waves owns a band of TH
 // full image rows of one clip and 128 output channels; the band's pixels,
@@ -1532,7 +1846,7 @@ void launch_rw(const ConvArgs& a, hipStream_t s) {
 // MFMAs per wave (wave w: output channels 32*(w%4).., column blocks
 // NBW*(w/4)..).  Every B fragment is read once per tap from the halo instead
 // of being re-fetched per tap as an im2col row.  The epilogue stages each
-// 32x32 block per wave through LDS and runs the shared finish8 epilogue on
+// 32x32 block per wave through LDS and runs the shared epilogue (epi8, store8) on
 // 16-byte channel rows.  Products and sums are the other conv kernels'
 // (f16 x f16 -> f32, tap-major / channel-minor within a chunk).
 // ---------------------------------------------------------------------------
@@ -2091,6 +2405,7 @@ struct TileCfg {
     bool halo;       // 3x3 stride-1 pad-1 dilation-1 only
     int rw_ic = 0;   // register-weight kernels: exactly IC = rw_ic and OC = bm, plain epilogue
     int band_w = 0;  // band kernels: W <= band_w, OC % 128 == 0, IC % 16 == 0
+    int sp_ic = 0;   // split-f16 register-weight kernels: exactly IC = sp_ic and OC = bm, split 2
 };
 
 // Entries 0-13 are the register-staged kernel (any layout; the only one with
@@ -2099,7 +2414,8 @@ struct TileCfg {
 // persistent 3x3 kernel, 57-59 the band kernel for wide 3x3 layers, 60-61
 // narrow LDS-DMA tiles, 62-63 narrow register-staged tiles, 64-65 the band
 // kernel with producer / compute waves (128-channel groups, maps up to 75 /
-// 38 wide), 66-69 the register-weight kernel with 3- and 4-stage rings.
+// 38 wide), 66-69 the register-weight kernel with 3- and 4-stage rings,
+// 70-75 the split-f16 register-weight kernel (ERes2Net's group convs).
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -2174,6 +2490,12 @@ const TileCfg kTiles[] = {
     {64, 64, 64, launch_rw<64, 64, 2, 8, 4>, true, 64},   // 67
     {32, 128, 32, launch_rw<32, 32, 4, 8, 4>, true, 32},  // 68
     {32, 256, 32, launch_rw<32, 32, 8, 8, 3>, true, 32},  // 69
+    {16, 256, 32, launch_sp<32, 16, 8, 8, 3, true>, true, 0, 0, 32},    // 70: split-f16 register-weight 3x3
+    {16, 256, 16, launch_sp<16, 16, 8, 8, 4, true>, true, 0, 0, 16},    // 71
+    {32, 256, 32, launch_sp<32, 32, 8, 8, 3, false>, true, 0, 0, 32},   // 72
+    {32, 64, 64, launch_sp<64, 32, 2, 4, 4, true>, true, 0, 0, 64},     // 73
+    {32, 128, 64, launch_sp<64, 32, 4, 4, 2, false>, true, 0, 0, 64},   // 74
+    {64, 128, 64, launch_sp<64, 64, 4, 8, 2, false>, true, 0, 0, 64},   // 75
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -2189,6 +2511,18 @@ bool plain_epilogue(const ConvArgs& a) {
     return !a.gate && !a.post_scale && !a.tanh_after && !a.y_f32 && !a.y_tr && !a.bias_bs && !a.split &&
            (a.act == VDK_ACT_NONE || (a.act == VDK_ACT_RELU && a.clamp_hi <= 0.0f)) && a.xs == a.IC &&
            a.ys == a.OC && (!a.res || a.rs == a.OC) && !a.res_f32 && !a.res_after && !a.y2 && !a.reflect;
+}
+
+// The split-f16 register-weight kernels: f16-exact weights (split 2), bias
+// and ReLU [clamp] or none, no residual; 16-byte aligned input rows and
+// planes, 8-byte aligned output ones, byte offsets within 31 bits.
+bool split_epilogue(const ConvArgs& a) {
+    const auto al = [](const void* p, int n) { return ((uintptr_t)p & (uintptr_t)(n - 1)) == 0; };
+    return a.split == 2 && !a.gate && !a.post_scale && !a.tanh_after && !a.y_f32 && !a.y_tr && !a.bias_bs &&
+           (a.act == VDK_ACT_NONE || a.act == VDK_ACT_RELU) && !a.res && !a.y2 && !a.reflect && !a.in_scale &&
+           !a.segsum && !a.wq && a.xs % 8 == 0 && a.x_lo % 8 == 0 && a.ys % 4 == 0 && a.y_lo % 4 == 0 &&
+           al(a.x, 16) && al(a.y, 8) && al(a.w, 16) && al(a.wc, 16) && al(a.bias, 4) &&
+           ((size_t)a.npix_in * a.xs + a.x_lo + (a.IC / 16 - 1) * a.xgs + 16) * 2 < ((size_t)1 << 31);
 }
 
 // The register-staged (igemm) entries: 0-13 and 62-63.
@@ -2212,6 +2546,9 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     // the in-image tap range for a single row of taps; longer 2-D kernels
     // take the register-staged kernel
     if (a.KH * a.KW > 32 && a.KH != 1 && idx >= kFirstDma) return false;
+    if (t.sp_ic) return a.IC == t.sp_ic && a.OC == t.bm && split_epilogue(a);
+    // 16-channel group strides: the LDS-DMA kernel's offsets and the shared store
+    if ((a.xgs != 16 || a.ygs != 16) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w)) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
     if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % t.bm == 0 && a.IC % 16 == 0;
     // split: the DMA and halo kernels only (IC % kc == 0 below keeps a chunk inside one plane)
@@ -2288,11 +2625,17 @@ int pick_tile(const ConvArgs& a) {
         if (a.H <= 20) return 60;
     }
     if (a.split && is_s1_3x3(a)) {   // ERes2Net's split-f16 group convs (random-data sweeps)
+        // f16-exact weights: the split-f16 register-weight kernel
+        if (a.OC == 16 && a.IC == 32 && tile_fits(kTiles[70], a)) return 70;
+        if (a.OC == 16 && a.IC == 16 && tile_fits(kTiles[71], a)) return 71;
+        if (a.OC == 32 && a.IC == 32 && tile_fits(kTiles[72], a)) return 72;
+        if (a.OC == 32 && a.IC == 64 && tile_fits(kTiles[73], a)) return 73;
+        if (a.OC == 64 && a.IC == 64 && tile_fits(kTiles[75], a)) return 75;
         // up to 64 output channels: the halo kernel (each input pixel fetched
         // once per chunk for all 9 taps; 2.5-2.8x faster than the DMA tiles
         // on the 16-64-channel layers), 8-row tiles on the 1998-frame maps
-        if (a.OC <= 32 && a.IC % 32 == 0) return a.W >= 1000 ? 27 : 28;
-        if (a.OC == 64 && a.IC % 32 == 0) return 30;
+        if (a.OC <= 32 && a.IC % 32 == 0 && tile_fits(kTiles[a.W >= 1000 ? 27 : 28], a)) return a.W >= 1000 ? 27 : 28;
+        if (a.OC == 64 && a.IC % 32 == 0 && tile_fits(kTiles[30], a)) return 30;
         if (a.IC == 128 && a.OC == 128 && tile_fits(kTiles[40], a)) return 40;
     }
     if (a.split && a.KH * a.KW == 1 && a.sh == 1 && a.sw == 1) {   // ERes2Net's split-f16 1x1s (same sweep)
@@ -2518,10 +2861,20 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
                                 aligned16(d.in_scale) && aligned16(d.in_shift)),
                 "conv2d: the input prologue needs a 1x1 conv without padding and 16-byte aligned vectors");
         require(d.split >= 0 && d.split <= 2, "conv2d: split must be 0, 1 or 2");
-        require(!d.split || (!d.y_f32 && !d.y_time_major && d.x_lo >= d.IC && d.y_lo >= d.OC &&
+        const int xgs = d.x_group_stride ? d.x_group_stride : 16, ygs = d.y_group_stride ? d.y_group_stride : 16;
+        // grouped split layouts: each group's lo half sits inside the group stride
+        const bool xg = xgs != 16, yg = ygs != 16;
+        require((!xg && !yg) ||
+                    (d.split && d.IC % 16 == 0 && d.OC % 16 == 0 && xgs % 8 == 0 && ygs % 8 == 0 &&
+                     (!xg || (d.x_lo >= 16 && d.x_lo + 16 <= xgs && (d.IC / 16 - 1) * xgs + 16 + d.x_lo <= xs)) &&
+                     (!yg || (d.y_lo >= 16 && d.y_lo + 16 <= ygs && (d.OC / 16 - 1) * ygs + 16 + d.y_lo <= ys))),
+                "conv2d: group strides need split-f16, 16-channel multiples, lo halves inside the group stride and "
+                "groups inside the pixel stride");
+        require(!d.split || (!d.y_f32 && !d.y_time_major && (xg || d.x_lo >= d.IC) && (yg || d.y_lo >= d.OC) &&
                              (!d.residual || d.res_lo >= d.OC) && d.x_lo % 8 == 0 && d.y_lo % 8 == 0 &&
-                             d.res_lo % 8 == 0 && d.IC % 32 == 0),
-                "conv2d: split-f16 needs IC % 32 == 0, f16 output and lo offsets past the channels");
+                             d.res_lo % 8 == 0 && (d.IC % 32 == 0 || (d.split == 2 && d.IC == 16))),
+                "conv2d: split-f16 needs IC % 32 == 0 (or 16 with split 2), f16 output and lo offsets past the "
+                "channels");
         require(!d.reflect_pad || (d.KH == 1 && d.pad_h == 0 && d.pad_w < d.W),
                 "conv2d: reflect padding is for 1-D convs (KH = 1) with pad_w < W");
         const int y2s = d.y2_stride ? d.y2_stride : d.OC, r2s = d.res2_stride ? d.res2_stride : d.OC;
@@ -2569,6 +2922,7 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         a.bias_bs = d.bias_batch_stride;
         a.split = d.split;
         a.x_lo = d.x_lo; a.r_lo = d.res_lo; a.y_lo = d.y_lo;
+        a.xgs = xgs; a.ygs = ygs;
         a.res_f32 = d.res_f32 ? 1 : 0;
         a.res_after = d.res_after_act ? 1 : 0;
         a.in_scale = d.in_scale;
@@ -2633,6 +2987,8 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.wq = static_cast<const uint8_t*>(d.w_q8_0);
     a.segsum = d.seg_sum;
     a.seg_len = d.seg_sum && d.seg_len > 0 ? d.seg_len : 1;
+    a.xgs = d.x_group_stride ? d.x_group_stride : 16;
+    a.ygs = d.y_group_stride ? d.y_group_stride : 16;
     return a;
 }
 

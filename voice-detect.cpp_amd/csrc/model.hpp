@@ -143,6 +143,7 @@ private:
         int ic = 0, oc = 0, k = 1, kh = 1;
         int split = 1;              // split-f16 weight terms: 1 = [hi|hi|lo], 2 = [hi|hi] (exact in f16)
         void* w = nullptr;          // f16 [OC][KH][K][IC]
+        void* wc = nullptr;         // chunk-major copy of w (split-f16 3x3 layers; may be null)
         float* b = nullptr;         // f32 [OC]
         float* scale = nullptr;     // BatchNorm after ReLU (nullptr = none)
         float* shift = nullptr;

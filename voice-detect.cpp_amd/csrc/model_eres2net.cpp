@@ -40,10 +40,18 @@ namespace {
 struct View {
     void* p;
     int stride, lo;   // elements between pixels / from hi to lo
-    View at(int ch) const { return {static_cast<uint8_t*>(p) + 2 * (size_t)ch, stride, lo}; }
+    int gs;           // elements between 16-channel groups (16: channels contiguous)
+    View at(int ch) const {
+        return {static_cast<uint8_t*>(p) + 2 * ((size_t)(ch / 16) * gs + ch % 16), stride, lo, gs};
+    }
 };
 
-View split_tensor(void* p, int channels) { return {p, 2 * channels, channels}; }
+// [hi C | lo C] per pixel
+View split_tensor(void* p, int channels) { return {p, 2 * channels, channels, 16}; }
+// [hi 16 | lo 16] per 16-channel group: a 16-channel slice is one 64-byte
+// piece of the pixel row, so convs over layer 1's 16-channel chunks read and
+// write whole 64-byte blocks
+View grouped_tensor(void* p, int channels) { return {p, 2 * channels, 16, 32}; }
 
 }  // namespace
 
@@ -81,7 +89,16 @@ void Model::upload_eres2net() {
         // weights that f16 holds exactly need no x_hi . w_lo term
         const bool exact = conv_f16_exact(c);
         l.split = exact ? 2 : 1;
-        arena.put(pack_conv_f16_split(c, icp, ocp, map, exact ? 2 : 3), &l.w);
+        const std::vector<uint16_t> packed = pack_conv_f16_split(c, icp, ocp, map, exact ? 2 : 3);
+        arena.put(packed, &l.w);
+        // the register-weight kernels load their A fragments from a
+        // chunk-major copy as whole cache lines
+        const int icw = (exact ? 2 : 3) * icp;
+        if (c.kh == 3 && c.kw == 3 && icw % 16 == 0) {
+            std::vector<uint16_t> chunked(packed.size());
+            vdk_conv_pack_chunked(packed.data(), ocp, 3, 3, icw, chunked.data());
+            arena.put(chunked, &l.wc);
+        }
         if (!ec.conv_bias[idx].empty()) {
             std::vector<float> b = g.to_f32(ec.conv_bias[idx]);
             require(b.size() == (size_t)c.oc, "voicedetect: '" + ec.conv_bias[idx] + "' has the wrong size");
@@ -128,9 +145,10 @@ void Model::upload_eres2net() {
             const int w = c1.first.oc / 2;
             b.width = w;
             require(w % 8 == 0, "voicedetect: eres2net chunk width must be a multiple of 8");
-            // chunk 0: [chunk0 (| chunk1 zero-weighted)]
+            // chunk 0: [chunk0 (| chunk1 zero-weighted)]; 16 channels alone when
+            // the weights are f16-exact (the split-f16 register-weight kernel)
             auto ca = next(w, 3, 1);
-            put(ca.first, ca.second, w % 32 == 0 ? w : 2 * w, b.conv_a);
+            put(ca.first, ca.second, (w % 32 == 0 || (w == 16 && conv_f16_exact(ca.first))) ? w : 2 * w, b.conv_a);
             if (b.aff) {
                 aff(w, true, b.fuse);
                 auto cb = next(w, 3, 1);
@@ -227,14 +245,18 @@ void Model::encode_eres2net(int batch, int T) {
                     float clamp, int tanh_after, View y) {
         vdk_conv_desc d{};
         d.x = x.p; d.batch = batch; d.H = H; d.W = W; d.IC = l.ic; d.x_stride = x.stride;
-        d.w = l.w; d.OC = l.oc; d.KH = l.kh; d.KW = l.k;
+        d.w = l.w; d.w_chunked = l.wc; d.OC = l.oc; d.KH = l.kh; d.KW = l.k;
         d.stride_h = d.stride_w = stride;
         d.pad_h = (l.kh - 1) / 2; d.pad_w = (l.k - 1) / 2;
         d.bias = l.b;
-        if (res) { d.residual = res->p; d.res_stride = res->stride; d.res_lo = res->lo; }
+        if (res) {
+            require(res->gs == 16, "voicedetect: eres2net residuals are contiguous split tensors");
+            d.residual = res->p; d.res_stride = res->stride; d.res_lo = res->lo;
+        }
         d.act = act; d.clamp_hi = clamp; d.tanh_after = tanh_after;
         d.y = y.p; d.y_stride = y.stride;
         d.split = l.split; d.x_lo = x.lo; d.y_lo = y.lo;
+        d.x_group_stride = x.gs; d.y_group_stride = y.gs;
         d.tile = -1;
         conv_ex(name, d);
     };
@@ -264,7 +286,7 @@ void Model::encode_eres2net(int batch, int T) {
             const EresBlock& b = m.layers[li][bi];
             const int Ho = (H - 1) / b.stride + 1, Wo = (W - 1) / b.stride + 1;
             const int wd = b.width;
-            const View s4 = split_tensor(w.es4, 4 * wd);
+            const View s4 = wd == 16 && !b.aff ? grouped_tensor(w.es4, 4 * wd) : split_tensor(w.es4, 4 * wd);
             // conv1 -> [chunk0 | chunk1]
             conv("eres_conv1", b.conv1, x, H, W, b.stride, nullptr, VDK_ACT_RELU, hi, 0, s4);
             // chunk 0 -> sp0

@@ -46,7 +46,8 @@ class ConvDesc(C.Structure):
                 ("tile", C.c_int), ("res_f32", C.c_int), ("res_after_act", C.c_int), ("out_w", C.c_int),
                 ("in_scale", _vp), ("in_shift", _vp), ("w_chunked", _vp),
                 ("reflect_pad", C.c_int), ("y2", _vp), ("y2_stride", C.c_int), ("res2", _vp),
-                ("res2_stride", C.c_int), ("w_q8_0", _vp), ("seg_sum", _vp), ("seg_len", C.c_int)]
+                ("res2_stride", C.c_int), ("w_q8_0", _vp), ("seg_sum", _vp), ("seg_len", C.c_int),
+                ("x_group_stride", C.c_int), ("y_group_stride", C.c_int)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
@@ -207,6 +208,11 @@ class DeviceBuffer:
         d = cls(a.nbytes)
         _ok(lib().vdk_memcpy_h2d(d.ptr, a.ctypes.data, a.nbytes))
         return d
+
+    def copy_from(self, a):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        _ok(lib().vdk_memcpy_h2d(self.ptr, a.ctypes.data, a.nbytes))
 
     def to_array(self, dtype, shape):
         out = np.empty(shape, dtype=dtype)
