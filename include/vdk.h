@@ -141,14 +141,16 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  * an f16, so the f64 sums are exact and independent of the order they are
  * added in (CAM++'s context pooling, src/encoder_campplus.cpp:159-170).
  * Register-staged tiles (f16 weights) whose pixel tile is at most seg_len wide.
- * x_group_stride / y_group_stride (0: 16, channels contiguous): split-f16
- * tensors stored in 16-channel groups, channel c of the hi plane at element
- * (c / 16) * group_stride + c % 16 of its pixel row (the lo plane x_lo / y_lo
- * after it), e.g. group_stride = 32 with x_lo = 16 keeps each group's hi and
- * lo halves as one 64-byte piece ([hi 16 | lo 16]), so 16-channel slices are
- * read and written as whole 64-byte blocks (narrower writes cost a
- * read-modify-write in HBM).  IC and OC % 16 == 0; the LDS-DMA and split-f16
- * register-weight kernels.
+ * x_group / y_group (16 or 32; 0: 16) and x_group_stride / y_group_stride
+ * (0: the group size, channels contiguous): split-f16 tensors stored in
+ * channel groups, channel c of the hi plane at element (c / group) *
+ * group_stride + c % group of its pixel row (the lo plane x_lo / y_lo after
+ * it); e.g. group 16, stride 32, lo 16 keeps each group's hi and lo halves as
+ * one 64-byte piece ([hi 16 | lo 16]) and group 32, stride 64, lo 32 as one
+ * 128-byte line, so channel slices are read and written as whole 64-byte
+ * blocks or lines (narrower writes cost a read-modify-write in HBM, half-line
+ * reads fetch whole lines).  IC / OC multiples of the group; the LDS-DMA and
+ * split-f16 register-weight kernels.
  * tile = -1 picks the kernel automatically. */
 typedef struct {
     const void* x; int batch, H, W, IC, x_stride;
@@ -172,6 +174,7 @@ typedef struct {
     const void* w_q8_0;
     double* seg_sum; int seg_len;
     int x_group_stride, y_group_stride;
+    int x_group, y_group;
 } vdk_conv_desc;
 /* Host: re-order f16 conv weights [OC][KH][KW][IC] (IC % 16 == 0) into the
  * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */
@@ -363,6 +366,23 @@ int vdk_cam_local(const void* d_x, int x_stride, int batch, int T, int C, int se
 int vdk_aff_combine(const void* d_t, int t_stride, int t_lo, const void* d_x, int x_stride, int x_lo,
                     const void* d_ds, int ds_stride, int ds_lo, long rows, int C, int split, void* d_y,
                     int y_stride, int y_lo, void* stream);
+
+/* ERes2Net: the two chained Res2Net 3x3 convs of a plain (non-AFF) scale-2
+ * block with 16-channel chunks (src/encoder_eres2net.cpp:111-137; layer 1 of
+ * ERes2Net base), one launch, split-f16 with f16-exact weights:
+ *   sp0 = min(relu(conv_a(c0) + b_a), clamp_hi),
+ *   sp1 = min(relu(conv_b(sp0 + c1) + b_b), clamp_hi)   (clamp_hi <= 0: no clamp)
+ * (3x3, stride 1, zero pad 1).  x: [batch][H][W] pixel rows of x_stride
+ * elements whose first 64 hold c0, c1 as 16-channel groups [hi 16 | lo 16];
+ * y: rows of y_stride elements whose first 64 receive sp0, sp1 the same way
+ * (x and y may be slices of one buffer when they do not overlap).  w_a, w_b:
+ * f16 [16][3][3][16]; b_a, b_b: f32 [16] (may be NULL).  Equal bit for bit to
+ * vdk_conv2d_ex's split-f16 convs over the same slices (conv_b's input as the
+ * 32 channels [c1 | sp0] with its weights on both halves).  16-byte aligned
+ * pointers. */
+int vdk_res2_pair3x3(const void* d_x, int x_stride, void* d_y, int y_stride, int batch, int H, int W,
+                     const void* d_w_a, const float* d_b_a, const void* d_w_b, const float* d_b_b, float clamp_hi,
+                     void* stream);
 
 /* ---- wav2vec2 analyze (src/analyze_w2v2.cpp) ----
  * Activations are time-major [B][T][C]; the GEMM-shaped layers run on

@@ -307,37 +307,40 @@ def test_split_register_weight_3x3(IC, OC, tile, ref_tile):
         assert err <= 2e-6
 
 
-def _grouped(vals, groups):
-    """f32 [.., 16 * n] -> f16 rows of `groups` 16-channel groups [hi 16 | lo 16]."""
+def _grouped(vals, groups, g=16):
+    """f32 [.., g * n] -> f16 rows of `groups` g-channel groups [hi g | lo g]."""
     hi, lo = _split(vals)
-    out = np.zeros(vals.shape[:-1] + (32 * groups,), np.float16)
-    for k in range(vals.shape[-1] // 16):
-        out[..., 32 * k:32 * k + 16] = hi[..., 16 * k:16 * k + 16]
-        out[..., 32 * k + 16:32 * k + 32] = lo[..., 16 * k:16 * k + 16]
+    out = np.zeros(vals.shape[:-1] + (2 * g * groups,), np.float16)
+    for k in range(vals.shape[-1] // g):
+        out[..., 2 * g * k:2 * g * k + g] = hi[..., g * k:g * k + g]
+        out[..., 2 * g * k + g:2 * g * (k + 1)] = lo[..., g * k:g * k + g]
     return out
 
 
-def _ungroup(rows, g0, n):
+def _ungroup(rows, g0, n, g=16):
     """The split values of groups g0 .. g0+n of grouped rows, as f64."""
-    parts = [rows[..., 32 * k:32 * k + 16].astype(np.float64) + rows[..., 32 * k + 16:32 * k + 32].astype(np.float64)
-             for k in range(g0, g0 + n)]
+    parts = [rows[..., 2 * g * k:2 * g * k + g].astype(np.float64) +
+             rows[..., 2 * g * k + g:2 * g * (k + 1)].astype(np.float64) for k in range(g0, g0 + n)]
     return np.concatenate(parts, axis=-1)
 
 
-@pytest.mark.parametrize("case", ["3x3_32_16", "3x3_16_16", "1x1_32_64_res", "1x1_64_32"])
-def test_split_grouped_layout(case):
-    """Split-f16 tensors stored as 16-channel groups [hi 16 | lo 16] (group stride
-    32, lo offset 16: layer 1's Res2Net chunks as whole 64-byte pieces): the
-    3x3 group convs on the split register-weight kernel and the LDS-DMA kernel,
-    and the 1x1 convs around them (grouped input with a contiguous split
-    residual; contiguous input into grouped output) on the LDS-DMA kernel,
-    against the f64 brute force; bytes outside the output groups keep their
-    values."""
-    rng = np.random.default_rng(880 + len(case))
-    Bt, H, T, G = 2, 42, 300, 4                           # 4 groups = 64 channels per pixel row
-    K, IC, OC = (3, 32, 16) if case == "3x3_32_16" else (3, 16, 16) if case == "3x3_16_16" else \
-        (1, 32, 64) if case == "1x1_32_64_res" else (1, 64, 32)
-    announce(f"eres grouped split layout {case} B={Bt} H={H} T={T}")
+@pytest.mark.parametrize("case,g", [("3x3_32_16", 16), ("3x3_16_16", 16), ("1x1_32_64_res", 16), ("1x1_64_32", 16),
+                                    ("3x3_32_32", 32), ("3x3_64_32", 32), ("1x1_64_128_res", 32),
+                                    ("1x1_128_64", 32)])
+def test_split_grouped_layout(case, g):
+    """Split-f16 tensors stored as g-channel groups [hi g | lo g] (group stride
+    2g, lo offset g: layer 1 / 2's Res2Net chunks as whole 64-byte pieces /
+    128-byte lines): the 3x3 group convs on the split register-weight kernel
+    and the LDS-DMA kernel, and the 1x1 convs around them (grouped input with a
+    contiguous split residual; contiguous input into grouped output) on the
+    LDS-DMA kernel, against the f64 brute force; bytes outside the output
+    groups keep their values."""
+    rng = np.random.default_rng(880 + len(case) + g)
+    Bt, H, T, G = 2, 42, 300, 4                           # 4 groups per pixel row
+    K, IC, OC = {"3x3_32_16": (3, 32, 16), "3x3_16_16": (3, 16, 16), "1x1_32_64_res": (1, 32, 64),
+                 "1x1_64_32": (1, 64, 32), "3x3_32_32": (3, 32, 32), "3x3_64_32": (3, 64, 32),
+                 "1x1_64_128_res": (1, 64, 128), "1x1_128_64": (1, 128, 64)}[case]
+    announce(f"eres grouped split layout {case} group {g} B={Bt} H={H} T={T}")
     w = (rng.standard_normal((OC, IC, K, K)) * np.sqrt(2.0 / (IC * K * K))).astype(np.float16).astype(np.float32)
     bias = rng.uniform(-0.5, 0.5, OC).astype(np.float32)
     wh = w.transpose(0, 2, 3, 1).astype(np.float16)
@@ -351,15 +354,16 @@ def test_split_grouped_layout(case):
     d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
     d.pad_h = d.pad_w = K // 2
     d.bias, d.act, d.clamp_hi, d.split = keep[1].ptr, lib.ACT_RELU, 20.0, 2
-    if K == 3 or case == "1x1_32_64_res":                 # grouped input from group 1, grouped / contiguous out
-        rows = rng.standard_normal((Bt, H, T, 32 * G)).astype(np.float16)
-        rows[..., 32:32 + 2 * IC] = _grouped(x, IC // 16)
+    res_case = case.endswith("_res")
+    if K == 3 or res_case:                                 # grouped input from group 1, grouped / contiguous out
+        rows = rng.standard_normal((Bt, H, T, 2 * g * G)).astype(np.float16)
+        rows[..., 2 * g:2 * g + 2 * IC] = _grouped(x, IC // g, g)
         din = lib.DeviceBuffer.from_array(rows)
-        d.x, d.x_stride, d.x_lo, d.x_group_stride = din.ptr + 32 * 2, 32 * G, 16, 32
+        d.x, d.x_stride, d.x_lo, d.x_group_stride, d.x_group = din.ptr + 2 * g * 2, 2 * g * G, g, 2 * g, g
     else:
         din = lib.DeviceBuffer.from_array(np.concatenate(_split(x), axis=3))
         d.x, d.x_stride, d.x_lo = din.ptr, 2 * IC, IC
-    if case == "1x1_32_64_res":                            # contiguous split output and residual
+    if res_case:                                           # contiguous split output and residual
         res = rng.standard_normal((Bt, H, T, OC)).astype(np.float32) * 2
         dres = lib.DeviceBuffer.from_array(np.concatenate(_split(res), axis=3))
         d.residual, d.res_stride, d.res_lo = dres.ptr, 2 * OC, OC
@@ -368,10 +372,12 @@ def test_split_grouped_layout(case):
         d.y, d.y_stride, d.y_lo = dy.ptr, 2 * OC, OC
     else:                                                  # grouped output into group 3 (K = 3) or 1
         g0 = 3 if K == 3 else 1
-        yrows = rows.copy() if K == 3 else rng.standard_normal((Bt, H, T, 32 * G)).astype(np.float16)
+        yrows = rows.copy() if K == 3 else rng.standard_normal((Bt, H, T, 2 * g * G)).astype(np.float16)
         dy = din if K == 3 else lib.DeviceBuffer.from_array(yrows)
-        d.y, d.y_stride, d.y_lo, d.y_group_stride = dy.ptr + 32 * g0 * 2, 32 * G, 16, 32
-    tiles = {"3x3_32_16": [70, 14], "3x3_16_16": [71], "1x1_32_64_res": [-1, 16], "1x1_64_32": [-1, 14]}[case]
+        d.y, d.y_stride, d.y_lo, d.y_group_stride, d.y_group = dy.ptr + 2 * g * g0 * 2, 2 * g * G, g, 2 * g, g
+    tiles = {"3x3_32_16": [70, 14], "3x3_16_16": [71], "1x1_32_64_res": [-1, 16], "1x1_64_32": [-1, 14],
+             "3x3_32_32": [72, 14], "3x3_64_32": [73, 74, 14], "1x1_64_128_res": [-1, 39],
+             "1x1_128_64": [-1, 15]}[case]
     outs = []
     for t in tiles:
         if K == 3:
@@ -379,14 +385,14 @@ def test_split_grouped_layout(case):
         d.tile = t
         lib.check(lib.lib().vdk_conv2d_ex(d, None))
         lib.check(lib.lib().vdk_synchronize())
-        if case == "1x1_32_64_res":
+        if res_case:
             o = dy.to_array(np.float16, (Bt, H, T, 2 * OC))
             got = o[..., :OC].astype(np.float64) + o[..., OC:].astype(np.float64)
         else:
-            o = dy.to_array(np.float16, (Bt, H, T, 32 * G))
-            got = _ungroup(o, g0, OC // 16)
-            mask = np.ones(32 * G, bool)
-            mask[32 * g0:32 * (g0 + OC // 16)] = False
+            o = dy.to_array(np.float16, (Bt, H, T, 2 * g * G))
+            got = _ungroup(o, g0, OC // g, g)
+            mask = np.ones(2 * g * G, bool)
+            mask[2 * g * g0:2 * g * (g0 + OC // g)] = False
             assert np.array_equal(o[..., mask], yrows[..., mask])
         outs.append(got)
         for c in (0, Bt - 1):
@@ -457,3 +463,61 @@ def test_eres2net_verify_matches_oracle(eres):
     assert abs(d_gpu - d_ref) <= 2e-3
     for thr in (d_ref - 5e-3, d_ref + 5e-3):
         assert ctx.verify_pcm(a, b, thr)[1] == (d_ref <= thr)
+
+
+@pytest.mark.parametrize("Bt,H,T", [(2, 42, 301), (B, 80, T20S)])
+def test_res2_pair_equals_two_convs(Bt, H, T):
+    """The fused Res2Net pair (layer 1's conv_a -> conv_b with sp0 kept on chip)
+    on grouped [hi 16 | lo 16] rows equals the two one-conv launches (conv_a on
+    c0, conv_b on [c1 | sp0] with its weights on both halves) bit for bit, at
+    partial row / column tiles and at the 80 x 1998 layer-1 map; sp0 and sp1
+    against the f64 brute force on the small map."""
+    rng = np.random.default_rng(990 + H)
+    announce(f"eres res2 pair B={Bt} H={H} T={T}")
+    c = rng.standard_normal((Bt, H, T, 32)).astype(np.float32) * 3     # [c0 | c1]
+    rows = rng.standard_normal((Bt, H, T, 128)).astype(np.float16)
+    rows[..., :64] = _grouped(c, 2)
+    wa = (rng.standard_normal((16, 16, 3, 3)) * np.sqrt(2.0 / 144)).astype(np.float16)
+    wb = (rng.standard_normal((16, 16, 3, 3)) * np.sqrt(2.0 / 144)).astype(np.float16)
+    ba = rng.uniform(-0.5, 0.5, 16).astype(np.float32)
+    bb = rng.uniform(-0.5, 0.5, 16).astype(np.float32)
+    wah, wbh = wa.transpose(0, 2, 3, 1), wb.transpose(0, 2, 3, 1)      # [16][3][3][16]
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(wah)), lib.DeviceBuffer.from_array(ba),
+            lib.DeviceBuffer.from_array(np.ascontiguousarray(wbh)), lib.DeviceBuffer.from_array(bb),
+            lib.DeviceBuffer.from_array(np.ascontiguousarray(np.concatenate([wah, wah], axis=3))),
+            lib.DeviceBuffer.from_array(np.ascontiguousarray(np.concatenate([wbh, wbh, wbh, wbh], axis=3)))]
+    L = lib.lib()
+    # two one-conv launches on the grouped rows: sp0 -> group 2, sp1 -> group 3
+    d2 = lib.DeviceBuffer.from_array(rows)
+    for xg, IC, w, bias, yg, tile in ((0, 16, keep[4], keep[1], 2, 71), (1, 32, keep[5], keep[3], 3, 70)):
+        d = lib.ConvDesc()
+        d.x, d.batch, d.H, d.W, d.IC, d.x_stride = d2.ptr + 32 * xg * 2, Bt, H, T, IC, 128
+        d.x_lo, d.x_group_stride = 16, 32
+        d.w, d.OC, d.KH, d.KW = w.ptr, 16, 3, 3
+        d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+        d.pad_h = d.pad_w = 1
+        d.bias, d.act, d.clamp_hi = bias.ptr, lib.ACT_RELU, 20.0
+        d.y, d.y_stride, d.y_lo, d.y_group_stride = d2.ptr + 32 * yg * 2, 128, 16, 32
+        d.split, d.tile = 2, tile
+        lib.check(L.vdk_conv2d_ex(d, None))
+    d1 = lib.DeviceBuffer.from_array(rows)
+    lib.check(L.vdk_res2_pair3x3(d1.ptr, 128, d1.ptr + 64 * 2, 128, Bt, H, T, keep[0].ptr, keep[1].ptr, keep[2].ptr,
+                                 keep[3].ptr, 20.0, None))
+    lib.check(L.vdk_synchronize())
+    two = d2.to_array(np.float16, (Bt, H, T, 128))
+    one = d1.to_array(np.float16, (Bt, H, T, 128))
+    assert np.array_equal(one[..., :64], rows[..., :64])
+    assert np.array_equal(one, two)
+    if Bt == B:
+        return
+    sp = _ungroup(one, 2, 2)
+    for ci in (0, Bt - 1):
+        s0 = np.clip(O.conv2d_g(c[ci, :, :, :16].transpose(2, 0, 1), wa.astype(np.float32), ph=1, pw=1, bias=ba,
+                                f64=True), 0.0, 20.0)
+        err0 = np.abs(sp[ci, :, :, :16].transpose(2, 0, 1) - s0).max() / np.abs(s0).max()
+        xin = sp[ci, :, :, :16] + c[ci, :, :, 16:].astype(np.float64)
+        s1 = np.clip(O.conv2d_g(xin.transpose(2, 0, 1).astype(np.float32), wb.astype(np.float32), ph=1, pw=1,
+                                bias=bb, f64=True), 0.0, 20.0)
+        err1 = np.abs(sp[ci, :, :, 16:].transpose(2, 0, 1) - s1).max() / np.abs(s1).max()
+        announce(f"res2 pair clip {ci}: sp0 err {err0:.2e}, sp1 err {err1:.2e}")
+        assert err0 <= 2e-6 and err1 <= 4e-6

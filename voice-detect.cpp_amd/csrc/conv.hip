@@ -58,11 +58,13 @@ struct ConvArgs {
     const uint8_t* wq;         // 1x1 weights as q8_0 blocks [OC][IC/32] x {f16 d, 32 x int8} (register-staged kernel)
     double* segsum;            // per-(clip, segment, OC) f64 sums of the stored outputs (may be NULL)
     int seg_len, seg_n;        // output columns per segment, segments per clip
-    int xgs = 16, ygs = 16;    // elements between 16-channel groups of x / y (16: contiguous channels)
+    int xgl = 4, ygl = 4;      // log2 of the channels per group of x / y (16 or 32)
+    int xgs = 16, ygs = 16;    // elements between channel groups of x / y (= group size: contiguous)
 };
 
-// Element offset of channel c (c % 8 == 0 reads / writes 8 channels of one group).
-__device__ __forceinline__ int chan_off(int c, int gs) { return (c >> 4) * gs + (c & 15); }
+// Element offset of channel c in a layout of 2^gl-channel groups gs elements
+// apart (an 8-channel access with c % 8 == 0 stays inside one group).
+__device__ __forceinline__ int chan_off(int c, int gl, int gs) { return (c >> gl) * gs + (c & ((1 << gl) - 1)); }
 
 // Epilogue for 8 consecutive output channels oc..oc+7 of pixel P (P
 // enumerates (clip, oh, ow) row-major), with every operand moved as 16-byte
@@ -139,7 +141,7 @@ __device__ __forceinline__ void store8(const ConvArgs& a, int P, int oc, const f
         const int b = P / HoWo, rem = P - b * HoWo, oh = rem / a.Wo, ow = rem - oh * a.Wo;
         Po = ((size_t)b * a.Wo + ow) * a.Ho + oh;
     }
-    const size_t o = Po * a.ys + chan_off(oc, a.ygs);
+    const size_t o = Po * a.ys + chan_off(oc, a.ygl, a.ygs);
     if (a.y2) {   // f16 only, no split, no time-major store (conv_impl)
         const half8 r = *reinterpret_cast<const half8*>(a.r2 + (size_t)P * a.r2s + oc);
         half8 h2;
@@ -594,7 +596,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     const int nc = ICW / KC;
     const int nk = KHW * nc;
 
-    const int xext = (a.IC / 16 - 1) * a.xgs + 16;   // elements of a pixel's channels (one plane)
+    const int xext = ((a.IC >> a.xgl) - 1) * a.xgs + (1 << a.xgl);   // elements of a pixel's channels (one plane)
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + xext + (a.split ? a.x_lo : 0)) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -631,7 +633,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
                 const int b = P / HoWo, rem = P - b * HoWo;
                 const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
                 const int ih0 = oh * a.sh - a.ph, iw0 = ow * a.sw - a.pw;
-                s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.xs + chan_off(c * 8, a.xgs)) * 2;
+                s_off[j] = (((b * a.H + ih0) * a.W + iw0) * a.xs + chan_off(c * 8, a.xgl, a.xgs)) * 2;
                 s_iw[j] = iw0;
                 if (tap_range) {
                     // one row of taps: the in-image ones are kw in [lo, hi)
@@ -679,7 +681,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
             }
         }
         f_c0 += KC;
-        f_xc += KC / 16 * a.xgs * 2;
+        f_xc += (KC >> a.xgl) * a.xgs * 2;
         if (f_c0 == ICW) {
             f_c0 = 0;
             f_xc = 0;
@@ -1709,7 +1711,7 @@ __device__ __forceinline__ void sp_tile(const uint8_t* st, uint8_t* nst, bool pr
 #pragma unroll
             for (int g = 0; g < NG; ++g) {
                 // register g*4+e: channel 16m + 4*(lane/16) + e (M16), 32mg + 8g + 4*(lane/32) + e (M32)
-                const int oc = chan_off(G::kM16 ? m * 16 + (lane >> 4) * 4 : mg * 32 + g * 8 + (lane >> 5) * 4, a.ygs);
+                const int oc = chan_off(G::kM16 ? m * 16 + (lane >> 4) * 4 : mg * 32 + g * 8 + (lane >> 5) * 4, a.ygl, a.ygs);
                 half4 h, l;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -1749,12 +1751,13 @@ __global__ __launch_bounds__(NW * 64) void conv3x3_split_kernel(ConvArgs a, int 
         const int r = p / G::SPR, cc = p - r * G::SPR;
         const int hr = r / G::XW, hc = r - hr * G::XW;
         const bool lo = cc >= IC / 8;
-        hofs[i] = (hr * W + hc) * xs2 + (lo ? a.x_lo : 0) * 2 + chan_off((lo ? cc - IC / 8 : cc) * 8, a.xgs) * 2;
+        hofs[i] = (hr * W + hc) * xs2 + (lo ? a.x_lo : 0) * 2 + chan_off((lo ? cc - IC / 8 : cc) * 8, a.xgl, a.xgs) * 2;
         hpos[i] = (r < G::XPIX && cc < G::C2 / 8) ? (hr << 8 | hc) : -1;
     }
     SpWalk k;
     k.hofs = hofs; k.hpos = hpos;
-    k.xr = dma_rsrc(a.x, (uint32_t)(((size_t)(a.npix_in - 1) * a.xs + a.x_lo + (IC / 16 - 1) * a.xgs + 16) * 2));
+    k.xr = dma_rsrc(a.x, (uint32_t)(((size_t)(a.npix_in - 1) * a.xs + a.x_lo + ((IC >> a.xgl) - 1) * a.xgs +
+                                     (1 << a.xgl)) * 2));
     k.H = a.H;
     k.W = W;
     k.xs2 = xs2;
@@ -2522,7 +2525,7 @@ bool split_epilogue(const ConvArgs& a) {
            (a.act == VDK_ACT_NONE || a.act == VDK_ACT_RELU) && !a.res && !a.y2 && !a.reflect && !a.in_scale &&
            !a.segsum && !a.wq && a.xs % 8 == 0 && a.x_lo % 8 == 0 && a.ys % 4 == 0 && a.y_lo % 4 == 0 &&
            al(a.x, 16) && al(a.y, 8) && al(a.w, 16) && al(a.wc, 16) && al(a.bias, 4) &&
-           ((size_t)a.npix_in * a.xs + a.x_lo + (a.IC / 16 - 1) * a.xgs + 16) * 2 < ((size_t)1 << 31);
+           ((size_t)a.npix_in * a.xs + a.x_lo + ((a.IC >> a.xgl) - 1) * a.xgs + (1 << a.xgl)) * 2 < ((size_t)1 << 31);
 }
 
 // The register-staged (igemm) entries: 0-13 and 62-63.
@@ -2548,7 +2551,10 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     if (a.KH * a.KW > 32 && a.KH != 1 && idx >= kFirstDma) return false;
     if (t.sp_ic) return a.IC == t.sp_ic && a.OC == t.bm && split_epilogue(a);
     // 16-channel group strides: the LDS-DMA kernel's offsets and the shared store
-    if ((a.xgs != 16 || a.ygs != 16) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w)) return false;
+    if ((a.xgs != (1 << a.xgl) || a.ygs != (1 << a.ygl)) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w))
+        return false;
+    // a DMA chunk covers whole groups
+    if (a.xgl == 5 && t.kc % 32 != 0) return false;
     if (t.rw_ic) return a.IC == t.rw_ic && a.OC == t.bm && plain_epilogue(a);
     if (t.band_w) return plain_epilogue(a) && a.W <= t.band_w && a.OC % t.bm == 0 && a.IC % 16 == 0;
     // split: the DMA and halo kernels only (IC % kc == 0 below keeps a chunk inside one plane)
@@ -2629,7 +2635,7 @@ int pick_tile(const ConvArgs& a) {
         if (a.OC == 16 && a.IC == 32 && tile_fits(kTiles[70], a)) return 70;
         if (a.OC == 16 && a.IC == 16 && tile_fits(kTiles[71], a)) return 71;
         if (a.OC == 32 && a.IC == 32 && tile_fits(kTiles[72], a)) return 72;
-        if (a.OC == 32 && a.IC == 64 && tile_fits(kTiles[73], a)) return 73;
+        if (a.OC == 32 && a.IC == 64 && tile_fits(kTiles[74], a)) return 74;
         if (a.OC == 64 && a.IC == 64 && tile_fits(kTiles[75], a)) return 75;
         // up to 64 output channels: the halo kernel (each input pixel fetched
         // once per chunk for all 9 taps; 2.5-2.8x faster than the DMA tiles
@@ -2861,15 +2867,17 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
                                 aligned16(d.in_scale) && aligned16(d.in_shift)),
                 "conv2d: the input prologue needs a 1x1 conv without padding and 16-byte aligned vectors");
         require(d.split >= 0 && d.split <= 2, "conv2d: split must be 0, 1 or 2");
-        const int xgs = d.x_group_stride ? d.x_group_stride : 16, ygs = d.y_group_stride ? d.y_group_stride : 16;
+        const int xgn = d.x_group ? d.x_group : 16, ygn = d.y_group ? d.y_group : 16;   // channels per group
+        const int xgs = d.x_group_stride ? d.x_group_stride : xgn, ygs = d.y_group_stride ? d.y_group_stride : ygn;
+        require((xgn == 16 || xgn == 32) && (ygn == 16 || ygn == 32), "conv2d: channel groups are 16 or 32 wide");
         // grouped split layouts: each group's lo half sits inside the group stride
-        const bool xg = xgs != 16, yg = ygs != 16;
+        const bool xg = xgs != xgn, yg = ygs != ygn;
         require((!xg && !yg) ||
-                    (d.split && d.IC % 16 == 0 && d.OC % 16 == 0 && xgs % 8 == 0 && ygs % 8 == 0 &&
-                     (!xg || (d.x_lo >= 16 && d.x_lo + 16 <= xgs && (d.IC / 16 - 1) * xgs + 16 + d.x_lo <= xs)) &&
-                     (!yg || (d.y_lo >= 16 && d.y_lo + 16 <= ygs && (d.OC / 16 - 1) * ygs + 16 + d.y_lo <= ys))),
-                "conv2d: group strides need split-f16, 16-channel multiples, lo halves inside the group stride and "
-                "groups inside the pixel stride");
+                    (d.split && d.IC % xgn == 0 && d.OC % ygn == 0 && xgs % 8 == 0 && ygs % 8 == 0 &&
+                     (!xg || (d.x_lo >= xgn && d.x_lo + xgn <= xgs && (d.IC / xgn - 1) * xgs + xgn + d.x_lo <= xs)) &&
+                     (!yg || (d.y_lo >= ygn && d.y_lo + ygn <= ygs && (d.OC / ygn - 1) * ygs + ygn + d.y_lo <= ys))),
+                "conv2d: group strides need split-f16, whole groups, lo halves inside the group stride and groups "
+                "inside the pixel stride");
         require(!d.split || (!d.y_f32 && !d.y_time_major && (xg || d.x_lo >= d.IC) && (yg || d.y_lo >= d.OC) &&
                              (!d.residual || d.res_lo >= d.OC) && d.x_lo % 8 == 0 && d.y_lo % 8 == 0 &&
                              d.res_lo % 8 == 0 && (d.IC % 32 == 0 || (d.split == 2 && d.IC == 16))),
@@ -2923,6 +2931,7 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         a.split = d.split;
         a.x_lo = d.x_lo; a.r_lo = d.res_lo; a.y_lo = d.y_lo;
         a.xgs = xgs; a.ygs = ygs;
+        a.xgl = xgn == 32 ? 5 : 4; a.ygl = ygn == 32 ? 5 : 4;
         a.res_f32 = d.res_f32 ? 1 : 0;
         a.res_after = d.res_after_act ? 1 : 0;
         a.in_scale = d.in_scale;
@@ -2987,8 +2996,10 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.wq = static_cast<const uint8_t*>(d.w_q8_0);
     a.segsum = d.seg_sum;
     a.seg_len = d.seg_sum && d.seg_len > 0 ? d.seg_len : 1;
-    a.xgs = d.x_group_stride ? d.x_group_stride : 16;
-    a.ygs = d.y_group_stride ? d.y_group_stride : 16;
+    a.xgl = d.x_group == 32 ? 5 : 4;
+    a.ygl = d.y_group == 32 ? 5 : 4;
+    a.xgs = d.x_group_stride ? d.x_group_stride : 1 << a.xgl;
+    a.ygs = d.y_group_stride ? d.y_group_stride : 1 << a.ygl;
     return a;
 }
 

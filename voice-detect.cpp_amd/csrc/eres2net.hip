@@ -50,6 +50,284 @@ __global__ __launch_bounds__(256) void aff_combine_kernel(const half_t* __restri
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// ---------------------------------------------------------------------------
+// res2_pair_kernel: the two chained Res2Net 3x3 convs of a plain (non-AFF)
+// scale-2 block with 16-channel chunks (src/encoder_eres2net.cpp:111-137,
+// ERes2Net's layer 1) in one launch, split-f16 with f16-exact weights:
+//   sp0 = min(relu(conv_a(c0) + b_a), clamp),
+//   sp1 = min(relu(conv_b(sp0 + c1) + b_b), clamp).
+// Maps are pixel rows of 16-channel groups [hi 16 | lo 16] (64 bytes): the
+// input row's groups 0, 1 hold c0, c1 and the output row's groups 0, 1
+// receive sp0, sp1, so the launch reads and writes whole 128-byte lines.  A
+// persistent workgroup walks TH x 30 output tiles (rows fastest) through a
+// ring of (TH+4) x 34 input halos, each DMA'd two tiles ahead; per tile
+// conv_a runs over the (TH+2) x 32 region around the tile into LDS (zero
+// outside the image: conv_b's zero padding) and the tile's own sp0 goes
+// out, then conv_b reads c1 from the halo and sp0 from LDS.  Both run on
+// 16x16x32 MFMAs (16 output channels x 16 pixels) with the K grouping of the
+// one-conv kernel: conv_a [c0 hi | c0 lo] per tap, conv_b [c1 hi | sp0 hi]
+// for every tap, then [c1 lo | sp0 lo] (its input sp0 + c1 is the two
+// 16-channel halves of one 32-channel MFMA operand with the weights
+// repeated), so sp0 and sp1 equal the two one-conv launches bit for bit.
+// ---------------------------------------------------------------------------
+namespace pair {
+constexpr int TH = 4, TW = 30, NW = 8, NS = 3;
+constexpr int XW = 34, XH = TH + 4, XPIX = XH * XW;     // input halo (tile origin - 2)
+constexpr int RBX = 144, SPRX = 9;                      // [c0h c0l c1h c1l] + 16 bytes of padding
+constexpr int X_INS = (XPIX * SPRX + 63) / 64, X_IPW = (X_INS + NW - 1) / NW;
+constexpr int STAGE = X_INS * 1024;
+constexpr int IW = 32, IH = TH + 2, IPIX = IH * IW;     // sp0 region (tile origin - 1)
+constexpr int RBT = 80;                                 // [sp0h sp0l] + 16 bytes of padding
+constexpr int NBA = IH * 2, NBB = TH * 2;               // 16-pixel column blocks of conv_a / conv_b
+constexpr int BPA = (NBA + NW - 1) / NW, BPB = (NBB + NW - 1) / NW;
+// one spare row: conv_b's discarded columns 30, 31 read up to two pixels past the region
+constexpr int INTER_BYTES = (IPIX + IW) * RBT;
+constexpr int SP = 18 / X_IPW;                          // conv_b steps between DMA instructions
+static_assert(NS * STAGE + INTER_BYTES <= 163840, "the ring and the sp0 region fit the 160 KB of LDS");
+static_assert(SP >= 1 && X_IPW * SP <= 18, "every DMA instruction has a conv_b step");
+}  // namespace pair
+
+__device__ __forceinline__ void wait_vm_le(int n) {
+    switch (n) {
+#define VDK_VM(N) case N: wait_vmcnt<N>(); break;
+        VDK_VM(0) VDK_VM(1) VDK_VM(2) VDK_VM(3) VDK_VM(4) VDK_VM(5) VDK_VM(6) VDK_VM(7) VDK_VM(8)
+#undef VDK_VM
+        default: __builtin_amdgcn_s_waitcnt(0); break;
+    }
+}
+
+struct PairWalk {
+    const int* hofs; const int* hpos;
+    int4v xr;
+    int tiles_w, tiles_h, H, W, xs2;
+};
+
+// This wave's DMA instructions for tile t's halo into stage st.
+struct PairDma {
+    uint8_t* st;
+    const PairWalk* k;
+    int oh0, ow0, xo, wave;
+    bool on;
+    __device__ __forceinline__ PairDma(uint8_t* st_, const PairWalk& k_, int t, int wave_, bool on_)
+        : st(st_), k(&k_), wave(wave_), on(on_) {
+        const int th = t % k_.tiles_h, r = t / k_.tiles_h, tw = r % k_.tiles_w, b = r / k_.tiles_w;
+        oh0 = th * pair::TH;
+        ow0 = tw * pair::TW;
+        xo = ((b * k_.H + oh0 - 2) * k_.W + ow0 - 2) * k_.xs2;
+    }
+    __device__ __forceinline__ void issue(int j) const {
+        const int ins = wave + j * pair::NW;
+        if (!on || ins >= pair::X_INS) return;
+        const int hp = k->hpos[j];
+        const int ih = oh0 - 2 + (hp >> 8), iw = ow0 - 2 + (hp & 255);
+        const uint32_t off = (hp >= 0 && (unsigned)ih < (unsigned)k->H && (unsigned)iw < (unsigned)k->W)
+                                 ? (uint32_t)(xo + k->hofs[j]) : kOOB;
+        dma16(st + ins * 1024, k->xr, off);
+    }
+};
+
+__device__ __forceinline__ void split_relu_clamp(const float4v& acc, const float* bv, float chi, half4& h, half4& l) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float v = fmaxf(acc[e] + bv[e], 0.0f);
+        if (chi > 0.0f) v = fminf(v, chi);
+        h[e] = (half_t)v;
+        l[e] = (half_t)(v - (float)h[e]);
+    }
+}
+
+__global__ __launch_bounds__(pair::NW * 64) void res2_pair_kernel(
+    const half_t* __restrict__ x, int xs, half_t* __restrict__ y, int ys, const half_t* __restrict__ wa,
+    const float* __restrict__ ba, const half_t* __restrict__ wb, const float* __restrict__ bb, float chi, int H,
+    int W, int npix, int ntiles, int per_wg) {
+    using namespace pair;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
+    __shared__ __attribute__((aligned(16))) uint8_t inter[INTER_BYTES];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t_begin = blockIdx.x * per_wg;
+    const int t_end = t_begin + per_wg < ntiles ? t_begin + per_wg : ntiles;
+    if (t_begin >= t_end) return;   // the whole workgroup: no barrier is pending
+
+    // DMA slots of this lane (the same for every tile): halo pixel row r,
+    // 16-byte slot cc of its 128 bytes [c0h c0l c1h c1l]
+    int hofs[X_IPW], hpos[X_IPW];
+#pragma unroll
+    for (int i = 0; i < X_IPW; ++i) {
+        const int p = (wave + i * NW) * 64 + lane;
+        const int r = p / SPRX, cc = p - r * SPRX;
+        const int hr = r / XW, hc = r - hr * XW;
+        hofs[i] = ((hr * W + hc) * xs + cc * 8) * 2;
+        hpos[i] = (r < XPIX && cc < 8) ? (hr << 8 | hc) : -1;
+    }
+    PairWalk k;
+    k.hofs = hofs; k.hpos = hpos;
+    k.xr = dma_rsrc(x, (uint32_t)(((size_t)(npix - 1) * xs + 64) * 2));
+    k.H = H; k.W = W; k.xs2 = xs * 2;
+    k.tiles_w = (W + TW - 1) / TW;
+    k.tiles_h = (H + TH - 1) / TH;
+    const int per_tile = (X_INS - wave + NW - 1) / NW;   // this wave's DMA instructions per tile
+
+    {
+        const PairDma d(ring, k, t_begin, wave, true);
+#pragma unroll
+        for (int j = 0; j < X_IPW; ++j) d.issue(j);
+    }
+    // A fragments: K = 32 is two 16-channel halves with the same weights
+    const int orow = lane & 15, kg = lane >> 4, lp = lane & 15;
+    half8 fa[9], fb[9];
+#pragma unroll
+    for (int tap = 0; tap < 9; ++tap) {
+        fa[tap] = *reinterpret_cast<const half8*>(wa + (orow * 9 + tap) * 16 + (kg & 1) * 8);
+        fb[tap] = *reinterpret_cast<const half8*>(wb + (orow * 9 + tap) * 16 + (kg & 1) * 8);
+    }
+    float bva[4], bvb[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        bva[e] = ba ? ba[kg * 4 + e] : 0.0f;
+        bvb[e] = bb ? bb[kg * 4 + e] : 0.0f;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int s = 1; s + 1 < NS; ++s)
+        if (t_begin + s < t_end) {
+            const PairDma d(ring + s * STAGE, k, t_begin + s, wave, true);
+#pragma unroll
+            for (int j = 0; j < X_IPW; ++j) d.issue(j);
+        }
+
+    int slot = 0;
+#pragma unroll 1
+    for (int t = t_begin; t < t_end; ++t) {
+        // tile t's halo has landed for every wave; tile t-1 is done with the
+        // sp0 region and with its stage, which tile t+NS-1 takes over
+        lds_barrier();
+        const int prev = slot == 0 ? NS - 1 : slot - 1;
+        const uint8_t* const st = ring + slot * STAGE;
+        const PairDma nd(ring + prev * STAGE, k, t + NS - 1, wave, t + NS - 1 < t_end);
+        const int th = t % k.tiles_h, rr = t / k.tiles_h, tw = rr % k.tiles_w, b = rr / k.tiles_w;
+        const int oh0 = th * TH, ow0 = tw * TW;
+
+        // conv_a over the sp0 region: block j = row j/2, columns 16*(j%2) ..
+        // (the B reads run PD steps ahead of the MFMAs)
+        constexpr int PD = 4;
+        float4v acc[BPA];
+        int aoff[BPA];
+#pragma unroll
+        for (int q = 0; q < BPA; ++q) {
+            acc[q] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+            const int j = wave + q * NW < NBA ? wave + q * NW : 0;   // a spare block reads block 0
+            aoff[q] = ((j >> 1) * XW + (j & 1) * 16 + lp) * RBX + kg * 16;
+        }
+        auto load_a = [&](int tap, half8* dst) {
+            const int kh = tap / 3, kw = tap - kh * 3;
+#pragma unroll
+            for (int q = 0; q < BPA; ++q) dst[q] = *reinterpret_cast<const half8*>(st + aoff[q] + (kh * XW + kw) * RBX);
+        };
+        {
+            half8 ring_a[PD][BPA];
+#pragma unroll
+            for (int s = 0; s < PD; ++s) load_a(s, ring_a[s]);
+#pragma unroll
+            for (int tap = 0; tap < 9; ++tap) {
+                half8 cur[BPA];
+#pragma unroll
+                for (int q = 0; q < BPA; ++q) cur[q] = ring_a[tap % PD][q];
+                if (tap + PD < 9) load_a(tap + PD, ring_a[tap % PD]);
+#pragma unroll
+                for (int q = 0; q < BPA; ++q)
+                    if (wave + q * NW < NBA)
+                        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[tap], cur[q], acc[q], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < BPA; ++q) {
+            const int j = wave + q * NW;
+            if (j >= NBA) continue;
+            const int r = j >> 1, col = (j & 1) * 16 + lp;
+            const int gh = oh0 - 1 + r, gw = ow0 - 1 + col;
+            half4 h, l;
+            split_relu_clamp(acc[q], bva, chi, h, l);
+            const bool in = (unsigned)gh < (unsigned)H && (unsigned)gw < (unsigned)W;
+            if (!in) h = l = half4{0, 0, 0, 0};
+            uint8_t* const tp = inter + (r * IW + col) * RBT + kg * 8;
+            *reinterpret_cast<half4*>(tp) = h;
+            *reinterpret_cast<half4*>(tp + 32) = l;
+            if (in && r >= 1 && r <= TH && col >= 1 && col <= TW) {
+                half_t* const yp = y + ((size_t)(b * H + gh) * W + gw) * ys + kg * 4;
+                *reinterpret_cast<half4*>(yp) = h;
+                *reinterpret_cast<half4*>(yp + 16) = l;
+            }
+        }
+        lds_barrier();
+
+        // conv_b: block j = output row j/2, columns 16*(j%2) .. (30, 31 are
+        // discarded); lanes of K half 0 read c1 from the halo, of half 1 sp0
+        float4v cb[BPB];
+        const bool fromx = kg < 2;
+        const int srow = fromx ? XW * RBX : IW * RBT, scol = fromx ? RBX : RBT;
+        const uint8_t* bbase[BPB];
+#pragma unroll
+        for (int q = 0; q < BPB; ++q) {
+            cb[q] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+            const int j = wave + q * NW < NBB ? wave + q * NW : 0;
+            const int i = j >> 1, c = (j & 1) * 16 + lp;
+            bbase[q] = fromx ? st + ((i + 1) * XW + c + 1) * RBX + 64 + kg * 16 : inter + (i * IW + c) * RBT + (kg - 2) * 16;
+        }
+        auto load_b = [&](int s, half8* dst) {
+            const int p = s / 9, tap = s - p * 9, kh = tap / 3, kw = tap - kh * 3;
+#pragma unroll
+            for (int q = 0; q < BPB; ++q)
+                dst[q] = *reinterpret_cast<const half8*>(bbase[q] + kh * srow + kw * scol + p * 32);
+        };
+        {
+            half8 ring_b[PD][BPB];
+#pragma unroll
+            for (int s = 0; s < PD; ++s) load_b(s, ring_b[s]);
+#pragma unroll
+            for (int s = 0; s < 18; ++s) {
+                half8 cur[BPB];
+#pragma unroll
+                for (int q = 0; q < BPB; ++q) cur[q] = ring_b[s % PD][q];
+                if (s + PD < 18) load_b(s + PD, ring_b[s % PD]);
+#pragma unroll
+                for (int q = 0; q < BPB; ++q)
+                    if (wave + q * NW < NBB)
+                        cb[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fb[s % 9], cur[q], cb[q], 0, 0, 0);
+                if (s % SP == 0 && s / SP < X_IPW) nd.issue(s / SP);
+            }
+        }
+        // tile t+1's loads have landed (this wave's): only tile t+2's may be in flight
+        const int last = t + NS - 1 < t_end - 1 ? t + NS - 1 : t_end - 1;
+        wait_vm_le(last > t + 1 ? (last - t - 1) * per_tile : 0);
+#pragma unroll
+        for (int q = 0; q < BPB; ++q) {
+            const int j = wave + q * NW;
+            if (j >= NBB) continue;
+            const int i = j >> 1, c = (j & 1) * 16 + lp;
+            const int oh = oh0 + i, ow = ow0 + c;
+            if (c >= TW || oh >= H || ow >= W) continue;
+            half4 h, l;
+            split_relu_clamp(cb[q], bvb, chi, h, l);
+            half_t* const yp = y + ((size_t)(b * H + oh) * W + ow) * ys + 32 + kg * 4;
+            *reinterpret_cast<half4*>(yp) = h;
+            *reinterpret_cast<half4*>(yp + 16) = l;
+        }
+        slot = slot + 1 == NS ? 0 : slot + 1;
+    }
+}
+
+int cu_count() {
+    static const int n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        return cus;
+    }();
+    return n;
+}
+
 }  // namespace
 }  // namespace vdk
 
@@ -71,6 +349,29 @@ extern "C" int vdk_aff_combine(const void* d_t, int t_stride, int t_lo, const vo
                            static_cast<const half_t*>(d_t), t_stride, t_lo, static_cast<const half_t*>(d_x), x_stride,
                            x_lo, static_cast<const half_t*>(d_ds), ds_stride, ds_lo, rows, C, split ? 1 : 0,
                            static_cast<half_t*>(d_y), y_stride, y_lo);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_res2_pair3x3(const void* d_x, int x_stride, void* d_y, int y_stride, int batch, int H, int W,
+                                const void* d_wa, const float* d_ba, const void* d_wb, const float* d_bb,
+                                float clamp_hi, void* stream) {
+    return guarded([&] {
+        require(d_x && d_y && d_wa && d_wb, "res2_pair3x3: NULL device pointer");
+        require(batch > 0 && H > 0 && W > 0, "res2_pair3x3: empty map");
+        require(x_stride >= 64 && y_stride >= 64 && x_stride % 8 == 0 && y_stride % 8 == 0,
+                "res2_pair3x3: pixel strides must hold the two 32-element groups and be multiples of 8");
+        require(al16(d_x) && al16(d_y) && al16(d_wa) && al16(d_wb) && al16(d_ba) && al16(d_bb),
+                "res2_pair3x3: device pointers must be 16-byte aligned");
+        const long npix = (long)batch * H * W;
+        require(npix * x_stride * 2 < (1L << 31) && npix * y_stride < (1L << 31) && W < 8192,
+                "res2_pair3x3: map too large for one launch");
+        const int ntiles = batch * cdiv(H, pair::TH) * cdiv(W, pair::TW);
+        const int per = cdiv(ntiles, cu_count());
+        hipLaunchKernelGGL(res2_pair_kernel, dim3(cdiv(ntiles, per)), dim3(pair::NW * 64), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride,
+                           static_cast<half_t*>(d_y), y_stride, static_cast<const half_t*>(d_wa), d_ba,
+                           static_cast<const half_t*>(d_wb), d_bb, clamp_hi, H, W, (int)npix, ntiles, per);
         VDK_HIP(hipGetLastError());
     });
 }

@@ -208,6 +208,10 @@ private:
         bool aff = false;
         EresAff fuse;     // AFF(sp0, chunk1); conv1 input order [chunk1 | sp0]
         Layer conv3;      // 1x1 over [sp0 | sp1] -> 2*planes (+ residual, clamp)
+        // 16-channel chunks with f16-exact conv_a / conv_b weights: both convs
+        // run as one launch (vdk_res2_pair3x3) from these f16 [16][3][3][16] copies
+        void* pair_a = nullptr;
+        void* pair_b = nullptr;
         bool has_sc = false;
         Layer sc;         // 1x1 shortcut, block stride
         int stride = 1, width = 0, planes = 0, in_c = 0;

@@ -40,18 +40,18 @@ namespace {
 struct View {
     void* p;
     int stride, lo;   // elements between pixels / from hi to lo
-    int gs;           // elements between 16-channel groups (16: channels contiguous)
+    int gn, gs;       // channels per group, elements between groups (gs == gn: channels contiguous)
     View at(int ch) const {
-        return {static_cast<uint8_t*>(p) + 2 * ((size_t)(ch / 16) * gs + ch % 16), stride, lo, gs};
+        return {static_cast<uint8_t*>(p) + 2 * ((size_t)(ch / gn) * gs + ch % gn), stride, lo, gn, gs};
     }
 };
 
 // [hi C | lo C] per pixel
-View split_tensor(void* p, int channels) { return {p, 2 * channels, channels, 16}; }
-// [hi 16 | lo 16] per 16-channel group: a 16-channel slice is one 64-byte
-// piece of the pixel row, so convs over layer 1's 16-channel chunks read and
-// write whole 64-byte blocks
-View grouped_tensor(void* p, int channels) { return {p, 2 * channels, 16, 32}; }
+View split_tensor(void* p, int channels) { return {p, 2 * channels, channels, 16, 16}; }
+// [hi g | lo g] per g-channel group: a Res2Net chunk of g = 16 channels is
+// one 64-byte piece of the pixel row, of 32 one 128-byte line, so the convs
+// over layer 1 / 2's chunks read and write whole blocks
+View grouped_tensor(void* p, int channels, int g) { return {p, 2 * channels, g, g, 2 * g}; }
 
 }  // namespace
 
@@ -156,6 +156,10 @@ void Model::upload_eres2net() {
             } else {
                 // [chunk1 | sp0] with the weights on both halves: conv(sp0 + chunk1)
                 auto cb = next(w, 3, 1);
+                if (w == 16 && conv_f16_exact(ca.first) && conv_f16_exact(cb.first)) {
+                    arena.put(pack_conv_f16(ca.first, w), &b.pair_a);
+                    arena.put(pack_conv_f16(cb.first, w), &b.pair_b);
+                }
                 HostConv dup = cb.first;
                 dup.ic = 2 * w;
                 dup.w.assign((size_t)dup.oc * 2 * w * 9, 0.0f);
@@ -250,13 +254,13 @@ void Model::encode_eres2net(int batch, int T) {
         d.pad_h = (l.kh - 1) / 2; d.pad_w = (l.k - 1) / 2;
         d.bias = l.b;
         if (res) {
-            require(res->gs == 16, "voicedetect: eres2net residuals are contiguous split tensors");
+            require(res->gs == res->gn, "voicedetect: eres2net residuals are contiguous split tensors");
             d.residual = res->p; d.res_stride = res->stride; d.res_lo = res->lo;
         }
         d.act = act; d.clamp_hi = clamp; d.tanh_after = tanh_after;
         d.y = y.p; d.y_stride = y.stride;
         d.split = l.split; d.x_lo = x.lo; d.y_lo = y.lo;
-        d.x_group_stride = x.gs; d.y_group_stride = y.gs;
+        d.x_group = x.gn; d.x_group_stride = x.gs; d.y_group = y.gn; d.y_group_stride = y.gs;
         d.tile = -1;
         conv_ex(name, d);
     };
@@ -286,18 +290,30 @@ void Model::encode_eres2net(int batch, int T) {
             const EresBlock& b = m.layers[li][bi];
             const int Ho = (H - 1) / b.stride + 1, Wo = (W - 1) / b.stride + 1;
             const int wd = b.width;
-            const View s4 = wd == 16 && !b.aff ? grouped_tensor(w.es4, 4 * wd) : split_tensor(w.es4, 4 * wd);
+            const View s4 = (wd == 16 || wd == 32) && !b.aff ? grouped_tensor(w.es4, 4 * wd, wd)
+                                                             : split_tensor(w.es4, 4 * wd);
             // conv1 -> [chunk0 | chunk1]
             conv("eres_conv1", b.conv1, x, H, W, b.stride, nullptr, VDK_ACT_RELU, hi, 0, s4);
-            // chunk 0 -> sp0
-            conv("eres_conv3x3", b.conv_a, s4, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(2 * wd));
-            // chunk 1 -> sp1
-            if (b.aff) {
-                const View f = split_tensor(w.ef, wd);
-                aff("eres_aff_block", b.fuse, s4.at(wd), s4.at(2 * wd), s4.at(wd), wd, Ho, Wo, f);
-                conv("eres_conv3x3", b.conv_b, f, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(3 * wd));
+            if (b.pair_a && s4.gn == 16) {
+                // chunk 0 -> sp0 and chunk 1 (+ sp0) -> sp1 in one launch
+                // MFMA work: conv_a 16 x 16 x 9 over both planes, conv_b the same twice (c1, sp0)
+                prof_begin("eres_res2_pair", 2.0 * 9 * 16 * 16 * 2 * 3 * (double)batch * Ho * Wo,
+                           2.0 * 2 * 64 * (double)batch * Ho * Wo);
+                check_rc(vdk_res2_pair3x3(s4.p, s4.stride, s4.at(2 * wd).p, s4.stride, batch, Ho, Wo, b.pair_a,
+                                          b.conv_a.b, b.pair_b, b.conv_b.b, hi, stream_));
+                prof_end();
             } else {
-                conv("eres_conv3x3", b.conv_b, s4.at(wd), Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(3 * wd));
+                // chunk 0 -> sp0
+                conv("eres_conv3x3", b.conv_a, s4, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(2 * wd));
+                // chunk 1 -> sp1
+                if (b.aff) {
+                    const View f = split_tensor(w.ef, wd);
+                    aff("eres_aff_block", b.fuse, s4.at(wd), s4.at(2 * wd), s4.at(wd), wd, Ho, Wo, f);
+                    conv("eres_conv3x3", b.conv_b, f, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(3 * wd));
+                } else {
+                    conv("eres_conv3x3", b.conv_b, s4.at(wd), Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0,
+                         s4.at(3 * wd));
+                }
             }
             // shortcut, then conv3 + residual -> clamp
             View res = x;

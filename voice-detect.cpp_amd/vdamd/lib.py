@@ -47,7 +47,8 @@ class ConvDesc(C.Structure):
                 ("in_scale", _vp), ("in_shift", _vp), ("w_chunked", _vp),
                 ("reflect_pad", C.c_int), ("y2", _vp), ("y2_stride", C.c_int), ("res2", _vp),
                 ("res2_stride", C.c_int), ("w_q8_0", _vp), ("seg_sum", _vp), ("seg_len", C.c_int),
-                ("x_group_stride", C.c_int), ("y_group_stride", C.c_int)]
+                ("x_group_stride", C.c_int), ("y_group_stride", C.c_int), ("x_group", C.c_int),
+                ("y_group", C.c_int)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
@@ -153,6 +154,8 @@ _SIGS = {
     "vdk_asp_pool": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "vdk_asp_attn_pool": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
                                     C.c_float, _vp, _vp]),
+    "vdk_res2_pair3x3": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp,
+                                   C.c_float, _vp]),
     "vdk_aff_combine": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_long,
                                   C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp]),
     "vdk_bn_act": (C.c_int, [_vp, C.c_int, C.c_long, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, _vp]),
