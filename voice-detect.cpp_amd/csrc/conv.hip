@@ -2644,6 +2644,11 @@ int pick_tile(const ConvArgs& a) {
         if (a.OC == 64 && a.IC % 32 == 0 && tile_fits(kTiles[30], a)) return 30;
         if (a.IC == 128 && a.OC == 128 && tile_fits(kTiles[40], a)) return 40;
     }
+    if (a.split && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2) {   // ERes2Net's cross-stage downsamples
+        if (a.IC == 64 && a.OC == 128 && tile_fits(kTiles[36], a)) return 36;
+        if (a.IC == 128 && a.OC == 256 && tile_fits(kTiles[34], a)) return 34;
+        if (a.IC == 256 && a.OC == 512 && tile_fits(kTiles[40], a)) return 40;
+    }
     if (a.split && a.KH * a.KW == 1 && a.sh == 1 && a.sw == 1) {   // ERes2Net's split-f16 1x1s (same sweep)
         if (a.IC == 64 && a.OC == 32) return 61;
         if (a.IC == 128 && a.OC == 64) return 23;
