@@ -99,6 +99,10 @@ enum { VDK_ACT_NONE = 0, VDK_ACT_RELU = 1, VDK_ACT_SIGMOID = 2, VDK_ACT_SILU = 3
  *   v += residual                  (instead of the add above when res_after_act)
  *   v = v*post_scale + post_shift  (a BatchNorm after the activation; may be NULL)
  *   v = tanh(v)                    (tanh_after)
+ *   v = (x + ds) + v * (x - ds)    (aff_x / aff_ds: ERes2Net's AFF combine,
+ *                                   src/encoder_eres2net.cpp:91-101; f16, or
+ *                                   split-f16 with split, at the output pixel
+ *                                   and channel, own pixel strides / lo offsets)
  * stored f16 (or f32 if y_f32) at pixel (b, oh, ow), or at (b, ow, oh) when
  * y_time_major (an NHWC [B][H][W][C] map written as [B][W][H*C], no residual).
  * in_scale / in_shift (1x1 convs without padding): the input channels pass
@@ -175,6 +179,8 @@ typedef struct {
     double* seg_sum; int seg_len;
     int x_group_stride, y_group_stride;
     int x_group, y_group;
+    const void* aff_x; int aff_x_stride, aff_x_lo;
+    const void* aff_ds; int aff_ds_stride, aff_ds_lo;
 } vdk_conv_desc;
 /* Host: re-order f16 conv weights [OC][KH][KW][IC] (IC % 16 == 0) into the
  * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */

@@ -169,6 +169,58 @@ def test_aff_local_att_and_combine():
     xv, dv, tv = cat[..., C:].astype(np.float64), cat[..., :C].astype(np.float64), gt.astype(np.float64)
     want = xv * (1 + tv) + dv * (1 - tv)            # the module's form x*x_att + ds*(2 - x_att)
     assert np.all(np.abs(gy - want) <= 2.0 ** -10 * np.abs(want) + 2e-3)
+    # the combine as the second conv's epilogue (aff_x / aff_ds): the same
+    # values with tanh's result kept in f32 instead of rounded to f16 first
+    y2 = lib.DeviceBuffer(B * H * T * C * 2)
+    d.y = y2.ptr
+    d.aff_x, d.aff_x_stride, d.aff_ds, d.aff_ds_stride = dcat.ptr + C * 2, 2 * C, dcat.ptr, 2 * C
+    lib.check(L.vdk_conv2d_ex(d, None))
+    lib.check(L.vdk_synchronize())
+    gf = y2.to_array(np.float16, (B, H, T, C)).astype(np.float64)
+    for c in (0, B - 1):
+        tf = np.tanh(O.conv2d_g(gz[c].astype(np.float32).transpose(2, 0, 1), w2.astype(np.float32), bias=b2,
+                                f64=True)).transpose(1, 2, 0)
+        wf = xv[c] * (1 + tf) + dv[c] * (1 - tf)
+        assert np.all(np.abs(gf[c] - wf) <= 2.0 ** -10 * np.abs(wf) + 2e-3)
+    assert np.abs(gf - gy).max() <= 2.0 ** -9 * np.abs(gy).max()
+
+
+def test_aff_combine_epilogue_split():
+    """The AFF combine in the second local_att conv's epilogue on split-f16
+    maps (x and ds as [ds | x] slices of one split tensor, as the cross-stage
+    AFF reads them) against the f64 module form, to split-f16 accuracy."""
+    rng = np.random.default_rng(105)
+    Bt, H, T, C, Z = 2, 20, 250, 64, 32
+    announce(f"eres aff combine epilogue split B={Bt} H={H} T={T} C={C}")
+    cat = rng.standard_normal((Bt, H, T, 2 * C)).astype(np.float32)              # [x | ds]
+    z = rng.standard_normal((Bt, H, T, Z)).astype(np.float32)
+    w = (rng.standard_normal((C, Z)) * np.sqrt(1.0 / Z)).astype(np.float16).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, C).astype(np.float32)
+    dcat = lib.DeviceBuffer.from_array(np.concatenate(_split(cat), axis=3))    # [hi 2C | lo 2C]
+    dz = lib.DeviceBuffer.from_array(np.concatenate(_split(z), axis=3))
+    wh = w.astype(np.float16)[:, None, None, :]
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(np.concatenate([wh, wh], axis=3))),
+            lib.DeviceBuffer.from_array(b)]
+    y = lib.DeviceBuffer(Bt * H * T * 2 * C * 2)
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride, d.x_lo = dz.ptr, Bt, H, T, Z, 2 * Z, Z
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, C, 1, 1
+    d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+    d.bias, d.act, d.tanh_after, d.split = keep[1].ptr, lib.ACT_NONE, 1, 2
+    d.y, d.y_stride, d.y_lo = y.ptr, 2 * C, C
+    d.aff_x, d.aff_x_stride, d.aff_x_lo = dcat.ptr, 4 * C, 2 * C
+    d.aff_ds, d.aff_ds_stride, d.aff_ds_lo = dcat.ptr + C * 2, 4 * C, 2 * C
+    d.tile = -1
+    lib.check(lib.lib().vdk_conv2d_ex(d, None))
+    lib.check(lib.lib().vdk_synchronize())
+    o = y.to_array(np.float16, (Bt, H, T, 2 * C))
+    got = o[..., :C].astype(np.float64) + o[..., C:].astype(np.float64)
+    t = np.tanh(z.astype(np.float64) @ w.T.astype(np.float64) + b)
+    xv, dv = cat[..., :C].astype(np.float64), cat[..., C:].astype(np.float64)
+    want = xv * (1 + t) + dv * (1 - t)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    announce(f"aff combine epilogue split: max err / max {err:.2e}")
+    assert err <= 2e-6
 
 
 def _split(a):

@@ -16,6 +16,7 @@
 //
 // stem_mfma_kernel: the IC=1 stem in f32 on v_mfma_f32_32x32x2_f32 (K = the 9
 // taps padded to 10); stem_conv3x3_kernel, the f32 FMA loop, serves OC = 16.
+#include <algorithm>
 #include <climits>
 #include <cstdlib>
 #include <type_traits>
@@ -58,6 +59,9 @@ struct ConvArgs {
     const uint8_t* wq;         // 1x1 weights as q8_0 blocks [OC][IC/32] x {f16 d, 32 x int8} (register-staged kernel)
     double* segsum;            // per-(clip, segment, OC) f64 sums of the stored outputs (may be NULL)
     int seg_len, seg_n;        // output columns per segment, segments per clip
+    const half_t* ax;          // AFF combine operands x, ds (may be NULL): v = (x + ds) + v * (x - ds)
+    const half_t* ads;
+    int axs, ax_lo, adss, ads_lo;
     int xgl = 4, ygl = 4;      // log2 of the channels per group of x / y (16 or 32)
     int xgs = 16, ygs = 16;    // elements between channel groups of x / y (= group size: contiguous)
 };
@@ -98,6 +102,18 @@ __device__ __forceinline__ void add_residual(const ConvArgs& a, int P, int oc, f
     }
 }
 
+// 8 f16 values at p (+ the lo halves at p + lo with split) as f32
+__device__ __forceinline__ void load8f(const half_t* p, int lo, int split, float* v) {
+    const half8 h = *reinterpret_cast<const half8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
+    if (split) {
+        const half8 l = *reinterpret_cast<const half8*>(p + lo);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += (float)l[e];
+    }
+}
+
 __device__ __forceinline__ void epi8(const ConvArgs& a, int P, int oc, float* v) {
     const int HoWo = a.Ho * a.Wo;
     if (a.bias) add8(v, a.bias + oc + (a.bias_bs ? (size_t)(P / HoWo) * a.bias_bs : 0));
@@ -131,6 +147,13 @@ __device__ __forceinline__ void epi8(const ConvArgs& a, int P, int oc, float* v)
     if (a.tanh_after) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = tanhf(v[e]);
+    }
+    if (a.ax) {
+        float xv[8], dv[8];
+        load8f(a.ax + (size_t)P * a.axs + oc, a.ax_lo, a.split, xv);
+        load8f(a.ads + (size_t)P * a.adss + oc, a.ads_lo, a.split, dv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (xv[e] + dv[e]) + v[e] * (xv[e] - dv[e]);
     }
 }
 
@@ -2511,7 +2534,7 @@ constexpr int kFirstDma = 14;   // then the halo tiles from 26, 8-wave DMA tiles
 // The register-weight kernels take the plain epilogue only: bias, residual,
 // ReLU or none, dense f16 NHWC in and out.
 bool plain_epilogue(const ConvArgs& a) {
-    return !a.gate && !a.post_scale && !a.tanh_after && !a.y_f32 && !a.y_tr && !a.bias_bs && !a.split &&
+    return !a.gate && !a.post_scale && !a.tanh_after && !a.ax && !a.y_f32 && !a.y_tr && !a.bias_bs && !a.split &&
            (a.act == VDK_ACT_NONE || (a.act == VDK_ACT_RELU && a.clamp_hi <= 0.0f)) && a.xs == a.IC &&
            a.ys == a.OC && (!a.res || a.rs == a.OC) && !a.res_f32 && !a.res_after && !a.y2 && !a.reflect;
 }
@@ -2521,7 +2544,7 @@ bool plain_epilogue(const ConvArgs& a) {
 // planes, 8-byte aligned output ones, byte offsets within 31 bits.
 bool split_epilogue(const ConvArgs& a) {
     const auto al = [](const void* p, int n) { return ((uintptr_t)p & (uintptr_t)(n - 1)) == 0; };
-    return a.split == 2 && !a.gate && !a.post_scale && !a.tanh_after && !a.y_f32 && !a.y_tr && !a.bias_bs &&
+    return a.split == 2 && !a.gate && !a.post_scale && !a.tanh_after && !a.ax && !a.y_f32 && !a.y_tr && !a.bias_bs &&
            (a.act == VDK_ACT_NONE || a.act == VDK_ACT_RELU) && !a.res && !a.y2 && !a.reflect && !a.in_scale &&
            !a.segsum && !a.wq && a.xs % 8 == 0 && a.x_lo % 8 == 0 && a.ys % 4 == 0 && a.y_lo % 4 == 0 &&
            al(a.x, 16) && al(a.y, 8) && al(a.w, 16) && al(a.wc, 16) && al(a.bias, 4) &&
@@ -2898,7 +2921,19 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
                                (reinterpret_cast<uintptr_t>(d.w_q8_0) & 3) == 0 &&
                                (long)d.OC * (d.IC / 32) * 34 < (1L << 31)),
                 "conv2d: q8_0 weights are for 1x1 convs with IC % 32 == 0 and no split-f16");
+        require(!d.aff_x == !d.aff_ds, "conv2d: aff_x and aff_ds go together");
+        const int axs = d.aff_x_stride ? d.aff_x_stride : d.OC, adss = d.aff_ds_stride ? d.aff_ds_stride : d.OC;
+        require(!d.aff_x || (!d.y_f32 && !d.y_time_major && !d.y2 && !yg && aligned16(d.aff_x) && aligned16(d.aff_ds) &&
+                             axs >= d.OC && adss >= d.OC && axs % 8 == 0 && adss % 8 == 0 &&
+                             (!d.split || (d.aff_x_lo >= d.OC && d.aff_ds_lo >= d.OC && d.aff_x_lo % 8 == 0 &&
+                                           d.aff_ds_lo % 8 == 0)) &&
+                             (long)d.batch * Ho * Wo * std::max(axs, adss) < (1L << 31)),
+                "conv2d: the AFF combine needs x and ds at the output's pixels (16-byte aligned, strides >= OC, "
+                "lo offsets past the channels with split) and an f16 NHWC output");
         ConvArgs a{};
+        a.ax = static_cast<const half_t*>(d.aff_x);
+        a.ads = static_cast<const half_t*>(d.aff_ds);
+        a.axs = axs; a.adss = adss; a.ax_lo = d.aff_x_lo; a.ads_lo = d.aff_ds_lo;
         a.wq = static_cast<const uint8_t*>(d.w_q8_0);
         require(!d.seg_sum || (Ho == 1 && d.seg_len > 0 && !d.split && !d.y_f32 && !d.y_time_major && !d.y2 &&
                                (reinterpret_cast<uintptr_t>(d.seg_sum) & 7) == 0),
@@ -3001,6 +3036,8 @@ ConvArgs shape_args(const vdk_conv_desc& d) {
     a.wq = static_cast<const uint8_t*>(d.w_q8_0);
     a.segsum = d.seg_sum;
     a.seg_len = d.seg_sum && d.seg_len > 0 ? d.seg_len : 1;
+    a.ax = static_cast<const half_t*>(d.aff_x);
+    a.ads = static_cast<const half_t*>(d.aff_ds);
     a.xgl = d.x_group == 32 ? 5 : 4;
     a.ygl = d.y_group == 32 ? 5 : 4;
     a.xgs = d.x_group_stride ? d.x_group_stride : 1 << a.xgl;

@@ -280,7 +280,7 @@ private:
         double* segsum[2] = {nullptr, nullptr};   // per-(clip, segment) sums of linear1's output, two layers' worth
         size_t segsum_bytes = 0;
         // ERes2Net
-        void *ex[2] = {nullptr, nullptr}, *es4 = nullptr, *esc = nullptr, *ez = nullptr, *ez2 = nullptr,
+        void *ex[2] = {nullptr, nullptr}, *es4 = nullptr, *esc = nullptr, *ez = nullptr,
              *ef = nullptr;
         void *ecat[3] = {nullptr, nullptr, nullptr}, *efuse[3] = {nullptr, nullptr, nullptr};
         // wav2vec2

@@ -236,7 +236,6 @@ void Model::alloc_eres2net_workspace(int batch, int T) {
     w.esc = ws_alloc(4 * x_max);
     w.es4 = ws_alloc(4 * s4_max);
     w.ez = ws_alloc(4 * std::max<size_t>(z_max, 8));
-    w.ez2 = ws_alloc(4 * std::max<size_t>(z_max, 8));
     w.ef = ws_alloc(4 * std::max<size_t>(f_max, 8));
     w.fc_work_bytes = vdk_linear_workspace_size(batch, pooled_dim_, cfg_.embedding_dim);
     w.fc_work = ws_alloc(w.fc_work_bytes);
@@ -245,6 +244,8 @@ void Model::alloc_eres2net_workspace(int batch, int T) {
 void Model::encode_eres2net(int batch, int T) {
     const Eres2net& m = eres_;
     Workspace& w = ws_;
+    const View* aff_x = nullptr;    // AFF combine operands of the next conv (the second local_att conv)
+    const View* aff_ds = nullptr;
     auto conv = [&](const char* name, const Layer& l, View x, int H, int W, int stride, const View* res, int act,
                     float clamp, int tanh_after, View y) {
         vdk_conv_desc d{};
@@ -261,18 +262,23 @@ void Model::encode_eres2net(int batch, int T) {
         d.y = y.p; d.y_stride = y.stride;
         d.split = l.split; d.x_lo = x.lo; d.y_lo = y.lo;
         d.x_group = x.gn; d.x_group_stride = x.gs; d.y_group = y.gn; d.y_group_stride = y.gs;
+        if (aff_x) {
+            d.aff_x = aff_x->p; d.aff_x_stride = aff_x->stride; d.aff_x_lo = aff_x->lo;
+            d.aff_ds = aff_ds->p; d.aff_ds_stride = aff_ds->stride; d.aff_ds_lo = aff_ds->lo;
+        }
         d.tile = -1;
         conv_ex(name, d);
     };
-    // AFF(x, ds): local_att over the [.. 2C] input `cat`, then the combine into y
+    // AFF(x, ds): local_att over the [.. 2C] input `cat`; the second conv's
+    // epilogue applies tanh and the combine (x + ds) + t * (x - ds) into y
     auto aff = [&](const char* name, const EresAff& a, View cat, View x, View ds, int C, int H, int W, View y) {
-        const View z = split_tensor(w.ez, a.c1.oc), z2 = split_tensor(w.ez2, C);
+        const View z = split_tensor(w.ez, a.c1.oc);
         conv(name, a.c1, cat, H, W, 1, nullptr, VDK_ACT_SILU, 0.0f, 0, z);
-        conv(name, a.c2, z, H, W, 1, nullptr, VDK_ACT_NONE, 0.0f, 1, z2);
-        prof_begin("eres_aff_combine", 0.0, 16.0 * batch * (double)H * W * C);
-        check_rc(vdk_aff_combine(z2.p, z2.stride, z2.lo, x.p, x.stride, x.lo, ds.p, ds.stride, ds.lo,
-                                 (long)batch * H * W, C, 1, y.p, y.stride, y.lo, stream_));
-        prof_end();
+        require(x.gs == x.gn && ds.gs == ds.gn, "voicedetect: eres2net AFF operands are contiguous split tensors");
+        aff_x = &x;
+        aff_ds = &ds;
+        conv(name, a.c2, z, H, W, 1, nullptr, VDK_ACT_NONE, 0.0f, 1, y);
+        aff_x = aff_ds = nullptr;
     };
 
     int H = m.n_mels, W = T;

@@ -48,7 +48,8 @@ class ConvDesc(C.Structure):
                 ("reflect_pad", C.c_int), ("y2", _vp), ("y2_stride", C.c_int), ("res2", _vp),
                 ("res2_stride", C.c_int), ("w_q8_0", _vp), ("seg_sum", _vp), ("seg_len", C.c_int),
                 ("x_group_stride", C.c_int), ("y_group_stride", C.c_int), ("x_group", C.c_int),
-                ("y_group", C.c_int)]
+                ("y_group", C.c_int), ("aff_x", _vp), ("aff_x_stride", C.c_int), ("aff_x_lo", C.c_int),
+                ("aff_ds", _vp), ("aff_ds_stride", C.c_int), ("aff_ds_lo", C.c_int)]
 
 
 def fbank_cfg(n_mels=80, n_fft=512, win=400, hop=160, preemph=0.97, low=20.0, high=0.0, cmn=True,
