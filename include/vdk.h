@@ -390,6 +390,18 @@ int vdk_res2_pair3x3(const void* d_x, int x_stride, void* d_y, int y_stride, int
                      const void* d_w_a, const float* d_b_a, const void* d_w_b, const float* d_b_b, float clamp_hi,
                      void* stream);
 
+/* vdk_res2_pair3x3 followed by the block's conv3 in the same launch, sp0 and
+ * sp1 never stored: y = min(relu(conv3([sp0 | sp1]) + b3 + res), clamp_hi),
+ * 64 output channels, split-f16 (y and res: rows of *_stride elements, the
+ * 64 hi halves first and the lo halves *_lo elements after them).  w3: the
+ * split-f16 weights [64][terms3 * 32] as vdk_conv_desc takes them ([hi | hi]
+ * for terms3 = 2, [hi | hi | lo] for 3).  Equal bit for bit to
+ * vdk_res2_pair3x3 then vdk_conv2d_ex's LDS-DMA kernel over [sp0 | sp1]. */
+int vdk_res2_pair3x3_conv3(const void* d_x, int x_stride, int batch, int H, int W, const void* d_w_a,
+                           const float* d_b_a, const void* d_w_b, const float* d_b_b, const void* d_w3,
+                           const float* d_b3, int terms3, const void* d_res, int res_stride, int res_lo, void* d_y,
+                           int y_stride, int y_lo, float clamp_hi, void* stream);
+
 /* ---- wav2vec2 analyze (src/analyze_w2v2.cpp) ----
  * Activations are time-major [B][T][C]; the GEMM-shaped layers run on
  * vdk_conv2d_ex (H = 1, W = T).  These cover the rest of the graph. */

@@ -573,3 +573,58 @@ def test_res2_pair_equals_two_convs(Bt, H, T):
         err1 = np.abs(sp[ci, :, :, 16:].transpose(2, 0, 1) - s1).max() / np.abs(s1).max()
         announce(f"res2 pair clip {ci}: sp0 err {err0:.2e}, sp1 err {err1:.2e}")
         assert err0 <= 2e-6 and err1 <= 4e-6
+
+
+@pytest.mark.parametrize("Bt,H,T,terms,tile", [(2, 42, 301, 3, 16), (2, 42, 301, 2, -1), (B, 80, T20S, 3, -1)])
+def test_res2_pair_conv3_equals_pair_then_conv3(Bt, H, T, terms, tile):
+    """The Res2Net pair with the block's conv3 fused (sp0, sp1 kept on chip)
+    equals the pair followed by the LDS-DMA conv3 over [sp0 | sp1] (split-f16
+    weights of two or three terms, bias, split residual, ReLU, clamp) bit for
+    bit, at partial tiles and at the 80 x 1998 layer-1 map."""
+    rng = np.random.default_rng(1990 + H + terms)
+    announce(f"eres res2 pair + conv3 B={Bt} H={H} T={T} terms={terms} tile={tile}")
+    c = rng.standard_normal((Bt, H, T, 32)).astype(np.float32) * 3
+    rows = np.zeros((Bt, H, T, 128), np.float16)
+    rows[..., :64] = _grouped(c, 2)
+    res = rng.standard_normal((Bt, H, T, 64)).astype(np.float32) * 2
+    wa = (rng.standard_normal((16, 16, 3, 3)) * np.sqrt(2.0 / 144)).astype(np.float16)
+    wb = (rng.standard_normal((16, 16, 3, 3)) * np.sqrt(2.0 / 144)).astype(np.float16)
+    ba = rng.uniform(-0.5, 0.5, 16).astype(np.float32)
+    bb = rng.uniform(-0.5, 0.5, 16).astype(np.float32)
+    w3 = (rng.standard_normal((64, 32)) * np.sqrt(2.0 / 32)).astype(np.float32)
+    if terms == 2:
+        w3 = w3.astype(np.float16).astype(np.float32)
+    w3h, w3l = _split(w3)
+    w3p = np.ascontiguousarray(np.concatenate([w3h, w3h, w3l] if terms == 3 else [w3h, w3h], axis=1))
+    b3 = rng.uniform(-0.5, 0.5, 64).astype(np.float32)
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(wa.transpose(0, 2, 3, 1))), lib.DeviceBuffer.from_array(ba),
+            lib.DeviceBuffer.from_array(np.ascontiguousarray(wb.transpose(0, 2, 3, 1))), lib.DeviceBuffer.from_array(bb),
+            lib.DeviceBuffer.from_array(w3p), lib.DeviceBuffer.from_array(b3),
+            lib.DeviceBuffer.from_array(np.concatenate(_split(res), axis=3))]
+    L = lib.lib()
+    # the pair into groups 2, 3, then conv3 from them
+    d1 = lib.DeviceBuffer.from_array(rows)
+    lib.check(L.vdk_res2_pair3x3(d1.ptr, 128, d1.ptr + 64 * 2, 128, Bt, H, T, keep[0].ptr, keep[1].ptr, keep[2].ptr,
+                                 keep[3].ptr, 20.0, None))
+    y1 = lib.DeviceBuffer(Bt * H * T * 128 * 2)
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = d1.ptr + 64 * 2, Bt, H, T, 32, 128
+    d.x_lo, d.x_group_stride = 16, 32
+    d.w, d.OC, d.KH, d.KW = keep[4].ptr, 64, 1, 1
+    d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+    d.bias, d.act, d.clamp_hi = keep[5].ptr, lib.ACT_RELU, 20.0
+    d.residual, d.res_stride, d.res_lo = keep[6].ptr, 128, 64
+    d.y, d.y_stride, d.y_lo = y1.ptr, 128, 64
+    d.split, d.tile = (1 if terms == 3 else 2), tile
+    lib.check(L.vdk_conv2d_ex(d, None))
+    # fused
+    d2 = lib.DeviceBuffer.from_array(rows)
+    y2 = lib.DeviceBuffer(Bt * H * T * 128 * 2)
+    lib.check(L.vdk_res2_pair3x3_conv3(d2.ptr, 128, Bt, H, T, keep[0].ptr, keep[1].ptr, keep[2].ptr, keep[3].ptr,
+                                       keep[4].ptr, keep[5].ptr, terms, keep[6].ptr, 128, 64, y2.ptr, 128, 64, 20.0,
+                                       None))
+    lib.check(L.vdk_synchronize())
+    a = y1.to_array(np.float16, (Bt, H, T, 128))
+    b = y2.to_array(np.float16, (Bt, H, T, 128))
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    assert np.array_equal(d2.to_array(np.float16, (Bt, H, T, 128)).view(np.uint16), rows.view(np.uint16))

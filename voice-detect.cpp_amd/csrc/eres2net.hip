@@ -136,13 +136,30 @@ __device__ __forceinline__ void split_relu_clamp(const float4v& acc, const float
     }
 }
 
+// The block's conv3 (1x1 over [sp0 | sp1] -> 64 channels, split-f16 weights
+// [hi | hi (| lo)] per input channel, bias, + residual, ReLU, clamp) fused
+// after conv_b: sp1 goes to LDS instead of memory, and wave w computes output
+// row w/2, channels 32 (w%2) .. on 32x32x16 MFMAs in the LDS-DMA kernel's
+// order (K chunks hi.w_hi, lo.w_hi [, hi.w_lo], each sp0 then sp1) with its
+// epilogue (+ bias, + residual hi, + lo, ReLU, clamp), so y equals the pair
+// followed by that conv bit for bit.
+struct PairConv3 {
+    const half_t* w;          // [64][terms * 32]
+    const float* b;
+    int terms;
+    const half_t* res; int rs, r_lo;
+    half_t* y; int ys, y_lo;
+};
+
+template <bool C3>
 __global__ __launch_bounds__(pair::NW * 64) void res2_pair_kernel(
     const half_t* __restrict__ x, int xs, half_t* __restrict__ y, int ys, const half_t* __restrict__ wa,
     const float* __restrict__ ba, const half_t* __restrict__ wb, const float* __restrict__ bb, float chi, int H,
-    int W, int npix, int ntiles, int per_wg) {
+    int W, int npix, int ntiles, int per_wg, PairConv3 c3) {
     using namespace pair;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
     __shared__ __attribute__((aligned(16))) uint8_t inter[INTER_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t s1t[C3 ? TH * 32 * RBT : 16];   // sp1 rows [hi 16 | lo 16]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t_begin = blockIdx.x * per_wg;
@@ -187,6 +204,21 @@ __global__ __launch_bounds__(pair::NW * 64) void res2_pair_kernel(
         bva[e] = ba ? ba[kg * 4 + e] : 0.0f;
         bvb[e] = bb ? bb[kg * 4 + e] : 0.0f;
     }
+    // conv3: wave w -> output row w / 2, channels 32 (w % 2) ..; K steps (term t, half h)
+    const int l32 = lane & 31, lh = lane >> 5, ob = wave & 1, crow = wave >> 1;
+    half8 f3[6];
+    float bv3[16];
+    if constexpr (C3) {
+        const int icw = c3.terms * 32;
+#pragma unroll
+        for (int st = 0; st < 6; ++st)
+            if (st < c3.terms * 2)
+                f3[st] = *reinterpret_cast<const half8*>(c3.w + (size_t)(ob * 32 + l32) * icw + st * 16 + lh * 8);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bv3[g * 4 + e] = c3.b ? c3.b[ob * 32 + g * 8 + lh * 4 + e] : 0.0f;
+    }
     __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
     for (int s = 1; s + 1 < NS; ++s)
@@ -207,6 +239,20 @@ __global__ __launch_bounds__(pair::NW * 64) void res2_pair_kernel(
         const PairDma nd(ring + prev * STAGE, k, t + NS - 1, wave, t + NS - 1 < t_end);
         const int th = t % k.tiles_h, rr = t / k.tiles_h, tw = rr % k.tiles_w, b = rr / k.tiles_w;
         const int oh0 = th * TH, ow0 = tw * TW;
+        // conv3's residual for this wave's 32 outputs, loaded before the next
+        // tiles' DMA goes out (a later load would wait for that DMA too)
+        const int c3h = oh0 + crow, c3w = ow0 + l32;
+        const bool ok = C3 && l32 < TW && c3h < H && c3w < W;
+        const size_t P = (size_t)(b * H + (ok ? c3h : 0)) * W + (ok ? c3w : 0);
+        half4 rh[4], rl[4];
+        if constexpr (C3) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int oc = ob * 32 + g * 8 + lh * 4;
+                rh[g] = *reinterpret_cast<const half4*>(c3.res + P * c3.rs + oc);
+                rl[g] = *reinterpret_cast<const half4*>(c3.res + P * c3.rs + c3.r_lo + oc);
+            }
+        }
 
         // conv_a over the sp0 region: block j = row j/2, columns 16*(j%2) ..
         // (the B reads run PD steps ahead of the MFMAs)
@@ -253,7 +299,7 @@ __global__ __launch_bounds__(pair::NW * 64) void res2_pair_kernel(
             uint8_t* const tp = inter + (r * IW + col) * RBT + kg * 8;
             *reinterpret_cast<half4*>(tp) = h;
             *reinterpret_cast<half4*>(tp + 32) = l;
-            if (in && r >= 1 && r <= TH && col >= 1 && col <= TW) {
+            if (!C3 && in && r >= 1 && r <= TH && col >= 1 && col <= TW) {
                 half_t* const yp = y + ((size_t)(b * H + gh) * W + gw) * ys + kg * 4;
                 *reinterpret_cast<half4*>(yp) = h;
                 *reinterpret_cast<half4*>(yp + 16) = l;
@@ -300,18 +346,68 @@ __global__ __launch_bounds__(pair::NW * 64) void res2_pair_kernel(
         // tile t+1's loads have landed (this wave's): only tile t+2's may be in flight
         const int last = t + NS - 1 < t_end - 1 ? t + NS - 1 : t_end - 1;
         wait_vm_le(last > t + 1 ? (last - t - 1) * per_tile : 0);
+        if constexpr (!C3) {
 #pragma unroll
-        for (int q = 0; q < BPB; ++q) {
-            const int j = wave + q * NW;
-            if (j >= NBB) continue;
-            const int i = j >> 1, c = (j & 1) * 16 + lp;
-            const int oh = oh0 + i, ow = ow0 + c;
-            if (c >= TW || oh >= H || ow >= W) continue;
-            half4 h, l;
-            split_relu_clamp(cb[q], bvb, chi, h, l);
-            half_t* const yp = y + ((size_t)(b * H + oh) * W + ow) * ys + 32 + kg * 4;
-            *reinterpret_cast<half4*>(yp) = h;
-            *reinterpret_cast<half4*>(yp + 16) = l;
+            for (int q = 0; q < BPB; ++q) {
+                const int j = wave + q * NW;
+                if (j >= NBB) continue;
+                const int i = j >> 1, c = (j & 1) * 16 + lp;
+                const int oh = oh0 + i, ow = ow0 + c;
+                if (c >= TW || oh >= H || ow >= W) continue;
+                half4 h, l;
+                split_relu_clamp(cb[q], bvb, chi, h, l);
+                half_t* const yp = y + ((size_t)(b * H + oh) * W + ow) * ys + 32 + kg * 4;
+                *reinterpret_cast<half4*>(yp) = h;
+                *reinterpret_cast<half4*>(yp + 16) = l;
+            }
+        } else {
+            // sp1 of the tile's 4 x 32 pixels (columns 30, 31 unused) into LDS
+#pragma unroll
+            for (int q = 0; q < BPB; ++q) {
+                const int j = wave + q * NW;
+                if (j >= NBB) continue;
+                const int i = j >> 1, c = (j & 1) * 16 + lp;
+                half4 h, l;
+                split_relu_clamp(cb[q], bvb, chi, h, l);
+                uint8_t* const tp = s1t + (i * 32 + c) * RBT + kg * 8;
+                *reinterpret_cast<half4*>(tp) = h;
+                *reinterpret_cast<half4*>(tp + 32) = l;
+            }
+            lds_barrier();
+            float16v a3;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) a3[e] = 0.0f;
+            // B: output pixel (crow, l32): sp0 at region (crow + 1, l32 + 1), sp1 at tile (crow, l32)
+            const uint8_t* const b0 = inter + ((crow + 1) * IW + l32 + 1) * RBT + lh * 16;
+            const uint8_t* const b1 = s1t + (crow * 32 + l32) * RBT + lh * 16;
+#pragma unroll
+            for (int st = 0; st < 6; ++st) {
+                if (st >= c3.terms * 2) break;
+                const int term = st >> 1, half = st & 1;
+                const int po = term == 1 ? 32 : 0;   // term 1 multiplies the lo halves
+                const half8 bf = *reinterpret_cast<const half8*>((half ? b1 : b0) + po);
+                a3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f3[st], bf, a3, 0, 0, 0);
+            }
+            if (ok) {
+                half_t* const yp = c3.y + P * c3.ys;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int oc = ob * 32 + g * 8 + lh * 4;
+                    half4 h, l;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float v = a3[g * 4 + e] + bv3[g * 4 + e];
+                        v += (float)rh[g][e];
+                        v += (float)rl[g][e];
+                        v = fmaxf(v, 0.0f);
+                        if (chi > 0.0f) v = fminf(v, chi);
+                        h[e] = (half_t)v;
+                        l[e] = (half_t)(v - (float)h[e]);
+                    }
+                    *reinterpret_cast<half4*>(yp + oc) = h;
+                    *reinterpret_cast<half4*>(yp + c3.y_lo + oc) = l;
+                }
+            }
         }
         slot = slot + 1 == NS ? 0 : slot + 1;
     }
@@ -368,10 +464,39 @@ extern "C" int vdk_res2_pair3x3(const void* d_x, int x_stride, void* d_y, int y_
                 "res2_pair3x3: map too large for one launch");
         const int ntiles = batch * cdiv(H, pair::TH) * cdiv(W, pair::TW);
         const int per = cdiv(ntiles, cu_count());
-        hipLaunchKernelGGL(res2_pair_kernel, dim3(cdiv(ntiles, per)), dim3(pair::NW * 64), 0,
+        hipLaunchKernelGGL(res2_pair_kernel<false>, dim3(cdiv(ntiles, per)), dim3(pair::NW * 64), 0,
                            static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride,
                            static_cast<half_t*>(d_y), y_stride, static_cast<const half_t*>(d_wa), d_ba,
-                           static_cast<const half_t*>(d_wb), d_bb, clamp_hi, H, W, (int)npix, ntiles, per);
+                           static_cast<const half_t*>(d_wb), d_bb, clamp_hi, H, W, (int)npix, ntiles, per,
+                           PairConv3{});
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_res2_pair3x3_conv3(const void* d_x, int x_stride, int batch, int H, int W, const void* d_wa,
+                                      const float* d_ba, const void* d_wb, const float* d_bb, const void* d_w3,
+                                      const float* d_b3, int terms3, const void* d_res, int res_stride, int res_lo,
+                                      void* d_y, int y_stride, int y_lo, float clamp_hi, void* stream) {
+    return guarded([&] {
+        require(d_x && d_wa && d_wb && d_w3 && d_res && d_y, "res2_pair3x3_conv3: NULL device pointer");
+        require(batch > 0 && H > 0 && W > 0, "res2_pair3x3_conv3: empty map");
+        require(terms3 == 2 || terms3 == 3, "res2_pair3x3_conv3: conv3 weights have 2 or 3 terms");
+        require(x_stride >= 64 && x_stride % 8 == 0 && res_stride >= 64 && res_stride % 4 == 0 && res_lo >= 64 &&
+                    res_lo % 4 == 0 && y_stride >= 64 && y_stride % 4 == 0 && y_lo >= 64 && y_lo % 4 == 0,
+                "res2_pair3x3_conv3: strides / lo offsets must hold the 64 channels and keep 8-byte alignment");
+        require(al16(d_x) && al16(d_wa) && al16(d_wb) && al16(d_w3) && al16(d_ba) && al16(d_bb) && al16(d_b3) &&
+                    (reinterpret_cast<uintptr_t>(d_res) & 7) == 0 && (reinterpret_cast<uintptr_t>(d_y) & 7) == 0,
+                "res2_pair3x3_conv3: x / weights / biases 16-byte, residual / y 8-byte aligned");
+        const long npix = (long)batch * H * W;
+        require(npix * x_stride * 2 < (1L << 31) && W < 8192, "res2_pair3x3_conv3: map too large for one launch");
+        const int ntiles = batch * cdiv(H, pair::TH) * cdiv(W, pair::TW);
+        const int per = cdiv(ntiles, cu_count());
+        PairConv3 c3{static_cast<const half_t*>(d_w3), d_b3, terms3, static_cast<const half_t*>(d_res), res_stride,
+                     res_lo, static_cast<half_t*>(d_y), y_stride, y_lo};
+        hipLaunchKernelGGL(res2_pair_kernel<true>, dim3(cdiv(ntiles, per)), dim3(pair::NW * 64), 0,
+                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, nullptr, 0,
+                           static_cast<const half_t*>(d_wa), d_ba, static_cast<const half_t*>(d_wb), d_bb, clamp_hi,
+                           H, W, (int)npix, ntiles, per, c3);
         VDK_HIP(hipGetLastError());
     });
 }

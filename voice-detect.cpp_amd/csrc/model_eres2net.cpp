@@ -300,28 +300,7 @@ void Model::encode_eres2net(int batch, int T) {
                                                              : split_tensor(w.es4, 4 * wd);
             // conv1 -> [chunk0 | chunk1]
             conv("eres_conv1", b.conv1, x, H, W, b.stride, nullptr, VDK_ACT_RELU, hi, 0, s4);
-            if (b.pair_a && s4.gn == 16) {
-                // chunk 0 -> sp0 and chunk 1 (+ sp0) -> sp1 in one launch
-                // MFMA work: conv_a 16 x 16 x 9 over both planes, conv_b the same twice (c1, sp0)
-                prof_begin("eres_res2_pair", 2.0 * 9 * 16 * 16 * 2 * 3 * (double)batch * Ho * Wo,
-                           2.0 * 2 * 64 * (double)batch * Ho * Wo);
-                check_rc(vdk_res2_pair3x3(s4.p, s4.stride, s4.at(2 * wd).p, s4.stride, batch, Ho, Wo, b.pair_a,
-                                          b.conv_a.b, b.pair_b, b.conv_b.b, hi, stream_));
-                prof_end();
-            } else {
-                // chunk 0 -> sp0
-                conv("eres_conv3x3", b.conv_a, s4, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(2 * wd));
-                // chunk 1 -> sp1
-                if (b.aff) {
-                    const View f = split_tensor(w.ef, wd);
-                    aff("eres_aff_block", b.fuse, s4.at(wd), s4.at(2 * wd), s4.at(wd), wd, Ho, Wo, f);
-                    conv("eres_conv3x3", b.conv_b, f, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(3 * wd));
-                } else {
-                    conv("eres_conv3x3", b.conv_b, s4.at(wd), Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0,
-                         s4.at(3 * wd));
-                }
-            }
-            // shortcut, then conv3 + residual -> clamp
+            // the shortcut (its input is the block input: independent of the chunks)
             View res = x;
             if (b.has_sc) {
                 res = split_tensor(w.esc, 2 * b.planes);
@@ -329,7 +308,44 @@ void Model::encode_eres2net(int batch, int T) {
             }
             const bool last = bi == nb - 1 && li >= 1;
             const View y = last ? split_tensor(w.ecat[li - 1], 4 * b.planes) : split_tensor(w.ex[xi ^ 1], 2 * b.planes);
-            conv("eres_conv3", b.conv3, s4.at(2 * wd), Ho, Wo, 1, &res, VDK_ACT_RELU, hi, 0, y);
+            const bool pair = b.pair_a && s4.gn == 16;
+            if (pair && b.conv3.kh * b.conv3.k == 1 && b.conv3.ic == 32 && b.conv3.oc == 64 && y.gs == y.gn &&
+                res.gs == res.gn) {
+                // chunk 0 -> sp0, chunk 1 (+ sp0) -> sp1 and conv3 + residual -> clamp in one launch
+                // (MFMA work: conv_a 16 x 16 x 9 over both planes, conv_b twice that, conv3 64 x 32 per term)
+                const int terms = b.conv3.split == 2 ? 2 : 3;
+                prof_begin("eres_res2_block",
+                           2.0 * ((double)9 * 16 * 16 * 2 * 3 + 64.0 * 32 * terms) * batch * Ho * Wo,
+                           2.0 * (2 * 32 + 2 * 64 + 2 * 64) * (double)batch * Ho * Wo);
+                check_rc(vdk_res2_pair3x3_conv3(s4.p, s4.stride, batch, Ho, Wo, b.pair_a, b.conv_a.b, b.pair_b,
+                                                b.conv_b.b, b.conv3.w, b.conv3.b, terms, res.p, res.stride, res.lo,
+                                                y.p, y.stride, y.lo, hi, stream_));
+                prof_end();
+            } else {
+                if (pair) {
+                    // chunk 0 -> sp0 and chunk 1 (+ sp0) -> sp1 in one launch
+                    // MFMA work: conv_a 16 x 16 x 9 over both planes, conv_b the same twice (c1, sp0)
+                    prof_begin("eres_res2_pair", 2.0 * 9 * 16 * 16 * 2 * 3 * (double)batch * Ho * Wo,
+                               2.0 * 2 * 64 * (double)batch * Ho * Wo);
+                    check_rc(vdk_res2_pair3x3(s4.p, s4.stride, s4.at(2 * wd).p, s4.stride, batch, Ho, Wo, b.pair_a,
+                                              b.conv_a.b, b.pair_b, b.conv_b.b, hi, stream_));
+                    prof_end();
+                } else {
+                    // chunk 0 -> sp0
+                    conv("eres_conv3x3", b.conv_a, s4, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(2 * wd));
+                    // chunk 1 -> sp1
+                    if (b.aff) {
+                        const View f = split_tensor(w.ef, wd);
+                        aff("eres_aff_block", b.fuse, s4.at(wd), s4.at(2 * wd), s4.at(wd), wd, Ho, Wo, f);
+                        conv("eres_conv3x3", b.conv_b, f, Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0, s4.at(3 * wd));
+                    } else {
+                        conv("eres_conv3x3", b.conv_b, s4.at(wd), Ho, Wo, 1, nullptr, VDK_ACT_RELU, hi, 0,
+                             s4.at(3 * wd));
+                    }
+                }
+                // conv3 + residual -> clamp
+                conv("eres_conv3", b.conv3, s4.at(2 * wd), Ho, Wo, 1, &res, VDK_ACT_RELU, hi, 0, y);
+            }
             if (!last) xi ^= 1;
             x = y;
             H = Ho;
