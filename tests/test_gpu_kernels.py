@@ -217,6 +217,31 @@ def test_conv_register_weight_tiles_plain_epilogues(case):
 
 
 @pytest.mark.parametrize("case", [
+    # (B, H, W, C, residual, relu): ResNet34's 128- and 256-channel maps at
+    # batch 1 and 3 (ragged last band), with and without residual
+    (1, 20, 75, 128, True, True), (3, 20, 75, 128, False, True), (2, 17, 61, 128, True, False),
+    (1, 10, 38, 256, True, True), (3, 7, 38, 256, False, True),
+])
+def test_one_row_band_tiles_equal_five_row_bands(case):
+    """Tiles 76-79 (one-row bands, picked for small batches) give the 5-row band
+    kernel's bits: each output's sum runs over the same chunks and taps in the
+    same order, so batch-1 and batch-64 embeddings stay bit-identical."""
+    B, H, W, C, with_res, relu = case
+    rng = np.random.default_rng(B * 100 + H + C)
+    x = rng.standard_normal((B, H, W, C)).astype(np.float16)
+    w = (rng.standard_normal((C, C, 3, 3)) * np.sqrt(2.0 / (9 * C))).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, C).astype(np.float32)
+    res = rng.standard_normal((B, H, W, C)).astype(np.float16) if with_res else None
+    base = 64 if C == 128 else 65
+    ref = conv_gpu(x, w, b, res, 1, 1, relu, tile=base)
+    for t in ((76, 77) if C == 128 else (78, 79)):
+        announce(f"one-row band tile {t} case {case}")
+        got = conv_gpu(x, w, b, res, 1, 1, relu, tile=t)
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), f"tile {t} differs from tile {base}"
+    assert np.array_equal(conv_gpu(x, w, b, res, 1, 1, relu).view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("case", [
     # (B, H, W, C, residual): enough tiles that each persistent workgroup
     # walks several, with walk lengths of every remainder modulo the ring
     # depths across the cases (13, 4, 5, 8 and 2 tiles per workgroup for the

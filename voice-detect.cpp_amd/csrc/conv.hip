@@ -2441,7 +2441,9 @@ struct TileCfg {
 // narrow LDS-DMA tiles, 62-63 narrow register-staged tiles, 64-65 the band
 // kernel with producer / compute waves (128-channel groups, maps up to 75 /
 // 38 wide), 66-69 the register-weight kernel with 3- and 4-stage rings,
-// 70-75 the split-f16 register-weight kernel (ERes2Net's group convs).
+// 70-75 the split-f16 register-weight kernel (ERes2Net's group convs), 76-79
+// the producer / compute band kernel on one-row bands (the same sums in the
+// same order as its 5-row bands, so the same bits, on 5x the workgroups).
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -2522,6 +2524,10 @@ const TileCfg kTiles[] = {
     {32, 64, 64, launch_sp<64, 32, 2, 4, 4, true>, true, 0, 0, 64},     // 73
     {32, 128, 64, launch_sp<64, 32, 4, 4, 2, false>, true, 0, 0, 64},   // 74
     {64, 128, 64, launch_sp<64, 64, 4, 8, 2, false>, true, 0, 0, 64},   // 75
+    {128, 96, 16, launch_bandws<1, 75, 4, 1, 3, 4>, true, 0, 75},   // 76: one-row bands (small batches)
+    {128, 96, 16, launch_bandws<1, 75, 4, 3, 1, 4>, true, 0, 75},   // 77
+    {128, 64, 16, launch_bandws<1, 38, 4, 1, 2, 4>, true, 0, 38},   // 78
+    {128, 64, 16, launch_bandws<1, 38, 4, 2, 1, 4>, true, 0, 38},   // 79
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -2680,10 +2686,27 @@ int pick_tile(const ConvArgs& a) {
         if (a.IC == 256 && a.OC == 512) return 51;
     }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 66;   // 3-stage ring
+    // small batches (5-row bands on under 48 workgroups): one-row bands, the
+    // same bits on 5x the workgroups; measured on ResNet34's maps: 128->128
+    // 22.1 -> 11.1 us at batch 1, 23.1 -> 15.0 us at batch 8, slower from
+    // batch 16 (64 workgroups); 256->256 23.8 -> 14.8 us at batch 1
+    const long bands5 = (long)(a.npix / (a.Ho * a.Wo)) * cdiv(a.H, 5) * (a.OC / 128);
+    if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && bands5 < 48 && tile_fits(kTiles[77], a))
+        return 77;
+    if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && bands5 < 48 && tile_fits(kTiles[78], a))
+        return 78;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[64], a)) return 64;
     if (is_s1_3x3(a) && a.OC == 128 && a.W > BandTile<5, 3>::MAXW && tile_fits(kTiles[57], a)) return 57;
     if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[65], a)) return 65;
     if (is_s1_3x3(a) && a.OC >= 256 && a.W <= BandTile<5, 3>::MAXW && tile_fits(kTiles[58], a)) return 58;
+    // ResNet's stride-2 convs at small batches (under 8192 output pixels, e.g.
+    // batch 1), measured: the 3x3s from 64 / 128 channels on the 128x32 DMA
+    // tile (18.8 -> 9.6 / 13.7 us), the rest on the 64x64 register-staged tile
+    // (32 -> 64 3x3 10.8 -> 7.0 us, the 1x1 shortcuts 9.1 -> 4.5 and 7.3 -> 5.1)
+    if (!a.split && a.KH == a.KW && a.sh == 2 && a.sw == 2 && a.npix < 8192 && a.IC % 32 == 0 && a.OC % 64 == 0) {
+        if (a.KH == 3 && a.IC % 64 == 0 && a.OC % 128 == 0 && tile_fits(kTiles[52], a)) return 52;
+        if (tile_fits(kTiles[63], a)) return 63;
+    }
     // ResNet's stride-2 32->64 pair (random-data sweep): the 1x1 on the 64x64
     // register-staged tile, the 3x3 on the 64x128 one
     if (!a.split && !is_s1_3x3(a) && a.IC == 32 && a.OC == 64) return a.KH * a.KW == 1 ? 63 : 2;

@@ -462,7 +462,10 @@ extern "C" int vdk_fbank(const vdk_fbank_cfg* cfg, const void* d_tables, const f
         p.waves = c.n_fft <= 512 ? kFbMaxWaves : 2;
         // frames per wavefront: enough to amortise the table copy, while
         // keeping >= ~4 workgroups per CU at batch 64
-        const int fpw = p.T >= 256 ? 4 : (p.T >= 64 ? 2 : 1);
+        int fpw = p.T >= 256 ? 4 : (p.T >= 64 ? 2 : 1);
+        // small batches: fewer frames per wavefront until the launch covers
+        // the CUs (each frame's arithmetic is the same whatever the grouping)
+        while (fpw > 1 && (long)batch * cdiv(p.T, p.waves * fpw) < 256) fpw /= 2;
         hipStream_t s = static_cast<hipStream_t>(stream);
         dim3 grid(cdiv(p.T, p.waves * fpw), batch);
         const bool radix8 = c.n_fft == 512 && c.win_length <= 512;
