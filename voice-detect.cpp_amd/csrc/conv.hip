@@ -2443,7 +2443,8 @@ struct TileCfg {
 // 38 wide), 66-69 the register-weight kernel with 3- and 4-stage rings,
 // 70-75 the split-f16 register-weight kernel (ERes2Net's group convs), 76-79
 // the producer / compute band kernel on one-row bands (the same sums in the
-// same order as its 5-row bands, so the same bits, on 5x the workgroups).
+// same order as its 5-row bands, so the same bits, on 5x the workgroups), 80
+// the register-staged 64x64 tile with 64-channel chunks.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -2528,6 +2529,7 @@ const TileCfg kTiles[] = {
     {128, 96, 16, launch_bandws<1, 75, 4, 3, 1, 4>, true, 0, 75},   // 77
     {128, 64, 16, launch_bandws<1, 38, 4, 1, 2, 4>, true, 0, 38},   // 78
     {128, 64, 16, launch_bandws<1, 38, 4, 2, 1, 4>, true, 0, 38},   // 79
+    {64, 64, 64, launch_igemm<64, 64, 32, 32, 64>},       // 80: register-staged, 64-channel chunks
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -2558,7 +2560,7 @@ bool split_epilogue(const ConvArgs& a) {
 }
 
 // The register-staged (igemm) entries: 0-13 and 62-63.
-bool igemm_tile(int idx) { return idx < kFirstDma || idx == 62 || idx == 63; }
+bool igemm_tile(int idx) { return idx < kFirstDma || idx == 62 || idx == 63 || idx == 80; }
 
 bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     const int idx = (int)(&t - kTiles);
@@ -2577,7 +2579,7 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
     // the in-image tap range for a single row of taps; longer 2-D kernels
     // take the register-staged kernel
-    if (a.KH * a.KW > 32 && a.KH != 1 && idx >= kFirstDma) return false;
+    if (a.KH * a.KW > 32 && a.KH != 1 && !igemm_tile(idx)) return false;
     if (t.sp_ic) return a.IC == t.sp_ic && a.OC == t.bm && split_epilogue(a);
     // 16-channel group strides: the LDS-DMA kernel's offsets and the shared store
     if ((a.xgs != (1 << a.xgl) || a.ygs != (1 << a.ygl)) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w))
@@ -2616,9 +2618,11 @@ int pick_tile(const ConvArgs& a) {
     const int bm = a.OC % 128 == 0 ? 128 : (a.OC % 64 == 0 ? 64 : 32);
     if (a.in_scale) {   // register-staged tiles for a few ten thousand pixels (CAM++'s
         // linear1: the LDS-DMA tiles, faster in isolation, measured slower in the model):
-        // 64-channel chunks on the 128x64 tile from 256 input channels (half the
-        // chunk steps, each a load round trip), else the 64x64 tile
-        if (a.IC >= 256 && a.IC % 64 == 0 && a.OC == 128 && a.npix < 65536 && tile_fits(kTiles[6], a)) return 6;
+        // 64-channel chunks from 256 input channels (half the chunk steps, each a
+        // load round trip) on the 64x64 tile (B=32 x 499 frames: 12.8 / 16.6 /
+        // 19.9 -> 12.0 / 15.8 / 19.5 us at 256 / 512 / 768 channels against the
+        // 128x64 one), else the 64x64 tile with 32-channel chunks
+        if (a.IC >= 256 && a.IC % 64 == 0 && a.OC == 128 && a.npix < 65536 && tile_fits(kTiles[80], a)) return 80;
         if (a.IC % 32 == 0) return bm >= 64 ? (a.npix < 32768 ? 63 : (bm == 128 ? 5 : 2)) : 10;
         return bm == 128 ? 13 : (bm == 64 ? 12 : 11);
     }
