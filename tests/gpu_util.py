@@ -2,6 +2,8 @@
 C ABI on host arrays, and the parity metrics (the reference's atol + rtol*|ref|
 form of tests/parity.hpp:44-70, cosine)."""
 import ctypes as C
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -96,3 +98,24 @@ def conv_ex(x_ptr, batch, H, W, IC, xs, w_khkwic, OC, KH, KW, y_ptr, ys=0, sh=1,
     d.tile = -1
     lib.check(lib.lib().vdk_conv2d_ex(d, None))
     lib.check(lib.lib().vdk_synchronize())
+
+
+def oracle_embed_all(net, pcm, threads=8):
+    """The oracle's embedding of every clip of a batch, clip-parallel on up to
+    `threads` threads (the C oracle runs outside the GIL)."""
+    import pyoracle as O
+    n = max(1, min(threads, os.cpu_count() or 1))
+    with ThreadPoolExecutor(n) as ex:
+        return np.stack(list(ex.map(lambda k: net.forward(O.fbank(pcm[k])), range(len(pcm)))))
+
+
+def check_every_clip(ctx, net, pcm, emb, label, invariance=()):
+    """Every clip's GPU embedding (emb, from one batch) at cosine >= 0.9999 to
+    the oracle's, and the clips in `invariance` bit-identical when embedded alone."""
+    ref = oracle_embed_all(net, pcm)
+    cs = np.array([cosine(emb[c], ref[c]) for c in range(len(pcm))])
+    announce(f"{label}: all {len(pcm)} clips, min cosine {cs.min():.7f} (clip {int(cs.argmin())})")
+    assert cs.min() >= 0.9999, f"{label}: clip {int(cs.argmin())} cosine {cs.min():.7f}"
+    for c in invariance:
+        one = ctx.embed_batch(pcm[c:c + 1])
+        assert np.array_equal(one[0], emb[c]), f"{label}: clip {c} alone differs from its batch row"

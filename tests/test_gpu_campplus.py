@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import pyoracle as O
-from gpu_util import announce, close_report, conv_ex, cosine, device_ok
+from gpu_util import announce, check_every_clip, close_report, conv_ex, cosine, device_ok
 from vdamd import gguf, lib, synth
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
@@ -260,6 +260,7 @@ def test_campplus_batch32_matches_oracle(campp):
         assert cs >= 0.9999
     one = ctx.embed_batch(pcm[15:16])
     assert np.array_equal(one[0], cap["emb"][15])
+    check_every_clip(ctx, net, pcm, cap["emb"], "campplus B=32", invariance=(1, 16, 30))
 
 
 @pytest.mark.parametrize("n", [400, 4000, 40000])

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import pyoracle as O
-from gpu_util import announce, cosine, device_ok
+from gpu_util import announce, check_every_clip, cosine, device_ok
 from vdamd import gguf, lib, synth
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
@@ -51,6 +51,7 @@ def test_resnet34_batch64_matches_oracle(resnet):
         announce(f"clip {c}: cosine {cs:.7f} pooled rel {rel:.2e}")
         assert cs >= 0.9999
         assert abs(np.linalg.norm(cap["emb"][c]) - 1.0) < 1e-5
+    check_every_clip(ctx, net, pcm, cap["emb"], "resnet34 B=64", invariance=(1, 32, 62))
 
 
 def test_resnet34_batch1_embed_pcm_matches_oracle(resnet):

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 import pyoracle as O
-from gpu_util import announce, close_report, cosine, device_ok
+from gpu_util import announce, check_every_clip, close_report, cosine, device_ok
 from vdamd import gguf, lib, synth
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
@@ -398,6 +398,7 @@ def test_ecapa_batch64_matches_oracle(ecapa):
         announce(f"ecapa clip {c}: cosine {cs:.7f} pooled rel {rel:.2e}")
         assert cs >= 0.9999
         assert abs(np.linalg.norm(cap["emb"][c]) - 1.0) < 1e-5
+    check_every_clip(ctx, net, pcm, cap["emb"], "ecapa B=64", invariance=(1, 32, 62))
     # batch invariance: the same clip alone gives the same bits
     one = ctx.embed_batch(pcm[31:32])
     assert np.array_equal(one[0], cap["emb"][31])

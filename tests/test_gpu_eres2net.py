@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import pyoracle as O
-from gpu_util import announce, close_report, conv_ex, cosine, device_ok
+from gpu_util import announce, check_every_clip, close_report, conv_ex, cosine, device_ok
 from vdamd import gguf, lib, synth
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not device_ok(), reason="no HIP device")]
@@ -491,6 +491,7 @@ def test_eres2net_batch16_matches_oracle(eres):
         assert cs >= 0.9999
     one = ctx.embed_batch(pcm[B - 1:B])
     assert np.array_equal(one[0], cap["emb"][B - 1])
+    check_every_clip(ctx, net, pcm, cap["emb"], "eres2net B=16", invariance=(0, 7, 14))
 
 
 @pytest.mark.parametrize("n", [400, 4000, 48000])

@@ -241,6 +241,23 @@ def test_one_row_band_tiles_equal_five_row_bands(case):
     assert np.array_equal(conv_gpu(x, w, b, res, 1, 1, relu).view(np.uint16), ref.view(np.uint16))
 
 
+@pytest.mark.parametrize("case", [(1, 40, 149, True, True), (3, 40, 149, False, True), (2, 13, 37, True, False)])
+def test_small_batch_64_channel_halo_tile_equals_register_weight(case):
+    """Tile 31 (halo kernel, one 64-channel chunk: picked for 64 -> 64 convs at
+    small batches) gives the register-weight kernel's bits, so batch-1 and
+    batch-64 ResNet34 embeddings stay bit-identical."""
+    B, H, W, with_res, relu = case
+    rng = np.random.default_rng(B * 31 + H)
+    x = rng.standard_normal((B, H, W, 64)).astype(np.float16)
+    w = (rng.standard_normal((64, 64, 3, 3)) * np.sqrt(2.0 / 576)).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, 64).astype(np.float32)
+    res = rng.standard_normal((B, H, W, 64)).astype(np.float16) if with_res else None
+    announce(f"64-channel halo tile vs register-weight {case}")
+    ref = conv_gpu(x, w, b, res, 1, 1, relu, tile=66)
+    assert np.array_equal(conv_gpu(x, w, b, res, 1, 1, relu, tile=31).view(np.uint16), ref.view(np.uint16))
+    assert np.array_equal(conv_gpu(x, w, b, res, 1, 1, relu).view(np.uint16), ref.view(np.uint16))
+
+
 @pytest.mark.parametrize("case", [
     # (B, H, W, C, residual): enough tiles that each persistent workgroup
     # walks several, with walk lengths of every remainder modulo the ring
