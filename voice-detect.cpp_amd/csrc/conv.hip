@@ -2792,17 +2792,17 @@ constexpr int kStemRuns = 10;
 template <int OC, bool SPLIT>
 __global__ __launch_bounds__(256) void stem_mfma_kernel(const float* __restrict__ feats, int B, int H, int W,
                                                         const float* __restrict__ w, const float* __restrict__ bias,
-                                                        int relu, half_t* __restrict__ y) {
+                                                        int relu, half_t* __restrict__ y, int rpw) {
     constexpr int NOB = OC / 32, PITCH = OC * 2 + 16;   // LDS row: OC f16 channels + 16 bytes
     static_assert(OC % 32 == 0, "whole 32-channel MFMA blocks");
     __shared__ __attribute__((aligned(16))) uint8_t stile[4][SPLIT ? 2 : 1][32 * PITCH];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 31, kk = lane >> 5;
-    const int ntb = (W + 31) >> 5, nch = (ntb + kStemRuns - 1) / kStemRuns;
+    const int ntb = (W + 31) >> 5, nch = (ntb + rpw - 1) / rpw;
     const int item = blockIdx.x * 4 + wave;
     if (item >= B * H * nch) return;   // no barrier below: a wave may leave alone
-    const int row = item / nch, r0 = (item - row * nch) * kStemRuns;
-    const int r1 = r0 + kStemRuns < ntb ? r0 + kStemRuns : ntb;
+    const int row = item / nch, r0 = (item - row * nch) * rpw;
+    const int r1 = r0 + rpw < ntb ? r0 + rpw : ntb;
     const int b = row / H, h = row - b * H;
     float wa[NOB][5];
     float16v bv[NOB];   // the accumulators start at the bias (register g*4+e: channel 8g + 4*kk + e)
@@ -3136,17 +3136,21 @@ extern "C" int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W
         require(n < (1L << 31), "stem: too many pixels for one launch");
         half_t* y = static_cast<half_t*>(d_y);
         const int sp = split ? 1 : 0;
-        // 32 / 64 channels: f32 MFMA, one wavefront per kStemRuns 32-pixel runs of a row
-        const long runs = (long)batch * H * cdiv(cdiv(W, 32), kStemRuns);
+        // 32 / 64 channels: f32 MFMA, one wavefront per rpw (up to kStemRuns)
+        // 32-pixel runs of a row; small batches take fewer runs per wavefront
+        // until there are 2048 wavefronts (each run's arithmetic is the same)
+        int rpw = kStemRuns;
+        while (rpw > 1 && (long)batch * H * cdiv(cdiv(W, 32), rpw) < 2048) rpw = (rpw + 1) / 2;
+        const long runs = (long)batch * H * cdiv(cdiv(W, 32), rpw);
         switch (OC) {
             case 16: hipLaunchKernelGGL(stem_conv3x3_kernel<16>, dim3(cdiv(n, 256)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
             case 32:
-                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<32, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y);
-                else hipLaunchKernelGGL((stem_mfma_kernel<32, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y);
+                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<32, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y, rpw);
+                else hipLaunchKernelGGL((stem_mfma_kernel<32, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y, rpw);
                 break;
             case 64:
-                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<64, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y);
-                else hipLaunchKernelGGL((stem_mfma_kernel<64, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y);
+                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<64, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y, rpw);
+                else hipLaunchKernelGGL((stem_mfma_kernel<64, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y, rpw);
                 break;
             default: throw Error("stem: OC must be 16, 32 or 64");
         }
