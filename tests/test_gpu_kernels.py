@@ -243,9 +243,10 @@ def test_one_row_band_tiles_equal_five_row_bands(case):
 
 @pytest.mark.parametrize("case", [(1, 40, 149, True, True), (3, 40, 149, False, True), (2, 13, 37, True, False)])
 def test_small_batch_64_channel_halo_tile_equals_register_weight(case):
-    """Tile 31 (halo kernel, one 64-channel chunk: picked for 64 -> 64 convs at
-    small batches) gives the register-weight kernel's bits, so batch-1 and
-    batch-64 ResNet34 embeddings stay bit-identical."""
+    """Tile 31 (halo kernel, one 64-channel chunk) gives the register-weight
+    kernel's bits for 64 -> 64 convs at small batches: both sum tap-major,
+    channel-minor, so either may serve a batch without breaking batch
+    invariance."""
     B, H, W, with_res, relu = case
     rng = np.random.default_rng(B * 31 + H)
     x = rng.standard_normal((B, H, W, 64)).astype(np.float16)

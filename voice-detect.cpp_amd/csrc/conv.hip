@@ -2689,12 +2689,6 @@ int pick_tile(const ConvArgs& a) {
         if (a.IC == 128 && a.OC == 256) return 39;
         if (a.IC == 256 && a.OC == 512) return 51;
     }
-    // 64 -> 64 at small batches (under 24000 output pixels, ResNet34 batch
-    // 1-4): the halo kernel with one 64-channel chunk (the register-weight
-    // kernel's tap-major, channel-minor sums: the same bits), 13.4 -> 10.0 us
-    // per launch at batch 1
-    if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && !a.split && a.npix < 24000 && tile_fits(kTiles[31], a))
-        return 31;
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 66;   // 3-stage ring
     // small batches (5-row bands on under 48 workgroups): one-row bands, the
     // same bits on 5x the workgroups; measured on ResNet34's maps: 128->128
