@@ -182,6 +182,11 @@ typedef struct {
     const void* aff_x; int aff_x_stride, aff_x_lo;
     const void* aff_ds; int aff_ds_stride, aff_ds_lo;
 } vdk_conv_desc;
+/* Host: tensor `name` of the GGUF file at `path` as f32 into out[n]
+ * (n = the tensor's element count; F16 widened exactly, Q8_0 blocks
+ * dequantised to q * d with the product in f32), the values every model
+ * upload starts from (src/model_loader.cpp:114-215 reads the same file). */
+int vdk_gguf_tensor_f32(const char* path, const char* name, float* out, long long n);
 /* Host: re-order f16 conv weights [OC][KH][KW][IC] (IC % 16 == 0) into the
  * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */
 void vdk_conv_pack_chunked(const unsigned short* w, int OC, int KH, int KW, int IC, unsigned short* out);

@@ -263,6 +263,17 @@ def test_campplus_batch32_matches_oracle(campp):
     check_every_clip(ctx, net, pcm, cap["emb"], "campplus B=32", invariance=(1, 16, 30))
 
 
+def test_campplus_batch8_3s_every_clip(campp):
+    """3 s clips (T' = 149: segments of 100 and 49 frames, so linear1's pixel
+    tiles run over three segments at clip boundaries) at batch 8: every clip
+    against the oracle and bitwise batch invariance."""
+    path, ctx, net = campp
+    pcm = synth.clips(5170, 8, 48000)
+    announce("e2e campplus B=8 3s")
+    emb = ctx.embed_batch(pcm)
+    check_every_clip(ctx, net, pcm, emb, "campplus B=8 3s", invariance=(0, 3, 7))
+
+
 @pytest.mark.parametrize("n", [400, 4000, 40000])
 def test_campplus_embed_pcm_lengths(campp, n):
     path, ctx, net = campp
@@ -287,13 +298,16 @@ def test_campplus_verify_matches_oracle(campp):
         assert ctx.verify_pcm(a, b, thr)[1] == (d_ref <= thr)
 
 
-@pytest.mark.parametrize("batch,T,c_in", [(B, TP, 320), (3, 257, 160), (2, 40, 128)])
+@pytest.mark.parametrize("batch,T,c_in", [(B, TP, 320), (3, 257, 160), (2, 40, 128),
+                                          (8, 149, 128), (8, 49, 160), (16, 101, 256), (12, 3, 128)])
 def test_linear1_segment_sums_feed_cam_local(batch, T, c_in):
     """linear1 with seg_sum (the per-(clip, segment) f64 sums of its stored
     f16 outputs, accumulated in the conv's epilogue) equals the exact f64
     sums of h and leaves h bit-identical; cam_local fed those sums (and
     clearing the next layer's buffer) writes the same bits as cam_local
-    summing h itself."""
+    summing h itself.  T' = 149 (last segment 49 frames), 49 (one short
+    segment per clip), 101 (a one-frame last segment) and 3 (clips shorter
+    than any pixel tile) put three or more segments into one pixel tile."""
     rng = np.random.default_rng(7 * T + c_in)
     L = lib.lib()
     BC, G, H1, SEG, CMAX = 128, 32, 64, 100, 512

@@ -56,7 +56,11 @@ def test_noalloc_linear_rejects_oversized_partials():
     L = lib.lib()
     B, I, E = 1024, 5120, 256            # 40 slices x 1024 x 256 floats = 40 MiB
     assert L.vdk_linear_workspace_size(B, I, E) > SCRATCH_BYTES
-    dx, dw, dy = lib.DeviceBuffer(16), lib.DeviceBuffer(16), lib.DeviceBuffer(16)
+    # operands at their full sizes (20 + 5 + 1 MiB), so that a regressed size
+    # guard computes a product over valid memory and fails the assertion
+    dx, dw, dy = lib.DeviceBuffer(4 * B * I), lib.DeviceBuffer(4 * I * E), lib.DeviceBuffer(4 * B * E)
     rc = L.vdk_linear_ex_noalloc(dx.ptr, B, I, dw.ptr, None, None, E, 0, dy.ptr, None)
+    err = L.vdk_last_error()
+    lib.check(L.vdk_synchronize())
     assert rc != 0
-    assert b"scratch" in L.vdk_last_error()
+    assert b"scratch" in err

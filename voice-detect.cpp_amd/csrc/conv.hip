@@ -214,7 +214,8 @@ __device__ __forceinline__ int seg_id(const ConvArgs& a, int P) {
 }
 
 // SEGS: part accumulates f64 sums of the stored f16 values of this thread's
-// 8 channels, per segment relative to sid0 (0 or 1); see stage_epilogue_impl.
+// 8 channels for the segments sid0 and sid0 + 1; values of any later segment
+// in the tile are added to ConvArgs::segsum directly; see stage_epilogue_impl.
 template <int M, bool SEGS = false, class PixFn>
 __device__ __forceinline__ void finish_staged(const ConvArgs& a, const float* sT, int npix_tile, int oc0, int tid,
                                               int nthreads, PixFn pix, double (&part)[2][8], int sid0) {
@@ -228,12 +229,22 @@ __device__ __forceinline__ void finish_staged(const ConvArgs& a, const float* sT
         float v[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};
         epi8(a, P, oc, v);
         if constexpr (SEGS) {
-            const bool first = seg_id(a, P) == sid0;
+            const int rel = seg_id(a, P) - sid0;
+            if (rel < 2) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const double h = (double)(float)(half_t)v[e];   // the stored value
-                part[0][e] += first ? h : 0.0;
-                part[1][e] += first ? 0.0 : h;
+                for (int e = 0; e < 8; ++e) {
+                    const double h = (double)(float)(half_t)v[e];   // the stored value
+                    part[0][e] += rel == 0 ? h : 0.0;
+                    part[1][e] += rel == 0 ? 0.0 : h;
+                }
+            } else {
+                // a third or later segment in this tile (a clip's short last
+                // segment, or clips shorter than the tile): straight to memory
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const double h = (double)(float)(half_t)v[e];
+                    if (oc + e < a.OC && h != 0.0) atomicAdd(a.segsum + (size_t)(sid0 + rel) * a.OC + oc + e, h);
+                }
             }
         }
         store8(a, P, oc, v);
@@ -251,14 +262,16 @@ __device__ __forceinline__ int xcd_swizzle(int bid, int nb) {
 // Staged epilogue of an implicit-GEMM tile (BM channels x BN consecutive
 // pixels): waves write their blocks in passes of PB pixel columns that fit the
 // kernel's LDS buffer, then all threads finish 8-channel rows.
-// Segment sums of the stored f16 outputs (ConvArgs::segsum): the tile's
-// pixels fall in at most two segments (the pixel tile is at most seg_len
-// wide), part 0 the segment of the tile's first pixel.  Each thread keeps
+// Segment sums of the stored f16 outputs (ConvArgs::segsum): part 0 is the
+// segment of the tile's first pixel, part 1 the next one.  Each thread keeps
 // its 8 channels' sums per part (a fixed channel chunk: NT is a multiple of
 // BM / 8), the threads of a chunk are summed within the wave and then across
-// the waves, and each (part, channel) goes out as one f64 atomic add; every
-// term is an f16, so all these sums are exact and the result does not depend
-// on the order of the additions.
+// the waves, and each (part, channel) goes out as one f64 atomic add.  A tile
+// can reach further segments (a clip's last segment may be a few frames, and
+// the tile runs on into the next clip): their values go out one atomic add
+// each.  Every term is an f16 (a multiple of 2^-24 below 2^16) and a segment
+// holds far fewer than 2^13 of them, so all these f64 sums are exact and the
+// result does not depend on the order of the additions.
 template <int BM, int BN, int WN, int SMEM, int NT, int TM, int TN, bool SEGS = false>
 __device__ __forceinline__ void stage_epilogue_impl(const ConvArgs& a, uint8_t* smem, const float16v (*acc)[TN],
                                                     int m_off, int n_off, int p0, int oc0, int tid, int lane) {
@@ -2574,7 +2587,8 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     // q8_0 weights are dequantised in the register-staged kernel's weight loads
     if (a.wq && !igemm_tile(idx)) return false;
     // segment sums live in the staged epilogue of the register-staged
-    // kernel (f16 weights), for pixel tiles that touch at most two segments
+    // kernel (f16 weights); pixel tiles at most seg_len wide keep most pixels
+    // in the two segments the epilogue sums locally
     if (a.segsum && (!igemm_tile(idx) || a.wq || t.bn > a.seg_len)) return false;
     // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
     // the in-image tap range for a single row of taps; longer 2-D kernels

@@ -1,6 +1,7 @@
 // gguf.cpp - GGUF reader (see gguf.hpp).
 #include "gguf.hpp"
 
+#include <algorithm>
 #include <climits>
 #include <cstring>
 #include <fstream>
@@ -240,3 +241,15 @@ std::vector<float> GgufFile::to_f32(const std::string& name) const {
 }
 
 }  // namespace vdk
+
+extern "C" int vdk_gguf_tensor_f32(const char* path, const char* name, float* out, long long n) {
+    return vdk::guarded([&] {
+        vdk::require(path && name && out, "gguf: NULL argument");
+        const vdk::GgufFile g(path);
+        const vdk::GgufTensor* t = g.tensor(name);
+        vdk::require(t != nullptr, std::string("gguf: no tensor '") + name + "'");
+        vdk::require(t->nelements() == n, std::string("gguf: tensor '") + name + "' has a different element count");
+        const std::vector<float> v = g.to_f32(name);
+        std::copy(v.begin(), v.end(), out);
+    });
+}

@@ -117,6 +117,7 @@ _SIGS = {
                                        C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int]),
     "vdk_conv2d_ex": (C.c_int, [C.POINTER(ConvDesc), _vp]),
     "vdk_conv_pack_chunked": (None, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp]),
+    "vdk_gguf_tensor_f32": (C.c_int, [C.c_char_p, C.c_char_p, _vp, C.c_longlong]),
     "vdk_conv2d_tile_fits_ex": (C.c_int, [C.c_int, C.POINTER(ConvDesc)]),
     "vdk_conv2d_tile_count": (C.c_int, []),
     "vdk_conv2d_tile_fits": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
