@@ -351,6 +351,12 @@ MUTANTS = {
 
 def _build_mutant(tmp, name):
     fname, subs = MUTANTS[name]
+    return _build_mutant_from(tmp, name, fname, subs)
+
+
+def _build_mutant_from(tmp, name, fname, subs):
+    """The oracle sources copied to tmp/name with `subs` applied to `fname`,
+    built as a shared library; returns its path."""
     d = os.path.join(tmp, name)
     os.makedirs(d)
     for f in os.listdir(ORACLE_DIR):
