@@ -65,6 +65,22 @@ size_t vdk_fbank_tables_size(const vdk_fbank_cfg* cfg);
 int    vdk_fbank_tables_fill(const vdk_fbank_cfg* cfg, void* d_tables);
 int    vdk_fbank(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pcm,
                  int batch, int n_samples, float* d_feats, void* stream);
+/* Same with a caller workspace (CMN: vdk_fbank_workspace_size bytes,
+ * 256-byte aligned; no initial contents needed).
+ * d_mean == NULL: the features come out normalised, as vdk_fbank.
+ * d_mean != NULL (and cfg->cmn): the features come out WITHOUT the CMN
+ * subtraction and d_mean [B][n_mels] receives each clip's per-bin means, for
+ * a consumer that subtracts them as it loads (vdk_stem_conv3x3_ex,
+ * vdk_feats_tmajor: row mean arguments) or for vdk_fbank_sub_mean; the f32
+ * values such a consumer sees are those vdk_fbank stores.  The means sum
+ * the log-mel values of a clip as fixed-point 2^-36 integers, so the result
+ * does not depend on how the frames are grouped into workgroups. */
+size_t vdk_fbank_workspace_size(const vdk_fbank_cfg* cfg, int batch, int n_samples);
+int    vdk_fbank_ex(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pcm,
+                    int batch, int n_samples, float* d_feats, float* d_mean,
+                    void* d_work, size_t work_size, void* stream);
+/* feats [B][n_mels][T] -= mean [B][n_mels] (the CMN subtraction, f32). */
+int    vdk_fbank_sub_mean(float* d_feats, const float* d_mean, int batch, int n_mels, int T, void* stream);
 
 /* ---- 2D convolution, implicit GEMM on f16 MFMA with f32 accumulation ----
  * Replaces the blocked-island ops blocked_conv3x3 / blocked_conv1x1 with their
@@ -228,8 +244,10 @@ int vdk_resblock3x3_variant(const void* d_x, int batch, int H, int W, int C,
 int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W,
                      const float* d_w, const float* d_bias, int OC, int relu,
                      void* d_y, void* stream);
-/* Same; split != 0 stores split-f16 [hi(OC) | lo(OC)] per pixel (see vdk_conv_desc). */
-int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W,
+/* Same; split != 0 stores split-f16 [hi(OC) | lo(OC)] per pixel (see vdk_conv_desc);
+ * d_row_mean (may be NULL): [B][H] subtracted from each in-map input value of
+ * its row as it is loaded (the CMN means of vdk_fbank_ex). */
+int vdk_stem_conv3x3_ex(const float* d_feats, const float* d_row_mean, int batch, int H, int W,
                         const float* d_w, const float* d_bias, int OC, int relu, int split,
                         void* d_y, void* stream);
 
@@ -280,9 +298,10 @@ int vdk_linear_ex_noalloc(const float* d_x, int batch, int in_dim, const float* 
  * offset + stride; strides and channel counts of the half8 kernels are
  * multiples of 8 and pointers 16-byte aligned). */
 /* FBank [B][n_mels][T] f32 -> [B][T+2*pad][c_pad] f16, reflect padded in time
- * without edge repeat (src/encoder.cpp:32-52) and zero channels n_mels..c_pad. */
-int vdk_feats_tmajor(const float* d_feats, int batch, int n_mels, int T, int pad, int c_pad,
-                     void* d_out, void* stream);
+ * without edge repeat (src/encoder.cpp:32-52) and zero channels n_mels..c_pad;
+ * d_row_mean (may be NULL): [B][n_mels] CMN means subtracted as it loads. */
+int vdk_feats_tmajor(const float* d_feats, const float* d_row_mean, int batch, int n_mels, int T, int pad,
+                     int c_pad, void* d_out, void* stream);
 /* out [B][T+2*pad][G] = reflect_pad(a (+ b)) over time: the Res2Net group
  * input x_i + y_{i-1} of src/encoder.cpp:174-200 padded for its dilated conv.
  * d_b may be NULL. */

@@ -98,7 +98,7 @@ def test_block0_reflect_pad_and_k5_conv():
     L = lib.lib()
     df = lib.DeviceBuffer.from_array(feats)
     x0p = lib.DeviceBuffer(B * (T + 4) * 96 * 2)
-    lib.check(L.vdk_feats_tmajor(df.ptr, B, nm, T, 2, 96, x0p.ptr, None))
+    lib.check(L.vdk_feats_tmajor(df.ptr, None, B, nm, T, 2, 96, x0p.ptr, None))
     _sync()
     got_x = x0p.to_array(np.float16, (B, T + 4, 96))
     want = np.zeros((B, T + 4, 96), dtype=np.float16)
@@ -426,3 +426,33 @@ def test_ecapa_verify_matches_oracle(ecapa, golden_dir):
     assert abs(d_gpu - d_ref) <= 2e-3
     for thr in (d_ref - 5e-3, d_ref + 5e-3):
         assert ctx.verify_pcm(a, b, thr)[1] == (d_ref <= thr)
+
+
+def test_ecapa_real_checkpoint_widths_q8_0_batch64():
+    """The published SpeechBrain layout (models/ecapa_tdnn_manifest.txt: MFA
+    3072, asp.tdnn 9216 -> 128, asp_bn 6144, fc 6144 -> 192) with the mfa
+    weight stored as 2-D Q8_0 the way the converter's q8_0 plan stores it;
+    B=64 x 4 s, every clip against the oracle on the same dequantised weights."""
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "ecapa_real_q8_0.gguf")
+    synth.write_ecapa(path, seed=17, mfa=3072, wtype=gguf.GGML_Q8_0)
+    g = gguf.GGUFFile(path)
+    assert g.tensors["mfa.conv.conv.weight"][0] == gguf.GGML_Q8_0
+    assert g.tensors["mfa.conv.conv.weight"][1] == [3072, 3072]
+    ctx = lib.Context(path)
+    try:
+        net = O.OracleEcapa(g)
+        pcm = synth.clips(4713, B, N4S)
+        announce("e2e ecapa MFA 3072 q8_0 B=64 4s capture")
+        cap = ctx.capture(pcm)
+        assert cap["pooled"].shape[1] == 2 * 3072
+        for c in CLIPS:
+            emb, caps = net.forward(O.fbank(pcm[c]), capture=True)
+            rel = np.linalg.norm(cap["pooled"][c] - caps["pooled"]) / np.linalg.norm(caps["pooled"])
+            assert rel <= 2e-3, f"pooled rel-L2 {rel:.2e} clip {c}"
+            cs = cosine(cap["emb"][c], emb)
+            announce(f"ecapa-3072 clip {c}: cosine {cs:.7f} pooled rel {rel:.2e}")
+            assert cs >= 0.9999
+        check_every_clip(ctx, net, pcm, cap["emb"], "ecapa MFA 3072 q8_0 B=64", invariance=(0, 40))
+    finally:
+        ctx.close()

@@ -67,6 +67,74 @@ def test_fbank_batched_config_lengths(seconds, batch):
     assert np.abs(got.mean(axis=2)).max() < 1e-5
 
 
+def _fbank_ex(L, cfg, tab, dp, B, n, T, d_mean):
+    df = lib.DeviceBuffer(B * cfg.n_mels * T * 4)
+    wsz = L.vdk_fbank_workspace_size(cfg, B, n)
+    work = lib.DeviceBuffer.from_array(np.full(wsz, 0xA5, dtype=np.uint8))   # no initial contents needed
+    lib.check(L.vdk_fbank_ex(cfg, tab.ptr, dp.ptr, B, n, df.ptr, d_mean, work.ptr, wsz, None))
+    lib.check(L.vdk_synchronize())
+    return df, work
+
+
+@pytest.mark.parametrize("seconds,batch", [(3.0, 64), (3.0, 1), (10.0, 5), (0.05, 3)])
+def test_fbank_deferred_cmn_means(seconds, batch):
+    """vdk_fbank_ex with a mean output: the features come out before the CMN
+    subtraction and features - means is bit-identical to vdk_fbank's output;
+    the means agree with the f64 means of the raw rows; the consumers'
+    row-mean arguments (stem, ECAPA's time-major copy)
+    reproduce their outputs on the normalised features bit for bit."""
+    L = lib.lib()
+    cfg = lib.fbank_cfg()
+    n = max(400, synth.seconds_to_samples(seconds))
+    T = 1 + (n - cfg.win_length) // cfg.hop_length
+    announce(f"fbank_ex deferred CMN batch={batch} n={n}")
+    pcm = synth.clips(300 + batch, batch, n)
+    tab = lib.DeviceBuffer(L.vdk_fbank_tables_size(cfg))
+    lib.check(L.vdk_fbank_tables_fill(cfg, tab.ptr))
+    dp = lib.DeviceBuffer.from_array(pcm)
+    dm = lib.DeviceBuffer(batch * cfg.n_mels * 4)
+    draw, work = _fbank_ex(L, cfg, tab, dp, batch, n, T, dm.ptr)
+    raw = draw.to_array(np.float32, (batch, cfg.n_mels, T))
+    mean = dm.to_array(np.float32, (batch, cfg.n_mels))
+    want_mean = raw.astype(np.float64).mean(axis=2)
+    assert np.all(np.abs(mean - want_mean) <= 1e-6 * np.maximum(1.0, np.abs(want_mean)))
+    norm = fbank_gpu(pcm, cfg)
+    assert np.array_equal((raw - mean[:, :, None]).view(np.uint32), norm.view(np.uint32))
+    # vdk_fbank_ex without a mean output normalises in place, like vdk_fbank
+    dn, _ = _fbank_ex(L, cfg, tab, dp, batch, n, T, None)
+    assert np.array_equal(dn.to_array(np.float32, (batch, cfg.n_mels, T)).view(np.uint32), norm.view(np.uint32))
+    # a second call on the same workspace gives the same bits
+    d2 = lib.DeviceBuffer(batch * cfg.n_mels * T * 4)
+    lib.check(L.vdk_fbank_ex(cfg, tab.ptr, dp.ptr, batch, n, d2.ptr, dm.ptr, work.ptr, work.nbytes, None))
+    lib.check(L.vdk_synchronize())
+    assert np.array_equal(d2.to_array(np.float32, (batch, cfg.n_mels, T)).view(np.uint32), raw.view(np.uint32))
+    assert np.array_equal(dm.to_array(np.float32, (batch, cfg.n_mels)).view(np.uint32), mean.view(np.uint32))
+    # consumers: the stem and ECAPA's time-major copy with the row means
+    dnorm = lib.DeviceBuffer.from_array(norm)
+    rng = np.random.default_rng(5)
+    for OC, split in ((32, 0), (64, 1), (16, 0)):
+        w = (rng.standard_normal((OC, 9)) * 0.4).astype(np.float32)
+        bias = (rng.standard_normal(OC) * 0.1).astype(np.float32)
+        dw, db = lib.DeviceBuffer.from_array(w), lib.DeviceBuffer.from_array(bias)
+        ch = OC * (2 if split else 1)
+        outs = []
+        for src, m in ((dnorm, None), (draw, dm.ptr)):
+            dy = lib.DeviceBuffer(batch * cfg.n_mels * T * ch * 2)
+            lib.check(L.vdk_stem_conv3x3_ex(src.ptr, m, batch, cfg.n_mels, T, dw.ptr, db.ptr, OC, 1, split, dy.ptr,
+                                            None))
+            lib.check(L.vdk_synchronize())
+            outs.append(dy.to_array(np.uint16, (batch * cfg.n_mels * T * ch,)))
+        assert np.array_equal(outs[0], outs[1]), (OC, split)
+    if T >= 3:
+        outs = []
+        for src, m in ((dnorm, None), (draw, dm.ptr)):
+            dx = lib.DeviceBuffer(batch * (T + 4) * 96 * 2)
+            lib.check(L.vdk_feats_tmajor(src.ptr, m, batch, cfg.n_mels, T, 2, 96, dx.ptr, None))
+            lib.check(L.vdk_synchronize())
+            outs.append(dx.to_array(np.uint16, (batch * (T + 4) * 96,)))
+        assert np.array_equal(outs[0], outs[1])
+
+
 def test_fbank_rejects_short_input():
     L = lib.lib()
     cfg = lib.fbank_cfg()
@@ -475,7 +543,7 @@ def test_stem_conv_matches_oracle(B, H, W, OC, split):
     db = lib.DeviceBuffer.from_array(b)
     ch = OC * (2 if split else 1)
     dy = lib.DeviceBuffer(B * H * W * ch * 2)
-    lib.check(L.vdk_stem_conv3x3_ex(df.ptr, B, H, W, dw.ptr, db.ptr, OC, 1, split, dy.ptr, None))
+    lib.check(L.vdk_stem_conv3x3_ex(df.ptr, None, B, H, W, dw.ptr, db.ptr, OC, 1, split, dy.ptr, None))
     lib.check(L.vdk_synchronize())
     y = dy.to_array(np.float16, (B, H, W, ch)).astype(np.float32)
     got = y[..., :OC] + y[..., OC:] if split else y

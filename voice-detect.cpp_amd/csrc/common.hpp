@@ -65,6 +65,15 @@ typedef int int4v __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kOOB = 0x80000000u;   // any buffer offset >= num_records reads as zero
 
+// Spread consecutive workgroup ids over the 8 XCDs in contiguous ranges so that
+// neighbouring tiles (which share input rows or output lines) run under the
+// same L2: workgroups are dispatched to the XCDs round robin.
+__device__ __forceinline__ int xcd_swizzle(int bid, int nb) {
+    const int per = nb >> 3;
+    if (bid >= (per << 3)) return bid;
+    return (bid & 7) * per + (bid >> 3);
+}
+
 // Workgroup barrier over LDS traffic only: this wave's LDS reads and writes
 // complete (lgkmcnt(0)) before s_barrier, while its global stores and LDS DMA
 // stay in flight.  (A workgroup-scope release fence would also drain vmcnt,

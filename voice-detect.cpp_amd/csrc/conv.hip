@@ -251,14 +251,6 @@ __device__ __forceinline__ void finish_staged(const ConvArgs& a, const float* sT
     }
 }
 
-// Spread consecutive workgroup ids over the 8 XCDs in contiguous ranges so that
-// neighbouring pixel tiles (which share input rows) run under the same L2.
-__device__ __forceinline__ int xcd_swizzle(int bid, int nb) {
-    const int per = nb >> 3;
-    if (bid >= (per << 3)) return bid;
-    return (bid & 7) * per + (bid >> 3);
-}
-
 // Staged epilogue of an implicit-GEMM tile (BM channels x BN consecutive
 // pixels): waves write their blocks in passes of PB pixel columns that fit the
 // kernel's LDS buffer, then all threads finish 8-channel rows.
@@ -2738,7 +2730,8 @@ int pick_tile(const ConvArgs& a) {
 }
 
 template <int OC>
-__global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restrict__ feats, int B, int H, int W,
+__global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restrict__ feats,
+                                                           const float* __restrict__ rmean, int B, int H, int W,
                                                            const float* __restrict__ w,
                                                            const float* __restrict__ bias, int relu, int split,
                                                            half_t* __restrict__ y) {
@@ -2763,7 +2756,9 @@ __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restri
 #pragma unroll
         for (int kw = 0; kw < 3; ++kw) {
             const int ih = h - 1 + kh, iw = t - 1 + kw;
-            xv[kh * 3 + kw] = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? feats[((long)b * H + ih) * W + iw] : 0.0f;
+            xv[kh * 3 + kw] = (ih >= 0 && ih < H && iw >= 0 && iw < W)
+                                  ? feats[((long)b * H + ih) * W + iw] - (rmean ? rmean[(long)b * H + ih] : 0.0f)
+                                  : 0.0f;
         }
     half8 hv, lv;
 #pragma unroll
@@ -2798,7 +2793,8 @@ __global__ __launch_bounds__(256) void stem_conv3x3_kernel(const float* __restri
 constexpr int kStemRuns = 10;
 
 template <int OC, bool SPLIT>
-__global__ __launch_bounds__(256) void stem_mfma_kernel(const float* __restrict__ feats, int B, int H, int W,
+__global__ __launch_bounds__(256) void stem_mfma_kernel(const float* __restrict__ feats,
+                                                        const float* __restrict__ rmean, int B, int H, int W,
                                                         const float* __restrict__ w, const float* __restrict__ bias,
                                                         int relu, half_t* __restrict__ y, int rpw) {
     constexpr int NOB = OC / 32, PITCH = OC * 2 + 16;   // LDS row: OC f16 channels + 16 bytes
@@ -2824,14 +2820,34 @@ __global__ __launch_bounds__(256) void stem_mfma_kernel(const float* __restrict_
 #pragma unroll
         for (int r = 0; r < 16; ++r) bv[ob][r] = bias[ob * 32 + (r >> 2) * 8 + kk * 4 + (r & 3)];
     }
-    auto load = [&](int r, float* xb) {
+    // the CMN means of the three input rows (rows outside the map stay zero
+    // padding, so their mean is never applied)
+    // the CMN means of the three input rows (0 outside the map), then the one
+    // this lane's tap q takes (selects, not an indexed array: an indexed
+    // private array would be placed in LDS)
+    float mu0 = 0.0f, mu1 = 0.0f, mu2 = 0.0f;
+    if (rmean) {
+        if (h >= 1) mu0 = rmean[(size_t)b * H + h - 1];
+        mu1 = rmean[(size_t)b * H + h];
+        if (h + 1 < H) mu2 = rmean[(size_t)b * H + h + 1];
+    }
+    float muq[5];
+#pragma unroll
+    for (int q = 0; q < 5; ++q) {
+        const int kh = (2 * q + kk) / 3;
+        muq[q] = kh == 0 ? mu0 : (kh == 1 ? mu1 : mu2);
+    }
+    // raw values, and the mean each one takes when it is used (0 for the
+    // zero padding), so the loads of the next run stay in flight meanwhile
+    auto load = [&](int r, float* xb, float* mb) {
         const int t0 = r * 32;
 #pragma unroll
         for (int q = 0; q < 5; ++q) {
             const int tap = 2 * q + kk, kh = tap / 3, kw = tap - kh * 3;
             const int ih = h - 1 + kh, iw = t0 + j - 1 + kw;
-            xb[q] = (tap < 9 && ih >= 0 && ih < H && iw >= 0 && iw < W) ? feats[((size_t)b * H + ih) * W + iw]
-                                                                           : 0.0f;
+            const bool in = tap < 9 && ih >= 0 && ih < H && iw >= 0 && iw < W;
+            xb[q] = in ? feats[((size_t)b * H + ih) * W + iw] : 0.0f;
+            mb[q] = in ? muq[q] : 0.0f;
         }
     };
     uint8_t* const hi = stile[wave][0];
@@ -2839,13 +2855,13 @@ __global__ __launch_bounds__(256) void stem_mfma_kernel(const float* __restrict_
     constexpr int CPP = OC / 8;                  // 16-byte chunks per pixel
     constexpr int PPI = 64 / CPP;                // pixels per store instruction
     constexpr int ostride = SPLIT ? 2 * OC : OC;
-    float xn[5];
-    load(r0, xn);
+    float xn[5], mn[5];
+    load(r0, xn, mn);
     for (int r = r0; r < r1; ++r) {
         float xb[5];
 #pragma unroll
-        for (int q = 0; q < 5; ++q) xb[q] = xn[q];
-        if (r + 1 < r1) load(r + 1, xn);
+        for (int q = 0; q < 5; ++q) xb[q] = xn[q] - mn[q];   // the CMN subtraction (x - 0 = x without it)
+        if (r + 1 < r1) load(r + 1, xn, mn);
 #pragma unroll
         for (int ob = 0; ob < NOB; ++ob) {
             float16v acc = bv[ob];
@@ -3132,8 +3148,9 @@ extern "C" int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* d) {
     return tile_fits(kTiles[tile], shape_args(*d)) ? 1 : 0;
 }
 
-extern "C" int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W, const float* d_w,
-                                   const float* d_bias, int OC, int relu, int split, void* d_y, void* stream) {
+extern "C" int vdk_stem_conv3x3_ex(const float* d_feats, const float* d_row_mean, int batch, int H, int W,
+                                   const float* d_w, const float* d_bias, int OC, int relu, int split, void* d_y,
+                                   void* stream) {
     return guarded([&] {
         require(d_feats && d_w && d_bias && d_y, "stem: NULL device pointer");
         require(batch > 0 && H > 0 && W > 0, "stem: empty input");
@@ -3151,14 +3168,14 @@ extern "C" int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W
         while (rpw > 1 && (long)batch * H * cdiv(cdiv(W, 32), rpw) < 2048) rpw = (rpw + 1) / 2;
         const long runs = (long)batch * H * cdiv(cdiv(W, 32), rpw);
         switch (OC) {
-            case 16: hipLaunchKernelGGL(stem_conv3x3_kernel<16>, dim3(cdiv(n, 256)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, sp, y); break;
+            case 16: hipLaunchKernelGGL(stem_conv3x3_kernel<16>, dim3(cdiv(n, 256)), dim3(256), 0, s, d_feats, d_row_mean, batch, H, W, d_w, d_bias, relu, sp, y); break;
             case 32:
-                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<32, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y, rpw);
-                else hipLaunchKernelGGL((stem_mfma_kernel<32, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y, rpw);
+                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<32, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, d_row_mean, batch, H, W, d_w, d_bias, relu, y, rpw);
+                else hipLaunchKernelGGL((stem_mfma_kernel<32, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, d_row_mean, batch, H, W, d_w, d_bias, relu, y, rpw);
                 break;
             case 64:
-                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<64, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y, rpw);
-                else hipLaunchKernelGGL((stem_mfma_kernel<64, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, batch, H, W, d_w, d_bias, relu, y, rpw);
+                if (sp) hipLaunchKernelGGL((stem_mfma_kernel<64, true>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, d_row_mean, batch, H, W, d_w, d_bias, relu, y, rpw);
+                else hipLaunchKernelGGL((stem_mfma_kernel<64, false>), dim3(cdiv(runs, 4)), dim3(256), 0, s, d_feats, d_row_mean, batch, H, W, d_w, d_bias, relu, y, rpw);
                 break;
             default: throw Error("stem: OC must be 16, 32 or 64");
         }
@@ -3168,7 +3185,7 @@ extern "C" int vdk_stem_conv3x3_ex(const float* d_feats, int batch, int H, int W
 
 extern "C" int vdk_stem_conv3x3(const float* d_feats, int batch, int H, int W, const float* d_w, const float* d_bias,
                                 int OC, int relu, void* d_y, void* stream) {
-    return vdk_stem_conv3x3_ex(d_feats, batch, H, W, d_w, d_bias, OC, relu, 0, d_y, stream);
+    return vdk_stem_conv3x3_ex(d_feats, nullptr, batch, H, W, d_w, d_bias, OC, relu, 0, d_y, stream);
 }
 
 extern "C" int vdk_resblock3x3_variant(const void* d_x, int batch, int H, int W, int C, const void* d_w1,

@@ -32,7 +32,8 @@ __device__ __forceinline__ int reflect_idx(int j, int pad, int T) {
     return t < 0 ? 0 : (t > T - 1 ? T - 1 : t);
 }
 
-__global__ __launch_bounds__(256) void feats_tmajor_kernel(const float* __restrict__ f, int B, int C, int T,
+__global__ __launch_bounds__(256) void feats_tmajor_kernel(const float* __restrict__ f,
+                                                           const float* __restrict__ rmean, int B, int C, int T,
                                                            int pad, int Cpad, half_t* __restrict__ out) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     const int Tp = T + 2 * pad;
@@ -40,7 +41,8 @@ __global__ __launch_bounds__(256) void feats_tmajor_kernel(const float* __restri
     const int c = (int)(i % Cpad);
     const long r = i / Cpad;
     const int j = (int)(r % Tp), b = (int)(r / Tp);
-    const float v = c < C ? f[((size_t)b * C + c) * T + reflect_idx(j, pad, T)] : 0.0f;
+    const float v = c < C ? f[((size_t)b * C + c) * T + reflect_idx(j, pad, T)] - (rmean ? rmean[(size_t)b * C + c] : 0.0f)
+                          : 0.0f;
     out[i] = (half_t)v;
 }
 
@@ -413,14 +415,14 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 using namespace vdk;
 
-extern "C" int vdk_feats_tmajor(const float* d_feats, int batch, int n_mels, int T, int pad, int c_pad, void* d_out,
-                                void* stream) {
+extern "C" int vdk_feats_tmajor(const float* d_feats, const float* d_row_mean, int batch, int n_mels, int T, int pad,
+                                int c_pad, void* d_out, void* stream) {
     return guarded([&] {
         require(d_feats && d_out, "feats_tmajor: NULL device pointer");
         require(batch > 0 && n_mels > 0 && T > 0 && pad >= 0 && c_pad >= n_mels, "feats_tmajor: bad shape");
         const long n = (long)batch * (T + 2 * pad) * c_pad;
         hipLaunchKernelGGL(feats_tmajor_kernel, dim3(cdiv(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                           d_feats, batch, n_mels, T, pad, c_pad, static_cast<half_t*>(d_out));
+                           d_feats, d_row_mean, batch, n_mels, T, pad, c_pad, static_cast<half_t*>(d_out));
         VDK_HIP(hipGetLastError());
     });
 }

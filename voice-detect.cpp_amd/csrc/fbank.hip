@@ -8,10 +8,15 @@
 // sums and log in f64 (MI355X runs f64 at full vector rate, and f64 keeps the
 // log of low-energy mel bins within 1e-4 of the reference).
 //
-// Layout: one wavefront per frame (4 frames per 256-thread workgroup), the
-// frame's complex spectrum in LDS (2 x n_fft doubles), radix-2 butterflies
-// spread over the 64 lanes; a second kernel does CMN with one workgroup per
-// (clip, mel bin) and a double-precision tree reduction over time.
+// Layout: one wavefront per frame, several frames per wavefront in turn (the
+// next frame's samples in flight during the current one), 4 wavefronts per
+// workgroup; the 512-point FFT is register resident (radix 8, two LDS
+// exchanges).  A workgroup's log-mel values collect in an LDS tile and leave
+// as runs of consecutive frames per mel row, and the workgroups of a clip run
+// on one XCD, so each output line is written once through one L2.  CMN: the
+// frames pass also writes each workgroup's per-mel sums, a small kernel adds
+// them into the per-clip means, and either a coalesced pass subtracts them or
+// the consumer of the features does as it loads them.
 #include <cfloat>
 #include <cmath>
 #include <cstring>
@@ -32,6 +37,16 @@ struct FbankDev {
     int n_mels, n_fft, log2n, pow2, win, hop, T, n_samples;
     int waves;              // frames processed concurrently per workgroup (one per wavefront)
     float preemph;
+};
+
+// Output side of the frames kernels.  CMN sums are fixed point (value * 2^36
+// rounded to a 64-bit integer), so they are exact whatever the grouping of
+// frames into workgroups (which changes with the batch size).
+constexpr double kCmnScale = 68719476736.0;   // 2^36
+struct FbankOut {
+    float* feats;               // [B][n_mels][T] log-mel energies (before CMN)
+    long long* part;            // [B][gc][n_mels] per-workgroup CMN sums, or NULL
+    int gc;                     // workgroups per clip
 };
 
 struct TableLayout {
@@ -265,91 +280,171 @@ __device__ __forceinline__ void dft8(cplx* x) {
     x[7] = {v[3].r - t3.r, v[3].i - t3.i};
 }
 
-constexpr int kX1 = 72;   // exchange-1 row stride (complex): row c, column a
+// The exchanges move the real parts through a per-wave buffer of doubles,
+// then the imaginary parts through the same buffer (half the LDS of a complex
+// buffer, so more workgroups fit on a CU).  Rows of 72 doubles keep each
+// half-wave of a ds_*_b64 on distinct banks for all three access patterns.
+constexpr int kX1 = 72;   // exchange-1 row stride (doubles): row c, column a
 constexpr int kX2 = 9;    // exchange-2: index c * 72 + d0 * 9 + a0
 
+// CMN sums of one workgroup's frames: per mel, the fixed-point sum of its
+// log values (`tile` [nf][pitch]) into part[b][g][m].
+__device__ __forceinline__ void cmn_part(const FbankOut& o, const float* tile, int pitch, int nf, int n_mels, int b,
+                                         int g) {
+    for (int m = threadIdx.x; m < n_mels; m += blockDim.x) {
+        long long s = 0;
+        for (int lf = 0; lf < nf; ++lf) s += __double2ll_rn((double)tile[lf * pitch + m] * kCmnScale);
+        o.part[((size_t)b * o.gc + g) * n_mels + m] = s;
+    }
+}
+
+// The workgroup's tile [nf][pitch] out to feats rows: consecutive threads
+// write consecutive frames of one mel row.
+__device__ __forceinline__ void store_tile(float* feats, const float* tile, int pitch, int nf, int F, int n_mels,
+                                           int T, int b, int t0) {
+    for (int i = threadIdx.x; i < n_mels * F; i += blockDim.x) {
+        const int m = i / F, lf = i - m * F;
+        if (lf < nf) feats[((size_t)b * n_mels + m) * T + t0 + lf] = tile[lf * pitch + m];
+    }
+}
+
+// The window and the twiddles are per-lane constants, read once from the
+// table block into registers; only the mel tables (from off_mel_start on) are
+// copied to LDS, which leaves room for three workgroups per CU.
 __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, const uint8_t* __restrict__ tables,
                                                                    int tab_bytes, int fpw,
-                                                                   const float* __restrict__ pcm,
-                                                                   float* __restrict__ feats) {
+                                                                   const float* __restrict__ pcm, FbankOut o) {
 #pragma clang fp contract(off)
     extern __shared__ double smem[];
     uint8_t* tab = reinterpret_cast<uint8_t*>(smem);
-    for (int i = threadIdx.x * 16; i < tab_bytes; i += blockDim.x * 16)
-        *reinterpret_cast<uint4*>(tab + i) = *reinterpret_cast<const uint4*>(tables + i);
+    const int mel0 = p.off_mel_start, mel_bytes = tab_bytes - mel0;   // both multiples of 256
+    for (int i = threadIdx.x * 16; i < mel_bytes; i += blockDim.x * 16)
+        *reinterpret_cast<uint4*>(tab + i) = *reinterpret_cast<const uint4*>(tables + mel0 + i);
     __syncthreads();
-    const double* window = reinterpret_cast<const double*>(tab + p.off_window);
-    const double* tw_re = reinterpret_cast<const double*>(tab + p.off_tw_re);   // cos(-2 pi j / 512)
-    const double* tw_im = reinterpret_cast<const double*>(tab + p.off_tw_im);
-    const int* mel_start = reinterpret_cast<const int*>(tab + p.off_mel_start);
-    const int* mel_len = reinterpret_cast<const int*>(tab + p.off_mel_len);
-    const int* mel_off = reinterpret_cast<const int*>(tab + p.off_mel_off);
-    const double* mel_w = reinterpret_cast<const double*>(tab + p.off_mel_w);
+    const double* window = reinterpret_cast<const double*>(tables + p.off_window);
+    const double* tw_re = reinterpret_cast<const double*>(tables + p.off_tw_re);   // cos(-2 pi j / 512)
+    const double* tw_im = reinterpret_cast<const double*>(tables + p.off_tw_im);
+    const int* mel_start = reinterpret_cast<const int*>(tab + p.off_mel_start - mel0);
+    const int* mel_len = reinterpret_cast<const int*>(tab + p.off_mel_len - mel0);
+    const int* mel_off = reinterpret_cast<const int*>(tab + p.off_mel_off - mel0);
+    const double* mel_w = reinterpret_cast<const double*>(tab + p.off_mel_w - mel0);
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int b = blockIdx.y;
-    cplx* xch = reinterpret_cast<cplx*>(smem + tab_bytes / 8) + (size_t)wave * (8 * kX1);
-    double* ps = reinterpret_cast<double*>(xch);   // reused after the last exchange (257 bins)
+    const int F = p.waves * fpw;                   // frames per workgroup
+    const int lid = xcd_swizzle(blockIdx.x, gridDim.x);
+    const int b = lid / o.gc, g = lid - b * o.gc, t0 = g * F;
+    cplx* const xbase = reinterpret_cast<cplx*>(smem + mel_bytes / 8);
+    cplx* const tw1 = xbase;                       // [c][lane]: W512^(lane c)
+    cplx* const tw2 = xbase + 8 * 64;              // [c][a0]: W64^(a0 c) = W512^(8 a0 c)
+    double* const xall = reinterpret_cast<double*>(xbase + 8 * 64 + 8 * 8);
+    double* xch = xall + (size_t)wave * (8 * kX1);
+    double* ps = xch;                              // reused after the last exchange (257 bins)
+    const int pitch = p.n_mels + 1;                // odd pitch: the row-wise tile reads hit distinct banks
+    float* tile = reinterpret_cast<float*>(xall + (size_t)p.waves * (8 * kX1));   // [F][pitch]
 
-    // per-lane twiddles, constant over frames: W512^(a c) for lane a and
+    // the twiddles, constant over frames, in LDS (in registers they would
+    // take 64 VGPRs and a wave per SIMD): W512^(a c) for lane a and
     // W64^(a0 d0) = W512^(8 a0 d0) for lane (c, a0) = (lane / 8, lane % 8)
-    cplx tw1[8], tw2[8];
-    const int a0 = lane & 7, cl = lane >> 3;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const int j1 = (lane * c) & 511, j2 = (8 * a0 * c) & 511;
-        tw1[c] = {j1 < 256 ? tw_re[j1] : -tw_re[j1 - 256], j1 < 256 ? tw_im[j1] : -tw_im[j1 - 256]};
-        tw2[c] = {j2 < 256 ? tw_re[j2] : -tw_re[j2 - 256], j2 < 256 ? tw_im[j2] : -tw_im[j2 - 256]};
+    auto w512 = [&](int j) {
+        return cplx{j < 256 ? tw_re[j] : -tw_re[j - 256], j < 256 ? tw_im[j] : -tw_im[j - 256]};
+    };
+    for (int i = threadIdx.x; i < 8 * 64 + 8 * 8; i += blockDim.x) {
+        if (i < 8 * 64) tw1[i] = w512(((i & 63) * (i >> 6)) & 511);
+        else tw2[i - 8 * 64] = w512((8 * ((i - 8 * 64) & 7) * ((i - 8 * 64) >> 3)) & 511);
     }
+    __syncthreads();
+    const int a0 = lane & 7, cl = lane >> 3;
 
-    for (int f = 0; f < fpw; ++f) {
-        const int t = (blockIdx.x * p.waves + wave) * fpw + f;
-        if (t >= p.T) break;                       // uniform per wavefront
+    double win[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) win[j] = lane + 64 * j < p.win ? window[lane + 64 * j] : 0.0;
+    // samples n = lane + 64 j of frame t (zero past the window)
+    auto load = [&](int t, float* xs) {
         const float* src = pcm + (size_t)b * p.n_samples + (size_t)t * p.hop;
-        // samples n = lane + 64 j; DC removal with a double sum (src/fbank.cpp:170-174)
-        float xs[8];
-        double s = 0.0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int n = lane + 64 * j;
             xs[j] = n < p.win ? src[n] : 0.0f;
-            s += (double)xs[j];
         }
+    };
+    const int tw0 = t0 + wave * fpw;               // this wave's frames: tw0 .. tw0 + fpw - 1
+    float xs[8];
+    if (tw0 < p.T) load(tw0, xs);
+    for (int f = 0; f < fpw; ++f) {
+        const int t = tw0 + f;
+        if (t >= p.T) break;                       // uniform per wavefront
+        float xn[8];
+        if (f + 1 < fpw && t + 1 < p.T) load(t + 1, xn);   // the next frame's samples, in flight meanwhile
+        // DC removal with a double sum (src/fbank.cpp:170-174)
+        double s = 0.0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += (double)xs[j];
         s = wave_sum(s);
         const float mean = (float)(s / p.win);
-        // pre-emphasis (replicate at n = 0) and povey window (src/fbank.cpp:176-183)
+        // pre-emphasis (replicate at n = 0) and povey window (src/fbank.cpp:176-183);
+        // sample n - 1 is lane - 1's value, or lane 63's of the previous j
         cplx v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int n = lane + 64 * j;
+            const float up = __shfl(xs[j], (lane + 63) & 63);
+            const float wrap =
+                j > 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xs[j > 0 ? j - 1 : 0]), 63)) : xs[0];
+            const float prev_raw = lane > 0 ? up : wrap;
             double y = 0.0;
             if (n < p.win) {
                 const float cur = xs[j] - mean;
-                const float prev = (n > 0 ? src[n - 1] : src[0]) - mean;
+                const float prev = prev_raw - mean;
                 const float e = cur - p.preemph * prev;
-                y = (double)(float)((double)e * window[n]);
+                y = (double)(float)((double)e * win[j]);
             }
             v[j] = {y, 0.0};
         }
         // pass 1: 8-point DFT over b, twiddle W512^(a c); store row c, column a
         dft8(v);
 #pragma unroll
-        for (int c = 0; c < 8; ++c) xch[c * kX1 + lane] = cmul(v[c], tw1[c]);
-        wave_sync();
+        for (int c = 0; c < 8; ++c) v[c] = cmul(v[c], tw1[c * 64 + lane]);
         // pass 2: lane (c, a0) gathers a = a0 + 8 a1, DFT over a1 -> d0, twiddle W64^(a0 d0)
+        {
+            cplx u[8];
 #pragma unroll
-        for (int a1 = 0; a1 < 8; ++a1) v[a1] = xch[cl * kX1 + a0 + 8 * a1];
+            for (int c = 0; c < 8; ++c) xch[c * kX1 + lane] = v[c].r;
+            wave_sync();
+#pragma unroll
+            for (int a1 = 0; a1 < 8; ++a1) u[a1].r = xch[cl * kX1 + a0 + 8 * a1];
+            wave_sync();
+#pragma unroll
+            for (int c = 0; c < 8; ++c) xch[c * kX1 + lane] = v[c].i;
+            wave_sync();
+#pragma unroll
+            for (int a1 = 0; a1 < 8; ++a1) u[a1].i = xch[cl * kX1 + a0 + 8 * a1];
+            wave_sync();
+#pragma unroll
+            for (int a1 = 0; a1 < 8; ++a1) v[a1] = u[a1];
+        }
         dft8(v);
-        wave_sync();
 #pragma unroll
-        for (int d0 = 0; d0 < 8; ++d0) xch[cl * kX1 + d0 * kX2 + a0] = cmul(v[d0], tw2[d0]);
-        wave_sync();
+        for (int d0 = 0; d0 < 8; ++d0) v[d0] = cmul(v[d0], tw2[d0 * 8 + a0]);
         // pass 3: lane (c, d0) gathers a0, DFT over a0 -> d1: X[c + 8 d0 + 64 d1]
         const int d0 = a0;
+        {
+            cplx u[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = xch[cl * kX1 + d0 * kX2 + q];
+            for (int k = 0; k < 8; ++k) xch[cl * kX1 + k * kX2 + a0] = v[k].r;
+            wave_sync();
+#pragma unroll
+            for (int q = 0; q < 8; ++q) u[q].r = xch[cl * kX1 + d0 * kX2 + q];
+            wave_sync();
+#pragma unroll
+            for (int k = 0; k < 8; ++k) xch[cl * kX1 + k * kX2 + a0] = v[k].i;
+            wave_sync();
+#pragma unroll
+            for (int q = 0; q < 8; ++q) u[q].i = xch[cl * kX1 + d0 * kX2 + q];
+            wave_sync();
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[q] = u[q];
+        }
         dft8(v);
-        wave_sync();
         // power spectrum |X_k|^2 for k <= 256
 #pragma unroll
         for (int d1 = 0; d1 < 8; ++d1) {
@@ -357,20 +452,30 @@ __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, 
             if (k <= 256) ps[k] = v[d1].r * v[d1].r + v[d1].i * v[d1].i;
         }
         wave_sync();
+        float* trow = tile + (t - t0) * pitch;
         for (int m = lane; m < p.n_mels; m += 64) {
             double e = 0.0;
             const int st = mel_start[m], n = mel_len[m];
             const double* w = mel_w + mel_off[m];
             for (int k = 0; k < n; ++k) e += w[k] * ps[st + k];
             const double fl = (double)FLT_EPSILON;
-            feats[((size_t)b * p.n_mels + m) * p.T + t] = (float)log(e > fl ? e : fl);
+            trow[m] = (float)log(e > fl ? e : fl);
         }
         wave_sync();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xs[j] = xn[j];
     }
+    __syncthreads();
+    const int nf = p.T - t0 < F ? p.T - t0 : F;
+    store_tile(o.feats, tile, pitch, nf, F, p.n_mels, p.T, b, t0);
+    if (o.part) cmn_part(o, tile, pitch, nf, p.n_mels, b, g);
 }
 
-// Per-utterance CMN (src/fbank.cpp:194-201): one workgroup per (mel bin, clip).
-__global__ __launch_bounds__(256) void fbank_cmn_kernel(float* __restrict__ feats, int n_mels, int T) {
+// CMN means of the generic path's features (src/fbank.cpp:194-201): one
+// workgroup per (mel bin, clip), a double tree reduction over time; the mean
+// goes to `mean` (may be NULL) and, with `apply`, is subtracted in place.
+__global__ __launch_bounds__(256) void fbank_cmn_kernel(float* __restrict__ feats, int n_mels, int T,
+                                                        float* __restrict__ mean, int apply) {
     __shared__ double part[4];
     float* row = feats + ((size_t)blockIdx.y * n_mels + blockIdx.x) * T;
     double s = 0.0;
@@ -380,7 +485,34 @@ __global__ __launch_bounds__(256) void fbank_cmn_kernel(float* __restrict__ feat
     __syncthreads();
     const double tot = part[0] + part[1] + part[2] + part[3];
     const float mu = (float)(tot / T);
-    for (int t = threadIdx.x; t < T; t += 256) row[t] = row[t] - mu;
+    if (mean && threadIdx.x == 0) mean[(size_t)blockIdx.y * n_mels + blockIdx.x] = mu;
+    if (apply)
+        for (int t = threadIdx.x; t < T; t += 256) row[t] = row[t] - mu;
+}
+
+// CMN means from the frames pass's per-workgroup sums: 16 lanes per (clip,
+// mel) row, each adding every 16th workgroup's sum, then a butterfly over the
+// 16 lanes (integer sums: exact in any order), then / 2^36 / T.
+__global__ __launch_bounds__(256) void fbank_mean_kernel(const long long* __restrict__ part, int gc, int n_mels,
+                                                         int rows, int T, float* __restrict__ mean) {
+    const int i = blockIdx.x * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
+    long long s = 0;
+    if (i < rows) {
+        const int b = i / n_mels, m = i - b * n_mels;
+        const long long* p = part + (size_t)b * gc * n_mels + m;
+        for (int g = l; g < gc; g += 16) s += p[(size_t)g * n_mels];
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
+    if (i < rows && l == 0) mean[i] = (float)((double)s / kCmnScale / T);
+}
+
+// feats[b][m][t] -= mean[b][m]: the CMN subtraction (f32) over the whole map.
+__global__ __launch_bounds__(256) void fbank_sub_mean_kernel(float* __restrict__ feats, const float* __restrict__ mean,
+                                                             long n, int T) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    feats[i] = feats[i] - mean[i / T];
 }
 
 }  // namespace
@@ -429,63 +561,149 @@ extern "C" int vdk_fbank_tables_fill(const vdk_fbank_cfg* cfg, void* d_tables) {
     });
 }
 
+namespace {
+
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int fbank_frames(const vdk_fbank_cfg& c, int n_samples) { return 1 + (n_samples - c.win_length) / c.hop_length; }
+
+// CMN workspace: per-workgroup sums [B][ceil(T/4)][n_mels] (workgroups hold at
+// least 4 frames) and the means [B][n_mels] when the caller takes none.
+size_t work_bytes(const vdk_fbank_cfg& c, int batch, int n_samples) {
+    const int T = n_samples >= c.win_length ? fbank_frames(c, n_samples) : 1;
+    return al256(8 * (size_t)batch * cdiv(T, 4) * c.n_mels) + al256(4 * (size_t)batch * c.n_mels);
+}
+
+void fbank_run(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pcm, int batch, int n_samples,
+               float* d_feats, float* d_mean, void* d_work, size_t work_size, hipStream_t s) {
+    check_cfg(cfg);
+    require(d_tables && d_pcm && d_feats, "fbank: NULL device pointer");
+    require(batch > 0, "fbank: batch must be positive");
+    require(n_samples >= cfg->win_length, "voicedetect: FBank produced no frames");
+    const vdk_fbank_cfg& c = *cfg;
+    require(!c.cmn || (d_work && work_size >= work_bytes(c, batch, n_samples) &&
+                       (reinterpret_cast<uintptr_t>(d_work) & 255) == 0),
+            "fbank: CMN needs a 256-byte aligned workspace of vdk_fbank_workspace_size bytes");
+    std::vector<int> st, ln, of;
+    std::vector<double> w;
+    mel_sparse(c, st, ln, of, w);
+    const TableLayout L = layout(c, (int)w.size());
+    FbankDev p;
+    p.off_window = (int)L.window;
+    p.off_tw_re = (int)L.tw_re;
+    p.off_tw_im = (int)L.tw_im;
+    p.off_mel_start = (int)L.mel_start;
+    p.off_mel_len = (int)L.mel_len;
+    p.off_mel_off = (int)L.mel_off;
+    p.off_mel_w = (int)L.mel_w;
+    p.n_mels = c.n_mels;
+    p.n_fft = c.n_fft;
+    p.pow2 = (c.n_fft & (c.n_fft - 1)) == 0;
+    p.log2n = 0;
+    while ((1 << p.log2n) < c.n_fft) ++p.log2n;
+    p.win = c.win_length;
+    p.hop = c.hop_length;
+    p.T = 1 + (n_samples - c.win_length) / c.hop_length;
+    p.n_samples = n_samples;
+    p.preemph = c.preemph;
+    p.waves = c.n_fft <= 512 ? kFbMaxWaves : 2;
+    // frames per wavefront: enough to amortise the table copy, while
+    // keeping >= ~4 workgroups per CU at batch 64
+    int fpw = p.T >= 256 ? 4 : (p.T >= 64 ? 2 : 1);
+    // small batches: fewer frames per wavefront until the launch covers
+    // the CUs (each frame's arithmetic is the same whatever the grouping)
+    while (fpw > 1 && (long)batch * cdiv(p.T, p.waves * fpw) < 256) fpw /= 2;
+    const int gc = cdiv(p.T, p.waves * fpw);
+    const bool radix8 = c.n_fft == 512 && c.win_length <= 512;
+    const size_t per_wave = radix8 ? (size_t)8 * kX1 * sizeof(double)
+                                   : (size_t)(2 * c.n_fft + c.n_fft / 2) * sizeof(double);
+    const size_t tile = radix8 ? (size_t)p.waves * fpw * (c.n_mels + 1) * sizeof(float) : 0;
+    const size_t twid = radix8 ? (size_t)(8 * 64 + 8 * 8) * sizeof(cplx) : 0;
+    const size_t shmem = (radix8 ? L.total - L.mel_start : L.total) + twid + (size_t)p.waves * per_wave + tile;
+    require(shmem <= 160 * 1024, "fbank: configuration needs more LDS than a workgroup has");
+    long long* const part = c.cmn ? static_cast<long long*>(d_work) : nullptr;
+    float* const mean = d_mean ? d_mean
+                               : (c.cmn ? reinterpret_cast<float*>(static_cast<uint8_t*>(d_work) +
+                                                                   al256(8 * (size_t)batch * cdiv(p.T, 4) * c.n_mels))
+                                        : nullptr);
+    if (radix8) {
+        if (shmem > 64 * 1024)
+            VDK_HIP(hipFuncSetAttribute((const void*)fbank512_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)shmem));
+        FbankOut o{d_feats, part, gc};
+        hipLaunchKernelGGL(fbank512_kernel, dim3(batch * gc), dim3(p.waves * 64), shmem, s, p,
+                           static_cast<const uint8_t*>(d_tables), (int)L.total, fpw, d_pcm, o);
+        VDK_HIP(hipGetLastError());
+        if (c.cmn) {
+            const int rows = batch * c.n_mels;
+            hipLaunchKernelGGL(fbank_mean_kernel, dim3(cdiv(rows, 16)), dim3(256), 0, s, part, gc, c.n_mels, rows,
+                               p.T, mean);
+            VDK_HIP(hipGetLastError());
+        }
+        if (c.cmn && !d_mean) {   // the means subtracted here, in place
+            const long n = (long)batch * c.n_mels * p.T;
+            hipLaunchKernelGGL(fbank_sub_mean_kernel, dim3(cdiv(n, 256)), dim3(256), 0, s, d_feats, mean, n, p.T);
+            VDK_HIP(hipGetLastError());
+        }
+    } else {
+        dim3 grid(gc, batch);
+        if (shmem > 64 * 1024)
+            VDK_HIP(hipFuncSetAttribute((const void*)fbank_frames_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)shmem));
+        hipLaunchKernelGGL(fbank_frames_kernel, grid, dim3(p.waves * 64), shmem, s, p,
+                           static_cast<const uint8_t*>(d_tables), (int)L.total, fpw, d_pcm, d_feats);
+        VDK_HIP(hipGetLastError());
+        if (c.cmn) {
+            hipLaunchKernelGGL(fbank_cmn_kernel, dim3(c.n_mels, batch), dim3(256), 0, s, d_feats, c.n_mels, p.T,
+                               d_mean, d_mean ? 0 : 1);
+            VDK_HIP(hipGetLastError());
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" size_t vdk_fbank_workspace_size(const vdk_fbank_cfg* cfg, int batch, int n_samples) {
+    if (!cfg || batch <= 0 || n_samples <= 0) {
+        set_error("fbank: bad workspace query");
+        return 0;
+    }
+    return cfg->cmn ? work_bytes(*cfg, batch, n_samples) : 0;
+}
+
+extern "C" int vdk_fbank_ex(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pcm, int batch,
+                            int n_samples, float* d_feats, float* d_mean, void* d_work, size_t work_size,
+                            void* stream) {
+    return guarded([&] {
+        fbank_run(cfg, d_tables, d_pcm, batch, n_samples, d_feats, d_mean, d_work, work_size,
+                  static_cast<hipStream_t>(stream));
+    });
+}
+
 extern "C" int vdk_fbank(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pcm,
                          int batch, int n_samples, float* d_feats, void* stream) {
     return guarded([&] {
-        check_cfg(cfg);
-        require(d_tables && d_pcm && d_feats, "fbank: NULL device pointer");
-        require(batch > 0, "fbank: batch must be positive");
-        require(n_samples >= cfg->win_length, "voicedetect: FBank produced no frames");
-        const vdk_fbank_cfg& c = *cfg;
-        std::vector<int> st, ln, of;
-        std::vector<double> w;
-        mel_sparse(c, st, ln, of, w);
-        const TableLayout L = layout(c, (int)w.size());
-        FbankDev p;
-        p.off_window = (int)L.window;
-        p.off_tw_re = (int)L.tw_re;
-        p.off_tw_im = (int)L.tw_im;
-        p.off_mel_start = (int)L.mel_start;
-        p.off_mel_len = (int)L.mel_len;
-        p.off_mel_off = (int)L.mel_off;
-        p.off_mel_w = (int)L.mel_w;
-        p.n_mels = c.n_mels;
-        p.n_fft = c.n_fft;
-        p.pow2 = (c.n_fft & (c.n_fft - 1)) == 0;
-        p.log2n = 0;
-        while ((1 << p.log2n) < c.n_fft) ++p.log2n;
-        p.win = c.win_length;
-        p.hop = c.hop_length;
-        p.T = 1 + (n_samples - c.win_length) / c.hop_length;
-        p.n_samples = n_samples;
-        p.preemph = c.preemph;
-        p.waves = c.n_fft <= 512 ? kFbMaxWaves : 2;
-        // frames per wavefront: enough to amortise the table copy, while
-        // keeping >= ~4 workgroups per CU at batch 64
-        int fpw = p.T >= 256 ? 4 : (p.T >= 64 ? 2 : 1);
-        // small batches: fewer frames per wavefront until the launch covers
-        // the CUs (each frame's arithmetic is the same whatever the grouping)
-        while (fpw > 1 && (long)batch * cdiv(p.T, p.waves * fpw) < 256) fpw /= 2;
+        require(cfg != nullptr && batch > 0, "fbank: cfg is NULL or batch not positive");
         hipStream_t s = static_cast<hipStream_t>(stream);
-        dim3 grid(cdiv(p.T, p.waves * fpw), batch);
-        const bool radix8 = c.n_fft == 512 && c.win_length <= 512;
-        const size_t per_wave = radix8 ? (size_t)8 * kX1 * sizeof(cplx)
-                                       : (size_t)(2 * c.n_fft + c.n_fft / 2) * sizeof(double);
-        const size_t shmem = L.total + (size_t)p.waves * per_wave;
-        require(shmem <= 160 * 1024, "fbank: configuration needs more LDS than a workgroup has");
-        const void* fn = radix8 ? (const void*)fbank512_kernel : (const void*)fbank_frames_kernel;
-        if (shmem > 64 * 1024)
-            VDK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
-        if (radix8)
-            hipLaunchKernelGGL(fbank512_kernel, grid, dim3(p.waves * 64), shmem, s, p,
-                               static_cast<const uint8_t*>(d_tables), (int)L.total, fpw, d_pcm, d_feats);
-        else
-            hipLaunchKernelGGL(fbank_frames_kernel, grid, dim3(p.waves * 64), shmem, s, p,
-                               static_cast<const uint8_t*>(d_tables), (int)L.total, fpw, d_pcm, d_feats);
-        VDK_HIP(hipGetLastError());
-        if (c.cmn) {
-            hipLaunchKernelGGL(fbank_cmn_kernel, dim3(c.n_mels, batch), dim3(256), 0, s, d_feats, c.n_mels, p.T);
-            VDK_HIP(hipGetLastError());
+        void* work = nullptr;
+        const size_t bytes = cfg->cmn && n_samples >= cfg->win_length ? work_bytes(*cfg, batch, n_samples) : 0;
+        if (bytes) VDK_HIP(hipMallocAsync(&work, bytes, s));
+        try {
+            fbank_run(cfg, d_tables, d_pcm, batch, n_samples, d_feats, nullptr, work, bytes, s);
+        } catch (...) {
+            if (work) (void)hipFreeAsync(work, s);
+            throw;
         }
+        if (work) VDK_HIP(hipFreeAsync(work, s));
+    });
+}
+
+extern "C" int vdk_fbank_sub_mean(float* d_feats, const float* d_mean, int batch, int n_mels, int T, void* stream) {
+    return guarded([&] {
+        require(d_feats && d_mean && batch > 0 && n_mels > 0 && T > 0, "fbank_sub_mean: bad arguments");
+        const long n = (long)batch * n_mels * T;
+        hipLaunchKernelGGL(fbank_sub_mean_kernel, dim3(cdiv(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           d_feats, d_mean, n, T);
+        VDK_HIP(hipGetLastError());
     });
 }

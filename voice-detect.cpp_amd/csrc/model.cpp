@@ -289,6 +289,11 @@ void Model::ensure_workspace(int batch, int n_samples) {
         return;
     }
     w.feats = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * nmel * T));
+    if (cfg_.fbank.cmn) {
+        w.fb_mean = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * nmel));
+        w.fb_work_bytes = vdk_fbank_workspace_size(&cfg_.fbank, batch, n_samples);
+        w.fb_work = ws_alloc(w.fb_work_bytes);
+    }
     w.pooled = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * pooled_dim_));
     w.pre = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * cfg_.embedding_dim));
     w.emb = static_cast<float*>(ws_alloc(sizeof(float) * (size_t)batch * cfg_.embedding_dim));
@@ -366,7 +371,10 @@ void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) 
     const int nmel = cfg_.fbank.n_mels;
     // FBank front end
     prof_begin("fbank", 0.0, 4.0 * batch * ((double)n_samples + (double)nmel * T));
-    check(vdk_fbank(&cfg_.fbank, fb_tables_, d_pcm, batch, n_samples, ws_.feats, stream_));
+    // the features stay un-normalised: the encoder's first kernel subtracts
+    // the CMN means as it loads them
+    check(vdk_fbank_ex(&cfg_.fbank, fb_tables_, d_pcm, batch, n_samples, ws_.feats, ws_.fb_mean, ws_.fb_work,
+                       ws_.fb_work_bytes, stream_));
     prof_end();
     if (cfg_.arch == "ecapa_tdnn") encode_ecapa(batch, T);
     else if (cfg_.arch == "campplus") encode_campplus(batch, T);
@@ -387,7 +395,8 @@ void Model::encode_resnet(int batch, int T) {
     // stem conv + ReLU
     prof_begin("stem3x3", 2.0 * 9 * stem_oc_ * (double)batch * nmel * T,
                4.0 * batch * nmel * T + 2.0 * batch * nmel * T * stem_oc_);
-    check(vdk_stem_conv3x3(ws_.feats, batch, nmel, T, stem_w_, stem_b_, stem_oc_, 1, ws_.act[0], stream_));
+    check(vdk_stem_conv3x3_ex(ws_.feats, ws_.fb_mean, batch, nmel, T, stem_w_, stem_b_, stem_oc_, 1, 0, ws_.act[0],
+                              stream_));
     prof_end();
     int xi = 0, C = stem_oc_, H = nmel, W = T;
     for (const Block& b : blocks_) {
@@ -455,19 +464,27 @@ void Model::embed_capture(const float* pcm, int batch, int n_samples, float* fea
     ensure_device();
     ensure_workspace(batch, n_samples);
     const size_t E = (size_t)cfg_.embedding_dim;
-    VDK_HIP(hipMemcpyAsync(ws_.pcm, pcm, sizeof(float) * (size_t)batch * n_samples, hipMemcpyHostToDevice, stream_));
+    if (!copy_pool_) {
+        const unsigned hw = std::thread::hardware_concurrency();
+        copy_pool_.reset(new CopyPool((int)std::min(3u, hw > 1 ? hw / 2 : 0u)));
+    }
+    stage_h2d(*copy_pool_, pin_in_, ws_.pcm, pcm, batch, sizeof(float) * (size_t)n_samples, 8, stream_);
     forward(ws_.pcm, batch, n_samples, ws_.emb);
     const size_t T = (size_t)frames(n_samples);
-    if (feats)
+    if (feats) {   // the features as vdk_fbank gives them: with the CMN subtraction
+        if (ws_.fb_mean) check(vdk_fbank_sub_mean(ws_.feats, ws_.fb_mean, batch, cfg_.fbank.n_mels, (int)T, stream_));
         VDK_HIP(hipMemcpyAsync(feats, ws_.feats, sizeof(float) * batch * cfg_.fbank.n_mels * T,
                                hipMemcpyDeviceToHost, stream_));
+    }
     if (pooled)
         VDK_HIP(hipMemcpyAsync(pooled, ws_.pooled, sizeof(float) * batch * pooled_dim_, hipMemcpyDeviceToHost,
                                stream_));
     if (pre_norm)
         VDK_HIP(hipMemcpyAsync(pre_norm, ws_.pre, sizeof(float) * batch * E, hipMemcpyDeviceToHost, stream_));
-    if (out) VDK_HIP(hipMemcpyAsync(out, ws_.emb, sizeof(float) * batch * E, hipMemcpyDeviceToHost, stream_));
+    float* const eo = out ? static_cast<float*>(pin_out_.get(sizeof(float) * batch * E)) : nullptr;
+    if (out) VDK_HIP(hipMemcpyAsync(eo, ws_.emb, sizeof(float) * batch * E, hipMemcpyDeviceToHost, stream_));
     VDK_HIP(hipStreamSynchronize(stream_));
+    if (out) std::memcpy(out, eo, sizeof(float) * batch * E);
 }
 
 void Model::embed_batch_host(const float* pcm, int batch, int n_samples, float* out) {

@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "gguf.hpp"
+#include "hoststage.hpp"
 #include "vdk.h"
 
 namespace vdk {
@@ -260,7 +261,10 @@ private:
         std::vector<void*> allocs;      // every allocation below, freed together
         size_t act_bytes = 0;
         float* pcm = nullptr;
-        float* feats = nullptr;
+        float* feats = nullptr;         // log-mel energies before CMN (the consumers subtract fb_mean)
+        float* fb_mean = nullptr;       // [B][n_mels] CMN means, or NULL without CMN
+        void* fb_work = nullptr;        // vdk_fbank_ex workspace (per-workgroup CMN sums)
+        size_t fb_work_bytes = 0;
         void* act[4] = {nullptr, nullptr, nullptr, nullptr};
         float* pooled = nullptr;
         float* pre = nullptr;
@@ -338,6 +342,9 @@ private:
     bool ready_ = false;
     int device_ = 0;
     hipStream_t stream_ = nullptr;
+    // host-buffer entry points: pinned staging of the PCM and of the results
+    std::unique_ptr<CopyPool> copy_pool_;
+    PinnedBuffer pin_in_, pin_out_;
     void* arena_ = nullptr;
     void* fb_tables_ = nullptr;
     float* stem_w_ = nullptr;

@@ -226,7 +226,8 @@ void Model::encode_campplus(int batch, int T) {
     int H = m.n_mels;
     prof_begin("campp_stem3x3", 2.0 * 9 * m.m_ch * (double)batch * H * T,
                4.0 * batch * H * T + 2.0 * batch * H * T * m.m_ch);
-    check_rc(vdk_stem_conv3x3(w.feats, batch, H, T, m.stem_w, m.stem_b, m.m_ch, 1, w.fcm[0], stream_));
+    check_rc(vdk_stem_conv3x3_ex(w.feats, w.fb_mean, batch, H, T, m.stem_w, m.stem_b, m.m_ch, 1, 0, w.fcm[0],
+                                 stream_));
     prof_end();
     auto fconv = [&](const char* name, const Layer& l, const void* x, int Hin, int sh, int pad, const void* res,
                      int relu, void* y) {

@@ -303,7 +303,7 @@ void Model::encode_ecapa(int batch, int T) {
     // block0: reflect pad (k-1)/2, time-major, zero channels to c_pad0
     const int pad0 = (e.block0.k - 1) / 2;
     prof_begin("ecapa_feats_tmajor", 0.0, 4.0 * batch * (double)e.n_mels * T + 2.0 * batch * (T + 2.0 * pad0) * e.c_pad0);
-    check_rc(vdk_feats_tmajor(w.feats, batch, e.n_mels, T, pad0, e.c_pad0, w.x0p, stream_));
+    check_rc(vdk_feats_tmajor(w.feats, w.fb_mean, batch, e.n_mels, T, pad0, e.c_pad0, w.x0p, stream_));
     prof_end();
     tdnn("ecapa_block0", e.block0, w.x0p, e.c_pad0, batch, T + 2 * pad0, 1, e.block0.b, 0, 1, 0, w.h0, C, 0);
 

@@ -283,7 +283,7 @@ void Model::encode_eres2net(int batch, int T) {
 
     int H = m.n_mels, W = T;
     prof_begin("eres_stem3x3", 2.0 * 9 * m.m * (double)batch * H * W, 4.0 * batch * H * W + 4.0 * batch * H * W * m.m);
-    check_rc(vdk_stem_conv3x3_ex(w.feats, batch, H, W, m.stem_w, m.stem_b, m.m, 1, 1, w.ex[0], stream_));
+    check_rc(vdk_stem_conv3x3_ex(w.feats, w.fb_mean, batch, H, W, m.stem_w, m.stem_b, m.m, 1, 1, w.ex[0], stream_));
     prof_end();
     View x = split_tensor(w.ex[0], m.m);
     int xi = 0;

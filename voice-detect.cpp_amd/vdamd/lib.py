@@ -111,6 +111,9 @@ _SIGS = {
     "vdk_fbank_tables_size": (C.c_size_t, [C.POINTER(FbankCfg)]),
     "vdk_fbank_tables_fill": (C.c_int, [C.POINTER(FbankCfg), _vp]),
     "vdk_fbank": (C.c_int, [C.POINTER(FbankCfg), _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_fbank_workspace_size": (C.c_size_t, [C.POINTER(FbankCfg), C.c_int, C.c_int]),
+    "vdk_fbank_ex": (C.c_int, [C.POINTER(FbankCfg), _vp, _vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_size_t, _vp]),
+    "vdk_fbank_sub_mean": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp]),
     "vdk_conv2d_nhwc": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
                                   C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp]),
     "vdk_conv2d_nhwc_tile": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_int,
@@ -138,8 +141,8 @@ _SIGS = {
     "vdk_stem_conv3x3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_tstp": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
     "vdk_tstp_ex": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, _vp, _vp]),
-    "vdk_stem_conv3x3_ex": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int, _vp,
-                                      _vp]),
+    "vdk_stem_conv3x3_ex": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int,
+                                      _vp, _vp]),
     "vdk_linear_workspace_size": (C.c_size_t, [C.c_int, C.c_int, C.c_int]),
     "vdk_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp, C.c_size_t, _vp]),
     "vdk_linear_ex": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _vp, C.c_size_t,
@@ -147,7 +150,7 @@ _SIGS = {
     "vdk_linear_ex_noalloc": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_l2norm": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
     "vdk_l2norm_to": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp]),
-    "vdk_feats_tmajor": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_feats_tmajor": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_reflect_pad_add": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_channel_mean": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_se_gate_residual": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int,
