@@ -25,9 +25,12 @@ timed pass of the same steps records events around that class's launches only
 achieved = algorithmic FLOPs (direct conv) or bytes per launch / duration,
 against the MFMA f16 or HBM peak depending on which side of the ridge the
 kernel's arithmetic intensity lies.  `traffic` is that kernel's HBM bytes per
-launch from rocprofv3 FETCH_SIZE / WRITE_SIZE counters scaled by the
-counters' reading for a device copy of known size (--copy-calibration-mib
-runs that copy); null where not measured.  The CPU baseline times the oracle
+launch, measured in the same run: before the bench touches the GPU, two
+child processes run the run's workloads under `rocprofv3 --pmc FETCH_SIZE`
+and `--pmc WRITE_SIZE`, each counter scaled by its reading for a device copy
+of known size; `traffic_source` names the kernel and launch grid it was read
+from (null with the reason where rocprofv3 is absent or --no-traffic is
+given).  The CPU baseline times the oracle
 (this repository's C restatement of the reference CPU path) on a bounded
 sample of the same clips, clip-parallel on min(cores, 8) threads like the
 reference's default.
@@ -52,16 +55,17 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 RIDGE_FLOP_PER_BYTE = PEAK_F16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
 CLIP_SEED = 1234
 
-# HBM bytes per launch of a workload's dominant kernel: rocprofv3 --pmc
-# FETCH_SIZE and WRITE_SIZE (KiB per dispatch, averaged over the class's
-# launches), each scaled by copy bytes / the counter's reading for a 256 MiB
-# device copy in the same run.
-TRAFFIC_BYTES_PER_LAUNCH = {
-    # conv3x3_bandws_kernel<5, 75, 2, 4, 3, 4> (the 11 stride-1 128->128 convs
-    # per step): FETCH 48.03 MB, WRITE 24.58 MB per launch after the copy
-    # calibration, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this bench
-    ("resnet34", "conv3x3_s1_128to128"): 72.61e6,
-}
+# HBM traffic of the dominant kernels, measured in the same bench run: before
+# this process touches the GPU, two child processes run every workload of the
+# run under `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` (one counter
+# per pass), with a device copy of known size after each workload that both
+# separates the workloads in the dispatch list and calibrates the counters
+# (bytes moved / counter reading).  A workload's dominant class is then the
+# (kernel, grid) group of its dispatches whose count matches the class's
+# launches per step and which takes the most time.
+TRAFFIC_STEPS = 3
+TRAFFIC_COPY_MIB = 96        # above any workload's PCM upload, so the copies are told apart
+TRAFFIC_TIMEOUT_S = 150
 
 # The reference's own published figures for these workloads (per clip, batch 1;
 # it publishes nothing batched): reported beside ours, not divided into them.
@@ -269,7 +273,107 @@ def cpu_baseline_w2v2(gguf_path, pcm, n_seconds, threads, avail, min_seconds):
                       f"host {_cpu_name()}, {avail} cores available"}
 
 
-def measure(L, key, steps, warmup, cpu_seconds, registry=0, copy_mib=0, b1_reps=0):
+def traffic_child(keys):
+    """Child of a traffic pass (run under rocprofv3 --pmc): each workload for
+    TRAFFIC_STEPS batches after one warmup batch, then TRAFFIC_COPY_MIB device
+    copies (3x) that close its segment of the dispatch list."""
+    L = lib.lib()
+    nb = TRAFFIC_COPY_MIB << 20
+    src, dst = lib.DeviceBuffer(nb), lib.DeviceBuffer(nb)
+    lib.check(L.vdk_memset(src.ptr, 1, nb))
+    for key in keys:
+        model = MODELS[key]
+        batch, n = model["batch"], model["n"]
+        path = os.path.join(tempfile.mkdtemp(), f"{key}.gguf")
+        model["write"](path, seed=model["seed"])
+        ctx = lib.Context(path)
+        d_pcm = lib.DeviceBuffer.from_array(synth.clips(CLIP_SEED, batch, n))
+        width = ctx.analyze_outputs() if model.get("kind") == "analyze" else ctx.dim
+        d_out = lib.DeviceBuffer(batch * width * 4)
+        run = (lambda: ctx.analyze_device_async(d_pcm.ptr, batch, n, d_out.ptr)) if model.get("kind") == "analyze" \
+            else (lambda: ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr))
+        for _ in range(1 + TRAFFIC_STEPS):
+            run()
+        ctx.synchronize()
+        ctx.close()
+        for _ in range(3):
+            lib.check(L.vdk_memcpy_d2d(dst.ptr, src.ptr, nb))
+        lib.check(L.vdk_synchronize())
+
+
+def traffic_passes(keys):
+    """Run the two counter passes; returns {key: [dispatch groups]} where a
+    group is {kernel, grid, count, us, fetch_b, write_b} (bytes per dispatch,
+    calibrated), or {"error": why}."""
+    import csv
+    import shutil
+    import subprocess
+    if shutil.which("rocprofv3") is None:
+        return {"error": "rocprofv3 not on PATH"}
+    out = {}
+    env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp()
+        cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "run", "--",
+               sys.executable, os.path.abspath(__file__), "--traffic-child", ",".join(keys)]
+        try:
+            r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, timeout=TRAFFIC_TIMEOUT_S,
+                               env=env)
+        except subprocess.TimeoutExpired:
+            return {"error": f"rocprofv3 --pmc {counter} pass timed out"}
+        files = [os.path.join(dp, f) for dp, _, fs in os.walk(d) for f in fs if f.endswith("counter_collection.csv")]
+        if not files:
+            return {"error": f"rocprofv3 --pmc {counter} wrote no counters (rc {r.returncode})"}
+        rows = sorted(csv.DictReader(open(files[0])), key=lambda row: int(row["Dispatch_Id"]))
+        # segments: the dispatches of workload i end at its 3 calibration copies
+        seg, segs, cal = [], [], []
+        for row in rows:
+            if "copyBuffer" in row["Kernel_Name"]:
+                if float(row["Counter_Value"]) > (TRAFFIC_COPY_MIB << 10) / 4:   # KiB: a calibration copy
+                    cal.append(float(row["Counter_Value"]) * 1024.0)
+                    if seg:
+                        segs.append(seg)
+                        seg = []
+                continue
+            seg.append(row)
+        if len(segs) != len(keys) or not cal:
+            return {"error": f"{counter}: {len(segs)} dispatch segments for {len(keys)} workloads"}
+        factor = (TRAFFIC_COPY_MIB << 20) / float(np.median(cal))
+        for key, sg in zip(keys, segs):
+            groups = out.setdefault(key, {})
+            for row in sg:
+                g = groups.setdefault((row["Kernel_Name"], int(row["Grid_Size"])),
+                                      {"count": 0, "us": 0.0, "FETCH_SIZE": 0.0, "WRITE_SIZE": 0.0})
+                if counter == "FETCH_SIZE":
+                    g["count"] += 1
+                    g["us"] += (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
+                g[counter] += float(row["Counter_Value"]) * 1024.0 * factor
+            out.setdefault("_factors", {})[counter] = round(factor, 4)
+    return out
+
+
+def traffic_of(tr, key, launches_per_step, label):
+    """Measured HBM bytes per launch of `key`'s dominant class, or (None, why):
+    the (kernel, grid) group with that many launches per step (a conv kernel
+    for a conv class) that takes the most time."""
+    if not tr or "error" in tr:
+        return None, (tr or {}).get("error", "traffic not measured")
+    groups = tr.get(key)
+    if not groups:
+        return None, f"no dispatches recorded for {key}"
+    want = launches_per_step * TRAFFIC_STEPS
+    cands = [(g["us"], name, grid, g) for (name, grid), g in groups.items()
+             if g["count"] in (want, want + launches_per_step) and (not label.startswith("conv") or "conv" in name)]
+    if not cands:
+        return None, (f"no single kernel launch group with the class's {launches_per_step} launches per step "
+                      "(its launches use several kernels or grids)")
+    _, name, grid, g = max(cands, key=lambda c: c[0])
+    n = g["count"]
+    return {"kernel": name, "grid": grid, "fetch_bytes": g["FETCH_SIZE"] / n, "write_bytes": g["WRITE_SIZE"] / n,
+            "factors": tr.get("_factors")}, None
+
+
+def measure(L, key, steps, warmup, cpu_seconds, registry=0, copy_mib=0, b1_reps=0, traffic=None):
     """One workload: throughput over `steps` batches, a per-kernel events pass,
     the dominant kernel's roofline from an events pass over its launches only,
     the host-buffer rate, optionally the batch-1 latency and the CPU baseline."""
@@ -335,10 +439,15 @@ def measure(L, key, steps, warmup, cpu_seconds, registry=0, copy_mib=0, b1_reps=
         bound, achieved, peak, r_unit = "mfma", fl / avg_s / 1e12, PEAK_F16_TFLOPS, "TFLOP/s"
     else:
         bound, achieved, peak, r_unit = "hbm", by / avg_s / 1e9, PEAK_HBM_GBS, "GB/s"
-    traffic = TRAFFIC_BYTES_PER_LAUNCH.get((key, dom))
+    tinfo, twhy = traffic_of(traffic, key, nl // steps, dom)
+    traffic = round(tinfo["fetch_bytes"] + tinfo["write_bytes"]) if tinfo else None
+    tsrc = ({"how": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes of this run, scaled by a "
+                    f"{TRAFFIC_COPY_MIB} MiB device copy", "kernel": tinfo["kernel"], "grid": tinfo["grid"],
+             "fetch_bytes": round(tinfo["fetch_bytes"]), "write_bytes": round(tinfo["write_bytes"]),
+             "counter_factors": tinfo["factors"]} if tinfo else {"how": "not measured", "why": twhy})
     roofline = {
         "kernel": dom, "bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": r_unit,
-        "frac": round(achieved / peak, 4), "traffic": traffic,
+        "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_source": tsrc,
         "launches_per_step": nl // steps, "avg_launch_us": round(avg_s * 1e6, 2),
         "flops_per_launch": fl, "algorithmic_bytes_per_launch": by,
         "traffic_over_algorithmic": round(traffic / by, 3) if traffic else None,
@@ -423,20 +532,31 @@ def main():
                     help="also time identify: the batch's embeddings scored against this many enrolled rows, top 10")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the bench, run 3 device-to-device copies of this many MiB (PMC traffic calibration)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes that measure the dominant kernels' HBM traffic")
+    ap.add_argument("--traffic-child", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.traffic_child:
+        traffic_child(args.traffic_child.split(","))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
               "clips are independent, so N GPUs would each run this same per-GPU batch.", file=sys.stderr)
         sys.exit(2)
+    key = args.model or "resnet34"
+    keys = [key] + ([] if args.model else list(CONFIG_SET))
+    # the counter passes run first, before this process initialises the GPU
+    traffic = None if args.no_traffic else traffic_passes(keys)
+    if traffic and "error" in traffic:
+        print(f"bench.py: traffic not measured: {traffic['error']}", file=sys.stderr)
     L = lib.lib()
     if L.vdk_device_count() < 1:
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(1)
-    key = args.model or "resnet34"
     cpu_s = 0.0 if args.no_cpu_baseline else args.cpu_seconds
     head = measure(L, key, args.steps, args.warmup, cpu_s, registry=args.registry,
-                   copy_mib=args.copy_calibration_mib, b1_reps=50 if key == "resnet34" else 0)
+                   copy_mib=args.copy_calibration_mib, b1_reps=50 if key == "resnet34" else 0, traffic=traffic)
     model = MODELS[key]
     out = {
         "metric": model["metric"], "value": head["value"], "unit": head["unit"], "n_gpus": 1,
@@ -457,12 +577,13 @@ def main():
                  "value": head["value"], "unit": head["unit"], "ms_per_step": head["ms_per_step"],
                  "dominant_kernel": head["roofline"]["kernel"], "roofline_frac": head["roofline"]["frac"]}]
         for ck in CONFIG_SET:
-            r = measure(L, ck, max(10, args.steps // 2), args.warmup, cpu_s / 2)
+            r = measure(L, ck, max(10, args.steps // 2), args.warmup, cpu_s / 2, traffic=traffic)
             m = MODELS[ck]
             e = {"config": m["config"]["workload"], "model": ck, "batch": m["batch"], "dtype": m["dtype"],
                  "value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
                  "dominant_kernel": r["roofline"]["kernel"], "roofline": {
-                     k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "avg_launch_us")},
+                     k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "avg_launch_us",
+                                                   "traffic", "traffic_over_algorithmic", "traffic_source")},
                  "all_conv_frac": r["roofline"]["all_conv"]["frac"], "host_buffers": r["host_buffers"]["value"],
                  "reference_published_ms_per_clip": {"cpu_8t": REFERENCE_PUBLISHED["per_clip_8t_ms"][ck],
                                                      "gb10_b1": REFERENCE_PUBLISHED["gb10_b1_ms"][ck]}}

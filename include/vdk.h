@@ -302,6 +302,21 @@ int vdk_linear_ex_noalloc(const float* d_x, int batch, int in_dim, const float* 
  * d_row_mean (may be NULL): [B][n_mels] CMN means subtracted as it loads. */
 int vdk_feats_tmajor(const float* d_feats, const float* d_row_mean, int batch, int n_mels, int T, int pad,
                      int c_pad, void* d_out, void* stream);
+/* All scale - 1 dependent group convs of one SE-Res2Net block's Res2Net
+ * (src/encoder.cpp:174-200) in one launch.  buf [B][T][stride] f16 holds
+ * the block's groups in slots of G channels: x_m (tdnn1's output chunk m) in
+ * slot m + 1; group j (1 .. scale-1) = conv_j(in_j) with in_1 = x_1 and
+ * in_j = f16(v_{j-1} + x_j), conv_j the k = 3 dilated conv with reflect
+ * padding + bias -> ReLU -> BN (v = relu(conv + bias) * scale + shift, f32),
+ * stored as f16 to slot 0 (j = 1) or slot j.  Weights [G][3][G] f16 (16-byte
+ * aligned); scale / shift may be NULL (1 / 0).  The same bits as the groups
+ * run one conv at a time (vdk_conv2d_ex with reflect_pad and the second
+ * output).  G = 128, scale <= 8, T > dil, (scale - 1) * dil <= 64. */
+typedef struct {
+    const void* w[7]; const float* bias[7]; const float* scale[7]; const float* shift[7];
+} vdk_res2_weights;
+int vdk_res2_block(void* d_buf, int stride, int batch, int T, int G, int scale, int dil,
+                   const vdk_res2_weights* w, void* stream);
 /* out [B][T+2*pad][G] = reflect_pad(a (+ b)) over time: the Res2Net group
  * input x_i + y_{i-1} of src/encoder.cpp:174-200 padded for its dilated conv.
  * d_b may be NULL. */
@@ -338,6 +353,13 @@ int vdk_asp_attn_pool(const void* d_a1, int a1_stride, const void* d_w, const fl
 /* ---- L2 normalisation ----
  * Replaces the host L2 of src/encoder_resnet.cpp:177-183 (double accumulation,
  * skipped when the norm is 0).  In place on x [B][dim]. */
+/* The embedding FC with the L2 normalisation in its reduce step: d_pre
+ * [B][out] the FC output as vdk_linear_ex (no activation) stores it, d_y the
+ * rows of d_pre normalised as vdk_l2norm_to does (src/encoder_resnet.cpp:
+ * 159-183); d_pre and d_y must not overlap. */
+int vdk_linear_l2_ex(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
+                     const float* d_mean_vec, int out_dim, float* d_pre, float* d_y, void* d_work,
+                     size_t work_bytes, void* stream);
 int vdk_l2norm(float* d_x, int batch, int dim, void* stream);
 /* Same, out of place: y [B][dim] = x / ||x|| (y may equal x; a zero row is copied). */
 int vdk_l2norm_to(const float* d_x, int batch, int dim, float* d_y, void* stream);

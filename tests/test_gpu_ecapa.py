@@ -195,6 +195,66 @@ def test_res2net_group_conv_reflect_and_next_input(batch, T, dil):
     assert not np.array_equal(z[:, :dil], got[:, :dil])
 
 
+@pytest.mark.parametrize("batch,T,dil,scale", [(B, T4S, 2, 8), (B, T4S, 3, 8), (B, T4S, 4, 8), (3, 37, 4, 8),
+                                              (2, 1001, 2, 8), (5, 61, 3, 4), (1, 5, 4, 8)])
+def test_res2net_block_one_launch_matches_group_chain(batch, T, dil, scale):
+    """vdk_res2_block (all scale - 1 groups of a Res2Net in one launch per time
+    tile, halo recomputed) writes the same bits into the same slots as the
+    groups run one conv at a time (reflect padding, y_j to slot 0 / j, the
+    next input f16(v + x_{j+1}) as the conv's second output), and leaves the
+    x slots alone; also a check of group 1 against the oracle conv."""
+    rng = np.random.default_rng(40 + dil + T + scale)
+    G = 128
+    S = (scale + 1) * G
+    announce(f"ecapa res2 block B={batch} T={T} dil={dil} scale={scale}")
+    t1 = rng.standard_normal((batch, T, S), dtype=np.float32).astype(np.float16)
+    L = lib.lib()
+    keep, rw = [], lib.Res2Weights()
+    ws, bs, bns = [], [], []
+    for j in range(scale - 1):
+        w = _f16w(rng, G, G, 3)
+        b = (0.01 * rng.standard_normal(G)).astype(np.float32)
+        bn = _bn_params(rng, G)
+        sc, sh = _scale_shift(bn)
+        bufs = [lib.DeviceBuffer.from_array(np.ascontiguousarray(w.transpose(0, 2, 1))), lib.DeviceBuffer.from_array(b),
+                lib.DeviceBuffer.from_array(sc), lib.DeviceBuffer.from_array(sh)]
+        keep += bufs
+        rw.w[j], rw.bias[j], rw.scale[j], rw.shift[j] = (x.ptr for x in bufs)
+        ws.append(w), bs.append(b), bns.append(bn)
+    # the chain: group j reads x_1 (slot 2) or the previous group's second
+    # output, writes slot 0 (j = 1) or slot j, and f16(v + x_{j+1}) to a side buffer
+    dchain = lib.DeviceBuffer.from_array(t1)
+    side = [lib.DeviceBuffer(batch * T * G * 2) for _ in range(2)]
+    for j in range(1, scale):
+        last = j + 1 == scale
+        d = lib.ConvDesc()
+        if j == 1:
+            d.x, d.x_stride = dchain.ptr + 2 * G * 2, S
+        else:
+            d.x, d.x_stride = side[j & 1].ptr, G
+        d.batch, d.H, d.W, d.IC = batch, 1, T, G
+        d.w, d.OC, d.KH, d.KW = rw.w[j - 1], G, 1, 3
+        d.stride_h, d.stride_w, d.pad_h, d.pad_w, d.dil_h, d.dil_w = 1, 1, 0, dil, 1, dil
+        d.reflect_pad = 1
+        d.bias, d.post_scale, d.post_shift = rw.bias[j - 1], rw.scale[j - 1], rw.shift[j - 1]
+        d.act = lib.ACT_RELU
+        d.y, d.y_stride = dchain.ptr + (0 if j == 1 else j) * G * 2, S
+        if not last:
+            d.y2, d.y2_stride, d.res2, d.res2_stride = side[(j + 1) & 1].ptr, G, dchain.ptr + (j + 2) * G * 2, S
+        d.tile = -1
+        lib.check(L.vdk_conv2d_ex(d, None))
+    dblk = lib.DeviceBuffer.from_array(t1)
+    lib.check(L.vdk_res2_block(dblk.ptr, S, batch, T, G, scale, dil, rw, None))
+    _sync()
+    want = dchain.to_array(np.float16, (batch, T, S))
+    got = dblk.to_array(np.float16, (batch, T, S))
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    assert np.array_equal(got[:, :, scale * G:].view(np.uint16), t1[:, :, scale * G:].view(np.uint16))
+    c = batch - 1
+    ref = _oracle_tdnn(t1[c, :, 2 * G:3 * G].astype(np.float32).T, ws[0], bs[0], dil, bns[0])
+    _assert_close(got[c, :, :G].astype(np.float32).T, ref, f"res2 block group 1 clip {c}")
+
+
 def test_1x1_layers_over_channel_slices():
     rng = np.random.default_rng(31)
     T, C, M = T4S, 1024, 1536

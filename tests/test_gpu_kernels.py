@@ -598,6 +598,42 @@ def test_tstp_linear_l2_match_oracle():
     lib.check(L.vdk_l2norm(z.ptr, 2, 8, None))
     lib.check(L.vdk_synchronize())
     assert np.array_equal(z.to_array(np.float32, (2, 8)), np.zeros((2, 8), np.float32))
+    # the FC with the L2 normalisation in its reduce: the same pre-norm bits,
+    # normalised rows within an f32 rounding of vdk_l2norm_to's
+    dpre, dl2 = lib.DeviceBuffer(B * E * 4), lib.DeviceBuffer(B * E * 4)
+    lib.check(L.vdk_linear_l2_ex(dp.ptr, B, P, dw.ptr, db.ptr, dm.ptr, E, dpre.ptr, dl2.ptr, dwk.ptr, wsz, None))
+    lib.check(L.vdk_synchronize())
+    assert np.array_equal(dpre.to_array(np.float32, (B, E)).view(np.uint32), pre.view(np.uint32))
+    assert np.abs(dl2.to_array(np.float32, (B, E)) - emb).max() <= 1.2e-7
+    assert L.vdk_linear_l2_ex(dp.ptr, B, P, dw.ptr, db.ptr, dm.ptr, E, dpre.ptr, dpre.ptr, dwk.ptr, wsz, None) != 0
+
+
+@pytest.mark.parametrize("B,H,W,C,lo", [(3, 10, 38, 256, 0), (2, 5, 250, 512, 512), (2, 4, 37, 200, 0),
+                                         (1, 3, 2, 64, 0)])
+def test_tstp_vector_and_scalar_paths(B, H, W, C, lo):
+    """TSTP on 16-byte channel vectors (16-byte aligned rows, C % 8 == 0)
+    and, for the same values through a view 4 bytes off alignment, on the
+    scalar path; split-f16 inputs (value = hi + lo); against the oracle's
+    two-pass statistics."""
+    L = lib.lib()
+    rng = np.random.default_rng(B * 100 + C)
+    xs = C * (2 if lo else 1)
+    x = (rng.standard_normal((B, H, W, xs)) * 20).astype(np.float16)
+    announce(f"tstp B={B} H={H} W={W} C={C} lo={lo}")
+    for off in (0, 2):   # off = 2 elements: a 4-byte aligned view, the scalar kernel
+        buf = np.zeros(x.size + 8, dtype=np.float16)
+        buf[off:off + x.size] = x.reshape(-1)
+        dx = lib.DeviceBuffer.from_array(buf)
+        dp = lib.DeviceBuffer(B * 2 * C * H * 4)
+        lib.check(L.vdk_tstp_ex(dx.ptr + 2 * off, xs, lo, B, H, W, C, 1e-8, dp.ptr, None))
+        lib.check(L.vdk_synchronize())
+        got = dp.to_array(np.float32, (B, 2 * C * H))
+        v = x.astype(np.float32)
+        if lo:
+            v = v[..., :C] + v[..., C:]
+        for c in range(B):
+            rp = O.tstp(v[c].transpose(2, 0, 1), 1e-8)
+            assert np.allclose(got[c], rp, rtol=2e-5, atol=2e-5), (off, c)
 
 
 @pytest.mark.parametrize("case", [(1, 3, 5, 0), (70, 130, 33, 1), (130, 5120, 200, 2), (64, 1024, 1024, 5),

@@ -93,6 +93,22 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// s_waitcnt until at most n (a run-time count) vector memory operations of
+// this wave are in flight; counts without a case wait for all of them.
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+    // s_waitcnt with vmcnt = n (6-bit field split [3:0] / [15:14]), expcnt and
+    // lgkmcnt left at their "no wait" maxima.
+    switch (n) {
+#define VDK_VM(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
+        VDK_VM(0) VDK_VM(1) VDK_VM(2) VDK_VM(3) VDK_VM(4) VDK_VM(5) VDK_VM(6) VDK_VM(7) VDK_VM(8)
+        VDK_VM(9) VDK_VM(10) VDK_VM(11) VDK_VM(12) VDK_VM(13) VDK_VM(14) VDK_VM(15) VDK_VM(16)
+        VDK_VM(18) VDK_VM(20) VDK_VM(24) VDK_VM(27) VDK_VM(28) VDK_VM(30) VDK_VM(32) VDK_VM(36) VDK_VM(40)
+        VDK_VM(42) VDK_VM(45) VDK_VM(48) VDK_VM(54) VDK_VM(56) VDK_VM(60)
+#undef VDK_VM
+        default: __builtin_amdgcn_s_waitcnt(0); break;
+    }
+}
+
 // Buffer resource words of [base, base + bytes) for dma16 (raw buffer,
 // offsets at or past `bytes` read as zero).
 __device__ __forceinline__ int4v dma_rsrc(const void* base, uint32_t bytes) {

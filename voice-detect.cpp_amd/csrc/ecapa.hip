@@ -410,6 +410,179 @@ __global__ __launch_bounds__(256, 2) void asp_attn_pool_kernel(const half_t* __r
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// ---------------------------------------------------------------------------
+// res2_block_kernel: the scale - 1 dependent group convs of one ECAPA Res2Net
+// block (src/encoder.cpp:174-200) in one launch.  A workgroup owns one clip's
+// time tile [t0, t1) and walks the groups j = 1 .. L (L = scale - 1): group
+// j is needed on R_j = [t0 - (L - j) D, t1 + (L - j) D) (clipped to the
+// clip; D the dilation), so the tile's halo shrinks by D per group and no
+// other workgroup's result is ever read.  Its input in_j (x_1, then
+// f16(v_{j-1} + x_j) with v the previous group's f32 output) lives in one of
+// two LDS buffers and the next one is written by the group's epilogue; the
+// weights stream through LDS one tap (128 x 128 f16) at a time in a
+// two-stage DMA ring; y_j = f16(v_j) leaves for its slot of the Res2Net
+// buffer for the tile's own frames.  Per group the conv runs exactly like the
+// one-group DMA conv (taps outer, 16-channel k-steps inner, accumulators from
+// zero, bias -> ReLU -> BN scale, shift, the same reflect rule), so the
+// results are the same bits as the chain of single-group launches.
+// Layout of the buffer (stride S per frame): x_m in slot m + 1 (m = 0 ..
+// scale - 1, slots of G = 128 channels), y_1 written to slot 0, y_j (j >= 2)
+// to slot j.
+// ---------------------------------------------------------------------------
+constexpr int kR2G = 128;          // channels per group
+constexpr int kR2Rows = 160;       // frames an input buffer holds (t1 - t0 + 2 L D <= 160)
+constexpr int kR2MaxL = 7;
+
+struct Res2Args {
+    half_t* t1;                    // [B][T][S]
+    int S, T, D, L, Tt, nt;
+    const half_t* w[kR2MaxL];      // [G][3][G] per group
+    const float* bias[kR2MaxL];
+    const float* scale[kR2MaxL];
+    const float* shift[kR2MaxL];
+};
+
+__device__ __forceinline__ int r2_refl(int s, int T) {
+    s = s < 0 ? -s : (s >= T ? 2 * (T - 1) - s : s);
+    return s < 0 ? 0 : (s >= T ? T - 1 : s);
+}
+
+// byte offset of 8-channel chunk c of LDS row r (rows of 256 bytes, chunk c
+// at slot c ^ (r & 15): the 16 rows an MFMA operand read touches hit
+// distinct 16-byte bank groups)
+__device__ __forceinline__ int r2_off(int r, int c) { return r * 256 + ((c ^ (r & 15)) << 4); }
+
+__global__ __launch_bounds__(512) void res2_block_kernel(Res2Args a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t s_in[2][kR2Rows * 256];
+    __shared__ __attribute__((aligned(1024))) uint8_t s_w[2][kR2G * 256];
+    __shared__ float s_ep[kR2MaxL][3][kR2G];   // bias, scale, shift
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, lhalf = lane >> 5;
+    const int b = blockIdx.x / a.nt, tile = blockIdx.x - b * a.nt;
+    const int T = a.T, D = a.D, L = a.L, S = a.S;
+    const int t0 = tile * a.Tt, t1 = t0 + a.Tt < T ? t0 + a.Tt : T;
+    auto lo = [&](int j) { const int v = t0 - (L - j) * D; return v > 0 ? v : 0; };
+    auto hi = [&](int j) { const int v = t1 + (L - j) * D; return v < T ? v : T; };
+    const int base = lo(0);
+    half_t* const clip = a.t1 + (size_t)b * T * S;
+
+    for (int i = tid; i < L * 3 * kR2G; i += 512) {
+        const int j = i / (3 * kR2G), r = i - j * 3 * kR2G, q = r / kR2G, c = r - q * kR2G;
+        const float* src = q == 0 ? a.bias[j] : (q == 1 ? a.scale[j] : a.shift[j]);
+        s_ep[j][q][c] = src ? src[c] : (q == 1 ? 1.0f : 0.0f);
+    }
+    // weights of tap k of group j: 2048 16-byte slots, 4 DMA instructions per wave
+    auto issue_w = [&](int c) {
+        const int j = c / 3, k = c - j * 3;
+        const int4v rs = dma_rsrc(a.w[j], (uint32_t)(kR2G * 3 * kR2G * 2));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ins = wave * 4 + i, s = ins * 64 + lane, r = s >> 4, pc = s & 15, lc = pc ^ (r & 15);
+            dma16(s_w[c & 1] + ins * 1024, rs, (uint32_t)(((r * 3 + k) * kR2G + lc * 8) * 2));
+        }
+    };
+    issue_w(0);
+    // in_1 = x_1 (slot 2) on R_0
+    {
+        const int n = (hi(0) - base) * 16;
+        for (int i = tid; i < n; i += 512) {
+            const int r = i >> 4, c = i & 15;
+            *reinterpret_cast<half8*>(s_in[0] + r2_off(r, c)) =
+                *reinterpret_cast<const half8*>(clip + (size_t)(base + r) * S + 2 * kR2G + c * 8);
+        }
+    }
+
+    const int ob = wave & 3, fb0 = wave >> 2;   // 32-channel block, first frame block (then every second)
+    float16v acc[3];
+    int fcol[3];        // per frame block: this lane's frame (masked columns: a valid one)
+    half4 xn[3][4];     // x_{j+1} of the epilogue's (frame, 4 channels)
+    int nfb = 0, lo_j = 0, hi_j = 0, nx = 0;
+    for (int c = 0; c < 3 * L; ++c) {
+        const int j = c / 3 + 1, k = c - (j - 1) * 3;
+        const uint8_t* const in = s_in[(j - 1) & 1];
+        if (k == 0) {
+            lo_j = lo(j);
+            hi_j = hi(j);
+            nfb = (hi_j - lo_j + 31) >> 5;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int fb = fb0 + 2 * i;
+                const int f = lo_j + fb * 32 + lrow;
+                fcol[i] = f < hi_j ? f : hi_j - 1;   // masked columns: any valid row, result dropped
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+            }
+        }
+        // chunk c (issued one step ago, or before the loop) has landed; after
+        // the barrier every wave is past chunk c - 1, so its stage is free,
+        // and the previous group's epilogue writes of `in` are complete
+        if (k == 0 || nx == 0) wait_vmcnt<0>();
+        else wait_vmcnt_le(nx);
+        lds_barrier();
+        if (c + 1 < 3 * L) issue_w(c + 1);
+        nx = 0;
+        if (k == 0 && j < L) {   // x_{j+1} for this group's epilogue, in flight behind the weights
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int fb = fb0 + 2 * i;
+                if (fb >= nfb) continue;
+                const int f = lo_j + fb * 32 + lrow;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int oc = ob * 32 + g * 8 + lhalf * 4;
+                    xn[i][g] = f < hi_j ? *reinterpret_cast<const half4*>(clip + (size_t)f * S + (j + 2) * kR2G + oc)
+                                        : half4{0, 0, 0, 0};
+                    ++nx;
+                }
+            }
+        }
+        const uint8_t* const wt = s_w[c & 1];
+        int rk[3];   // per frame block: the LDS input row of tap k (reflected into the clip)
+#pragma unroll
+        for (int i = 0; i < 3; ++i) rk[i] = r2_refl(fcol[i] + (k - 1) * D, T) - base;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const int ch = ks * 2 + lhalf;
+            const half8 af = *reinterpret_cast<const half8*>(wt + r2_off(ob * 32 + lrow, ch));
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                if (fb0 + 2 * i >= nfb) continue;
+                const half8 bf = *reinterpret_cast<const half8*>(in + r2_off(rk[i], ch));
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[i], 0, 0, 0);
+            }
+        }
+        if (k < 2) continue;
+        // epilogue of group j: bias -> ReLU -> BN; y_j out for the tile's frames,
+        // in_{j+1} = f16(v + x_{j+1}) into the other input buffer on R_j
+        uint8_t* const out = s_in[j & 1];
+        half_t* const yslot = clip + (j == 1 ? 0 : j) * kR2G;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int fb = fb0 + 2 * i;
+            if (fb >= nfb) continue;
+            const int f = lo_j + fb * 32 + lrow;
+            if (f >= hi_j) continue;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int oc = ob * 32 + g * 8 + lhalf * 4;
+                half4 yv, iv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v = acc[i][g * 4 + e] + s_ep[j - 1][0][oc + e];
+                    v = fmaxf(v, 0.0f);
+                    v = v * s_ep[j - 1][1][oc + e];
+                    v = v + s_ep[j - 1][2][oc + e];
+                    yv[e] = (half_t)v;
+                    iv[e] = (half_t)(v + (float)xn[i][g][e]);
+                }
+                if (f >= t0 && f < t1) *reinterpret_cast<half4*>(yslot + (size_t)f * S + oc) = yv;
+                if (j < L) *reinterpret_cast<half4*>(out + r2_off(f - base, oc >> 3) + (oc & 7) * 2) = iv;
+            }
+        }
+    }
+}
+
 }  // namespace
 }  // namespace vdk
 
@@ -468,6 +641,34 @@ extern "C" int vdk_se_gate_residual(const void* d_x, int x_stride, const float* 
                            static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, d_gate,
                            static_cast<const half_t*>(d_res), res_stride, batch, T, C, static_cast<half_t*>(d_y),
                            y_stride);
+        VDK_HIP(hipGetLastError());
+    });
+}
+
+extern "C" int vdk_res2_block(void* d_buf, int stride, int batch, int T, int G, int scale, int dil,
+                              const vdk_res2_weights* wts, void* stream) {
+    return guarded([&] {
+        require(d_buf && wts, "res2_block: NULL pointer");
+        require(G == kR2G, "res2_block: groups of 128 channels only");
+        require(scale >= 2 && scale - 1 <= kR2MaxL, "res2_block: scale must be 2 .. 8");
+        require(batch > 0 && T > dil && dil >= 1, "res2_block: T must exceed the dilation");
+        require(stride >= (scale + 1) * G && stride % 8 == 0 && al16(d_buf), "res2_block: bad buffer stride / alignment");
+        require((size_t)batch * T * stride < (1ull << 31), "res2_block: buffer too large for one launch");
+        Res2Args a{};
+        a.t1 = static_cast<half_t*>(d_buf);
+        a.S = stride; a.T = T; a.D = dil; a.L = scale - 1;
+        const int tmax = kR2Rows - 2 * a.L * dil;
+        require(tmax >= 32, "res2_block: dilation too large for the LDS tile");
+        a.nt = cdiv(T, tmax);
+        a.Tt = cdiv(T, a.nt);
+        for (int j = 0; j < a.L; ++j) {
+            require(wts->w[j] && wts->bias[j] && al16(wts->w[j]), "res2_block: missing group weights");
+            a.w[j] = static_cast<const half_t*>(wts->w[j]);
+            a.bias[j] = wts->bias[j];
+            a.scale[j] = wts->scale[j];
+            a.shift[j] = wts->shift[j];
+        }
+        hipLaunchKernelGGL(res2_block_kernel, dim3(batch * a.nt), dim3(512), 0, static_cast<hipStream_t>(stream), a);
         VDK_HIP(hipGetLastError());
     });
 }

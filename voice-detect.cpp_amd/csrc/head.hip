@@ -1,9 +1,10 @@
 // head.hip - statistics pooling, embedding FC and L2 normalisation on gfx950.
 //
 // These are bandwidth-bound reductions: TSTP reads the last feature map twice
-// (coalesced over channels; 64 channels x 4 time partitions per workgroup); the FC is
-// a split-K tiled dot product with a fixed-order reduction; L2 is one
-// wavefront per clip.  Sums are accumulated in f64 like the reference's ggml
+// (16-byte loads of 8 channels, 256 channels x 8 time partitions per
+// workgroup); the FC is a split-K tiled dot product with a fixed-order
+// reduction, which for the embedding also does the L2 normalisation (one
+// workgroup per clip).  Sums are accumulated in f64 like the reference's ggml
 // reductions and host L2 (src/encoder_resnet.cpp:140-183).
 #include <cmath>
 #include <mutex>
@@ -65,6 +66,88 @@ __global__ __launch_bounds__(256) void tstp_kernel(const half_t* __restrict__ x,
         float* out = pooled + (size_t)b * 2 * CH;
         out[(size_t)c * H + h] = mean;
         out[CH + (size_t)c * H + h] = sqrtf(var + eps);
+    }
+}
+
+// TSTP over 8-channel vectors: a workgroup covers 256 channels (32 groups of
+// 8, one 16-byte load each) of one (clip, freq row) in NP time partitions,
+// partition p taking time steps p, p + NP, ...; f64 partial sums per
+// channel, combined in a fixed order through LDS, then the squared deviations
+// from the f32 mean the same way.  The row's values (W x 256 channels) stay
+// in the L1 between the two passes.  NP = 32 for long rows (CAM++'s and
+// ERes2Net's hundreds of frames), 8 otherwise.
+template <int NP>
+__global__ __launch_bounds__(NP * 32) void tstp8_kernel(const half_t* __restrict__ x, int xs, int x_lo, int H,
+                                                        int W, int C, float eps, float* __restrict__ pooled) {
+#pragma clang fp contract(off)
+    __shared__ double part[NP][257];
+    const int g = threadIdx.x & 31, tp = threadIdx.x >> 5;
+    const int c0 = blockIdx.x * 256 + g * 8, h = blockIdx.y, b = blockIdx.z;
+    const bool ok = c0 < C;
+    const size_t CH = (size_t)C * H;
+    const half_t* row = x + ((size_t)b * H + h) * W * xs + (ok ? c0 : 0);
+    auto load8 = [&](int t, float* v) {
+        const half8 hv = *reinterpret_cast<const half8*>(row + (size_t)t * xs);
+        if (x_lo) {
+            const half8 lv = *reinterpret_cast<const half8*>(row + (size_t)t * xs + x_lo);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (float)hv[e] + (float)lv[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (float)hv[e];
+        }
+    };
+    double s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = 0.0;
+    if (ok)
+#pragma unroll 4
+        for (int t = tp; t < W; t += NP) {
+            float v[8];
+            load8(t, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] += (double)v[e];
+        }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[tp][g * 8 + e] = s[e];
+    __syncthreads();
+    float mean[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        double m = 0.0;
+#pragma unroll
+        for (int q = 0; q < NP; ++q) m += part[q][g * 8 + e];
+        mean[e] = (float)(m / W);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = 0.0;
+    if (ok)
+#pragma unroll 4
+        for (int t = tp; t < W; t += NP) {
+            float v[8];
+            load8(t, v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = v[e] - mean[e];
+                s[e] += (double)(d * d);
+            }
+        }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[tp][g * 8 + e] = s[e];
+    __syncthreads();
+    if (tp == 0 && ok) {
+        float* out = pooled + (size_t)b * 2 * CH;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            double q2 = 0.0;
+#pragma unroll
+            for (int q = 0; q < NP; ++q) q2 += part[q][g * 8 + e];
+            float var = (float)(q2 / W);
+            if (W > 1) var = var * ((float)W / (float)(W - 1));
+            out[(size_t)(c0 + e) * H + h] = mean[e];
+            out[CH + (size_t)(c0 + e) * H + h] = sqrtf(var + eps);
+        }
     }
 }
 
@@ -175,6 +258,46 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restr
     y[i] = r;
 }
 
+// The reduce of the embedding FC with the L2 normalisation: one workgroup per
+// clip row, the pre-norm row to `pre`, then y = row / ||row|| (f64 norm; a
+// zero row copied unchanged) as l2norm_kernel computes it.
+__global__ __launch_bounds__(256) void linear_reduce_l2_kernel(const float* __restrict__ part, int nsplit, int B,
+                                                               int out_dim, const float* __restrict__ bias,
+                                                               const float* __restrict__ mv,
+                                                               float* __restrict__ pre, float* __restrict__ y) {
+    __shared__ double red[4];
+    const int b = blockIdx.x;
+    const size_t stride = (size_t)B * out_dim;
+    double sq = 0.0;
+    for (int o = threadIdx.x; o < out_dim; o += 256) {
+        const size_t i = (size_t)b * out_dim + o;
+        double s = 0.0;
+        int k = 0;
+        for (; k + 8 <= nsplit; k += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = part[(size_t)(k + j) * stride + i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s += (double)v[j];
+        }
+        for (; k < nsplit; ++k) s += (double)part[(size_t)k * stride + i];
+        float r = (float)s;
+        if (bias) r += bias[o];
+        if (mv) r -= mv[o];
+        pre[i] = r;
+        sq += (double)r * (double)r;
+    }
+    sq = wave_sum_d(sq);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    const double norm = sqrt((red[0] + red[1]) + (red[2] + red[3]));
+    for (int o = threadIdx.x; o < out_dim; o += 256) {
+        const size_t i = (size_t)b * out_dim + o;
+        const float v = pre[i];   // this thread's own write above
+        y[i] = norm > 0.0 ? (float)((double)v / norm) : v;
+    }
+}
+
 int linear_splits(int in_dim) {
     const int want = (in_dim + kLinSlice - 1) / kLinSlice;   // ~128 inputs per slice
     return want < 1 ? 1 : (want > 64 ? 64 : want);
@@ -204,8 +327,19 @@ extern "C" int vdk_tstp_ex(const void* d_x, int x_stride, int x_lo, int batch, i
         require(batch > 0 && H > 0 && W > 0 && C > 0, "tstp: empty input");
         const int xs = x_stride ? x_stride : C;
         require(xs >= C && (x_lo == 0 || (x_lo >= C && x_lo + C <= xs)), "tstp: bad pixel stride / lo offset");
-        hipLaunchKernelGGL(tstp_kernel, dim3(cdiv(C, 64), H, batch), dim3(256), 0, static_cast<hipStream_t>(stream),
-                           static_cast<const half_t*>(d_x), xs, x_lo, H, W, C, eps, d_pooled);
+        const bool vec = C % 8 == 0 && xs % 8 == 0 && x_lo % 8 == 0 && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0;
+        if (vec && W >= 128)
+            hipLaunchKernelGGL(tstp8_kernel<32>, dim3(cdiv(C, 256), H, batch), dim3(1024), 0,
+                               static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), xs, x_lo, H, W, C,
+                               eps, d_pooled);
+        else if (vec)
+            hipLaunchKernelGGL(tstp8_kernel<8>, dim3(cdiv(C, 256), H, batch), dim3(256), 0,
+                               static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), xs, x_lo, H, W, C,
+                               eps, d_pooled);
+        else
+            hipLaunchKernelGGL(tstp_kernel, dim3(cdiv(C, 64), H, batch), dim3(256), 0,
+                               static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), xs, x_lo, H, W, C,
+                               eps, d_pooled);
         VDK_HIP(hipGetLastError());
     });
 }
@@ -234,7 +368,8 @@ void linear_check(const float* d_x, int batch, int in_dim, const float* d_w, int
 // floats, every one of which the partial kernel writes before the reduce
 // reads it (nothing needs clearing between calls).
 void linear_launch(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
-                   const float* d_mean_vec, int out_dim, int act, float* d_y, float* part, hipStream_t s) {
+                   const float* d_mean_vec, int out_dim, int act, float* d_y, float* part, hipStream_t s,
+                   float* d_l2 = nullptr) {
     const int ns = linear_splits(in_dim);
     const int slice = ((in_dim + ns - 1) / ns + kLinK - 1) / kLinK * kLinK;
     const int nsplit = (in_dim + slice - 1) / slice;
@@ -247,8 +382,12 @@ void linear_launch(const float* d_x, int batch, int in_dim, const float* d_w, co
         hipLaunchKernelGGL(linear_partial_kernel<1>, dim3(cdiv(out_dim, 16), cdiv(batch, 16), nsplit), dim3(256),
                            0, s, d_x, batch, in_dim, d_w, out_dim, slice, vec4, part);
     VDK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(linear_reduce_kernel, dim3(cdiv((long)batch * out_dim, 256)), dim3(256), 0, s, part,
-                       nsplit, batch, out_dim, d_bias, d_mean_vec, act, d_y);
+    if (d_l2)
+        hipLaunchKernelGGL(linear_reduce_l2_kernel, dim3(batch), dim3(256), 0, s, part, nsplit, batch, out_dim,
+                           d_bias, d_mean_vec, d_y, d_l2);
+    else
+        hipLaunchKernelGGL(linear_reduce_kernel, dim3(cdiv((long)batch * out_dim, 256)), dim3(256), 0, s, part,
+                           nsplit, batch, out_dim, d_bias, d_mean_vec, act, d_y);
     VDK_HIP(hipGetLastError());
 }
 
@@ -314,6 +453,22 @@ extern "C" int vdk_linear(const float* d_x, int batch, int in_dim, const float* 
                           const float* d_mean_vec, int out_dim, float* d_y, void* d_work, size_t work_bytes,
                           void* stream) {
     return vdk_linear_ex(d_x, batch, in_dim, d_w, d_bias, d_mean_vec, out_dim, 0, d_y, d_work, work_bytes, stream);
+}
+
+extern "C" int vdk_linear_l2_ex(const float* d_x, int batch, int in_dim, const float* d_w, const float* d_bias,
+                                const float* d_mean_vec, int out_dim, float* d_pre, float* d_y, void* d_work,
+                                size_t work_bytes, void* stream) {
+    return guarded([&] {
+        linear_check(d_x, batch, in_dim, d_w, out_dim, VDK_ACT_NONE, d_pre);
+        require(d_y != nullptr && d_work != nullptr, "linear_l2: NULL device pointer");
+        require(work_bytes >= vdk_linear_workspace_size(batch, in_dim, out_dim),
+                "linear_l2: workspace smaller than vdk_linear_workspace_size()");
+        const uintptr_t pa = reinterpret_cast<uintptr_t>(d_pre), ya = reinterpret_cast<uintptr_t>(d_y);
+        const size_t bytes = sizeof(float) * (size_t)batch * out_dim;
+        require(pa + bytes <= ya || ya + bytes <= pa, "linear_l2: pre and y overlap");
+        linear_launch(d_x, batch, in_dim, d_w, d_bias, d_mean_vec, out_dim, VDK_ACT_NONE, d_pre,
+                      static_cast<float*>(d_work), static_cast<hipStream_t>(stream), d_y);
+    });
 }
 
 extern "C" int vdk_l2norm(float* d_x, int batch, int dim, void* stream) {

@@ -376,18 +376,30 @@ void Model::forward(const float* d_pcm, int batch, int n_samples, float* d_out) 
     check(vdk_fbank_ex(&cfg_.fbank, fb_tables_, d_pcm, batch, n_samples, ws_.feats, ws_.fb_mean, ws_.fb_work,
                        ws_.fb_work_bytes, stream_));
     prof_end();
+    // with L2 normalisation the encoder's embedding FC writes the normalised
+    // rows straight into the output (the pre-norm rows stay in ws_.pre)
+    l2_dst_ = cfg_.l2_normalize ? d_out : nullptr;
     if (cfg_.arch == "ecapa_tdnn") encode_ecapa(batch, T);
     else if (cfg_.arch == "campplus") encode_campplus(batch, T);
     else if (cfg_.arch == "eres2net") encode_eres2net(batch, T);
     else encode_resnet(batch, T);
+    l2_dst_ = nullptr;
     const int E = cfg_.embedding_dim;
-    if (cfg_.l2_normalize) {   // normalised straight into the output (the pre-norm rows stay in ws_.pre)
-        prof_begin("l2norm", 0.0, 8.0 * batch * E);
-        check(vdk_l2norm_to(ws_.pre, batch, E, d_out, stream_));
-        prof_end();
-    } else {
+    if (!cfg_.l2_normalize)
         VDK_HIP(hipMemcpyAsync(d_out, ws_.pre, sizeof(float) * (size_t)batch * E, hipMemcpyDeviceToDevice, stream_));
-    }
+}
+
+void Model::embed_fc(const char* name, const float* x, int batch, int in_dim, const float* w, const float* b,
+                     const float* mv, int out_dim) {
+    prof_begin(name, 2.0 * batch * (double)in_dim * out_dim,
+               4.0 * ((double)batch * in_dim + (double)in_dim * out_dim + 2.0 * batch * out_dim));
+    if (l2_dst_)
+        check(vdk_linear_l2_ex(x, batch, in_dim, w, b, mv, out_dim, ws_.pre, l2_dst_, ws_.fc_work, ws_.fc_work_bytes,
+                               stream_));
+    else
+        check(vdk_linear_ex(x, batch, in_dim, w, b, mv, out_dim, VDK_ACT_NONE, ws_.pre, ws_.fc_work,
+                            ws_.fc_work_bytes, stream_));
+    prof_end();
 }
 
 void Model::encode_resnet(int batch, int T) {
@@ -436,12 +448,7 @@ void Model::encode_resnet(int batch, int T) {
     prof_begin("tstp", 0.0, 2.0 * batch * (double)H * W * C + 4.0 * batch * pooled_dim_);
     check(vdk_tstp(ws_.act[xi], batch, H, W, C, cfg_.resnet.var_eps, ws_.pooled, stream_));
     prof_end();
-    const int E = cfg_.embedding_dim;
-    prof_begin("linear", 2.0 * batch * (double)pooled_dim_ * E,
-               4.0 * ((double)batch * pooled_dim_ + (double)pooled_dim_ * E + (double)batch * E));
-    check(vdk_linear(ws_.pooled, batch, pooled_dim_, seg_w_, seg_b_, mean_vec_, E, ws_.pre, ws_.fc_work,
-                     ws_.fc_work_bytes, stream_));
-    prof_end();
+    embed_fc("linear", ws_.pooled, batch, pooled_dim_, seg_w_, seg_b_, mean_vec_, cfg_.embedding_dim);
 }
 
 void Model::embed_batch_device(const float* d_pcm, int batch, int n_samples, float* d_out) {

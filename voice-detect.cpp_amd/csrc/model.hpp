@@ -329,6 +329,10 @@ private:
                    const void* r2, int r2_stride, void* y2);
     void linear(const char* name, const float* x, int batch, int in_dim, const float* w, const float* b,
                 const float* mv, int out_dim, int relu, float* y);
+    // The embedding FC into ws_.pre; with L2 normalisation the same launch
+    // pair also writes the normalised rows to l2_dst_.
+    void embed_fc(const char* name, const float* x, int batch, int in_dim, const float* w, const float* b,
+                  const float* mv, int out_dim);
     void prof_begin(const char* name, double flops, double bytes);
     void prof_end();
     int frames(int n_samples) const;
@@ -339,6 +343,7 @@ private:
     ModelConfig cfg_;
     std::mutex mu_;
 
+    float* l2_dst_ = nullptr;   // forward's output while an encoder runs (L2 in the FC's reduce)
     bool ready_ = false;
     int device_ = 0;
     hipStream_t stream_ = nullptr;

@@ -330,8 +330,7 @@ void Model::encode_campplus(int batch, int T) {
     prof_begin("campp_stats", 0.0, 2.0 * rows * m.c_out + 8.0 * batch * m.c_out);
     check_rc(vdk_tstp(w.fin, batch, 1, Tp, m.c_out, 0.0f, w.pooled, stream_));
     prof_end();
-    linear("campp_dense", w.pooled, batch, pooled_dim_, m.dense_w, m.dense_b, nullptr, cfg_.embedding_dim, 0,
-           w.pre);
+    embed_fc("campp_dense", w.pooled, batch, pooled_dim_, m.dense_w, m.dense_b, nullptr, cfg_.embedding_dim);
 }
 
 }  // namespace vdk

@@ -322,11 +322,29 @@ void Model::encode_ecapa(int batch, int T) {
         const int S = C + G;
         uint8_t* t1 = static_cast<uint8_t*>(w.t1);
         tdnn("ecapa_tdnn1", b.tdnn1, xin, xs, batch, T, 1, b.tdnn1.b, 0, 1, 0, t1 + gB, S, 0);
-        for (int j = 1; j < e.scale; ++j) {
-            const bool last = j + 1 == e.scale;
-            const void* in = j == 1 ? static_cast<const void*>(t1 + 2 * gB) : w.s2b[j & 1];
-            res2_conv(b.res[j - 1], in, j == 1 ? S : G, batch, T, b.dil, t1 + (j == 1 ? 0 : j) * gB, S,
-                      last ? nullptr : t1 + (j + 2) * gB, S, last ? nullptr : w.s2b[(j + 1) & 1]);
+        if (G == 128 && e.scale <= 8 && (e.scale - 1) * b.dil <= 64) {
+            // all groups in one launch per time tile, the same bits as the chain below
+            vdk_res2_weights rw{};
+            for (int j = 0; j + 1 < e.scale; ++j) {
+                rw.w[j] = b.res[j].w;
+                rw.bias[j] = b.res[j].b;
+                rw.scale[j] = b.res[j].scale;
+                rw.shift[j] = b.res[j].shift;
+            }
+            if (profiling_) {
+                const double npix = (double)batch * T, n = e.scale - 1.0;
+                prof_begin("conv.ecapa_res2_block", n * 2.0 * 3 * G * G * npix,
+                           2.0 * npix * G * (2.0 * n) + n * 2.0 * 3 * G * G);
+            }
+            check_rc(vdk_res2_block(w.t1, S, batch, T, G, e.scale, b.dil, &rw, stream_));
+            prof_end();
+        } else {
+            for (int j = 1; j < e.scale; ++j) {
+                const bool last = j + 1 == e.scale;
+                const void* in = j == 1 ? static_cast<const void*>(t1 + 2 * gB) : w.s2b[j & 1];
+                res2_conv(b.res[j - 1], in, j == 1 ? S : G, batch, T, b.dil, t1 + (j == 1 ? 0 : j) * gB, S,
+                          last ? nullptr : t1 + (j + 2) * gB, S, last ? nullptr : w.s2b[(j + 1) & 1]);
+            }
         }
         tdnn("ecapa_tdnn2", b.tdnn2, w.t1, S, batch, T, 1, b.tdnn2.b, 0, 1, 0, w.t2, C, 0);
         // SE (src/encoder.cpp:207-219) and the residual (src/encoder.cpp:243)
@@ -362,7 +380,7 @@ void Model::encode_ecapa(int batch, int T) {
         prof_end();
     }
 
-    linear("ecapa_fc", w.pooled, batch, 2 * M, e.fc_w, e.fc_b, nullptr, cfg_.embedding_dim, 0, w.pre);
+    embed_fc("ecapa_fc", w.pooled, batch, 2 * M, e.fc_w, e.fc_b, nullptr, cfg_.embedding_dim);
 }
 
 }  // namespace vdk

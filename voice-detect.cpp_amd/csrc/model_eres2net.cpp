@@ -370,7 +370,7 @@ void Model::encode_eres2net(int batch, int T) {
     prof_begin("eres_tstp", 0.0, 4.0 * batch * (double)H * W * m.c_out + 4.0 * batch * pooled_dim_);
     check_rc(vdk_tstp_ex(fin.p, fin.stride, fin.lo, batch, H, W, m.c_out, m.eps, w.pooled, stream_));
     prof_end();
-    linear("eres_seg1", w.pooled, batch, pooled_dim_, m.seg_w, m.seg_b, nullptr, cfg_.embedding_dim, 0, w.pre);
+    embed_fc("eres_seg1", w.pooled, batch, pooled_dim_, m.seg_w, m.seg_b, nullptr, cfg_.embedding_dim);
 }
 
 }  // namespace vdk

@@ -28,6 +28,11 @@ class FbankCfg(C.Structure):
 ACT_NONE, ACT_RELU, ACT_SIGMOID, ACT_SILU, ACT_GELU, ACT_TANH = 0, 1, 2, 3, 4, 5
 
 
+class Res2Weights(C.Structure):
+    """vdk_res2_weights (include/vdk.h)."""
+    _fields_ = [("w", _vp * 7), ("bias", _vp * 7), ("scale", _vp * 7), ("shift", _vp * 7)]
+
+
 class ConvDesc(C.Structure):
     """vdk_conv_desc (include/vdk.h)."""
     _fields_ = [("x", _vp), ("batch", C.c_int), ("H", C.c_int), ("W", C.c_int), ("IC", C.c_int),
@@ -147,10 +152,14 @@ _SIGS = {
     "vdk_linear": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp, C.c_size_t, _vp]),
     "vdk_linear_ex": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _vp, C.c_size_t,
                                 _vp]),
+    "vdk_linear_l2_ex": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, _vp, _vp, _vp, C.c_size_t,
+                                   _vp]),
     "vdk_linear_ex_noalloc": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_l2norm": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
     "vdk_l2norm_to": (C.c_int, [_vp, C.c_int, C.c_int, _vp, _vp]),
     "vdk_feats_tmajor": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_res2_block": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                 C.POINTER(Res2Weights), _vp]),
     "vdk_reflect_pad_add": (C.c_int, [_vp, C.c_int, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_channel_mean": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "vdk_se_gate_residual": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int,
