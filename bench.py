@@ -352,6 +352,65 @@ def traffic_passes(keys):
     return out
 
 
+def short_kernel_name(name):
+    """A kernel trace name without its namespace and argument list (names the
+    profiler left mangled: the identifier and its integer template arguments)."""
+    import re
+    if name.startswith("_ZN"):
+        i, ident = 3, name
+        while i < len(name) and name[i].isdigit():   # <length><identifier> parts of the nested name
+            j = i
+            while name[j].isdigit():
+                j += 1
+            n = int(name[i:j])
+            ident, i = name[j:j + n], j + n
+        rest = name[i:]
+        targs = re.findall(r"L[ib](\d+)E", rest.split("EEv")[0]) if rest.startswith("I") else []
+        return ident + ("<" + ", ".join(targs) + ">" if targs else "")
+    name = re.sub(r"^void ", "", name)
+    name = re.sub(r"\bvdk::|\(anonymous namespace\)::", "", name)
+    depth, cut = 0, len(name)
+    for i, ch in enumerate(name):       # the argument list: the first '(' outside template brackets
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            cut = i
+            break
+    return name[:cut].replace("_Float16", "half")
+
+
+def traffic_table(tr, keys, path):
+    """Markdown table of every (kernel, grid) group's HBM bytes per launch from
+    the two counter passes, one section per workload."""
+    lines = ["# HBM traffic per launch (rocprofv3 FETCH_SIZE / WRITE_SIZE)", "",
+             "Made by `python bench.py " + " ".join(sys.argv[1:]) + "` on one MI355X.  Each workload ran "
+             f"{1 + TRAFFIC_STEPS} batches (the first a warmup) under `rocprofv3 --pmc FETCH_SIZE` and again under "
+             "`--pmc WRITE_SIZE` in a child process; each counter's KiB per dispatch is scaled by its reading for a "
+             f"{TRAFFIC_COPY_MIB} MiB device-to-device copy run right after the workload "
+             f"(bytes per counted byte: {tr.get('_factors')}).  Durations are from the counter runs "
+             "(slower than the bench's own passes).", ""]
+    for key in keys:
+        groups = tr.get(key) or {}
+        steps = 1 + TRAFFIC_STEPS
+        lines += [f"## {key}: {MODELS[key]['config']['workload']}", "",
+                  "| kernel | grid (threads) | launches / batch | us / launch | FETCH MB | WRITE MB | HBM MB / launch |",
+                  "|---|---:|---:|---:|---:|---:|---:|"]
+        for (name, grid), g in sorted(groups.items(), key=lambda kv: -(kv[1]["FETCH_SIZE"] + kv[1]["WRITE_SIZE"])):
+            n = g["count"]
+            if n == 0:
+                continue
+            f, w = g["FETCH_SIZE"] / n / 1e6, g["WRITE_SIZE"] / n / 1e6
+            if (f + w) * n / steps < 1.0:      # under 1 MB per batch: left out
+                continue
+            lines.append(f"| `{short_kernel_name(name)}` | {grid} | {n / steps:g} | {g['us'] / n:.1f} | "
+                         f"{f:.2f} | {w:.2f} | {f + w:.2f} |")
+        lines.append("")
+    with open(path, "w") as fh:
+        fh.write("\n".join(lines))
+
+
 def traffic_of(tr, key, launches_per_step, label):
     """Measured HBM bytes per launch of `key`'s dominant class, or (None, why):
     the (kernel, grid) group with that many launches per step (a conv kernel
@@ -534,6 +593,8 @@ def main():
                     help="after the bench, run 3 device-to-device copies of this many MiB (PMC traffic calibration)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes that measure the dominant kernels' HBM traffic")
+    ap.add_argument("--traffic-table", default=None, metavar="PATH",
+                    help="also write every kernel's measured HBM bytes per launch as a markdown table to PATH")
     ap.add_argument("--traffic-child", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.traffic_child:
@@ -550,6 +611,8 @@ def main():
     traffic = None if args.no_traffic else traffic_passes(keys)
     if traffic and "error" in traffic:
         print(f"bench.py: traffic not measured: {traffic['error']}", file=sys.stderr)
+    elif traffic and args.traffic_table:
+        traffic_table(traffic, keys, args.traffic_table)
     L = lib.lib()
     if L.vdk_device_count() < 1:
         print("bench.py: no HIP device visible", file=sys.stderr)
