@@ -448,6 +448,25 @@ int vdk_res2_pair3x3_conv3(const void* d_x, int x_stride, int batch, int H, int 
                            const float* d_b3, int terms3, const void* d_res, int res_stride, int res_lo, void* d_y,
                            int y_stride, int y_lo, float clamp_hi, void* stream);
 
+/* A whole layer-1 block of ERes2Net (src/encoder_eres2net.cpp:111-137, the
+ * Bottle2neck with scale 2 and 16-channel chunks, stride 1) in one launch,
+ * split-f16: c = min(relu(conv1(x) + b1), clamp_hi) (1x1, ic1 -> 32, [c0 | c1])
+ * then vdk_res2_pair3x3_conv3's pair and conv3 from c, with
+ * res = x when d_res is NULL (ic1 = 64: the block without a shortcut conv),
+ * else the given map (the shortcut output).  x: [batch][H][W] rows of
+ * x_stride elements, the ic1 hi halves first and the lo halves x_lo
+ * elements after them (ic1 = 32 or 64); w1: the split-f16 weights
+ * [32][terms1 * ic1] as vdk_conv_desc takes them ([hi | hi] for terms1 = 2,
+ * [hi | hi | lo] for 3); b1: f32 [32]; w_a, w_b, b_a, b_b, w3,
+ * b3, terms3, res, y as for vdk_res2_pair3x3_conv3.  c never reaches
+ * memory, so HBM sees x once and y once.  Equal bit for bit to vdk_conv2d_ex's
+ * split-f16 conv1 into [c0 | c1] rows followed by vdk_res2_pair3x3_conv3.
+ * y must not overlap x or res. */
+int vdk_res2_bottleneck(const void* d_x, int x_stride, int x_lo, int ic1, int batch, int H, int W, const void* d_w1,
+                        int terms1, const float* d_b1, const void* d_w_a, const float* d_b_a, const void* d_w_b,
+                        const float* d_b_b, const void* d_w3, const float* d_b3, int terms3, const void* d_res,
+                        int res_stride, int res_lo, void* d_y, int y_stride, int y_lo, float clamp_hi, void* stream);
+
 /* ---- wav2vec2 analyze (src/analyze_w2v2.cpp) ----
  * Activations are time-major [B][T][C]; the GEMM-shaped layers run on
  * vdk_conv2d_ex (H = 1, W = T).  These cover the rest of the graph. */

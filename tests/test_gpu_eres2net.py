@@ -629,3 +629,72 @@ def test_res2_pair_conv3_equals_pair_then_conv3(Bt, H, T, terms, tile):
     b = y2.to_array(np.float16, (Bt, H, T, 128))
     assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
     assert np.array_equal(d2.to_array(np.float16, (Bt, H, T, 128)).view(np.uint16), rows.view(np.uint16))
+
+
+@pytest.mark.parametrize("Bt,H,T,ic1,resx,t1,terms", [(2, 42, 301, 64, True, 3, 2), (2, 42, 301, 64, False, 2, 3),
+                                                      (2, 42, 301, 32, False, 2, 2), (1, 3, 5, 64, True, 2, 3),
+                                                      (3, 7, 61, 32, False, 3, 3), (B, 80, T20S, 64, True, 3, 3),
+                                                      (B, 80, T20S, 32, False, 3, 3)])
+def test_res2_bottleneck_equals_conv1_then_pair_conv3(Bt, H, T, ic1, resx, t1, terms):
+    """The whole layer-1 block in one launch (conv1 over an LDS x halo into the
+    [c0 | c1] halo, the pair, conv3 + residual) equals vdk_conv2d_ex's split
+    conv1 into grouped [c0 | c1] rows followed by vdk_res2_pair3x3_conv3, bit
+    for bit: x as the residual (64 channels) or a separate map, two- and
+    three-term conv1 / conv3 weights, maps smaller than one tile, partial
+    tiles and the 80 x 1998 layer-1 map at batch 16."""
+    rng = np.random.default_rng(2990 + H + ic1 + terms + 10 * t1)
+    announce(f"eres bottleneck B={Bt} H={H} T={T} ic1={ic1} resx={resx} t1={t1} terms={terms}")
+    xv = rng.standard_normal((Bt, H, T, ic1)).astype(np.float32) * 2
+    xh, xl = _split(xv)
+    xrows = np.ascontiguousarray(np.concatenate([xh, xl], axis=3))            # [hi ic1 | lo ic1]
+    w1 = (rng.standard_normal((32, ic1)) * np.sqrt(2.0 / ic1)).astype(np.float32)
+    if t1 == 2:
+        w1 = w1.astype(np.float16).astype(np.float32)
+    w1h, w1l = _split(w1)
+    w1p = np.ascontiguousarray(np.concatenate([w1h, w1h, w1l] if t1 == 3 else [w1h, w1h], axis=1))
+    b1 = rng.uniform(-0.5, 0.5, 32).astype(np.float32)
+    wa = (rng.standard_normal((16, 16, 3, 3)) * np.sqrt(2.0 / 144)).astype(np.float16)
+    wb = (rng.standard_normal((16, 16, 3, 3)) * np.sqrt(2.0 / 144)).astype(np.float16)
+    ba = rng.uniform(-0.5, 0.5, 16).astype(np.float32)
+    bb = rng.uniform(-0.5, 0.5, 16).astype(np.float32)
+    w3 = (rng.standard_normal((64, 32)) * np.sqrt(2.0 / 32)).astype(np.float32)
+    if terms == 2:
+        w3 = w3.astype(np.float16).astype(np.float32)
+    w3h, w3l = _split(w3)
+    w3p = np.ascontiguousarray(np.concatenate([w3h, w3h, w3l] if terms == 3 else [w3h, w3h], axis=1))
+    b3 = rng.uniform(-0.5, 0.5, 64).astype(np.float32)
+    keep = [lib.DeviceBuffer.from_array(w1p), lib.DeviceBuffer.from_array(b1),
+            lib.DeviceBuffer.from_array(np.ascontiguousarray(wa.transpose(0, 2, 3, 1))), lib.DeviceBuffer.from_array(ba),
+            lib.DeviceBuffer.from_array(np.ascontiguousarray(wb.transpose(0, 2, 3, 1))), lib.DeviceBuffer.from_array(bb),
+            lib.DeviceBuffer.from_array(w3p), lib.DeviceBuffer.from_array(b3)]
+    d_x = lib.DeviceBuffer.from_array(xrows)
+    if resx:
+        d_res, rs, rlo = d_x, 128, 64
+    else:
+        d_res = lib.DeviceBuffer.from_array(np.concatenate(_split(rng.standard_normal((Bt, H, T, 64)).astype(
+            np.float32) * 2), axis=3))
+        rs, rlo = 128, 64
+    L = lib.lib()
+    # conv1 into grouped [c0 | c1] rows, then the pair with conv3
+    rows = lib.DeviceBuffer(Bt * H * T * 128 * 2)
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride, d.x_lo = d_x.ptr, Bt, H, T, ic1, 2 * ic1, ic1
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, 32, 1, 1
+    d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+    d.bias, d.act, d.clamp_hi = keep[1].ptr, lib.ACT_RELU, 20.0
+    d.y, d.y_stride, d.y_lo, d.y_group_stride = rows.ptr, 128, 16, 32
+    d.split, d.tile = (2 if t1 == 2 else 1), -1
+    lib.check(L.vdk_conv2d_ex(d, None))
+    y1 = lib.DeviceBuffer(Bt * H * T * 128 * 2)
+    lib.check(L.vdk_res2_pair3x3_conv3(rows.ptr, 128, Bt, H, T, keep[2].ptr, keep[3].ptr, keep[4].ptr, keep[5].ptr,
+                                       keep[6].ptr, keep[7].ptr, terms, d_res.ptr, rs, rlo, y1.ptr, 128, 64, 20.0,
+                                       None))
+    y2 = lib.DeviceBuffer(Bt * H * T * 128 * 2)
+    lib.check(L.vdk_res2_bottleneck(d_x.ptr, 2 * ic1, ic1, ic1, Bt, H, T, keep[0].ptr, t1, keep[1].ptr, keep[2].ptr,
+                                    keep[3].ptr, keep[4].ptr, keep[5].ptr, keep[6].ptr, keep[7].ptr, terms,
+                                    None if resx else d_res.ptr, rs, rlo, y2.ptr, 128, 64, 20.0, None))
+    lib.check(L.vdk_synchronize())
+    a = y1.to_array(np.uint16, (Bt, H, T, 128))
+    b = y2.to_array(np.uint16, (Bt, H, T, 128))
+    assert np.array_equal(a, b)
+    assert np.array_equal(d_x.to_array(np.float16, xrows.shape).view(np.uint16), xrows.view(np.uint16))

@@ -298,19 +298,39 @@ void Model::encode_eres2net(int batch, int T) {
             const int wd = b.width;
             const View s4 = (wd == 16 || wd == 32) && !b.aff ? grouped_tensor(w.es4, 4 * wd, wd)
                                                              : split_tensor(w.es4, 4 * wd);
+            const bool last = bi == nb - 1 && li >= 1;
+            const View y = last ? split_tensor(w.ecat[li - 1], 4 * b.planes) : split_tensor(w.ex[xi ^ 1], 2 * b.planes);
+            const bool pair = b.pair_a && s4.gn == 16;
+            const bool pair_c3 = pair && b.conv3.kh * b.conv3.k == 1 && b.conv3.ic == 32 && b.conv3.oc == 64 &&
+                                 y.gs == y.gn;
+            // the whole block in one launch: stride 1, x contiguous
+            // (the residual is x or the shortcut's split_tensor output: contiguous either way)
+            const bool whole = pair_c3 && b.conv1.kh * b.conv1.k == 1 && b.conv1.split != 0 && b.stride == 1 &&
+                               b.conv1.oc == 32 && (b.conv1.ic == 32 || b.conv1.ic == 64) && x.gs == x.gn &&
+                               x.lo == b.conv1.ic && (b.has_sc || b.conv1.ic == 64);
             // conv1 -> [chunk0 | chunk1]
-            conv("eres_conv1", b.conv1, x, H, W, b.stride, nullptr, VDK_ACT_RELU, hi, 0, s4);
+            if (!whole) conv("eres_conv1", b.conv1, x, H, W, b.stride, nullptr, VDK_ACT_RELU, hi, 0, s4);
             // the shortcut (its input is the block input: independent of the chunks)
             View res = x;
             if (b.has_sc) {
                 res = split_tensor(w.esc, 2 * b.planes);
                 conv("eres_shortcut", b.sc, x, H, W, b.stride, nullptr, VDK_ACT_NONE, 0.0f, 0, res);
             }
-            const bool last = bi == nb - 1 && li >= 1;
-            const View y = last ? split_tensor(w.ecat[li - 1], 4 * b.planes) : split_tensor(w.ex[xi ^ 1], 2 * b.planes);
-            const bool pair = b.pair_a && s4.gn == 16;
-            if (pair && b.conv3.kh * b.conv3.k == 1 && b.conv3.ic == 32 && b.conv3.oc == 64 && y.gs == y.gn &&
-                res.gs == res.gn) {
+            if (whole) {
+                // conv1, the pair and conv3 + residual in one launch; [c0 | c1] and sp0 / sp1 stay on chip
+                const int terms = b.conv3.split == 2 ? 2 : 3;
+                const int ic = b.conv1.ic;
+                prof_begin("eres_res2_whole",
+                           2.0 * ((double)32 * (b.conv1.split == 2 ? 2 : 3) * ic + 9 * 16 * 16 * 2 * 3 +
+                                  64.0 * 32 * terms) * batch * Ho * Wo,
+                           2.0 * (2 * ic + 2 * 64 + (b.has_sc ? 2 * 64 : 0)) * (double)batch * Ho * Wo);
+                check_rc(vdk_res2_bottleneck(x.p, x.stride, x.lo, ic, batch, Ho, Wo, b.conv1.w,
+                                             b.conv1.split == 2 ? 2 : 3, b.conv1.b, b.pair_a,
+                                             b.conv_a.b, b.pair_b, b.conv_b.b, b.conv3.w, b.conv3.b, terms,
+                                             b.has_sc ? res.p : nullptr, res.stride, res.lo, y.p, y.stride, y.lo, hi,
+                                             stream_));
+                prof_end();
+            } else if (pair_c3 && res.gs == res.gn) {
                 // chunk 0 -> sp0, chunk 1 (+ sp0) -> sp1 and conv3 + residual -> clamp in one launch
                 // (MFMA work: conv_a 16 x 16 x 9 over both planes, conv_b twice that, conv3 64 x 32 per term)
                 const int terms = b.conv3.split == 2 ? 2 : 3;

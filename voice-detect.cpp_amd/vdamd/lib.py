@@ -172,6 +172,9 @@ _SIGS = {
                                    C.c_float, _vp]),
     "vdk_res2_pair3x3_conv3": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                          C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_float, _vp]),
+    "vdk_res2_bottleneck": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp,
+                                      _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int,
+                                      C.c_float, _vp]),
     "vdk_aff_combine": (C.c_int, [_vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp, C.c_int, C.c_int, C.c_long,
                                   C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp]),
     "vdk_bn_act": (C.c_int, [_vp, C.c_int, C.c_long, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, _vp]),
