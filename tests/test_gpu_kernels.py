@@ -609,7 +609,7 @@ def test_tstp_linear_l2_match_oracle():
 
 
 @pytest.mark.parametrize("B,H,W,C,lo", [(3, 10, 38, 256, 0), (2, 5, 250, 512, 512), (2, 4, 37, 200, 0),
-                                         (1, 3, 2, 64, 0)])
+                                         (1, 3, 2, 64, 0), (2, 3, 128, 264, 0)])
 def test_tstp_vector_and_scalar_paths(B, H, W, C, lo):
     """TSTP on 16-byte channel vectors (16-byte aligned rows, C % 8 == 0)
     and, for the same values through a view 4 bytes off alignment, on the

@@ -69,20 +69,23 @@ __global__ __launch_bounds__(256) void tstp_kernel(const half_t* __restrict__ x,
     }
 }
 
-// TSTP over 8-channel vectors: a workgroup covers 256 channels (32 groups of
-// 8, one 16-byte load each) of one (clip, freq row) in NP time partitions,
-// partition p taking time steps p, p + NP, ...; f64 partial sums per
-// channel, combined in a fixed order through LDS, then the squared deviations
-// from the f32 mean the same way.  The row's values (W x 256 channels) stay
-// in the L1 between the two passes.  NP = 32 for long rows (CAM++'s and
-// ERes2Net's hundreds of frames), 8 otherwise.
-template <int NP>
-__global__ __launch_bounds__(NP * 32) void tstp8_kernel(const half_t* __restrict__ x, int xs, int x_lo, int H,
-                                                        int W, int C, float eps, float* __restrict__ pooled) {
+// TSTP over 8-channel vectors: a workgroup covers 64 channels of one (clip,
+// freq row); thread (p, g) = (tid / 8, tid % 8) loads channels 8 g .. 8 g + 7
+// (one 16-byte vector, two for split inputs) at time steps p, p + 32, ...
+// and keeps their f64 partial sums.  One thread per channel then adds the 32
+// partitions in a fixed order (so the result does not depend on scheduling)
+// and publishes the f32 mean through LDS; the squared deviations from it go
+// the same way.  A wave's load covers 8 time steps x 128 bytes, and the
+// loops per thread are short (CAM++'s 499 frames: 16 steps), so many loads
+// are in flight.
+__global__ __launch_bounds__(256) void tstp64_kernel(const half_t* __restrict__ x, int xs, int x_lo, int H, int W,
+                                                     int C, float eps, float* __restrict__ pooled) {
 #pragma clang fp contract(off)
-    __shared__ double part[NP][257];
-    const int g = threadIdx.x & 31, tp = threadIdx.x >> 5;
-    const int c0 = blockIdx.x * 256 + g * 8, h = blockIdx.y, b = blockIdx.z;
+    constexpr int NP = 32;
+    __shared__ double part[NP][65];
+    __shared__ float smean[64];
+    const int tid = threadIdx.x, g = tid & 7, tp = tid >> 3;
+    const int c0 = blockIdx.x * 64 + g * 8, h = blockIdx.y, b = blockIdx.z;
     const bool ok = c0 < C;
     const size_t CH = (size_t)C * H;
     const half_t* row = x + ((size_t)b * H + h) * W * xs + (ok ? c0 : 0);
@@ -111,17 +114,19 @@ __global__ __launch_bounds__(NP * 32) void tstp8_kernel(const half_t* __restrict
 #pragma unroll
     for (int e = 0; e < 8; ++e) part[tp][g * 8 + e] = s[e];
     __syncthreads();
+    if (tid < 64) {
+        double m = 0.0;
+#pragma unroll 8
+        for (int q = 0; q < NP; ++q) m += part[q][tid];
+        smean[tid] = (float)(m / W);
+    }
+    __syncthreads();
     float mean[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        double m = 0.0;
-#pragma unroll
-        for (int q = 0; q < NP; ++q) m += part[q][g * 8 + e];
-        mean[e] = (float)(m / W);
+        mean[e] = smean[g * 8 + e];
+        s[e] = 0.0;
     }
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s[e] = 0.0;
     if (ok)
 #pragma unroll 4
         for (int t = tp; t < W; t += NP) {
@@ -136,18 +141,16 @@ __global__ __launch_bounds__(NP * 32) void tstp8_kernel(const half_t* __restrict
 #pragma unroll
     for (int e = 0; e < 8; ++e) part[tp][g * 8 + e] = s[e];
     __syncthreads();
-    if (tp == 0 && ok) {
+    const int c = blockIdx.x * 64 + tid;
+    if (tid < 64 && c < C) {
+        double q2 = 0.0;
+#pragma unroll 8
+        for (int q = 0; q < NP; ++q) q2 += part[q][tid];
+        float var = (float)(q2 / W);
+        if (W > 1) var = var * ((float)W / (float)(W - 1));
         float* out = pooled + (size_t)b * 2 * CH;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            double q2 = 0.0;
-#pragma unroll
-            for (int q = 0; q < NP; ++q) q2 += part[q][g * 8 + e];
-            float var = (float)(q2 / W);
-            if (W > 1) var = var * ((float)W / (float)(W - 1));
-            out[(size_t)(c0 + e) * H + h] = mean[e];
-            out[CH + (size_t)(c0 + e) * H + h] = sqrtf(var + eps);
-        }
+        out[(size_t)c * H + h] = smean[tid];
+        out[CH + (size_t)c * H + h] = sqrtf(var + eps);
     }
 }
 
@@ -328,12 +331,8 @@ extern "C" int vdk_tstp_ex(const void* d_x, int x_stride, int x_lo, int batch, i
         const int xs = x_stride ? x_stride : C;
         require(xs >= C && (x_lo == 0 || (x_lo >= C && x_lo + C <= xs)), "tstp: bad pixel stride / lo offset");
         const bool vec = C % 8 == 0 && xs % 8 == 0 && x_lo % 8 == 0 && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0;
-        if (vec && W >= 128)
-            hipLaunchKernelGGL(tstp8_kernel<32>, dim3(cdiv(C, 256), H, batch), dim3(1024), 0,
-                               static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), xs, x_lo, H, W, C,
-                               eps, d_pooled);
-        else if (vec)
-            hipLaunchKernelGGL(tstp8_kernel<8>, dim3(cdiv(C, 256), H, batch), dim3(256), 0,
+        if (vec)
+            hipLaunchKernelGGL(tstp64_kernel, dim3(cdiv(C, 64), H, batch), dim3(256), 0,
                                static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), xs, x_lo, H, W, C,
                                eps, d_pooled);
         else
