@@ -215,6 +215,7 @@ TILE_SHAPES = [
     # (B, H, W, IC, OC, K, stride, pad): small maps with ragged tile edges per kernel family
     (2, 13, 75, 32, 32, 3, 1, 1), (2, 9, 70, 64, 64, 3, 1, 1), (2, 7, 38, 128, 128, 3, 1, 1),
     (2, 6, 19, 256, 256, 3, 1, 1), (2, 11, 37, 32, 64, 3, 2, 1), (2, 11, 37, 64, 128, 1, 2, 0),
+    (2, 1, 301, 256, 136, 1, 1, 0), (3, 5, 37, 128, 64, 1, 1, 0),
 ]
 
 
@@ -408,6 +409,58 @@ def test_conv_chunked_weights_bitwise(shape):
         assert np.array_equal(outs[0], outs[1]), f"tile {t}"
         n += 1
     assert n >= 2
+
+
+@pytest.mark.parametrize("case", [
+    # (B, T, IC, OC, x_stride, epilogue)
+    (2, 301, 1024, 1024, 1024, "bias_relu_bn"), (3, 149, 3072, 768, 3072, "bias_res"),
+    (2, 37, 768, 2304, 776, "gelu"), (1, 5, 256, 136, 256, "res_f32_y_f32"), (2, 70, 4608, 128, 4608, "tmajor"),
+])
+def test_gemm_ws_tiles_bitwise(case):
+    """The 1x1 GEMM kernel with producer / compute waves (tiles 81-84) returns
+    the LDS-DMA kernel's bits (same MFMA shape, K order and staged epilogue)
+    for every epilogue form the time-major models use: bias + ReLU + post-BN,
+    f16 residual, exact GELU, f32 residual into an f32 output, a time-major
+    store; ragged pixel counts, output channels off the tile grid and a
+    padded input stride."""
+    L = lib.lib()
+    B, T, IC, OC, xs, epi = case
+    rng = np.random.default_rng(B * 10 + T + IC + OC)
+    announce(f"gemm_ws B={B} T={T} {IC}->{OC} {epi}")
+    dx = lib.DeviceBuffer.from_array((rng.standard_normal((B, T, xs)) * 0.5).astype(np.float16))
+    dw = lib.DeviceBuffer.from_array((rng.standard_normal((OC, 1, 1, IC)) * np.sqrt(1.0 / IC)).astype(np.float16))
+    db = lib.DeviceBuffer.from_array(rng.standard_normal(OC).astype(np.float32))
+    dsc = lib.DeviceBuffer.from_array(rng.uniform(0.5, 1.5, OC).astype(np.float32))
+    dsh = lib.DeviceBuffer.from_array(rng.standard_normal(OC).astype(np.float32))
+    f32 = epi == "res_f32_y_f32"
+    dr = lib.DeviceBuffer.from_array(rng.standard_normal((B, T, OC)).astype(np.float32 if f32 else np.float16))
+    outs = {}
+    for t in (36, 81, 82, 83, 84):
+        d = lib.ConvDesc()
+        d.x, d.batch, d.H, d.W, d.IC, d.x_stride = dx.ptr, B, 1, T, IC, xs
+        d.w, d.OC, d.KH, d.KW = dw.ptr, OC, 1, 1
+        d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+        d.bias = db.ptr
+        if epi == "bias_relu_bn":
+            d.act, d.post_scale, d.post_shift = lib.ACT_RELU, dsc.ptr, dsh.ptr
+        elif epi == "bias_res":
+            d.residual = dr.ptr
+        elif epi == "gelu":
+            d.act = lib.ACT_GELU
+        elif f32:
+            d.residual, d.res_f32, d.y_f32 = dr.ptr, 1, 1
+        else:
+            d.act, d.y_time_major = lib.ACT_RELU, 1
+        dy = lib.DeviceBuffer(B * T * OC * 4)
+        d.y, d.tile = dy.ptr, t
+        if not L.vdk_conv2d_tile_fits_ex(t, d):
+            continue
+        lib.check(L.vdk_conv2d_ex(d, None))
+        lib.check(L.vdk_synchronize())
+        outs[t] = dy.to_array(np.uint32 if f32 else np.uint16, (B, T, OC))
+    assert 36 in outs and len(outs) >= 3, sorted(outs)
+    for t, o in outs.items():
+        assert np.array_equal(o, outs[36]), f"tile {t}"
 
 
 def test_conv_invariants_delta_and_zero():

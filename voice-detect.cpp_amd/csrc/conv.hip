@@ -814,6 +814,159 @@ void launch_dma(const ConvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// gemm_ws_kernel: 1x1 stride-1 convs (the time-major GEMMs of ECAPA's TDNN /
+// MFA layers and wav2vec2's linears: M = output channels, N = pixels, K =
+// input channels) with the waves split by role, as in the band kernel: NP
+// producer waves DMA each KC-channel chunk of the tile's BM weight rows and
+// BN pixel rows into an NST-stage LDS ring (rows XOR-swizzled as in the
+// LDS-DMA kernel), and the compute waves only read LDS and run MFMAs, each
+// k-step's fragment reads issued between the previous step's MFMAs.  One
+// barrier per chunk; the producers keep NST-1 chunks in flight.  The
+// epilogue is the implicit-GEMM kernels' staged one (every epilogue option),
+// run by all waves.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int WMG, int WNG, int KC, int NST, int NP>
+struct GemmWs {
+    static constexpr int NCW = WMG * WNG, NW = NCW + NP;
+    static constexpr int WM = BM / WMG, WN = BN / WNG, TM = WM / 32, TN = WN / 32;
+    static constexpr int CPR = KC / 8, RB = KC * 2;
+    static constexpr int NINS = (BM + BN) * CPR / 64, IPP = NINS / NP;   // DMA instructions per chunk / producer
+    static constexpr int STAGE = NINS * 1024;
+    static_assert(KC == 32 || KC == 64, "KC");
+    static_assert(NINS % NP == 0 && (BM * CPR) % 64 == 0, "whole DMA instructions, split evenly over the producers");
+    static_assert(NST >= 2 && NST * STAGE <= 163840, "the ring fits the 160 KB of LDS");
+    static_assert(TM >= 1 && TN >= 1, "wave tiles of whole 32 x 32 blocks");
+    static_assert(IPP * (NST - 2) <= 60, "vmcnt range");
+};
+
+template <int BM, int BN, int WMG, int WNG, int KC, int NST, int NP>
+__global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs a) {
+    using G = GemmWs<BM, BN, WMG, WNG, KC, NST, NP>;
+    constexpr int TM = G::TM, TN = G::TN, RB = G::RB, CPR = G::CPR;
+    constexpr int SMEM_E = G::WN * (BM + 4) * 4;   // one epilogue pass of a wave's pixel columns
+    constexpr int SMEM = NST * G::STAGE > SMEM_E ? NST * G::STAGE : SMEM_E;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int ptile, otile;
+    tile_ids(ptile, otile);
+    const int p0 = ptile * BN, oc0 = otile * BM;
+    const int nk = a.IC / KC;
+
+    float16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    int m_off = 0, n_off = -1;   // producers stage nothing in the epilogue
+
+    if (wave >= G::NCW) {
+        // ---------------- producers ----------------
+        const int p = wave - G::NCW;
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)a.w, 0, (int)((size_t)a.OC * a.IC * 2), 0x00020000);
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)a.x, 0, (int)(((size_t)(a.npix - 1) * a.xs + a.IC) * 2), 0x00020000);
+        // this lane's slot of each of its instructions (at channel 0): LDS row
+        // r, 16-byte slot s holds chunk swz(r, s) of weight row oc0 + r or of
+        // pixel row p0 + r - BM; -1: past the weights / pixels (reads zeros)
+        int off[G::IPP];
+#pragma unroll
+        for (int i = 0; i < G::IPP; ++i) {
+            const int ins = p + NP * i;
+            const int q = ins * 64 + lane, r = q / CPR, c = swz<KC>(r, q - r * CPR);
+            if (r < BM) {
+                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.IC + c * 8) * 2 : -1;
+            } else {
+                const int P = p0 + r - BM;
+                off[i] = P < a.npix ? (P * a.xs + c * 8) * 2 : -1;
+            }
+        }
+        auto issue = [&](int k) {
+            uint8_t* const dst = smem + (k % NST) * G::STAGE;
+#pragma unroll
+            for (int i = 0; i < G::IPP; ++i) {
+                const int ins = p + NP * i;
+                const uint32_t o = off[i] < 0 ? kOOB : (uint32_t)(off[i] + k * KC * 2);
+                if (ins * (64 / CPR) < BM)   // wave-uniform: the weight rows fill whole instructions
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
+                else
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
+            }
+        };
+#pragma unroll
+        for (int k = 0; k < NST - 1; ++k)
+            if (k < nk) issue(k);
+#pragma unroll 1
+        for (int k = 0; k < nk; ++k) {
+            // chunk k has landed once at most min(NST-2, nk-1-k) younger chunks are in flight
+            const int younger = nk - 1 - k < NST - 2 ? nk - 1 - k : NST - 2;
+            wait_vmcnt_le(younger * G::IPP);
+            lds_barrier();   // chunk k is visible; the compute waves are done with chunk k-1's stage
+            if (k + NST - 1 < nk) issue(k + NST - 1);
+        }
+    } else {
+        // ---------------- compute waves ----------------
+        const int wm = wave % WMG, wn = wave / WMG;
+        m_off = wm * G::WM;
+        n_off = wn * G::WN;
+        const int lrow = lane & 31, lhalf = lane >> 5;
+        int aoff[TM], boff[TN];   // row bases; the swizzled chunk is added per k-step
+#pragma unroll
+        for (int i = 0; i < TM; ++i) aoff[i] = (m_off + i * 32 + lrow) * RB;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) boff[j] = (BM + n_off + j * 32 + lrow) * RB;
+        constexpr int KS = KC / 16;
+#pragma unroll 1
+        for (int k = 0; k < nk; ++k) {
+            lds_barrier();   // chunk k has landed; chunk k-1's reads are done
+            const uint8_t* const sa = smem + (k % NST) * G::STAGE;
+            half8 af[2][TM], bf[2][TN];
+            auto load = [&](int kk, int buf) {
+                const int c = kk * 2 + lhalf;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+                    af[buf][i] = *reinterpret_cast<const half8*>(sa + aoff[i] + swz<KC>(m_off + i * 32 + lrow, c) * 16);
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    bf[buf][j] = *reinterpret_cast<const half8*>(
+                        sa + boff[j] + swz<KC>(BM + n_off + j * 32 + lrow, c) * 16);
+            };
+            load(0, 0);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                const int cb = kk & 1;
+                if (kk + 1 < KS) load(kk + 1, cb ^ 1);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cb][i], bf[cb][j], acc[i][j], 0, 0, 0);
+                if (kk + 1 < KS) {
+                    // one MFMA, then one fragment read, in turn
+#pragma unroll
+                    for (int q = 0; q < TM + TN; ++q) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+    stage_epilogue_impl<BM, BN, G::WN, SMEM, G::NW * 64, TM, TN>(a, smem, acc, m_off, n_off, p0, oc0, tid, lane);
+}
+
+template <int BM, int BN, int WMG, int WNG, int KC, int NST, int NP>
+void launch_gemm_ws(const ConvArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL((gemm_ws_kernel<BM, BN, WMG, WNG, KC, NST, NP>), dim3(cdiv(a.npix, BN), cdiv(a.OC, BM)),
+                       dim3((WMG * WNG + NP) * 64), 0, s, a);
+}
+
+// ---------------------------------------------------------------------------
 // conv3x3_halo_kernel: stride-1 3x3 conv for narrow layers (IC, OC <= 64).
 // A workgroup owns a TH x TW output tile of one image and OCB output
 // channels.  Per IC chunk it DMAs the (TH+2) x (TW+2) input halo and the
@@ -2440,6 +2593,7 @@ struct TileCfg {
     int rw_ic = 0;   // register-weight kernels: exactly IC = rw_ic and OC = bm, plain epilogue
     int band_w = 0;  // band kernels: W <= band_w, OC % 128 == 0, IC % 16 == 0
     int sp_ic = 0;   // split-f16 register-weight kernels: exactly IC = sp_ic and OC = bm, split 2
+    bool gemm = false;   // 1x1 stride-1 GEMM kernels: contiguous channels, no prologue / reflect / q8_0 / segment sums
 };
 
 // Entries 0-13 are the register-staged kernel (any layout; the only one with
@@ -2452,7 +2606,8 @@ struct TileCfg {
 // 70-75 the split-f16 register-weight kernel (ERes2Net's group convs), 76-79
 // the producer / compute band kernel on one-row bands (the same sums in the
 // same order as its 5-row bands, so the same bits, on 5x the workgroups), 80
-// the register-staged 64x64 tile with 64-channel chunks.
+// the register-staged 64x64 tile with 64-channel chunks, 81-84 the 1x1 GEMM
+// kernel with producer / compute waves.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -2538,6 +2693,10 @@ const TileCfg kTiles[] = {
     {128, 64, 16, launch_bandws<1, 38, 4, 1, 2, 4>, true, 0, 38},   // 78
     {128, 64, 16, launch_bandws<1, 38, 4, 2, 1, 4>, true, 0, 38},   // 79
     {64, 64, 64, launch_igemm<64, 64, 32, 32, 64>},       // 80: register-staged, 64-channel chunks
+    {128, 256, 64, launch_gemm_ws<128, 256, 2, 4, 64, 3, 4>, false, 0, 0, 0, true},   // 81: 1x1 GEMMs, producer / compute waves
+    {128, 384, 32, launch_gemm_ws<128, 384, 2, 4, 32, 4, 4>, false, 0, 0, 0, true},   // 82
+    {256, 128, 64, launch_gemm_ws<256, 128, 4, 2, 64, 3, 4>, false, 0, 0, 0, true},   // 83
+    {128, 288, 64, launch_gemm_ws<128, 288, 2, 3, 64, 3, 4>, false, 0, 0, 0, true},   // 84
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -2590,6 +2749,10 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     // take the register-staged kernel
     if (a.KH * a.KW > 32 && a.KH != 1 && !igemm_tile(idx)) return false;
     if (t.sp_ic) return a.IC == t.sp_ic && a.OC == t.bm && split_epilogue(a);
+    if (t.gemm)
+        return a.KH == 1 && a.KW == 1 && a.sh == 1 && a.sw == 1 && a.ph == 0 && a.pw == 0 && !a.split && !a.in_scale &&
+               !a.reflect && !a.wq && !a.segsum && a.xgs == (1 << a.xgl) && a.IC % t.kc == 0 && a.xs % 8 == 0 &&
+               a.npix == a.npix_in;
     // 16-channel group strides: the LDS-DMA kernel's offsets and the shared store
     if ((a.xgs != (1 << a.xgl) || a.ygs != (1 << a.ygl)) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w))
         return false;
@@ -2648,6 +2811,23 @@ int pick_tile(const ConvArgs& a) {
         // (re-checked with random data: zeros draw less MFMA power and run
         // at higher clocks, which had favoured some tiles)
         if (a.KW > 32 && a.IC % 64 == 0) return 52;
+        // 1x1 GEMMs on the producer / compute wave kernel, from a sweep of the
+        // ECAPA (64 x 398 frames) and wav2vec2 (64 x 149 frames) layer shapes
+        // with random data: MFA 3072 -> 1536 313 -> 238 us, asp.tdnn 4608 ->
+        // 128 64 -> 49 us, the TDNNs 1024 -> 1024 84 -> 78 us, wav2vec2 ff2
+        // 62 -> 49 us (base) / 115 -> 90 us (large), out-projections 23.5 ->
+        // 20.3 / 39.8 -> 31.7 us (base ff1, 768 -> 3072 with its GELU, measured
+        // no faster in the model and stays on the LDS-DMA tile).  The
+        // 128 x 384 tile where it covers a 9536-pixel map in one round of
+        // workgroups, 128 x 288 for the 25472-pixel TDNNs (712 workgroups:
+        // 2.8 rounds where 128 x 256 makes 3.1), 256 x 128 for 768 outputs,
+        // else 128 x 256 for long K or wide outputs
+        if (a.KW == 1 && tile_fits(kTiles[81], a)) {
+            if (a.OC == 768 && a.IC >= 768) return 83;
+            if (a.npix < 16384 && (a.OC == 1024 || a.OC == 2304) && tile_fits(kTiles[82], a)) return 82;
+            if (a.npix >= 16384 && a.OC == 1024 && a.IC == 1024 && tile_fits(kTiles[84], a)) return 84;
+            if (a.IC >= 2048 || (a.IC >= 1024 && a.OC >= 3072)) return 81;
+        }
         // ECAPA's block0 (k = 5 over the 96 padded mel channels, 1024 out) on
         // the 128x256 8-wave tile (52.9 against 69.2 us at batch 64 x 4 s),
         // and asp.tdnn's 1536 -> 128 GEMM on the 128x64 tile (398 workgroups
