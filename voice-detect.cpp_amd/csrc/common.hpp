@@ -102,8 +102,8 @@ __device__ __forceinline__ void wait_vmcnt_le(int n) {
 #define VDK_VM(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
         VDK_VM(0) VDK_VM(1) VDK_VM(2) VDK_VM(3) VDK_VM(4) VDK_VM(5) VDK_VM(6) VDK_VM(7) VDK_VM(8)
         VDK_VM(9) VDK_VM(10) VDK_VM(11) VDK_VM(12) VDK_VM(13) VDK_VM(14) VDK_VM(15) VDK_VM(16)
-        VDK_VM(18) VDK_VM(20) VDK_VM(24) VDK_VM(27) VDK_VM(28) VDK_VM(30) VDK_VM(32) VDK_VM(36) VDK_VM(40)
-        VDK_VM(42) VDK_VM(45) VDK_VM(48) VDK_VM(54) VDK_VM(56) VDK_VM(60)
+        VDK_VM(18) VDK_VM(20) VDK_VM(21) VDK_VM(24) VDK_VM(26) VDK_VM(27) VDK_VM(28) VDK_VM(30) VDK_VM(32)
+        VDK_VM(36) VDK_VM(39) VDK_VM(40) VDK_VM(42) VDK_VM(45) VDK_VM(48) VDK_VM(54) VDK_VM(56) VDK_VM(60)
 #undef VDK_VM
         default: __builtin_amdgcn_s_waitcnt(0); break;
     }

@@ -814,9 +814,11 @@ void launch_dma(const ConvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// gemm_ws_kernel: 1x1 stride-1 convs (the time-major GEMMs of ECAPA's TDNN /
-// MFA layers and wav2vec2's linears: M = output channels, N = pixels, K =
-// input channels) with the waves split by role, as in the band kernel: NP
+// gemm_ws_kernel: convs with one row of taps (KH = 1, no row padding, zero
+// column padding, any stride / dilation; the time-major GEMMs of ECAPA's
+// TDNN / MFA layers, wav2vec2's linears and strided feature convs, 1x1
+// stride-2 shortcuts: M = output channels, N = pixels, K = taps x input
+// channels) with the waves split by role, as in the band kernel: NP
 // producer waves DMA each KC-channel chunk of the tile's BM weight rows and
 // BN pixel rows into an NST-stage LDS ring (rows XOR-swizzled as in the
 // LDS-DMA kernel), and the compute waves only read LDS and run MFMAs, each
@@ -851,7 +853,8 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
     int ptile, otile;
     tile_ids(ptile, otile);
     const int p0 = ptile * BN, oc0 = otile * BM;
-    const int nk = a.IC / KC;
+    const int ncpt = a.IC / KC;        // chunks per tap
+    const int nk = a.KW * ncpt;        // K = taps x input channels, taps outermost
 
     float16v acc[TM][TN];
 #pragma unroll
@@ -866,34 +869,51 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
         // ---------------- producers ----------------
         const int p = wave - G::NCW;
         const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)a.w, 0, (int)((size_t)a.OC * a.IC * 2), 0x00020000);
+            (void*)a.w, 0, (int)((size_t)a.OC * a.KW * a.IC * 2), 0x00020000);
         const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)a.x, 0, (int)(((size_t)(a.npix - 1) * a.xs + a.IC) * 2), 0x00020000);
-        // this lane's slot of each of its instructions (at channel 0): LDS row
-        // r, 16-byte slot s holds chunk swz(r, s) of weight row oc0 + r or of
-        // pixel row p0 + r - BM; -1: past the weights / pixels (reads zeros)
-        int off[G::IPP];
+            (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
+        // this lane's slot of each of its instructions: LDS row r, 16-byte
+        // slot s holds chunk swz(r, s) of weight row oc0 + r ([OC][KW][IC])
+        // or of output pixel p0 + r - BM.  A weight slot keeps its byte
+        // offset at tap 0 / channel 0 (-1: past the weights, reads zeros); a
+        // pixel slot its input row's first pixel (-1: past the pixels) and
+        // the tap-0 input column iw0, checked against [0, W) per tap.
+        int off[G::IPP], iw0[G::IPP];
+        const int HoWo = a.Ho * a.Wo;
 #pragma unroll
         for (int i = 0; i < G::IPP; ++i) {
             const int ins = p + NP * i;
             const int q = ins * 64 + lane, r = q / CPR, c = swz<KC>(r, q - r * CPR);
+            iw0[i] = 0;
             if (r < BM) {
-                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.IC + c * 8) * 2 : -1;
+                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.KW * a.IC + c * 8) * 2 : -1;
             } else {
                 const int P = p0 + r - BM;
-                off[i] = P < a.npix ? (P * a.xs + c * 8) * 2 : -1;
+                off[i] = -1;
+                if (P < a.npix) {
+                    const int b = P / HoWo, rem = P - b * HoWo;
+                    const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
+                    off[i] = (b * a.H + oh * a.sh) * a.W;   // input row (KH = 1, no row padding)
+                    iw0[i] = ow * a.sw - a.pw;
+                }
+                iw0[i] = iw0[i] * 16 + c;   // the slot's chunk rides in the low 4 bits
             }
         }
         auto issue = [&](int k) {
             uint8_t* const dst = smem + (k % NST) * G::STAGE;
+            const int tap = k / ncpt, c0 = (k - tap * ncpt) * KC;
 #pragma unroll
             for (int i = 0; i < G::IPP; ++i) {
                 const int ins = p + NP * i;
-                const uint32_t o = off[i] < 0 ? kOOB : (uint32_t)(off[i] + k * KC * 2);
-                if (ins * (64 / CPR) < BM)   // wave-uniform: the weight rows fill whole instructions
+                if (ins * (64 / CPR) < BM) {   // wave-uniform: the weight rows fill whole instructions
+                    const uint32_t o = off[i] < 0 ? kOOB : (uint32_t)(off[i] + (tap * a.IC + c0) * 2);
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
-                else
+                } else {
+                    const int iw = (iw0[i] >> 4) + tap * a.dw, c = iw0[i] & 15;
+                    const bool in = off[i] >= 0 && (unsigned)iw < (unsigned)a.W;
+                    const uint32_t o = in ? (uint32_t)(((off[i] + iw) * a.xs + c0 + c * 8) * 2) : kOOB;
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
+                }
             }
         };
 #pragma unroll
@@ -2750,9 +2770,8 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     if (a.KH * a.KW > 32 && a.KH != 1 && !igemm_tile(idx)) return false;
     if (t.sp_ic) return a.IC == t.sp_ic && a.OC == t.bm && split_epilogue(a);
     if (t.gemm)
-        return a.KH == 1 && a.KW == 1 && a.sh == 1 && a.sw == 1 && a.ph == 0 && a.pw == 0 && !a.split && !a.in_scale &&
-               !a.reflect && !a.wq && !a.segsum && a.xgs == (1 << a.xgl) && a.IC % t.kc == 0 && a.xs % 8 == 0 &&
-               a.npix == a.npix_in;
+        return a.KH == 1 && a.ph == 0 && !a.split && !a.in_scale && !a.reflect && !a.wq && !a.segsum &&
+               a.xgs == (1 << a.xgl) && a.IC % t.kc == 0 && a.xs % 8 == 0;
     // 16-channel group strides: the LDS-DMA kernel's offsets and the shared store
     if ((a.xgs != (1 << a.xgl) || a.ygs != (1 << a.ygl)) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w))
         return false;
@@ -2816,17 +2835,26 @@ int pick_tile(const ConvArgs& a) {
         // with random data: MFA 3072 -> 1536 313 -> 238 us, asp.tdnn 4608 ->
         // 128 64 -> 49 us, the TDNNs 1024 -> 1024 84 -> 78 us, wav2vec2 ff2
         // 62 -> 49 us (base) / 115 -> 90 us (large), out-projections 23.5 ->
-        // 20.3 / 39.8 -> 31.7 us (base ff1, 768 -> 3072 with its GELU, measured
-        // no faster in the model and stays on the LDS-DMA tile).  The
+        // 20.3 / 39.8 -> 31.7 us (the 768- / 1024-input ff1 and qkv GEMMs
+        // measured no faster and stay on the LDS-DMA tile).  The
         // 128 x 384 tile where it covers a 9536-pixel map in one round of
         // workgroups, 128 x 288 for the 25472-pixel TDNNs (712 workgroups:
         // 2.8 rounds where 128 x 256 makes 3.1), 256 x 128 for 768 outputs,
-        // else 128 x 256 for long K or wide outputs
+        // 128 x 256 from 2048 input channels
         if (a.KW == 1 && tile_fits(kTiles[81], a)) {
             if (a.OC == 768 && a.IC >= 768) return 83;
             if (a.npix < 16384 && (a.OC == 1024 || a.OC == 2304) && tile_fits(kTiles[82], a)) return 82;
             if (a.npix >= 16384 && a.OC == 1024 && a.IC == 1024 && tile_fits(kTiles[84], a)) return 84;
-            if (a.IC >= 2048 || (a.IC >= 1024 && a.OC >= 3072)) return 81;
+            if (a.IC >= 2048) return 81;
+        }
+        // the same kernel for wav2vec2's strided feature convs (512 -> 512,
+        // 3 / 2 taps, stride 2, exact GELU; 64 x 3 s clips, interleaved
+        // timing): from 64k output pixels the 128 x 256 tile (conv1 .. conv3:
+        // 779 -> 745, 413 -> 404, 200 -> 181 us), 2-tap ones of 16k-32k
+        // pixels the 128 x 384 tile (conv5: 47.2 -> 40.9 us)
+        if (a.sw == 2 && a.KW <= 3 && a.IC == 512 && a.OC == 512 && tile_fits(kTiles[81], a)) {
+            if (a.npix >= 65536) return 81;
+            if (a.KW == 2 && a.npix >= 16384 && a.npix < 32768 && tile_fits(kTiles[82], a)) return 82;
         }
         // ECAPA's block0 (k = 5 over the 96 padded mel channels, 1024 out) on
         // the 128x256 8-wave tile (52.9 against 69.2 us at batch 64 x 4 s),
