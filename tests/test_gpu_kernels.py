@@ -412,12 +412,13 @@ def test_conv_chunked_weights_bitwise(shape):
 
 
 @pytest.mark.parametrize("case", [
-    # (B, H, T, IC, OC, x_stride, KW, stride, pad, epilogue)
-    (2, 1, 301, 1024, 1024, 1024, 1, 1, 0, "bias_relu_bn"), (3, 1, 149, 3072, 768, 3072, 1, 1, 0, "bias_res"),
-    (2, 1, 37, 768, 2304, 776, 1, 1, 0, "gelu"), (1, 1, 5, 256, 136, 256, 1, 1, 0, "res_f32_y_f32"),
-    (2, 1, 70, 4608, 128, 4608, 1, 1, 0, "tmajor"), (2, 1, 301, 512, 512, 512, 3, 2, 0, "gelu"),
-    (3, 1, 99, 512, 512, 520, 2, 2, 0, "gelu"), (2, 1, 40, 256, 256, 256, 5, 1, 2, "bias_relu_bn"),
-    (2, 9, 31, 64, 128, 64, 1, 2, 0, "bias_res"),
+    # (B, H, T, IC, OC, x_stride, KH, KW, stride, pad, epilogue)
+    (2, 1, 301, 1024, 1024, 1024, 1, 1, 1, 0, "bias_relu_bn"), (3, 1, 149, 3072, 768, 3072, 1, 1, 1, 0, "bias_res"),
+    (2, 1, 37, 768, 2304, 776, 1, 1, 1, 0, "gelu"), (1, 1, 5, 256, 136, 256, 1, 1, 1, 0, "res_f32_y_f32"),
+    (2, 1, 70, 4608, 128, 4608, 1, 1, 1, 0, "tmajor"), (2, 1, 301, 512, 512, 512, 1, 3, 2, 0, "gelu"),
+    (3, 1, 99, 512, 512, 520, 1, 2, 2, 0, "gelu"), (2, 1, 40, 256, 256, 256, 1, 5, 1, 2, "bias_relu_bn"),
+    (2, 9, 31, 64, 128, 64, 1, 1, 2, 0, "bias_res"), (2, 11, 37, 64, 128, 64, 3, 3, 2, 1, "bias_res"),
+    (2, 7, 19, 128, 256, 128, 3, 3, 1, 1, "bias_relu_bn"),
 ])
 def test_gemm_ws_tiles_bitwise(case):
     """The one-row-of-taps GEMM kernel with producer / compute waves (tiles
@@ -429,13 +430,14 @@ def test_gemm_ws_tiles_bitwise(case):
     shortcut; ragged pixel counts, output channels off the tile grid and
     padded input strides."""
     L = lib.lib()
-    B, H, T, IC, OC, xs, KW, st, pad, epi = case
-    rng = np.random.default_rng(B * 10 + T + IC + OC + KW)
-    announce(f"gemm_ws B={B} H={H} T={T} {IC}->{OC} k{KW} s{st} p{pad} {epi}")
-    Ho = (H - 1) // st + 1 if KW == 1 else H
+    B, H, T, IC, OC, xs, KH, KW, st, pad, epi = case
+    rng = np.random.default_rng(B * 10 + T + IC + OC + KW + KH)
+    announce(f"gemm_ws B={B} H={H} T={T} {IC}->{OC} k{KH}x{KW} s{st} p{pad} {epi}")
+    sh, ph = (st, pad) if KH > 1 or H > 1 else (1, 0)
+    Ho = (H + 2 * ph - KH) // sh + 1
     To = (T + 2 * pad - KW) // st + 1
     dx = lib.DeviceBuffer.from_array((rng.standard_normal((B, H, T, xs)) * 0.5).astype(np.float16))
-    dw = lib.DeviceBuffer.from_array((rng.standard_normal((OC, 1, KW, IC)) * np.sqrt(1.0 / (KW * IC))).astype(
+    dw = lib.DeviceBuffer.from_array((rng.standard_normal((OC, KH, KW, IC)) * np.sqrt(1.0 / (KH * KW * IC))).astype(
         np.float16))
     db = lib.DeviceBuffer.from_array(rng.standard_normal(OC).astype(np.float32))
     dsc = lib.DeviceBuffer.from_array(rng.uniform(0.5, 1.5, OC).astype(np.float32))
@@ -446,8 +448,8 @@ def test_gemm_ws_tiles_bitwise(case):
     for t in (36, 81, 82, 83, 84):
         d = lib.ConvDesc()
         d.x, d.batch, d.H, d.W, d.IC, d.x_stride = dx.ptr, B, H, T, IC, xs
-        d.w, d.OC, d.KH, d.KW = dw.ptr, OC, 1, KW
-        d.stride_h = st if KW == 1 else 1
+        d.w, d.OC, d.KH, d.KW = dw.ptr, OC, KH, KW
+        d.stride_h, d.pad_h = sh, ph
         d.stride_w, d.pad_w = st, pad
         d.dil_h = d.dil_w = 1
         d.bias = db.ptr

@@ -814,11 +814,10 @@ void launch_dma(const ConvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// gemm_ws_kernel: convs with one row of taps (KH = 1, no row padding, zero
-// column padding, any stride / dilation; the time-major GEMMs of ECAPA's
-// TDNN / MFA layers, wav2vec2's linears and strided feature convs, 1x1
-// stride-2 shortcuts: M = output channels, N = pixels, K = taps x input
-// channels) with the waves split by role, as in the band kernel: NP
+// gemm_ws_kernel: implicit-GEMM convs (zero padding, any stride /
+// dilation; the time-major GEMMs of ECAPA's TDNN / MFA layers, wav2vec2's
+// linears and strided feature convs: M = output channels, N = pixels, K =
+// taps x input channels) with the waves split by role, as in the band kernel: NP
 // producer waves DMA each KC-channel chunk of the tile's BM weight rows and
 // BN pixel rows into an NST-stage LDS ring (rows XOR-swizzled as in the
 // LDS-DMA kernel), and the compute waves only read LDS and run MFMAs, each
@@ -854,7 +853,7 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
     tile_ids(ptile, otile);
     const int p0 = ptile * BN, oc0 = otile * BM;
     const int ncpt = a.IC / KC;        // chunks per tap
-    const int nk = a.KW * ncpt;        // K = taps x input channels, taps outermost
+    const int nk = a.KH * a.KW * ncpt; // K = taps x input channels, taps outermost
 
     float16v acc[TM][TN];
 #pragma unroll
@@ -869,39 +868,42 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
         // ---------------- producers ----------------
         const int p = wave - G::NCW;
         const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)a.w, 0, (int)((size_t)a.OC * a.KW * a.IC * 2), 0x00020000);
+            (void*)a.w, 0, (int)((size_t)a.OC * a.KH * a.KW * a.IC * 2), 0x00020000);
         const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
         // this lane's slot of each of its instructions: LDS row r, 16-byte
-        // slot s holds chunk swz(r, s) of weight row oc0 + r ([OC][KW][IC])
+        // slot s holds chunk swz(r, s) of weight row oc0 + r ([OC][KH][KW][IC])
         // or of output pixel p0 + r - BM.  A weight slot keeps its byte
         // offset at tap 0 / channel 0 (-1: past the weights, reads zeros); a
-        // pixel slot its input row's first pixel (-1: past the pixels) and
-        // the tap-0 input column iw0, checked against [0, W) per tap.
-        int off[G::IPP], iw0[G::IPP];
+        // pixel slot its clip's first input row b * H (-1: past the pixels)
+        // and the tap-0 input row / column ih0, iw0 (with the slot's chunk
+        // in the low 4 bits), checked against the map per tap.
+        int off[G::IPP], ih0[G::IPP], iw0[G::IPP];
         const int HoWo = a.Ho * a.Wo;
 #pragma unroll
         for (int i = 0; i < G::IPP; ++i) {
             const int ins = p + NP * i;
             const int q = ins * 64 + lane, r = q / CPR, c = swz<KC>(r, q - r * CPR);
-            iw0[i] = 0;
+            ih0[i] = iw0[i] = 0;
             if (r < BM) {
-                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.KW * a.IC + c * 8) * 2 : -1;
+                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.KH * a.KW * a.IC + c * 8) * 2 : -1;
             } else {
                 const int P = p0 + r - BM;
                 off[i] = -1;
                 if (P < a.npix) {
                     const int b = P / HoWo, rem = P - b * HoWo;
                     const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
-                    off[i] = (b * a.H + oh * a.sh) * a.W;   // input row (KH = 1, no row padding)
+                    off[i] = b * a.H;
+                    ih0[i] = oh * a.sh - a.ph;
                     iw0[i] = ow * a.sw - a.pw;
                 }
-                iw0[i] = iw0[i] * 16 + c;   // the slot's chunk rides in the low 4 bits
+                iw0[i] = iw0[i] * 16 + c;
             }
         }
         auto issue = [&](int k) {
             uint8_t* const dst = smem + (k % NST) * G::STAGE;
             const int tap = k / ncpt, c0 = (k - tap * ncpt) * KC;
+            const int kh = tap / a.KW, kw = tap - kh * a.KW;
 #pragma unroll
             for (int i = 0; i < G::IPP; ++i) {
                 const int ins = p + NP * i;
@@ -909,9 +911,9 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
                     const uint32_t o = off[i] < 0 ? kOOB : (uint32_t)(off[i] + (tap * a.IC + c0) * 2);
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
                 } else {
-                    const int iw = (iw0[i] >> 4) + tap * a.dw, c = iw0[i] & 15;
-                    const bool in = off[i] >= 0 && (unsigned)iw < (unsigned)a.W;
-                    const uint32_t o = in ? (uint32_t)(((off[i] + iw) * a.xs + c0 + c * 8) * 2) : kOOB;
+                    const int ih = ih0[i] + kh * a.dh, iw = (iw0[i] >> 4) + kw * a.dw, c = iw0[i] & 15;
+                    const bool in = off[i] >= 0 && (unsigned)ih < (unsigned)a.H && (unsigned)iw < (unsigned)a.W;
+                    const uint32_t o = in ? (uint32_t)((((off[i] + ih) * a.W + iw) * a.xs + c0 + c * 8) * 2) : kOOB;
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
                 }
             }
@@ -2770,8 +2772,8 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     if (a.KH * a.KW > 32 && a.KH != 1 && !igemm_tile(idx)) return false;
     if (t.sp_ic) return a.IC == t.sp_ic && a.OC == t.bm && split_epilogue(a);
     if (t.gemm)
-        return a.KH == 1 && a.ph == 0 && !a.split && !a.in_scale && !a.reflect && !a.wq && !a.segsum &&
-               a.xgs == (1 << a.xgl) && a.IC % t.kc == 0 && a.xs % 8 == 0;
+        return !a.split && !a.in_scale && !a.reflect && !a.wq && !a.segsum && a.xgs == (1 << a.xgl) &&
+               a.IC % t.kc == 0 && a.xs % 8 == 0;
     // 16-channel group strides: the LDS-DMA kernel's offsets and the shared store
     if ((a.xgs != (1 << a.xgl) || a.ygs != (1 << a.ygl)) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w))
         return false;
@@ -2930,6 +2932,13 @@ int pick_tile(const ConvArgs& a) {
     if (!a.split && a.KH == a.KW && a.sh == 2 && a.sw == 2 && a.npix < 8192 && a.IC % 32 == 0 && a.OC % 64 == 0) {
         if (a.KH == 3 && a.IC % 64 == 0 && a.OC % 128 == 0 && tile_fits(kTiles[52], a)) return 52;
         if (tile_fits(kTiles[63], a)) return 63;
+    }
+    // ResNet's stride-2 3x3s from 64 / 128 channels at batch 64 on the GEMM
+    // producer / compute kernel (interleaved timing: 32.5 -> 29.3 us on the
+    // 128 x 384 tile, 28.3 -> 26.3 us on 256 x 128)
+    if (!a.split && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2 && a.npix >= 16384) {
+        if (a.IC == 64 && a.OC == 128 && tile_fits(kTiles[82], a)) return 82;
+        if (a.IC == 128 && a.OC == 256 && tile_fits(kTiles[83], a)) return 83;
     }
     // ResNet's stride-2 32->64 pair (random-data sweep): the 1x1 on the 64x64
     // register-staged tile, the 3x3 on the 64x128 one
