@@ -410,6 +410,26 @@ int vdk_cam_local(const void* d_x, int x_stride, int batch, int T, int C, int se
                   const void* d_wl, const float* d_bl, void* d_y, int y_stride, const double* d_segsum,
                   double* d_zero_next, void* stream);
 
+/* One dense layer's CAM (vdk_cam_local with C = 128 channels of h, its
+ * context from segsum, zero_next NULL) and the next layer's linear1 in the
+ * same launch, per (clip, segment) (src/encoder_campplus.cpp:250-281,
+ * 110-134, 159-182): the CAM writes its 32 outputs into the block buffer
+ * dense [B][T][dense_stride] at channel cin, then
+ * hn = relu(wn . relu(dense[.., 0 : cin + 32] * scale_n + shift_n) + bn)
+ * for the segment's frames (wn f16 [128][cin + 32], bn / scale_n / shift_n
+ * f32; the prologue rounded to f16 as the GEMM operand) into hn [B][T][128],
+ * and the segment's f64 sums of the stored hn values into its row of
+ * seg_next [B][ceil(T / seg)][128] (stored, not added: nothing needs
+ * clearing).  Equal bit for bit to vdk_cam_local followed by vdk_conv2d_ex's
+ * linear1 with in_scale / in_shift and seg_sum.  h [B][T][128] f16 is read
+ * with a dil-frame halo from the neighbouring segments, so hn must be
+ * another buffer; cin % 32 == 0, cin + 32 <= 1024 and <= dense_stride,
+ * seg <= 128.  A one-layer CAM++ block step in one launch instead of two. */
+int vdk_cam_dense(const void* d_h, int batch, int T, int seg, int dil, const float* d_w1, const float* d_b1, int H1,
+                  const float* d_w2, const float* d_b2, const void* d_wl, const float* d_bl, void* d_dense,
+                  int dense_stride, int cin, const double* d_segsum, const void* d_wn, const float* d_bn,
+                  const float* d_scale_n, const float* d_shift_n, void* d_hn, double* d_seg_next, void* stream);
+
 /* ---- ERes2Net helper (src/encoder_eres2net.cpp:91-101) ----
  * AFF output y = (x + ds) + t * (x - ds) with t = tanh(local_att(cat(x, ds)))
  * already computed; all f16 rows of C channels with their own strides.  With

@@ -298,6 +298,68 @@ def test_campplus_verify_matches_oracle(campp):
         assert ctx.verify_pcm(a, b, thr)[1] == (d_ref <= thr)
 
 
+@pytest.mark.parametrize("batch,T,cin,dil", [(B, TP, 128, 1), (3, 257, 480, 2), (8, 149, 160, 2),
+                                             (2, 40, 992, 2), (12, 3, 128, 1), (4, 101, 224, 2)])
+def test_cam_dense_equals_cam_then_linear1(batch, T, cin, dil):
+    """One launch of a dense layer's CAM and the next layer's linear1
+    (vdk_cam_dense) against vdk_cam_local followed by the linear1 conv with
+    its BN+ReLU prologue and segment sums: the block buffer (the 32 new
+    channels, nothing else touched), the next h and its per-segment sums
+    bit for bit; a short last segment (T' = 149, 101), one short segment
+    (40), clips of 3 frames, the widest input (992 + 32 = 1024 channels)."""
+    rng = np.random.default_rng(31 * T + cin + dil)
+    L = lib.lib()
+    BC, G, H1, SEG, CMAX = 128, 32, 64, 100, 1024
+    nseg = (T + SEG - 1) // SEG
+    cn = cin + G
+    announce(f"campp cam_dense B={batch} T'={T} cin={cin} dil={dil}")
+    dense = rng.standard_normal((batch, T, CMAX), dtype=np.float32).astype(np.float16)
+    h = np.maximum(rng.standard_normal((batch, T, BC), dtype=np.float32), 0).astype(np.float16)
+    hd = h.astype(np.float64)
+    seg = np.stack([hd[:, i * SEG:(i + 1) * SEG].sum(axis=1) for i in range(nseg)], axis=1)   # exact
+    w1 = rng.standard_normal((H1, BC), dtype=np.float32) / 8
+    b1 = rng.standard_normal(H1, dtype=np.float32) / 4
+    w2 = rng.standard_normal((G, H1), dtype=np.float32) / 8
+    b2 = rng.standard_normal(G, dtype=np.float32) / 4
+    wl = (rng.standard_normal((G, 3, BC), dtype=np.float32) / np.sqrt(3 * BC)).astype(np.float16)
+    bl = (rng.standard_normal(G, dtype=np.float32) * 0.1).astype(np.float32)
+    wn = (rng.standard_normal((BC, cn), dtype=np.float32) / np.sqrt(cn)).astype(np.float16)
+    bn = (rng.standard_normal(BC, dtype=np.float32) * 0.1).astype(np.float32)
+    sc = (rng.random(cn, dtype=np.float32) + 0.5).astype(np.float32)
+    sh = (rng.standard_normal(cn, dtype=np.float32) * 0.2).astype(np.float32)
+    keep = [lib.DeviceBuffer.from_array(a) for a in (h, seg, w1, b1, w2, b2, wl, bl, wn, bn, sc, sh)]
+    dh, dseg, dw1, db1, dw2, db2, dwl, dbl, dwn, dbn, dsc, dsh = keep
+    # reference: the CAM launch, then linear1 as a conv accumulating into cleared sums
+    dA = lib.DeviceBuffer.from_array(dense)
+    lib.check(L.vdk_cam_local(dh.ptr, BC, batch, T, BC, SEG, dil, dw1.ptr, db1.ptr, H1, dw2.ptr, db2.ptr, dwl.ptr,
+                              dbl.ptr, dA.ptr + 2 * cin, CMAX, dseg.ptr, None, None))
+    hA = lib.DeviceBuffer(batch * T * BC * 2)
+    segA = lib.DeviceBuffer.from_array(np.zeros((batch, nseg, BC)))
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride = dA.ptr, batch, 1, T, cn, CMAX
+    d.w, d.OC, d.KH, d.KW = dwn.ptr, BC, 1, 1
+    d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+    d.bias, d.act = dbn.ptr, lib.ACT_RELU
+    d.in_scale, d.in_shift = dsc.ptr, dsh.ptr
+    d.seg_sum, d.seg_len = segA.ptr, SEG
+    d.y, d.y_stride, d.tile = hA.ptr, BC, -1
+    lib.check(L.vdk_conv2d_ex(d, None))
+    # one launch
+    dB = lib.DeviceBuffer.from_array(dense)
+    hB = lib.DeviceBuffer(batch * T * BC * 2)
+    segB = lib.DeviceBuffer.from_array(np.full((batch, nseg, BC), 7.0))
+    lib.check(L.vdk_cam_dense(dh.ptr, batch, T, SEG, dil, dw1.ptr, db1.ptr, H1, dw2.ptr, db2.ptr, dwl.ptr, dbl.ptr,
+                              dB.ptr, CMAX, cin, dseg.ptr, dwn.ptr, dbn.ptr, dsc.ptr, dsh.ptr, hB.ptr, segB.ptr, None))
+    _sync()
+    a, b = dA.to_array(np.uint16, dense.shape), dB.to_array(np.uint16, dense.shape)
+    assert np.array_equal(a, b)
+    assert np.array_equal(np.delete(b, np.s_[cin:cn], axis=2), np.delete(dense.view(np.uint16), np.s_[cin:cn], axis=2))
+    assert np.array_equal(hA.to_array(np.uint16, (batch, T, BC)), hB.to_array(np.uint16, (batch, T, BC)))
+    assert np.array_equal(segA.to_array(np.float64, (batch, nseg, BC)), segB.to_array(np.float64, (batch, nseg, BC)))
+    assert L.vdk_cam_dense(dh.ptr, batch, T, SEG, dil, dw1.ptr, db1.ptr, H1, dw2.ptr, db2.ptr, dwl.ptr, dbl.ptr,
+                           dB.ptr, CMAX, cin, dseg.ptr, dwn.ptr, dbn.ptr, dsc.ptr, dsh.ptr, dh.ptr, segB.ptr, None) != 0
+
+
 @pytest.mark.parametrize("batch,T,c_in", [(B, TP, 320), (3, 257, 160), (2, 40, 128),
                                           (8, 149, 128), (8, 49, 160), (16, 101, 256), (12, 3, 128)])
 def test_linear1_segment_sums_feed_cam_local(batch, T, c_in):

@@ -280,7 +280,7 @@ private:
         void* fcm[3] = {nullptr, nullptr, nullptr};
         void* fcm_t = nullptr;
         void* dense[3] = {nullptr, nullptr, nullptr};
-        void *cc = nullptr, *fin = nullptr;
+        void *cc = nullptr, *cc2 = nullptr, *fin = nullptr;   // CAM++: linear1 outputs (two layers' worth)
         double* segsum[2] = {nullptr, nullptr};   // per-(clip, segment) sums of linear1's output, two layers' worth
         size_t segsum_bytes = 0;
         // ERes2Net

@@ -21,6 +21,7 @@
 // Weights: conv weights f16 [OC][KH][KW][IC] (Q8_0 / F16 / F32 dequantised at
 // load), the context MLP and the dense head f32.
 #include <algorithm>
+#include <utility>
 #include <cmath>
 #include <string>
 
@@ -190,6 +191,7 @@ void Model::alloc_campplus_workspace(int batch, int T) {
         cmax = std::max(cmax, m.blocks[b].cmax);
     }
     w.cc = ws_alloc(2 * BTp * m.bn_ch);
+    w.cc2 = ws_alloc(2 * BTp * m.bn_ch);
     w.segsum_bytes = 8 * (size_t)batch * ((Tp + kCamSeg - 1) / kCamSeg) * m.bn_ch;
     w.segsum[0] = static_cast<double*>(ws_alloc(w.segsum_bytes));
     w.segsum[1] = static_cast<double*>(ws_alloc(w.segsum_bytes));
@@ -292,34 +294,70 @@ void Model::encode_campplus(int batch, int T) {
     };
     tconv("campp_tdnn", m.tdnn, w.fcm_t, m.tdnn.ic, T, 2, 2, 1, nullptr, VDK_ACT_RELU, w.dense[0], m.blocks[0].cmax);
 
-    // dense blocks (src/encoder_campplus.cpp:250-281).  linear1 adds its
-    // output's per-(clip, segment) sums to segsum[layer & 1] (the CAM
-    // context's pooling, exact in f64) and the CAM launch clears the other
-    // buffer for the next layer; both start cleared.
+    // dense blocks (src/encoder_campplus.cpp:250-281).  A block's first
+    // linear1 runs as a conv that adds its output's per-(clip, segment) sums
+    // to a cleared buffer (the CAM context's pooling, exact in f64); then
+    // each launch runs one layer's CAM and the next layer's linear1 over the
+    // same (clip, segment) (vdk_cam_dense: the next layer's input at a frame
+    // is the block buffer plus the 32 channels just written), writing that
+    // linear1's output h into the other h buffer and its segment sums into
+    // the other sums buffer; the block's last CAM runs alone and clears the
+    // buffer the next block's first linear1 accumulates into.
     VDK_HIP(hipMemsetAsync(w.segsum[0], 0, w.segsum_bytes, stream_));
     VDK_HIP(hipMemsetAsync(w.segsum[1], 0, w.segsum_bytes, stream_));
-    int layer = 0;
+    int p = 0;   // the sums buffer of the current h
     for (int b = 0; b < 3; ++b) {
         const CamBlock& blk = m.blocks[b];
         uint8_t* D = static_cast<uint8_t*>(w.dense[b]);
-        for (const CamDense& d : blk.layers) {
-            double* seg = w.segsum[layer & 1];
-            double* seg_next = w.segsum[(layer + 1) & 1];
-            ++layer;
-            // nonlinear1 BN + ReLU (src/encoder_campplus.cpp:110-134) folded into
-            // linear1's operand loads
-            tconv("campp_linear1", d.l1, D, blk.cmax, Tp, 1, 0, 1, nullptr, VDK_ACT_RELU, w.cc, m.bn_ch, d.bn_s,
-                  d.bn_t, seg);
-            // the CAM layer: context from the segment sums, mask MLP and the gated
-            // linear_local in one launch
+        void* h = w.cc;
+        void* hn = w.cc2;
+        const int L = (int)blk.layers.size();
+        for (int l = 0; l < L; ++l) {
+            const CamDense& d = blk.layers[l];
+            double* seg = w.segsum[p];
+            double* seg_next = w.segsum[p ^ 1];
+            if (l == 0) {
+                // nonlinear1 BN + ReLU (src/encoder_campplus.cpp:110-134) folded into
+                // linear1's operand loads
+                tconv("campp_linear1", d.l1, D, blk.cmax, Tp, 1, 0, 1, nullptr, VDK_ACT_RELU, h, m.bn_ch, d.bn_s,
+                      d.bn_t, seg);
+            }
+            const CamDense* dn = l + 1 < L ? &blk.layers[l + 1] : nullptr;
+            // (measured at 32 x 10 s: the launch pair 19.4 / 22.1 / 25.9 / 27.9 / 32.3 us against 17.0 / 20.6 /
+            // 24.5 / 29.2 / 34.7 us in one for 160 / 352 / 544 / 768 / 1024 input channels: the linear1 conv
+            // streams wide inputs faster on its 500 workgroups, so only narrow layers take the one launch)
+            const bool fuse = dn && m.bn_ch == 128 && m.growth == 32 && d.c_in % 32 == 0 && dn->c_in == d.c_in + 32 &&
+                              dn->c_in <= 544 && dn->l1.k == 1 && dn->l1.oc == 128 && dn->l1.b && dn->bn_s;
+            if (fuse) {
+                prof_begin("campp_cam_dense",
+                           2.0 * rows * 3 * m.bn_ch * m.growth +
+                               2.0 * batch * nseg * ((double)d.h1 * m.bn_ch + (double)m.growth * d.h1) +
+                               2.0 * rows * dn->c_in * m.bn_ch,
+                           2.0 * rows * m.bn_ch * (1.0 + nseg) + 2.0 * rows * m.growth +
+                               2.0 * rows * (dn->c_in + m.bn_ch));
+                check_rc(vdk_cam_dense(h, batch, Tp, kCamSeg, blk.dil, d.c1_w, d.c1_b, d.h1, d.c2_w, d.c2_b,
+                                       d.local.w, d.local.b, D, blk.cmax, d.c_in, seg, dn->l1.w, dn->l1.b, dn->bn_s,
+                                       dn->bn_t, hn, seg_next, stream_));
+                prof_end();
+                std::swap(h, hn);
+                p ^= 1;
+                continue;
+            }
+            // the CAM layer alone: context from the segment sums, mask MLP and the gated
+            // linear_local in one launch; it clears the other sums buffer
             prof_begin("campp_cam_local",
                        2.0 * rows * 3 * m.bn_ch * m.growth +
                            2.0 * batch * nseg * ((double)d.h1 * m.bn_ch + (double)m.growth * d.h1),
                        2.0 * rows * m.bn_ch * (1.0 + nseg) + 2.0 * rows * m.growth);
-            check_rc(vdk_cam_local(w.cc, m.bn_ch, batch, Tp, m.bn_ch, kCamSeg, blk.dil, d.c1_w, d.c1_b, d.h1, d.c2_w,
+            check_rc(vdk_cam_local(h, m.bn_ch, batch, Tp, m.bn_ch, kCamSeg, blk.dil, d.c1_w, d.c1_b, d.h1, d.c2_w,
                                    d.c2_b, d.local.w, d.local.b, D + 2 * (size_t)d.c_in, blk.cmax, seg, seg_next,
                                    stream_));
             prof_end();
+            p ^= 1;
+            if (dn) {   // the next layer's linear1 as a conv into the cleared buffer
+                tconv("campp_linear1", dn->l1, D, blk.cmax, Tp, 1, 0, 1, nullptr, VDK_ACT_RELU, h, m.bn_ch,
+                      dn->bn_s, dn->bn_t, w.segsum[p]);
+            }
         }
         const bool last = b == 2;
         tconv("campp_transit", blk.transit, D, blk.cmax, Tp, 1, 0, 1, nullptr, last ? VDK_ACT_RELU : VDK_ACT_NONE,

@@ -179,6 +179,8 @@ _SIGS = {
                                   C.c_int, C.c_int, _vp, C.c_int, C.c_int, _vp]),
     "vdk_bn_act": (C.c_int, [_vp, C.c_int, C.c_long, C.c_int, _vp, _vp, C.c_int, _vp, C.c_int, _vp]),
     "vdk_segment_sums": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "vdk_cam_dense": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, _vp, _vp, _vp,
+                                C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdk_cam_local": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int,
                                 _vp, _vp, _vp, _vp, _vp, C.c_int, _vp, _vp, _vp]),
     "vdk_cam_context": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int,
