@@ -421,8 +421,9 @@ def traffic_of(tr, key, launches_per_step, label):
     if not groups:
         return None, f"no dispatches recorded for {key}"
     want = launches_per_step * TRAFFIC_STEPS
+    conv_kernel = lambda name: "conv" in name or "gemm" in name   # the kernels behind vdk_conv2d_ex
     cands = [(g["us"], name, grid, g) for (name, grid), g in groups.items()
-             if g["count"] in (want, want + launches_per_step) and (not label.startswith("conv") or "conv" in name)]
+             if g["count"] in (want, want + launches_per_step) and (not label.startswith("conv") or conv_kernel(name))]
     if not cands:
         return None, (f"no single kernel launch group with the class's {launches_per_step} launches per step "
                       "(its launches use several kernels or grids)")
