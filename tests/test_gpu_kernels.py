@@ -419,16 +419,17 @@ def test_conv_chunked_weights_bitwise(shape):
     (3, 1, 99, 512, 512, 520, 1, 2, 2, 0, "gelu"), (2, 1, 40, 256, 256, 256, 1, 5, 1, 2, "bias_relu_bn"),
     (2, 9, 31, 64, 128, 64, 1, 1, 2, 0, "bias_res"), (2, 11, 37, 64, 128, 64, 3, 3, 2, 1, "bias_res"),
     (2, 7, 19, 128, 256, 128, 3, 3, 1, 1, "bias_relu_bn"),
+    (2, 1, 45, 32, 256, 32, 1, 1, 1, 0, "bias_res"), (3, 1, 77, 64, 384, 72, 1, 1, 1, 0, "gelu"),
 ])
 def test_gemm_ws_tiles_bitwise(case):
-    """The one-row-of-taps GEMM kernel with producer / compute waves (tiles
-    81-84) returns the LDS-DMA kernel's bits (same MFMA shape, K order and
-    staged epilogue) for every epilogue form the models use: bias + ReLU +
-    post-BN, f16 residual, exact GELU, f32 residual into an f32 output, a
-    time-major store; 1x1 GEMMs, strided 2- / 3-tap convs (wav2vec2's
-    feature encoder), a zero-padded 5-tap conv and a 2-D 1x1 stride-2
-    shortcut; ragged pixel counts, output channels off the tile grid and
-    padded input strides."""
+    """The GEMM kernel with producer / compute waves (tiles 81-84) returns
+    the LDS-DMA kernel's bits (same MFMA shape, K order and staged epilogue)
+    for every epilogue form the models use: bias + ReLU + post-BN, f16
+    residual, exact GELU, f32 residual into an f32 output, a time-major
+    store; 1x1 GEMMs, strided 2- / 3-tap convs (wav2vec2's feature encoder),
+    a zero-padded 5-tap conv and a 2-D 1x1 stride-2 shortcut; ragged pixel
+    counts, output channels off the tile grid, padded input strides, and K
+    of one or two chunks (the ring's shortest walks)."""
     L = lib.lib()
     B, H, T, IC, OC, xs, KH, KW, st, pad, epi = case
     rng = np.random.default_rng(B * 10 + T + IC + OC + KW + KH)
@@ -470,7 +471,7 @@ def test_gemm_ws_tiles_bitwise(case):
         lib.check(L.vdk_conv2d_ex(d, None))
         lib.check(L.vdk_synchronize())
         outs[t] = dy.to_array(np.uint32 if f32 else np.uint16, (B, Ho, To, OC))
-    assert 36 in outs and len(outs) >= 3, sorted(outs)
+    assert 36 in outs and len(outs) >= (2 if IC % 64 else 3), sorted(outs)
     for t, o in outs.items():
         assert np.array_equal(o, outs[36]), f"tile {t}"
 

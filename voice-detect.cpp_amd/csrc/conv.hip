@@ -689,27 +689,47 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_dma_kernel(Co
     int f_tap = 0, f_kw = 0, f_c0 = 0, f_x = 0, f_xc = 0;
     const int tap_bytes = a.dw * a.xs * 2;                       // next kw
     const int row_bytes = a.dh * a.W * a.xs * 2 - a.KW * tap_bytes;   // next kh, back to kw = 0
-    auto issue = [&](int st) {
+    // This wave's DMA instructions of the cursor's chunk into stage st,
+    // branch-free inside: the weight / pixel split of an instruction is fixed
+    // at compile time when the weight instructions divide evenly over the
+    // waves, and the tap test / reflect padding variants are chosen once per
+    // chunk (a wave-uniform branch), so the loads go out back to back.
+    constexpr int WI = BM * CPR / 64;   // weight instructions per stage
+    auto issue_all = [&](int st, auto tap_in, auto refl) {
         const int w_soff = (f_tap * ICW + f_c0) * 2;
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
             lds_void* dst = (lds_void*)(smem + st * STAGE + (wave + j * NW) * 1024);
-            if (s_is_w[j]) {
+            const bool isw = WI % NW == 0 ? j < WI / NW : s_is_w[j];
+            if (isw) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, dst, 16, (uint32_t)s_off[j], w_soff, 0, 0);
             } else {
-                const bool in = tap_range ? (uint32_t)(f_tap - (int)(s_mask[j] & 0xFFFFu)) <
-                                                (uint32_t)((int)(s_mask[j] >> 16) - (int)(s_mask[j] & 0xFFFFu))
-                                          : ((s_mask[j] >> f_tap) & 1u) != 0;
+                const bool in = tap_in(s_mask[j]);
                 uint32_t off = in ? (uint32_t)(s_off[j] + f_x + f_xc) : kOOB;
-                if (a.reflect && !in && s_iw[j] != INT_MIN) {
+                if constexpr (decltype(refl)::value) {
                     // the tap's column reflected back into [0, W) (KH = 1: f_tap is the column tap)
-                    int iw = s_iw[j] + f_tap * a.dw;
+                    const bool pix = s_iw[j] != INT_MIN;
+                    const int iw0 = pix ? s_iw[j] : 0;
+                    int iw = iw0 + f_tap * a.dw;
                     iw = iw < 0 ? -iw : (iw >= a.W ? 2 * (a.W - 1) - iw : iw);
                     iw = iw < 0 ? 0 : (iw >= a.W ? a.W - 1 : iw);
-                    off = (uint32_t)(s_off[j] + (iw - s_iw[j]) * a.xs * 2 + f_xc);
+                    const uint32_t roff = (uint32_t)(s_off[j] + (iw - iw0) * a.xs * 2 + f_xc);
+                    off = !in && pix ? roff : off;
                 }
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, off, 0, 0, 0);
             }
+        }
+    };
+    auto issue = [&](int st) {
+        const auto bit_in = [&](uint32_t m) { return ((m >> f_tap) & 1u) != 0; };
+        if (tap_range) {
+            issue_all(st, [&](uint32_t m) {
+                return (uint32_t)(f_tap - (int)(m & 0xFFFFu)) < (uint32_t)((int)(m >> 16) - (int)(m & 0xFFFFu));
+            }, std::false_type());
+        } else if (a.reflect) {
+            issue_all(st, bit_in, std::true_type());
+        } else {
+            issue_all(st, bit_in, std::false_type());
         }
         f_c0 += KC;
         f_xc += (KC >> a.xgl) * a.xgs * 2;
@@ -826,6 +846,75 @@ void launch_dma(const ConvArgs& a, hipStream_t s) {
 // epilogue is the implicit-GEMM kernels' staged one (every epilogue option),
 // run by all waves.
 // ---------------------------------------------------------------------------
+// DMA slots of one feeding wave of the GEMM kernels: instruction i of wave p
+// (p + NPW * i of the chunk's NINS) fills LDS row r = q / CPR (q = 64 * ins
+// + lane), 16-byte slot s with chunk swz(r, s) of weight row oc0 + r
+// ([OC][KH][KW][IC]) or, past the BM weight rows, of output pixel
+// p0 + r - BM.  A weight slot keeps its byte offset at tap 0 / channel 0
+// (-1: past the weights, reads zeros); a pixel slot its clip's first input
+// row b * H (-1: past the pixels) and the tap-0 input row / column ih0, iw0
+// (with the slot's chunk in the low 4 bits), checked against the map per tap.
+template <int BM, int KC, int IPW, int NPW>
+struct GemmFeed {
+    static constexpr int CPR = KC / 8;
+    int p, lane;
+    int off[IPW], ih0[IPW], iw0[IPW];
+    __amdgpu_buffer_rsrc_t wr, xr;
+    __device__ __forceinline__ GemmFeed(const ConvArgs& a, int p_, int lane_, int p0, int oc0) : p(p_), lane(lane_) {
+        wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)((size_t)a.OC * a.KH * a.KW * a.IC * 2),
+                                               0x00020000);
+        xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2),
+                                               0x00020000);
+        const int HoWo = a.Ho * a.Wo;
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+            const int ins = p + NPW * i;
+            const int q = ins * 64 + lane, r = q / CPR, c = swz<KC>(r, q - r * CPR);
+            ih0[i] = iw0[i] = 0;
+            if (r < BM) {
+                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.KH * a.KW * a.IC + c * 8) * 2 : -1;
+            } else {
+                const int P = p0 + r - BM;
+                off[i] = -1;
+                if (P < a.npix) {
+                    const int b = P / HoWo, rem = P - b * HoWo;
+                    const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
+                    off[i] = b * a.H;
+                    ih0[i] = oh * a.sh - a.ph;
+                    iw0[i] = ow * a.sw - a.pw;
+                }
+                iw0[i] = iw0[i] * 16 + c;
+            }
+        }
+    }
+    // This wave's instructions of chunk k (tap k / ncpt, channels from
+    // (k % ncpt) * KC) into the stage at dst: branch-free (selects of
+    // out-of-range offsets, the weight / pixel split fixed at compile time),
+    // so the loads go out back to back.
+    __device__ __forceinline__ void issue(const ConvArgs& a, uint8_t* dst, int k, int ncpt) const {
+        const int tap = k / ncpt, c0 = (k - tap * ncpt) * KC;
+        const int kh = tap / a.KW, kw = tap - kh * a.KW;
+        constexpr int WI = BM * CPR / 64;   // the weight rows' instructions (whole ones)
+#pragma unroll
+        for (int i = 0; i < IPW; ++i) {
+            const int ins = p + NPW * i;
+            // wave-uniform; known at compile time when the weight instructions
+            // split evenly over the feeding waves (ins < WI iff i < WI / NPW)
+            const bool wrow = WI % NPW == 0 ? i < WI / NPW : ins < WI;
+            if (wrow) {
+                const uint32_t o = off[i] < 0 ? kOOB : (uint32_t)(off[i] + (tap * a.IC + c0) * 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
+            } else {
+                const int ih = ih0[i] + kh * a.dh, iw = (iw0[i] >> 4) + kw * a.dw, c = iw0[i] & 15;
+                const bool in = off[i] >= 0 && (unsigned)ih < (unsigned)a.H && (unsigned)iw < (unsigned)a.W;
+                const uint32_t pos = (uint32_t)((((off[i] + ih) * a.W + iw) * a.xs + c0 + c * 8) * 2);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(dst + ins * 1024), 16, in ? pos : kOOB, 0, 0,
+                                                         0);
+            }
+        }
+    }
+};
+
 template <int BM, int BN, int WMG, int WNG, int KC, int NST, int NP>
 struct GemmWs {
     static constexpr int NCW = WMG * WNG, NW = NCW + NP;
@@ -866,58 +955,8 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
 
     if (wave >= G::NCW) {
         // ---------------- producers ----------------
-        const int p = wave - G::NCW;
-        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)a.w, 0, (int)((size_t)a.OC * a.KH * a.KW * a.IC * 2), 0x00020000);
-        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2), 0x00020000);
-        // this lane's slot of each of its instructions: LDS row r, 16-byte
-        // slot s holds chunk swz(r, s) of weight row oc0 + r ([OC][KH][KW][IC])
-        // or of output pixel p0 + r - BM.  A weight slot keeps its byte
-        // offset at tap 0 / channel 0 (-1: past the weights, reads zeros); a
-        // pixel slot its clip's first input row b * H (-1: past the pixels)
-        // and the tap-0 input row / column ih0, iw0 (with the slot's chunk
-        // in the low 4 bits), checked against the map per tap.
-        int off[G::IPP], ih0[G::IPP], iw0[G::IPP];
-        const int HoWo = a.Ho * a.Wo;
-#pragma unroll
-        for (int i = 0; i < G::IPP; ++i) {
-            const int ins = p + NP * i;
-            const int q = ins * 64 + lane, r = q / CPR, c = swz<KC>(r, q - r * CPR);
-            ih0[i] = iw0[i] = 0;
-            if (r < BM) {
-                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.KH * a.KW * a.IC + c * 8) * 2 : -1;
-            } else {
-                const int P = p0 + r - BM;
-                off[i] = -1;
-                if (P < a.npix) {
-                    const int b = P / HoWo, rem = P - b * HoWo;
-                    const int oh = rem / a.Wo, ow = rem - oh * a.Wo;
-                    off[i] = b * a.H;
-                    ih0[i] = oh * a.sh - a.ph;
-                    iw0[i] = ow * a.sw - a.pw;
-                }
-                iw0[i] = iw0[i] * 16 + c;
-            }
-        }
-        auto issue = [&](int k) {
-            uint8_t* const dst = smem + (k % NST) * G::STAGE;
-            const int tap = k / ncpt, c0 = (k - tap * ncpt) * KC;
-            const int kh = tap / a.KW, kw = tap - kh * a.KW;
-#pragma unroll
-            for (int i = 0; i < G::IPP; ++i) {
-                const int ins = p + NP * i;
-                if (ins * (64 / CPR) < BM) {   // wave-uniform: the weight rows fill whole instructions
-                    const uint32_t o = off[i] < 0 ? kOOB : (uint32_t)(off[i] + (tap * a.IC + c0) * 2);
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
-                } else {
-                    const int ih = ih0[i] + kh * a.dh, iw = (iw0[i] >> 4) + kw * a.dw, c = iw0[i] & 15;
-                    const bool in = off[i] >= 0 && (unsigned)ih < (unsigned)a.H && (unsigned)iw < (unsigned)a.W;
-                    const uint32_t o = in ? (uint32_t)((((off[i] + ih) * a.W + iw) * a.xs + c0 + c * 8) * 2) : kOOB;
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
-                }
-            }
-        };
+        GemmFeed<BM, KC, G::IPP, NP> feed(a, wave - G::NCW, lane, p0, oc0);
+        auto issue = [&](int k) { feed.issue(a, smem + (k % NST) * G::STAGE, k, ncpt); };
 #pragma unroll
         for (int k = 0; k < NST - 1; ++k)
             if (k < nk) issue(k);
@@ -2758,8 +2797,9 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     // and the LDS-DMA kernel's B fragments (up to 1024 input channels: their
     // scale / shift stage in LDS)
     if (a.in_scale && (t.halo || t.rw_ic || t.band_w || a.IC > 1024)) return false;
-    // reflect padding lives in the LDS-DMA kernel's pixel offsets
-    if (a.reflect && (igemm_tile(idx) || t.halo)) return false;
+    // reflect padding lives in the LDS-DMA kernel's pixel offsets (one row
+    // of at most 32 taps)
+    if (a.reflect && (igemm_tile(idx) || t.halo || a.KH * a.KW > 32)) return false;
     // q8_0 weights are dequantised in the register-staged kernel's weight loads
     if (a.wq && !igemm_tile(idx)) return false;
     // segment sums live in the staged epilogue of the register-staged
@@ -2841,21 +2881,24 @@ int pick_tile(const ConvArgs& a) {
         // measured no faster and stay on the LDS-DMA tile).  The
         // 128 x 384 tile where it covers a 9536-pixel map in one round of
         // workgroups, 128 x 288 for the 25472-pixel TDNNs (712 workgroups:
-        // 2.8 rounds where 128 x 256 makes 3.1), 256 x 128 for 768 outputs,
-        // 128 x 256 from 2048 input channels
+        // 2.8 rounds where 128 x 256 makes 3.1), 256 x 128 for 768 outputs
+        // and from 2048 input channels (the MFA's 3072 -> 1536: 272 -> 253
+        // us against 128 x 256 once the producers' loads went out
+        // branch-free), 128 x 256 for narrower outputs from 2048 channels
         if (a.KW == 1 && tile_fits(kTiles[81], a)) {
             if (a.OC == 768 && a.IC >= 768) return 83;
             if (a.npix < 16384 && (a.OC == 1024 || a.OC == 2304) && tile_fits(kTiles[82], a)) return 82;
             if (a.npix >= 16384 && a.OC == 1024 && a.IC == 1024 && tile_fits(kTiles[84], a)) return 84;
-            if (a.IC >= 2048) return 81;
+            if (a.IC >= 2048) return a.OC % 256 == 0 ? 83 : 81;
         }
         // the same kernel for wav2vec2's strided feature convs (512 -> 512,
         // 3 / 2 taps, stride 2, exact GELU; 64 x 3 s clips, interleaved
-        // timing): from 64k output pixels the 128 x 256 tile (conv1 .. conv3:
-        // 779 -> 745, 413 -> 404, 200 -> 181 us), 2-tap ones of 16k-32k
-        // pixels the 128 x 384 tile (conv5: 47.2 -> 40.9 us)
-        if (a.sw == 2 && a.KW <= 3 && a.IC == 512 && a.OC == 512 && tile_fits(kTiles[81], a)) {
-            if (a.npix >= 65536) return 81;
+        // timing): from 64k output pixels and under 16k the 256 x 128 tile
+        // (conv1 .. conv3: 617 -> 583, 322 -> 306, 157 -> 148 us against
+        // 128 x 256; conv6: 21.2 us), 2-tap ones of 16k-32k pixels the
+        // 128 x 384 tile (conv5: 34.6 us)
+        if (a.sw == 2 && a.KW <= 3 && a.IC == 512 && a.OC == 512 && tile_fits(kTiles[83], a)) {
+            if (a.npix >= 65536 || a.npix < 16384) return 83;
             if (a.KW == 2 && a.npix >= 16384 && a.npix < 32768 && tile_fits(kTiles[82], a)) return 82;
         }
         // ECAPA's block0 (k = 5 over the 96 padded mel channels, 1024 out) on
