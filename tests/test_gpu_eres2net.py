@@ -430,7 +430,9 @@ def test_split_grouped_layout(case, g):
     tiles = {"3x3_32_16": [70, 14], "3x3_16_16": [71], "1x1_32_64_res": [-1, 16], "1x1_64_32": [-1, 14],
              "3x3_32_32": [72, 14], "3x3_64_32": [73, 74, 14], "1x1_64_128_res": [-1, 39],
              "1x1_128_64": [-1, 15]}[case]
-    outs = []
+    if K == 1:   # the GEMM kernel's tiles where they fit: the LDS-DMA tile's bits
+        tiles += [t for t in (81, 82, 83, 84) if lib.lib().vdk_conv2d_tile_fits_ex(t, d)]
+    outs, raw = [], {}
     for t in tiles:
         if K == 3:
             dy.copy_from(rows)
@@ -442,6 +444,8 @@ def test_split_grouped_layout(case, g):
             got = o[..., :OC].astype(np.float64) + o[..., OC:].astype(np.float64)
         else:
             o = dy.to_array(np.float16, (Bt, H, T, 2 * g * G))
+        raw[t] = o.copy()
+        if not res_case:
             got = _ungroup(o, g0, OC // g, g)
             mask = np.ones(2 * g * G, bool)
             mask[2 * g * g0:2 * g * (g0 + OC // g)] = False
@@ -456,6 +460,51 @@ def test_split_grouped_layout(case, g):
             assert err <= 2e-6
     for o in outs[1:]:
         assert np.abs(o - outs[0]).max() <= 1e-6 * np.abs(outs[0]).max()
+    if K == 1:
+        gemm = [t for t in raw if t >= 81]
+        assert gemm, "no GEMM tile fits"
+        for t in gemm:
+            assert np.array_equal(raw[t], raw[tiles[1]]), f"GEMM tile {t} vs LDS-DMA tile {tiles[1]}"
+
+
+@pytest.mark.parametrize("IC,OC,res", [(64, 128, True), (128, 64, False), (256, 512, True)])
+def test_gemm_ws_split_three_terms_bitwise(IC, OC, res):
+    """Split-f16 1x1 convs with q8_0-style weights f16 does not hold (three
+    MFMA terms: x_hi.w_hi + x_lo.w_hi + x_hi.w_lo, K over [hi | lo | hi]) on
+    the GEMM kernel's tiles: the LDS-DMA tile's bits (same K order), with a
+    split residual, ReLU and the clamp."""
+    rng = np.random.default_rng(IC + OC)
+    Bt, H, T = 2, 20, 333
+    announce(f"gemm split 3-term 1x1 B={Bt} H={H} T={T} {IC}->{OC} res={res}")
+    x = rng.standard_normal((Bt, H, T, IC)).astype(np.float32) * 3
+    w = (rng.standard_normal((OC, IC)) * np.sqrt(2.0 / IC)).astype(np.float32)
+    wh, wl = _split(w)
+    keep = [lib.DeviceBuffer.from_array(np.ascontiguousarray(np.concatenate([wh, wh, wl], axis=1))),
+            lib.DeviceBuffer.from_array(rng.uniform(-0.5, 0.5, OC).astype(np.float32)),
+            lib.DeviceBuffer.from_array(np.concatenate(_split(x), axis=3))]
+    d = lib.ConvDesc()
+    d.x, d.batch, d.H, d.W, d.IC, d.x_stride, d.x_lo = keep[2].ptr, Bt, H, T, IC, 2 * IC, IC
+    d.w, d.OC, d.KH, d.KW = keep[0].ptr, OC, 1, 1
+    d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+    d.bias, d.act, d.clamp_hi, d.split = keep[1].ptr, lib.ACT_RELU, 20.0, 1
+    if res:
+        keep.append(lib.DeviceBuffer.from_array(np.concatenate(_split(
+            rng.standard_normal((Bt, H, T, OC)).astype(np.float32)), axis=3)))
+        d.residual, d.res_stride, d.res_lo = keep[-1].ptr, 2 * OC, OC
+    dy = lib.DeviceBuffer(Bt * H * T * 2 * OC * 2)
+    d.y, d.y_stride, d.y_lo = dy.ptr, 2 * OC, OC
+    outs = {}
+    for t in (39, 15, 81, 82, 83, 84):
+        d.tile = t
+        if not lib.lib().vdk_conv2d_tile_fits_ex(t, d):
+            continue
+        lib.check(lib.lib().vdk_conv2d_ex(d, None))
+        lib.check(lib.lib().vdk_synchronize())
+        outs[t] = dy.to_array(np.uint16, (Bt, H, T, 2 * OC))
+    ref = 39 if 39 in outs else 15
+    assert ref in outs and sum(t >= 81 for t in outs) >= 2, sorted(outs)
+    for t, o in outs.items():
+        assert np.array_equal(o, outs[ref]), f"tile {t}"
 
 
 # ------------------------------------------------------------------ end to end

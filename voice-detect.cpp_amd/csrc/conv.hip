@@ -857,22 +857,26 @@ void launch_dma(const ConvArgs& a, hipStream_t s) {
 template <int BM, int KC, int IPW, int NPW>
 struct GemmFeed {
     static constexpr int CPR = KC / 8;
-    int p, lane;
-    int off[IPW], ih0[IPW], iw0[IPW];
+    int p, lane, icw;
+    int off[IPW], ih0[IPW], iw0[IPW], cof[IPW];
     __amdgpu_buffer_rsrc_t wr, xr;
     __device__ __forceinline__ GemmFeed(const ConvArgs& a, int p_, int lane_, int p0, int oc0) : p(p_), lane(lane_) {
-        wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)((size_t)a.OC * a.KH * a.KW * a.IC * 2),
+        // split-f16 (1x1 only): K per tap runs over [x_hi . w_hi | x_lo . w_hi | x_hi . w_lo]
+        icw = a.split ? (a.split == 2 ? 2 : 3) * a.IC : a.IC;
+        const int xext = ((a.IC >> a.xgl) - 1) * a.xgs + (1 << a.xgl);   // a pixel's channels in one plane
+        wr = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (int)((size_t)a.OC * a.KH * a.KW * icw * 2),
                                                0x00020000);
-        xr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + a.IC) * 2),
-                                               0x00020000);
+        xr = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)a.x, 0, (int)(((size_t)(a.npix_in - 1) * a.xs + xext + (a.split ? a.x_lo : 0)) * 2), 0x00020000);
         const int HoWo = a.Ho * a.Wo;
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
             const int ins = p + NPW * i;
             const int q = ins * 64 + lane, r = q / CPR, c = swz<KC>(r, q - r * CPR);
             ih0[i] = iw0[i] = 0;
+            cof[i] = chan_off(c * 8, a.xgl, a.xgs);   // the slot's 8 channels within a chunk
             if (r < BM) {
-                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.KH * a.KW * a.IC + c * 8) * 2 : -1;
+                off[i] = oc0 + r < a.OC ? ((oc0 + r) * a.KH * a.KW * icw + c * 8) * 2 : -1;
             } else {
                 const int P = p0 + r - BM;
                 off[i] = -1;
@@ -883,17 +887,19 @@ struct GemmFeed {
                     ih0[i] = oh * a.sh - a.ph;
                     iw0[i] = ow * a.sw - a.pw;
                 }
-                iw0[i] = iw0[i] * 16 + c;
             }
         }
     }
-    // This wave's instructions of chunk k (tap k / ncpt, channels from
-    // (k % ncpt) * KC) into the stage at dst: branch-free (selects of
-    // out-of-range offsets, the weight / pixel split fixed at compile time),
-    // so the loads go out back to back.
+    // This wave's instructions of chunk k (tap k / ncpt, K offset (k % ncpt)
+    // * KC) into the stage at dst: branch-free (selects of out-of-range
+    // offsets, the weight / pixel split fixed at compile time), so the loads
+    // go out back to back.  Chunks cover whole channel groups and, split,
+    // lie inside one plane term.
     __device__ __forceinline__ void issue(const ConvArgs& a, uint8_t* dst, int k, int ncpt) const {
         const int tap = k / ncpt, c0 = (k - tap * ncpt) * KC;
         const int kh = tap / a.KW, kw = tap - kh * a.KW;
+        const int term = a.split ? (c0 >= 2 * a.IC ? 2 : (c0 >= a.IC ? 1 : 0)) : 0;
+        const int xc = (term == 1 ? a.x_lo : 0) + chan_off(c0 - term * a.IC, a.xgl, a.xgs);   // the chunk's first channel
         constexpr int WI = BM * CPR / 64;   // the weight rows' instructions (whole ones)
 #pragma unroll
         for (int i = 0; i < IPW; ++i) {
@@ -902,12 +908,12 @@ struct GemmFeed {
             // split evenly over the feeding waves (ins < WI iff i < WI / NPW)
             const bool wrow = WI % NPW == 0 ? i < WI / NPW : ins < WI;
             if (wrow) {
-                const uint32_t o = off[i] < 0 ? kOOB : (uint32_t)(off[i] + (tap * a.IC + c0) * 2);
+                const uint32_t o = off[i] < 0 ? kOOB : (uint32_t)(off[i] + (tap * icw + c0) * 2);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(dst + ins * 1024), 16, o, 0, 0, 0);
             } else {
-                const int ih = ih0[i] + kh * a.dh, iw = (iw0[i] >> 4) + kw * a.dw, c = iw0[i] & 15;
+                const int ih = ih0[i] + kh * a.dh, iw = iw0[i] + kw * a.dw;
                 const bool in = off[i] >= 0 && (unsigned)ih < (unsigned)a.H && (unsigned)iw < (unsigned)a.W;
-                const uint32_t pos = (uint32_t)((((off[i] + ih) * a.W + iw) * a.xs + c0 + c * 8) * 2);
+                const uint32_t pos = (uint32_t)((((off[i] + ih) * a.W + iw) * a.xs + xc + cof[i]) * 2);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(dst + ins * 1024), 16, in ? pos : kOOB, 0, 0,
                                                          0);
             }
@@ -941,7 +947,8 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
     int ptile, otile;
     tile_ids(ptile, otile);
     const int p0 = ptile * BN, oc0 = otile * BM;
-    const int ncpt = a.IC / KC;        // chunks per tap
+    // chunks per tap (split-f16: over the [hi | lo | hi] plane terms)
+    const int ncpt = (a.split ? (a.split == 2 ? 2 : 3) * a.IC : a.IC) / KC;
     const int nk = a.KH * a.KW * ncpt; // K = taps x input channels, taps outermost
 
     float16v acc[TM][TN];
@@ -2811,9 +2818,11 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     // take the register-staged kernel
     if (a.KH * a.KW > 32 && a.KH != 1 && !igemm_tile(idx)) return false;
     if (t.sp_ic) return a.IC == t.sp_ic && a.OC == t.bm && split_epilogue(a);
+    // the GEMM kernel: split-f16 inputs for 1x1 convs only (the plane terms
+    // are consecutive chunks of one tap), channel groups whole per chunk
     if (t.gemm)
-        return !a.split && !a.in_scale && !a.reflect && !a.wq && !a.segsum && a.xgs == (1 << a.xgl) &&
-               a.IC % t.kc == 0 && a.xs % 8 == 0;
+        return (!a.split || a.KH * a.KW == 1) && !a.in_scale && !a.reflect && !a.wq && !a.segsum &&
+               t.kc % (1 << a.xgl) == 0 && a.IC % t.kc == 0 && a.xs % 8 == 0 && (!a.split || a.x_lo % 8 == 0);
     // 16-channel group strides: the LDS-DMA kernel's offsets and the shared store
     if ((a.xgs != (1 << a.xgl) || a.ygs != (1 << a.ygl)) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w))
         return false;

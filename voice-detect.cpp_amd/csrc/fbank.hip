@@ -11,7 +11,8 @@
 // Layout: one wavefront per frame, several frames per wavefront in turn (the
 // next frame's samples in flight during the current one), 4 wavefronts per
 // workgroup; the 512-point FFT is register resident (radix 8, two LDS
-// exchanges).  A workgroup's log-mel values collect in an LDS tile and leave
+// exchanges) and transforms two frames at once (one as the real, one as the
+// imaginary part; their spectra separated through the mirror bins).  A workgroup's log-mel values collect in an LDS tile and leave
 // as runs of consecutive frames per mel row, and the workgroups of a clip run
 // on one XCD, so each output line is written once through one L2.  CMN: the
 // frames pass also writes each workgroup's per-mel sums, a small kernel adds
@@ -368,22 +369,21 @@ __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, 
         }
     };
     const int tw0 = t0 + wave * fpw;               // this wave's frames: tw0 .. tw0 + fpw - 1
-    float xs[8];
-    if (tw0 < p.T) load(tw0, xs);
-    for (int f = 0; f < fpw; ++f) {
-        const int t = tw0 + f;
-        if (t >= p.T) break;                       // uniform per wavefront
-        float xn[8];
-        if (f + 1 < fpw && t + 1 < p.T) load(t + 1, xn);   // the next frame's samples, in flight meanwhile
-        // DC removal with a double sum (src/fbank.cpp:170-174)
+    // Frames go through the FFT in pairs: frame t as the real part and frame
+    // t + 1 as the imaginary part of one complex 512-point input z, so
+    // Z = A + iB with A, B the frames' spectra, and with m = (512 - k) mod 512
+    //   A[k] = (Z[k] + conj Z[m]) / 2,   B[k] = (Z[k] - conj Z[m]) / 2i
+    // (A and B are Hermitian): one FFT per two frames.  A pair past the
+    // wave's last frame (or the clip's) runs with B = 0 and drops its output.
+    // DC removal, pre-emphasis and window of one frame's samples
+    // (src/fbank.cpp:170-183): y[j] for sample n = lane + 64 j
+    auto prep = [&](const float* xs, double* y) {
         double s = 0.0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) s += (double)xs[j];
         s = wave_sum(s);
         const float mean = (float)(s / p.win);
-        // pre-emphasis (replicate at n = 0) and povey window (src/fbank.cpp:176-183);
         // sample n - 1 is lane - 1's value, or lane 63's of the previous j
-        cplx v[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int n = lane + 64 * j;
@@ -391,15 +391,35 @@ __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, 
             const float wrap =
                 j > 0 ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xs[j > 0 ? j - 1 : 0]), 63)) : xs[0];
             const float prev_raw = lane > 0 ? up : wrap;
-            double y = 0.0;
+            y[j] = 0.0;
             if (n < p.win) {
                 const float cur = xs[j] - mean;
                 const float prev = prev_raw - mean;
                 const float e = cur - p.preemph * prev;
-                y = (double)(float)((double)e * win[j]);
+                y[j] = (double)(float)((double)e * win[j]);
             }
-            v[j] = {y, 0.0};
         }
+    };
+    const int tend = tw0 + fpw < p.T ? tw0 + fpw : p.T;   // this wave's frames end here
+    float xa[8], xb[8];
+    if (tw0 < tend) load(tw0, xa);
+    if (tw0 + 1 < tend) load(tw0 + 1, xb);
+    for (int t = tw0; t < tend; t += 2) {          // uniform per wavefront
+        const bool two = t + 1 < tend;
+        float na[8], nb[8];                        // the next pair's samples, in flight meanwhile
+        if (t + 2 < tend) load(t + 2, na);
+        if (t + 3 < tend) load(t + 3, nb);
+        double ya[8], yb[8];
+        prep(xa, ya);
+        if (two) {
+            prep(xb, yb);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) yb[j] = 0.0;
+        }
+        cplx v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = {ya[j], yb[j]};
         // pass 1: 8-point DFT over b, twiddle W512^(a c); store row c, column a
         dft8(v);
 #pragma unroll
@@ -425,7 +445,7 @@ __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, 
         dft8(v);
 #pragma unroll
         for (int d0 = 0; d0 < 8; ++d0) v[d0] = cmul(v[d0], tw2[d0 * 8 + a0]);
-        // pass 3: lane (c, d0) gathers a0, DFT over a0 -> d1: X[c + 8 d0 + 64 d1]
+        // pass 3: lane (c, d0) gathers a0, DFT over a0 -> d1: Z[c + 8 d0 + 64 d1]
         const int d0 = a0;
         {
             cplx u[8];
@@ -445,25 +465,66 @@ __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, 
             for (int q = 0; q < 8; ++q) v[q] = u[q];
         }
         dft8(v);
-        // power spectrum |X_k|^2 for k <= 256
+        // Z in natural order through the buffer (real parts, then imaginary
+        // parts), each lane reading bins k = lane + 64 j (j < 4, and 256 for
+        // lane 0) and their mirrors m = 512 - k; then the two power spectra
+        // |A[k]|^2 = ((Zr_k + Zr_m)^2 + (Zi_k - Zi_m)^2) / 4 and
+        // |B[k]|^2 = ((Zi_k + Zi_m)^2 + (Zr_k - Zr_m)^2) / 4 for k <= 256.
+        double zr[5], zrm[5], zi[5], zim[5];
+        auto zidx = [](int k) { return k + (k >> 6); };   // rows of 64 padded by one: lanes of a write spread over banks
 #pragma unroll
-        for (int d1 = 0; d1 < 8; ++d1) {
-            const int k = cl + 8 * d0 + 64 * d1;
-            if (k <= 256) ps[k] = v[d1].r * v[d1].r + v[d1].i * v[d1].i;
+        for (int d1 = 0; d1 < 8; ++d1) xch[zidx(cl + 8 * d0 + 64 * d1)] = v[d1].r;
+        wave_sync();
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const int k = j < 4 ? lane + 64 * j : 256;
+            zr[j] = xch[zidx(k)];
+            zrm[j] = xch[zidx((512 - k) & 511)];
+        }
+        wave_sync();
+#pragma unroll
+        for (int d1 = 0; d1 < 8; ++d1) xch[zidx(cl + 8 * d0 + 64 * d1)] = v[d1].i;
+        wave_sync();
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const int k = j < 4 ? lane + 64 * j : 256;
+            zi[j] = xch[zidx(k)];
+            zim[j] = xch[zidx((512 - k) & 511)];
+        }
+        wave_sync();
+        double* const psa = ps;                    // [257]
+        double* const psb = ps + 288;              // [257]
+#pragma unroll
+        for (int j = 0; j < 5; ++j) {
+            const int k = j < 4 ? lane + 64 * j : 256;
+            if (j < 4 || lane == 0) {
+                const double ar = 0.5 * (zr[j] + zrm[j]), ai = 0.5 * (zi[j] - zim[j]);
+                const double br = 0.5 * (zi[j] + zim[j]), bi = 0.5 * (zr[j] - zrm[j]);
+                psa[k] = ar * ar + ai * ai;
+                psb[k] = br * br + bi * bi;
+            }
         }
         wave_sync();
         float* trow = tile + (t - t0) * pitch;
         for (int m = lane; m < p.n_mels; m += 64) {
-            double e = 0.0;
+            double ea = 0.0, eb = 0.0;
             const int st = mel_start[m], n = mel_len[m];
             const double* w = mel_w + mel_off[m];
-            for (int k = 0; k < n; ++k) e += w[k] * ps[st + k];
+            for (int k = 0; k < n; ++k) {
+                const double wk = w[k];
+                ea += wk * psa[st + k];
+                eb += wk * psb[st + k];
+            }
             const double fl = (double)FLT_EPSILON;
-            trow[m] = (float)log(e > fl ? e : fl);
+            trow[m] = (float)log(ea > fl ? ea : fl);
+            if (two) trow[pitch + m] = (float)log(eb > fl ? eb : fl);
         }
         wave_sync();
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xs[j] = xn[j];
+        for (int j = 0; j < 8; ++j) {
+            xa[j] = na[j];
+            xb[j] = nb[j];
+        }
     }
     __syncthreads();
     const int nf = p.T - t0 < F ? p.T - t0 : F;
@@ -607,14 +668,19 @@ void fbank_run(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pc
     p.n_samples = n_samples;
     p.preemph = c.preemph;
     p.waves = c.n_fft <= 512 ? kFbMaxWaves : 2;
+    const bool radix8 = c.n_fft == 512 && c.win_length <= 512;
     // frames per wavefront: enough to amortise the table copy, while
     // keeping >= ~4 workgroups per CU at batch 64
     int fpw = p.T >= 256 ? 4 : (p.T >= 64 ? 2 : 1);
+    // the 512-point path transforms frames in pairs (2j, 2j + 1) of the clip:
+    // an even count per wavefront keeps every pair in one wavefront, so a
+    // frame's bits never depend on the batch
+    const int min_fpw = radix8 ? 2 : 1;
+    fpw = fpw < min_fpw ? min_fpw : fpw;
     // small batches: fewer frames per wavefront until the launch covers
     // the CUs (each frame's arithmetic is the same whatever the grouping)
-    while (fpw > 1 && (long)batch * cdiv(p.T, p.waves * fpw) < 256) fpw /= 2;
+    while (fpw > min_fpw && (long)batch * cdiv(p.T, p.waves * fpw) < 256) fpw /= 2;
     const int gc = cdiv(p.T, p.waves * fpw);
-    const bool radix8 = c.n_fft == 512 && c.win_length <= 512;
     const size_t per_wave = radix8 ? (size_t)8 * kX1 * sizeof(double)
                                    : (size_t)(2 * c.n_fft + c.n_fft / 2) * sizeof(double);
     const size_t tile = radix8 ? (size_t)p.waves * fpw * (c.n_mels + 1) * sizeof(float) : 0;
