@@ -18,6 +18,7 @@
 // frames pass also writes each workgroup's per-mel sums, a small kernel adds
 // them into the per-clip means, and either a coalesced pass subtracts them or
 // the consumer of the features does as it loads them.
+#include <algorithm>
 #include <cfloat>
 #include <cmath>
 #include <cstring>
@@ -34,7 +35,8 @@ constexpr double kPi = 3.14159265358979323846;
 
 struct FbankDev {
     // byte offsets of the tables inside the table block (copied to LDS)
-    int off_window, off_tw_re, off_tw_im, off_mel_start, off_mel_len, off_mel_off, off_mel_w;
+    int off_window, off_tw_re, off_tw_im, off_mel_start, off_mel_len, off_mel_off, off_mel_w, off_mel_lane;
+    int mel_q;              // mels per lane in the mel_lane table (512-point path)
     int n_mels, n_fft, log2n, pow2, win, hop, T, n_samples;
     int waves;              // frames processed concurrently per workgroup (one per wavefront)
     float preemph;
@@ -51,9 +53,35 @@ struct FbankOut {
 };
 
 struct TableLayout {
-    size_t window, tw_re, tw_im, mel_start, mel_len, mel_off, mel_w, total;
+    size_t window, tw_re, tw_im, mel_start, mel_len, mel_off, mel_lane, mel_w, total;
     int nnz;
 };
+
+constexpr int kMelQ = 8;   // at most this many mels per lane in the mel_lane table
+
+// The mel bins of the 512-point path split over the 64 lanes of a wavefront
+// by filter length (longest first, each to the lane with the least work so
+// far), so no lane runs far more filter taps than the others: table
+// [kMelQ][64] of mel indices, -1 past a lane's list; returns the longest list.
+int mel_lanes(const std::vector<int>& len, std::vector<int>& lane_tab) {
+    const int n = (int)len.size();
+    std::vector<int> order(n), load(64, 0), count(64, 0);
+    for (int m = 0; m < n; ++m) order[m] = m;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return len[a] > len[b]; });
+    lane_tab.assign(kMelQ * 64, -1);
+    int q = 0;
+    for (int m : order) {
+        int best = 0;
+        for (int l = 1; l < 64; ++l)
+            if (load[l] + count[l] < load[best] + count[best]) best = l;   // + 1 per mel: its log and store
+        require(count[best] < kMelQ, "fbank: too many mel bins for the 512-point path");
+        lane_tab[count[best] * 64 + best] = m;
+        load[best] += len[m];
+        ++count[best];
+        q = count[best] > q ? count[best] : q;
+    }
+    return q;
+}
 
 double mel_scale(double f) { return 1127.0 * std::log(1.0 + f / 700.0); }
 
@@ -103,6 +131,7 @@ TableLayout layout(const vdk_fbank_cfg& c, int nnz) {
     t.mel_start = o; o = al(o + sizeof(int) * c.n_mels);
     t.mel_len = o;   o = al(o + sizeof(int) * c.n_mels);
     t.mel_off = o;   o = al(o + sizeof(int) * c.n_mels);
+    t.mel_lane = o;  o = al(o + sizeof(int) * kMelQ * 64);
     t.mel_w = o;     o = al(o + sizeof(double) * (nnz > 0 ? nnz : 1));
     t.total = o;
     t.nnz = nnz;
@@ -328,6 +357,7 @@ __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, 
     const int* mel_start = reinterpret_cast<const int*>(tab + p.off_mel_start - mel0);
     const int* mel_len = reinterpret_cast<const int*>(tab + p.off_mel_len - mel0);
     const int* mel_off = reinterpret_cast<const int*>(tab + p.off_mel_off - mel0);
+    const int* mel_lane = reinterpret_cast<const int*>(tab + p.off_mel_lane - mel0);
     const double* mel_w = reinterpret_cast<const double*>(tab + p.off_mel_w - mel0);
 
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -505,8 +535,14 @@ __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, 
             }
         }
         wave_sync();
+        // mel sums in the reference's order (src/fbank.cpp:187-191), each lane
+        // over its mels from the length-balanced table; the log of the f64
+        // energy rounded to f32 (v_log_f32, within a few f32 ulps of the f64
+        // log rounded to f32)
         float* trow = tile + (t - t0) * pitch;
-        for (int m = lane; m < p.n_mels; m += 64) {
+        for (int q = 0; q < p.mel_q; ++q) {
+            const int m = mel_lane[q * 64 + lane];
+            if (m < 0) continue;
             double ea = 0.0, eb = 0.0;
             const int st = mel_start[m], n = mel_len[m];
             const double* w = mel_w + mel_off[m];
@@ -516,8 +552,9 @@ __global__ __launch_bounds__(kFbMaxWaves * 64) void fbank512_kernel(FbankDev p, 
                 eb += wk * psb[st + k];
             }
             const double fl = (double)FLT_EPSILON;
-            trow[m] = (float)log(ea > fl ? ea : fl);
-            if (two) trow[pitch + m] = (float)log(eb > fl ? eb : fl);
+            constexpr float kLn2 = 0.693147180559945309f;
+            trow[m] = __builtin_amdgcn_logf((float)(ea > fl ? ea : fl)) * kLn2;
+            if (two) trow[pitch + m] = __builtin_amdgcn_logf((float)(eb > fl ? eb : fl)) * kLn2;
         }
         wave_sync();
 #pragma unroll
@@ -617,6 +654,11 @@ extern "C" int vdk_fbank_tables_fill(const vdk_fbank_cfg* cfg, void* d_tables) {
         std::memcpy(host.data() + L.mel_start, st.data(), sizeof(int) * c.n_mels);
         std::memcpy(host.data() + L.mel_len, ln.data(), sizeof(int) * c.n_mels);
         std::memcpy(host.data() + L.mel_off, of.data(), sizeof(int) * c.n_mels);
+        if (c.n_mels <= kMelQ * 64) {
+            std::vector<int> lanes;
+            mel_lanes(ln, lanes);
+            std::memcpy(host.data() + L.mel_lane, lanes.data(), sizeof(int) * lanes.size());
+        }
         if (!w.empty()) std::memcpy(host.data() + L.mel_w, w.data(), sizeof(double) * w.size());
         VDK_HIP(hipMemcpy(d_tables, host.data(), L.total, hipMemcpyHostToDevice));
     });
@@ -657,6 +699,8 @@ void fbank_run(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pc
     p.off_mel_len = (int)L.mel_len;
     p.off_mel_off = (int)L.mel_off;
     p.off_mel_w = (int)L.mel_w;
+    p.off_mel_lane = (int)L.mel_lane;
+    p.mel_q = 0;
     p.n_mels = c.n_mels;
     p.n_fft = c.n_fft;
     p.pow2 = (c.n_fft & (c.n_fft - 1)) == 0;
@@ -668,7 +712,11 @@ void fbank_run(const vdk_fbank_cfg* cfg, const void* d_tables, const float* d_pc
     p.n_samples = n_samples;
     p.preemph = c.preemph;
     p.waves = c.n_fft <= 512 ? kFbMaxWaves : 2;
-    const bool radix8 = c.n_fft == 512 && c.win_length <= 512;
+    const bool radix8 = c.n_fft == 512 && c.win_length <= 512 && c.n_mels <= kMelQ * 64;
+    if (radix8) {
+        std::vector<int> lanes;
+        p.mel_q = mel_lanes(ln, lanes);
+    }
     // frames per wavefront: enough to amortise the table copy, while
     // keeping >= ~4 workgroups per CU at batch 64
     int fpw = p.T >= 256 ? 4 : (p.T >= 64 ? 2 : 1);
