@@ -424,3 +424,45 @@ def test_linear1_segment_sums_feed_cam_local(batch, T, c_in):
         outs.append(dy.to_array(np.float16, (batch, T, G)))
     assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
     assert not nxt.to_array(np.float64, (batch, nseg, BC)).any()
+
+
+@pytest.mark.parametrize("batch,T,c_in", [(B, TP, 320), (B, TP, 1024), (3, 257, 160), (8, 149, 288),
+                                          (8, 49, 160), (16, 101, 256), (12, 3, 128)])
+def test_linear1_tiles_bitwise(batch, T, c_in):
+    """linear1 (BN + ReLU prologue, bias, ReLU, segment sums) on the GEMM
+    kernel's narrow tiles with producer / compute waves: the register-staged
+    tiles' bits, outputs and f64 segment sums alike (same operand rounding,
+    K order and exact sums), including pixel tiles that reach three
+    segments."""
+    rng = np.random.default_rng(11 * T + c_in)
+    L = lib.lib()
+    BC, SEG, CMAX = 128, 100, 1056
+    nseg = (T + SEG - 1) // SEG
+    announce(f"campp linear1 tiles B={batch} T'={T} c_in={c_in}")
+    dense = rng.standard_normal((batch, T, CMAX), dtype=np.float32).astype(np.float16)
+    s1 = (rng.random(c_in, dtype=np.float32) + 0.5).astype(np.float32)
+    t1 = (rng.standard_normal(c_in, dtype=np.float32) * 0.2).astype(np.float32)
+    w = (rng.standard_normal((BC, c_in), dtype=np.float32) / np.sqrt(c_in)).astype(np.float16)
+    bias = (rng.standard_normal(BC, dtype=np.float32) * 0.1).astype(np.float32)
+    dd, ds1, dt1, dw, db = (lib.DeviceBuffer.from_array(a) for a in (dense, s1, t1, w, bias))
+    outs = {}
+    for tile in (63, 80, 85, 86, 87, 88):
+        d = lib.ConvDesc()
+        d.x, d.batch, d.H, d.W, d.IC, d.x_stride = dd.ptr, batch, 1, T, c_in, CMAX
+        d.w, d.OC, d.KH, d.KW = dw.ptr, BC, 1, 1
+        d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+        d.bias, d.act = db.ptr, lib.ACT_RELU
+        d.in_scale, d.in_shift = ds1.ptr, dt1.ptr
+        seg = lib.DeviceBuffer.from_array(np.zeros((batch, nseg, BC), dtype=np.float64))
+        d.seg_sum, d.seg_len = seg.ptr, SEG
+        dh = lib.DeviceBuffer(batch * T * BC * 2)
+        d.y, d.y_stride, d.tile = dh.ptr, BC, tile
+        if not L.vdk_conv2d_tile_fits_ex(tile, d):
+            continue
+        lib.check(L.vdk_conv2d_ex(d, None))
+        _sync()
+        outs[tile] = (dh.to_array(np.uint16, (batch, T, BC)), seg.to_array(np.float64, (batch, nseg, BC)))
+    assert 63 in outs and sum(t >= 85 for t in outs) >= 3, sorted(outs)
+    for t, (h, sg) in outs.items():
+        assert np.array_equal(h, outs[63][0]), f"tile {t} outputs"
+        assert np.array_equal(sg, outs[63][1]), f"tile {t} segment sums"

@@ -935,15 +935,28 @@ struct GemmWs {
     static_assert(IPP * (NST - 2) <= 60, "vmcnt range");
 };
 
-template <int BM, int BN, int WMG, int WNG, int KC, int NST, int NP>
+// PRO: the input prologue relu(x * in_scale + in_shift) of 1x1 convs (CAM++'s
+// linear1), applied to the B fragments at their k-step with the scale /
+// shift staged in LDS, rounded to f16 as the operand like the other kernels'
+// prologues.  SEGS: the staged epilogue's segment sums of the stored outputs.
+template <int BM, int BN, int WMG, int WNG, int KC, int NST, int NP, bool PRO = false, bool SEGS = false>
 __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs a) {
     using G = GemmWs<BM, BN, WMG, WNG, KC, NST, NP>;
     constexpr int TM = G::TM, TN = G::TN, RB = G::RB, CPR = G::CPR;
     constexpr int SMEM_E = G::WN * (BM + 4) * 4;   // one epilogue pass of a wave's pixel columns
     constexpr int SMEM = NST * G::STAGE > SMEM_E ? NST * G::STAGE : SMEM_E;
+    constexpr int PRO_MAX = 1024;                  // input channels with a staged prologue
     __shared__ __attribute__((aligned(1024))) uint8_t smem[SMEM];
+    __shared__ __attribute__((aligned(16))) float s_in[PRO ? 2 * PRO_MAX : 4];   // in_scale | in_shift
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if constexpr (PRO) {   // 1x1: chunk k covers input channels k * KC .. (the launch checks IC <= PRO_MAX)
+        for (int c = tid; c < a.IC; c += G::NW * 64) {
+            s_in[c] = a.in_scale[c];
+            s_in[PRO_MAX + c] = a.in_shift[c];
+        }
+        __syncthreads();
+    }
     int ptile, otile;
     tile_ids(ptile, otile);
     const int p0 = ptile * BN, oc0 = otile * BM;
@@ -1006,6 +1019,20 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
 #pragma unroll
             for (int kk = 0; kk < KS; ++kk) {
                 const int cb = kk & 1;
+                if constexpr (PRO) {   // BatchNorm + ReLU of the input channels, as the f16 operand
+                    const int ch = k * KC + kk * 16 + lhalf * 8;
+                    const float4v sc0 = *reinterpret_cast<const float4v*>(s_in + ch);
+                    const float4v sc1 = *reinterpret_cast<const float4v*>(s_in + ch + 4);
+                    const float4v sh0 = *reinterpret_cast<const float4v*>(s_in + PRO_MAX + ch);
+                    const float4v sh1 = *reinterpret_cast<const float4v*>(s_in + PRO_MAX + ch + 4);
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            bf[cb][j][e] = (half_t)fmaxf((float)bf[cb][j][e] * sc0[e] + sh0[e], 0.0f);
+                            bf[cb][j][e + 4] = (half_t)fmaxf((float)bf[cb][j][e + 4] * sc1[e] + sh1[e], 0.0f);
+                        }
+                }
                 if (kk + 1 < KS) load(kk + 1, cb ^ 1);
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
@@ -1019,19 +1046,33 @@ __global__ __launch_bounds__((WMG * WNG + NP) * 64) void gemm_ws_kernel(ConvArgs
                         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
                     }
-                    __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+                    if constexpr (TM * TN > TM + TN)
+                        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
     }
-    stage_epilogue_impl<BM, BN, G::WN, SMEM, G::NW * 64, TM, TN>(a, smem, acc, m_off, n_off, p0, oc0, tid, lane);
+    stage_epilogue_impl<BM, BN, G::WN, SMEM, G::NW * 64, TM, TN, SEGS>(a, smem, acc, m_off, n_off, p0, oc0, tid,
+                                                                       lane);
 }
 
-template <int BM, int BN, int WMG, int WNG, int KC, int NST, int NP>
+// EXT: the tile also runs the prologue / segment-sum variants (CAM++'s linear1).
+template <int BM, int BN, int WMG, int WNG, int KC, int NST, int NP, bool EXT = false>
 void launch_gemm_ws(const ConvArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((gemm_ws_kernel<BM, BN, WMG, WNG, KC, NST, NP>), dim3(cdiv(a.npix, BN), cdiv(a.OC, BM)),
-                       dim3((WMG * WNG + NP) * 64), 0, s, a);
+    const dim3 grid(cdiv(a.npix, BN), cdiv(a.OC, BM)), block((WMG * WNG + NP) * 64);
+    if constexpr (EXT) {
+        if (a.in_scale && a.segsum)
+            hipLaunchKernelGGL((gemm_ws_kernel<BM, BN, WMG, WNG, KC, NST, NP, true, true>), grid, block, 0, s, a);
+        else if (a.in_scale)
+            hipLaunchKernelGGL((gemm_ws_kernel<BM, BN, WMG, WNG, KC, NST, NP, true, false>), grid, block, 0, s, a);
+        else if (a.segsum)
+            hipLaunchKernelGGL((gemm_ws_kernel<BM, BN, WMG, WNG, KC, NST, NP, false, true>), grid, block, 0, s, a);
+        else
+            hipLaunchKernelGGL((gemm_ws_kernel<BM, BN, WMG, WNG, KC, NST, NP>), grid, block, 0, s, a);
+    } else {
+        hipLaunchKernelGGL((gemm_ws_kernel<BM, BN, WMG, WNG, KC, NST, NP>), grid, block, 0, s, a);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -2661,7 +2702,8 @@ struct TileCfg {
     int rw_ic = 0;   // register-weight kernels: exactly IC = rw_ic and OC = bm, plain epilogue
     int band_w = 0;  // band kernels: W <= band_w, OC % 128 == 0, IC % 16 == 0
     int sp_ic = 0;   // split-f16 register-weight kernels: exactly IC = sp_ic and OC = bm, split 2
-    bool gemm = false;   // 1x1 stride-1 GEMM kernels: contiguous channels, no prologue / reflect / q8_0 / segment sums
+    bool gemm = false;   // the GEMM kernel with producer / compute waves: no reflect / q8_0
+    bool gemm_ext = false;   // ... and its prologue / segment-sum variants (1x1, no padding)
 };
 
 // Entries 0-13 are the register-staged kernel (any layout; the only one with
@@ -2675,7 +2717,8 @@ struct TileCfg {
 // the producer / compute band kernel on one-row bands (the same sums in the
 // same order as its 5-row bands, so the same bits, on 5x the workgroups), 80
 // the register-staged 64x64 tile with 64-channel chunks, 81-84 the 1x1 GEMM
-// kernel with producer / compute waves.
+// kernel with producer / compute waves, 85-88 narrow tiles of that kernel
+// with the prologue / segment-sum variants.
 
 // Tile table.  Wave tiles are WM x WN = (bm / waves_m) x (bn / waves_n) with
 // 4 waves per workgroup; entries are selected per layer by pick_tile().
@@ -2765,6 +2808,10 @@ const TileCfg kTiles[] = {
     {128, 384, 32, launch_gemm_ws<128, 384, 2, 4, 32, 4, 4>, false, 0, 0, 0, true},   // 82
     {256, 128, 64, launch_gemm_ws<256, 128, 4, 2, 64, 3, 4>, false, 0, 0, 0, true},   // 83
     {128, 288, 64, launch_gemm_ws<128, 288, 2, 3, 64, 3, 4>, false, 0, 0, 0, true},   // 84
+    {128, 64, 32, launch_gemm_ws<128, 64, 2, 2, 32, 4, 2, true>, false, 0, 0, 0, true, true},   // 85: narrow GEMMs
+    {128, 64, 64, launch_gemm_ws<128, 64, 2, 2, 64, 3, 2, true>, false, 0, 0, 0, true, true},   // 86
+    {128, 32, 32, launch_gemm_ws<128, 32, 4, 1, 32, 4, 2, true>, false, 0, 0, 0, true, true},   // 87
+    {64, 64, 32, launch_gemm_ws<64, 64, 2, 2, 32, 4, 2, true>, false, 0, 0, 0, true, true},     // 88
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -2812,7 +2859,7 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     // segment sums live in the staged epilogue of the register-staged
     // kernel (f16 weights); pixel tiles at most seg_len wide keep most pixels
     // in the two segments the epilogue sums locally
-    if (a.segsum && (!igemm_tile(idx) || a.wq || t.bn > a.seg_len)) return false;
+    if (a.segsum && (!(igemm_tile(idx) || t.gemm_ext) || a.wq || t.bn > a.seg_len)) return false;
     // the LDS-DMA kernels keep one bit per tap in a 32-bit in-image mask, or
     // the in-image tap range for a single row of taps; longer 2-D kernels
     // take the register-staged kernel
@@ -2820,9 +2867,16 @@ bool tile_fits(const TileCfg& t, const ConvArgs& a) {
     if (t.sp_ic) return a.IC == t.sp_ic && a.OC == t.bm && split_epilogue(a);
     // the GEMM kernel: split-f16 inputs for 1x1 convs only (the plane terms
     // are consecutive chunks of one tap), channel groups whole per chunk
-    if (t.gemm)
-        return (!a.split || a.KH * a.KW == 1) && !a.in_scale && !a.reflect && !a.wq && !a.segsum &&
-               t.kc % (1 << a.xgl) == 0 && a.IC % t.kc == 0 && a.xs % 8 == 0 && (!a.split || a.x_lo % 8 == 0);
+    // (prologue / segment sums: the EXT tiles, 1x1 without padding, up to
+    // 1024 input channels, pixel tiles at most seg_len wide)
+    if (t.gemm) {
+        const bool one = a.KH * a.KW == 1 && a.ph == 0 && a.pw == 0;
+        if ((a.in_scale || a.segsum) && !(t.gemm_ext && one && !a.split)) return false;
+        if (a.in_scale && a.IC > 1024) return false;
+        if (a.segsum && t.bn > a.seg_len) return false;
+        return (!a.split || a.KH * a.KW == 1) && !a.reflect && !a.wq && t.kc % (1 << a.xgl) == 0 &&
+               a.IC % t.kc == 0 && a.xs % 8 == 0 && (!a.split || a.x_lo % 8 == 0);
+    }
     // 16-channel group strides: the LDS-DMA kernel's offsets and the shared store
     if ((a.xgs != (1 << a.xgl) || a.ygs != (1 << a.ygl)) && (igemm_tile(idx) || t.halo || t.rw_ic || t.band_w))
         return false;
@@ -2864,6 +2918,12 @@ int pick_tile(const ConvArgs& a) {
         // load round trip) on the 64x64 tile (B=32 x 499 frames: 12.8 / 16.6 /
         // 19.9 -> 12.0 / 15.8 / 19.5 us at 256 / 512 / 768 channels against the
         // 128x64 one), else the 64x64 tile with 32-channel chunks
+        // the GEMM kernel's narrow tiles from 800 channels (B=32 x 499 frames,
+        // interleaved: 800 22.5 -> 21.2 us, 1024 23.5 -> 22.1 us)
+        if (a.IC >= 800 && a.OC == 128 && a.npix < 65536) {
+            if (a.IC % 64 == 0 && tile_fits(kTiles[86], a)) return 86;
+            if (tile_fits(kTiles[85], a)) return 85;
+        }
         if (a.IC >= 256 && a.IC % 64 == 0 && a.OC == 128 && a.npix < 65536 && tile_fits(kTiles[80], a)) return 80;
         if (a.IC % 32 == 0) return bm >= 64 ? (a.npix < 32768 ? 63 : (bm == 128 ? 5 : 2)) : 10;
         return bm == 128 ? 13 : (bm == 64 ? 12 : 11);
