@@ -3016,12 +3016,15 @@ int pick_tile(const ConvArgs& a) {
         if (a.IC == 128 && a.OC == 256 && tile_fits(kTiles[34], a)) return 34;
         if (a.IC == 256 && a.OC == 512 && tile_fits(kTiles[40], a)) return 40;
     }
-    if (a.split && a.KH * a.KW == 1 && a.sh == 1 && a.sw == 1) {   // ERes2Net's split-f16 1x1s (same sweep)
+    if (a.split && a.KH * a.KW == 1 && a.sh == 1 && a.sw == 1) {   // ERes2Net's split-f16 1x1s (same sweep;
+        // the 128 -> 64, 128 -> 256 and 256 -> 512 rules re-swept interleaved
+        // at B=16 x 20 s with three-term weights: 133 -> 129, 125 -> 120 and
+        // 76 -> 64 us)
         if (a.IC == 64 && a.OC == 32) return 61;
-        if (a.IC == 128 && a.OC == 64) return 23;
+        if (a.IC == 128 && a.OC == 64) return 16;
         if (a.IC == 256 && a.OC == 128) return 45;
-        if (a.IC == 128 && a.OC == 256) return 39;
-        if (a.IC == 256 && a.OC == 512) return 51;
+        if (a.IC == 128 && a.OC == 256) return 40;
+        if (a.IC == 256 && a.OC == 512) return 40;
     }
     if (is_s1_3x3(a) && a.IC == 64 && a.OC == 64 && plain_epilogue(a)) return 66;   // 3-stage ring
     // small batches (5-row bands on under 48 workgroups): one-row bands, the
