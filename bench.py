@@ -292,10 +292,21 @@ def traffic_child(keys):
         d_out = lib.DeviceBuffer(batch * width * 4)
         run = (lambda: ctx.analyze_device_async(d_pcm.ptr, batch, n, d_out.ptr)) if model.get("kind") == "analyze" \
             else (lambda: ctx.embed_device_async(d_pcm.ptr, batch, n, d_out.ptr))
-        for _ in range(1 + TRAFFIC_STEPS):
+        run()                                    # warmup, unmarked
+        ctx.synchronize()
+        # the measured batches with every labelled launch bracketed by marker
+        # dispatches, so the parent can attribute each dispatch to its label
+        ctx.set_profiling(True)
+        ctx.set_profiling_markers(True)
+        for _ in range(TRAFFIC_STEPS):
             run()
         ctx.synchronize()
+        labels = [r[0] for r in ctx.profile()]
+        ctx.set_profiling_markers(False)
+        ctx.set_profiling(False)
         ctx.close()
+        with open(os.environ["VDK_TRAFFIC_LABELS"] + "." + key, "w") as fh:
+            json.dump(labels, fh)
         for _ in range(3):
             lib.check(L.vdk_memcpy_d2d(dst.ptr, src.ptr, nb))
         lib.check(L.vdk_synchronize())
@@ -314,6 +325,7 @@ def traffic_passes(keys):
     env = dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp"))
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         d = tempfile.mkdtemp()
+        env["VDK_TRAFFIC_LABELS"] = os.path.join(d, "labels")
         cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "run", "--",
                sys.executable, os.path.abspath(__file__), "--traffic-child", ",".join(keys)]
         try:
@@ -341,13 +353,44 @@ def traffic_passes(keys):
         factor = (TRAFFIC_COPY_MIB << 20) / float(np.median(cal))
         for key, sg in zip(keys, segs):
             groups = out.setdefault(key, {})
+            marker = lambda row: "profile_marker_kernel" in row["Kernel_Name"]
             for row in sg:
+                if marker(row):
+                    continue
                 g = groups.setdefault((row["Kernel_Name"], int(row["Grid_Size"])),
                                       {"count": 0, "us": 0.0, "FETCH_SIZE": 0.0, "WRITE_SIZE": 0.0})
                 if counter == "FETCH_SIZE":
                     g["count"] += 1
                     g["us"] += (int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3
                 g[counter] += float(row["Counter_Value"]) * 1024.0 * factor
+            # per label: the dispatches between each pair of markers (begin,
+            # end alternate: labelled launches do not nest), in launch order
+            try:
+                labels = json.load(open(env["VDK_TRAFFIC_LABELS"] + "." + key))
+            except (OSError, ValueError):
+                labels = None
+            per_label, i, inside, cur = {}, 0, False, 0.0
+            ok = labels is not None
+            for row in sg:
+                if not ok:
+                    break
+                if marker(row):
+                    if inside:
+                        if i >= len(labels):
+                            ok = False
+                            break
+                        p = per_label.setdefault(labels[i], {"launches": 0, "bytes": 0.0})
+                        p["launches"] += 1
+                        p["bytes"] += cur
+                        i += 1
+                    inside, cur = not inside, 0.0
+                elif inside:
+                    cur += float(row["Counter_Value"]) * 1024.0 * factor
+            if ok and i == len(labels) and not inside:
+                lab = out.setdefault(key + "/labels", {})
+                for name, p in per_label.items():
+                    q = lab.setdefault(name, {"launches": p["launches"]})
+                    q[counter] = p["bytes"]
             out.setdefault("_factors", {})[counter] = round(factor, 4)
     return out
 
@@ -407,16 +450,37 @@ def traffic_table(tr, keys, path):
             lines.append(f"| `{short_kernel_name(name)}` | {grid} | {n / steps:g} | {g['us'] / n:.1f} | "
                          f"{f:.2f} | {w:.2f} | {f + w:.2f} |")
         lines.append("")
+        lab = tr.get(key + "/labels") or {}
+        if lab:
+            lines += ["Per launch class (the dispatches between the marker dispatches around each labelled "
+                      f"launch of the {TRAFFIC_STEPS} measured batches):", "",
+                      "| class | launches / batch | FETCH MB | WRITE MB | HBM MB / launch |", "|---|---:|---:|---:|---:|"]
+            for name, q in sorted(lab.items(), key=lambda kv: -(kv[1].get("FETCH_SIZE", 0) +
+                                                                kv[1].get("WRITE_SIZE", 0))):
+                n = q["launches"]
+                f, w = q.get("FETCH_SIZE", 0.0) / n / 1e6, q.get("WRITE_SIZE", 0.0) / n / 1e6
+                if (f + w) * n / TRAFFIC_STEPS < 1.0:
+                    continue
+                lines.append(f"| `{name}` | {n / TRAFFIC_STEPS:g} | {f:.2f} | {w:.2f} | {f + w:.2f} |")
+            lines.append("")
     with open(path, "w") as fh:
         fh.write("\n".join(lines))
 
 
 def traffic_of(tr, key, launches_per_step, label):
     """Measured HBM bytes per launch of `key`'s dominant class, or (None, why):
-    the (kernel, grid) group with that many launches per step (a conv kernel
-    for a conv class) that takes the most time."""
+    the dispatches between the markers around that label's launches (every
+    kernel and grid the class uses), else the (kernel, grid) group with that
+    many launches per step (a conv kernel for a conv class) that takes the
+    most time."""
     if not tr or "error" in tr:
         return None, (tr or {}).get("error", "traffic not measured")
+    lab = (tr.get(key + "/labels") or {}).get(label)
+    if lab and lab.get("launches") and "FETCH_SIZE" in lab and "WRITE_SIZE" in lab:
+        n = lab["launches"]
+        return {"kernel": f"every dispatch between the markers around the {label} launches", "grid": None,
+                "fetch_bytes": lab["FETCH_SIZE"] / n, "write_bytes": lab["WRITE_SIZE"] / n,
+                "factors": tr.get("_factors")}, None
     groups = tr.get(key)
     if not groups:
         return None, f"no dispatches recorded for {key}"
@@ -524,14 +588,16 @@ def measure(L, key, steps, warmup, cpu_seconds, registry=0, copy_mib=0, b1_reps=
     # included), reported beside `value`, never as it
     host = (lambda: ctx.analyze_pcm(pcm)) if analyze else (lambda: ctx.embed_batch(pcm))
     host()
-    hs = min(steps, 10)
-    t0 = time.perf_counter()
-    for _ in range(hs):
+    times = []
+    for _ in range(max(5, min(steps, 15))):
+        t0 = time.perf_counter()
         host()
-    dt = (time.perf_counter() - t0) / hs
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))   # the median call: one slow host-side call does not move it
     out["host_buffers"] = {"value": round(batch / dt, 2), "unit": unit, "ms_per_step": round(dt * 1e3, 4),
+                           "calls": len(times), "min_ms": round(min(times) * 1e3, 4),
                            "note": ("voicedetect_gpu_analyze_pcm" if analyze else "voicedetect_capi_embed_pcm_batch") +
-                                   ": host PCM in, host results out (PCIe included)"}
+                                   ": host PCM in, host results out (PCIe included), median of the calls"}
     if b1_reps > 0 and not analyze:
         out["batch1"] = batch1_latency(ctx, pcm[0], n, b1_reps)
     if registry > 0 and not analyze:

@@ -40,6 +40,11 @@ int voicedetect_gpu_set_profiling(voicedetect_ctx* ctx, int on);
 /* Same, recording only launches whose name starts with name_prefix (NULL or
  * "": all), so one kernel can be timed with few events in the stream. */
 int voicedetect_gpu_set_profiling_filter(voicedetect_ctx* ctx, int on, const char* name_prefix);
+/* While profiling, bracket every recorded launch with a one-thread marker
+ * dispatch (kernel profile_marker_kernel storing 1 before, 2 after), so a
+ * hardware-counter run that lists dispatches in order can attribute each
+ * dispatch to its record. No counterpart in the reference (a measurement aid). */
+int voicedetect_gpu_set_profiling_markers(voicedetect_ctx* ctx, int on);
 /* Waits, then returns the number of launch records collected since the last
  * read (or -1 on error); records are read with voicedetect_gpu_profile_get. */
 int voicedetect_gpu_profile_collect(voicedetect_ctx* ctx);

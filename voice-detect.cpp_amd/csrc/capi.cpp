@@ -301,6 +301,14 @@ extern "C" int voicedetect_gpu_set_profiling_filter(voicedetect_ctx* ctx, int on
     return 0;
 }
 
+extern "C" int voicedetect_gpu_set_profiling_markers(voicedetect_ctx* ctx, int on) {
+    if (!ctx || !ctx->model) return 1;
+    return run(ctx, [&] {
+        ctx->model->set_profiling_markers(on != 0);
+        return 0;
+    });
+}
+
 extern "C" int voicedetect_gpu_profile_collect(voicedetect_ctx* ctx) {
     if (!ctx || !ctx->model) return -1;
     int n = -1;

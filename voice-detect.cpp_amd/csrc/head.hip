@@ -321,6 +321,20 @@ __global__ __launch_bounds__(64) void l2norm_kernel(const float* x, int dim, flo
 }  // namespace
 }  // namespace vdk
 
+namespace vdk {
+namespace {
+// One vector store of v: a dispatch that counter-collection runs can find by
+// name, bracketing a labelled launch (Model::set_profiling_markers).
+__global__ __launch_bounds__(64) void profile_marker_kernel(int* p, int v) {
+    if (threadIdx.x == 0) p[0] = v;
+}
+}  // namespace
+
+void launch_profile_marker(int* p, int v, hipStream_t s) {
+    hipLaunchKernelGGL(profile_marker_kernel, dim3(1), dim3(64), 0, s, p, v);
+}
+}  // namespace vdk
+
 using namespace vdk;
 
 extern "C" int vdk_tstp_ex(const void* d_x, int x_stride, int x_lo, int batch, int H, int W, int C, float eps,

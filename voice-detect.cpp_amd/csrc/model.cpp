@@ -117,6 +117,7 @@ Model::~Model() {
     for (auto& p : pending_) { (void)hipEventDestroy(p.a); (void)hipEventDestroy(p.b); }
     if (arena_) (void)hipFree(arena_);
     if (fb_tables_) (void)hipFree(fb_tables_);
+    if (prof_marker_) (void)hipFree(prof_marker_);
     if (stream_) (void)hipStreamDestroy(stream_);
 }
 
@@ -333,6 +334,7 @@ void Model::prof_begin(const char* name, double flops, double bytes) {
         return e;
     };
     Pending p{name, flops, bytes, ev(), ev()};
+    if (prof_markers_) launch_profile_marker(prof_marker_, 1, stream_);
     VDK_HIP(hipEventRecord(p.a, stream_));
     pending_.push_back(p);
     prof_open_ = true;
@@ -341,6 +343,7 @@ void Model::prof_begin(const char* name, double flops, double bytes) {
 void Model::prof_end() {
     if (!prof_open_) return;
     VDK_HIP(hipEventRecord(pending_.back().b, stream_));
+    if (prof_markers_) launch_profile_marker(prof_marker_, 2, stream_);
     prof_open_ = false;
 }
 
@@ -522,6 +525,13 @@ void Model::set_profiling(bool on, const std::string& name_prefix) {
     std::lock_guard<std::mutex> lock(mu_);
     profiling_ = on;
     prof_filter_ = name_prefix;
+}
+
+void Model::set_profiling_markers(bool on) {
+    std::lock_guard<std::mutex> lock(mu_);
+    ensure_device();
+    if (on && !prof_marker_) VDK_HIP(hipMalloc(&prof_marker_, 256));
+    prof_markers_ = on;
 }
 
 std::vector<ProfileRecord> Model::take_profile() {

@@ -21,6 +21,9 @@
 
 namespace vdk {
 
+// head.hip: the marker dispatch of Model::set_profiling_markers.
+void launch_profile_marker(int* p, int v, hipStream_t s);
+
 struct ResNetCfg {
     std::string stem_weight, stem_bias;
     std::vector<std::string> conv1_weight, conv1_bias, conv2_weight, conv2_bias, down_weight, down_bias;
@@ -119,6 +122,10 @@ public:
     std::string analyze_json(const std::vector<float>& pcm, int sample_rate);
 
     void set_profiling(bool on, const std::string& name_prefix = std::string());
+    // While profiling: bracket every recorded launch with a one-thread marker
+    // dispatch (profile_marker_kernel), so a counter-collection run can tell
+    // which dispatches belong to which record.
+    void set_profiling_markers(bool on);
     // Waits for the stream and returns the per-launch records since the last call.
     std::vector<ProfileRecord> take_profile();
 
@@ -369,6 +376,8 @@ private:
     bool profiling_ = false;
     std::string prof_filter_;   // record only launches whose name starts with this (empty: all)
     bool prof_open_ = false;    // the last prof_begin recorded a start event
+    bool prof_markers_ = false; // marker dispatches around recorded launches
+    int* prof_marker_ = nullptr;
     struct Pending { std::string name; double flops, bytes; hipEvent_t a, b; };
     std::vector<Pending> pending_;
     std::vector<hipEvent_t> event_pool_;

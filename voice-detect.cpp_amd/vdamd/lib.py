@@ -96,6 +96,7 @@ _SIGS = {
     "voicedetect_gpu_embed_capture": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp, C.POINTER(C.c_int), _vp, _vp]),
     "voicedetect_gpu_set_profiling": (C.c_int, [_vp, C.c_int]),
     "voicedetect_gpu_set_profiling_filter": (C.c_int, [_vp, C.c_int, C.c_char_p]),
+    "voicedetect_gpu_set_profiling_markers": (C.c_int, [_vp, C.c_int]),
     "voicedetect_gpu_profile_collect": (C.c_int, [_vp]),
     "voicedetect_gpu_profile_get": (C.c_int, [_vp, C.c_int, C.c_char_p, C.c_int, C.POINTER(C.c_double),
                                               C.POINTER(C.c_double), C.POINTER(C.c_double)]),
@@ -444,6 +445,10 @@ class Context:
             self.L.voicedetect_gpu_set_profiling_filter(self.ctx, int(on), name_prefix.encode())
         else:
             self.L.voicedetect_gpu_set_profiling(self.ctx, int(on))
+
+    def set_profiling_markers(self, on):
+        if self.L.voicedetect_gpu_set_profiling_markers(self.ctx, int(on)) != 0:
+            raise VdkError(self.last_error())
 
     def profile(self):
         n = self.L.voicedetect_gpu_profile_collect(self.ctx)
