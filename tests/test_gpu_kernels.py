@@ -552,12 +552,15 @@ def test_conv_q8_0_weights_dequantised_in_registers(IC, OC, npix, prologue):
     assert ok, (ratio, rel)
 
 
-@pytest.mark.parametrize("IC,OC,npix", [(320, 128, 15968), (128, 128, 15968), (512, 128, 1000), (96, 32, 777)])
+@pytest.mark.parametrize("IC,OC,npix", [(320, 128, 15968), (128, 128, 15968), (512, 128, 1000), (96, 32, 777),
+                                        (1024, 512, 15968), (512, 256, 4001)])
 def test_conv_input_prologue_every_tile_bitwise(IC, OC, npix):
     """1x1 convs with the BN+ReLU input prologue relu(x * in_scale +
     in_shift): every tile that takes the shape (register-staged: applied on
-    the operand loads; LDS-DMA: applied to the B fragments leaving LDS) gives
-    the same bits, and the oracle's conv of the prologued input agrees."""
+    the operand loads; LDS-DMA and GEMM kernels: applied to the B fragments
+    leaving LDS) gives the same bits, and the oracle's conv of the prologued
+    input agrees; the last two shapes are CAM++'s transits (B=32 x 499
+    frames, and a ragged pixel count)."""
     L = lib.lib()
     rng = np.random.default_rng(3 * IC + OC + npix)
     announce(f"prologue 1x1 IC={IC} OC={OC} npix={npix}")

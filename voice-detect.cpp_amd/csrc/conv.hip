@@ -2812,6 +2812,9 @@ const TileCfg kTiles[] = {
     {128, 64, 64, launch_gemm_ws<128, 64, 2, 2, 64, 3, 2, true>, false, 0, 0, 0, true, true},   // 86
     {128, 32, 32, launch_gemm_ws<128, 32, 4, 1, 32, 4, 2, true>, false, 0, 0, 0, true, true},   // 87
     {64, 64, 32, launch_gemm_ws<64, 64, 2, 2, 32, 4, 2, true>, false, 0, 0, 0, true, true},     // 88
+    {128, 256, 64, launch_gemm_ws<128, 256, 2, 4, 64, 3, 4, true>, false, 0, 0, 0, true, true},   // 89: wide, + prologue
+    {256, 128, 64, launch_gemm_ws<256, 128, 4, 2, 64, 3, 4, true>, false, 0, 0, 0, true, true},   // 90
+    {128, 384, 32, launch_gemm_ws<128, 384, 2, 4, 32, 4, 4, true>, false, 0, 0, 0, true, true},   // 91
 };
 constexpr int kNumTiles = (int)(sizeof(kTiles) / sizeof(kTiles[0]));
 
@@ -2920,6 +2923,11 @@ int pick_tile(const ConvArgs& a) {
         // 128x64 one), else the 64x64 tile with 32-channel chunks
         // the GEMM kernel's narrow tiles from 800 channels (B=32 x 499 frames,
         // interleaved: 800 22.5 -> 21.2 us, 1024 23.5 -> 22.1 us)
+        // CAM++'s 1024 -> 512 transits (B=32 x 499 frames): the GEMM kernel's
+        // 256x128 prologue tile, 55.5 -> 31.8 us (512 -> 256: no gain)
+        if (a.KH * a.KW == 1 && a.IC >= 1024 && a.OC >= 512 && a.OC % 256 == 0 && !a.segsum &&
+            tile_fits(kTiles[90], a))
+            return 90;
         if (a.IC >= 800 && a.OC == 128 && a.npix < 65536) {
             if (a.IC % 64 == 0 && tile_fits(kTiles[86], a)) return 86;
             if (tile_fits(kTiles[85], a)) return 85;
