@@ -2998,13 +2998,18 @@ int pick_tile(const ConvArgs& a) {
         if (a.KW == 3 && a.OC == 32 && a.IC % 32 == 0) return 60;     // CAM++'s gated linear_local
     }
     // CAM++'s FCM: 32 -> 32 convs with a frequency stride (measured in the
-    // model): the 1x1 shortcuts on the 128x32 register-staged tile, the final
-    // 20 -> 10 conv on the narrow 32x64 DMA tile (the wider maps' strided 3x3s
-    // stay on the default)
+    // model): the 1x1 shortcuts and the 40 -> 20 3x3 on the 128x32
+    // register-staged tile, the final 20 -> 10 conv on the narrow 32x64 DMA
+    // tile (the 80 -> 40 3x3 stays on the default)
     if (!a.split && a.IC == 32 && a.OC == 32 && (a.sh != 1 || a.sw != 1)) {
         if (a.KH * a.KW == 1) return 10;
         if (a.H <= 20) return 60;
+        if (a.H <= 40) return 10;   // the second stage's 40 -> 20 conv (B=32 x 10 s: 48.1 -> 43.4 us)
     }
+    // the FCM blocks' stride-1 conv2 (+ the shortcut): the 32-channel
+    // register-weight tile at every batch (B=32 x 10 s, 40 rows: 54.4 -> 45.6 us;
+    // in the model fcm_conv1 + fcm_conv2 0.256 -> 0.219 ms per step)
+    if (!a.split && is_s1_3x3(a) && a.IC == 32 && a.OC == 32 && a.res && tile_fits(kTiles[69], a)) return 69;
     if (a.split && is_s1_3x3(a)) {   // ERes2Net's split-f16 group convs (random-data sweeps)
         // f16-exact weights: the split-f16 register-weight kernel
         if (a.OC == 16 && a.IC == 32 && tile_fits(kTiles[70], a)) return 70;
