@@ -3022,12 +3022,36 @@ int pick_tile(const ConvArgs& a) {
         // on the 16-64-channel layers), 8-row tiles on the 1998-frame maps
         if (a.OC <= 32 && a.IC % 32 == 0 && tile_fits(kTiles[a.W >= 1000 ? 27 : 28], a)) return a.W >= 1000 ? 27 : 28;
         if (a.OC == 64 && a.IC % 32 == 0 && tile_fits(kTiles[30], a)) return 30;
+        // layer 4's 10-row maps: the halo tile (in-model sweep, 41.8 -> 37.7 us)
+        if (a.IC == 128 && a.OC == 128 && a.H <= 10 && tile_fits(kTiles[26], a)) return 26;
         if (a.IC == 128 && a.OC == 128 && tile_fits(kTiles[40], a)) return 40;
     }
     if (a.split && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2) {   // ERes2Net's cross-stage downsamples
         if (a.IC == 64 && a.OC == 128 && tile_fits(kTiles[36], a)) return 36;
         if (a.IC == 128 && a.OC == 256 && tile_fits(kTiles[34], a)) return 34;
         if (a.IC == 256 && a.OC == 512 && tile_fits(kTiles[40], a)) return 40;
+    }
+    if (a.split && a.KH * a.KW == 1) {
+        // ERes2Net's split-f16 1x1s from an in-model sweep (B=16 x 20 s, every
+        // fitting tile timed in place on the model's buffers): the widening /
+        // narrowing convs and the AFF local_att convs
+        auto fit = [&](int t) { return tile_fits(kTiles[t], a) ? t : -1; };
+        int t = -1;
+        if (a.sh == 1 && a.sw == 1) {
+            if (a.IC == 32 && a.OC == 64 && a.split == 2) t = fit(61);              // 37.9 -> 29.4 us
+            else if (a.IC == 32 && a.OC == 128) t = fit(a.H <= 10 ? 61 : 47);      // 31.1 -> 19.3 / 244.8 -> 230.1
+            else if (a.IC == 64 && a.OC == 256) t = fit(47);                       // 162.4 -> 131.9
+            else if (a.IC == 128 && a.OC == 32) t = fit(60);                       // 27.4 -> 23.6
+            else if (a.IC == 256 && a.OC == 32) t = fit(a.H <= 10 ? 60 : 22);      // 25.2 -> 18.3 / 197.0 -> 184.2
+            else if (a.IC == 1024 && a.OC == 128) t = fit(18);                     // 71.5 -> 54.0
+            else if (a.IC == 128 && a.OC == 512) t = fit(47);                      // 85.1 -> 73.4
+            else if (a.IC == 512 && a.OC == 64) t = fit(23);                       // 96.4 -> 91.6
+        } else if (a.sh == 2 && a.sw == 2) {   // the shortcuts' stride-2 1x1s
+            if (a.IC == 128 && a.OC == 256) t = fit(36);                           // 79.5 -> 68.4
+            else if (a.IC == 64 && a.OC == 64) t = fit(16);                        // 89.1 -> 82.5
+            else if (a.IC == 256 && a.OC == 512) t = fit(40);                      // 54.6 -> 50.4
+        }
+        if (t >= 0) return t;
     }
     if (a.split && a.KH * a.KW == 1 && a.sh == 1 && a.sw == 1) {   // ERes2Net's split-f16 1x1s (same sweep;
         // the 128 -> 64, 128 -> 256 and 256 -> 512 rules re-swept interleaved
