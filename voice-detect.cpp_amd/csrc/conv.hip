@@ -2928,6 +2928,8 @@ int pick_tile(const ConvArgs& a) {
         if (a.KH * a.KW == 1 && a.IC >= 1024 && a.OC >= 512 && a.OC % 256 == 0 && !a.segsum &&
             tile_fits(kTiles[90], a))
             return 90;
+        // the 512 -> 256 transit on the 128x64 LDS-DMA tile (in-model: 21.3 -> 16.8 us)
+        if (a.KH * a.KW == 1 && a.IC == 512 && a.OC == 256 && !a.segsum && tile_fits(kTiles[18], a)) return 18;
         if (a.IC >= 800 && a.OC == 128 && a.npix < 65536) {
             if (a.IC % 64 == 0 && tile_fits(kTiles[86], a)) return 86;
             if (tile_fits(kTiles[85], a)) return 85;
@@ -2964,8 +2966,12 @@ int pick_tile(const ConvArgs& a) {
         // branch-free), 128 x 256 for narrower outputs from 2048 channels
         if (a.KW == 1 && tile_fits(kTiles[81], a)) {
             if (a.OC == 768 && a.IC >= 768) return 83;
+            // (in-model sweep, every fitting tile timed in place: wav2vec2-base's
+            // qkv 768 -> 2304 on the 8-wave LDS-DMA tile, 60.9 -> 55.8 us; ECAPA's
+            // 1024 -> 1024 TDNNs the same, 88.5 -> 84.6 us)
+            if (a.npix < 16384 && a.OC == 2304 && a.IC == 768 && tile_fits(kTiles[40], a)) return 40;
             if (a.npix < 16384 && (a.OC == 1024 || a.OC == 2304) && tile_fits(kTiles[82], a)) return 82;
-            if (a.npix >= 16384 && a.OC == 1024 && a.IC == 1024 && tile_fits(kTiles[84], a)) return 84;
+            if (a.npix >= 16384 && a.OC == 1024 && a.IC == 1024 && tile_fits(kTiles[40], a)) return 40;
             if (a.IC >= 2048) return a.OC % 256 == 0 ? 83 : 81;
         }
         // the same kernel for wav2vec2's strided feature convs (512 -> 512,
@@ -2983,6 +2989,8 @@ int pick_tile(const ConvArgs& a) {
         // and asp.tdnn's 1536 -> 128 GEMM on the 128x64 tile (398 workgroups
         // instead of 199: 25.0 against 38.7 us)
         if (a.KW == 5 && a.IC % 32 == 0 && a.OC >= 512 && a.OC % 128 == 0 && tile_fits(kTiles[36], a)) return 36;
+        // CAM++'s TDNN (k = 5, stride 2, 320 -> 128) on the 128x32 tile (in-model: 30.2 -> 19.2 us)
+        if (a.KW == 5 && a.sw == 2 && a.OC == 128 && a.IC % 64 == 0 && tile_fits(kTiles[52], a)) return 52;
         if (a.KW == 1 && a.IC >= 1024 && a.OC == 128 && a.IC % 64 == 0 && tile_fits(kTiles[18], a)) return 18;
         if (a.KW == 1 && a.IC == 768 && a.OC == 768 && tile_fits(kTiles[40], a)) return 40;
         if (a.KW == 1 && a.IC >= 512 && a.OC == 768 && a.IC % 64 == 0) return 34;
@@ -2999,12 +3007,13 @@ int pick_tile(const ConvArgs& a) {
     }
     // CAM++'s FCM: 32 -> 32 convs with a frequency stride (measured in the
     // model): the 1x1 shortcuts and the 40 -> 20 3x3 on the 128x32
-    // register-staged tile, the final 20 -> 10 conv on the narrow 32x64 DMA
-    // tile (the 80 -> 40 3x3 stays on the default)
+    // register-staged tile, the 80 -> 40 and the final 20 -> 10 3x3s on the
+    // narrow 32x64 DMA tile
     if (!a.split && a.IC == 32 && a.OC == 32 && (a.sh != 1 || a.sw != 1)) {
         if (a.KH * a.KW == 1) return 10;
         if (a.H <= 20) return 60;
         if (a.H <= 40) return 10;   // the second stage's 40 -> 20 conv (B=32 x 10 s: 48.1 -> 43.4 us)
+        if (tile_fits(kTiles[60], a)) return 60;   // 80 -> 40 (in-model: 87.2 -> 80.5 us)
     }
     // the FCM blocks' stride-1 conv2 (+ the shortcut): the 32-channel
     // register-weight tile at every batch (B=32 x 10 s, 40 rows: 54.4 -> 45.6 us;
