@@ -185,6 +185,26 @@ __device__ __forceinline__ void cam_local_segment(uint8_t* smem, int b, int s, c
     const int wave = tid >> 6, lane = tid & 63;
     const int t0 = s * seg, t1 = min(T, t0 + seg);
     const half_t* xb = x + (size_t)b * T * xs;
+    // the mask MLP's weights (128 inputs, 64 hidden units: thread tid holds
+    // quarter tid % 4 of hidden row tid / 4 and, below 128, of mask row
+    // tid / 4), loaded now so their latency overlaps steps 0-1
+    constexpr bool kPre = CT == 128;
+    const bool pre = kPre && H1 == 64;
+    const int q4 = tid & 3, o4 = tid >> 2;
+    float4v w1r[kPre ? 8 : 1], w2r[kPre ? 4 : 1];
+    float b1o = 0.0f, b2o = 0.0f;
+    if constexpr (kPre) {
+        if (pre) {
+            const float4v* p1 = reinterpret_cast<const float4v*>(w1 + (size_t)o4 * 128 + q4 * 32);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w1r[i] = p1[i];
+            const float4v* p2 = reinterpret_cast<const float4v*>(w2 + (size_t)(o4 < kLocalOC ? o4 : 0) * 64 + q4 * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w2r[i] = p2[i];
+            b1o = b1 ? b1[o4] : 0.0f;
+            b2o = b2 && o4 < kLocalOC ? b2[o4] : 0.0f;
+        }
+    }
     {   // 0. the segment's frames t0 - dil .. t1 + dil and the weights into LDS
         const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
             (void*)xb, 0, (int)(((size_t)(T - 1) * xs + C) * 2), 0x00020000);
@@ -262,7 +282,37 @@ __device__ __forceinline__ void cam_local_segment(uint8_t* smem, int b, int s, c
         }
     }
     __syncthreads();
-    {   // 2. the mask MLP
+    if (pre) {   // 2. the mask MLP from the preloaded rows (dot4's order: quarters, then (a0 + a1) + (a2 + a3))
+        if constexpr (kPre) {
+            double a = 0.0;
+            const float4v* v4 = reinterpret_cast<const float4v*>(ctx + q4 * 32);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4v wv = w1r[i], xv = v4[i];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a += (double)wv[e] * (double)xv[e];
+            }
+            double a1 = __shfl_down(a, 1, 4), a2 = __shfl_down(a, 2, 4), a3 = __shfl_down(a, 3, 4);
+            a = (a + a1) + (a2 + a3);
+            if (q4 == 0) hid[o4] = fmaxf((float)a + b1o, 0.0f);
+            __syncthreads();
+            if (o4 < kLocalOC) {
+                a = 0.0;
+                const float4v* h4 = reinterpret_cast<const float4v*>(hid + q4 * 16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4v wv = w2r[i], xv = h4[i];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) a += (double)wv[e] * (double)xv[e];
+                }
+                a1 = __shfl_down(a, 1, 4);
+                a2 = __shfl_down(a, 2, 4);
+                a3 = __shfl_down(a, 3, 4);
+                a = (a + a1) + (a2 + a3);
+                if (q4 == 0) gate[o4] = 1.0f / (1.0f + expf(-((float)a + b2o)));
+            }
+        }
+    } else {   // 2. the mask MLP
         const int q = tid & 3;
         for (int o = tid >> 2; o < H1; o += 64) {
             const double a = dot4(w1 + (size_t)o * C, ctx, C, q);
