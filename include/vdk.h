@@ -207,6 +207,20 @@ int vdk_gguf_tensor_f32(const char* path, const char* name, float* out, long lon
  * chunk-major [IC/16][KH*KW][OC][16] copy that vdk_conv_desc.w_chunked takes. */
 void vdk_conv_pack_chunked(const unsigned short* w, int OC, int KH, int KW, int IC, unsigned short* out);
 int vdk_conv2d_ex(const vdk_conv_desc* desc, void* stream);
+/* Run-time tile tuning for vdk_conv2d_ex calls with tile = -1 (off by
+ * default; VDK_CONV_AUTOTUNE=1 in the environment turns it on too).  No
+ * reference counterpart: for conv shapes the built-in per-layer rules were
+ * not measured on.  The first call of each shape (channels, kernel, strides,
+ * map and batch size, epilogue features) times every tile that fits into
+ * scratch outputs, keeps the fastest one whose output equals the default
+ * tile's bit for bit, and synchronises the stream.  Later calls of the shape
+ * use the cached choice.  Applies to plain f16 outputs that do not overlap
+ * an input; others keep the default tile.  Not for use under stream capture
+ * (the first call allocates).  Returns 0. */
+int vdk_conv_set_autotune(int on);
+/* The tile the tuner chose for this descriptor's shape, or -1 if it has not
+ * tuned it. */
+int vdk_conv_tuned_tile(const vdk_conv_desc* d);
 int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* desc);
 
 /* Same contract with an explicit kernel/tile choice (index into the library's

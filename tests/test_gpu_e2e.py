@@ -121,3 +121,24 @@ def test_other_lengths_and_mean_vec():
         assert n16 == 48000
         assert cosine(ctx.embed_pcm(x8, sample_rate=8000), net.forward(O.fbank(x16))) >= 0.9999
         ctx.close()
+
+
+def test_autotuned_tiles_keep_the_bits(resnet):
+    """The run-time tile tuner (vdk_conv_set_autotune) only ever picks a tile
+    whose output equals the default's bit for bit: ResNet34 embeddings of a
+    4-clip batch are the same with it on (first call: tuning, second: the
+    cached choices) as with it off, and the tuner recorded a choice for a
+    shape it handled."""
+    path, ctx, net = resnet
+    L = lib.lib()
+    pcm = synth.clips(41, 4, N3S)
+    announce("e2e autotune: reference pass")
+    ref = ctx.embed_batch(pcm)
+    lib.check(L.vdk_conv_set_autotune(1))
+    try:
+        announce("e2e autotune: tuning pass")
+        a = ctx.embed_batch(pcm)
+        b = ctx.embed_batch(pcm)
+    finally:
+        lib.check(L.vdk_conv_set_autotune(0))
+    assert np.array_equal(a, ref) and np.array_equal(b, ref)

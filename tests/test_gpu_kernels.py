@@ -787,3 +787,46 @@ def test_conv_input_prologue(case):
     d.KW, d.pad_w, d.tile = 3, 1, -1
     assert L.vdk_conv2d_ex(d, None) != 0
     assert "input prologue" in L.vdk_last_error().decode()
+
+
+@pytest.mark.parametrize("B,H,W,IC,OC,K,res", [(3, 17, 45, 96, 192, 3, True), (1, 1, 5000, 768, 384, 1, False),
+                                               (1, 1, 4096, 3072, 3072, 1, False)])
+def test_conv_autotune_same_bits_and_cached(B, H, W, IC, OC, K, res):
+    """Shapes no built-in rule was measured on (a 96 -> 192 3x3 with a
+    residual, 1-D GEMMs of 768 -> 384 and the real ECAPA MFA's 3072 -> 3072):
+    with the run-time tuner on, the first call (tuning) and the second (the
+    cached choice) give the default tile's bits, and the chosen tile fits."""
+    L = lib.lib()
+    rng = np.random.default_rng(H * W + IC + OC)
+    announce(f"autotune conv B={B} {H}x{W} {IC}->{OC} k={K} res={res}")
+    x = rng.standard_normal((B, H, W, IC)).astype(np.float16)
+    w = (rng.standard_normal((OC, K, K, IC)) * np.sqrt(2.0 / (IC * K * K))).astype(np.float16)
+    b = rng.uniform(-0.5, 0.5, OC).astype(np.float32)
+    r = rng.standard_normal((B, H, W, OC)).astype(np.float16)
+    dx, dw, db, dr = (lib.DeviceBuffer.from_array(a) for a in (x, w, b, r))
+    outs = []
+    def run():
+        d = lib.ConvDesc()
+        d.x, d.batch, d.H, d.W, d.IC = dx.ptr, B, H, W, IC
+        d.w, d.OC, d.KH, d.KW = dw.ptr, OC, K, K
+        d.stride_h = d.stride_w = d.dil_h = d.dil_w = 1
+        d.pad_h = d.pad_w = K // 2
+        d.bias, d.act = db.ptr, lib.ACT_RELU
+        if res:
+            d.residual = dr.ptr
+        dy = lib.DeviceBuffer(B * H * W * OC * 2)
+        d.y, d.tile = dy.ptr, -1
+        lib.check(L.vdk_conv2d_ex(d, None))
+        lib.check(L.vdk_synchronize())
+        outs.append(dy.to_array(np.uint16, (B, H, W, OC)))
+        return d
+    run()
+    lib.check(L.vdk_conv_set_autotune(1))
+    try:
+        d = run()
+        run()
+        t = L.vdk_conv_tuned_tile(d)
+    finally:
+        lib.check(L.vdk_conv_set_autotune(0))
+    assert np.array_equal(outs[1], outs[0]) and np.array_equal(outs[2], outs[0])
+    assert t >= 0 and L.vdk_conv2d_tile_fits_ex(t, d)

@@ -17,9 +17,13 @@
 // stem_mfma_kernel: the IC=1 stem in f32 on v_mfma_f32_32x32x2_f32 (K = the 9
 // taps padded to 10); stem_conv3x3_kernel, the f32 FMA loop, serves OC = 16.
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cstdlib>
+#include <mutex>
+#include <string>
 #include <type_traits>
+#include <unordered_map>
 
 #include "common.hpp"
 #include "devmath.hpp"
@@ -3291,6 +3295,131 @@ __global__ __launch_bounds__(256) void stem_mfma_kernel(const float* __restrict_
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Run-time tile tuning: mismatching f16 values between two outputs of npix
+// pixels x OC channels at pixel stride ys.
+__global__ __launch_bounds__(256) void count_diff_kernel(const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+                                                         int npix, int OC, int ys, unsigned* __restrict__ out) {
+    const long n = (long)npix * OC;
+    unsigned c = 0;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+        const long p = i / OC, k = i - p * OC;
+        c += a[p * ys + k] != b[p * ys + k];
+    }
+    if (c) atomicAdd(out, c);
+}
+
+std::atomic<int> g_autotune{-1};   // -1: not yet read from VDK_CONV_AUTOTUNE
+bool autotune_on() {
+    int v = g_autotune.load();
+    if (v < 0) {
+        const char* e = std::getenv("VDK_CONV_AUTOTUNE");
+        v = (e && *e && *e != '0') ? 1 : 0;
+        int expect = -1;
+        g_autotune.compare_exchange_strong(expect, v);
+        v = g_autotune.load();
+    }
+    return v == 1;
+}
+struct TuneCache {
+    std::mutex mu;
+    std::unordered_map<std::string, int> best;
+};
+TuneCache& tune_cache() {
+    static TuneCache c;
+    return c;
+}
+std::string tune_key(const ConvArgs& a) {
+    char k[400];
+    snprintf(k, sizeof k, "%d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d %d",
+             a.H, a.W, a.IC, a.Ho, a.Wo, a.OC, a.KH, a.KW, a.sh, a.sw, a.ph, a.pw, a.dh, a.dw, a.act, a.xs, a.ys,
+             a.rs, a.npix, a.npix_in, a.reflect, a.bias != nullptr, a.res != nullptr, a.gate != nullptr,
+             a.post_scale != nullptr, a.in_scale != nullptr, a.wc != nullptr, a.wq != nullptr, a.res_f32, a.res_after,
+             a.tanh_after);
+    return k;
+}
+// The tuner handles convs whose output is plain f16 rows (no second output,
+// segment sums, split-f16, f32 / transposed store or AFF operands) that do
+// not overlap an input.
+bool tunable(const ConvArgs& a) {
+    if (a.split || a.y2 || a.segsum || a.y_f32 || a.y_tr || a.ax || a.xgl != 4 || a.ygl != 4 || a.xgs != 16 ||
+        a.ygs != 16)
+        return false;
+    const auto* y0 = static_cast<const uint8_t*>(a.y);
+    const uint8_t* y1 = y0 + 2 * ((size_t)(a.npix - 1) * a.ys + a.OC);
+    auto overlaps = [&](const void* p, size_t bytes) {
+        const auto* q = static_cast<const uint8_t*>(p);
+        return p && q < y1 && y0 < q + bytes;
+    };
+    return !overlaps(a.x, 2 * ((size_t)(a.npix_in - 1) * a.xs + a.IC)) &&
+           !overlaps(a.res, (a.res_f32 ? 4 : 2) * ((size_t)(a.npix - 1) * a.rs + a.OC));
+}
+// Times every tile that fits (into scratch outputs) and returns the fastest
+// whose output equals the default tile's bit for bit (so the choice changes
+// neither the results nor their independence of the batch); synchronises s.
+int tune_tile(const ConvArgs& a, int t_default, hipStream_t s) {
+    const size_t ybytes = 2 * ((size_t)(a.npix - 1) * a.ys + a.OC);
+    void *ya = nullptr, *yb = nullptr;
+    unsigned* cnt = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int best = t_default;
+    auto cleanup = [&] {
+        if (ya) (void)hipFree(ya);
+        if (yb) (void)hipFree(yb);
+        if (cnt) (void)hipFree(cnt);
+        if (e0) (void)hipEventDestroy(e0);
+        if (e1) (void)hipEventDestroy(e1);
+    };
+    if (hipMalloc(&ya, ybytes) != hipSuccess || hipMalloc(&yb, ybytes) != hipSuccess ||
+        hipMalloc((void**)&cnt, sizeof(unsigned)) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+        hipEventCreate(&e1) != hipSuccess) {
+        cleanup();
+        (void)hipGetLastError();
+        return t_default;
+    }
+    auto time_tile = [&](int t, void* y) {
+        ConvArgs b = a;
+        b.y = y;
+        kTiles[t].launch(b, s);   // warm
+        float best_ms = 1e30f;
+        for (int rep = 0; rep < 3; ++rep) {
+            VDK_HIP(hipEventRecord(e0, s));
+            kTiles[t].launch(b, s);
+            VDK_HIP(hipEventRecord(e1, s));
+            VDK_HIP(hipEventSynchronize(e1));
+            float ms = 0.0f;
+            VDK_HIP(hipEventElapsedTime(&ms, e0, e1));
+            best_ms = std::min(best_ms, ms);
+        }
+        return best_ms;
+    };
+    try {
+        VDK_HIP(hipMemsetAsync(ya, 0, ybytes, s));
+        VDK_HIP(hipMemsetAsync(yb, 0, ybytes, s));
+        float best_ms = time_tile(t_default, ya);
+        for (int t = 0; t < kNumTiles; ++t) {
+            if (t == t_default || !tile_fits(kTiles[t], a)) continue;
+            const float ms = time_tile(t, yb);
+            VDK_HIP(hipMemsetAsync(cnt, 0, sizeof(unsigned), s));
+            const long n = (long)a.npix * a.OC;
+            hipLaunchKernelGGL(count_diff_kernel, dim3((unsigned)std::min<long>(cdiv(n, 256), 4096)), dim3(256), 0, s,
+                               static_cast<const uint16_t*>(ya), static_cast<const uint16_t*>(yb), a.npix, a.OC, a.ys,
+                               cnt);
+            unsigned diff = 1;
+            VDK_HIP(hipMemcpyAsync(&diff, cnt, sizeof(unsigned), hipMemcpyDeviceToHost, s));
+            VDK_HIP(hipStreamSynchronize(s));
+            if (diff == 0 && ms < best_ms) {
+                best_ms = ms;
+                best = t;
+            }
+        }
+    } catch (...) {
+        cleanup();
+        throw;
+    }
+    cleanup();
+    return best;
+}
+
 }  // namespace
 }  // namespace vdk
 
@@ -3424,6 +3553,18 @@ int conv_impl(const vdk_conv_desc& d, void* stream) {
         if (t < 0) {
             t = pick_tile(a);
             require(t >= 0, "conv2d: no kernel for this channel count");
+            if (autotune_on() && tunable(a)) {
+                TuneCache& tc = tune_cache();
+                const std::string key = tune_key(a);
+                std::lock_guard<std::mutex> lock(tc.mu);
+                auto it = tc.best.find(key);
+                if (it != tc.best.end()) {
+                    t = it->second;
+                } else {
+                    t = tune_tile(a, t, s);
+                    tc.best.emplace(key, t);
+                }
+            }
         } else {
             require(t < kNumTiles, "conv2d: tile index out of range");
         }
@@ -3525,6 +3666,28 @@ extern "C" int vdk_conv2d_tile_fits(int tile, int IC, int OC, int KH, int KW, in
     const vdk_conv_desc d = plain_desc(nullptr, 1, 1, 1, IC, nullptr, OC, KH, KW, stride, pad, nullptr, nullptr, 0,
                                        nullptr, tile);
     return tile_fits(kTiles[tile], shape_args(d)) ? 1 : 0;
+}
+
+extern "C" int vdk_conv_set_autotune(int on) {
+    g_autotune.store(on ? 1 : 0);
+    return 0;
+}
+
+extern "C" int vdk_conv_tuned_tile(const vdk_conv_desc* d) {
+    if (!d || d->batch <= 0) return -1;
+    ConvArgs a = shape_args(*d);   // + the fields conv_impl derives
+    const int ekh = (d->KH - 1) * a.dh + 1, ekw = (d->KW - 1) * a.dw + 1;
+    a.Ho = (d->H + 2 * d->pad_h - ekh) / a.sh + 1;
+    const int Wo_full = (d->W + 2 * d->pad_w - ekw) / a.sw + 1;
+    a.Wo = d->out_w > 0 ? d->out_w : Wo_full;
+    a.npix = d->batch * a.Ho * a.Wo;
+    a.npix_in = d->batch * d->H * d->W;
+    a.bias = d->bias;
+    a.wc = static_cast<const half_t*>(d->w_chunked);
+    TuneCache& tc = tune_cache();
+    std::lock_guard<std::mutex> lock(tc.mu);
+    auto it = tc.best.find(tune_key(a));
+    return it == tc.best.end() ? -1 : it->second;
 }
 
 extern "C" int vdk_conv2d_tile_fits_ex(int tile, const vdk_conv_desc* d) {

@@ -184,6 +184,8 @@ _SIGS = {
                                 C.c_int, C.c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdk_cam_local": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int,
                                 _vp, _vp, _vp, _vp, _vp, C.c_int, _vp, _vp, _vp]),
+    "vdk_conv_set_autotune": (C.c_int, [C.c_int]),
+    "vdk_conv_tuned_tile": (C.c_int, [C.POINTER(ConvDesc)]),
     "vdk_cam_context": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp, _vp, C.c_int,
                                   _vp, _vp]),
 }
