@@ -404,6 +404,7 @@ __global__ __launch_bounds__(64 * NWQ) void attention_kernel(const half_t* __res
     constexpr int NCH = kKB * kHD / 8;          // 16-byte K (and V) chunks per block
     constexpr int NLD = (NCH + NT - 1) / NT;     // per thread (the last slot partial when NT does not divide NCH)
     __shared__ __attribute__((aligned(16))) half_t sK[kKB * kKR];   // [key][dim]
+    __shared__ __attribute__((aligned(16))) half_t sVs[kKB * kKR];  // [key][dim] staging of V
     __shared__ __attribute__((aligned(16))) half_t sV[kHD * kVR];   // [dim][key]
     const int b = blockIdx.z, h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = lane >> 5, lr = lane & 31;
@@ -439,11 +440,22 @@ __global__ __launch_bounds__(64 * NWQ) void attention_kernel(const half_t* __res
             const int i = tid + j * NT, key = i >> 3, d0 = (i & 7) * 8;
             if (NCH % NT != 0 && i >= NCH) continue;
             *reinterpret_cast<half8*>(&sK[key * kKR + d0]) = kn[j];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sV[(d0 + e) * kVR + key] = vn[j][e];
+            *reinterpret_cast<half8*>(&sVs[key * kKR + d0]) = vn[j];
         }
         __syncthreads();
         if (kb + kKB < T) fetch(kb + kKB);
+        // V transposed through the staging rows: item (dim d, keys 8g .. 8g+7)
+        // gathers one dim of 8 key rows (a wave's 64 lanes read 64 dims of one
+        // row) and writes them as one 16-byte chunk of the [dim][key] tile
+        // (2-byte scattered writes had made most LDS cycles bank conflicts)
+        for (int it = tid; it < kHD * (kKB / 8); it += NT) {
+            const int d = it & (kHD - 1), g = it >> 6;
+            half8 col;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) col[e] = sVs[(8 * g + e) * kKR + d];
+            *reinterpret_cast<half8*>(&sV[d * kVR + 8 * g]) = col;
+        }
+        __syncthreads();
         float16v s[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
