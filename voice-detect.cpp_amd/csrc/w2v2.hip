@@ -422,14 +422,21 @@ __global__ __launch_bounds__(64 * NWQ) void attention_kernel(const half_t* __res
     float m = -INFINITY, l = 0.0f;
     const half8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
     half8 kn[NLD], vn[NLD];
+    // 32-bit element offsets within the clip (T * 3H stays far below 2^31)
+    int koff[NLD];
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+        const int i = tid + j * NT;
+        koff[j] = (i >> 3) * (int)rs + h * kHD + (i & 7) * 8 + H;
+    }
     auto fetch = [&](int kb) {
 #pragma unroll
         for (int j = 0; j < NLD; ++j) {
-            const int i = tid + j * NT, key = i >> 3, d0 = (i & 7) * 8, kg = kb + key;
-            const half_t* src = base + (size_t)kg * rs + h * kHD + d0;
+            const int i = tid + j * NT, kg = kb + (i >> 3);
+            const half_t* src = base + (koff[j] + kb * (int)rs);
             const bool ok = (NCH % NT == 0 || i < NCH) && kg < T;
-            kn[j] = ok ? *reinterpret_cast<const half8*>(src + H) : zero8;
-            vn[j] = ok ? *reinterpret_cast<const half8*>(src + 2 * H) : zero8;
+            kn[j] = ok ? *reinterpret_cast<const half8*>(src) : zero8;
+            vn[j] = ok ? *reinterpret_cast<const half8*>(src + H) : zero8;
         }
     };
     fetch(0);
@@ -468,25 +475,39 @@ __global__ __launch_bounds__(64 * NWQ) void attention_kernel(const half_t* __res
             }
         }
         // s[kt][r]: key kb + 32 kt + 8 (r / 4) + 4 hl + r % 4 of query q0 + lr
+        // (keys past T masked, in the last block only)
         float mx = -INFINITY;
+        if (kb + kKB <= T) {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kb + kt * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-                const float v = key < T ? s[kt][r] * scale_log2 : -INFINITY;
-                s[kt][r] = v;
-                mx = fmaxf(mx, v);
-            }
+                for (int r = 0; r < 16; ++r) {
+                    const float v = s[kt][r] * scale_log2;
+                    s[kt][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb + kt * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+                    const float v = key < T ? s[kt][r] * scale_log2 : -INFINITY;
+                    s[kt][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m_new = fmaxf(m, mx);   // finite: every block holds a key < T
-        const float alpha = exp2f(m - m_new);
+        // v_exp_f32 directly: it differs from exp2f only below 2^-126, where
+        // p rounds to an f16 zero and is nothing against the row sum (>= 1)
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
         float ls = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = exp2f(s[kt][r] - m_new);
+                const float p = __builtin_amdgcn_exp2f(s[kt][r] - m_new);
                 s[kt][r] = p;
                 ls += p;
             }
