@@ -210,11 +210,12 @@ __global__ __launch_bounds__(1024) void asp_pool_kernel(const float* __restrict_
 // all ATT channels, and x rows, its 64 channels, DMA'd two chunks ahead
 // into a three-stage LDS ring), computing each 32-channel x 32-frame logit
 // block with MFMAs (W from registers, a1 from LDS, the bias added after the
-// K sum like the conv kernels).  Each (lane, register) keeps an online
-// softmax state: running max m and the sums z = sum e, s1 = sum e x,
-// s2 = sum e x^2 with e = exp(l - m), in f64, rescaled when m grows; the
-// states of the 32 frame lanes merge by a butterfly and the two frame-block
-// waves in a fixed order.  Then mu = s1 / z and var = s2 / z - mu^2 (f64:
+// K sum like the conv kernels).  The chunk's f32 logits then take the
+// bytes of its a1 rows, and each thread pools one channel over a quarter
+// of the chunk's frames: an online softmax state (running max m and the
+// sums z = sum e, s1 = sum e x, s2 = sum e x^2 with e = exp(l - m), in
+// f64) rescaled once per chunk by the chunk's own max.  The four quarters
+// merge in a fixed order.  Then mu = s1 / z and var = s2 / z - mu^2 (f64:
 // the cancellation loses ~1e-16 mu^2, far below the f16 resolution of x).
 // Rows 256 / 128 bytes wide with their 16-byte chunks XOR-swizzled by row,
 // so the MFMA operand reads hit 16 distinct chunks per 16 lanes.
@@ -307,9 +308,10 @@ __global__ __launch_bounds__(256, 2) void asp_attn_pool_kernel(const half_t* __r
                                                                const half_t* __restrict__ x, int xs, int T, int C,
                                                                float eps, float* __restrict__ out) {
     using G = AspLds<ATT>;
+    static_assert(G::A_BYTES >= kAspChunk * 64 * 4, "a chunk's f32 logits fit its a1 rows");
     __shared__ __attribute__((aligned(1024))) uint8_t ring[kAspStages * G::STAGE];
-    __shared__ float pm[2][64];            // per frame-block wave: merged state of each channel
-    __shared__ double pz[2][64], ps1[2][64], ps2[2][64];
+    __shared__ float pm[4][64];            // per frame quarter: each channel's state
+    __shared__ double pz[4][64], ps1[4][64], ps2[4][64];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -333,9 +335,9 @@ __global__ __launch_bounds__(256, 2) void asp_attn_pool_kernel(const half_t* __r
         for (int e = 0; e < 4; ++e) bv[g * 4 + e] = bc[c0 + cb * 32 + g * 8 + lhalf * 4 + e];
     __builtin_amdgcn_s_waitcnt(0);
 
-    AspState st_[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) st_[r] = AspState{-INFINITY, 0.0, 0.0, 0.0};
+    // pooling: thread = channel pc of the 64, frames fq * 16 .. + 15 of each chunk
+    const int pc = tid & 63, fq = tid >> 6;
+    AspState S{-INFINITY, 0.0, 0.0, 0.0};
     // chunks 0 and 1 go out together; then the ring stays two chunks ahead
     asp_issue<ATT>(ring, ar, xr, as, xs, b, T, 0, c0, wave, lane);
     if (nq > 1) asp_issue<ATT>(ring + G::STAGE, ar, xr, as, xs, b, T, kAspChunk, c0, wave, lane);
@@ -346,62 +348,73 @@ __global__ __launch_bounds__(256, 2) void asp_attn_pool_kernel(const half_t* __r
         if (q + 1 < nq) wait_vmcnt<G::INS / 4>();
         else __builtin_amdgcn_s_waitcnt(0);
         lds_barrier();   // everyone's; chunk q-1's stage is free for chunk q+2
-        const uint8_t* const st = ring + slot * G::STAGE;
+        uint8_t* const st = ring + slot * G::STAGE;
         if (q + 2 < nq) {
             const int s2 = slot == 0 ? 2 : slot - 1;
             asp_issue<ATT>(ring + s2 * G::STAGE, ar, xr, as, xs, b, T, (q + 2) * kAspChunk, c0, wave, lane);
         }
-        const int row = tb * 32 + lrow, t = q * kAspChunk + row;
         float16v acc;
         asp_logits<ATT>(st, wf, tb, lrow, lhalf, acc);
-        if (t < T) {
+        lds_barrier();   // every wave has read the chunk's a1 rows: their bytes take the logits
+        {   // l = acc + bias as f32 [frame][64 channels], 16-byte columns XOR-swizzled by frame
+            const int row = tb * 32 + lrow;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const half4 xv = asp_x4(st + G::A_BYTES, row, cb, g, lhalf);
+                const int c4 = cb * 8 + g * 2 + lhalf;
+                const float4v l4 = {acc[g * 4] + bv[g * 4], acc[g * 4 + 1] + bv[g * 4 + 1],
+                                    acc[g * 4 + 2] + bv[g * 4 + 2], acc[g * 4 + 3] + bv[g * 4 + 3]};
+                *reinterpret_cast<float4v*>(st + row * 256 + ((c4 ^ (row & 15)) * 16)) = l4;
+            }
+        }
+        lds_barrier();
+        {   // this thread's 16 frames: the chunk's max first, one rescale, then the sums
+            const uint8_t* const xs_lds = st + G::A_BYTES;
+            float lv[16];
+            float mc = -INFINITY;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // branch-free update: rescale by exp(m - m') (1 while the
-                    // max holds, 0 for the first frame)
-                    AspState& S = st_[g * 4 + e];
-                    const float l = acc[g * 4 + e] + bv[g * 4 + e];
-                    const float mn = fmaxf(S.m, l);
-                    const double f = (double)__expf(S.m - mn), ex = (double)__expf(l - mn);
-                    const double xd = (double)(float)xv[e], ex_x = ex * xd;
-                    S.z = S.z * f + ex;
-                    S.s1 = S.s1 * f + ex_x;
-                    S.s2 = S.s2 * f + ex_x * xd;
-                    S.m = mn;
+            for (int i = 0; i < 16; ++i) {
+                const int row = fq * 16 + i;
+                lv[i] = q * kAspChunk + row < T
+                            ? *reinterpret_cast<const float*>(st + row * 256 + (((pc >> 2) ^ (row & 15)) * 16) +
+                                                              (pc & 3) * 4)
+                            : -INFINITY;
+                mc = fmaxf(mc, lv[i]);
+            }
+            if (mc > -INFINITY) {   // (S.m - mn is -inf on the first update: the scale is 0)
+                const float mn = fmaxf(S.m, mc);
+                const double sc = (double)__expf(S.m - mn);
+                S.z *= sc;
+                S.s1 *= sc;
+                S.s2 *= sc;
+                S.m = mn;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = fq * 16 + i;
+                    if (q * kAspChunk + row < T) {
+                        const half_t xh = *reinterpret_cast<const half_t*>(
+                            xs_lds + row * 128 + (((pc >> 3) ^ (row & 7)) * 16) + (pc & 7) * 2);
+                        const double ex = (double)__expf(lv[i] - mn), xd = (double)(float)xh, ex_x = ex * xd;
+                        S.z += ex;
+                        S.s1 += ex_x;
+                        S.s2 += ex_x * xd;
+                    }
                 }
             }
         }
         slot = slot == 2 ? 0 : slot + 1;
     }
-    // merge over the 32 frame lanes (butterfly, fixed order), then over the
-    // two frame-block waves
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-#pragma unroll
-        for (int msk = 1; msk < 32; msk <<= 1) {
-            const AspState o{__shfl_xor(st_[r].m, msk), __shfl_xor(st_[r].z, msk), __shfl_xor(st_[r].s1, msk),
-                             __shfl_xor(st_[r].s2, msk)};
-            asp_merge(st_[r], o);
-        }
-    if (lrow == 0) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int ch = cb * 32 + (r >> 2) * 8 + lhalf * 4 + (r & 3);
-            pm[tb][ch] = st_[r].m;
-            pz[tb][ch] = st_[r].z;
-            ps1[tb][ch] = st_[r].s1;
-            ps2[tb][ch] = st_[r].s2;
-        }
-    }
+    // the four frame quarters of each channel, merged in a fixed order
+    pm[fq][pc] = S.m;
+    pz[fq][pc] = S.z;
+    ps1[fq][pc] = S.s1;
+    ps2[fq][pc] = S.s2;
     __syncthreads();
     if (tid < 64) {
-        AspState S{pm[0][tid], pz[0][tid], ps1[0][tid], ps2[0][tid]};
-        asp_merge(S, AspState{pm[1][tid], pz[1][tid], ps1[1][tid], ps2[1][tid]});
-        const double mu = S.s1 / S.z;
-        float var = (float)(S.s2 / S.z - mu * mu);
+        AspState R{pm[0][tid], pz[0][tid], ps1[0][tid], ps2[0][tid]};
+#pragma unroll
+        for (int k = 1; k < 4; ++k) asp_merge(R, AspState{pm[k][tid], pz[k][tid], ps1[k][tid], ps2[k][tid]});
+        const double mu = R.s1 / R.z;
+        float var = (float)(R.s2 / R.z - mu * mu);
         if (var < eps) var = eps;
         out[(size_t)b * 2 * C + c0 + tid] = (float)mu;
         out[(size_t)b * 2 * C + C + c0 + tid] = sqrtf(var);
