@@ -83,6 +83,7 @@ __global__ __launch_bounds__(256) void channel_stats_kernel(const half_t* __rest
     for (int e = 0; e < 8; ++e) { s[e] = 0.0; q[e] = 0.0; }
     if (c8 < C) {
         const half_t* p = x + (size_t)b * T * xs + c8;
+#pragma unroll 4   // four rows' loads in flight; the sums keep their order
         for (int t = tp; t < T; t += NP) {
             const half8 v = *reinterpret_cast<const half8*>(p + (size_t)t * xs);
 #pragma unroll

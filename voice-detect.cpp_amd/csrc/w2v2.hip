@@ -667,6 +667,7 @@ __global__ __launch_bounds__(1024) void time_mean_kernel(const void* __restrict_
     const int c = blockIdx.x * 256 + cg * 4, b = blockIdx.y;
     double s[4] = {0.0, 0.0, 0.0, 0.0};
     if (c < C) {
+#pragma unroll 4   // four rows' loads in flight; the sums keep their order
         for (int t = tp; t < T; t += 16) {
             const size_t i = ((size_t)b * T + t) * C + c;
             if (x_f32) {
