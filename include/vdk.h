@@ -343,6 +343,11 @@ int vdk_channel_mean(const void* d_x, int x_stride, int batch, int T, int C, flo
  * src/encoder.cpp:218-244). */
 int vdk_se_gate_residual(const void* d_x, int x_stride, const float* d_gate, const void* d_res,
                          int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream);
+/* y = x * scale[b][c] + res: vdk_se_gate_residual with the sigmoid already
+ * applied to the gate (once per clip and channel, e.g. by vdk_linear_ex's
+ * VDK_ACT_SIGMOID, whose expression is the same, so y has the same bits). */
+int vdk_se_scale_residual(const void* d_x, int x_stride, const float* d_scale, const void* d_res,
+                          int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream);
 /* out [B][2C] = [mean_t x ; sqrt(max(var_t x, eps))] (ASP global context,
  * src/encoder.cpp:269-271): one pass of f64 sums of x and x^2, var =
  * E[x^2] - mean^2; C, x_stride and d_x 8-channel (16-byte) aligned. */

@@ -340,6 +340,19 @@ def test_se_and_asp_reductions():
     got = gcat[:, :, 2 * C:].astype(np.float64)
     assert np.all(np.abs(got - want) <= 2.0 ** -10 * np.abs(want) + 1e-6)
     assert not gcat[:, :, :2 * C].any()
+    # the same with the sigmoid taken once per (clip, channel) by the FC's
+    # reduce (VDK_ACT_SIGMOID, the model's path): the same bits
+    ident = np.eye(C, dtype=np.float32)
+    dgi, dsig = lib.DeviceBuffer.from_array(np.ascontiguousarray(gate)), lib.DeviceBuffer(B * C * 4)
+    dwi = lib.DeviceBuffer.from_array(ident)
+    wsz = L.vdk_linear_workspace_size(B, C, C)
+    dwk = lib.DeviceBuffer(wsz)
+    lib.check(L.vdk_linear_ex(dgi.ptr, B, C, dwi.ptr, None, None, C, lib.ACT_SIGMOID, dsig.ptr, dwk.ptr, wsz, None))
+    dcat2 = lib.DeviceBuffer.from_array(cat)
+    lib.check(L.vdk_se_scale_residual(dt2.ptr, 2 * C, dsig.ptr, dr.ptr, C, B, T, C, dcat2.ptr + 2 * C * 2, 3 * C,
+                                      None))
+    _sync()
+    assert np.array_equal(dcat2.to_array(np.float16, (B, T, 3 * C)).view(np.uint16), gcat.view(np.uint16))
     # ASP global statistics and attentive pooling
     x = (rng.standard_normal((B, T, M), dtype=np.float32) * 2 + 1).astype(np.float16)
     x[1, :, 5] = 0.5           # a constant channel: variance clamps to eps

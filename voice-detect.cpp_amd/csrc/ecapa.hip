@@ -120,6 +120,9 @@ __global__ __launch_bounds__(256) void channel_stats_kernel(const half_t* __rest
     }
 }
 
+// y = x * g + res with g = sigmoid(gate) (SIG) or g = gate, the sigmoid
+// already taken once per (clip, channel).
+template <bool SIG>
 __global__ __launch_bounds__(256) void se_gate_residual_kernel(const half_t* __restrict__ x, int xs,
                                                                const float* __restrict__ gate,
                                                                const half_t* __restrict__ res, int rs, int B, int T,
@@ -132,11 +135,16 @@ __global__ __launch_bounds__(256) void se_gate_residual_kernel(const half_t* __r
     const int b = (int)(r / T);
     const half8 xv = *reinterpret_cast<const half8*>(x + r * xs + c);
     const half8 rv = *reinterpret_cast<const half8*>(res + r * rs + c);
+    const float4v ga = *reinterpret_cast<const float4v*>(gate + (size_t)b * C + c);
+    const float4v gb = *reinterpret_cast<const float4v*>(gate + (size_t)b * C + c + 4);
     half8 o;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float g = 1.0f / (1.0f + expf(-gate[(size_t)b * C + c + e]));
-        o[e] = (half_t)((float)xv[e] * g + (float)rv[e]);
+        const float gv = e < 4 ? ga[e] : gb[e - 4];
+        const float g = SIG ? 1.0f / (1.0f + expf(-gv)) : gv;
+        float v = (float)xv[e] * g + (float)rv[e];
+        asm volatile("" : "+v"(v));   // rounded to f32, then to f16 (no one-rounding v_fma_mix*_f16)
+        o[e] = (half_t)v;
     }
     *reinterpret_cast<half8*>(y + r * ys + c) = o;
 }
@@ -642,21 +650,35 @@ extern "C" int vdk_channel_mean(const void* d_x, int x_stride, int batch, int T,
     });
 }
 
-extern "C" int vdk_se_gate_residual(const void* d_x, int x_stride, const float* d_gate, const void* d_res,
-                                    int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream) {
+namespace vdk {
+namespace {
+int se_residual(const void* d_x, int x_stride, const float* d_gate, bool sig, const void* d_res, int res_stride,
+                int batch, int T, int C, void* d_y, int y_stride, void* stream) {
     return guarded([&] {
         require(d_x && d_gate && d_res && d_y, "se_gate_residual: NULL device pointer");
         require(batch > 0 && T > 0 && C > 0 && C % 8 == 0 && x_stride >= C && res_stride >= C && y_stride >= C,
                 "se_gate_residual: bad shape");
         require(x_stride % 8 == 0 && res_stride % 8 == 0 && y_stride % 8 == 0 && al16(d_x) && al16(d_res) &&
-                    al16(d_y), "se_gate_residual: strides/pointers must be 8-channel aligned");
+                    al16(d_y) && al16(d_gate), "se_gate_residual: strides/pointers must be 8-channel aligned");
         const long n = (long)batch * T * (C / 8);
-        hipLaunchKernelGGL(se_gate_residual_kernel, dim3(cdiv(n, 256)), dim3(256), 0,
-                           static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride, d_gate,
-                           static_cast<const half_t*>(d_res), res_stride, batch, T, C, static_cast<half_t*>(d_y),
-                           y_stride);
+        hipLaunchKernelGGL(sig ? se_gate_residual_kernel<true> : se_gate_residual_kernel<false>, dim3(cdiv(n, 256)),
+                           dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const half_t*>(d_x), x_stride,
+                           d_gate, static_cast<const half_t*>(d_res), res_stride, batch, T, C,
+                           static_cast<half_t*>(d_y), y_stride);
         VDK_HIP(hipGetLastError());
     });
+}
+}  // namespace
+}  // namespace vdk
+
+extern "C" int vdk_se_gate_residual(const void* d_x, int x_stride, const float* d_gate, const void* d_res,
+                                    int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream) {
+    return vdk::se_residual(d_x, x_stride, d_gate, true, d_res, res_stride, batch, T, C, d_y, y_stride, stream);
+}
+
+extern "C" int vdk_se_scale_residual(const void* d_x, int x_stride, const float* d_scale, const void* d_res,
+                                     int res_stride, int batch, int T, int C, void* d_y, int y_stride, void* stream) {
+    return vdk::se_residual(d_x, x_stride, d_scale, false, d_res, res_stride, batch, T, C, d_y, y_stride, stream);
 }
 
 extern "C" int vdk_res2_block(void* d_buf, int stride, int batch, int T, int G, int scale, int dil,

@@ -352,10 +352,11 @@ void Model::encode_ecapa(int batch, int T) {
         check_rc(vdk_channel_mean(w.t2, C, batch, T, C, w.se_m, stream_));
         prof_end();
         linear("ecapa_se_fc1", w.se_m, batch, C, b.se1_w, b.se1_b, nullptr, b.se_ch, 1, w.se_h);
-        linear("ecapa_se_fc2", w.se_h, batch, b.se_ch, b.se2_w, b.se2_b, nullptr, C, 0, w.se_g);
+        // the sigmoid once per (clip, channel) in fc2's reduce
+        linear("ecapa_se_fc2", w.se_h, batch, b.se_ch, b.se2_w, b.se2_b, nullptr, C, VDK_ACT_SIGMOID, w.se_g);
         void* out = static_cast<uint8_t*>(w.cat) + 2 * (size_t)i * C;
         prof_begin("ecapa_se_gate", 0.0, 6.0 * batch * (double)T * C);
-        check_rc(vdk_se_gate_residual(w.t2, C, w.se_g, xin, xs, batch, T, C, out, catS, stream_));
+        check_rc(vdk_se_scale_residual(w.t2, C, w.se_g, xin, xs, batch, T, C, out, catS, stream_));
         prof_end();
     }
 
