@@ -1,7 +1,7 @@
 /*
  * oracle.c - CPU restatement of the reference speaker-embedding path.
  *
- * TEST INFRASTRUCTURE ONLY (see oracle.h): the parity checker and the CPU
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): the parity reference and the CPU
  * baseline, never part of the product library.
  */
 #include "oracle.h"

@@ -1,8 +1,8 @@
 /*
  * oracle.h - CPU restatement of the reference speaker-embedding path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
- * implementation: only the test suite, the smoke check and the CPU-baseline
+ * TEST INFRASTRUCTURE ONLY.  The HIP implementation's results are compared
+ * against this library: only the test suite, the smoke check and the CPU-baseline
  * leg of the benchmark may load it.  The product library never links it and
  * has no CPU fallback.
  *

@@ -1,7 +1,8 @@
 """numpy (f64) restatement of the reference's wav2vec2 analyze path.
 
 TEST INFRASTRUCTURE ONLY: imported by the test suite, the smoke check and the
-CPU-baseline leg of bench.py.  It is the checker, never the thing measured.
+CPU-baseline leg of bench.py.  Results are compared against it; it is never
+the thing measured.
 
 Follows src/analyze_w2v2.cpp of the reference, function by function:
   conv feature encoder      build_conv_encoder        :52-131 (conv1d_strided :34-45)

@@ -1,7 +1,8 @@
 """ctypes binding of the oracle (liboracle.so) and of oracle/_ref/libref.so.
 
 TEST INFRASTRUCTURE ONLY: imported by the test suite, the smoke check and the
-CPU-baseline leg of bench.py.  It is the checker, never the thing measured.
+CPU-baseline leg of bench.py.  Results are compared against it; it is never
+the thing measured.
 """
 import contextlib
 import ctypes as C

@@ -1,4 +1,4 @@
-"""Pins the oracle's FBank (oracle/oracle_fbank.c) before it is trusted as a checker.
+"""Pins the oracle's FBank (oracle/oracle_fbank.c) before results are compared against it.
 
 1. Golden vectors written by the reference's own src/fbank.cpp (tests/golden).
 2. The reference library itself (oracle/_ref/libref.so) when it is built here.
