@@ -116,6 +116,33 @@ def test_block0_reflect_pad_and_k5_conv():
         announce(f"block0 clip {c} rel-L2 {rel:.2e}")
 
 
+@pytest.mark.parametrize("T", [1, 2, 60, 62, 130, T4S])
+def test_feats_tmajor_tiled_matches_elementwise(T):
+    """vdk_feats_tmajor's LDS-tiled transpose (c_pad a multiple of 8) against
+    its element-wise path (c_pad = 100) and numpy, with per-row means:
+    frame blocks cut at 64 frames, reflect padding of short clips."""
+    rng = np.random.default_rng(90 + T)
+    nb, nm, pad = 3, 80, 2
+    feats = (3.0 * rng.standard_normal((nb, nm, T), dtype=np.float32))
+    rmean = rng.standard_normal((nb, nm), dtype=np.float32)
+    L = lib.lib()
+    df, dmn = lib.DeviceBuffer.from_array(feats), lib.DeviceBuffer.from_array(rmean)
+    Tp = T + 2 * pad
+    outs = {}
+    for cp in (96, 100):
+        d = lib.DeviceBuffer.from_array(np.full((nb, Tp, cp), 7.0, np.float16))
+        lib.check(L.vdk_feats_tmajor(df.ptr, dmn.ptr, nb, nm, T, pad, cp, d.ptr, None))
+        _sync()
+        outs[cp] = d.to_array(np.float16, (nb, Tp, cp))
+    assert np.array_equal(outs[96].view(np.uint16), outs[100][:, :, :96].view(np.uint16))
+    assert not outs[100][:, :, 96:].any()
+    idx = np.array([min(max(abs(j - pad) if j < pad + T else 2 * (T - 1) - (j - pad), 0), T - 1)
+                    for j in range(Tp)])
+    want = np.zeros((nb, Tp, 96), np.float16)
+    want[:, :, :nm] = (feats[:, :, idx] - rmean[:, :, None]).transpose(0, 2, 1).astype(np.float16)
+    assert np.array_equal(outs[96].view(np.uint16), want.view(np.uint16))
+
+
 @pytest.mark.parametrize("dil", [2, 3, 4])
 def test_reflect_pad_add_kernel(dil):
     """vdk_reflect_pad_add: the Res2Net group input x_j + y_{j-1}, reflect padded, bit-exact."""

@@ -46,6 +46,33 @@ __global__ __launch_bounds__(256) void feats_tmajor_kernel(const float* __restri
     out[i] = (half_t)v;
 }
 
+// The same map through an LDS tile: workgroup (64-frame block, clip) reads
+// the frames of every mel row along time (coalesced) and stores each frame's
+// Cpad channels as 16-byte chunks.  Cpad % 8 == 0, Cpad <= kFtC.
+constexpr int kFtF = 64, kFtC = 128;
+__global__ __launch_bounds__(256) void feats_tmajor_tiled_kernel(const float* __restrict__ f,
+                                                                 const float* __restrict__ rmean, int C, int T,
+                                                                 int pad, int Cpad, half_t* __restrict__ out) {
+    __shared__ float sv[kFtC][kFtF + 1];
+    const int Tp = T + 2 * pad, j0 = blockIdx.x * kFtF, b = blockIdx.y, tid = threadIdx.x;
+    const int nf = Tp - j0 < kFtF ? Tp - j0 : kFtF;
+    for (int i = tid; i < C * kFtF; i += 256) {
+        const int c = i / kFtF, jj = i - c * kFtF;
+        if (jj < nf)
+            sv[c][jj] = f[((size_t)b * C + c) * T + reflect_idx(j0 + jj, pad, T)] -
+                        (rmean ? rmean[(size_t)b * C + c] : 0.0f);
+    }
+    __syncthreads();
+    const int C8 = Cpad / 8;
+    for (int i = tid; i < nf * C8; i += 256) {
+        const int jj = i / C8, c0 = (i - jj * C8) * 8;
+        half8 h;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = c0 + e < C ? (half_t)sv[c0 + e][jj] : (half_t)0.0f;
+        *reinterpret_cast<half8*>(out + ((size_t)b * Tp + j0 + jj) * Cpad + c0) = h;
+    }
+}
+
 __global__ __launch_bounds__(256) void reflect_pad_add_kernel(const half_t* __restrict__ a, int as,
                                                               const half_t* __restrict__ bsrc, int bs, int B,
                                                               int T, int G, int pad, half_t* __restrict__ out) {
@@ -615,9 +642,16 @@ extern "C" int vdk_feats_tmajor(const float* d_feats, const float* d_row_mean, i
     return guarded([&] {
         require(d_feats && d_out, "feats_tmajor: NULL device pointer");
         require(batch > 0 && n_mels > 0 && T > 0 && pad >= 0 && c_pad >= n_mels, "feats_tmajor: bad shape");
-        const long n = (long)batch * (T + 2 * pad) * c_pad;
-        hipLaunchKernelGGL(feats_tmajor_kernel, dim3(cdiv(n, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                           d_feats, d_row_mean, batch, n_mels, T, pad, c_pad, static_cast<half_t*>(d_out));
+        if (c_pad % 8 == 0 && c_pad <= kFtC && al16(d_out)) {
+            hipLaunchKernelGGL(feats_tmajor_tiled_kernel, dim3(cdiv(T + 2 * pad, kFtF), batch), dim3(256), 0,
+                               static_cast<hipStream_t>(stream), d_feats, d_row_mean, n_mels, T, pad, c_pad,
+                               static_cast<half_t*>(d_out));
+        } else {
+            const long n = (long)batch * (T + 2 * pad) * c_pad;
+            hipLaunchKernelGGL(feats_tmajor_kernel, dim3(cdiv(n, 256)), dim3(256), 0,
+                               static_cast<hipStream_t>(stream), d_feats, d_row_mean, batch, n_mels, T, pad, c_pad,
+                               static_cast<half_t*>(d_out));
+        }
         VDK_HIP(hipGetLastError());
     });
 }
