@@ -241,15 +241,15 @@ __global__ __launch_bounds__(256) void linear_reduce_kernel(const float* __restr
     if (i >= (long)B * out_dim) return;
     const int o = (int)(i % out_dim);
     const size_t stride = (size_t)B * out_dim;
-    // fixed summation order, 8 loads in flight per step
+    // fixed summation order, 16 loads in flight per step
     double s = 0.0;
     int k = 0;
-    for (; k + 8 <= nsplit; k += 8) {
-        float v[8];
+    for (; k + 16 <= nsplit; k += 16) {
+        float v[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = part[(size_t)(k + j) * stride + i];
+        for (int j = 0; j < 16; ++j) v[j] = part[(size_t)(k + j) * stride + i];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s += (double)v[j];
+        for (int j = 0; j < 16; ++j) s += (double)v[j];
     }
     for (; k < nsplit; ++k) s += (double)part[(size_t)k * stride + i];
     float r = (float)s;
@@ -276,12 +276,12 @@ __global__ __launch_bounds__(256) void linear_reduce_l2_kernel(const float* __re
         const size_t i = (size_t)b * out_dim + o;
         double s = 0.0;
         int k = 0;
-        for (; k + 8 <= nsplit; k += 8) {
-            float v[8];
+        for (; k + 16 <= nsplit; k += 16) {   // 16 loads in flight, the sums in order
+            float v[16];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = part[(size_t)(k + j) * stride + i];
+            for (int j = 0; j < 16; ++j) v[j] = part[(size_t)(k + j) * stride + i];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) s += (double)v[j];
+            for (int j = 0; j < 16; ++j) s += (double)v[j];
         }
         for (; k < nsplit; ++k) s += (double)part[(size_t)k * stride + i];
         float r = (float)s;
